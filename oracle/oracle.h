@@ -1,0 +1,176 @@
+/*
+ * CPU oracle for the fine-tuning hot path: a plain-C restatement of the reference's backward kernels, the forward
+ * kernels a training step runs, its portable math, its random generator and the step orchestration.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product (etalii_dllm_amd/, include/) includes, links or calls this code.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as the checker or as the CPU
+ * baseline, never as the thing measured on the GPU.
+ *
+ * Every function cites the reference source it restates (paths relative to the reference checkout). Each output
+ * element has one accumulation in double over its reduced index in ascending order, rounded to float once; products
+ * of two floats are exact in double. The build uses -ffp-contract=off -fno-fast-math so every + - * / rounds once.
+ */
+#ifndef DLLM_ORACLE_H
+#define DLLM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- portable math: cpp/include/dllm/math.hpp ---- */
+double orc_exp(double x);     /* math.hpp:64-109 */
+double orc_log(double x);     /* math.hpp:113-162 */
+double orc_sin(double x);     /* math.hpp:220-232 */
+double orc_cos(double x);     /* math.hpp:234-246 */
+double orc_tanh(double x);    /* math.hpp:296-319 */
+double orc_sigmoid(double x); /* math.hpp:322-328 */
+float orc_dot(const float* a, const float* b, size_t n);                 /* math.hpp:31-37 */
+size_t orc_argmax(const float* v, size_t n);                             /* math.hpp:40-53 */
+void orc_softmax(const float* logits, float* out, size_t n);             /* math.hpp:387-398 */
+
+/* ---- random: cpp/include/dllm/random.hpp ---- */
+typedef struct { uint64_t s[4]; } orc_random;
+void orc_random_init(orc_random* r, uint64_t seed);                      /* random.hpp:12-18 */
+uint64_t orc_random_next(orc_random* r);                                 /* random.hpp:20-30 */
+double orc_random_double(orc_random* r);                                 /* random.hpp:33 */
+float orc_random_gaussian(orc_random* r);                                /* random.hpp:36-42 */
+void orc_fill_gaussian(uint64_t seed, float* out, size_t n);             /* kernels.cpp:207-218 */
+
+/* ---- forward kernels: cpp/include/dllm/nn.hpp ---- */
+void orc_linear(const float* x, const float* w, const float* bias, float* out, size_t rows, size_t in,
+                size_t out_features);                                    /* nn.hpp:28-50 */
+void orc_rms_norm(const float* x, const float* w, float* out, size_t rows, size_t dim, double eps,
+                  int unit_offset);                                      /* nn.hpp:391-408 */
+float orc_silu(float x);                                                 /* nn.hpp:467-470 */
+void orc_swiglu(const float* gate, const float* up, float* out, size_t n); /* nn.hpp:489-492 */
+void orc_rope(const float* x, const int64_t* positions, const double* inv_freq, float* out, size_t tokens,
+              size_t heads, size_t head_dim, size_t rotary_dim, int interleaved, int inverse); /* nn.hpp:501-530 */
+void orc_attention(const float* q, const float* k, const float* v, float* out, size_t q_len, size_t kv_len,
+                   size_t q_heads, size_t kv_heads, size_t head_dim, size_t value_dim, double scale, int causal,
+                   size_t q_offset, size_t window, double softcap);       /* nn.hpp:535-615,729-748,870-884 */
+void orc_moe_route(const float* logits, int64_t* indices, float* weights, size_t rows, size_t experts, size_t k,
+                   int normalize);                                       /* nn.hpp:864-896 */
+
+/* ---- backward kernels: cpp/include/dllm/grad.hpp ---- */
+void orc_linear_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, float* db,
+                         size_t rows, size_t in, size_t out_features);   /* grad.hpp:26-72 */
+void orc_rms_norm_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, size_t rows,
+                           size_t dim, double eps, int unit_offset);     /* grad.hpp:79-111 */
+float orc_silu_backward(float x, float dy);                              /* grad.hpp:177-181 */
+void orc_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,
+                            float* dv, size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads,
+                            size_t head_dim, size_t value_dim, double scale, int causal, size_t q_offset,
+                            size_t window, double softcap);              /* grad.hpp:206-301 */
+double orc_cross_entropy(const float* logits, const int64_t* targets, float* dlogits, size_t rows, size_t vocab,
+                         double scale);                                  /* grad.hpp:395-426 */
+int orc_embedding_backward(const float* dy, const int64_t* tokens, float* out, size_t rows, size_t dim,
+                           size_t vocab);                                /* grad.hpp:431-464 */
+double orc_sum_squares(const float* v, size_t n);                        /* grad.hpp:467-473 */
+void orc_adamw_step(float* param, const float* grad, float* m, float* v, size_t n, double lr, double beta1,
+                    double beta2, double eps, double weight_decay, double bc1, double bc2,
+                    double grad_scale);                                  /* grad.hpp:481-495 */
+void orc_moe_route_backward(const float* logits, const int64_t* indices, const float* dweights,
+                            const float* dprobabilities, float* dlogits, size_t rows, size_t experts, size_t k,
+                            int normalize);                              /* grad.hpp:507-541 */
+void orc_column_mean(const float* x, float* out, size_t rows, size_t cols); /* interp.hpp:146-155 */
+void orc_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n); /* quant.hpp:27-60 */
+
+/* ---- rotary frequencies: src/etalii_dllm/numerics.py:267-297 (default scaling) ---- */
+void orc_rope_inv_freq(size_t rotary_dim, double theta, double* out);
+
+/* ---- the kernel table a step driver calls (the oracle's own, or the reference's through oracle/_ref) ---- */
+typedef struct {
+    void (*linear)(const float*, const float*, const float*, float*, size_t, size_t, size_t);
+    void (*linear_backward)(const float*, const float*, const float*, float*, float*, float*, size_t, size_t, size_t);
+    void (*rms_norm)(const float*, const float*, float*, size_t, size_t, double, int);
+    void (*rms_norm_backward)(const float*, const float*, const float*, float*, float*, size_t, size_t, double, int);
+    void (*rope)(const float*, const int64_t*, const double*, float*, size_t, size_t, size_t, size_t, int, int);
+    void (*attention)(const float*, const float*, const float*, float*, size_t, size_t, size_t, size_t, size_t,
+                      size_t, double, int, size_t, size_t, double);
+    void (*attention_backward)(const float*, const float*, const float*, const float*, float*, float*, float*,
+                               size_t, size_t, size_t, size_t, size_t, size_t, double, int, size_t, size_t, double);
+    void (*silu)(const float*, float*, size_t);
+    void (*swiglu)(const float*, const float*, float*, size_t);
+    void (*silu_backward)(const float*, const float*, float*, size_t);
+    double (*cross_entropy)(const float*, const int64_t*, float*, size_t, size_t, double);
+    int (*embedding_backward)(const float*, const int64_t*, float*, size_t, size_t, size_t);
+    double (*sum_squares)(const float*, size_t);
+    void (*adamw_step)(float*, const float*, float*, float*, size_t, double, double, double, double, double, double,
+                       double, double);
+    void (*softmax)(const float*, float*, size_t);
+    void (*moe_route)(const float*, int64_t*, float*, size_t, size_t, size_t, int);
+    void (*moe_route_backward)(const float*, const int64_t*, const float*, const float*, float*, size_t, size_t,
+                               size_t, int);
+    void (*column_mean)(const float*, float*, size_t, size_t);
+    float (*dot)(const float*, const float*, size_t);
+} orc_ops;
+
+const orc_ops* orc_default_ops(void);
+
+/* ---- decoder configuration: src/etalii_dllm/architecture.py (the fields a decoder step reads) ---- */
+typedef struct {
+    int64_t vocab, hidden, inter, layers, heads, kv_heads, head_dim;
+    int64_t attn_bias;   /* q/k/v biases (Qwen2) */
+    int64_t qk_norm;     /* 0 none, 1 per head (Qwen3), 2 over the whole projection (OLMo 2, OLMoE) */
+    int64_t window;      /* sliding window, 0 = full causal attention */
+    int64_t tied;        /* lm head = token embedding */
+    int64_t experts, topk, normalize, expert_inter; /* mixture of experts; experts == 0 for dense */
+    int64_t rotary_dim;
+    double eps, rope_theta, attention_scale;
+} orc_config;
+
+/*
+ * Tensor slots. Every tensor of the decoder has a fixed slot: the globals, then per layer a block of
+ * ORC_LAYER_FIXED slots followed by 3 slots per expert. Absent tensors (no bias, no QK-norm, dense vs sparse) have
+ * a NULL pointer in their slot.
+ */
+enum {
+    ORC_EMBEDDING = 0, ORC_FINAL_NORM = 1, ORC_LM_HEAD = 2, ORC_GLOBALS = 3,
+    ORC_ATTN_NORM = 0, ORC_Q = 1, ORC_K = 2, ORC_V = 3, ORC_QB = 4, ORC_KB = 5, ORC_VB = 6, ORC_QNORM = 7,
+    ORC_KNORM = 8, ORC_O = 9, ORC_MLP_NORM = 10, ORC_GATE = 11, ORC_UP = 12, ORC_DOWN = 13, ORC_ROUTER = 14,
+    ORC_LAYER_FIXED = 15
+};
+int64_t orc_layer_slots(const orc_config* c);
+int64_t orc_slot_count(const orc_config* c);
+int64_t orc_slot(const orc_config* c, int64_t layer, int64_t kind);            /* layer tensor */
+int64_t orc_expert_slot(const orc_config* c, int64_t layer, int64_t expert, int64_t which); /* 0 gate 1 up 2 down */
+
+/*
+ * One window: loss and the gradient of every tensor (src/etalii_dllm/training/backprop.py:88-118). grads[slot] must
+ * be allocated (zeroing is not required) for every present slot. Returns 0 on success. *loss gets the summed
+ * cross-entropy, *router_loss the load-balancing loss (0 for dense models).
+ */
+int orc_window_gradients(const orc_ops* ops, const orc_config* c, float* const* w, const int64_t* tokens,
+                         const int64_t* targets, int64_t n, double scale, double router_scale, float* const* grads,
+                         double* loss, double* router_loss);
+
+/* Logits [n, vocab] of the forward pass (backprop.py:69-73). */
+int orc_logits(const orc_ops* ops, const orc_config* c, float* const* w, const int64_t* tokens, int64_t n,
+               float* logits);
+
+/*
+ * One full fine-tuning step (training/trainer.py:290-335, training/optimizer.py:82-109): per-window gradients summed
+ * in batch order, the global norm over tensors in `order` (natural name order), clipping, bias corrections by repeated
+ * multiplication and AdamW per tensor (decay only for matrices). windows: `count` windows, window i has
+ * lengths[i] tokens at tokens + offsets[i]. params/m/v are updated in place; grads receives the summed gradients.
+ */
+typedef struct {
+    double lr, beta1, beta2, eps, weight_decay, max_grad_norm, router_aux_loss;
+    int64_t step; /* 1-based number of this update */
+} orc_adamw;
+
+int orc_train_step(const orc_ops* ops, const orc_config* c, float* const* params, float* const* m, float* const* v,
+                   float* const* grads, const int64_t* order, int64_t order_len, const int64_t* tokens,
+                   const int64_t* offsets, const int64_t* lengths, int64_t count, const orc_adamw* opt,
+                   double* loss_out, double* norm_out);
+
+int64_t orc_tensor_numel(const orc_config* c, int64_t slot); /* 0 for absent slots */
+int orc_tensor_ndim(const orc_config* c, int64_t slot);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

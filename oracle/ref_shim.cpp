@@ -1,0 +1,167 @@
+// C shim over the reference's own header-only CPU kernels (cpp/include/dllm/*.hpp, compiled from the reference
+// checkout by oracle/Makefile into oracle/_ref/libdllm_ref.so). TEST INFRASTRUCTURE ONLY: it pins the oracle's C
+// restatement bit for bit and, driven by the oracle's step orchestration, times the reference CPU path as the
+// baseline. The wrappers only adapt calling conventions; every computation is the reference's.
+#include "dllm/fpenv.hpp"
+#include "dllm/grad.hpp"
+#include "dllm/interp.hpp"
+#include "dllm/math.hpp"
+#include "dllm/nn.hpp"
+#include "dllm/parallel.hpp"
+#include "dllm/quant.hpp"
+#include "dllm/random.hpp"
+
+#include <cstring>
+#include <exception>
+#include <vector>
+
+#include "oracle.h"
+
+namespace {
+
+using dllm::FpEnvGuard;
+
+void linear(const float* x, const float* w, const float* b, float* out, size_t rows, size_t in, size_t n) {
+    FpEnvGuard guard;
+    dllm::linear(x, w, b, out, rows, in, n);
+}
+void linear_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, float* db, size_t rows,
+                     size_t in, size_t n) {
+    FpEnvGuard guard;
+    dllm::linear_backward(x, w, dy, dx, dw, db, rows, in, n);
+}
+void rms_norm(const float* x, const float* w, float* out, size_t rows, size_t dim, double eps, int unit) {
+    FpEnvGuard guard;
+    dllm::rms_norm(x, w, out, rows, dim, eps, unit != 0);
+}
+void rms_norm_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, size_t rows, size_t dim,
+                       double eps, int unit) {
+    FpEnvGuard guard;
+    dllm::rms_norm_backward(x, w, dy, dx, dw, rows, dim, eps, unit != 0);
+}
+void rope(const float* x, const int64_t* pos, const double* f, float* out, size_t tokens, size_t heads, size_t hd,
+          size_t rot, int interleaved, int inverse) {
+    FpEnvGuard guard;
+    dllm::rope(x, pos, f, out, tokens, heads, hd, rot, interleaved != 0, inverse != 0);
+}
+void attention(const float* q, const float* k, const float* v, float* out, size_t ql, size_t kl, size_t qh, size_t kh,
+               size_t hd, size_t vd, double scale, int causal, size_t qo, size_t window, double softcap) {
+    FpEnvGuard guard;
+    dllm::attention(q, k, v, out, ql, kl, qh, kh, hd, vd, scale, causal != 0, qo, window, softcap);
+}
+void attention_backward(const float* q, const float* k, const float* v, const float* d, float* dq, float* dk,
+                        float* dv, size_t ql, size_t kl, size_t qh, size_t kh, size_t hd, size_t vd, double scale,
+                        int causal, size_t qo, size_t window, double softcap) {
+    FpEnvGuard guard;
+    dllm::attention_backward(q, k, v, d, dq, dk, dv, ql, kl, qh, kh, hd, vd, scale, causal != 0, qo, window, softcap);
+}
+void silu(const float* x, float* out, size_t n) {
+    FpEnvGuard guard;
+    dllm::parallel_elementwise(n, [&](std::size_t i) { out[i] = dllm::silu(x[i]); });
+}
+void swiglu(const float* g, const float* u, float* out, size_t n) {
+    FpEnvGuard guard;
+    dllm::gated_activation<dllm::silu>(g, u, out, n);
+}
+void silu_backward(const float* x, const float* dy, float* out, size_t n) {
+    FpEnvGuard guard;
+    for (size_t i = 0; i < n; ++i) out[i] = dllm::silu_backward(x[i], dy[i]);
+}
+double cross_entropy(const float* l, const int64_t* t, float* dl, size_t rows, size_t vocab, double scale) {
+    FpEnvGuard guard;
+    try {
+        return dllm::cross_entropy(l, t, dl, rows, vocab, scale);
+    } catch (const std::exception&) {
+        return __builtin_nan("");
+    }
+}
+int embedding_backward(const float* dy, const int64_t* tokens, float* out, size_t rows, size_t dim, size_t vocab) {
+    FpEnvGuard guard;
+    try {
+        dllm::embedding_backward(dy, tokens, out, rows, dim, vocab);
+    } catch (const std::exception&) {
+        return -1;
+    }
+    return 0;
+}
+double sum_squares(const float* v, size_t n) {
+    FpEnvGuard guard;
+    return dllm::sum_squares(v, n);
+}
+void adamw_step(float* p, const float* g, float* m, float* v, size_t n, double lr, double b1, double b2, double eps,
+                double wd, double bc1, double bc2, double gs) {
+    FpEnvGuard guard;
+    dllm::adamw_step(p, g, m, v, n, lr, b1, b2, eps, wd, bc1, bc2, gs);
+}
+void softmax(const float* l, float* out, size_t n) {
+    FpEnvGuard guard;
+    std::vector<double> scratch(n);
+    dllm::softmax(l, out, scratch.data(), n);
+}
+void moe_route(const float* l, int64_t* idx, float* w, size_t rows, size_t e, size_t k, int normalize) {
+    FpEnvGuard guard;
+    dllm::moe_route(l, idx, w, rows, e, k, normalize != 0);
+}
+void moe_route_backward(const float* l, const int64_t* idx, const float* dw, const float* dp, float* dl, size_t rows,
+                        size_t e, size_t k, int normalize) {
+    FpEnvGuard guard;
+    dllm::moe_route_backward(l, idx, dw, dp, dl, rows, e, k, normalize != 0);
+}
+void column_mean(const float* x, float* out, size_t rows, size_t cols) {
+    FpEnvGuard guard;
+    dllm::column_mean(x, out, rows, cols);
+}
+float dot(const float* a, const float* b, size_t n) {
+    FpEnvGuard guard;
+    return dllm::dot(a, b, n);
+}
+
+const orc_ops kRefOps = {
+    linear, linear_backward, rms_norm, rms_norm_backward, rope, attention, attention_backward, silu, swiglu,
+    silu_backward, cross_entropy, embedding_backward, sum_squares, adamw_step, softmax, moe_route,
+    moe_route_backward, column_mean, dot,
+};
+
+}  // namespace
+
+extern "C" {
+
+const orc_ops* ref_ops(void) { return &kRefOps; }
+
+void ref_set_threads(size_t n) { dllm::ThreadPool::global().set_threads(n); }
+size_t ref_threads(void) { return dllm::ThreadPool::global().threads(); }
+
+double ref_exp(double x) { FpEnvGuard g; return dllm::exp(x); }
+double ref_log(double x) { FpEnvGuard g; return dllm::log(x); }
+double ref_sin(double x) { FpEnvGuard g; return dllm::sin(x); }
+double ref_cos(double x) { FpEnvGuard g; return dllm::cos(x); }
+double ref_tanh(double x) { FpEnvGuard g; return dllm::tanh(x); }
+double ref_sigmoid(double x) { FpEnvGuard g; return dllm::sigmoid(x); }
+float ref_silu(float x) { FpEnvGuard g; return dllm::silu(x); }
+float ref_silu_backward(float x, float dy) { FpEnvGuard g; return dllm::silu_backward(x, dy); }
+
+void ref_fill_gaussian(uint64_t seed, float* out, size_t n) {
+    dllm::Random r(seed);
+    for (size_t i = 0; i < n; ++i) out[i] = r.next_gaussian();
+}
+uint64_t ref_random_first(uint64_t seed) {
+    dllm::Random r(seed);
+    return r.next_u64();
+}
+void ref_linear_reference(const float* x, const float* w, const float* b, float* out, size_t rows, size_t in,
+                          size_t n) {
+    FpEnvGuard guard;
+    dllm::linear_reference(x, w, b, out, rows, in, n);
+}
+void ref_attention_reference(const float* q, const float* k, const float* v, float* out, size_t ql, size_t kl,
+                             size_t qh, size_t kh, size_t hd, size_t vd, double scale, int causal, size_t qo,
+                             size_t window, double softcap) {
+    FpEnvGuard guard;
+    dllm::attention_reference(q, k, v, out, ql, kl, qh, kh, hd, vd, scale, causal != 0, qo, window, softcap);
+}
+void ref_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n) {
+    FpEnvGuard guard;
+    dllm::quantize_q8_0(x, q, scales, n);
+}
+
+}  // extern "C"

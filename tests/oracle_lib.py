@@ -1,0 +1,580 @@
+"""ctypes access to the CPU oracle (oracle/liboracle.so) and the reference-kernel shim (oracle/_ref/libdllm_ref.so),
+plus the decoder configurations, tensor names and fixture weights the parity tests use.
+
+Test infrastructure: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
+Names, shapes and orders follow src/etalii_dllm/architecture.py:418-468 and modelfile.py:40-47 of the reference;
+fixture weights follow tests/model_fixtures.py:216-336.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import hashlib
+import math
+import re
+from dataclasses import dataclass, replace
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libdllm_ref.so"
+
+_f32p = C.POINTER(C.c_float)
+_f64p = C.POINTER(C.c_double)
+_i64p = C.POINTER(C.c_int64)
+_sz = C.c_size_t
+
+
+class OrcConfig(C.Structure):
+    _fields_ = [(name, C.c_int64) for name in (
+        "vocab", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "attn_bias", "qk_norm", "window",
+        "tied", "experts", "topk", "normalize", "expert_inter", "rotary_dim")] + [
+        ("eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double)]
+
+
+class OrcAdamW(C.Structure):
+    _fields_ = [(name, C.c_double) for name in (
+        "lr", "beta1", "beta2", "eps", "weight_decay", "max_grad_norm", "router_aux_loss")] + [("step", C.c_int64)]
+
+
+def ptr(a: np.ndarray | None, kind=_f32p):
+    if a is None:
+        return None
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(kind)
+
+
+_libs: dict[str, C.CDLL] = {}
+
+
+def oracle() -> C.CDLL:
+    if "oracle" not in _libs:
+        lib = C.CDLL(str(ORACLE_SO))
+        for name in ("orc_exp", "orc_log", "orc_sin", "orc_cos", "orc_tanh", "orc_sigmoid"):
+            getattr(lib, name).restype = C.c_double
+            getattr(lib, name).argtypes = [C.c_double]
+        lib.orc_cross_entropy.restype = C.c_double
+        lib.orc_sum_squares.restype = C.c_double
+        lib.orc_default_ops.restype = C.c_void_p
+        lib.orc_silu.restype = C.c_float
+        lib.orc_silu.argtypes = [C.c_float]
+        lib.orc_silu_backward.restype = C.c_float
+        lib.orc_silu_backward.argtypes = [C.c_float, C.c_float]
+        lib.orc_random_next.restype = C.c_uint64
+        lib.orc_window_gradients.argtypes = [C.c_void_p, C.POINTER(OrcConfig), C.POINTER(_f32p), _i64p, _i64p,
+                                             C.c_int64, C.c_double, C.c_double, C.POINTER(_f32p), _f64p, _f64p]
+        lib.orc_train_step.argtypes = [C.c_void_p, C.POINTER(OrcConfig), C.POINTER(_f32p), C.POINTER(_f32p),
+                                       C.POINTER(_f32p), C.POINTER(_f32p), _i64p, C.c_int64, _i64p, _i64p, _i64p,
+                                       C.c_int64, C.POINTER(OrcAdamW), _f64p, _f64p]
+        lib.orc_logits.argtypes = [C.c_void_p, C.POINTER(OrcConfig), C.POINTER(_f32p), _i64p, C.c_int64, _f32p]
+        _libs["oracle"] = lib
+    return _libs["oracle"]
+
+
+def reference_available() -> bool:
+    return REF_SO.exists()
+
+
+def ref() -> C.CDLL:
+    if "ref" not in _libs:
+        lib = C.CDLL(str(REF_SO))
+        for name in ("ref_exp", "ref_log", "ref_sin", "ref_cos", "ref_tanh", "ref_sigmoid"):
+            getattr(lib, name).restype = C.c_double
+            getattr(lib, name).argtypes = [C.c_double]
+        lib.ref_ops.restype = C.c_void_p
+        lib.ref_silu.restype = C.c_float
+        lib.ref_silu.argtypes = [C.c_float]
+        lib.ref_silu_backward.restype = C.c_float
+        lib.ref_silu_backward.argtypes = [C.c_float, C.c_float]
+        lib.ref_random_first.restype = C.c_uint64
+        lib.ref_random_first.argtypes = [C.c_uint64]
+        lib.ref_threads.restype = C.c_size_t
+        _libs["ref"] = lib
+    return _libs["ref"]
+
+
+# ---- the kernel table, callable from Python for either library ----
+
+class _OpsTable(C.Structure):
+    _fields_ = [(name, C.c_void_p) for name in (
+        "linear", "linear_backward", "rms_norm", "rms_norm_backward", "rope", "attention", "attention_backward", "silu",
+        "swiglu", "silu_backward", "cross_entropy", "embedding_backward", "sum_squares", "adamw_step", "softmax",
+        "moe_route", "moe_route_backward", "column_mean", "dot")]
+
+
+_SIGS = {
+    "linear": (None, [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz]),
+    "linear_backward": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz]),
+    "rms_norm": (None, [_f32p, _f32p, _f32p, _sz, _sz, C.c_double, C.c_int]),
+    "rms_norm_backward": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz, C.c_double, C.c_int]),
+    "rope": (None, [_f32p, _i64p, _f64p, _f32p, _sz, _sz, _sz, _sz, C.c_int, C.c_int]),
+    "attention": (None, [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz, _sz, C.c_double, C.c_int, _sz, _sz,
+                         C.c_double]),
+    "attention_backward": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz, _sz,
+                                  C.c_double, C.c_int, _sz, _sz, C.c_double]),
+    "silu": (None, [_f32p, _f32p, _sz]),
+    "swiglu": (None, [_f32p, _f32p, _f32p, _sz]),
+    "silu_backward": (None, [_f32p, _f32p, _f32p, _sz]),
+    "cross_entropy": (C.c_double, [_f32p, _i64p, _f32p, _sz, _sz, C.c_double]),
+    "embedding_backward": (C.c_int, [_f32p, _i64p, _f32p, _sz, _sz, _sz]),
+    "sum_squares": (C.c_double, [_f32p, _sz]),
+    "adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, _sz] + [C.c_double] * 8),
+    "softmax": (None, [_f32p, _f32p, _sz]),
+    "moe_route": (None, [_f32p, _i64p, _f32p, _sz, _sz, _sz, C.c_int]),
+    "moe_route_backward": (None, [_f32p, _i64p, _f32p, _f32p, _f32p, _sz, _sz, _sz, C.c_int]),
+    "column_mean": (None, [_f32p, _f32p, _sz, _sz]),
+    "dot": (C.c_float, [_f32p, _f32p, _sz]),
+}
+
+
+class Kernels:
+    """NumPy-level calls of one kernel table (the oracle's or the reference's), with the reference binding's
+    argument conventions (cpp/kernels.cpp)."""
+
+    def __init__(self, table_address: int, name: str) -> None:
+        self.name = name
+        self.address = table_address
+        table = _OpsTable.from_address(table_address)
+        self._fn = {}
+        for field, (restype, argtypes) in _SIGS.items():
+            self._fn[field] = C.CFUNCTYPE(restype, *argtypes)(getattr(table, field))
+
+    def linear(self, x, w, bias=None):
+        rows, inf = x.shape[0], x.shape[1]
+        out = np.empty((rows, w.shape[0]), np.float32)
+        self._fn["linear"](ptr(x), ptr(w), ptr(bias), ptr(out), rows, inf, w.shape[0])
+        return out
+
+    def linear_backward(self, x, w, dy, with_bias=False):
+        rows, inf, outf = x.shape[0], w.shape[1], w.shape[0]
+        dx = np.empty((rows, inf), np.float32)
+        dw = np.empty((outf, inf), np.float32)
+        db = np.empty(outf, np.float32) if with_bias else None
+        self._fn["linear_backward"](ptr(x), ptr(w), ptr(dy), ptr(dx), ptr(dw), ptr(db), rows, inf, outf)
+        return dx, dw, db
+
+    def rms_norm(self, x, w, eps=1e-6, unit_offset=False):
+        out = np.empty_like(x)
+        dim = x.shape[-1]
+        self._fn["rms_norm"](ptr(x), ptr(w), ptr(out), x.size // dim, dim, eps, int(unit_offset))
+        return out
+
+    def rms_norm_backward(self, x, w, dy, eps=1e-6, unit_offset=False):
+        dim = x.shape[-1]
+        dx = np.empty_like(x)
+        dw = np.empty(dim, np.float32)
+        self._fn["rms_norm_backward"](ptr(x), ptr(w), ptr(dy), ptr(dx), ptr(dw), x.size // dim, dim, eps,
+                                      int(unit_offset))
+        return dx, dw
+
+    def rope(self, x, positions, inv_freq, interleaved=False, inverse=False):
+        out = np.empty_like(x)
+        t, h, d = x.shape
+        self._fn["rope"](ptr(x), ptr(positions, _i64p), ptr(inv_freq, _f64p), ptr(out), t, h, d, 2 * len(inv_freq),
+                         int(interleaved), int(inverse))
+        return out
+
+    def attention(self, q, k, v, scale, causal=True, q_offset=0, window=0, softcap=0.0):
+        out = np.empty((q.shape[0], q.shape[1], v.shape[2]), np.float32)
+        self._fn["attention"](ptr(q), ptr(k), ptr(v), ptr(out), q.shape[0], k.shape[0], q.shape[1], k.shape[1],
+                              q.shape[2], v.shape[2], scale, int(causal), q_offset, window, softcap)
+        return out
+
+    def attention_backward(self, q, k, v, dout, scale, causal=True, q_offset=0, window=0, softcap=0.0):
+        dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+        self._fn["attention_backward"](ptr(q), ptr(k), ptr(v), ptr(dout), ptr(dq), ptr(dk), ptr(dv), q.shape[0],
+                                       k.shape[0], q.shape[1], k.shape[1], q.shape[2], v.shape[2], scale,
+                                       int(causal), q_offset, window, softcap)
+        return dq, dk, dv
+
+    def silu(self, x):
+        out = np.empty_like(x)
+        self._fn["silu"](ptr(x), ptr(out), x.size)
+        return out
+
+    def swiglu(self, gate, up):
+        out = np.empty_like(gate)
+        self._fn["swiglu"](ptr(gate), ptr(up), ptr(out), gate.size)
+        return out
+
+    def silu_backward(self, x, dy):
+        out = np.empty_like(x)
+        self._fn["silu_backward"](ptr(x), ptr(dy), ptr(out), x.size)
+        return out
+
+    def cross_entropy(self, logits, targets, scale=1.0):
+        d = np.empty_like(logits)
+        loss = self._fn["cross_entropy"](ptr(logits), ptr(targets, _i64p), ptr(d), logits.shape[0], logits.shape[1],
+                                         scale)
+        return loss, d
+
+    def embedding_backward(self, dy, tokens, vocab):
+        out = np.empty((vocab, dy.shape[1]), np.float32)
+        rc = self._fn["embedding_backward"](ptr(dy), ptr(tokens, _i64p), ptr(out), dy.shape[0], dy.shape[1], vocab)
+        if rc != 0:
+            raise ValueError("token id out of range")
+        return out
+
+    def sum_squares(self, v):
+        return self._fn["sum_squares"](ptr(v), v.size)
+
+    def adamw_step(self, p, g, m, v, lr, b1, b2, eps, wd, bc1, bc2, gs=1.0):
+        self._fn["adamw_step"](ptr(p), ptr(g), ptr(m), ptr(v), p.size, lr, b1, b2, eps, wd, bc1, bc2, gs)
+
+    def softmax(self, x):
+        out = np.empty_like(x)
+        self._fn["softmax"](ptr(x), ptr(out), x.size)
+        return out
+
+    def moe_route(self, logits, k, normalize):
+        rows, e = logits.shape
+        idx = np.empty((rows, k), np.int64)
+        w = np.empty((rows, k), np.float32)
+        self._fn["moe_route"](ptr(logits), ptr(idx, _i64p), ptr(w), rows, e, k, int(normalize))
+        return idx, w
+
+    def moe_route_backward(self, logits, idx, dweights, dprob, normalize):
+        rows, e = logits.shape
+        out = np.empty_like(logits)
+        self._fn["moe_route_backward"](ptr(logits), ptr(idx, _i64p), ptr(dweights), ptr(dprob), ptr(out), rows, e,
+                                       idx.shape[1], int(normalize))
+        return out
+
+    def column_mean(self, x):
+        out = np.empty(x.shape[1], np.float32)
+        self._fn["column_mean"](ptr(x), ptr(out), x.shape[0], x.shape[1])
+        return out
+
+    def dot(self, a, b):
+        return self._fn["dot"](ptr(a), ptr(b), a.size)
+
+
+def oracle_kernels() -> Kernels:
+    return Kernels(oracle().orc_default_ops(), "oracle")
+
+
+def ref_kernels() -> Kernels:
+    return Kernels(ref().ref_ops(), "reference")
+
+
+def fill_gaussian(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    oracle().orc_fill_gaussian(C.c_uint64(seed), ptr(out), C.c_size_t(n))
+    return out
+
+
+def gaussian(seed: int, *shape: int, scale: float = 1.0) -> np.ndarray:
+    values = fill_gaussian(seed, int(np.prod(shape))).reshape(shape)
+    return values if scale == 1.0 else values * np.float32(scale)
+
+
+def rope_inv_freq(rotary_dim: int, theta: float) -> np.ndarray:
+    out = np.empty(rotary_dim // 2, np.float64)
+    oracle().orc_rope_inv_freq(C.c_size_t(rotary_dim), C.c_double(theta), ptr(out, _f64p))
+    return out
+
+
+def tensor_fingerprint(values: np.ndarray) -> str:
+    """Tensor.fingerprint (src/etalii_dllm/tensor.py:93-98): SHA-256 of the shape as int64 LE, '|', then the bits."""
+    digest = hashlib.sha256(np.asarray(values.shape, dtype="<i8").tobytes())
+    digest.update(b"|")
+    digest.update(np.ascontiguousarray(values).tobytes())
+    return digest.hexdigest()
+
+
+def fingerprint(values: np.ndarray) -> str:
+    """numerics.fingerprint (numerics.py:76-79): SHA-256 of the little-endian float32 bits."""
+    return hashlib.sha256(np.ascontiguousarray(values, dtype="<f4").tobytes()).hexdigest()
+
+
+# ---- decoder configurations ----
+
+@dataclass(frozen=True)
+class Decoder:
+    family: str
+    vocab: int
+    hidden: int
+    inter: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    eps: float
+    rope_theta: float
+    tied: bool
+    attn_bias: bool = False
+    qk_norm: int = 0  # 0 none, 1 per head, 2 whole projection
+    window: int = 0
+    experts: int = 0
+    topk: int = 0
+    normalize: bool = False
+    expert_inter: int = 0
+
+    @property
+    def attention_scale(self) -> float:
+        return 1.0 / math.sqrt(self.head_dim)
+
+    def c(self) -> OrcConfig:
+        return OrcConfig(self.vocab, self.hidden, self.inter, self.layers, self.heads, self.kv_heads, self.head_dim,
+                         int(self.attn_bias), self.qk_norm, self.window, int(self.tied), self.experts, self.topk,
+                         int(self.normalize), self.expert_inter or self.inter, self.head_dim, self.eps,
+                         self.rope_theta, self.attention_scale)
+
+    def tensor_shapes(self) -> dict[str, tuple[int, ...]]:
+        """architecture.py:418-468 (pre-norm decoders)."""
+        q, kv, H = self.heads * self.head_dim, self.kv_heads * self.head_dim, self.hidden
+        shapes = {"token_embedding.weight": (self.vocab, H)}
+        for i in range(self.layers):
+            p = f"layers.{i}."
+            shapes[p + "attention_norm.weight"] = (H,)
+            shapes[p + "attention.q.weight"] = (q, H)
+            shapes[p + "attention.k.weight"] = (kv, H)
+            shapes[p + "attention.v.weight"] = (kv, H)
+            if self.attn_bias:
+                shapes[p + "attention.q.bias"] = (q,)
+                shapes[p + "attention.k.bias"] = (kv,)
+                shapes[p + "attention.v.bias"] = (kv,)
+            if self.qk_norm:
+                shapes[p + "attention.q_norm.weight"] = (q if self.qk_norm == 2 else self.head_dim,)
+                shapes[p + "attention.k_norm.weight"] = (kv if self.qk_norm == 2 else self.head_dim,)
+            shapes[p + "attention.o.weight"] = (H, q)
+            shapes[p + "mlp_norm.weight"] = (H,)
+            if self.experts:
+                e_inter = self.expert_inter or self.inter
+                shapes[p + "mlp.router.weight"] = (self.experts, H)
+                for e in range(self.experts):
+                    shapes[p + f"mlp.experts.{e}.gate.weight"] = (e_inter, H)
+                    shapes[p + f"mlp.experts.{e}.up.weight"] = (e_inter, H)
+                    shapes[p + f"mlp.experts.{e}.down.weight"] = (H, e_inter)
+            else:
+                shapes[p + "mlp.gate.weight"] = (self.inter, H)
+                shapes[p + "mlp.up.weight"] = (self.inter, H)
+                shapes[p + "mlp.down.weight"] = (H, self.inter)
+        shapes["final_norm.weight"] = (H,)
+        if not self.tied:
+            shapes["lm_head.weight"] = (self.vocab, H)
+        return shapes
+
+    def slot_of(self, name: str) -> int:
+        """The oracle's fixed slot of a tensor name (oracle/oracle.h)."""
+        fixed = {"token_embedding.weight": 0, "final_norm.weight": 1, "lm_head.weight": 2}
+        if name in fixed:
+            return fixed[name]
+        kinds = {"attention_norm.weight": 0, "attention.q.weight": 1, "attention.k.weight": 2,
+                 "attention.v.weight": 3, "attention.q.bias": 4, "attention.k.bias": 5, "attention.v.bias": 6,
+                 "attention.q_norm.weight": 7, "attention.k_norm.weight": 8, "attention.o.weight": 9,
+                 "mlp_norm.weight": 10, "mlp.gate.weight": 11, "mlp.up.weight": 12, "mlp.down.weight": 13,
+                 "mlp.router.weight": 14}
+        _, layer, rest = name.split(".", 2)
+        per_layer = 15 + 3 * self.experts
+        base = 3 + int(layer) * per_layer
+        if rest in kinds:
+            return base + kinds[rest]
+        _, _, expert, which, _ = rest.split(".")
+        return base + 15 + 3 * int(expert) + {"gate": 0, "up": 1, "down": 2}[which]
+
+    def slot_count(self) -> int:
+        return 3 + self.layers * (15 + 3 * self.experts)
+
+
+def natural_key(name: str):
+    """modelfile.py:40-43: digit runs compare as numbers, the name itself breaks ties."""
+    parts = re.split(r"(\d+)", name)
+    return (*((0, int(p), "") if p.isdigit() else (1, 0, p) for p in parts), name)
+
+
+def tensor_order(names) -> list[str]:
+    return sorted(names, key=natural_key)
+
+
+TINY = dict(vocab=64, hidden=16, inter=32, layers=2, heads=4, kv_heads=2, head_dim=4, eps=1e-5, rope_theta=1e5)
+
+# tests/model_fixtures.py:38-171 and the importer's reading of them (importing/importer.py:291-343)
+FIXTURES = {
+    "llama": Decoder("llama", tied=True, **TINY),
+    "mistral": Decoder("mistral", tied=False, window=3, **TINY),
+    "qwen2": Decoder("qwen2", tied=False, attn_bias=True, **TINY),
+    "qwen3": Decoder("qwen3", tied=True, qk_norm=1, **{**TINY, "head_dim": 8}),
+    "mixtral": Decoder("mixtral", tied=False, experts=4, topk=2, normalize=True, **TINY),
+    "olmoe": Decoder("olmoe", tied=False, qk_norm=2, experts=4, topk=2, normalize=False,
+                     **{**TINY, "inter": 8}),
+}
+
+
+def bf16_round(values: np.ndarray) -> np.ndarray:
+    """model_fixtures.py:196-204: round to bfloat16 (nearest even) and back to float32."""
+    bits = np.ascontiguousarray(values, dtype="<f4").view("<u4").astype(np.uint64)
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype("<u4")
+    return (rounded << np.uint32(16)).view("<f4")
+
+
+def fixture_weights(d: Decoder, seed: int = 11) -> dict[str, np.ndarray]:
+    """model_fixtures.hf_weights in our names (the Hugging Face import maps names one to one for these families)."""
+    weights = {}
+    for index, (name, shape) in enumerate(sorted(d.tensor_shapes().items())):
+        values = fill_gaussian(seed * 1000 + index, int(np.prod(shape))).reshape(shape) * np.float32(0.1)
+        if name.endswith("mlp.router.weight"):
+            values = values * np.float32(16)
+        weights[name] = bf16_round(values)
+    return weights
+
+
+def synthetic_weights(d: Decoder, seed: int, scale: float = 0.02) -> dict[str, np.ndarray]:
+    """Benchmark inputs: fill_gaussian(seed * 1000 + i) * scale per tensor in tensor order, norms at 1.0."""
+    weights = {}
+    for index, name in enumerate(tensor_order(d.tensor_shapes())):
+        shape = d.tensor_shapes()[name]
+        if name.endswith("norm.weight"):
+            weights[name] = np.ones(shape, np.float32)
+        else:
+            weights[name] = fill_gaussian(seed * 1000 + index, int(np.prod(shape))).reshape(shape) * np.float32(scale)
+    return weights
+
+
+def slot_array(d: Decoder, tensors: dict[str, np.ndarray]):
+    arr = (_f32p * d.slot_count())()
+    for name, values in tensors.items():
+        arr[d.slot_of(name)] = ptr(values)
+    return arr
+
+
+def window_gradients(kern: Kernels, d: Decoder, weights, tokens, targets, scale=1.0, router_scale=0.0):
+    """DecoderGradients.losses_and_gradients through the oracle's orchestration and the given kernel table."""
+    grads = {name: np.empty(shape, np.float32) for name, shape in d.tensor_shapes().items()}
+    tok = np.ascontiguousarray(tokens, np.int64)
+    tgt = np.ascontiguousarray(targets, np.int64)
+    loss, rl = C.c_double(), C.c_double()
+    cfg = d.c()
+    rc = oracle().orc_window_gradients(kern.address, C.byref(cfg), slot_array(d, weights), ptr(tok, _i64p),
+                                       ptr(tgt, _i64p), len(tok), scale, router_scale, slot_array(d, grads),
+                                       C.byref(loss), C.byref(rl))
+    if rc != 0:
+        raise ValueError(f"window gradients failed ({rc})")
+    return loss.value, rl.value, grads
+
+
+def logits(kern: Kernels, d: Decoder, weights, tokens) -> np.ndarray:
+    tok = np.ascontiguousarray(tokens, np.int64)
+    out = np.empty((len(tok), d.vocab), np.float32)
+    cfg = d.c()
+    oracle().orc_logits(kern.address, C.byref(cfg), slot_array(d, weights), ptr(tok, _i64p), len(tok), ptr(out))
+    return out
+
+
+def concatenated(grads: dict[str, np.ndarray]) -> np.ndarray:
+    return np.concatenate([grads[name].ravel() for name in tensor_order(grads)])
+
+
+def data_fingerprint(tensors: dict[str, np.ndarray]) -> str:
+    """modelfile.data_fingerprint (modelfile.py:228-235): float32 bytes in tensor order, each padded to 64 bytes."""
+    digest = hashlib.sha256()
+    for name in tensor_order(tensors):
+        data = np.ascontiguousarray(tensors[name], dtype="<f4").tobytes()
+        digest.update(data + b"\0" * (-len(data) % 64))
+    return digest.hexdigest()
+
+
+# ---- training data and schedule (training/data.py, training/optimizer.py) ----
+
+_EPOCH_MIX = 0x9E3779B97F4A7C15
+_MASK64 = (1 << 64) - 1
+
+
+class Random:
+    """xoshiro256** through the oracle (random.hpp)."""
+
+    def __init__(self, seed: int) -> None:
+        self._state = (C.c_uint64 * 4)()
+        oracle().orc_random_init(self._state, C.c_uint64(seed & _MASK64))
+
+    def next_u64(self) -> int:
+        return oracle().orc_random_next(self._state)
+
+
+def windows_from_documents(documents, encode, sequence_length, separator):
+    """TrainingData.from_documents (data.py:105-124)."""
+    stream = []
+    for document in documents:
+        stream.extend(encode(document))
+        if separator is not None:
+            stream.append(separator)
+    windows = []
+    for start in range(0, max(len(stream) - 1, 0), sequence_length):
+        window = tuple(stream[start:start + sequence_length + 1])
+        if len(window) >= 2:
+            windows.append(window)
+    return windows
+
+
+def epoch_order(count: int, seed: int, epoch: int) -> list[int]:
+    """data.py:38-45: Fisher-Yates driven by Random((seed + (epoch + 1) * mix) mod 2^64)."""
+    random = Random((seed + (epoch + 1) * _EPOCH_MIX) & _MASK64)
+    order = list(range(count))
+    for i in range(len(order) - 1, 0, -1):
+        j = random.next_u64() % (i + 1)
+        order[i], order[j] = order[j], order[i]
+    return order
+
+
+def batch_indices(count: int, step: int, batch_size: int, seed: int) -> list[int]:
+    """data.py:48-57."""
+    orders: dict[int, list[int]] = {}
+    result = []
+    for sample in range(step * batch_size, (step + 1) * batch_size):
+        epoch, index = divmod(sample, count)
+        if epoch not in orders:
+            orders[epoch] = epoch_order(count, seed, epoch)
+        result.append(orders[epoch][index])
+    return result
+
+
+@dataclass(frozen=True)
+class AdamWConfig:
+    learning_rate: float = 1e-4
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    weight_decay: float = 0.01
+    max_grad_norm: float = 1.0
+    warmup_steps: int = 0
+    schedule: str = "cosine"
+    min_learning_rate: float = 0.0
+
+    def learning_rate_at(self, step: int, total_steps: int) -> float:
+        """optimizer.py:48-56 with the portable cosine."""
+        if self.warmup_steps and step <= self.warmup_steps:
+            return self.learning_rate * step / self.warmup_steps
+        if self.schedule == "constant" or total_steps <= self.warmup_steps:
+            return self.learning_rate
+        progress = (step - self.warmup_steps) / (total_steps - self.warmup_steps)
+        span = self.learning_rate - self.min_learning_rate
+        return self.min_learning_rate + 0.5 * span * (1.0 + oracle().orc_cos(math.pi * progress))
+
+
+def train_step(kern: Kernels, d: Decoder, params, m, v, windows, opt: AdamWConfig, step: int, total_steps: int,
+               router_aux_loss: float = 0.0):
+    """One FineTuner.train_step (trainer.py:290-335) through the oracle: updates params, m, v in place and returns
+    (loss, learning rate, gradient norm, summed gradients)."""
+    names = tensor_order(d.tensor_shapes())
+    grads = {name: np.empty(d.tensor_shapes()[name], np.float32) for name in names}
+    order = np.array([d.slot_of(n) for n in names], np.int64)
+    flat = np.array([t for w in windows for t in w], np.int64)
+    lengths = np.array([len(w) for w in windows], np.int64)
+    offsets = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
+    lr = opt.learning_rate_at(step, total_steps)
+    cfg = d.c()
+    adam = OrcAdamW(lr, opt.beta1, opt.beta2, opt.eps, opt.weight_decay, opt.max_grad_norm, router_aux_loss, step)
+    loss, norm = C.c_double(), C.c_double()
+    rc = oracle().orc_train_step(kern.address, C.byref(cfg), slot_array(d, params), slot_array(d, m),
+                                 slot_array(d, v), slot_array(d, grads), ptr(order, _i64p), len(order),
+                                 ptr(flat, _i64p), ptr(offsets, _i64p), ptr(lengths, _i64p), len(windows),
+                                 C.byref(adam), C.byref(loss), C.byref(norm))
+    if rc != 0:
+        raise ValueError(f"train step failed ({rc})")
+    return loss.value, lr, norm.value, grads
+
+
+def with_family(d: Decoder, **changes) -> Decoder:
+    return replace(d, **changes)

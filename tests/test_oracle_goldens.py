@@ -1,0 +1,71 @@
+"""The oracle against the reference's own golden values (tests/golden/reference_goldens.json, extracted from the
+reference's tests/golden_values.py): random generator, forward kernel fingerprints, the gradient fingerprints of the
+tiny fixture models and the 6-step fine-tuning fingerprints. These pin the C restatement of kernels and
+orchestration end to end."""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_goldens.json").read_text())
+TOKENS = [1, 17, 42, 5, 63, 0, 9, 9, 30]  # reference tests/test_training.py:32
+TARGETS = [*TOKENS[1:], 2]  # reference tests/test_training.py:50
+
+
+def test_random_generator_matches_the_reference_goldens():
+    r = O.Random(42)
+    assert r.next_u64() == GOLDEN["RANDOM_FIRST"]
+    assert r.next_u64() == GOLDEN["RANDOM_SECOND"]
+
+
+def test_forward_kernel_fingerprints():
+    """reference tests/test_kernels.py:331-350 for the kernels the training forward pass uses."""
+    k = O.oracle_kernels()
+    x, w = O.gaussian(20, 8, 64), O.gaussian(21, 48, 64)
+    q, kk, v = O.gaussian(22, 8, 4, 16), O.gaussian(23, 8, 2, 16), O.gaussian(24, 8, 2, 16)
+    outputs = {
+        "linear": k.linear(x, w, O.gaussian(25, 48)),
+        "rms_norm": k.rms_norm(x, O.gaussian(26, 64), 1e-6),
+        "silu": k.silu(x),
+        "rope": k.rope(q, np.arange(8, dtype=np.int64) * 97, O.rope_inv_freq(16, 10000.0)),
+        "attention": k.attention(q, kk, v, 1.0 / np.sqrt(16.0)),
+    }
+    for name, values in outputs.items():
+        assert O.tensor_fingerprint(values) == GOLDEN["KERNEL_FINGERPRINTS"][name], name
+
+
+@pytest.mark.parametrize("family", sorted(O.FIXTURES))
+def test_gradient_fingerprint(family):
+    d = O.FIXTURES[family]
+    _, _, grads = O.window_gradients(O.oracle_kernels(), d, O.fixture_weights(d), TOKENS, TARGETS)
+    assert O.fingerprint(O.concatenated(grads)) == GOLDEN["GRADIENT_FINGERPRINT"][family]
+
+
+def ascii_windows():
+    """reference tests/test_training.py:310-312 (ascii_data, sequence length 8)."""
+    documents = ["the quick brown fox jumps over the lazy dog", "pack my box with five dozen liquor jugs"]
+    return O.windows_from_documents(documents, lambda text: [ord(c) % 64 for c in text], 8, 2)
+
+
+@pytest.mark.parametrize("family", sorted(O.FIXTURES))
+def test_finetune_fingerprint(family):
+    """RUN = 6 steps, batch 3, sequence 8, seed 3, lr 1e-2, cosine (reference tests/test_training.py:357)."""
+    d = O.FIXTURES[family]
+    windows = ascii_windows()
+    params = {n: a.copy() for n, a in O.fixture_weights(d).items()}
+    m = {n: np.zeros_like(a) for n, a in params.items()}
+    v = {n: np.zeros_like(a) for n, a in params.items()}
+    opt = O.AdamWConfig(learning_rate=1e-2)
+    losses = []
+    for step in range(6):
+        batch = [windows[i] for i in O.batch_indices(len(windows), step, 3, 3)]
+        loss, _, _, _ = O.train_step(O.oracle_kernels(), d, params, m, v, batch, opt, step + 1, 6)
+        losses.append(loss)
+    assert O.data_fingerprint(params) == GOLDEN["FINETUNE_FINGERPRINT"][family]
+    assert losses[-1] < losses[0]

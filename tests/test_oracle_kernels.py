@@ -1,0 +1,268 @@
+"""Per-kernel pins of the oracle: bit equality with the reference's own kernels (oracle/_ref, built from the reference
+headers; skipped where that prebuilt library is absent), and closed forms / invariants that a dropped term, a wrong
+sign or a transposed operand would break (the reference's float64 yardsticks, tests/test_training.py:78-229)."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+needs_ref = pytest.mark.skipif(not O.reference_available(), reason="oracle/_ref not built (no reference checkout)")
+
+
+def adversarial(seed: int, *shape: int) -> np.ndarray:
+    """Values spanning 1e-30 .. 1e20 with both signs and exact zeros (reference test_batch_invariance.py:68-78)."""
+    values = O.gaussian(seed, *shape).astype(np.float64)
+    exponents = O.gaussian(seed + 1000, *shape).astype(np.float64)
+    out = values * np.power(10.0, np.clip(np.round(exponents * 8), -30, 20))
+    out[np.abs(O.gaussian(seed + 2000, *shape)) < 0.05] = 0.0
+    return out.astype(np.float32)
+
+
+def same(a, b) -> bool:
+    return np.asarray(a).tobytes() == np.asarray(b).tobytes()
+
+
+@needs_ref
+def test_math_matches_reference():
+    o, r = O.oracle(), O.ref()
+    xs = np.concatenate([O.gaussian(1, 4000).astype(np.float64) * 30, np.linspace(-800, 800, 3001),
+                         [0.0, -0.0, 1e-300, 5e-324, 709.7, 709.79, -745.1, -745.3, 1e6, 3e7, np.inf, -np.inf]])
+    for name in ("exp", "log", "sin", "cos", "tanh", "sigmoid"):
+        for x in xs:
+            a, b = getattr(o, "orc_" + name)(float(x)), getattr(r, "ref_" + name)(float(x))
+            assert (math.isnan(a) and math.isnan(b)) or np.float64(a).tobytes() == np.float64(b).tobytes(), (name, x)
+
+
+@needs_ref
+@pytest.mark.parametrize("rows", [1, 7, 33])
+def test_linear_and_backward_match_reference(rows):
+    o, r = O.oracle_kernels(), O.ref_kernels()
+    x, w, b, dy = adversarial(1, rows, 37), adversarial(2, 19, 37), adversarial(3, 19), adversarial(4, rows, 19)
+    assert same(o.linear(x, w, b), r.linear(x, w, b))
+    for a, c in zip(o.linear_backward(x, w, dy, True), r.linear_backward(x, w, dy, True)):
+        assert same(a, c)
+
+
+@needs_ref
+def test_row_kernels_match_reference():
+    o, r = O.oracle_kernels(), O.ref_kernels()
+    x, w, dy = O.gaussian(5, 9, 48, scale=3.0), O.gaussian(6, 48), O.gaussian(7, 9, 48)
+    assert same(o.rms_norm(x, w, 1e-5), r.rms_norm(x, w, 1e-5))
+    assert same(o.rms_norm(x, w, 1e-6, True), r.rms_norm(x, w, 1e-6, True))
+    for a, c in zip(o.rms_norm_backward(x, w, dy, 1e-5), r.rms_norm_backward(x, w, dy, 1e-5)):
+        assert same(a, c)
+    g, up = O.gaussian(8, 500, scale=6.0), O.gaussian(11, 500)
+    assert same(o.silu(g), r.silu(g))
+    assert same(o.swiglu(g, up), r.swiglu(g, up))
+    assert same(o.silu_backward(g, up), r.silu_backward(g, up))
+    q = O.gaussian(9, 11, 3, 16)
+    pos = np.arange(11, dtype=np.int64) * 131
+    for inv in (O.rope_inv_freq(16, 1e6), O.rope_inv_freq(8, 1e4)):
+        for interleaved in (False, True):
+            for inverse in (False, True):
+                assert same(o.rope(q, pos, inv, interleaved, inverse), r.rope(q, pos, inv, interleaved, inverse))
+
+
+@needs_ref
+@pytest.mark.parametrize(("q_len", "kv_len", "window", "softcap", "offset"),
+                         [(9, 9, 0, 0.0, 0), (5, 9, 0, 0.0, 4), (9, 9, 3, 0.0, 0), (9, 9, 0, 0.7, 0)])
+def test_attention_matches_reference(q_len, kv_len, window, softcap, offset):
+    o, r = O.oracle_kernels(), O.ref_kernels()
+    q, k, v = O.gaussian(12, q_len, 6, 8), O.gaussian(13, kv_len, 2, 8), O.gaussian(14, kv_len, 2, 8)
+    dout = O.gaussian(15, q_len, 6, 8)
+    args = (0.35, True, offset, window, softcap)
+    assert same(o.attention(q, k, v, *args), r.attention(q, k, v, *args))
+    for a, c in zip(o.attention_backward(q, k, v, dout, *args), r.attention_backward(q, k, v, dout, *args)):
+        assert same(a, c)
+
+
+@needs_ref
+def test_loss_embedding_optimizer_and_routing_match_reference():
+    o, r = O.oracle_kernels(), O.ref_kernels()
+    logits = O.gaussian(16, 6, 301, scale=4.0)
+    targets = np.array([3, -1, 300, 0, 17, 17], np.int64)
+    (la, da), (lb, db) = o.cross_entropy(logits, targets, 0.25), r.cross_entropy(logits, targets, 0.25)
+    assert la == lb and same(da, db)
+    dy, tokens = O.gaussian(17, 12, 5), np.array([3, 1, 3, 0, 3, 1, 9, 9, 9, 2, 0, 3], np.int64)
+    assert same(o.embedding_backward(dy, tokens, 10), r.embedding_backward(dy, tokens, 10))
+    g = adversarial(18, 1000)
+    assert o.sum_squares(g) == r.sum_squares(g)
+    p, grad = O.gaussian(18, 300), O.gaussian(19, 300)
+    m, v = O.gaussian(20, 300, scale=0.1), np.abs(O.gaussian(21, 300, scale=0.1))
+    pa, ma, va = p.copy(), m.copy(), v.copy()
+    pb, mb, vb = p.copy(), m.copy(), v.copy()
+    o.adamw_step(pa, grad, ma, va, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1 - 0.9**3, 1 - 0.999**3, 0.5)
+    r.adamw_step(pb, grad, mb, vb, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1 - 0.9**3, 1 - 0.999**3, 0.5)
+    assert same(pa, pb) and same(ma, mb) and same(va, vb)
+    rl = O.gaussian(22, 20, 8, scale=3.0)
+    for normalize in (False, True):
+        ia, wa = o.moe_route(rl, 3, normalize)
+        ib, wb = r.moe_route(rl, 3, normalize)
+        assert same(ia, ib) and same(wa, wb)
+        dw, dp = O.gaussian(23, 20, 3), O.gaussian(24, 20, 8)
+        assert same(o.moe_route_backward(rl, ia, dw, dp, normalize), r.moe_route_backward(rl, ia, dw, dp, normalize))
+        assert same(o.moe_route_backward(rl, ia, dw, None, normalize),
+                    r.moe_route_backward(rl, ia, dw, None, normalize))
+    assert same(o.column_mean(rl), r.column_mean(rl))
+    assert same(o.softmax(rl[0].copy()), r.softmax(rl[0].copy()))
+
+
+# ---- closed forms and invariants (no reference needed) ----
+
+def close(ours, reference, tolerance=1e-5):
+    reference = np.asarray(reference, dtype=np.float64)
+    scale = max(1.0, float(np.abs(reference).max()))
+    np.testing.assert_allclose(np.asarray(ours, np.float64), reference, rtol=0, atol=tolerance * scale)
+
+
+def test_math_special_values_and_accuracy():
+    o = O.oracle()
+    assert o.orc_exp(0.0) == 1.0 and o.orc_log(1.0) == 0.0 and o.orc_sin(0.0) == 0.0 and o.orc_cos(0.0) == 1.0
+    assert o.orc_exp(-800.0) == 0.0 and o.orc_exp(800.0) == math.inf and math.isnan(o.orc_log(-1.0))
+    xs = np.linspace(-50, 50, 2001)
+    assert max(abs(o.orc_exp(x) / math.exp(x) - 1) for x in xs) < 1e-14
+    assert max(abs(o.orc_log(math.exp(x)) - x) for x in xs) < 1e-13
+    assert max(abs(o.orc_sin(x) - math.sin(x)) for x in xs) < 1e-14
+    assert max(abs(o.orc_cos(x) - math.cos(x)) for x in xs) < 1e-14
+    assert max(abs(o.orc_tanh(x) - math.tanh(x)) for x in xs) < 1e-15
+    assert all(o.orc_tanh(-x) == -o.orc_tanh(x) for x in xs)
+
+
+def test_linear_backward_matches_float64():
+    k = O.oracle_kernels()
+    x, w, dy = O.gaussian(1, 5, 7), O.gaussian(2, 3, 7), O.gaussian(4, 5, 3)
+    dx, dw, db = k.linear_backward(x, w, dy, True)
+    x64, w64, dy64 = (a.astype(np.float64) for a in (x, w, dy))
+    close(dx, dy64 @ w64)
+    close(dw, dy64.T @ x64)
+    close(db, dy64.sum(0))
+    assert same(k.linear_backward(x[2:3].copy(), w, dy[2:3].copy())[0], dx[2:3])
+
+
+def numeric_gradient(f, x, eps=1e-6):
+    grad = np.zeros_like(x, dtype=np.float64)
+    for index in np.ndindex(x.shape):
+        plus, minus = x.astype(np.float64), x.astype(np.float64)
+        plus[index] += eps
+        minus[index] -= eps
+        grad[index] = (f(plus) - f(minus)) / (2 * eps)
+    return grad
+
+
+def test_rms_norm_backward_matches_numeric_gradient():
+    k = O.oracle_kernels()
+    x, w, dy = O.gaussian(5, 3, 8), O.gaussian(6, 8), O.gaussian(7, 3, 8)
+    eps = 1e-5
+    dx, dw = k.rms_norm_backward(x, w, dy, eps)
+
+    def forward(xv, wv):
+        return xv / np.sqrt(np.mean(xv * xv, -1, keepdims=True) + eps) * wv
+
+    close(dx, numeric_gradient(lambda a: float((forward(a, w) * dy).sum()), x), 1e-6)
+    close(dw, numeric_gradient(lambda a: float((forward(x.astype(np.float64), a) * dy).sum()), w), 1e-6)
+
+
+def test_silu_backward_matches_numeric_gradient():
+    k = O.oracle_kernels()
+    x, dy = O.gaussian(8, 20, scale=4.0), O.gaussian(9, 20)
+    reference = numeric_gradient(lambda a: float((a / (1 + np.exp(-a)) * dy).sum()), x)
+    close(k.silu_backward(x, dy), reference, 1e-7)
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope_inverse_is_the_transpose(interleaved):
+    k = O.oracle_kernels()
+    x, dy = O.gaussian(10, 5, 2, 8), O.gaussian(11, 5, 2, 8)
+    positions, inv = np.arange(3, 8, dtype=np.int64), O.rope_inv_freq(8, 10000.0)
+    rotated = k.rope(x, positions, inv, interleaved).astype(np.float64)
+    back = k.rope(dy, positions, inv, interleaved, True).astype(np.float64)
+    assert abs((rotated * dy).sum() - (x.astype(np.float64) * back).sum()) < 1e-5
+    close(k.rope(rotated.astype(np.float32), positions, inv, interleaved, True), x, 1e-6)
+
+
+def reference_attention(q, k, v, scale, window=None):
+    q_len, heads, _ = q.shape
+    group = heads // k.shape[1]
+    out = np.zeros((q_len, heads, v.shape[2]))
+    offset = k.shape[0] - q_len
+    for h in range(heads):
+        scores = q[:, h] @ k[:, h // group].T * scale
+        scores = scores + np.triu(np.full(scores.shape, -np.inf), offset + 1)
+        if window is not None:
+            scores = scores + np.tril(np.full(scores.shape, -np.inf), offset - window)
+        p = np.exp(scores - scores.max(-1, keepdims=True))
+        out[:, h] = (p / p.sum(-1, keepdims=True)) @ v[:, h // group]
+    return out
+
+
+@pytest.mark.parametrize(("q_len", "window"), [(4, None), (2, None), (4, 2)])
+def test_attention_backward_matches_numeric_gradient(q_len, window):
+    kern = O.oracle_kernels()
+    q, k, v = O.gaussian(12, q_len, 4, 6), O.gaussian(13, 4, 2, 6), O.gaussian(14, 4, 2, 6)
+    dout = O.gaussian(15, q_len, 4, 6)
+    scale = 1 / np.sqrt(6)
+    dq, dk, dv = kern.attention_backward(q, k, v, dout, scale, True, 4 - q_len, window or 0)
+    q64, k64, v64 = (a.astype(np.float64) for a in (q, k, v))
+
+    def loss(a, b, c):
+        return float((reference_attention(a, b, c, scale, window) * dout).sum())
+
+    close(dq, numeric_gradient(lambda a: loss(a, k64, v64), q), 1e-6)
+    close(dk, numeric_gradient(lambda a: loss(q64, a, v64), k), 1e-6)
+    close(dv, numeric_gradient(lambda a: loss(q64, k64, a), v), 1e-6)
+    close(kern.attention(q, k, v, scale, True, 4 - q_len, window or 0), reference_attention(q64, k64, v64, scale,
+                                                                                           window), 1e-6)
+
+
+def test_cross_entropy_matches_float64():
+    k = O.oracle_kernels()
+    logits = O.gaussian(16, 4, 11, scale=3.0)
+    targets = np.array([3, -1, 10, 0], np.int64)
+    loss, dlogits = k.cross_entropy(logits, targets, 0.25)
+    l64 = logits.astype(np.float64)
+    lse = np.log(np.exp(l64 - l64.max(1, keepdims=True)).sum(1)) + l64.max(1)
+    kept = targets >= 0
+    assert abs(loss - float((lse - l64[np.arange(4), targets])[kept].sum())) < 1e-12
+    probs = np.exp(l64 - lse[:, None])
+    probs[np.arange(4)[kept], targets[kept]] -= 1
+    probs[~kept] = 0
+    close(dlogits, probs * 0.25, 1e-7)
+
+
+def test_embedding_backward_sums_rows_per_token():
+    k = O.oracle_kernels()
+    dy, tokens = O.gaussian(17, 6, 5), np.array([3, 1, 3, 0, 3, 1], np.int64)
+    expected = np.zeros((4, 5))
+    np.add.at(expected, tokens, dy.astype(np.float64))
+    close(k.embedding_backward(dy, tokens, 4), expected, 1e-7)
+    with pytest.raises(ValueError):
+        k.embedding_backward(dy, np.array([4, 0, 0, 0, 0, 0], np.int64), 4)
+
+
+def test_adamw_step_is_the_documented_formula():
+    """Bitwise against the float64 closed form (reference tests/test_training.py:217-229)."""
+    k = O.oracle_kernels()
+    param, grad = O.gaussian(18, 50), O.gaussian(19, 50)
+    m, v = O.gaussian(20, 50, scale=0.1), np.abs(O.gaussian(21, 50, scale=0.1))
+    p64, g64, m64, v64 = (a.astype(np.float64) for a in (param, grad, m, v))
+    lr, b1, b2, eps, wd, c1, c2, s = 1e-3, 0.9, 0.999, 1e-8, 0.01, 1 - 0.9**3, 1 - 0.999**3, 0.5
+    g = g64 * s
+    m_new = (b1 * m64 + (1 - b1) * g).astype(np.float32)
+    v_new = (b2 * v64 + (1 - b2) * g * g).astype(np.float32)
+    expected = (p64 * (1 - lr * wd) - lr * (m_new / c1) / (np.sqrt(v_new / c2) + eps)).astype(np.float32)
+    param, m, v = param.copy(), m.copy(), v.copy()
+    k.adamw_step(param, grad, m, v, lr, b1, b2, eps, wd, c1, c2, s)
+    assert same(param, expected) and same(m, m_new) and same(v, v_new)
+
+
+def test_sum_squares_is_the_serial_double_chain():
+    g = O.gaussian(30, 5000, scale=3.0)
+    acc = 0.0
+    for value in g.astype(np.float64):
+        acc += value * value
+    assert O.oracle_kernels().sum_squares(g) == acc
