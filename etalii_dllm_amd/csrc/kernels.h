@@ -1,0 +1,137 @@
+// Internal launchers of the HIP kernels (device pointers, explicit sizes, one stream). The C-ABI in capi.hip and the
+// device-resident trainer in trainer.hip are built on these; nothing here allocates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dllm_hip {
+
+// ---- matmuls (gemm.hip) ----
+
+// Rows of the double operand are padded to whole row tiles: lda >= padded_rows(I).
+int64_t padded_rows(int64_t n);
+
+struct GemmCall {
+    const double* A = nullptr;  // [L][lda] doubles, i contiguous
+    int64_t lda = 0;
+    const float* B = nullptr;  // [L][ldb] floats, j contiguous
+    int64_t ldb = 0;
+    float* C = nullptr;  // [I][ldc]
+    int64_t ldc = 0;
+    int64_t I = 0, J = 0;
+    int64_t l0 = 0, l1 = 0;            // plain mode: reduce over l in [l0, l1)
+    const int64_t* seg = nullptr;      // segmented mode (device): nseg + 1 offsets; C = window-ordered float sum
+    int nseg = 1;
+    const float* bias = nullptr;       // plain: + bias[j] in double before rounding
+    const float* addsrc = nullptr;     // plain: C = addsrc[i][j] + f32(sum) (may alias C)
+    int64_t ld_add = 0;
+    const float* seg_addend = nullptr; // segmented: per-window addend rows
+    const int* seg_addrow = nullptr;   // [nseg][I] rows into seg_addend, -1 for none
+    int64_t ld_seg_add = 0;
+};
+
+int launch_gemm(const GemmCall& g, hipStream_t stream);
+
+// dst[r][c] = src[r][c] and dstT[c][r] = src[r][c] as doubles (either may be null).
+int launch_to_double(const float* src, int64_t rows, int64_t cols, int64_t lds, double* dst, int64_t ldd,
+                     double* dstT, int64_t lddT, hipStream_t stream);
+int launch_transpose_f32(const float* src, int64_t rows, int64_t cols, float* dst, hipStream_t stream);
+
+// ---- row-local and elementwise kernels (rows.hip) ----
+
+// rms_norm (nn.hpp:391-408); inv_rms (optional, double per row) records 1/sqrt(mean(x^2)+eps).
+int launch_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t dim, double eps, int unit_offset,
+                    double* inv_rms, hipStream_t stream);
+// rms_norm_backward's dx (grad.hpp:79-105): dx = addend + dx_norm when addend is given (the residual glue); writes
+// inv_rms per row for the weight gradient.
+int launch_rms_norm_backward_dx(const float* x, const float* w, const float* dy, float* dx, const float* addend,
+                                int64_t rows, int64_t dim, double eps, int unit_offset, double* inv_rms,
+                                hipStream_t stream);
+// Column sums over segments of rows with a float sum over segments (rms_norm dw, linear db):
+//   part[s][i] = f32(sum over rows r of segment s, ascending, of term(r, i))   then out[i] = window-ordered sum.
+// kind 0: term = dy[r][i] (bias); kind 1: term = (dy[r][i] x[r][i]) inv_rms[r] (norm weight).
+int launch_column_sums(int kind, const float* dy, const float* x, const double* inv_rms, int64_t dim,
+                       const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream);
+// rope (nn.hpp:501-530) with precomputed cos/sin tables [positions][half] (double, sin already negated for inverse).
+int launch_rope_tables(const int64_t* positions, int64_t n, const double* inv_freq, int64_t half, double* cos_table,
+                       double* sin_table, hipStream_t stream);
+int launch_rope(const float* x, const int64_t* pos_index, const double* cos_table, const double* sin_table,
+                float* out, int64_t tokens, int64_t heads, int64_t head_dim, int64_t rotary_dim, int interleaved,
+                int inverse, hipStream_t stream);
+int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream);
+// gate_act = silu(gate) (saved), product = gate_act * up (nn.hpp:489-492 and backprop.py:492-499).
+int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
+                          hipStream_t stream);
+int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
+// _swiglu_backward's elementwise glue (backprop.py:301-303): dgate = silu_backward(gate, dproduct * up),
+// dup = dproduct * gate_act.
+int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
+                           float* dgate, float* dup, int64_t n, hipStream_t stream);
+int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream);
+int launch_gather_rows(const float* table, const int64_t* index, float* out, int64_t rows, int64_t dim,
+                       hipStream_t stream);
+
+// ---- attention (attention.hip) ----
+
+struct AttentionShape {
+    int64_t q_len, kv_len;  // packed totals over all sequences
+    int64_t q_heads, kv_heads, head_dim, value_dim;
+    double scale;
+    int causal;
+    int64_t q_offset, window;
+    double softcap;
+};
+
+// Segments: `count` independent sequences; sequence s has queries [q_off[s], q_off[s] + q_len[s]) and keys
+// [kv_off[s], ...) of the packed tensors (device arrays). A plain call is one sequence.
+struct AttentionBatch {
+    const int64_t* q_start;   // device [count]
+    const int64_t* q_len;     // device [count]
+    const int64_t* kv_start;  // device [count]
+    const int64_t* kv_len;    // device [count]
+    int count;
+    int64_t max_q, max_kv;    // host bounds of the lengths
+};
+
+int launch_attention(const float* q, const float* k, const float* v, float* out, const AttentionShape& s,
+                     const AttentionBatch& b, hipStream_t stream);
+// Workspace bytes of attention_backward: row statistics plus the probabilities and score gradients.
+size_t attention_backward_workspace(const AttentionShape& s, const AttentionBatch& b, int64_t total_q);
+int launch_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,
+                              float* dv, const AttentionShape& s, const AttentionBatch& b, int64_t total_q,
+                              int64_t total_kv, void* workspace, hipStream_t stream);
+
+// ---- loss and embedding (loss.hip) ----
+
+// cross_entropy (grad.hpp:395-426) over segments: per row the dlogits, and the summed loss of each segment
+// (rows ascending, double) into loss_out[s] (seg_dev: nseg + 1 row offsets in device memory). row_max, row_total,
+// row_loss: workspace of rows doubles each. error_flag is set to 1 when a target is >= vocab.
+int launch_cross_entropy(const float* logits, const int64_t* targets, float* dlogits, int64_t rows, int64_t vocab,
+                         double scale, const int64_t* seg_dev, int nseg, double* row_max, double* row_total,
+                         double* row_loss, double* loss_out, int* error_flag, hipStream_t stream);
+// out[v] = sum over rows with tokens == v, in row order (grad.hpp:431-464), from a host-built grouping:
+// group g covers order[start[g] .. start[g+1]) and writes row out_row[g].
+int launch_embedding_groups(const float* dy, int64_t dim, const int64_t* order, const int64_t* start,
+                            const int64_t* out_row, int64_t groups, float* out, int64_t ld_out, hipStream_t stream);
+
+// ---- optimizer (optim.hip) ----
+
+// Serial sum of squares of each tensor (grad.hpp:467-473), tensors given by device arrays of (offset, count) into
+// one arena; then the total over tensors in table order, its square root and the clipping scale
+// (optimizer.py:66-90), all in double on the device: stats = {total, norm, clip}.
+int launch_global_norm(const float* arena, const int64_t* offsets, const int64_t* counts, int64_t tensors,
+                       double* per_tensor, double max_grad_norm, double* stats, hipStream_t stream);
+int launch_sum_squares(const float* values, int64_t n, double* result, hipStream_t stream);
+// adamw_step (grad.hpp:481-495) over an arena; chunk table: chunk c covers [chunk_start[c], chunk_end[c]) with
+// weight decay chunk_decay[c]; grad_scale read from device memory (the clip factor) when grad_scale_dev != null.
+struct AdamWArgs {
+    double lr, beta1, beta2, eps, bc1, bc2, grad_scale;
+};
+int launch_adamw_plain(float* param, const float* grad, float* m, float* v, int64_t n, double weight_decay,
+                       const AdamWArgs& a, hipStream_t stream);
+int launch_adamw(float* param, const float* grad, float* m, float* v, const int64_t* chunk_start,
+                 const int64_t* chunk_end, const double* chunk_decay, int64_t chunks, const AdamWArgs& a,
+                 const double* grad_scale_dev, hipStream_t stream);
+
+}  // namespace dllm_hip

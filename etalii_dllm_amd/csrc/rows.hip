@@ -1,0 +1,323 @@
+// Row-local and elementwise kernels of the step: RMSNorm forward and backward, the column sums behind the norm weight
+// and bias gradients, RoPE, SiLU/SwiGLU and their gradients, and the float32 glue between them.
+//
+// Reductions that the reference runs as one serial double chain per row (sum of squares, the backward dot) are run
+// by lane 0 of the row's wave, in index order, after the other lanes are done loading; the per-element work around
+// them is spread over the 64 lanes. Every float32 glue operation is one IEEE float op per element, in the
+// reference's operand order.
+#include "common.h"
+#include "devmath.h"
+#include "kernels.h"
+
+namespace dllm_hip {
+
+namespace {
+
+constexpr int kRowWaves = 4;  // rows (waves) per 256-thread block
+
+__device__ __forceinline__ double bcast0(double v) { return __shfl(v, 0, 64); }
+
+// sum over i ascending of x[i]^2 in double (nn.hpp:395-398), on the calling lane.
+__device__ __forceinline__ double serial_sum_squares(const float* __restrict__ x, int64_t dim) {
+    double s = 0.0;
+    int64_t i = 0;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        for (; i + 4 <= dim; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(x + i);
+            s += static_cast<double>(v.x) * static_cast<double>(v.x);
+            s += static_cast<double>(v.y) * static_cast<double>(v.y);
+            s += static_cast<double>(v.z) * static_cast<double>(v.z);
+            s += static_cast<double>(v.w) * static_cast<double>(v.w);
+        }
+    }
+    for (; i < dim; ++i) s += static_cast<double>(x[i]) * static_cast<double>(x[i]);
+    return s;
+}
+
+// The forward scale (nn.hpp:401-404): w, or 1 + w with the unit offset.
+__device__ __forceinline__ double norm_scale(const float* w, int64_t i, int unit_offset) {
+    if (w == nullptr) return 1.0;
+    return unit_offset ? 1.0 + static_cast<double>(w[i]) : static_cast<double>(w[i]);
+}
+
+// The backward scale (grad.hpp:81,93): offset + w with offset 0 or 1 (so a -0.0 weight reads as +0.0, as there).
+__device__ __forceinline__ double norm_scale_backward(const float* w, int64_t i, int unit_offset) {
+    if (w == nullptr) return 1.0;
+    return (unit_offset ? 1.0 : 0.0) + static_cast<double>(w[i]);
+}
+
+// rms_norm (nn.hpp:391-408): out = f32((x inv) scale), inv = 1 / sqrt(sum x^2 / dim + eps).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                       float* __restrict__ out, int64_t rows, int64_t dim, double eps,
+                                                       int unit_offset, double* __restrict__ inv_out) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + row * dim;
+    double inv = 0.0;
+    if (lane == 0) inv = 1.0 / sqrt(serial_sum_squares(xr, dim) / static_cast<double>(dim) + eps);
+    inv = bcast0(inv);
+    for (int64_t i = lane; i < dim; i += 64)
+        out[row * dim + i] = static_cast<float>(static_cast<double>(xr[i]) * inv * norm_scale(w, i, unit_offset));
+    if (inv_out && lane == 0) inv_out[row] = inv;
+}
+
+// rms_norm_backward's dx (grad.hpp:83-104): per row the same inv, D = sum_i ((g_i dy_i) x_i) ascending,
+// coef = D inv inv inv / dim, dx = f32((inv g) dy - x coef); then out = addend + dx when addend is given.
+__global__ __launch_bounds__(256) void rms_norm_backward_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                                const float* __restrict__ dy, float* __restrict__ dx,
+                                                                const float* __restrict__ addend, int64_t rows,
+                                                                int64_t dim, double eps, int unit_offset,
+                                                                double* __restrict__ inv_out) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + row * dim;
+    const float* dyr = dy + row * dim;
+    double inv = 0.0, coef = 0.0;
+    if (lane == 0) {
+        inv = 1.0 / sqrt(serial_sum_squares(xr, dim) / static_cast<double>(dim) + eps);
+        double d = 0.0;
+        for (int64_t i = 0; i < dim; ++i)
+            d += norm_scale_backward(w, i, unit_offset) * static_cast<double>(dyr[i]) * static_cast<double>(xr[i]);
+        coef = d * inv * inv * inv / static_cast<double>(dim);
+    }
+    inv = bcast0(inv);
+    coef = bcast0(coef);
+    for (int64_t i = lane; i < dim; i += 64) {
+        const double g = norm_scale_backward(w, i, unit_offset);
+        float v = static_cast<float>(inv * g * static_cast<double>(dyr[i]) - static_cast<double>(xr[i]) * coef);
+        if (addend) v = addend[row * dim + i] + v;
+        dx[row * dim + i] = v;
+    }
+    if (inv_out && lane == 0) inv_out[row] = inv;
+}
+
+// part[s][i] = f32(sum over rows of segment s ascending of term(r, i)): kind 0 term = dy (db, grad.hpp:52-54),
+// kind 1 term = (dy x) inv_rms[r] (norm weight, grad.hpp:95).
+__global__ __launch_bounds__(256) void column_partial_kernel(int kind, const float* __restrict__ dy,
+                                                             const float* __restrict__ x,
+                                                             const double* __restrict__ inv, int64_t dim, int64_t r0,
+                                                             int64_t r1, float* __restrict__ part) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= dim) return;
+    double acc = 0.0;
+    if (kind == 0) {
+        for (int64_t r = r0; r < r1; ++r) acc += static_cast<double>(dy[r * dim + i]);
+    } else {
+        for (int64_t r = r0; r < r1; ++r)
+            acc += static_cast<double>(dy[r * dim + i]) * static_cast<double>(x[r * dim + i]) * inv[r];
+    }
+    part[i] = static_cast<float>(acc);
+}
+
+// out[i] = part[0][i] + part[1][i] + ... in float, segment order (trainer.py:328-332: the first copied).
+__global__ __launch_bounds__(256) void segment_float_sum_kernel(const float* __restrict__ part, int64_t dim, int nseg,
+                                                                float* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= dim) return;
+    float t = part[i];
+    for (int s = 1; s < nseg; ++s) t = t + part[static_cast<int64_t>(s) * dim + i];
+    out[i] = t;
+}
+
+// cos and sin of positions[t] * inv_freq[i] with the portable sin/cos (nn.hpp:508-513).
+__global__ __launch_bounds__(256) void rope_table_kernel(const int64_t* __restrict__ positions, int64_t n,
+                                                         const double* __restrict__ inv_freq, int64_t half,
+                                                         double* __restrict__ ct, double* __restrict__ st) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= n * half) return;
+    const int64_t t = idx / half, i = idx % half;
+    const double pos = positions ? static_cast<double>(positions[t]) : static_cast<double>(t);
+    const double angle = pos * inv_freq[i];
+    ct[idx] = dcos(angle);
+    st[idx] = dsin(angle);
+}
+
+// rope (nn.hpp:515-527); inverse negates the sine exactly.
+__global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, const int64_t* __restrict__ pos_index,
+                                                   const double* __restrict__ ct, const double* __restrict__ st,
+                                                   float* __restrict__ out, int64_t tokens, int64_t heads,
+                                                   int64_t head_dim, int64_t rotary_dim, int interleaved, int inverse) {
+    const int64_t half = rotary_dim / 2;
+    const int64_t per_head = half + (head_dim - rotary_dim);
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= tokens * heads * per_head) return;
+    const int64_t t = idx / (heads * per_head);
+    const int64_t rem = idx % (heads * per_head);
+    const int64_t h = rem / per_head, k = rem % per_head;
+    const float* xh = x + (t * heads + h) * head_dim;
+    float* oh = out + (t * heads + h) * head_dim;
+    if (k >= half) {
+        const int64_t i = rotary_dim + (k - half);
+        oh[i] = xh[i];
+        return;
+    }
+    const int64_t row = pos_index ? pos_index[t] : t;
+    const double c = ct[row * half + k];
+    const double s = inverse ? -st[row * half + k] : st[row * half + k];
+    const int64_t i0 = interleaved ? 2 * k : k;
+    const int64_t i1 = interleaved ? 2 * k + 1 : k + half;
+    const double a = xh[i0];
+    const double b = xh[i1];
+    oh[i0] = static_cast<float>(a * c - b * s);
+    oh[i1] = static_cast<float>(a * s + b * c);
+}
+
+__global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        out[i] = dsilu(x[i]);
+}
+
+__global__ __launch_bounds__(256) void swiglu_forward_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                             float* __restrict__ gate_act, float* __restrict__ product,
+                                                             int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const float a = dsilu(gate[i]);
+        if (gate_act) gate_act[i] = a;
+        product[i] = a * up[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void silu_backward_kernel(const float* __restrict__ x, const float* __restrict__ dy,
+                                                            float* __restrict__ out, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        out[i] = dsilu_backward(x[i], dy[i]);
+}
+
+__global__ __launch_bounds__(256) void swiglu_backward_kernel(const float* __restrict__ gate,
+                                                              const float* __restrict__ up,
+                                                              const float* __restrict__ gate_act,
+                                                              const float* __restrict__ dproduct,
+                                                              float* __restrict__ dgate, float* __restrict__ dup,
+                                                              int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const float dp = dproduct[i];
+        dgate[i] = dsilu_backward(gate[i], dp * up[i]);
+        dup[i] = dp * gate_act[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                  float* __restrict__ out, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        out[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restrict__ table,
+                                                          const int64_t* __restrict__ index, float* __restrict__ out,
+                                                          int64_t rows, int64_t dim) {
+    const int64_t r = blockIdx.x;
+    if (r >= rows) return;
+    const float* src = table + index[r] * dim;
+    for (int64_t i = threadIdx.x; i < dim; i += 256) out[r * dim + i] = src[i];
+}
+
+unsigned elementwise_grid(int64_t n) {
+    const int64_t blocks = (n + 255) / 256;
+    return static_cast<unsigned>(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
+}
+
+}  // namespace
+
+int launch_rms_norm(const float* x, const float* w, float* out, int64_t rows, int64_t dim, double eps, int unit_offset,
+                    double* inv_rms, hipStream_t stream) {
+    if (rows == 0) return kOk;
+    DLLM_REQUIRE(dim > 0, "rms_norm needs a non-empty last dimension");
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(ceil_div(rows, kRowWaves))), dim3(256), 0, stream,
+                       x, w, out, rows, dim, eps, unit_offset, inv_rms);
+    return check_launch("rms_norm");
+}
+
+int launch_rms_norm_backward_dx(const float* x, const float* w, const float* dy, float* dx, const float* addend,
+                                int64_t rows, int64_t dim, double eps, int unit_offset, double* inv_rms,
+                                hipStream_t stream) {
+    if (rows == 0) return kOk;
+    DLLM_REQUIRE(dim > 0, "rms_norm_backward needs a non-empty last dimension");
+    hipLaunchKernelGGL(rms_norm_backward_kernel, dim3(static_cast<unsigned>(ceil_div(rows, kRowWaves))), dim3(256), 0,
+                       stream, x, w, dy, dx, addend, rows, dim, eps, unit_offset, inv_rms);
+    return check_launch("rms_norm_backward");
+}
+
+int launch_column_sums(int kind, const float* dy, const float* x, const double* inv_rms, int64_t dim,
+                       const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream) {
+    if (dim == 0) return kOk;
+    DLLM_REQUIRE(nseg >= 1, "column sums need a segment");
+    const unsigned blocks = static_cast<unsigned>(ceil_div(dim, 256));
+    for (int s = 0; s < nseg; ++s) {
+        float* part = nseg == 1 ? out : partial + static_cast<int64_t>(s) * dim;
+        hipLaunchKernelGGL(column_partial_kernel, dim3(blocks), dim3(256), 0, stream, kind, dy, x, inv_rms, dim,
+                           seg_host[s], seg_host[s + 1], part);
+    }
+    if (nseg > 1) hipLaunchKernelGGL(segment_float_sum_kernel, dim3(blocks), dim3(256), 0, stream, partial, dim, nseg, out);
+    return check_launch("column_sums");
+}
+
+int launch_rope_tables(const int64_t* positions, int64_t n, const double* inv_freq, int64_t half, double* cos_table,
+                       double* sin_table, hipStream_t stream) {
+    if (n * half == 0) return kOk;
+    hipLaunchKernelGGL(rope_table_kernel, dim3(static_cast<unsigned>(ceil_div(n * half, 256))), dim3(256), 0, stream,
+                       positions, n, inv_freq, half, cos_table, sin_table);
+    return check_launch("rope_tables");
+}
+
+int launch_rope(const float* x, const int64_t* pos_index, const double* cos_table, const double* sin_table,
+                float* out, int64_t tokens, int64_t heads, int64_t head_dim, int64_t rotary_dim, int interleaved,
+                int inverse, hipStream_t stream) {
+    DLLM_REQUIRE(rotary_dim % 2 == 0 && rotary_dim <= head_dim, "rotary_dim must be even and at most head_dim");
+    const int64_t n = tokens * heads * (rotary_dim / 2 + head_dim - rotary_dim);
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream, x, pos_index,
+                       cos_table, sin_table, out, tokens, heads, head_dim, rotary_dim, interleaved, inverse);
+    return check_launch("rope");
+}
+
+int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(silu_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, out, n);
+    return check_launch("silu");
+}
+
+int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
+                          hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(swiglu_forward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, gate, up, gate_act,
+                       product, n);
+    return check_launch("swiglu");
+}
+
+int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(silu_backward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, dy, out, n);
+    return check_launch("silu_backward");
+}
+
+int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
+                           float* dgate, float* dup, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(swiglu_backward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, gate, up, gate_act,
+                       dproduct, dgate, dup, n);
+    return check_launch("swiglu_backward");
+}
+
+int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(add_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, a, b, out, n);
+    return check_launch("add");
+}
+
+int launch_gather_rows(const float* table, const int64_t* index, float* out, int64_t rows, int64_t dim,
+                       hipStream_t stream) {
+    if (rows == 0) return kOk;
+    DLLM_REQUIRE(rows <= 2147483647, "too many rows to gather");
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, table, index, out,
+                       rows, dim);
+    return check_launch("gather_rows");
+}
+
+}  // namespace dllm_hip

@@ -1,0 +1,803 @@
+// The device-resident fine-tuning step (include/dllm_hip.h, dllm_hip_trainer_*).
+//
+// Restates FineTuner.train_step (src/etalii_dllm/training/trainer.py:290-335), DecoderGradients
+// (training/backprop.py:88-118, 183-306, 399-499) and AdamW.step (training/optimizer.py:82-109) for pre-norm dense
+// decoders (Llama, Mistral, Qwen2, Qwen3 families) on one GPU:
+//  - all windows of a step are packed into one batch of rows. Row-local work (linear, dX, norms, RoPE, SwiGLU,
+//    cross-entropy) is independent of the rows it is batched with, so packing changes no bit;
+//  - every reduction over a window's rows (dW, db, norm weights, the embedding) is done per window and the per-window
+//    float32 results are added in window order, the first copied (trainer.py:328-332), inside the kernels;
+//  - the float32 glue of backprop.py is fused into the producing kernels with its operand order: x_mid = x + out and
+//    x_out = x_mid + mlp in the projection epilogues, dh1 = (dq + dk) + dv and dh2 = dx_gate + dx_up in the dX
+//    epilogues, dx_mid = dx + dh2' and dx = dx_mid + dh1' in the norm-backward kernels;
+//  - the tied embedding's gradient (dembedding + dhead per window, then summed over windows) is the head dW with the
+//    window's embedding rows as an addend.
+// Weights, gradients and AdamW moments live in one arena each, tensors in natural name order.
+#include <string.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "devmath.h"
+#include "dllm_hip.h"
+#include "kernels.h"
+
+using namespace dllm_hip;
+
+namespace {
+
+// ---- natural name order (modelfile.py:40-47) ----
+struct Part {
+    bool digits;
+    long long number;
+    std::string text;
+};
+
+std::vector<Part> split_name(const std::string& name) {
+    std::vector<Part> parts;
+    size_t i = 0;
+    std::string text;
+    while (i <= name.size()) {
+        if (i < name.size() && isdigit(static_cast<unsigned char>(name[i]))) {
+            parts.push_back({false, 0, text});
+            text.clear();
+            size_t j = i;
+            while (j < name.size() && isdigit(static_cast<unsigned char>(name[j]))) ++j;
+            parts.push_back({true, std::strtoll(name.substr(i, j - i).c_str(), nullptr, 10), ""});
+            i = j;
+            continue;
+        }
+        if (i == name.size()) break;
+        text.push_back(name[i]);
+        ++i;
+    }
+    parts.push_back({false, 0, text});
+    return parts;
+}
+
+bool natural_less(const std::string& a, const std::string& b) {
+    const std::vector<Part> pa = split_name(a), pb = split_name(b);
+    const size_t n = std::min(pa.size(), pb.size());
+    for (size_t i = 0; i < n; ++i) {
+        const Part &x = pa[i], &y = pb[i];
+        if (x.digits != y.digits) return x.digits;  // (0, n, "") sorts before (1, 0, text)
+        if (x.digits) {
+            if (x.number != y.number) return x.number < y.number;
+        } else if (x.text != y.text) {
+            return x.text < y.text;
+        }
+    }
+    if (pa.size() != pb.size()) return pa.size() < pb.size();
+    return a < b;
+}
+
+// ---- device memory ----
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() {
+        if (p) (void)hipFree(p);
+    }
+    int alloc(size_t n) {
+        bytes = n > 0 ? n : 1;
+        return check_hip(hipMalloc(&p, bytes), "hipMalloc");
+    }
+    template <typename T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+struct TensorInfo {
+    std::string name;
+    int64_t offset = 0, numel = 0, rows = 0, cols = 0;
+    int ndim = 1;
+    int64_t wt_offset = -1;  // transposed copy for the forward matmul, if it is a linear weight
+};
+
+// rope_inv_freq (numerics.py:267-297, default scaling): exp(-(2i / dim) log(theta)) with the portable exp and log.
+__global__ void inv_freq_kernel(int64_t rotary_dim, double theta, double* out) {
+    const int64_t i = threadIdx.x + static_cast<int64_t>(blockIdx.x) * blockDim.x;
+    if (i >= rotary_dim / 2) return;
+    const double log_theta = dlog(theta);
+    const double frac = static_cast<double>(2 * i) / static_cast<double>(rotary_dim);
+    out[i] = dexp(-frac * log_theta);
+}
+
+// Untied embedding gradient: out[v][d] = window-ordered float sum of the windows' rows for token v (a window without
+// token v contributes +0.0f), the first window copied.
+__global__ __launch_bounds__(256) void sparse_window_sum_kernel(const float* __restrict__ rows,
+                                                                const int* __restrict__ addrow, int64_t vocab,
+                                                                int64_t dim, int windows, float* __restrict__ out) {
+    const int64_t v = blockIdx.x;
+    for (int64_t d = threadIdx.x; d < dim; d += 256) {
+        float t = 0.0f;
+        for (int w = 0; w < windows; ++w) {
+            const int r = addrow[static_cast<int64_t>(w) * vocab + v];
+            const float val = r >= 0 ? rows[static_cast<int64_t>(r) * dim + d] : 0.0f;
+            t = w == 0 ? val : t + val;
+        }
+        out[v * dim + d] = t;
+    }
+}
+
+}  // namespace
+
+struct dllm_hip_trainer {
+    dllm_hip_decoder_config c{};
+    int64_t R_max = 0, W_max = 0, T_max = 0;
+    int64_t H = 0, QD = 0, KVD = 0, I = 0, V = 0;
+    std::vector<TensorInfo> tensors;
+    std::map<std::string, int> index;
+    DevBuf params, grads, m1, m2, wt;
+
+    struct LayerIds {
+        int attn_norm, q, k, v, qb = -1, kb = -1, vb = -1, qn = -1, kn = -1, o, mlp_norm, gate, up, down;
+    };
+    std::vector<LayerIds> layer_ids;
+    int emb = -1, final_norm = -1, lm_head = -1;
+
+    struct Saved {
+        float *x_in, *h1, *q_raw, *k_raw, *qn, *kn, *q, *k, *v, *attended, *x_mid, *h2, *gate, *up, *gate_act, *product;
+    };
+    std::vector<Saved> saved;
+    std::vector<std::unique_ptr<DevBuf>> owned;
+    float *x_final = nullptr, *hidden = nullptr, *logits = nullptr, *dlogits = nullptr;
+    double *dl_d = nullptr, *big_T = nullptr, *dy_d = nullptr;
+    float *dx = nullptr, *dh = nullptr, *dx_mid = nullptr, *dattended = nullptr, *dq_t = nullptr, *dk_t = nullptr,
+          *dv_t = nullptr, *dq = nullptr, *dk = nullptr, *dq2 = nullptr, *dk2 = nullptr, *dproduct = nullptr,
+          *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *emb_rows = nullptr;
+    double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
+           *per_tensor = nullptr, *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+    void* attn_ws = nullptr;
+    int64_t *tok_in = nullptr, *tok_tgt = nullptr, *pos_index = nullptr, *seg_d = nullptr, *batch_d = nullptr,
+            *grp_order = nullptr, *grp_start = nullptr, *grp_out = nullptr, *ten_off = nullptr, *ten_cnt = nullptr,
+            *chunk_start = nullptr, *chunk_end = nullptr;
+    double* chunk_decay = nullptr;
+    int* addrow = nullptr;
+    int* err_flag = nullptr;
+    int64_t chunks = 0;
+    std::vector<int64_t> seg_host;
+    bool wt_valid = false;
+
+    template <typename T>
+    int make(T** out, size_t n) {
+        owned.emplace_back(new DevBuf());
+        DLLM_TRY(owned.back()->alloc(n * sizeof(T)));
+        *out = owned.back()->as<T>();
+        return kOk;
+    }
+
+    int add_tensor(const std::string& name, int64_t rows, int64_t cols, bool linear_weight) {
+        TensorInfo t;
+        t.name = name;
+        t.rows = rows;
+        t.cols = cols;
+        t.ndim = cols > 0 ? 2 : 1;
+        t.numel = cols > 0 ? rows * cols : rows;
+        t.wt_offset = linear_weight ? 0 : -1;
+        tensors.push_back(t);
+        return kOk;
+    }
+
+    int build_tensors() {
+        const auto& k = c;
+        add_tensor("token_embedding.weight", V, H, k.tie_embeddings != 0);
+        for (int64_t l = 0; l < k.layers; ++l) {
+            const std::string p = "layers." + std::to_string(l) + ".";
+            add_tensor(p + "attention_norm.weight", H, 0, false);
+            add_tensor(p + "attention.q.weight", QD, H, true);
+            add_tensor(p + "attention.k.weight", KVD, H, true);
+            add_tensor(p + "attention.v.weight", KVD, H, true);
+            if (k.attention_bias) {
+                add_tensor(p + "attention.q.bias", QD, 0, false);
+                add_tensor(p + "attention.k.bias", KVD, 0, false);
+                add_tensor(p + "attention.v.bias", KVD, 0, false);
+            }
+            if (k.qk_norm) {
+                add_tensor(p + "attention.q_norm.weight", k.qk_norm == 2 ? QD : k.head_dim, 0, false);
+                add_tensor(p + "attention.k_norm.weight", k.qk_norm == 2 ? KVD : k.head_dim, 0, false);
+            }
+            add_tensor(p + "attention.o.weight", H, QD, true);
+            add_tensor(p + "mlp_norm.weight", H, 0, false);
+            add_tensor(p + "mlp.gate.weight", I, H, true);
+            add_tensor(p + "mlp.up.weight", I, H, true);
+            add_tensor(p + "mlp.down.weight", H, I, true);
+        }
+        add_tensor("final_norm.weight", H, 0, false);
+        if (!k.tie_embeddings) add_tensor("lm_head.weight", V, H, true);
+        std::stable_sort(tensors.begin(), tensors.end(),
+                         [](const TensorInfo& a, const TensorInfo& b) { return natural_less(a.name, b.name); });
+        int64_t off = 0, wt_off = 0;
+        for (size_t i = 0; i < tensors.size(); ++i) {
+            TensorInfo& t = tensors[i];
+            off = static_cast<int64_t>(round_up(static_cast<size_t>(off), 64));  // 256-byte aligned tensors
+            t.offset = off;
+            off += t.numel;
+            if (t.wt_offset >= 0) {
+                wt_off = static_cast<int64_t>(round_up(static_cast<size_t>(wt_off), 64));
+                t.wt_offset = wt_off;
+                wt_off += t.numel;
+            }
+            index[t.name] = static_cast<int>(i);
+        }
+        const size_t arena = static_cast<size_t>(round_up(static_cast<size_t>(off), 64)) * sizeof(float);
+        DLLM_TRY(params.alloc(arena));
+        DLLM_TRY(grads.alloc(arena));
+        DLLM_TRY(m1.alloc(arena));
+        DLLM_TRY(m2.alloc(arena));
+        DLLM_TRY(wt.alloc(static_cast<size_t>(wt_off > 0 ? wt_off : 1) * sizeof(float)));
+        DLLM_TRY(check_hip(hipMemset(params.p, 0, arena), "memset"));
+        DLLM_TRY(check_hip(hipMemset(grads.p, 0, arena), "memset"));
+        DLLM_TRY(check_hip(hipMemset(m1.p, 0, arena), "memset"));
+        DLLM_TRY(check_hip(hipMemset(m2.p, 0, arena), "memset"));
+        auto id = [&](const std::string& n) { return index.count(n) ? index[n] : -1; };
+        emb = id("token_embedding.weight");
+        final_norm = id("final_norm.weight");
+        lm_head = id("lm_head.weight");
+        for (int64_t l = 0; l < c.layers; ++l) {
+            const std::string p = "layers." + std::to_string(l) + ".";
+            LayerIds L;
+            L.attn_norm = id(p + "attention_norm.weight");
+            L.q = id(p + "attention.q.weight");
+            L.k = id(p + "attention.k.weight");
+            L.v = id(p + "attention.v.weight");
+            L.qb = id(p + "attention.q.bias");
+            L.kb = id(p + "attention.k.bias");
+            L.vb = id(p + "attention.v.bias");
+            L.qn = id(p + "attention.q_norm.weight");
+            L.kn = id(p + "attention.k_norm.weight");
+            L.o = id(p + "attention.o.weight");
+            L.mlp_norm = id(p + "mlp_norm.weight");
+            L.gate = id(p + "mlp.gate.weight");
+            L.up = id(p + "mlp.up.weight");
+            L.down = id(p + "mlp.down.weight");
+            layer_ids.push_back(L);
+        }
+        // AdamW chunk table: 64K-element chunks inside each tensor, decay for matrices (optimizer.py:93).
+        std::vector<int64_t> cs, ce, to, tc;
+        std::vector<double> cd;
+        for (const TensorInfo& t : tensors) {
+            to.push_back(t.offset);
+            tc.push_back(t.numel);
+            for (int64_t s = 0; s < t.numel; s += 65536) {
+                cs.push_back(t.offset + s);
+                ce.push_back(t.offset + std::min<int64_t>(t.numel, s + 65536));
+                cd.push_back(t.ndim >= 2 ? 1.0 : 0.0);
+            }
+        }
+        chunks = static_cast<int64_t>(cs.size());
+        DLLM_TRY(make(&chunk_start, cs.size()));
+        DLLM_TRY(make(&chunk_end, ce.size()));
+        DLLM_TRY(make(&chunk_decay, cd.size()));
+        DLLM_TRY(make(&ten_off, to.size()));
+        DLLM_TRY(make(&ten_cnt, tc.size()));
+        DLLM_TRY(check_hip(hipMemcpy(chunk_start, cs.data(), cs.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(chunk_end, ce.data(), ce.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(chunk_decay, cd.data(), cd.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(ten_off, to.data(), to.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(ten_cnt, tc.data(), tc.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(make(&per_tensor, tensors.size()));
+        DLLM_TRY(make(&stats, 3));
+        return kOk;
+    }
+
+    int build_activations() {
+        const int64_t R = R_max, heads = c.heads, kvh = c.kv_heads;
+        saved.resize(static_cast<size_t>(c.layers));
+        // x_in of layer l + 1 is x_out of layer l: one chain of L + 1 residual buffers.
+        std::vector<float*> xs(static_cast<size_t>(c.layers) + 1);
+        for (auto& p : xs) DLLM_TRY(make(&p, R * H));
+        for (int64_t l = 0; l < c.layers; ++l) {
+            Saved& s = saved[static_cast<size_t>(l)];
+            s.x_in = xs[static_cast<size_t>(l)];
+            DLLM_TRY(make(&s.h1, R * H));
+            DLLM_TRY(make(&s.q_raw, R * QD));
+            DLLM_TRY(make(&s.k_raw, R * KVD));
+            s.qn = s.kn = nullptr;
+            if (c.qk_norm) {
+                DLLM_TRY(make(&s.qn, R * QD));
+                DLLM_TRY(make(&s.kn, R * KVD));
+            }
+            DLLM_TRY(make(&s.q, R * QD));
+            DLLM_TRY(make(&s.k, R * KVD));
+            DLLM_TRY(make(&s.v, R * KVD));
+            DLLM_TRY(make(&s.attended, R * QD));
+            DLLM_TRY(make(&s.x_mid, R * H));
+            DLLM_TRY(make(&s.h2, R * H));
+            DLLM_TRY(make(&s.gate, R * I));
+            DLLM_TRY(make(&s.up, R * I));
+            DLLM_TRY(make(&s.gate_act, R * I));
+            DLLM_TRY(make(&s.product, R * I));
+        }
+        x_final = xs.back();
+        DLLM_TRY(make(&hidden, R * H));
+        DLLM_TRY(make(&logits, R * V));
+        DLLM_TRY(make(&dlogits, R * V));
+        const int64_t Rp = padded_rows(R);
+        const int64_t maxN = std::max<int64_t>({V, H, QD, I});
+        DLLM_TRY(make(&dl_d, R * padded_rows(V)));
+        DLLM_TRY(make(&big_T, std::max<int64_t>(V, std::max<int64_t>({H, QD, I})) * Rp));
+        DLLM_TRY(make(&dy_d, R * padded_rows(std::max<int64_t>({H, QD, I}))));
+        (void)maxN;
+        DLLM_TRY(make(&dx, R * H));
+        DLLM_TRY(make(&dh, R * H));
+        DLLM_TRY(make(&dx_mid, R * H));
+        DLLM_TRY(make(&dattended, R * QD));
+        DLLM_TRY(make(&dq_t, R * QD));
+        DLLM_TRY(make(&dk_t, R * KVD));
+        DLLM_TRY(make(&dv_t, R * KVD));
+        DLLM_TRY(make(&dq, R * QD));
+        DLLM_TRY(make(&dk, R * KVD));
+        DLLM_TRY(make(&dq2, R * QD));
+        DLLM_TRY(make(&dk2, R * KVD));
+        DLLM_TRY(make(&dproduct, R * I));
+        DLLM_TRY(make(&dgate, R * I));
+        DLLM_TRY(make(&dup, R * I));
+        DLLM_TRY(make(&col_part, W_max * std::max<int64_t>({H, QD, KVD, I})));
+        DLLM_TRY(make(&emb_rows, R * H));
+        DLLM_TRY(make(&inv_rms, R * std::max<int64_t>(heads, 1)));
+        DLLM_TRY(make(&row_max, R));
+        DLLM_TRY(make(&row_total, R));
+        DLLM_TRY(make(&row_loss, R));
+        DLLM_TRY(make(&loss_w, W_max));
+        DLLM_TRY(make(&inv_freq, std::max<int64_t>(c.rotary_dim / 2, 1)));
+        DLLM_TRY(make(&cos_t, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
+        DLLM_TRY(make(&sin_t, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
+        AttentionShape sh{R, R, heads, kvh, c.head_dim, c.head_dim, c.attention_scale, 1, 0, c.sliding_window, 0.0};
+        AttentionBatch b{};
+        b.max_kv = T_max;
+        const size_t ws = attention_backward_workspace(sh, b, R);
+        char* p = nullptr;
+        DLLM_TRY(make(&p, ws));
+        attn_ws = p;
+        DLLM_TRY(make(&tok_in, R));
+        DLLM_TRY(make(&tok_tgt, R));
+        DLLM_TRY(make(&pos_index, R));
+        DLLM_TRY(make(&seg_d, W_max + 1));
+        DLLM_TRY(make(&batch_d, 4 * W_max));
+        DLLM_TRY(make(&grp_order, R));
+        DLLM_TRY(make(&grp_start, R + 1));
+        DLLM_TRY(make(&grp_out, R));
+        DLLM_TRY(make(&addrow, W_max * V));
+        DLLM_TRY(make(&err_flag, 1));
+        // RoPE tables for positions 0 .. T_max - 1 (every window starts at position 0)
+        hipLaunchKernelGGL(inv_freq_kernel, dim3(1), dim3(1024), 0, nullptr, c.rotary_dim, c.rope_theta, inv_freq);
+        DLLM_TRY(check_launch("inv_freq"));
+        DLLM_TRY(launch_rope_tables(nullptr, T_max, inv_freq, c.rotary_dim / 2, cos_t, sin_t, nullptr));
+        return check_hip(hipDeviceSynchronize(), "trainer setup");
+    }
+
+    float* P(int id) const { return params.as<float>() + tensors[static_cast<size_t>(id)].offset; }
+    float* G(int id) const { return grads.as<float>() + tensors[static_cast<size_t>(id)].offset; }
+    float* WT(int id) const { return wt.as<float>() + tensors[static_cast<size_t>(id)].wt_offset; }
+    const float* Popt(int id) const { return id >= 0 ? P(id) : nullptr; }
+
+    // W^T of every linear weight for the forward matmuls.
+    int refresh_transposes(hipStream_t s) {
+        for (const TensorInfo& t : tensors)
+            if (t.wt_offset >= 0)
+                DLLM_TRY(launch_transpose_f32(params.as<float>() + t.offset, t.rows, t.cols,
+                                              wt.as<float>() + t.wt_offset, s));
+        wt_valid = true;
+        return kOk;
+    }
+
+    // out[R][N] (+)= x[R][K] @ W^T (+ bias), x converted to x^T as doubles into big_T.
+    int linear_fwd(const float* x, int64_t R, int64_t K, int w_id, const float* bias, float* out, const float* addsrc,
+                   hipStream_t s) {
+        const int64_t N = tensors[static_cast<size_t>(w_id)].rows;
+        DLLM_TRY(launch_to_double(x, R, K, K, nullptr, 0, big_T, padded_rows(R), s));
+        GemmCall g;
+        g.A = big_T;
+        g.lda = padded_rows(R);
+        g.B = WT(w_id);
+        g.ldb = N;
+        g.C = out;
+        g.ldc = N;
+        g.I = R;
+        g.J = N;
+        g.l0 = 0;
+        g.l1 = K;
+        g.bias = bias;
+        g.addsrc = addsrc;
+        g.ld_add = N;
+        return launch_gemm(g, s);
+    }
+
+    // Converts dy[R][N] to dy_d [R][N_pad] and dy^T [N][R_pad] (doubles) for the dW and dX matmuls.
+    int prepare_dy(const float* dyv, int64_t R, int64_t N, double* as_rows, double* as_cols, hipStream_t s) {
+        return launch_to_double(dyv, R, N, N, as_rows, padded_rows(N), as_cols, padded_rows(R), s);
+    }
+
+    // dx[R][K] (= addsrc +) sum_n dy[r][n] W[n][k], from dy^T in `cols`.
+    int linear_dx(const double* cols, int64_t R, int w_id, float* out, const float* addsrc, hipStream_t s) {
+        const TensorInfo& t = tensors[static_cast<size_t>(w_id)];
+        GemmCall g;
+        g.A = cols;
+        g.lda = padded_rows(R);
+        g.B = P(w_id);
+        g.ldb = t.cols;
+        g.C = out;
+        g.ldc = t.cols;
+        g.I = R;
+        g.J = t.cols;
+        g.l0 = 0;
+        g.l1 = t.rows;
+        g.addsrc = addsrc;
+        g.ld_add = t.cols;
+        return launch_gemm(g, s);
+    }
+
+    // grad[w] = window-ordered float sum of per-window dW = sum over window rows of dy[r][n] x[r][k].
+    int linear_dw(const double* rows_d, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
+                  const float* addend, hipStream_t s) {
+        GemmCall g;
+        g.A = rows_d;
+        g.lda = padded_rows(N);
+        g.B = x;
+        g.ldb = K;
+        g.C = out;
+        g.ldc = K;
+        g.I = N;
+        g.J = K;
+        g.seg = seg_d;
+        g.nseg = nseg;
+        g.seg_addrow = addrow_;
+        g.seg_addend = addend;
+        g.ld_seg_add = K;
+        return launch_gemm(g, s);
+    }
+
+    int norm_dw(const float* dyv, const float* x, const double* inv, int64_t dim, int64_t rows_per_token, int nseg,
+                float* out, hipStream_t s) {
+        std::vector<int64_t> seg(seg_host.size());
+        for (size_t i = 0; i < seg.size(); ++i) seg[i] = seg_host[i] * rows_per_token;
+        return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s);
+    }
+
+    // One layer's forward (backprop.py:423-487).
+    int forward_layer(int64_t l, int64_t R, const AttentionBatch& b, float* x_out, hipStream_t s) {
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        Saved& sv = saved[static_cast<size_t>(l)];
+        const double eps = c.rms_norm_eps;
+        DLLM_TRY(launch_rms_norm(sv.x_in, P(L.attn_norm), sv.h1, R, H, eps, 0, nullptr, s));
+        DLLM_TRY(linear_fwd(sv.h1, R, H, L.q, Popt(L.qb), sv.q_raw, nullptr, s));
+        DLLM_TRY(linear_fwd(sv.h1, R, H, L.k, Popt(L.kb), sv.k_raw, nullptr, s));
+        DLLM_TRY(linear_fwd(sv.h1, R, H, L.v, Popt(L.vb), sv.v, nullptr, s));
+        const float* qsrc = sv.q_raw;
+        const float* ksrc = sv.k_raw;
+        if (c.qk_norm == 2) {
+            DLLM_TRY(launch_rms_norm(sv.q_raw, P(L.qn), sv.qn, R, QD, eps, 0, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.k_raw, P(L.kn), sv.kn, R, KVD, eps, 0, nullptr, s));
+            qsrc = sv.qn;
+            ksrc = sv.kn;
+        } else if (c.qk_norm == 1) {
+            DLLM_TRY(launch_rms_norm(sv.q_raw, P(L.qn), sv.qn, R * c.heads, c.head_dim, eps, 0, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.k_raw, P(L.kn), sv.kn, R * c.kv_heads, c.head_dim, eps, 0, nullptr, s));
+            qsrc = sv.qn;
+            ksrc = sv.kn;
+        }
+        DLLM_TRY(launch_rope(qsrc, pos_index, cos_t, sin_t, sv.q, R, c.heads, c.head_dim, c.rotary_dim, 0, 0, s));
+        DLLM_TRY(launch_rope(ksrc, pos_index, cos_t, sin_t, sv.k, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 0, s));
+        AttentionShape sh{R, R, c.heads, c.kv_heads, c.head_dim, c.head_dim, c.attention_scale, 1, 0,
+                          c.sliding_window, 0.0};
+        DLLM_TRY(launch_attention(sv.q, sv.k, sv.v, sv.attended, sh, b, s));
+        DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
+        DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
+        DLLM_TRY(linear_fwd(sv.h2, R, H, L.gate, nullptr, sv.gate, nullptr, s));
+        DLLM_TRY(linear_fwd(sv.h2, R, H, L.up, nullptr, sv.up, nullptr, s));
+        DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * I, s));
+        return linear_fwd(sv.product, R, I, L.down, nullptr, x_out, sv.x_mid, s);  // x_out = x_mid + mlp
+    }
+
+    // One layer's backward (backprop.py:208-306); dx holds the gradient of the layer output on entry and of its input
+    // on exit.
+    int backward_layer(int64_t l, int64_t R, int nseg, const AttentionBatch& b, hipStream_t s) {
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        const Saved& sv = saved[static_cast<size_t>(l)];
+        const double eps = c.rms_norm_eps;
+        // SwiGLU (backprop.py:289-306)
+        DLLM_TRY(prepare_dy(dx, R, H, dy_d, big_T, s));
+        DLLM_TRY(linear_dx(big_T, R, L.down, dproduct, nullptr, s));
+        DLLM_TRY(linear_dw(dy_d, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, s));
+        DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s));
+        DLLM_TRY(prepare_dy(dgate, R, I, dy_d, big_T, s));
+        DLLM_TRY(linear_dx(big_T, R, L.gate, dh, nullptr, s));
+        DLLM_TRY(linear_dw(dy_d, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, s));
+        DLLM_TRY(prepare_dy(dup, R, I, dy_d, big_T, s));
+        DLLM_TRY(linear_dx(big_T, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
+        DLLM_TRY(linear_dw(dy_d, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, s));
+        // mlp norm; dx_mid = dx + dh2'
+        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_rms, s));
+        DLLM_TRY(norm_dw(dh, sv.x_mid, inv_rms, H, 1, nseg, G(L.mlp_norm), s));
+        // attention output projection
+        DLLM_TRY(prepare_dy(dx_mid, R, H, dy_d, big_T, s));
+        DLLM_TRY(linear_dx(big_T, R, L.o, dattended, nullptr, s));
+        DLLM_TRY(linear_dw(dy_d, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, s));
+        AttentionShape sh{R, R, c.heads, c.kv_heads, c.head_dim, c.head_dim, c.attention_scale, 1, 0,
+                          c.sliding_window, 0.0};
+        DLLM_TRY(launch_attention_backward(sv.q, sv.k, sv.v, dattended, dq_t, dk_t, dv_t, sh, b, R, R, attn_ws, s));
+        DLLM_TRY(launch_rope(dq_t, pos_index, cos_t, sin_t, dq, R, c.heads, c.head_dim, c.rotary_dim, 0, 1, s));
+        DLLM_TRY(launch_rope(dk_t, pos_index, cos_t, sin_t, dk, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 1, s));
+        const float* dqf = dq;
+        const float* dkf = dk;
+        if (c.qk_norm == 1) {
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R * c.heads, c.head_dim, eps, 0,
+                                                 inv_rms, s));
+            DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, c.head_dim, c.heads, nseg, G(L.qn), s));
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.k_raw, P(L.kn), dk, dk2, nullptr, R * c.kv_heads, c.head_dim, eps,
+                                                 0, inv_rms, s));
+            DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, c.head_dim, c.kv_heads, nseg, G(L.kn), s));
+            dqf = dq2;
+            dkf = dk2;
+        } else if (c.qk_norm == 2) {
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R, QD, eps, 0, inv_rms, s));
+            DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, QD, 1, nseg, G(L.qn), s));
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.k_raw, P(L.kn), dk, dk2, nullptr, R, KVD, eps, 0, inv_rms, s));
+            DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, KVD, 1, nseg, G(L.kn), s));
+            dqf = dq2;
+            dkf = dk2;
+        }
+        // q, k, v projections: dh1 = (dh_q + dh_k) + dh_v
+        const float* ds[3] = {dqf, dkf, dv_t};
+        const int ws_[3] = {L.q, L.k, L.v};
+        const int bs_[3] = {L.qb, L.kb, L.vb};
+        const int64_t ns[3] = {QD, KVD, KVD};
+        for (int p = 0; p < 3; ++p) {
+            DLLM_TRY(prepare_dy(ds[p], R, ns[p], dy_d, big_T, s));
+            DLLM_TRY(linear_dx(big_T, R, ws_[p], dh, p == 0 ? nullptr : dh, s));
+            DLLM_TRY(linear_dw(dy_d, ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s));
+            if (bs_[p] >= 0)
+                DLLM_TRY(launch_column_sums(0, ds[p], nullptr, nullptr, ns[p], seg_host.data(), nseg, col_part,
+                                            G(bs_[p]), s));
+        }
+        // attention norm; dx = dx_mid + dh1'
+        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh, dx, dx_mid, R, H, eps, 0, inv_rms, s));
+        return norm_dw(dh, sv.x_in, inv_rms, H, 1, nseg, G(L.attn_norm), s);
+    }
+
+    // Host preparation of a batch of windows; returns the packed row count.
+    int prepare(const int64_t* tokens, const int64_t* offsets, const int64_t* lengths, int64_t windows, int64_t* rows_out,
+                AttentionBatch* b, int64_t* groups_out, hipStream_t s) {
+        DLLM_REQUIRE(windows >= 1 && windows <= W_max, "number of windows outside the trainer's capacity");
+        std::vector<int64_t> in, tgt, pos, seg(1, 0), qs, ql;
+        int64_t max_len = 0;
+        for (int64_t w = 0; w < windows; ++w) {
+            DLLM_REQUIRE(lengths[w] >= 2, "a window needs at least two tokens");
+            const int64_t n = lengths[w] - 1;
+            DLLM_REQUIRE(n <= T_max, "window longer than the trainer's capacity");
+            qs.push_back(seg.back());
+            ql.push_back(n);
+            for (int64_t t = 0; t < n; ++t) {
+                const int64_t a = tokens[offsets[w] + t], z = tokens[offsets[w] + t + 1];
+                DLLM_REQUIRE(a >= 0 && a < V && z >= 0 && z < V, "token id out of range");
+                in.push_back(a);
+                tgt.push_back(z);
+                pos.push_back(t);
+            }
+            seg.push_back(seg.back() + n);
+            max_len = std::max(max_len, n);
+        }
+        const int64_t R = seg.back();
+        DLLM_REQUIRE(R <= R_max, "more tokens than the trainer's capacity");
+        seg_host = seg;
+        // embedding groups (grad.hpp:433-447 per window): rows of each window grouped by token, positions ascending
+        std::vector<int64_t> order, starts, outs;
+        std::vector<int> amap(static_cast<size_t>(windows * V), -1);
+        for (int64_t w = 0; w < windows; ++w) {
+            std::vector<int64_t> rows;
+            for (int64_t r = seg[w]; r < seg[w + 1]; ++r) rows.push_back(r);
+            std::stable_sort(rows.begin(), rows.end(), [&](int64_t a, int64_t z) { return in[a] < in[z]; });
+            for (size_t i = 0; i < rows.size(); ++i) {
+                if (i == 0 || in[rows[i]] != in[rows[i - 1]]) {
+                    amap[static_cast<size_t>(w * V + in[rows[i]])] = static_cast<int>(starts.size());
+                    outs.push_back(static_cast<int64_t>(starts.size()));
+                    starts.push_back(static_cast<int64_t>(order.size()));
+                }
+                order.push_back(rows[i]);
+            }
+        }
+        starts.push_back(static_cast<int64_t>(order.size()));
+        std::vector<int64_t> batch(qs);
+        batch.insert(batch.end(), ql.begin(), ql.end());
+        batch.insert(batch.end(), qs.begin(), qs.end());
+        batch.insert(batch.end(), ql.begin(), ql.end());
+        DLLM_TRY(check_hip(hipMemcpy(tok_in, in.data(), R * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(tok_tgt, tgt.data(), R * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(pos_index, pos.data(), R * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(seg_d, seg.data(), seg.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(batch_d, batch.data(), batch.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(grp_order, order.data(), order.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(grp_start, starts.data(), starts.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(grp_out, outs.data(), outs.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(addrow, amap.data(), amap.size() * sizeof(int), hipMemcpyHostToDevice), "upload"));
+        b->q_start = batch_d;
+        b->q_len = batch_d + windows;
+        b->kv_start = batch_d + 2 * windows;
+        b->kv_len = batch_d + 3 * windows;
+        b->count = static_cast<int>(windows);
+        b->max_q = max_len;
+        b->max_kv = max_len;
+        *rows_out = R;
+        *groups_out = static_cast<int64_t>(outs.size());
+        (void)s;
+        return kOk;
+    }
+
+    int gradients(const int64_t* tokens, const int64_t* offsets, const int64_t* lengths, int64_t windows,
+                  double scale, double* loss, hipStream_t s) {
+        int64_t R = 0, groups = 0;
+        AttentionBatch b{};
+        DLLM_TRY(prepare(tokens, offsets, lengths, windows, &R, &b, &groups, s));
+        if (!wt_valid) DLLM_TRY(refresh_transposes(s));
+        const int nseg = static_cast<int>(windows);
+        const double eps = c.rms_norm_eps;
+        // forward (backprop.py:411-490)
+        DLLM_TRY(launch_gather_rows(P(emb), tok_in, saved[0].x_in, R, H, s));
+        for (int64_t l = 0; l < c.layers; ++l) {
+            float* x_out = l + 1 < c.layers ? saved[static_cast<size_t>(l + 1)].x_in : x_final;
+            DLLM_TRY(forward_layer(l, R, b, x_out, s));
+        }
+        DLLM_TRY(launch_rms_norm(x_final, P(final_norm), hidden, R, H, eps, 0, nullptr, s));
+        const int head = c.tie_embeddings ? emb : lm_head;
+        DLLM_TRY(linear_fwd(hidden, R, H, head, nullptr, logits, nullptr, s));
+        // loss and the head (backprop.py:183-206)
+        DLLM_TRY(check_hip(hipMemsetAsync(err_flag, 0, sizeof(int), s), "memset"));
+        DLLM_TRY(launch_cross_entropy(logits, tok_tgt, dlogits, R, V, scale, seg_d, nseg, row_max, row_total, row_loss,
+                                      loss_w, err_flag, s));
+        DLLM_TRY(prepare_dy(dlogits, R, V, dl_d, big_T, s));
+        float* dhidden = dh;
+        DLLM_TRY(linear_dx(big_T, R, head, dhidden, nullptr, s));
+        DLLM_TRY(launch_rms_norm_backward_dx(x_final, P(final_norm), dhidden, dx, nullptr, R, H, eps, 0, inv_rms, s));
+        DLLM_TRY(norm_dw(dhidden, x_final, inv_rms, H, 1, nseg, G(final_norm), s));
+        for (int64_t l = c.layers - 1; l >= 0; --l) DLLM_TRY(backward_layer(l, R, nseg, b, s));
+        // embedding (backprop.py:112-117): per-window token rows, then the head's dW with them as the tied addend
+        DLLM_TRY(launch_embedding_groups(dx, H, grp_order, grp_start, grp_out, groups, emb_rows, H, s));
+        if (c.tie_embeddings) {
+            DLLM_TRY(linear_dw(dl_d, V, hidden, H, nseg, G(emb), addrow, emb_rows, s));
+        } else {
+            DLLM_TRY(linear_dw(dl_d, V, hidden, H, nseg, G(lm_head), nullptr, nullptr, s));
+            hipLaunchKernelGGL(sparse_window_sum_kernel, dim3(static_cast<unsigned>(V)), dim3(256), 0, s, emb_rows,
+                               addrow, V, H, nseg, G(emb));
+            DLLM_TRY(check_launch("embedding window sum"));
+        }
+        std::vector<double> lw(static_cast<size_t>(windows));
+        int flag = 0;
+        DLLM_TRY(check_hip(hipMemcpyAsync(lw.data(), loss_w, lw.size() * 8, hipMemcpyDeviceToHost, s), "download"));
+        DLLM_TRY(check_hip(hipMemcpyAsync(&flag, err_flag, sizeof flag, hipMemcpyDeviceToHost, s), "download"));
+        DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
+        DLLM_REQUIRE(flag == 0, "target out of range");
+        double total = 0.0;
+        for (double x : lw) total += x;  // trainer.py:326 (loss_total += loss, batch order)
+        if (loss) *loss = total;
+        return kOk;
+    }
+
+    int step(const int64_t* tokens, const int64_t* offsets, const int64_t* lengths, int64_t windows,
+             const dllm_hip_adamw* a, double* loss, double* norm, hipStream_t s) {
+        int64_t targets_total = 0;
+        for (int64_t w = 0; w < windows; ++w) targets_total += lengths[w] - 1;
+        DLLM_REQUIRE(targets_total > 0, "a step needs targets");
+        const double scale = 1.0 / static_cast<double>(targets_total);
+        double loss_total = 0.0;
+        DLLM_TRY(gradients(tokens, offsets, lengths, windows, scale, &loss_total, s));
+        // global norm, clip (optimizer.py:66-90), bias corrections by repeated multiplication (optimizer.py:59-63)
+        DLLM_TRY(launch_global_norm(grads.as<float>(), ten_off, ten_cnt, static_cast<int64_t>(tensors.size()),
+                                    per_tensor, a->max_grad_norm, stats, s));
+        double p1 = 1.0, p2 = 1.0;
+        for (int64_t i = 0; i < a->step; ++i) {
+            p1 *= a->beta1;
+            p2 *= a->beta2;
+        }
+        AdamWArgs args{a->learning_rate, a->beta1, a->beta2, a->eps, 1.0 - p1, 1.0 - p2, 1.0};
+        // the chunk table holds 1 for matrices: decay = weight_decay * 1 or * 0 (optimizer.py:93)
+        DLLM_TRY(scale_decay(a->weight_decay, s));
+        DLLM_TRY(launch_adamw(params.as<float>(), grads.as<float>(), m1.as<float>(), m2.as<float>(), chunk_start,
+                              chunk_end, chunk_decay_scaled, chunks, args, stats + 2, s));
+        DLLM_TRY(refresh_transposes(s));
+        double st[3];
+        DLLM_TRY(check_hip(hipMemcpyAsync(st, stats, sizeof st, hipMemcpyDeviceToHost, s), "download"));
+        DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
+        if (loss) *loss = loss_total / static_cast<double>(targets_total);
+        if (norm) *norm = st[1];
+        return kOk;
+    }
+
+    double* chunk_decay_scaled = nullptr;
+    double last_decay = -1.0;
+
+    int scale_decay(double wd, hipStream_t s) {
+        if (chunk_decay_scaled && wd == last_decay) return kOk;
+        if (!chunk_decay_scaled) DLLM_TRY(make(&chunk_decay_scaled, static_cast<size_t>(chunks)));
+        std::vector<double> d(static_cast<size_t>(chunks));
+        DLLM_TRY(check_hip(hipMemcpy(d.data(), chunk_decay, d.size() * 8, hipMemcpyDeviceToHost), "download"));
+        for (double& x : d) x = x != 0.0 ? wd : 0.0;
+        DLLM_TRY(check_hip(hipMemcpy(chunk_decay_scaled, d.data(), d.size() * 8, hipMemcpyHostToDevice), "upload"));
+        last_decay = wd;
+        (void)s;
+        return kOk;
+    }
+};
+
+extern "C" {
+
+int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_tokens, int64_t max_windows,
+                            int64_t max_window_tokens, dllm_hip_trainer** out) {
+    DLLM_REQUIRE(config && out, "null argument");
+    const dllm_hip_decoder_config& c = *config;
+    DLLM_REQUIRE(c.experts == 0, "mixture-of-experts layers are not supported by this trainer yet");
+    DLLM_REQUIRE(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, "heads must be a multiple of kv_heads");
+    DLLM_REQUIRE(c.rotary_dim > 0 && c.rotary_dim % 2 == 0 && c.rotary_dim <= c.head_dim, "invalid rotary_dim");
+    DLLM_REQUIRE(max_tokens > 0 && max_windows > 0 && max_window_tokens > 0, "capacities must be positive");
+    DLLM_REQUIRE(max_window_tokens <= 2048, "windows longer than 2048 tokens are not supported");
+    DLLM_REQUIRE(max_tokens <= 65535, "at most 65535 tokens per step");
+    std::unique_ptr<dllm_hip_trainer> t(new dllm_hip_trainer());
+    t->c = c;
+    t->R_max = max_tokens;
+    t->W_max = max_windows;
+    t->T_max = max_window_tokens;
+    t->H = c.hidden;
+    t->QD = c.heads * c.head_dim;
+    t->KVD = c.kv_heads * c.head_dim;
+    t->I = c.intermediate;
+    t->V = c.vocab;
+    DLLM_TRY(t->build_tensors());
+    DLLM_TRY(t->build_activations());
+    *out = t.release();
+    return kOk;
+}
+
+int dllm_hip_trainer_destroy(dllm_hip_trainer* t) {
+    delete t;
+    return kOk;
+}
+
+int dllm_hip_trainer_tensor(dllm_hip_trainer* t, const char* name, int which, float** ptr, int64_t* numel) {
+    DLLM_REQUIRE(t && name && ptr, "null argument");
+    auto it = t->index.find(name);
+    DLLM_REQUIRE(it != t->index.end(), std::string("unknown tensor ") + name);
+    const TensorInfo& info = t->tensors[static_cast<size_t>(it->second)];
+    const DevBuf* arenas[4] = {&t->params, &t->grads, &t->m1, &t->m2};
+    DLLM_REQUIRE(which >= 0 && which < 4, "which must be 0 (parameter), 1 (gradient), 2 (m) or 3 (v)");
+    *ptr = arenas[which]->as<float>() + info.offset;
+    if (numel) *numel = info.numel;
+    if (which == 0) t->wt_valid = false;  // the caller may write parameters
+    return kOk;
+}
+
+int dllm_hip_trainer_tensor_count(dllm_hip_trainer* t, int64_t* count) {
+    DLLM_REQUIRE(t && count, "null argument");
+    *count = static_cast<int64_t>(t->tensors.size());
+    return kOk;
+}
+
+const char* dllm_hip_trainer_tensor_name(dllm_hip_trainer* t, int64_t i) {
+    if (!t || i < 0 || i >= static_cast<int64_t>(t->tensors.size())) return nullptr;
+    return t->tensors[static_cast<size_t>(i)].name.c_str();
+}
+
+int dllm_hip_trainer_gradients(dllm_hip_trainer* t, const int64_t* tokens, const int64_t* offsets,
+                               const int64_t* lengths, int64_t windows, double scale, double router_scale,
+                               double* loss, void* stream) {
+    DLLM_REQUIRE(t && tokens && offsets && lengths, "null argument");
+    (void)router_scale;  // dense models have no router loss
+    return t->gradients(tokens, offsets, lengths, windows, scale, loss, static_cast<hipStream_t>(stream));
+}
+
+int dllm_hip_trainer_step(dllm_hip_trainer* t, const int64_t* tokens, const int64_t* offsets, const int64_t* lengths,
+                          int64_t windows, const dllm_hip_adamw* adamw, double* loss, double* grad_norm,
+                          void* stream) {
+    DLLM_REQUIRE(t && tokens && offsets && lengths && adamw, "null argument");
+    return t->step(tokens, offsets, lengths, windows, adamw, loss, grad_norm, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

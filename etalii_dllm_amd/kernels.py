@@ -1,0 +1,360 @@
+"""The reference's kernel module interface (etalii_dllm._kernels, cpp/kernels.cpp) over the MI355X library.
+
+Each function takes and returns NumPy arrays with the reference binding's names, argument meaning and errors
+(ValueError where the binding raises it): inputs are uploaded to the GPU, the HIP kernels run through the C ABI of
+include/dllm_hip.h, and the results come back. This is the drop-in surface for parity checks and for callers that
+hold host arrays; device-resident callers use the C ABI or :mod:`etalii_dllm_amd.trainer` directly.
+
+There is no CPU fallback: importing this module without the built library (libdllm_hip.so, see build.py) raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+from pathlib import Path
+
+import numpy as np
+
+LIBRARY = Path(__file__).resolve().parent / "libdllm_hip.so"
+
+_f32p = C.POINTER(C.c_float)
+_f64p = C.POINTER(C.c_double)
+_i64p = C.POINTER(C.c_int64)
+_sz = C.c_size_t
+_vp = C.c_void_p
+
+
+def _load() -> C.CDLL:
+    if not LIBRARY.exists():
+        raise ImportError(f"{LIBRARY} is not built; run etalii_dllm_amd/build.py (hipcc, gfx950)")
+    lib = C.CDLL(str(LIBRARY))
+    lib.dllm_hip_last_error.restype = C.c_char_p
+    lib.dllm_hip_version.restype = C.c_char_p
+    lib.dllm_hip_trainer_tensor_name.restype = C.c_char_p
+    lib.dllm_hip_trainer_tensor_name.argtypes = [_vp, C.c_int64]
+    for name in ("linear", "linear_backward", "rope", "attention_backward", "cross_entropy",
+                 "embedding_backward", "rms_norm_backward"):
+        getattr(lib, f"dllm_hip_{name}_workspace").restype = _sz
+    lib.dllm_hip_attention_workspace.restype = _sz
+    lib.dllm_hip_linear_workspace.argtypes = [_sz, _sz, _sz]
+    lib.dllm_hip_linear_backward_workspace.argtypes = [_sz, _sz, _sz]
+    lib.dllm_hip_rope_workspace.argtypes = [_sz, _sz]
+    lib.dllm_hip_attention_backward_workspace.argtypes = [_sz, _sz, _sz]
+    lib.dllm_hip_cross_entropy_workspace.argtypes = [_sz]
+    lib.dllm_hip_embedding_backward_workspace.argtypes = [_sz]
+    lib.dllm_hip_rms_norm_backward_workspace.argtypes = [_sz]
+    lib.dllm_hip_alloc.argtypes = [C.POINTER(_vp), _sz]
+    lib.dllm_hip_release.argtypes = [_vp]
+    lib.dllm_hip_upload.argtypes = [_vp, _vp, _sz]
+    lib.dllm_hip_download.argtypes = [_vp, _vp, _sz]
+    lib.dllm_hip_memset.argtypes = [_vp, C.c_int, _sz]
+    lib.dllm_hip_linear.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
+    lib.dllm_hip_rms_norm.argtypes = [_vp, _vp, _vp, _sz, _sz, C.c_double, C.c_int, _vp]
+    lib.dllm_hip_rope.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _sz, _vp]
+    lib.dllm_hip_attention.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_double, C.c_int,
+                                       C.c_int64, _sz, C.c_double, _vp, _sz, _vp]
+    lib.dllm_hip_silu.argtypes = [_vp, _vp, _sz, _vp]
+    lib.dllm_hip_swiglu.argtypes = [_vp, _vp, _vp, _sz, _vp]
+    lib.dllm_hip_linear_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
+    lib.dllm_hip_rms_norm_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, C.c_double, C.c_int, _vp, _sz,
+                                               _vp]
+    lib.dllm_hip_silu_backward.argtypes = [_vp, _vp, _vp, _sz, _vp]
+    lib.dllm_hip_attention_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz,
+                                                C.c_double, C.c_int, C.c_int64, _sz, C.c_double, _vp, _sz, _vp]
+    lib.dllm_hip_cross_entropy.argtypes = [_vp, _vp, _vp, _sz, _sz, C.c_double, _f64p, _vp, _sz, _vp]
+    lib.dllm_hip_embedding_backward.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
+    lib.dllm_hip_sum_squares.argtypes = [_vp, _sz, _f64p, _vp, _sz, _vp]
+    lib.dllm_hip_adamw_step.argtypes = [_vp, _vp, _vp, _vp, _sz] + [C.c_double] * 8 + [_vp]
+    return lib
+
+
+lib = _load()
+
+
+class HipError(RuntimeError):
+    """A HIP runtime failure inside the library."""
+
+
+def check(status: int) -> None:
+    if status == 0:
+        return
+    message = (lib.dllm_hip_last_error() or b"").decode()
+    if status == 1:
+        raise ValueError(message)
+    if status == 3:
+        raise MemoryError(message)
+    raise HipError(message)
+
+
+class Device:
+    """One device allocation (freed with the object)."""
+
+    def __init__(self, nbytes: int) -> None:
+        self.nbytes = int(nbytes)
+        self.ptr = _vp()
+        check(lib.dllm_hip_alloc(C.byref(self.ptr), max(self.nbytes, 1)))
+
+    @classmethod
+    def of(cls, array: np.ndarray) -> Device:
+        a = np.ascontiguousarray(array)
+        d = cls(a.nbytes)
+        if a.nbytes:
+            check(lib.dllm_hip_upload(d.ptr, a.ctypes.data, a.nbytes))
+        return d
+
+    def download(self, shape, dtype=np.float32) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        if out.nbytes:
+            check(lib.dllm_hip_download(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def __del__(self) -> None:
+        if getattr(self, "ptr", None) is not None and self.ptr.value:
+            lib.dllm_hip_release(self.ptr)
+            self.ptr = _vp()
+
+
+def _f32(values) -> np.ndarray:
+    return np.ascontiguousarray(values, dtype=np.float32)
+
+
+def _rows(x: np.ndarray) -> int:
+    return int(np.prod(x.shape[:-1])) if x.ndim > 1 else 1
+
+
+# ---- forward kernels (cpp/kernels.cpp) ----
+
+def linear(x, weight, bias=None) -> np.ndarray:
+    """kernels.cpp:220-238: x[..., in] @ weight[out, in]^T (+ bias), k ascending in double."""
+    x, w = _f32(x), _f32(weight)
+    if x.ndim < 1:
+        raise ValueError("x must have at least one dimension")
+    if w.ndim != 2:
+        raise ValueError("weight must be [out_features, in_features]")
+    out_f, in_f = w.shape
+    if x.shape[-1] != in_f:
+        raise ValueError("weight in_features does not match the last dimension of x")
+    if bias is not None and _f32(bias).shape[0] != out_f:
+        raise ValueError("bias length must equal out_features")
+    rows = _rows(x)
+    ws = Device(lib.dllm_hip_linear_workspace(rows, in_f, out_f))
+    dx, dw = Device.of(x), Device.of(w)
+    db = Device.of(_f32(bias)) if bias is not None else None
+    out = Device(rows * out_f * 4)
+    check(lib.dllm_hip_linear(dx.ptr, dw.ptr, db.ptr if db else None, out.ptr, rows, in_f, out_f, ws.ptr, ws.nbytes,
+                              None))
+    return out.download((*x.shape[:-1], out_f))
+
+
+def rms_norm(x, weight=None, eps=1e-6, add_unit_offset=False) -> np.ndarray:
+    """kernels.cpp:598-611."""
+    x = _f32(x)
+    dim = x.shape[-1]
+    if weight is not None and _f32(weight).shape[0] != dim:
+        raise ValueError("weight length must equal the last dimension of x")
+    dx = Device.of(x)
+    dw = Device.of(_f32(weight)) if weight is not None else None
+    out = Device(x.nbytes)
+    check(lib.dllm_hip_rms_norm(dx.ptr, dw.ptr if dw else None, out.ptr, _rows(x), dim, float(eps),
+                                int(add_unit_offset), None))
+    return out.download(x.shape)
+
+
+def rope(x, positions, inv_freq, interleaved=False, inverse=False) -> np.ndarray:
+    """kernels.cpp:662-679."""
+    x = _f32(x)
+    pos = np.ascontiguousarray(positions, dtype=np.int64)
+    freqs = np.ascontiguousarray(inv_freq, dtype=np.float64)
+    if x.ndim != 3:
+        raise ValueError("x must be [tokens, heads, head_dim]")
+    tokens, heads, head_dim = x.shape
+    rotary = 2 * len(freqs)
+    if len(pos) != tokens:
+        raise ValueError("positions must have one entry per token")
+    if rotary > head_dim:
+        raise ValueError("2 * len(inv_freq) must not exceed head_dim")
+    ws = Device(lib.dllm_hip_rope_workspace(tokens, rotary))
+    dx, dp, df, out = Device.of(x), Device.of(pos), Device.of(freqs), Device(x.nbytes)
+    check(lib.dllm_hip_rope(dx.ptr, dp.ptr, df.ptr, out.ptr, tokens, heads, head_dim, rotary, int(interleaved),
+                            int(inverse), ws.ptr, ws.nbytes, None))
+    return out.download(x.shape)
+
+
+def _attention_args(q, k, v, q_offset):
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("q, k and v must be [length, heads, dim]")
+    if v.shape[0] != k.shape[0] or v.shape[1] != k.shape[1]:
+        raise ValueError("k and v must have the same length and heads")
+    if q.shape[2] != k.shape[2]:
+        raise ValueError("q and k must have the same head_dim")
+    if k.shape[1] == 0 or q.shape[1] % k.shape[1]:
+        raise ValueError("q heads must be a multiple of kv heads")
+    if q_offset < 0:
+        q_offset = k.shape[0] - q.shape[0]
+    if q_offset < 0:
+        raise ValueError("q_offset must be non-negative")
+    return q_offset
+
+
+def attention(q, k, v, scale, causal=True, q_offset=-1, window=0, softcap=0.0, reference=False) -> np.ndarray:
+    """kernels.cpp:680-705 (`reference` selects the same bits on the CPU there; it has no effect here)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    q_offset = _attention_args(q, k, v, q_offset)
+    out_shape = (q.shape[0], q.shape[1], v.shape[2])
+    ws = Device(lib.dllm_hip_attention_workspace())
+    dq, dk, dv, out = Device.of(q), Device.of(k), Device.of(v), Device(int(np.prod(out_shape)) * 4)
+    check(lib.dllm_hip_attention(dq.ptr, dk.ptr, dv.ptr, out.ptr, q.shape[0], k.shape[0], q.shape[1], k.shape[1],
+                                 q.shape[2], v.shape[2], float(scale), int(causal), int(q_offset), int(window),
+                                 float(softcap), ws.ptr, ws.nbytes, None))
+    return out.download(out_shape)
+
+
+def silu(x) -> np.ndarray:
+    x = _f32(x)
+    dx, out = Device.of(x), Device(x.nbytes)
+    check(lib.dllm_hip_silu(dx.ptr, out.ptr, x.size, None))
+    return out.download(x.shape)
+
+
+def swiglu(gate, up, kind=0) -> np.ndarray:
+    """kernels.cpp:633-649 (kind 0, silu; the tanh-GELU kind is outside this backend's families)."""
+    gate, up = _f32(gate), _f32(up)
+    if gate.size != up.size:
+        raise ValueError("gate and up must have the same size")
+    if kind != 0:
+        raise ValueError("kind must be silu (0)")
+    dg, du, out = Device.of(gate), Device.of(up), Device(gate.nbytes)
+    check(lib.dllm_hip_swiglu(dg.ptr, du.ptr, out.ptr, gate.size, None))
+    return out.download(gate.shape)
+
+
+# ---- backward kernels ----
+
+def linear_backward(x, weight, dy, with_bias=False):
+    """kernels.cpp:811-837: (dx, dweight, dbias or None)."""
+    x, w, dy = _f32(x), _f32(weight), _f32(dy)
+    if w.ndim != 2:
+        raise ValueError("weight must be [out_features, in_features]")
+    out_f, in_f = w.shape
+    if x.ndim < 1 or x.shape[-1] != in_f:
+        raise ValueError("x does not match the weight")
+    if dy.ndim != x.ndim or dy.shape[-1] != out_f:
+        raise ValueError("dy does not match the weight")
+    rows = _rows(x)
+    if _rows(dy) != rows:
+        raise ValueError("x and dy must have the same leading dimensions")
+    ws = Device(lib.dllm_hip_linear_backward_workspace(rows, in_f, out_f))
+    d_x, d_w, d_dy = Device.of(x), Device.of(w), Device.of(dy)
+    gx, gw = Device(x.nbytes), Device(w.nbytes)
+    gb = Device(out_f * 4) if with_bias else None
+    check(lib.dllm_hip_linear_backward(d_x.ptr, d_w.ptr, d_dy.ptr, gx.ptr, gw.ptr, gb.ptr if gb else None, rows,
+                                       in_f, out_f, ws.ptr, ws.nbytes, None))
+    return gx.download(x.shape), gw.download(w.shape), gb.download((out_f,)) if gb else None
+
+
+def rms_norm_backward(x, weight, dy, eps=1e-6, add_unit_offset=False):
+    """kernels.cpp:839-856: (dx, dweight)."""
+    x, dy = _f32(x), _f32(dy)
+    dim = x.shape[-1]
+    if dy.size != x.size or dy.shape[-1] != dim:
+        raise ValueError("dy must have the shape of x")
+    if weight is not None and _f32(weight).shape[0] != dim:
+        raise ValueError("weight length must equal the last dimension of x")
+    rows = _rows(x)
+    ws = Device(lib.dllm_hip_rms_norm_backward_workspace(rows))
+    d_x, d_dy = Device.of(x), Device.of(dy)
+    d_w = Device.of(_f32(weight)) if weight is not None else None
+    gx, gw = Device(x.nbytes), Device(dim * 4)
+    check(lib.dllm_hip_rms_norm_backward(d_x.ptr, d_w.ptr if d_w else None, d_dy.ptr, gx.ptr, gw.ptr, rows, dim,
+                                         float(eps), int(add_unit_offset), ws.ptr, ws.nbytes, None))
+    return gx.download(x.shape), gw.download((dim,))
+
+
+def silu_backward(x, dy) -> np.ndarray:
+    x, dy = _f32(x), _f32(dy)
+    if x.size != dy.size:
+        raise ValueError("x and dy must have the same size")
+    d_x, d_dy, out = Device.of(x), Device.of(dy), Device(x.nbytes)
+    check(lib.dllm_hip_silu_backward(d_x.ptr, d_dy.ptr, out.ptr, x.size, None))
+    return out.download(x.shape)
+
+
+def attention_backward(q, k, v, dout, scale, causal=True, q_offset=-1, window=0, softcap=0.0):
+    """kernels.cpp:930-959: (dq, dk, dv)."""
+    q, k, v, dout = _f32(q), _f32(k), _f32(v), _f32(dout)
+    q_offset = _attention_args(q, k, v, q_offset)
+    if dout.ndim != 3 or dout.shape != (q.shape[0], q.shape[1], v.shape[2]):
+        raise ValueError("dout must be [q_len, q_heads, value_dim]")
+    ws = Device(lib.dllm_hip_attention_backward_workspace(q.shape[0], k.shape[0], q.shape[1]))
+    d = [Device.of(a) for a in (q, k, v, dout)]
+    gq, gk, gv = Device(q.nbytes), Device(k.nbytes), Device(v.nbytes)
+    check(lib.dllm_hip_attention_backward(d[0].ptr, d[1].ptr, d[2].ptr, d[3].ptr, gq.ptr, gk.ptr, gv.ptr, q.shape[0],
+                                          k.shape[0], q.shape[1], k.shape[1], q.shape[2], v.shape[2], float(scale),
+                                          int(causal), int(q_offset), int(window), float(softcap), ws.ptr, ws.nbytes,
+                                          None))
+    return gq.download(q.shape), gk.download(k.shape), gv.download(v.shape)
+
+
+def cross_entropy(logits, targets, scale=1.0):
+    """kernels.cpp:991-1003: (summed loss, dlogits * scale)."""
+    logits = _f32(logits)
+    targets = np.ascontiguousarray(targets, dtype=np.int64)
+    if logits.ndim != 2:
+        raise ValueError("logits must be [rows, vocab]")
+    if targets.shape[0] != logits.shape[0]:
+        raise ValueError("targets must have one entry per row")
+    rows, vocab = logits.shape
+    ws = Device(lib.dllm_hip_cross_entropy_workspace(rows))
+    dl, dt, out = Device.of(logits), Device.of(targets), Device(logits.nbytes)
+    loss = C.c_double()
+    check(lib.dllm_hip_cross_entropy(dl.ptr, dt.ptr, out.ptr, rows, vocab, float(scale), C.byref(loss), ws.ptr,
+                                     ws.nbytes, None))
+    return loss.value, out.download(logits.shape)
+
+
+def embedding_backward(dy, tokens, vocabulary_size) -> np.ndarray:
+    """kernels.cpp:1029-1039."""
+    dy = _f32(dy)
+    tokens = np.ascontiguousarray(tokens, dtype=np.int64)
+    if dy.ndim != 2 or dy.shape[0] != tokens.shape[0]:
+        raise ValueError("dy must be [len(tokens), dim]")
+    rows, dim = dy.shape
+    ws = Device(lib.dllm_hip_embedding_backward_workspace(rows))
+    d_dy, d_t, out = Device.of(dy), Device.of(tokens), Device(vocabulary_size * dim * 4)
+    check(lib.dllm_hip_embedding_backward(d_dy.ptr, d_t.ptr, out.ptr, rows, dim, int(vocabulary_size), ws.ptr,
+                                          ws.nbytes, None))
+    return out.download((int(vocabulary_size), dim))
+
+
+def sum_squares(values) -> float:
+    """kernels.cpp:1041-1043."""
+    v = _f32(values)
+    d, ws = Device.of(v), Device(8)
+    result = C.c_double()
+    check(lib.dllm_hip_sum_squares(d.ptr, v.size, C.byref(result), ws.ptr, ws.nbytes, None))
+    return result.value
+
+
+def adamw_step(param, grad, m, v, lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2,
+               grad_scale=1.0) -> None:
+    """kernels.cpp:1045-1057: in place on param, m and v (float32 C-contiguous arrays)."""
+    for a in (param, m, v):
+        if a.dtype != np.float32 or not a.flags.c_contiguous:
+            raise ValueError("param, m and v must be C-contiguous float32 arrays")
+    g = _f32(grad)
+    n = param.size
+    if g.size != n or m.size != n or v.size != n:
+        raise ValueError("param, grad, m and v must have one size")
+    dp, dg, dm, dv = Device.of(param), Device.of(g), Device.of(m), Device.of(v)
+    check(lib.dllm_hip_adamw_step(dp.ptr, dg.ptr, dm.ptr, dv.ptr, n, float(lr), float(beta1), float(beta2),
+                                  float(eps), float(weight_decay), float(bias_correction1), float(bias_correction2),
+                                  float(grad_scale), None))
+    param[...] = dp.download(param.shape)
+    m[...] = dm.download(m.shape)
+    v[...] = dv.download(v.shape)
+
+
+def attention_scale(head_dim: int) -> float:
+    """architecture.py:311-312: 1 / sqrt(head_dim)."""
+    return 1.0 / math.sqrt(head_dim)

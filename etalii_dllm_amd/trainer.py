@@ -1,0 +1,147 @@
+"""Device-resident fine-tuning steps on the MI355X: the host-side mirror of the reference's training loop pieces
+(FineTuner._language_model_gradients and AdamW.step, src/etalii_dllm/training/trainer.py:290-335 and
+training/optimizer.py:82-109) over the dllm_hip_trainer C ABI.
+
+Weights, gradients, moments and activations stay on the GPU between steps; only token ids go in and the loss and
+gradient norm come out.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from etalii_dllm_amd.kernels import check, lib
+
+_i64p = C.POINTER(C.c_int64)
+
+
+class DecoderConfig(C.Structure):
+    """dllm_hip_decoder_config: the TransformerConfig fields a decoder step reads (architecture.py)."""
+
+    _fields_ = [(name, C.c_int64) for name in (
+        "vocab", "hidden", "intermediate", "layers", "heads", "kv_heads", "head_dim", "attention_bias", "qk_norm",
+        "sliding_window", "tie_embeddings", "experts", "experts_per_token", "normalize_expert_weights",
+        "expert_intermediate", "rotary_dim")] + [
+        ("rms_norm_eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double)]
+
+
+class AdamWArgs(C.Structure):
+    _fields_ = [(name, C.c_double) for name in (
+        "learning_rate", "beta1", "beta2", "eps", "weight_decay", "max_grad_norm", "router_aux_loss")] + [
+        ("step", C.c_int64)]
+
+
+lib.dllm_hip_trainer_create.argtypes = [C.POINTER(DecoderConfig), C.c_int64, C.c_int64, C.c_int64,
+                                        C.POINTER(C.c_void_p)]
+lib.dllm_hip_trainer_destroy.argtypes = [C.c_void_p]
+lib.dllm_hip_trainer_tensor.argtypes = [C.c_void_p, C.c_char_p, C.c_int, C.POINTER(C.c_void_p),
+                                        C.POINTER(C.c_int64)]
+lib.dllm_hip_trainer_tensor_count.argtypes = [C.c_void_p, C.POINTER(C.c_int64)]
+lib.dllm_hip_trainer_gradients.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_int64, C.c_double, C.c_double,
+                                           C.POINTER(C.c_double), C.c_void_p]
+lib.dllm_hip_trainer_step.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_int64, C.POINTER(AdamWArgs),
+                                      C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_void_p]
+
+
+@dataclass(frozen=True)
+class Decoder:
+    """A pre-norm decoder's shape (architecture.py's TransformerConfig for the Llama/Qwen2/Qwen3 families)."""
+
+    vocab: int
+    hidden: int
+    intermediate: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rms_norm_eps: float
+    rope_theta: float
+    tie_embeddings: bool
+    attention_bias: bool = False
+    qk_norm: int = 0
+    sliding_window: int = 0
+
+    def native(self) -> DecoderConfig:
+        return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
+                             self.head_dim, int(self.attention_bias), self.qk_norm, self.sliding_window,
+                             int(self.tie_embeddings), 0, 0, 0, 0, self.head_dim, self.rms_norm_eps, self.rope_theta,
+                             1.0 / float(np.sqrt(np.float64(self.head_dim))))
+
+
+def _windows(windows):
+    flat = np.ascontiguousarray([t for w in windows for t in w], dtype=np.int64)
+    lengths = np.ascontiguousarray([len(w) for w in windows], dtype=np.int64)
+    offsets = np.ascontiguousarray(np.concatenate([[0], np.cumsum(lengths)[:-1]]), dtype=np.int64)
+    return flat, offsets, lengths
+
+
+class Trainer:
+    """One model's training state on the GPU."""
+
+    PARAM, GRAD, M, V = 0, 1, 2, 3
+
+    def __init__(self, decoder: Decoder, max_tokens: int, max_windows: int, max_window_tokens: int) -> None:
+        self.decoder = decoder
+        self._cfg = decoder.native()
+        handle = C.c_void_p()
+        check(lib.dllm_hip_trainer_create(C.byref(self._cfg), max_tokens, max_windows, max_window_tokens,
+                                          C.byref(handle)))
+        self.handle = handle
+        count = C.c_int64()
+        check(lib.dllm_hip_trainer_tensor_count(handle, C.byref(count)))
+        self.names = [lib.dllm_hip_trainer_tensor_name(handle, i).decode() for i in range(count.value)]
+
+    def close(self) -> None:
+        if self.handle:
+            lib.dllm_hip_trainer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self) -> None:
+        self.close()
+
+    def _tensor(self, name: str, which: int):
+        ptr, numel = C.c_void_p(), C.c_int64()
+        check(lib.dllm_hip_trainer_tensor(self.handle, name.encode(), which, C.byref(ptr), C.byref(numel)))
+        return ptr, numel.value
+
+    def set(self, name: str, values: np.ndarray, which: int = 0) -> None:
+        a = np.ascontiguousarray(values, dtype=np.float32)
+        ptr, numel = self._tensor(name, which)
+        if a.size != numel:
+            raise ValueError(f"{name}: expected {numel} values, got {a.size}")
+        check(lib.dllm_hip_upload(ptr, a.ctypes.data, a.nbytes))
+
+    def get(self, name: str, shape, which: int = 0) -> np.ndarray:
+        ptr, numel = self._tensor(name, which)
+        out = np.empty(shape, np.float32)
+        if out.size != numel:
+            raise ValueError(f"{name}: has {numel} values")
+        check(lib.dllm_hip_download(out.ctypes.data, ptr, out.nbytes))
+        return out
+
+    def load(self, tensors: dict[str, np.ndarray], which: int = 0) -> None:
+        for name, values in tensors.items():
+            self.set(name, values, which)
+
+    def gradients(self, windows, scale: float = 1.0) -> float:
+        """DecoderGradients over each window, summed in window order; returns the summed loss."""
+        flat, offsets, lengths = _windows(windows)
+        loss = C.c_double()
+        check(lib.dllm_hip_trainer_gradients(self.handle, flat.ctypes.data_as(_i64p), offsets.ctypes.data_as(_i64p),
+                                             lengths.ctypes.data_as(_i64p), len(windows), scale, 0.0, C.byref(loss),
+                                             None))
+        return loss.value
+
+    def step(self, windows, learning_rate: float, step: int, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
+             max_grad_norm=1.0) -> tuple[float, float]:
+        """One fine-tuning step (trainer.py:290-310) at the given learning rate: (mean loss, gradient norm)."""
+        flat, offsets, lengths = _windows(windows)
+        args = AdamWArgs(learning_rate, beta1, beta2, eps, weight_decay, max_grad_norm, 0.0, step)
+        loss, norm = C.c_double(), C.c_double()
+        check(lib.dllm_hip_trainer_step(self.handle, flat.ctypes.data_as(_i64p), offsets.ctypes.data_as(_i64p),
+                                        lengths.ctypes.data_as(_i64p), len(windows), C.byref(args), C.byref(loss),
+                                        C.byref(norm), None))
+        return loss.value, norm.value

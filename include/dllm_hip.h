@@ -1,0 +1,183 @@
+/*
+ * dllm_hip: MI355X (gfx950) backend for EtAlii.Dllm's fine-tuning hot path (the backward pass and the AdamW step
+ * behind `dllm finetune`), as a C ABI over hand-written HIP kernels.
+ *
+ * Every result is bit-identical to the reference CPU kernels (cpp/include/dllm/{nn,grad,math}.hpp of EtAlii.Dllm)
+ * on the same inputs, for any batch size, row count or CU count: each output keeps the reference's one double
+ * accumulation in its fixed order.
+ *
+ * Conventions
+ *  - Array arguments are DEVICE pointers (hipMalloc'd or equivalent), C-contiguous, float32 unless stated; sizes are
+ *    element counts. `stream` is a hipStream_t passed as void* (NULL = the default stream). Calls are asynchronous
+ *    unless documented to return a host value.
+ *  - Return value: 0 on success; 1 invalid argument (where the reference binding raises ValueError); 2 HIP error;
+ *    3 out of device memory. dllm_hip_last_error() gives the calling thread's last message.
+ *  - Entry points that need scratch memory take (workspace, workspace_bytes); the matching *_workspace() query gives
+ *    the bytes needed. The kernel entry points never allocate; the trainer allocates once, at creation.
+ *
+ * Each kernel entry point names the reference interface it replaces: the Python binding in cpp/kernels.cpp and the
+ * C++ kernel it wraps.
+ */
+#ifndef DLLM_HIP_H
+#define DLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status, device plumbing (for hosts without their own GPU allocator) ---- */
+const char* dllm_hip_last_error(void);
+const char* dllm_hip_version(void);
+int dllm_hip_device_count(int* count);
+int dllm_hip_alloc(void** device_ptr, size_t bytes);
+int dllm_hip_release(void* device_ptr);
+int dllm_hip_upload(void* device_dst, const void* host_src, size_t bytes);
+int dllm_hip_download(void* host_dst, const void* device_src, size_t bytes);
+int dllm_hip_memset(void* device_ptr, int value, size_t bytes);
+int dllm_hip_synchronize(void);
+
+/* ---- forward kernels ---- */
+
+/* linear: out[rows, out_f] = x[rows, in_f] @ weight[out_f, in_f]^T (+ bias); k ascending in double, bias added before
+ * the one rounding. Replaces kernels.cpp:220-238 `linear` (nn.hpp:28-50, 348-359). */
+size_t dllm_hip_linear_workspace(size_t rows, size_t in_features, size_t out_features);
+int dllm_hip_linear(const float* x, const float* weight, const float* bias, float* out, size_t rows,
+                    size_t in_features, size_t out_features, void* workspace, size_t workspace_bytes, void* stream);
+
+/* rms_norm over the last dimension (weight may be NULL). Replaces kernels.cpp:598-611 `rms_norm` (nn.hpp:391-408). */
+int dllm_hip_rms_norm(const float* x, const float* weight, float* out, size_t rows, size_t dim, double eps,
+                      int add_unit_offset, void* stream);
+
+/* rope of x[tokens, heads, head_dim] at positions (int64) with inv_freq (double, rotary_dim / 2 entries).
+ * Replaces kernels.cpp:662-679 `rope` (nn.hpp:501-530); inverse = 1 is the RoPE backward. */
+size_t dllm_hip_rope_workspace(size_t tokens, size_t rotary_dim);
+int dllm_hip_rope(const float* x, const int64_t* positions, const double* inv_freq, float* out, size_t tokens,
+                  size_t heads, size_t head_dim, size_t rotary_dim, int interleaved, int inverse, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* Causal / windowed grouped-query attention, q[q_len, q_heads, head_dim], k[kv_len, kv_heads, head_dim],
+ * v[kv_len, kv_heads, value_dim] -> out[q_len, q_heads, value_dim]; q_offset < 0 means kv_len - q_len.
+ * Replaces kernels.cpp:680-705 `attention` (nn.hpp:761-796). Key lengths up to 2048. */
+size_t dllm_hip_attention_workspace(void);
+int dllm_hip_attention(const float* q, const float* k, const float* v, float* out, size_t q_len, size_t kv_len,
+                       size_t q_heads, size_t kv_heads, size_t head_dim, size_t value_dim, double scale, int causal,
+                       int64_t q_offset, size_t window, double softcap, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* silu elementwise (kernels.cpp:628, nn.hpp:467-470) and swiglu = f32(silu(gate)) * up (kernels.cpp:633-649 with
+ * kind 0, nn.hpp:489-492). */
+int dllm_hip_silu(const float* x, float* out, size_t n, void* stream);
+int dllm_hip_swiglu(const float* gate, const float* up, float* out, size_t n, void* stream);
+
+/* ---- backward kernels ---- */
+
+/* (dx, dweight, dbias) of linear; dx, dweight, dbias may each be NULL. Replaces kernels.cpp:811-837
+ * `linear_backward` (grad.hpp:26-72). */
+size_t dllm_hip_linear_backward_workspace(size_t rows, size_t in_features, size_t out_features);
+int dllm_hip_linear_backward(const float* x, const float* weight, const float* dy, float* dx, float* dweight,
+                             float* dbias, size_t rows, size_t in_features, size_t out_features, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* (dx, dweight) of rms_norm; dweight may be NULL. Replaces kernels.cpp:839-856 `rms_norm_backward`
+ * (grad.hpp:79-111). */
+size_t dllm_hip_rms_norm_backward_workspace(size_t rows);
+int dllm_hip_rms_norm_backward(const float* x, const float* weight, const float* dy, float* dx, float* dweight,
+                               size_t rows, size_t dim, double eps, int add_unit_offset, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* dy * silu'(x) elementwise. Replaces kernels.cpp:890-901 `silu_backward` (grad.hpp:177-181). */
+int dllm_hip_silu_backward(const float* x, const float* dy, float* out, size_t n, void* stream);
+
+/* (dq, dk, dv) of attention. Replaces kernels.cpp:930-959 `attention_backward` (grad.hpp:206-301). */
+size_t dllm_hip_attention_backward_workspace(size_t q_len, size_t kv_len, size_t q_heads);
+int dllm_hip_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq,
+                                float* dk, float* dv, size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads,
+                                size_t head_dim, size_t value_dim, double scale, int causal, int64_t q_offset,
+                                size_t window, double softcap, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Softmax cross-entropy of logits[rows, vocab] against int64 targets (negative = ignored): dlogits * scale, and the
+ * summed loss written to *loss (HOST pointer; the call waits for the stream). A target >= vocab is an invalid
+ * argument, as in the reference. Replaces kernels.cpp:991-1003 `cross_entropy` (grad.hpp:395-426). */
+size_t dllm_hip_cross_entropy_workspace(size_t rows);
+int dllm_hip_cross_entropy(const float* logits, const int64_t* targets, float* dlogits, size_t rows, size_t vocab,
+                           double scale, double* loss, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Embedding gradient out[vocab, dim]: dy rows summed per token id in position order. Reads the token ids back to the
+ * host to group them (the call waits for the stream); an id outside [0, vocab) is an invalid argument.
+ * Replaces kernels.cpp:1029-1039 `embedding_backward` (grad.hpp:431-464). */
+size_t dllm_hip_embedding_backward_workspace(size_t rows);
+int dllm_hip_embedding_backward(const float* dy, const int64_t* tokens, float* out, size_t rows, size_t dim,
+                                size_t vocab, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Sum of squares in index order with a double accumulator, written to *result (HOST pointer; waits). The workspace
+ * holds one double. Replaces kernels.cpp:1041-1043 `sum_squares` (grad.hpp:467-473). */
+int dllm_hip_sum_squares(const float* values, size_t n, double* result, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* One in-place AdamW step. Replaces kernels.cpp:1045-1057 `adamw_step` (grad.hpp:481-495). */
+int dllm_hip_adamw_step(float* param, const float* grad, float* m, float* v, size_t n, double lr, double beta1,
+                        double beta2, double eps, double weight_decay, double bias_correction1,
+                        double bias_correction2, double grad_scale, void* stream);
+
+/* ---- the device-resident fine-tuning step ----
+ *
+ * Replaces the Python step the reference runs through those kernels: FineTuner.train_step
+ * (src/etalii_dllm/training/trainer.py:290-335) over DecoderGradients (training/backprop.py:88-118, 183-357, 399-527)
+ * and AdamW.step (training/optimizer.py:82-109). Weights, gradients, AdamW moments and every activation stay in
+ * device memory; all windows of a step run as one packed batch (row-local work is batch-invariant), and every
+ * reduction over a window's rows is kept per window and summed across windows in float in window order, exactly
+ * as the reference sums its per-window gradient sets.
+ */
+typedef struct {
+    int64_t vocab, hidden, intermediate, layers, heads, kv_heads, head_dim;
+    int64_t attention_bias;   /* q/k/v biases (Qwen2) */
+    int64_t qk_norm;          /* 0 none, 1 per head (Qwen3), 2 whole projection (OLMo 2) */
+    int64_t sliding_window;   /* 0 = full causal attention */
+    int64_t tie_embeddings;
+    int64_t experts, experts_per_token, normalize_expert_weights, expert_intermediate; /* 0 experts: dense */
+    int64_t rotary_dim;
+    double rms_norm_eps, rope_theta, attention_scale;
+} dllm_hip_decoder_config;
+
+typedef struct dllm_hip_trainer dllm_hip_trainer;
+
+/* Allocates every buffer for steps of up to max_tokens tokens (rows, summed over windows) in up to max_windows
+ * windows, each at most max_window_tokens long. Weights start at zero; moments at zero. */
+int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_tokens, int64_t max_windows,
+                            int64_t max_window_tokens, dllm_hip_trainer** trainer);
+int dllm_hip_trainer_destroy(dllm_hip_trainer* trainer);
+
+/* The device buffer of one tensor, by the reference's tensor name (architecture.py:418-468), e.g.
+ * "layers.3.attention.q.weight": which = 0 parameter, 1 gradient (of the last step), 2 first moment, 3 second moment.
+ * Parameters written through this pointer take effect at the next step. */
+int dllm_hip_trainer_tensor(dllm_hip_trainer* trainer, const char* name, int which, float** device_ptr,
+                            int64_t* numel);
+/* Tensor names in natural order (modelfile.py:40-47); index in [0, count). */
+int dllm_hip_trainer_tensor_count(dllm_hip_trainer* trainer, int64_t* count);
+const char* dllm_hip_trainer_tensor_name(dllm_hip_trainer* trainer, int64_t index);
+
+/* Gradients only (DecoderGradients.losses_and_gradients summed over windows in batch order): tokens is a HOST int64
+ * array; window w is tokens[offsets[w] .. offsets[w] + lengths[w]) and predicts its own next tokens (inputs are the
+ * first lengths[w] - 1 tokens). scale multiplies the summed cross-entropy; *loss (host) receives the summed loss. */
+int dllm_hip_trainer_gradients(dllm_hip_trainer* trainer, const int64_t* tokens, const int64_t* offsets,
+                               const int64_t* lengths, int64_t windows, double scale, double router_scale,
+                               double* loss, void* stream);
+
+typedef struct {
+    double learning_rate, beta1, beta2, eps, weight_decay, max_grad_norm, router_aux_loss;
+    int64_t step; /* 1-based number of this update */
+} dllm_hip_adamw;
+
+/* One full step: gradients with scale 1 / (sum of lengths - windows), the global norm, clipping and AdamW in
+ * natural tensor order. *loss gets the mean loss, *grad_norm the norm before clipping (host pointers; waits). */
+int dllm_hip_trainer_step(dllm_hip_trainer* trainer, const int64_t* tokens, const int64_t* offsets,
+                          const int64_t* lengths, int64_t windows, const dllm_hip_adamw* adamw, double* loss,
+                          double* grad_norm, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,156 @@
+"""GPU parity: every kernel entry point of the C ABI (through etalii_dllm_amd.kernels) against the CPU oracle, bit for
+bit, on seeded ordinary and adversarial inputs and the reference tests' edge cases (ignored targets, ragged and
+single rows, windows, soft-caps, offsets, errors)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def K():
+    from etalii_dllm_amd import kernels
+
+    return kernels
+
+
+@pytest.fixture(scope="module")
+def ora():
+    return O.oracle_kernels()
+
+
+def adversarial(seed: int, *shape: int) -> np.ndarray:
+    values = O.gaussian(seed, *shape).astype(np.float64)
+    exponents = O.gaussian(seed + 1000, *shape).astype(np.float64)
+    out = values * np.power(10.0, np.clip(np.round(exponents * 8), -30, 20))
+    out[np.abs(O.gaussian(seed + 2000, *shape)) < 0.05] = 0.0
+    return out.astype(np.float32)
+
+
+def assert_same(a, b, what=""):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape, (what, a.shape, b.shape)
+    if a.tobytes() != b.tobytes():
+        diff = np.flatnonzero(a.view(np.uint32).ravel() != b.view(np.uint32).ravel()) if a.dtype == np.float32 else []
+        raise AssertionError(f"{what}: {len(diff)} of {a.size} elements differ, first at {diff[:5]}")
+
+
+@pytest.mark.parametrize(("rows", "inf", "outf"), [(1, 37, 19), (7, 64, 259), (64, 128, 256), (130, 96, 64)])
+@pytest.mark.parametrize("kind", ["gaussian", "adversarial"])
+def test_linear_forward_and_backward(K, ora, rows, inf, outf, kind):
+    make = adversarial if kind == "adversarial" else O.gaussian
+    x, w, b, dy = make(1, rows, inf), make(2, outf, inf), make(3, outf), make(4, rows, outf)
+    assert_same(K.linear(x, w, b), ora.linear(x, w, b), "linear+bias")
+    assert_same(K.linear(x, w), ora.linear(x, w), "linear")
+    for got, want, name in zip(K.linear_backward(x, w, dy, True), ora.linear_backward(x, w, dy, True),
+                               ("dx", "dw", "db")):
+        assert_same(got, want, name)
+    dx, dw, db = K.linear_backward(x, w, dy)
+    assert db is None
+
+
+def test_linear_rows_are_batch_invariant(K):
+    """The bits of a row of linear / dx do not depend on how many rows are computed with it (M swept)."""
+    w, dyw = O.gaussian(5, 300, 160), O.gaussian(6, 300, 160)
+    x_all, dy_all = O.gaussian(7, 2048, 160), O.gaussian(8, 2048, 300)
+    full = K.linear(x_all, w)
+    dfull = K.linear_backward(x_all, dyw, dy_all)[0]
+    for m in (1, 7, 64):
+        assert_same(K.linear(x_all[:m], w), full[:m], f"linear M={m}")
+        assert_same(K.linear_backward(x_all[:m], dyw, dy_all[:m])[0], dfull[:m], f"dx M={m}")
+
+
+@pytest.mark.parametrize(("rows", "dim"), [(1, 8), (9, 48), (33, 576), (5, 1536)])
+def test_rms_norm_forward_and_backward(K, ora, rows, dim):
+    x, w, dy = O.gaussian(5, rows, dim, scale=3.0), O.gaussian(6, dim), O.gaussian(7, rows, dim)
+    assert_same(K.rms_norm(x, w, 1e-5), ora.rms_norm(x, w, 1e-5), "rms_norm")
+    assert_same(K.rms_norm(x, w, 1e-6, True), ora.rms_norm(x, w, 1e-6, True), "rms_norm unit offset")
+    assert_same(K.rms_norm(x, None, 1e-6), ora.rms_norm(x, None, 1e-6), "rms_norm no weight")
+    for got, want, name in zip(K.rms_norm_backward(x, w, dy, 1e-5), ora.rms_norm_backward(x, w, dy, 1e-5),
+                               ("dx", "dw")):
+        assert_same(got, want, name)
+    for got, want, name in zip(K.rms_norm_backward(x, w, dy, 1e-6, True),
+                               ora.rms_norm_backward(x, w, dy, 1e-6, True), ("dx unit", "dw unit")):
+        assert_same(got, want, name)
+
+
+@pytest.mark.parametrize(("rotary", "theta"), [(16, 1e6), (8, 1e4), (128, 1e6)])
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope(K, ora, rotary, theta, interleaved):
+    hd = max(16, rotary)
+    x = O.gaussian(9, 11, 3, hd)
+    pos = np.arange(11, dtype=np.int64) * 131
+    inv = O.rope_inv_freq(rotary, theta)
+    for inverse in (False, True):
+        assert_same(K.rope(x, pos, inv, interleaved, inverse), ora.rope(x, pos, inv, interleaved, inverse),
+                    f"rope inverse={inverse}")
+
+
+@pytest.mark.parametrize(("q_len", "kv_len", "heads", "kvh", "hd", "window", "softcap", "offset"), [
+    (9, 9, 6, 2, 8, 0, 0.0, 0),
+    (5, 9, 6, 2, 8, 0, 0.0, 4),
+    (9, 9, 6, 3, 8, 3, 0.0, 0),
+    (9, 9, 4, 4, 8, 0, 0.7, 0),
+    (130, 130, 4, 2, 64, 0, 0.0, 0),
+    (70, 70, 2, 1, 128, 17, 0.0, 0),
+])
+def test_attention_forward_and_backward(K, ora, q_len, kv_len, heads, kvh, hd, window, softcap, offset):
+    q, k, v = O.gaussian(12, q_len, heads, hd), O.gaussian(13, kv_len, kvh, hd), O.gaussian(14, kv_len, kvh, hd)
+    dout = O.gaussian(15, q_len, heads, hd)
+    scale = 1.0 / np.sqrt(hd)
+    assert_same(K.attention(q, k, v, scale, True, offset, window, softcap),
+                ora.attention(q, k, v, scale, True, offset, window, softcap), "attention")
+    got = K.attention_backward(q, k, v, dout, scale, True, offset, window, softcap)
+    want = ora.attention_backward(q, k, v, dout, scale, True, offset, window, softcap)
+    for g, w, name in zip(got, want, ("dq", "dk", "dv")):
+        assert_same(g, w, name)
+
+
+def test_elementwise(K, ora):
+    g, up = O.gaussian(8, 5000, scale=6.0), O.gaussian(11, 5000)
+    g[:8] = [0.0, -0.0, 40.0, -40.0, 800.0, -800.0, 1e-30, -1e-30]
+    assert_same(K.silu(g), ora.silu(g), "silu")
+    assert_same(K.swiglu(g, up), ora.swiglu(g, up), "swiglu")
+    assert_same(K.silu_backward(g, up), ora.silu_backward(g, up), "silu_backward")
+
+
+@pytest.mark.parametrize(("rows", "vocab"), [(6, 301), (3, 5000), (2, 49152)])
+def test_cross_entropy(K, ora, rows, vocab):
+    logits = O.gaussian(16, rows, vocab, scale=4.0)
+    targets = np.array([3, -1, vocab - 1, 0, 17, 17][:rows], np.int64)
+    la, da = K.cross_entropy(logits, targets, 0.25)
+    lb, db = ora.cross_entropy(logits, targets, 0.25)
+    assert la == lb
+    assert_same(da, db, "dlogits")
+
+
+def test_cross_entropy_rejects_target_out_of_range(K):
+    with pytest.raises(ValueError, match="target out of range"):
+        K.cross_entropy(O.gaussian(1, 2, 10), np.array([1, 10], np.int64))
+
+
+def test_embedding_backward(K, ora):
+    dy, tokens = O.gaussian(17, 12, 5), np.array([3, 1, 3, 0, 3, 1, 9, 9, 9, 2, 0, 3], np.int64)
+    assert_same(K.embedding_backward(dy, tokens, 10), ora.embedding_backward(dy, tokens, 10), "embedding")
+    with pytest.raises(ValueError, match="out of range"):
+        K.embedding_backward(dy, np.array([10] + [0] * 11, np.int64), 10)
+
+
+def test_sum_squares_and_adamw(K, ora):
+    g = adversarial(18, 100003)
+    assert K.sum_squares(g) == ora.sum_squares(g)
+    p, grad = O.gaussian(18, 3000), O.gaussian(19, 3000)
+    m, v = O.gaussian(20, 3000, scale=0.1), np.abs(O.gaussian(21, 3000, scale=0.1))
+    pa, ma, va = p.copy(), m.copy(), v.copy()
+    pb, mb, vb = p.copy(), m.copy(), v.copy()
+    args = (1e-3, 0.9, 0.999, 1e-8, 0.01, 1 - 0.9**3, 1 - 0.999**3, 0.5)
+    K.adamw_step(pa, grad, ma, va, *args)
+    ora.adamw_step(pb, grad, mb, vb, *args)
+    assert_same(pa, pb, "param")
+    assert_same(ma, mb, "m")
+    assert_same(va, vb, "v")
