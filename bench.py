@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Fine-tuning step throughput on one MI355X: Qwen2.5-1.5B-architecture decoder (fp32 weights, gradients and AdamW
+state; random-init seeded Gaussians), one full step = forward + backward over batch 8 x seq 1024 random tokens with
+next-token cross-entropy, global-norm clipping and AdamW, bit-identical to the reference CPU kernels.
+
+Prints one JSON line (the driver's contract): tokens/s of whole steps with inputs already resident in HBM, the
+roofline of the dominant kernel (the FP64-FMA matmul, timed live with HIP events on its stream during the timed
+steps) and the reference CPU path timed on this host's cores for a bounded sample of the same step.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c1] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+FP64_PEAK_TFLOPS = 78.6  # MI355X dense FP64 (vector FMA and matrix alike)
+
+CONFIGS = {
+    # the metric's workload
+    "c3": dict(name="Qwen2.5-1.5B", vocab=151936, hidden=1536, intermediate=8960, layers=28, heads=12, kv_heads=2,
+               head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6, tie_embeddings=True, attention_bias=True,
+               batch=8, seq=1024),
+    # the reference's CPU-runnable case
+    "c1": dict(name="SmolLM2-135M", vocab=49152, hidden=576, intermediate=1536, layers=30, heads=9, kv_heads=3,
+               head_dim=64, rms_norm_eps=1e-5, rope_theta=1e5, tie_embeddings=True, attention_bias=False,
+               batch=4, seq=256),
+}
+
+SEED = 0
+LEARNING_RATE = 1e-4  # schedule "constant", betas 0.9 / 0.999, eps 1e-8, weight decay 0.01, max_grad_norm 1.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def natural_key(name: str):
+    import re
+
+    parts = re.split(r"(\d+)", name)
+    return (*((0, int(p), "") if p.isdigit() else (1, 0, p) for p in parts), name)
+
+
+def init_weights(trainer, lib, shapes: dict[str, tuple[int, ...]]) -> None:
+    """fill_gaussian(SEED * 1000 + i) * 0.02f per tensor, i its index in natural name order; norm weights 1.0."""
+    names = sorted(shapes, key=natural_key)
+
+    def one(item):
+        index, name = item
+        n = int(np.prod(shapes[name]))
+        if name.endswith("norm.weight"):
+            values = np.ones(n, np.float32)
+        else:
+            values = np.empty(n, np.float32)
+            rc = lib.dllm_hip_fill_gaussian(C.c_uint64(SEED * 1000 + index), values.ctypes.data_as(C.c_void_p),
+                                            C.c_size_t(n), C.c_float(0.02))
+            assert rc == 0
+        trainer.set(name, values)
+
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as pool:
+        list(pool.map(one, enumerate(names)))
+
+
+def tensor_shapes(cfg) -> dict[str, tuple[int, ...]]:
+    H, q, kv, inter = cfg["hidden"], cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"], cfg["intermediate"]
+    shapes = {"token_embedding.weight": (cfg["vocab"], H), "final_norm.weight": (H,)}
+    for i in range(cfg["layers"]):
+        p = f"layers.{i}."
+        shapes.update({p + "attention_norm.weight": (H,), p + "attention.q.weight": (q, H),
+                       p + "attention.k.weight": (kv, H), p + "attention.v.weight": (kv, H),
+                       p + "attention.o.weight": (H, q), p + "mlp_norm.weight": (H,),
+                       p + "mlp.gate.weight": (inter, H), p + "mlp.up.weight": (inter, H),
+                       p + "mlp.down.weight": (H, inter)})
+        if cfg["attention_bias"]:
+            shapes.update({p + "attention.q.bias": (q,), p + "attention.k.bias": (kv,), p + "attention.v.bias": (kv,)})
+    if not cfg["tie_embeddings"]:
+        shapes["lm_head.weight"] = (cfg["vocab"], H)
+    return shapes
+
+
+def make_windows(lib, cfg, step: int) -> list[list[int]]:
+    """Random(SEED + step).next_u64() % vocab, batch windows of seq + 1 tokens."""
+    n = cfg["batch"] * (cfg["seq"] + 1)
+    tokens = np.empty(n, np.int64)
+    assert lib.dllm_hip_random_tokens(C.c_uint64(SEED + step), tokens.ctypes.data_as(C.c_void_p), C.c_size_t(n),
+                                      C.c_int64(cfg["vocab"])) == 0
+    w = cfg["seq"] + 1
+    return [tokens[i * w:(i + 1) * w].tolist() for i in range(cfg["batch"])]
+
+
+def matmul_flops_per_step(cfg) -> float:
+    """Algorithmic matmul work of one step: 6 x matmul parameters x tokens (forward, dX, dW)."""
+    H, q, kv, inter, V = (cfg["hidden"], cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"],
+                          cfg["intermediate"], cfg["vocab"])
+    per_layer = H * q * 2 + H * kv * 2 + 3 * H * inter
+    params = cfg["layers"] * per_layer + V * H
+    return 6.0 * params * cfg["batch"] * cfg["seq"]
+
+
+def cpu_baseline(cfg) -> dict | None:
+    """The reference CPU path (its own kernels from oracle/_ref, or the oracle's C restatement when that library is
+    absent), driven by the oracle's step orchestration, timed on a bounded sample of the step and scaled to it:
+      one window of `seq` tokens through a 1-layer model of this architecture with a 4096-token vocabulary;
+      the head (linear, cross-entropy, linear_backward) at 8192 vocabulary rows over seq rows, scaled to the vocab;
+      adamw_step and sum_squares on 16M elements, scaled to the parameter count.
+    step = batch x (layers x (window - head share) + head x vocab / 8192) + optimizer x params / 16M."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+
+    kind = "reference" if O.reference_available() else "port"
+    cores = 1
+    if kind == "reference":
+        kern = O.ref_kernels()
+        cores = min(16, os.cpu_count() or 1)
+        O.ref().ref_set_threads(C.c_size_t(cores))
+    else:
+        kern = O.oracle_kernels()
+    T, V, H = cfg["seq"], cfg["vocab"], cfg["hidden"]
+    small = O.Decoder("sample", vocab=4096, hidden=H, inter=cfg["intermediate"], layers=1, heads=cfg["heads"],
+                      kv_heads=cfg["kv_heads"], head_dim=cfg["head_dim"], eps=cfg["rms_norm_eps"],
+                      rope_theta=cfg["rope_theta"], tied=cfg["tie_embeddings"], attn_bias=cfg["attention_bias"])
+    weights = O.synthetic_weights(small, seed=SEED, scale=0.02)
+    rng = O.Random(SEED)
+    tokens = [rng.next_u64() % small.vocab for _ in range(T + 1)]
+    t0 = time.perf_counter()
+    O.window_gradients(kern, small, weights, tokens[:-1], tokens[1:], scale=1.0 / T)
+    t_window = time.perf_counter() - t0
+    hidden = O.gaussian(SEED + 1, T, H)
+    head = O.gaussian(SEED + 2, 8192, H, scale=0.02)
+    targets = np.array([rng.next_u64() % 8192 for _ in range(T)], np.int64)
+    t0 = time.perf_counter()
+    logits = kern.linear(hidden, head)
+    _, dlogits = kern.cross_entropy(logits, targets, 1.0 / T)
+    kern.linear_backward(hidden, head, dlogits)
+    t_head = time.perf_counter() - t0
+    n = 16 * 1024 * 1024
+    p, g = O.gaussian(SEED + 3, n, scale=0.02), O.gaussian(SEED + 4, n, scale=1e-3)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    t0 = time.perf_counter()
+    kern.sum_squares(g)
+    kern.adamw_step(p, g, m, v, 1e-4, 0.9, 0.999, 1e-8, 0.01, 0.1, 0.001, 1.0)
+    t_opt = time.perf_counter() - t0
+    params = sum(int(np.prod(s)) for s in tensor_shapes(cfg).values())
+    layer = t_window - t_head * 4096 / 8192
+    step = cfg["batch"] * (cfg["layers"] * layer + t_head * V / 8192) + t_opt * params / n
+    tokens_per_step = cfg["batch"] * T
+    return {
+        "value": tokens_per_step / step,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": (f"1-layer {cfg['name']}-shaped model, 1 window x {T} tokens, vocab 4096 ({t_window:.2f} s); "
+                   f"head at 8192 vocab rows ({t_head:.2f} s); optimizer on 16M params ({t_opt:.2f} s); "
+                   f"scaled to {cfg['layers']} layers, vocab {V}, batch {cfg['batch']}, {params} params: "
+                   f"{step:.1f} s per step (extrapolated)"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this backend runs the step on a single MI355X (got --gpus {args.gpus}); "
+              "the multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        return 2
+    cfg = CONFIGS[args.config]
+    from etalii_dllm_amd.kernels import check, lib
+    from etalii_dllm_amd.trainer import Decoder, Trainer
+
+    lib.dllm_hip_trainer_profile.argtypes = [C.c_void_p, C.c_int]
+    lib.dllm_hip_trainer_profile_read.argtypes = [C.c_void_p, C.POINTER(C.c_int64), C.POINTER(C.c_double),
+                                                  C.POINTER(C.c_double)]
+    decoder = Decoder(cfg["vocab"], cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
+                      cfg["head_dim"], cfg["rms_norm_eps"], cfg["rope_theta"], cfg["tie_embeddings"],
+                      cfg["attention_bias"])
+    tokens_per_step = cfg["batch"] * cfg["seq"]
+    log(f"creating trainer for {cfg['name']} ({tokens_per_step} tokens per step)")
+    t0 = time.perf_counter()
+    trainer = Trainer(decoder, tokens_per_step, cfg["batch"], cfg["seq"])
+    init_weights(trainer, lib, tensor_shapes(cfg))
+    log(f"weights ready in {time.perf_counter() - t0:.1f} s")
+    windows = [make_windows(lib, cfg, s) for s in range(args.warmup + args.steps)]
+    for s in range(args.warmup):
+        t1 = time.perf_counter()
+        loss, norm = trainer.step(windows[s], LEARNING_RATE, s + 1)
+        log(f"warmup step {s + 1}: loss {loss:.6f} norm {norm:.6f} ({time.perf_counter() - t1:.2f} s)")
+    check(lib.dllm_hip_synchronize())
+    check(lib.dllm_hip_trainer_profile(trainer.handle, 1))
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        loss, norm = trainer.step(windows[args.warmup + s], LEARNING_RATE, args.warmup + s + 1)
+        log(f"step {args.warmup + s + 1}: loss {loss:.6f} norm {norm:.6f}")
+    check(lib.dllm_hip_synchronize())
+    elapsed = time.perf_counter() - t0
+    launches, ms, flops = C.c_int64(), C.c_double(), C.c_double()
+    check(lib.dllm_hip_trainer_profile_read(trainer.handle, C.byref(launches), C.byref(ms), C.byref(flops)))
+    check(lib.dllm_hip_trainer_profile(trainer.handle, 0))
+    trainer.close()
+    ms_per_step = elapsed * 1000.0 / args.steps
+    achieved = flops.value / (ms.value * 1e9) if ms.value > 0 else 0.0  # TFLOP/s
+    log(f"matmuls: {launches.value} launches, {ms.value:.1f} ms, {flops.value:.3e} flop "
+        f"({100.0 * ms.value / (elapsed * 1000.0):.1f}% of step time)")
+    traffic = None
+    traffic_file = ROOT / "profiles" / "gemm_traffic.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get(args.config)
+    baseline = None
+    if not args.no_cpu_baseline:
+        log("timing the reference CPU path on a bounded sample")
+        baseline = cpu_baseline(cfg)
+    result = {
+        "metric": "finetune tokens/s, Qwen2.5-1.5B fp32 step, bit-exact vs CPU; % of roofline",
+        "value": tokens_per_step * args.steps / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic (seeded Gaussian weights x 0.02, uniform random token ids)",
+        "config": {"workload": f"{cfg['name']} full fine-tune step (forward, backward, global-norm clip, AdamW)",
+                   "global_batch": cfg["batch"], "seq_len": cfg["seq"], "parallelism": "single GPU",
+                   "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"]},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic,
+                     "kernel": "gemm_kernel (FP64 FMA matmul, all launches of the timed steps)",
+                     "step_fraction_of_peak": matmul_flops_per_step(cfg) / (ms_per_step * 1e9) / FP64_PEAK_TFLOPS},
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

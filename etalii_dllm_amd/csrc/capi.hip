@@ -372,14 +372,46 @@ int dllm_hip_embedding_backward(const float* dy, const int64_t* tokens, float* o
     return check_hip(hipStreamSynchronize(s), "embedding_backward");
 }
 
+size_t dllm_hip_sum_squares_workspace(size_t n) {
+    const int64_t count = static_cast<int64_t>(n);
+    const size_t blocks = exact_sum_squares_blocks(&count, 1);
+    Layout l;
+    l.add<int64_t>(2);           // first block, block count
+    l.add<int64_t>(2 * blocks);  // block starts and counts
+    l.add<char>(exact_sum_squares_workspace(blocks));
+    l.add<double>(1);
+    return l.bytes;
+}
+
 int dllm_hip_sum_squares(const float* values, size_t n, double* result, void* workspace, size_t workspace_bytes,
                          void* stream) {
-    DLLM_REQUIRE(workspace_bytes >= sizeof(double), "workspace too small for sum_squares");
+    DLLM_REQUIRE(workspace_bytes >= dllm_hip_sum_squares_workspace(n), "workspace too small for sum_squares");
     const hipStream_t s = as_stream(stream);
-    double* d = static_cast<double*>(workspace);
-    DLLM_TRY(launch_sum_squares(values, static_cast<int64_t>(n), d, s));
+    const int64_t count = static_cast<int64_t>(n), offset = 0;
+    const size_t blocks = exact_sum_squares_blocks(&count, 1);
+    std::vector<int64_t> tf(1), tb(1), bs(blocks), bc(blocks);
+    exact_sum_squares_plan(&offset, &count, 1, tf.data(), tb.data(), bs.data(), bc.data());
+    std::vector<int64_t> head = {tf[0], tb[0]}, table(bs);
+    table.insert(table.end(), bc.begin(), bc.end());
+    Carve c(workspace, workspace_bytes);
+    int64_t* d_head = c.take<int64_t>(2);
+    int64_t* d_table = c.take<int64_t>(2 * blocks);
+    char* ws = c.take<char>(exact_sum_squares_workspace(blocks));
+    double* d_result = c.take<double>(1);
+    DLLM_REQUIRE(!c.overflow, "workspace layout overflow");
+    DLLM_TRY(check_hip(hipMemcpyAsync(d_head, head.data(), 2 * sizeof(int64_t), hipMemcpyHostToDevice, s), "upload"));
+    DLLM_TRY(check_hip(hipMemcpyAsync(d_table, table.data(), table.size() * sizeof(int64_t), hipMemcpyHostToDevice, s),
+                       "upload"));
+    ExactSumPlan plan;
+    plan.tensors = 1;
+    plan.blocks = static_cast<int64_t>(blocks);
+    plan.tfirst = d_head;
+    plan.tblocks = d_head + 1;
+    plan.bstart = d_table;
+    plan.bcount = d_table + blocks;
+    DLLM_TRY(launch_exact_sum_squares(values, plan, ws, d_result, s));
     double host = 0.0;
-    DLLM_TRY(check_hip(hipMemcpyAsync(&host, d, sizeof host, hipMemcpyDeviceToHost, s), "download"));
+    DLLM_TRY(check_hip(hipMemcpyAsync(&host, d_result, sizeof host, hipMemcpyDeviceToHost, s), "download"));
     DLLM_TRY(check_hip(hipStreamSynchronize(s), "sum_squares"));
     if (result) *result = host;
     return kOk;

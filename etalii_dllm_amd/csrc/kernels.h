@@ -123,6 +123,26 @@ int launch_embedding_groups(const float* dy, int64_t dim, const int64_t* order, 
 int launch_global_norm(const float* arena, const int64_t* offsets, const int64_t* counts, int64_t tensors,
                        double* per_tensor, double max_grad_norm, double* stats, hipStream_t stream);
 int launch_sum_squares(const float* values, int64_t n, double* result, hipStream_t stream);
+// total = sum of per_tensor in order, norm = sqrt(total), clip factor (optimizer.py:66-90): stats = {total, norm, clip}.
+int launch_norm_finish(const double* per_tensor, int64_t tensors, double max_grad_norm, double* stats,
+                       hipStream_t stream);
+
+// ---- exact parallel sum of squares (sumsq.hip) ----
+// Tensors of one arena split into fixed blocks; the plan arrays live in device memory.
+struct ExactSumPlan {
+    int64_t tensors = 0, blocks = 0;
+    const int64_t* tfirst = nullptr;   // [tensors] first block of each tensor
+    const int64_t* tblocks = nullptr;  // [tensors] block count of each tensor
+    const int64_t* bstart = nullptr;   // [blocks] arena offset of each block
+    const int64_t* bcount = nullptr;   // [blocks] elements in each block
+};
+size_t exact_sum_squares_blocks(const int64_t* counts, int64_t tensors);
+void exact_sum_squares_plan(const int64_t* offsets, const int64_t* counts, int64_t tensors, int64_t* tfirst,
+                            int64_t* tblocks, int64_t* bstart, int64_t* bcount);
+size_t exact_sum_squares_workspace(size_t blocks);
+// per_tensor[t] = the serial double sum of squares of tensor t, bit for bit (grad.hpp:467-473).
+int launch_exact_sum_squares(const float* arena, const ExactSumPlan& plan, void* workspace, double* per_tensor,
+                             hipStream_t stream);
 // adamw_step (grad.hpp:481-495) over an arena; chunk table: chunk c covers [chunk_start[c], chunk_end[c]) with
 // weight decay chunk_decay[c]; grad_scale read from device memory (the clip factor) when grad_scale_dev != null.
 struct AdamWArgs {

@@ -118,6 +118,12 @@ int launch_global_norm(const float* arena, const int64_t* offsets, const int64_t
     return check_launch("global norm");
 }
 
+int launch_norm_finish(const double* per_tensor, int64_t tensors, double max_grad_norm, double* stats,
+                       hipStream_t stream) {
+    hipLaunchKernelGGL(norm_finish_kernel, dim3(1), dim3(64), 0, stream, per_tensor, tensors, max_grad_norm, stats);
+    return check_launch("global norm");
+}
+
 int launch_sum_squares(const float* values, int64_t n, double* result, hipStream_t stream) {
     hipLaunchKernelGGL(sum_squares_kernel, dim3(1), dim3(64), 0, stream, values, n, result);
     return check_launch("sum_squares");

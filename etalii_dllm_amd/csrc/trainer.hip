@@ -167,6 +167,8 @@ struct dllm_hip_trainer {
     int64_t chunks = 0;
     std::vector<int64_t> seg_host;
     bool wt_valid = false;
+    ExactSumPlan norm_plan;
+    void* norm_ws = nullptr;
 
     template <typename T>
     int make(T** out, size_t n) {
@@ -287,6 +289,29 @@ struct dllm_hip_trainer {
         DLLM_TRY(check_hip(hipMemcpy(ten_cnt, tc.data(), tc.size() * 8, hipMemcpyHostToDevice), "upload"));
         DLLM_TRY(make(&per_tensor, tensors.size()));
         DLLM_TRY(make(&stats, 3));
+        // exact parallel global norm plan (sumsq.hip)
+        const size_t nb = exact_sum_squares_blocks(tc.data(), static_cast<int64_t>(tc.size()));
+        std::vector<int64_t> tf(tc.size()), tb(tc.size()), bs(nb), bc(nb);
+        exact_sum_squares_plan(to.data(), tc.data(), static_cast<int64_t>(tc.size()), tf.data(), tb.data(), bs.data(),
+                               bc.data());
+        int64_t *d_tf, *d_tb, *d_bs, *d_bc;
+        DLLM_TRY(make(&d_tf, tf.size()));
+        DLLM_TRY(make(&d_tb, tb.size()));
+        DLLM_TRY(make(&d_bs, bs.size()));
+        DLLM_TRY(make(&d_bc, bc.size()));
+        DLLM_TRY(check_hip(hipMemcpy(d_tf, tf.data(), tf.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(d_tb, tb.data(), tb.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(d_bs, bs.data(), bs.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(d_bc, bc.data(), bc.size() * 8, hipMemcpyHostToDevice), "upload"));
+        norm_plan.tensors = static_cast<int64_t>(tc.size());
+        norm_plan.blocks = static_cast<int64_t>(nb);
+        norm_plan.tfirst = d_tf;
+        norm_plan.tblocks = d_tb;
+        norm_plan.bstart = d_bs;
+        norm_plan.bcount = d_bc;
+        char* ws = nullptr;
+        DLLM_TRY(make(&ws, exact_sum_squares_workspace(nb)));
+        norm_ws = ws;
         return kOk;
     }
 
@@ -381,6 +406,45 @@ struct dllm_hip_trainer {
     float* WT(int id) const { return wt.as<float>() + tensors[static_cast<size_t>(id)].wt_offset; }
     const float* Popt(int id) const { return id >= 0 ? P(id) : nullptr; }
 
+    // ---- matmul timing (dllm_hip_trainer_profile) ----
+    bool profiling = false;
+    std::vector<hipEvent_t> events;  // pairs
+    size_t event_used = 0;
+    double profile_flops = 0.0;
+    int64_t profile_launches = 0;
+    double profile_ms_done = 0.0;
+
+    int drain_events() {
+        for (size_t i = 0; i + 1 < event_used; i += 2) {
+            DLLM_TRY(check_hip(hipEventSynchronize(events[i + 1]), "event"));
+            float ms = 0.0f;
+            DLLM_TRY(check_hip(hipEventElapsedTime(&ms, events[i], events[i + 1]), "event"));
+            profile_ms_done += ms;
+        }
+        event_used = 0;
+        return kOk;
+    }
+
+    int gemm(const GemmCall& g, hipStream_t s) {
+        if (!profiling) return launch_gemm(g, s);
+        if (event_used + 2 > events.size()) {
+            if (events.size() >= 8192) DLLM_TRY(drain_events());
+            while (event_used + 2 > events.size()) {
+                hipEvent_t e;
+                DLLM_TRY(check_hip(hipEventCreate(&e), "event"));
+                events.push_back(e);
+            }
+        }
+        DLLM_TRY(check_hip(hipEventRecord(events[event_used], s), "event"));
+        DLLM_TRY(launch_gemm(g, s));
+        DLLM_TRY(check_hip(hipEventRecord(events[event_used + 1], s), "event"));
+        event_used += 2;
+        const double L = g.seg ? static_cast<double>(seg_host.back()) : static_cast<double>(g.l1 - g.l0);
+        profile_flops += 2.0 * static_cast<double>(g.I) * static_cast<double>(g.J) * L;
+        profile_launches += 1;
+        return kOk;
+    }
+
     // W^T of every linear weight for the forward matmuls.
     int refresh_transposes(hipStream_t s) {
         for (const TensorInfo& t : tensors)
@@ -410,7 +474,7 @@ struct dllm_hip_trainer {
         g.bias = bias;
         g.addsrc = addsrc;
         g.ld_add = N;
-        return launch_gemm(g, s);
+        return gemm(g, s);
     }
 
     // Converts dy[R][N] to dy_d [R][N_pad] and dy^T [N][R_pad] (doubles) for the dW and dX matmuls.
@@ -434,7 +498,7 @@ struct dllm_hip_trainer {
         g.l1 = t.rows;
         g.addsrc = addsrc;
         g.ld_add = t.cols;
-        return launch_gemm(g, s);
+        return gemm(g, s);
     }
 
     // grad[w] = window-ordered float sum of per-window dW = sum over window rows of dy[r][n] x[r][k].
@@ -454,7 +518,7 @@ struct dllm_hip_trainer {
         g.seg_addrow = addrow_;
         g.seg_addend = addend;
         g.ld_seg_add = K;
-        return launch_gemm(g, s);
+        return gemm(g, s);
     }
 
     int norm_dw(const float* dyv, const float* x, const double* inv, int64_t dim, int64_t rows_per_token, int nseg,
@@ -691,8 +755,8 @@ struct dllm_hip_trainer {
         double loss_total = 0.0;
         DLLM_TRY(gradients(tokens, offsets, lengths, windows, scale, &loss_total, s));
         // global norm, clip (optimizer.py:66-90), bias corrections by repeated multiplication (optimizer.py:59-63)
-        DLLM_TRY(launch_global_norm(grads.as<float>(), ten_off, ten_cnt, static_cast<int64_t>(tensors.size()),
-                                    per_tensor, a->max_grad_norm, stats, s));
+        DLLM_TRY(launch_exact_sum_squares(grads.as<float>(), norm_plan, norm_ws, per_tensor, s));
+        DLLM_TRY(launch_norm_finish(per_tensor, static_cast<int64_t>(tensors.size()), a->max_grad_norm, stats, s));
         double p1 = 1.0, p2 = 1.0;
         for (int64_t i = 0; i < a->step; ++i) {
             p1 *= a->beta1;
@@ -757,7 +821,32 @@ int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_t
 }
 
 int dllm_hip_trainer_destroy(dllm_hip_trainer* t) {
+    if (t) {
+        (void)hipDeviceSynchronize();
+        for (hipEvent_t e : t->events) (void)hipEventDestroy(e);
+    }
     delete t;
+    return kOk;
+}
+
+int dllm_hip_trainer_profile(dllm_hip_trainer* t, int enable) {
+    DLLM_REQUIRE(t, "null argument");
+    DLLM_TRY(t->drain_events());
+    t->profiling = enable != 0;
+    if (t->profiling) {
+        t->profile_flops = 0.0;
+        t->profile_launches = 0;
+        t->profile_ms_done = 0.0;
+    }
+    return kOk;
+}
+
+int dllm_hip_trainer_profile_read(dllm_hip_trainer* t, int64_t* launches, double* ms, double* flops) {
+    DLLM_REQUIRE(t, "null argument");
+    DLLM_TRY(t->drain_events());
+    if (launches) *launches = t->profile_launches;
+    if (ms) *ms = t->profile_ms_done;
+    if (flops) *flops = t->profile_flops;
     return kOk;
 }
 

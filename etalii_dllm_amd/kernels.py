@@ -65,6 +65,8 @@ def _load() -> C.CDLL:
     lib.dllm_hip_cross_entropy.argtypes = [_vp, _vp, _vp, _sz, _sz, C.c_double, _f64p, _vp, _sz, _vp]
     lib.dllm_hip_embedding_backward.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
     lib.dllm_hip_sum_squares.argtypes = [_vp, _sz, _f64p, _vp, _sz, _vp]
+    lib.dllm_hip_sum_squares_workspace.restype = _sz
+    lib.dllm_hip_sum_squares_workspace.argtypes = [_sz]
     lib.dllm_hip_adamw_step.argtypes = [_vp, _vp, _vp, _vp, _sz] + [C.c_double] * 8 + [_vp]
     return lib
 
@@ -330,7 +332,7 @@ def embedding_backward(dy, tokens, vocabulary_size) -> np.ndarray:
 def sum_squares(values) -> float:
     """kernels.cpp:1041-1043."""
     v = _f32(values)
-    d, ws = Device.of(v), Device(8)
+    d, ws = Device.of(v), Device(lib.dllm_hip_sum_squares_workspace(v.size))
     result = C.c_double()
     check(lib.dllm_hip_sum_squares(d.ptr, v.size, C.byref(result), ws.ptr, ws.nbytes, None))
     return result.value

@@ -112,8 +112,11 @@ size_t dllm_hip_embedding_backward_workspace(size_t rows);
 int dllm_hip_embedding_backward(const float* dy, const int64_t* tokens, float* out, size_t rows, size_t dim,
                                 size_t vocab, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Sum of squares in index order with a double accumulator, written to *result (HOST pointer; waits). The workspace
- * holds one double. Replaces kernels.cpp:1041-1043 `sum_squares` (grad.hpp:467-473). */
+/* Sum of squares in index order with a double accumulator, written to *result (HOST pointer; waits): the bits of the
+ * serial chain, computed in parallel (each add within one binade of the running sum is an integer increment plus a
+ * parity-dependent rounding bit, composed as an associative scan; binade changes are replayed as real adds).
+ * Replaces kernels.cpp:1041-1043 `sum_squares` (grad.hpp:467-473). */
+size_t dllm_hip_sum_squares_workspace(size_t n);
 int dllm_hip_sum_squares(const float* values, size_t n, double* result, void* workspace, size_t workspace_bytes,
                          void* stream);
 
@@ -176,6 +179,18 @@ typedef struct {
 int dllm_hip_trainer_step(dllm_hip_trainer* trainer, const int64_t* tokens, const int64_t* offsets,
                           const int64_t* lengths, int64_t windows, const dllm_hip_adamw* adamw, double* loss,
                           double* grad_norm, void* stream);
+
+/* Matmul timing inside steps: with profiling on, every matmul launch of the trainer is bracketed by HIP events on its
+ * stream; _read sums them (waiting for the events) into the number of launches, their total milliseconds and their
+ * algorithmic flops (2 * rows * columns * reduction length each). Enabling resets the totals. */
+int dllm_hip_trainer_profile(dllm_hip_trainer* trainer, int enable);
+int dllm_hip_trainer_profile_read(dllm_hip_trainer* trainer, int64_t* launches, double* milliseconds, double* flops);
+
+/* ---- seeded synthetic inputs (kernels.cpp:130-136 `Random`, kernels.cpp:206-218 `fill_gaussian`) ----
+ * Host functions: n Irwin-Hall Gaussians of Random(seed), times scale (one float multiply; 1 keeps them as is), and
+ * n token ids Random(seed).next_u64() % vocab. */
+int dllm_hip_fill_gaussian(uint64_t seed, float* host_out, size_t n, float scale);
+int dllm_hip_random_tokens(uint64_t seed, int64_t* host_out, size_t n, int64_t vocab);
 
 #ifdef __cplusplus
 }

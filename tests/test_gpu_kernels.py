@@ -154,3 +154,40 @@ def test_sum_squares_and_adamw(K, ora):
     assert_same(pa, pb, "param")
     assert_same(ma, mb, "m")
     assert_same(va, vb, "v")
+
+
+def sum_squares_cases():
+    """Adversarial inputs for the exact parallel sum of squares: binade crossings at every scale, exact round-half-even
+    ties of both parities (x = odd * 2^-26 while the sum is in [2, 4): x^2 / ulp ends in .5), leading zeros, a huge
+    first element then tiny ones, monotone ramps, and non-finite values."""
+    n = 3 * 8192 + 77
+    g = O.gaussian(40, n)
+    cases = {"gaussian": g, "small": g * np.float32(1e-20), "adversarial": adversarial(41, n)}
+    odd = (2 * (np.arange(n) % 4096) + 1).astype(np.float32) * np.float32(2.0 ** -26)
+    ties = odd.copy()
+    ties[0] = np.float32(1.5)  # s = 2.25 after the first element
+    cases["ties"] = ties
+    cases["ties_late"] = np.concatenate([np.zeros(5000, np.float32), ties])
+    ramp = np.float32(2.0) ** (np.linspace(-60, 60, n).astype(np.float32))
+    cases["ramp_up"] = ramp
+    cases["ramp_down"] = ramp[::-1].copy()
+    cases["huge_then_tiny"] = np.concatenate([[np.float32(3e18)], g * np.float32(1e-12)]).astype(np.float32)
+    z = np.zeros(20000, np.float32)
+    z[-3:] = [0.5, -0.25, 3.0]
+    cases["zeros"] = z
+    cases["all_zero"] = np.zeros(9000, np.float32)
+    inf_case = g.copy()
+    inf_case[9000] = np.inf
+    cases["inf"] = inf_case
+    nan_case = g.copy()
+    nan_case[17000] = np.nan
+    cases["nan"] = nan_case
+    cases["one"] = np.array([3.0], np.float32)
+    return cases
+
+
+@pytest.mark.parametrize("name", sorted(sum_squares_cases()))
+def test_exact_parallel_sum_squares_matches_the_serial_chain(K, ora, name):
+    values = sum_squares_cases()[name]
+    got, want = K.sum_squares(values), ora.sum_squares(values)
+    assert np.float64(got).tobytes() == np.float64(want).tobytes(), (name, got, want)
