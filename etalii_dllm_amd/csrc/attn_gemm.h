@@ -1,0 +1,54 @@
+// Launchers of the training step's attention as batched matmuls plus per-query chains (attn_gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dllm_hip {
+
+enum AttnMask {
+    kMaskNone = 0,
+    kMaskQueryRows = 1,   // rows are queries t; reduce over the keys t sees, ascending
+    kMaskKeyRows = 2,     // rows are keys j; reduce over (query, head of the group) pairs that see j, ascending
+    kMaskTileCausal = 3,  // output [key][query] tiles nothing can see are skipped (scores, dP)
+};
+
+// Where operand rows live for batch entry z = (window w, head hz):
+// base = ptr + w * w_stride + seg[w] * seg_stride + (hz / head_div) * head_stride, row(l) = (l / group) * ld +
+// (l % group) * ld_inner (elements of the operand's type).
+struct AttnOperand {
+    const void* ptr = nullptr;
+    int64_t w_stride = 0, seg_stride = 0, head_stride = 0, head_div = 1;
+    int64_t ld = 0, ld_inner = 0, group = 1;
+};
+
+struct AttnGemmCall {
+    AttnOperand A;  // double [L rows][>= 16-row tiles], the wave-uniform operand
+    AttnOperand B;  // float [L rows][columns]
+    AttnOperand C;  // float or double output [rows][columns]
+    const double* rowscale = nullptr;  // output row multiplier before rounding, [z][row]
+    int64_t rowscale_zstride = 0;
+    const int64_t* seg = nullptr;  // device window offsets
+    int64_t windows = 0, heads = 0, max_len = 0, head_dim = 0, group = 1, window = 0, L = 0;
+    int rows_kind = 0, cols_kind = 0;  // 0: window positions, 1: head_dim
+    int mask = kMaskNone;
+    int cols_per_lane = 4;
+    bool exact_products = true;  // float x float products: fused multiply-add is exact
+    bool out_double = false;
+    double out_scale = 1.0;
+};
+
+int launch_attn_gemm(const AttnGemmCall& c, hipStream_t stream);
+int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
+                        int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream);
+int launch_dsoftmax_rows(double* et, double* dpt, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows,
+                         int64_t heads, int64_t max_len, int64_t window, const double* inv, int64_t inv_zstride,
+                         double scale, hipStream_t stream);
+int launch_regroup(const double* src, int64_t ld, int64_t zstride, double* dst, int64_t dst_ld, int64_t dst_zstride,
+                   const int64_t* seg, int64_t windows, int64_t heads, int64_t group, int64_t max_len,
+                   hipStream_t stream);
+int launch_heads_transpose(const float* src, int64_t row_stride, int64_t head_dim, void* dst, bool to_double,
+                           int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
+                           int64_t max_len, hipStream_t stream);
+
+}  // namespace dllm_hip

@@ -22,6 +22,7 @@
 #include <string>
 #include <vector>
 
+#include "attn_gemm.h"
 #include "common.h"
 #include "devmath.h"
 #include "dllm_hip.h"
@@ -169,6 +170,11 @@ struct dllm_hip_trainer {
     bool wt_valid = false;
     ExactSumPlan norm_plan;
     void* norm_ws = nullptr;
+    // attention as batched matmuls (attn_gemm.hip): per (window, head) transposed operands and score matrices
+    int64_t Tp = 0;
+    double *attn_kt = nullptr, *attn_vt = nullptr, *attn_et = nullptr, *attn_inv = nullptr, *attn_dpt = nullptr,
+           *attn_pg = nullptr, *attn_dsg = nullptr;
+    float *attn_qt = nullptr, *attn_dot = nullptr;
 
     template <typename T>
     int make(T** out, size_t n) {
@@ -377,13 +383,17 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&inv_freq, std::max<int64_t>(c.rotary_dim / 2, 1)));
         DLLM_TRY(make(&cos_t, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
         DLLM_TRY(make(&sin_t, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
-        AttentionShape sh{R, R, heads, kvh, c.head_dim, c.head_dim, c.attention_scale, 1, 0, c.sliding_window, 0.0};
-        AttentionBatch b{};
-        b.max_kv = T_max;
-        const size_t ws = attention_backward_workspace(sh, b, R);
-        char* p = nullptr;
-        DLLM_TRY(make(&p, ws));
-        attn_ws = p;
+        Tp = padded_rows(T_max);
+        const int64_t hd = c.head_dim, G = heads / kvh;
+        DLLM_TRY(make(&attn_kt, W_max * kvh * hd * Tp));
+        DLLM_TRY(make(&attn_vt, W_max * kvh * hd * Tp));
+        DLLM_TRY(make(&attn_qt, W_max * heads * hd * Tp));
+        DLLM_TRY(make(&attn_dot, W_max * heads * hd * Tp));
+        DLLM_TRY(make(&attn_et, c.layers * W_max * heads * Tp * Tp));  // E^T saved per layer for the backward
+        DLLM_TRY(make(&attn_inv, c.layers * W_max * heads * Tp));
+        DLLM_TRY(make(&attn_dpt, W_max * heads * Tp * Tp));
+        DLLM_TRY(make(&attn_pg, W_max * kvh * Tp * G * Tp));
+        DLLM_TRY(make(&attn_dsg, W_max * kvh * Tp * G * Tp));
         DLLM_TRY(make(&tok_in, R));
         DLLM_TRY(make(&tok_tgt, R));
         DLLM_TRY(make(&pos_index, R));
@@ -528,6 +538,124 @@ struct dllm_hip_trainer {
         return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s);
     }
 
+    // ---- attention (attn_gemm.hip) ----
+    int64_t nwin = 0;  // windows of the current step
+
+    double* et_of(int64_t l) const { return attn_et + l * W_max * c.heads * Tp * Tp; }
+    double* inv_of(int64_t l) const { return attn_inv + l * W_max * c.heads * Tp; }
+
+    // attention() of every (window, head) of the step (nn.hpp:761-796): S^T = K Q^T scale, the softmax chains per
+    // query, out = (E V) inv.
+    int attention_forward(int64_t l, const Saved& sv, const AttentionBatch& b, hipStream_t s) {
+        const int64_t nh = c.heads, nkv = c.kv_heads, hd = c.head_dim, G = nh / nkv, n = b.max_q;
+        DLLM_TRY(launch_heads_transpose(sv.k, KVD, hd, attn_kt, true, Tp, hd * Tp, seg_d, nwin, nkv, n, s));
+        DLLM_TRY(launch_heads_transpose(sv.q, QD, hd, attn_qt, false, Tp, hd * Tp, seg_d, nwin, nh, n, s));
+        double* et = et_of(l);
+        AttnGemmCall g;
+        g.seg = seg_d;
+        g.windows = nwin;
+        g.heads = nh;
+        g.max_len = n;
+        g.head_dim = hd;
+        g.group = G;
+        g.window = c.sliding_window;
+        // S^T[j][t] = sum_i k[j][i] q[t][i], times scale
+        g.A = AttnOperand{attn_kt, nkv * hd * Tp, 0, hd * Tp, G, Tp, 0, 1};
+        g.B = AttnOperand{attn_qt, nh * hd * Tp, 0, hd * Tp, 1, Tp, 0, 1};
+        g.C = AttnOperand{et, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
+        g.rows_kind = 0;
+        g.cols_kind = 0;
+        g.L = hd;
+        g.mask = kMaskTileCausal;
+        g.cols_per_lane = 4;
+        g.exact_products = true;
+        g.out_double = true;
+        g.out_scale = c.attention_scale;
+        DLLM_TRY(launch_attn_gemm(g, s));
+        DLLM_TRY(launch_softmax_rows(et, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp, s));
+        // out[t] = f32((sum_j e_j v_j) inv_t)
+        AttnGemmCall o = g;
+        o.A = AttnOperand{et, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
+        o.B = AttnOperand{sv.v, 0, nkv * hd, hd, G, nkv * hd, 0, 1};
+        o.C = AttnOperand{sv.attended, 0, nh * hd, hd, 1, nh * hd, 0, 1};
+        o.rows_kind = 0;
+        o.cols_kind = 1;
+        o.L = 0;
+        o.mask = kMaskQueryRows;
+        o.cols_per_lane = hd % 256 == 0 ? 4 : 2;
+        o.exact_products = false;
+        o.out_double = false;
+        o.rowscale = inv_of(l);
+        o.rowscale_zstride = Tp;
+        return launch_attn_gemm(o, s);
+    }
+
+    // attention_backward (grad.hpp:206-301) of every (window, head): dq_t, dk_t, dv_t from dattended.
+    int attention_backward(int64_t l, const Saved& sv, const AttentionBatch& b, hipStream_t s) {
+        const int64_t nh = c.heads, nkv = c.kv_heads, hd = c.head_dim, G = nh / nkv, n = b.max_q;
+        double* et = et_of(l);
+        DLLM_TRY(launch_heads_transpose(sv.v, KVD, hd, attn_vt, true, Tp, hd * Tp, seg_d, nwin, nkv, n, s));
+        DLLM_TRY(launch_heads_transpose(dattended, QD, hd, attn_dot, false, Tp, hd * Tp, seg_d, nwin, nh, n, s));
+        AttnGemmCall g;
+        g.seg = seg_d;
+        g.windows = nwin;
+        g.heads = nh;
+        g.max_len = n;
+        g.head_dim = hd;
+        g.group = G;
+        g.window = c.sliding_window;
+        // dP^T[j][t] = sum_i v[j][i] dout[t][i]
+        g.A = AttnOperand{attn_vt, nkv * hd * Tp, 0, hd * Tp, G, Tp, 0, 1};
+        g.B = AttnOperand{attn_dot, nh * hd * Tp, 0, hd * Tp, 1, Tp, 0, 1};
+        g.C = AttnOperand{attn_dpt, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
+        g.rows_kind = 0;
+        g.cols_kind = 0;
+        g.L = hd;
+        g.mask = kMaskTileCausal;
+        g.cols_per_lane = 4;
+        g.exact_products = true;
+        g.out_double = true;
+        g.out_scale = 1.0;
+        DLLM_TRY(launch_attn_gemm(g, s));
+        // p = e inv, D, ds = p (dp - D) scale (in place over E^T and dP^T)
+        DLLM_TRY(launch_dsoftmax_rows(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp,
+                                      c.attention_scale, s));
+        // dq[t] = sum_j ds[t][j] k[j]
+        AttnGemmCall q = g;
+        q.A = AttnOperand{attn_dpt, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
+        q.B = AttnOperand{sv.k, 0, nkv * hd, hd, G, nkv * hd, 0, 1};
+        q.C = AttnOperand{dq_t, 0, nh * hd, hd, 1, nh * hd, 0, 1};
+        q.cols_kind = 1;
+        q.L = 0;
+        q.mask = kMaskQueryRows;
+        q.cols_per_lane = hd % 256 == 0 ? 4 : 2;
+        q.exact_products = false;
+        q.out_double = false;
+        DLLM_TRY(launch_attn_gemm(q, s));
+        // key-row operands: [w][g][(t, hh)][j]
+        const int64_t gz = Tp * G * Tp;
+        DLLM_TRY(launch_regroup(attn_dpt, Tp, Tp * Tp, attn_dsg, Tp, gz, seg_d, nwin, nh, G, n, s));
+        DLLM_TRY(launch_regroup(et, Tp, Tp * Tp, attn_pg, Tp, gz, seg_d, nwin, nh, G, n, s));
+        // dk[j] = sum over (t, hh) of ds q, dv[j] = sum of p dout
+        AttnGemmCall k = g;
+        k.heads = nkv;
+        k.A = AttnOperand{attn_dsg, nkv * gz, 0, gz, 1, Tp, 0, 1};
+        k.B = AttnOperand{sv.q, 0, nh * hd, G * hd, 1, nh * hd, hd, G};
+        k.C = AttnOperand{dk_t, 0, nkv * hd, hd, 1, nkv * hd, 0, 1};
+        k.cols_kind = 1;
+        k.L = 0;
+        k.mask = kMaskKeyRows;
+        k.cols_per_lane = hd % 256 == 0 ? 4 : 2;
+        k.exact_products = false;
+        k.out_double = false;
+        DLLM_TRY(launch_attn_gemm(k, s));
+        AttnGemmCall v = k;
+        v.A = AttnOperand{attn_pg, nkv * gz, 0, gz, 1, Tp, 0, 1};
+        v.B = AttnOperand{dattended, 0, nh * hd, G * hd, 1, nh * hd, hd, G};
+        v.C = AttnOperand{dv_t, 0, nkv * hd, hd, 1, nkv * hd, 0, 1};
+        return launch_attn_gemm(v, s);
+    }
+
     // One layer's forward (backprop.py:423-487).
     int forward_layer(int64_t l, int64_t R, const AttentionBatch& b, float* x_out, hipStream_t s) {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
@@ -552,9 +680,7 @@ struct dllm_hip_trainer {
         }
         DLLM_TRY(launch_rope(qsrc, pos_index, cos_t, sin_t, sv.q, R, c.heads, c.head_dim, c.rotary_dim, 0, 0, s));
         DLLM_TRY(launch_rope(ksrc, pos_index, cos_t, sin_t, sv.k, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 0, s));
-        AttentionShape sh{R, R, c.heads, c.kv_heads, c.head_dim, c.head_dim, c.attention_scale, 1, 0,
-                          c.sliding_window, 0.0};
-        DLLM_TRY(launch_attention(sv.q, sv.k, sv.v, sv.attended, sh, b, s));
+        DLLM_TRY(attention_forward(l, sv, b, s));
         DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
         DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
         DLLM_TRY(linear_fwd(sv.h2, R, H, L.gate, nullptr, sv.gate, nullptr, s));
@@ -587,9 +713,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(prepare_dy(dx_mid, R, H, dy_d, big_T, s));
         DLLM_TRY(linear_dx(big_T, R, L.o, dattended, nullptr, s));
         DLLM_TRY(linear_dw(dy_d, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, s));
-        AttentionShape sh{R, R, c.heads, c.kv_heads, c.head_dim, c.head_dim, c.attention_scale, 1, 0,
-                          c.sliding_window, 0.0};
-        DLLM_TRY(launch_attention_backward(sv.q, sv.k, sv.v, dattended, dq_t, dk_t, dv_t, sh, b, R, R, attn_ws, s));
+        DLLM_TRY(attention_backward(l, sv, b, s));
         DLLM_TRY(launch_rope(dq_t, pos_index, cos_t, sin_t, dq, R, c.heads, c.head_dim, c.rotary_dim, 0, 1, s));
         DLLM_TRY(launch_rope(dk_t, pos_index, cos_t, sin_t, dk, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 1, s));
         const float* dqf = dq;
@@ -704,6 +828,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(prepare(tokens, offsets, lengths, windows, &R, &b, &groups, s));
         if (!wt_valid) DLLM_TRY(refresh_transposes(s));
         const int nseg = static_cast<int>(windows);
+        nwin = windows;
         const double eps = c.rms_norm_eps;
         // forward (backprop.py:411-490)
         DLLM_TRY(launch_gather_rows(P(emb), tok_in, saved[0].x_in, R, H, s));
