@@ -10,14 +10,21 @@
 // ascending order, whatever the tile shape or grid: no split-K, no atomics, no cross-lane reduction, so the bits are
 // independent of M, of the batch and of the CU count.
 //
-// Mapping to CDNA4: a wave owns 16 consecutive i (wave-uniform, so its A values come through scalar loads and are
-// broadcast to all 64 lanes for free as SGPR operands of v_fma_f64) by 256 consecutive j (4 per lane, one 16-byte
-// coalesced load of B per l, converted to double in registers). Per l a lane issues 64 DFMAs for one vector load
-// and 4 conversions; the 4 waves of a workgroup are stacked along i and share the B row through L1/L2.
+// Mapping to CDNA4: a wave owns 16 consecutive i (wave-uniform A values, broadcast to all 64 lanes) by 256
+// consecutive j (4 per lane, converted to double in registers); per l a lane issues 64 DFMAs for one 16-byte B read
+// and 4 conversions. The 4 waves of a workgroup are stacked along i. Two kernels share that mapping:
+//   gemm_lds_kernel (B rows 16-byte aligned, J % 4 == 0: every matmul of the training step): the workgroup's A and
+//     B tiles for 16 consecutive l are copied global -> LDS with gfx950's direct-to-LDS loads, double-buffered, so
+//     the next stage is in flight during the 16 x 64 DFMAs of the current one; A is read from LDS as a broadcast.
+//     Workgroups are renumbered so each XCD (own L2) gets a contiguous range of tiles, which share A and B rows.
+//   gemm_kernel (any J and alignment): A through scalar loads as SGPR operands, B through per-lane loads.
 //
 // Segmented mode (dW over several training windows): the l range is split into segments (one per window); each
 // segment's sum is rounded to float and the per-window results are added in float in window order, the first one
 // copied (trainer.py:328-332), optionally plus a per-window addend row (the tied embedding's own gradient).
+// When the tile grid is too small to fill the GPU and a scratch buffer is given, the windows run as separate
+// workgroups into per-window float partials, and a second pass adds them in window order: the same roundings in
+// the same order.
 #include "common.h"
 #include "kernels.h"
 
@@ -29,6 +36,7 @@ constexpr int kTileI = 16;     // rows per wave
 constexpr int kWavesI = 4;     // waves per workgroup, stacked along i
 constexpr int kTileJ = 256;    // columns per wave (4 per lane)
 constexpr int kBlockI = kTileI * kWavesI;
+constexpr int64_t kParallelWindowsBelow = 2048;  // tiles
 
 struct GemmParams {
     const double* A;
@@ -47,6 +55,7 @@ struct GemmParams {
     const float* seg_addend;  // segmented mode: per-window addend rows
     const int* seg_addrow;    // [nseg][I]: row of seg_addend for (window, i), or -1 (adds +0.0f)
     int64_t ld_seg_add;
+    float* partial;  // segment-parallel mode: [nseg][I][J] per-window results (null: windows run in sequence)
 };
 
 // The raw B values of row l for this lane's 4 columns. Lanes past J read a clamped in-bounds column instead (their
@@ -152,6 +161,223 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
 }
 
+constexpr int kChunk = 16;      // l per LDS stage
+constexpr int kStageLoads = 6;  // 16-byte direct-to-LDS loads per lane per stage: 2 for A, 4 for B
+
+struct Stage {
+    double a[kChunk][kBlockI];  // A[l][i] for the stage's l and the workgroup's 64 i
+    float b[kChunk][kTileJ];    // B[l][j] for the stage's l and the workgroup's 256 j
+};
+
+// 16 bytes from global memory to LDS at lds_row + 16 * lane (gfx950 direct-to-LDS load; M0 holds the LDS address).
+// Written as inline assembly so the compiler's wait-count pass does not stall the LDS reads of the current stage on
+// the in-flight copies of the next one; the pipeline waits for its own copies explicitly (wait_stage).
+__device__ __forceinline__ void copy16_to_lds(const void* src, const void* lds_row) {
+    typedef __attribute__((address_space(3))) const void* lds_address;
+    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+// Waits until at most `pending` of this wave's vector-memory operations are outstanding, then joins the workgroup.
+template <int kPending>
+__device__ __forceinline__ void wait_stage() {
+    if (kPending == 0)
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPending) : "memory");
+}
+
+__device__ __forceinline__ void workgroup_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Issues the copies of stage rows l .. l + kChunk - 1 (rows past `last` repeat row `last`; they are never read).
+// Wave w copies A rows 4w .. 4w + 3 (two rows of 64 doubles per instruction) and B rows 4w .. 4w + 3.
+__device__ __forceinline__ void issue_stage(const GemmParams& p, Stage& st, const double* a_src, const float* b_src,
+                                            int64_t l, int64_t last, int wave, int lane) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int r = 4 * wave + 2 * t;
+        const int64_t lr = l + r + (lane >> 5) <= last ? l + r + (lane >> 5) : last;
+        copy16_to_lds(a_src + lr * p.lda, &st.a[r][0]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int r = 4 * wave + t;
+        const int64_t lr = l + r <= last ? l + r : last;
+        copy16_to_lds(b_src + lr * p.ldb, &st.b[r][0]);
+    }
+}
+
+// acc[Q][c] = fma(A[l][i0 + Q], b[c], acc[Q][c]) for c < 4. Lane L's `a` holds A[l][i0 + L % 16]; the DPP64
+// modifier row_newbcast:Q on the FMA itself hands lane Q of each 16-lane row to the whole row, so the wave's 16 A
+// values cost one 8-byte register per lane instead of 16 broadcast reads. s_nop 1 gives the two wait states a DPP
+// source needs after a vector write (the compiler's hazard checks do not look inside the statement).
+template <int Q>
+__device__ __forceinline__ void fma4_bcast(double (&acc)[kTileI][4], double a, const double (&b)[4]) {
+    asm("s_nop 1\n\t"
+        "v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+        : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
+        : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
+}
+
+template <int Q>
+__device__ __forceinline__ void fma_row(double (&acc)[kTileI][4], double a, const double (&b)[4]) {
+    if constexpr (Q < kTileI) {
+        fma4_bcast<Q>(acc, a, b);
+        fma_row<Q + 1>(acc, a, b);
+    }
+}
+
+// One stage row in registers: this lane's A value (A[l][i0 + lane % 16]) and its 4 raw B values.
+struct RowOperands {
+    double a;
+    float4 b;
+};
+
+__device__ __forceinline__ RowOperands read_row(const Stage& st, int k, int wave, int lane) {
+    return {st.a[k][wave * kTileI + (lane & 15)], *reinterpret_cast<const float4*>(&st.b[k][lane * 4])};
+}
+
+// acc[q][c] += A[l][i0 + q] * B[l][j0 + c] for one stage row.
+__device__ __forceinline__ void row_fma(const RowOperands& r, double (&acc)[kTileI][4]) {
+    const double bd[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    fma_row<0>(acc, r.a, bd);
+}
+
+// Rows 0 .. n-1 of a stage, l ascending; row k + 1 is read from LDS while row k's 64 FMAs run.
+template <int kN>
+__device__ __forceinline__ void stage_rows(const Stage& st, int n, int wave, int lane, double (&acc)[kTileI][4]) {
+    if (kN > 0) {
+        RowOperands cur = read_row(st, 0, wave, lane);
+#pragma unroll
+        for (int k = 0; k < kN; ++k) {
+            RowOperands next = cur;
+            if (k + 1 < kN) next = read_row(st, k + 1, wave, lane);
+            row_fma(cur, acc);
+            cur = next;
+        }
+    } else {
+        for (int k = 0; k < n; ++k) row_fma(read_row(st, k, wave, lane), acc);
+    }
+}
+
+// One segment's sums through the double-buffered LDS pipeline: acc[q][c] = sum over l in [l0, l1), ascending.
+__device__ __forceinline__ void accumulate_lds(const GemmParams& p, Stage (&st)[2], int64_t i_blk, int64_t j_blk,
+                                               int wave, int lane, int64_t l0, int64_t l1, double (&acc)[kTileI][4]) {
+#pragma unroll
+    for (int q = 0; q < kTileI; ++q)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[q][c] = 0.0;
+    if (l0 >= l1) return;
+    const int64_t last = l1 - 1;
+    const double* a_src = p.A + i_blk + (lane & 31) * 2;
+    const int64_t jl = j_blk + lane * 4 <= p.J - 4 ? j_blk + lane * 4 : p.J - 4;
+    const float* b_src = p.B + jl;
+    const int64_t full = (l1 - l0) / kChunk;
+    const int tail = static_cast<int>((l1 - l0) % kChunk);
+    const int64_t chunks = full + (tail ? 1 : 0);
+    issue_stage(p, st[0], a_src, b_src, l0, last, wave, lane);
+    for (int64_t c = 0; c < full; ++c) {
+        if (c + 1 < chunks) {
+            issue_stage(p, st[(c + 1) & 1], a_src, b_src, l0 + (c + 1) * kChunk, last, wave, lane);
+            wait_stage<kStageLoads>();
+        } else {
+            wait_stage<0>();
+        }
+        stage_rows<kChunk>(st[c & 1], kChunk, wave, lane, acc);
+        workgroup_barrier();  // the stage is read by every wave before the next issue overwrites it
+    }
+    if (tail) {  // its copies were issued with the last full stage (or first, when there is none)
+        wait_stage<0>();
+        stage_rows<0>(st[full & 1], tail, wave, lane, acc);
+        workgroup_barrier();
+    }
+}
+
+// Hardware workgroup id -> logical tile id such that each XCD (workgroups are dealt round-robin over the 8 XCDs)
+// runs one contiguous range of tiles.
+__device__ __forceinline__ int64_t xcd_contiguous(int64_t hw, int64_t n) {
+    constexpr int64_t kXcds = 8;
+    const int64_t q = n / kXcds, r = n % kXcds, x = hw % kXcds, k = hw / kXcds;
+    return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+}
+
+enum LdsMode { kPlain = 0, kWindowsInSequence = 1, kWindowsInParallel = 2 };
+
+template <int kMode>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_lds_kernel(GemmParams p,
+                                                                                                   int64_t gx,
+                                                                                                   int64_t gy,
+                                                                                                   int64_t gz) {
+    __shared__ Stage st[2];
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int64_t id = xcd_contiguous(blockIdx.x, gx * gy * gz);
+    const int64_t bx = id % gx, by = (id / gx) % gy, bz = id / (gx * gy);
+    const int64_t i_blk = by * kBlockI, j_blk = bx * kTileJ;
+    const int64_t i0 = i_blk + wave * kTileI;
+    const int64_t j0 = j_blk + lane * 4;
+    double acc[kTileI][4];
+    if (kMode == kPlain) {
+        accumulate_lds(p, st, i_blk, j_blk, wave, lane, p.l0, p.l1, acc);
+        if (i0 >= p.I) return;
+#pragma unroll
+        for (int q = 0; q < kTileI; ++q) {
+            const int64_t i = i0 + q;
+            if (i >= p.I) break;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int64_t j = j0 + c;
+                if (j >= p.J) continue;
+                double v = acc[q][c];
+                if (p.bias) v += static_cast<double>(p.bias[j]);
+                float r = static_cast<float>(v);
+                if (p.addsrc) r = p.addsrc[i * p.ld_add + j] + r;
+                p.C[i * p.ldc + j] = r;
+            }
+        }
+        return;
+    }
+    const int s_begin = kMode == kWindowsInParallel ? static_cast<int>(bz) : 0;
+    const int s_end = kMode == kWindowsInParallel ? s_begin + 1 : p.nseg;
+    for (int s = s_begin; s < s_end; ++s) {
+        accumulate_lds(p, st, i_blk, j_blk, wave, lane, p.seg[s], p.seg[s + 1], acc);
+        if (i0 >= p.I) continue;
+        float* out_base = kMode == kWindowsInParallel ? p.partial + static_cast<int64_t>(s) * p.I * p.J : p.C;
+        int64_t ld_out = kMode == kWindowsInParallel ? p.J : p.ldc;
+        // opaque per window, so the compiler keeps no 64 output addresses live across the reduction
+        asm volatile("" : "+s"(out_base), "+s"(ld_out));
+#pragma unroll
+        for (int q = 0; q < kTileI; ++q) {
+            const int64_t i = i0 + q;
+            if (i >= p.I) break;
+            const int arow = p.seg_addrow ? p.seg_addrow[static_cast<int64_t>(s) * p.I + i] : -1;
+            float* out = out_base + i * ld_out + j0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (j0 + c >= p.J) continue;
+                float r = static_cast<float>(acc[q][c]);
+                if (p.seg_addrow) r = r + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j0 + c] : 0.0f);
+                out[c] = (kMode == kWindowsInParallel || s == 0) ? r : out[c] + r;
+            }
+        }
+    }
+}
+
+// C[i][j] = partial[0][i][j] + partial[1][i][j] + ... in float, window order (trainer.py:328-332).
+__global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict__ partial, int64_t I, int64_t J,
+                                                         int nseg, float* __restrict__ C, int64_t ldc) {
+    const int64_t n = I * J;
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; e < n;
+         e += static_cast<int64_t>(gridDim.x) * 256) {
+        float t = partial[e];
+        for (int s = 1; s < nseg; ++s) t = t + partial[static_cast<int64_t>(s) * n + e];
+        C[(e / J) * ldc + e % J] = t;
+    }
+}
+
 // dst[r][c] (double, row stride ldd) = src[r][c] and dstT[c][r] (double, row stride lddT) = src[r][c]; either may
 // be null. Tiles of 64 x 64 through LDS so both the reads and the transposed writes are coalesced.
 __global__ __launch_bounds__(256) void to_double_kernel(const float* __restrict__ src, int64_t rows, int64_t cols,
@@ -209,8 +435,35 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     DLLM_REQUIRE(g.lda >= padded_rows(g.I), "the double operand must be padded to whole row tiles");
     if (g.I == 0 || g.J == 0) return kOk;
     GemmParams p{g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.I, g.J, g.l0, g.l1, g.seg, g.nseg, g.bias, g.addsrc,
-                 g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add};
+                 g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr};
     const bool vec = (g.J % 4 == 0) && (g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.B) % 16 == 0);
+    if (vec && (g.lda % 2 == 0) && (reinterpret_cast<uintptr_t>(g.A) % 16 == 0)) {
+        const int64_t gx = ceil_div(g.J, kTileJ), gy = ceil_div(g.I, kBlockI);
+        int64_t gz = 1;
+        // windows in parallel when the tile grid alone leaves most of the 256 CUs x 3 workgroups idle
+        if (g.seg && g.nseg > 1 && g.seg_partial && gx * gy < kParallelWindowsBelow &&
+            static_cast<int64_t>(g.nseg) * g.I * g.J <= g.seg_partial_cap) {
+            p.partial = g.seg_partial;
+            gz = g.nseg;
+        }
+        DLLM_REQUIRE(gx * gy * gz < (int64_t{1} << 31), "matmul grid too large for one launch");
+        const dim3 grid(static_cast<unsigned>(gx * gy * gz));
+        if (p.partial)
+            hipLaunchKernelGGL(gemm_lds_kernel<kWindowsInParallel>, grid, dim3(256), 0, stream, p, gx, gy, gz);
+        else if (g.seg)
+            hipLaunchKernelGGL(gemm_lds_kernel<kWindowsInSequence>, grid, dim3(256), 0, stream, p, gx, gy, gz);
+        else
+            hipLaunchKernelGGL(gemm_lds_kernel<kPlain>, grid, dim3(256), 0, stream, p, gx, gy, gz);
+        DLLM_TRY(check_launch("gemm"));
+        if (p.partial) {
+            const int64_t n = g.I * g.J;
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 256), 8192));
+            hipLaunchKernelGGL(window_sum_kernel, dim3(blocks), dim3(256), 0, stream, p.partial, g.I, g.J, g.nseg,
+                               g.C, g.ldc);
+            return check_launch("gemm window sum");
+        }
+        return kOk;
+    }
     dim3 grid(static_cast<unsigned>(ceil_div(g.J, kTileJ)), static_cast<unsigned>(ceil_div(g.I, kBlockI)));
     DLLM_REQUIRE(grid.y <= 65535u, "matmul has too many rows for one launch");
     if (vec)

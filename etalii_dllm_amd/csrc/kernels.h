@@ -29,6 +29,10 @@ struct GemmCall {
     const float* seg_addend = nullptr; // segmented: per-window addend rows
     const int* seg_addrow = nullptr;   // [nseg][I] rows into seg_addend, -1 for none
     int64_t ld_seg_add = 0;
+    // segmented: optional scratch of seg_partial_cap floats; when nseg * I * J fit and the tile grid is small, the
+    // windows run in parallel into it and a second pass adds them in window order
+    float* seg_partial = nullptr;
+    int64_t seg_partial_cap = 0;
 };
 
 int launch_gemm(const GemmCall& g, hipStream_t stream);

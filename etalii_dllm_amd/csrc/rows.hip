@@ -95,20 +95,44 @@ __global__ __launch_bounds__(256) void rms_norm_backward_kernel(const float* __r
 
 // part[s][i] = f32(sum over rows of segment s ascending of term(r, i)): kind 0 term = dy (db, grad.hpp:52-54),
 // kind 1 term = (dy x) inv_rms[r] (norm weight, grad.hpp:95).
+constexpr int kColSegs = 64;  // segments per column-sums launch
+
+struct ColSegments {
+    int64_t off[kColSegs + 1];
+};
+
+// part[s][i] = f32(sum over rows r of segment s, ascending, of term(r, i)) for 64 columns per workgroup: the four
+// waves stage the terms of 64 rows x 64 columns in LDS (64 independent loads in flight per lane group), then one
+// wave runs the 64 serial additions per column out of LDS, and the next 64 rows follow.
 __global__ __launch_bounds__(256) void column_partial_kernel(int kind, const float* __restrict__ dy,
                                                              const float* __restrict__ x,
-                                                             const double* __restrict__ inv, int64_t dim, int64_t r0,
-                                                             int64_t r1, float* __restrict__ part) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= dim) return;
+                                                             const double* __restrict__ inv, int64_t dim,
+                                                             ColSegments seg, float* __restrict__ part) {
+    __shared__ double terms[64][64];
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+    const int64_t col = i < dim ? i : dim - 1;
+    const int64_t r0 = seg.off[blockIdx.y], r1 = seg.off[blockIdx.y + 1];
     double acc = 0.0;
-    if (kind == 0) {
-        for (int64_t r = r0; r < r1; ++r) acc += static_cast<double>(dy[r * dim + i]);
-    } else {
-        for (int64_t r = r0; r < r1; ++r)
-            acc += static_cast<double>(dy[r * dim + i]) * static_cast<double>(x[r * dim + i]) * inv[r];
+    for (int64_t base = r0; base < r1; base += 64) {
+        const int n = static_cast<int>(r1 - base < 64 ? r1 - base : 64);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int row = wave + 4 * k;
+            if (row < n) {
+                const int64_t r = base + row;
+                double t = static_cast<double>(dy[r * dim + col]);
+                if (kind != 0) t = t * static_cast<double>(x[r * dim + col]) * inv[r];
+                terms[row][lane] = t;
+            }
+        }
+        __syncthreads();
+        if (wave == 0)
+            for (int row = 0; row < n; ++row) acc += terms[row][lane];
+        __syncthreads();
     }
-    part[i] = static_cast<float>(acc);
+    if (wave == 0 && i < dim) part[static_cast<int64_t>(blockIdx.y) * dim + i] = static_cast<float>(acc);
 }
 
 // out[i] = part[0][i] + part[1][i] + ... in float, segment order (trainer.py:328-332: the first copied).
@@ -248,12 +272,17 @@ int launch_column_sums(int kind, const float* dy, const float* x, const double* 
                        const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream) {
     if (dim == 0) return kOk;
     DLLM_REQUIRE(nseg >= 1, "column sums need a segment");
-    const unsigned blocks = static_cast<unsigned>(ceil_div(dim, 256));
-    for (int s = 0; s < nseg; ++s) {
-        float* part = nseg == 1 ? out : partial + static_cast<int64_t>(s) * dim;
-        hipLaunchKernelGGL(column_partial_kernel, dim3(blocks), dim3(256), 0, stream, kind, dy, x, inv_rms, dim,
-                           seg_host[s], seg_host[s + 1], part);
+    DLLM_REQUIRE(nseg == 1 || partial != nullptr, "column sums over several segments need a partial buffer");
+    const unsigned col_blocks = static_cast<unsigned>(ceil_div(dim, 64));
+    for (int s0 = 0; s0 < nseg; s0 += kColSegs) {
+        const int count = nseg - s0 < kColSegs ? nseg - s0 : kColSegs;
+        ColSegments seg{};
+        for (int s = 0; s <= count; ++s) seg.off[s] = seg_host[s0 + s];
+        float* part = nseg == 1 ? out : partial + static_cast<int64_t>(s0) * dim;
+        hipLaunchKernelGGL(column_partial_kernel, dim3(col_blocks, static_cast<unsigned>(count)), dim3(256), 0, stream,
+                           kind, dy, x, inv_rms, dim, seg, part);
     }
+    const unsigned blocks = static_cast<unsigned>(ceil_div(dim, 256));
     if (nseg > 1) hipLaunchKernelGGL(segment_float_sum_kernel, dim3(blocks), dim3(256), 0, stream, partial, dim, nseg, out);
     return check_launch("column_sums");
 }

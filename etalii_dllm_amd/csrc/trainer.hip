@@ -155,7 +155,8 @@ struct dllm_hip_trainer {
     double *dl_d = nullptr, *big_T = nullptr, *dy_d = nullptr;
     float *dx = nullptr, *dh = nullptr, *dx_mid = nullptr, *dattended = nullptr, *dq_t = nullptr, *dk_t = nullptr,
           *dv_t = nullptr, *dq = nullptr, *dk = nullptr, *dq2 = nullptr, *dk2 = nullptr, *dproduct = nullptr,
-          *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *emb_rows = nullptr;
+          *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *emb_rows = nullptr, *gemm_part = nullptr;
+    int64_t gemm_part_cap = 0;  // floats: per-window partials of the layer weight gradients
     double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
            *per_tensor = nullptr, *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
     void* attn_ws = nullptr;
@@ -374,6 +375,10 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&dgate, R * I));
         DLLM_TRY(make(&dup, R * I));
         DLLM_TRY(make(&col_part, W_max * std::max<int64_t>({H, QD, KVD, I})));
+        if (W_max > 1) {
+            gemm_part_cap = W_max * H * std::max<int64_t>({QD, KVD, I});
+            DLLM_TRY(make(&gemm_part, gemm_part_cap));
+        }
         DLLM_TRY(make(&emb_rows, R * H));
         DLLM_TRY(make(&inv_rms, R * std::max<int64_t>(heads, 1)));
         DLLM_TRY(make(&row_max, R));
@@ -528,6 +533,8 @@ struct dllm_hip_trainer {
         g.seg_addrow = addrow_;
         g.seg_addend = addend;
         g.ld_seg_add = K;
+        g.seg_partial = gemm_part;
+        g.seg_partial_cap = gemm_part_cap;
         return gemm(g, s);
     }
 
