@@ -169,6 +169,55 @@ def cpu_baseline(cfg) -> dict | None:
     }
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration() -> int:
+    """A plain copy kernel of known size (1 GiB read, 1 GiB written), three times: under rocprofv3 --pmc its
+    FETCH_SIZE / WRITE_SIZE give the counters' scale against bytes actually moved."""
+    import torch
+
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return 0
+
+
+def _counter_rows(path: str, kernel_substring: str, counter: str) -> list[float]:
+    import csv
+
+    out = []
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            if kernel_substring in row["Kernel_Name"] and row["Counter_Name"] == counter:
+                out.append(float(row["Counter_Value"]))
+    return out
+
+
+def traffic_summary(config: str, fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_csv: str) -> int:
+    """HBM bytes per matmul launch = mean(FETCH_SIZE) x fetch scale + mean(WRITE_SIZE) x write scale, the scales
+    being the copy kernel's known bytes over what the same counters read for it (counters are in KiB)."""
+    fetch = _counter_rows(fetch_csv, "gemm_lds_kernel", "FETCH_SIZE")
+    write = _counter_rows(write_csv, "gemm_lds_kernel", "WRITE_SIZE")
+    copy_fetch = max(_counter_rows(copy_fetch_csv, "copy", "FETCH_SIZE") or
+                     _counter_rows(copy_fetch_csv, "elementwise", "FETCH_SIZE"))
+    copy_write = max(_counter_rows(copy_write_csv, "copy", "WRITE_SIZE") or
+                     _counter_rows(copy_write_csv, "elementwise", "WRITE_SIZE"))
+    fetch_scale = COPY_BYTES / (copy_fetch * 1024.0)
+    write_scale = COPY_BYTES / (copy_write * 1024.0)
+    per_launch = (sum(fetch) / len(fetch) * 1024.0 * fetch_scale + sum(write) / len(write) * 1024.0 * write_scale)
+    path = ROOT / "profiles" / "gemm_traffic.json"
+    data = json.loads(path.read_text()) if path.exists() else {}
+    data[config] = {"bytes_per_launch": per_launch, "launches": len(fetch), "fetch_scale": fetch_scale,
+                    "write_scale": write_scale, "fetch_kib_mean": sum(fetch) / len(fetch),
+                    "write_kib_mean": sum(write) / len(write)}
+    path.write_text(json.dumps(data, indent=1) + "\n")
+    print(json.dumps(data[config]))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,7 +225,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of 1 GiB (the reference kernel for HBM byte counters)")
+    ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
+                    help="turn rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter files into profiles/gemm_traffic.json")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
+    if args.traffic_summary:
+        return traffic_summary(args.config, *args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this backend runs the step on a single MI355X (got --gpus {args.gpus}); "
               "the multi-GPU design is described in DESIGN.md", file=sys.stderr)
@@ -221,7 +278,8 @@ def main() -> int:
     traffic = None
     traffic_file = ROOT / "profiles" / "gemm_traffic.json"
     if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get(args.config)
+        entry = json.loads(traffic_file.read_text()).get(args.config)
+        traffic = entry["bytes_per_launch"] if entry else None
     baseline = None
     if not args.no_cpu_baseline:
         log("timing the reference CPU path on a bounded sample")

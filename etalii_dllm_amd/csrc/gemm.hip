@@ -16,7 +16,8 @@
 //   gemm_lds_kernel (B rows 16-byte aligned, J % 4 == 0: every matmul of the training step): the workgroup's A and
 //     B tiles for 16 consecutive l are copied global -> LDS with gfx950's direct-to-LDS loads, double-buffered, so
 //     the next stage is in flight during the 16 x 64 DFMAs of the current one; A is read from LDS as a broadcast.
-//     Workgroups are renumbered so each XCD (own L2) gets a contiguous range of tiles, which share A and B rows.
+//     Workgroups are renumbered so each XCD (own L2) gets a contiguous range of tiles, grouped 8 row blocks deep
+//     so the tiles resident together share their A and B stages (fewer HBM re-reads).
 //   gemm_kernel (any J and alignment): A through scalar loads as SGPR operands, B through per-lane loads.
 //
 // Segmented mode (dW over several training windows): the l range is split into segments (one per window); each
@@ -37,6 +38,7 @@ constexpr int kWavesI = 4;     // waves per workgroup, stacked along i
 constexpr int kTileJ = 256;    // columns per wave (4 per lane)
 constexpr int kBlockI = kTileI * kWavesI;
 constexpr int64_t kParallelWindowsBelow = 2048;  // tiles
+constexpr int64_t kGroupRows = 8;                // row blocks per L2 group
 
 struct GemmParams {
     const double* A;
@@ -315,7 +317,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int64_t id = xcd_contiguous(blockIdx.x, gx * gy * gz);
-    const int64_t bx = id % gx, by = (id / gx) % gy, bz = id / (gx * gy);
+    // groups of kGroupRows row blocks x all column blocks, column-major inside a group: an XCD's resident
+    // workgroups cover about 8 x 12 tiles and share their A and B stages through its L2
+    const int64_t t = id % (gx * gy), bz = id / (gx * gy);
+    const int64_t first = t / (kGroupRows * gx) * kGroupRows;
+    const int64_t rows_in_group = gy - first < kGroupRows ? gy - first : kGroupRows;
+    const int64_t by = first + (t % (kGroupRows * gx)) % rows_in_group;
+    const int64_t bx = (t % (kGroupRows * gx)) / rows_in_group;
     const int64_t i_blk = by * kBlockI, j_blk = bx * kTileJ;
     const int64_t i0 = i_blk + wave * kTileI;
     const int64_t j0 = j_blk + lane * 4;
