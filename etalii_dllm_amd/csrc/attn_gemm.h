@@ -23,7 +23,7 @@ struct AttnOperand {
 };
 
 struct AttnGemmCall {
-    AttnOperand A;  // double [L rows][>= 16-row tiles], the wave-uniform operand
+    AttnOperand A;  // double [L rows][>= 16-row tiles, even], the broadcast operand
     AttnOperand B;  // float [L rows][columns]
     AttnOperand C;  // float or double output [rows][columns]
     const double* rowscale = nullptr;  // output row multiplier before rounding, [z][row]
@@ -32,7 +32,11 @@ struct AttnGemmCall {
     int64_t windows = 0, heads = 0, max_len = 0, head_dim = 0, group = 1, window = 0, L = 0;
     int rows_kind = 0, cols_kind = 0;  // 0: window positions, 1: head_dim
     int mask = kMaskNone;
-    int cols_per_lane = 4;
+    int cols_per_lane = 4;           // 1, 2 or 4: a workgroup covers 64 x cols_per_lane columns
+    int tile_rows = 16;              // 16, or 8 with cols_per_lane 1 (twice the workgroups for long reductions)
+    int64_t b_row_alloc = 0;         // floats readable per B row from column 0 (multiple of 4, >= J); 0: J
+    double* scratch = nullptr;       // float outputs: running sums between the kernels, windows*heads*I*J doubles
+    int64_t scratch_doubles = 0;
     bool exact_products = true;  // float x float products: fused multiply-add is exact
     bool out_double = false;
     double out_scale = 1.0;

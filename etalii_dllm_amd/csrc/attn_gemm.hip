@@ -13,8 +13,8 @@
 //             D_t = sum_j p dp (serial), dS^T = p (dp - D) scale                     (one lane per query)
 //             dq[t] = f32(sum_j dS[t][j] k[j])                                       (keys ascending)
 //             dk[j] = f32(sum over (t ascending, head of the group ascending) dS q), dv[j] likewise with p and dOut
-// Each reduction runs exactly over the keys (or queries) the reference visits, in its order: rows of a tile that
-// see fewer keys are predicated off the extra steps, never fed zeros.
+// Each reduction runs exactly over the keys (or queries) the reference visits, in its order: the steps only some rows
+// of a tile take run in separate per-output kernels before and after the tile's common steps, never fed zeros.
 #include "attn_gemm.h"
 #include "common.h"
 #include "devmath.h"
@@ -23,9 +23,6 @@
 namespace dllm_hip {
 
 namespace {
-
-constexpr int kTI = 16;    // wave-uniform rows per wave
-constexpr int kWaves = 4;  // waves per workgroup, stacked along rows
 
 struct Operand {
     const void* ptr;
@@ -53,6 +50,11 @@ struct AttnGemmParams {
     int64_t window;
     int64_t L;        // reduction length when unmasked (head_dim)
     double out_scale; // double outputs: value = acc * out_scale
+    int64_t b_row_alloc;  // floats readable in each B row from column 0 (multiple of 4, >= J)
+    double* partial;      // running sums between the edge and body kernels: [z][i][j]
+    int64_t partial_zstride, partial_ld;
+    int cols_per_lane;
+    int tile_rows;        // 8 or 16 (the edge kernels rebuild the body kernel's tiles)
 };
 
 // The keys query t sees (causal, q_offset 0, optional window): [lo, hi).
@@ -68,117 +70,377 @@ __device__ __forceinline__ void key_span(int64_t j, int64_t n, int64_t window, i
     *hi = (t_hi + 1) * G;
 }
 
-template <int CJ>
-__device__ __forceinline__ void load_cols(const float* row, int64_t j0, int64_t J, float out[CJ]) {
-#pragma unroll
-    for (int c = 0; c < CJ; ++c) out[c] = row[j0 + c < J ? j0 + c : J - 1];
+// 16 bytes global -> LDS at lds_row + 16 * lane (gfx950 direct-to-LDS load, M0 = LDS address). Inline assembly keeps
+// the compiler's wait-count pass from stalling reads of the current stage on the next stage's copies; the kernel
+// waits for its copies explicitly.
+__device__ __forceinline__ void copy16_to_lds(const void* src, const void* lds_row) {
+    typedef __attribute__((address_space(3))) const void* lds_address;
+    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
-template <int CJ, bool kFma, bool kPredicated>
-__device__ __forceinline__ void run_steps(const double* __restrict__ A, int64_t lda, const float* __restrict__ B,
-                                          const Operand& bo, int64_t i0, int64_t j0, int64_t J, int64_t l_begin,
-                                          int64_t l_end, const int64_t lo[kTI], const int64_t hi[kTI],
-                                          double acc[kTI][CJ]) {
-    int64_t t = l_begin / bo.group, hh = l_begin % bo.group;
-    for (int64_t l = l_begin; l < l_end; ++l) {
-        const float* brow = B + t * bo.ld + hh * bo.ld_inner;
-        float bv[CJ];
-        load_cols<CJ>(brow, j0, J, bv);
-        const double* arow = A + l * lda + i0;
+template <int kPending>
+__device__ __forceinline__ void wait_copies() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPending) : "memory");
+}
+
+// A body tile: TI rows (8 or 16) x 64 CJ columns, one wave; a stage holds TI x (128 / TI) = 128 A values (1 KB, one
+// copy) and 128 / TI rows of 64 CJ B values.
+template <int CJ, int TI>
+struct Tile {
+    static constexpr int kSteps = 128 / TI;            // reduction steps per LDS stage
+    static constexpr int kBCopies = kSteps * CJ / 4;   // 16-byte copies per lane for B
+    static constexpr int kCopies = 1 + kBCopies;
+    static constexpr int kBuffers = CJ == 4 ? 2 : CJ == 2 ? 3 : 4;  // stages in flight (LDS: 5-18 KB per workgroup)
+    struct Stage {
+        double a[kSteps][TI];
+        float b[kSteps][64 * CJ];
+    };
+};
+
+// acc[Q][c] = fma(A[l][i0 + Q], b[c], acc[Q][c]): lane L's `a` holds A[l][i0 + L % TI] and the DPP64 modifier
+// row_newbcast:Q on the FMA hands lane Q of each 16-lane row to the whole row. s_nop 1: the two wait states a DPP
+// source needs after a vector write (the compiler's hazard checks do not look inside the statement).
+template <int CJ, int TI, int Q>
+__device__ __forceinline__ void fma_bcast(double (&acc)[TI][CJ], double a, const double (&b)[CJ]) {
+    if constexpr (CJ == 4)
+        asm("s_nop 1\n\t"
+            "v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+            : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
+            : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
+    else if constexpr (CJ == 2)
+        asm("s_nop 1\n\t"
+            "v_fmac_f64_dpp %0, %2, %3 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
+            "v_fmac_f64_dpp %1, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf"
+            : "+v"(acc[Q][0]), "+v"(acc[Q][1])
+            : "v"(a), "v"(b[0]), "v"(b[1]), "n"(Q));
+    else
+        asm("s_nop 1\n\t"
+            "v_fmac_f64_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+            : "+v"(acc[Q][0])
+            : "v"(a), "v"(b[0]), "n"(Q));
+}
+
+// A[l][i0 + Q + k] in every lane for k < 4 (lane Q + k of each 16-lane row, broadcast by DPP64 moves); four at a
+// time so the products that follow are four independent chains.
+template <int Q>
+__device__ __forceinline__ void broadcast_rows4(double a, double (&r)[4]) {
+    asm("s_nop 1\n\t"
+        "v_mov_b64_dpp %0, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b64_dpp %1, %4 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b64_dpp %2, %4 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b64_dpp %3, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(a), "n"(Q), "n"(Q + 1), "n"(Q + 2), "n"(Q + 3));
+}
+
+// The reduction steps of tile rows i0 .. i0 + rows - 1 (rows past I behave like row I - 1 and are never stored)
+// split in three ascending parts per row: a ragged head [lo(i), m0), a body [m0, m1) that every row of the tile
+// takes, in whole LDS stages, and a ragged tail [m1, hi(i)). The body runs in the pipelined matmul kernel; the head
+// before it and the tail after it run in one-thread-per-output kernels (attn_edge_kernel), the running double sum
+// passed through `partial` - so each output is still one accumulation over its steps in the reference's order.
+struct TileSplit {
+    int64_t m0, m1;   // the body
+    bool head, tail;  // some row has steps before m0 / after m1
+};
+
+__device__ __forceinline__ void row_span(const AttnGemmParams& p, int64_t r, int64_t n, int64_t* lo, int64_t* hi) {
+    if (p.mask == kMaskQueryRows) {
+        query_span(r, p.window, lo, hi);
+    } else if (p.mask == kMaskKeyRows) {
+        key_span(r, n, p.window, p.group, lo, hi);
+    } else {
+        *lo = 0;
+        *hi = p.L;
+    }
+}
+
+__device__ __forceinline__ TileSplit tile_split(const AttnGemmParams& p, int64_t i0, int64_t rows, int64_t steps,
+                                                int64_t I, int64_t n) {
+    // the spans' ends are non-decreasing in the row, so the tile's first and last rows bound them
+    const int64_t r_last = i0 + rows - 1 < I ? i0 + rows - 1 : I - 1;
+    int64_t lo_f, hi_f, lo_l, hi_l;
+    row_span(p, i0, n, &lo_f, &hi_f);
+    row_span(p, r_last, n, &lo_l, &hi_l);
+    TileSplit t;
+    if (lo_l < hi_f) {  // steps every row takes: [lo_l, hi_f)
+        t.m0 = lo_l;
+        t.m1 = lo_l + (hi_f - lo_l) / steps * steps;
+    } else {
+        t.m0 = t.m1 = lo_l;
+    }
+    t.head = lo_f < t.m0;
+    t.tail = hi_l > t.m1;
+    return t;
+}
+
+// S^T / dP^T tiles (rows keys j, columns queries t) none of whose queries sees any of their keys are skipped.
+__device__ __forceinline__ bool tile_unseen(const AttnGemmParams& p, int64_t i0, int64_t rows, int64_t jw0,
+                                            int64_t cols) {
+    if (p.mask != kMaskTileCausal) return false;
+    if (i0 > jw0 + cols - 1) return true;
+    return p.window != 0 && i0 + rows - 1 + p.window - 1 < jw0;
+}
+
+template <int CJ>
+struct RowOperands {
+    double a;
+    float b[CJ];
+};
+
+template <int CJ, int TI>
+__device__ __forceinline__ RowOperands<CJ> read_row(const typename Tile<CJ, TI>::Stage& st, int k, int lane) {
+    RowOperands<CJ> r;
+    r.a = st.a[k][lane & (TI - 1)];
+    if constexpr (CJ == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&st.b[k][lane * 4]);
+        r.b[0] = v.x; r.b[1] = v.y; r.b[2] = v.z; r.b[3] = v.w;
+    } else if constexpr (CJ == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(&st.b[k][lane * 2]);
+        r.b[0] = v.x; r.b[1] = v.y;
+    } else {
+        r.b[0] = st.b[k][lane];
+    }
+    return r;
+}
+
+// One step for every row of the tile: exact products by fused multiply-add, the others as a rounded product then a
+// rounded sum (four rows at a time).
+template <int CJ, int TI, bool kExact, int Q>
+__device__ __forceinline__ void step_rows(double (&acc)[TI][CJ], double a, const double (&b)[CJ]) {
+    if constexpr (Q < TI) {
+        if constexpr (kExact) {
+            fma_bcast<CJ, TI, Q>(acc, a, b);
+            step_rows<CJ, TI, kExact, Q + 1>(acc, a, b);
+        } else {
+            double aq[4];
+            broadcast_rows4<Q>(a, aq);
+            double prod[4][CJ];
 #pragma unroll
-        for (int q = 0; q < kTI; ++q) {
-            const double a = arow[q];
-            if (kPredicated && !(l >= lo[q] && l < hi[q])) continue;
+            for (int k = 0; k < 4; ++k)
 #pragma unroll
-            for (int c = 0; c < CJ; ++c) {
-                if (kFma)
-                    acc[q][c] = __builtin_fma(a, static_cast<double>(bv[c]), acc[q][c]);
-                else
-                    acc[q][c] = acc[q][c] + a * static_cast<double>(bv[c]);
-            }
-        }
-        if (++hh == bo.group) {
-            hh = 0;
-            ++t;
+                for (int c = 0; c < CJ; ++c) prod[k][c] = aq[k] * b[c];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int c = 0; c < CJ; ++c) acc[Q + k][c] = acc[Q + k][c] + prod[k][c];
+            step_rows<CJ, TI, kExact, Q + 4>(acc, a, b);
         }
     }
 }
 
-template <int CJ, bool kFma, bool kOutDouble>
-__global__ __launch_bounds__(256) void attn_gemm_kernel(AttnGemmParams p) {
-    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-    const int lane = static_cast<int>(threadIdx.x) & 63;
+// Copies of the stage holding steps l .. l + kSteps - 1.
+template <int CJ, int TI>
+__device__ __forceinline__ void issue_stage(typename Tile<CJ, TI>::Stage& st, const double* a_base, int64_t lda,
+                                            const float* b_base, const Operand& bo, int64_t b_col, int64_t l,
+                                            int lane) {
+    using T = Tile<CJ, TI>;
+    // A: kSteps rows x TI doubles (TI / 2 lanes per row), lane L -> row L / (TI / 2), doubles 2 (L % (TI / 2)) .. + 1
+    copy16_to_lds(a_base + (l + lane / (TI / 2)) * lda + (lane % (TI / 2)) * 2, &st.a[0][0]);
+    // B: kSteps rows x 64 CJ floats, 16 CJ lanes per row; b_col is this lane's chunk (see run_tile). Row offsets
+    // stepped from one (uniform, scalar) division
+    int64_t off[T::kSteps];
+    {
+        int64_t t = l / bo.group, hh = l % bo.group;
+#pragma unroll
+        for (int r = 0; r < T::kSteps; ++r) {
+            off[r] = t * bo.ld + hh * bo.ld_inner;
+            if (++hh == bo.group) {
+                hh = 0;
+                ++t;
+            }
+        }
+    }
+    constexpr int kLanesPerRow = 16 * CJ;
+    constexpr int kRowsPerCopy = 64 / kLanesPerRow;
+    const int sub = lane / kLanesPerRow;
+#pragma unroll
+    for (int t = 0; t < T::kBCopies; ++t) {
+        int64_t row = off[t * kRowsPerCopy];
+#pragma unroll
+        for (int k = 1; k < kRowsPerCopy; ++k)
+            if (sub == k) row = off[t * kRowsPerCopy + k];
+        copy16_to_lds(b_base + row + b_col, &st.b[t * kRowsPerCopy][0]);
+    }
+}
+
+// The steps of a stage, unrolled; the next step's operands are read from LDS while this step's products run.
+template <int CJ, int TI, bool kExact>
+__device__ __forceinline__ void stage_steps(const typename Tile<CJ, TI>::Stage& st, int lane, double (&acc)[TI][CJ]) {
+    using T = Tile<CJ, TI>;
+    RowOperands<CJ> cur = read_row<CJ, TI>(st, 0, lane);
+#pragma unroll
+    for (int k = 0; k < T::kSteps; ++k) {
+        RowOperands<CJ> next = cur;
+        if (k + 1 < T::kSteps) next = read_row<CJ, TI>(st, k + 1, lane);
+        double bd[CJ];
+#pragma unroll
+        for (int c = 0; c < CJ; ++c) bd[c] = cur.b[c];
+        step_rows<CJ, TI, kExact, 0>(acc, cur.a, bd);
+        cur = next;
+    }
+}
+
+// Where a running sum waits between kernels: the double output itself (finished in place by the tail kernel), or
+// the float outputs' scratch [z][i][j].
+template <bool kOutDouble>
+__device__ __forceinline__ double* partial_base(const AttnGemmParams& p, int64_t w, int64_t seg_w, int64_t hz,
+                                                int64_t z, int64_t* ld) {
+    if (kOutDouble) {
+        *ld = p.C.ld;
+        return const_cast<double*>(base_of<double>(p.C, w, seg_w, hz));
+    }
+    *ld = p.partial_ld;
+    return p.partial + z * p.partial_zstride;
+}
+
+template <bool kOutDouble>
+__device__ __forceinline__ void store_output(const AttnGemmParams& p, int64_t w, int64_t seg_w, int64_t hz, int64_t z,
+                                             int64_t i, int64_t j, double v) {
+    if (kOutDouble) {
+        double* C = const_cast<double*>(base_of<double>(p.C, w, seg_w, hz));
+        C[i * p.C.ld + j] = v * p.out_scale;
+    } else {
+        float* C = const_cast<float*>(base_of<float>(p.C, w, seg_w, hz));
+        if (p.rowscale) v = v * p.rowscale[z * p.rowscale_zstride + i];
+        C[i * p.C.ld + j] = static_cast<float>(v);
+    }
+}
+
+// The body of one TI-row x 64 CJ-column tile of (window, head) z: acc[q][c] (+)= sum over l in [m0, m1), ascending,
+// of A_z[l][i0 + q] * B_z[l][jw0 + lane CJ + c]; operands staged through LDS in a ring of stages filled by gfx950's
+// direct-to-LDS loads.
+template <int CJ, int TI, bool kExact, bool kOutDouble>
+__device__ __forceinline__ void run_tile(const AttnGemmParams& p, typename Tile<CJ, TI>::Stage* st, int lane,
+                                         int64_t z, int64_t w, int64_t hz, int64_t seg_w, int64_t n, int64_t I,
+                                         int64_t J, int64_t i0, int64_t jw0) {
+    using T = Tile<CJ, TI>;
+    if (i0 >= I || jw0 >= J || tile_unseen(p, i0, TI, jw0, 64 * CJ)) return;  // workgroup-uniform
+    const TileSplit ts = tile_split(p, i0, TI, T::kSteps, I, n);
+    const double* A = base_of<double>(p.A, w, seg_w, hz) + i0;
+    const float* B = base_of<float>(p.B, w, seg_w, hz);
+    // this lane's 16-byte B chunk in each row: columns jw0 + 4 (lane % 16 CJ) .. + 3; chunks past the readable row
+    // (b_row_alloc, a multiple of 4 that is >= J) read its last chunk instead, and their columns are never stored
+    const int64_t chunk = jw0 + 4 * (lane % (16 * CJ));
+    const int64_t b_col = chunk + 4 <= p.b_row_alloc ? chunk : p.b_row_alloc - 4;
+    int64_t part_ld;
+    double* part = partial_base<kOutDouble>(p, w, seg_w, hz, z, &part_ld);
+    double acc[TI][CJ];
+#pragma unroll
+    for (int q = 0; q < TI; ++q)
+#pragma unroll
+        for (int c = 0; c < CJ; ++c) {
+            const int64_t i = i0 + q, j = jw0 + lane * CJ + c;
+            acc[q][c] = ts.head && i < I && j < J ? part[i * part_ld + j] : 0.0;
+        }
+    // consume the loaded sums here, so the wait for them is placed before the copy pipeline rather than inside it
+    // (a vector-memory wait there would also drain the stage copies in flight)
+#pragma unroll
+    for (int q = 0; q < TI; ++q)
+#pragma unroll
+        for (int c = 0; c < CJ; ++c) asm volatile("" ::"v"(acc[q][c]));
+    const int64_t stages = (ts.m1 - ts.m0) / T::kSteps;
+    // a ring of kBuffers stages: stage s + kBuffers - 1 is requested before stage s is computed
+    for (int64_t s0 = 0; s0 < T::kBuffers - 1 && s0 < stages; ++s0)
+        issue_stage<CJ, TI>(st[s0], A, p.A.ld, B, p.B, b_col, ts.m0 + s0 * T::kSteps, lane);
+    for (int64_t sidx = 0; sidx < stages; ++sidx) {
+        const int64_t ahead = sidx + T::kBuffers - 1;
+        if (ahead < stages)
+            issue_stage<CJ, TI>(st[ahead % T::kBuffers], A, p.A.ld, B, p.B, b_col, ts.m0 + ahead * T::kSteps, lane);
+        // stages issued after this one: min(kBuffers - 1, stages - 1 - sidx)
+        const int64_t later = stages - 1 - sidx < T::kBuffers - 1 ? stages - 1 - sidx : T::kBuffers - 1;
+        if (later >= 3)
+            wait_copies<3 * T::kCopies>();
+        else if (later == 2)
+            wait_copies<2 * T::kCopies>();
+        else if (later == 1)
+            wait_copies<T::kCopies>();
+        else
+            wait_copies<0>();
+        stage_steps<CJ, TI, kExact>(st[sidx % T::kBuffers], lane, acc);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this stage's reads are done before it is refilled
+    }
+#pragma unroll
+    for (int q = 0; q < TI; ++q) {
+        const int64_t i = i0 + q;
+        if (i >= I) break;
+#pragma unroll
+        for (int c = 0; c < CJ; ++c) {
+            const int64_t j = jw0 + lane * CJ + c;
+            if (j >= J) continue;
+            if (ts.tail)
+                part[i * part_ld + j] = acc[q][c];
+            else
+                store_output<kOutDouble>(p, w, seg_w, hz, z, i, j, acc[q][c]);
+        }
+    }
+}
+
+// One workgroup (one wave) runs row tiles y and tiles - 1 - y of one (z, column block): the tiles' serial
+// reductions grow (or shrink) with the row, so every workgroup gets about the same total work.
+template <int CJ, int TI, bool kExact, bool kOutDouble>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(CJ == 4 ? 3 : 4))) void attn_gemm_kernel(
+    AttnGemmParams p) {
+    using T = Tile<CJ, TI>;
+    __shared__ typename T::Stage st[T::kBuffers];
+    const int lane = static_cast<int>(threadIdx.x);
     const int64_t z = blockIdx.z;
     const int64_t w = z / p.heads, hz = z % p.heads;
     const int64_t seg_w = p.seg[w], n = p.seg[w + 1] - seg_w;
     const int64_t I = p.rows_kind == 0 ? n : p.head_dim;
     const int64_t J = p.cols_kind == 0 ? n : p.head_dim;
-    const int64_t i0 = (static_cast<int64_t>(blockIdx.y) * kWaves + wave) * kTI;
-    const int64_t j0 = static_cast<int64_t>(blockIdx.x) * 64 * CJ + lane * CJ;
-    const int64_t jw0 = static_cast<int64_t>(blockIdx.x) * 64 * CJ;  // first column of the wave
-    if (i0 >= I || jw0 >= J) return;  // wave-uniform
-    if (p.mask == kMaskTileCausal) {
-        // S^T / dP^T tiles: rows are keys j, columns queries t; a tile no query of which sees any of its keys is skipped
-        const int64_t t_last = jw0 + 64 * CJ - 1;
-        if (i0 > t_last) return;
-        if (p.window != 0 && i0 + kTI - 1 + p.window - 1 < jw0) return;
-    }
-    int64_t lo[kTI], hi[kTI];
-    int64_t l_begin = 0, l_end = p.L, common_lo = 0, common_hi = p.L;
-    if (p.mask == kMaskQueryRows || p.mask == kMaskKeyRows) {
-        l_begin = INT64_MAX;
-        l_end = 0;
-        common_lo = 0;
-        common_hi = INT64_MAX;
-#pragma unroll
-        for (int q = 0; q < kTI; ++q) {
-            const int64_t r = i0 + q < I ? i0 + q : I - 1;
-            if (p.mask == kMaskQueryRows)
-                query_span(r, p.window, &lo[q], &hi[q]);
-            else
-                key_span(r, n, p.window, p.group, &lo[q], &hi[q]);
-            l_begin = lo[q] < l_begin ? lo[q] : l_begin;
-            l_end = hi[q] > l_end ? hi[q] : l_end;
-            common_lo = lo[q] > common_lo ? lo[q] : common_lo;
-            common_hi = hi[q] < common_hi ? hi[q] : common_hi;
-        }
-        if (common_lo > common_hi) common_lo = common_hi = l_begin;  // no step shared by all rows
+    const int64_t tiles = (I + TI - 1) / TI;
+    const int64_t y = blockIdx.y, y2 = tiles - 1 - y;
+    const int64_t jw0 = static_cast<int64_t>(blockIdx.x) * 64 * CJ;
+    if (y > y2) return;
+    run_tile<CJ, TI, kExact, kOutDouble>(p, st, lane, z, w, hz, seg_w, n, I, J, y * TI, jw0);
+    if (y2 != y) run_tile<CJ, TI, kExact, kOutDouble>(p, st, lane, z, w, hz, seg_w, n, I, J, y2 * TI, jw0);
+}
+
+// The ragged head (kHead) or tail of every output: one thread per (z, i, j), continuing the running sum in `partial`
+// over its row's steps outside the tile body, then (tail) rounding and storing the output.
+template <bool kHead, bool kExact, bool kOutDouble>
+__global__ __launch_bounds__(256) void attn_edge_kernel(AttnGemmParams p, int64_t max_i, int64_t max_j) {
+    const int64_t z = blockIdx.z;
+    const int64_t w = z / p.heads, hz = z % p.heads;
+    const int64_t seg_w = p.seg[w], n = p.seg[w + 1] - seg_w;
+    const int64_t I = p.rows_kind == 0 ? n : p.head_dim;
+    const int64_t J = p.cols_kind == 0 ? n : p.head_dim;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 64 + (threadIdx.x & 63);
+    const int64_t i = static_cast<int64_t>(blockIdx.y) * 4 + (threadIdx.x >> 6);
+    if (i >= I || j >= J || i >= max_i || j >= max_j) return;
+    const int64_t rows = p.tile_rows, cols = 64 * p.cols_per_lane;
+    const int64_t i0 = i / rows * rows;
+    if (tile_unseen(p, i0, rows, j / cols * cols, cols)) return;  // the body kernel's tiles
+    const TileSplit ts = tile_split(p, i0, rows, 128 / rows, I, n);
+    if (kHead ? !ts.head : !ts.tail) return;
+    int64_t lo, hi;
+    row_span(p, i, n, &lo, &hi);
+    int64_t from, to;
+    if (kHead) {
+        from = lo;
+        to = hi < ts.m0 ? hi : ts.m0;
     } else {
-#pragma unroll
-        for (int q = 0; q < kTI; ++q) {
-            lo[q] = 0;
-            hi[q] = p.L;
-        }
+        from = lo > ts.m1 ? lo : ts.m1;
+        to = hi;
     }
-    const double* A = base_of<double>(p.A, w, seg_w, hz);
-    const float* B = base_of<float>(p.B, w, seg_w, hz);
-    double acc[kTI][CJ];
-#pragma unroll
-    for (int q = 0; q < kTI; ++q)
-#pragma unroll
-        for (int c = 0; c < CJ; ++c) acc[q][c] = 0.0;
-    if (common_lo > l_begin) run_steps<CJ, kFma, true>(A, p.A.ld, B, p.B, i0, j0, J, l_begin, common_lo, lo, hi, acc);
-    run_steps<CJ, kFma, false>(A, p.A.ld, B, p.B, i0, j0, J, common_lo, common_hi, lo, hi, acc);
-    if (l_end > common_hi) run_steps<CJ, kFma, true>(A, p.A.ld, B, p.B, i0, j0, J, common_hi, l_end, lo, hi, acc);
-#pragma unroll
-    for (int q = 0; q < kTI; ++q) {
-        const int64_t i = i0 + q;
-        if (i >= I) break;
-#pragma unroll
-        for (int c = 0; c < CJ; ++c) {
-            const int64_t j = j0 + c;
-            if (j >= J) continue;
-            if (kOutDouble) {
-                double* C = const_cast<double*>(base_of<double>(p.C, w, seg_w, hz));
-                C[i * p.C.ld + j] = acc[q][c] * p.out_scale;
-            } else {
-                float* C = const_cast<float*>(base_of<float>(p.C, w, seg_w, hz));
-                double v = acc[q][c];
-                if (p.rowscale) v = v * p.rowscale[z * p.rowscale_zstride + i];
-                C[i * p.C.ld + j] = static_cast<float>(v);
-            }
-        }
+    int64_t part_ld;
+    double* part = partial_base<kOutDouble>(p, w, seg_w, hz, z, &part_ld) + i * part_ld + j;
+    double acc = kHead ? 0.0 : *part;
+    const double* A = base_of<double>(p.A, w, seg_w, hz) + i;
+    const float* B = base_of<float>(p.B, w, seg_w, hz) + j;
+    for (int64_t l = from; l < to; ++l) {
+        const double a = A[l * p.A.ld];
+        const double b = static_cast<double>(B[(l / p.B.group) * p.B.ld + (l % p.B.group) * p.B.ld_inner]);
+        acc = kExact ? __builtin_fma(a, b, acc) : acc + a * b;
     }
+    if (kHead)
+        *part = acc;
+    else
+        store_output<kOutDouble>(p, w, seg_w, hz, z, i, j, acc);
 }
 
 // One lane per query t of a (window, head): the forward softmax chains over its visible keys (nn.hpp:541-561):
@@ -311,22 +573,57 @@ int launch_attn_gemm(const AttnGemmCall& c, hipStream_t stream) {
     p.out_scale = c.out_scale;
     const int64_t I = c.rows_kind == 0 ? c.max_len : c.head_dim;
     const int64_t J = c.cols_kind == 0 ? c.max_len : c.head_dim;
-    const int cj = c.cols_per_lane;
-    DLLM_REQUIRE(cj == 2 || cj == 4, "columns per lane must be 2 or 4");
-    dim3 grid(static_cast<unsigned>(ceil_div(J, 64 * cj)), static_cast<unsigned>(ceil_div(I, kTI * kWaves)),
-              static_cast<unsigned>(c.windows * c.heads));
-    if (I == 0 || J == 0 || grid.z == 0) return kOk;
-#define DLLM_ATTN_LAUNCH(CJ, FMA, OUTD)                                                                 \
-    hipLaunchKernelGGL((attn_gemm_kernel<CJ, FMA, OUTD>), grid, dim3(256), 0, stream, p)
-    if (cj == 4 && c.exact_products && c.out_double) DLLM_ATTN_LAUNCH(4, true, true);
-    else if (cj == 4 && c.exact_products) DLLM_ATTN_LAUNCH(4, true, false);
-    else if (cj == 4 && c.out_double) DLLM_ATTN_LAUNCH(4, false, true);
-    else if (cj == 4) DLLM_ATTN_LAUNCH(4, false, false);
-    else if (c.exact_products && c.out_double) DLLM_ATTN_LAUNCH(2, true, true);
-    else if (c.exact_products) DLLM_ATTN_LAUNCH(2, true, false);
-    else if (c.out_double) DLLM_ATTN_LAUNCH(2, false, true);
-    else DLLM_ATTN_LAUNCH(2, false, false);
-#undef DLLM_ATTN_LAUNCH
+    const int64_t Z = c.windows * c.heads;
+    p.b_row_alloc = c.b_row_alloc > 0 ? c.b_row_alloc : J;
+    p.partial = c.scratch;
+    p.partial_ld = J;
+    p.partial_zstride = I * J;
+    p.cols_per_lane = c.cols_per_lane;
+    p.tile_rows = c.tile_rows;
+    const int cj = c.cols_per_lane, ti = c.tile_rows;
+    DLLM_REQUIRE((ti == 16 && (cj == 1 || cj == 2 || cj == 4)) || (ti == 8 && cj == 1),
+                 "attention tiles are 16 rows x 64, 128 or 256 columns, or 8 rows x 64 columns");
+    DLLM_REQUIRE(p.b_row_alloc % 4 == 0 && p.b_row_alloc >= J, "attention operand rows must hold whole 16-byte chunks");
+    DLLM_REQUIRE(c.A.ld % 2 == 0 && c.A.ld >= static_cast<int64_t>(round_up(static_cast<size_t>(I), 16)),
+                 "attention double operand rows must be padded to whole 16-row tiles");
+    DLLM_REQUIRE(c.out_double || (c.scratch != nullptr && c.scratch_doubles >= Z * I * J),
+                 "attention matmul scratch too small");
+    if (I == 0 || J == 0 || Z == 0) return kOk;
+    const dim3 body(static_cast<unsigned>(ceil_div(J, 64 * cj)), static_cast<unsigned>(ceil_div(ceil_div(I, ti), 2)),
+                    static_cast<unsigned>(Z));
+    const dim3 edge(static_cast<unsigned>(ceil_div(J, 64)), static_cast<unsigned>(ceil_div(I, 4)),
+                    static_cast<unsigned>(Z));
+    const bool heads_possible = c.mask == kMaskKeyRows || (c.mask == kMaskQueryRows && c.window != 0);
+    const bool tails_possible = c.mask == kMaskQueryRows || c.mask == kMaskKeyRows || c.L % (128 / ti) != 0;
+    const bool ex = c.exact_products, od = c.out_double;
+#define DLLM_ATTN_EDGE(HEAD, EXACT, OUTD) \
+    hipLaunchKernelGGL((attn_edge_kernel<HEAD, EXACT, OUTD>), edge, dim3(256), 0, stream, p, I, J)
+#define DLLM_ATTN_EDGES(HEAD)                            \
+    do {                                                \
+        if (ex && od) DLLM_ATTN_EDGE(HEAD, true, true); \
+        else if (ex) DLLM_ATTN_EDGE(HEAD, true, false); \
+        else if (od) DLLM_ATTN_EDGE(HEAD, false, true); \
+        else DLLM_ATTN_EDGE(HEAD, false, false);        \
+    } while (0)
+#define DLLM_ATTN_BODY(CJ, TI, EXACT, OUTD) \
+    hipLaunchKernelGGL((attn_gemm_kernel<CJ, TI, EXACT, OUTD>), body, dim3(64), 0, stream, p)
+#define DLLM_ATTN_BODIES(CJ, TI)                            \
+    do {                                                   \
+        if (ex && od) DLLM_ATTN_BODY(CJ, TI, true, true);  \
+        else if (ex) DLLM_ATTN_BODY(CJ, TI, true, false);  \
+        else if (od) DLLM_ATTN_BODY(CJ, TI, false, true);  \
+        else DLLM_ATTN_BODY(CJ, TI, false, false);         \
+    } while (0)
+    if (heads_possible) DLLM_ATTN_EDGES(true);
+    if (ti == 8) DLLM_ATTN_BODIES(1, 8);
+    else if (cj == 4) DLLM_ATTN_BODIES(4, 16);
+    else if (cj == 2) DLLM_ATTN_BODIES(2, 16);
+    else DLLM_ATTN_BODIES(1, 16);
+    if (tails_possible) DLLM_ATTN_EDGES(false);
+#undef DLLM_ATTN_BODIES
+#undef DLLM_ATTN_BODY
+#undef DLLM_ATTN_EDGES
+#undef DLLM_ATTN_EDGE
     return check_launch("attention matmul");
 }
 

@@ -173,6 +173,8 @@ struct dllm_hip_trainer {
     void* norm_ws = nullptr;
     // attention as batched matmuls (attn_gemm.hip): per (window, head) transposed operands and score matrices
     int64_t Tp = 0;
+    double* attn_scratch = nullptr;  // running sums of the attention matmuls' float outputs
+    int64_t attn_scratch_doubles = 0;
     double *attn_kt = nullptr, *attn_vt = nullptr, *attn_et = nullptr, *attn_inv = nullptr, *attn_dpt = nullptr,
            *attn_pg = nullptr, *attn_dsg = nullptr;
     float *attn_qt = nullptr, *attn_dot = nullptr;
@@ -399,6 +401,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&attn_dpt, W_max * heads * Tp * Tp));
         DLLM_TRY(make(&attn_pg, W_max * kvh * Tp * G * Tp));
         DLLM_TRY(make(&attn_dsg, W_max * kvh * Tp * G * Tp));
+        attn_scratch_doubles = W_max * heads * T_max * hd;
+        DLLM_TRY(make(&attn_scratch, attn_scratch_doubles));
         DLLM_TRY(make(&tok_in, R));
         DLLM_TRY(make(&tok_tgt, R));
         DLLM_TRY(make(&pos_index, R));
@@ -559,6 +563,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_heads_transpose(sv.q, QD, hd, attn_qt, false, Tp, hd * Tp, seg_d, nwin, nh, n, s));
         double* et = et_of(l);
         AttnGemmCall g;
+        g.scratch = attn_scratch;
+        g.scratch_doubles = attn_scratch_doubles;
         g.seg = seg_d;
         g.windows = nwin;
         g.heads = nh;
@@ -575,6 +581,7 @@ struct dllm_hip_trainer {
         g.L = hd;
         g.mask = kMaskTileCausal;
         g.cols_per_lane = 4;
+        g.b_row_alloc = Tp;
         g.exact_products = true;
         g.out_double = true;
         g.out_scale = c.attention_scale;
@@ -589,7 +596,8 @@ struct dllm_hip_trainer {
         o.cols_kind = 1;
         o.L = 0;
         o.mask = kMaskQueryRows;
-        o.cols_per_lane = hd % 256 == 0 ? 4 : 2;
+        o.cols_per_lane = hd >= 128 ? 2 : 1;
+        o.b_row_alloc = 0;
         o.exact_products = false;
         o.out_double = false;
         o.rowscale = inv_of(l);
@@ -604,6 +612,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_heads_transpose(sv.v, KVD, hd, attn_vt, true, Tp, hd * Tp, seg_d, nwin, nkv, n, s));
         DLLM_TRY(launch_heads_transpose(dattended, QD, hd, attn_dot, false, Tp, hd * Tp, seg_d, nwin, nh, n, s));
         AttnGemmCall g;
+        g.scratch = attn_scratch;
+        g.scratch_doubles = attn_scratch_doubles;
         g.seg = seg_d;
         g.windows = nwin;
         g.heads = nh;
@@ -620,6 +630,7 @@ struct dllm_hip_trainer {
         g.L = hd;
         g.mask = kMaskTileCausal;
         g.cols_per_lane = 4;
+        g.b_row_alloc = Tp;
         g.exact_products = true;
         g.out_double = true;
         g.out_scale = 1.0;
@@ -635,7 +646,8 @@ struct dllm_hip_trainer {
         q.cols_kind = 1;
         q.L = 0;
         q.mask = kMaskQueryRows;
-        q.cols_per_lane = hd % 256 == 0 ? 4 : 2;
+        q.cols_per_lane = hd >= 128 ? 2 : 1;
+        q.b_row_alloc = 0;
         q.exact_products = false;
         q.out_double = false;
         DLLM_TRY(launch_attn_gemm(q, s));
@@ -652,7 +664,9 @@ struct dllm_hip_trainer {
         k.cols_kind = 1;
         k.L = 0;
         k.mask = kMaskKeyRows;
-        k.cols_per_lane = hd % 256 == 0 ? 4 : 2;
+        k.cols_per_lane = 1;  // long serial chains: more, smaller tiles
+        k.tile_rows = 8;
+        k.b_row_alloc = 0;
         k.exact_products = false;
         k.out_double = false;
         DLLM_TRY(launch_attn_gemm(k, s));
@@ -933,6 +947,7 @@ int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_t
     DLLM_REQUIRE(c.experts == 0, "mixture-of-experts layers are not supported by this trainer yet");
     DLLM_REQUIRE(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, "heads must be a multiple of kv_heads");
     DLLM_REQUIRE(c.rotary_dim > 0 && c.rotary_dim % 2 == 0 && c.rotary_dim <= c.head_dim, "invalid rotary_dim");
+    DLLM_REQUIRE(c.head_dim % 4 == 0, "head_dim must be a multiple of 4");
     DLLM_REQUIRE(max_tokens > 0 && max_windows > 0 && max_window_tokens > 0, "capacities must be positive");
     DLLM_REQUIRE(max_window_tokens <= 2048, "windows longer than 2048 tokens are not supported");
     DLLM_REQUIRE(max_tokens <= 65535, "at most 65535 tokens per step");
