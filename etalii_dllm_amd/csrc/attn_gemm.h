@@ -45,9 +45,10 @@ struct AttnGemmCall {
 int launch_attn_gemm(const AttnGemmCall& c, hipStream_t stream);
 int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
                         int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream);
+// dvec: windows * heads * inv_zstride doubles of workspace (the per-query D)
 int launch_dsoftmax_rows(double* et, double* dpt, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows,
                          int64_t heads, int64_t max_len, int64_t window, const double* inv, int64_t inv_zstride,
-                         double scale, hipStream_t stream);
+                         double scale, double* dvec, hipStream_t stream);
 int launch_regroup(const double* src, int64_t ld, int64_t zstride, double* dst, int64_t dst_ld, int64_t dst_zstride,
                    const int64_t* seg, int64_t windows, int64_t heads, int64_t group, int64_t max_len,
                    hipStream_t stream);

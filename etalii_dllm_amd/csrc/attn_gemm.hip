@@ -443,58 +443,148 @@ __global__ __launch_bounds__(256) void attn_edge_kernel(AttnGemmParams p, int64_
         store_output<kOutDouble>(p, w, seg_w, hz, z, i, j, acc);
 }
 
-// One lane per query t of a (window, head): the forward softmax chains over its visible keys (nn.hpp:541-561):
-// first maximum, then e = exp(s - max) written back over S^T and their serial total; inv_t = 1 / total.
-__global__ __launch_bounds__(64) void softmax_rows_kernel(double* __restrict__ st, int64_t ld, int64_t zstride,
-                                                          const int64_t* __restrict__ seg, int64_t heads,
-                                                          int64_t window, double* __restrict__ inv,
-                                                          int64_t inv_zstride) {
+// The forward softmax of every query (nn.hpp:541-561) in three passes over S^T (keys j, queries t; one lane per query
+// where the reference's order matters, every element in parallel where it does not):
+//   softmax_max_kernel    mx_t = first maximum over the visible keys, ascending (strictly greater replaces)
+//   softmax_exp_kernel    e = exp(s - mx_t) written over S^T (each element independent)
+//   softmax_total_kernel  total_t = sum of e over the visible keys ascending, inv_t = 1 / total_t
+// The lanes' loads are issued 8 keys ahead of their serial use.
+constexpr int kChainUnroll = 8;
+
+__global__ __launch_bounds__(64) void softmax_max_kernel(const double* __restrict__ st, int64_t ld, int64_t zstride,
+                                                         const int64_t* __restrict__ seg, int64_t heads,
+                                                         int64_t window, double* __restrict__ mx_out,
+                                                         int64_t mx_zstride) {
     const int64_t z = blockIdx.y;
     const int64_t w = z / heads;
     const int64_t n = seg[w + 1] - seg[w];
     const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
     if (t >= n) return;
-    double* s = st + z * zstride;
+    const double* s = st + z * zstride + t;
     int64_t lo, hi;
     query_span(t, window, &lo, &hi);
-    double mx = s[lo * ld + t];
-    for (int64_t j = lo + 1; j < hi; ++j) {
-        const double v = s[j * ld + t];
+    double mx = s[lo * ld];
+    int64_t j = lo + 1;
+    for (; j + kChainUnroll <= hi; j += kChainUnroll) {
+        double v[kChainUnroll];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) v[k] = s[(j + k) * ld];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k)
+            if (v[k] > mx) mx = v[k];
+    }
+    for (; j < hi; ++j) {
+        const double v = s[j * ld];
         if (v > mx) mx = v;
     }
-    double total = 0.0;
-    for (int64_t j = lo; j < hi; ++j) {
-        const double e = dexp(s[j * ld + t] - mx);
-        s[j * ld + t] = e;
-        total += e;
+    mx_out[z * mx_zstride + t] = mx;
+}
+
+// 256 queries x 8 keys per workgroup.
+__global__ __launch_bounds__(256) void softmax_exp_kernel(double* __restrict__ st, int64_t ld, int64_t zstride,
+                                                          const int64_t* __restrict__ seg, int64_t heads,
+                                                          int64_t window, const double* __restrict__ mx,
+                                                          int64_t mx_zstride) {
+    const int64_t z = blockIdx.z;
+    const int64_t w = z / heads;
+    const int64_t n = seg[w + 1] - seg[w];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t j0 = static_cast<int64_t>(blockIdx.y) * 8;
+    if (t >= n || j0 > t) return;
+    int64_t lo, hi;
+    query_span(t, window, &lo, &hi);
+    const double m = mx[z * mx_zstride + t];
+    double* s = st + z * zstride + t;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int64_t j = j0 + k;
+        if (j >= lo && j < hi) s[j * ld] = dexp(s[j * ld] - m);
     }
+}
+
+__global__ __launch_bounds__(64) void softmax_total_kernel(const double* __restrict__ st, int64_t ld, int64_t zstride,
+                                                           const int64_t* __restrict__ seg, int64_t heads,
+                                                           int64_t window, double* __restrict__ inv,
+                                                           int64_t inv_zstride) {
+    const int64_t z = blockIdx.y;
+    const int64_t w = z / heads;
+    const int64_t n = seg[w + 1] - seg[w];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (t >= n) return;
+    const double* s = st + z * zstride + t;
+    int64_t lo, hi;
+    query_span(t, window, &lo, &hi);
+    double total = 0.0;
+    int64_t j = lo;
+    for (; j + kChainUnroll <= hi; j += kChainUnroll) {
+        double v[kChainUnroll];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) v[k] = s[(j + k) * ld];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) total += v[k];
+    }
+    for (; j < hi; ++j) total += s[j * ld];
     inv[z * inv_zstride + t] = 1.0 / total;
 }
 
-// Backward chains per query (grad.hpp:262-278): p = e * inv (over E^T, in place), D = sum p dp (serial), and
-// ds = (p (dp - D)) scale over dP^T in place.
-__global__ __launch_bounds__(64) void dsoftmax_rows_kernel(double* __restrict__ et, double* __restrict__ dpt,
-                                                           int64_t ld, int64_t zstride,
-                                                           const int64_t* __restrict__ seg, int64_t heads,
-                                                           int64_t window, const double* __restrict__ inv,
-                                                           int64_t inv_zstride, double scale) {
+// The backward chains per query (grad.hpp:262-278) in two passes:
+//   dsoftmax_dot_kernel    D_t = sum over visible keys ascending of (e inv_t) dp (one lane per query)
+//   dsoftmax_apply_kernel  p = e inv_t over E^T and ds = (p (dp - D_t)) scale over dP^T (each element independent)
+__global__ __launch_bounds__(64) void dsoftmax_dot_kernel(const double* __restrict__ et, const double* __restrict__ dpt,
+                                                          int64_t ld, int64_t zstride,
+                                                          const int64_t* __restrict__ seg, int64_t heads,
+                                                          int64_t window, const double* __restrict__ inv,
+                                                          int64_t inv_zstride, double* __restrict__ dvec) {
     const int64_t z = blockIdx.y;
     const int64_t w = z / heads;
     const int64_t n = seg[w + 1] - seg[w];
     const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
     if (t >= n) return;
-    double* e = et + z * zstride;
-    double* d = dpt + z * zstride;
+    const double* e = et + z * zstride + t;
+    const double* d = dpt + z * zstride + t;
     const double iv = inv[z * inv_zstride + t];
     int64_t lo, hi;
     query_span(t, window, &lo, &hi);
     double weighted = 0.0;
-    for (int64_t j = lo; j < hi; ++j) {
-        const double pj = e[j * ld + t] * iv;
-        e[j * ld + t] = pj;
-        weighted += pj * d[j * ld + t];
+    int64_t j = lo;
+    for (; j + kChainUnroll <= hi; j += kChainUnroll) {
+        double term[kChainUnroll];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) term[k] = (e[(j + k) * ld] * iv) * d[(j + k) * ld];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) weighted += term[k];
     }
-    for (int64_t j = lo; j < hi; ++j) d[j * ld + t] = e[j * ld + t] * (d[j * ld + t] - weighted) * scale;
+    for (; j < hi; ++j) weighted += (e[j * ld] * iv) * d[j * ld];
+    dvec[z * inv_zstride + t] = weighted;
+}
+
+__global__ __launch_bounds__(256) void dsoftmax_apply_kernel(double* __restrict__ et, double* __restrict__ dpt,
+                                                             int64_t ld, int64_t zstride,
+                                                             const int64_t* __restrict__ seg, int64_t heads,
+                                                             int64_t window, const double* __restrict__ inv,
+                                                             int64_t inv_zstride, const double* __restrict__ dvec,
+                                                             double scale) {
+    const int64_t z = blockIdx.z;
+    const int64_t w = z / heads;
+    const int64_t n = seg[w + 1] - seg[w];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t j0 = static_cast<int64_t>(blockIdx.y) * 8;
+    if (t >= n || j0 > t) return;
+    int64_t lo, hi;
+    query_span(t, window, &lo, &hi);
+    const double iv = inv[z * inv_zstride + t];
+    const double D = dvec[z * inv_zstride + t];
+    double* e = et + z * zstride + t;
+    double* d = dpt + z * zstride + t;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int64_t j = j0 + k;
+        if (j >= lo && j < hi) {
+            const double p = e[j * ld] * iv;
+            e[j * ld] = p;
+            d[j * ld] = p * (d[j * ld] - D) * scale;
+        }
+    }
 }
 
 // dst[w][g][(t * G + hh)][j] = src[w][g * G + hh][j][t] (doubles): the key-row operand layout of dk / dv.
@@ -629,18 +719,31 @@ int launch_attn_gemm(const AttnGemmCall& c, hipStream_t stream) {
 
 int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
                         int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream) {
-    dim3 grid(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(windows * heads));
-    hipLaunchKernelGGL(softmax_rows_kernel, grid, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
+    if (max_len == 0 || windows * heads == 0) return kOk;
+    const dim3 lanes(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(windows * heads));
+    const dim3 elems(static_cast<unsigned>(ceil_div(max_len, 256)), static_cast<unsigned>(ceil_div(max_len, 8)),
+                     static_cast<unsigned>(windows * heads));
+    // the maxima wait in `inv` until the totals replace them
+    hipLaunchKernelGGL(softmax_max_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
+                       inv_zstride);
+    hipLaunchKernelGGL(softmax_exp_kernel, elems, dim3(256), 0, stream, st, ld, zstride, seg, heads, window, inv,
+                       inv_zstride);
+    hipLaunchKernelGGL(softmax_total_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
                        inv_zstride);
     return check_launch("attention softmax");
 }
 
 int launch_dsoftmax_rows(double* et, double* dpt, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows,
                          int64_t heads, int64_t max_len, int64_t window, const double* inv, int64_t inv_zstride,
-                         double scale, hipStream_t stream) {
-    dim3 grid(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(windows * heads));
-    hipLaunchKernelGGL(dsoftmax_rows_kernel, grid, dim3(64), 0, stream, et, dpt, ld, zstride, seg, heads, window, inv,
-                       inv_zstride, scale);
+                         double scale, double* dvec, hipStream_t stream) {
+    if (max_len == 0 || windows * heads == 0) return kOk;
+    const dim3 lanes(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(windows * heads));
+    const dim3 elems(static_cast<unsigned>(ceil_div(max_len, 256)), static_cast<unsigned>(ceil_div(max_len, 8)),
+                     static_cast<unsigned>(windows * heads));
+    hipLaunchKernelGGL(dsoftmax_dot_kernel, lanes, dim3(64), 0, stream, et, dpt, ld, zstride, seg, heads, window, inv,
+                       inv_zstride, dvec);
+    hipLaunchKernelGGL(dsoftmax_apply_kernel, elems, dim3(256), 0, stream, et, dpt, ld, zstride, seg, heads, window,
+                       inv, inv_zstride, dvec, scale);
     return check_launch("attention softmax backward");
 }
 

@@ -13,27 +13,6 @@ namespace dllm_hip {
 
 namespace {
 
-constexpr int kRowWaves = 4;  // rows (waves) per 256-thread block
-
-__device__ __forceinline__ double bcast0(double v) { return __shfl(v, 0, 64); }
-
-// sum over i ascending of x[i]^2 in double (nn.hpp:395-398), on the calling lane.
-__device__ __forceinline__ double serial_sum_squares(const float* __restrict__ x, int64_t dim) {
-    double s = 0.0;
-    int64_t i = 0;
-    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
-        for (; i + 4 <= dim; i += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(x + i);
-            s += static_cast<double>(v.x) * static_cast<double>(v.x);
-            s += static_cast<double>(v.y) * static_cast<double>(v.y);
-            s += static_cast<double>(v.z) * static_cast<double>(v.z);
-            s += static_cast<double>(v.w) * static_cast<double>(v.w);
-        }
-    }
-    for (; i < dim; ++i) s += static_cast<double>(x[i]) * static_cast<double>(x[i]);
-    return s;
-}
-
 // The forward scale (nn.hpp:401-404): w, or 1 + w with the unit offset.
 __device__ __forceinline__ double norm_scale(const float* w, int64_t i, int unit_offset) {
     if (w == nullptr) return 1.0;
@@ -46,51 +25,80 @@ __device__ __forceinline__ double norm_scale_backward(const float* w, int64_t i,
     return (unit_offset ? 1.0 : 0.0) + static_cast<double>(w[i]);
 }
 
-// rms_norm (nn.hpp:391-408): out = f32((x inv) scale), inv = 1 / sqrt(sum x^2 / dim + eps).
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                       float* __restrict__ out, int64_t rows, int64_t dim, double eps,
-                                                       int unit_offset, double* __restrict__ inv_out) {
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const float* xr = x + row * dim;
-    double inv = 0.0;
-    if (lane == 0) inv = 1.0 / sqrt(serial_sum_squares(xr, dim) / static_cast<double>(dim) + eps);
-    inv = bcast0(inv);
-    for (int64_t i = lane; i < dim; i += 64)
-        out[row * dim + i] = static_cast<float>(static_cast<double>(xr[i]) * inv * norm_scale(w, i, unit_offset));
-    if (inv_out && lane == 0) inv_out[row] = inv;
-}
+constexpr int kNormRows = 32;  // rows per 256-thread workgroup of the norm kernels
 
-// rms_norm_backward's dx (grad.hpp:83-104): per row the same inv, D = sum_i ((g_i dy_i) x_i) ascending,
-// coef = D inv inv inv / dim, dx = f32((inv g) dy - x coef); then out = addend + dx when addend is given.
-__global__ __launch_bounds__(256) void rms_norm_backward_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                                const float* __restrict__ dy, float* __restrict__ dx,
-                                                                const float* __restrict__ addend, int64_t rows,
-                                                                int64_t dim, double eps, int unit_offset,
-                                                                double* __restrict__ inv_out) {
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowWaves + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const float* xr = x + row * dim;
-    const float* dyr = dy + row * dim;
-    double inv = 0.0, coef = 0.0;
-    if (lane == 0) {
-        inv = 1.0 / sqrt(serial_sum_squares(xr, dim) / static_cast<double>(dim) + eps);
-        double d = 0.0;
-        for (int64_t i = 0; i < dim; ++i)
-            d += norm_scale_backward(w, i, unit_offset) * static_cast<double>(dyr[i]) * static_cast<double>(xr[i]);
-        coef = d * inv * inv * inv / static_cast<double>(dim);
+// rms_norm (nn.hpp:391-408) and rms_norm_backward's dx (grad.hpp:83-104), 32 rows per workgroup. Per row the serial
+// chains run one lane per row out of LDS: the four waves stage the terms of 32 rows x 64 columns (x^2, and for the
+// backward (g dy) x), then lanes 0-31 of wave 0 add the squares and lanes 32-63 the products, 64 columns at a time in
+// ascending order. Then every thread writes its elements:
+//   forward   out = f32((x inv) scale),              inv = 1 / sqrt(sum x^2 / dim + eps)
+//   backward  dx = f32((inv g) dy - x coef) (+ addend), coef = D inv inv inv / dim, D = sum (g dy) x
+template <bool kBackward>
+__global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                        const float* __restrict__ dy, float* __restrict__ out,
+                                                        const float* __restrict__ addend, int64_t rows, int64_t dim,
+                                                        double eps, int unit_offset, double* __restrict__ inv_out) {
+    __shared__ double squares[kNormRows][65];
+    __shared__ double products[kNormRows][65];
+    __shared__ double row_inv[kNormRows], row_coef[kNormRows];
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = static_cast<int>(threadIdx.x) >> 6;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kNormRows;
+    const int64_t nrows = rows - r0 < kNormRows ? rows - r0 : kNormRows;
+    double chain = 0.0;  // wave 0: lanes 0-31 the squares of row lane, lanes 32-63 the products of row lane - 32
+    for (int64_t c0 = 0; c0 < dim; c0 += 64) {
+        const int n = static_cast<int>(dim - c0 < 64 ? dim - c0 : 64);
+        if (lane < n) {
+            const int64_t col = c0 + lane;
+            const double g = kBackward ? norm_scale_backward(w, col, unit_offset) : 0.0;
+#pragma unroll
+            for (int k = 0; k < kNormRows / 4; ++k) {
+                const int r = wave * (kNormRows / 4) + k;
+                if (r < nrows) {
+                    const double xv = static_cast<double>(x[(r0 + r) * dim + col]);
+                    squares[r][lane] = xv * xv;
+                    if (kBackward) products[r][lane] = g * static_cast<double>(dy[(r0 + r) * dim + col]) * xv;
+                }
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            if (lane < kNormRows) {
+                for (int k = 0; k < n; ++k) chain += squares[lane][k];
+            } else if (kBackward) {
+                for (int k = 0; k < n; ++k) chain += products[lane - kNormRows][k];
+            }
+        }
+        __syncthreads();
     }
-    inv = bcast0(inv);
-    coef = bcast0(coef);
-    for (int64_t i = lane; i < dim; i += 64) {
-        const double g = norm_scale_backward(w, i, unit_offset);
-        float v = static_cast<float>(inv * g * static_cast<double>(dyr[i]) - static_cast<double>(xr[i]) * coef);
-        if (addend) v = addend[row * dim + i] + v;
-        dx[row * dim + i] = v;
+    if (wave == 0 && lane < kNormRows && lane < nrows) {
+        const double inv = 1.0 / sqrt(chain / static_cast<double>(dim) + eps);
+        row_inv[lane] = inv;
+        if (inv_out) inv_out[r0 + lane] = inv;
     }
-    if (inv_out && lane == 0) inv_out[row] = inv;
+    __syncthreads();
+    if (kBackward && wave == 0 && lane >= kNormRows && lane - kNormRows < nrows) {
+        const double inv = row_inv[lane - kNormRows];
+        row_coef[lane - kNormRows] = chain * inv * inv * inv / static_cast<double>(dim);
+    }
+    __syncthreads();
+    for (int r = wave; r < nrows; r += 4) {
+        const double inv = row_inv[r];
+        const int64_t base = (r0 + r) * dim;
+        if (kBackward) {
+            const double coef = row_coef[r];
+            for (int64_t i = lane; i < dim; i += 64) {
+                const double g = norm_scale_backward(w, i, unit_offset);
+                float v = static_cast<float>(inv * g * static_cast<double>(dy[base + i]) -
+                                             static_cast<double>(x[base + i]) * coef);
+                if (addend) v = addend[base + i] + v;
+                out[base + i] = v;
+            }
+        } else {
+            for (int64_t i = lane; i < dim; i += 64)
+                out[base + i] = static_cast<float>(static_cast<double>(x[base + i]) * inv * norm_scale(w, i, unit_offset));
+        }
+    }
 }
 
 // part[s][i] = f32(sum over rows of segment s ascending of term(r, i)): kind 0 term = dy (db, grad.hpp:52-54),
@@ -253,8 +261,8 @@ int launch_rms_norm(const float* x, const float* w, float* out, int64_t rows, in
                     double* inv_rms, hipStream_t stream) {
     if (rows == 0) return kOk;
     DLLM_REQUIRE(dim > 0, "rms_norm needs a non-empty last dimension");
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(ceil_div(rows, kRowWaves))), dim3(256), 0, stream,
-                       x, w, out, rows, dim, eps, unit_offset, inv_rms);
+    hipLaunchKernelGGL(norm_rows_kernel<false>, dim3(static_cast<unsigned>(ceil_div(rows, kNormRows))), dim3(256), 0,
+                       stream, x, w, nullptr, out, nullptr, rows, dim, eps, unit_offset, inv_rms);
     return check_launch("rms_norm");
 }
 
@@ -263,7 +271,7 @@ int launch_rms_norm_backward_dx(const float* x, const float* w, const float* dy,
                                 hipStream_t stream) {
     if (rows == 0) return kOk;
     DLLM_REQUIRE(dim > 0, "rms_norm_backward needs a non-empty last dimension");
-    hipLaunchKernelGGL(rms_norm_backward_kernel, dim3(static_cast<unsigned>(ceil_div(rows, kRowWaves))), dim3(256), 0,
+    hipLaunchKernelGGL(norm_rows_kernel<true>, dim3(static_cast<unsigned>(ceil_div(rows, kNormRows))), dim3(256), 0,
                        stream, x, w, dy, dx, addend, rows, dim, eps, unit_offset, inv_rms);
     return check_launch("rms_norm_backward");
 }

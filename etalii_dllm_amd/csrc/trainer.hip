@@ -174,6 +174,7 @@ struct dllm_hip_trainer {
     // attention as batched matmuls (attn_gemm.hip): per (window, head) transposed operands and score matrices
     int64_t Tp = 0;
     double* attn_scratch = nullptr;  // running sums of the attention matmuls' float outputs
+    double* attn_dvec = nullptr;     // the softmax backward's per-query D
     int64_t attn_scratch_doubles = 0;
     double *attn_kt = nullptr, *attn_vt = nullptr, *attn_et = nullptr, *attn_inv = nullptr, *attn_dpt = nullptr,
            *attn_pg = nullptr, *attn_dsg = nullptr;
@@ -402,6 +403,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&attn_pg, W_max * kvh * Tp * G * Tp));
         DLLM_TRY(make(&attn_dsg, W_max * kvh * Tp * G * Tp));
         attn_scratch_doubles = W_max * heads * T_max * hd;
+        DLLM_TRY(make(&attn_dvec, W_max * heads * Tp));
         DLLM_TRY(make(&attn_scratch, attn_scratch_doubles));
         DLLM_TRY(make(&tok_in, R));
         DLLM_TRY(make(&tok_tgt, R));
@@ -637,7 +639,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_attn_gemm(g, s));
         // p = e inv, D, ds = p (dp - D) scale (in place over E^T and dP^T)
         DLLM_TRY(launch_dsoftmax_rows(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp,
-                                      c.attention_scale, s));
+                                      c.attention_scale, attn_dvec, s));
         // dq[t] = sum_j ds[t][j] k[j]
         AttnGemmCall q = g;
         q.A = AttnOperand{attn_dpt, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
