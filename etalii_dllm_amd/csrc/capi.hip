@@ -53,6 +53,10 @@ int dllm_hip_download(void* dst, const void* src, size_t bytes) {
 int dllm_hip_memset(void* p, int value, size_t bytes) { return check_hip(hipMemset(p, value, bytes), "memset"); }
 int dllm_hip_synchronize(void) { return check_hip(hipDeviceSynchronize(), "synchronize"); }
 
+namespace {
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+}  // namespace
+
 size_t dllm_hip_linear_workspace(size_t rows, size_t in, size_t out) { return linear_ws(rows, in, out); }
 
 int dllm_hip_linear(const float* x, const float* w, const float* bias, float* out, size_t rows, size_t in, size_t out_f,
@@ -65,11 +69,17 @@ int dllm_hip_linear(const float* x, const float* w, const float* bias, float* ou
     float* wT = c.take<float>(K * N);
     DLLM_REQUIRE(!c.overflow, "workspace layout overflow");
     const hipStream_t s = as_stream(stream);
-    DLLM_TRY(launch_to_double(x, R, K, K, nullptr, 0, xT, padded_rows(R), s));
     DLLM_TRY(launch_transpose_f32(w, N, K, wT, s));
     GemmCall g;
-    g.A = xT;
-    g.lda = padded_rows(R);
+    if (K % 4 == 0 && N % 4 == 0 && aligned16(x)) {  // the matmul reads x itself
+        g.Af = x;
+        g.a_kind = 2;
+        g.lda = K;
+    } else {
+        DLLM_TRY(launch_to_double(x, R, K, K, nullptr, 0, xT, padded_rows(R), s));
+        g.A = xT;
+        g.lda = padded_rows(R);
+    }
     g.B = wT;
     g.ldb = N;
     g.C = out;
@@ -181,15 +191,25 @@ int dllm_hip_linear_backward(const float* x, const float* w, const float* dy, fl
     double* dyT_d = c.take<double>(N * padded_rows(R));
     DLLM_REQUIRE(!c.overflow, "workspace layout overflow");
     const hipStream_t s = as_stream(stream);
-    DLLM_TRY(launch_to_double(dy, R, N, N, dw ? dy_d : nullptr, padded_rows(N), dx ? dyT_d : nullptr, padded_rows(R),
-                              s));
+    // the matmuls read dy itself when its rows are whole 16-byte chunks; otherwise as doubles
+    const bool float_dx = N % 4 == 0 && K % 4 == 0 && aligned16(dy) && aligned16(w);
+    const bool float_dw = N % 4 == 0 && K % 4 == 0 && aligned16(dy) && aligned16(x);
+    if ((dw && !float_dw) || (dx && !float_dx))
+        DLLM_TRY(launch_to_double(dy, R, N, N, dw && !float_dw ? dy_d : nullptr, padded_rows(N),
+                                  dx && !float_dx ? dyT_d : nullptr, padded_rows(R), s));
     if (dx) {
         if (N == 0) {
             DLLM_TRY(check_hip(hipMemsetAsync(dx, 0, sizeof(float) * R * K, s), "memset"));
         } else {
             GemmCall g;  // dx[r][k] = sum_n dy[r][n] w[n][k]
-            g.A = dyT_d;
-            g.lda = padded_rows(R);
+            if (float_dx) {
+                g.Af = dy;
+                g.a_kind = 2;
+                g.lda = N;
+            } else {
+                g.A = dyT_d;
+                g.lda = padded_rows(R);
+            }
             g.B = w;
             g.ldb = K;
             g.C = dx;
@@ -206,8 +226,14 @@ int dllm_hip_linear_backward(const float* x, const float* w, const float* dy, fl
             DLLM_TRY(check_hip(hipMemsetAsync(dw, 0, sizeof(float) * N * K, s), "memset"));
         } else {
             GemmCall g;  // dw[n][k] = sum_r dy[r][n] x[r][k]
-            g.A = dy_d;
-            g.lda = padded_rows(N);
+            if (float_dw) {
+                g.Af = dy;
+                g.a_kind = 1;
+                g.lda = N;
+            } else {
+                g.A = dy_d;
+                g.lda = padded_rows(N);
+            }
             g.B = x;
             g.ldb = K;
             g.C = dw;

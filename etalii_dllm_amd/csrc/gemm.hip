@@ -18,6 +18,8 @@
 //     the next stage is in flight during the 16 x 64 DFMAs of the current one; A is read from LDS as a broadcast.
 //     Workgroups are renumbered so each XCD (own L2) gets a contiguous range of tiles, grouped 8 row blocks deep
 //     so the tiles resident together share their A and B stages (fewer HBM re-reads).
+//     A arrives either as doubles (A[l][i], rows padded to whole tiles) or straight from the float activations (rows
+//     Af[l][i], or transposed Af[i][l]), converted to double as it is read from LDS.
 //   gemm_kernel (any J and alignment): A through scalar loads as SGPR operands, B through per-lane loads.
 //
 // Segmented mode (dW over several training windows): the l range is split into segments (one per window); each
@@ -26,6 +28,8 @@
 // When the tile grid is too small to fill the GPU and a scratch buffer is given, the windows run as separate
 // workgroups into per-window float partials, and a second pass adds them in window order: the same roundings in
 // the same order.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -58,6 +62,7 @@ struct GemmParams {
     const int* seg_addrow;    // [nseg][I]: row of seg_addend for (window, i), or -1 (adds +0.0f)
     int64_t ld_seg_add;
     float* partial;  // segment-parallel mode: [nseg][I][J] per-window results (null: windows run in sequence)
+    const float* Af;  // float A operands: [L][lda] (A rows) or [I][lda] (A transposed: Af[i][l] = A[l][i])
 };
 
 // The raw B values of row l for this lane's 4 columns. Lanes past J read a clamped in-bounds column instead (their
@@ -164,12 +169,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 }
 
 constexpr int kChunk = 16;      // l per LDS stage
-constexpr int kStageLoads = 6;  // 16-byte direct-to-LDS loads per lane per stage: 2 for A, 4 for B
 
+// How A arrives: as doubles A[l][i] (rows padded to whole tiles), or straight from float activations, as rows
+// Af[l][i] or transposed Af[i][l] (a row per i), converted to double when read from LDS.
+enum AKind { kADouble = 0, kAFloatRows = 1, kAFloatT = 2 };
+
+template <int kA>
 struct Stage {
-    double a[kChunk][kBlockI];  // A[l][i] for the stage's l and the workgroup's 64 i
-    float b[kChunk][kTileJ];    // B[l][j] for the stage's l and the workgroup's 256 j
+    // A for the stage's l and the workgroup's 64 i: [l][i] (double or float), or [i][l] (float, transposed)
+    typename std::conditional<kA == kADouble, double, float>::type a[kA == kAFloatT ? kBlockI : kChunk]
+                                                                     [kA == kAFloatT ? kChunk : kBlockI];
+    float b[kChunk][kTileJ];  // B[l][j] for the stage's l and the workgroup's 256 j
 };
+
+// 16-byte direct-to-LDS loads per lane per stage: A (2 of doubles, 1 of floats) and B (4)
+template <int kA>
+constexpr int stage_loads() {
+    return (kA == kADouble ? 2 : 1) + 4;
+}
 
 // 16 bytes from global memory to LDS at lds_row + 16 * lane (gfx950 direct-to-LDS load; M0 holds the LDS address).
 // Written as inline assembly so the compiler's wait-count pass does not stall the LDS reads of the current stage on
@@ -192,20 +209,35 @@ __device__ __forceinline__ void wait_stage() {
 __device__ __forceinline__ void workgroup_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // Issues the copies of stage rows l .. l + kChunk - 1 (rows past `last` repeat row `last`; they are never read).
-// Wave w copies A rows 4w .. 4w + 3 (two rows of 64 doubles per instruction) and B rows 4w .. 4w + 3.
-__device__ __forceinline__ void issue_stage(const GemmParams& p, Stage& st, const double* a_src, const float* b_src,
-                                            int64_t l, int64_t last, int wave, int lane) {
+// Wave w copies A rows 4w .. 4w + 3 (doubles: two rows of 64 per instruction; float rows: four rows of 64; float
+// transposed: i rows 16w .. 16w + 15, 16 l each) and B rows 4w .. 4w + 3. `jl` is this lane's B column chunk.
+template <int kA>
+__device__ __forceinline__ void issue_stage(const GemmParams& p, Stage<kA>& st, int64_t i_blk, int64_t jl, int64_t l,
+                                            int64_t last, int wave, int lane) {
+    if constexpr (kA == kADouble) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int r = 4 * wave + 2 * t;
-        const int64_t lr = l + r + (lane >> 5) <= last ? l + r + (lane >> 5) : last;
-        copy16_to_lds(a_src + lr * p.lda, &st.a[r][0]);
+        for (int t = 0; t < 2; ++t) {
+            const int r = 4 * wave + 2 * t;
+            const int64_t lr = l + r + (lane >> 5) <= last ? l + r + (lane >> 5) : last;
+            copy16_to_lds(p.A + lr * p.lda + i_blk + (lane & 31) * 2, &st.a[r][0]);
+        }
+    } else if constexpr (kA == kAFloatRows) {
+        // chunks past I (a multiple of 4) read the last chunk; their columns are never stored
+        const int r = 4 * wave + (lane >> 4);
+        const int64_t lr = l + r <= last ? l + r : last;
+        const int64_t i = i_blk + (lane & 15) * 4 <= p.I - 4 ? i_blk + (lane & 15) * 4 : p.I - 4;
+        copy16_to_lds(p.Af + lr * p.lda + i, &st.a[4 * wave][0]);
+    } else {
+        // rows past I read row I - 1, chunks past the row's end (l1, a multiple of 4) its last chunk: never read
+        const int64_t i = i_blk + 16 * wave + (lane >> 2) < p.I ? i_blk + 16 * wave + (lane >> 2) : p.I - 1;
+        const int64_t lc = l + (lane & 3) * 4 <= p.l1 - 4 ? l + (lane & 3) * 4 : p.l1 - 4;
+        copy16_to_lds(p.Af + i * p.lda + lc, &st.a[16 * wave][0]);
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const int r = 4 * wave + t;
         const int64_t lr = l + r <= last ? l + r : last;
-        copy16_to_lds(b_src + lr * p.ldb, &st.b[r][0]);
+        copy16_to_lds(p.B + lr * p.ldb + jl, &st.b[r][0]);
     }
 }
 
@@ -238,8 +270,15 @@ struct RowOperands {
     float4 b;
 };
 
-__device__ __forceinline__ RowOperands read_row(const Stage& st, int k, int wave, int lane) {
-    return {st.a[k][wave * kTileI + (lane & 15)], *reinterpret_cast<const float4*>(&st.b[k][lane * 4])};
+template <int kA>
+__device__ __forceinline__ RowOperands read_row(const Stage<kA>& st, int k, int wave, int lane) {
+    const int i = wave * kTileI + (lane & 15);
+    double a;
+    if constexpr (kA == kAFloatT)
+        a = static_cast<double>(st.a[i][k]);
+    else
+        a = static_cast<double>(st.a[k][i]);
+    return {a, *reinterpret_cast<const float4*>(&st.b[k][lane * 4])};
 }
 
 // acc[q][c] += A[l][i0 + q] * B[l][j0 + c] for one stage row.
@@ -249,24 +288,25 @@ __device__ __forceinline__ void row_fma(const RowOperands& r, double (&acc)[kTil
 }
 
 // Rows 0 .. n-1 of a stage, l ascending; row k + 1 is read from LDS while row k's 64 FMAs run.
-template <int kN>
-__device__ __forceinline__ void stage_rows(const Stage& st, int n, int wave, int lane, double (&acc)[kTileI][4]) {
+template <int kN, int kA>
+__device__ __forceinline__ void stage_rows(const Stage<kA>& st, int n, int wave, int lane, double (&acc)[kTileI][4]) {
     if (kN > 0) {
-        RowOperands cur = read_row(st, 0, wave, lane);
+        RowOperands cur = read_row<kA>(st, 0, wave, lane);
 #pragma unroll
         for (int k = 0; k < kN; ++k) {
             RowOperands next = cur;
-            if (k + 1 < kN) next = read_row(st, k + 1, wave, lane);
+            if (k + 1 < kN) next = read_row<kA>(st, k + 1, wave, lane);
             row_fma(cur, acc);
             cur = next;
         }
     } else {
-        for (int k = 0; k < n; ++k) row_fma(read_row(st, k, wave, lane), acc);
+        for (int k = 0; k < n; ++k) row_fma(read_row<kA>(st, k, wave, lane), acc);
     }
 }
 
 // One segment's sums through the double-buffered LDS pipeline: acc[q][c] = sum over l in [l0, l1), ascending.
-__device__ __forceinline__ void accumulate_lds(const GemmParams& p, Stage (&st)[2], int64_t i_blk, int64_t j_blk,
+template <int kA>
+__device__ __forceinline__ void accumulate_lds(const GemmParams& p, Stage<kA> (&st)[2], int64_t i_blk, int64_t j_blk,
                                                int wave, int lane, int64_t l0, int64_t l1, double (&acc)[kTileI][4]) {
 #pragma unroll
     for (int q = 0; q < kTileI; ++q)
@@ -274,26 +314,24 @@ __device__ __forceinline__ void accumulate_lds(const GemmParams& p, Stage (&st)[
         for (int c = 0; c < 4; ++c) acc[q][c] = 0.0;
     if (l0 >= l1) return;
     const int64_t last = l1 - 1;
-    const double* a_src = p.A + i_blk + (lane & 31) * 2;
     const int64_t jl = j_blk + lane * 4 <= p.J - 4 ? j_blk + lane * 4 : p.J - 4;
-    const float* b_src = p.B + jl;
     const int64_t full = (l1 - l0) / kChunk;
     const int tail = static_cast<int>((l1 - l0) % kChunk);
     const int64_t chunks = full + (tail ? 1 : 0);
-    issue_stage(p, st[0], a_src, b_src, l0, last, wave, lane);
+    issue_stage<kA>(p, st[0], i_blk, jl, l0, last, wave, lane);
     for (int64_t c = 0; c < full; ++c) {
         if (c + 1 < chunks) {
-            issue_stage(p, st[(c + 1) & 1], a_src, b_src, l0 + (c + 1) * kChunk, last, wave, lane);
-            wait_stage<kStageLoads>();
+            issue_stage<kA>(p, st[(c + 1) & 1], i_blk, jl, l0 + (c + 1) * kChunk, last, wave, lane);
+            wait_stage<stage_loads<kA>()>();
         } else {
             wait_stage<0>();
         }
-        stage_rows<kChunk>(st[c & 1], kChunk, wave, lane, acc);
+        stage_rows<kChunk, kA>(st[c & 1], kChunk, wave, lane, acc);
         workgroup_barrier();  // the stage is read by every wave before the next issue overwrites it
     }
     if (tail) {  // its copies were issued with the last full stage (or first, when there is none)
         wait_stage<0>();
-        stage_rows<0>(st[full & 1], tail, wave, lane, acc);
+        stage_rows<0, kA>(st[full & 1], tail, wave, lane, acc);
         workgroup_barrier();
     }
 }
@@ -308,12 +346,12 @@ __device__ __forceinline__ int64_t xcd_contiguous(int64_t hw, int64_t n) {
 
 enum LdsMode { kPlain = 0, kWindowsInSequence = 1, kWindowsInParallel = 2 };
 
-template <int kMode>
+template <int kMode, int kA>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_lds_kernel(GemmParams p,
                                                                                                    int64_t gx,
                                                                                                    int64_t gy,
                                                                                                    int64_t gz) {
-    __shared__ Stage st[2];
+    __shared__ Stage<kA> st[2];
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int64_t id = xcd_contiguous(blockIdx.x, gx * gy * gz);
@@ -329,7 +367,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int64_t j0 = j_blk + lane * 4;
     double acc[kTileI][4];
     if (kMode == kPlain) {
-        accumulate_lds(p, st, i_blk, j_blk, wave, lane, p.l0, p.l1, acc);
+        accumulate_lds<kA>(p, st, i_blk, j_blk, wave, lane, p.l0, p.l1, acc);
         if (i0 >= p.I) return;
 #pragma unroll
         for (int q = 0; q < kTileI; ++q) {
@@ -351,7 +389,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const int s_begin = kMode == kWindowsInParallel ? static_cast<int>(bz) : 0;
     const int s_end = kMode == kWindowsInParallel ? s_begin + 1 : p.nseg;
     for (int s = s_begin; s < s_end; ++s) {
-        accumulate_lds(p, st, i_blk, j_blk, wave, lane, p.seg[s], p.seg[s + 1], acc);
+        accumulate_lds<kA>(p, st, i_blk, j_blk, wave, lane, p.seg[s], p.seg[s + 1], acc);
         if (i0 >= p.I) continue;
         float* out_base = kMode == kWindowsInParallel ? p.partial + static_cast<int64_t>(s) * p.I * p.J : p.C;
         int64_t ld_out = kMode == kWindowsInParallel ? p.J : p.ldc;
@@ -440,12 +478,23 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     DLLM_REQUIRE(g.I >= 0 && g.J >= 0, "negative matmul size");
     DLLM_REQUIRE(g.seg == nullptr || g.nseg >= 1, "segmented matmul needs at least one segment");
     DLLM_REQUIRE(g.seg != nullptr || g.seg_addrow == nullptr, "per-window addends need segments");
-    DLLM_REQUIRE(g.lda >= padded_rows(g.I), "the double operand must be padded to whole row tiles");
+    const int ak = g.a_kind;
+    DLLM_REQUIRE(ak == kADouble || ak == kAFloatRows || ak == kAFloatT, "unknown A operand kind");
+    if (ak == kADouble) DLLM_REQUIRE(g.lda >= padded_rows(g.I), "the double operand must be padded to whole row tiles");
     if (g.I == 0 || g.J == 0) return kOk;
     GemmParams p{g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.I, g.J, g.l0, g.l1, g.seg, g.nseg, g.bias, g.addsrc,
-                 g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr};
+                 g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af};
     const bool vec = (g.J % 4 == 0) && (g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.B) % 16 == 0);
-    if (vec && (g.lda % 2 == 0) && (reinterpret_cast<uintptr_t>(g.A) % 16 == 0)) {
+    if (ak != kADouble) {
+        // float A: 16-byte chunks of whole rows (and, transposed, a plain reduction over l in [0, l1))
+        DLLM_REQUIRE(vec, "float A operands need B rows of whole 16-byte chunks");
+        DLLM_REQUIRE(g.lda % 4 == 0 && reinterpret_cast<uintptr_t>(g.Af) % 16 == 0, "float A rows must be 16-byte aligned");
+        if (ak == kAFloatRows) DLLM_REQUIRE(g.I % 4 == 0 && g.lda >= g.I, "float A rows must hold whole chunks of I");
+        if (ak == kAFloatT)
+            DLLM_REQUIRE(g.seg == nullptr && g.l0 == 0 && g.l1 % 4 == 0 && g.l1 >= 4 && g.lda >= g.l1,
+                         "transposed float A needs a plain reduction over whole 16-byte chunks");
+    }
+    if (vec && (ak != kADouble || ((g.lda % 2 == 0) && (reinterpret_cast<uintptr_t>(g.A) % 16 == 0)))) {
         const int64_t gx = ceil_div(g.J, kTileJ), gy = ceil_div(g.I, kBlockI);
         int64_t gz = 1;
         // windows in parallel when the tile grid alone leaves most of the 256 CUs x 3 workgroups idle
@@ -456,12 +505,20 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
         }
         DLLM_REQUIRE(gx * gy * gz < (int64_t{1} << 31), "matmul grid too large for one launch");
         const dim3 grid(static_cast<unsigned>(gx * gy * gz));
-        if (p.partial)
-            hipLaunchKernelGGL(gemm_lds_kernel<kWindowsInParallel>, grid, dim3(256), 0, stream, p, gx, gy, gz);
-        else if (g.seg)
-            hipLaunchKernelGGL(gemm_lds_kernel<kWindowsInSequence>, grid, dim3(256), 0, stream, p, gx, gy, gz);
-        else
-            hipLaunchKernelGGL(gemm_lds_kernel<kPlain>, grid, dim3(256), 0, stream, p, gx, gy, gz);
+#define DLLM_GEMM_LAUNCH(MODE, AK) \
+    hipLaunchKernelGGL((gemm_lds_kernel<MODE, AK>), grid, dim3(256), 0, stream, p, gx, gy, gz)
+        if (ak == kAFloatT) {
+            DLLM_GEMM_LAUNCH(kPlain, kAFloatT);
+        } else if (ak == kAFloatRows) {
+            if (p.partial) DLLM_GEMM_LAUNCH(kWindowsInParallel, kAFloatRows);
+            else if (g.seg) DLLM_GEMM_LAUNCH(kWindowsInSequence, kAFloatRows);
+            else DLLM_GEMM_LAUNCH(kPlain, kAFloatRows);
+        } else {
+            if (p.partial) DLLM_GEMM_LAUNCH(kWindowsInParallel, kADouble);
+            else if (g.seg) DLLM_GEMM_LAUNCH(kWindowsInSequence, kADouble);
+            else DLLM_GEMM_LAUNCH(kPlain, kADouble);
+        }
+#undef DLLM_GEMM_LAUNCH
         DLLM_TRY(check_launch("gemm"));
         if (p.partial) {
             const int64_t n = g.I * g.J;
@@ -472,6 +529,7 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
         }
         return kOk;
     }
+    DLLM_REQUIRE(ak == kADouble, "float A operands need the LDS matmul");
     dim3 grid(static_cast<unsigned>(ceil_div(g.J, kTileJ)), static_cast<unsigned>(ceil_div(g.I, kBlockI)));
     DLLM_REQUIRE(grid.y <= 65535u, "matmul has too many rows for one launch");
     if (vec)

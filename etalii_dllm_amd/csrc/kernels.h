@@ -13,8 +13,10 @@ namespace dllm_hip {
 int64_t padded_rows(int64_t n);
 
 struct GemmCall {
-    const double* A = nullptr;  // [L][lda] doubles, i contiguous
-    int64_t lda = 0;
+    const double* A = nullptr;  // [L][lda] doubles, i contiguous (a_kind 0)
+    int64_t lda = 0;            // row stride of A, or of Af
+    const float* Af = nullptr;  // a_kind 1: Af[l][i] = A[l][i]; a_kind 2: Af[i][l] = A[l][i] (plain mode, l1 % 4 == 0)
+    int a_kind = 0;
     const float* B = nullptr;  // [L][ldb] floats, j contiguous
     int64_t ldb = 0;
     float* C = nullptr;  // [I][ldc]

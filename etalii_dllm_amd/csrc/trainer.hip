@@ -152,7 +152,6 @@ struct dllm_hip_trainer {
     std::vector<Saved> saved;
     std::vector<std::unique_ptr<DevBuf>> owned;
     float *x_final = nullptr, *hidden = nullptr, *logits = nullptr, *dlogits = nullptr;
-    double *dl_d = nullptr, *big_T = nullptr, *dy_d = nullptr;
     float *dx = nullptr, *dh = nullptr, *dx_mid = nullptr, *dattended = nullptr, *dq_t = nullptr, *dk_t = nullptr,
           *dv_t = nullptr, *dq = nullptr, *dk = nullptr, *dq2 = nullptr, *dk2 = nullptr, *dproduct = nullptr,
           *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *emb_rows = nullptr, *gemm_part = nullptr;
@@ -357,12 +356,6 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&hidden, R * H));
         DLLM_TRY(make(&logits, R * V));
         DLLM_TRY(make(&dlogits, R * V));
-        const int64_t Rp = padded_rows(R);
-        const int64_t maxN = std::max<int64_t>({V, H, QD, I});
-        DLLM_TRY(make(&dl_d, R * padded_rows(V)));
-        DLLM_TRY(make(&big_T, std::max<int64_t>(V, std::max<int64_t>({H, QD, I})) * Rp));
-        DLLM_TRY(make(&dy_d, R * padded_rows(std::max<int64_t>({H, QD, I}))));
-        (void)maxN;
         DLLM_TRY(make(&dx, R * H));
         DLLM_TRY(make(&dh, R * H));
         DLLM_TRY(make(&dx_mid, R * H));
@@ -476,14 +469,14 @@ struct dllm_hip_trainer {
         return kOk;
     }
 
-    // out[R][N] (+)= x[R][K] @ W^T (+ bias), x converted to x^T as doubles into big_T.
+    // out[R][N] (+)= x[R][K] @ W^T (+ bias); the matmul reads x itself (A transposed: A[k][r] = x[r][k]).
     int linear_fwd(const float* x, int64_t R, int64_t K, int w_id, const float* bias, float* out, const float* addsrc,
                    hipStream_t s) {
         const int64_t N = tensors[static_cast<size_t>(w_id)].rows;
-        DLLM_TRY(launch_to_double(x, R, K, K, nullptr, 0, big_T, padded_rows(R), s));
         GemmCall g;
-        g.A = big_T;
-        g.lda = padded_rows(R);
+        g.Af = x;
+        g.a_kind = 2;
+        g.lda = K;
         g.B = WT(w_id);
         g.ldb = N;
         g.C = out;
@@ -498,17 +491,13 @@ struct dllm_hip_trainer {
         return gemm(g, s);
     }
 
-    // Converts dy[R][N] to dy_d [R][N_pad] and dy^T [N][R_pad] (doubles) for the dW and dX matmuls.
-    int prepare_dy(const float* dyv, int64_t R, int64_t N, double* as_rows, double* as_cols, hipStream_t s) {
-        return launch_to_double(dyv, R, N, N, as_rows, padded_rows(N), as_cols, padded_rows(R), s);
-    }
-
-    // dx[R][K] (= addsrc +) sum_n dy[r][n] W[n][k], from dy^T in `cols`.
-    int linear_dx(const double* cols, int64_t R, int w_id, float* out, const float* addsrc, hipStream_t s) {
+    // dx[R][K] (= addsrc +) sum_n dy[r][n] W[n][k]; the matmul reads dy[R][N] itself (A transposed).
+    int linear_dx(const float* dyv, int64_t R, int w_id, float* out, const float* addsrc, hipStream_t s) {
         const TensorInfo& t = tensors[static_cast<size_t>(w_id)];
         GemmCall g;
-        g.A = cols;
-        g.lda = padded_rows(R);
+        g.Af = dyv;
+        g.a_kind = 2;
+        g.lda = t.rows;
         g.B = P(w_id);
         g.ldb = t.cols;
         g.C = out;
@@ -523,11 +512,12 @@ struct dllm_hip_trainer {
     }
 
     // grad[w] = window-ordered float sum of per-window dW = sum over window rows of dy[r][n] x[r][k].
-    int linear_dw(const double* rows_d, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
+    int linear_dw(const float* dyv, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
                   const float* addend, hipStream_t s) {
         GemmCall g;
-        g.A = rows_d;
-        g.lda = padded_rows(N);
+        g.Af = dyv;  // A rows: A[r][n] = dy[r][n]
+        g.a_kind = 1;
+        g.lda = N;
         g.B = x;
         g.ldb = K;
         g.C = out;
@@ -719,23 +709,19 @@ struct dllm_hip_trainer {
         const Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
         // SwiGLU (backprop.py:289-306)
-        DLLM_TRY(prepare_dy(dx, R, H, dy_d, big_T, s));
-        DLLM_TRY(linear_dx(big_T, R, L.down, dproduct, nullptr, s));
-        DLLM_TRY(linear_dw(dy_d, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, s));
+        DLLM_TRY(linear_dx(dx, R, L.down, dproduct, nullptr, s));
+        DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, s));
         DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s));
-        DLLM_TRY(prepare_dy(dgate, R, I, dy_d, big_T, s));
-        DLLM_TRY(linear_dx(big_T, R, L.gate, dh, nullptr, s));
-        DLLM_TRY(linear_dw(dy_d, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, s));
-        DLLM_TRY(prepare_dy(dup, R, I, dy_d, big_T, s));
-        DLLM_TRY(linear_dx(big_T, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
-        DLLM_TRY(linear_dw(dy_d, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, s));
+        DLLM_TRY(linear_dx(dgate, R, L.gate, dh, nullptr, s));
+        DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, s));
+        DLLM_TRY(linear_dx(dup, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
+        DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, s));
         // mlp norm; dx_mid = dx + dh2'
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_rms, s));
         DLLM_TRY(norm_dw(dh, sv.x_mid, inv_rms, H, 1, nseg, G(L.mlp_norm), s));
         // attention output projection
-        DLLM_TRY(prepare_dy(dx_mid, R, H, dy_d, big_T, s));
-        DLLM_TRY(linear_dx(big_T, R, L.o, dattended, nullptr, s));
-        DLLM_TRY(linear_dw(dy_d, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, s));
+        DLLM_TRY(linear_dx(dx_mid, R, L.o, dattended, nullptr, s));
+        DLLM_TRY(linear_dw(dx_mid, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, s));
         DLLM_TRY(attention_backward(l, sv, b, s));
         DLLM_TRY(launch_rope(dq_t, pos_index, cos_t, sin_t, dq, R, c.heads, c.head_dim, c.rotary_dim, 0, 1, s));
         DLLM_TRY(launch_rope(dk_t, pos_index, cos_t, sin_t, dk, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 1, s));
@@ -764,9 +750,8 @@ struct dllm_hip_trainer {
         const int bs_[3] = {L.qb, L.kb, L.vb};
         const int64_t ns[3] = {QD, KVD, KVD};
         for (int p = 0; p < 3; ++p) {
-            DLLM_TRY(prepare_dy(ds[p], R, ns[p], dy_d, big_T, s));
-            DLLM_TRY(linear_dx(big_T, R, ws_[p], dh, p == 0 ? nullptr : dh, s));
-            DLLM_TRY(linear_dw(dy_d, ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s));
+            DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
+            DLLM_TRY(linear_dw(ds[p], ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s));
             if (bs_[p] >= 0)
                 DLLM_TRY(launch_column_sums(0, ds[p], nullptr, nullptr, ns[p], seg_host.data(), nseg, col_part,
                                             G(bs_[p]), s));
@@ -866,18 +851,17 @@ struct dllm_hip_trainer {
         DLLM_TRY(check_hip(hipMemsetAsync(err_flag, 0, sizeof(int), s), "memset"));
         DLLM_TRY(launch_cross_entropy(logits, tok_tgt, dlogits, R, V, scale, seg_d, nseg, row_max, row_total, row_loss,
                                       loss_w, err_flag, s));
-        DLLM_TRY(prepare_dy(dlogits, R, V, dl_d, big_T, s));
         float* dhidden = dh;
-        DLLM_TRY(linear_dx(big_T, R, head, dhidden, nullptr, s));
+        DLLM_TRY(linear_dx(dlogits, R, head, dhidden, nullptr, s));
         DLLM_TRY(launch_rms_norm_backward_dx(x_final, P(final_norm), dhidden, dx, nullptr, R, H, eps, 0, inv_rms, s));
         DLLM_TRY(norm_dw(dhidden, x_final, inv_rms, H, 1, nseg, G(final_norm), s));
         for (int64_t l = c.layers - 1; l >= 0; --l) DLLM_TRY(backward_layer(l, R, nseg, b, s));
         // embedding (backprop.py:112-117): per-window token rows, then the head's dW with them as the tied addend
         DLLM_TRY(launch_embedding_groups(dx, H, grp_order, grp_start, grp_out, groups, emb_rows, H, s));
         if (c.tie_embeddings) {
-            DLLM_TRY(linear_dw(dl_d, V, hidden, H, nseg, G(emb), addrow, emb_rows, s));
+            DLLM_TRY(linear_dw(dlogits, V, hidden, H, nseg, G(emb), addrow, emb_rows, s));
         } else {
-            DLLM_TRY(linear_dw(dl_d, V, hidden, H, nseg, G(lm_head), nullptr, nullptr, s));
+            DLLM_TRY(linear_dw(dlogits, V, hidden, H, nseg, G(lm_head), nullptr, nullptr, s));
             hipLaunchKernelGGL(sparse_window_sum_kernel, dim3(static_cast<unsigned>(V)), dim3(256), 0, s, emb_rows,
                                addrow, V, H, nseg, G(emb));
             DLLM_TRY(check_launch("embedding window sum"));
@@ -950,6 +934,8 @@ int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_t
     DLLM_REQUIRE(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, "heads must be a multiple of kv_heads");
     DLLM_REQUIRE(c.rotary_dim > 0 && c.rotary_dim % 2 == 0 && c.rotary_dim <= c.head_dim, "invalid rotary_dim");
     DLLM_REQUIRE(c.head_dim % 4 == 0, "head_dim must be a multiple of 4");
+    DLLM_REQUIRE(c.vocab % 4 == 0 && c.hidden % 4 == 0 && c.intermediate % 4 == 0,
+                 "vocabulary, hidden and intermediate sizes must be multiples of 4 (16-byte matmul operand chunks)");
     DLLM_REQUIRE(max_tokens > 0 && max_windows > 0 && max_window_tokens > 0, "capacities must be positive");
     DLLM_REQUIRE(max_window_tokens <= 2048, "windows longer than 2048 tokens are not supported");
     DLLM_REQUIRE(max_tokens <= 65535, "at most 65535 tokens per step");
