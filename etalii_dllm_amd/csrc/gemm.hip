@@ -243,17 +243,28 @@ __device__ __forceinline__ void issue_stage(const GemmParams& p, Stage<kA>& st, 
 
 // acc[Q][c] = fma(A[l][i0 + Q], b[c], acc[Q][c]) for c < 4. Lane L's `a` holds A[l][i0 + L % 16]; the DPP64
 // modifier row_newbcast:Q on the FMA itself hands lane Q of each 16-lane row to the whole row, so the wave's 16 A
-// values cost one 8-byte register per lane instead of 16 broadcast reads. s_nop 1 gives the two wait states a DPP
-// source needs after a vector write (the compiler's hazard checks do not look inside the statement).
+// values cost one 8-byte register per lane instead of 16 broadcast reads.
+// A DPP instruction must come two wait states after any vector write of a register it reads, and the compiler's
+// hazard checks do not look inside these statements: the first block of a row starts with s_nop 1 (after the
+// conversions that produce b), and the blocks are volatile so they stay in order, each reading registers the
+// block before it did not write (tests/test_dpp_hazards.py checks the built code).
 template <int Q>
 __device__ __forceinline__ void fma4_bcast(double (&acc)[kTileI][4], double a, const double (&b)[4]) {
-    asm("s_nop 1\n\t"
-        "v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
-        : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
-        : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
+    if constexpr (Q == 0)
+        asm volatile("s_nop 1\n\t"
+                     "v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
+                     : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
+    else
+        asm volatile("v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
+                     : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
 }
 
 template <int Q>

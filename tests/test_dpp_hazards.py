@@ -1,0 +1,78 @@
+"""Static check of the hand-written DPP instructions in the matmul kernels (no GPU needed).
+
+The FMAs and moves with the DPP64 modifier row_newbcast sit in inline assembly, so the compiler's hazard recognizer
+does not see them. The CDNA rule they must obey: a DPP instruction comes at least two wait states after any vector
+ALU write of a VGPR it reads (the previous instruction and `s_nop n` count 1 and n + 1 states). This test compiles
+the two kernel sources to gfx950 assembly with the library's own flags and walks back from every DPP instruction.
+"""
+
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from etalii_dllm_amd import build as B
+
+SOURCES = ["gemm.hip", "attn_gemm.hip"]
+
+
+def _regs(token: str) -> set[int]:
+    m = re.match(r"v\[(\d+):(\d+)\]", token)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", token)
+    return {int(m.group(1))} if m else set()
+
+
+def _instructions(asm: str) -> list[str]:
+    out = []
+    for line in asm.splitlines():
+        line = line.split(";")[0].strip()
+        if not line or line.startswith(".") or line.endswith(":"):
+            continue
+        out.append(line)
+    return out
+
+
+def dpp_hazards(asm: str) -> tuple[int, list[str]]:
+    lines = _instructions(asm)
+    checked, bad = 0, []
+    for idx, line in enumerate(lines):
+        if "_dpp" not in line.split()[0]:
+            continue
+        checked += 1
+        operands = [o.strip().split()[0] for o in line.split(None, 1)[1].split(",")]
+        read = set().union(*(_regs(o) for o in operands))  # the destination too: v_fmac reads it
+        states, j = 0, idx - 1
+        while j >= 0 and states < 2:
+            parts = lines[j].split(None, 1)
+            if parts[0] == "s_nop":
+                states += int(parts[1]) + 1
+            else:
+                if parts[0].startswith("v_") and len(parts) > 1 and _regs(parts[1].split(",")[0].strip()) & read:
+                    bad.append(f"{lines[j]}  ->  {line}")
+                states += 1
+            j -= 1
+    return checked, bad
+
+
+@pytest.mark.skipif(not Path(B.HIPCC).exists() and shutil.which("hipcc") is None, reason="hipcc not available")
+@pytest.mark.parametrize("source", SOURCES)
+def test_dpp_instructions_respect_their_wait_states(tmp_path, source):
+    asm = tmp_path / (source + ".s")
+    cmd = [B.HIPCC, *B.FLAGS, "--cuda-device-only", "-S", str(B.CSRC / source), "-o", str(asm)]
+    result = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert result.returncode == 0, result.stderr[-2000:]
+    checked, bad = dpp_hazards(asm.read_text())
+    assert checked > 0
+    assert not bad, f"{len(bad)} DPP hazards, e.g. {bad[:3]}"
+
+
+def test_the_checker_finds_a_hazard():
+    asm = "v_cvt_f64_f32_e32 v[4:5], v1\nv_fmac_f64_dpp v[8:9], v[2:3], v[4:5] row_newbcast:1\n"
+    assert dpp_hazards(asm)[1]
+    assert not dpp_hazards("v_cvt_f64_f32_e32 v[4:5], v1\ns_nop 1\nv_fmac_f64_dpp v[8:9], v[2:3], v[4:5] row_newbcast:1\n")[1]
