@@ -578,3 +578,169 @@ def train_step(kern: Kernels, d: Decoder, params, m, v, windows, opt: AdamWConfi
 
 def with_family(d: Decoder, **changes) -> Decoder:
     return replace(d, **changes)
+
+
+# ---- LoRA (src/etalii_dllm/lora.py) ----
+
+LORA_TARGETS = ("q", "k", "v", "o", "gate", "up", "down")  # lora.py:56-65 (ALL_TARGETS)
+LORA_WEIGHT_NAMES = {"q": "attention.q.weight", "k": "attention.k.weight", "v": "attention.v.weight",
+                     "o": "attention.o.weight", "gate": "mlp.gate.weight", "up": "mlp.up.weight",
+                     "down": "mlp.down.weight"}  # lora.py:66-74
+
+
+@dataclass(frozen=True)
+class Lora:
+    """LoraConfig (lora.py:159-177): scale = alpha / rank (alpha / sqrt(rank) with rsLoRA)."""
+
+    rank: int
+    alpha: float
+    targets: tuple[str, ...] = LORA_TARGETS
+    rslora: bool = False
+
+    @property
+    def scale(self) -> float:
+        return self.alpha / (math.sqrt(self.rank) if self.rslora else self.rank)
+
+
+def lora_target_weights(d: Decoder, lora: Lora) -> list[str]:
+    """target_weights (lora.py:211-242) for pre-norm decoders: every expert's gate/up/down in a sparse layer."""
+    names = []
+    for layer in range(d.layers):
+        for target in lora.targets:
+            if target in ("gate", "up", "down") and d.experts:
+                names.extend(f"layers.{layer}.mlp.experts.{e}.{target}.weight" for e in range(d.experts))
+            else:
+                names.append(f"layers.{layer}.{LORA_WEIGHT_NAMES[target]}")
+    return tensor_order(names)
+
+
+def adapter_shapes(d: Decoder, lora: Lora) -> dict[str, tuple[int, int]]:
+    """lora.py:245-255: <weight>.lora_a [rank, in] and <weight>.lora_b [out, rank], weights in tensor order."""
+    shapes = d.tensor_shapes()
+    result = {}
+    for name in lora_target_weights(d, lora):
+        out_features, in_features = shapes[name]
+        result[name + ".lora_a"] = (lora.rank, in_features)
+        result[name + ".lora_b"] = (out_features, lora.rank)
+    return result
+
+
+def init_adapters(d: Decoder, lora: Lora, seed: int) -> dict[str, np.ndarray]:
+    """lora.py:258-268: A = fill_gaussian(seed * 1000003 + index) * f32(1 / rank), B = 0."""
+    adapters = {}
+    for index, (name, shape) in enumerate(adapter_shapes(d, lora).items()):
+        if name.endswith(".lora_a"):
+            values = fill_gaussian(seed * 1_000_003 + index, shape[0] * shape[1]).reshape(shape)
+            adapters[name] = np.ascontiguousarray(values * np.float32(1.0 / lora.rank), dtype=np.float32)
+        else:
+            adapters[name] = np.zeros(shape, dtype=np.float32)
+    return adapters
+
+
+def lora_merge(kern: Kernels, weight, a, b, scale: float) -> np.ndarray:
+    """lora.py:271-276: weight + f32(linear(b, a^T)) * f32(scale), in float32."""
+    delta = kern.linear(np.ascontiguousarray(b, np.float32), np.ascontiguousarray(a.T, np.float32))
+    return np.asarray(weight, np.float32) + delta * np.float32(scale)
+
+
+def adapter_gradients(kern: Kernels, gradient, a, b, scale: float):
+    """lora.py:374-383: dA = linear(B^T, dW^T) * s, dB = linear(dW, A) * s (float32 products with s)."""
+    s = np.float32(scale)
+    gradient = np.ascontiguousarray(gradient, np.float32)
+    da = kern.linear(np.ascontiguousarray(b.T, np.float32), np.ascontiguousarray(gradient.T)) * s
+    db = kern.linear(gradient, np.ascontiguousarray(a, np.float32)) * s
+    return da, db
+
+
+def merged_weights(kern: Kernels, d: Decoder, base, adapters, lora: Lora) -> dict[str, np.ndarray]:
+    """lora.py:279-287."""
+    merged = dict(base)
+    for name in lora_target_weights(d, lora):
+        merged[name] = lora_merge(kern, base[name], adapters[name + ".lora_a"], adapters[name + ".lora_b"], lora.scale)
+    return merged
+
+
+def _power(base: float, exponent: int) -> float:
+    """optimizer.py:59-63: repeated multiplication."""
+    result = 1.0
+    for _ in range(exponent):
+        result *= base
+    return result
+
+
+def lora_train_step(kern: Kernels, d: Decoder, base, adapters, m, v, windows, opt: AdamWConfig, step: int,
+                    total_steps: int, lora: Lora, router_aux_loss: float = 0.0):
+    """FineTuner.train_step for a LoRA run (trainer.py:290-335, 463-474; optimizer.py:66-109): gradients of the
+    merged weights summed over the windows in float32 (the first copied), the adapters' gradients, then AdamW over
+    the adapters in tensor order. Updates adapters, m and v in place; returns (loss, gradient norm)."""
+    merged = merged_weights(kern, d, base, adapters, lora)
+    targets_total = sum(len(w) - 1 for w in windows)
+    scale = 1.0 / targets_total
+    loss_total, router_total, grads = 0.0, 0.0, {}
+    for w in windows:
+        loss, router_loss, g = window_gradients(kern, d, merged, w[:-1], w[1:], scale=scale,
+                                                router_scale=router_aux_loss / len(windows))
+        loss_total += loss
+        router_total += router_loss
+        for name, value in g.items():
+            if name in grads:
+                grads[name] += value
+            else:
+                grads[name] = value.copy()
+    result = {}
+    for name in adapters:
+        if name.endswith(".lora_b"):
+            weight = name[: -len(".lora_b")]
+            a_name = weight + ".lora_a"
+            result[a_name], result[name] = adapter_gradients(kern, grads[weight], adapters[a_name], adapters[name],
+                                                             lora.scale)
+    total = 0.0
+    for name in tensor_order(result):
+        total += kern.sum_squares(result[name])
+    norm = math.sqrt(total)
+    clip = 1.0
+    if opt.max_grad_norm > 0 and norm > opt.max_grad_norm:
+        clip = opt.max_grad_norm / (norm + 1e-6)
+    c1, c2 = 1.0 - _power(opt.beta1, step), 1.0 - _power(opt.beta2, step)
+    lr = opt.learning_rate_at(step, total_steps)
+    for name in tensor_order(adapters):
+        decay = opt.weight_decay if adapters[name].ndim >= 2 else 0.0
+        kern.adamw_step(adapters[name], np.ascontiguousarray(result[name], np.float32), m[name], v[name], lr,
+                        opt.beta1, opt.beta2, opt.eps, decay, c1, c2, clip)
+    loss = loss_total / targets_total
+    if router_aux_loss:
+        loss += router_aux_loss * router_total / len(windows)
+    return loss, norm
+
+
+# ---- Q8_0 (cpp/include/dllm/quant.hpp:27-60, numerics.py:106-139) ----
+
+def quantize_q8_0(fn, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """(values int8 [n], scales f32 [n / 32]) from a quantize_q8_0(x, q, scales, n) C function."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    assert x.size % 32 == 0
+    q = np.empty(x.size, np.int8)
+    s = np.empty(x.size // 32, np.float32)
+    fn.argtypes = [_f32p, C.POINTER(C.c_int8), _f32p, C.c_size_t]
+    fn(ptr(x), q.ctypes.data_as(C.POINTER(C.c_int8)), ptr(s), x.size)
+    return q, s
+
+
+def dequantize_q8_0(q: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """QuantizedWeight.dequantize (numerics.py:138-139): int8 -> float32 times the block's scale, in float32."""
+    return q.astype(np.float32) * np.repeat(scales, 32)
+
+
+def q8_0_cases() -> dict[str, np.ndarray]:
+    """Blocks exercising the rounding: exact half-way products of both parities, zeros, a block of zeros, non-finite
+    values (ignored for the scale, stored as 0), a value at -amax, tiny and huge magnitudes."""
+    g = gaussian(31, 32 * 64)
+    cases = {"gaussian": g, "scaled": g * np.float32(1e-30), "huge": g * np.float32(1e30)}
+    ties = np.tile((np.arange(32, dtype=np.float32) - 16) * np.float32(0.5), 4)
+    ties[0], ties[32], ties[64], ties[96] = np.float32(63.5), np.float32(-63.5), np.float32(127.0), np.float32(-8.0)
+    cases["ties"] = ties  # amax 63.5 or 127: x * (127 / amax) lands on halves
+    special = gaussian(32, 32 * 4)
+    special[3], special[40], special[77] = np.inf, -np.inf, np.nan
+    special[96:128] = 0.0
+    cases["special"] = special
+    return cases

@@ -69,3 +69,26 @@ def test_finetune_fingerprint(family):
         losses.append(loss)
     assert O.data_fingerprint(params) == GOLDEN["FINETUNE_FINGERPRINT"][family]
     assert losses[-1] < losses[0]
+
+
+LORA_FAMILIES = sorted(set(O.FIXTURES) & set(GOLDEN["LORA_FINETUNE_FINGERPRINT"]))
+
+
+@pytest.mark.parametrize("family", LORA_FAMILIES)
+def test_lora_finetune_fingerprint(family):
+    """RUN = 6 steps, batch 3, sequence 8, seed 3, lr 3e-2 cosine, LoRA rank 2 alpha 4 on every target; the merged
+    export's fingerprint (reference tests/test_lora.py:26-27,151-171)."""
+    d = O.FIXTURES[family]
+    lora = O.Lora(rank=2, alpha=4.0)
+    kern = O.oracle_kernels()
+    base = O.fixture_weights(d)
+    adapters = O.init_adapters(d, lora, 3)
+    m = {n: np.zeros_like(a) for n, a in adapters.items()}
+    v = {n: np.zeros_like(a) for n, a in adapters.items()}
+    windows = ascii_windows()
+    opt = O.AdamWConfig(learning_rate=3e-2)
+    for step in range(6):
+        batch = [windows[i] for i in O.batch_indices(len(windows), step, 3, 3)]
+        O.lora_train_step(kern, d, base, adapters, m, v, batch, opt, step + 1, 6, lora)
+    merged = O.merged_weights(kern, d, base, adapters, lora)
+    assert O.data_fingerprint(merged) == GOLDEN["LORA_FINETUNE_FINGERPRINT"][family]

@@ -266,3 +266,23 @@ def test_sum_squares_is_the_serial_double_chain():
     for value in g.astype(np.float64):
         acc += value * value
     assert O.oracle_kernels().sum_squares(g) == acc
+
+
+@pytest.mark.parametrize("name", sorted(O.q8_0_cases()))
+def test_quantize_q8_0_matches_reference(name):
+    x = O.q8_0_cases()[name]
+    qa, sa = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, x)
+    qb, sb = O.quantize_q8_0(O.ref().ref_quantize_q8_0, x)
+    assert qa.tobytes() == qb.tobytes() and sa.tobytes() == sb.tobytes()
+
+
+def test_q8_0_round_trips_values_on_its_grid():
+    """Values k * d for |k| <= 127 with one |k| = 127 quantise to k exactly and dequantise to k * d (closed form)."""
+    rng = np.random.default_rng(5)
+    k = rng.integers(-127, 128, size=(8, 32)).astype(np.float32)
+    k[:, 0] = 127.0
+    d = np.float32(0.25)
+    x = (k * d).ravel()
+    q, s = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, x)
+    assert np.all(s == d) and np.array_equal(q.astype(np.float32), k.ravel())
+    assert O.dequantize_q8_0(q, s).tobytes() == x.tobytes()
