@@ -450,4 +450,38 @@ int dllm_hip_adamw_step(float* param, const float* grad, float* m, float* v, siz
     return launch_adamw_plain(param, grad, m, v, static_cast<int64_t>(n), weight_decay, a, as_stream(stream));
 }
 
+int dllm_hip_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n, void* stream) {
+    DLLM_REQUIRE(n % 32 == 0, "q8_0 needs a weight whose in_features is a multiple of 32");
+    return launch_quantize_q8_0(x, q, scales, static_cast<int64_t>(n), as_stream(stream));
+}
+
+int dllm_hip_dequantize_q8_0(const int8_t* q, const float* scales, float* out, size_t n, void* stream) {
+    DLLM_REQUIRE(n % 32 == 0, "q8_0 needs a weight whose in_features is a multiple of 32");
+    return launch_dequantize_q8_0(q, scales, out, static_cast<int64_t>(n), as_stream(stream));
+}
+
+size_t dllm_hip_lora_merge_workspace(size_t out_f, size_t in_f, size_t rank) {
+    return lora_merge_workspace(static_cast<int64_t>(out_f), static_cast<int64_t>(in_f), static_cast<int64_t>(rank));
+}
+
+int dllm_hip_lora_merge(const float* weight, const float* a, const float* b, float* out, size_t out_f, size_t in_f,
+                        size_t rank, double scale, void* workspace, size_t workspace_bytes, void* stream) {
+    return launch_lora_merge(weight, a, b, out, static_cast<int64_t>(out_f), static_cast<int64_t>(in_f),
+                             static_cast<int64_t>(rank), static_cast<float>(scale), workspace, workspace_bytes,
+                             as_stream(stream));
+}
+
+size_t dllm_hip_lora_adapter_gradients_workspace(size_t out_f, size_t in_f, size_t rank) {
+    return lora_adapter_gradients_workspace(static_cast<int64_t>(out_f), static_cast<int64_t>(in_f),
+                                            static_cast<int64_t>(rank));
+}
+
+int dllm_hip_lora_adapter_gradients(const float* grad, const float* a, const float* b, float* da, float* db,
+                                    size_t out_f, size_t in_f, size_t rank, double scale, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+    return launch_lora_adapter_gradients(grad, a, b, da, db, static_cast<int64_t>(out_f), static_cast<int64_t>(in_f),
+                                         static_cast<int64_t>(rank), static_cast<float>(scale), workspace,
+                                         workspace_bytes, as_stream(stream));
+}
+
 }  // extern "C"

@@ -160,4 +160,20 @@ int launch_adamw(float* param, const float* grad, float* m, float* v, const int6
                  const int64_t* chunk_end, const double* chunk_decay, int64_t chunks, const AdamWArgs& a,
                  const double* grad_scale_dev, hipStream_t stream);
 
+// ---- LoRA and the Q8_0 base (lora.hip) ----
+
+int launch_quantize_q8_0(const float* x, int8_t* q, float* scales, int64_t n, hipStream_t stream);
+int launch_dequantize_q8_0(const int8_t* q, const float* scales, float* out, int64_t n, hipStream_t stream);
+// out = base + x * s in float32 (base may be null: out = x * s)
+int launch_scale_add(const float* base, const float* x, float s, float* out, int64_t n, hipStream_t stream);
+// out = weight + f32(linear(b, a^T)) * scale; a [rank][in], b [out][rank] (lora.py:271-276)
+size_t lora_merge_workspace(int64_t out_f, int64_t in_f, int64_t rank);
+int launch_lora_merge(const float* weight, const float* a, const float* b, float* out, int64_t out_f, int64_t in_f,
+                      int64_t rank, float scale, void* ws, size_t ws_bytes, hipStream_t stream);
+// da = f32(linear(b^T, grad^T)) * scale, db = f32(linear(grad, a)) * scale (lora.py:374-383)
+size_t lora_adapter_gradients_workspace(int64_t out_f, int64_t in_f, int64_t rank);
+int launch_lora_adapter_gradients(const float* grad, const float* a, const float* b, float* da, float* db,
+                                  int64_t out_f, int64_t in_f, int64_t rank, float scale, void* ws, size_t ws_bytes,
+                                  hipStream_t stream);
+
 }  // namespace dllm_hip

@@ -13,6 +13,7 @@
 //  - the tied embedding's gradient (dembedding + dhead per window, then summed over windows) is the head dW with the
 //    window's embedding rows as an addend.
 // Weights, gradients and AdamW moments live in one arena each, tensors in natural name order.
+#include <math.h>
 #include <string.h>
 
 #include <algorithm>
@@ -157,19 +158,46 @@ struct dllm_hip_trainer {
           *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *emb_rows = nullptr, *gemm_part = nullptr;
     int64_t gemm_part_cap = 0;  // floats: per-window partials of the layer weight gradients
     double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
-           *per_tensor = nullptr, *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+           *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
     void* attn_ws = nullptr;
     int64_t *tok_in = nullptr, *tok_tgt = nullptr, *pos_index = nullptr, *seg_d = nullptr, *batch_d = nullptr,
-            *grp_order = nullptr, *grp_start = nullptr, *grp_out = nullptr, *ten_off = nullptr, *ten_cnt = nullptr,
-            *chunk_start = nullptr, *chunk_end = nullptr;
-    double* chunk_decay = nullptr;
+            *grp_order = nullptr, *grp_start = nullptr, *grp_out = nullptr;
     int* addrow = nullptr;
     int* err_flag = nullptr;
-    int64_t chunks = 0;
     std::vector<int64_t> seg_host;
     bool wt_valid = false;
-    ExactSumPlan norm_plan;
-    void* norm_ws = nullptr;
+
+    // What AdamW updates: parameters, gradients and moments of one set of tensors in one arena each, the chunk table
+    // of the fused update and the plan of the exact global norm (optimizer.py:66-109).
+    struct OptimizerSet {
+        float *p = nullptr, *g = nullptr, *m = nullptr, *v = nullptr;
+        int64_t tensors = 0, chunks = 0;
+        int64_t *chunk_start = nullptr, *chunk_end = nullptr;
+        double *chunk_decay = nullptr, *chunk_decay_scaled = nullptr, *per_tensor = nullptr;
+        double last_decay = -1.0;
+        ExactSumPlan norm_plan;
+        void* norm_ws = nullptr;
+    };
+    OptimizerSet main_opt, lora_opt;
+
+    // LoRA runs (lora.py): adapters in natural name order in their own arenas, the merged weights the step uses for
+    // the targets, and (Q8_0 base) the quantisable matrices held as their dequantised values.
+    bool lora_on = false;
+    dllm_hip_lora_config lc{};
+    float lora_scale = 0.0f;
+    std::vector<TensorInfo> adapters;
+    std::map<std::string, int> adapter_index;
+    struct LoraTarget {
+        int weight, a, b;  // tensor id, adapter ids
+    };
+    std::vector<LoraTarget> lora_targets;
+    DevBuf lora_p, lora_g, lora_m, lora_v, merged;
+    std::vector<int64_t> merged_offset;  // per tensor id: offset in `merged`, or -1
+    bool base_ready = true;              // the Q8_0 base has been applied to the current parameters
+    void* lora_ws = nullptr;
+    size_t lora_ws_bytes = 0;
+    int8_t* q8_values = nullptr;
+    float* q8_scales = nullptr;
     // attention as batched matmuls (attn_gemm.hip): per (window, head) transposed operands and score matrices
     int64_t Tp = 0;
     double* attn_scratch = nullptr;  // running sums of the attention matmuls' float outputs
@@ -273,54 +301,62 @@ struct dllm_hip_trainer {
             L.down = id(p + "mlp.down.weight");
             layer_ids.push_back(L);
         }
-        // AdamW chunk table: 64K-element chunks inside each tensor, decay for matrices (optimizer.py:93).
+        merged_offset.assign(tensors.size(), -1);
+        DLLM_TRY(make(&stats, 3));
+        return build_optimizer(tensors, params.as<float>(), grads.as<float>(), m1.as<float>(), m2.as<float>(),
+                               &main_opt);
+    }
+
+    // AdamW chunk table (64K-element chunks inside each tensor, decay for matrices: optimizer.py:93) and the exact
+    // parallel global-norm plan (sumsq.hip) over one arena's tensors.
+    int build_optimizer(const std::vector<TensorInfo>& ts, float* p, float* g, float* m, float* v, OptimizerSet* o) {
+        o->p = p;
+        o->g = g;
+        o->m = m;
+        o->v = v;
         std::vector<int64_t> cs, ce, to, tc;
         std::vector<double> cd;
-        for (const TensorInfo& t : tensors) {
+        for (const TensorInfo& t : ts) {
             to.push_back(t.offset);
             tc.push_back(t.numel);
-            for (int64_t s = 0; s < t.numel; s += 65536) {
-                cs.push_back(t.offset + s);
-                ce.push_back(t.offset + std::min<int64_t>(t.numel, s + 65536));
+            for (int64_t st = 0; st < t.numel; st += 65536) {
+                cs.push_back(t.offset + st);
+                ce.push_back(t.offset + std::min<int64_t>(t.numel, st + 65536));
                 cd.push_back(t.ndim >= 2 ? 1.0 : 0.0);
             }
         }
-        chunks = static_cast<int64_t>(cs.size());
-        DLLM_TRY(make(&chunk_start, cs.size()));
-        DLLM_TRY(make(&chunk_end, ce.size()));
-        DLLM_TRY(make(&chunk_decay, cd.size()));
-        DLLM_TRY(make(&ten_off, to.size()));
-        DLLM_TRY(make(&ten_cnt, tc.size()));
-        DLLM_TRY(check_hip(hipMemcpy(chunk_start, cs.data(), cs.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(chunk_end, ce.data(), ce.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(chunk_decay, cd.data(), cd.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(ten_off, to.data(), to.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(ten_cnt, tc.data(), tc.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(make(&per_tensor, tensors.size()));
-        DLLM_TRY(make(&stats, 3));
-        // exact parallel global norm plan (sumsq.hip)
+        o->tensors = static_cast<int64_t>(ts.size());
+        o->chunks = static_cast<int64_t>(cs.size());
+        DLLM_TRY(make(&o->chunk_start, std::max<size_t>(cs.size(), 1)));
+        DLLM_TRY(make(&o->chunk_end, std::max<size_t>(ce.size(), 1)));
+        DLLM_TRY(make(&o->chunk_decay, std::max<size_t>(cd.size(), 1)));
+        DLLM_TRY(make(&o->chunk_decay_scaled, std::max<size_t>(cd.size(), 1)));
+        DLLM_TRY(check_hip(hipMemcpy(o->chunk_start, cs.data(), cs.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(o->chunk_end, ce.data(), ce.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(check_hip(hipMemcpy(o->chunk_decay, cd.data(), cd.size() * 8, hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(make(&o->per_tensor, std::max<size_t>(ts.size(), 1)));
         const size_t nb = exact_sum_squares_blocks(tc.data(), static_cast<int64_t>(tc.size()));
         std::vector<int64_t> tf(tc.size()), tb(tc.size()), bs(nb), bc(nb);
         exact_sum_squares_plan(to.data(), tc.data(), static_cast<int64_t>(tc.size()), tf.data(), tb.data(), bs.data(),
                                bc.data());
         int64_t *d_tf, *d_tb, *d_bs, *d_bc;
-        DLLM_TRY(make(&d_tf, tf.size()));
-        DLLM_TRY(make(&d_tb, tb.size()));
-        DLLM_TRY(make(&d_bs, bs.size()));
-        DLLM_TRY(make(&d_bc, bc.size()));
+        DLLM_TRY(make(&d_tf, std::max<size_t>(tf.size(), 1)));
+        DLLM_TRY(make(&d_tb, std::max<size_t>(tb.size(), 1)));
+        DLLM_TRY(make(&d_bs, std::max<size_t>(bs.size(), 1)));
+        DLLM_TRY(make(&d_bc, std::max<size_t>(bc.size(), 1)));
         DLLM_TRY(check_hip(hipMemcpy(d_tf, tf.data(), tf.size() * 8, hipMemcpyHostToDevice), "upload"));
         DLLM_TRY(check_hip(hipMemcpy(d_tb, tb.data(), tb.size() * 8, hipMemcpyHostToDevice), "upload"));
         DLLM_TRY(check_hip(hipMemcpy(d_bs, bs.data(), bs.size() * 8, hipMemcpyHostToDevice), "upload"));
         DLLM_TRY(check_hip(hipMemcpy(d_bc, bc.data(), bc.size() * 8, hipMemcpyHostToDevice), "upload"));
-        norm_plan.tensors = static_cast<int64_t>(tc.size());
-        norm_plan.blocks = static_cast<int64_t>(nb);
-        norm_plan.tfirst = d_tf;
-        norm_plan.tblocks = d_tb;
-        norm_plan.bstart = d_bs;
-        norm_plan.bcount = d_bc;
+        o->norm_plan.tensors = static_cast<int64_t>(tc.size());
+        o->norm_plan.blocks = static_cast<int64_t>(nb);
+        o->norm_plan.tfirst = d_tf;
+        o->norm_plan.tblocks = d_tb;
+        o->norm_plan.bstart = d_bs;
+        o->norm_plan.bcount = d_bc;
         char* ws = nullptr;
         DLLM_TRY(make(&ws, exact_sum_squares_workspace(nb)));
-        norm_ws = ws;
+        o->norm_ws = ws;
         return kOk;
     }
 
@@ -415,7 +451,10 @@ struct dllm_hip_trainer {
         return check_hip(hipDeviceSynchronize(), "trainer setup");
     }
 
-    float* P(int id) const { return params.as<float>() + tensors[static_cast<size_t>(id)].offset; }
+    float* P(int id) const {
+        const int64_t mo = merged_offset.empty() ? -1 : merged_offset[static_cast<size_t>(id)];
+        return mo >= 0 ? merged.as<float>() + mo : params.as<float>() + tensors[static_cast<size_t>(id)].offset;
+    }
     float* G(int id) const { return grads.as<float>() + tensors[static_cast<size_t>(id)].offset; }
     float* WT(int id) const { return wt.as<float>() + tensors[static_cast<size_t>(id)].wt_offset; }
     const float* Popt(int id) const { return id >= 0 ? P(id) : nullptr; }
@@ -461,10 +500,11 @@ struct dllm_hip_trainer {
 
     // W^T of every linear weight for the forward matmuls.
     int refresh_transposes(hipStream_t s) {
-        for (const TensorInfo& t : tensors)
+        for (size_t i = 0; i < tensors.size(); ++i) {
+            const TensorInfo& t = tensors[i];
             if (t.wt_offset >= 0)
-                DLLM_TRY(launch_transpose_f32(params.as<float>() + t.offset, t.rows, t.cols,
-                                              wt.as<float>() + t.wt_offset, s));
+                DLLM_TRY(launch_transpose_f32(P(static_cast<int>(i)), t.rows, t.cols, wt.as<float>() + t.wt_offset, s));
+        }
         wt_valid = true;
         return kOk;
     }
@@ -834,7 +874,10 @@ struct dllm_hip_trainer {
         int64_t R = 0, groups = 0;
         AttentionBatch b{};
         DLLM_TRY(prepare(tokens, offsets, lengths, windows, &R, &b, &groups, s));
-        if (!wt_valid) DLLM_TRY(refresh_transposes(s));
+        if (lora_on)
+            DLLM_TRY(prepare_lora(s));
+        else if (!wt_valid)
+            DLLM_TRY(refresh_transposes(s));
         const int nseg = static_cast<int>(windows);
         nwin = windows;
         const double eps = c.rms_norm_eps;
@@ -886,9 +929,11 @@ struct dllm_hip_trainer {
         const double scale = 1.0 / static_cast<double>(targets_total);
         double loss_total = 0.0;
         DLLM_TRY(gradients(tokens, offsets, lengths, windows, scale, &loss_total, s));
+        if (lora_on) DLLM_TRY(adapter_gradients(s));  // trainer.py:463-474
+        OptimizerSet& o = lora_on ? lora_opt : main_opt;
         // global norm, clip (optimizer.py:66-90), bias corrections by repeated multiplication (optimizer.py:59-63)
-        DLLM_TRY(launch_exact_sum_squares(grads.as<float>(), norm_plan, norm_ws, per_tensor, s));
-        DLLM_TRY(launch_norm_finish(per_tensor, static_cast<int64_t>(tensors.size()), a->max_grad_norm, stats, s));
+        DLLM_TRY(launch_exact_sum_squares(o.g, o.norm_plan, o.norm_ws, o.per_tensor, s));
+        DLLM_TRY(launch_norm_finish(o.per_tensor, o.tensors, a->max_grad_norm, stats, s));
         double p1 = 1.0, p2 = 1.0;
         for (int64_t i = 0; i < a->step; ++i) {
             p1 *= a->beta1;
@@ -896,10 +941,13 @@ struct dllm_hip_trainer {
         }
         AdamWArgs args{a->learning_rate, a->beta1, a->beta2, a->eps, 1.0 - p1, 1.0 - p2, 1.0};
         // the chunk table holds 1 for matrices: decay = weight_decay * 1 or * 0 (optimizer.py:93)
-        DLLM_TRY(scale_decay(a->weight_decay, s));
-        DLLM_TRY(launch_adamw(params.as<float>(), grads.as<float>(), m1.as<float>(), m2.as<float>(), chunk_start,
-                              chunk_end, chunk_decay_scaled, chunks, args, stats + 2, s));
-        DLLM_TRY(refresh_transposes(s));
+        DLLM_TRY(scale_decay(o, a->weight_decay));
+        DLLM_TRY(launch_adamw(o.p, o.g, o.m, o.v, o.chunk_start, o.chunk_end, o.chunk_decay_scaled, o.chunks, args,
+                              stats + 2, s));
+        if (lora_on)
+            merged_valid = false;  // the next step merges the updated adapters
+        else
+            DLLM_TRY(refresh_transposes(s));
         double st[3];
         DLLM_TRY(check_hip(hipMemcpyAsync(st, stats, sizeof st, hipMemcpyDeviceToHost, s), "download"));
         DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
@@ -908,27 +956,155 @@ struct dllm_hip_trainer {
         return kOk;
     }
 
-    double* chunk_decay_scaled = nullptr;
-    double last_decay = -1.0;
+    int scale_decay(OptimizerSet& o, double wd) {
+        if (wd == o.last_decay) return kOk;
+        std::vector<double> d(static_cast<size_t>(o.chunks));
+        if (!d.empty()) {
+            DLLM_TRY(check_hip(hipMemcpy(d.data(), o.chunk_decay, d.size() * 8, hipMemcpyDeviceToHost), "download"));
+            for (double& x : d) x = x != 0.0 ? wd : 0.0;
+            DLLM_TRY(check_hip(hipMemcpy(o.chunk_decay_scaled, d.data(), d.size() * 8, hipMemcpyHostToDevice), "upload"));
+        }
+        o.last_decay = wd;
+        return kOk;
+    }
 
-    int scale_decay(double wd, hipStream_t s) {
-        if (chunk_decay_scaled && wd == last_decay) return kOk;
-        if (!chunk_decay_scaled) DLLM_TRY(make(&chunk_decay_scaled, static_cast<size_t>(chunks)));
-        std::vector<double> d(static_cast<size_t>(chunks));
-        DLLM_TRY(check_hip(hipMemcpy(d.data(), chunk_decay, d.size() * 8, hipMemcpyDeviceToHost), "download"));
-        for (double& x : d) x = x != 0.0 ? wd : 0.0;
-        DLLM_TRY(check_hip(hipMemcpy(chunk_decay_scaled, d.data(), d.size() * 8, hipMemcpyHostToDevice), "upload"));
-        last_decay = wd;
-        (void)s;
+    // ---- LoRA (lora.py) ----
+    bool merged_valid = false;
+
+    // The adapted weights (target_weights, lora.py:211-242): q k v o gate up down by the target mask.
+    int build_lora(const dllm_hip_lora_config& l) {
+        lora_on = true;
+        lc = l;
+        lora_scale = static_cast<float>(l.alpha / (l.rslora ? std::sqrt(static_cast<double>(l.rank))
+                                                           : static_cast<double>(l.rank)));
+        static const char* kTargets[7] = {"attention.q.weight", "attention.k.weight", "attention.v.weight",
+                                          "attention.o.weight", "mlp.gate.weight", "mlp.up.weight",
+                                          "mlp.down.weight"};
+        std::vector<int> weights;
+        for (int64_t layer = 0; layer < c.layers; ++layer)
+            for (int t = 0; t < 7; ++t)
+                if (l.targets & (int64_t{1} << t))
+                    weights.push_back(index["layers." + std::to_string(layer) + "." + kTargets[t]]);
+        for (int w : weights) {
+            const TensorInfo& t = tensors[static_cast<size_t>(w)];
+            TensorInfo a, b;
+            a.name = t.name + ".lora_a";
+            a.rows = l.rank;
+            a.cols = t.cols;
+            b.name = t.name + ".lora_b";
+            b.rows = t.rows;
+            b.cols = l.rank;
+            a.ndim = b.ndim = 2;
+            a.numel = a.rows * a.cols;
+            b.numel = b.rows * b.cols;
+            adapters.push_back(a);
+            adapters.push_back(b);
+        }
+        std::stable_sort(adapters.begin(), adapters.end(),
+                         [](const TensorInfo& x, const TensorInfo& y) { return natural_less(x.name, y.name); });
+        int64_t off = 0;
+        for (size_t i = 0; i < adapters.size(); ++i) {
+            off = static_cast<int64_t>(round_up(static_cast<size_t>(off), 64));
+            adapters[i].offset = off;
+            off += adapters[i].numel;
+            adapter_index[adapters[i].name] = static_cast<int>(i);
+        }
+        const size_t arena = static_cast<size_t>(round_up(static_cast<size_t>(off > 0 ? off : 1), 64)) * sizeof(float);
+        for (DevBuf* d : {&lora_p, &lora_g, &lora_m, &lora_v}) {
+            DLLM_TRY(d->alloc(arena));
+            DLLM_TRY(check_hip(hipMemset(d->p, 0, arena), "memset"));
+        }
+        int64_t moff = 0;
+        size_t ws = 0;
+        int64_t largest = 0;
+        for (int w : weights) {
+            const TensorInfo& t = tensors[static_cast<size_t>(w)];
+            moff = static_cast<int64_t>(round_up(static_cast<size_t>(moff), 64));
+            merged_offset[static_cast<size_t>(w)] = moff;
+            moff += t.numel;
+            lora_targets.push_back({w, adapter_index[t.name + ".lora_a"], adapter_index[t.name + ".lora_b"]});
+            ws = std::max(ws, lora_merge_workspace(t.rows, t.cols, l.rank));
+            ws = std::max(ws, lora_adapter_gradients_workspace(t.rows, t.cols, l.rank));
+        }
+        for (const TensorInfo& t : tensors)
+            if (quantizable(t)) largest = std::max(largest, t.numel);
+        DLLM_TRY(merged.alloc(static_cast<size_t>(moff > 0 ? moff : 1) * sizeof(float)));
+        char* w = nullptr;
+        DLLM_TRY(make(&w, std::max<size_t>(ws, 1)));
+        lora_ws = w;
+        lora_ws_bytes = std::max<size_t>(ws, 1);
+        if (l.base_quantize) {
+            DLLM_TRY(make(&q8_values, static_cast<size_t>(std::max<int64_t>(largest, 32))));
+            DLLM_TRY(make(&q8_scales, static_cast<size_t>(std::max<int64_t>(largest / 32, 1))));
+            base_ready = false;
+        }
+        return build_optimizer(adapters, lora_p.as<float>(), lora_g.as<float>(), lora_m.as<float>(),
+                               lora_v.as<float>(), &lora_opt);
+    }
+
+    // quantizable (lora.py:300-302): the q k v o gate up down matrices whose input size is a multiple of 32
+    static bool quantizable(const TensorInfo& t) {
+        static const char* kSuffix[7] = {".q.weight", ".k.weight", ".v.weight", ".o.weight", ".gate.weight",
+                                         ".up.weight", ".down.weight"};
+        if (t.ndim != 2 || t.cols % 32 != 0) return false;
+        for (const char* sfx : kSuffix) {
+            const size_t n = strlen(sfx);
+            if (t.name.size() > n && t.name.compare(t.name.size() - n, n, sfx) == 0) return true;
+        }
+        return false;
+    }
+
+    // Before a step: the Q8_0 base once per parameter write (QuantizedBase: reading a quantised matrix gives its
+    // dequantised values), then W' = merge(W, A, B) for every target (lora.py:271-287) and their W'^T.
+    int prepare_lora(hipStream_t s) {
+        if (!base_ready) {
+            for (const TensorInfo& t : tensors) {
+                if (!quantizable(t)) continue;
+                float* w = params.as<float>() + t.offset;
+                DLLM_TRY(launch_quantize_q8_0(w, q8_values, q8_scales, t.numel, s));
+                DLLM_TRY(launch_dequantize_q8_0(q8_values, q8_scales, w, t.numel, s));
+            }
+            base_ready = true;
+            wt_valid = false;
+            merged_valid = false;
+        }
+        if (merged_valid && wt_valid) return kOk;
+        for (const LoraTarget& lt : lora_targets) {
+            const TensorInfo& t = tensors[static_cast<size_t>(lt.weight)];
+            DLLM_TRY(launch_lora_merge(params.as<float>() + t.offset, lora_p.as<float>() + adapters[lt.a].offset,
+                                       lora_p.as<float>() + adapters[lt.b].offset,
+                                       merged.as<float>() + merged_offset[static_cast<size_t>(lt.weight)], t.rows,
+                                       t.cols, lc.rank, lora_scale, lora_ws, lora_ws_bytes, s));
+        }
+        merged_valid = true;
+        return refresh_transposes(s);
+    }
+
+    // dA, dB of every target from the merged weight's gradient (trainer.py:463-474, lora.py:374-383).
+    int adapter_gradients(hipStream_t s) {
+        for (const LoraTarget& lt : lora_targets) {
+            const TensorInfo& t = tensors[static_cast<size_t>(lt.weight)];
+            DLLM_TRY(launch_lora_adapter_gradients(G(lt.weight), lora_p.as<float>() + adapters[lt.a].offset,
+                                                   lora_p.as<float>() + adapters[lt.b].offset,
+                                                   lora_g.as<float>() + adapters[lt.a].offset,
+                                                   lora_g.as<float>() + adapters[lt.b].offset, t.rows, t.cols,
+                                                   lc.rank, lora_scale, lora_ws, lora_ws_bytes, s));
+        }
         return kOk;
     }
 };
 
 extern "C" {
 
-int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_tokens, int64_t max_windows,
-                            int64_t max_window_tokens, dllm_hip_trainer** out) {
+int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dllm_hip_lora_config* lora,
+                                 int64_t max_tokens, int64_t max_windows, int64_t max_window_tokens,
+                                 dllm_hip_trainer** out) {
     DLLM_REQUIRE(config && out, "null argument");
+    if (lora) {
+        DLLM_REQUIRE(lora->rank >= 1, "the LoRA rank must be positive");
+        DLLM_REQUIRE(lora->targets > 0 && lora->targets < 128, "LoRA targets must be a non-empty subset of q k v o gate up down");
+        DLLM_REQUIRE(lora->base_quantize == 0 || lora->base_quantize == 1, "base_quantize must be 0 (float) or 1 (q8_0)");
+    }
     const dllm_hip_decoder_config& c = *config;
     DLLM_REQUIRE(c.experts == 0, "mixture-of-experts layers are not supported by this trainer yet");
     DLLM_REQUIRE(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, "heads must be a multiple of kv_heads");
@@ -950,9 +1126,15 @@ int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_t
     t->I = c.intermediate;
     t->V = c.vocab;
     DLLM_TRY(t->build_tensors());
+    if (lora) DLLM_TRY(t->build_lora(*lora));
     DLLM_TRY(t->build_activations());
     *out = t.release();
     return kOk;
+}
+
+int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_tokens, int64_t max_windows,
+                            int64_t max_window_tokens, dllm_hip_trainer** out) {
+    return dllm_hip_trainer_create_lora(config, nullptr, max_tokens, max_windows, max_window_tokens, out);
 }
 
 int dllm_hip_trainer_destroy(dllm_hip_trainer* t) {
@@ -987,6 +1169,16 @@ int dllm_hip_trainer_profile_read(dllm_hip_trainer* t, int64_t* launches, double
 
 int dllm_hip_trainer_tensor(dllm_hip_trainer* t, const char* name, int which, float** ptr, int64_t* numel) {
     DLLM_REQUIRE(t && name && ptr, "null argument");
+    DLLM_REQUIRE(which >= 0 && which < 4, "which must be 0 (parameter), 1 (gradient), 2 (m) or 3 (v)");
+    auto ad = t->adapter_index.find(name);
+    if (ad != t->adapter_index.end()) {  // a LoRA adapter: the parameters AdamW updates
+        const TensorInfo& info = t->adapters[static_cast<size_t>(ad->second)];
+        const DevBuf* arenas[4] = {&t->lora_p, &t->lora_g, &t->lora_m, &t->lora_v};
+        *ptr = arenas[which]->as<float>() + info.offset;
+        if (numel) *numel = info.numel;
+        if (which == 0) t->merged_valid = false;
+        return kOk;
+    }
     auto it = t->index.find(name);
     DLLM_REQUIRE(it != t->index.end(), std::string("unknown tensor ") + name);
     const TensorInfo& info = t->tensors[static_cast<size_t>(it->second)];
@@ -994,19 +1186,24 @@ int dllm_hip_trainer_tensor(dllm_hip_trainer* t, const char* name, int which, fl
     DLLM_REQUIRE(which >= 0 && which < 4, "which must be 0 (parameter), 1 (gradient), 2 (m) or 3 (v)");
     *ptr = arenas[which]->as<float>() + info.offset;
     if (numel) *numel = info.numel;
-    if (which == 0) t->wt_valid = false;  // the caller may write parameters
+    if (which == 0) {  // the caller may write parameters
+        t->wt_valid = false;
+        t->merged_valid = false;
+        if (t->lora_on && t->lc.base_quantize) t->base_ready = false;
+    }
     return kOk;
 }
 
 int dllm_hip_trainer_tensor_count(dllm_hip_trainer* t, int64_t* count) {
     DLLM_REQUIRE(t && count, "null argument");
-    *count = static_cast<int64_t>(t->tensors.size());
+    *count = static_cast<int64_t>(t->tensors.size() + t->adapters.size());
     return kOk;
 }
 
 const char* dllm_hip_trainer_tensor_name(dllm_hip_trainer* t, int64_t i) {
-    if (!t || i < 0 || i >= static_cast<int64_t>(t->tensors.size())) return nullptr;
-    return t->tensors[static_cast<size_t>(i)].name.c_str();
+    const int64_t n = t ? static_cast<int64_t>(t->tensors.size()) : 0;
+    if (!t || i < 0 || i >= n + static_cast<int64_t>(t->adapters.size())) return nullptr;
+    return i < n ? t->tensors[static_cast<size_t>(i)].name.c_str() : t->adapters[static_cast<size_t>(i - n)].name.c_str();
 }
 
 int dllm_hip_trainer_gradients(dllm_hip_trainer* t, const int64_t* tokens, const int64_t* offsets,

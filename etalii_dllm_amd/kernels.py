@@ -68,6 +68,15 @@ def _load() -> C.CDLL:
     lib.dllm_hip_sum_squares_workspace.restype = _sz
     lib.dllm_hip_sum_squares_workspace.argtypes = [_sz]
     lib.dllm_hip_adamw_step.argtypes = [_vp, _vp, _vp, _vp, _sz] + [C.c_double] * 8 + [_vp]
+    lib.dllm_hip_quantize_q8_0.argtypes = [_vp, _vp, _vp, _sz, _vp]
+    lib.dllm_hip_dequantize_q8_0.argtypes = [_vp, _vp, _vp, _sz, _vp]
+    lib.dllm_hip_lora_merge_workspace.restype = _sz
+    lib.dllm_hip_lora_merge_workspace.argtypes = [_sz, _sz, _sz]
+    lib.dllm_hip_lora_merge.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_double, _vp, _sz, _vp]
+    lib.dllm_hip_lora_adapter_gradients_workspace.restype = _sz
+    lib.dllm_hip_lora_adapter_gradients_workspace.argtypes = [_sz, _sz, _sz]
+    lib.dllm_hip_lora_adapter_gradients.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_double, _vp, _sz,
+                                                    _vp]
     return lib
 
 
@@ -355,6 +364,58 @@ def adamw_step(param, grad, m, v, lr, beta1, beta2, eps, weight_decay, bias_corr
     param[...] = dp.download(param.shape)
     m[...] = dm.download(m.shape)
     v[...] = dv.download(v.shape)
+
+
+# ---- LoRA and Q8_0 (src/etalii_dllm/lora.py, numerics.py:106-139) ----
+
+def quantize_q8_0(weight) -> tuple[np.ndarray, np.ndarray]:
+    """kernels.cpp quantize_q8_0 as QuantizedWeight uses it: (int8 values [out, in], float scales [out, in / 32])."""
+    w = _f32(weight)
+    if w.ndim != 2 or w.shape[1] % 32:
+        raise ValueError("q8_0 needs a [out_features, in_features] weight with in_features a multiple of 32")
+    d, q, s = Device.of(w), Device(w.size), Device(w.size // 32 * 4)
+    check(lib.dllm_hip_quantize_q8_0(d.ptr, q.ptr, s.ptr, w.size, None))
+    return q.download(w.shape, np.int8), s.download((w.shape[0], w.shape[1] // 32))
+
+
+def dequantize_q8_0(values, scales) -> np.ndarray:
+    """QuantizedWeight.dequantize (numerics.py:138-139): the int8 values times their block's scale, float32."""
+    q = np.ascontiguousarray(values, dtype=np.int8)
+    s = _f32(scales)
+    if q.size % 32 or s.size * 32 != q.size:
+        raise ValueError("q8_0 values come in blocks of 32 with one scale each")
+    dq, ds, out = Device.of(q), Device.of(s), Device(q.size * 4)
+    check(lib.dllm_hip_dequantize_q8_0(dq.ptr, ds.ptr, out.ptr, q.size, None))
+    return out.download(q.shape)
+
+
+def lora_merge(weight, a, b, scale: float) -> np.ndarray:
+    """lora.py:271-276: weight + f32(linear(b, a^T)) * f32(scale), a [rank, in], b [out, rank]."""
+    w, a, b = _f32(weight), _f32(a), _f32(b)
+    out_f, in_f = w.shape
+    rank = a.shape[0]
+    if a.shape != (rank, in_f) or b.shape != (out_f, rank):
+        raise ValueError("adapters do not match the weight")
+    ws = Device(lib.dllm_hip_lora_merge_workspace(out_f, in_f, rank))
+    dw, da, db, out = Device.of(w), Device.of(a), Device.of(b), Device(w.nbytes)
+    check(lib.dllm_hip_lora_merge(dw.ptr, da.ptr, db.ptr, out.ptr, out_f, in_f, rank, float(scale), ws.ptr, ws.nbytes,
+                                  None))
+    return out.download(w.shape)
+
+
+def lora_adapter_gradients(gradient, a, b, scale: float) -> tuple[np.ndarray, np.ndarray]:
+    """lora.py:374-383: (dA, dB) = (f32(linear(b^T, dW^T)) * s, f32(linear(dW, a)) * s)."""
+    g, a, b = _f32(gradient), _f32(a), _f32(b)
+    out_f, in_f = g.shape
+    rank = a.shape[0]
+    if a.shape != (rank, in_f) or b.shape != (out_f, rank):
+        raise ValueError("adapters do not match the gradient")
+    ws = Device(lib.dllm_hip_lora_adapter_gradients_workspace(out_f, in_f, rank))
+    dg, da, db = Device.of(g), Device.of(a), Device.of(b)
+    ga, gb = Device(a.nbytes), Device(b.nbytes)
+    check(lib.dllm_hip_lora_adapter_gradients(dg.ptr, da.ptr, db.ptr, ga.ptr, gb.ptr, out_f, in_f, rank, float(scale),
+                                              ws.ptr, ws.nbytes, None))
+    return ga.download(a.shape), gb.download(b.shape)
 
 
 def attention_scale(head_dim: int) -> float:

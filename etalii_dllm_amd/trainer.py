@@ -37,6 +37,30 @@ class AdamWArgs(C.Structure):
 lib.dllm_hip_trainer_create.argtypes = [C.POINTER(DecoderConfig), C.c_int64, C.c_int64, C.c_int64,
                                         C.POINTER(C.c_void_p)]
 lib.dllm_hip_trainer_destroy.argtypes = [C.c_void_p]
+
+
+class LoraConfig(C.Structure):
+    """dllm_hip_lora_config: LoraConfig (lora.py:159-177) with the targets as a mask and the base quantisation."""
+
+    _fields_ = [("rank", C.c_int64), ("alpha", C.c_double), ("targets", C.c_int64), ("rslora", C.c_int64),
+                ("base_quantize", C.c_int64)]
+
+
+LORA_TARGET_BITS = {"q": 1, "k": 2, "v": 4, "o": 8, "gate": 16, "up": 32, "down": 64}
+
+
+def lora_config(rank: int, alpha: float, targets=tuple(LORA_TARGET_BITS), rslora: bool = False,
+                base_quantize: str | None = None) -> LoraConfig:
+    if base_quantize not in (None, "q8_0"):
+        raise ValueError(f"unsupported base quantisation {base_quantize!r}; supported: q8_0")
+    mask = 0
+    for t in targets:
+        mask |= LORA_TARGET_BITS[t]
+    return LoraConfig(rank, alpha, mask, int(rslora), 1 if base_quantize == "q8_0" else 0)
+
+
+lib.dllm_hip_trainer_create_lora.argtypes = [C.POINTER(DecoderConfig), C.POINTER(LoraConfig), C.c_int64, C.c_int64,
+                                             C.c_int64, C.POINTER(C.c_void_p)]
 lib.dllm_hip_trainer_tensor.argtypes = [C.c_void_p, C.c_char_p, C.c_int, C.POINTER(C.c_void_p),
                                         C.POINTER(C.c_int64)]
 lib.dllm_hip_trainer_tensor_count.argtypes = [C.c_void_p, C.POINTER(C.c_int64)]
@@ -83,12 +107,15 @@ class Trainer:
 
     PARAM, GRAD, M, V = 0, 1, 2, 3
 
-    def __init__(self, decoder: Decoder, max_tokens: int, max_windows: int, max_window_tokens: int) -> None:
+    def __init__(self, decoder: Decoder, max_tokens: int, max_windows: int, max_window_tokens: int,
+                 lora: LoraConfig | None = None) -> None:
+        """lora: train LoRA adapters (tensors "<weight>.lora_a" / ".lora_b") on the frozen base instead."""
         self.decoder = decoder
         self._cfg = decoder.native()
+        self._lora = lora
         handle = C.c_void_p()
-        check(lib.dllm_hip_trainer_create(C.byref(self._cfg), max_tokens, max_windows, max_window_tokens,
-                                          C.byref(handle)))
+        check(lib.dllm_hip_trainer_create_lora(C.byref(self._cfg), C.byref(lora) if lora is not None else None,
+                                               max_tokens, max_windows, max_window_tokens, C.byref(handle)))
         self.handle = handle
         count = C.c_int64()
         check(lib.dllm_hip_trainer_tensor_count(handle, C.byref(count)))

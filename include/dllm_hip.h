@@ -125,6 +125,26 @@ int dllm_hip_adamw_step(float* param, const float* grad, float* m, float* v, siz
                         double beta2, double eps, double weight_decay, double bias_correction1,
                         double bias_correction2, double grad_scale, void* stream);
 
+/* ---- LoRA on a frozen (optionally Q8_0) base ---- */
+
+/* quantize_q8_0 of n values (a multiple of 32): int8 values and one float scale per 32-value block. Replaces
+ * kernels.cpp's `quantize_q8_0` binding (quant.hpp:27-60) as QuantizedWeight uses it (numerics.py:122-124). */
+int dllm_hip_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n, void* stream);
+/* out = f32(q) * scale of the value's block. Replaces QuantizedWeight.dequantize (numerics.py:138-139). */
+int dllm_hip_dequantize_q8_0(const int8_t* q, const float* scales, float* out, size_t n, void* stream);
+/* out = weight + f32(linear(b, a^T)) * f32(scale) for weight [out_f, in_f], a [rank, in_f], b [out_f, rank].
+ * Replaces lora.merge (src/etalii_dllm/lora.py:271-276). */
+size_t dllm_hip_lora_merge_workspace(size_t out_features, size_t in_features, size_t rank);
+int dllm_hip_lora_merge(const float* weight, const float* a, const float* b, float* out, size_t out_features,
+                        size_t in_features, size_t rank, double scale, void* workspace, size_t workspace_bytes,
+                        void* stream);
+/* da = f32(linear(b^T, grad^T)) * f32(scale), db = f32(linear(grad, a)) * f32(scale) from the merged weight's
+ * gradient grad [out_f, in_f]. Replaces lora.adapter_gradients (src/etalii_dllm/lora.py:374-383). */
+size_t dllm_hip_lora_adapter_gradients_workspace(size_t out_features, size_t in_features, size_t rank);
+int dllm_hip_lora_adapter_gradients(const float* grad, const float* a, const float* b, float* da, float* db,
+                                    size_t out_features, size_t in_features, size_t rank, double scale,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- the device-resident fine-tuning step ----
  *
  * Replaces the Python step the reference runs through those kernels: FineTuner.train_step
@@ -149,9 +169,28 @@ typedef struct dllm_hip_trainer dllm_hip_trainer;
 
 /* Allocates every buffer for steps of up to max_tokens tokens (rows, summed over windows) in up to max_windows
  * windows, each at most max_window_tokens long. Weights start at zero; moments at zero. */
+/* LoRA runs (src/etalii_dllm/lora.py, training/trainer.py:463-474): AdamW updates the adapters only. Targets are a
+ * mask of q (1) k (2) v (4) o (8) gate (16) up (32) down (64); scale = alpha / rank (alpha / sqrt(rank) with
+ * rslora). base_quantize 1 holds the quantisable matrices (lora.py:300-302) as their Q8_0-dequantised values, applied
+ * at the step after the parameters are written (QuantizedBase: a quantised run is LoRA on the dequantised base). */
+typedef struct {
+    int64_t rank;
+    double alpha;
+    int64_t targets;
+    int64_t rslora;
+    int64_t base_quantize;
+} dllm_hip_lora_config;
+
 int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_tokens, int64_t max_windows,
                             int64_t max_window_tokens, dllm_hip_trainer** trainer);
 int dllm_hip_trainer_destroy(dllm_hip_trainer* trainer);
+/* A LoRA trainer (lora may be NULL: as dllm_hip_trainer_create). The adapters are tensors "<weight>.lora_a"
+ * ([rank, in]) and "<weight>.lora_b" ([out, rank]) beside the base tensors; set them (init_adapters) before the first
+ * step. The base tensors' gradients (which 1) are those of the merged weights. No counterpart in the reference's
+ * kernel module: it replaces FineTuner's LoRA branch (trainer.py:247-250, 304-305). */
+int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dllm_hip_lora_config* lora,
+                                 int64_t max_tokens, int64_t max_windows, int64_t max_window_tokens,
+                                 dllm_hip_trainer** trainer);
 
 /* The device buffer of one tensor, by the reference's tensor name (architecture.py:418-468), e.g.
  * "layers.3.attention.q.weight": which = 0 parameter, 1 gradient (of the last step), 2 first moment, 3 second moment.

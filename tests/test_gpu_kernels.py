@@ -191,3 +191,23 @@ def test_exact_parallel_sum_squares_matches_the_serial_chain(K, ora, name):
     values = sum_squares_cases()[name]
     got, want = K.sum_squares(values), ora.sum_squares(values)
     assert np.float64(got).tobytes() == np.float64(want).tobytes(), (name, got, want)
+
+
+@pytest.mark.parametrize("name", sorted(O.q8_0_cases()))
+def test_quantize_and_dequantize_q8_0(K, ora, name):
+    x = O.q8_0_cases()[name].reshape(-1, 64)
+    q, s = K.quantize_q8_0(x)
+    qo, so = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, x)
+    assert_same(q.ravel(), qo, "values")
+    assert_same(s.ravel(), so, "scales")
+    assert_same(K.dequantize_q8_0(q, s).ravel(), O.dequantize_q8_0(qo, so), "dequantized")
+
+
+@pytest.mark.parametrize(("out_f", "in_f", "rank"), [(48, 32, 2), (64, 96, 16), (130, 257, 3), (8, 12, 4)])
+def test_lora_merge_and_adapter_gradients(K, ora, out_f, in_f, rank):
+    w, a, b = O.gaussian(61, out_f, in_f), O.gaussian(62, rank, in_f, scale=0.5), O.gaussian(63, out_f, rank)
+    g = adversarial(64, out_f, in_f)
+    assert_same(K.lora_merge(w, a, b, 2.0), O.lora_merge(ora, w, a, b, 2.0), "merge")
+    for got, want, name in zip(K.lora_adapter_gradients(g, a, b, 2.0), O.adapter_gradients(ora, g, a, b, 2.0),
+                               ("dA", "dB")):
+        assert_same(got, want, name)

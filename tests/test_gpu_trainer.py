@@ -86,3 +86,75 @@ def test_step_matches_the_oracle_on_ragged_windows():
             assert t.get(name, shape).tobytes() == params[name].tobytes(), name
             assert t.get(name, shape, t.M).tobytes() == m[name].tobytes(), name
             assert t.get(name, shape, t.V).tobytes() == v[name].tobytes(), name
+
+
+def make_lora_trainer(d: O.Decoder, weights, lora: O.Lora, adapters, base_quantize=None, max_tokens=64,
+                      max_windows=8, max_window=32):
+    from etalii_dllm_amd.trainer import Trainer, lora_config
+
+    t = Trainer(gpu_decoder(d), max_tokens, max_windows, max_window,
+                lora=lora_config(lora.rank, lora.alpha, lora.targets, lora.rslora, base_quantize))
+    assert t.names == O.tensor_order(d.tensor_shapes()) + O.tensor_order(O.adapter_shapes(d, lora))
+    t.load(weights)
+    t.load(adapters)
+    return t
+
+
+@pytest.mark.parametrize("family", [f for f in DENSE if f in GOLDEN["LORA_FINETUNE_FINGERPRINT"]])
+def test_lora_finetune_fingerprint_on_gpu(family):
+    """The reference's LoRA run (tests/test_lora.py:26-27,151-171) on the GPU; the merged export through the GPU
+    merge."""
+    from etalii_dllm_amd import kernels as K
+
+    d = O.FIXTURES[family]
+    lora = O.Lora(rank=2, alpha=4.0)
+    base = O.fixture_weights(d)
+    shapes = O.adapter_shapes(d, lora)
+    t = make_lora_trainer(d, base, lora, O.init_adapters(d, lora, 3))
+    windows = ascii_windows()
+    opt = O.AdamWConfig(learning_rate=3e-2)
+    for step in range(6):
+        batch = [windows[i] for i in O.batch_indices(len(windows), step, 3, 3)]
+        t.step(batch, opt.learning_rate_at(step + 1, 6), step + 1)
+    adapters = {n: t.get(n, shapes[n]) for n in shapes}
+    merged = dict(base)
+    for name in O.lora_target_weights(d, lora):
+        merged[name] = K.lora_merge(base[name], adapters[name + ".lora_a"], adapters[name + ".lora_b"], lora.scale)
+    assert O.data_fingerprint(merged) == GOLDEN["LORA_FINETUNE_FINGERPRINT"][family]
+
+
+@pytest.mark.parametrize("base_quantize", [None, "q8_0"])
+def test_lora_step_matches_the_oracle_on_ragged_windows(base_quantize):
+    """LoRA (rank 16, attention and MLP targets) on a float or Q8_0 base; the Q8_0 run against the oracle's LoRA on
+    the dequantised base (test_quantized_finetuning.py:96-106: a quantised run is LoRA on the dequantised base)."""
+    d = O.Decoder("qwen2", vocab=300, hidden=64, inter=160, layers=2, heads=4, kv_heads=2, head_dim=16, eps=1e-6,
+                  rope_theta=1e6, tied=True, attn_bias=True)
+    weights = O.synthetic_weights(d, seed=5, scale=0.05)
+    lora = O.Lora(rank=16, alpha=32.0, targets=("q", "v", "o", "gate", "down"))
+    adapters = O.init_adapters(d, lora, 7)
+    for name in adapters:  # non-zero B so the merge and both adapter gradients are exercised
+        if name.endswith(".lora_b"):
+            adapters[name] = O.gaussian(len(name), *adapters[name].shape, scale=0.02)
+    base = dict(weights)
+    if base_quantize:
+        for name, shape in d.tensor_shapes().items():
+            if name.endswith((".q.weight", ".k.weight", ".v.weight", ".o.weight", ".gate.weight", ".up.weight",
+                              ".down.weight")) and len(shape) == 2 and shape[1] % 32 == 0:
+                q, s = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, weights[name])
+                base[name] = O.dequantize_q8_0(q, s).reshape(shape)
+    rng = O.Random(9)
+    windows = [[rng.next_u64() % d.vocab for _ in range(n)] for n in (33, 2, 70, 17)]
+    t = make_lora_trainer(d, weights, lora, adapters, base_quantize, max_tokens=256, max_windows=4, max_window=128)
+    kern = O.oracle_kernels()
+    params = {n: a.copy() for n, a in adapters.items()}
+    m = {n: np.zeros_like(a) for n, a in params.items()}
+    v = {n: np.zeros_like(a) for n, a in params.items()}
+    opt = O.AdamWConfig(learning_rate=1e-3, schedule="constant")
+    for step in (1, 2):
+        loss_gpu, norm_gpu = t.step(windows, 1e-3, step)
+        loss_cpu, norm_cpu = O.lora_train_step(kern, d, base, params, m, v, windows, opt, step, 2, lora)
+        assert loss_gpu == loss_cpu and norm_gpu == norm_cpu
+        for name, a in params.items():
+            assert t.get(name, a.shape).tobytes() == a.tobytes(), name
+            assert t.get(name, a.shape, t.M).tobytes() == m[name].tobytes(), name
+            assert t.get(name, a.shape, t.V).tobytes() == v[name].tobytes(), name
