@@ -450,6 +450,20 @@ int dllm_hip_adamw_step(float* param, const float* grad, float* m, float* v, siz
     return launch_adamw_plain(param, grad, m, v, static_cast<int64_t>(n), weight_decay, a, as_stream(stream));
 }
 
+int dllm_hip_moe_route(const float* logits, int64_t* indices, float* weights, size_t rows, size_t experts, size_t k,
+                       int normalize, void* stream) {
+    return launch_moe_route(logits, static_cast<int64_t>(rows), static_cast<int64_t>(experts),
+                            static_cast<int64_t>(k), normalize, indices, weights, nullptr, as_stream(stream));
+}
+
+int dllm_hip_moe_route_backward(const float* logits, const int64_t* indices, const float* dweights,
+                                const float* dprobabilities, float* dlogits, size_t rows, size_t experts, size_t k,
+                                int normalize, void* stream) {
+    return launch_moe_route_backward(logits, indices, dweights, dprobabilities, static_cast<int64_t>(rows),
+                                     static_cast<int64_t>(experts), static_cast<int64_t>(k), normalize, dlogits,
+                                     as_stream(stream));
+}
+
 int dllm_hip_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n, void* stream) {
     DLLM_REQUIRE(n % 32 == 0, "q8_0 needs a weight whose in_features is a multiple of 32");
     return launch_quantize_q8_0(x, q, scales, static_cast<int64_t>(n), as_stream(stream));

@@ -78,6 +78,29 @@ int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_
 int launch_gather_rows(const float* table, const int64_t* index, float* out, int64_t rows, int64_t dim,
                        hipStream_t stream);
 
+// ---- mixture of experts (moe.hip) ----
+
+// moe_route (nn.hpp:864-896): indices/weights [rows][k] in rank order; probs [rows][experts] (optional) the softmax.
+int launch_moe_route(const float* logits, int64_t rows, int64_t experts, int64_t k, int normalize, int64_t* indices,
+                     float* weights, float* probs, hipStream_t stream);
+// moe_route_backward (grad.hpp:507-541); dprob [rows][experts] may be null.
+int launch_moe_route_backward(const float* logits, const int64_t* indices, const float* dweights, const float* dprob,
+                              int64_t rows, int64_t experts, int64_t k, int normalize, float* dlogits,
+                              hipStream_t stream);
+// out[r] = (0 + the row's k terms in expert order) + addend[r]; term = y[order] * weights[slot] or y[order].
+int launch_moe_combine(const float* y, const int64_t* order, const int64_t* slot, const float* weights,
+                       const float* addend, float* out, int64_t rows, int64_t k, int64_t dim, hipStream_t stream);
+// dweights[slot[p]] = dot(dout[row_of[p]], y[p]) and dy[p] = dout[row_of[p]] * weights[slot[p]] per position p.
+int launch_moe_dweights(const float* dout, const float* y, const int64_t* row_of, const int64_t* slot,
+                        const float* weights, int64_t positions, int64_t dim, float* dweights, float* dy,
+                        hipStream_t stream);
+// The router load-balancing loss per window (backprop.py:359-377); grad_row [nseg][experts] may be null.
+int launch_router_stats(const float* probs, int64_t layer_stride, int64_t layers, const int64_t* seg, int nseg,
+                        const int64_t* counts, int64_t experts, double router_scale, double* loss, float* grad_row,
+                        hipStream_t stream);
+int launch_broadcast_window_rows(const float* grad_row, const int64_t* seg, int nseg, int64_t rows, int64_t experts,
+                                 float* out, hipStream_t stream);
+
 // ---- attention (attention.hip) ----
 
 struct AttentionShape {

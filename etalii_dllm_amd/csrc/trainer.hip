@@ -1,8 +1,8 @@
 // The device-resident fine-tuning step (include/dllm_hip.h, dllm_hip_trainer_*).
 //
 // Restates FineTuner.train_step (src/etalii_dllm/training/trainer.py:290-335), DecoderGradients
-// (training/backprop.py:88-118, 183-306, 399-499) and AdamW.step (training/optimizer.py:82-109) for pre-norm dense
-// decoders (Llama, Mistral, Qwen2, Qwen3 families) on one GPU:
+// (training/backprop.py:88-118, 183-377, 399-527) and AdamW.step (training/optimizer.py:82-109) for pre-norm
+// decoders (Llama, Mistral, Qwen2, Qwen3 dense; Mixtral, OLMoE routed experts) on one GPU:
 //  - all windows of a step are packed into one batch of rows. Row-local work (linear, dX, norms, RoPE, SwiGLU,
 //    cross-entropy) is independent of the rows it is batched with, so packing changes no bit;
 //  - every reduction over a window's rows (dW, db, norm weights, the embedding) is done per window and the per-window
@@ -11,7 +11,12 @@
 //    x_out = x_mid + mlp in the projection epilogues, dh1 = (dq + dk) + dv and dh2 = dx_gate + dx_up in the dX
 //    epilogues, dx_mid = dx + dh2' and dx = dx_mid + dh1' in the norm-backward kernels;
 //  - the tied embedding's gradient (dembedding + dhead per window, then summed over windows) is the head dW with the
-//    window's embedding rows as an addend.
+//    window's embedding rows as an addend;
+//  - routed experts (backprop.py:308-357, 501-527): after each layer's routing the chosen experts come back to the
+//    host, which groups the step's rows by expert (experts ascending, rows ascending: a window's group is a
+//    contiguous run inside the step's group) and splits each group at the window boundaries, so an expert's dW is
+//    the same per-window float sum as any other weight's. An expert no row of a window reaches adds that window's
+//    +0.0f, as the reference's zero gradient does.
 // Weights, gradients and AdamW moments live in one arena each, tensors in natural name order.
 #include <math.h>
 #include <string.h>
@@ -143,12 +148,22 @@ struct dllm_hip_trainer {
 
     struct LayerIds {
         int attn_norm, q, k, v, qb = -1, kb = -1, vb = -1, qn = -1, kn = -1, o, mlp_norm, gate, up, down;
+        int router = -1;
+        std::vector<int> egate, eup, edown;  // routed experts
     };
     std::vector<LayerIds> layer_ids;
     int emb = -1, final_norm = -1, lm_head = -1;
 
     struct Saved {
         float *x_in, *h1, *q_raw, *k_raw, *qn, *kn, *q, *k, *v, *attended, *x_mid, *h2, *gate, *up, *gate_act, *product;
+        // routed experts: router logits and probabilities [R][E], the choices [R][K] (rank order), the expert
+        // outputs y [R K][H] in grouped order (gate, up, gate_act, product are grouped [R K][EI] then)
+        float *router_logits = nullptr, *probs = nullptr, *routing = nullptr, *y = nullptr;
+        int64_t* chosen = nullptr;
+        // grouping: position p of the grouped rows holds row row_of[p], routing slot slot[p]; order[r K + i] is the
+        // position of row r's i-th choice by ascending expert; eseg[e][w] the window boundaries in expert e's group
+        int64_t *row_of = nullptr, *slot = nullptr, *order = nullptr, *eseg = nullptr;
+        std::vector<int64_t> estart;  // host: E + 1 group starts
     };
     std::vector<Saved> saved;
     std::vector<std::unique_ptr<DevBuf>> owned;
@@ -157,6 +172,15 @@ struct dllm_hip_trainer {
           *dv_t = nullptr, *dq = nullptr, *dk = nullptr, *dq2 = nullptr, *dk2 = nullptr, *dproduct = nullptr,
           *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *emb_rows = nullptr, *gemm_part = nullptr;
     int64_t gemm_part_cap = 0;  // floats: per-window partials of the layer weight gradients
+    // routed experts: E experts, K per token, EI expert intermediate size; shared buffers of the grouped rows
+    int64_t E = 0, K = 0, EI = 0, RK = 0;
+    float *xg = nullptr, *dyg = nullptr, *dxg = nullptr, *dweights = nullptr, *dlogits_r = nullptr, *dprob = nullptr,
+          *dh2r = nullptr, *grad_row = nullptr;
+    double* router_loss_w = nullptr;
+    float* probs_all = nullptr;
+    int64_t* counts_d = nullptr;
+    std::vector<int64_t> counts_host;  // [windows][E] choices per window over all layers
+    double router_scale_cur = 0.0, last_router_loss = 0.0;
     double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
            *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
     void* attn_ws = nullptr;
@@ -247,9 +271,19 @@ struct dllm_hip_trainer {
             }
             add_tensor(p + "attention.o.weight", H, QD, true);
             add_tensor(p + "mlp_norm.weight", H, 0, false);
-            add_tensor(p + "mlp.gate.weight", I, H, true);
-            add_tensor(p + "mlp.up.weight", I, H, true);
-            add_tensor(p + "mlp.down.weight", H, I, true);
+            if (E > 0) {  // architecture.py: a routed layer has the router and E experts instead of the dense MLP
+                add_tensor(p + "mlp.router.weight", E, H, true);
+                for (int64_t e = 0; e < E; ++e) {
+                    const std::string x = p + "mlp.experts." + std::to_string(e) + ".";
+                    add_tensor(x + "gate.weight", EI, H, true);
+                    add_tensor(x + "up.weight", EI, H, true);
+                    add_tensor(x + "down.weight", H, EI, true);
+                }
+            } else {
+                add_tensor(p + "mlp.gate.weight", I, H, true);
+                add_tensor(p + "mlp.up.weight", I, H, true);
+                add_tensor(p + "mlp.down.weight", H, I, true);
+            }
         }
         add_tensor("final_norm.weight", H, 0, false);
         if (!k.tie_embeddings) add_tensor("lm_head.weight", V, H, true);
@@ -299,6 +333,13 @@ struct dllm_hip_trainer {
             L.gate = id(p + "mlp.gate.weight");
             L.up = id(p + "mlp.up.weight");
             L.down = id(p + "mlp.down.weight");
+            L.router = id(p + "mlp.router.weight");
+            for (int64_t e = 0; e < E; ++e) {
+                const std::string x = p + "mlp.experts." + std::to_string(e) + ".";
+                L.egate.push_back(id(x + "gate.weight"));
+                L.eup.push_back(id(x + "up.weight"));
+                L.edown.push_back(id(x + "down.weight"));
+            }
             layer_ids.push_back(L);
         }
         merged_offset.assign(tensors.size(), -1);
@@ -363,6 +404,7 @@ struct dllm_hip_trainer {
     int build_activations() {
         const int64_t R = R_max, heads = c.heads, kvh = c.kv_heads;
         saved.resize(static_cast<size_t>(c.layers));
+        if (E > 0) DLLM_TRY(make(&probs_all, c.layers * R * E));  // [layer][row][expert], the router statistics' input
         // x_in of layer l + 1 is x_out of layer l: one chain of L + 1 residual buffers.
         std::vector<float*> xs(static_cast<size_t>(c.layers) + 1);
         for (auto& p : xs) DLLM_TRY(make(&p, R * H));
@@ -383,11 +425,36 @@ struct dllm_hip_trainer {
             DLLM_TRY(make(&s.attended, R * QD));
             DLLM_TRY(make(&s.x_mid, R * H));
             DLLM_TRY(make(&s.h2, R * H));
-            DLLM_TRY(make(&s.gate, R * I));
-            DLLM_TRY(make(&s.up, R * I));
-            DLLM_TRY(make(&s.gate_act, R * I));
-            DLLM_TRY(make(&s.product, R * I));
+            const int64_t mlp_rows = E > 0 ? RK : R, mlp_inter = E > 0 ? EI : I;
+            DLLM_TRY(make(&s.gate, mlp_rows * mlp_inter));
+            DLLM_TRY(make(&s.up, mlp_rows * mlp_inter));
+            DLLM_TRY(make(&s.gate_act, mlp_rows * mlp_inter));
+            DLLM_TRY(make(&s.product, mlp_rows * mlp_inter));
+            if (E > 0) {
+                DLLM_TRY(make(&s.router_logits, R * E));
+                s.probs = probs_all + l * R * E;
+                DLLM_TRY(make(&s.routing, RK));
+                DLLM_TRY(make(&s.y, RK * H));
+                DLLM_TRY(make(&s.chosen, RK));
+                DLLM_TRY(make(&s.row_of, RK));
+                DLLM_TRY(make(&s.slot, RK));
+                DLLM_TRY(make(&s.order, RK));
+                DLLM_TRY(make(&s.eseg, E * (W_max + 1)));
+            }
         }
+        if (E > 0) {
+            DLLM_TRY(make(&xg, RK * H));
+            DLLM_TRY(make(&dyg, RK * H));
+            DLLM_TRY(make(&dxg, RK * H));
+            DLLM_TRY(make(&dweights, RK));
+            DLLM_TRY(make(&dlogits_r, R * E));
+            DLLM_TRY(make(&dprob, R * E));
+            DLLM_TRY(make(&dh2r, R * H));
+            DLLM_TRY(make(&grad_row, W_max * E));
+            DLLM_TRY(make(&router_loss_w, W_max));
+            DLLM_TRY(make(&counts_d, W_max * E));
+        }
+        const int64_t dmlp = std::max(R * I, RK * EI);
         x_final = xs.back();
         DLLM_TRY(make(&hidden, R * H));
         DLLM_TRY(make(&logits, R * V));
@@ -403,12 +470,12 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&dk, R * KVD));
         DLLM_TRY(make(&dq2, R * QD));
         DLLM_TRY(make(&dk2, R * KVD));
-        DLLM_TRY(make(&dproduct, R * I));
-        DLLM_TRY(make(&dgate, R * I));
-        DLLM_TRY(make(&dup, R * I));
+        DLLM_TRY(make(&dproduct, dmlp));
+        DLLM_TRY(make(&dgate, dmlp));
+        DLLM_TRY(make(&dup, dmlp));
         DLLM_TRY(make(&col_part, W_max * std::max<int64_t>({H, QD, KVD, I})));
         if (W_max > 1) {
-            gemm_part_cap = W_max * H * std::max<int64_t>({QD, KVD, I});
+            gemm_part_cap = W_max * H * std::max<int64_t>({QD, KVD, I, EI, E});
             DLLM_TRY(make(&gemm_part, gemm_part_cap));
         }
         DLLM_TRY(make(&emb_rows, R * H));
@@ -492,7 +559,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_gemm(g, s));
         DLLM_TRY(check_hip(hipEventRecord(events[event_used + 1], s), "event"));
         event_used += 2;
-        const double L = g.seg ? static_cast<double>(seg_host.back()) : static_cast<double>(g.l1 - g.l0);
+        const double L = static_cast<double>(g.l1 - g.l0);  // segmented calls set [l0, l1) to their whole row range
         profile_flops += 2.0 * static_cast<double>(g.I) * static_cast<double>(g.J) * L;
         profile_launches += 1;
         return kOk;
@@ -551,9 +618,10 @@ struct dllm_hip_trainer {
         return gemm(g, s);
     }
 
-    // grad[w] = window-ordered float sum of per-window dW = sum over window rows of dy[r][n] x[r][k].
+    // grad[w] = window-ordered float sum of per-window dW = sum over window rows of dy[r][n] x[r][k]. The windows are
+    // the step's (seg_d), or those of an expert's group (seg, over `rows` grouped rows).
     int linear_dw(const float* dyv, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
-                  const float* addend, hipStream_t s) {
+                  const float* addend, hipStream_t s, const int64_t* seg = nullptr, int64_t rows = -1) {
         GemmCall g;
         g.Af = dyv;  // A rows: A[r][n] = dy[r][n]
         g.a_kind = 1;
@@ -564,8 +632,10 @@ struct dllm_hip_trainer {
         g.ldc = K;
         g.I = N;
         g.J = K;
-        g.seg = seg_d;
+        g.seg = seg ? seg : seg_d;
         g.nseg = nseg;
+        g.l0 = 0;
+        g.l1 = seg ? rows : seg_host.back();
         g.seg_addrow = addrow_;
         g.seg_addend = addend;
         g.ld_seg_add = K;
@@ -736,6 +806,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(attention_forward(l, sv, b, s));
         DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
         DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
+        if (E > 0) return moe_forward(l, R, x_out, s);
         DLLM_TRY(linear_fwd(sv.h2, R, H, L.gate, nullptr, sv.gate, nullptr, s));
         DLLM_TRY(linear_fwd(sv.h2, R, H, L.up, nullptr, sv.up, nullptr, s));
         DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * I, s));
@@ -748,14 +819,18 @@ struct dllm_hip_trainer {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
         const Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
-        // SwiGLU (backprop.py:289-306)
-        DLLM_TRY(linear_dx(dx, R, L.down, dproduct, nullptr, s));
-        DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, s));
-        DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s));
-        DLLM_TRY(linear_dx(dgate, R, L.gate, dh, nullptr, s));
-        DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, s));
-        DLLM_TRY(linear_dx(dup, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
-        DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, s));
+        if (E > 0) {
+            DLLM_TRY(moe_backward(l, R, nseg, s));
+        } else {
+            // SwiGLU (backprop.py:289-306)
+            DLLM_TRY(linear_dx(dx, R, L.down, dproduct, nullptr, s));
+            DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, s));
+            DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s));
+            DLLM_TRY(linear_dx(dgate, R, L.gate, dh, nullptr, s));
+            DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, s));
+            DLLM_TRY(linear_dx(dup, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
+            DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, s));
+        }
         // mlp norm; dx_mid = dx + dh2'
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_rms, s));
         DLLM_TRY(norm_dw(dh, sv.x_mid, inv_rms, H, 1, nseg, G(L.mlp_norm), s));
@@ -799,6 +874,121 @@ struct dllm_hip_trainer {
         // attention norm; dx = dx_mid + dh1'
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh, dx, dx_mid, R, H, eps, 0, inv_rms, s));
         return norm_dw(dh, sv.x_in, inv_rms, H, 1, nseg, G(L.attn_norm), s);
+    }
+
+    // ---- routed experts (backprop.py:308-377, 501-527) ----
+
+    // Groups the step's rows by expert from the layer's choices (host; the choices come back first): experts
+    // ascending, within an expert rows ascending (np.nonzero), and the per-window split of each group.
+    int group_rows(Saved& sv, int64_t R, hipStream_t s) {
+        std::vector<int64_t> chosen(static_cast<size_t>(R * K));
+        DLLM_TRY(check_hip(hipMemcpyAsync(chosen.data(), sv.chosen, chosen.size() * 8, hipMemcpyDeviceToHost, s),
+                           "download"));
+        DLLM_TRY(check_hip(hipStreamSynchronize(s), "routing"));
+        const int64_t nw = nwin;
+        std::vector<int64_t> count(static_cast<size_t>(E), 0);
+        for (int64_t i = 0; i < R * K; ++i) {
+            const int64_t e = chosen[static_cast<size_t>(i)];
+            DLLM_REQUIRE(e >= 0 && e < E, "routing produced an expert out of range");
+            ++count[static_cast<size_t>(e)];
+        }
+        sv.estart.assign(static_cast<size_t>(E + 1), 0);
+        for (int64_t e = 0; e < E; ++e) sv.estart[static_cast<size_t>(e + 1)] = sv.estart[e] + count[e];
+        std::vector<int64_t> fill(sv.estart.begin(), sv.estart.end() - 1);
+        std::vector<int64_t> row_of(static_cast<size_t>(R * K)), slot(row_of.size()), order(row_of.size());
+        std::vector<int64_t> eseg(static_cast<size_t>(E * (W_max + 1)), 0);
+        std::vector<std::pair<int64_t, int64_t>> pick(static_cast<size_t>(K));
+        int64_t w = 0;
+        for (int64_t r = 0; r < R; ++r) {
+            while (seg_host[static_cast<size_t>(w + 1)] <= r) ++w;
+            for (int64_t j = 0; j < K; ++j) {
+                const int64_t e = chosen[static_cast<size_t>(r * K + j)];
+                const int64_t p = fill[static_cast<size_t>(e)]++;
+                row_of[static_cast<size_t>(p)] = r;
+                slot[static_cast<size_t>(p)] = r * K + j;
+                ++eseg[static_cast<size_t>(e * (W_max + 1) + w + 1)];
+                ++counts_host[static_cast<size_t>(w * E + e)];
+            }
+            // the row's positions by ascending expert (a row chooses an expert at most once)
+            for (int64_t j = 0; j < K; ++j) {
+                const int64_t e = chosen[static_cast<size_t>(r * K + j)];
+                pick[static_cast<size_t>(j)] = {e, fill[static_cast<size_t>(e)] - 1};
+            }
+            std::sort(pick.begin(), pick.end());
+            for (int64_t j = 0; j < K; ++j) order[static_cast<size_t>(r * K + j)] = pick[static_cast<size_t>(j)].second;
+        }
+        for (int64_t e = 0; e < E; ++e)
+            for (int64_t i = 1; i <= nw; ++i) eseg[static_cast<size_t>(e * (W_max + 1) + i)] +=
+                eseg[static_cast<size_t>(e * (W_max + 1) + i - 1)];
+        DLLM_TRY(check_hip(hipMemcpyAsync(sv.row_of, row_of.data(), row_of.size() * 8, hipMemcpyHostToDevice, s),
+                           "upload"));
+        DLLM_TRY(check_hip(hipMemcpyAsync(sv.slot, slot.data(), slot.size() * 8, hipMemcpyHostToDevice, s), "upload"));
+        DLLM_TRY(check_hip(hipMemcpyAsync(sv.order, order.data(), order.size() * 8, hipMemcpyHostToDevice, s),
+                           "upload"));
+        DLLM_TRY(check_hip(hipMemcpyAsync(sv.eseg, eseg.data(), eseg.size() * 8, hipMemcpyHostToDevice, s), "upload"));
+        // the host vectors die here: wait for the copies
+        return check_hip(hipStreamSynchronize(s), "grouping");
+    }
+
+    // _experts (backprop.py:501-527): route, group, the SwiGLU of every expert over its rows, and
+    // x_out = x_mid + sum over the row's experts (ascending) of f32(y w).
+    int moe_forward(int64_t l, int64_t R, float* x_out, hipStream_t s) {
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        Saved& sv = saved[static_cast<size_t>(l)];
+        DLLM_TRY(linear_fwd(sv.h2, R, H, L.router, nullptr, sv.router_logits, nullptr, s));
+        DLLM_TRY(launch_moe_route(sv.router_logits, R, E, K, c.normalize_expert_weights ? 1 : 0, sv.chosen,
+                                  sv.routing, sv.probs, s));
+        DLLM_TRY(group_rows(sv, R, s));
+        DLLM_TRY(launch_gather_rows(sv.h2, sv.row_of, xg, R * K, H, s));
+        for (int64_t e = 0; e < E; ++e) {
+            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
+            if (n == 0) continue;
+            DLLM_TRY(linear_fwd(xg + st * H, n, H, L.egate[e], nullptr, sv.gate + st * EI, nullptr, s));
+            DLLM_TRY(linear_fwd(xg + st * H, n, H, L.eup[e], nullptr, sv.up + st * EI, nullptr, s));
+        }
+        DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * K * EI, s));
+        for (int64_t e = 0; e < E; ++e) {
+            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
+            if (n == 0) continue;
+            DLLM_TRY(linear_fwd(sv.product + st * EI, n, EI, L.edown[e], nullptr, sv.y + st * H, nullptr, s));
+        }
+        return launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sv.x_mid, x_out, R, K, H, s);
+    }
+
+    // _experts_backward (backprop.py:308-357): dh (dh2) from dx (the gradient of the layer's MLP output).
+    int moe_backward(int64_t l, int64_t R, int nseg, hipStream_t s) {
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        const Saved& sv = saved[static_cast<size_t>(l)];
+        const int64_t P = R * K;
+        DLLM_TRY(launch_moe_dweights(dx, sv.y, sv.row_of, sv.slot, sv.routing, P, H, dweights, dyg, s));
+        DLLM_TRY(launch_gather_rows(sv.h2, sv.row_of, xg, P, H, s));
+        const auto eseg = [&](int64_t e) { return sv.eseg + e * (W_max + 1); };
+        for (int64_t e = 0; e < E; ++e) {
+            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
+            DLLM_TRY(linear_dx(dyg + st * H, n, L.edown[e], dproduct + st * EI, nullptr, s));
+            DLLM_TRY(linear_dw(dyg + st * H, H, sv.product + st * EI, EI, nseg, G(L.edown[e]), nullptr, nullptr, s,
+                               eseg(e), n));
+        }
+        DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, P * EI, s));
+        for (int64_t e = 0; e < E; ++e) {
+            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
+            DLLM_TRY(linear_dx(dgate + st * EI, n, L.egate[e], dxg + st * H, nullptr, s));
+            DLLM_TRY(linear_dw(dgate + st * EI, EI, xg + st * H, H, nseg, G(L.egate[e]), nullptr, nullptr, s,
+                               eseg(e), n));
+            DLLM_TRY(linear_dx(dup + st * EI, n, L.eup[e], dxg + st * H, dxg + st * H, s));  // dx_gate + dx_up
+            DLLM_TRY(linear_dw(dup + st * EI, EI, xg + st * H, H, nseg, G(L.eup[e]), nullptr, nullptr, s, eseg(e),
+                               n));
+        }
+        // the router: dlogits from the routing weights' gradients (and the load-balancing loss's), then its linear
+        if (router_scale_cur != 0.0)
+            DLLM_TRY(launch_broadcast_window_rows(grad_row, seg_d, nseg, R, E, dprob, s));
+        DLLM_TRY(launch_moe_route_backward(sv.router_logits, sv.chosen, dweights,
+                                           router_scale_cur != 0.0 ? dprob : nullptr, R, E, K,
+                                           c.normalize_expert_weights ? 1 : 0, dlogits_r, s));
+        DLLM_TRY(linear_dx(dlogits_r, R, L.router, dh2r, nullptr, s));
+        DLLM_TRY(linear_dw(dlogits_r, E, sv.h2, H, nseg, G(L.router), nullptr, nullptr, s));
+        // dh2 = (0 + the experts' dx in expert order) + dh2_router
+        return launch_moe_combine(dxg, sv.order, sv.slot, nullptr, dh2r, dh, R, K, H, s);
     }
 
     // Host preparation of a batch of windows; returns the packed row count.
@@ -870,7 +1060,7 @@ struct dllm_hip_trainer {
     }
 
     int gradients(const int64_t* tokens, const int64_t* offsets, const int64_t* lengths, int64_t windows,
-                  double scale, double* loss, hipStream_t s) {
+                  double scale, double router_scale, double* loss, double* router_loss, hipStream_t s) {
         int64_t R = 0, groups = 0;
         AttentionBatch b{};
         DLLM_TRY(prepare(tokens, offsets, lengths, windows, &R, &b, &groups, s));
@@ -880,12 +1070,20 @@ struct dllm_hip_trainer {
             DLLM_TRY(refresh_transposes(s));
         const int nseg = static_cast<int>(windows);
         nwin = windows;
+        router_scale_cur = router_scale;
+        if (E > 0) counts_host.assign(static_cast<size_t>(windows * E), 0);
         const double eps = c.rms_norm_eps;
         // forward (backprop.py:411-490)
         DLLM_TRY(launch_gather_rows(P(emb), tok_in, saved[0].x_in, R, H, s));
         for (int64_t l = 0; l < c.layers; ++l) {
             float* x_out = l + 1 < c.layers ? saved[static_cast<size_t>(l + 1)].x_in : x_final;
             DLLM_TRY(forward_layer(l, R, b, x_out, s));
+        }
+        if (E > 0) {  // _router_loss (backprop.py:359-377): per window, over every layer's rows
+            DLLM_TRY(check_hip(hipMemcpyAsync(counts_d, counts_host.data(), counts_host.size() * 8,
+                                              hipMemcpyHostToDevice, s), "upload"));
+            DLLM_TRY(launch_router_stats(probs_all, R_max * E, c.layers, seg_d, nseg, counts_d, E, router_scale,
+                                         router_loss_w, router_scale != 0.0 ? grad_row : nullptr, s));
         }
         DLLM_TRY(launch_rms_norm(x_final, P(final_norm), hidden, R, H, eps, 0, nullptr, s));
         const int head = c.tie_embeddings ? emb : lm_head;
@@ -909,15 +1107,22 @@ struct dllm_hip_trainer {
                                addrow, V, H, nseg, G(emb));
             DLLM_TRY(check_launch("embedding window sum"));
         }
-        std::vector<double> lw(static_cast<size_t>(windows));
+        std::vector<double> lw(static_cast<size_t>(windows)), rw(static_cast<size_t>(windows), 0.0);
         int flag = 0;
         DLLM_TRY(check_hip(hipMemcpyAsync(lw.data(), loss_w, lw.size() * 8, hipMemcpyDeviceToHost, s), "download"));
+        if (E > 0)
+            DLLM_TRY(check_hip(hipMemcpyAsync(rw.data(), router_loss_w, rw.size() * 8, hipMemcpyDeviceToHost, s),
+                               "download"));
         DLLM_TRY(check_hip(hipMemcpyAsync(&flag, err_flag, sizeof flag, hipMemcpyDeviceToHost, s), "download"));
         DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
         DLLM_REQUIRE(flag == 0, "target out of range");
         double total = 0.0;
         for (double x : lw) total += x;  // trainer.py:326 (loss_total += loss, batch order)
         if (loss) *loss = total;
+        double rtotal = 0.0;
+        for (double x : rw) rtotal += x;  // trainer.py:327 (router_total += router_loss, batch order)
+        last_router_loss = rtotal;
+        if (router_loss) *router_loss = rtotal;
         return kOk;
     }
 
@@ -927,8 +1132,9 @@ struct dllm_hip_trainer {
         for (int64_t w = 0; w < windows; ++w) targets_total += lengths[w] - 1;
         DLLM_REQUIRE(targets_total > 0, "a step needs targets");
         const double scale = 1.0 / static_cast<double>(targets_total);
-        double loss_total = 0.0;
-        DLLM_TRY(gradients(tokens, offsets, lengths, windows, scale, &loss_total, s));
+        double loss_total = 0.0, router_total = 0.0;
+        DLLM_TRY(gradients(tokens, offsets, lengths, windows, scale, a->router_aux_loss / static_cast<double>(windows),
+                           &loss_total, &router_total, s));
         if (lora_on) DLLM_TRY(adapter_gradients(s));  // trainer.py:463-474
         OptimizerSet& o = lora_on ? lora_opt : main_opt;
         // global norm, clip (optimizer.py:66-90), bias corrections by repeated multiplication (optimizer.py:59-63)
@@ -951,7 +1157,11 @@ struct dllm_hip_trainer {
         double st[3];
         DLLM_TRY(check_hip(hipMemcpyAsync(st, stats, sizeof st, hipMemcpyDeviceToHost, s), "download"));
         DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
-        if (loss) *loss = loss_total / static_cast<double>(targets_total);
+        if (loss) {
+            *loss = loss_total / static_cast<double>(targets_total);
+            if (a->router_aux_loss != 0.0)  // trainer.py:333-335
+                *loss += a->router_aux_loss * router_total / static_cast<double>(windows);
+        }
         if (norm) *norm = st[1];
         return kOk;
     }
@@ -982,9 +1192,16 @@ struct dllm_hip_trainer {
                                           "mlp.down.weight"};
         std::vector<int> weights;
         for (int64_t layer = 0; layer < c.layers; ++layer)
-            for (int t = 0; t < 7; ++t)
-                if (l.targets & (int64_t{1} << t))
+            for (int t = 0; t < 7; ++t) {
+                if (!(l.targets & (int64_t{1} << t))) continue;
+                const LayerIds& L = layer_ids[static_cast<size_t>(layer)];
+                if (t >= 4 && E > 0) {  // gate, up, down of a routed layer: every expert's (the router never)
+                    const std::vector<int>& ids = t == 4 ? L.egate : (t == 5 ? L.eup : L.edown);
+                    weights.insert(weights.end(), ids.begin(), ids.end());
+                } else {
                     weights.push_back(index["layers." + std::to_string(layer) + "." + kTargets[t]]);
+                }
+            }
         for (int w : weights) {
             const TensorInfo& t = tensors[static_cast<size_t>(w)];
             TensorInfo a, b;
@@ -1106,7 +1323,14 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
         DLLM_REQUIRE(lora->base_quantize == 0 || lora->base_quantize == 1, "base_quantize must be 0 (float) or 1 (q8_0)");
     }
     const dllm_hip_decoder_config& c = *config;
-    DLLM_REQUIRE(c.experts == 0, "mixture-of-experts layers are not supported by this trainer yet");
+    const int64_t ei = c.experts > 0 ? (c.expert_intermediate > 0 ? c.expert_intermediate : c.intermediate) : 0;
+    DLLM_REQUIRE(c.experts >= 0, "negative number of experts");
+    if (c.experts > 0) {
+        DLLM_REQUIRE(c.experts_per_token >= 1 && c.experts_per_token <= c.experts,
+                     "experts per token must be between 1 and the number of experts");
+        DLLM_REQUIRE(c.experts % 4 == 0 && ei % 4 == 0,
+                     "the number of experts and the expert intermediate size must be multiples of 4");
+    }
     DLLM_REQUIRE(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, "heads must be a multiple of kv_heads");
     DLLM_REQUIRE(c.rotary_dim > 0 && c.rotary_dim % 2 == 0 && c.rotary_dim <= c.head_dim, "invalid rotary_dim");
     DLLM_REQUIRE(c.head_dim % 4 == 0, "head_dim must be a multiple of 4");
@@ -1125,6 +1349,10 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     t->KVD = c.kv_heads * c.head_dim;
     t->I = c.intermediate;
     t->V = c.vocab;
+    t->E = c.experts;
+    t->K = c.experts > 0 ? c.experts_per_token : 0;
+    t->EI = ei;
+    t->RK = max_tokens * t->K;
     DLLM_TRY(t->build_tensors());
     if (lora) DLLM_TRY(t->build_lora(*lora));
     DLLM_TRY(t->build_activations());
@@ -1210,8 +1438,14 @@ int dllm_hip_trainer_gradients(dllm_hip_trainer* t, const int64_t* tokens, const
                                const int64_t* lengths, int64_t windows, double scale, double router_scale,
                                double* loss, void* stream) {
     DLLM_REQUIRE(t && tokens && offsets && lengths, "null argument");
-    (void)router_scale;  // dense models have no router loss
-    return t->gradients(tokens, offsets, lengths, windows, scale, loss, static_cast<hipStream_t>(stream));
+    return t->gradients(tokens, offsets, lengths, windows, scale, router_scale, loss, nullptr,
+                        static_cast<hipStream_t>(stream));
+}
+
+int dllm_hip_trainer_router_loss(dllm_hip_trainer* t, double* router_loss) {
+    DLLM_REQUIRE(t && router_loss, "null argument");
+    *router_loss = t->last_router_loss;
+    return kOk;
 }
 
 int dllm_hip_trainer_step(dllm_hip_trainer* t, const int64_t* tokens, const int64_t* offsets, const int64_t* lengths,

@@ -68,6 +68,8 @@ def _load() -> C.CDLL:
     lib.dllm_hip_sum_squares_workspace.restype = _sz
     lib.dllm_hip_sum_squares_workspace.argtypes = [_sz]
     lib.dllm_hip_adamw_step.argtypes = [_vp, _vp, _vp, _vp, _sz] + [C.c_double] * 8 + [_vp]
+    lib.dllm_hip_moe_route.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp]
+    lib.dllm_hip_moe_route_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp]
     lib.dllm_hip_quantize_q8_0.argtypes = [_vp, _vp, _vp, _sz, _vp]
     lib.dllm_hip_dequantize_q8_0.argtypes = [_vp, _vp, _vp, _sz, _vp]
     lib.dllm_hip_lora_merge_workspace.restype = _sz
@@ -367,6 +369,44 @@ def adamw_step(param, grad, m, v, lr, beta1, beta2, eps, weight_decay, bias_corr
 
 
 # ---- LoRA and Q8_0 (src/etalii_dllm/lora.py, numerics.py:106-139) ----
+
+def moe_route(logits, k: int, normalize: bool) -> tuple[np.ndarray, np.ndarray]:
+    """kernels.cpp:190-204: (indices int64 [rows, k], weights [rows, k]) in rank order."""
+    x = _f32(logits)
+    if x.ndim != 2:
+        raise ValueError("logits must be [rows, experts]")
+    rows, experts = x.shape
+    if not 1 <= k <= experts:
+        raise ValueError("experts per token must be between 1 and the number of experts")
+    d, idx, w = Device.of(x), Device(max(rows * k, 1) * 8), Device(max(rows * k, 1) * 4)
+    check(lib.dllm_hip_moe_route(d.ptr, idx.ptr, w.ptr, rows, experts, k, int(bool(normalize)), None))
+    return idx.download((rows, k), np.int64), w.download((rows, k))
+
+
+def moe_route_backward(logits, indices, dweights, dprobabilities, normalize: bool) -> np.ndarray:
+    """kernels.cpp:1005-1027: dlogits [rows, experts]."""
+    x = _f32(logits)
+    idx = np.ascontiguousarray(indices, dtype=np.int64)
+    dw = _f32(dweights)
+    rows, experts = x.shape
+    if idx.ndim != 2 or idx.shape[0] != rows or not 1 <= idx.shape[1] <= experts:
+        raise ValueError("indices must be [rows, k] with k between 1 and the number of experts")
+    k = idx.shape[1]
+    if dw.shape != idx.shape:
+        raise ValueError("dweights must have the shape of indices")
+    dp = None
+    if dprobabilities is not None:
+        dp = _f32(dprobabilities)
+        if dp.shape != x.shape:
+            raise ValueError("dprobabilities must have the shape of logits")
+    if np.any(idx < 0) or np.any(idx >= experts):
+        raise ValueError("expert index out of range")
+    d, di, ddw, out = Device.of(x), Device.of(idx), Device.of(dw), Device(max(x.size, 1) * 4)
+    ddp = Device.of(dp) if dp is not None else None
+    check(lib.dllm_hip_moe_route_backward(d.ptr, di.ptr, ddw.ptr, ddp.ptr if ddp else None, out.ptr, rows, experts,
+                                          k, int(bool(normalize)), None))
+    return out.download((rows, experts))
+
 
 def quantize_q8_0(weight) -> tuple[np.ndarray, np.ndarray]:
     """kernels.cpp quantize_q8_0 as QuantizedWeight uses it: (int8 values [out, in], float scales [out, in / 32])."""

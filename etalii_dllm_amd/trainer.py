@@ -66,6 +66,7 @@ lib.dllm_hip_trainer_tensor.argtypes = [C.c_void_p, C.c_char_p, C.c_int, C.POINT
 lib.dllm_hip_trainer_tensor_count.argtypes = [C.c_void_p, C.POINTER(C.c_int64)]
 lib.dllm_hip_trainer_gradients.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_int64, C.c_double, C.c_double,
                                            C.POINTER(C.c_double), C.c_void_p]
+lib.dllm_hip_trainer_router_loss.argtypes = [C.c_void_p, C.POINTER(C.c_double)]
 lib.dllm_hip_trainer_step.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_int64, C.POINTER(AdamWArgs),
                                       C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_void_p]
 
@@ -87,12 +88,17 @@ class Decoder:
     attention_bias: bool = False
     qk_norm: int = 0
     sliding_window: int = 0
+    experts: int = 0  # routed experts per layer (Mixtral, OLMoE); 0 is a dense MLP
+    experts_per_token: int = 0
+    normalize_expert_weights: bool = False
+    expert_intermediate: int = 0  # 0: the intermediate size
 
     def native(self) -> DecoderConfig:
         return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
                              self.head_dim, int(self.attention_bias), self.qk_norm, self.sliding_window,
-                             int(self.tie_embeddings), 0, 0, 0, 0, self.head_dim, self.rms_norm_eps, self.rope_theta,
-                             1.0 / float(np.sqrt(np.float64(self.head_dim))))
+                             int(self.tie_embeddings), self.experts, self.experts_per_token,
+                             int(self.normalize_expert_weights), self.expert_intermediate, self.head_dim,
+                             self.rms_norm_eps, self.rope_theta, 1.0 / float(np.sqrt(np.float64(self.head_dim))))
 
 
 def _windows(windows):
@@ -153,20 +159,27 @@ class Trainer:
         for name, values in tensors.items():
             self.set(name, values, which)
 
-    def gradients(self, windows, scale: float = 1.0) -> float:
-        """DecoderGradients over each window, summed in window order; returns the summed loss."""
+    def gradients(self, windows, scale: float = 1.0, router_scale: float = 0.0) -> float:
+        """DecoderGradients over each window, summed in window order; returns the summed loss (the summed router
+        loss is `router_loss()` afterwards)."""
         flat, offsets, lengths = _windows(windows)
         loss = C.c_double()
         check(lib.dllm_hip_trainer_gradients(self.handle, flat.ctypes.data_as(_i64p), offsets.ctypes.data_as(_i64p),
-                                             lengths.ctypes.data_as(_i64p), len(windows), scale, 0.0, C.byref(loss),
-                                             None))
+                                             lengths.ctypes.data_as(_i64p), len(windows), scale, router_scale,
+                                             C.byref(loss), None))
         return loss.value
 
+    def router_loss(self) -> float:
+        """The router load-balancing loss summed over the windows of the last gradients or step call."""
+        value = C.c_double()
+        check(lib.dllm_hip_trainer_router_loss(self.handle, C.byref(value)))
+        return value.value
+
     def step(self, windows, learning_rate: float, step: int, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
-             max_grad_norm=1.0) -> tuple[float, float]:
+             max_grad_norm=1.0, router_aux_loss=0.0) -> tuple[float, float]:
         """One fine-tuning step (trainer.py:290-310) at the given learning rate: (mean loss, gradient norm)."""
         flat, offsets, lengths = _windows(windows)
-        args = AdamWArgs(learning_rate, beta1, beta2, eps, weight_decay, max_grad_norm, 0.0, step)
+        args = AdamWArgs(learning_rate, beta1, beta2, eps, weight_decay, max_grad_norm, router_aux_loss, step)
         loss, norm = C.c_double(), C.c_double()
         check(lib.dllm_hip_trainer_step(self.handle, flat.ctypes.data_as(_i64p), offsets.ctypes.data_as(_i64p),
                                         lengths.ctypes.data_as(_i64p), len(windows), C.byref(args), C.byref(loss),

@@ -125,6 +125,20 @@ int dllm_hip_adamw_step(float* param, const float* grad, float* m, float* v, siz
                         double beta2, double eps, double weight_decay, double bias_correction1,
                         double bias_correction2, double grad_scale, void* stream);
 
+/* ---- mixture-of-experts routing ---- */
+
+/* indices [rows, k] (int64) and weights [rows, k] of MoE routing: each row's softmax, the k largest probabilities in
+ * a total order (ties to the lower expert), divided by their total with normalize; rank order. Replaces
+ * kernels.cpp:190-204 `moe_route` (nn.hpp:864-896). k outside [1, experts] is an invalid argument. */
+int dllm_hip_moe_route(const float* logits, int64_t* indices, float* weights, size_t rows, size_t experts, size_t k,
+                       int normalize, void* stream);
+/* dlogits [rows, experts] from the gradients of the routing weights dweights [rows, k] and (optional, may be NULL)
+ * of the softmax probabilities dprobabilities [rows, experts]. Replaces kernels.cpp:1005-1027
+ * `moe_route_backward` (grad.hpp:507-541). */
+int dllm_hip_moe_route_backward(const float* logits, const int64_t* indices, const float* dweights,
+                                const float* dprobabilities, float* dlogits, size_t rows, size_t experts, size_t k,
+                                int normalize, void* stream);
+
 /* ---- LoRA on a frozen (optionally Q8_0) base ---- */
 
 /* quantize_q8_0 of n values (a multiple of 32): int8 values and one float scale per 32-value block. Replaces
@@ -203,18 +217,24 @@ const char* dllm_hip_trainer_tensor_name(dllm_hip_trainer* trainer, int64_t inde
 
 /* Gradients only (DecoderGradients.losses_and_gradients summed over windows in batch order): tokens is a HOST int64
  * array; window w is tokens[offsets[w] .. offsets[w] + lengths[w]) and predicts its own next tokens (inputs are the
- * first lengths[w] - 1 tokens). scale multiplies the summed cross-entropy; *loss (host) receives the summed loss. */
+ * first lengths[w] - 1 tokens). scale multiplies the summed cross-entropy; *loss (host) receives the summed loss.
+ * router_scale multiplies each window's router load-balancing loss in the gradients (routed experts; backprop.py
+ * 359-377); the summed router loss of the call is read with dllm_hip_trainer_router_loss. */
 int dllm_hip_trainer_gradients(dllm_hip_trainer* trainer, const int64_t* tokens, const int64_t* offsets,
                                const int64_t* lengths, int64_t windows, double scale, double router_scale,
                                double* loss, void* stream);
+/* The router loss summed over the windows of the last gradients or step call (0 for dense models). No counterpart in
+ * the kernel module: it is the second value of losses_and_gradients (backprop.py:88-118) summed as trainer.py:327. */
+int dllm_hip_trainer_router_loss(dllm_hip_trainer* trainer, double* router_loss);
 
 typedef struct {
     double learning_rate, beta1, beta2, eps, weight_decay, max_grad_norm, router_aux_loss;
     int64_t step; /* 1-based number of this update */
 } dllm_hip_adamw;
 
-/* One full step: gradients with scale 1 / (sum of lengths - windows), the global norm, clipping and AdamW in
- * natural tensor order. *loss gets the mean loss, *grad_norm the norm before clipping (host pointers; waits). */
+/* One full step: gradients with scale 1 / (sum of lengths - windows) and router_scale router_aux_loss / windows, the
+ * global norm, clipping and AdamW in natural tensor order. *loss gets the mean loss plus router_aux_loss times the mean
+ * router loss (trainer.py:312-335), *grad_norm the norm before clipping (host pointers; waits). */
 int dllm_hip_trainer_step(dllm_hip_trainer* trainer, const int64_t* tokens, const int64_t* offsets,
                           const int64_t* lengths, int64_t windows, const dllm_hip_adamw* adamw, double* loss,
                           double* grad_norm, void* stream);

@@ -211,3 +211,33 @@ def test_lora_merge_and_adapter_gradients(K, ora, out_f, in_f, rank):
     for got, want, name in zip(K.lora_adapter_gradients(g, a, b, 2.0), O.adapter_gradients(ora, g, a, b, 2.0),
                                ("dA", "dB")):
         assert_same(got, want, name)
+
+
+@pytest.mark.parametrize("rows,experts,k", [(1, 4, 1), (37, 8, 2), (300, 64, 8), (5, 128, 4)])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_moe_route_and_backward(K, ora, rows, experts, k, normalize):
+    """nn.hpp:864-896 and grad.hpp:507-541: Gaussian logits plus rows of exact ties (the lower expert wins) and a row
+    of one large logit; with and without the load-balancing loss's dprobabilities."""
+    logits = O.gaussian(rows * 7 + experts, rows, experts, scale=2.0)
+    if rows > 2:
+        logits[1] = 0.5  # every probability equal
+        logits[2, ::2] = logits[2, 1::2]  # pairs of equal probabilities
+    logits[0, experts // 2] = 40.0
+    ia, wa = K.moe_route(logits, k, normalize)
+    ib, wb = ora.moe_route(logits, k, normalize)
+    assert ia.tobytes() == ib.tobytes()
+    assert_same(wa, wb, "weights")
+    dw = O.gaussian(rows + 3, rows, k)
+    dp = O.gaussian(rows + 4, rows, experts, scale=1e-2)
+    assert_same(K.moe_route_backward(logits, ia, dw, dp, normalize),
+                ora.moe_route_backward(logits, ib, dw, dp, normalize), "dlogits")
+    assert_same(K.moe_route_backward(logits, ia, dw, None, normalize),
+                ora.moe_route_backward(logits, ib, dw, None, normalize), "dlogits without dprobabilities")
+
+
+def test_moe_route_rejects_bad_k(K):
+    with pytest.raises(ValueError):
+        K.moe_route(np.zeros((2, 4), np.float32), 5, False)
+    with pytest.raises(ValueError):
+        K.moe_route_backward(np.zeros((2, 4), np.float32), np.zeros((2, 1), np.int64), np.zeros((2, 2), np.float32),
+                             None, False)

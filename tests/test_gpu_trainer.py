@@ -1,6 +1,6 @@
-"""GPU parity of the device-resident step: the reference's own whole-model goldens (GRADIENT_FINGERPRINT and the
-6-step FINETUNE_FINGERPRINT for the dense tiny fixtures) and bit equality with the oracle's step on a larger
-random model with ragged windows."""
+"""GPU parity of the device-resident step: the reference's own whole-model goldens (GRADIENT_FINGERPRINT, the
+6-step FINETUNE_FINGERPRINT and LORA_FINETUNE_FINGERPRINT for the tiny dense and mixture-of-experts fixtures) and bit
+equality with the oracle's step on larger random models with ragged windows."""
 
 from __future__ import annotations
 
@@ -16,14 +16,14 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_goldens.json").read_text())
 TOKENS = [1, 17, 42, 5, 63, 0, 9, 9, 30]
-DENSE = ["llama", "mistral", "qwen2", "qwen3"]
+FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe"]
 
 
 def gpu_decoder(d: O.Decoder):
     from etalii_dllm_amd.trainer import Decoder
 
     return Decoder(d.vocab, d.hidden, d.inter, d.layers, d.heads, d.kv_heads, d.head_dim, d.eps, d.rope_theta,
-                   d.tied, d.attn_bias, d.qk_norm, d.window)
+                   d.tied, d.attn_bias, d.qk_norm, d.window, d.experts, d.topk, d.normalize, d.expert_inter)
 
 
 def make_trainer(d: O.Decoder, weights, max_tokens=64, max_windows=8, max_window=32):
@@ -35,7 +35,7 @@ def make_trainer(d: O.Decoder, weights, max_tokens=64, max_windows=8, max_window
     return t
 
 
-@pytest.mark.parametrize("family", DENSE)
+@pytest.mark.parametrize("family", FAMILIES)
 def test_gradient_fingerprint_on_gpu(family):
     d = O.FIXTURES[family]
     t = make_trainer(d, O.fixture_weights(d))
@@ -51,7 +51,7 @@ def ascii_windows():
     return O.windows_from_documents(documents, lambda text: [ord(c) % 64 for c in text], 8, 2)
 
 
-@pytest.mark.parametrize("family", DENSE)
+@pytest.mark.parametrize("family", FAMILIES)
 def test_finetune_fingerprint_on_gpu(family):
     d = O.FIXTURES[family]
     windows = ascii_windows()
@@ -100,7 +100,7 @@ def make_lora_trainer(d: O.Decoder, weights, lora: O.Lora, adapters, base_quanti
     return t
 
 
-@pytest.mark.parametrize("family", [f for f in DENSE if f in GOLDEN["LORA_FINETUNE_FINGERPRINT"]])
+@pytest.mark.parametrize("family", [f for f in FAMILIES if f in GOLDEN["LORA_FINETUNE_FINGERPRINT"]])
 def test_lora_finetune_fingerprint_on_gpu(family):
     """The reference's LoRA run (tests/test_lora.py:26-27,151-171) on the GPU; the merged export through the GPU
     merge."""
@@ -158,3 +158,77 @@ def test_lora_step_matches_the_oracle_on_ragged_windows(base_quantize):
             assert t.get(name, a.shape).tobytes() == a.tobytes(), name
             assert t.get(name, a.shape, t.M).tobytes() == m[name].tobytes(), name
             assert t.get(name, a.shape, t.V).tobytes() == v[name].tobytes(), name
+
+
+MOE = {
+    "mixtral": O.Decoder("mixtral", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16,
+                         eps=1e-5, rope_theta=1e6, tied=False, experts=8, topk=2, normalize=True, expert_inter=48),
+    "olmoe": O.Decoder("olmoe", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=4, head_dim=16,
+                       eps=1e-5, rope_theta=1e4, tied=False, qk_norm=2, experts=16, topk=4, normalize=False,
+                       expert_inter=32),
+}
+
+
+@pytest.mark.parametrize("family", sorted(MOE))
+def test_moe_step_matches_the_oracle_on_ragged_windows(family):
+    """Routed experts with the load-balancing loss (router_aux_loss 0.05): two steps over windows of 33, 2, 70 and
+    17 tokens (the 1-row window reaches only topk experts, so most experts get a window of no rows), every gradient,
+    parameter and moment against the oracle; then a 1-row batch in which most experts get no row at all
+    (backprop.py:339-341: their gradients are zero)."""
+    d = MOE[family]
+    weights = O.synthetic_weights(d, seed=11, scale=0.05)
+    rng = O.Random(21)
+    windows = [[rng.next_u64() % d.vocab for _ in range(n)] for n in (33, 2, 70, 17)]
+    t = make_trainer(d, weights, max_tokens=256, max_windows=4, max_window=128)
+    params = {n: a.copy() for n, a in weights.items()}
+    m = {n: np.zeros_like(a) for n, a in params.items()}
+    v = {n: np.zeros_like(a) for n, a in params.items()}
+    opt = O.AdamWConfig(learning_rate=1e-3, schedule="constant")
+    for step in (1, 2):
+        loss_gpu, norm_gpu = t.step(windows, 1e-3, step, router_aux_loss=0.05)
+        loss_cpu, _, norm_cpu, grads = O.train_step(O.oracle_kernels(), d, params, m, v, windows, opt, step, 2,
+                                                    router_aux_loss=0.05)
+        assert loss_gpu == loss_cpu and norm_gpu == norm_cpu
+        for name in t.names:
+            shape = d.tensor_shapes()[name]
+            assert t.get(name, shape, t.GRAD).tobytes() == grads[name].tobytes(), name
+            assert t.get(name, shape).tobytes() == params[name].tobytes(), name
+            assert t.get(name, shape, t.M).tobytes() == m[name].tobytes(), name
+            assert t.get(name, shape, t.V).tobytes() == v[name].tobytes(), name
+    window = windows[0][:2]
+    loss = t.gradients([window], scale=0.5, router_scale=0.25)
+    want_loss, want_router, want = O.window_gradients(O.oracle_kernels(), d, params, window[:1], window[1:],
+                                                      scale=0.5, router_scale=0.25)
+    assert loss == want_loss and t.router_loss() == want_router
+    unreached = 0
+    for name in t.names:
+        got = t.get(name, d.tensor_shapes()[name], t.GRAD)
+        assert got.tobytes() == want[name].tobytes(), name
+        unreached += ".experts." in name and not np.any(got)
+    assert unreached >= 3 * (d.experts - d.topk) * d.layers
+
+
+def test_moe_lora_step_matches_the_oracle():
+    """LoRA on a routed model: gate/up/down adapt every expert's projection, the router is never adapted
+    (lora.py:211-242); two steps against the oracle's LoRA step."""
+    d = MOE["mixtral"]
+    weights = O.synthetic_weights(d, seed=12, scale=0.05)
+    lora = O.Lora(rank=4, alpha=8.0, targets=("q", "o", "gate", "down"))
+    adapters = O.init_adapters(d, lora, 5)
+    for name in adapters:
+        if name.endswith(".lora_b"):
+            adapters[name] = O.gaussian(len(name) + 1, *adapters[name].shape, scale=0.02)
+    rng = O.Random(23)
+    windows = [[rng.next_u64() % d.vocab for _ in range(n)] for n in (20, 41, 3)]
+    t = make_lora_trainer(d, weights, lora, adapters, max_tokens=128, max_windows=4, max_window=64)
+    state = {n: a.copy() for n, a in adapters.items()}
+    m = {n: np.zeros_like(a) for n, a in state.items()}
+    v = {n: np.zeros_like(a) for n, a in state.items()}
+    opt = O.AdamWConfig(learning_rate=1e-3, schedule="constant")
+    for step in (1, 2):
+        loss_gpu, norm_gpu = t.step(windows, 1e-3, step, router_aux_loss=0.1)
+        loss_cpu, norm_cpu = O.lora_train_step(O.oracle_kernels(), d, weights, state, m, v, windows, opt, step, 2,
+                                               lora, router_aux_loss=0.1)
+        assert loss_gpu == loss_cpu and norm_gpu == norm_cpu
+        for name, value in state.items():
+            assert t.get(name, value.shape).tobytes() == value.tobytes(), name
