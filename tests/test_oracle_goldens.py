@@ -92,3 +92,53 @@ def test_lora_finetune_fingerprint(family):
         O.lora_train_step(kern, d, base, adapters, m, v, batch, opt, step + 1, 6, lora)
     merged = O.merged_weights(kern, d, base, adapters, lora)
     assert O.data_fingerprint(merged) == GOLDEN["LORA_FINETUNE_FINGERPRINT"][family]
+
+
+# -- the router load-balancing loss: the reference pins it by formula and finite differences
+#    (tests/test_moe_training.py:141-172); no golden holds it, so the oracle is pinned the same way.
+
+@pytest.mark.parametrize("family", ["mixtral", "olmoe"])
+def test_router_loss_gradient_matches_finite_differences(family):
+    """Scale 0: only the load-balancing loss has a gradient (test_moe_training.py:151-172), through the router of
+    the last layer and, via the routed mixture, a first-layer projection; the final norm gets none."""
+    d = O.FIXTURES[family]
+    weights = {n: a.copy() for n, a in O.fixture_weights(d).items()}
+    kern = O.oracle_kernels()
+    _, _, grads = O.window_gradients(kern, d, weights, TOKENS, TARGETS, scale=0.0, router_scale=1.0)
+    rng = O.Random(3)
+    for name in (f"layers.{d.layers - 1}.mlp.router.weight", "layers.0.attention.q.weight"):
+        index = np.unravel_index(rng.next_u64() % weights[name].size, weights[name].shape)
+        eps = 1e-2
+
+        def at(delta, name=name, index=index):
+            changed = dict(weights)
+            changed[name] = weights[name].copy()
+            changed[name][index] += np.float32(delta)
+            return O.window_gradients(kern, d, changed, TOKENS, TARGETS, scale=0.0, router_scale=1.0)[1]
+
+        numeric = (at(eps) - at(-eps)) / (2 * eps)
+        assert float(grads[name][index]) == pytest.approx(numeric, rel=5e-2, abs=1e-4), name
+    assert not np.any(grads["final_norm.weight"])
+
+
+def test_router_loss_of_a_uniform_router_is_k():
+    """Zero router weights: every probability is 1/E and every row picks experts 0..k-1 (ties to the lower index), so
+    E * sum_e f_e * mean_e = E * k * (1/E) = k, and the gradient row is router_scale * E * f_e / T."""
+    d = O.FIXTURES["mixtral"]
+    weights = {n: (np.zeros_like(a) if n.endswith("router.weight") else a) for n, a in O.fixture_weights(d).items()}
+    _, router_loss, _ = O.window_gradients(O.oracle_kernels(), d, weights, TOKENS, TARGETS, router_scale=0.0)
+    assert router_loss == d.topk
+
+
+def test_experts_no_token_reaches_get_zero_gradients():
+    """test_moe_training.py:103-114: a one-token window routes to topk experts per layer; the others' gradients are
+    exactly zero and the reached ones' are not."""
+    d = O.FIXTURES["mixtral"]
+    weights = O.fixture_weights(d)
+    _, _, grads = O.window_gradients(O.oracle_kernels(), d, weights, [5], [7])
+    for layer in range(d.layers):
+        reached = [e for e in range(d.experts) if np.any(grads[f"layers.{layer}.mlp.experts.{e}.down.weight"])]
+        assert len(reached) == d.topk
+        for e in range(d.experts):
+            for which in ("gate", "up", "down"):
+                assert bool(np.any(grads[f"layers.{layer}.mlp.experts.{e}.{which}.weight"])) == (e in reached)
