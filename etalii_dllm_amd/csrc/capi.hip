@@ -450,6 +450,35 @@ int dllm_hip_adamw_step(float* param, const float* grad, float* m, float* v, siz
     return launch_adamw_plain(param, grad, m, v, static_cast<int64_t>(n), weight_decay, a, as_stream(stream));
 }
 
+int dllm_hip_gelu_tanh_backward(const float* x, const float* dy, float* out, size_t n, void* stream) {
+    return launch_gelu_tanh_backward(x, dy, out, static_cast<int64_t>(n), as_stream(stream));
+}
+
+int dllm_hip_softcap_backward(const float* x, const float* dy, float* out, size_t n, double cap, void* stream) {
+    DLLM_REQUIRE(cap > 0.0, "cap must be positive");
+    return launch_softcap_backward(x, dy, out, static_cast<int64_t>(n), cap, as_stream(stream));
+}
+
+int dllm_hip_softmax(const float* logits, float* out, size_t rows, size_t n, void* stream) {
+    return launch_softmax_rows(logits, out, static_cast<int64_t>(rows), static_cast<int64_t>(n), as_stream(stream));
+}
+
+int dllm_hip_column_mean(const float* x, float* out, size_t rows, size_t cols, void* stream) {
+    return launch_column_mean(x, out, static_cast<int64_t>(rows), static_cast<int64_t>(cols), as_stream(stream));
+}
+
+size_t dllm_hip_dot_workspace(void) { return sizeof(float); }
+
+int dllm_hip_dot(const float* a, const float* b, size_t n, float* result, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+    DLLM_REQUIRE(result && workspace && workspace_bytes >= sizeof(float), "dot needs a result and a workspace");
+    const hipStream_t s = as_stream(stream);
+    float* d = static_cast<float*>(workspace);
+    DLLM_TRY(launch_dot(a, b, static_cast<int64_t>(n), d, s));
+    DLLM_TRY(check_hip(hipMemcpyAsync(result, d, sizeof(float), hipMemcpyDeviceToHost, s), "download"));
+    return check_hip(hipStreamSynchronize(s), "dot");
+}
+
 int dllm_hip_moe_route(const float* logits, int64_t* indices, float* weights, size_t rows, size_t experts, size_t k,
                        int normalize, void* stream) {
     return launch_moe_route(logits, static_cast<int64_t>(rows), static_cast<int64_t>(experts),

@@ -70,6 +70,8 @@ int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream);
 int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
                           hipStream_t stream);
 int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
+int launch_gelu_tanh_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
+int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t n, double cap, hipStream_t stream);
 // _swiglu_backward's elementwise glue (backprop.py:301-303): dgate = silu_backward(gate, dproduct * up),
 // dup = dproduct * gate_act.
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
@@ -98,6 +100,11 @@ int launch_moe_dweights(const float* dout, const float* y, const int64_t* row_of
 int launch_router_stats(const float* probs, int64_t layer_stride, int64_t layers, const int64_t* seg, int nseg,
                         const int64_t* counts, int64_t experts, double router_scale, double* loss, float* grad_row,
                         hipStream_t stream);
+// softmax of each row (math.hpp:387-398), column_mean (interp.hpp:146-155), dot (math.hpp:31-37: one serial chain;
+// result is a device float).
+int launch_softmax_rows(const float* logits, float* out, int64_t rows, int64_t n, hipStream_t stream);
+int launch_column_mean(const float* x, float* out, int64_t rows, int64_t cols, hipStream_t stream);
+int launch_dot(const float* a, const float* b, int64_t n, float* result, hipStream_t stream);
 int launch_broadcast_window_rows(const float* grad_row, const int64_t* seg, int nseg, int64_t rows, int64_t experts,
                                  float* out, hipStream_t stream);
 

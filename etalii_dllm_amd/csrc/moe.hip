@@ -209,6 +209,31 @@ __global__ __launch_bounds__(256) void broadcast_rows_kernel(const float* __rest
     for (int64_t e = threadIdx.x; e < E; e += 256) out[r * E + e] = grad_row[w * E + e];
 }
 
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restrict__ logits, float* __restrict__ out,
+                                                           int64_t rows, int64_t n) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (r >= rows) return;
+    const RowSoftmax s = row_softmax(logits + r * n, n);
+    for (int64_t e = 0; e < n; ++e) out[r * n + e] = row_prob(logits + r * n, s, e);
+}
+
+__global__ __launch_bounds__(256) void column_mean_kernel(const float* __restrict__ x, float* __restrict__ out,
+                                                          int64_t rows, int64_t cols) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (c >= cols) return;
+    double total = 0.0;
+    for (int64_t r = 0; r < rows; ++r) total += static_cast<double>(x[r * cols + c]);
+    out[c] = rows > 0 ? static_cast<float>(total / static_cast<double>(rows)) : 0.0f;
+}
+
+__global__ void dot_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t n,
+                           float* __restrict__ result) {
+    if (threadIdx.x != 0) return;
+    double acc = 0.0;
+    for (int64_t i = 0; i < n; ++i) acc += static_cast<double>(a[i]) * static_cast<double>(b[i]);
+    *result = static_cast<float>(acc);
+}
+
 unsigned row_grid(int64_t rows) { return static_cast<unsigned>(ceil_div(static_cast<size_t>(rows), 256)); }
 
 }  // namespace
@@ -260,6 +285,24 @@ int launch_router_stats(const float* probs, int64_t layer_stride, int64_t layers
                        2 * experts * sizeof(float), stream, probs, layer_stride, layers, seg, counts, experts,
                        router_scale, loss, grad_row);
     return check_launch("router_stats");
+}
+
+int launch_softmax_rows(const float* logits, float* out, int64_t rows, int64_t n, hipStream_t stream) {
+    DLLM_REQUIRE(n >= 1, "softmax needs at least one value");
+    if (rows == 0) return kOk;
+    hipLaunchKernelGGL(softmax_rows_kernel, dim3(row_grid(rows)), dim3(256), 0, stream, logits, out, rows, n);
+    return check_launch("softmax");
+}
+
+int launch_column_mean(const float* x, float* out, int64_t rows, int64_t cols, hipStream_t stream) {
+    if (cols == 0) return kOk;
+    hipLaunchKernelGGL(column_mean_kernel, dim3(row_grid(cols)), dim3(256), 0, stream, x, out, rows, cols);
+    return check_launch("column_mean");
+}
+
+int launch_dot(const float* a, const float* b, int64_t n, float* result, hipStream_t stream) {
+    hipLaunchKernelGGL(dot_kernel, dim3(1), dim3(64), 0, stream, a, b, n, result);
+    return check_launch("dot");
 }
 
 int launch_broadcast_window_rows(const float* grad_row, const int64_t* seg, int nseg, int64_t rows, int64_t experts,

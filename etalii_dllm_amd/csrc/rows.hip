@@ -220,6 +220,29 @@ __global__ __launch_bounds__(256) void silu_backward_kernel(const float* __restr
         out[i] = dsilu_backward(x[i], dy[i]);
 }
 
+// gelu_tanh_backward (grad.hpp:183-191) and softcap_backward (grad.hpp:193-197), elementwise, in double, rounded once.
+__global__ __launch_bounds__(256) void gelu_tanh_backward_kernel(const float* __restrict__ x,
+                                                                 const float* __restrict__ dy, float* __restrict__ out,
+                                                                 int64_t n) {
+    const double c = 7.97884560802865355879e-01;  // sqrt(2 / pi)
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const double d = x[i];
+        const double t = dtanh(c * (d + 0.044715 * d * d * d));
+        const double slope = 0.5 * (1.0 + t) + 0.5 * d * (1.0 - t * t) * c * (1.0 + 3.0 * 0.044715 * d * d);
+        out[i] = static_cast<float>(static_cast<double>(dy[i]) * slope);
+    }
+}
+
+__global__ __launch_bounds__(256) void softcap_backward_kernel(const float* __restrict__ x, const float* __restrict__ dy,
+                                                               float* __restrict__ out, int64_t n, double cap) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const double t = dtanh(static_cast<double>(x[i]) / cap);
+        out[i] = static_cast<float>(static_cast<double>(dy[i]) * (1.0 - t * t));
+    }
+}
+
 __global__ __launch_bounds__(256) void swiglu_backward_kernel(const float* __restrict__ gate,
                                                               const float* __restrict__ up,
                                                               const float* __restrict__ gate_act,
@@ -332,6 +355,18 @@ int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n,
     if (n == 0) return kOk;
     hipLaunchKernelGGL(silu_backward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, dy, out, n);
     return check_launch("silu_backward");
+}
+
+int launch_gelu_tanh_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(gelu_tanh_backward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, dy, out, n);
+    return check_launch("gelu_tanh_backward");
+}
+
+int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t n, double cap, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(softcap_backward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, dy, out, n, cap);
+    return check_launch("softcap_backward");
 }
 
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,

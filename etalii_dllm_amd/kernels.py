@@ -68,6 +68,13 @@ def _load() -> C.CDLL:
     lib.dllm_hip_sum_squares_workspace.restype = _sz
     lib.dllm_hip_sum_squares_workspace.argtypes = [_sz]
     lib.dllm_hip_adamw_step.argtypes = [_vp, _vp, _vp, _vp, _sz] + [C.c_double] * 8 + [_vp]
+    lib.dllm_hip_gelu_tanh_backward.argtypes = [_vp, _vp, _vp, _sz, _vp]
+    lib.dllm_hip_softcap_backward.argtypes = [_vp, _vp, _vp, _sz, C.c_double, _vp]
+    lib.dllm_hip_softmax.argtypes = [_vp, _vp, _sz, _sz, _vp]
+    lib.dllm_hip_column_mean.argtypes = [_vp, _vp, _sz, _sz, _vp]
+    lib.dllm_hip_dot_workspace.restype = _sz
+    lib.dllm_hip_dot_workspace.argtypes = []
+    lib.dllm_hip_dot.argtypes = [_vp, _vp, _sz, C.POINTER(C.c_float), _vp, _sz, _vp]
     lib.dllm_hip_moe_route.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp]
     lib.dllm_hip_moe_route_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp]
     lib.dllm_hip_quantize_q8_0.argtypes = [_vp, _vp, _vp, _sz, _vp]
@@ -369,6 +376,60 @@ def adamw_step(param, grad, m, v, lr, beta1, beta2, eps, weight_decay, bias_corr
 
 
 # ---- LoRA and Q8_0 (src/etalii_dllm/lora.py, numerics.py:106-139) ----
+
+def gelu_tanh_backward(x, dy) -> np.ndarray:
+    """kernels.cpp:903-914."""
+    x, dy = _f32(x), _f32(dy)
+    if x.size != dy.size:
+        raise ValueError("x and dy must have the same size")
+    dx, ddy, out = Device.of(x), Device.of(dy), Device(x.nbytes)
+    check(lib.dllm_hip_gelu_tanh_backward(dx.ptr, ddy.ptr, out.ptr, x.size, None))
+    return out.download(x.shape)
+
+
+def softcap_backward(x, dy, cap: float) -> np.ndarray:
+    """kernels.cpp:916-928."""
+    x, dy = _f32(x), _f32(dy)
+    if x.size != dy.size:
+        raise ValueError("x and dy must have the same size")
+    if not cap > 0.0:
+        raise ValueError("cap must be positive")
+    dx, ddy, out = Device.of(x), Device.of(dy), Device(x.nbytes)
+    check(lib.dllm_hip_softcap_backward(dx.ptr, ddy.ptr, out.ptr, x.size, float(cap), None))
+    return out.download(x.shape)
+
+
+def softmax(logits) -> np.ndarray:
+    """kernels.cpp:166-176 (a vector; a matrix is taken row by row)."""
+    x = _f32(logits)
+    if x.size == 0:
+        raise ValueError("softmax needs at least one value")
+    n = x.shape[-1]
+    d, out = Device.of(x), Device(x.nbytes)
+    check(lib.dllm_hip_softmax(d.ptr, out.ptr, x.size // n, n, None))
+    return out.download(x.shape)
+
+
+def column_mean(x) -> np.ndarray:
+    """kernels.cpp:787-796."""
+    x = _f32(x)
+    if x.ndim != 2:
+        raise ValueError("x must be [rows, cols]")
+    d, out = Device.of(x), Device(max(x.shape[1], 1) * 4)
+    check(lib.dllm_hip_column_mean(d.ptr, out.ptr, x.shape[0], x.shape[1], None))
+    return out.download((x.shape[1],))
+
+
+def dot(a, b) -> float:
+    """kernels.cpp:153-161: a float (returned as a Python float, as the binding does)."""
+    a, b = _f32(a).ravel(), _f32(b).ravel()
+    if a.size != b.size:
+        raise ValueError("vectors must have the same length")
+    da, db, ws = Device.of(a), Device.of(b), Device(lib.dllm_hip_dot_workspace())
+    result = C.c_float()
+    check(lib.dllm_hip_dot(da.ptr, db.ptr, a.size, C.byref(result), ws.ptr, ws.nbytes, None))
+    return float(result.value)
+
 
 def moe_route(logits, k: int, normalize: bool) -> tuple[np.ndarray, np.ndarray]:
     """kernels.cpp:190-204: (indices int64 [rows, k], weights [rows, k]) in rank order."""

@@ -90,6 +90,11 @@ int dllm_hip_rms_norm_backward(const float* x, const float* weight, const float*
 
 /* dy * silu'(x) elementwise. Replaces kernels.cpp:890-901 `silu_backward` (grad.hpp:177-181). */
 int dllm_hip_silu_backward(const float* x, const float* dy, float* out, size_t n, void* stream);
+/* dy * gelu_tanh'(x) elementwise. Replaces kernels.cpp:903-914 `gelu_tanh_backward` (grad.hpp:183-191). */
+int dllm_hip_gelu_tanh_backward(const float* x, const float* dy, float* out, size_t n, void* stream);
+/* dy * softcap'(x) = dy (1 - tanh(x / cap)^2) elementwise; cap > 0. Replaces kernels.cpp:916-928
+ * `softcap_backward` (grad.hpp:193-197). */
+int dllm_hip_softcap_backward(const float* x, const float* dy, float* out, size_t n, double cap, void* stream);
 
 /* (dq, dk, dv) of attention. Replaces kernels.cpp:930-959 `attention_backward` (grad.hpp:206-301). */
 size_t dllm_hip_attention_backward_workspace(size_t q_len, size_t kv_len, size_t q_heads);
@@ -138,6 +143,18 @@ int dllm_hip_moe_route(const float* logits, int64_t* indices, float* weights, si
 int dllm_hip_moe_route_backward(const float* logits, const int64_t* indices, const float* dweights,
                                 const float* dprobabilities, float* dlogits, size_t rows, size_t experts, size_t k,
                                 int normalize, void* stream);
+
+/* softmax of each of rows vectors of n logits (rows = 1 is the binding). Replaces kernels.cpp:166-176 `softmax`
+ * (math.hpp:387-398). */
+int dllm_hip_softmax(const float* logits, float* out, size_t rows, size_t n, void* stream);
+/* out[c] = f32(sum over rows ascending of x[r][c] in double / rows). Replaces kernels.cpp:787-796 `column_mean`
+ * (interp.hpp:146-155). */
+int dllm_hip_column_mean(const float* x, float* out, size_t rows, size_t cols, void* stream);
+/* *result (HOST) = f32(sum over i ascending of a[i] b[i] in double); waits. The workspace holds one float
+ * (dllm_hip_dot_workspace). Replaces kernels.cpp:153-161 `dot` (math.hpp:31-37). */
+size_t dllm_hip_dot_workspace(void);
+int dllm_hip_dot(const float* a, const float* b, size_t n, float* result, void* workspace, size_t workspace_bytes,
+                 void* stream);
 
 /* ---- LoRA on a frozen (optionally Q8_0) base ---- */
 

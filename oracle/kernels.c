@@ -473,6 +473,22 @@ float orc_silu_backward(float x, float dy) {
     return (float)((double)dy * s * (1.0 + d * (1.0 - s)));
 }
 
+/* gelu_tanh_backward (grad.hpp:183-191): u = sqrt(2/pi) (x + 0.044715 x^3), t = tanh(u), dy times
+ * 0.5 (1 + t) + 0.5 x (1 - t^2) sqrt(2/pi) (1 + 3 0.044715 x^2), in double, rounded once. */
+float orc_gelu_tanh_backward(float x, float dy) {
+    const double c = 7.97884560802865355879e-01; /* sqrt(2 / pi) */
+    const double d = x;
+    const double t = orc_tanh(c * (d + 0.044715 * d * d * d));
+    const double slope = 0.5 * (1.0 + t) + 0.5 * d * (1.0 - t * t) * c * (1.0 + 3.0 * 0.044715 * d * d);
+    return (float)((double)dy * slope);
+}
+
+/* softcap_backward (grad.hpp:193-197): dy (1 - tanh(x / cap)^2), rounded once. */
+float orc_softcap_backward(float x, float dy, double cap) {
+    const double t = orc_tanh((double)x / cap);
+    return (float)((double)dy * (1.0 - t * t));
+}
+
 /* attention_backward (grad.hpp:206-301): rows (t ascending, then h ascending) recompute p exactly, then dq per row and
  * the key/value gradients as double accumulators visited in (t, h) order. */
 void orc_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,

@@ -60,6 +60,8 @@ void orc_linear_backward(const float* x, const float* w, const float* dy, float*
 void orc_rms_norm_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, size_t rows,
                            size_t dim, double eps, int unit_offset);     /* grad.hpp:79-111 */
 float orc_silu_backward(float x, float dy);                              /* grad.hpp:177-181 */
+float orc_gelu_tanh_backward(float x, float dy);                         /* grad.hpp:183-191 */
+float orc_softcap_backward(float x, float dy, double cap);               /* grad.hpp:193-197 */
 void orc_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,
                             float* dv, size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads,
                             size_t head_dim, size_t value_dim, double scale, int causal, size_t q_offset,

@@ -139,6 +139,8 @@ double ref_tanh(double x) { FpEnvGuard g; return dllm::tanh(x); }
 double ref_sigmoid(double x) { FpEnvGuard g; return dllm::sigmoid(x); }
 float ref_silu(float x) { FpEnvGuard g; return dllm::silu(x); }
 float ref_silu_backward(float x, float dy) { FpEnvGuard g; return dllm::silu_backward(x, dy); }
+float ref_gelu_tanh_backward(float x, float dy) { FpEnvGuard g; return dllm::gelu_tanh_backward(x, dy); }
+float ref_softcap_backward(float x, float dy, double cap) { FpEnvGuard g; return dllm::softcap_backward(x, dy, cap); }
 
 void ref_fill_gaussian(uint64_t seed, float* out, size_t n) {
     dllm::Random r(seed);

@@ -62,6 +62,10 @@ def oracle() -> C.CDLL:
         lib.orc_silu.argtypes = [C.c_float]
         lib.orc_silu_backward.restype = C.c_float
         lib.orc_silu_backward.argtypes = [C.c_float, C.c_float]
+        lib.orc_gelu_tanh_backward.restype = C.c_float
+        lib.orc_gelu_tanh_backward.argtypes = [C.c_float, C.c_float]
+        lib.orc_softcap_backward.restype = C.c_float
+        lib.orc_softcap_backward.argtypes = [C.c_float, C.c_float, C.c_double]
         lib.orc_random_next.restype = C.c_uint64
         lib.orc_window_gradients.argtypes = [C.c_void_p, C.POINTER(OrcConfig), C.POINTER(_f32p), _i64p, _i64p,
                                              C.c_int64, C.c_double, C.c_double, C.POINTER(_f32p), _f64p, _f64p]
@@ -88,6 +92,10 @@ def ref() -> C.CDLL:
         lib.ref_silu.argtypes = [C.c_float]
         lib.ref_silu_backward.restype = C.c_float
         lib.ref_silu_backward.argtypes = [C.c_float, C.c_float]
+        lib.ref_gelu_tanh_backward.restype = C.c_float
+        lib.ref_gelu_tanh_backward.argtypes = [C.c_float, C.c_float]
+        lib.ref_softcap_backward.restype = C.c_float
+        lib.ref_softcap_backward.argtypes = [C.c_float, C.c_float, C.c_double]
         lib.ref_random_first.restype = C.c_uint64
         lib.ref_random_first.argtypes = [C.c_uint64]
         lib.ref_threads.restype = C.c_size_t
@@ -744,3 +752,16 @@ def q8_0_cases() -> dict[str, np.ndarray]:
     special[96:128] = 0.0
     cases["special"] = special
     return cases
+
+
+def gelu_tanh_backward(x, dy) -> np.ndarray:
+    """The oracle's gelu_tanh_backward (grad.hpp:183-191), elementwise."""
+    f = oracle().orc_gelu_tanh_backward
+    return np.array([f(float(a), float(b)) for a, b in zip(np.ravel(x), np.ravel(dy))], np.float32).reshape(np.shape(x))
+
+
+def softcap_backward(x, dy, cap: float) -> np.ndarray:
+    """The oracle's softcap_backward (grad.hpp:193-197), elementwise."""
+    f = oracle().orc_softcap_backward
+    return np.array([f(float(a), float(b), cap) for a, b in zip(np.ravel(x), np.ravel(dy))],
+                    np.float32).reshape(np.shape(x))

@@ -241,3 +241,32 @@ def test_moe_route_rejects_bad_k(K):
     with pytest.raises(ValueError):
         K.moe_route_backward(np.zeros((2, 4), np.float32), np.zeros((2, 1), np.int64), np.zeros((2, 2), np.float32),
                              None, False)
+
+
+def test_gelu_tanh_and_softcap_backward(K):
+    x = np.concatenate([O.gaussian(41, 3000, scale=3.0), adversarial(42, 1000),
+                        np.array([0.0, -0.0, 20.0, -20.0, 1e4, np.inf, -np.inf, np.nan], np.float32)])
+    dy = O.gaussian(43, x.size)
+
+    def same_up_to_nan_bits(a, b, what):  # a NaN the hardware generates has no defined sign or payload
+        nan = np.isnan(a)
+        assert np.array_equal(nan, np.isnan(b)), what
+        assert_same(np.where(nan, 0, a), np.where(nan, 0, b), what)
+
+    same_up_to_nan_bits(K.gelu_tanh_backward(x, dy), O.gelu_tanh_backward(x, dy), "gelu_tanh_backward")
+    for cap in (30.0, 50.0, 0.5):
+        same_up_to_nan_bits(K.softcap_backward(x, dy, cap), O.softcap_backward(x, dy, cap), f"softcap {cap}")
+    with pytest.raises(ValueError):
+        K.softcap_backward(x, dy, 0.0)
+
+
+def test_softmax_column_mean_and_dot(K, ora):
+    logits = O.gaussian(44, 9, 301, scale=4.0)
+    logits[3] = 1.5
+    for row in logits:
+        assert_same(K.softmax(row), ora.softmax(row.copy()), "softmax")
+    assert_same(K.softmax(logits), np.stack([ora.softmax(r.copy()) for r in logits]), "softmax rows")
+    x = adversarial(45, 1000, 7)
+    assert_same(K.column_mean(x), ora.column_mean(x), "column_mean")
+    a, b = adversarial(46, 5000), O.gaussian(47, 5000)
+    assert K.dot(a, b) == ora.dot(a, b)

@@ -286,3 +286,31 @@ def test_q8_0_round_trips_values_on_its_grid():
     q, s = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, x)
     assert np.all(s == d) and np.array_equal(q.astype(np.float32), k.ravel())
     assert O.dequantize_q8_0(q, s).tobytes() == x.tobytes()
+
+
+def test_gelu_tanh_and_softcap_backward_match_reference():
+    """grad.hpp:183-197 against the compiled reference, on Gaussians, large magnitudes and special values."""
+    if not O.reference_available():
+        pytest.skip("oracle/_ref not built")
+    r = O.ref()
+    x = np.concatenate([O.gaussian(31, 400, scale=3.0), adversarial(32, 200),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0, 1e4, np.inf, -np.inf, np.nan], np.float32)])
+    dy = O.gaussian(33, x.size)
+    want = np.array([r.ref_gelu_tanh_backward(float(a), float(b)) for a, b in zip(x, dy)], np.float32)
+    assert same(O.gelu_tanh_backward(x, dy), want)
+    for cap in (30.0, 50.0, 0.5):
+        want = np.array([r.ref_softcap_backward(float(a), float(b), cap) for a, b in zip(x, dy)], np.float32)
+        assert same(O.softcap_backward(x, dy, cap), want)
+
+
+def test_gelu_tanh_and_softcap_backward_match_numeric_gradients():
+    x = O.gaussian(34, 64, scale=2.0).astype(np.float64)
+    h = 1e-4
+    c = np.sqrt(2.0 / np.pi)
+    gelu = lambda v: 0.5 * v * (1.0 + np.tanh(c * (v + 0.044715 * v ** 3)))  # noqa: E731
+    close(O.gelu_tanh_backward(x.astype(np.float32), np.ones(64, np.float32)),
+          (gelu(x.astype(np.float32).astype(np.float64) + h) - gelu(x.astype(np.float32).astype(np.float64) - h)) / (2 * h), 1e-6)
+    cap = 5.0
+    soft = lambda v: cap * np.tanh(v / cap)  # noqa: E731
+    xf = x.astype(np.float32).astype(np.float64)
+    close(O.softcap_backward(x.astype(np.float32), np.ones(64, np.float32), cap), (soft(xf + h) - soft(xf - h)) / (2 * h), 1e-6)
