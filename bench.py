@@ -37,8 +37,19 @@ CONFIGS = {
     "c1": dict(name="SmolLM2-135M", vocab=49152, hidden=576, intermediate=1536, layers=30, heads=9, kv_heads=3,
                head_dim=64, rms_norm_eps=1e-5, rope_theta=1e5, tie_embeddings=True, attention_bias=False,
                batch=4, seq=256),
+    # LoRA (rank 16, alpha 32, q k v o gate up down; A ~ N(0, 0.02), B = 0) on a Q8_0 base
+    "c4": dict(name="Qwen3-0.6B LoRA on a Q8_0 base", vocab=151936, hidden=1024, intermediate=3072, layers=28,
+               heads=16, kv_heads=8, head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6, tie_embeddings=True,
+               attention_bias=False, qk_norm=1, batch=8, seq=2048,
+               lora=dict(rank=16, alpha=32.0, targets=("q", "k", "v", "o", "gate", "up", "down"))),
+    # routed experts with the load-balancing loss (router_aux_loss 0.01)
+    "c5": dict(name="OLMoE-1B-7B", vocab=50304, hidden=2048, intermediate=1024, layers=16, heads=16, kv_heads=16,
+               head_dim=128, rms_norm_eps=1e-5, rope_theta=1e4, tie_embeddings=False, attention_bias=False,
+               qk_norm=2, experts=64, experts_per_token=8, normalize_expert_weights=False, expert_intermediate=1024,
+               router_aux_loss=0.01, batch=4, seq=2048),
 }
 
+METRIC = "finetune tokens/s, Qwen2.5-1.5B fp32 step, bit-exact vs CPU; % of roofline"
 SEED = 0
 LEARNING_RATE = 1e-4  # schedule "constant", betas 0.9 / 0.999, eps 1e-8, weight decay 0.01, max_grad_norm 1.0
 
@@ -77,18 +88,42 @@ def init_weights(trainer, lib, shapes: dict[str, tuple[int, ...]]) -> None:
 def tensor_shapes(cfg) -> dict[str, tuple[int, ...]]:
     H, q, kv, inter = cfg["hidden"], cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"], cfg["intermediate"]
     shapes = {"token_embedding.weight": (cfg["vocab"], H), "final_norm.weight": (H,)}
+    experts, ei = cfg.get("experts", 0), cfg.get("expert_intermediate", 0) or inter
     for i in range(cfg["layers"]):
         p = f"layers.{i}."
         shapes.update({p + "attention_norm.weight": (H,), p + "attention.q.weight": (q, H),
                        p + "attention.k.weight": (kv, H), p + "attention.v.weight": (kv, H),
-                       p + "attention.o.weight": (H, q), p + "mlp_norm.weight": (H,),
-                       p + "mlp.gate.weight": (inter, H), p + "mlp.up.weight": (inter, H),
-                       p + "mlp.down.weight": (H, inter)})
+                       p + "attention.o.weight": (H, q), p + "mlp_norm.weight": (H,)})
+        if experts:
+            shapes[p + "mlp.router.weight"] = (experts, H)
+            for e in range(experts):
+                x = f"{p}mlp.experts.{e}."
+                shapes.update({x + "gate.weight": (ei, H), x + "up.weight": (ei, H), x + "down.weight": (H, ei)})
+        else:
+            shapes.update({p + "mlp.gate.weight": (inter, H), p + "mlp.up.weight": (inter, H),
+                           p + "mlp.down.weight": (H, inter)})
+        if cfg.get("qk_norm"):
+            per_head = cfg["qk_norm"] == 1
+            shapes.update({p + "attention.q_norm.weight": (cfg["head_dim"] if per_head else q,),
+                           p + "attention.k_norm.weight": (cfg["head_dim"] if per_head else kv,)})
         if cfg["attention_bias"]:
             shapes.update({p + "attention.q.bias": (q,), p + "attention.k.bias": (kv,), p + "attention.v.bias": (kv,)})
     if not cfg["tie_embeddings"]:
         shapes["lm_head.weight"] = (cfg["vocab"], H)
     return shapes
+
+
+def init_adapters(trainer, lib, cfg) -> None:
+    """LoRA adapters: A = fill_gaussian(SEED * 1000 + 500000 + i) * 0.02f (i its index among the adapters in
+    natural order), B = 0."""
+    names = sorted((n for n in trainer.names if n.endswith((".lora_a", ".lora_b"))), key=natural_key)
+    for i, name in enumerate(names):
+        ptr, numel = trainer._tensor(name, trainer.PARAM)
+        values = np.zeros(numel, np.float32)
+        if name.endswith(".lora_a"):
+            assert lib.dllm_hip_fill_gaussian(C.c_uint64(SEED * 1000 + 500000 + i), values.ctypes.data_as(C.c_void_p),
+                                              C.c_size_t(numel), C.c_float(0.02)) == 0
+        trainer.set(name, values)
 
 
 def make_windows(lib, cfg, step: int) -> list[list[int]]:
@@ -102,10 +137,15 @@ def make_windows(lib, cfg, step: int) -> list[list[int]]:
 
 
 def matmul_flops_per_step(cfg) -> float:
-    """Algorithmic matmul work of one step: 6 x matmul parameters x tokens (forward, dX, dW)."""
+    """Algorithmic matmul work of one step: 6 x matmul parameters a token passes through x tokens (forward, dX, dW);
+    a routed layer counts its router and experts_per_token experts."""
     H, q, kv, inter, V = (cfg["hidden"], cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"],
                           cfg["intermediate"], cfg["vocab"])
-    per_layer = H * q * 2 + H * kv * 2 + 3 * H * inter
+    if cfg.get("experts"):
+        mlp = cfg["experts"] * H + cfg["experts_per_token"] * 3 * H * (cfg.get("expert_intermediate") or inter)
+    else:
+        mlp = 3 * H * inter
+    per_layer = H * q * 2 + H * kv * 2 + mlp
     params = cfg["layers"] * per_layer + V * H
     return 6.0 * params * cfg["batch"] * cfg["seq"]
 
@@ -128,15 +168,19 @@ def cpu_baseline(cfg) -> dict | None:
         O.ref().ref_set_threads(C.c_size_t(cores))
     else:
         kern = O.oracle_kernels()
-    T, V, H = cfg["seq"], cfg["vocab"], cfg["hidden"]
+    T, V, H = min(cfg["seq"], 1024), cfg["vocab"], cfg["hidden"]
     small = O.Decoder("sample", vocab=4096, hidden=H, inter=cfg["intermediate"], layers=1, heads=cfg["heads"],
                       kv_heads=cfg["kv_heads"], head_dim=cfg["head_dim"], eps=cfg["rms_norm_eps"],
-                      rope_theta=cfg["rope_theta"], tied=cfg["tie_embeddings"], attn_bias=cfg["attention_bias"])
+                      rope_theta=cfg["rope_theta"], tied=cfg["tie_embeddings"], attn_bias=cfg["attention_bias"],
+                      qk_norm=cfg.get("qk_norm", 0), experts=cfg.get("experts", 0),
+                      topk=cfg.get("experts_per_token", 0), normalize=cfg.get("normalize_expert_weights", False),
+                      expert_inter=cfg.get("expert_intermediate", 0))
     weights = O.synthetic_weights(small, seed=SEED, scale=0.02)
     rng = O.Random(SEED)
     tokens = [rng.next_u64() % small.vocab for _ in range(T + 1)]
     t0 = time.perf_counter()
-    O.window_gradients(kern, small, weights, tokens[:-1], tokens[1:], scale=1.0 / T)
+    O.window_gradients(kern, small, weights, tokens[:-1], tokens[1:], scale=1.0 / T,
+                       router_scale=cfg.get("router_aux_loss", 0.0) / cfg["batch"])
     t_window = time.perf_counter() - t0
     hidden = O.gaussian(SEED + 1, T, H)
     head = O.gaussian(SEED + 2, 8192, H, scale=0.02)
@@ -154,15 +198,21 @@ def cpu_baseline(cfg) -> dict | None:
     kern.adamw_step(p, g, m, v, 1e-4, 0.9, 0.999, 1e-8, 0.01, 0.1, 0.001, 1.0)
     t_opt = time.perf_counter() - t0
     params = sum(int(np.prod(s)) for s in tensor_shapes(cfg).values())
+    if "lora" in cfg:  # AdamW runs over the adapters only
+        q, kv, inter = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"], cfg["intermediate"]
+        params = cfg["layers"] * cfg["lora"]["rank"] * (2 * (H + q) + 2 * (H + kv) + 3 * (H + inter))
+    stretch = cfg["seq"] / T  # a window longer than the sample: linear in tokens (understates the attention)
     layer = t_window - t_head * 4096 / 8192
-    step = cfg["batch"] * (cfg["layers"] * layer + t_head * V / 8192) + t_opt * params / n
-    tokens_per_step = cfg["batch"] * T
+    step = cfg["batch"] * stretch * (cfg["layers"] * layer + t_head * V / 8192) + t_opt * params / n
+    tokens_per_step = cfg["batch"] * cfg["seq"]
     return {
         "value": tokens_per_step / step,
         "unit": "tokens/s",
         "cores": cores,
         "kind": kind,
         "sample": (f"1-layer {cfg['name']}-shaped model, 1 window x {T} tokens, vocab 4096 ({t_window:.2f} s); "
+                   + (f"scaled linearly to {cfg['seq']}-token windows; " if stretch != 1 else "")
+                   + ("the base's gradients stand for the LoRA step; " if "lora" in cfg else "") +
                    f"head at 8192 vocab rows ({t_head:.2f} s); optimizer on 16M params ({t_opt:.2f} s); "
                    f"scaled to {cfg['layers']} layers, vocab {V}, batch {cfg['batch']}, {params} params: "
                    f"{step:.1f} s per step (extrapolated)"),
@@ -247,23 +297,34 @@ def main() -> int:
                                                   C.POINTER(C.c_double)]
     decoder = Decoder(cfg["vocab"], cfg["hidden"], cfg["intermediate"], cfg["layers"], cfg["heads"], cfg["kv_heads"],
                       cfg["head_dim"], cfg["rms_norm_eps"], cfg["rope_theta"], cfg["tie_embeddings"],
-                      cfg["attention_bias"])
+                      cfg["attention_bias"], cfg.get("qk_norm", 0), 0, cfg.get("experts", 0),
+                      cfg.get("experts_per_token", 0), cfg.get("normalize_expert_weights", False),
+                      cfg.get("expert_intermediate", 0))
+    lora = None
+    if "lora" in cfg:
+        from etalii_dllm_amd.trainer import lora_config
+
+        lora = lora_config(cfg["lora"]["rank"], cfg["lora"]["alpha"], cfg["lora"]["targets"], base_quantize="q8_0")
+    router_aux = cfg.get("router_aux_loss", 0.0)
     tokens_per_step = cfg["batch"] * cfg["seq"]
     log(f"creating trainer for {cfg['name']} ({tokens_per_step} tokens per step)")
     t0 = time.perf_counter()
-    trainer = Trainer(decoder, tokens_per_step, cfg["batch"], cfg["seq"])
+    trainer = Trainer(decoder, tokens_per_step, cfg["batch"], cfg["seq"], lora=lora)
     init_weights(trainer, lib, tensor_shapes(cfg))
+    if lora is not None:
+        init_adapters(trainer, lib, cfg)
     log(f"weights ready in {time.perf_counter() - t0:.1f} s")
     windows = [make_windows(lib, cfg, s) for s in range(args.warmup + args.steps)]
     for s in range(args.warmup):
         t1 = time.perf_counter()
-        loss, norm = trainer.step(windows[s], LEARNING_RATE, s + 1)
+        loss, norm = trainer.step(windows[s], LEARNING_RATE, s + 1, router_aux_loss=router_aux)
         log(f"warmup step {s + 1}: loss {loss:.6f} norm {norm:.6f} ({time.perf_counter() - t1:.2f} s)")
     check(lib.dllm_hip_synchronize())
     check(lib.dllm_hip_trainer_profile(trainer.handle, 1))
     t0 = time.perf_counter()
     for s in range(args.steps):
-        loss, norm = trainer.step(windows[args.warmup + s], LEARNING_RATE, args.warmup + s + 1)
+        loss, norm = trainer.step(windows[args.warmup + s], LEARNING_RATE, args.warmup + s + 1,
+                                  router_aux_loss=router_aux)
         log(f"step {args.warmup + s + 1}: loss {loss:.6f} norm {norm:.6f}")
     check(lib.dllm_hip_synchronize())
     elapsed = time.perf_counter() - t0
@@ -285,7 +346,7 @@ def main() -> int:
         log("timing the reference CPU path on a bounded sample")
         baseline = cpu_baseline(cfg)
     result = {
-        "metric": "finetune tokens/s, Qwen2.5-1.5B fp32 step, bit-exact vs CPU; % of roofline",
+        "metric": METRIC if args.config == "c3" else f"finetune tokens/s, {cfg['name']} fp32 step, bit-exact vs CPU",
         "value": tokens_per_step * args.steps / elapsed,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -297,7 +358,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f64",
         "data": "synthetic (seeded Gaussian weights x 0.02, uniform random token ids)",
-        "config": {"workload": f"{cfg['name']} full fine-tune step (forward, backward, global-norm clip, AdamW)",
+        "config": {"workload": f"{cfg['name']} " + ("LoRA step (forward, backward, adapter gradients, global-norm "
+                                                     "clip, AdamW on the adapters)" if lora is not None else
+                                                     "full fine-tune step (forward, backward, global-norm clip, AdamW)"),
                    "global_batch": cfg["batch"], "seq_len": cfg["seq"], "parallelism": "single GPU",
                    "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
