@@ -357,15 +357,33 @@ __device__ __forceinline__ int64_t xcd_contiguous(int64_t hw, int64_t n) {
 
 enum LdsMode { kPlain = 0, kWindowsInSequence = 1, kWindowsInParallel = 2 };
 
-template <int kMode, int kA>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_lds_kernel(GemmParams p,
-                                                                                                   int64_t gx,
-                                                                                                   int64_t gy,
-                                                                                                   int64_t gz) {
+// Grouped launches (kGrouped): one grid over the tiles of several independent matmuls (the experts of a layer); gx
+// is then the total tile count, and a workgroup finds its matmul in the ascending tile_start table and reads that
+// matmul's parameters from `groups`. The tiles of one matmul are numbered exactly as in its own launch.
+template <int kMode, int kA, bool kGrouped = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_lds_kernel(
+    GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmParams* __restrict__ groups,
+    const int64_t* __restrict__ tile_start, int ngroups) {
     __shared__ Stage<kA> st[2];
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int lane = static_cast<int>(threadIdx.x) & 63;
-    const int64_t id = xcd_contiguous(blockIdx.x, gx * gy * gz);
+    int64_t id;
+    if constexpr (kGrouped) {
+        id = xcd_contiguous(blockIdx.x, gx);
+        int lo = 0, hi = ngroups - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (tile_start[mid] <= id) lo = mid;
+            else hi = mid - 1;
+        }
+        p = groups[lo];
+        id -= tile_start[lo];
+        gx = (p.J + kTileJ - 1) / kTileJ;
+        gy = (p.I + kBlockI - 1) / kBlockI;
+        gz = 1;
+    } else {
+        id = xcd_contiguous(blockIdx.x, gx * gy * gz);
+    }
     // groups of kGroupRows row blocks x all column blocks, column-major inside a group: an XCD's resident
     // workgroups cover about 8 x 12 tiles and share their A and B stages through its L2
     const int64_t t = id % (gx * gy), bz = id / (gx * gy);
@@ -485,6 +503,77 @@ __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restr
 
 int64_t padded_rows(int64_t n) { return static_cast<int64_t>(round_up(static_cast<size_t>(n > 0 ? n : 1), kBlockI)); }
 
+namespace {
+
+GemmParams params_of(const GemmCall& g) {
+    return GemmParams{g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.I, g.J, g.l0, g.l1, g.seg, g.nseg, g.bias, g.addsrc,
+                      g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af};
+}
+
+}  // namespace
+
+size_t gemm_group_bytes(int n) {
+    return round_up(sizeof(GemmParams) * static_cast<size_t>(n), 8) + sizeof(int64_t) * (static_cast<size_t>(n) + 1);
+}
+
+int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_table, GemmGroup* group) {
+    DLLM_REQUIRE(n >= 1 && n <= capacity, "a matmul group needs between one and `capacity` matmuls");
+    const int ak = calls[0].a_kind;
+    const bool seg = calls[0].seg != nullptr;
+    DLLM_REQUIRE(ak == kAFloatRows || ak == kAFloatT, "grouped matmuls read float A operands");
+    GemmParams* ps = static_cast<GemmParams*>(host_table);
+    int64_t* starts = reinterpret_cast<int64_t*>(static_cast<char*>(host_table) +
+                                                 round_up(sizeof(GemmParams) * static_cast<size_t>(capacity), 8));
+    int64_t tiles = 0;
+    int used = 0;
+    for (int k = 0; k < n; ++k) {
+        const GemmCall& g = calls[k];
+        DLLM_REQUIRE(g.a_kind == ak && (g.seg != nullptr) == seg, "the matmuls of a group share their mode");
+        DLLM_REQUIRE(g.seg_addrow == nullptr && g.seg_partial == nullptr, "grouped matmuls take no window addends");
+        DLLM_REQUIRE(g.J % 4 == 0 && g.ldb % 4 == 0 && reinterpret_cast<uintptr_t>(g.B) % 16 == 0,
+                     "float A operands need B rows of whole 16-byte chunks");
+        DLLM_REQUIRE(g.lda % 4 == 0 && reinterpret_cast<uintptr_t>(g.Af) % 16 == 0,
+                     "float A rows must be 16-byte aligned");
+        if (ak == kAFloatRows) DLLM_REQUIRE(g.I % 4 == 0 && g.lda >= g.I, "float A rows must hold whole chunks of I");
+        if (ak == kAFloatT)
+            DLLM_REQUIRE(!seg && g.l0 == 0 && g.l1 % 4 == 0 && g.l1 >= 4 && g.lda >= g.l1,
+                         "transposed float A needs a plain reduction over whole 16-byte chunks");
+        if (g.I == 0 || g.J == 0) continue;
+        ps[used] = params_of(g);
+        starts[used] = tiles;
+        tiles += static_cast<int64_t>(ceil_div(g.J, kTileJ) * ceil_div(g.I, kBlockI));
+        ++used;
+    }
+    starts[used] = tiles;
+    DLLM_REQUIRE(tiles < (int64_t{1} << 31), "matmul group too large for one launch");
+    group->count = used;
+    group->tiles = tiles;
+    group->a_kind = ak;
+    group->segmented = seg ? 1 : 0;
+    group->capacity = capacity;
+    return kOk;
+}
+
+int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStream_t stream) {
+    if (group.tiles == 0) return kOk;
+    const GemmParams* ps = static_cast<const GemmParams*>(device_table);
+    // the tile table sits after the capacity the table was laid out for
+    const int64_t* starts = reinterpret_cast<const int64_t*>(
+        static_cast<const char*>(device_table) + round_up(sizeof(GemmParams) * static_cast<size_t>(group.capacity), 8));
+    const GemmParams none{};
+    const dim3 grid(static_cast<unsigned>(group.tiles));
+    if (group.a_kind == kAFloatT)
+        hipLaunchKernelGGL((gemm_lds_kernel<kPlain, kAFloatT, true>), grid, dim3(256), 0, stream, none, group.tiles,
+                           int64_t{0}, int64_t{1}, ps, starts, group.count);
+    else if (group.segmented)
+        hipLaunchKernelGGL((gemm_lds_kernel<kWindowsInSequence, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
+                           group.tiles, int64_t{0}, int64_t{1}, ps, starts, group.count);
+    else
+        hipLaunchKernelGGL((gemm_lds_kernel<kPlain, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
+                           group.tiles, int64_t{0}, int64_t{1}, ps, starts, group.count);
+    return check_launch("gemm group");
+}
+
 int launch_gemm(const GemmCall& g, hipStream_t stream) {
     DLLM_REQUIRE(g.I >= 0 && g.J >= 0, "negative matmul size");
     DLLM_REQUIRE(g.seg == nullptr || g.nseg >= 1, "segmented matmul needs at least one segment");
@@ -493,8 +582,7 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     DLLM_REQUIRE(ak == kADouble || ak == kAFloatRows || ak == kAFloatT, "unknown A operand kind");
     if (ak == kADouble) DLLM_REQUIRE(g.lda >= padded_rows(g.I), "the double operand must be padded to whole row tiles");
     if (g.I == 0 || g.J == 0) return kOk;
-    GemmParams p{g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.I, g.J, g.l0, g.l1, g.seg, g.nseg, g.bias, g.addsrc,
-                 g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af};
+    GemmParams p = params_of(g);
     const bool vec = (g.J % 4 == 0) && (g.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(g.B) % 16 == 0);
     if (ak != kADouble) {
         // float A: 16-byte chunks of whole rows (and, transposed, a plain reduction over l in [0, l1))
@@ -517,7 +605,7 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
         DLLM_REQUIRE(gx * gy * gz < (int64_t{1} << 31), "matmul grid too large for one launch");
         const dim3 grid(static_cast<unsigned>(gx * gy * gz));
 #define DLLM_GEMM_LAUNCH(MODE, AK) \
-    hipLaunchKernelGGL((gemm_lds_kernel<MODE, AK>), grid, dim3(256), 0, stream, p, gx, gy, gz)
+    hipLaunchKernelGGL((gemm_lds_kernel<MODE, AK>), grid, dim3(256), 0, stream, p, gx, gy, gz, nullptr, nullptr, 0)
         if (ak == kAFloatT) {
             DLLM_GEMM_LAUNCH(kPlain, kAFloatT);
         } else if (ak == kAFloatRows) {

@@ -39,6 +39,19 @@ struct GemmCall {
 
 int launch_gemm(const GemmCall& g, hipStream_t stream);
 
+// Several independent matmuls in one launch (the experts of a layer). All are float-A of one kind: transposed
+// (plain mode) or rows (plain or windowed, no addends). gemm_group_prepare lays the parameters of n <= capacity calls
+// out in host_table (gemm_group_bytes(capacity) bytes; calls with no output are dropped); the caller copies that
+// table to device memory and launches it with launch_gemm_group. Each output is bit-identical to launch_gemm of its
+// call.
+struct GemmGroup {
+    int count = 0, capacity = 0, a_kind = 0, segmented = 0;
+    int64_t tiles = 0;
+};
+size_t gemm_group_bytes(int n);
+int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_table, GemmGroup* group);
+int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStream_t stream);
+
 // dst[r][c] = src[r][c] and dstT[c][r] = src[r][c] as doubles (either may be null).
 int launch_to_double(const float* src, int64_t rows, int64_t cols, int64_t lds, double* dst, int64_t ldd,
                      double* dstT, int64_t lddT, hipStream_t stream);

@@ -164,7 +164,12 @@ struct dllm_hip_trainer {
         // position of row r's i-th choice by ascending expert; eseg[e][w] the window boundaries in expert e's group
         int64_t *row_of = nullptr, *slot = nullptr, *order = nullptr, *eseg = nullptr;
         std::vector<int64_t> estart;  // host: E + 1 group starts
+        // the layer's expert matmuls, one grouped launch per kind (tables in device memory, made by group_rows)
+        GemmGroup groups[9];
+        double group_flops[9] = {};
+        char* tables = nullptr;
     };
+    enum ExpertMatmul { kFwdGate, kFwdUp, kFwdDown, kDxDown, kDwDown, kDxGate, kDwGate, kDxUp, kDwUp, kExpertMatmuls };
     std::vector<Saved> saved;
     std::vector<std::unique_ptr<DevBuf>> owned;
     float *x_final = nullptr, *hidden = nullptr, *logits = nullptr, *dlogits = nullptr;
@@ -215,6 +220,11 @@ struct dllm_hip_trainer {
         int weight, a, b;  // tensor id, adapter ids
     };
     std::vector<LoraTarget> lora_targets;
+    // LoRA runs compute the gradients of the adapted weights only: the others reach no optimizer (trainer.py:463-474)
+    std::vector<const float*> target_grads;
+    bool grad_wanted(const float* g) const {
+        return !lora_on || std::find(target_grads.begin(), target_grads.end(), g) != target_grads.end();
+    }
     DevBuf lora_p, lora_g, lora_m, lora_v, merged;
     std::vector<int64_t> merged_offset;  // per tensor id: offset in `merged`, or -1
     bool base_ready = true;              // the Q8_0 base has been applied to the current parameters
@@ -440,6 +450,7 @@ struct dllm_hip_trainer {
                 DLLM_TRY(make(&s.slot, RK));
                 DLLM_TRY(make(&s.order, RK));
                 DLLM_TRY(make(&s.eseg, E * (W_max + 1)));
+                DLLM_TRY(make(&s.tables, kExpertMatmuls * gemm_group_bytes(static_cast<int>(E))));
             }
         }
         if (E > 0) {
@@ -547,6 +558,25 @@ struct dllm_hip_trainer {
 
     int gemm(const GemmCall& g, hipStream_t s) {
         if (!profiling) return launch_gemm(g, s);
+        DLLM_TRY(profile_begin(s));
+        DLLM_TRY(launch_gemm(g, s));
+        return profile_end(flops_of(g), s);
+    }
+
+    // One launch of a layer's expert matmuls (a group table made by group_rows).
+    int gemm_group(const GemmGroup& grp, const void* table, double flops, hipStream_t s) {
+        if (!profiling) return launch_gemm_group(grp, table, s);
+        DLLM_TRY(profile_begin(s));
+        DLLM_TRY(launch_gemm_group(grp, table, s));
+        return profile_end(flops, s);
+    }
+
+    static double flops_of(const GemmCall& g) {
+        const double L = static_cast<double>(g.l1 - g.l0);  // segmented calls set [l0, l1) to their whole row range
+        return 2.0 * static_cast<double>(g.I) * static_cast<double>(g.J) * L;
+    }
+
+    int profile_begin(hipStream_t s) {
         if (event_used + 2 > events.size()) {
             if (events.size() >= 8192) DLLM_TRY(drain_events());
             while (event_used + 2 > events.size()) {
@@ -555,12 +585,13 @@ struct dllm_hip_trainer {
                 events.push_back(e);
             }
         }
-        DLLM_TRY(check_hip(hipEventRecord(events[event_used], s), "event"));
-        DLLM_TRY(launch_gemm(g, s));
+        return check_hip(hipEventRecord(events[event_used], s), "event");
+    }
+
+    int profile_end(double flops, hipStream_t s) {
         DLLM_TRY(check_hip(hipEventRecord(events[event_used + 1], s), "event"));
         event_used += 2;
-        const double L = static_cast<double>(g.l1 - g.l0);  // segmented calls set [l0, l1) to their whole row range
-        profile_flops += 2.0 * static_cast<double>(g.I) * static_cast<double>(g.J) * L;
+        profile_flops += flops;
         profile_launches += 1;
         return kOk;
     }
@@ -579,6 +610,11 @@ struct dllm_hip_trainer {
     // out[R][N] (+)= x[R][K] @ W^T (+ bias); the matmul reads x itself (A transposed: A[k][r] = x[r][k]).
     int linear_fwd(const float* x, int64_t R, int64_t K, int w_id, const float* bias, float* out, const float* addsrc,
                    hipStream_t s) {
+        return gemm(fwd_call(x, R, K, w_id, bias, out, addsrc), s);
+    }
+
+    GemmCall fwd_call(const float* x, int64_t R, int64_t K, int w_id, const float* bias, float* out,
+                      const float* addsrc) const {
         const int64_t N = tensors[static_cast<size_t>(w_id)].rows;
         GemmCall g;
         g.Af = x;
@@ -595,11 +631,15 @@ struct dllm_hip_trainer {
         g.bias = bias;
         g.addsrc = addsrc;
         g.ld_add = N;
-        return gemm(g, s);
+        return g;
     }
 
     // dx[R][K] (= addsrc +) sum_n dy[r][n] W[n][k]; the matmul reads dy[R][N] itself (A transposed).
     int linear_dx(const float* dyv, int64_t R, int w_id, float* out, const float* addsrc, hipStream_t s) {
+        return gemm(dx_call(dyv, R, w_id, out, addsrc), s);
+    }
+
+    GemmCall dx_call(const float* dyv, int64_t R, int w_id, float* out, const float* addsrc) const {
         const TensorInfo& t = tensors[static_cast<size_t>(w_id)];
         GemmCall g;
         g.Af = dyv;
@@ -615,13 +655,19 @@ struct dllm_hip_trainer {
         g.l1 = t.rows;
         g.addsrc = addsrc;
         g.ld_add = t.cols;
-        return gemm(g, s);
+        return g;
     }
 
     // grad[w] = window-ordered float sum of per-window dW = sum over window rows of dy[r][n] x[r][k]. The windows are
     // the step's (seg_d), or those of an expert's group (seg, over `rows` grouped rows).
     int linear_dw(const float* dyv, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
                   const float* addend, hipStream_t s, const int64_t* seg = nullptr, int64_t rows = -1) {
+        if (!grad_wanted(out)) return kOk;
+        return gemm(dw_call(dyv, N, x, K, nseg, out, addrow_, addend, seg, rows), s);
+    }
+
+    GemmCall dw_call(const float* dyv, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
+                     const float* addend, const int64_t* seg = nullptr, int64_t rows = -1) const {
         GemmCall g;
         g.Af = dyv;  // A rows: A[r][n] = dy[r][n]
         g.a_kind = 1;
@@ -641,11 +687,12 @@ struct dllm_hip_trainer {
         g.ld_seg_add = K;
         g.seg_partial = gemm_part;
         g.seg_partial_cap = gemm_part_cap;
-        return gemm(g, s);
+        return g;
     }
 
     int norm_dw(const float* dyv, const float* x, const double* inv, int64_t dim, int64_t rows_per_token, int nseg,
                 float* out, hipStream_t s) {
+        if (!grad_wanted(out)) return kOk;
         std::vector<int64_t> seg(seg_host.size());
         for (size_t i = 0; i < seg.size(); ++i) seg[i] = seg_host[i] * rows_per_token;
         return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s);
@@ -867,7 +914,7 @@ struct dllm_hip_trainer {
         for (int p = 0; p < 3; ++p) {
             DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
             DLLM_TRY(linear_dw(ds[p], ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s));
-            if (bs_[p] >= 0)
+            if (bs_[p] >= 0 && grad_wanted(G(bs_[p])))
                 DLLM_TRY(launch_column_sums(0, ds[p], nullptr, nullptr, ns[p], seg_host.data(), nseg, col_part,
                                             G(bs_[p]), s));
         }
@@ -880,7 +927,7 @@ struct dllm_hip_trainer {
 
     // Groups the step's rows by expert from the layer's choices (host; the choices come back first): experts
     // ascending, within an expert rows ascending (np.nonzero), and the per-window split of each group.
-    int group_rows(Saved& sv, int64_t R, hipStream_t s) {
+    int group_rows(int64_t l, Saved& sv, int64_t R, hipStream_t s) {
         std::vector<int64_t> chosen(static_cast<size_t>(R * K));
         DLLM_TRY(check_hip(hipMemcpyAsync(chosen.data(), sv.chosen, chosen.size() * 8, hipMemcpyDeviceToHost, s),
                            "download"));
@@ -926,8 +973,71 @@ struct dllm_hip_trainer {
         DLLM_TRY(check_hip(hipMemcpyAsync(sv.order, order.data(), order.size() * 8, hipMemcpyHostToDevice, s),
                            "upload"));
         DLLM_TRY(check_hip(hipMemcpyAsync(sv.eseg, eseg.data(), eseg.size() * 8, hipMemcpyHostToDevice, s), "upload"));
+        std::vector<char> tables;
+        DLLM_TRY(expert_tables(l, sv, &tables));
+        DLLM_TRY(check_hip(hipMemcpyAsync(sv.tables, tables.data(), tables.size(), hipMemcpyHostToDevice, s),
+                           "upload"));
         // the host vectors die here: wait for the copies
         return check_hip(hipStreamSynchronize(s), "grouping");
+    }
+
+    // The layer's nine kinds of expert matmuls over the grouped rows (expert e's rows are st .. st + n - 1):
+    //   forward  gate/up = xg W^T, y = product Wd^T;  backward  dproduct = dy Wd, dxg = dgate Wg (+ dup Wu),
+    //   and each weight's dW over the expert's rows split at the window boundaries.
+    int expert_tables(int64_t l, Saved& sv, std::vector<char>* out) {
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        const size_t gb = gemm_group_bytes(static_cast<int>(E));
+        out->assign(kExpertMatmuls * gb, 0);
+        std::vector<GemmCall> calls;
+        for (int kind = 0; kind < kExpertMatmuls; ++kind) {
+            calls.clear();
+            for (int64_t e = 0; e < E; ++e) {
+                const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
+                const int64_t* es = sv.eseg + e * (W_max + 1);
+                GemmCall g;
+                switch (kind) {
+                    case kFwdGate: g = fwd_call(xg + st * H, n, H, L.egate[e], nullptr, sv.gate + st * EI, nullptr); break;
+                    case kFwdUp: g = fwd_call(xg + st * H, n, H, L.eup[e], nullptr, sv.up + st * EI, nullptr); break;
+                    case kFwdDown:
+                        g = fwd_call(sv.product + st * EI, n, EI, L.edown[e], nullptr, sv.y + st * H, nullptr);
+                        break;
+                    case kDxDown: g = dx_call(dyg + st * H, n, L.edown[e], dproduct + st * EI, nullptr); break;
+                    case kDwDown:
+                        if (!grad_wanted(G(L.edown[e]))) continue;
+                        g = dw_call(dyg + st * H, H, sv.product + st * EI, EI, static_cast<int>(nwin), G(L.edown[e]),
+                                    nullptr, nullptr, es, n);
+                        break;
+                    case kDxGate: g = dx_call(dgate + st * EI, n, L.egate[e], dxg + st * H, nullptr); break;
+                    case kDwGate:
+                        if (!grad_wanted(G(L.egate[e]))) continue;
+                        g = dw_call(dgate + st * EI, EI, xg + st * H, H, static_cast<int>(nwin), G(L.egate[e]),
+                                    nullptr, nullptr, es, n);
+                        break;
+                    case kDxUp: g = dx_call(dup + st * EI, n, L.eup[e], dxg + st * H, dxg + st * H); break;
+                    default:
+                        if (!grad_wanted(G(L.eup[e]))) continue;
+                        g = dw_call(dup + st * EI, EI, xg + st * H, H, static_cast<int>(nwin), G(L.eup[e]), nullptr,
+                                    nullptr, es, n);
+                        break;
+                }
+                g.seg_partial = nullptr;
+                g.seg_partial_cap = 0;
+                calls.push_back(g);
+            }
+            GemmGroup& grp = sv.groups[kind];
+            grp = GemmGroup{};
+            sv.group_flops[kind] = 0.0;
+            if (calls.empty()) continue;
+            DLLM_TRY(gemm_group_prepare(calls.data(), static_cast<int>(calls.size()), static_cast<int>(E),
+                                        out->data() + kind * gb, &grp));
+            for (const GemmCall& g : calls) sv.group_flops[kind] += flops_of(g);
+        }
+        return kOk;
+    }
+
+    int expert_matmul(const Saved& sv, int kind, hipStream_t s) {
+        const size_t gb = gemm_group_bytes(static_cast<int>(E));
+        return gemm_group(sv.groups[kind], sv.tables + kind * gb, sv.group_flops[kind], s);
     }
 
     // _experts (backprop.py:501-527): route, group, the SwiGLU of every expert over its rows, and
@@ -938,20 +1048,12 @@ struct dllm_hip_trainer {
         DLLM_TRY(linear_fwd(sv.h2, R, H, L.router, nullptr, sv.router_logits, nullptr, s));
         DLLM_TRY(launch_moe_route(sv.router_logits, R, E, K, c.normalize_expert_weights ? 1 : 0, sv.chosen,
                                   sv.routing, sv.probs, s));
-        DLLM_TRY(group_rows(sv, R, s));
+        DLLM_TRY(group_rows(l, sv, R, s));
         DLLM_TRY(launch_gather_rows(sv.h2, sv.row_of, xg, R * K, H, s));
-        for (int64_t e = 0; e < E; ++e) {
-            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
-            if (n == 0) continue;
-            DLLM_TRY(linear_fwd(xg + st * H, n, H, L.egate[e], nullptr, sv.gate + st * EI, nullptr, s));
-            DLLM_TRY(linear_fwd(xg + st * H, n, H, L.eup[e], nullptr, sv.up + st * EI, nullptr, s));
-        }
+        DLLM_TRY(expert_matmul(sv, kFwdGate, s));
+        DLLM_TRY(expert_matmul(sv, kFwdUp, s));
         DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * K * EI, s));
-        for (int64_t e = 0; e < E; ++e) {
-            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
-            if (n == 0) continue;
-            DLLM_TRY(linear_fwd(sv.product + st * EI, n, EI, L.edown[e], nullptr, sv.y + st * H, nullptr, s));
-        }
+        DLLM_TRY(expert_matmul(sv, kFwdDown, s));
         return launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sv.x_mid, x_out, R, K, H, s);
     }
 
@@ -962,23 +1064,13 @@ struct dllm_hip_trainer {
         const int64_t P = R * K;
         DLLM_TRY(launch_moe_dweights(dx, sv.y, sv.row_of, sv.slot, sv.routing, P, H, dweights, dyg, s));
         DLLM_TRY(launch_gather_rows(sv.h2, sv.row_of, xg, P, H, s));
-        const auto eseg = [&](int64_t e) { return sv.eseg + e * (W_max + 1); };
-        for (int64_t e = 0; e < E; ++e) {
-            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
-            DLLM_TRY(linear_dx(dyg + st * H, n, L.edown[e], dproduct + st * EI, nullptr, s));
-            DLLM_TRY(linear_dw(dyg + st * H, H, sv.product + st * EI, EI, nseg, G(L.edown[e]), nullptr, nullptr, s,
-                               eseg(e), n));
-        }
+        DLLM_TRY(expert_matmul(sv, kDxDown, s));
+        DLLM_TRY(expert_matmul(sv, kDwDown, s));
         DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, P * EI, s));
-        for (int64_t e = 0; e < E; ++e) {
-            const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
-            DLLM_TRY(linear_dx(dgate + st * EI, n, L.egate[e], dxg + st * H, nullptr, s));
-            DLLM_TRY(linear_dw(dgate + st * EI, EI, xg + st * H, H, nseg, G(L.egate[e]), nullptr, nullptr, s,
-                               eseg(e), n));
-            DLLM_TRY(linear_dx(dup + st * EI, n, L.eup[e], dxg + st * H, dxg + st * H, s));  // dx_gate + dx_up
-            DLLM_TRY(linear_dw(dup + st * EI, EI, xg + st * H, H, nseg, G(L.eup[e]), nullptr, nullptr, s, eseg(e),
-                               n));
-        }
+        DLLM_TRY(expert_matmul(sv, kDxGate, s));
+        DLLM_TRY(expert_matmul(sv, kDwGate, s));
+        DLLM_TRY(expert_matmul(sv, kDxUp, s));  // dx_gate + dx_up
+        DLLM_TRY(expert_matmul(sv, kDwUp, s));
         // the router: dlogits from the routing weights' gradients (and the load-balancing loss's), then its linear
         if (router_scale_cur != 0.0)
             DLLM_TRY(launch_broadcast_window_rows(grad_row, seg_d, nseg, R, E, dprob, s));
@@ -1098,6 +1190,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(norm_dw(dhidden, x_final, inv_rms, H, 1, nseg, G(final_norm), s));
         for (int64_t l = c.layers - 1; l >= 0; --l) DLLM_TRY(backward_layer(l, R, nseg, b, s));
         // embedding (backprop.py:112-117): per-window token rows, then the head's dW with them as the tied addend
+        if (lora_on) return finish_gradients(windows, loss, router_loss, s);  // neither is adapted
         DLLM_TRY(launch_embedding_groups(dx, H, grp_order, grp_start, grp_out, groups, emb_rows, H, s));
         if (c.tie_embeddings) {
             DLLM_TRY(linear_dw(dlogits, V, hidden, H, nseg, G(emb), addrow, emb_rows, s));
@@ -1107,6 +1200,11 @@ struct dllm_hip_trainer {
                                addrow, V, H, nseg, G(emb));
             DLLM_TRY(check_launch("embedding window sum"));
         }
+        return finish_gradients(windows, loss, router_loss, s);
+    }
+
+    // The losses of the step's windows, summed in window order on the host.
+    int finish_gradients(int64_t windows, double* loss, double* router_loss, hipStream_t s) {
         std::vector<double> lw(static_cast<size_t>(windows)), rw(static_cast<size_t>(windows), 0.0);
         int flag = 0;
         DLLM_TRY(check_hip(hipMemcpyAsync(lw.data(), loss_w, lw.size() * 8, hipMemcpyDeviceToHost, s), "download"));
@@ -1240,6 +1338,7 @@ struct dllm_hip_trainer {
             merged_offset[static_cast<size_t>(w)] = moff;
             moff += t.numel;
             lora_targets.push_back({w, adapter_index[t.name + ".lora_a"], adapter_index[t.name + ".lora_b"]});
+            target_grads.push_back(G(w));
             ws = std::max(ws, lora_merge_workspace(t.rows, t.cols, l.rank));
             ws = std::max(ws, lora_adapter_gradients_workspace(t.rows, t.cols, l.rank));
         }

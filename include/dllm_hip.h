@@ -217,7 +217,8 @@ int dllm_hip_trainer_create(const dllm_hip_decoder_config* config, int64_t max_t
 int dllm_hip_trainer_destroy(dllm_hip_trainer* trainer);
 /* A LoRA trainer (lora may be NULL: as dllm_hip_trainer_create). The adapters are tensors "<weight>.lora_a"
  * ([rank, in]) and "<weight>.lora_b" ([out, rank]) beside the base tensors; set them (init_adapters) before the first
- * step. The base tensors' gradients (which 1) are those of the merged weights. No counterpart in the reference's
+ * step. The adapted base tensors' gradients (which 1) are those of the merged weights; the other base tensors'
+ * gradients reach no optimizer and are not computed (they stay zero). No counterpart in the reference's
  * kernel module: it replaces FineTuner's LoRA branch (trainer.py:247-250, 304-305). */
 int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dllm_hip_lora_config* lora,
                                  int64_t max_tokens, int64_t max_windows, int64_t max_window_tokens,

@@ -158,6 +158,11 @@ def test_lora_step_matches_the_oracle_on_ragged_windows(base_quantize):
             assert t.get(name, a.shape).tobytes() == a.tobytes(), name
             assert t.get(name, a.shape, t.M).tobytes() == m[name].tobytes(), name
             assert t.get(name, a.shape, t.V).tobytes() == v[name].tobytes(), name
+    # only the adapted weights' gradients are computed; the others reach no optimizer and stay zero
+    for name in ("token_embedding.weight", "layers.0.attention.k.weight", "layers.1.mlp_norm.weight",
+                 "layers.0.attention.q.bias", "final_norm.weight"):
+        assert not np.any(t.get(name, d.tensor_shapes()[name], t.GRAD)), name
+    assert np.any(t.get("layers.1.attention.v.weight", d.tensor_shapes()["layers.1.attention.v.weight"], t.GRAD))
 
 
 MOE = {
