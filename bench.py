@@ -365,7 +365,7 @@ def main() -> int:
                    "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic,
-                     "kernel": "gemm_kernel (FP64 FMA matmul, all launches of the timed steps)",
+                     "kernel": "gemm_lds_kernel (FP64 FMA matmul, all launches of the timed steps)",
                      "step_fraction_of_peak": matmul_flops_per_step(cfg) / (ms_per_step * 1e9) / FP64_PEAK_TFLOPS},
         "cpu_baseline": baseline,
     }
