@@ -43,6 +43,18 @@ struct AttnGemmCall {
 };
 
 int launch_attn_gemm(const AttnGemmCall& c, hipStream_t stream);
+
+// The same matmuls as 64-row tiles through a double-buffered LDS pipeline (attn_lds.hip), ragged causal spans
+// predicated per row inside the tile. A is double [L][rows padded to 64] (products multiply-then-add, float output,
+// 64 or 128 columns per tile) or, for the scores and dP, float rows A[i][l] read transposed (a_float: exact
+// products, 256 columns per tile). `second` runs a second matmul of the same shape in the same launch (dk and dv).
+struct AttnTileCall : AttnGemmCall {
+    bool a_float = false;
+    int64_t a_row_alloc = 0;  // a_float: floats readable in each A row (multiple of 4, >= L)
+    bool second = false;
+    AttnOperand A2, B2, C2;
+};
+int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream);
 int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
                         int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream);
 // dvec: windows * heads * inv_zstride doubles of workspace (the per-query D)

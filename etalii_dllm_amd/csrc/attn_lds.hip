@@ -1,0 +1,488 @@
+// The attention matmuls of the training step (attn_gemm.h) as 64-row tiles through a double-buffered LDS pipeline,
+// one workgroup of four waves per tile, every (window, head) of the step in one launch.
+//
+// Each output is C[i][j] = sum over l in row i's span, ascending, of A[l][i] * B[l][j] (then times a row scale or a
+// constant), accumulated in double and rounded once:
+//   scores      S^T[key][query] = sum_d K[key][d] Q[query][d]        A = K (float, read transposed), exact: fma
+//   dP^T        dP^T[key][query] = sum_d V[key][d] dOut[query][d]     A = V (float, read transposed), exact: fma
+//   out, dq     row t (query): sum over the keys t sees of E^T / dS^T times V / K    A double: multiply, then add
+//   dk, dv      row j (key): sum over (query t, head of the group) that see j of dS / P times Q / dOut  (as above)
+// The products with a double factor are not exact, so they are a rounded multiply and a rounded add, as the
+// reference computes them (grad.hpp:262-301, nn.hpp:535-569).
+//
+// Mapping: a wave owns 16 consecutive rows (its A values broadcast to all 64 lanes) by 64 CJ columns (CJ per lane).
+// A stage is 16 consecutive l: the workgroup's A (16 l x 64 rows) and B (16 l x 64 CJ columns) are copied
+// global -> LDS with gfx950's direct-to-LDS loads while the previous stage is computed. The broadcast is the DPP64
+// row_newbcast modifier: on the FMA itself for exact products, on a 64-bit move feeding the multiply otherwise.
+// Causal rows have ragged spans: stages inside every row's span of the wave run unpredicated; at the ragged ends
+// each (row, l) is taken only when l lies in that row's span (a wave-uniform test), so every row adds exactly its
+// own steps, in order, and nothing else. Tiles are dispatched longest reduction first.
+#include <type_traits>
+
+#include "attn_gemm.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace dllm_hip {
+
+namespace {
+
+constexpr int kChunk = 16;  // reduction steps per stage
+constexpr int kTileRows = 64;
+
+struct Op {
+    const void* ptr;
+    int64_t w_stride, seg_stride, head_stride, head_div;
+    int64_t ld, ld_inner, group;  // row(l) = (l / group) * ld + (l % group) * ld_inner
+};
+
+template <typename T>
+__device__ __forceinline__ const T* op_base(const Op& o, int64_t w, int64_t seg_w, int64_t hz) {
+    return static_cast<const T*>(o.ptr) + w * o.w_stride + seg_w * o.seg_stride + (hz / o.head_div) * o.head_stride;
+}
+
+struct OperandSet {
+    Op A, B, C;
+};
+
+struct TileParams {
+    OperandSet set[2];         // one launch may run two matmuls of the same shape (dk and dv)
+    int sets;
+    const double* rowscale;    // float outputs: value * rowscale[z][i] before rounding; may be null
+    int64_t rowscale_zstride;
+    double out_scale;          // double outputs: value * out_scale
+    const int64_t* seg;
+    int64_t heads, Z;          // z = w * heads + hz in [0, Z)
+    int rows_kind, cols_kind;  // 0: window positions, 1: head_dim
+    int64_t head_dim, group, window, L;
+    int mask;
+    int64_t b_row_alloc;  // floats readable in each B row from column 0 (multiple of 4, >= J)
+    int64_t a_row_alloc;  // float A: floats readable in each A row (multiple of 4)
+    int64_t tiles_i, tiles_j;
+};
+
+__device__ __forceinline__ void query_span(int64_t t, int64_t window, int64_t* lo, int64_t* hi) {
+    *hi = t + 1;
+    *lo = window != 0 && t + 1 > window ? t + 1 - window : 0;
+}
+
+__device__ __forceinline__ void key_span(int64_t j, int64_t n, int64_t window, int64_t G, int64_t* lo, int64_t* hi) {
+    *lo = j * G;
+    const int64_t t_hi = window != 0 && j + window - 1 < n - 1 ? j + window - 1 : n - 1;
+    *hi = (t_hi + 1) * G;
+}
+
+// The steps row r takes: [lo, hi). Rows past I take none.
+__device__ __forceinline__ void row_span(const TileParams& p, int64_t r, int64_t n, int64_t I, int64_t* lo,
+                                         int64_t* hi) {
+    if (r >= I) {
+        *lo = *hi = 0;
+    } else if (p.mask == kMaskQueryRows) {
+        query_span(r, p.window, lo, hi);
+    } else if (p.mask == kMaskKeyRows) {
+        key_span(r, n, p.window, p.group, lo, hi);
+    } else {
+        *lo = 0;
+        *hi = p.L;
+    }
+}
+
+template <int CJ, bool kAFloat>
+struct Stage {
+    typename std::conditional<kAFloat, float, double>::type a[kAFloat ? kTileRows : kChunk]
+                                                             [kAFloat ? kChunk : kTileRows];
+    float b[kChunk][64 * CJ];
+};
+
+template <int CJ, bool kAFloat>
+constexpr int stage_copies() {
+    return (kAFloat ? 1 : 2) + CJ;
+}
+
+__device__ __forceinline__ void copy16_to_lds(const void* src, const void* lds_row) {
+    typedef __attribute__((address_space(3))) const void* lds_address;
+    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+template <int kPending>
+__device__ __forceinline__ void wait_stage() {
+    if (kPending == 0)
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPending) : "memory");
+}
+
+__device__ __forceinline__ void workgroup_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Copies of the stage holding steps l .. l + 15 (steps past `last` repeat step `last`; they are never used). Wave w
+// copies A rows (steps) 4w .. 4w + 3 (doubles: two per instruction) or, transposed, A rows 16w .. 16w + 15 (16
+// steps of floats each), and B rows 4w .. 4w + 3.
+template <int CJ, bool kAFloat>
+__device__ __forceinline__ void issue_stage(Stage<CJ, kAFloat>& st, const void* a_base, const Op& ao, int64_t i0,
+                                            int64_t I, int64_t a_row_alloc, const float* b_base, const Op& bo,
+                                            int64_t b_col, int64_t l, int64_t last, int wave, int lane) {
+    if constexpr (kAFloat) {
+        // row i (clamped to I - 1), steps l + 4 (lane % 4) .. + 3 (clamped to the row's readable end)
+        const int64_t i = i0 + 16 * wave + (lane >> 2) < I ? i0 + 16 * wave + (lane >> 2) : I - 1;
+        const int64_t lc = l + (lane & 3) * 4 <= a_row_alloc - 4 ? l + (lane & 3) * 4 : a_row_alloc - 4;
+        copy16_to_lds(static_cast<const float*>(a_base) + i * ao.ld + lc, &st.a[16 * wave][0]);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int r = 4 * wave + 2 * t;
+            const int64_t lr = l + r + (lane >> 5) <= last ? l + r + (lane >> 5) : last;
+            copy16_to_lds(static_cast<const double*>(a_base) + lr * ao.ld + i0 + (lane & 31) * 2, &st.a[r][0]);
+        }
+    }
+    constexpr int kLanesPerRow = 16 * CJ;
+    constexpr int kRowsPerCopy = 64 / kLanesPerRow;
+    const int sub = lane / kLanesPerRow;
+#pragma unroll
+    for (int t = 0; t < CJ; ++t) {
+        const int r = 4 * wave + t * kRowsPerCopy + sub;
+        const int64_t lr = l + r <= last ? l + r : last;
+        int64_t row;
+        if (bo.group == 1) {
+            row = lr * bo.ld;
+        } else {  // (query, head of the group) rows; l < 2^32
+            const uint32_t g = static_cast<uint32_t>(bo.group), u = static_cast<uint32_t>(lr), qt = u / g;
+            row = static_cast<int64_t>(qt) * bo.ld + static_cast<int64_t>(u - qt * g) * bo.ld_inner;
+        }
+        copy16_to_lds(b_base + row + b_col, &st.b[4 * wave + t * kRowsPerCopy][0]);
+    }
+}
+
+template <int CJ>
+struct RowOperands {
+    double a;
+    float b[CJ];
+};
+
+template <int CJ, bool kAFloat>
+__device__ __forceinline__ RowOperands<CJ> read_row(const Stage<CJ, kAFloat>& st, int k, int wave, int lane) {
+    RowOperands<CJ> r;
+    const int i = wave * 16 + (lane & 15);
+    if constexpr (kAFloat)
+        r.a = static_cast<double>(st.a[i][k]);
+    else
+        r.a = st.a[k][i];
+    if constexpr (CJ == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&st.b[k][lane * 4]);
+        r.b[0] = v.x; r.b[1] = v.y; r.b[2] = v.z; r.b[3] = v.w;
+    } else if constexpr (CJ == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(&st.b[k][lane * 2]);
+        r.b[0] = v.x; r.b[1] = v.y;
+    } else {
+        r.b[0] = st.b[k][lane];
+    }
+    return r;
+}
+
+// acc[Q][c] = fma(A[l][row Q], b[c], acc[Q][c]) with A[l][row Q] taken from lane Q of each 16-lane row by the DPP64
+// row_newbcast modifier. A DPP instruction reads its registers two wait states after their last vector write; in a
+// step every row takes, only the first block follows the conversions that wrote b (and, for float A, a), so only it
+// starts with s_nop 1 (kNop: every block does, for steps some rows skip), and the blocks stay in order (volatile).
+// tests/test_dpp_hazards.py checks the built code.
+template <int CJ, int Q, bool kNop>
+__device__ __forceinline__ void fma_bcast(double (&acc)[16][CJ], double a, const double (&b)[CJ]) {
+    if constexpr (CJ == 4) {
+        if constexpr (Q == 0 || kNop)
+            asm volatile("s_nop 1\n\t"
+                         "v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                         "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                         "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                         "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+                         : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
+                         : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
+        else
+            asm volatile("v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                         "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                         "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                         "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
+                         : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
+                         : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
+    } else if constexpr (CJ == 2) {
+        asm volatile("s_nop 1\n\t"
+                     "v_fmac_f64_dpp %0, %2, %3 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
+                     "v_fmac_f64_dpp %1, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc[Q][0]), "+v"(acc[Q][1])
+                     : "v"(a), "v"(b[0]), "v"(b[1]), "n"(Q));
+    } else {
+        asm volatile("s_nop 1\n\t"
+                     "v_fmac_f64_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc[Q][0])
+                     : "v"(a), "v"(b[0]), "n"(Q));
+    }
+}
+
+// A[l][rows Q .. Q + 3] in every lane (DPP64 moves); the wait states before the first move as above.
+template <int Q>
+__device__ __forceinline__ void broadcast_rows4(double a, double (&r)[4]) {
+    asm volatile("s_nop 1\n\t"
+                 "v_mov_b64_dpp %0, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_mov_b64_dpp %1, %4 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_mov_b64_dpp %2, %4 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_mov_b64_dpp %3, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf"
+                 : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+                 : "v"(a), "n"(Q), "n"(Q + 1), "n"(Q + 2), "n"(Q + 3));
+}
+
+// One step for the wave's 16 rows; kAll: every row takes it, otherwise row q only when `take` has bit q.
+template <int CJ, bool kExact, bool kAll, int Q>
+__device__ __forceinline__ void step_rows(double (&acc)[16][CJ], double a, const double (&b)[CJ], uint32_t take) {
+    if constexpr (Q < 16) {
+        if constexpr (kExact) {
+            if (kAll || (take >> Q) & 1u) fma_bcast<CJ, Q, !kAll>(acc, a, b);
+            step_rows<CJ, kExact, kAll, Q + 1>(acc, a, b, take);
+        } else {
+            double aq[4];
+            broadcast_rows4<Q>(a, aq);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (kAll || (take >> (Q + k)) & 1u) {
+#pragma unroll
+                    for (int c = 0; c < CJ; ++c) {
+                        const double prod = aq[k] * b[c];
+                        acc[Q + k][c] = acc[Q + k][c] + prod;
+                    }
+                }
+            }
+            step_rows<CJ, kExact, kAll, Q + 4>(acc, a, b, take);
+        }
+    }
+}
+
+template <int CJ>
+__device__ __forceinline__ void widen(const RowOperands<CJ>& r, double (&b)[CJ]) {
+#pragma unroll
+    for (int c = 0; c < CJ; ++c) b[c] = r.b[c];
+}
+
+template <int CJ, bool kAFloat, bool kExact>
+__device__ __forceinline__ void stage_all(const Stage<CJ, kAFloat>& st, int wave, int lane, double (&acc)[16][CJ]) {
+    RowOperands<CJ> cur = read_row<CJ, kAFloat>(st, 0, wave, lane);
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        RowOperands<CJ> next = cur;
+        if (k + 1 < kChunk) next = read_row<CJ, kAFloat>(st, k + 1, wave, lane);
+        double b[CJ];
+        widen<CJ>(cur, b);
+        step_rows<CJ, kExact, true, 0>(acc, cur.a, b, 0u);
+        cur = next;
+    }
+}
+
+// The wave's rows (tw + q, q < 16) that take step l, as a bit mask: the spans are intervals whose ends grow with the
+// row, so the rows taking l are one run of q, from the span formulas of row_span.
+__device__ __forceinline__ uint32_t rows_taking(const TileParams& p, int64_t l, int64_t tw, int64_t n, int64_t I) {
+    int64_t qa = 0, qb = (I - tw < 16 ? I - tw : 16) - 1;  // rows q in [qa, qb]
+    if (p.mask == kMaskQueryRows) {  // l < t + 1, and l >= t + 1 - window
+        qa = l - tw > qa ? l - tw : qa;
+        if (p.window != 0) qb = l - tw + p.window - 1 < qb ? l - tw + p.window - 1 : qb;
+    } else if (p.mask == kMaskKeyRows) {  // l >= j G, and (windowed) l / G < j + window
+        const int64_t t = l / p.group;
+        qb = t - tw < qb ? t - tw : qb;
+        if (p.window != 0) qa = t - tw - p.window + 1 > qa ? t - tw - p.window + 1 : qa;
+    } else if (l >= p.L) {
+        return 0u;
+    }
+    if (qa > qb) return 0u;
+    const uint32_t upto = qb >= 31 ? 0xffffffffu : (2u << qb) - 1u;
+    return upto & ~((1u << qa) - 1u);
+}
+
+// Steps l0 .. l0 + n - 1 of a stage, each taken by the rows whose span holds it.
+template <int CJ, bool kAFloat, bool kExact>
+__device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ, kAFloat>& st, int wave, int lane,
+                                             int64_t l0, int n, int64_t tw, int64_t rows_n, int64_t I,
+                                             double (&acc)[16][CJ]) {
+    if constexpr (kExact) {  // the scores and dP: every row takes the steps below L (here: the first n)
+        for (int k = 0; k < n; ++k) {
+            const RowOperands<CJ> r = read_row<CJ, kAFloat>(st, k, wave, lane);
+            double b[CJ];
+            widen<CJ>(r, b);
+            step_rows<CJ, kExact, true, 0>(acc, r.a, b, 0u);
+        }
+        return;
+    }
+    for (int k = 0; k < n; ++k) {
+        const uint32_t take = __builtin_amdgcn_readfirstlane(rows_taking(p, l0 + k, tw, rows_n, I));
+        if (take == 0) continue;
+        const RowOperands<CJ> r = read_row<CJ, kAFloat>(st, k, wave, lane);
+        double b[CJ];
+        widen<CJ>(r, b);
+        step_rows<CJ, kExact, false, 0>(acc, r.a, b, take);
+    }
+}
+
+template <int CJ, bool kAFloat, bool kExact, bool kOutDouble>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4 : CJ == 2 ? 2 : 3))) void attn_tile_kernel(
+    TileParams p) {
+    __shared__ Stage<CJ, kAFloat> st[2];
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    // block -> (rank by work, column tile, set, z): the longest reductions go first
+    int64_t id = blockIdx.x;
+    const int64_t zs = p.Z * p.sets;
+    const int64_t zz = id % zs;
+    id /= zs;
+    const int64_t tj = id % p.tiles_j;
+    const int64_t rank = id / p.tiles_j;
+    const int64_t ti = p.mask == kMaskQueryRows ? p.tiles_i - 1 - rank : rank;
+    const int set = static_cast<int>(zz / p.Z);
+    const int64_t z = zz % p.Z;
+    const OperandSet& o = p.set[set];
+    const int64_t w = z / p.heads, hz = z % p.heads;
+    const int64_t seg_w = p.seg[w], n = p.seg[w + 1] - seg_w;
+    const int64_t I = p.rows_kind == 0 ? n : p.head_dim;
+    const int64_t J = p.cols_kind == 0 ? n : p.head_dim;
+    const int64_t i0 = ti * kTileRows, j0 = tj * 64 * CJ;
+    if (i0 >= I || j0 >= J) return;
+    if (p.mask == kMaskTileCausal) {  // score tiles no query sees: every key row above every query column
+        if (i0 > j0 + 64 * CJ - 1) return;
+        if (p.window != 0 && i0 + kTileRows - 1 + p.window - 1 < j0) return;
+    }
+    // spans are intervals whose ends grow with the row: the tile's steps are [lo(first row), hi(last row)), and the
+    // steps every row of this wave takes are [lo(its last row), hi(its first row))
+    int64_t t_lo, t_hi, w_lo, w_hi, dummy;
+    row_span(p, i0, n, I, &t_lo, &dummy);
+    row_span(p, (i0 + kTileRows - 1 < I ? i0 + kTileRows - 1 : I - 1), n, I, &dummy, &t_hi);
+    const int64_t tw = i0 + wave * 16;
+    if (tw < I) {
+        row_span(p, tw, n, I, &dummy, &w_hi);
+        row_span(p, (tw + 15 < I ? tw + 15 : I - 1), n, I, &w_lo, &dummy);
+    } else {
+        w_lo = w_hi = 0;
+    }
+    const void* A = kAFloat ? static_cast<const void*>(op_base<float>(o.A, w, seg_w, hz))
+                            : static_cast<const void*>(op_base<double>(o.A, w, seg_w, hz));
+    const float* B = op_base<float>(o.B, w, seg_w, hz);
+    const int64_t chunk = j0 + 4 * (lane % (16 * CJ));
+    const int64_t b_col = chunk + 4 <= p.b_row_alloc ? chunk : p.b_row_alloc - 4;
+    double acc[16][CJ];
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+#pragma unroll
+        for (int c = 0; c < CJ; ++c) acc[q][c] = 0.0;
+    const int64_t steps = t_hi - t_lo;
+    const int64_t stages = steps > 0 ? (steps + kChunk - 1) / kChunk : 0;
+    const int64_t last = t_hi - 1;
+    if (stages > 0)
+        issue_stage<CJ, kAFloat>(st[0], A, o.A, i0, I, p.a_row_alloc, B, o.B, b_col, t_lo, last, wave, lane);
+    for (int64_t s = 0; s < stages; ++s) {
+        if (s + 1 < stages) {
+            issue_stage<CJ, kAFloat>(st[(s + 1) & 1], A, o.A, i0, I, p.a_row_alloc, B, o.B, b_col,
+                                     t_lo + (s + 1) * kChunk, last, wave, lane);
+            wait_stage<stage_copies<CJ, kAFloat>()>();
+        } else {
+            wait_stage<0>();
+        }
+        const int64_t l0 = t_lo + s * kChunk;
+        const int n_steps = static_cast<int>(t_hi - l0 < kChunk ? t_hi - l0 : kChunk);
+        if constexpr (kExact) {  // every row takes every step: full stages here, a partial last one after the loop
+            if (n_steps < kChunk) break;
+            stage_all<CJ, kAFloat, kExact>(st[s & 1], wave, lane, acc);
+        } else {
+            if (n_steps == kChunk && l0 >= w_lo && l0 + kChunk <= w_hi)
+                stage_all<CJ, kAFloat, kExact>(st[s & 1], wave, lane, acc);
+            else
+                stage_masked<CJ, kAFloat, kExact>(p, st[s & 1], wave, lane, l0, n_steps, tw, n, I, acc);
+        }
+        workgroup_barrier();  // every wave is done with this stage before the next issue refills it
+    }
+    if constexpr (kExact) {
+        const int64_t full = steps / kChunk;
+        const int tail = static_cast<int>(steps - full * kChunk);
+        if (tail > 0)  // its copies were issued and waited for in the loop's last round
+            stage_masked<CJ, kAFloat, kExact>(p, st[full & 1], wave, lane, t_lo + full * kChunk, tail, tw, n, I, acc);
+    }
+    // the output rows' base and stride, opaque so the compiler keeps no per-element addresses across the reduction
+    const int64_t elem = kOutDouble ? 8 : 4;
+    char* c_base = reinterpret_cast<char*>(const_cast<void*>(o.C.ptr)) +
+                   (w * o.C.w_stride + seg_w * o.C.seg_stride + (hz / o.C.head_div) * o.C.head_stride +
+                    tw * o.C.ld + j0) * elem;
+    int64_t c_ld = o.C.ld * elem;
+    asm volatile("" : "+s"(c_base), "+s"(c_ld));
+    const double* rs = p.rowscale ? p.rowscale + z * p.rowscale_zstride + tw : nullptr;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        if (tw + q >= I) break;
+        const double scale = kOutDouble ? p.out_scale : (rs ? rs[q] : 1.0);
+#pragma unroll
+        for (int c = 0; c < CJ; ++c) {
+            const int64_t jl = lane * CJ + c;
+            if (j0 + jl >= J) continue;
+            if constexpr (kOutDouble) {
+                reinterpret_cast<double*>(c_base + q * c_ld)[jl] = acc[q][c] * scale;
+            } else {
+                double v = acc[q][c];
+                if (rs) v = v * scale;
+                reinterpret_cast<float*>(c_base + q * c_ld)[jl] = static_cast<float>(v);
+            }
+        }
+    }
+}
+
+Op op_of(const AttnOperand& o) {
+    return Op{o.ptr, o.w_stride, o.seg_stride, o.head_stride, o.head_div > 0 ? o.head_div : 1, o.ld, o.ld_inner,
+              o.group > 0 ? o.group : 1};
+}
+
+}  // namespace
+
+int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream) {
+    TileParams p{};
+    p.sets = c.second ? 2 : 1;
+    p.set[0] = OperandSet{op_of(c.A), op_of(c.B), op_of(c.C)};
+    p.set[1] = c.second ? OperandSet{op_of(c.A2), op_of(c.B2), op_of(c.C2)} : p.set[0];
+    p.rowscale = c.rowscale;
+    p.rowscale_zstride = c.rowscale_zstride;
+    p.out_scale = c.out_scale;
+    p.seg = c.seg;
+    p.heads = c.heads;
+    p.Z = c.windows * c.heads;
+    p.rows_kind = c.rows_kind;
+    p.cols_kind = c.cols_kind;
+    p.head_dim = c.head_dim;
+    p.group = c.group > 0 ? c.group : 1;
+    p.window = c.window;
+    p.L = c.L;
+    p.mask = c.mask;
+    const int64_t I = c.rows_kind == 0 ? c.max_len : c.head_dim;
+    const int64_t J = c.cols_kind == 0 ? c.max_len : c.head_dim;
+    const int cj = c.cols_per_lane;
+    p.b_row_alloc = c.b_row_alloc > 0 ? c.b_row_alloc : J;
+    p.a_row_alloc = c.a_row_alloc;
+    p.tiles_i = static_cast<int64_t>(ceil_div(I, kTileRows));
+    p.tiles_j = static_cast<int64_t>(ceil_div(J, 64 * cj));
+    DLLM_REQUIRE(cj == 1 || cj == 2 || cj == 4, "attention tiles are 64 rows x 64, 128 or 256 columns");
+    DLLM_REQUIRE(p.b_row_alloc % 4 == 0 && p.b_row_alloc >= J, "attention operand rows must hold whole 16-byte chunks");
+    if (c.a_float)
+        DLLM_REQUIRE(c.exact_products && cj == 4 && c.mask != kMaskQueryRows && c.mask != kMaskKeyRows &&
+                         p.a_row_alloc % 4 == 0 && p.a_row_alloc >= c.L && c.A.ld % 4 == 0,
+                     "float A operands are the scores' K or V rows (exact products over head_dim)");
+    else
+        DLLM_REQUIRE(c.A.ld % 2 == 0 && c.A.ld >= static_cast<int64_t>(round_up(static_cast<size_t>(I), kTileRows)),
+                     "attention double operand rows must be padded to whole 64-row tiles");
+    const int64_t blocks = p.tiles_i * p.tiles_j * p.Z * p.sets;
+    if (blocks == 0) return kOk;
+    DLLM_REQUIRE(blocks < (int64_t{1} << 31), "attention matmul grid too large");
+    const dim3 grid(static_cast<unsigned>(blocks));
+#define DLLM_ATTN_TILES(CJ, AF, EX, OD) \
+    hipLaunchKernelGGL((attn_tile_kernel<CJ, AF, EX, OD>), grid, dim3(256), 0, stream, p)
+    if (c.a_float) {
+        if (c.out_double) DLLM_ATTN_TILES(4, true, true, true);
+        else DLLM_ATTN_TILES(4, true, true, false);
+    } else {
+        DLLM_REQUIRE(!c.exact_products && !c.out_double,
+                     "double A operands are the probability and dS rows (multiply, then add; float outputs)");
+        if (cj == 2) DLLM_ATTN_TILES(2, false, false, false);
+        else if (cj == 1) DLLM_ATTN_TILES(1, false, false, false);
+        else return fail(kInvalidArgument, "double A operands take 64 or 128 columns per tile");
+    }
+#undef DLLM_ATTN_TILES
+    return check_launch("attention tiles");
+}
+
+}  // namespace dllm_hip

@@ -499,6 +499,34 @@ __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restr
     }
 }
 
+// Many transposes in one launch: workgroup -> job through the ascending tile-start table, then one 64 x 64 tile.
+__global__ __launch_bounds__(256) void transpose_batch_kernel(const TransposeJob* __restrict__ jobs,
+                                                              const int64_t* __restrict__ tile_start, int njobs) {
+    __shared__ float tile[64][65];
+    const int64_t id = blockIdx.x;
+    int lo = 0, hi = njobs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tile_start[mid] <= id) lo = mid;
+        else hi = mid - 1;
+    }
+    const TransposeJob jb = jobs[lo];
+    const int64_t t = id - tile_start[lo];
+    const int64_t tiles_c = (jb.cols + 63) / 64;
+    const int64_t r0 = t / tiles_c * 64, c0 = t % tiles_c * 64;
+    const int tx = threadIdx.x & 63;
+    const int ty = threadIdx.x >> 6;
+    for (int k = ty; k < 64; k += 4) {
+        const int64_t r = r0 + k, c = c0 + tx;
+        tile[k][tx] = (r < jb.rows && c < jb.cols) ? jb.src[r * jb.cols + c] : 0.0f;
+    }
+    __syncthreads();
+    for (int k = ty; k < 64; k += 4) {
+        const int64_t c = c0 + k, r = r0 + tx;
+        if (c < jb.cols && r < jb.rows) jb.dst[c * jb.rows + r] = tile[tx][k];
+    }
+}
+
 }  // namespace
 
 int64_t padded_rows(int64_t n) { return static_cast<int64_t>(round_up(static_cast<size_t>(n > 0 ? n : 1), kBlockI)); }
@@ -645,6 +673,25 @@ int launch_to_double(const float* src, int64_t rows, int64_t cols, int64_t lds, 
     DLLM_REQUIRE(grid.y <= 65535u, "too many rows for one conversion launch");
     hipLaunchKernelGGL(to_double_kernel, grid, dim3(256), 0, stream, src, rows, cols, lds, dst, ldd, dstT, lddT);
     return check_launch("to_double");
+}
+
+int64_t transpose_batch_tiles(const TransposeJob* jobs, int n, int64_t* tile_start) {
+    int64_t tiles = 0;
+    for (int k = 0; k < n; ++k) {
+        tile_start[k] = tiles;
+        tiles += static_cast<int64_t>(ceil_div(jobs[k].rows, 64) * ceil_div(jobs[k].cols, 64));
+    }
+    tile_start[n] = tiles;
+    return tiles;
+}
+
+int launch_transpose_batch(const TransposeJob* device_jobs, const int64_t* device_tile_start, int n, int64_t tiles,
+                           hipStream_t stream) {
+    if (tiles == 0) return kOk;
+    DLLM_REQUIRE(tiles < (int64_t{1} << 31), "too many transpose tiles for one launch");
+    hipLaunchKernelGGL(transpose_batch_kernel, dim3(static_cast<unsigned>(tiles)), dim3(256), 0, stream, device_jobs,
+                       device_tile_start, n);
+    return check_launch("transpose batch");
 }
 
 int launch_transpose_f32(const float* src, int64_t rows, int64_t cols, float* dst, hipStream_t stream) {

@@ -56,6 +56,16 @@ int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStrea
 int launch_to_double(const float* src, int64_t rows, int64_t cols, int64_t lds, double* dst, int64_t ldd,
                      double* dstT, int64_t lddT, hipStream_t stream);
 int launch_transpose_f32(const float* src, int64_t rows, int64_t cols, float* dst, hipStream_t stream);
+// dst = src^T for many matrices in one launch: transpose_batch_tiles fills the n + 1 tile starts (host) and returns
+// the tile count; the jobs and the starts are then passed in device memory.
+struct TransposeJob {
+    const float* src;
+    int64_t rows, cols;
+    float* dst;
+};
+int64_t transpose_batch_tiles(const TransposeJob* jobs, int n, int64_t* tile_start);
+int launch_transpose_batch(const TransposeJob* device_jobs, const int64_t* device_tile_start, int n, int64_t tiles,
+                           hipStream_t stream);
 
 // ---- row-local and elementwise kernels (rows.hip) ----
 

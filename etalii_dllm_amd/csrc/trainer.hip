@@ -232,13 +232,11 @@ struct dllm_hip_trainer {
     size_t lora_ws_bytes = 0;
     int8_t* q8_values = nullptr;
     float* q8_scales = nullptr;
-    // attention as batched matmuls (attn_gemm.hip): per (window, head) transposed operands and score matrices
+    // attention as batched matmuls (attn_lds.hip, attn_gemm.hip): per (window, head) transposed operands and score
+    // matrices
     int64_t Tp = 0;
-    double* attn_scratch = nullptr;  // running sums of the attention matmuls' float outputs
-    double* attn_dvec = nullptr;     // the softmax backward's per-query D
-    int64_t attn_scratch_doubles = 0;
-    double *attn_kt = nullptr, *attn_vt = nullptr, *attn_et = nullptr, *attn_inv = nullptr, *attn_dpt = nullptr,
-           *attn_pg = nullptr, *attn_dsg = nullptr;
+    double* attn_dvec = nullptr;  // the softmax backward's per-query D
+    double *attn_et = nullptr, *attn_inv = nullptr, *attn_dpt = nullptr, *attn_pg = nullptr, *attn_dsg = nullptr;
     float *attn_qt = nullptr, *attn_dot = nullptr;
 
     template <typename T>
@@ -500,8 +498,6 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&sin_t, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
         Tp = padded_rows(T_max);
         const int64_t hd = c.head_dim, G = heads / kvh;
-        DLLM_TRY(make(&attn_kt, W_max * kvh * hd * Tp));
-        DLLM_TRY(make(&attn_vt, W_max * kvh * hd * Tp));
         DLLM_TRY(make(&attn_qt, W_max * heads * hd * Tp));
         DLLM_TRY(make(&attn_dot, W_max * heads * hd * Tp));
         DLLM_TRY(make(&attn_et, c.layers * W_max * heads * Tp * Tp));  // E^T saved per layer for the backward
@@ -509,9 +505,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&attn_dpt, W_max * heads * Tp * Tp));
         DLLM_TRY(make(&attn_pg, W_max * kvh * Tp * G * Tp));
         DLLM_TRY(make(&attn_dsg, W_max * kvh * Tp * G * Tp));
-        attn_scratch_doubles = W_max * heads * T_max * hd;
         DLLM_TRY(make(&attn_dvec, W_max * heads * Tp));
-        DLLM_TRY(make(&attn_scratch, attn_scratch_doubles));
         DLLM_TRY(make(&tok_in, R));
         DLLM_TRY(make(&tok_tgt, R));
         DLLM_TRY(make(&pos_index, R));
@@ -596,13 +590,30 @@ struct dllm_hip_trainer {
         return kOk;
     }
 
-    // W^T of every linear weight for the forward matmuls.
+    // W^T of every linear weight for the forward matmuls, in one launch (the job table is made on first use: the
+    // weights' addresses, merged ones included, are fixed from then on).
+    TransposeJob* wt_jobs = nullptr;
+    int64_t* wt_tiles = nullptr;
+    int wt_njobs = 0;
+    int64_t wt_ntiles = 0;
+
     int refresh_transposes(hipStream_t s) {
-        for (size_t i = 0; i < tensors.size(); ++i) {
-            const TensorInfo& t = tensors[i];
-            if (t.wt_offset >= 0)
-                DLLM_TRY(launch_transpose_f32(P(static_cast<int>(i)), t.rows, t.cols, wt.as<float>() + t.wt_offset, s));
+        if (wt_jobs == nullptr) {
+            std::vector<TransposeJob> jobs;
+            for (size_t i = 0; i < tensors.size(); ++i) {
+                const TensorInfo& t = tensors[i];
+                if (t.wt_offset >= 0) jobs.push_back({P(static_cast<int>(i)), t.rows, t.cols, wt.as<float>() + t.wt_offset});
+            }
+            std::vector<int64_t> starts(jobs.size() + 1);
+            wt_njobs = static_cast<int>(jobs.size());
+            wt_ntiles = transpose_batch_tiles(jobs.data(), wt_njobs, starts.data());
+            DLLM_TRY(make(&wt_jobs, std::max<size_t>(jobs.size(), 1)));
+            DLLM_TRY(make(&wt_tiles, starts.size()));
+            DLLM_TRY(check_hip(hipMemcpy(wt_jobs, jobs.data(), jobs.size() * sizeof(TransposeJob),
+                                         hipMemcpyHostToDevice), "upload"));
+            DLLM_TRY(check_hip(hipMemcpy(wt_tiles, starts.data(), starts.size() * 8, hipMemcpyHostToDevice), "upload"));
         }
+        if (wt_njobs > 0) DLLM_TRY(launch_transpose_batch(wt_jobs, wt_tiles, wt_njobs, wt_ntiles, s));
         wt_valid = true;
         return kOk;
     }
@@ -708,12 +719,9 @@ struct dllm_hip_trainer {
     // query, out = (E V) inv.
     int attention_forward(int64_t l, const Saved& sv, const AttentionBatch& b, hipStream_t s) {
         const int64_t nh = c.heads, nkv = c.kv_heads, hd = c.head_dim, G = nh / nkv, n = b.max_q;
-        DLLM_TRY(launch_heads_transpose(sv.k, KVD, hd, attn_kt, true, Tp, hd * Tp, seg_d, nwin, nkv, n, s));
         DLLM_TRY(launch_heads_transpose(sv.q, QD, hd, attn_qt, false, Tp, hd * Tp, seg_d, nwin, nh, n, s));
         double* et = et_of(l);
-        AttnGemmCall g;
-        g.scratch = attn_scratch;
-        g.scratch_doubles = attn_scratch_doubles;
+        AttnTileCall g;
         g.seg = seg_d;
         g.windows = nwin;
         g.heads = nh;
@@ -721,8 +729,10 @@ struct dllm_hip_trainer {
         g.head_dim = hd;
         g.group = G;
         g.window = c.sliding_window;
-        // S^T[j][t] = sum_i k[j][i] q[t][i], times scale
-        g.A = AttnOperand{attn_kt, nkv * hd * Tp, 0, hd * Tp, G, Tp, 0, 1};
+        // S^T[j][t] = sum_i k[j][i] q[t][i], times scale: A = the key rows themselves, read transposed
+        g.A = AttnOperand{sv.k, 0, KVD, hd, G, KVD, 0, 1};
+        g.a_float = true;
+        g.a_row_alloc = hd;
         g.B = AttnOperand{attn_qt, nh * hd * Tp, 0, hd * Tp, 1, Tp, 0, 1};
         g.C = AttnOperand{et, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
         g.rows_kind = 0;
@@ -734,35 +744,36 @@ struct dllm_hip_trainer {
         g.exact_products = true;
         g.out_double = true;
         g.out_scale = c.attention_scale;
-        DLLM_TRY(launch_attn_gemm(g, s));
+        DLLM_TRY(launch_attn_tiles(g, s));
         DLLM_TRY(launch_softmax_rows(et, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp, s));
         // out[t] = f32((sum_j e_j v_j) inv_t)
-        AttnGemmCall o = g;
+        AttnTileCall o = g;
         o.A = AttnOperand{et, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
-        o.B = AttnOperand{sv.v, 0, nkv * hd, hd, G, nkv * hd, 0, 1};
-        o.C = AttnOperand{sv.attended, 0, nh * hd, hd, 1, nh * hd, 0, 1};
+        o.a_float = false;
+        o.B = AttnOperand{sv.v, 0, KVD, hd, G, KVD, 0, 1};
+        o.C = AttnOperand{sv.attended, 0, QD, hd, 1, QD, 0, 1};
         o.rows_kind = 0;
         o.cols_kind = 1;
         o.L = 0;
         o.mask = kMaskQueryRows;
-        o.cols_per_lane = hd >= 128 ? 2 : 1;
+        o.cols_per_lane = value_cols_per_lane();
         o.b_row_alloc = 0;
         o.exact_products = false;
         o.out_double = false;
         o.rowscale = inv_of(l);
         o.rowscale_zstride = Tp;
-        return launch_attn_gemm(o, s);
+        return launch_attn_tiles(o, s);
     }
+
+    // Columns per lane of the head_dim-wide attention outputs: whole 64-column tiles of head_dim.
+    int value_cols_per_lane() const { return c.head_dim > 64 ? 2 : 1; }
 
     // attention_backward (grad.hpp:206-301) of every (window, head): dq_t, dk_t, dv_t from dattended.
     int attention_backward(int64_t l, const Saved& sv, const AttentionBatch& b, hipStream_t s) {
         const int64_t nh = c.heads, nkv = c.kv_heads, hd = c.head_dim, G = nh / nkv, n = b.max_q;
         double* et = et_of(l);
-        DLLM_TRY(launch_heads_transpose(sv.v, KVD, hd, attn_vt, true, Tp, hd * Tp, seg_d, nwin, nkv, n, s));
         DLLM_TRY(launch_heads_transpose(dattended, QD, hd, attn_dot, false, Tp, hd * Tp, seg_d, nwin, nh, n, s));
-        AttnGemmCall g;
-        g.scratch = attn_scratch;
-        g.scratch_doubles = attn_scratch_doubles;
+        AttnTileCall g;
         g.seg = seg_d;
         g.windows = nwin;
         g.heads = nh;
@@ -771,7 +782,9 @@ struct dllm_hip_trainer {
         g.group = G;
         g.window = c.sliding_window;
         // dP^T[j][t] = sum_i v[j][i] dout[t][i]
-        g.A = AttnOperand{attn_vt, nkv * hd * Tp, 0, hd * Tp, G, Tp, 0, 1};
+        g.A = AttnOperand{sv.v, 0, KVD, hd, G, KVD, 0, 1};
+        g.a_float = true;
+        g.a_row_alloc = hd;
         g.B = AttnOperand{attn_dot, nh * hd * Tp, 0, hd * Tp, 1, Tp, 0, 1};
         g.C = AttnOperand{attn_dpt, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
         g.rows_kind = 0;
@@ -783,47 +796,40 @@ struct dllm_hip_trainer {
         g.exact_products = true;
         g.out_double = true;
         g.out_scale = 1.0;
-        DLLM_TRY(launch_attn_gemm(g, s));
+        DLLM_TRY(launch_attn_tiles(g, s));
         // p = e inv, D, ds = p (dp - D) scale (in place over E^T and dP^T)
         DLLM_TRY(launch_dsoftmax_rows(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp,
                                       c.attention_scale, attn_dvec, s));
         // dq[t] = sum_j ds[t][j] k[j]
-        AttnGemmCall q = g;
+        AttnTileCall q = g;
         q.A = AttnOperand{attn_dpt, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
-        q.B = AttnOperand{sv.k, 0, nkv * hd, hd, G, nkv * hd, 0, 1};
-        q.C = AttnOperand{dq_t, 0, nh * hd, hd, 1, nh * hd, 0, 1};
+        q.a_float = false;
+        q.B = AttnOperand{sv.k, 0, KVD, hd, G, KVD, 0, 1};
+        q.C = AttnOperand{dq_t, 0, QD, hd, 1, QD, 0, 1};
         q.cols_kind = 1;
         q.L = 0;
         q.mask = kMaskQueryRows;
-        q.cols_per_lane = hd >= 128 ? 2 : 1;
+        q.cols_per_lane = value_cols_per_lane();
         q.b_row_alloc = 0;
         q.exact_products = false;
         q.out_double = false;
-        DLLM_TRY(launch_attn_gemm(q, s));
+        DLLM_TRY(launch_attn_tiles(q, s));
         // key-row operands: [w][g][(t, hh)][j]
         const int64_t gz = Tp * G * Tp;
         DLLM_TRY(launch_regroup(attn_dpt, Tp, Tp * Tp, attn_dsg, Tp, gz, seg_d, nwin, nh, G, n, s));
         DLLM_TRY(launch_regroup(et, Tp, Tp * Tp, attn_pg, Tp, gz, seg_d, nwin, nh, G, n, s));
-        // dk[j] = sum over (t, hh) of ds q, dv[j] = sum of p dout
-        AttnGemmCall k = g;
+        // dk[j] = sum over (t, hh) of ds q and dv[j] = sum of p dout, in one launch
+        AttnTileCall k = q;
         k.heads = nkv;
         k.A = AttnOperand{attn_dsg, nkv * gz, 0, gz, 1, Tp, 0, 1};
-        k.B = AttnOperand{sv.q, 0, nh * hd, G * hd, 1, nh * hd, hd, G};
-        k.C = AttnOperand{dk_t, 0, nkv * hd, hd, 1, nkv * hd, 0, 1};
-        k.cols_kind = 1;
-        k.L = 0;
+        k.B = AttnOperand{sv.q, 0, QD, G * hd, 1, QD, hd, G};
+        k.C = AttnOperand{dk_t, 0, KVD, hd, 1, KVD, 0, 1};
+        k.second = true;
+        k.A2 = AttnOperand{attn_pg, nkv * gz, 0, gz, 1, Tp, 0, 1};
+        k.B2 = AttnOperand{dattended, 0, QD, G * hd, 1, QD, hd, G};
+        k.C2 = AttnOperand{dv_t, 0, KVD, hd, 1, KVD, 0, 1};
         k.mask = kMaskKeyRows;
-        k.cols_per_lane = 1;  // long serial chains: more, smaller tiles
-        k.tile_rows = 8;
-        k.b_row_alloc = 0;
-        k.exact_products = false;
-        k.out_double = false;
-        DLLM_TRY(launch_attn_gemm(k, s));
-        AttnGemmCall v = k;
-        v.A = AttnOperand{attn_pg, nkv * gz, 0, gz, 1, Tp, 0, 1};
-        v.B = AttnOperand{dattended, 0, nh * hd, G * hd, 1, nh * hd, hd, G};
-        v.C = AttnOperand{dv_t, 0, nkv * hd, hd, 1, nkv * hd, 0, 1};
-        return launch_attn_gemm(v, s);
+        return launch_attn_tiles(k, s);
     }
 
     // One layer's forward (backprop.py:423-487).

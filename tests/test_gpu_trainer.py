@@ -237,3 +237,28 @@ def test_moe_lora_step_matches_the_oracle():
         assert loss_gpu == loss_cpu and norm_gpu == norm_cpu
         for name, value in state.items():
             assert t.get(name, value.shape).tobytes() == value.tobytes(), name
+
+
+@pytest.mark.parametrize("window", [0, 100])
+def test_attention_at_head_dim_128_matches_the_oracle(window):
+    """The attention matmuls at their real tile shapes (head_dim 128: two 64-column tiles per lane; several 64-row
+    tiles; grouped heads), causal and sliding-window, on windows of 300, 129 and 64 tokens: every gradient of one
+    gradients() call against the oracle."""
+    d = O.Decoder("mistral", vocab=256, hidden=128, inter=128, layers=1, heads=4, kv_heads=2, head_dim=128,
+                  eps=1e-5, rope_theta=1e4, tied=False, window=window)
+    weights = O.synthetic_weights(d, seed=31, scale=0.05)
+    rng = O.Random(37)
+    windows = [[rng.next_u64() % d.vocab for _ in range(n)] for n in (301, 130, 65)]
+    t = make_trainer(d, weights, max_tokens=512, max_windows=4, max_window=320)
+    scale = 1.0 / sum(len(w) - 1 for w in windows)
+    loss = t.gradients(windows, scale=scale)
+    kern = O.oracle_kernels()
+    want_loss, want = 0.0, {}
+    for w in windows:
+        l, _, g = O.window_gradients(kern, d, weights, w[:-1], w[1:], scale=scale)
+        want_loss += l
+        for name, value in g.items():
+            want[name] = want[name] + value if name in want else value.copy()
+    assert loss == want_loss
+    for name in t.names:
+        assert t.get(name, d.tensor_shapes()[name], t.GRAD).tobytes() == want[name].tobytes(), name
