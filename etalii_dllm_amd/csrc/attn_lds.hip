@@ -1,4 +1,4 @@
-// The attention matmuls of the training step (attn_gemm.h) as 64-row tiles through a double-buffered LDS pipeline,
+// The attention matmuls of the training step (attn_step.h) as 64-row tiles through a double-buffered LDS pipeline,
 // one workgroup of four waves per tile, every (window, head) of the step in one launch.
 //
 // Each output is C[i][j] = sum over l in row i's span, ascending, of A[l][i] * B[l][j] (then times a row scale or a
@@ -19,7 +19,7 @@
 // own steps, in order, and nothing else. Tiles are dispatched longest reduction first.
 #include <type_traits>
 
-#include "attn_gemm.h"
+#include "attn_step.h"
 #include "common.h"
 #include "kernels.h"
 

@@ -1,0 +1,63 @@
+// Launchers of the training step's attention: batched matmuls (attn_lds.hip) and per-query chains (attn_chains.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dllm_hip {
+
+enum AttnMask {
+    kMaskNone = 0,
+    kMaskQueryRows = 1,   // rows are queries t; reduce over the keys t sees, ascending
+    kMaskKeyRows = 2,     // rows are keys j; reduce over (query, head of the group) pairs that see j, ascending
+    kMaskTileCausal = 3,  // output [key][query] tiles nothing can see are skipped (scores, dP)
+};
+
+// Where operand rows live for batch entry z = (window w, head hz):
+// base = ptr + w * w_stride + seg[w] * seg_stride + (hz / head_div) * head_stride, row(l) = (l / group) * ld +
+// (l % group) * ld_inner (elements of the operand's type).
+struct AttnOperand {
+    const void* ptr = nullptr;
+    int64_t w_stride = 0, seg_stride = 0, head_stride = 0, head_div = 1;
+    int64_t ld = 0, ld_inner = 0, group = 1;
+};
+
+// One attention matmul (attn_lds.hip) over every (window, head) z = w * heads + hz of a step:
+// C[i][j] = sum over l in row i's span, ascending, of A[l][i] * B[l][j], times a row scale or a constant.
+// A is double [L][rows padded to 64] (products multiply-then-add, float output, 64 or 128 columns per tile) or, for
+// the scores and dP, float rows A[i][l] read transposed (a_float: exact products, 256 columns per tile). `second`
+// runs a second matmul of the same shape in the same launch (dk and dv).
+struct AttnTileCall {
+    AttnOperand A, B, C;
+    bool second = false;
+    AttnOperand A2, B2, C2;
+    const double* rowscale = nullptr;  // float outputs: row multiplier before rounding, [z][row]
+    int64_t rowscale_zstride = 0;
+    const int64_t* seg = nullptr;  // device window offsets
+    int64_t windows = 0, heads = 0, max_len = 0, head_dim = 0, group = 1, window = 0, L = 0;
+    int rows_kind = 0, cols_kind = 0;  // 0: window positions, 1: head_dim
+    int mask = kMaskNone;
+    int cols_per_lane = 4;    // 1, 2 or 4: a workgroup covers 64 x cols_per_lane columns
+    int64_t b_row_alloc = 0;  // floats readable per B row from column 0 (multiple of 4, >= J); 0: J
+    bool a_float = false;
+    int64_t a_row_alloc = 0;  // a_float: floats readable in each A row (multiple of 4, >= L)
+    bool exact_products = true;  // float x float products: fused multiply-add is exact
+    bool out_double = false;
+    double out_scale = 1.0;
+};
+
+int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream);
+int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
+                        int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream);
+// The softmax backward (grad.hpp:262-278): D per query (dvec: windows * heads * inv_zstride doubles of workspace),
+// then ds written over dpt and p, ds in the key-row layout of dk / dv:
+// pg / dsg[w][g][(t * group + hh)][j] (dst_ld per row, dst_zstride per (window, kv head)).
+int launch_dsoftmax_regroup(const double* et, double* dpt, int64_t ld, int64_t zstride, const int64_t* seg,
+                            int64_t windows, int64_t heads, int64_t group, int64_t max_len, int64_t window,
+                            const double* inv, int64_t inv_zstride, double scale, double* dvec, double* pg,
+                            double* dsg, int64_t dst_ld, int64_t dst_zstride, hipStream_t stream);
+int launch_heads_transpose(const float* src, int64_t row_stride, int64_t head_dim, void* dst, bool to_double,
+                           int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
+                           int64_t max_len, hipStream_t stream);
+
+}  // namespace dllm_hip

@@ -28,7 +28,7 @@
 #include <string>
 #include <vector>
 
-#include "attn_gemm.h"
+#include "attn_step.h"
 #include "common.h"
 #include "devmath.h"
 #include "dllm_hip.h"
@@ -232,7 +232,7 @@ struct dllm_hip_trainer {
     size_t lora_ws_bytes = 0;
     int8_t* q8_values = nullptr;
     float* q8_scales = nullptr;
-    // attention as batched matmuls (attn_lds.hip, attn_gemm.hip): per (window, head) transposed operands and score
+    // attention as batched matmuls (attn_lds.hip, attn_chains.hip): per (window, head) transposed operands and score
     // matrices
     int64_t Tp = 0;
     double* attn_dvec = nullptr;  // the softmax backward's per-query D
@@ -709,7 +709,7 @@ struct dllm_hip_trainer {
         return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s);
     }
 
-    // ---- attention (attn_gemm.hip) ----
+    // ---- attention (attn_lds.hip, attn_chains.hip) ----
     int64_t nwin = 0;  // windows of the current step
 
     double* et_of(int64_t l) const { return attn_et + l * W_max * c.heads * Tp * Tp; }
@@ -797,9 +797,11 @@ struct dllm_hip_trainer {
         g.out_double = true;
         g.out_scale = 1.0;
         DLLM_TRY(launch_attn_tiles(g, s));
-        // p = e inv, D, ds = p (dp - D) scale (in place over E^T and dP^T)
-        DLLM_TRY(launch_dsoftmax_rows(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp,
-                                      c.attention_scale, attn_dvec, s));
+        // D, p = e inv and ds = p (dp - D) scale: ds over dP^T (dq's operand), p and ds in the key-row layout
+        // [w][g][(t, hh)][j] of dk and dv
+        const int64_t gz = Tp * G * Tp;
+        DLLM_TRY(launch_dsoftmax_regroup(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, G, n, c.sliding_window, inv_of(l),
+                                         Tp, c.attention_scale, attn_dvec, attn_pg, attn_dsg, Tp, gz, s));
         // dq[t] = sum_j ds[t][j] k[j]
         AttnTileCall q = g;
         q.A = AttnOperand{attn_dpt, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
@@ -814,10 +816,6 @@ struct dllm_hip_trainer {
         q.exact_products = false;
         q.out_double = false;
         DLLM_TRY(launch_attn_tiles(q, s));
-        // key-row operands: [w][g][(t, hh)][j]
-        const int64_t gz = Tp * G * Tp;
-        DLLM_TRY(launch_regroup(attn_dpt, Tp, Tp * Tp, attn_dsg, Tp, gz, seg_d, nwin, nh, G, n, s));
-        DLLM_TRY(launch_regroup(et, Tp, Tp * Tp, attn_pg, Tp, gz, seg_d, nwin, nh, G, n, s));
         // dk[j] = sum over (t, hh) of ds q and dv[j] = sum of p dout, in one launch
         AttnTileCall k = q;
         k.heads = nkv;

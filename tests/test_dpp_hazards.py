@@ -17,7 +17,7 @@ import pytest
 
 from etalii_dllm_amd import build as B
 
-SOURCES = ["gemm.hip", "attn_gemm.hip", "attn_lds.hip"]
+SOURCES = ["gemm.hip", "attn_lds.hip"]
 
 
 def _regs(token: str) -> set[int]:
