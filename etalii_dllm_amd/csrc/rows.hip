@@ -25,12 +25,25 @@ __device__ __forceinline__ double norm_scale_backward(const float* w, int64_t i,
     return (unit_offset ? 1.0 : 0.0) + static_cast<double>(w[i]);
 }
 
-constexpr int kNormRows = 32;  // rows per 256-thread workgroup of the norm kernels
+constexpr int kNormRows = 16;  // rows per 256-thread workgroup of the norm kernels
 
-// rms_norm (nn.hpp:391-408) and rms_norm_backward's dx (grad.hpp:83-104), 32 rows per workgroup. Per row the serial
-// chains run one lane per row out of LDS: the four waves stage the terms of 32 rows x 64 columns (x^2, and for the
-// backward (g dy) x), then lanes 0-31 of wave 0 add the squares and lanes 32-63 the products, 64 columns at a time in
-// ascending order. Then every thread writes its elements:
+// Adds terms[0 .. n) to `chain` in index order, reading them from LDS 16 at a time ahead of the dependent adds.
+__device__ __forceinline__ void chain_add(double& chain, const double* terms, int n) {
+    int k = 0;
+    for (; k + 16 <= n; k += 16) {
+        double v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = terms[k + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) chain += v[u];
+    }
+    for (; k < n; ++k) chain += terms[k];
+}
+
+// rms_norm (nn.hpp:391-408) and rms_norm_backward's dx (grad.hpp:83-104), 16 rows per workgroup. Per row the serial
+// chains run one lane per row out of LDS: the four waves stage the terms of 16 rows x 64 columns (x^2, and for the
+// backward (g dy) x) in one of two buffers, then lanes 0-15 of wave 0 add the squares and lanes 16-31 the products
+// in ascending column order, while the next 64 columns' loads are in flight. Then every thread writes its elements:
 //   forward   out = f32((x inv) scale),              inv = 1 / sqrt(sum x^2 / dim + eps)
 //   backward  dx = f32((inv g) dy - x coef) (+ addend), coef = D inv inv inv / dim, D = sum (g dy) x
 template <bool kBackward>
@@ -38,37 +51,51 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
                                                         const float* __restrict__ dy, float* __restrict__ out,
                                                         const float* __restrict__ addend, int64_t rows, int64_t dim,
                                                         double eps, int unit_offset, double* __restrict__ inv_out) {
-    __shared__ double squares[kNormRows][65];
-    __shared__ double products[kNormRows][65];
+    constexpr int kPer = kNormRows / 4;  // rows each wave stages
+    __shared__ double squares[2][kNormRows][65];
+    __shared__ double products[kBackward ? 2 : 1][kBackward ? kNormRows : 1][65];
     __shared__ double row_inv[kNormRows], row_coef[kNormRows];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kNormRows;
     const int64_t nrows = rows - r0 < kNormRows ? rows - r0 : kNormRows;
-    double chain = 0.0;  // wave 0: lanes 0-31 the squares of row lane, lanes 32-63 the products of row lane - 32
-    for (int64_t c0 = 0; c0 < dim; c0 += 64) {
-        const int n = static_cast<int>(dim - c0 < 64 ? dim - c0 : 64);
-        if (lane < n) {
-            const int64_t col = c0 + lane;
-            const double g = kBackward ? norm_scale_backward(w, col, unit_offset) : 0.0;
+    const int64_t chunks = (dim + 63) / 64;
+    float xv[kPer], dv[kPer];
+    auto load = [&](int64_t c) {  // this thread's x (and dy) of chunk c, rows wave * kPer + k
+        const int64_t col = c * 64 + lane;
 #pragma unroll
-            for (int k = 0; k < kNormRows / 4; ++k) {
-                const int r = wave * (kNormRows / 4) + k;
-                if (r < nrows) {
-                    const double xv = static_cast<double>(x[(r0 + r) * dim + col]);
-                    squares[r][lane] = xv * xv;
-                    if (kBackward) products[r][lane] = g * static_cast<double>(dy[(r0 + r) * dim + col]) * xv;
-                }
-            }
+        for (int k = 0; k < kPer; ++k) {
+            const int r = wave * kPer + k;
+            const bool in = col < dim && r < nrows;
+            xv[k] = in ? x[(r0 + r) * dim + col] : 0.0f;
+            if (kBackward) dv[k] = in ? dy[(r0 + r) * dim + col] : 0.0f;
         }
-        __syncthreads();
+    };
+    auto store = [&](int64_t c) {
+        const int64_t col = c * 64 + lane;
+        const double g = kBackward && col < dim ? norm_scale_backward(w, col, unit_offset) : 0.0;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int r = wave * kPer + k;
+            const double xd = static_cast<double>(xv[k]);
+            squares[c & 1][r][lane] = xd * xd;
+            if (kBackward) products[c & 1][r][lane] = g * static_cast<double>(dv[k]) * xd;
+        }
+    };
+    double chain = 0.0;  // wave 0: lanes 0-15 the squares of row lane, lanes 16-31 the products of row lane - 16
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t c = 0; c < chunks; ++c) {
+        if (c + 1 < chunks) load(c + 1);
+        const int n = static_cast<int>(dim - c * 64 < 64 ? dim - c * 64 : 64);
         if (wave == 0) {
-            if (lane < kNormRows) {
-                for (int k = 0; k < n; ++k) chain += squares[lane][k];
-            } else if (kBackward) {
-                for (int k = 0; k < n; ++k) chain += products[lane - kNormRows][k];
-            }
+            if (lane < kNormRows)
+                chain_add(chain, &squares[c & 1][lane][0], n);
+            else if (kBackward && lane < 2 * kNormRows)
+                chain_add(chain, &products[c & 1][lane - kNormRows][0], n);
         }
+        if (c + 1 < chunks) store(c + 1);
         __syncthreads();
     }
     if (wave == 0 && lane < kNormRows && lane < nrows) {
@@ -77,7 +104,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
         if (inv_out) inv_out[r0 + lane] = inv;
     }
     __syncthreads();
-    if (kBackward && wave == 0 && lane >= kNormRows && lane - kNormRows < nrows) {
+    if (kBackward && wave == 0 && lane >= kNormRows && lane < 2 * kNormRows && lane - kNormRows < nrows) {
         const double inv = row_inv[lane - kNormRows];
         row_coef[lane - kNormRows] = chain * inv * inv * inv / static_cast<double>(dim);
     }
@@ -110,34 +137,57 @@ struct ColSegments {
 };
 
 // part[s][i] = f32(sum over rows r of segment s, ascending, of term(r, i)) for 64 columns per workgroup: the four
-// waves stage the terms of 64 rows x 64 columns in LDS (64 independent loads in flight per lane group), then one
-// wave runs the 64 serial additions per column out of LDS, and the next 64 rows follow.
+// waves stage the terms of 64 rows x 64 columns in one of two LDS buffers, then one wave runs the 64 serial
+// additions per column while the next 64 rows' loads are in flight.
 __global__ __launch_bounds__(256) void column_partial_kernel(int kind, const float* __restrict__ dy,
                                                              const float* __restrict__ x,
                                                              const double* __restrict__ inv, int64_t dim,
                                                              ColSegments seg, float* __restrict__ part) {
-    __shared__ double terms[64][64];
+    __shared__ double terms[2][64][64];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 64 + lane;
     const int64_t col = i < dim ? i : dim - 1;
     const int64_t r0 = seg.off[blockIdx.y], r1 = seg.off[blockIdx.y + 1];
-    double acc = 0.0;
-    for (int64_t base = r0; base < r1; base += 64) {
-        const int n = static_cast<int>(r1 - base < 64 ? r1 - base : 64);
+    const int64_t blocks = (r1 - r0 + 63) / 64;
+    double tv[16];
+    auto load = [&](int64_t b) {  // rows wave + 4 k of block b
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-            const int row = wave + 4 * k;
-            if (row < n) {
-                const int64_t r = base + row;
-                double t = static_cast<double>(dy[r * dim + col]);
+            const int64_t r = r0 + b * 64 + wave + 4 * k;
+            double t = 0.0;
+            if (r < r1) {
+                t = static_cast<double>(dy[r * dim + col]);
                 if (kind != 0) t = t * static_cast<double>(x[r * dim + col]) * inv[r];
-                terms[row][lane] = t;
             }
+            tv[k] = t;
         }
-        __syncthreads();
-        if (wave == 0)
-            for (int row = 0; row < n; ++row) acc += terms[row][lane];
+    };
+    auto store = [&](int64_t b) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) terms[b & 1][wave + 4 * k][lane] = tv[k];
+    };
+    double acc = 0.0;
+    if (blocks > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int64_t b = 0; b < blocks; ++b) {
+        if (b + 1 < blocks) load(b + 1);
+        const int n = static_cast<int>(r1 - r0 - b * 64 < 64 ? r1 - r0 - b * 64 : 64);
+        if (wave == 0) {
+            int row = 0;
+            for (; row + 16 <= n; row += 16) {
+                double v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v[u] = terms[b & 1][row + u][lane];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) acc += v[u];
+            }
+            for (; row < n; ++row) acc += terms[b & 1][row][lane];
+        }
+        if (b + 1 < blocks) store(b + 1);
         __syncthreads();
     }
     if (wave == 0 && i < dim) part[static_cast<int64_t>(blockIdx.y) * dim + i] = static_cast<float>(acc);
