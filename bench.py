@@ -249,8 +249,8 @@ def _counter_rows(path: str, kernel_substring: str, counter: str) -> list[float]
 def traffic_summary(config: str, fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_csv: str) -> int:
     """HBM bytes per matmul launch = mean(FETCH_SIZE) x fetch scale + mean(WRITE_SIZE) x write scale, the scales
     being the copy kernel's known bytes over what the same counters read for it (counters are in KiB)."""
-    fetch = _counter_rows(fetch_csv, "gemm_lds_kernel", "FETCH_SIZE")
-    write = _counter_rows(write_csv, "gemm_lds_kernel", "WRITE_SIZE")
+    fetch = _counter_rows(fetch_csv, "gemm_mfma_kernel", "FETCH_SIZE")
+    write = _counter_rows(write_csv, "gemm_mfma_kernel", "WRITE_SIZE")
     copy_fetch = max(_counter_rows(copy_fetch_csv, "copy", "FETCH_SIZE") or
                      _counter_rows(copy_fetch_csv, "elementwise", "FETCH_SIZE"))
     copy_write = max(_counter_rows(copy_write_csv, "copy", "WRITE_SIZE") or
@@ -365,7 +365,7 @@ def main() -> int:
                    "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic,
-                     "kernel": "gemm_lds_kernel (FP64 FMA matmul, all launches of the timed steps)",
+                     "kernel": "gemm_mfma_kernel (FP64 MFMA matmul, all launches of the timed steps)",
                      "step_fraction_of_peak": matmul_flops_per_step(cfg) / (ms_per_step * 1e9) / FP64_PEAK_TFLOPS},
         "cpu_baseline": baseline,
     }

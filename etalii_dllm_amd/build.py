@@ -29,6 +29,8 @@ FLAGS = [
     "-ffp-contract=off",
     "-fno-fast-math",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core accumulators in architectural VGPRs (no AGPR copies around each MFMA)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
 ]

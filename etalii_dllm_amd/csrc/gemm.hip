@@ -441,6 +441,246 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// FP64 matrix-core matmul (float A operands: every matmul of the training step).
+//
+// v_mfma_f64_16x16x4_f64 computes D[i][j] = C[i][j] + A[i][0]B[0][j] + ... + A[i][3]B[3][j] as four FMAs in
+// ascending k, each rounded: exactly the serial chain acc = fma(a_l, b_l, acc) over l ascending. Issued once per 4
+// consecutive l on the same accumulator, the instruction sequence is the reference's single double accumulator per
+// output over l ascending, rounded to float once. The operands are floats converted to double, so every product is
+// exact and each FMA rounds like the reference's multiply-then-add. Register layout (wave64): lane L supplies
+// A[i = L % 16][k = L / 16] and B[k = L / 16][j = L % 16]; accumulator register r of lane L is D[L / 16 + 4r][L % 16].
+//
+// Padding: a stage whose l range ends inside a 4-l step feeds +0.0 in both operands for the missing l. The product is
+// +0.0 and the accumulator is never -0.0 (it starts at +0.0, and a round-to-nearest sum is -0.0 only when both
+// addends are), so acc + 0 == acc bit for bit, infinities and NaNs included.
+//
+// Mapping: a workgroup computes a 128 i x 128 j tile with 4 waves in a 2 x 2 grid; a wave owns 64 x 64 outputs as
+// 4 x 4 MFMA blocks (128 accumulator VGPRs). Stages of 16 l (both operands, 16 KB) are copied global -> LDS with
+// direct-to-LDS loads, double-buffered; per 4-l step a wave reads 8 fragment values from LDS, converts them, and
+// issues 16 MFMAs (1024 cycles of matrix-core work).
+typedef double mf_v4d __attribute__((ext_vector_type(4)));
+constexpr int kMTileI = 128;  // workgroup tile along i
+constexpr int kMTileJ = 128;  // workgroup tile along j
+constexpr int kMStage = 16;   // l per LDS stage
+constexpr int kMWave = 64;    // wave tile edge (4 MFMA blocks of 16)
+
+template <int kA>
+struct MStage {
+    float a[kMStage * kMTileI];  // A rows: [l][i]; A transposed: [l / 4][i][l % 4]
+    float b[kMStage * kMTileJ];  // [l][j]
+};
+
+// Copies stage rows l .. l + 15 of both operands (rows past `last` repeat row `last`; their values are masked).
+// Each operand is 512 16-byte pieces, two per thread; piece ids run contiguously over a wave, so one instruction fills
+// 1 KB of LDS from M0.
+template <int kA>
+__device__ __forceinline__ void missue_stage(const GemmParams& p, MStage<kA>& st, int64_t i_blk, int64_t j_blk,
+                                             int64_t l, int64_t last, int tid) {
+    const int wave_base = tid & ~63;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int id = t * 256 + tid;
+        const int lds = (t * 256 + wave_base) * 4;  // float offset of this instruction's 1 KB
+        {
+            const int r = id >> 5, cc = id & 31;
+            const int64_t lr = l + r <= last ? l + r : last;
+            const int64_t j = j_blk + cc * 4 <= p.J - 4 ? j_blk + cc * 4 : p.J - 4;
+            copy16_to_lds(p.B + lr * p.ldb + j, &st.b[lds]);
+        }
+        if constexpr (kA == kAFloatRows) {
+            const int r = id >> 5, cc = id & 31;
+            const int64_t lr = l + r <= last ? l + r : last;
+            const int64_t i = i_blk + cc * 4 <= p.I - 4 ? i_blk + cc * 4 : p.I - 4;
+            copy16_to_lds(p.Af + lr * p.lda + i, &st.a[lds]);
+        } else {
+            const int c = id >> 7, ii = id & 127;
+            const int64_t row = i_blk + ii < p.I ? i_blk + ii : p.I - 1;
+            const int64_t lc = l + 4 * c <= p.l1 - 4 ? l + 4 * c : p.l1 - 4;
+            copy16_to_lds(p.Af + row * p.lda + lc, &st.a[lds]);
+        }
+    }
+}
+
+// The fragments of 4-l step s: a[q] = A[l = 4s + L/16][i = wave row base + 16q + L%16], b[q] likewise for j.
+template <int kA>
+__device__ __forceinline__ void mread_frags(const MStage<kA>& st, int s, int wi, int wj, int lane, double (&a)[4],
+                                            double (&b)[4]) {
+    const int k = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = wi * kMWave + 16 * q + c16;
+        if constexpr (kA == kAFloatT)
+            a[q] = static_cast<double>(st.a[(s * kMTileI + i) * 4 + k]);
+        else
+            a[q] = static_cast<double>(st.a[(4 * s + k) * kMTileI + i]);
+        b[q] = static_cast<double>(st.b[(4 * s + k) * kMTileJ + wj * kMWave + 16 * q + c16]);
+    }
+}
+
+__device__ __forceinline__ void mfma_step(const double (&a)[4], const double (&b)[4], mf_v4d (&acc)[4][4]) {
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
+}
+
+// A full stage: 4 steps, the fragments of step s + 1 read while the MFMAs of step s run.
+template <int kA>
+__device__ __forceinline__ void mstage_full(const MStage<kA>& st, int wi, int wj, int lane, mf_v4d (&acc)[4][4]) {
+    double a[4], b[4];
+    mread_frags<kA>(st, 0, wi, wj, lane, a, b);
+#pragma unroll
+    for (int s = 0; s < kMStage / 4; ++s) {
+        double an[4], bn[4];
+        if (s + 1 < kMStage / 4) mread_frags<kA>(st, s + 1, wi, wj, lane, an, bn);
+        mfma_step(a, b, acc);
+        if (s + 1 < kMStage / 4)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a[q] = an[q];
+                b[q] = bn[q];
+            }
+    }
+}
+
+// The last, partial stage: n < 16 valid rows; lanes whose l is past the end feed +0.0 in both operands.
+template <int kA>
+__device__ __forceinline__ void mstage_tail(const MStage<kA>& st, int n, int wi, int wj, int lane,
+                                            mf_v4d (&acc)[4][4]) {
+    const int k = lane >> 4;
+    for (int s = 0; 4 * s < n; ++s) {
+        double a[4], b[4];
+        mread_frags<kA>(st, s, wi, wj, lane, a, b);
+        if (4 * s + k >= n)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a[q] = 0.0;
+                b[q] = 0.0;
+            }
+        mfma_step(a, b, acc);
+    }
+}
+
+// One segment's sums: acc = sum over l in [l0, l1), ascending, through the double-buffered LDS pipeline.
+template <int kA>
+__device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA> (&st)[2], int64_t i_blk, int64_t j_blk,
+                                            int tid, int wi, int wj, int lane, int64_t l0, int64_t l1,
+                                            mf_v4d (&acc)[4][4]) {
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) acc[bi][bj] = mf_v4d{0.0, 0.0, 0.0, 0.0};
+    if (l0 >= l1) return;
+    const int64_t last = l1 - 1;
+    const int64_t full = (l1 - l0) / kMStage;
+    const int tail = static_cast<int>((l1 - l0) % kMStage);
+    const int64_t chunks = full + (tail ? 1 : 0);
+    missue_stage<kA>(p, st[0], i_blk, j_blk, l0, last, tid);
+    for (int64_t c = 0; c < full; ++c) {
+        if (c + 1 < chunks) {
+            missue_stage<kA>(p, st[(c + 1) & 1], i_blk, j_blk, l0 + (c + 1) * kMStage, last, tid);
+            wait_stage<4>();
+        } else {
+            wait_stage<0>();
+        }
+        mstage_full<kA>(st[c & 1], wi, wj, lane, acc);
+        workgroup_barrier();  // every wave has read the stage before the next issue overwrites it
+    }
+    if (tail) {
+        wait_stage<0>();
+        mstage_tail<kA>(st[full & 1], tail, wi, wj, lane, acc);
+        workgroup_barrier();
+    }
+}
+
+template <int kMode, int kA, bool kGrouped = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_mfma_kernel(
+    GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmParams* __restrict__ groups,
+    const int64_t* __restrict__ tile_start, int ngroups) {
+    __shared__ MStage<kA> st[2];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int wi = wave >> 1, wj = wave & 1;
+    int64_t id;
+    if constexpr (kGrouped) {
+        id = xcd_contiguous(blockIdx.x, gx);
+        int lo = 0, hi = ngroups - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (tile_start[mid] <= id) lo = mid;
+            else hi = mid - 1;
+        }
+        p = groups[lo];
+        id -= tile_start[lo];
+        gx = (p.J + kMTileJ - 1) / kMTileJ;
+        gy = (p.I + kMTileI - 1) / kMTileI;
+        gz = 1;
+    } else {
+        id = xcd_contiguous(blockIdx.x, gx * gy * gz);
+    }
+    // groups of kGroupRows row blocks x all column blocks, column-major inside a group (L2 reuse on one XCD)
+    const int64_t t = id % (gx * gy), bz = id / (gx * gy);
+    const int64_t first = t / (kGroupRows * gx) * kGroupRows;
+    const int64_t rows_in_group = gy - first < kGroupRows ? gy - first : kGroupRows;
+    const int64_t by = first + (t % (kGroupRows * gx)) % rows_in_group;
+    const int64_t bx = (t % (kGroupRows * gx)) / rows_in_group;
+    const int64_t i_blk = by * kMTileI, j_blk = bx * kMTileJ;
+    const int64_t iw = i_blk + wi * kMWave;  // this wave's first row
+    const int64_t jw = j_blk + wj * kMWave + (lane & 15);
+    const int ri = lane >> 4;
+    mf_v4d acc[4][4];
+    if (kMode == kPlain) {
+        maccumulate<kA>(p, st, i_blk, j_blk, tid, wi, wj, lane, p.l0, p.l1, acc);
+        if (iw >= p.I) return;
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t i = iw + 16 * bi + ri + 4 * r;
+                if (i >= p.I) continue;
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj) {
+                    const int64_t j = jw + 16 * bj;
+                    if (j >= p.J) continue;
+                    double v = acc[bi][bj][r];
+                    if (p.bias) v += static_cast<double>(p.bias[j]);
+                    float o = static_cast<float>(v);
+                    if (p.addsrc) o = p.addsrc[i * p.ld_add + j] + o;
+                    p.C[i * p.ldc + j] = o;
+                }
+            }
+        return;
+    }
+    const int s_begin = kMode == kWindowsInParallel ? static_cast<int>(bz) : 0;
+    const int s_end = kMode == kWindowsInParallel ? s_begin + 1 : p.nseg;
+    for (int s = s_begin; s < s_end; ++s) {
+        maccumulate<kA>(p, st, i_blk, j_blk, tid, wi, wj, lane, p.seg[s], p.seg[s + 1], acc);
+        if (iw >= p.I) continue;
+        float* out_base = kMode == kWindowsInParallel ? p.partial + static_cast<int64_t>(s) * p.I * p.J : p.C;
+        int64_t ld_out = kMode == kWindowsInParallel ? p.J : p.ldc;
+        asm volatile("" : "+s"(out_base), "+s"(ld_out));
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t i = iw + 16 * bi + ri + 4 * r;
+                if (i >= p.I) continue;
+                const int arow = p.seg_addrow ? p.seg_addrow[static_cast<int64_t>(s) * p.I + i] : -1;
+                float* out = out_base + i * ld_out;
+#pragma unroll
+                for (int bj = 0; bj < 4; ++bj) {
+                    const int64_t j = jw + 16 * bj;
+                    if (j >= p.J) continue;
+                    float o = static_cast<float>(acc[bi][bj][r]);
+                    if (p.seg_addrow) o = o + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j] : 0.0f);
+                    out[j] = (kMode == kWindowsInParallel || s == 0) ? o : out[j] + o;
+                }
+            }
+    }
+}
+
 // C[i][j] = partial[0][i][j] + partial[1][i][j] + ... in float, window order (trainer.py:328-332).
 __global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict__ partial, int64_t I, int64_t J,
                                                          int nseg, float* __restrict__ C, int64_t ldc) {
@@ -569,7 +809,7 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
         if (g.I == 0 || g.J == 0) continue;
         ps[used] = params_of(g);
         starts[used] = tiles;
-        tiles += static_cast<int64_t>(ceil_div(g.J, kTileJ) * ceil_div(g.I, kBlockI));
+        tiles += static_cast<int64_t>(ceil_div(g.J, kMTileJ) * ceil_div(g.I, kMTileI));
         ++used;
     }
     starts[used] = tiles;
@@ -591,13 +831,13 @@ int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStrea
     const GemmParams none{};
     const dim3 grid(static_cast<unsigned>(group.tiles));
     if (group.a_kind == kAFloatT)
-        hipLaunchKernelGGL((gemm_lds_kernel<kPlain, kAFloatT, true>), grid, dim3(256), 0, stream, none, group.tiles,
+        hipLaunchKernelGGL((gemm_mfma_kernel<kPlain, kAFloatT, true>), grid, dim3(256), 0, stream, none, group.tiles,
                            int64_t{0}, int64_t{1}, ps, starts, group.count);
     else if (group.segmented)
-        hipLaunchKernelGGL((gemm_lds_kernel<kWindowsInSequence, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
+        hipLaunchKernelGGL((gemm_mfma_kernel<kWindowsInSequence, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
                            group.tiles, int64_t{0}, int64_t{1}, ps, starts, group.count);
     else
-        hipLaunchKernelGGL((gemm_lds_kernel<kPlain, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
+        hipLaunchKernelGGL((gemm_mfma_kernel<kPlain, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
                            group.tiles, int64_t{0}, int64_t{1}, ps, starts, group.count);
     return check_launch("gemm group");
 }
@@ -622,7 +862,9 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
                          "transposed float A needs a plain reduction over whole 16-byte chunks");
     }
     if (vec && (ak != kADouble || ((g.lda % 2 == 0) && (reinterpret_cast<uintptr_t>(g.A) % 16 == 0)))) {
-        const int64_t gx = ceil_div(g.J, kTileJ), gy = ceil_div(g.I, kBlockI);
+        const bool mfma = ak != kADouble;
+        const int64_t gx = mfma ? ceil_div(g.J, kMTileJ) : ceil_div(g.J, kTileJ);
+        const int64_t gy = mfma ? ceil_div(g.I, kMTileI) : ceil_div(g.I, kBlockI);
         int64_t gz = 1;
         // windows in parallel when the tile grid alone leaves most of the 256 CUs x 3 workgroups idle
         if (g.seg && g.nseg > 1 && g.seg_partial && gx * gy < kParallelWindowsBelow &&
@@ -634,18 +876,21 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
         const dim3 grid(static_cast<unsigned>(gx * gy * gz));
 #define DLLM_GEMM_LAUNCH(MODE, AK) \
     hipLaunchKernelGGL((gemm_lds_kernel<MODE, AK>), grid, dim3(256), 0, stream, p, gx, gy, gz, nullptr, nullptr, 0)
+#define DLLM_GEMM_MFMA(MODE, AK) \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MODE, AK>), grid, dim3(256), 0, stream, p, gx, gy, gz, nullptr, nullptr, 0)
         if (ak == kAFloatT) {
-            DLLM_GEMM_LAUNCH(kPlain, kAFloatT);
+            DLLM_GEMM_MFMA(kPlain, kAFloatT);
         } else if (ak == kAFloatRows) {
-            if (p.partial) DLLM_GEMM_LAUNCH(kWindowsInParallel, kAFloatRows);
-            else if (g.seg) DLLM_GEMM_LAUNCH(kWindowsInSequence, kAFloatRows);
-            else DLLM_GEMM_LAUNCH(kPlain, kAFloatRows);
+            if (p.partial) DLLM_GEMM_MFMA(kWindowsInParallel, kAFloatRows);
+            else if (g.seg) DLLM_GEMM_MFMA(kWindowsInSequence, kAFloatRows);
+            else DLLM_GEMM_MFMA(kPlain, kAFloatRows);
         } else {
             if (p.partial) DLLM_GEMM_LAUNCH(kWindowsInParallel, kADouble);
             else if (g.seg) DLLM_GEMM_LAUNCH(kWindowsInSequence, kADouble);
             else DLLM_GEMM_LAUNCH(kPlain, kADouble);
         }
 #undef DLLM_GEMM_LAUNCH
+#undef DLLM_GEMM_MFMA
         DLLM_TRY(check_launch("gemm"));
         if (p.partial) {
             const int64_t n = g.I * g.J;
