@@ -455,15 +455,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // +0.0 and the accumulator is never -0.0 (it starts at +0.0, and a round-to-nearest sum is -0.0 only when both
 // addends are), so acc + 0 == acc bit for bit, infinities and NaNs included.
 //
-// Mapping: a workgroup computes a 128 i x 128 j tile with 4 waves in a 2 x 2 grid; a wave owns 64 x 64 outputs as
-// 4 x 4 MFMA blocks (128 accumulator VGPRs). Stages of 16 l (both operands, 16 KB) are copied global -> LDS with
-// direct-to-LDS loads, double-buffered; per 4-l step a wave reads 8 fragment values from LDS, converts them, and
-// issues 16 MFMAs (1024 cycles of matrix-core work).
+// Mapping: a workgroup computes a kMTileI x kMTileJ tile with 4 waves in a 2 x 2 grid; a wave owns 64 i x 16 kMBJ j
+// as 4 x kMBJ MFMA blocks (32 kMBJ accumulator VGPRs). Stages of kMStage l of both operands are copied global -> LDS
+// with direct-to-LDS loads, double-buffered; per 4-l step a wave reads 4 + kMBJ fragment values from LDS, converts
+// them, and issues 4 kMBJ MFMAs. On gfx950 the FP64 matrix core and the vector ALU share issue cycles, so the copies
+// run without vector instructions (SGPR base + fixed lane offset) and each fragment value feeds 4 or kMBJ MFMAs.
 typedef double mf_v4d __attribute__((ext_vector_type(4)));
-constexpr int kMTileI = 128;  // workgroup tile along i
-constexpr int kMTileJ = 128;  // workgroup tile along j
-constexpr int kMStage = 16;   // l per LDS stage
-constexpr int kMWave = 64;    // wave tile edge (4 MFMA blocks of 16)
+constexpr int kMBI = 4;                  // MFMA blocks per wave along i
+constexpr int kMBJ = 4;                  // MFMA blocks per wave along j
+constexpr int kMTileI = 2 * 16 * kMBI;   // workgroup tile along i (128)
+constexpr int kMTileJ = 2 * 16 * kMBJ;   // workgroup tile along j (128)
+constexpr int kMStage = 32;              // l per LDS stage
+constexpr int kMPiecesA = kMStage * kMTileI / 4 / 256;  // 16-byte copies per thread per stage
+constexpr int kMPiecesB = kMStage * kMTileJ / 4 / 256;
+static_assert(kMStage * kMTileI % 1024 == 0 && kMStage * kMTileJ % 1024 == 0, "whole copies per thread");
+static_assert(kMTileI == 128, "the transposed-A copy layout assumes 128 rows");
 
 template <int kA>
 struct MStage {
@@ -471,116 +477,182 @@ struct MStage {
     float b[kMStage * kMTileJ];  // [l][j]
 };
 
-// Copies stage rows l .. l + 15 of both operands (rows past `last` repeat row `last`; their values are masked).
-// Each operand is 512 16-byte pieces, two per thread; piece ids run contiguously over a wave, so one instruction fills
-// 1 KB of LDS from M0.
+// The global source of copy `id` of a stage at row l, with every index clamped in bounds (rows past `last` repeat
+// row `last`; their values are masked); the LDS destination of copy id is 16 * id bytes into the operand's array.
+__host__ __device__ __forceinline__ const float* msrc_b(const GemmParams& p, int id, int64_t j_blk, int64_t l, int64_t last) {
+    const int r = id / (kMTileJ / 4), cc = id % (kMTileJ / 4);
+    const int64_t lr = l + r <= last ? l + r : last;
+    const int64_t j = j_blk + cc * 4 <= p.J - 4 ? j_blk + cc * 4 : p.J - 4;
+    return p.B + lr * p.ldb + j;
+}
+
+template <int kA>
+__host__ __device__ __forceinline__ const float* msrc_a(const GemmParams& p, int id, int64_t i_blk, int64_t l, int64_t last) {
+    if constexpr (kA == kAFloatRows) {
+        const int r = id / (kMTileI / 4), cc = id % (kMTileI / 4);
+        const int64_t lr = l + r <= last ? l + r : last;
+        const int64_t i = i_blk + cc * 4 <= p.I - 4 ? i_blk + cc * 4 : p.I - 4;
+        return p.Af + lr * p.lda + i;
+    } else {
+        const int c = id / kMTileI, ii = id % kMTileI;
+        const int64_t row = i_blk + ii < p.I ? i_blk + ii : p.I - 1;
+        const int64_t lc = l + 4 * c <= p.l1 - 4 ? l + 4 * c : p.l1 - 4;
+        return p.Af + row * p.lda + lc;
+    }
+}
+
+// A stage with rows past the segment's end (the last one): every address clamped per lane.
 template <int kA>
 __device__ __forceinline__ void missue_stage(const GemmParams& p, MStage<kA>& st, int64_t i_blk, int64_t j_blk,
                                              int64_t l, int64_t last, int tid) {
     const int wave_base = tid & ~63;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int id = t * 256 + tid;
-        const int lds = (t * 256 + wave_base) * 4;  // float offset of this instruction's 1 KB
-        {
-            const int r = id >> 5, cc = id & 31;
-            const int64_t lr = l + r <= last ? l + r : last;
-            const int64_t j = j_blk + cc * 4 <= p.J - 4 ? j_blk + cc * 4 : p.J - 4;
-            copy16_to_lds(p.B + lr * p.ldb + j, &st.b[lds]);
-        }
-        if constexpr (kA == kAFloatRows) {
-            const int r = id >> 5, cc = id & 31;
-            const int64_t lr = l + r <= last ? l + r : last;
-            const int64_t i = i_blk + cc * 4 <= p.I - 4 ? i_blk + cc * 4 : p.I - 4;
-            copy16_to_lds(p.Af + lr * p.lda + i, &st.a[lds]);
-        } else {
-            const int c = id >> 7, ii = id & 127;
-            const int64_t row = i_blk + ii < p.I ? i_blk + ii : p.I - 1;
-            const int64_t lc = l + 4 * c <= p.l1 - 4 ? l + 4 * c : p.l1 - 4;
-            copy16_to_lds(p.Af + row * p.lda + lc, &st.a[lds]);
-        }
+    for (int t = 0; t < kMPiecesB; ++t)
+        copy16_to_lds(msrc_b(p, t * 256 + tid, j_blk, l, last), &st.b[(t * 256 + wave_base) * 4]);
+#pragma unroll
+    for (int t = 0; t < kMPiecesA; ++t)
+        copy16_to_lds(msrc_a<kA>(p, t * 256 + tid, i_blk, l, last), &st.a[(t * 256 + wave_base) * 4]);
+}
+
+// Steady-state copies: a stage whose rows all lie inside the segment needs no clamping along l, so each copy is a
+// wave-uniform base (SGPRs, advanced per stage by scalar adds) plus this lane's fixed 32-bit byte offset, computed
+// once per workgroup from the stage at l = 0.
+struct MCopyOffsets {
+    uint32_t b[kMPiecesB], a[kMPiecesA];
+};
+
+template <int kA>
+__host__ __device__ __forceinline__ MCopyOffsets mcopy_offsets(const GemmParams& p, int64_t i_blk, int64_t j_blk, int tid) {
+    MCopyOffsets o;
+    const int64_t big = int64_t{1} << 40;  // no l clamp
+#pragma unroll
+    for (int t = 0; t < kMPiecesB; ++t)
+        o.b[t] = static_cast<uint32_t>(reinterpret_cast<const char*>(msrc_b(p, t * 256 + tid, j_blk, 0, big)) -
+                                       reinterpret_cast<const char*>(p.B));
+#pragma unroll
+    for (int t = 0; t < kMPiecesA; ++t) {
+        GemmParams q = p;
+        q.l1 = big;
+        o.a[t] = static_cast<uint32_t>(reinterpret_cast<const char*>(msrc_a<kA>(q, t * 256 + tid, i_blk, 0, big)) -
+                                       reinterpret_cast<const char*>(p.Af));
     }
+    return o;
+}
+
+// 16 bytes from sbase + voff (SGPR base, VGPR offset) to LDS at lds_row + 16 * lane.
+__device__ __forceinline__ void copy16_to_lds_s(const float* sbase, uint32_t voff, const void* lds_row) {
+    typedef __attribute__((address_space(3))) const void* lds_address;
+    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
+    // the base is wave-uniform; readfirstlane states it where the compiler cannot prove it (grouped launches)
+    const uint64_t a = reinterpret_cast<uint64_t>(sbase);
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu)));
+    const uint64_t u = (static_cast<uint64_t>(hi) << 32) | lo;
+    // s_nop 4: a vector instruction that wrote the base SGPRs (readfirstlane) must be 5 wait states ahead of a memory
+    // instruction reading them, and the compiler's hazard checks do not look inside this statement
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u), "{m0}"(m0) : "memory");
+}
+
+template <int kA>
+__device__ __forceinline__ void missue_full(const GemmParams& p, MStage<kA>& st, const MCopyOffsets& o, int64_t l,
+                                            int wave) {
+    const float* bb = p.B + l * p.ldb;
+    const float* ab = kA == kAFloatT ? p.Af + l : p.Af + l * p.lda;
+#pragma unroll
+    for (int t = 0; t < kMPiecesB; ++t) copy16_to_lds_s(bb, o.b[t], &st.b[(t * 256 + wave * 64) * 4]);
+#pragma unroll
+    for (int t = 0; t < kMPiecesA; ++t) copy16_to_lds_s(ab, o.a[t], &st.a[(t * 256 + wave * 64) * 4]);
 }
 
 // The fragments of 4-l step s: a[q] = A[l = 4s + L/16][i = wave row base + 16q + L%16], b[q] likewise for j.
 template <int kA>
-__device__ __forceinline__ void mread_frags(const MStage<kA>& st, int s, int wi, int wj, int lane, double (&a)[4],
-                                            double (&b)[4]) {
+__device__ __forceinline__ void mread_frags(const MStage<kA>& st, int s, int wi, int wj, int lane,
+                                            double (&a)[kMBI], double (&b)[kMBJ]) {
     const int k = lane >> 4, c16 = lane & 15;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int i = wi * kMWave + 16 * q + c16;
+    for (int q = 0; q < kMBI; ++q) {
+        const int i = wi * 16 * kMBI + 16 * q + c16;
         if constexpr (kA == kAFloatT)
             a[q] = static_cast<double>(st.a[(s * kMTileI + i) * 4 + k]);
         else
             a[q] = static_cast<double>(st.a[(4 * s + k) * kMTileI + i]);
-        b[q] = static_cast<double>(st.b[(4 * s + k) * kMTileJ + wj * kMWave + 16 * q + c16]);
     }
+#pragma unroll
+    for (int q = 0; q < kMBJ; ++q)
+        b[q] = static_cast<double>(st.b[(4 * s + k) * kMTileJ + wj * 16 * kMBJ + 16 * q + c16]);
 }
 
-__device__ __forceinline__ void mfma_step(const double (&a)[4], const double (&b)[4], mf_v4d (&acc)[4][4]) {
+__device__ __forceinline__ void mfma_step(const double (&a)[kMBI], const double (&b)[kMBJ],
+                                          mf_v4d (&acc)[kMBI][kMBJ]) {
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi)
+    for (int bi = 0; bi < kMBI; ++bi)
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj) acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
+        for (int bj = 0; bj < kMBJ; ++bj)
+            acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
 }
 
-// A full stage: 4 steps, the fragments of step s + 1 read while the MFMAs of step s run.
+// A full stage, the fragments of step s + 1 read while the MFMAs of step s run.
 template <int kA>
-__device__ __forceinline__ void mstage_full(const MStage<kA>& st, int wi, int wj, int lane, mf_v4d (&acc)[4][4]) {
-    double a[4], b[4];
+__device__ __forceinline__ void mstage_full(const MStage<kA>& st, int wi, int wj, int lane,
+                                            mf_v4d (&acc)[kMBI][kMBJ]) {
+    double a[kMBI], b[kMBJ];
     mread_frags<kA>(st, 0, wi, wj, lane, a, b);
 #pragma unroll
     for (int s = 0; s < kMStage / 4; ++s) {
-        double an[4], bn[4];
+        double an[kMBI], bn[kMBJ];
         if (s + 1 < kMStage / 4) mread_frags<kA>(st, s + 1, wi, wj, lane, an, bn);
         mfma_step(a, b, acc);
-        if (s + 1 < kMStage / 4)
+        if (s + 1 < kMStage / 4) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                a[q] = an[q];
-                b[q] = bn[q];
-            }
+            for (int q = 0; q < kMBI; ++q) a[q] = an[q];
+#pragma unroll
+            for (int q = 0; q < kMBJ; ++q) b[q] = bn[q];
+        }
     }
 }
 
-// The last, partial stage: n < 16 valid rows; lanes whose l is past the end feed +0.0 in both operands.
+// The last, partial stage: n < kMStage valid rows; lanes whose l is past the end feed +0.0 in both operands.
 template <int kA>
 __device__ __forceinline__ void mstage_tail(const MStage<kA>& st, int n, int wi, int wj, int lane,
-                                            mf_v4d (&acc)[4][4]) {
+                                            mf_v4d (&acc)[kMBI][kMBJ]) {
     const int k = lane >> 4;
     for (int s = 0; 4 * s < n; ++s) {
-        double a[4], b[4];
+        double a[kMBI], b[kMBJ];
         mread_frags<kA>(st, s, wi, wj, lane, a, b);
-        if (4 * s + k >= n)
+        if (4 * s + k >= n) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                a[q] = 0.0;
-                b[q] = 0.0;
-            }
+            for (int q = 0; q < kMBI; ++q) a[q] = 0.0;
+#pragma unroll
+            for (int q = 0; q < kMBJ; ++q) b[q] = 0.0;
+        }
         mfma_step(a, b, acc);
     }
 }
 
 // One segment's sums: acc = sum over l in [l0, l1), ascending, through the double-buffered LDS pipeline.
 template <int kA>
-__device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA> (&st)[2], int64_t i_blk, int64_t j_blk,
-                                            int tid, int wi, int wj, int lane, int64_t l0, int64_t l1,
-                                            mf_v4d (&acc)[4][4]) {
+__device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA> (&st)[2], const MCopyOffsets& o,
+                                            int64_t i_blk, int64_t j_blk, int tid, int wi, int wj, int lane,
+                                            int64_t l0, int64_t l1, mf_v4d (&acc)[kMBI][kMBJ]) {
 #pragma unroll
-    for (int bi = 0; bi < 4; ++bi)
+    for (int bi = 0; bi < kMBI; ++bi)
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj) acc[bi][bj] = mf_v4d{0.0, 0.0, 0.0, 0.0};
+        for (int bj = 0; bj < kMBJ; ++bj) acc[bi][bj] = mf_v4d{0.0, 0.0, 0.0, 0.0};
     if (l0 >= l1) return;
     const int64_t last = l1 - 1;
     const int64_t full = (l1 - l0) / kMStage;
     const int tail = static_cast<int>((l1 - l0) % kMStage);
     const int64_t chunks = full + (tail ? 1 : 0);
-    missue_stage<kA>(p, st[0], i_blk, j_blk, l0, last, tid);
+    const int wave = wi * 2 + wj;
+    auto issue = [&](MStage<kA>& buf, int64_t l) {
+        if (l + kMStage - 1 <= last) missue_full<kA>(p, buf, o, l, wave);
+        else missue_stage<kA>(p, buf, i_blk, j_blk, l, last, tid);
+    };
+    issue(st[0], l0);
     for (int64_t c = 0; c < full; ++c) {
         if (c + 1 < chunks) {
-            missue_stage<kA>(p, st[(c + 1) & 1], i_blk, j_blk, l0 + (c + 1) * kMStage, last, tid);
-            wait_stage<4>();
+            issue(st[(c + 1) & 1], l0 + (c + 1) * kMStage);
+            wait_stage<kMPiecesA + kMPiecesB>();  // this stage landed; the next one's copies in flight
         } else {
             wait_stage<0>();
         }
@@ -627,28 +699,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int64_t by = first + (t % (kGroupRows * gx)) % rows_in_group;
     const int64_t bx = (t % (kGroupRows * gx)) / rows_in_group;
     const int64_t i_blk = by * kMTileI, j_blk = bx * kMTileJ;
-    const int64_t iw = i_blk + wi * kMWave;  // this wave's first row
-    const int64_t jw = j_blk + wj * kMWave + (lane & 15);
+    const int64_t iw = i_blk + wi * 16 * kMBI;  // this wave's first row
+    const int64_t jw = j_blk + wj * 16 * kMBJ + (lane & 15);
     const int ri = lane >> 4;
-    mf_v4d acc[4][4];
+    const MCopyOffsets o = mcopy_offsets<kA>(p, i_blk, j_blk, tid);
+    mf_v4d acc[kMBI][kMBJ];
     if (kMode == kPlain) {
-        maccumulate<kA>(p, st, i_blk, j_blk, tid, wi, wj, lane, p.l0, p.l1, acc);
+        maccumulate<kA>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.l0, p.l1, acc);
         if (iw >= p.I) return;
 #pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
+        for (int bi = 0; bi < kMBI; ++bi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t i = iw + 16 * bi + ri + 4 * r;
                 if (i >= p.I) continue;
 #pragma unroll
-                for (int bj = 0; bj < 4; ++bj) {
+                for (int bj = 0; bj < kMBJ; ++bj) {
                     const int64_t j = jw + 16 * bj;
                     if (j >= p.J) continue;
                     double v = acc[bi][bj][r];
                     if (p.bias) v += static_cast<double>(p.bias[j]);
-                    float o = static_cast<float>(v);
-                    if (p.addsrc) o = p.addsrc[i * p.ld_add + j] + o;
-                    p.C[i * p.ldc + j] = o;
+                    float out = static_cast<float>(v);
+                    if (p.addsrc) out = p.addsrc[i * p.ld_add + j] + out;
+                    p.C[i * p.ldc + j] = out;
                 }
             }
         return;
@@ -656,13 +729,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int s_begin = kMode == kWindowsInParallel ? static_cast<int>(bz) : 0;
     const int s_end = kMode == kWindowsInParallel ? s_begin + 1 : p.nseg;
     for (int s = s_begin; s < s_end; ++s) {
-        maccumulate<kA>(p, st, i_blk, j_blk, tid, wi, wj, lane, p.seg[s], p.seg[s + 1], acc);
+        maccumulate<kA>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.seg[s], p.seg[s + 1], acc);
         if (iw >= p.I) continue;
         float* out_base = kMode == kWindowsInParallel ? p.partial + static_cast<int64_t>(s) * p.I * p.J : p.C;
         int64_t ld_out = kMode == kWindowsInParallel ? p.J : p.ldc;
         asm volatile("" : "+s"(out_base), "+s"(ld_out));
 #pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
+        for (int bi = 0; bi < kMBI; ++bi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t i = iw + 16 * bi + ri + 4 * r;
@@ -670,12 +743,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const int arow = p.seg_addrow ? p.seg_addrow[static_cast<int64_t>(s) * p.I + i] : -1;
                 float* out = out_base + i * ld_out;
 #pragma unroll
-                for (int bj = 0; bj < 4; ++bj) {
+                for (int bj = 0; bj < kMBJ; ++bj) {
                     const int64_t j = jw + 16 * bj;
                     if (j >= p.J) continue;
-                    float o = static_cast<float>(acc[bi][bj][r]);
-                    if (p.seg_addrow) o = o + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j] : 0.0f);
-                    out[j] = (kMode == kWindowsInParallel || s == 0) ? o : out[j] + o;
+                    float v = static_cast<float>(acc[bi][bj][r]);
+                    if (p.seg_addrow) v = v + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j] : 0.0f);
+                    out[j] = (kMode == kWindowsInParallel || s == 0) ? v : out[j] + v;
                 }
             }
     }

@@ -270,3 +270,23 @@ def test_softmax_column_mean_and_dot(K, ora):
     assert_same(K.column_mean(x), ora.column_mean(x), "column_mean")
     a, b = adversarial(46, 5000), O.gaussian(47, 5000)
     assert K.dot(a, b) == ora.dot(a, b)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 15, 17, 33])
+def test_linear_matrix_core_tails_and_non_finite(K, ora, rows):
+    """Reductions of every length mod 16 through the matrix-core path (K and N multiples of 4), with infinities and
+    NaNs in the operands: the padded steps of a partial stage must leave every sum's bits alone."""
+    x, w, dy = adversarial(11, rows, 64), adversarial(12, 128, 64), adversarial(13, rows, 128)
+    for got, want, name in zip(K.linear_backward(x, w, dy), ora.linear_backward(x, w, dy), ("dx", "dw", "db")):
+        if want is not None:
+            assert_same(got, want, f"{name} rows={rows}")
+    x[0, 3] = np.inf
+    dy[rows - 1, 5] = np.nan
+    w[7, 9] = -np.inf
+    pairs = list(zip(K.linear_backward(x, w, dy)[:2], ora.linear_backward(x, w, dy)[:2], ("dx", "dw")))
+    pairs.append((K.linear(x, w), ora.linear(x, w), "linear"))
+    for got, want, name in pairs:
+        got, want = np.asarray(got), np.asarray(want)
+        nan = np.isnan(want)  # a NaN the hardware generates has no defined sign or payload
+        assert np.array_equal(np.isnan(got), nan), f"{name} rows={rows}: NaN positions"
+        assert_same(np.where(nan, 0, got), np.where(nan, 0, want), f"{name} rows={rows} non-finite")
