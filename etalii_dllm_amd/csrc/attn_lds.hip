@@ -3,24 +3,23 @@
 //
 // Each output is C[i][j] = sum over l in row i's span, ascending, of A[l][i] * B[l][j] (then times a row scale or a
 // constant), accumulated in double and rounded once:
-//   scores      S^T[key][query] = sum_d K[key][d] Q[query][d]        A = K (float, read transposed), exact: fma
-//   dP^T        dP^T[key][query] = sum_d V[key][d] dOut[query][d]     A = V (float, read transposed), exact: fma
+//   scores      S^T[key][query] = sum_d K[key][d] Q[query][d]        exact products: matrix cores (attn_mfma_kernel)
+//   dP^T        dP^T[key][query] = sum_d V[key][d] dOut[query][d]     (as above)
 //   out, dq     row t (query): sum over the keys t sees of E^T / dS^T times V / K    A double: multiply, then add
 //   dk, dv      row j (key): sum over (query t, head of the group) that see j of dS / P times Q / dOut  (as above)
 // The products with a double factor are not exact, so they are a rounded multiply and a rounded add, as the
-// reference computes them (grad.hpp:262-301, nn.hpp:535-569).
+// reference computes them (grad.hpp:262-301, nn.hpp:535-569); attn_tile_kernel runs them on the vector ALU.
 //
-// Mapping: a wave owns 16 consecutive rows (its A values broadcast to all 64 lanes) by 64 CJ columns (CJ per lane).
-// A stage is 16 consecutive l: the workgroup's A (16 l x 64 rows) and B (16 l x 64 CJ columns) are copied
-// global -> LDS with gfx950's direct-to-LDS loads while the previous stage is computed. The broadcast is the DPP64
-// row_newbcast modifier: on the FMA itself for exact products, on a 64-bit move feeding the multiply otherwise.
+// attn_tile_kernel mapping: a wave owns 16 consecutive rows (its A values broadcast to all 64 lanes) by 64 CJ
+// columns (CJ per lane). A stage is 16 consecutive l: the workgroup's A (16 l x 64 rows) and B (16 l x 64 CJ
+// columns) are copied global -> LDS with gfx950's direct-to-LDS loads while the previous stage is computed. The
+// broadcast is the DPP64 row_newbcast modifier on a 64-bit move feeding the multiply.
 // Causal rows have ragged spans: stages inside every row's span of the wave run unpredicated; at the ragged ends
 // each (row, l) is taken only when l lies in that row's span (a wave-uniform test), so every row adds exactly its
 // own steps, in order, and nothing else. Tiles are dispatched longest reduction first.
-#include <type_traits>
-
 #include "attn_step.h"
 #include "common.h"
+#include "lds_copy.h"
 #include "kernels.h"
 
 namespace dllm_hip {
@@ -87,22 +86,15 @@ __device__ __forceinline__ void row_span(const TileParams& p, int64_t r, int64_t
     }
 }
 
-template <int CJ, bool kAFloat>
+template <int CJ>
 struct Stage {
-    typename std::conditional<kAFloat, float, double>::type a[kAFloat ? kTileRows : kChunk]
-                                                             [kAFloat ? kChunk : kTileRows];
+    double a[kChunk][kTileRows];
     float b[kChunk][64 * CJ];
 };
 
-template <int CJ, bool kAFloat>
+template <int CJ>
 constexpr int stage_copies() {
-    return (kAFloat ? 1 : 2) + CJ;
-}
-
-__device__ __forceinline__ void copy16_to_lds(const void* src, const void* lds_row) {
-    typedef __attribute__((address_space(3))) const void* lds_address;
-    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+    return 2 + CJ;
 }
 
 template <int kPending>
@@ -116,24 +108,16 @@ __device__ __forceinline__ void wait_stage() {
 __device__ __forceinline__ void workgroup_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // Copies of the stage holding steps l .. l + 15 (steps past `last` repeat step `last`; they are never used). Wave w
-// copies A rows (steps) 4w .. 4w + 3 (doubles: two per instruction) or, transposed, A rows 16w .. 16w + 15 (16
-// steps of floats each), and B rows 4w .. 4w + 3.
-template <int CJ, bool kAFloat>
-__device__ __forceinline__ void issue_stage(Stage<CJ, kAFloat>& st, const void* a_base, const Op& ao, int64_t i0,
-                                            int64_t I, int64_t a_row_alloc, const float* b_base, const Op& bo,
-                                            int64_t b_col, int64_t l, int64_t last, int wave, int lane) {
-    if constexpr (kAFloat) {
-        // row i (clamped to I - 1), steps l + 4 (lane % 4) .. + 3 (clamped to the row's readable end)
-        const int64_t i = i0 + 16 * wave + (lane >> 2) < I ? i0 + 16 * wave + (lane >> 2) : I - 1;
-        const int64_t lc = l + (lane & 3) * 4 <= a_row_alloc - 4 ? l + (lane & 3) * 4 : a_row_alloc - 4;
-        copy16_to_lds(static_cast<const float*>(a_base) + i * ao.ld + lc, &st.a[16 * wave][0]);
-    } else {
+// copies A rows (steps) 4w .. 4w + 3 (doubles: two per instruction) and B rows 4w .. 4w + 3.
+template <int CJ>
+__device__ __forceinline__ void issue_stage(Stage<CJ>& st, const double* a_base, const Op& ao, int64_t i0,
+                                            const float* b_base, const Op& bo, int64_t b_col, int64_t l, int64_t last,
+                                            int wave, int lane) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int r = 4 * wave + 2 * t;
-            const int64_t lr = l + r + (lane >> 5) <= last ? l + r + (lane >> 5) : last;
-            copy16_to_lds(static_cast<const double*>(a_base) + lr * ao.ld + i0 + (lane & 31) * 2, &st.a[r][0]);
-        }
+    for (int t = 0; t < 2; ++t) {
+        const int r = 4 * wave + 2 * t;
+        const int64_t lr = l + r + (lane >> 5) <= last ? l + r + (lane >> 5) : last;
+        copy16_to_lds(a_base + lr * ao.ld + i0 + (lane & 31) * 2, &st.a[r][0]);
     }
     constexpr int kLanesPerRow = 16 * CJ;
     constexpr int kRowsPerCopy = 64 / kLanesPerRow;
@@ -159,61 +143,18 @@ struct RowOperands {
     float b[CJ];
 };
 
-template <int CJ, bool kAFloat>
-__device__ __forceinline__ RowOperands<CJ> read_row(const Stage<CJ, kAFloat>& st, int k, int wave, int lane) {
+template <int CJ>
+__device__ __forceinline__ RowOperands<CJ> read_row(const Stage<CJ>& st, int k, int wave, int lane) {
     RowOperands<CJ> r;
-    const int i = wave * 16 + (lane & 15);
-    if constexpr (kAFloat)
-        r.a = static_cast<double>(st.a[i][k]);
-    else
-        r.a = st.a[k][i];
-    if constexpr (CJ == 4) {
-        const float4 v = *reinterpret_cast<const float4*>(&st.b[k][lane * 4]);
-        r.b[0] = v.x; r.b[1] = v.y; r.b[2] = v.z; r.b[3] = v.w;
-    } else if constexpr (CJ == 2) {
+    r.a = st.a[k][wave * 16 + (lane & 15)];
+    if constexpr (CJ == 2) {
         const float2 v = *reinterpret_cast<const float2*>(&st.b[k][lane * 2]);
-        r.b[0] = v.x; r.b[1] = v.y;
+        r.b[0] = v.x;
+        r.b[1] = v.y;
     } else {
         r.b[0] = st.b[k][lane];
     }
     return r;
-}
-
-// acc[Q][c] = fma(A[l][row Q], b[c], acc[Q][c]) with A[l][row Q] taken from lane Q of each 16-lane row by the DPP64
-// row_newbcast modifier. A DPP instruction reads its registers two wait states after their last vector write; in a
-// step every row takes, only the first block follows the conversions that wrote b (and, for float A, a), so only it
-// starts with s_nop 1 (kNop: every block does, for steps some rows skip), and the blocks stay in order (volatile).
-// tests/test_dpp_hazards.py checks the built code.
-template <int CJ, int Q, bool kNop>
-__device__ __forceinline__ void fma_bcast(double (&acc)[16][CJ], double a, const double (&b)[CJ]) {
-    if constexpr (CJ == 4) {
-        if constexpr (Q == 0 || kNop)
-            asm volatile("s_nop 1\n\t"
-                         "v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-                         "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-                         "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-                         "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
-                         : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
-                         : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
-        else
-            asm volatile("v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-                         "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-                         "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-                         "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%9 row_mask:0xf bank_mask:0xf"
-                         : "+v"(acc[Q][0]), "+v"(acc[Q][1]), "+v"(acc[Q][2]), "+v"(acc[Q][3])
-                         : "v"(a), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "n"(Q));
-    } else if constexpr (CJ == 2) {
-        asm volatile("s_nop 1\n\t"
-                     "v_fmac_f64_dpp %0, %2, %3 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
-                     "v_fmac_f64_dpp %1, %2, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf"
-                     : "+v"(acc[Q][0]), "+v"(acc[Q][1])
-                     : "v"(a), "v"(b[0]), "v"(b[1]), "n"(Q));
-    } else {
-        asm volatile("s_nop 1\n\t"
-                     "v_fmac_f64_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-                     : "+v"(acc[Q][0])
-                     : "v"(a), "v"(b[0]), "n"(Q));
-    }
 }
 
 // A[l][rows Q .. Q + 3] in every lane (DPP64 moves); the wait states before the first move as above.
@@ -228,28 +169,25 @@ __device__ __forceinline__ void broadcast_rows4(double a, double (&r)[4]) {
                  : "v"(a), "n"(Q), "n"(Q + 1), "n"(Q + 2), "n"(Q + 3));
 }
 
-// One step for the wave's 16 rows; kAll: every row takes it, otherwise row q only when `take` has bit q.
-template <int CJ, bool kExact, bool kAll, int Q>
+// One step for the wave's 16 rows; kAll: every row takes it, otherwise row q only when `take` has bit q. The
+// broadcast moves are DPP instructions: they read their source two wait states after its last vector write (the
+// s_nop 1 in broadcast_rows4; tests/test_dpp_hazards.py checks the built code).
+template <int CJ, bool kAll, int Q>
 __device__ __forceinline__ void step_rows(double (&acc)[16][CJ], double a, const double (&b)[CJ], uint32_t take) {
     if constexpr (Q < 16) {
-        if constexpr (kExact) {
-            if (kAll || (take >> Q) & 1u) fma_bcast<CJ, Q, !kAll>(acc, a, b);
-            step_rows<CJ, kExact, kAll, Q + 1>(acc, a, b, take);
-        } else {
-            double aq[4];
-            broadcast_rows4<Q>(a, aq);
+        double aq[4];
+        broadcast_rows4<Q>(a, aq);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (kAll || (take >> (Q + k)) & 1u) {
+        for (int k = 0; k < 4; ++k) {
+            if (kAll || (take >> (Q + k)) & 1u) {
 #pragma unroll
-                    for (int c = 0; c < CJ; ++c) {
-                        const double prod = aq[k] * b[c];
-                        acc[Q + k][c] = acc[Q + k][c] + prod;
-                    }
+                for (int c = 0; c < CJ; ++c) {
+                    const double prod = aq[k] * b[c];
+                    acc[Q + k][c] = acc[Q + k][c] + prod;
                 }
             }
-            step_rows<CJ, kExact, kAll, Q + 4>(acc, a, b, take);
         }
+        step_rows<CJ, kAll, Q + 4>(acc, a, b, take);
     }
 }
 
@@ -259,16 +197,16 @@ __device__ __forceinline__ void widen(const RowOperands<CJ>& r, double (&b)[CJ])
     for (int c = 0; c < CJ; ++c) b[c] = r.b[c];
 }
 
-template <int CJ, bool kAFloat, bool kExact>
-__device__ __forceinline__ void stage_all(const Stage<CJ, kAFloat>& st, int wave, int lane, double (&acc)[16][CJ]) {
-    RowOperands<CJ> cur = read_row<CJ, kAFloat>(st, 0, wave, lane);
+template <int CJ>
+__device__ __forceinline__ void stage_all(const Stage<CJ>& st, int wave, int lane, double (&acc)[16][CJ]) {
+    RowOperands<CJ> cur = read_row<CJ>(st, 0, wave, lane);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
         RowOperands<CJ> next = cur;
-        if (k + 1 < kChunk) next = read_row<CJ, kAFloat>(st, k + 1, wave, lane);
+        if (k + 1 < kChunk) next = read_row<CJ>(st, k + 1, wave, lane);
         double b[CJ];
         widen<CJ>(cur, b);
-        step_rows<CJ, kExact, true, 0>(acc, cur.a, b, 0u);
+        step_rows<CJ, true, 0>(acc, cur.a, b, 0u);
         cur = next;
     }
 }
@@ -293,33 +231,23 @@ __device__ __forceinline__ uint32_t rows_taking(const TileParams& p, int64_t l, 
 }
 
 // Steps l0 .. l0 + n - 1 of a stage, each taken by the rows whose span holds it.
-template <int CJ, bool kAFloat, bool kExact>
-__device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ, kAFloat>& st, int wave, int lane,
-                                             int64_t l0, int n, int64_t tw, int64_t rows_n, int64_t I,
-                                             double (&acc)[16][CJ]) {
-    if constexpr (kExact) {  // the scores and dP: every row takes the steps below L (here: the first n)
-        for (int k = 0; k < n; ++k) {
-            const RowOperands<CJ> r = read_row<CJ, kAFloat>(st, k, wave, lane);
-            double b[CJ];
-            widen<CJ>(r, b);
-            step_rows<CJ, kExact, true, 0>(acc, r.a, b, 0u);
-        }
-        return;
-    }
+template <int CJ>
+__device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ>& st, int wave, int lane, int64_t l0,
+                                             int n, int64_t tw, int64_t rows_n, int64_t I, double (&acc)[16][CJ]) {
     for (int k = 0; k < n; ++k) {
         const uint32_t take = __builtin_amdgcn_readfirstlane(rows_taking(p, l0 + k, tw, rows_n, I));
         if (take == 0) continue;
-        const RowOperands<CJ> r = read_row<CJ, kAFloat>(st, k, wave, lane);
+        const RowOperands<CJ> r = read_row<CJ>(st, k, wave, lane);
         double b[CJ];
         widen<CJ>(r, b);
-        step_rows<CJ, kExact, false, 0>(acc, r.a, b, take);
+        step_rows<CJ, false, 0>(acc, r.a, b, take);
     }
 }
 
-template <int CJ, bool kAFloat, bool kExact, bool kOutDouble>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4 : CJ == 2 ? 2 : 3))) void attn_tile_kernel(
+template <int CJ>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4 : 2))) void attn_tile_kernel(
     TileParams p) {
-    __shared__ Stage<CJ, kAFloat> st[2];
+    __shared__ Stage<CJ> st[2];
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int lane = static_cast<int>(threadIdx.x) & 63;
     // block -> (rank by work, column tile, set, z): the longest reductions go first
@@ -339,10 +267,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     const int64_t J = p.cols_kind == 0 ? n : p.head_dim;
     const int64_t i0 = ti * kTileRows, j0 = tj * 64 * CJ;
     if (i0 >= I || j0 >= J) return;
-    if (p.mask == kMaskTileCausal) {  // score tiles no query sees: every key row above every query column
-        if (i0 > j0 + 64 * CJ - 1) return;
-        if (p.window != 0 && i0 + kTileRows - 1 + p.window - 1 < j0) return;
-    }
     // spans are intervals whose ends grow with the row: the tile's steps are [lo(first row), hi(last row)), and the
     // steps every row of this wave takes are [lo(its last row), hi(its first row))
     int64_t t_lo, t_hi, w_lo, w_hi, dummy;
@@ -355,8 +279,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     } else {
         w_lo = w_hi = 0;
     }
-    const void* A = kAFloat ? static_cast<const void*>(op_base<float>(o.A, w, seg_w, hz))
-                            : static_cast<const void*>(op_base<double>(o.A, w, seg_w, hz));
+    const double* A = op_base<double>(o.A, w, seg_w, hz);
     const float* B = op_base<float>(o.B, w, seg_w, hz);
     const int64_t chunk = j0 + 4 * (lane % (16 * CJ));
     const int64_t b_col = chunk + 4 <= p.b_row_alloc ? chunk : p.b_row_alloc - 4;
@@ -368,60 +291,209 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     const int64_t steps = t_hi - t_lo;
     const int64_t stages = steps > 0 ? (steps + kChunk - 1) / kChunk : 0;
     const int64_t last = t_hi - 1;
-    if (stages > 0)
-        issue_stage<CJ, kAFloat>(st[0], A, o.A, i0, I, p.a_row_alloc, B, o.B, b_col, t_lo, last, wave, lane);
+    if (stages > 0) issue_stage<CJ>(st[0], A, o.A, i0, B, o.B, b_col, t_lo, last, wave, lane);
     for (int64_t s = 0; s < stages; ++s) {
         if (s + 1 < stages) {
-            issue_stage<CJ, kAFloat>(st[(s + 1) & 1], A, o.A, i0, I, p.a_row_alloc, B, o.B, b_col,
-                                     t_lo + (s + 1) * kChunk, last, wave, lane);
-            wait_stage<stage_copies<CJ, kAFloat>()>();
+            issue_stage<CJ>(st[(s + 1) & 1], A, o.A, i0, B, o.B, b_col, t_lo + (s + 1) * kChunk, last, wave, lane);
+            wait_stage<stage_copies<CJ>()>();
         } else {
             wait_stage<0>();
         }
         const int64_t l0 = t_lo + s * kChunk;
         const int n_steps = static_cast<int>(t_hi - l0 < kChunk ? t_hi - l0 : kChunk);
-        if constexpr (kExact) {  // every row takes every step: full stages here, a partial last one after the loop
-            if (n_steps < kChunk) break;
-            stage_all<CJ, kAFloat, kExact>(st[s & 1], wave, lane, acc);
-        } else {
-            if (n_steps == kChunk && l0 >= w_lo && l0 + kChunk <= w_hi)
-                stage_all<CJ, kAFloat, kExact>(st[s & 1], wave, lane, acc);
-            else
-                stage_masked<CJ, kAFloat, kExact>(p, st[s & 1], wave, lane, l0, n_steps, tw, n, I, acc);
-        }
+        if (n_steps == kChunk && l0 >= w_lo && l0 + kChunk <= w_hi)
+            stage_all<CJ>(st[s & 1], wave, lane, acc);
+        else
+            stage_masked<CJ>(p, st[s & 1], wave, lane, l0, n_steps, tw, n, I, acc);
         workgroup_barrier();  // every wave is done with this stage before the next issue refills it
     }
-    if constexpr (kExact) {
-        const int64_t full = steps / kChunk;
-        const int tail = static_cast<int>(steps - full * kChunk);
-        if (tail > 0)  // its copies were issued and waited for in the loop's last round
-            stage_masked<CJ, kAFloat, kExact>(p, st[full & 1], wave, lane, t_lo + full * kChunk, tail, tw, n, I, acc);
-    }
     // the output rows' base and stride, opaque so the compiler keeps no per-element addresses across the reduction
-    const int64_t elem = kOutDouble ? 8 : 4;
-    char* c_base = reinterpret_cast<char*>(const_cast<void*>(o.C.ptr)) +
-                   (w * o.C.w_stride + seg_w * o.C.seg_stride + (hz / o.C.head_div) * o.C.head_stride +
-                    tw * o.C.ld + j0) * elem;
-    int64_t c_ld = o.C.ld * elem;
+    float* c_base = static_cast<float*>(const_cast<void*>(o.C.ptr)) + w * o.C.w_stride + seg_w * o.C.seg_stride +
+                    (hz / o.C.head_div) * o.C.head_stride + tw * o.C.ld + j0;
+    int64_t c_ld = o.C.ld;
     asm volatile("" : "+s"(c_base), "+s"(c_ld));
     const double* rs = p.rowscale ? p.rowscale + z * p.rowscale_zstride + tw : nullptr;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
         if (tw + q >= I) break;
-        const double scale = kOutDouble ? p.out_scale : (rs ? rs[q] : 1.0);
 #pragma unroll
         for (int c = 0; c < CJ; ++c) {
             const int64_t jl = lane * CJ + c;
             if (j0 + jl >= J) continue;
-            if constexpr (kOutDouble) {
-                reinterpret_cast<double*>(c_base + q * c_ld)[jl] = acc[q][c] * scale;
-            } else {
-                double v = acc[q][c];
-                if (rs) v = v * scale;
-                reinterpret_cast<float*>(c_base + q * c_ld)[jl] = static_cast<float>(v);
-            }
+            double v = acc[q][c];
+            if (rs) v = v * rs[q];
+            c_base[q * c_ld + jl] = static_cast<float>(v);
         }
     }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// The scores and dP (float x float, exact products) on the FP64 matrix cores.
+//
+// v_mfma_f64_16x16x4_f64 adds its four products to the accumulator as four FMAs in ascending k, each rounded: one
+// instruction per 4 consecutive l is the serial chain over l = 0 .. head_dim - 1 that the vector FMAs computed
+// (head_dim is a multiple of 4, so no step is padded). Same tiles as attn_tile_kernel<4, true, true, *>: 64 rows
+// (keys) x 256 columns (queries); the 4 waves sit side by side along the columns, each owning 64 x 64 outputs as
+// 4 x 4 MFMA blocks. A stage is 16 l: A as [l / 4][row][l % 4] (one 16-byte copy per thread) and B as [l][column]
+// (four per thread).
+typedef double ma_v4d __attribute__((ext_vector_type(4)));
+constexpr int kMfmaChunk = 16;
+
+struct MfmaStage {
+    float a[kMfmaChunk * kTileRows];  // [l / 4][row][l % 4]
+    float b[kMfmaChunk * 256];        // [l][column]
+};
+
+// The copies: a wave-uniform base (SGPRs) plus this lane's byte offset, computed once per tile, so a stage's copies
+// cost the matrix core no vector instructions. Rows past the tile repeat its last row; in a last, partial stage
+// (L % 16 != 0) the offsets are pulled back so every read stays inside the operand rows (those values are unused).
+struct MfmaOffsets {
+    uint32_t a, b[4];
+};
+
+__device__ __forceinline__ MfmaOffsets mfma_offsets(int64_t a_ld, int64_t i0, int64_t I, int64_t b_ld, int64_t j0,
+                                                    int64_t b_row_alloc, int tid) {
+    MfmaOffsets o;
+    const int c = tid >> 6, ii = tid & 63;  // A copy: chunk c (l = 4c .. 4c + 3) of tile row ii
+    const int64_t row = i0 + ii < I ? i0 + ii : I - 1;
+    o.a = static_cast<uint32_t>((row * a_ld + 4 * c) * 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {  // B copy t: row r (l), 16-byte column chunk cc
+        const int id = t * 256 + tid;
+        const int r = id >> 6, cc = id & 63;
+        const int64_t col = j0 + cc * 4 <= b_row_alloc - 4 ? j0 + cc * 4 : b_row_alloc - 4;
+        o.b[t] = static_cast<uint32_t>((r * b_ld + col) * 4);
+    }
+    return o;
+}
+
+// Stage l .. l + 15 of A (row chunks, l < a_row_alloc) and B (rows l .. min(l + 15, L - 1)).
+__device__ __forceinline__ void mfma_issue(MfmaStage& st, const float* A, int64_t a_row_alloc, const float* B,
+                                           int64_t b_ld, const MfmaOffsets& o, int64_t l, int64_t L, int tid,
+                                           int wave) {
+    const bool full = l + kMfmaChunk <= L;
+    uint32_t va = o.a;
+    if (!full) {
+        const int64_t over = l + 4 * (tid >> 6) - (a_row_alloc - 4);
+        if (over > 0) va -= static_cast<uint32_t>(over * 4);
+    }
+    copy16_to_lds_s(A + l, va, &st.a[wave * 64 * 4]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        uint32_t vb = o.b[t];
+        if (!full) {
+            const int64_t over = l + ((t * 256 + tid) >> 6) - (L - 1);
+            if (over > 0) vb -= static_cast<uint32_t>(over * b_ld * 4);
+        }
+        copy16_to_lds_s(B + l * b_ld, vb, &st.b[(t * 256 + wave * 64) * 4]);
+    }
+}
+
+__device__ __forceinline__ void mfma_frags(const MfmaStage& st, int s, int wave, int lane, double (&a)[4],
+                                           double (&b)[4]) {
+    const int k = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        a[q] = static_cast<double>(st.a[(s * kTileRows + 16 * q + c16) * 4 + k]);
+        b[q] = static_cast<double>(st.b[(4 * s + k) * 256 + wave * 64 + 16 * q + c16]);
+    }
+}
+
+__device__ __forceinline__ void mfma_4x4(const double (&a)[4], const double (&b)[4], ma_v4d (&acc)[4][4]) {
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj)
+            acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
+}
+
+template <bool kOutDouble>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_mfma_kernel(TileParams p) {
+    __shared__ MfmaStage st[2];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    int64_t id = blockIdx.x;
+    const int64_t zz = id % p.Z;
+    id /= p.Z;
+    const int64_t tj = id % p.tiles_j;
+    const int64_t ti = id / p.tiles_j;
+    const OperandSet& o = p.set[0];
+    const int64_t w = zz / p.heads, hz = zz % p.heads;
+    const int64_t seg_w = p.seg[w], n = p.seg[w + 1] - seg_w;
+    const int64_t I = p.rows_kind == 0 ? n : p.head_dim;
+    const int64_t J = p.cols_kind == 0 ? n : p.head_dim;
+    const int64_t i0 = ti * kTileRows, j0 = tj * 256;
+    if (i0 >= I || j0 >= J) return;
+    if (p.mask == kMaskTileCausal) {  // score tiles no query sees: every key row above every query column
+        if (i0 > j0 + 255) return;
+        if (p.window != 0 && i0 + kTileRows - 1 + p.window - 1 < j0) return;
+    }
+    const float* A = op_base<float>(o.A, w, seg_w, hz);
+    const float* B = op_base<float>(o.B, w, seg_w, hz);
+    ma_v4d acc[4][4];
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) acc[bi][bj] = ma_v4d{0.0, 0.0, 0.0, 0.0};
+    const int64_t L = p.L;
+    const int64_t stages = (L + kMfmaChunk - 1) / kMfmaChunk;
+    const MfmaOffsets off = mfma_offsets(o.A.ld, i0, I, o.B.ld, j0, p.b_row_alloc, tid);
+    mfma_issue(st[0], A, p.a_row_alloc, B, o.B.ld, off, 0, L, tid, wave);
+    for (int64_t s = 0; s < stages; ++s) {
+        if (s + 1 < stages) {
+            mfma_issue(st[(s + 1) & 1], A, p.a_row_alloc, B, o.B.ld, off, (s + 1) * kMfmaChunk, L, tid, wave);
+            wait_stage<5>();
+        } else {
+            wait_stage<0>();
+        }
+        // 4-l steps of this stage (L is a multiple of 4); the fragments of step k + 1 are read during step k
+        const int steps = static_cast<int>((L - s * kMfmaChunk < kMfmaChunk ? L - s * kMfmaChunk : kMfmaChunk) / 4);
+        double a[4], b[4];
+        mfma_frags(st[s & 1], 0, wave, lane, a, b);
+#pragma unroll
+        for (int k = 0; k < kMfmaChunk / 4; ++k) {
+            if (k < steps) {
+                double an[4], bn[4];
+                if (k + 1 < kMfmaChunk / 4 && k + 1 < steps) mfma_frags(st[s & 1], k + 1, wave, lane, an, bn);
+                mfma_4x4(a, b, acc);
+                if (k + 1 < kMfmaChunk / 4 && k + 1 < steps)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        a[q] = an[q];
+                        b[q] = bn[q];
+                    }
+            }
+        }
+        workgroup_barrier();  // every wave is done with this stage before the next issue refills it
+    }
+    const int64_t elem = kOutDouble ? 8 : 4;
+    char* c_base = reinterpret_cast<char*>(const_cast<void*>(o.C.ptr)) +
+                   (w * o.C.w_stride + seg_w * o.C.seg_stride + (hz / o.C.head_div) * o.C.head_stride) * elem;
+    int64_t c_ld = o.C.ld * elem;
+    asm volatile("" : "+s"(c_base), "+s"(c_ld));  // no output addresses kept live across the reduction
+    const double* rs = p.rowscale ? p.rowscale + zz * p.rowscale_zstride : nullptr;
+    const int64_t jw = j0 + wave * 64 + (lane & 15);
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t i = i0 + 16 * bi + (lane >> 4) + 4 * r;
+            if (i >= I) continue;
+            char* row = c_base + i * c_ld;
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) {
+                const int64_t j = jw + 16 * bj;
+                if (j >= J) continue;
+                if constexpr (kOutDouble) {
+                    reinterpret_cast<double*>(row)[j] = acc[bi][bj][r] * p.out_scale;
+                } else {
+                    double v = acc[bi][bj][r];
+                    if (rs) v = v * rs[i];
+                    reinterpret_cast<float*>(row)[j] = static_cast<float>(v);
+                }
+            }
+        }
 }
 
 Op op_of(const AttnOperand& o) {
@@ -469,19 +541,22 @@ int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream) {
     if (blocks == 0) return kOk;
     DLLM_REQUIRE(blocks < (int64_t{1} << 31), "attention matmul grid too large");
     const dim3 grid(static_cast<unsigned>(blocks));
-#define DLLM_ATTN_TILES(CJ, AF, EX, OD) \
-    hipLaunchKernelGGL((attn_tile_kernel<CJ, AF, EX, OD>), grid, dim3(256), 0, stream, p)
     if (c.a_float) {
-        if (c.out_double) DLLM_ATTN_TILES(4, true, true, true);
-        else DLLM_ATTN_TILES(4, true, true, false);
+        DLLM_REQUIRE(c.L % 4 == 0 && c.B.group <= 1 && c.A.group <= 1 && !c.second,
+                     "the matrix-core scores take whole 4-l steps and plain operand rows");
+        if (c.out_double)
+            hipLaunchKernelGGL(attn_mfma_kernel<true>, dim3(static_cast<unsigned>(p.tiles_i * p.tiles_j * p.Z)),
+                               dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL(attn_mfma_kernel<false>, dim3(static_cast<unsigned>(p.tiles_i * p.tiles_j * p.Z)),
+                               dim3(256), 0, stream, p);
     } else {
         DLLM_REQUIRE(!c.exact_products && !c.out_double,
                      "double A operands are the probability and dS rows (multiply, then add; float outputs)");
-        if (cj == 2) DLLM_ATTN_TILES(2, false, false, false);
-        else if (cj == 1) DLLM_ATTN_TILES(1, false, false, false);
+        if (cj == 2) hipLaunchKernelGGL(attn_tile_kernel<2>, grid, dim3(256), 0, stream, p);
+        else if (cj == 1) hipLaunchKernelGGL(attn_tile_kernel<1>, grid, dim3(256), 0, stream, p);
         else return fail(kInvalidArgument, "double A operands take 64 or 128 columns per tile");
     }
-#undef DLLM_ATTN_TILES
     return check_launch("attention tiles");
 }
 

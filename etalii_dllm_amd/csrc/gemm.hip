@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "lds_copy.h"
 #include "kernels.h"
 
 namespace dllm_hip {
@@ -186,15 +187,6 @@ struct Stage {
 template <int kA>
 constexpr int stage_loads() {
     return (kA == kADouble ? 2 : 1) + 4;
-}
-
-// 16 bytes from global memory to LDS at lds_row + 16 * lane (gfx950 direct-to-LDS load; M0 holds the LDS address).
-// Written as inline assembly so the compiler's wait-count pass does not stall the LDS reads of the current stage on
-// the in-flight copies of the next one; the pipeline waits for its own copies explicitly (wait_stage).
-__device__ __forceinline__ void copy16_to_lds(const void* src, const void* lds_row) {
-    typedef __attribute__((address_space(3))) const void* lds_address;
-    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
 // Waits until at most `pending` of this wave's vector-memory operations are outstanding, then joins the workgroup.
@@ -537,20 +529,6 @@ __host__ __device__ __forceinline__ MCopyOffsets mcopy_offsets(const GemmParams&
                                        reinterpret_cast<const char*>(p.Af));
     }
     return o;
-}
-
-// 16 bytes from sbase + voff (SGPR base, VGPR offset) to LDS at lds_row + 16 * lane.
-__device__ __forceinline__ void copy16_to_lds_s(const float* sbase, uint32_t voff, const void* lds_row) {
-    typedef __attribute__((address_space(3))) const void* lds_address;
-    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
-    // the base is wave-uniform; readfirstlane states it where the compiler cannot prove it (grouped launches)
-    const uint64_t a = reinterpret_cast<uint64_t>(sbase);
-    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu)));
-    const uint64_t u = (static_cast<uint64_t>(hi) << 32) | lo;
-    // s_nop 4: a vector instruction that wrote the base SGPRs (readfirstlane) must be 5 wait states ahead of a memory
-    // instruction reading them, and the compiler's hazard checks do not look inside this statement
-    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u), "{m0}"(m0) : "memory");
 }
 
 template <int kA>
