@@ -275,6 +275,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--export-timing", action="store_true",
+                    help="after the timed steps, time the model and checkpoint fingerprints streamed from device "
+                         "memory (stderr only)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of 1 GiB (the reference kernel for HBM byte counters)")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
@@ -331,6 +334,12 @@ def main() -> int:
     launches, ms, flops = C.c_int64(), C.c_double(), C.c_double()
     check(lib.dllm_hip_trainer_profile_read(trainer.handle, C.byref(launches), C.byref(ms), C.byref(flops)))
     check(lib.dllm_hip_trainer_profile(trainer.handle, 0))
+    if args.export_timing:
+        for kind, what in ((0, "model.dllm data"), (1, "checkpoint data")):
+            t_start = time.perf_counter()
+            digest = trainer.fingerprint(kind)
+            seconds = time.perf_counter() - t_start
+            log(f"{what} fingerprint {digest[:16]}...: {seconds:.2f} s")
     trainer.close()
     ms_per_step = elapsed * 1000.0 / args.steps
     achieved = flops.value / (ms.value * 1e9) if ms.value > 0 else 0.0  # TFLOP/s

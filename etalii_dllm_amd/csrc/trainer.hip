@@ -32,6 +32,7 @@
 #include "common.h"
 #include "devmath.h"
 #include "dllm_hip.h"
+#include "export.h"
 #include "kernels.h"
 
 using namespace dllm_hip;
@@ -1412,6 +1413,37 @@ struct dllm_hip_trainer {
         }
         return kOk;
     }
+
+    // The data sections of the reference's files (device pointers, in file order):
+    //   kModelFile: weights() in natural order (trainer.py:460-468): the parameters, with every LoRA target merged
+    //     (and a Q8_0 base applied), as FineTuner.export writes them (trainer.py:477-509);
+    //   kCheckpointFile: _checkpoint_tensors (trainer.py:519-522): "param/<name>" for the trained tensors (the
+    //     adapters in a LoRA run) in natural order, then adam_m/<name>, adam_v/<name> per tensor in natural order
+    //     (optimizer.py:111-114).
+    int file_tensors(int kind, std::vector<TensorSource>* out, hipStream_t s) {
+        out->clear();
+        if (kind == kModelFile) {
+            if (lora_on) DLLM_TRY(prepare_lora(s));
+            for (size_t i = 0; i < tensors.size(); ++i) {
+                const TensorInfo& t = tensors[i];
+                const bool merged_t = lora_on && merged_offset[i] >= 0;
+                out->push_back(TensorSource{(merged_t ? merged.as<float>() + merged_offset[i] : params.as<float>() +
+                                                                                                      t.offset),
+                                            t.numel, true});
+            }
+            return kOk;
+        }
+        const std::vector<TensorInfo>& set = lora_on ? adapters : tensors;
+        const DevBuf& p = lora_on ? lora_p : params;
+        const DevBuf& m = lora_on ? lora_m : m1;
+        const DevBuf& v = lora_on ? lora_v : m2;
+        for (const TensorInfo& t : set) out->push_back(TensorSource{p.as<float>() + t.offset, t.numel, true});
+        for (const TensorInfo& t : set) {
+            out->push_back(TensorSource{m.as<float>() + t.offset, t.numel, true});
+            out->push_back(TensorSource{v.as<float>() + t.offset, t.numel, true});
+        }
+        return kOk;
+    }
 };
 
 extern "C" {
@@ -1556,6 +1588,43 @@ int dllm_hip_trainer_step(dllm_hip_trainer* t, const int64_t* tokens, const int6
                           void* stream) {
     DLLM_REQUIRE(t && tokens && offsets && lengths && adamw, "null argument");
     return t->step(tokens, offsets, lengths, windows, adamw, loss, grad_norm, static_cast<hipStream_t>(stream));
+}
+
+int dllm_hip_trainer_fingerprint(dllm_hip_trainer* t, int kind, char* hex_out, void* stream) {
+    DLLM_REQUIRE(t && hex_out, "null argument");
+    DLLM_REQUIRE(kind == kModelFile || kind == kCheckpointFile, "kind must be 0 (model.dllm) or 1 (.dllmckpt)");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<TensorSource> src;
+    DLLM_TRY(t->file_tensors(kind, &src, s));
+    return stream_tensor_data(src.data(), src.size(), nullptr, hex_out, s);
+}
+
+int dllm_hip_trainer_write_file(dllm_hip_trainer* t, int kind, const char* path, const char* header,
+                                size_t header_len, char* hex_out, void* stream) {
+    DLLM_REQUIRE(t && path && header && hex_out, "null argument");
+    DLLM_REQUIRE(kind == kModelFile || kind == kCheckpointFile, "kind must be 0 (model.dllm) or 1 (.dllmckpt)");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<TensorSource> src;
+    DLLM_TRY(t->file_tensors(kind, &src, s));
+    return write_tensor_file(path, kind, header, header_len, src.data(), src.size(), hex_out, s);
+}
+
+int dllm_hip_trainer_read_checkpoint(dllm_hip_trainer* t, const char* path, const char* fingerprint, void* stream) {
+    DLLM_REQUIRE(t && path && fingerprint, "null argument");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    std::vector<TensorSource> src;
+    DLLM_TRY(t->file_tensors(kCheckpointFile, &src, s));
+    char hex[65];
+    // verify the whole data section first (trainer.py:593-594), then load it
+    DLLM_TRY(read_tensor_file_data(path, kCheckpointFile, nullptr, 0, hex, 0, s));
+    DLLM_REQUIRE(strncmp(hex, fingerprint, 64) == 0 && strlen(fingerprint) == 64,
+                 std::string(path) + ": tensor data does not match the fingerprint (corrupt file?)");
+    DLLM_TRY(read_tensor_file_data(path, kCheckpointFile, src.data(), src.size(), hex, 1, s));
+    DLLM_REQUIRE(strncmp(hex, fingerprint, 64) == 0, std::string(path) + ": the file changed while it was read");
+    t->wt_valid = false;  // new parameters: transposes, merged weights and the quantised base are rebuilt
+    t->merged_valid = false;
+    if (t->lora_on && t->lc.base_quantize) t->base_ready = false;
+    return kOk;
 }
 
 }  // extern "C"

@@ -185,3 +185,66 @@ class Trainer:
                                         lengths.ctypes.data_as(_i64p), len(windows), C.byref(args), C.byref(loss),
                                         C.byref(norm), None))
         return loss.value, norm.value
+
+    # ---- files (modelfile.py, trainer.py:477-630) ----
+
+    def fingerprint(self, kind: int = 0) -> str:
+        """The SHA-256 of the data section the trainer would write: kind 0 the model file of weights() (equal to
+        modelfile.data_fingerprint of the exported weights), kind 1 the checkpoint; streamed from device memory."""
+        from etalii_dllm_amd.files import lib as flib
+
+        out = C.create_string_buffer(65)
+        check(flib.dllm_hip_trainer_fingerprint(self.handle, kind, out, None))
+        return out.value.decode()
+
+    def base_names(self) -> list[str]:
+        """The model's tensors (weights()) in natural order."""
+        return [n for n in self.names if not (n.endswith(".lora_a") or n.endswith(".lora_b"))]
+
+    def trained_names(self) -> list[str]:
+        """What AdamW updates: the adapters in a LoRA run, every tensor otherwise (natural order)."""
+        if self._lora is None:
+            return list(self.names)
+        return [n for n in self.names if n.endswith(".lora_a") or n.endswith(".lora_b")]
+
+    def export(self, path, architecture: dict, metadata: dict, shapes: dict) -> str:
+        """FineTuner.export's file (trainer.py:477-509): `metadata` is the complete metadata the reference passes to
+        write_model_file (with its fine_tuning and lineage sections); returns the fingerprint."""
+        from etalii_dllm_amd import files
+
+        header = files.model_header(architecture, shapes, metadata, self.base_names())
+        out = C.create_string_buffer(65)
+        check(files.lib.dllm_hip_trainer_write_file(self.handle, files.MODEL, str(path).encode(), header, len(header),
+                                                    out, None))
+        return out.value.decode()
+
+    def save_checkpoint(self, path, shapes: dict, **fields) -> str:
+        """FineTuner.save_checkpoint (trainer.py:524-568): fields are the header's architecture, run, step, losses,
+        base_fingerprint, data_fingerprint, metadata (and reference); returns the checkpoint fingerprint."""
+        from etalii_dllm_amd import files
+
+        header = files.checkpoint_header(shapes=shapes, order=self.trained_names(), **fields)
+        out = C.create_string_buffer(65)
+        check(files.lib.dllm_hip_trainer_write_file(self.handle, files.CHECKPOINT, str(path).encode(), header,
+                                                    len(header), out, None))
+        return out.value.decode()
+
+    def load_checkpoint(self, path, data_fingerprint: str | None = None) -> dict:
+        """FineTuner.load_checkpoint's checks and restore (trainer.py:570-630) for this trainer's tensors: the data
+        must match the header's fingerprint (and the run's data fingerprint, when given), the tensor list must be
+        this trainer's. Returns the header (step, losses, run, metadata ...) for the caller's loop state."""
+        from etalii_dllm_amd import files
+
+        header = files.read_header(path, files.CHECKPOINT)
+        if data_fingerprint is not None and header.get("data_fingerprint") != data_fingerprint:
+            raise files.CheckpointError(f"{path}: the checkpoint was trained on different data")
+        order = self.trained_names()
+        want = [f"param/{n}" for n in order] + [f"{k}/{n}" for n in order for k in ("adam_m", "adam_v")]
+        if [e["name"] for e in header.get("tensors", [])] != want:
+            raise files.CheckpointError(f"{path}: the checkpoint holds other tensors than this run trains")
+        status = files.lib.dllm_hip_trainer_read_checkpoint(self.handle, str(path).encode(),
+                                                            str(header.get("fingerprint", "")).encode(), None)
+        if status == 1:
+            raise files.CheckpointError(lib.dllm_hip_last_error().decode())
+        check(status)
+        return header

@@ -263,6 +263,36 @@ int dllm_hip_trainer_step(dllm_hip_trainer* trainer, const int64_t* tokens, cons
 int dllm_hip_trainer_profile(dllm_hip_trainer* trainer, int enable);
 int dllm_hip_trainer_profile_read(dllm_hip_trainer* trainer, int64_t* launches, double* milliseconds, double* flops);
 
+/* ---- model and checkpoint files (src/etalii_dllm/modelfile.py, training/trainer.py:477-630) ----
+ * kind 0: model.dllm (write_model_file, modelfile.py:68-136): prefix "DLLM", u32 1, u64 header length; the data
+ *   section is weights() (trainer.py:460-468; LoRA targets merged) in natural order.
+ * kind 1: .dllmckpt (FineTuner.save_checkpoint, trainer.py:524-568): prefix "DLLMCKPT", u32 1, u64 header length;
+ *   the data section is param/<name> for the trained tensors, then adam_m/<name>, adam_v/<name> per tensor.
+ * Every tensor is float32, padded with zeros to 64 bytes; the fingerprint is the SHA-256 of the data section
+ * (modelfile.data_fingerprint, modelfile.py:228-235, for kind 0). hex_out receives 64 hex digits and a NUL. */
+
+/* The fingerprint of a trainer's current data section, streamed from device memory (waits). Replaces
+ * modelfile.data_fingerprint(FineTuner.weights()) and the checkpoint's data hash without a host copy. */
+int dllm_hip_trainer_fingerprint(dllm_hip_trainer* trainer, int kind, char* hex_out, void* stream);
+/* Writes a file: header is the caller's canonical JSON (modelfile.canonical_json of the header dict, with
+ * "fingerprint" set to 64 zeros, unpadded); the library pads it with spaces so the data starts at a multiple of 64,
+ * streams the data section from device memory and patches the fingerprint into the header. Same bytes as
+ * write_model_file / save_checkpoint for the same header. */
+int dllm_hip_trainer_write_file(dllm_hip_trainer* trainer, int kind, const char* path, const char* header,
+                                size_t header_len, char* hex_out, void* stream);
+/* Restores the trained tensors and both moments from a checkpoint (FineTuner.load_checkpoint, trainer.py:570-630):
+ * the data section's SHA-256 must equal `fingerprint` (the header's, 64 hex digits) or status 1 is returned and
+ * nothing is loaded. The caller checks the header (data fingerprint, base model, tensor list). */
+int dllm_hip_trainer_read_checkpoint(dllm_hip_trainer* trainer, const char* path, const char* fingerprint,
+                                     void* stream);
+/* Host-only helpers (no GPU): SHA-256 of a buffer (impl 0 fastest, 1 portable, 2 x86 SHA extensions when present);
+ * a tensor file from host arrays (the layout above); the SHA-256 of a file's data section. No counterpart in the
+ * kernel module: hashlib.sha256, write_model_file with host tensors, and ModelFile.verify's hash. */
+int dllm_hip_sha256(const void* data, size_t n, int impl, char* hex_out);
+int dllm_hip_write_tensor_file(const char* path, int kind, const char* header, size_t header_len,
+                               const float* const* host_tensors, const int64_t* numels, size_t count, char* hex_out);
+int dllm_hip_tensor_file_fingerprint(const char* path, int kind, char* hex_out);
+
 /* ---- seeded synthetic inputs (kernels.cpp:130-136 `Random`, kernels.cpp:206-218 `fill_gaussian`) ----
  * Host functions: n Irwin-Hall Gaussians of Random(seed), times scale (one float multiply; 1 keeps them as is), and
  * n token ids Random(seed).next_u64() % vocab. */

@@ -62,6 +62,61 @@ def test_finetune_fingerprint_on_gpu(family):
         t.step(batch, opt.learning_rate_at(step + 1, 6), step + 1)
     params = {n: t.get(n, d.tensor_shapes()[n]) for n in t.names}
     assert O.data_fingerprint(params) == GOLDEN["FINETUNE_FINGERPRINT"][family]
+    assert t.fingerprint() == GOLDEN["FINETUNE_FINGERPRINT"][family]  # hashed from device memory
+
+
+def checkpoint_fields(d: O.Decoder, step: int, losses):
+    return {"architecture": {"family": d.family, "hidden": d.hidden, "layers": d.layers}, "run": {"steps": 6},
+            "step": step, "losses": losses, "base_fingerprint": "b" * 64, "data_fingerprint": "d" * 64,
+            "metadata": {"lineage": [{"step": "import"}]}}
+
+
+@pytest.mark.parametrize("family", ["llama", "olmoe"])
+def test_export_and_checkpoint_resume_on_gpu(family, tmp_path):
+    """test_training.py:365-400 on the GPU: a run checkpointed at step 3 and resumed in a fresh trainer gives the
+    same final checkpoint and the same exported model, whose fingerprint is the reference's FINETUNE_FINGERPRINT."""
+    from etalii_dllm_amd import files
+
+    d = O.FIXTURES[family]
+    shapes = d.tensor_shapes()
+    windows = ascii_windows()
+    opt = O.AdamWConfig(learning_rate=1e-2)
+    batches = [[windows[i] for i in O.batch_indices(len(windows), step, 3, 3)] for step in range(6)]
+    first = make_trainer(d, O.fixture_weights(d))
+    losses = []
+    for step in range(3):
+        losses.append(first.step(batches[step], opt.learning_rate_at(step + 1, 6), step + 1)[0])
+    middle = first.save_checkpoint(tmp_path / "middle.dllmckpt", shapes, **checkpoint_fields(d, 3, losses))
+    assert middle == first.fingerprint(files.CHECKPOINT)
+    for step in range(3, 6):
+        losses.append(first.step(batches[step], opt.learning_rate_at(step + 1, 6), step + 1)[0])
+    final = first.save_checkpoint(tmp_path / "final.dllmckpt", shapes, **checkpoint_fields(d, 6, losses))
+    metadata = {"licence": {"id": "apache-2.0"}, "fine_tuning": {"steps_completed": 6, "final_loss": losses[-1]}}
+    arch = {"family": d.family, "hidden": d.hidden}
+    exported = first.export(tmp_path / "first.dllm", arch, metadata, shapes)
+    assert exported == GOLDEN["FINETUNE_FINGERPRINT"][family]
+    assert files.file_fingerprint(tmp_path / "first.dllm", files.MODEL) == exported
+    header = files.read_header(tmp_path / "first.dllm", files.MODEL)
+    assert [e["name"] for e in header["tensors"]] == O.tensor_order(shapes) and header["fingerprint"] == exported
+
+    second = make_trainer(d, {n: np.zeros(s, np.float32) for n, s in shapes.items()})
+    restored = second.load_checkpoint(tmp_path / "middle.dllmckpt", data_fingerprint="d" * 64)
+    assert restored["step"] == 3 and restored["losses"] == losses[:3]
+    for step in range(3, 6):
+        assert second.step(batches[step], opt.learning_rate_at(step + 1, 6), step + 1)[0] == losses[step]
+    assert second.save_checkpoint(tmp_path / "resumed.dllmckpt", shapes, **checkpoint_fields(d, 6, losses)) == final
+    assert (tmp_path / "resumed.dllmckpt").read_bytes() == (tmp_path / "final.dllmckpt").read_bytes()
+    assert second.export(tmp_path / "second.dllm", arch, metadata, shapes) == exported
+    assert (tmp_path / "second.dllm").read_bytes() == (tmp_path / "first.dllm").read_bytes()
+
+    with pytest.raises(files.CheckpointError, match="different data"):
+        second.load_checkpoint(tmp_path / "middle.dllmckpt", data_fingerprint="e" * 64)
+    raw = bytearray((tmp_path / "middle.dllmckpt").read_bytes())
+    raw[-1] ^= 1
+    (tmp_path / "corrupt.dllmckpt").write_bytes(bytes(raw))
+    with pytest.raises(files.CheckpointError, match="fingerprint"):
+        second.load_checkpoint(tmp_path / "corrupt.dllmckpt")
+    assert second.fingerprint(files.CHECKPOINT) == final  # a rejected file leaves the state alone
 
 
 def test_step_matches_the_oracle_on_ragged_windows():
@@ -121,6 +176,32 @@ def test_lora_finetune_fingerprint_on_gpu(family):
     for name in O.lora_target_weights(d, lora):
         merged[name] = K.lora_merge(base[name], adapters[name + ".lora_a"], adapters[name + ".lora_b"], lora.scale)
     assert O.data_fingerprint(merged) == GOLDEN["LORA_FINETUNE_FINGERPRINT"][family]
+    assert t.fingerprint() == GOLDEN["LORA_FINETUNE_FINGERPRINT"][family]  # merged on and hashed from the device
+
+
+def test_lora_checkpoint_holds_the_adapters_and_restores_the_run(tmp_path):
+    """A LoRA checkpoint holds the adapters and their moments only (trainer.py:519-522, 616-622); restored into a
+    trainer on the same base, the export is the reference's LORA_FINETUNE_FINGERPRINT."""
+    from etalii_dllm_amd import files
+
+    d = O.FIXTURES["llama"]
+    lora = O.Lora(rank=2, alpha=4.0)
+    base = O.fixture_weights(d)
+    shapes = {**d.tensor_shapes(), **O.adapter_shapes(d, lora)}
+    t = make_lora_trainer(d, base, lora, O.init_adapters(d, lora, 3))
+    windows = ascii_windows()
+    opt = O.AdamWConfig(learning_rate=3e-2)
+    for step in range(6):
+        batch = [windows[i] for i in O.batch_indices(len(windows), step, 3, 3)]
+        t.step(batch, opt.learning_rate_at(step + 1, 6), step + 1)
+    fields = checkpoint_fields(d, 6, [])
+    saved = t.save_checkpoint(tmp_path / "lora.dllmckpt", shapes, **fields)
+    header = files.read_header(tmp_path / "lora.dllmckpt", files.CHECKPOINT)
+    assert all(e["name"].endswith((".lora_a", ".lora_b")) for e in header["tensors"])
+    fresh = make_lora_trainer(d, base, lora, {n: np.zeros(s, np.float32) for n, s in O.adapter_shapes(d, lora).items()})
+    fresh.load_checkpoint(tmp_path / "lora.dllmckpt")
+    assert fresh.fingerprint(files.CHECKPOINT) == saved
+    assert fresh.fingerprint() == GOLDEN["LORA_FINETUNE_FINGERPRINT"]["llama"]
 
 
 @pytest.mark.parametrize("base_quantize", [None, "q8_0"])
