@@ -10,17 +10,18 @@
 
 namespace dllm_hip {
 
-__host__ __device__ inline double pow2_bits(int k) {
-    return __longlong_as_double(static_cast<long long>(static_cast<uint64_t>(k + 1023) << 52));
-}
+__host__ __device__ inline double bits_double(uint64_t b) { return __builtin_bit_cast(double, b); }
+__host__ __device__ inline uint64_t double_bits(double x) { return __builtin_bit_cast(uint64_t, x); }
+
+__host__ __device__ inline double pow2_bits(int k) { return bits_double(static_cast<uint64_t>(k + 1023) << 52); }
 
 // e^x (math.hpp:64-109).
-__device__ inline double dexp(double x) {
+__host__ __device__ inline double dexp(double x) {
     const double ln2_hi = 6.93147180369123816490e-01;
     const double ln2_lo = 1.90821492927058770002e-10;
     const double inv_ln2 = 1.44269504088896338700e+00;
     if (x != x) return x;
-    if (x > 709.78) return __longlong_as_double(0x7ff0000000000000LL);
+    if (x > 709.78) return bits_double(0x7ff0000000000000ULL);
     if (x < -745.2) return 0.0;
     const double kd = x * inv_ln2;
     const int k = static_cast<int>(kd >= 0 ? kd + 0.5 : kd - 0.5);
@@ -52,22 +53,22 @@ __device__ inline double dexp(double x) {
 }
 
 // log x (math.hpp:113-162).
-__device__ inline double dlog(double x) {
+__host__ __device__ inline double dlog(double x) {
     const double ln2_hi = 6.93147180369123816490e-01;
     const double ln2_lo = 1.90821492927058770002e-10;
     const double sqrt_half = 7.07106781186547524401e-01;
-    if (x != x || x < 0.0) return __longlong_as_double(0x7ff8000000000000LL);
-    if (x == 0.0) return __longlong_as_double(static_cast<long long>(0xfff0000000000000ULL));
-    if (x == __longlong_as_double(0x7ff0000000000000LL)) return x;
+    if (x != x || x < 0.0) return bits_double(0x7ff8000000000000ULL);
+    if (x == 0.0) return bits_double(0xfff0000000000000ULL);
+    if (x == bits_double(0x7ff0000000000000ULL)) return x;
     int e = 0;
     if (x < 2.2250738585072014e-308) {
         x *= pow2_bits(54);
         e -= 54;
     }
-    uint64_t bits = static_cast<uint64_t>(__double_as_longlong(x));
+    uint64_t bits = double_bits(x);
     e += static_cast<int>((bits >> 52) & 0x7ff) - 1023;
     bits = (bits & 0x000fffffffffffffULL) | 0x3ff0000000000000ULL;
-    double m = __longlong_as_double(static_cast<long long>(bits));
+    double m = bits_double(bits);
     if (m >= 2.0 * sqrt_half) {
         m *= 0.5;
         e += 1;
@@ -187,7 +188,7 @@ __device__ inline double dtanh(double x) {
 }
 
 // sigmoid (math.hpp:322-328).
-__device__ inline double dsigmoid(double x) {
+__host__ __device__ inline double dsigmoid(double x) {
     if (x >= 0) return 1.0 / (1.0 + dexp(-x));
     const double e = dexp(x);
     return e / (1.0 + e);

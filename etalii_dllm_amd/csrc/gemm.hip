@@ -64,6 +64,7 @@ struct GemmParams {
     int64_t ld_seg_add;
     float* partial;  // segment-parallel mode: [nseg][I][J] per-window results (null: windows run in sequence)
     const float* Af;  // float A operands: [L][lda] (A rows) or [I][lda] (A transposed: Af[i][l] = A[l][i])
+    const float* seg_weight;  // segmented mode: per-window factors on each window's result (null: none)
 };
 
 // The raw B values of row l for this lane's 4 columns. Lanes past J read a clamped in-bounds column instead (their
@@ -726,6 +727,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     if (j >= p.J) continue;
                     float v = static_cast<float>(acc[bi][bj][r]);
                     if (p.seg_addrow) v = v + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j] : 0.0f);
+                    if (p.seg_weight) v = v * p.seg_weight[s];  // the window's whole gradient times its factor
                     out[j] = (kMode == kWindowsInParallel || s == 0) ? v : out[j] + v;
                 }
             }
@@ -826,7 +828,7 @@ namespace {
 
 GemmParams params_of(const GemmCall& g) {
     return GemmParams{g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.I, g.J, g.l0, g.l1, g.seg, g.nseg, g.bias, g.addsrc,
-                      g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af};
+                      g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af, g.seg_weight};
 }
 
 }  // namespace
@@ -897,6 +899,8 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     DLLM_REQUIRE(g.I >= 0 && g.J >= 0, "negative matmul size");
     DLLM_REQUIRE(g.seg == nullptr || g.nseg >= 1, "segmented matmul needs at least one segment");
     DLLM_REQUIRE(g.seg != nullptr || g.seg_addrow == nullptr, "per-window addends need segments");
+    DLLM_REQUIRE(g.seg_weight == nullptr || (g.seg != nullptr && g.a_kind == kAFloatRows),
+                 "per-window factors are for windowed weight gradients with float A rows");
     const int ak = g.a_kind;
     DLLM_REQUIRE(ak == kADouble || ak == kAFloatRows || ak == kAFloatT, "unknown A operand kind");
     if (ak == kADouble) DLLM_REQUIRE(g.lda >= padded_rows(g.I), "the double operand must be padded to whole row tiles");

@@ -194,12 +194,17 @@ __global__ __launch_bounds__(256) void column_partial_kernel(int kind, const flo
 }
 
 // out[i] = part[0][i] + part[1][i] + ... in float, segment order (trainer.py:328-332: the first copied).
+// out = part[0] + part[1] + ... in float, window order, the first copied; with factors, each window's part is first
+// multiplied by its factor (window s adds f32(part[s] * w[s])).
 __global__ __launch_bounds__(256) void segment_float_sum_kernel(const float* __restrict__ part, int64_t dim, int nseg,
-                                                                float* __restrict__ out) {
+                                                                const float* __restrict__ w, float* __restrict__ out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= dim) return;
-    float t = part[i];
-    for (int s = 1; s < nseg; ++s) t = t + part[static_cast<int64_t>(s) * dim + i];
+    float t = w ? part[i] * w[0] : part[i];
+    for (int s = 1; s < nseg; ++s) {
+        const float v = part[static_cast<int64_t>(s) * dim + i];
+        t = t + (w ? v * w[s] : v);
+    }
     out[i] = t;
 }
 
@@ -350,21 +355,26 @@ int launch_rms_norm_backward_dx(const float* x, const float* w, const float* dy,
 }
 
 int launch_column_sums(int kind, const float* dy, const float* x, const double* inv_rms, int64_t dim,
-                       const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream) {
+                       const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream,
+                       const float* weights) {
     if (dim == 0) return kOk;
     DLLM_REQUIRE(nseg >= 1, "column sums need a segment");
-    DLLM_REQUIRE(nseg == 1 || partial != nullptr, "column sums over several segments need a partial buffer");
+    DLLM_REQUIRE((nseg == 1 && !weights) || partial != nullptr,
+                 "column sums over several segments (or with factors) need a partial buffer");
+    const bool direct = nseg == 1 && !weights;
     const unsigned col_blocks = static_cast<unsigned>(ceil_div(dim, 64));
     for (int s0 = 0; s0 < nseg; s0 += kColSegs) {
         const int count = nseg - s0 < kColSegs ? nseg - s0 : kColSegs;
         ColSegments seg{};
         for (int s = 0; s <= count; ++s) seg.off[s] = seg_host[s0 + s];
-        float* part = nseg == 1 ? out : partial + static_cast<int64_t>(s0) * dim;
+        float* part = direct ? out : partial + static_cast<int64_t>(s0) * dim;
         hipLaunchKernelGGL(column_partial_kernel, dim3(col_blocks, static_cast<unsigned>(count)), dim3(256), 0, stream,
                            kind, dy, x, inv_rms, dim, seg, part);
     }
     const unsigned blocks = static_cast<unsigned>(ceil_div(dim, 256));
-    if (nseg > 1) hipLaunchKernelGGL(segment_float_sum_kernel, dim3(blocks), dim3(256), 0, stream, partial, dim, nseg, out);
+    if (!direct)
+        hipLaunchKernelGGL(segment_float_sum_kernel, dim3(blocks), dim3(256), 0, stream, partial, dim, nseg, weights,
+                           out);
     return check_launch("column_sums");
 }
 

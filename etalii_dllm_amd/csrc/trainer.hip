@@ -124,13 +124,16 @@ __global__ void inv_freq_kernel(int64_t rotary_dim, double theta, double* out) {
 // token v contributes +0.0f), the first window copied.
 __global__ __launch_bounds__(256) void sparse_window_sum_kernel(const float* __restrict__ rows,
                                                                 const int* __restrict__ addrow, int64_t vocab,
-                                                                int64_t dim, int windows, float* __restrict__ out) {
+                                                                int64_t dim, int windows,
+                                                                const float* __restrict__ weights,
+                                                                float* __restrict__ out) {
     const int64_t v = blockIdx.x;
     for (int64_t d = threadIdx.x; d < dim; d += 256) {
         float t = 0.0f;
         for (int w = 0; w < windows; ++w) {
             const int r = addrow[static_cast<int64_t>(w) * vocab + v];
-            const float val = r >= 0 ? rows[static_cast<int64_t>(r) * dim + d] : 0.0f;
+            float val = r >= 0 ? rows[static_cast<int64_t>(r) * dim + d] : 0.0f;
+            if (weights) val = val * weights[w];  // the window's whole gradient times its factor
             t = w == 0 ? val : t + val;
         }
         out[v * dim + d] = t;
@@ -494,6 +497,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&row_total, R));
         DLLM_TRY(make(&row_loss, R));
         DLLM_TRY(make(&loss_w, W_max));
+        DLLM_TRY(make(&win_weight, W_max));
         DLLM_TRY(make(&inv_freq, std::max<int64_t>(c.rotary_dim / 2, 1)));
         DLLM_TRY(make(&cos_t, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
         DLLM_TRY(make(&sin_t, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
@@ -699,6 +703,7 @@ struct dllm_hip_trainer {
         g.ld_seg_add = K;
         g.seg_partial = gemm_part;
         g.seg_partial_cap = gemm_part_cap;
+        g.seg_weight = window_weights();
         return g;
     }
 
@@ -707,7 +712,7 @@ struct dllm_hip_trainer {
         if (!grad_wanted(out)) return kOk;
         std::vector<int64_t> seg(seg_host.size());
         for (size_t i = 0; i < seg.size(); ++i) seg[i] = seg_host[i] * rows_per_token;
-        return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s);
+        return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s, window_weights());
     }
 
     // ---- attention (attn_lds.hip, attn_chains.hip) ----
@@ -921,7 +926,7 @@ struct dllm_hip_trainer {
             DLLM_TRY(linear_dw(ds[p], ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s));
             if (bs_[p] >= 0 && grad_wanted(G(bs_[p])))
                 DLLM_TRY(launch_column_sums(0, ds[p], nullptr, nullptr, ns[p], seg_host.data(), nseg, col_part,
-                                            G(bs_[p]), s));
+                                            G(bs_[p]), s, window_weights()));
         }
         // attention norm; dx = dx_mid + dh1'
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh, dx, dx_mid, R, H, eps, 0, inv_rms, s));
@@ -1104,7 +1109,7 @@ struct dllm_hip_trainer {
                 const int64_t a = tokens[offsets[w] + t], z = tokens[offsets[w] + t + 1];
                 DLLM_REQUIRE(a >= 0 && a < V && z >= 0 && z < V, "token id out of range");
                 in.push_back(a);
-                tgt.push_back(z);
+                tgt.push_back(ignore_targets != nullptr && t < ignore_targets[w] ? -1 : z);
                 pos.push_back(t);
             }
             seg.push_back(seg.back() + n);
@@ -1189,6 +1194,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(check_hip(hipMemsetAsync(err_flag, 0, sizeof(int), s), "memset"));
         DLLM_TRY(launch_cross_entropy(logits, tok_tgt, dlogits, R, V, scale, seg_d, nseg, row_max, row_total, row_loss,
                                       loss_w, err_flag, s));
+        if (dpo.on) DLLM_TRY(dpo_weights(windows, s));
         float* dhidden = dh;
         DLLM_TRY(linear_dx(dlogits, R, head, dhidden, nullptr, s));
         DLLM_TRY(launch_rms_norm_backward_dx(x_final, P(final_norm), dhidden, dx, nullptr, R, H, eps, 0, inv_rms, s));
@@ -1202,7 +1208,7 @@ struct dllm_hip_trainer {
         } else {
             DLLM_TRY(linear_dw(dlogits, V, hidden, H, nseg, G(lm_head), nullptr, nullptr, s));
             hipLaunchKernelGGL(sparse_window_sum_kernel, dim3(static_cast<unsigned>(V)), dim3(256), 0, s, emb_rows,
-                               addrow, V, H, nseg, G(emb));
+                               addrow, V, H, nseg, window_weights(), G(emb));
             DLLM_TRY(check_launch("embedding window sum"));
         }
         return finish_gradients(windows, loss, router_loss, s);
@@ -1219,6 +1225,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(check_hip(hipMemcpyAsync(&flag, err_flag, sizeof flag, hipMemcpyDeviceToHost, s), "download"));
         DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
         DLLM_REQUIRE(flag == 0, "target out of range");
+        window_losses = lw;
         double total = 0.0;
         for (double x : lw) total += x;  // trainer.py:326 (loss_total += loss, batch order)
         if (loss) *loss = total;
@@ -1238,6 +1245,20 @@ struct dllm_hip_trainer {
         double loss_total = 0.0, router_total = 0.0;
         DLLM_TRY(gradients(tokens, offsets, lengths, windows, scale, a->router_aux_loss / static_cast<double>(windows),
                            &loss_total, &router_total, s));
+        double grad_norm = 0.0;
+        DLLM_TRY(optimizer_step(a, &grad_norm, s));
+        if (loss) {
+            *loss = loss_total / static_cast<double>(targets_total);
+            if (a->router_aux_loss != 0.0)  // trainer.py:333-335
+                *loss += a->router_aux_loss * router_total / static_cast<double>(windows);
+        }
+        if (norm) *norm = grad_norm;
+        return kOk;
+    }
+
+    // The update of a step from its summed gradients (trainer.py:303-306): LoRA adapter gradients, the global norm and
+    // clip, and AdamW over what the run trains (waits; *norm gets the norm before clipping).
+    int optimizer_step(const dllm_hip_adamw* a, double* norm, hipStream_t s) {
         if (lora_on) DLLM_TRY(adapter_gradients(s));  // trainer.py:463-474
         OptimizerSet& o = lora_on ? lora_opt : main_opt;
         // global norm, clip (optimizer.py:66-90), bias corrections by repeated multiplication (optimizer.py:59-63)
@@ -1260,12 +1281,93 @@ struct dllm_hip_trainer {
         double st[3];
         DLLM_TRY(check_hip(hipMemcpyAsync(st, stats, sizeof st, hipMemcpyDeviceToHost, s), "download"));
         DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
-        if (loss) {
-            *loss = loss_total / static_cast<double>(targets_total);
-            if (a->router_aux_loss != 0.0)  // trainer.py:333-335
-                *loss += a->router_aux_loss * router_total / static_cast<double>(windows);
+        *norm = st[1];
+        return kOk;
+    }
+
+    // ---- direct preference optimization (trainer.py:364-384, preference.py:166-179) ----
+    // Windows 2p and 2p + 1 are pair p's chosen and rejected sequences; their targets over the prompt are ignored, so
+    // each window's summed cross-entropy is minus its answer's log-probability. Once the forward pass has the window
+    // losses, the host computes every pair's z and weight; each window's gradient is then multiplied by its factor
+    // (w for the chosen, -w for the rejected answer) before the window-ordered float sum, as
+    // `gradients[name] += gradient * sign` does.
+    struct Dpo {
+        bool on = false;
+        int64_t pairs = 0;
+        double beta = 0.0;
+        const double* reference = nullptr;  // [pairs][2]: the reference model's chosen and rejected log-probabilities
+        double loss_total = 0.0;
+    } dpo;
+    const int64_t* ignore_targets = nullptr;  // per window: leading targets ignored (-1), or null
+    float* win_weight = nullptr;
+    std::vector<double> window_losses;  // the last call's per-window summed cross-entropy
+
+    const float* window_weights() const { return dpo.on ? win_weight : nullptr; }
+
+    static double log_sigmoid(double z) {  // preference.py:174-179 with the portable exp and log
+        if (z >= 0.0) return -dlog(1.0 + dexp(-z));
+        return z - dlog(1.0 + dexp(z));
+    }
+
+    int dpo_weights(int64_t windows, hipStream_t s) {
+        std::vector<double> lw(static_cast<size_t>(windows));
+        DLLM_TRY(check_hip(hipMemcpyAsync(lw.data(), loss_w, lw.size() * 8, hipMemcpyDeviceToHost, s), "download"));
+        DLLM_TRY(check_hip(hipStreamSynchronize(s), "dpo losses"));
+        std::vector<float> w(static_cast<size_t>(windows));
+        dpo.loss_total = 0.0;
+        for (int64_t p = 0; p < dpo.pairs; ++p) {
+            const double chosen_loss = lw[static_cast<size_t>(2 * p)], rejected_loss = lw[static_cast<size_t>(2 * p + 1)];
+            const double rc = dpo.reference[2 * p], rr = dpo.reference[2 * p + 1];
+            const double z = dpo.beta * ((-chosen_loss - rc) - (-rejected_loss - rr));
+            dpo.loss_total += -log_sigmoid(z);
+            const float weight = static_cast<float>(dpo.beta * (1.0 - dsigmoid(z)) / static_cast<double>(dpo.pairs));
+            w[static_cast<size_t>(2 * p)] = weight;
+            w[static_cast<size_t>(2 * p + 1)] = -weight;
         }
-        if (norm) *norm = st[1];
+        return check_hip(hipMemcpyAsync(win_weight, w.data(), w.size() * sizeof(float), hipMemcpyHostToDevice, s),
+                         "upload");
+    }
+
+    int dpo_step(const int64_t* tokens, const int64_t* offsets, const int64_t* lengths, const int64_t* prompt_lengths,
+                 int64_t pairs, const double* reference, double beta, const dllm_hip_adamw* a, double* loss,
+                 double* norm, hipStream_t s) {
+        DLLM_REQUIRE(pairs >= 1 && 2 * pairs <= W_max, "pairs outside the trainer's capacity");
+        DLLM_REQUIRE(beta > 0.0 && beta < HUGE_VAL, "beta must be a positive number");
+        std::vector<int64_t> ignore(static_cast<size_t>(2 * pairs));
+        for (int64_t p = 0; p < pairs; ++p) {
+            DLLM_REQUIRE(prompt_lengths[p] >= 1, "a pair needs a prompt");
+            for (int k = 0; k < 2; ++k) {
+                DLLM_REQUIRE(lengths[2 * p + k] > prompt_lengths[p], "an answer is empty");
+                ignore[static_cast<size_t>(2 * p + k)] = prompt_lengths[p] - 1;
+            }
+        }
+        dpo = Dpo{true, pairs, beta, reference, 0.0};
+        ignore_targets = ignore.data();
+        const int status = gradients(tokens, offsets, lengths, 2 * pairs, 1.0, 0.0, nullptr, nullptr, s);
+        ignore_targets = nullptr;
+        dpo.on = false;
+        DLLM_TRY(status);
+        double grad_norm = 0.0;
+        DLLM_TRY(optimizer_step(a, &grad_norm, s));
+        if (loss) *loss = dpo.loss_total / static_cast<double>(pairs);  // trainer.py:384
+        if (norm) *norm = grad_norm;
+        return kOk;
+    }
+
+    // Minus the summed cross-entropy of each window with the leading targets ignored: the answers' log-probabilities
+    // (FineTuner.log_probability, trainer.py:443-453; the gradients are computed and not used).
+    int log_probabilities(const int64_t* tokens, const int64_t* offsets, const int64_t* lengths,
+                          const int64_t* prompt_lengths, int64_t windows, double* out, hipStream_t s) {
+        std::vector<int64_t> ignore(static_cast<size_t>(windows));
+        for (int64_t w = 0; w < windows; ++w) {
+            DLLM_REQUIRE(prompt_lengths[w] >= 1 && lengths[w] > prompt_lengths[w], "a window needs a prompt and an answer");
+            ignore[static_cast<size_t>(w)] = prompt_lengths[w] - 1;
+        }
+        ignore_targets = ignore.data();
+        const int status = gradients(tokens, offsets, lengths, windows, 1.0, 0.0, nullptr, nullptr, s);
+        ignore_targets = nullptr;
+        DLLM_TRY(status);
+        for (int64_t w = 0; w < windows; ++w) out[w] = -window_losses[static_cast<size_t>(w)];
         return kOk;
     }
 
@@ -1588,6 +1690,23 @@ int dllm_hip_trainer_step(dllm_hip_trainer* t, const int64_t* tokens, const int6
                           void* stream) {
     DLLM_REQUIRE(t && tokens && offsets && lengths && adamw, "null argument");
     return t->step(tokens, offsets, lengths, windows, adamw, loss, grad_norm, static_cast<hipStream_t>(stream));
+}
+
+int dllm_hip_trainer_dpo_step(dllm_hip_trainer* t, const int64_t* tokens, const int64_t* offsets,
+                              const int64_t* lengths, const int64_t* prompt_lengths, int64_t pairs,
+                              const double* reference, double beta, const dllm_hip_adamw* adamw, double* loss,
+                              double* grad_norm, void* stream) {
+    DLLM_REQUIRE(t && tokens && offsets && lengths && prompt_lengths && reference && adamw, "null argument");
+    return t->dpo_step(tokens, offsets, lengths, prompt_lengths, pairs, reference, beta, adamw, loss, grad_norm,
+                       static_cast<hipStream_t>(stream));
+}
+
+int dllm_hip_trainer_log_probabilities(dllm_hip_trainer* t, const int64_t* tokens, const int64_t* offsets,
+                                       const int64_t* lengths, const int64_t* prompt_lengths, int64_t windows,
+                                       double* out, void* stream) {
+    DLLM_REQUIRE(t && tokens && offsets && lengths && prompt_lengths && out, "null argument");
+    return t->log_probabilities(tokens, offsets, lengths, prompt_lengths, windows, out,
+                                static_cast<hipStream_t>(stream));
 }
 
 int dllm_hip_trainer_fingerprint(dllm_hip_trainer* t, int kind, char* hex_out, void* stream) {

@@ -69,6 +69,11 @@ lib.dllm_hip_trainer_gradients.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_
 lib.dllm_hip_trainer_router_loss.argtypes = [C.c_void_p, C.POINTER(C.c_double)]
 lib.dllm_hip_trainer_step.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_int64, C.POINTER(AdamWArgs),
                                       C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_void_p]
+lib.dllm_hip_trainer_dpo_step.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, _i64p, C.c_int64, C.POINTER(C.c_double),
+                                          C.c_double, C.POINTER(AdamWArgs), C.POINTER(C.c_double),
+                                          C.POINTER(C.c_double), C.c_void_p]
+lib.dllm_hip_trainer_log_probabilities.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, _i64p, C.c_int64,
+                                                   C.POINTER(C.c_double), C.c_void_p]
 
 
 @dataclass(frozen=True)
@@ -248,3 +253,42 @@ class Trainer:
             raise files.CheckpointError(lib.dllm_hip_last_error().decode())
         check(status)
         return header
+
+    # ---- direct preference optimization (trainer.py:364-384, preference.py) ----
+
+    @staticmethod
+    def _pair_windows(pairs):
+        """Windows 2p, 2p + 1: prompt + chosen and prompt + rejected tokens (PreferencePair.sequence)."""
+        windows, prompts = [], []
+        for prompt, chosen, rejected in pairs:
+            windows += [[*prompt, *chosen], [*prompt, *rejected]]
+            prompts.append(len(prompt))
+        return windows, np.ascontiguousarray(prompts, dtype=np.int64)
+
+    def log_probabilities(self, pairs) -> list[tuple[float, float]]:
+        """(chosen, rejected) log-probabilities of each pair under the current weights (FineTuner.log_probability,
+        trainer.py:443-453): the reference values of a DPO run when taken before its first step."""
+        windows, prompts = self._pair_windows(pairs)
+        flat, offsets, lengths = _windows(windows)
+        per_window = np.ascontiguousarray(np.repeat(prompts, 2), dtype=np.int64)
+        out = np.zeros(len(windows), np.float64)
+        check(lib.dllm_hip_trainer_log_probabilities(self.handle, flat.ctypes.data_as(_i64p),
+                                                      offsets.ctypes.data_as(_i64p), lengths.ctypes.data_as(_i64p),
+                                                      per_window.ctypes.data_as(_i64p), len(windows),
+                                                      out.ctypes.data_as(C.POINTER(C.c_double)), None))
+        return [(float(out[2 * p]), float(out[2 * p + 1])) for p in range(len(pairs))]
+
+    def dpo_step(self, pairs, reference, beta: float, learning_rate: float, step: int, beta1=0.9, beta2=0.999,
+                 eps=1e-8, weight_decay=0.01, max_grad_norm=1.0) -> tuple[float, float]:
+        """One DPO step over `pairs` ((prompt, chosen, rejected) token tuples, in batch order) with their reference
+        log-probabilities: (mean loss, gradient norm)."""
+        windows, prompts = self._pair_windows(pairs)
+        flat, offsets, lengths = _windows(windows)
+        ref = np.ascontiguousarray(reference, dtype=np.float64).reshape(-1)
+        args = AdamWArgs(learning_rate, beta1, beta2, eps, weight_decay, max_grad_norm, 0.0, step)
+        loss, norm = C.c_double(), C.c_double()
+        check(lib.dllm_hip_trainer_dpo_step(self.handle, flat.ctypes.data_as(_i64p), offsets.ctypes.data_as(_i64p),
+                                             lengths.ctypes.data_as(_i64p), prompts.ctypes.data_as(_i64p),
+                                             len(pairs), ref.ctypes.data_as(C.POINTER(C.c_double)), beta,
+                                             C.byref(args), C.byref(loss), C.byref(norm), None))
+        return loss.value, norm.value

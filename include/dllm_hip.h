@@ -257,6 +257,23 @@ int dllm_hip_trainer_step(dllm_hip_trainer* trainer, const int64_t* tokens, cons
                           const int64_t* lengths, int64_t windows, const dllm_hip_adamw* adamw, double* loss,
                           double* grad_norm, void* stream);
 
+/* One direct-preference-optimization step (FineTuner._preference_gradients, trainer.py:364-384, then the update of
+ * trainer.py:303-306). Windows 2p and 2p + 1 are pair p's tokens prompt + chosen answer and prompt + rejected answer
+ * (PreferencePair.sequence, preference.py:97-102); their first prompt_lengths[p] - 1 targets are not scored.
+ * reference holds the reference model's log-probabilities, [pairs][chosen, rejected]. With z = beta ((-l_c - r_c) -
+ * (-l_r - r_r)) from the windows' summed cross-entropies l, the gradient is the window-ordered float sum of each
+ * window's gradient times f32(beta (1 - sigmoid(z)) / pairs) (minus that for the rejected answer); *loss is the mean
+ * of -log_sigmoid(z) over the pairs, *grad_norm the norm before clipping (host pointers; waits). */
+int dllm_hip_trainer_dpo_step(dllm_hip_trainer* trainer, const int64_t* tokens, const int64_t* offsets,
+                              const int64_t* lengths, const int64_t* prompt_lengths, int64_t pairs,
+                              const double* reference, double beta, const dllm_hip_adamw* adamw, double* loss,
+                              double* grad_norm, void* stream);
+/* Minus each window's summed cross-entropy with its first prompt_lengths[w] - 1 targets not scored: an answer's
+ * log-probability after its prompt (FineTuner.log_probability, trainer.py:443-453); out is a host array. */
+int dllm_hip_trainer_log_probabilities(dllm_hip_trainer* trainer, const int64_t* tokens, const int64_t* offsets,
+                                       const int64_t* lengths, const int64_t* prompt_lengths, int64_t windows,
+                                       double* out, void* stream);
+
 /* Matmul timing inside steps: with profiling on, every matmul launch of the trainer is bracketed by HIP events on its
  * stream; _read sums them (waiting for the events) into the number of launches, their total milliseconds and their
  * algorithmic flops (2 * rows * columns * reduction length each). Enabling resets the totals. */

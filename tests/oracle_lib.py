@@ -721,6 +721,80 @@ def lora_train_step(kern: Kernels, d: Decoder, base, adapters, m, v, windows, op
     return loss, norm
 
 
+# ---- direct preference optimization (src/etalii_dllm/training/trainer.py:364-384, preference.py) ----
+
+def log_sigmoid(z: float) -> float:
+    """preference.py:174-179 with the portable exp and log."""
+    o = oracle()
+    if z >= 0.0:
+        return -o.orc_log(1.0 + o.orc_exp(-z))
+    return z - o.orc_log(1.0 + o.orc_exp(z))
+
+
+def preference_pairs(records, encode, sequence_length: int, end: int | None):
+    """PreferenceData.from_records (preference.py:110-136): (prompt, chosen, rejected) token tuples."""
+    pairs = []
+    for prompt_text, chosen_text, rejected_text in records:
+        prompt = tuple(encode(prompt_text))
+        room = sequence_length + 1 - len(prompt)
+        suffix = () if end is None else (end,)
+        pairs.append((prompt, (*encode(chosen_text), *suffix)[:room], (*encode(rejected_text), *suffix)[:room]))
+    return pairs
+
+
+def pair_sequence(pair, which: str):
+    """PreferencePair.sequence (preference.py:97-102): inputs and targets, the prompt's targets -1."""
+    prompt, chosen, rejected = pair
+    answer = chosen if which == "chosen" else rejected
+    tokens = [*prompt, *answer]
+    return tokens[:-1], [-1] * (len(prompt) - 1) + list(answer)
+
+
+def log_probability(kern: Kernels, d: Decoder, weights, pair, which: str) -> float:
+    """FineTuner.log_probability (trainer.py:443-453): minus the answer's summed cross-entropy."""
+    tokens, targets = pair_sequence(pair, which)
+    loss, _, _ = window_gradients(kern, d, weights, tokens, targets)
+    return -loss
+
+
+def adamw_update(kern: Kernels, params, grads, m, v, opt: AdamWConfig, step: int, total_steps: int) -> float:
+    """AdamW.step over `params` in tensor order (optimizer.py:66-109); returns the gradient norm."""
+    total = 0.0
+    for name in tensor_order(grads):
+        total += kern.sum_squares(grads[name])
+    norm = math.sqrt(total)
+    clip = 1.0
+    if opt.max_grad_norm > 0 and norm > opt.max_grad_norm:
+        clip = opt.max_grad_norm / (norm + 1e-6)
+    c1, c2 = 1.0 - _power(opt.beta1, step), 1.0 - _power(opt.beta2, step)
+    lr = opt.learning_rate_at(step, total_steps)
+    for name in tensor_order(params):
+        decay = opt.weight_decay if params[name].ndim >= 2 else 0.0
+        kern.adamw_step(params[name], np.ascontiguousarray(grads[name], np.float32), m[name], v[name], lr,
+                        opt.beta1, opt.beta2, opt.eps, decay, c1, c2, clip)
+    return norm
+
+
+def dpo_train_step(kern: Kernels, d: Decoder, params, m, v, pairs, reference, beta: float, opt: AdamWConfig,
+                   step: int, total_steps: int):
+    """FineTuner.train_step with the DPO objective (trainer.py:290-310, 364-384): per pair the chosen and rejected
+    answers' gradients times +-f32(beta (1 - sigmoid(z)) / pairs), summed in float32 (the first product taken as is);
+    then AdamW. Updates params, m, v in place; returns (loss, gradient norm, summed gradients)."""
+    o = oracle()
+    loss_total, grads = 0.0, {}
+    for pair, (reference_chosen, reference_rejected) in zip(pairs, reference):
+        chosen_loss, _, chosen_grads = window_gradients(kern, d, params, *pair_sequence(pair, "chosen"))
+        rejected_loss, _, rejected_grads = window_gradients(kern, d, params, *pair_sequence(pair, "rejected"))
+        z = beta * ((-chosen_loss - reference_chosen) - (-rejected_loss - reference_rejected))
+        loss_total += -log_sigmoid(z)
+        weight = np.float32(beta * (1.0 - o.orc_sigmoid(z)) / len(pairs))
+        for sign, pair_grads in ((weight, chosen_grads), (-weight, rejected_grads)):
+            for name, gradient in pair_grads.items():
+                grads[name] = grads[name] + gradient * sign if name in grads else gradient * sign
+    norm = adamw_update(kern, params, grads, m, v, opt, step, total_steps)
+    return loss_total / len(pairs), norm, grads
+
+
 # ---- Q8_0 (cpp/include/dllm/quant.hpp:27-60, numerics.py:106-139) ----
 
 def quantize_q8_0(fn, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:

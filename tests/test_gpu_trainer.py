@@ -343,3 +343,59 @@ def test_attention_at_head_dim_128_matches_the_oracle(window):
     assert loss == want_loss
     for name in t.names:
         assert t.get(name, d.tensor_shapes()[name], t.GRAD).tobytes() == want[name].tobytes(), name
+
+
+DPO_RECORDS = [("the quick brown", " fox", " cat"), ("pack my box", " with jugs", " of"),
+               ("two plus two is", " four", " five and a lot more words"), ("hello", " there", " go away"),
+               ("the lazy", " dog", " frog")]
+
+
+@pytest.mark.parametrize("family", [f for f in FAMILIES if f in GOLDEN["DPO_FINETUNE_FINGERPRINT"]])
+def test_dpo_finetune_fingerprint_on_gpu(family):
+    """The reference's DPO run (tests/test_preference.py:30-47, 223-244) on the GPU: the reference log-probabilities
+    from the initial weights, five steps of two pairs, the loss log 2 at the first step, the export fingerprint."""
+    d = O.FIXTURES[family]
+    pairs = O.preference_pairs(DPO_RECORDS, lambda text: [ord(c) % 64 for c in text], 24, 2)
+    t = make_trainer(d, O.fixture_weights(d), max_tokens=256, max_windows=10, max_window=32)
+    reference = t.log_probabilities(pairs)
+    kern = O.oracle_kernels()
+    want = [(O.log_probability(kern, d, O.fixture_weights(d), p, "chosen"),
+             O.log_probability(kern, d, O.fixture_weights(d), p, "rejected")) for p in pairs]
+    assert reference == want
+    opt = O.AdamWConfig(learning_rate=1e-2)
+    losses = []
+    for step in range(5):
+        batch = O.batch_indices(len(pairs), step, 2, 3)
+        losses.append(t.dpo_step([pairs[i] for i in batch], [reference[i] for i in batch], 0.5,
+                                 opt.learning_rate_at(step + 1, 5), step + 1)[0])
+    assert losses[0] == O.oracle().orc_log(2.0)
+    assert t.fingerprint() == GOLDEN["DPO_FINETUNE_FINGERPRINT"][family]
+
+
+def test_dpo_step_matches_the_oracle_on_ragged_pairs():
+    """A DPO step on a larger random model with prompts and answers of uneven lengths: loss, norm, gradients,
+    parameters and moments bit-equal to the oracle's (trainer.py:364-384)."""
+    d = O.Decoder("qwen2", vocab=300, hidden=64, inter=160, layers=2, heads=4, kv_heads=2, head_dim=16, eps=1e-6,
+                  rope_theta=1e6, tied=True, attn_bias=True)
+    weights = O.synthetic_weights(d, seed=7, scale=0.05)
+    rng = O.Random(11)
+    shapes = [(5, 9, 3), (1, 40, 17), (23, 2, 30)]
+    pairs = [(tuple(rng.next_u64() % d.vocab for _ in range(p)), tuple(rng.next_u64() % d.vocab for _ in range(c)),
+              tuple(rng.next_u64() % d.vocab for _ in range(r))) for p, c, r in shapes]
+    reference = [(-3.25, -4.5), (-61.0, -20.0), (-7.0, -80.0)]
+    t = make_trainer(d, weights, max_tokens=256, max_windows=6, max_window=64)
+    params = {n: a.copy() for n, a in weights.items()}
+    m = {n: np.zeros_like(a) for n, a in params.items()}
+    v = {n: np.zeros_like(a) for n, a in params.items()}
+    opt = O.AdamWConfig(learning_rate=1e-3, schedule="constant")
+    for step in (1, 2):
+        loss_gpu, norm_gpu = t.dpo_step(pairs, reference, 0.3, 1e-3, step)
+        loss_cpu, norm_cpu, grads = O.dpo_train_step(O.oracle_kernels(), d, params, m, v, pairs, reference, 0.3, opt,
+                                                     step, 2)
+        assert loss_gpu == loss_cpu and norm_gpu == norm_cpu
+        for name in t.names:
+            shape = d.tensor_shapes()[name]
+            assert t.get(name, shape, t.GRAD).tobytes() == grads[name].tobytes(), name
+            assert t.get(name, shape).tobytes() == params[name].tobytes(), name
+            assert t.get(name, shape, t.M).tobytes() == m[name].tobytes(), name
+            assert t.get(name, shape, t.V).tobytes() == v[name].tobytes(), name

@@ -142,3 +142,36 @@ def test_experts_no_token_reaches_get_zero_gradients():
         for e in range(d.experts):
             for which in ("gate", "up", "down"):
                 assert bool(np.any(grads[f"layers.{layer}.mlp.experts.{e}.{which}.weight"])) == (e in reached)
+
+
+# The reference's DPO run (tests/test_preference.py:30-47, 223-244): five pairs, sequence length 24, end token 2,
+# RunConfig(5, 2, 24, 3, AdamWConfig(learning_rate=1e-2), objective="dpo", beta=0.5).
+DPO_RECORDS = [("the quick brown", " fox", " cat"), ("pack my box", " with jugs", " of"),
+               ("two plus two is", " four", " five and a lot more words"), ("hello", " there", " go away"),
+               ("the lazy", " dog", " frog")]
+DPO_FAMILIES = sorted(set(O.FIXTURES) & set(GOLDEN["DPO_FINETUNE_FINGERPRINT"]))
+
+
+def dpo_pairs():
+    return O.preference_pairs(DPO_RECORDS, lambda text: [ord(c) % 64 for c in text], 24, 2)
+
+
+@pytest.mark.parametrize("family", DPO_FAMILIES)
+def test_oracle_reproduces_the_dpo_finetune_fingerprint(family):
+    d = O.FIXTURES[family]
+    kern = O.oracle_kernels()
+    params = O.fixture_weights(d)
+    pairs = dpo_pairs()
+    reference = [(O.log_probability(kern, d, params, p, "chosen"), O.log_probability(kern, d, params, p, "rejected"))
+                 for p in pairs]
+    m = {n: np.zeros_like(a) for n, a in params.items()}
+    v = {n: np.zeros_like(a) for n, a in params.items()}
+    opt = O.AdamWConfig(learning_rate=1e-2)
+    losses = []
+    for step in range(5):
+        batch = O.batch_indices(len(pairs), step, 2, 3)
+        loss, _, _ = O.dpo_train_step(kern, d, params, m, v, [pairs[i] for i in batch],
+                                      [reference[i] for i in batch], 0.5, opt, step + 1, 5)
+        losses.append(loss)
+    assert losses[0] == O.oracle().orc_log(2.0)  # the model is its own reference at step 1 (z = 0)
+    assert O.data_fingerprint(params) == GOLDEN["DPO_FINETUNE_FINGERPRINT"][family]
