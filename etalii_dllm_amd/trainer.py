@@ -122,6 +122,7 @@ class Trainer:
                  lora: LoraConfig | None = None) -> None:
         """lora: train LoRA adapters (tensors "<weight>.lora_a" / ".lora_b") on the frozen base instead."""
         self.decoder = decoder
+        self.max_windows = max_windows
         self._cfg = decoder.native()
         self._lora = lora
         handle = C.c_void_p()
@@ -268,6 +269,9 @@ class Trainer:
     def log_probabilities(self, pairs) -> list[tuple[float, float]]:
         """(chosen, rejected) log-probabilities of each pair under the current weights (FineTuner.log_probability,
         trainer.py:443-453): the reference values of a DPO run when taken before its first step."""
+        chunk = max(self.max_windows // 2, 1)  # pairs per call within the trainer's window capacity
+        if len(pairs) > chunk:
+            return [lp for i in range(0, len(pairs), chunk) for lp in self.log_probabilities(pairs[i:i + chunk])]
         windows, prompts = self._pair_windows(pairs)
         flat, offsets, lengths = _windows(windows)
         per_window = np.ascontiguousarray(np.repeat(prompts, 2), dtype=np.int64)

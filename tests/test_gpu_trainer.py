@@ -356,7 +356,7 @@ def test_dpo_finetune_fingerprint_on_gpu(family):
     from the initial weights, five steps of two pairs, the loss log 2 at the first step, the export fingerprint."""
     d = O.FIXTURES[family]
     pairs = O.preference_pairs(DPO_RECORDS, lambda text: [ord(c) % 64 for c in text], 24, 2)
-    t = make_trainer(d, O.fixture_weights(d), max_tokens=256, max_windows=10, max_window=32)
+    t = make_trainer(d, O.fixture_weights(d), max_tokens=128, max_windows=4, max_window=32)
     reference = t.log_probabilities(pairs)
     kern = O.oracle_kernels()
     want = [(O.log_probability(kern, d, O.fixture_weights(d), p, "chosen"),
