@@ -220,6 +220,10 @@ int launch_adamw(float* param, const float* grad, float* m, float* v, const int6
 // ---- LoRA and the Q8_0 base (lora.hip) ----
 
 int launch_quantize_q8_0(const float* x, int8_t* q, float* scales, int64_t n, hipStream_t stream);
+// out[r][n] = linear_q8 of the quantised activations (xq int8 [rows][K], xs [rows][K / 32]) and weights (wq [N][K],
+// ws [N][K / 32]) (quant.hpp:143-169): exact int32 block dots on the int8 matrix cores, combined in double.
+int launch_linear_q8(const int8_t* xq, const float* xs, const int8_t* wq, const float* ws, const float* bias,
+                     float* out, int64_t rows, int64_t K, int64_t N, hipStream_t stream);
 int launch_dequantize_q8_0(const int8_t* q, const float* scales, float* out, int64_t n, hipStream_t stream);
 // out = base + x * s in float32 (base may be null: out = x * s)
 int launch_scale_add(const float* base, const float* x, float s, float* out, int64_t n, hipStream_t stream);

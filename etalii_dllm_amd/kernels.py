@@ -479,6 +479,72 @@ def quantize_q8_0(weight) -> tuple[np.ndarray, np.ndarray]:
     return q.download(w.shape, np.int8), s.download((w.shape[0], w.shape[1] // 32))
 
 
+lib.dllm_hip_linear_q8_workspace.restype = _sz
+lib.dllm_hip_linear_q8_workspace.argtypes = [_sz, _sz]
+lib.dllm_hip_linear_q8.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
+lib.dllm_hip_linear_q4_workspace.restype = _sz
+lib.dllm_hip_linear_q4_workspace.argtypes = [_sz, _sz, _sz]
+lib.dllm_hip_linear_q4.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
+lib.dllm_hip_quantize_q4_0.argtypes = [_vp, _vp, _vp, _sz, _vp]
+lib.dllm_hip_unpack_q4_0.argtypes = [_vp, _vp, _sz, _vp]
+
+
+def _quantized_linear(name, x, q, scales, bias, in_per_row):
+    x, s = _f32(x), _f32(scales)
+    if x.ndim < 1:
+        raise ValueError("x must have at least one dimension")
+    in_f = x.shape[-1]
+    out_f = q.shape[0]
+    if q.ndim != 2 or q.shape[1] * in_per_row != in_f:
+        raise ValueError("weight in_features does not match the last dimension of x")
+    if in_f % 32:
+        raise ValueError(f"{name} needs in_features to be a multiple of 32")
+    if s.shape != (out_f, in_f // 32):
+        raise ValueError("scales must be [out_features, in_features / 32]")
+    if bias is not None and _f32(bias).shape[0] != out_f:
+        raise ValueError("bias length must equal out_features")
+    rows = _rows(x)
+    size = (lib.dllm_hip_linear_q8_workspace(rows, in_f) if name == "Q8_0"
+            else lib.dllm_hip_linear_q4_workspace(rows, in_f, out_f))
+    ws, dx, dq, ds = Device(size), Device.of(x), Device.of(q), Device.of(s)
+    db = Device.of(_f32(bias)) if bias is not None else None
+    out = Device(rows * out_f * 4)
+    fn = lib.dllm_hip_linear_q8 if name == "Q8_0" else lib.dllm_hip_linear_q4
+    check(fn(dx.ptr, dq.ptr, ds.ptr, db.ptr if db else None, out.ptr, rows, in_f, out_f, ws.ptr, ws.nbytes, None))
+    return out.download((*x.shape[:-1], out_f))
+
+
+def linear_q8(x, q, scales, bias=None) -> np.ndarray:
+    """kernels.cpp:310-329: Q8_0 linear, activations quantised per 32-block, exact int32 block sums (int8 matrix
+    cores), combined in double in block order."""
+    return _quantized_linear("Q8_0", x, np.ascontiguousarray(q, dtype=np.int8), scales, bias, 1)
+
+
+def quantize_q4_0(weight) -> tuple[np.ndarray, np.ndarray]:
+    """kernels.cpp:331-348: (packed 4-bit values as bytes [out, in / 2], float32 scales [out, in / 32])."""
+    w = _f32(weight)
+    if w.ndim != 2 or w.shape[1] % 32:
+        raise ValueError("Q4_0 needs in_features to be a multiple of 32")
+    d, q, s = Device.of(w), Device(w.size // 2), Device(w.size // 32 * 4)
+    check(lib.dllm_hip_quantize_q4_0(d.ptr, q.ptr, s.ptr, w.size, None))
+    return q.download((w.shape[0], w.shape[1] // 2), np.int8), s.download((w.shape[0], w.shape[1] // 32))
+
+
+def unpack_q4_0(q) -> np.ndarray:
+    """kernels.cpp:350-363: the int8 values [out, in] of packed Q4_0 values [out, in / 2]."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    if q.ndim != 2 or (q.shape[1] * 2) % 32:
+        raise ValueError("Q4_0 needs in_features to be a multiple of 32")
+    dq, out = Device.of(q), Device(q.size * 2)
+    check(lib.dllm_hip_unpack_q4_0(dq.ptr, out.ptr, q.size * 2, None))
+    return out.download((q.shape[0], q.shape[1] * 2), np.int8)
+
+
+def linear_q4(x, q, scales, bias=None) -> np.ndarray:
+    """kernels.cpp:365-385: the weights unpacked to int8, then exactly linear_q8."""
+    return _quantized_linear("Q4_0", x, np.ascontiguousarray(q, dtype=np.int8), scales, bias, 2)
+
+
 def dequantize_q8_0(values, scales) -> np.ndarray:
     """QuantizedWeight.dequantize (numerics.py:138-139): the int8 values times their block's scale, float32."""
     q = np.ascontiguousarray(values, dtype=np.int8)

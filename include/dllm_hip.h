@@ -163,6 +163,21 @@ int dllm_hip_dot(const float* a, const float* b, size_t n, float* result, void* 
 int dllm_hip_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n, void* stream);
 /* out = f32(q) * scale of the value's block. Replaces QuantizedWeight.dequantize (numerics.py:138-139). */
 int dllm_hip_dequantize_q8_0(const int8_t* q, const float* scales, float* out, size_t n, void* stream);
+
+/* ---- quantised linear layers for inference (cpp/include/dllm/quant.hpp:143-169, 355-403; kernels.cpp:310-385) ----
+ * linear_q8: x [rows, in] quantised to Q8_0 per row block of 32, q [out, in] int8 (8-byte aligned) and scales
+ * [out, in / 32]; out[r][n] = f32(sum over blocks ascending of (f64(xs) f64(ws)) f64(isum) + bias[n]), isum the
+ * exact int32 dot of a block (replaces kernels.cpp:310-329 `linear_q8`). in must be a multiple of 32. */
+size_t dllm_hip_linear_q8_workspace(size_t rows, size_t in);
+int dllm_hip_linear_q8(const float* x, const int8_t* q, const float* scales, const float* bias, float* out,
+                       size_t rows, size_t in, size_t out_f, void* workspace, size_t workspace_bytes, void* stream);
+/* Q4_0 (kernels.cpp:331-385): quantize_q4_0 of n floats into n / 2 packed bytes and n / 32 scales; unpack_q4_0 to
+ * int8; linear_q4 = linear_q8 of the unpacked weights. */
+int dllm_hip_quantize_q4_0(const float* x, uint8_t* packed, float* scales, size_t n, void* stream);
+int dllm_hip_unpack_q4_0(const uint8_t* packed, int8_t* values, size_t n, void* stream);
+size_t dllm_hip_linear_q4_workspace(size_t rows, size_t in, size_t out);
+int dllm_hip_linear_q4(const float* x, const uint8_t* q, const float* scales, const float* bias, float* out,
+                       size_t rows, size_t in, size_t out_f, void* workspace, size_t workspace_bytes, void* stream);
 /* out = weight + f32(linear(b, a^T)) * f32(scale) for weight [out_f, in_f], a [rank, in_f], b [out_f, rank].
  * Replaces lora.merge (src/etalii_dllm/lora.py:271-276). */
 size_t dllm_hip_lora_merge_workspace(size_t out_features, size_t in_features, size_t rank);

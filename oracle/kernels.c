@@ -705,6 +705,72 @@ void orc_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n) {
     }
 }
 
+/* linear_q8 (quant.hpp:143-169, 355-383): each row's activations quantised to Q8_0 (quant.hpp:27-60), then per output
+ * acc = sum over blocks b ascending of (f64(xs[r][b]) f64(ws[n][b])) f64(isum_b), isum_b the exact int32 dot of the
+ * block's 32 int8 pairs; acc += bias[n]; rounded to float once. in_features is a multiple of 32. */
+void orc_linear_q8(const float* x, const int8_t* wq, const float* ws, const float* bias, float* out, size_t rows,
+                   size_t in, size_t n_out) {
+    const size_t blocks = in / 32;
+    int8_t* xq = (int8_t*)malloc(in > 0 ? in : 1);
+    float* xs = (float*)malloc((blocks > 0 ? blocks : 1) * sizeof(float));
+    for (size_t r = 0; r < rows; ++r) {
+        orc_quantize_q8_0(x + r * in, xq, xs, in);
+        for (size_t n = 0; n < n_out; ++n) {
+            double acc = 0.0;
+            for (size_t b = 0; b < blocks; ++b) {
+                int32_t isum = 0;
+                for (size_t i = 0; i < 32; ++i) isum += (int32_t)xq[b * 32 + i] * (int32_t)wq[n * in + b * 32 + i];
+                acc += ((double)xs[b] * (double)ws[n * blocks + b]) * (double)isum;
+            }
+            if (bias) acc += bias[n];
+            out[r * n_out + n] = (float)acc;
+        }
+    }
+    free(xq);
+    free(xs);
+}
+
+/* quantize_q4_0 (quant.hpp:67-94): amax over finite values, d = amax / 7, q = round-half-even(x / d) clamped to +-7;
+ * byte j of a block holds q_j + 8 (low four bits) and q_(j+16) + 8 (high four bits). */
+void orc_quantize_q4_0(const float* x, uint8_t* packed, float* scales, size_t n) {
+    for (size_t b = 0; b * 32 < n; ++b) {
+        const float* xb = x + b * 32;
+        float amax = 0.0f;
+        for (size_t i = 0; i < 32; ++i) {
+            const float a = fabsf(xb[i]);
+            if (a > amax && isfinite(a)) amax = a;
+        }
+        const float d = amax / 7.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        scales[b] = d;
+        int q[32];
+        for (size_t i = 0; i < 32; ++i) {
+            float val = isfinite(xb[i]) ? round_half_even(xb[i] * id) : 0.0f;
+            val = val > 7.0f ? 7.0f : (val < -7.0f ? -7.0f : val);
+            q[i] = (int)val;
+        }
+        for (size_t j = 0; j < 16; ++j) packed[b * 16 + j] = (uint8_t)((q[j] + 8) | ((q[j + 16] + 8) << 4));
+    }
+}
+
+/* unpack_q4_0 (quant.hpp:97-108). */
+void orc_unpack_q4_0(const uint8_t* packed, int8_t* values, size_t n) {
+    for (size_t b = 0; b * 32 < n; ++b)
+        for (size_t j = 0; j < 16; ++j) {
+            values[b * 32 + j] = (int8_t)((packed[b * 16 + j] & 0x0F) - 8);
+            values[b * 32 + j + 16] = (int8_t)((packed[b * 16 + j] >> 4) - 8);
+        }
+}
+
+/* linear_q4 (quant.hpp:385-403): the weights unpacked to int8, then exactly linear_q8. */
+void orc_linear_q4(const float* x, const uint8_t* wq, const float* ws, const float* bias, float* out, size_t rows,
+                   size_t in, size_t n_out) {
+    int8_t* w = (int8_t*)malloc(n_out * in > 0 ? n_out * in : 1);
+    orc_unpack_q4_0(wq, w, n_out * in);
+    orc_linear_q8(x, w, ws, bias, out, rows, in, n_out);
+    free(w);
+}
+
 /* rope_inv_freq with default scaling (numerics.py:267-297): theta^(-2i/dim) = exp(-(2i/dim) log theta). */
 void orc_rope_inv_freq(size_t rotary_dim, double theta, double* out) {
     const double log_theta = orc_log(theta);

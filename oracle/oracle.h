@@ -79,6 +79,12 @@ void orc_moe_route_backward(const float* logits, const int64_t* indices, const f
                             int normalize);                              /* grad.hpp:507-541 */
 void orc_column_mean(const float* x, float* out, size_t rows, size_t cols); /* interp.hpp:146-155 */
 void orc_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n); /* quant.hpp:27-60 */
+void orc_linear_q8(const float* x, const int8_t* wq, const float* ws, const float* bias, float* out, size_t rows,
+                   size_t in, size_t n_out);                                            /* quant.hpp:143-169,355-383 */
+void orc_quantize_q4_0(const float* x, uint8_t* packed, float* scales, size_t n);       /* quant.hpp:67-94 */
+void orc_unpack_q4_0(const uint8_t* packed, int8_t* values, size_t n);                  /* quant.hpp:97-108 */
+void orc_linear_q4(const float* x, const uint8_t* wq, const float* ws, const float* bias, float* out, size_t rows,
+                   size_t in, size_t n_out);                                            /* quant.hpp:385-403 */
 
 /* ---- rotary frequencies: src/etalii_dllm/numerics.py:267-297 (default scaling) ---- */
 void orc_rope_inv_freq(size_t rotary_dim, double theta, double* out);

@@ -165,5 +165,20 @@ void ref_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n) {
     FpEnvGuard guard;
     dllm::quantize_q8_0(x, q, scales, n);
 }
+void ref_linear_q8(const float* x, const int8_t* wq, const float* ws, const float* bias, float* out, size_t rows,
+                   size_t in, size_t n_out) {
+    FpEnvGuard guard;
+    dllm::linear_q8(x, wq, ws, bias, out, rows, in, n_out);
+}
+void ref_quantize_q4_0(const float* x, uint8_t* packed, float* scales, size_t n) {
+    FpEnvGuard guard;
+    dllm::quantize_q4_0(x, packed, scales, n);
+}
+void ref_unpack_q4_0(const uint8_t* packed, int8_t* values, size_t n) { dllm::unpack_q4_0(packed, values, n); }
+void ref_linear_q4(const float* x, const uint8_t* wq, const float* ws, const float* bias, float* out, size_t rows,
+                   size_t in, size_t n_out) {
+    FpEnvGuard guard;
+    dllm::linear_q4(x, wq, ws, bias, out, rows, in, n_out);
+}
 
 }  // extern "C"

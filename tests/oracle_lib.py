@@ -808,6 +808,45 @@ def quantize_q8_0(fn, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return q, s
 
 
+def linear_q8(fn, x: np.ndarray, q: np.ndarray, scales: np.ndarray, bias=None) -> np.ndarray:
+    """A linear_q8(x, wq, ws, bias, out, rows, in, out) C function on x [rows, in], q [out, in], scales [out, in/32]."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.ascontiguousarray(q, np.int8)
+    s = np.ascontiguousarray(scales, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    out = np.empty((x.shape[0], q.shape[0]), np.float32)
+    fn(ptr(x), q.ctypes.data_as(C.c_void_p), ptr(s), ptr(b) if b is not None else None, ptr(out),
+       C.c_size_t(x.shape[0]), C.c_size_t(x.shape[1]), C.c_size_t(q.shape[0]))
+    return out
+
+
+def quantize_q4_0(fn, x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """(packed bytes [n / 2], scales [n / 32]) from a quantize_q4_0(x, packed, scales, n) C function."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    q = np.empty(x.size // 2, np.uint8)
+    s = np.empty(x.size // 32, np.float32)
+    fn(ptr(x), q.ctypes.data_as(C.c_void_p), ptr(s), C.c_size_t(x.size))
+    return q, s
+
+
+def unpack_q4_0(fn, packed: np.ndarray) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, np.uint8).ravel()
+    out = np.empty(packed.size * 2, np.int8)
+    fn(packed.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p), C.c_size_t(out.size))
+    return out
+
+
+def linear_q4(fn, x: np.ndarray, packed: np.ndarray, scales: np.ndarray, bias=None) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.ascontiguousarray(packed, np.uint8)
+    s = np.ascontiguousarray(scales, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    out = np.empty((x.shape[0], q.shape[0]), np.float32)
+    fn(ptr(x), q.ctypes.data_as(C.c_void_p), ptr(s), ptr(b) if b is not None else None, ptr(out),
+       C.c_size_t(x.shape[0]), C.c_size_t(x.shape[1]), C.c_size_t(q.shape[0]))
+    return out
+
+
 def dequantize_q8_0(q: np.ndarray, scales: np.ndarray) -> np.ndarray:
     """QuantizedWeight.dequantize (numerics.py:138-139): int8 -> float32 times the block's scale, in float32."""
     return q.astype(np.float32) * np.repeat(scales, 32)

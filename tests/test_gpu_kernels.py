@@ -290,3 +290,39 @@ def test_linear_matrix_core_tails_and_non_finite(K, ora, rows):
         nan = np.isnan(want)  # a NaN the hardware generates has no defined sign or payload
         assert np.array_equal(np.isnan(got), nan), f"{name} rows={rows}: NaN positions"
         assert_same(np.where(nan, 0, got), np.where(nan, 0, want), f"{name} rows={rows} non-finite")
+
+
+def q8_case(seed: int, rows: int, in_f: int, out_f: int):
+    x = O.gaussian(seed, rows, in_f)
+    x[0, :32] = 0.0
+    if rows > 2:
+        x[2, 5] = np.inf
+        x[2, 40 % in_f] = -7e30
+    w = O.gaussian(seed + 1, out_f, in_f, scale=0.02)
+    q, s = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, w)
+    return x, q.reshape(out_f, in_f), s.reshape(out_f, in_f // 32), O.gaussian(seed + 2, out_f)
+
+
+@pytest.mark.parametrize(("rows", "in_f", "out_f"), [(1, 32, 1), (7, 64, 19), (65, 256, 48), (130, 1024, 200)])
+def test_linear_q8_and_q4(K, rows, in_f, out_f):
+    """Q8_0 / Q4_0 linear (quant.hpp:143-169, 355-403) on the int8 matrix cores against the oracle, bit for bit."""
+    x, q, s, b = q8_case(5, rows, in_f, out_f)
+    for bias in (None, b):
+        assert_same(K.linear_q8(x, q, s, bias), O.linear_q8(O.oracle().orc_linear_q8, x, q, s, bias), "linear_q8")
+    w = O.gaussian(9, out_f, in_f, scale=0.05)
+    w[0, 3] = np.nan
+    packed, scales = K.quantize_q4_0(w)
+    want_p, want_s = O.quantize_q4_0(O.oracle().orc_quantize_q4_0, w)
+    assert packed.view(np.uint8).tobytes() == want_p.tobytes() and scales.tobytes() == want_s.tobytes()
+    assert_same(K.unpack_q4_0(packed), O.unpack_q4_0(O.oracle().orc_unpack_q4_0, want_p).reshape(out_f, in_f),
+                "unpack_q4_0")
+    assert_same(K.linear_q4(x, packed, scales, b),
+                O.linear_q4(O.oracle().orc_linear_q4, x, want_p.reshape(out_f, in_f // 2), want_s.reshape(out_f, -1), b),
+                "linear_q4")
+
+
+def test_linear_q8_rows_are_batch_invariant(K):
+    x, q, s, _ = q8_case(7, 300, 128, 96)
+    full = K.linear_q8(x, q, s)
+    for m in (1, 7, 64):
+        assert_same(K.linear_q8(x[:m], q, s), full[:m], f"linear_q8 M={m}")

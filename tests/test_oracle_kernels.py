@@ -314,3 +314,65 @@ def test_gelu_tanh_and_softcap_backward_match_numeric_gradients():
     soft = lambda v: cap * np.tanh(v / cap)  # noqa: E731
     xf = x.astype(np.float32).astype(np.float64)
     close(O.softcap_backward(x.astype(np.float32), np.ones(64, np.float32), cap), (soft(xf + h) - soft(xf - h)) / (2 * h), 1e-6)
+
+
+def q8_linear_case(seed: int, rows: int, in_f: int, out_f: int):
+    x = O.gaussian(seed, rows, in_f)
+    x[0, :32] = 0.0  # an all-zero block: scale 0
+    if rows > 2:
+        x[2, 5] = np.inf  # a non-finite value is quantised as 0 and left out of the block's amax
+        x[2, 40 % in_f] = -7e30
+    w = O.gaussian(seed + 1, out_f, in_f, scale=0.02)
+    q, s = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, w)
+    return x, q.reshape(out_f, in_f), s.reshape(out_f, in_f // 32), O.gaussian(seed + 2, out_f)
+
+
+@needs_ref
+@pytest.mark.parametrize(("rows", "in_f", "out_f"), [(1, 32, 1), (7, 64, 19), (65, 256, 48)])
+def test_linear_q8_and_q4_match_reference(rows, in_f, out_f):
+    """quant.hpp:143-169, 355-403 compiled from the reference against the oracle, bit for bit."""
+    x, q, s, b = q8_linear_case(3, rows, in_f, out_f)
+    for bias in (None, b):
+        want = O.linear_q8(O.ref().ref_linear_q8, x, q, s, bias)
+        assert O.linear_q8(O.oracle().orc_linear_q8, x, q, s, bias).tobytes() == want.tobytes()
+    w = O.gaussian(9, out_f, in_f, scale=0.05)
+    pa, sa = O.quantize_q4_0(O.oracle().orc_quantize_q4_0, w)
+    pb, sb = O.quantize_q4_0(O.ref().ref_quantize_q4_0, w)
+    assert pa.tobytes() == pb.tobytes() and sa.tobytes() == sb.tobytes()
+    assert O.unpack_q4_0(O.oracle().orc_unpack_q4_0, pa).tobytes() == O.unpack_q4_0(O.ref().ref_unpack_q4_0, pa).tobytes()
+    packed, scales = pa.reshape(out_f, in_f // 2), sa.reshape(out_f, in_f // 32)
+    assert (O.linear_q4(O.oracle().orc_linear_q4, x, packed, scales, b).tobytes()
+            == O.linear_q4(O.ref().ref_linear_q4, x, packed, scales, b).tobytes())
+
+
+def test_linear_q8_closed_form_on_the_integer_grid():
+    """With x and w already on their Q8_0 grids (values k d, one |k| = 127 per block) every block sum is an exact
+    integer and the output is the float64 sum of scaled integer dots (quant.hpp:143-169 by hand)."""
+    rng = np.random.default_rng(2)
+    kx = rng.integers(-127, 128, size=(3, 64)).astype(np.float32)
+    kw = rng.integers(-127, 128, size=(5, 64)).astype(np.float32)
+    kx[:, ::32] = 127.0
+    kw[:, ::32] = -127.0
+    dx, dw = np.float32(0.5), np.float32(0.125)
+    x = kx * dx
+    q, s = O.quantize_q8_0(O.oracle().orc_quantize_q8_0, kw * dw)
+    assert np.all(s == dw)
+    out = O.linear_q8(O.oracle().orc_linear_q8, x, q.reshape(5, 64), s.reshape(5, 2))
+    for r in range(3):
+        for n in range(5):
+            acc = 0.0
+            for b in range(2):
+                isum = int(np.dot(kx[r, 32 * b:32 * b + 32].astype(np.int64), kw[n, 32 * b:32 * b + 32].astype(np.int64)))
+                acc += (float(dx) * float(dw)) * float(isum)
+            assert out[r, n] == np.float32(acc)
+
+
+def test_q4_0_packs_two_values_per_byte():
+    """Values on the Q4_0 grid (k d, |k| <= 7, one |k| = 7 per block) pack as k + 8 in nibbles and unpack to k."""
+    rng = np.random.default_rng(4)
+    k = rng.integers(-7, 8, size=(4, 32)).astype(np.float32)
+    k[:, 3] = 7.0
+    packed, scales = O.quantize_q4_0(O.oracle().orc_quantize_q4_0, (k * np.float32(0.5)).ravel())
+    assert np.all(scales == np.float32(0.5))
+    assert np.array_equal(O.unpack_q4_0(O.oracle().orc_unpack_q4_0, packed).astype(np.float32), k.ravel())
+    assert packed[0] == (int(k[0, 0]) + 8) | ((int(k[0, 16]) + 8) << 4)
