@@ -545,6 +545,110 @@ def linear_q4(x, q, scales, bias=None) -> np.ndarray:
     return _quantized_linear("Q4_0", x, np.ascontiguousarray(q, dtype=np.int8), scales, bias, 2)
 
 
+lib.dllm_hip_gelu.argtypes = [_vp, _vp, _sz, _vp]
+lib.dllm_hip_gelu_backward.argtypes = [_vp, _vp, _vp, _sz, _vp]
+lib.dllm_hip_layer_norm.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, C.c_double, _vp]
+lib.dllm_hip_layer_norm_backward_workspace.restype = _sz
+lib.dllm_hip_layer_norm_backward_workspace.argtypes = [_sz]
+lib.dllm_hip_layer_norm_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, C.c_double, _vp, _sz, _vp]
+for _name in ("biased_attention", "biased_attention_backward"):
+    getattr(lib, f"dllm_hip_{_name}_workspace").restype = _sz
+    getattr(lib, f"dllm_hip_{_name}_workspace").argtypes = [_sz, _sz, _sz]
+lib.dllm_hip_biased_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, C.c_double, _vp, _sz, _vp]
+lib.dllm_hip_biased_attention_backward.argtypes = [_vp] * 9 + [_sz] * 5 + [C.c_double, _vp, _sz, _vp]
+
+
+def gelu(x) -> np.ndarray:
+    """kernels.cpp:631: elementwise exact (erf) GELU."""
+    x = _f32(x)
+    dx, out = Device.of(x), Device(x.nbytes)
+    check(lib.dllm_hip_gelu(dx.ptr, out.ptr, x.size, None))
+    return out.download(x.shape)
+
+
+def gelu_backward(x, dy) -> np.ndarray:
+    """kernels.cpp:877-889: dy * gelu'(x) for the exact (erf) GELU."""
+    x, dy = _f32(x), _f32(dy)
+    if x.size != dy.size:
+        raise ValueError("x and dy must have the same size")
+    dx, dd, out = Device.of(x), Device.of(dy), Device(x.nbytes)
+    check(lib.dllm_hip_gelu_backward(dx.ptr, dd.ptr, out.ptr, x.size, None))
+    return out.download(x.shape)
+
+
+def layer_norm(x, weight, bias, eps=1e-12) -> np.ndarray:
+    """kernels.cpp:612-625: LayerNorm over the last dimension, fixed order, double accumulators."""
+    x, w, b = _f32(x), _f32(weight), _f32(bias)
+    if x.ndim < 1:
+        raise ValueError("x must have at least one dimension")
+    dim = x.shape[-1]
+    if w.shape[0] != dim or b.shape[0] != dim:
+        raise ValueError("weight and bias lengths must equal the last dimension of x")
+    dx, dw, db, out = Device.of(x), Device.of(w), Device.of(b), Device(x.nbytes)
+    check(lib.dllm_hip_layer_norm(dx.ptr, dw.ptr, db.ptr, out.ptr, _rows(x), dim, eps, None))
+    return out.download(x.shape)
+
+
+def layer_norm_backward(x, weight, dy, eps=1e-12):
+    """kernels.cpp:858-875: (dx, dweight, dbias) of layer_norm()."""
+    x, w, dy = _f32(x), _f32(weight), _f32(dy)
+    if x.ndim < 1:
+        raise ValueError("x must have at least one dimension")
+    dim = x.shape[-1]
+    if dy.size != x.size or dy.shape[-1] != dim:
+        raise ValueError("dy must have the shape of x")
+    if w.shape[0] != dim:
+        raise ValueError("weight length must equal the last dimension of x")
+    rows = _rows(x)
+    ws = Device(lib.dllm_hip_layer_norm_backward_workspace(rows))
+    d_x, d_w, d_dy = Device.of(x), Device.of(w), Device.of(dy)
+    ddx, ddw, ddb = Device(x.nbytes), Device(dim * 4), Device(dim * 4)
+    check(lib.dllm_hip_layer_norm_backward(d_x.ptr, d_w.ptr, d_dy.ptr, ddx.ptr, ddw.ptr, ddb.ptr, rows, dim, eps,
+                                           ws.ptr, ws.nbytes, None))
+    return ddx.download(x.shape), ddw.download((dim,)), ddb.download((dim,))
+
+
+def _biased_shapes(q, k, v, bias):
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("q, k and v must be [length, heads, dim]")
+    q_len, heads, kv_len = q.shape[0], q.shape[1], k.shape[0]
+    if k.shape[1] != heads or v.shape[1] != heads:
+        raise ValueError("q, k and v must have the same heads")
+    if v.shape[0] != kv_len:
+        raise ValueError("k and v must have the same length")
+    if q.shape[2] != k.shape[2]:
+        raise ValueError("q and k must have the same head_dim")
+    if bias.shape != (heads, q_len, kv_len):
+        raise ValueError("bias must be [heads, q_len, kv_len]")
+    return q_len, kv_len, heads, q.shape[2], v.shape[2]
+
+
+def biased_attention(q, k, v, bias, scale) -> np.ndarray:
+    """kernels.cpp:707-727: T5 attention with an additive bias [heads, q_len, kv_len]."""
+    q, k, v, bias = _f32(q), _f32(k), _f32(v), _f32(bias)
+    q_len, kv_len, heads, hd, vd = _biased_shapes(q, k, v, bias)
+    ws = Device(lib.dllm_hip_biased_attention_workspace(q_len, kv_len, heads))
+    dq, dk, dv, db = Device.of(q), Device.of(k), Device.of(v), Device.of(bias)
+    out = Device(q_len * heads * vd * 4)
+    check(lib.dllm_hip_biased_attention(dq.ptr, dk.ptr, dv.ptr, db.ptr, out.ptr, q_len, kv_len, heads, hd, vd, scale,
+                                        ws.ptr, ws.nbytes, None))
+    return out.download((q_len, heads, vd))
+
+
+def biased_attention_backward(q, k, v, bias, dout, scale):
+    """kernels.cpp:961-990: (dq, dk, dv, dbias) of biased_attention()."""
+    q, k, v, bias, dout = _f32(q), _f32(k), _f32(v), _f32(bias), _f32(dout)
+    q_len, kv_len, heads, hd, vd = _biased_shapes(q, k, v, bias)
+    if dout.shape != (q_len, heads, vd):
+        raise ValueError("dout must be [q_len, heads, value_dim]")
+    ws = Device(lib.dllm_hip_biased_attention_backward_workspace(q_len, kv_len, heads))
+    d = [Device.of(a) for a in (q, k, v, bias, dout)]
+    outs = [Device(max(a.nbytes, 4)) for a in (q, k, v, bias)]
+    check(lib.dllm_hip_biased_attention_backward(*(x.ptr for x in d), *(o.ptr for o in outs), q_len, kv_len, heads,
+                                                 hd, vd, scale, ws.ptr, ws.nbytes, None))
+    return tuple(o.download(a.shape) for o, a in zip(outs, (q, k, v, bias)))
+
+
 def dequantize_q8_0(values, scales) -> np.ndarray:
     """QuantizedWeight.dequantize (numerics.py:138-139): the int8 values times their block's scale, float32."""
     q = np.ascontiguousarray(values, dtype=np.int8)

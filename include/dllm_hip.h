@@ -164,6 +164,31 @@ int dllm_hip_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n, v
 /* out = f32(q) * scale of the value's block. Replaces QuantizedWeight.dequantize (numerics.py:138-139). */
 int dllm_hip_dequantize_q8_0(const int8_t* q, const float* scales, float* out, size_t n, void* stream);
 
+/* ---- encoder and T5 training kernels (cpp/include/dllm/grad.hpp:112-174, 300-389; nn.hpp:412-432, 474-478,
+ * 827-856) ----
+ * gelu / gelu_backward: kernels.cpp:631, 877-889 (exact erf GELU with the portable erfc). layer_norm /
+ * layer_norm_backward: kernels.cpp:612-625, 858-875 (dx, dw, db; dw and db summed over all rows in order; any of the
+ * three outputs may be NULL). biased_attention / biased_attention_backward: kernels.cpp:707-727, 961-990 (T5's
+ * attention with bias [heads, q_len, kv_len]; q [q_len, heads, head_dim], k [kv_len, heads, head_dim], v [kv_len,
+ * heads, value_dim]; returns dq, dk, dv, dbias). */
+int dllm_hip_gelu(const float* x, float* out, size_t n, void* stream);
+int dllm_hip_gelu_backward(const float* x, const float* dy, float* out, size_t n, void* stream);
+int dllm_hip_layer_norm(const float* x, const float* weight, const float* bias, float* out, size_t rows, size_t dim,
+                        double eps, void* stream);
+size_t dllm_hip_layer_norm_backward_workspace(size_t rows);
+int dllm_hip_layer_norm_backward(const float* x, const float* weight, const float* dy, float* dx, float* dw,
+                                 float* db, size_t rows, size_t dim, double eps, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+size_t dllm_hip_biased_attention_workspace(size_t q_len, size_t kv_len, size_t heads);
+int dllm_hip_biased_attention(const float* q, const float* k, const float* v, const float* bias, float* out,
+                              size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
+                              double scale, void* workspace, size_t workspace_bytes, void* stream);
+size_t dllm_hip_biased_attention_backward_workspace(size_t q_len, size_t kv_len, size_t heads);
+int dllm_hip_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
+                                       const float* dout, float* dq, float* dk, float* dv, float* dbias,
+                                       size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
+                                       double scale, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- quantised linear layers for inference (cpp/include/dllm/quant.hpp:143-169, 355-403; kernels.cpp:310-385) ----
  * linear_q8: x [rows, in] quantised to Q8_0 per row block of 32, q [out, in] int8 (8-byte aligned) and scales
  * [out, in / 32]; out[r][n] = f32(sum over blocks ascending of (f64(xs) f64(ws)) f64(isum) + bias[n]), isum the

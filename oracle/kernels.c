@@ -771,6 +771,241 @@ void orc_linear_q4(const float* x, const uint8_t* wq, const float* ws, const flo
     free(w);
 }
 
+/* ---- encoder and T5 training kernels (grad.hpp:112-174, 300-389; nn.hpp:412-432, 474-478, 827-856) ---- */
+
+/* erfc(a) for a >= 2.5 (math.hpp:332-341): e^(-a^2) / sqrt(pi) / K(a), K the Laplace continued fraction evaluated
+ * backwards from depth 80. */
+static double erfc_tail(double a) {
+    const double inv_sqrt_pi = 5.64189583547756286948e-01;
+    double k = a;
+    for (int n = 80; n >= 1; --n) k = a + (0.5 * n) / k;
+    return orc_exp(-a * a) * inv_sqrt_pi / k;
+}
+
+/* erf (math.hpp:345-370): the 60-term Maclaurin series below 2.5, 1 - erfc_tail(|x|) up to 6, 1 beyond. */
+double orc_erf(double x) {
+    const double two_over_sqrt_pi = 1.12837916709551257390e+00;
+    if (x != x) return x;
+    const double a = x < 0 ? -x : x;
+    double result;
+    if (a < 2.5) {
+        const double a2 = a * a;
+        double term = a, total = a;
+        for (int n = 1; n < 60; ++n) {
+            term = -term * a2 / n;
+            total += term / (2 * n + 1);
+        }
+        result = two_over_sqrt_pi * total;
+    } else if (a > 6.0) {
+        result = 1.0;
+    } else {
+        result = 1.0 - erfc_tail(a);
+    }
+    return x < 0 ? -result : result;
+}
+
+/* erfc (math.hpp:373-384). */
+double orc_erfc(double x) {
+    if (x != x) return x;
+    if (x < 2.5) return 1.0 - orc_erf(x);
+    if (x > 27.3) return 0.0;
+    return erfc_tail(x);
+}
+
+/* gelu (nn.hpp:474-478): 0.5 x erfc(-x / sqrt 2) in double, rounded once. */
+float orc_gelu(float x) {
+    const double inv_sqrt2 = 7.07106781186547524401e-01;
+    const double d = x;
+    return (float)(0.5 * d * orc_erfc(-d * inv_sqrt2));
+}
+
+/* gelu_backward (grad.hpp:165-172): dy (0.5 erfc(-x / sqrt 2) + x e^(-x^2 / 2) / sqrt(2 pi)), rounded once. */
+float orc_gelu_backward(float x, float dy) {
+    const double inv_sqrt2 = 7.07106781186547524401e-01;
+    const double inv_sqrt_2pi = 3.98942280401432677940e-01;
+    const double d = x;
+    const double slope = 0.5 * orc_erfc(-d * inv_sqrt2) + d * orc_exp(-0.5 * d * d) * inv_sqrt_2pi;
+    return (float)((double)dy * slope);
+}
+
+/* layer_norm (nn.hpp:412-432): mean and the centred sum of squares over the row ascending, inv_std = 1 / sqrt(. /
+ * dim + eps); out = f32((x - mean) inv_std w + b). */
+void orc_layer_norm(const float* x, const float* w, const float* b, float* out, size_t rows, size_t dim, double eps) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * dim;
+        double total = 0.0;
+        for (size_t i = 0; i < dim; ++i) total += (double)xr[i];
+        const double mean = total / (double)dim;
+        double sum_sq = 0.0;
+        for (size_t i = 0; i < dim; ++i) {
+            const double c = (double)xr[i] - mean;
+            sum_sq += c * c;
+        }
+        const double inv_std = 1.0 / sqrt(sum_sq / (double)dim + eps);
+        for (size_t i = 0; i < dim; ++i) {
+            const double scaled = ((double)xr[i] - mean) * inv_std * (double)w[i];
+            out[r * dim + i] = (float)(scaled + (double)b[i]);
+        }
+    }
+}
+
+/* layer_norm_backward (grad.hpp:112-163): per row the forward's mean and inv_std, xhat = (x - mean) inv_std,
+ * g = w dy; sums of g and g xhat over the row ascending; dx = f32(inv_std (g - sum g / dim - xhat sum(g xhat) / dim));
+ * dw = f32(sum over rows ascending of dy xhat), db = f32(sum of dy). */
+void orc_layer_norm_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, float* db,
+                             size_t rows, size_t dim, double eps) {
+    double* dw_acc = (double*)calloc(dim ? dim : 1, sizeof(double));
+    double* db_acc = (double*)calloc(dim ? dim : 1, sizeof(double));
+    double* xhat = (double*)malloc((dim ? dim : 1) * sizeof(double));
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * dim;
+        const float* dyr = dy + r * dim;
+        double total = 0.0;
+        for (size_t i = 0; i < dim; ++i) total += (double)xr[i];
+        const double mean = total / (double)dim;
+        double sum_sq = 0.0;
+        for (size_t i = 0; i < dim; ++i) {
+            const double c = (double)xr[i] - mean;
+            sum_sq += c * c;
+        }
+        const double inv_std = 1.0 / sqrt(sum_sq / (double)dim + eps);
+        double g_sum = 0.0, gx_sum = 0.0;
+        for (size_t i = 0; i < dim; ++i) {
+            xhat[i] = ((double)xr[i] - mean) * inv_std;
+            const double g = (double)w[i] * (double)dyr[i];
+            g_sum += g;
+            gx_sum += g * xhat[i];
+            dw_acc[i] += (double)dyr[i] * xhat[i];
+            db_acc[i] += (double)dyr[i];
+        }
+        if (dx) {
+            const double g_mean = g_sum / (double)dim;
+            const double gx_mean = gx_sum / (double)dim;
+            for (size_t i = 0; i < dim; ++i) {
+                const double g = (double)w[i] * (double)dyr[i];
+                dx[r * dim + i] = (float)(inv_std * (g - g_mean - xhat[i] * gx_mean));
+            }
+        }
+    }
+    for (size_t i = 0; i < dim; ++i) {
+        if (dw) dw[i] = (float)dw_acc[i];
+        if (db) db[i] = (float)db_acc[i];
+    }
+    free(dw_acc);
+    free(db_acc);
+    free(xhat);
+}
+
+/* biased_attention (nn.hpp:827-856): scores (q k + bias) scale, then attention_finish without soft-cap. q [q_len,
+ * heads, head_dim], k [kv_len, heads, head_dim], v [kv_len, heads, value_dim], bias [heads, q_len, kv_len]. */
+void orc_biased_attention(const float* q, const float* k, const float* v, const float* bias, float* out, size_t q_len,
+                          size_t kv_len, size_t heads, size_t head_dim, size_t value_dim, double scale) {
+    double* s = (double*)malloc((kv_len ? kv_len : 1) * sizeof(double));
+    double* acc = (double*)malloc((value_dim ? value_dim : 1) * sizeof(double));
+    for (size_t t = 0; t < q_len; ++t)
+        for (size_t h = 0; h < heads; ++h) {
+            float* oh = out + (t * heads + h) * value_dim;
+            if (kv_len == 0) {
+                for (size_t i = 0; i < value_dim; ++i) oh[i] = 0.0f;
+                continue;
+            }
+            const float* qh = q + (t * heads + h) * head_dim;
+            const float* bh = bias + (h * q_len + t) * kv_len;
+            for (size_t j = 0; j < kv_len; ++j) {
+                const float* kj = k + (j * heads + h) * head_dim;
+                double d = 0.0;
+                for (size_t i = 0; i < head_dim; ++i) d += (double)qh[i] * (double)kj[i];
+                s[j] = (d + (double)bh[j]) * scale;
+            }
+            double max = s[0];
+            for (size_t j = 1; j < kv_len; ++j)
+                if (s[j] > max) max = s[j];
+            double total = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) {
+                s[j] = orc_exp(s[j] - max);
+                total += s[j];
+            }
+            for (size_t i = 0; i < value_dim; ++i) acc[i] = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) {
+                const float* vj = v + (j * heads + h) * value_dim;
+                for (size_t i = 0; i < value_dim; ++i) acc[i] += s[j] * (double)vj[i];
+            }
+            const double inv = 1.0 / total;
+            for (size_t i = 0; i < value_dim; ++i) oh[i] = (float)(acc[i] * inv);
+        }
+    free(s);
+    free(acc);
+}
+
+/* biased_attention_backward (grad.hpp:300-389): per (t, h), t then h ascending: p recomputed (scores, max, exp,
+ * total, times 1 / total), dp_j = dout . v_j, D = sum p dp, ds = p (dp - D) scale (dbias = f32(ds)), dq = sum_j ds
+ * k_j; dk[j] += ds q, dv[j] += p dout in double, rounded once at the end. */
+void orc_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
+                                   const float* dout, float* dq, float* dk, float* dv, float* dbias, size_t q_len,
+                                   size_t kv_len, size_t heads, size_t head_dim, size_t value_dim, double scale) {
+    double* probs = (double*)malloc((kv_len ? kv_len : 1) * sizeof(double));
+    double* dprobs = (double*)malloc((kv_len ? kv_len : 1) * sizeof(double));
+    double* dq_acc = (double*)malloc((head_dim ? head_dim : 1) * sizeof(double));
+    double* dk_acc = (double*)calloc(kv_len * heads * head_dim + 1, sizeof(double));
+    double* dv_acc = (double*)calloc(kv_len * heads * value_dim + 1, sizeof(double));
+    for (size_t t = 0; t < q_len; ++t)
+        for (size_t h = 0; h < heads; ++h) {
+            const float* qh = q + (t * heads + h) * head_dim;
+            const float* bh = bias + (h * q_len + t) * kv_len;
+            const float* doh = dout + (t * heads + h) * value_dim;
+            float* dqh = dq + (t * heads + h) * head_dim;
+            float* dbh = dbias + (h * q_len + t) * kv_len;
+            if (kv_len == 0) {
+                for (size_t i = 0; i < head_dim; ++i) dqh[i] = 0.0f;
+                continue;
+            }
+            double max = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) {
+                const float* kj = k + (j * heads + h) * head_dim;
+                double d = 0.0;
+                for (size_t i = 0; i < head_dim; ++i) d += (double)qh[i] * (double)kj[i];
+                probs[j] = (d + (double)bh[j]) * scale;
+                if (j == 0 || probs[j] > max) max = probs[j];
+            }
+            double total = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) {
+                probs[j] = orc_exp(probs[j] - max);
+                total += probs[j];
+            }
+            const double inv = 1.0 / total;
+            double weighted = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) {
+                probs[j] *= inv;
+                const float* vj = v + (j * heads + h) * value_dim;
+                double d = 0.0;
+                for (size_t i = 0; i < value_dim; ++i) d += (double)doh[i] * (double)vj[i];
+                dprobs[j] = d;
+                weighted += probs[j] * d;
+            }
+            for (size_t i = 0; i < head_dim; ++i) dq_acc[i] = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) {
+                const double ds = probs[j] * (dprobs[j] - weighted) * scale;
+                dbh[j] = (float)ds;
+                const float* kj = k + (j * heads + h) * head_dim;
+                double* dkj = dk_acc + (j * heads + h) * head_dim;
+                double* dvj = dv_acc + (j * heads + h) * value_dim;
+                for (size_t i = 0; i < head_dim; ++i) {
+                    dq_acc[i] += ds * (double)kj[i];
+                    dkj[i] += ds * (double)qh[i];
+                }
+                for (size_t i = 0; i < value_dim; ++i) dvj[i] += probs[j] * (double)doh[i];
+            }
+            for (size_t i = 0; i < head_dim; ++i) dqh[i] = (float)dq_acc[i];
+        }
+    for (size_t i = 0; i < kv_len * heads * head_dim; ++i) dk[i] = (float)dk_acc[i];
+    for (size_t i = 0; i < kv_len * heads * value_dim; ++i) dv[i] = (float)dv_acc[i];
+    free(probs);
+    free(dprobs);
+    free(dq_acc);
+    free(dk_acc);
+    free(dv_acc);
+}
+
 /* rope_inv_freq with default scaling (numerics.py:267-297): theta^(-2i/dim) = exp(-(2i/dim) log theta). */
 void orc_rope_inv_freq(size_t rotary_dim, double theta, double* out) {
     const double log_theta = orc_log(theta);

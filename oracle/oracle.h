@@ -81,6 +81,21 @@ void orc_column_mean(const float* x, float* out, size_t rows, size_t cols); /* i
 void orc_quantize_q8_0(const float* x, int8_t* q, float* scales, size_t n); /* quant.hpp:27-60 */
 void orc_linear_q8(const float* x, const int8_t* wq, const float* ws, const float* bias, float* out, size_t rows,
                    size_t in, size_t n_out);                                            /* quant.hpp:143-169,355-383 */
+double orc_erf(double x);                                                               /* math.hpp:345-370 */
+double orc_erfc(double x);                                                              /* math.hpp:373-384 */
+float orc_gelu(float x);                                                                /* nn.hpp:474-478 */
+float orc_gelu_backward(float x, float dy);                                             /* grad.hpp:165-172 */
+void orc_layer_norm(const float* x, const float* w, const float* b, float* out, size_t rows, size_t dim,
+                    double eps);                                                        /* nn.hpp:412-432 */
+void orc_layer_norm_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, float* db,
+                             size_t rows, size_t dim, double eps);                      /* grad.hpp:112-163 */
+void orc_biased_attention(const float* q, const float* k, const float* v, const float* bias, float* out,
+                          size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
+                          double scale);                                                /* nn.hpp:827-856 */
+void orc_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
+                                   const float* dout, float* dq, float* dk, float* dv, float* dbias, size_t q_len,
+                                   size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
+                                   double scale);                                       /* grad.hpp:300-389 */
 void orc_quantize_q4_0(const float* x, uint8_t* packed, float* scales, size_t n);       /* quant.hpp:67-94 */
 void orc_unpack_q4_0(const uint8_t* packed, int8_t* values, size_t n);                  /* quant.hpp:97-108 */
 void orc_linear_q4(const float* x, const uint8_t* wq, const float* ws, const float* bias, float* out, size_t rows,

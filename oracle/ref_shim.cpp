@@ -181,4 +181,35 @@ void ref_linear_q4(const float* x, const uint8_t* wq, const float* ws, const flo
     dllm::linear_q4(x, wq, ws, bias, out, rows, in, n_out);
 }
 
+double ref_erf(double x) { return dllm::erf(x); }
+double ref_erfc(double x) { return dllm::erfc(x); }
+void ref_gelu_n(const float* x, float* out, size_t n) {
+    FpEnvGuard guard;
+    for (size_t i = 0; i < n; ++i) out[i] = dllm::gelu(x[i]);
+}
+void ref_gelu_backward_n(const float* x, const float* dy, float* out, size_t n) {
+    FpEnvGuard guard;
+    for (size_t i = 0; i < n; ++i) out[i] = dllm::gelu_backward(x[i], dy[i]);
+}
+void ref_layer_norm(const float* x, const float* w, const float* b, float* out, size_t rows, size_t dim, double eps) {
+    FpEnvGuard guard;
+    dllm::layer_norm(x, w, b, out, rows, dim, eps);
+}
+void ref_layer_norm_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, float* db,
+                             size_t rows, size_t dim, double eps) {
+    FpEnvGuard guard;
+    dllm::layer_norm_backward(x, w, dy, dx, dw, db, rows, dim, eps);
+}
+void ref_biased_attention(const float* q, const float* k, const float* v, const float* bias, float* out, size_t ql,
+                          size_t kl, size_t heads, size_t hd, size_t vd, double scale) {
+    FpEnvGuard guard;
+    dllm::biased_attention(q, k, v, bias, out, ql, kl, heads, hd, vd, scale);
+}
+void ref_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
+                                   const float* dout, float* dq, float* dk, float* dv, float* dbias, size_t ql,
+                                   size_t kl, size_t heads, size_t hd, size_t vd, double scale) {
+    FpEnvGuard guard;
+    dllm::biased_attention_backward(q, k, v, bias, dout, dq, dk, dv, dbias, ql, kl, heads, hd, vd, scale);
+}
+
 }  // extern "C"

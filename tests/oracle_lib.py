@@ -847,6 +847,98 @@ def linear_q4(fn, x: np.ndarray, packed: np.ndarray, scales: np.ndarray, bias=No
     return out
 
 
+# ---- encoder and T5 kernels (grad.hpp:112-174, 300-389; nn.hpp:412-432, 474-478, 827-856) ----
+
+def _declare_encoder(lib, prefix: str) -> None:
+    d, f, sz, vp = C.c_double, C.c_float, C.c_size_t, C.c_void_p
+    for name, res, args in (
+            ("erf", d, [d]), ("erfc", d, [d]),
+            ("layer_norm", None, [vp, vp, vp, vp, sz, sz, d]),
+            ("layer_norm_backward", None, [vp, vp, vp, vp, vp, vp, sz, sz, d]),
+            ("biased_attention", None, [vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d]),
+            ("biased_attention_backward", None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d])):
+        fn = getattr(lib, f"{prefix}_{name}")
+        fn.restype, fn.argtypes = res, args
+    if prefix == "orc":
+        lib.orc_gelu.restype, lib.orc_gelu.argtypes = f, [f]
+        lib.orc_gelu_backward.restype, lib.orc_gelu_backward.argtypes = f, [f, f]
+    else:
+        lib.ref_gelu_n.argtypes = [vp, vp, sz]
+        lib.ref_gelu_backward_n.argtypes = [vp, vp, vp, sz]
+
+
+class Encoder:
+    """The encoder/T5 kernels of the oracle (prefix "orc") or of the compiled reference (prefix "ref")."""
+
+    def __init__(self, lib, prefix: str) -> None:
+        _declare_encoder(lib, prefix)
+        self.lib, self.p = lib, prefix
+
+    def fn(self, name):
+        return getattr(self.lib, f"{self.p}_{name}")
+
+    def erf(self, x: float) -> float:
+        return self.fn("erf")(x)
+
+    def erfc(self, x: float) -> float:
+        return self.fn("erfc")(x)
+
+    def gelu(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        if self.p == "orc":
+            return np.array([self.lib.orc_gelu(float(v)) for v in x.ravel()], np.float32).reshape(x.shape)
+        out = np.empty_like(x)
+        self.lib.ref_gelu_n(ptr(x), ptr(out), x.size)
+        return out
+
+    def gelu_backward(self, x, dy):
+        x, dy = np.ascontiguousarray(x, np.float32), np.ascontiguousarray(dy, np.float32)
+        if self.p == "orc":
+            return np.array([self.lib.orc_gelu_backward(float(a), float(b)) for a, b in zip(x.ravel(), dy.ravel())],
+                            np.float32).reshape(x.shape)
+        out = np.empty_like(x)
+        self.lib.ref_gelu_backward_n(ptr(x), ptr(dy), ptr(out), x.size)
+        return out
+
+    def layer_norm(self, x, w, b, eps=1e-12):
+        x, w, b = (np.ascontiguousarray(a, np.float32) for a in (x, w, b))
+        out = np.empty_like(x)
+        dim = x.shape[-1]
+        self.fn("layer_norm")(ptr(x), ptr(w), ptr(b), ptr(out), x.size // dim if dim else 0, dim, eps)
+        return out
+
+    def layer_norm_backward(self, x, w, dy, eps=1e-12):
+        x, w, dy = (np.ascontiguousarray(a, np.float32) for a in (x, w, dy))
+        dim = x.shape[-1]
+        dx, dw, db = np.empty_like(x), np.empty(dim, np.float32), np.empty(dim, np.float32)
+        self.fn("layer_norm_backward")(ptr(x), ptr(w), ptr(dy), ptr(dx), ptr(dw), ptr(db),
+                                       x.size // dim if dim else 0, dim, eps)
+        return dx, dw, db
+
+    def biased_attention(self, q, k, v, bias, scale):
+        q, k, v, bias = (np.ascontiguousarray(a, np.float32) for a in (q, k, v, bias))
+        out = np.empty((q.shape[0], q.shape[1], v.shape[2]), np.float32)
+        self.fn("biased_attention")(ptr(q), ptr(k), ptr(v), ptr(bias), ptr(out), q.shape[0], k.shape[0], q.shape[1],
+                                    q.shape[2], v.shape[2], scale)
+        return out
+
+    def biased_attention_backward(self, q, k, v, bias, dout, scale):
+        q, k, v, bias, dout = (np.ascontiguousarray(a, np.float32) for a in (q, k, v, bias, dout))
+        dq, dk, dv, dbias = np.empty_like(q), np.empty_like(k), np.empty_like(v), np.empty_like(bias)
+        self.fn("biased_attention_backward")(ptr(q), ptr(k), ptr(v), ptr(bias), ptr(dout), ptr(dq), ptr(dk), ptr(dv),
+                                             ptr(dbias), q.shape[0], k.shape[0], q.shape[1], q.shape[2], v.shape[2],
+                                             scale)
+        return dq, dk, dv, dbias
+
+
+def oracle_encoder() -> Encoder:
+    return Encoder(oracle(), "orc")
+
+
+def ref_encoder() -> Encoder:
+    return Encoder(ref(), "ref")
+
+
 def dequantize_q8_0(q: np.ndarray, scales: np.ndarray) -> np.ndarray:
     """QuantizedWeight.dequantize (numerics.py:138-139): int8 -> float32 times the block's scale, in float32."""
     return q.astype(np.float32) * np.repeat(scales, 32)

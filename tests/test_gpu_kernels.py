@@ -326,3 +326,51 @@ def test_linear_q8_rows_are_batch_invariant(K):
     full = K.linear_q8(x, q, s)
     for m in (1, 7, 64):
         assert_same(K.linear_q8(x[:m], q, s), full[:m], f"linear_q8 M={m}")
+
+
+def assert_same_or_nan(a, b, what=""):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a)
+    assert np.array_equal(nan, np.isnan(b)), f"{what}: NaN positions differ"
+    assert_same(np.where(nan, 0, a), np.where(nan, 0, b), what)
+
+
+def test_gelu_and_backward_match_the_oracle(K):
+    """Exact GELU and its gradient (kernels.cpp:631, 877-889), bit for bit, over the erf/erfc branch points and
+    non-finite inputs."""
+    x = np.concatenate([O.gaussian(11, 4001, scale=3.0),
+                        np.array([0, -0.0, 0.5, -0.5, 0.84375, -0.84375, 1.25, -1.25, 2.857, -2.857, 6, -6, 28, -28,
+                                  1e-30, -1e-30, 1e-40, np.inf, -np.inf, np.nan, 3e38, -3e38], np.float32)])
+    dy = O.gaussian(12, x.size)
+    enc = O.oracle_encoder()
+    assert_same_or_nan(K.gelu(x), enc.gelu(x), "gelu")
+    assert_same_or_nan(K.gelu_backward(x, dy), enc.gelu_backward(x, dy), "gelu_backward")
+
+
+@pytest.mark.parametrize(("rows", "dim"), [(1, 1), (3, 7), (37, 64), (130, 768), (5, 1031)])
+def test_layer_norm_and_backward_match_the_oracle(K, rows, dim):
+    """LayerNorm forward and backward (kernels.cpp:612-625, 858-875), bit for bit."""
+    x, w, b, dy = O.gaussian(21, rows, dim), O.gaussian(22, dim), O.gaussian(23, dim), O.gaussian(24, rows, dim)
+    enc = O.oracle_encoder()
+    for eps in (1e-12, 1e-6):
+        assert_same(K.layer_norm(x, w, b, eps), enc.layer_norm(x, w, b, eps), "layer_norm")
+        for got, want, what in zip(K.layer_norm_backward(x, w, dy, eps), enc.layer_norm_backward(x, w, dy, eps),
+                                   ("dx", "dw", "db")):
+            assert_same(got, want, f"layer_norm_backward {what}")
+
+
+@pytest.mark.parametrize(("q_len", "kv_len", "heads", "hd", "vd"),
+                         [(1, 3, 1, 4, 4), (5, 7, 2, 8, 8), (17, 17, 4, 16, 12), (33, 70, 3, 64, 64), (3, 0, 2, 4, 4)])
+def test_biased_attention_and_backward_match_the_oracle(K, q_len, kv_len, heads, hd, vd):
+    """T5 biased attention forward and backward (kernels.cpp:707-727, 961-990), bit for bit; kv_len 0 is the empty
+    case (zero output and gradients)."""
+    q, k, v = O.gaussian(31, q_len, heads, hd), O.gaussian(32, kv_len, heads, hd), O.gaussian(33, kv_len, heads, vd)
+    bias, dout = O.gaussian(34, heads, q_len, kv_len), O.gaussian(35, q_len, heads, vd)
+    if kv_len > 2:
+        bias[0, 0, :2] = -np.inf  # masked keys
+    enc = O.oracle_encoder()
+    assert_same(K.biased_attention(q, k, v, bias, 0.25), enc.biased_attention(q, k, v, bias, 0.25), "forward")
+    for got, want, what in zip(K.biased_attention_backward(q, k, v, bias, dout, 0.25),
+                               enc.biased_attention_backward(q, k, v, bias, dout, 0.25),
+                               ("dq", "dk", "dv", "dbias")):
+        assert_same_or_nan(got, want, f"biased_attention_backward {what}")

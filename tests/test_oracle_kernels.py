@@ -376,3 +376,81 @@ def test_q4_0_packs_two_values_per_byte():
     assert np.all(scales == np.float32(0.5))
     assert np.array_equal(O.unpack_q4_0(O.oracle().orc_unpack_q4_0, packed).astype(np.float32), k.ravel())
     assert packed[0] == (int(k[0, 0]) + 8) | ((int(k[0, 16]) + 8) << 4)
+
+
+# ---- encoder and T5 kernels ----
+
+ERF_POINTS = [0.0, -0.0, 1e-300, 0.3, -0.3, 1.0, 2.4999999, 2.5, -2.5, 3.7, 6.0, 6.0000001, -7.0, 27.3, 27.31, 30.0,
+              -30.0, 1e-5, float("inf"), float("-inf"), float("nan")]
+
+
+@needs_ref
+def test_erf_and_erfc_match_reference_and_mathematics():
+    o, r = O.oracle_encoder(), O.ref_encoder()
+    pts = ERF_POINTS + list(np.linspace(-8, 8, 1001))
+    for x in pts:
+        for name in ("erf", "erfc"):
+            a, b = getattr(o, name)(x), getattr(r, name)(x)
+            assert np.float64(a).tobytes() == np.float64(b).tobytes(), (name, x)
+    for x in np.linspace(-5.5, 5.5, 221):
+        assert math.isclose(o.erf(x), math.erf(x), rel_tol=1e-13, abs_tol=1e-15)
+        assert math.isclose(o.erfc(x), math.erfc(x), rel_tol=1e-11, abs_tol=1e-300)
+
+
+@needs_ref
+def test_gelu_and_gelu_backward_match_reference():
+    o, r = O.oracle_encoder(), O.ref_encoder()
+    x = np.concatenate([O.gaussian(41, 3000, scale=3.0),
+                        np.array([0.0, -0.0, 40.0, -40.0, 1e-30, np.inf, -np.inf, np.nan], np.float32)])
+    dy = O.gaussian(42, x.size)
+    same = lambda a, b: np.array_equal(np.isnan(a), np.isnan(b)) and np.where(np.isnan(a), 0, a).tobytes() == np.where(
+        np.isnan(b), 0, b).tobytes()
+    assert same(o.gelu(x), r.gelu(x))
+    assert same(o.gelu_backward(x, dy), r.gelu_backward(x, dy))
+
+
+@needs_ref
+@pytest.mark.parametrize(("rows", "dim"), [(1, 8), (9, 48), (33, 768)])
+def test_layer_norm_and_backward_match_reference(rows, dim):
+    o, r = O.oracle_encoder(), O.ref_encoder()
+    x, w, b, dy = O.gaussian(1, rows, dim, scale=2.0), O.gaussian(2, dim), O.gaussian(3, dim), O.gaussian(4, rows, dim)
+    assert o.layer_norm(x, w, b).tobytes() == r.layer_norm(x, w, b).tobytes()
+    for got, want in zip(o.layer_norm_backward(x, w, dy, 1e-6), r.layer_norm_backward(x, w, dy, 1e-6)):
+        assert got.tobytes() == want.tobytes()
+
+
+def test_layer_norm_backward_finite_differences():
+    """dx, dw, db of layer_norm against central differences of sum(layer_norm * dy) (float64 tolerance)."""
+    o = O.oracle_encoder()
+    x, w, b, dy = O.gaussian(5, 3, 16, scale=2.0), O.gaussian(6, 16), O.gaussian(7, 16), O.gaussian(8, 3, 16)
+    dx, dw, db = o.layer_norm_backward(x, w, dy, 1e-5)
+
+    def f(xx, ww, bb):  # float64 layer_norm
+        xx = xx.astype(np.float64)
+        mean = xx.mean(axis=1, keepdims=True)
+        inv = 1.0 / np.sqrt(((xx - mean) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+        return float(np.sum(((xx - mean) * inv * ww + bb) * dy.astype(np.float64)))
+
+    h = 1e-4
+    for k, grad in enumerate((dx, dw, db)):
+        base = [a.astype(np.float64) for a in (x, w, b)]
+        flat = base[k].ravel()
+        for idx in (0, flat.size // 2, flat.size - 1):
+            plus, minus = [a.copy() for a in base], [a.copy() for a in base]
+            plus[k].ravel()[idx] += h
+            minus[k].ravel()[idx] -= h
+            numeric = (f(*plus) - f(*minus)) / (2 * h)
+            assert math.isclose(grad.ravel()[idx], numeric, rel_tol=1e-3, abs_tol=1e-4)
+
+
+@needs_ref
+@pytest.mark.parametrize(("q_len", "kv_len", "heads", "hd", "vd"), [(5, 7, 2, 8, 8), (17, 17, 4, 16, 12), (1, 3, 1, 4, 4),
+                                                                    (3, 0, 2, 4, 4)])
+def test_biased_attention_and_backward_match_reference(q_len, kv_len, heads, hd, vd):
+    o, r = O.oracle_encoder(), O.ref_encoder()
+    q, k, v = O.gaussian(11, q_len, heads, hd), O.gaussian(12, kv_len, heads, hd), O.gaussian(13, kv_len, heads, vd)
+    bias, dout = O.gaussian(14, heads, q_len, kv_len, scale=3.0), O.gaussian(15, q_len, heads, vd)
+    assert o.biased_attention(q, k, v, bias, 0.25).tobytes() == r.biased_attention(q, k, v, bias, 0.25).tobytes()
+    for got, want in zip(o.biased_attention_backward(q, k, v, bias, dout, 0.25),
+                         r.biased_attention_backward(q, k, v, bias, dout, 0.25)):
+        assert got.tobytes() == want.tobytes()
