@@ -303,7 +303,7 @@ def q8_case(seed: int, rows: int, in_f: int, out_f: int):
     return x, q.reshape(out_f, in_f), s.reshape(out_f, in_f // 32), O.gaussian(seed + 2, out_f)
 
 
-@pytest.mark.parametrize(("rows", "in_f", "out_f"), [(1, 32, 1), (7, 64, 19), (65, 256, 48), (130, 1024, 200)])
+@pytest.mark.parametrize(("rows", "in_f", "out_f"), [(1, 32, 1), (7, 64, 19), (8, 8960, 37), (9, 96, 40), (2, 8192 + 32, 5), (65, 256, 48), (130, 1024, 200)])
 def test_linear_q8_and_q4(K, rows, in_f, out_f):
     """Q8_0 / Q4_0 linear (quant.hpp:143-169, 355-403) on the int8 matrix cores against the oracle, bit for bit."""
     x, q, s, b = q8_case(5, rows, in_f, out_f)
