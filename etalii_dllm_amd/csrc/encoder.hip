@@ -5,8 +5,8 @@
 // Every reduction keeps the reference's order and double accumulator:
 // - GELU: elementwise, 0.5 x erfc(-x / sqrt 2) and its slope with the portable erf/erfc (devmath.h), rounded once.
 // - LayerNorm: one lane per row runs the row's chains (sum, centred squares, sum of g = w dy and of g xhat) in index
-//   order; dw and db are one lane per column over the rows in order, xhat recomputed from the row's saved mean and
-//   inv_std exactly as the row pass computes it.
+//   order over columns staged in LDS; dw and db are one lane per column over the rows in order, xhat recomputed from
+//   the row's saved mean and inv_std exactly as the row pass computes it.
 // - Biased attention: one wave per (query t, head h). Scores are one lane per key (dot over head_dim ascending); the
 //   maximum, the exponentials' total and D = sum p dp are one lane's scans over the keys in order; dq and the
 //   forward's value sums are one lane per output column, keys ascending. dk[j, h] and dv[j, h] sum over queries t
@@ -15,6 +15,7 @@
 #include "devmath.h"
 #include "dllm_hip.h"
 #include "kernels.h"
+#include "lds_copy.h"
 
 namespace dllm_hip {
 
@@ -39,83 +40,308 @@ __global__ __launch_bounds__(256) void gelu_backward_kernel(const float* __restr
     out[i] = static_cast<float>(static_cast<double>(dy[i]) * slope);
 }
 
-// mean and inv_std of row r (nn.hpp:412-426)
-__device__ inline void row_moments(const float* xr, int64_t dim, double eps, double* mean_out, double* inv_out) {
+// LayerNorm rows: a 64-thread workgroup takes 16 rows. Each pass over the columns stages 64 columns of the 16 rows
+// (and of dy, and the weights) in LDS with coalesced loads, the next chunk's loads in flight while lane r (r < 16)
+// runs row r's chain over the staged columns in order. The chains are those of nn.hpp:412-426 and grad.hpp:112-163:
+// total, then the centred squares, then (backward) the sums of g = w dy and of g xhat, each a double in index order.
+constexpr int kLnRows = 16;
+
+template <bool kBackward>
+struct LnTiles {
+    float x[kLnRows][65];
+    float dy[kBackward ? kLnRows : 1][65];
+    float w[64];
+    float b[64];
+};
+
+template <bool kBackward>
+struct LnChunk {
+    float x[kLnRows];
+    float dy[kBackward ? kLnRows : 1];
+    float w, b;
+};
+
+template <bool kBackward>
+__device__ inline void ln_fetch(LnChunk<kBackward>& c, const float* x, const float* dy, const float* w,
+                                const float* b, int64_t r0, int64_t c0, int64_t rows, int64_t dim, int lane) {
+    const int64_t col = c0 + lane;
+    const bool in_col = col < dim;
+    for (int rr = 0; rr < kLnRows; ++rr) {
+        const bool ok = in_col && r0 + rr < rows;
+        c.x[rr] = ok ? x[(r0 + rr) * dim + col] : 0.0f;
+        if constexpr (kBackward) c.dy[rr] = ok ? dy[(r0 + rr) * dim + col] : 0.0f;
+    }
+    c.w = in_col ? w[col] : 0.0f;
+    c.b = (in_col && b) ? b[col] : 0.0f;
+}
+
+template <bool kBackward>
+__device__ inline void ln_stage(LnTiles<kBackward>& t, const LnChunk<kBackward>& c, int lane) {
+    for (int rr = 0; rr < kLnRows; ++rr) {
+        t.x[rr][lane] = c.x[rr];
+        if constexpr (kBackward) t.dy[rr][lane] = c.dy[rr];
+    }
+    t.w[lane] = c.w;
+    t.b[lane] = c.b;
+}
+
+// One pass over the columns: body(c0, n) runs on lanes 0..15 with chunk [c0, c0 + n) staged; after(c0, n) runs on
+// all lanes once body is done (a store of the chunk's results).
+template <bool kBackward, typename Body, typename After>
+__device__ inline void ln_pass(LnTiles<kBackward>& t, const float* x, const float* dy, const float* w, const float* b,
+                               int64_t r0, int64_t rows, int64_t dim, int lane, Body body, After after) {
+    LnChunk<kBackward> c;
+    ln_fetch<kBackward>(c, x, dy, w, b, r0, 0, rows, dim, lane);
+    for (int64_t c0 = 0; c0 < dim; c0 += 64) {
+        lds_barrier();
+        ln_stage<kBackward>(t, c, lane);
+        lds_barrier();
+        if (c0 + 64 < dim) ln_fetch<kBackward>(c, x, dy, w, b, r0, c0 + 64, rows, dim, lane);
+        const int n = dim - c0 < 64 ? static_cast<int>(dim - c0) : 64;
+        if (lane < kLnRows) body(c0, n);
+        lds_barrier();
+        after(c0, n);
+    }
+}
+
+// mean and inv_std of the workgroup's rows (lane r holds row r's); two passes.
+template <bool kBackward>
+__device__ inline void ln_moments(LnTiles<kBackward>& t, const float* x, const float* dy, const float* w,
+                                  int64_t r0, int64_t rows, int64_t dim, double eps, int lane, double* mean_out,
+                                  double* inv_out) {
     double total = 0.0;
-    for (int64_t i = 0; i < dim; ++i) total += static_cast<double>(xr[i]);
+    ln_pass<kBackward>(
+        t, x, dy, w, nullptr, r0, rows, dim, lane,
+        [&](int64_t, int n) {
+            for (int j = 0; j < n; ++j) total += static_cast<double>(t.x[lane][j]);
+        },
+        [](int64_t, int) {});
     const double mean = total / static_cast<double>(dim);
     double sum_sq = 0.0;
-    for (int64_t i = 0; i < dim; ++i) {
-        const double c = static_cast<double>(xr[i]) - mean;
-        sum_sq += c * c;
-    }
+    ln_pass<kBackward>(
+        t, x, dy, w, nullptr, r0, rows, dim, lane,
+        [&](int64_t, int n) {
+            for (int j = 0; j < n; ++j) {
+                const double c = static_cast<double>(t.x[lane][j]) - mean;
+                sum_sq += c * c;
+            }
+        },
+        [](int64_t, int) {});
     *mean_out = mean;
     *inv_out = 1.0 / sqrt(sum_sq / static_cast<double>(dim) + eps);
 }
 
-__global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                         const float* __restrict__ b, float* __restrict__ out,
-                                                         int64_t rows, int64_t dim, double eps) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (r >= rows) return;
-    const float* xr = x + r * dim;
-    double mean, inv_std;
-    row_moments(xr, dim, eps, &mean, &inv_std);
-    for (int64_t i = 0; i < dim; ++i) {
-        const double scaled = (static_cast<double>(xr[i]) - mean) * inv_std * static_cast<double>(w[i]);
-        out[r * dim + i] = static_cast<float>(scaled + static_cast<double>(b[i]));
-    }
+// the chunk's results, written by lanes 0..15 into t.x, stored by all lanes with coalesced writes
+template <bool kBackward>
+__device__ inline void ln_store(const LnTiles<kBackward>& t, float* out, int64_t r0, int64_t c0, int n, int64_t rows,
+                                int64_t dim, int lane) {
+    if (lane >= n) return;
+    for (int rr = 0; rr < kLnRows; ++rr)
+        if (r0 + rr < rows) out[(r0 + rr) * dim + c0 + lane] = t.x[rr][lane];
+}
+
+__global__ __launch_bounds__(64) void layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                        const float* __restrict__ b, float* __restrict__ out,
+                                                        int64_t rows, int64_t dim, double eps) {
+    __shared__ LnTiles<false> t;
+    const int lane = static_cast<int>(threadIdx.x);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kLnRows;
+    double mean = 0.0, inv_std = 0.0;
+    ln_moments<false>(t, x, nullptr, w, r0, rows, dim, eps, lane, &mean, &inv_std);
+    ln_pass<false>(
+        t, x, nullptr, w, b, r0, rows, dim, lane,
+        [&](int64_t, int n) {
+            for (int j = 0; j < n; ++j) {
+                const double scaled = (static_cast<double>(t.x[lane][j]) - mean) * inv_std *
+                                      static_cast<double>(t.w[j]);
+                t.x[lane][j] = static_cast<float>(scaled + static_cast<double>(t.b[j]));
+            }
+        },
+        [&](int64_t c0, int n) { ln_store<false>(t, out, r0, c0, n, rows, dim, lane); });
 }
 
 // grad.hpp:112-163, the row part: dx, and each row's mean and inv_std for the column sums.
-__global__ __launch_bounds__(256) void layer_norm_backward_rows_kernel(const float* __restrict__ x,
-                                                                       const float* __restrict__ w,
-                                                                       const float* __restrict__ dy,
-                                                                       float* __restrict__ dx,
-                                                                       double* __restrict__ stats, int64_t rows,
-                                                                       int64_t dim, double eps) {
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (r >= rows) return;
-    const float* xr = x + r * dim;
-    const float* dyr = dy + r * dim;
-    double mean, inv_std;
-    row_moments(xr, dim, eps, &mean, &inv_std);
-    stats[2 * r] = mean;
-    stats[2 * r + 1] = inv_std;
+__global__ __launch_bounds__(64) void layer_norm_backward_rows_kernel(const float* __restrict__ x,
+                                                                      const float* __restrict__ w,
+                                                                      const float* __restrict__ dy,
+                                                                      float* __restrict__ dx,
+                                                                      double* __restrict__ stats, int64_t rows,
+                                                                      int64_t dim, double eps) {
+    __shared__ LnTiles<true> t;
+    const int lane = static_cast<int>(threadIdx.x);
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kLnRows;
+    double mean = 0.0, inv_std = 0.0;
+    ln_moments<true>(t, x, dy, w, r0, rows, dim, eps, lane, &mean, &inv_std);
+    if (lane < kLnRows && r0 + lane < rows) {
+        stats[2 * (r0 + lane)] = mean;
+        stats[2 * (r0 + lane) + 1] = inv_std;
+    }
     if (!dx) return;
     double g_sum = 0.0, gx_sum = 0.0;
-    for (int64_t i = 0; i < dim; ++i) {
-        const double xhat = (static_cast<double>(xr[i]) - mean) * inv_std;
-        const double g = static_cast<double>(w[i]) * static_cast<double>(dyr[i]);
-        g_sum += g;
-        gx_sum += g * xhat;
-    }
+    ln_pass<true>(
+        t, x, dy, w, nullptr, r0, rows, dim, lane,
+        [&](int64_t, int n) {
+            for (int j = 0; j < n; ++j) {
+                const double xhat = (static_cast<double>(t.x[lane][j]) - mean) * inv_std;
+                const double g = static_cast<double>(t.w[j]) * static_cast<double>(t.dy[lane][j]);
+                g_sum += g;
+                gx_sum += g * xhat;
+            }
+        },
+        [](int64_t, int) {});
     const double g_mean = g_sum / static_cast<double>(dim);
     const double gx_mean = gx_sum / static_cast<double>(dim);
-    for (int64_t i = 0; i < dim; ++i) {
-        const double xhat = (static_cast<double>(xr[i]) - mean) * inv_std;
-        const double g = static_cast<double>(w[i]) * static_cast<double>(dyr[i]);
-        dx[r * dim + i] = static_cast<float>(inv_std * (g - g_mean - xhat * gx_mean));
+    ln_pass<true>(
+        t, x, dy, w, nullptr, r0, rows, dim, lane,
+        [&](int64_t, int n) {
+            for (int j = 0; j < n; ++j) {
+                const double xhat = (static_cast<double>(t.x[lane][j]) - mean) * inv_std;
+                const double g = static_cast<double>(t.w[j]) * static_cast<double>(t.dy[lane][j]);
+                t.x[lane][j] = static_cast<float>(inv_std * (g - g_mean - xhat * gx_mean));
+            }
+        },
+        [&](int64_t c0, int n) { ln_store<true>(t, dx, r0, c0, n, rows, dim, lane); });
+}
+
+// The column part: dw_i = sum over rows ascending of dy xhat, db_i = sum of dy. A chain has one term per row, so the
+// kernel is bound by how many rows' loads are in flight: a 1024-thread workgroup takes 16 columns, thread t holds row
+// slot t / 16 of each 64-row chunk for column t % 16, with kLnColDepth chunks loaded ahead in registers. Each
+// chunk's terms dy xhat (double) and dy go to LDS, and lanes 0-15 of wave 0 add the previous chunk's onto the chains
+// in row order; two LDS buffers.
+constexpr int kLnColRows = 64;
+constexpr int kLnColWidth = 16;
+constexpr int kLnColDepth = 8;
+
+__global__ __launch_bounds__(1024) void layer_norm_backward_cols_kernel(const float* __restrict__ x,
+                                                                        const float* __restrict__ dy,
+                                                                        const double* __restrict__ stats,
+                                                                        float* __restrict__ dw, float* __restrict__ db,
+                                                                        int64_t rows, int64_t dim) {
+    __shared__ double terms[2][kLnColRows][kLnColWidth];
+    __shared__ float dys[2][kLnColRows][kLnColWidth];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int c16 = tid % kLnColWidth, slot = tid / kLnColWidth;
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * kLnColWidth + c16;
+    const bool in_col = col < dim;
+    const int64_t chunks = (rows + kLnColRows - 1) / kLnColRows;
+    double dw_acc = 0.0, db_acc = 0.0;
+    float xv[kLnColDepth], dv[kLnColDepth];
+    double mv[kLnColDepth], sv[kLnColDepth];
+    // loads at clamped addresses, unconditionally (the counter waits then cover exactly the older slots); terms of
+    // rows or columns past the end are formed but never added or stored
+    const int64_t col_c = in_col ? col : dim - 1;
+    const auto fetch = [&](int64_t c, int k) {
+        const int64_t r = c * kLnColRows + slot < rows ? c * kLnColRows + slot : rows - 1;
+        xv[k] = x[r * dim + col_c];
+        dv[k] = dy[r * dim + col_c];
+        mv[k] = stats[2 * r];
+        sv[k] = stats[2 * r + 1];
+    };
+#pragma unroll
+    for (int k = 0; k < kLnColDepth; ++k) fetch(k < chunks ? k : chunks - 1, k);
+    for (int64_t c0 = 0; c0 <= chunks; c0 += kLnColDepth) {
+#pragma unroll
+        for (int k = 0; k < kLnColDepth; ++k) {
+            const int64_t c = c0 + k;
+            if (c > chunks) break;
+            const int buf = static_cast<int>(c & 1);
+            const double xhat = (static_cast<double>(xv[k]) - mv[k]) * sv[k];
+            terms[buf][slot][c16] = static_cast<double>(dv[k]) * xhat;
+            dys[buf][slot][c16] = dv[k];
+            fetch(c + kLnColDepth < chunks ? c + kLnColDepth : chunks - 1, k);
+            if (c > 0 && tid < kLnColWidth) {
+                const int pbuf = buf ^ 1;
+                const int64_t r0 = (c - 1) * kLnColRows;
+                const int n = rows - r0 < kLnColRows ? static_cast<int>(rows - r0) : kLnColRows;
+                // straight-line (no inner loop, so the compiler's load-counter waits stay exact); rows past the
+                // end are skipped by selects
+#pragma unroll
+                for (int rr = 0; rr < kLnColRows; ++rr) {
+                    const double t = dw_acc + terms[pbuf][rr][tid];
+                    const double d = db_acc + static_cast<double>(dys[pbuf][rr][tid]);
+                    dw_acc = rr < n ? t : dw_acc;
+                    db_acc = rr < n ? d : db_acc;
+                }
+            }
+            lds_barrier();
+        }
+    }
+    if (tid < kLnColWidth && in_col) {
+        if (dw) dw[col] = static_cast<float>(dw_acc);
+        if (db) db[col] = static_cast<float>(db_acc);
     }
 }
 
-// The column part: dw_i = sum over rows ascending of dy xhat, db_i = sum of dy.
-__global__ __launch_bounds__(256) void layer_norm_backward_cols_kernel(const float* __restrict__ x,
-                                                                       const float* __restrict__ dy,
-                                                                       const double* __restrict__ stats,
-                                                                       float* __restrict__ dw, float* __restrict__ db,
-                                                                       int64_t rows, int64_t dim) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= dim) return;
-    double dw_acc = 0.0, db_acc = 0.0;
-    for (int64_t r = 0; r < rows; ++r) {
-        const double xhat = (static_cast<double>(x[r * dim + i]) - stats[2 * r]) * stats[2 * r + 1];
-        const double d = static_cast<double>(dy[r * dim + i]);
-        dw_acc += d * xhat;
-        db_acc += d;
+// The same column sums with the raw chunks copied straight to LDS (global_load_lds_dwordx4) kLnColRing chunks
+// ahead, so the copies in flight are tracked by explicit counter waits rather than by registers (dim % 4 == 0 and
+// 16-byte aligned x, dy). Waves 0-3 copy x (16 rows each, 4 lanes per row), waves 4-7 dy, wave 8 the rows' (mean,
+// inv_std): one copy per wave per chunk, so "at most kLnColRing - 2 newer copies pending" means this chunk landed.
+constexpr int kLnColRing = 8;
+
+struct LnColSlot {
+    float x[kLnColRows][kLnColWidth];
+    float dy[kLnColRows][kLnColWidth];
+    double st[kLnColRows][2];
+};
+
+__global__ __launch_bounds__(1024) void layer_norm_backward_cols_lds_kernel(const float* __restrict__ x,
+                                                                            const float* __restrict__ dy,
+                                                                            const double* __restrict__ stats,
+                                                                            float* __restrict__ dw,
+                                                                            float* __restrict__ db, int64_t rows,
+                                                                            int64_t dim) {
+    __shared__ __align__(16) LnColSlot ring[kLnColRing];
+    // [buffer][row][column]: dy xhat in columns 0-15, f64(dy) in 16-31 (lane l < 32 runs chain l)
+    __shared__ double terms[2][kLnColRows][2 * kLnColWidth];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid >> 6, lane = tid & 63;
+    const int c16 = tid % kLnColWidth, slot = tid / kLnColWidth;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kLnColWidth;
+    const int64_t chunks = (rows + kLnColRows - 1) / kLnColRows;
+    // this wave's copy: row (clamped) and 4-column group (clamped) of the chunk
+    const auto issue = [&](int64_t c) {
+        if (wave > 8) return;
+        const int64_t cc = c < chunks ? c : chunks - 1;
+        LnColSlot& dst = ring[cc % kLnColRing];
+        if (wave < 8) {
+            const int rr = 16 * (wave & 3) + lane / 4;
+            const int64_t r = cc * kLnColRows + rr < rows ? cc * kLnColRows + rr : rows - 1;
+            const int64_t g = col0 + 4 * (lane & 3) < dim ? col0 + 4 * (lane & 3) : dim - 4;
+            const float* src = (wave < 4 ? x : dy) + r * dim + g;
+            copy16_to_lds(src, wave < 4 ? &dst.x[16 * (wave & 3)][0] : &dst.dy[16 * (wave & 3)][0]);
+        } else {
+            const int64_t r = cc * kLnColRows + lane < rows ? cc * kLnColRows + lane : rows - 1;
+            copy16_to_lds(stats + 2 * r, &dst.st[0][0]);
+        }
+    };
+    for (int k = 0; k < kLnColRing - 1; ++k) issue(k);
+    double acc = 0.0;  // lane l < 16: dw of column l; 16 <= l < 32: db of column l - 16
+    for (int64_t c = 0; c <= chunks; ++c) {
+        // chunk c landed (kLnColRing - 2 newer copies may be pending), the previous chunk's terms are written, and
+        // every wave is done reading the ring slot the next copy refills
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kLnColRing - 2) : "memory");
+        issue(c + kLnColRing - 1);
+        const LnColSlot& src = ring[(c < chunks ? c : chunks - 1) % kLnColRing];
+        const double xhat = (static_cast<double>(src.x[slot][c16]) - src.st[slot][0]) * src.st[slot][1];
+        const int buf = static_cast<int>(c & 1);
+        terms[buf][slot][c16] = static_cast<double>(src.dy[slot][c16]) * xhat;
+        terms[buf][slot][kLnColWidth + c16] = static_cast<double>(src.dy[slot][c16]);
+        if (c > 0 && tid < 2 * kLnColWidth) {
+            const int pbuf = buf ^ 1;
+            const int64_t r0 = (c - 1) * kLnColRows;
+            const int n = rows - r0 < kLnColRows ? static_cast<int>(rows - r0) : kLnColRows;
+            if (n == kLnColRows) {
+#pragma unroll
+                for (int rr = 0; rr < kLnColRows; ++rr) acc += terms[pbuf][rr][tid];
+            } else {
+                for (int rr = 0; rr < n; ++rr) acc += terms[pbuf][rr][tid];
+            }
+        }
     }
-    if (dw) dw[i] = static_cast<float>(dw_acc);
-    if (db) db[i] = static_cast<float>(db_acc);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the end drain before exit
+    if (tid < kLnColWidth && col0 + tid < dim && dw) dw[col0 + tid] = static_cast<float>(acc);
+    if (tid >= kLnColWidth && tid < 2 * kLnColWidth && col0 + tid - kLnColWidth < dim && db)
+        db[col0 + tid - kLnColWidth] = static_cast<float>(acc);
 }
 
 struct BiasedShape {
@@ -281,7 +507,7 @@ int dllm_hip_layer_norm(const float* x, const float* w, const float* b, float* o
                         double eps, void* stream) {
     if (rows == 0 || dim == 0) return kOk;
     DLLM_REQUIRE(x && w && b && out, "null argument");
-    hipLaunchKernelGGL(layer_norm_kernel, dim3(blocks_for(static_cast<int64_t>(rows), 256)), dim3(256), 0,
+    hipLaunchKernelGGL(layer_norm_kernel, dim3(blocks_for(static_cast<int64_t>(rows), kLnRows)), dim3(64), 0,
                        static_cast<hipStream_t>(stream), x, w, b, out, static_cast<int64_t>(rows),
                        static_cast<int64_t>(dim), eps);
     return check_launch("layer_norm");
@@ -303,12 +529,15 @@ int dllm_hip_layer_norm_backward(const float* x, const float* w, const float* dy
     }
     DLLM_REQUIRE(x && w && dy && workspace, "null argument");
     double* stats = static_cast<double*>(workspace);
-    hipLaunchKernelGGL(layer_norm_backward_rows_kernel, dim3(blocks_for(static_cast<int64_t>(rows), 256)), dim3(256),
-                       0, s, x, w, dy, dx, stats, static_cast<int64_t>(rows), static_cast<int64_t>(dim), eps);
+    hipLaunchKernelGGL(layer_norm_backward_rows_kernel, dim3(blocks_for(static_cast<int64_t>(rows), kLnRows)),
+                       dim3(64), 0, s, x, w, dy, dx, stats, static_cast<int64_t>(rows), static_cast<int64_t>(dim), eps);
     DLLM_TRY(check_launch("layer_norm_backward rows"));
     if (!dw && !db) return kOk;
-    hipLaunchKernelGGL(layer_norm_backward_cols_kernel, dim3(blocks_for(static_cast<int64_t>(dim), 256)), dim3(256),
-                       0, s, x, dy, stats, dw, db, static_cast<int64_t>(rows), static_cast<int64_t>(dim));
+    const bool aligned = dim % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(dy) % 16 == 0;
+    hipLaunchKernelGGL(aligned ? layer_norm_backward_cols_lds_kernel : layer_norm_backward_cols_kernel,
+                       dim3(blocks_for(static_cast<int64_t>(dim), kLnColWidth)), dim3(1024), 0, s, x, dy, stats, dw,
+                       db, static_cast<int64_t>(rows), static_cast<int64_t>(dim));
     return check_launch("layer_norm_backward columns");
 }
 

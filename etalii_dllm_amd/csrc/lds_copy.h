@@ -30,4 +30,9 @@ __device__ __forceinline__ void copy16_to_lds_s(const void* sbase, uint32_t voff
     asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u), "{m0}"(m0) : "memory");
 }
 
+// A workgroup barrier for LDS staged from registers: this wave's LDS writes complete (lgkmcnt), then s_barrier.
+// Unlike __syncthreads(), whose release fence also waits for every outstanding global load, it leaves the loads of
+// a register prefetch in flight across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 }  // namespace dllm_hip

@@ -13,6 +13,7 @@
 #include "common.h"
 #include "dllm_hip.h"
 #include "kernels.h"
+#include "lds_copy.h"
 
 namespace dllm_hip {
 
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(256) void linear_q8_kernel(const int8_t* __restrict
     Q8Stage st;
     q8_load_stage(st, xq, xs, wq, ws, i0, n0, rows, K, N, 0, tid);
     for (int64_t b0 = 0; b0 < blocks; b0 += kStageBlocks) {
-        __syncthreads();  // the previous stage's reads are done
+        lds_barrier();  // the previous stage's reads are done
         for (int h = 0; h < 2; ++h) {
             const int c = tid + 256 * h;
             const int off = (c >> 3) * kLdsRow + (c & 7) * 16;
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(256) void linear_q8_kernel(const int8_t* __restrict
         }
         xs_lds[tid >> 2][tid & 3] = static_cast<double>(st.xs);
         ws_lds[tid >> 2][tid & 3] = static_cast<double>(st.ws);
-        __syncthreads();
+        lds_barrier();
         if (b0 + kStageBlocks < blocks) q8_load_stage(st, xq, xs, wq, ws, i0, n0, rows, K, N, b0 + kStageBlocks, tid);
         const auto compute = [&](int blk) {
             long a[2], b[2];

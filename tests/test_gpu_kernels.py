@@ -347,7 +347,8 @@ def test_gelu_and_backward_match_the_oracle(K):
     assert_same_or_nan(K.gelu_backward(x, dy), enc.gelu_backward(x, dy), "gelu_backward")
 
 
-@pytest.mark.parametrize(("rows", "dim"), [(1, 1), (3, 7), (37, 64), (130, 768), (5, 1031)])
+@pytest.mark.parametrize(("rows", "dim"),
+                         [(1, 1), (3, 7), (37, 64), (130, 768), (5, 1031), (70, 20), (1, 4), (300, 1028)])
 def test_layer_norm_and_backward_match_the_oracle(K, rows, dim):
     """LayerNorm forward and backward (kernels.cpp:612-625, 858-875), bit for bit."""
     x, w, b, dy = O.gaussian(21, rows, dim), O.gaussian(22, dim), O.gaussian(23, dim), O.gaussian(24, rows, dim)
