@@ -17,8 +17,14 @@ namespace dllm_hip {
 
 namespace {
 
-// The keys query t sees (causal, q_offset 0, optional window): [lo, hi).
-__device__ __forceinline__ void query_span(int64_t t, int64_t window, int64_t* lo, int64_t* hi) {
+// The keys query t of a window of n sees: causal with q_offset 0 and an optional sliding window, or every key when
+// window is kAllKeys: [lo, hi).
+__device__ __forceinline__ void query_span(int64_t t, int64_t n, int64_t window, int64_t* lo, int64_t* hi) {
+    if (window < 0) {
+        *lo = 0;
+        *hi = n;
+        return;
+    }
     *hi = t + 1;
     *lo = window != 0 && t + 1 > window ? t + 1 - window : 0;
 }
@@ -42,7 +48,7 @@ __global__ __launch_bounds__(64) void softmax_max_kernel(const double* __restric
     if (t >= n) return;
     const double* s = st + z * zstride + t;
     int64_t lo, hi;
-    query_span(t, window, &lo, &hi);
+    query_span(t, n, window, &lo, &hi);
     double mx = s[lo * ld];
     int64_t j = lo + 1;
     for (; j + kChainUnroll <= hi; j += kChainUnroll) {
@@ -70,9 +76,9 @@ __global__ __launch_bounds__(256) void softmax_exp_kernel(double* __restrict__ s
     const int64_t n = seg[w + 1] - seg[w];
     const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     const int64_t j0 = static_cast<int64_t>(blockIdx.y) * 8;
-    if (t >= n || j0 > t) return;
+    if (t >= n || (window >= 0 && j0 > t)) return;
     int64_t lo, hi;
-    query_span(t, window, &lo, &hi);
+    query_span(t, n, window, &lo, &hi);
     const double m = mx[z * mx_zstride + t];
     double* s = st + z * zstride + t;
 #pragma unroll
@@ -93,7 +99,7 @@ __global__ __launch_bounds__(64) void softmax_total_kernel(const double* __restr
     if (t >= n) return;
     const double* s = st + z * zstride + t;
     int64_t lo, hi;
-    query_span(t, window, &lo, &hi);
+    query_span(t, n, window, &lo, &hi);
     double total = 0.0;
     int64_t j = lo;
     for (; j + kChainUnroll <= hi; j += kChainUnroll) {
@@ -124,7 +130,7 @@ __global__ __launch_bounds__(64) void dsoftmax_dot_kernel(const double* __restri
     const double* d = dpt + z * zstride + t;
     const double iv = inv[z * inv_zstride + t];
     int64_t lo, hi;
-    query_span(t, window, &lo, &hi);
+    query_span(t, n, window, &lo, &hi);
     double weighted = 0.0;
     int64_t j = lo;
     for (; j + kChainUnroll <= hi; j += kChainUnroll) {
@@ -155,15 +161,15 @@ __global__ __launch_bounds__(256) void dsoftmax_apply_regroup_kernel(
     const int64_t g = h / group, hh = h % group;
     const int64_t n = seg[w + 1] - seg[w];
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64, j0 = static_cast<int64_t>(blockIdx.y) * kJ;
-    if (t0 >= n || j0 >= n || j0 > t0 + 63) return;
+    if (t0 >= n || j0 >= n || (window >= 0 && j0 > t0 + 63)) return;
     int64_t lo0, hi0;
-    query_span(t0, window, &lo0, &hi0);
+    query_span(t0, n, window, &lo0, &hi0);
     if (j0 + kJ - 1 < lo0) return;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     {
         const int64_t t = t0 + tx;
         int64_t lo = 0, hi = 0;
-        if (t < n) query_span(t, window, &lo, &hi);
+        if (t < n) query_span(t, n, window, &lo, &hi);
         const double iv = t < n ? inv[z * inv_zstride + t] : 0.0;
         const double D = t < n ? dvec[z * inv_zstride + t] : 0.0;
         const double* e = et + z * zstride + t;
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(256) void dsoftmax_apply_regroup_kernel(
         const int64_t t = t0 + tr + 8 * k, j = j0 + jx;
         if (t >= n) break;
         int64_t lo, hi;
-        query_span(t, window, &lo, &hi);
+        query_span(t, n, window, &lo, &hi);
         if (j >= lo && j < hi) {
             const int64_t at = row0 + (t * group + hh) * dst_ld + j;
             pg[at] = tp[jx][tr + 8 * k];

@@ -6,6 +6,9 @@
 
 namespace dllm_hip {
 
+// The `window` of the chain launchers that makes every key visible to every query (no causal mask).
+constexpr int64_t kAllKeys = -1;
+
 enum AttnMask {
     kMaskNone = 0,
     kMaskQueryRows = 1,   // rows are queries t; reduce over the keys t sees, ascending

@@ -11,6 +11,7 @@
 //   maximum, the exponentials' total and D = sum p dp are one lane's scans over the keys in order; dq and the
 //   forward's value sums are one lane per output column, keys ascending. dk[j, h] and dv[j, h] sum over queries t
 //   ascending, one lane per output element, from the probabilities and ds saved per (t, h).
+#include "attn_step.h"
 #include "common.h"
 #include "devmath.h"
 #include "dllm_hip.h"
@@ -477,7 +478,265 @@ __global__ __launch_bounds__(256) void biased_attention_backward_kv_kernel(
     }
 }
 
+// biased_attention_weights (interp.hpp:79-121) on the per-(query, head) path: f32(e_j (1 / total)).
+__global__ __launch_bounds__(64) void biased_weights_rows_kernel(const float* __restrict__ q,
+                                                                 const float* __restrict__ k,
+                                                                 const float* __restrict__ bias,
+                                                                 float* __restrict__ out, double* __restrict__ scratch,
+                                                                 BiasedShape s) {
+    __shared__ double shared[2];
+    const int64_t row = blockIdx.x;
+    const int64_t t = row / s.heads, h = row % s.heads;
+    const int lane = static_cast<int>(threadIdx.x);
+    double* e = scratch + row * s.kv_len;
+    const double inv = biased_probabilities(q + row * s.hd, k, bias + (h * s.q_len + t) * s.kv_len, s, h, e, shared,
+                                            lane);
+    for (int64_t j = lane; j < s.kv_len; j += 64) out[row * s.kv_len + j] = static_cast<float>(e[j] * inv);
+}
+
+// ---- the matrix-core path for self-attention shapes (q_len == kv_len = n, head_dim and value_dim multiples of 4) --
+// Per head, as the training step's attention lays it out: S^T[j][t] = sum_i k[j][i] q[t][i] (FP64 matrix cores,
+// exact products), then s = (S^T + bias[h][t][j]) scale, the softmax chains per query over every key, and the value,
+// dq, dk and dv sums as multiply-then-add tiles over keys (or queries) ascending: the reference's orders.
+
+__global__ void biased_seg_kernel(int64_t* seg, int64_t n) {
+    if (threadIdx.x == 0) {
+        seg[0] = 0;
+        seg[1] = n;
+    }
+}
+
+// et[h][j][t] = (et[h][j][t] + bias[h][t][j]) scale for j, t < n; a 64 x 64 tile through LDS so the bias is read
+// along j and the scores along t.
+__global__ __launch_bounds__(256) void biased_scores_kernel(double* __restrict__ et, const float* __restrict__ bias,
+                                                            int64_t n, int64_t Tp, double scale) {
+    __shared__ float tile[64][65];
+    const int64_t h = blockIdx.z;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64, j0 = static_cast<int64_t>(blockIdx.y) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const float* bh = bias + h * n * n;
+    for (int k = ty; k < 64; k += 4) {
+        const int64_t t = t0 + k, j = j0 + tx;
+        tile[k][tx] = (t < n && j < n) ? bh[t * n + j] : 0.0f;
+    }
+    __syncthreads();
+    double* eh = et + h * Tp * Tp;
+    for (int k = ty; k < 64; k += 4) {
+        const int64_t j = j0 + k, t = t0 + tx;
+        if (j < n && t < n) eh[j * Tp + t] = (eh[j * Tp + t] + static_cast<double>(tile[tx][k])) * scale;
+    }
+}
+
+// out[t][h][j] = f32(e[h][j][t] inv[h][t]) (biased_attention_weights), transposed through LDS.
+__global__ __launch_bounds__(256) void biased_weights_kernel(const double* __restrict__ et,
+                                                             const double* __restrict__ inv, float* __restrict__ out,
+                                                             int64_t n, int64_t Tp, int64_t heads) {
+    __shared__ float tile[64][65];
+    const int64_t h = blockIdx.z;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64, j0 = static_cast<int64_t>(blockIdx.y) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const double* eh = et + h * Tp * Tp;
+    const double iv = t0 + tx < n ? inv[h * Tp + t0 + tx] : 0.0;
+    for (int k = ty; k < 64; k += 4) {
+        const int64_t j = j0 + k, t = t0 + tx;
+        tile[k][tx] = (j < n && t < n) ? static_cast<float>(eh[j * Tp + t] * iv) : 0.0f;
+    }
+    __syncthreads();
+    for (int k = ty; k < 64; k += 4) {
+        const int64_t t = t0 + k, j = j0 + tx;
+        if (t < n && j < n) out[(t * heads + h) * n + j] = tile[tx][k];
+    }
+}
+
+// dbias[h][t][j] = f32(ds[h][t][j]) from the key-row layout the softmax backward writes.
+__global__ __launch_bounds__(256) void biased_dbias_kernel(const double* __restrict__ dsg, float* __restrict__ dbias,
+                                                           int64_t n, int64_t Tp) {
+    const int64_t h = blockIdx.z, t = blockIdx.y;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (j < n) dbias[(h * n + t) * n + j] = static_cast<float>(dsg[h * Tp * Tp + t * Tp + j]);
+}
+
 unsigned blocks_for(int64_t n, int per) { return static_cast<unsigned>(ceil_div(static_cast<size_t>(n), per)); }
+
+
+// Workspace of the matrix-core path: [seg | q^T | E^T | inv] for the forward and the weights, then
+// [dout^T | dP^T | D | p | ds] for the backward.
+struct BiasedLayout {
+    int64_t n = 0, Tp = 0, heads = 0, hd = 0, vd = 0;
+    size_t seg = 0, qt = 0, et = 0, inv = 0, forward = 0;
+    size_t dot = 0, dpt = 0, dvec = 0, pg = 0, dsg = 0, backward = 0;
+};
+
+bool biased_fast(size_t q_len, size_t kv_len, size_t heads, size_t hd, size_t vd) {
+    return q_len == kv_len && q_len > 0 && q_len <= 65535 && heads > 0 && hd > 0 && vd > 0 && hd % 4 == 0 &&
+           vd % 4 == 0;
+}
+
+BiasedLayout biased_layout(size_t n, size_t heads, size_t hd, size_t vd) {
+    BiasedLayout L;
+    L.n = static_cast<int64_t>(n);
+    L.Tp = static_cast<int64_t>(round_up(n, 64));
+    L.heads = static_cast<int64_t>(heads);
+    L.hd = static_cast<int64_t>(hd);
+    L.vd = static_cast<int64_t>(vd);
+    const size_t Tp = static_cast<size_t>(L.Tp), sq = heads * Tp * Tp * sizeof(double);
+    size_t off = 0;
+    const auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += round_up(bytes, 256);
+        return at;
+    };
+    L.seg = take(2 * sizeof(int64_t));
+    L.qt = take(heads * hd * Tp * sizeof(float));
+    L.et = take(sq);
+    L.inv = take(heads * Tp * sizeof(double));
+    L.forward = off;
+    L.dot = take(heads * vd * Tp * sizeof(float));
+    L.dpt = take(sq);
+    L.dvec = take(heads * Tp * sizeof(double));
+    L.pg = take(sq);
+    L.dsg = take(sq);
+    L.backward = off;
+    return L;
+}
+
+template <typename T>
+T* at(void* ws, size_t off) {
+    return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+AttnTileCall biased_call(const BiasedLayout& L, const int64_t* seg) {
+    AttnTileCall c;
+    c.seg = seg;
+    c.windows = 1;
+    c.heads = L.heads;
+    c.max_len = L.n;
+    c.group = 1;
+    c.window = 0;
+    c.mask = kMaskNone;
+    return c;
+}
+
+// rows of one head in a [length][heads][dim] tensor
+AttnOperand head_rows(const float* p, int64_t heads, int64_t dim) {
+    return AttnOperand{p, 0, heads * dim, dim, 1, heads * dim, 0, 1};
+}
+
+// [head][Tp][Tp] or [head][dim][Tp] blocks
+AttnOperand head_block(const void* p, int64_t rows, int64_t Tp, int64_t heads) {
+    return AttnOperand{p, heads * rows * Tp, 0, rows * Tp, 1, Tp, 0, 1};
+}
+
+// S^T, the biased scores, E^T and inv of every head (the forward's probabilities)
+int biased_probabilities_fast(const float* q, const float* k, const float* bias, const BiasedLayout& L, double scale,
+                              void* ws, hipStream_t s) {
+    int64_t* seg = at<int64_t>(ws, L.seg);
+    float* qt = at<float>(ws, L.qt);
+    double* et = at<double>(ws, L.et);
+    hipLaunchKernelGGL(biased_seg_kernel, dim3(1), dim3(64), 0, s, seg, L.n);
+    DLLM_TRY(launch_heads_transpose(q, L.heads * L.hd, L.hd, qt, false, L.Tp, L.hd * L.Tp, seg, 1, L.heads, L.n, s));
+    AttnTileCall g = biased_call(L, seg);
+    g.A = head_rows(k, L.heads, L.hd);
+    g.a_float = true;
+    g.a_row_alloc = L.hd;
+    g.B = head_block(qt, L.hd, L.Tp, L.heads);
+    g.C = head_block(et, L.Tp, L.Tp, L.heads);
+    g.head_dim = L.hd;
+    g.rows_kind = 0;
+    g.cols_kind = 0;
+    g.L = L.hd;
+    g.cols_per_lane = 4;
+    g.b_row_alloc = L.Tp;
+    g.exact_products = true;
+    g.out_double = true;
+    g.out_scale = 1.0;
+    DLLM_TRY(launch_attn_tiles(g, s));
+    const unsigned tiles = static_cast<unsigned>(ceil_div(static_cast<size_t>(L.n), 64));
+    hipLaunchKernelGGL(biased_scores_kernel, dim3(tiles, tiles, static_cast<unsigned>(L.heads)), dim3(256), 0, s, et,
+                       bias, L.n, L.Tp, scale);
+    DLLM_TRY(check_launch("biased scores"));
+    return launch_softmax_rows(et, L.Tp, L.Tp * L.Tp, seg, 1, L.heads, L.n, kAllKeys, at<double>(ws, L.inv), L.Tp, s);
+}
+
+// C[i] = sum over l < n ascending of A[l][i] B[l] (multiply, then add), float output, optional row scale
+AttnTileCall biased_sum(const BiasedLayout& L, const int64_t* seg, const double* A, const float* B, int64_t b_dim,
+                        float* C, const double* rowscale) {
+    AttnTileCall c = biased_call(L, seg);
+    c.A = head_block(A, L.Tp, L.Tp, L.heads);
+    c.B = head_rows(B, L.heads, b_dim);
+    c.C = head_rows(C, L.heads, b_dim);
+    c.head_dim = b_dim;
+    c.rows_kind = 0;
+    c.cols_kind = 1;
+    c.L = L.n;
+    c.cols_per_lane = b_dim > 64 ? 2 : 1;
+    c.exact_products = false;
+    c.out_double = false;
+    c.rowscale = rowscale;
+    c.rowscale_zstride = rowscale ? L.Tp : 0;
+    return c;
+}
+
+int biased_forward_fast(const float* q, const float* k, const float* v, const float* bias, float* out,
+                        const BiasedLayout& L, double scale, void* ws, hipStream_t s) {
+    DLLM_TRY(biased_probabilities_fast(q, k, bias, L, scale, ws, s));
+    return launch_attn_tiles(biased_sum(L, at<int64_t>(ws, L.seg), at<double>(ws, L.et), v, L.vd, out,
+                                        at<double>(ws, L.inv)),
+                             s);
+}
+
+int biased_backward_fast(const float* q, const float* k, const float* v, const float* bias, const float* dout,
+                         float* dq, float* dk, float* dv, float* dbias, const BiasedLayout& L, double scale, void* ws,
+                         hipStream_t s) {
+    DLLM_TRY(biased_probabilities_fast(q, k, bias, L, scale, ws, s));
+    const int64_t* seg = at<int64_t>(ws, L.seg);
+    double* et = at<double>(ws, L.et);
+    double* dpt = at<double>(ws, L.dpt);
+    double* pg = at<double>(ws, L.pg);
+    double* dsg = at<double>(ws, L.dsg);
+    float* dot = at<float>(ws, L.dot);
+    DLLM_TRY(launch_heads_transpose(dout, L.heads * L.vd, L.vd, dot, false, L.Tp, L.vd * L.Tp, seg, 1, L.heads, L.n,
+                                    s));
+    // dP^T[j][t] = sum_i v[j][i] dout[t][i]
+    AttnTileCall g = biased_call(L, seg);
+    g.A = head_rows(v, L.heads, L.vd);
+    g.a_float = true;
+    g.a_row_alloc = L.vd;
+    g.B = head_block(dot, L.vd, L.Tp, L.heads);
+    g.C = head_block(dpt, L.Tp, L.Tp, L.heads);
+    g.head_dim = L.vd;
+    g.rows_kind = 0;
+    g.cols_kind = 0;
+    g.L = L.vd;
+    g.cols_per_lane = 4;
+    g.b_row_alloc = L.Tp;
+    g.exact_products = true;
+    g.out_double = true;
+    g.out_scale = 1.0;
+    DLLM_TRY(launch_attn_tiles(g, s));
+    // D, p = e inv, ds = p (dp - D) scale: ds over dP^T, p and ds as [h][t][j]
+    DLLM_TRY(launch_dsoftmax_regroup(et, dpt, L.Tp, L.Tp * L.Tp, seg, 1, L.heads, 1, L.n, kAllKeys,
+                                     at<double>(ws, L.inv), L.Tp, scale, at<double>(ws, L.dvec), pg, dsg, L.Tp,
+                                     L.Tp * L.Tp, s));
+    hipLaunchKernelGGL(biased_dbias_kernel,
+                       dim3(static_cast<unsigned>(ceil_div(static_cast<size_t>(L.n), 256)),
+                            static_cast<unsigned>(L.n), static_cast<unsigned>(L.heads)),
+                       dim3(256), 0, s, dsg, dbias, L.n, L.Tp);
+    DLLM_TRY(check_launch("biased dbias"));
+    // dq[t] = sum_j ds[t][j] k[j]; dk[j] = sum_t ds[t][j] q[t]; dv[j] = sum_t p[t][j] dout[t]
+    DLLM_TRY(launch_attn_tiles(biased_sum(L, seg, dpt, k, L.hd, dq, nullptr), s));
+    AttnTileCall kc = biased_sum(L, seg, dsg, q, L.hd, dk, nullptr);
+    AttnTileCall vc = biased_sum(L, seg, pg, dout, L.vd, dv, nullptr);
+    if (L.hd == L.vd) {
+        kc.second = true;
+        kc.A2 = vc.A;
+        kc.B2 = vc.B;
+        kc.C2 = vc.C;
+        return launch_attn_tiles(kc, s);
+    }
+    DLLM_TRY(launch_attn_tiles(kc, s));
+    return launch_attn_tiles(vc, s);
+}
 
 }  // namespace
 
@@ -541,40 +800,80 @@ int dllm_hip_layer_norm_backward(const float* x, const float* w, const float* dy
     return check_launch("layer_norm_backward columns");
 }
 
-size_t dllm_hip_biased_attention_workspace(size_t q_len, size_t kv_len, size_t heads) {
+size_t dllm_hip_biased_attention_workspace(size_t q_len, size_t kv_len, size_t heads, size_t head_dim,
+                                           size_t value_dim) {
+    if (biased_fast(q_len, kv_len, heads, head_dim, value_dim))
+        return biased_layout(q_len, heads, head_dim, value_dim).forward;
     return round_up(q_len * heads * kv_len * sizeof(double), 256);
 }
 
 int dllm_hip_biased_attention(const float* q, const float* k, const float* v, const float* bias, float* out,
                               size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
                               double scale, void* workspace, size_t workspace_bytes, void* stream) {
-    DLLM_REQUIRE(workspace_bytes >= dllm_hip_biased_attention_workspace(q_len, kv_len, heads),
+    DLLM_REQUIRE(workspace_bytes >= dllm_hip_biased_attention_workspace(q_len, kv_len, heads, head_dim, value_dim),
                  "workspace too small for biased_attention");
     if (q_len == 0 || heads == 0) return kOk;
     DLLM_REQUIRE(q && out && (kv_len == 0 || (k && v && bias && workspace)), "null argument");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (biased_fast(q_len, kv_len, heads, head_dim, value_dim))
+        return biased_forward_fast(q, k, v, bias, out, biased_layout(q_len, heads, head_dim, value_dim), scale,
+                                   workspace, st);
     const BiasedShape s{static_cast<int64_t>(q_len), static_cast<int64_t>(kv_len), static_cast<int64_t>(heads),
                         static_cast<int64_t>(head_dim), static_cast<int64_t>(value_dim), scale};
-    hipLaunchKernelGGL(biased_attention_kernel, dim3(static_cast<unsigned>(q_len * heads)), dim3(64), 0,
-                       static_cast<hipStream_t>(stream), q, k, v, bias, out, static_cast<double*>(workspace), s);
+    hipLaunchKernelGGL(biased_attention_kernel, dim3(static_cast<unsigned>(q_len * heads)), dim3(64), 0, st, q, k, v,
+                       bias, out, static_cast<double*>(workspace), s);
     return check_launch("biased_attention");
 }
 
-size_t dllm_hip_biased_attention_backward_workspace(size_t q_len, size_t kv_len, size_t heads) {
-    return 2 * dllm_hip_biased_attention_workspace(q_len, kv_len, heads);
+int dllm_hip_biased_attention_weights(const float* q, const float* k, const float* bias, float* out, size_t q_len,
+                                      size_t kv_len, size_t heads, size_t head_dim, double scale, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    // the forward's workspace with value_dim = 4 (the value sums are not formed)
+    DLLM_REQUIRE(workspace_bytes >= dllm_hip_biased_attention_workspace(q_len, kv_len, heads, head_dim, 4),
+                 "workspace too small for biased_attention_weights");
+    if (q_len == 0 || heads == 0 || kv_len == 0) return kOk;
+    DLLM_REQUIRE(q && k && bias && out && workspace, "null argument");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (biased_fast(q_len, kv_len, heads, head_dim, 4)) {
+        const BiasedLayout L = biased_layout(q_len, heads, head_dim, 4);
+        DLLM_TRY(biased_probabilities_fast(q, k, bias, L, scale, workspace, st));
+        const unsigned tiles = static_cast<unsigned>(ceil_div(q_len, 64));
+        hipLaunchKernelGGL(biased_weights_kernel, dim3(tiles, tiles, static_cast<unsigned>(heads)), dim3(256), 0, st,
+                           at<double>(workspace, L.et), at<double>(workspace, L.inv), out, L.n, L.Tp, L.heads);
+        return check_launch("biased_attention_weights");
+    }
+    const BiasedShape s{static_cast<int64_t>(q_len), static_cast<int64_t>(kv_len), static_cast<int64_t>(heads),
+                        static_cast<int64_t>(head_dim), 0, scale};
+    hipLaunchKernelGGL(biased_weights_rows_kernel, dim3(static_cast<unsigned>(q_len * heads)), dim3(64), 0, st, q, k,
+                       bias, out, static_cast<double*>(workspace), s);
+    return check_launch("biased_attention_weights");
+}
+
+size_t dllm_hip_biased_attention_backward_workspace(size_t q_len, size_t kv_len, size_t heads, size_t head_dim,
+                                                    size_t value_dim) {
+    if (biased_fast(q_len, kv_len, heads, head_dim, value_dim))
+        return biased_layout(q_len, heads, head_dim, value_dim).backward;
+    return 2 * round_up(q_len * heads * kv_len * sizeof(double), 256);
 }
 
 int dllm_hip_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
                                        const float* dout, float* dq, float* dk, float* dv, float* dbias,
                                        size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
                                        double scale, void* workspace, size_t workspace_bytes, void* stream) {
-    DLLM_REQUIRE(workspace_bytes >= dllm_hip_biased_attention_backward_workspace(q_len, kv_len, heads),
+    DLLM_REQUIRE(workspace_bytes >=
+                     dllm_hip_biased_attention_backward_workspace(q_len, kv_len, heads, head_dim, value_dim),
                  "workspace too small for biased_attention_backward");
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (biased_fast(q_len, kv_len, heads, head_dim, value_dim)) {
+        DLLM_REQUIRE(q && k && v && bias && dout && dq && dk && dv && dbias && workspace, "null argument");
+        return biased_backward_fast(q, k, v, bias, dout, dq, dk, dv, dbias,
+                                    biased_layout(q_len, heads, head_dim, value_dim), scale, workspace, st);
+    }
     const BiasedShape s{static_cast<int64_t>(q_len), static_cast<int64_t>(kv_len), static_cast<int64_t>(heads),
                         static_cast<int64_t>(head_dim), static_cast<int64_t>(value_dim), scale};
     double* p_save = static_cast<double*>(workspace);
     double* ds_save = reinterpret_cast<double*>(static_cast<char*>(workspace) +
-                                                dllm_hip_biased_attention_workspace(q_len, kv_len, heads));
+                                                round_up(q_len * heads * kv_len * sizeof(double), 256));
     if (q_len > 0 && heads > 0) {
         DLLM_REQUIRE(q && dout && dq && (kv_len == 0 || (k && v && bias && dbias && workspace)), "null argument");
         hipLaunchKernelGGL(biased_attention_backward_rows_kernel, dim3(static_cast<unsigned>(q_len * heads)), dim3(64),

@@ -553,7 +553,8 @@ lib.dllm_hip_layer_norm_backward_workspace.argtypes = [_sz]
 lib.dllm_hip_layer_norm_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, C.c_double, _vp, _sz, _vp]
 for _name in ("biased_attention", "biased_attention_backward"):
     getattr(lib, f"dllm_hip_{_name}_workspace").restype = _sz
-    getattr(lib, f"dllm_hip_{_name}_workspace").argtypes = [_sz, _sz, _sz]
+    getattr(lib, f"dllm_hip_{_name}_workspace").argtypes = [_sz] * 5
+lib.dllm_hip_biased_attention_weights.argtypes = [_vp] * 4 + [_sz] * 4 + [C.c_double, _vp, _sz, _vp]
 lib.dllm_hip_biased_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, C.c_double, _vp, _sz, _vp]
 lib.dllm_hip_biased_attention_backward.argtypes = [_vp] * 9 + [_sz] * 5 + [C.c_double, _vp, _sz, _vp]
 
@@ -627,12 +628,32 @@ def biased_attention(q, k, v, bias, scale) -> np.ndarray:
     """kernels.cpp:707-727: T5 attention with an additive bias [heads, q_len, kv_len]."""
     q, k, v, bias = _f32(q), _f32(k), _f32(v), _f32(bias)
     q_len, kv_len, heads, hd, vd = _biased_shapes(q, k, v, bias)
-    ws = Device(lib.dllm_hip_biased_attention_workspace(q_len, kv_len, heads))
+    ws = Device(lib.dllm_hip_biased_attention_workspace(q_len, kv_len, heads, hd, vd))
     dq, dk, dv, db = Device.of(q), Device.of(k), Device.of(v), Device.of(bias)
     out = Device(q_len * heads * vd * 4)
     check(lib.dllm_hip_biased_attention(dq.ptr, dk.ptr, dv.ptr, db.ptr, out.ptr, q_len, kv_len, heads, hd, vd, scale,
                                         ws.ptr, ws.nbytes, None))
     return out.download((q_len, heads, vd))
+
+
+def biased_attention_weights(q, k, bias, scale) -> np.ndarray:
+    """kernels.cpp:753-773: the probabilities [q_len, heads, kv_len] of biased_attention()."""
+    q, k, bias = _f32(q), _f32(k), _f32(bias)
+    if q.ndim != 3 or k.ndim != 3:
+        raise ValueError("q and k must be [length, heads, dim]")
+    q_len, heads, hd, kv_len = q.shape[0], q.shape[1], q.shape[2], k.shape[0]
+    if k.shape[1] != heads:
+        raise ValueError("q and k must have the same heads")
+    if k.shape[2] != hd:
+        raise ValueError("q and k must have the same head_dim")
+    if bias.shape != (heads, q_len, kv_len):
+        raise ValueError("bias must be [heads, q_len, kv_len]")
+    ws = Device(lib.dllm_hip_biased_attention_workspace(q_len, kv_len, heads, hd, 4))
+    dq, dk, db = Device.of(q), Device.of(k), Device.of(bias)
+    out = Device(q_len * heads * kv_len * 4)
+    check(lib.dllm_hip_biased_attention_weights(dq.ptr, dk.ptr, db.ptr, out.ptr, q_len, kv_len, heads, hd, scale,
+                                                ws.ptr, ws.nbytes, None))
+    return out.download((q_len, heads, kv_len))
 
 
 def biased_attention_backward(q, k, v, bias, dout, scale):
@@ -641,7 +662,7 @@ def biased_attention_backward(q, k, v, bias, dout, scale):
     q_len, kv_len, heads, hd, vd = _biased_shapes(q, k, v, bias)
     if dout.shape != (q_len, heads, vd):
         raise ValueError("dout must be [q_len, heads, value_dim]")
-    ws = Device(lib.dllm_hip_biased_attention_backward_workspace(q_len, kv_len, heads))
+    ws = Device(lib.dllm_hip_biased_attention_backward_workspace(q_len, kv_len, heads, hd, vd))
     d = [Device.of(a) for a in (q, k, v, bias, dout)]
     outs = [Device(max(a.nbytes, 4)) for a in (q, k, v, bias)]
     check(lib.dllm_hip_biased_attention_backward(*(x.ptr for x in d), *(o.ptr for o in outs), q_len, kv_len, heads,

@@ -170,7 +170,8 @@ int dllm_hip_dequantize_q8_0(const int8_t* q, const float* scales, float* out, s
  * layer_norm_backward: kernels.cpp:612-625, 858-875 (dx, dw, db; dw and db summed over all rows in order; any of the
  * three outputs may be NULL). biased_attention / biased_attention_backward: kernels.cpp:707-727, 961-990 (T5's
  * attention with bias [heads, q_len, kv_len]; q [q_len, heads, head_dim], k [kv_len, heads, head_dim], v [kv_len,
- * heads, value_dim]; returns dq, dk, dv, dbias). */
+ * heads, value_dim]; returns dq, dk, dv, dbias). Self-attention shapes (q_len == kv_len, head_dim and value_dim
+ * multiples of 4) run on the matrix-core tiles, with a larger workspace; the results are the same bits either way. */
 int dllm_hip_gelu(const float* x, float* out, size_t n, void* stream);
 int dllm_hip_gelu_backward(const float* x, const float* dy, float* out, size_t n, void* stream);
 int dllm_hip_layer_norm(const float* x, const float* weight, const float* bias, float* out, size_t rows, size_t dim,
@@ -179,11 +180,19 @@ size_t dllm_hip_layer_norm_backward_workspace(size_t rows);
 int dllm_hip_layer_norm_backward(const float* x, const float* weight, const float* dy, float* dx, float* dw,
                                  float* db, size_t rows, size_t dim, double eps, void* workspace,
                                  size_t workspace_bytes, void* stream);
-size_t dllm_hip_biased_attention_workspace(size_t q_len, size_t kv_len, size_t heads);
+size_t dllm_hip_biased_attention_workspace(size_t q_len, size_t kv_len, size_t heads, size_t head_dim,
+                                           size_t value_dim);
 int dllm_hip_biased_attention(const float* q, const float* k, const float* v, const float* bias, float* out,
                               size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
                               double scale, void* workspace, size_t workspace_bytes, void* stream);
-size_t dllm_hip_biased_attention_backward_workspace(size_t q_len, size_t kv_len, size_t heads);
+/* biased_attention_weights (kernels.cpp:753-773, interp.hpp:79-121): the probabilities [q_len, heads, kv_len] of
+ * biased_attention, f32(e (1 / total)); workspace: dllm_hip_biased_attention_workspace(q_len, kv_len, heads,
+ * head_dim, 4). */
+int dllm_hip_biased_attention_weights(const float* q, const float* k, const float* bias, float* out, size_t q_len,
+                                      size_t kv_len, size_t heads, size_t head_dim, double scale, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+size_t dllm_hip_biased_attention_backward_workspace(size_t q_len, size_t kv_len, size_t heads, size_t head_dim,
+                                                    size_t value_dim);
 int dllm_hip_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
                                        const float* dout, float* dq, float* dk, float* dv, float* dbias,
                                        size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,

@@ -937,6 +937,37 @@ void orc_biased_attention(const float* q, const float* k, const float* v, const 
     free(acc);
 }
 
+/* biased_attention_weights (interp.hpp:79-121): biased_attention's probabilities, f32(exp(s_j - max) (1 / total))
+ * per (t, h) into out [q_len, heads, kv_len]; nothing is written when kv_len is 0. */
+void orc_biased_attention_weights(const float* q, const float* k, const float* bias, float* out, size_t q_len,
+                                  size_t kv_len, size_t heads, size_t head_dim, double scale) {
+    if (kv_len == 0) return;
+    double* s = (double*)malloc(kv_len * sizeof(double));
+    for (size_t t = 0; t < q_len; ++t)
+        for (size_t h = 0; h < heads; ++h) {
+            const float* qh = q + (t * heads + h) * head_dim;
+            const float* bh = bias + (h * q_len + t) * kv_len;
+            float* row = out + (t * heads + h) * kv_len;
+            for (size_t j = 0; j < kv_len; ++j) {
+                const float* kj = k + (j * heads + h) * head_dim;
+                double d = 0.0;
+                for (size_t i = 0; i < head_dim; ++i) d += (double)qh[i] * (double)kj[i];
+                s[j] = (d + (double)bh[j]) * scale;
+            }
+            double max = s[0];
+            for (size_t j = 1; j < kv_len; ++j)
+                if (s[j] > max) max = s[j];
+            double total = 0.0;
+            for (size_t j = 0; j < kv_len; ++j) {
+                s[j] = orc_exp(s[j] - max);
+                total += s[j];
+            }
+            const double inv = 1.0 / total;
+            for (size_t j = 0; j < kv_len; ++j) row[j] = (float)(s[j] * inv);
+        }
+    free(s);
+}
+
 /* biased_attention_backward (grad.hpp:300-389): per (t, h), t then h ascending: p recomputed (scores, max, exp,
  * total, times 1 / total), dp_j = dout . v_j, D = sum p dp, ds = p (dp - D) scale (dbias = f32(ds)), dq = sum_j ds
  * k_j; dk[j] += ds q, dv[j] += p dout in double, rounded once at the end. */

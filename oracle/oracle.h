@@ -92,6 +92,8 @@ void orc_layer_norm_backward(const float* x, const float* w, const float* dy, fl
 void orc_biased_attention(const float* q, const float* k, const float* v, const float* bias, float* out,
                           size_t q_len, size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,
                           double scale);                                                /* nn.hpp:827-856 */
+void orc_biased_attention_weights(const float* q, const float* k, const float* bias, float* out, size_t q_len,
+                                  size_t kv_len, size_t heads, size_t head_dim, double scale);
 void orc_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
                                    const float* dout, float* dq, float* dk, float* dv, float* dbias, size_t q_len,
                                    size_t kv_len, size_t heads, size_t head_dim, size_t value_dim,

@@ -205,6 +205,10 @@ void ref_biased_attention(const float* q, const float* k, const float* v, const 
     FpEnvGuard guard;
     dllm::biased_attention(q, k, v, bias, out, ql, kl, heads, hd, vd, scale);
 }
+void ref_biased_attention_weights(const float* q, const float* k, const float* bias, float* out, size_t ql, size_t kl,
+                                  size_t heads, size_t hd, double scale) {
+    dllm::biased_attention_weights(q, k, bias, out, ql, kl, heads, hd, scale);
+}
 void ref_biased_attention_backward(const float* q, const float* k, const float* v, const float* bias,
                                    const float* dout, float* dq, float* dk, float* dv, float* dbias, size_t ql,
                                    size_t kl, size_t heads, size_t hd, size_t vd, double scale) {

@@ -856,6 +856,7 @@ def _declare_encoder(lib, prefix: str) -> None:
             ("layer_norm", None, [vp, vp, vp, vp, sz, sz, d]),
             ("layer_norm_backward", None, [vp, vp, vp, vp, vp, vp, sz, sz, d]),
             ("biased_attention", None, [vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d]),
+            ("biased_attention_weights", None, [vp, vp, vp, vp, sz, sz, sz, sz, d]),
             ("biased_attention_backward", None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, d])):
         fn = getattr(lib, f"{prefix}_{name}")
         fn.restype, fn.argtypes = res, args
@@ -920,6 +921,13 @@ class Encoder:
         out = np.empty((q.shape[0], q.shape[1], v.shape[2]), np.float32)
         self.fn("biased_attention")(ptr(q), ptr(k), ptr(v), ptr(bias), ptr(out), q.shape[0], k.shape[0], q.shape[1],
                                     q.shape[2], v.shape[2], scale)
+        return out
+
+    def biased_attention_weights(self, q, k, bias, scale):
+        q, k, bias = (np.ascontiguousarray(a, np.float32) for a in (q, k, bias))
+        out = np.zeros((q.shape[0], q.shape[1], k.shape[0]), np.float32)
+        self.fn("biased_attention_weights")(ptr(q), ptr(k), ptr(bias), ptr(out), q.shape[0], k.shape[0], q.shape[1],
+                                            q.shape[2], scale)
         return out
 
     def biased_attention_backward(self, q, k, v, bias, dout, scale):

@@ -361,16 +361,22 @@ def test_layer_norm_and_backward_match_the_oracle(K, rows, dim):
 
 
 @pytest.mark.parametrize(("q_len", "kv_len", "heads", "hd", "vd"),
-                         [(1, 3, 1, 4, 4), (5, 7, 2, 8, 8), (17, 17, 4, 16, 12), (33, 70, 3, 64, 64), (3, 0, 2, 4, 4)])
+                         [(1, 3, 1, 4, 4), (5, 7, 2, 8, 8), (33, 70, 3, 64, 64), (3, 0, 2, 4, 4), (6, 6, 2, 6, 8),
+                          (17, 17, 4, 16, 12), (1, 1, 1, 4, 4), (64, 64, 2, 64, 64), (130, 130, 3, 64, 32),
+                          (70, 70, 1, 12, 20), (200, 200, 2, 8, 128)])
 def test_biased_attention_and_backward_match_the_oracle(K, q_len, kv_len, heads, hd, vd):
-    """T5 biased attention forward and backward (kernels.cpp:707-727, 961-990), bit for bit; kv_len 0 is the empty
-    case (zero output and gradients)."""
+    """T5 biased attention forward, weights and backward (kernels.cpp:707-727, 753-773, 961-990), bit for bit, on
+    the per-(query, head) kernels (cross-attention shapes, head_dim not a multiple of 4) and the matrix-core tiles
+    (self-attention shapes); kv_len 0 is the empty case (zero output and gradients)."""
     q, k, v = O.gaussian(31, q_len, heads, hd), O.gaussian(32, kv_len, heads, hd), O.gaussian(33, kv_len, heads, vd)
     bias, dout = O.gaussian(34, heads, q_len, kv_len), O.gaussian(35, q_len, heads, vd)
     if kv_len > 2:
         bias[0, 0, :2] = -np.inf  # masked keys
     enc = O.oracle_encoder()
     assert_same(K.biased_attention(q, k, v, bias, 0.25), enc.biased_attention(q, k, v, bias, 0.25), "forward")
+    if kv_len:
+        assert_same(K.biased_attention_weights(q, k, bias, 0.25), enc.biased_attention_weights(q, k, bias, 0.25),
+                    "weights")
     for got, want, what in zip(K.biased_attention_backward(q, k, v, bias, dout, 0.25),
                                enc.biased_attention_backward(q, k, v, bias, dout, 0.25),
                                ("dq", "dk", "dv", "dbias")):

@@ -451,6 +451,7 @@ def test_biased_attention_and_backward_match_reference(q_len, kv_len, heads, hd,
     q, k, v = O.gaussian(11, q_len, heads, hd), O.gaussian(12, kv_len, heads, hd), O.gaussian(13, kv_len, heads, vd)
     bias, dout = O.gaussian(14, heads, q_len, kv_len, scale=3.0), O.gaussian(15, q_len, heads, vd)
     assert o.biased_attention(q, k, v, bias, 0.25).tobytes() == r.biased_attention(q, k, v, bias, 0.25).tobytes()
+    assert o.biased_attention_weights(q, k, bias, 0.25).tobytes() == r.biased_attention_weights(q, k, bias, 0.25).tobytes()
     for got, want in zip(o.biased_attention_backward(q, k, v, bias, dout, 0.25),
                          r.biased_attention_backward(q, k, v, bias, dout, 0.25)):
         assert got.tobytes() == want.tobytes()
