@@ -30,6 +30,13 @@ __device__ __forceinline__ void copy16_to_lds_s(const void* sbase, uint32_t voff
     asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u), "{m0}"(m0) : "memory");
 }
 
+// 4 bytes from src (a per-lane address, 4-byte aligned) to LDS at lds_row + 4 * lane.
+__device__ __forceinline__ void copy4_to_lds(const void* src, const void* lds_row) {
+    typedef __attribute__((address_space(3))) const void* lds_address;
+    const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_address)lds_row));
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
 // A workgroup barrier for LDS staged from registers: this wave's LDS writes complete (lgkmcnt), then s_barrier.
 // Unlike __syncthreads(), whose release fence also waits for every outstanding global load, it leaves the loads of
 // a register prefetch in flight across the barrier.

@@ -19,7 +19,7 @@ __global__ __launch_bounds__(64) void ce_rows_kernel(const float* __restrict__ l
                                                      int64_t rows, int64_t vocab, double* __restrict__ row_max,
                                                      double* __restrict__ row_total, double* __restrict__ row_loss,
                                                      int* __restrict__ error_flag) {
-    __shared__ double e[kChunk];
+    __shared__ __align__(16) double e[kChunk];
     const int64_t r = blockIdx.x;
     const int lane = threadIdx.x;
     if (r >= rows) return;
@@ -56,8 +56,21 @@ __global__ __launch_bounds__(64) void ce_rows_kernel(const float* __restrict__ l
         const int64_t n = vocab - c0 < kChunk ? vocab - c0 : kChunk;
         for (int64_t j = lane; j < n; j += 64) e[j] = dexp(static_cast<double>(lr[c0 + j]) - mx);
         __syncthreads();
-        if (lane == 0)
-            for (int64_t j = 0; j < n; ++j) total += e[j];
+        if (lane == 0) {  // 16 values read ahead of their adds (the chain is bound by the adds, not LDS latency)
+            const double2* e2 = reinterpret_cast<const double2*>(e);
+            int64_t j = 0;
+            for (; j + 16 <= n; j += 16) {
+                double2 v[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = e2[j / 2 + k];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    total += v[k].x;
+                    total += v[k].y;
+                }
+            }
+            for (; j < n; ++j) total += e[j];
+        }
         __syncthreads();
     }
     if (lane == 0) {

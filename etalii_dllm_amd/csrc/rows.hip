@@ -8,6 +8,7 @@
 #include "common.h"
 #include "devmath.h"
 #include "kernels.h"
+#include "lds_copy.h"
 
 namespace dllm_hip {
 
@@ -193,6 +194,80 @@ __global__ __launch_bounds__(256) void column_partial_kernel(int kind, const flo
     if (wave == 0 && i < dim) part[static_cast<int64_t>(blockIdx.y) * dim + i] = static_cast<float>(acc);
 }
 
+// The same sums with the raw rows copied straight to LDS (global_load_lds) kCsRing chunks of 64 rows ahead, tracked by
+// explicit counter waits (dim % 4 == 0, 16-byte aligned dy and x). A 1024-thread workgroup takes 16 columns of one
+// segment: waves 0-3 copy dy (16 rows each, 4 lanes per row), waves 4-7 x, waves 8 and 9 the rows' inv_rms as
+// 4-byte halves (kind 1); one copy per wave per chunk. Thread t forms the term of row slot t / 16, column t % 16
+// into LDS, and lanes 0-15 of wave 0 add the previous chunk's terms onto the column chains in row order.
+constexpr int kCsRing = 8;
+
+struct CsSlot {
+    float dy[64][16];
+    float x[64][16];
+    double inv[64];
+};
+
+__global__ __launch_bounds__(1024) void column_partial_lds_kernel(int kind, const float* __restrict__ dy,
+                                                                  const float* __restrict__ x,
+                                                                  const double* __restrict__ inv, int64_t dim,
+                                                                  ColSegments seg, float* __restrict__ part) {
+    __shared__ __align__(16) CsSlot ring[kCsRing];
+    __shared__ double terms[2][64][16];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int wave = tid >> 6, lane = tid & 63;
+    const int c16 = tid & 15, slot = tid >> 4;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t r0 = seg.off[blockIdx.y], r1 = seg.off[blockIdx.y + 1];
+    const int64_t chunks = (r1 - r0 + 63) / 64;
+    double acc = 0.0;
+    if (chunks > 0) {
+        const auto issue = [&](int64_t c) {
+            const int64_t cc = c < chunks ? c : chunks - 1;
+            CsSlot& dst = ring[cc % kCsRing];
+            const int64_t base = r0 + cc * 64;
+            if (wave < 8) {
+                if (wave >= 4 && kind == 0) return;
+                const int rr = 16 * (wave & 3) + lane / 4;
+                const int64_t r = base + rr < r1 ? base + rr : r1 - 1;
+                const int64_t g = col0 + 4 * (lane & 3) < dim ? col0 + 4 * (lane & 3) : dim - 4;
+                copy16_to_lds((wave < 4 ? dy : x) + r * dim + g,
+                              wave < 4 ? &dst.dy[16 * (wave & 3)][0] : &dst.x[16 * (wave & 3)][0]);
+            } else if (wave < 10 && kind != 0) {
+                const int half = wave - 8;  // rows 32 half .. 32 half + 31, two 4-byte lanes each
+                const int64_t rr = 32 * half + lane / 2;
+                const int64_t r = base + rr < r1 ? base + rr : r1 - 1;
+                copy4_to_lds(reinterpret_cast<const char*>(inv + r) + 4 * (lane & 1), &dst.inv[32 * half]);
+            }
+        };
+        for (int k = 0; k < kCsRing - 1; ++k) issue(k);
+        for (int64_t c = 0; c <= chunks; ++c) {
+            // chunk c landed (kCsRing - 2 newer copies may be pending per wave), the previous terms are written, and
+            // every wave is done reading the ring slot the next copy refills
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kCsRing - 2) : "memory");
+            issue(c + kCsRing - 1);
+            const CsSlot& src = ring[(c < chunks ? c : chunks - 1) % kCsRing];
+            const int buf = static_cast<int>(c & 1);
+            double t = static_cast<double>(src.dy[slot][c16]);
+            if (kind != 0) t = t * static_cast<double>(src.x[slot][c16]) * src.inv[slot];
+            terms[buf][slot][c16] = t;
+            if (c > 0 && tid < 16) {
+                const double(&tp)[64][16] = terms[buf ^ 1];
+                const int64_t rs = (c - 1) * 64;
+                const int n = r1 - r0 - rs < 64 ? static_cast<int>(r1 - r0 - rs) : 64;
+                if (n == 64) {
+#pragma unroll
+                    for (int rr = 0; rr < 64; ++rr) acc += tp[rr][tid];
+                } else {
+                    for (int rr = 0; rr < n; ++rr) acc += tp[rr][tid];
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the end drain before exit
+    }
+    if (tid < 16 && col0 + tid < dim)
+        part[static_cast<int64_t>(blockIdx.y) * dim + col0 + tid] = static_cast<float>(acc);
+}
+
 // out[i] = part[0][i] + part[1][i] + ... in float, segment order (trainer.py:328-332: the first copied).
 // out = part[0] + part[1] + ... in float, window order, the first copied; with factors, each window's part is first
 // multiplied by its factor (window s adds f32(part[s] * w[s])).
@@ -363,13 +438,21 @@ int launch_column_sums(int kind, const float* dy, const float* x, const double* 
                  "column sums over several segments (or with factors) need a partial buffer");
     const bool direct = nseg == 1 && !weights;
     const unsigned col_blocks = static_cast<unsigned>(ceil_div(dim, 64));
+    // the direct-to-LDS kernel: whole 16-byte pieces of rows
+    const bool ring = dim % 4 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0 &&
+                      (kind == 0 || (reinterpret_cast<uintptr_t>(x) % 16 == 0 && inv_rms != nullptr));
     for (int s0 = 0; s0 < nseg; s0 += kColSegs) {
         const int count = nseg - s0 < kColSegs ? nseg - s0 : kColSegs;
         ColSegments seg{};
         for (int s = 0; s <= count; ++s) seg.off[s] = seg_host[s0 + s];
         float* part = direct ? out : partial + static_cast<int64_t>(s0) * dim;
-        hipLaunchKernelGGL(column_partial_kernel, dim3(col_blocks, static_cast<unsigned>(count)), dim3(256), 0, stream,
-                           kind, dy, x, inv_rms, dim, seg, part);
+        if (ring)
+            hipLaunchKernelGGL(column_partial_lds_kernel, dim3(static_cast<unsigned>(ceil_div(dim, 16)),
+                                                               static_cast<unsigned>(count)),
+                               dim3(1024), 0, stream, kind, dy, x, inv_rms, dim, seg, part);
+        else
+            hipLaunchKernelGGL(column_partial_kernel, dim3(col_blocks, static_cast<unsigned>(count)), dim3(256), 0,
+                               stream, kind, dy, x, inv_rms, dim, seg, part);
     }
     const unsigned blocks = static_cast<unsigned>(ceil_div(dim, 256));
     if (!direct)
