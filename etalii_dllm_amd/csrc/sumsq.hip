@@ -229,13 +229,32 @@ __global__ __launch_bounds__(256) void block_fn_kernel(const float* __restrict__
     Fn f = identity_fn();
     bool ok = true;
     const int64_t i0 = static_cast<int64_t>(tid) * 32;
-    for (int k = 0; k < 32; ++k) {
-        const int64_t i = i0 + k;
-        if (i >= n) break;
-        Fn g;
-        long long q;
-        ok = ok && element_fn(sq(x[i]), inv_u, &g, &q);
-        f = compose(f, g);
+    if (i0 + 32 <= n && reinterpret_cast<uintptr_t>(x + i0) % 16 == 0) {
+        // a whole run: 8 vector loads, then the 32 elements in order
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 q4 = reinterpret_cast<const float4*>(x + i0)[k];
+            v[4 * k] = q4.x;
+            v[4 * k + 1] = q4.y;
+            v[4 * k + 2] = q4.z;
+            v[4 * k + 3] = q4.w;
+        }
+        for (int k = 0; k < 32; ++k) {
+            Fn g;
+            long long q;
+            ok = ok && element_fn(sq(v[k]), inv_u, &g, &q);
+            f = compose(f, g);
+        }
+    } else {
+        for (int k = 0; k < 32; ++k) {
+            const int64_t i = i0 + k;
+            if (i >= n) break;
+            Fn g;
+            long long q;
+            ok = ok && element_fn(sq(x[i]), inv_u, &g, &q);
+            f = compose(f, g);
+        }
     }
     // ordered reduction over the wave's lanes
     for (int off = 1; off < 64; off <<= 1) {
@@ -259,7 +278,16 @@ __global__ __launch_bounds__(256) void block_fn_kernel(const float* __restrict__
     }
 }
 
-// Pass C: per tensor, the exact walk over its blocks.
+// Pass C: per tensor, the exact walk over its blocks. The lanes load the records of 64 blocks at a time and the walk
+// takes block k's fields from lane k. While consecutive regular blocks share a binade e the state stays the integer
+// M (s = M 2^(e-52), M in [2^52, 2^53)): after an application M + tot <= 2^53 - 1 and tot >= 0, so s stays in
+// binade e and the next block's M = s 2^(52-e) is that same integer. s is formed only when the walk leaves that path.
+__device__ __forceinline__ long long readlane64(long long v, int k) {
+    const int lo = __builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffLL), k);
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), k);
+    return (static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo);
+}
+
 __global__ __launch_bounds__(64) void tensor_walk_kernel(const float* __restrict__ arena,
                                                          const int64_t* __restrict__ tfirst,
                                                          const int64_t* __restrict__ tblocks,
@@ -268,20 +296,59 @@ __global__ __launch_bounds__(64) void tensor_walk_kernel(const float* __restrict
                                                          const BlockRec* __restrict__ rec,
                                                          double* __restrict__ per_tensor) {
     const int64_t t = blockIdx.x;
+    const int lane = static_cast<int>(threadIdx.x);
     const int64_t b0 = tfirst[t], nb = tblocks[t];
     double s = 0.0;
-    for (int64_t b = b0; b < b0 + nb; ++b) {
-        const BlockRec r = rec[b];
-        if (r.regular && s > 0.0 && s < infinity() && binade(s) == r.e) {
-            const long long M = static_cast<long long>(s * pow2(52 - r.e));
-            const long long tot = (M & 1) ? r.d1 : r.d0;
+    bool have = false;  // s == M 2^(e - 52)
+    long long M = 0;
+    int e = 0;
+    for (int64_t bc = b0; bc < b0 + nb; bc += 64) {
+        const BlockRec mine = bc + lane < b0 + nb ? rec[bc + lane] : BlockRec{0, 0, 0, 1, 0, 0};
+        const int cnt = static_cast<int>(b0 + nb - bc < 64 ? b0 + nb - bc : 64);
+        // the 64 blocks at once when all are regular in the current binade: their functions compose in order, and
+        // since increments are non-negative, the whole run's bound covers every block's
+        if (have && __ballot(lane < cnt && !(mine.regular && mine.e == e)) == 0) {
+            Fn f = lane < cnt ? Fn{mine.d0, mine.d1, mine.p0, mine.p1} : identity_fn();
+            for (int off = 1; off < 64; off <<= 1) {
+                const Fn g = shfl_down_fn(f, off);
+                if ((lane & (2 * off - 1)) == 0) f = compose(f, g);
+            }
+            const long long tot = (M & 1) ? readlane64(f.d1, 0) : readlane64(f.d0, 0);
             if (M + tot <= kTop) {
-                s = static_cast<double>(M + tot) * pow2(r.e - 52);
+                M += tot;
                 continue;
             }
         }
-        s = walk(arena, bstart[b], bstart[b] + bcount[b], s);
+        for (int k = 0; k < cnt; ++k) {
+            const int regular = __builtin_amdgcn_readlane(mine.regular, k);
+            const int re = __builtin_amdgcn_readlane(mine.e, k);
+            const long long d0 = readlane64(mine.d0, k), d1 = readlane64(mine.d1, k);
+            if (have && regular && re == e) {
+                const long long tot = (M & 1) ? d1 : d0;
+                if (M + tot <= kTop) {
+                    M += tot;
+                    continue;
+                }
+            }
+            if (have) {
+                s = static_cast<double>(M) * pow2(e - 52);
+                have = false;
+            }
+            if (regular && s > 0.0 && s < infinity() && binade(s) == re) {
+                const long long M0 = static_cast<long long>(s * pow2(52 - re));
+                const long long tot = (M0 & 1) ? d1 : d0;
+                if (M0 + tot <= kTop) {
+                    M = M0 + tot;
+                    e = re;
+                    have = true;
+                    continue;
+                }
+            }
+            const int64_t b = bc + k;
+            s = walk(arena, bstart[b], bstart[b] + bcount[b], s);
+        }
     }
+    if (have) s = static_cast<double>(M) * pow2(e - 52);
     if (threadIdx.x == 0) per_tensor[t] = s;
 }
 
