@@ -1,7 +1,8 @@
 // Softmax cross-entropy with its logit gradient (grad.hpp:395-426), and the embedding gradient (grad.hpp:431-464).
 //
 // Per row: the first maximum of the logits (a wave reduction with lowest-index ties); the total of
-// exp(l_j - max) as one serial double chain over j ascending on lane 0, fed by the 64 lanes in LDS chunks; the loss
+// exp(l_j - max) as one serial double chain over j ascending on one lane (a wave takes 4 rows, lane q row q's chain),
+// fed by the 64 lanes in LDS chunks; the loss
 // term (max + log(total)) - l[target]; then the gradient f32((e_j (1/total) - onehot) scale), fully parallel. The
 // loss of a window is the serial double sum of its rows' terms in row order (negative targets skipped).
 #include "common.h"
@@ -12,20 +13,13 @@ namespace dllm_hip {
 
 namespace {
 
-constexpr int kChunk = 2048;  // exponentials staged per lane-0 pass (16 KB of LDS)
+constexpr int kCeRows = 4;     // rows per wave
+constexpr int kCeChunk = 512;  // exponentials per row staged per pass
+constexpr int kCeLd = kCeChunk + 2;  // LDS row stride (doubles): the rows' chains read different banks
 
-// Row max + serial total + loss term: one 64-lane wave per row.
-__global__ __launch_bounds__(64) void ce_rows_kernel(const float* __restrict__ logits, const int64_t* __restrict__ targets,
-                                                     int64_t rows, int64_t vocab, double* __restrict__ row_max,
-                                                     double* __restrict__ row_total, double* __restrict__ row_loss,
-                                                     int* __restrict__ error_flag) {
-    __shared__ __align__(16) double e[kChunk];
-    const int64_t r = blockIdx.x;
-    const int lane = threadIdx.x;
-    if (r >= rows) return;
-    const float* lr = logits + r * vocab;
-    // argmax (math.hpp:40-53): the first index of the largest value. Each lane scans its own indices in ascending
-    // order; lanes combine by "strictly larger wins, otherwise the lower index".
+// argmax (math.hpp:40-53) of row lr: the first index of the largest value. Each lane scans its own indices in
+// ascending order; lanes combine by "strictly larger wins, otherwise the lower index".
+__device__ inline int64_t row_argmax(const float* lr, int64_t vocab, int lane) {
     float best = 0.0f;
     int64_t bi = -1;
     for (int64_t j = lane; j < vocab; j += 64) {
@@ -49,16 +43,43 @@ __global__ __launch_bounds__(64) void ce_rows_kernel(const float* __restrict__ l
             bi = oi;
         }
     }
-    bi = __shfl(bi, 0, 64);
-    const double mx = static_cast<double>(lr[bi]);
+    return __shfl(bi, 0, 64);
+}
+
+// Row max + serial total + loss term for kCeRows rows per wave: all lanes form the exponentials exp(l - max) of a
+// chunk of each row into LDS, then lane q adds row q's chunk onto its total in column order (16 values read ahead).
+__global__ __launch_bounds__(64) void ce_rows_kernel(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+                                                     int64_t rows, int64_t vocab, double* __restrict__ row_max,
+                                                     double* __restrict__ row_total, double* __restrict__ row_loss,
+                                                     int* __restrict__ error_flag) {
+    __shared__ __align__(16) double e[kCeRows * kCeLd];
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kCeRows;
+    const int lane = threadIdx.x;
+    const int nr = rows - r0 < kCeRows ? static_cast<int>(rows - r0) : kCeRows;
+    double mx[kCeRows];
+    double my_mx = 0.0;  // lane q < nr: row r0 + q's maximum
+#pragma unroll
+    for (int q = 0; q < kCeRows; ++q) {
+        mx[q] = 0.0;
+        if (q < nr) {
+            const float* lr = logits + (r0 + q) * vocab;
+            mx[q] = static_cast<double>(lr[row_argmax(lr, vocab, lane)]);
+        }
+        if (lane == q) my_mx = mx[q];
+    }
     double total = 0.0;
-    for (int64_t c0 = 0; c0 < vocab; c0 += kChunk) {
-        const int64_t n = vocab - c0 < kChunk ? vocab - c0 : kChunk;
-        for (int64_t j = lane; j < n; j += 64) e[j] = dexp(static_cast<double>(lr[c0 + j]) - mx);
+    for (int64_t c0 = 0; c0 < vocab; c0 += kCeChunk) {
+        const int n = vocab - c0 < kCeChunk ? static_cast<int>(vocab - c0) : kCeChunk;
+#pragma unroll
+        for (int q = 0; q < kCeRows; ++q) {
+            if (q >= nr) break;
+            const float* lr = logits + (r0 + q) * vocab + c0;
+            for (int j = lane; j < n; j += 64) e[q * kCeLd + j] = dexp(static_cast<double>(lr[j]) - mx[q]);
+        }
         __syncthreads();
-        if (lane == 0) {  // 16 values read ahead of their adds (the chain is bound by the adds, not LDS latency)
-            const double2* e2 = reinterpret_cast<const double2*>(e);
-            int64_t j = 0;
+        if (lane < nr) {
+            const double2* e2 = reinterpret_cast<const double2*>(e + lane * kCeLd);
+            int j = 0;
             for (; j + 16 <= n; j += 16) {
                 double2 v[8];
 #pragma unroll
@@ -69,16 +90,17 @@ __global__ __launch_bounds__(64) void ce_rows_kernel(const float* __restrict__ l
                     total += v[k].y;
                 }
             }
-            for (; j < n; ++j) total += e[j];
+            for (; j < n; ++j) total += e[lane * kCeLd + j];
         }
         __syncthreads();
     }
-    if (lane == 0) {
-        row_max[r] = mx;
+    if (lane < nr) {
+        const int64_t r = r0 + lane;
+        row_max[r] = my_mx;
         row_total[r] = total;
         const int64_t t = targets[r];
         if (t >= vocab) *error_flag = 1;
-        row_loss[r] = (t >= 0 && t < vocab) ? mx + dlog(total) - static_cast<double>(lr[t]) : 0.0;
+        row_loss[r] = (t >= 0 && t < vocab) ? my_mx + dlog(total) - static_cast<double>(logits[r * vocab + t]) : 0.0;
     }
 }
 
@@ -136,8 +158,8 @@ int launch_cross_entropy(const float* logits, const int64_t* targets, float* dlo
     if (rows == 0) return kOk;
     DLLM_REQUIRE(vocab > 0, "cross_entropy needs a non-empty vocabulary");
     DLLM_REQUIRE(rows <= 65535 * 1024LL, "too many rows");
-    hipLaunchKernelGGL(ce_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, stream, logits, targets, rows,
-                       vocab, row_max, row_total, row_loss, error_flag);
+    hipLaunchKernelGGL(ce_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, kCeRows))), dim3(64), 0, stream,
+                       logits, targets, rows, vocab, row_max, row_total, row_loss, error_flag);
     DLLM_TRY(check_launch("cross_entropy rows"));
     DLLM_REQUIRE(rows <= 65535, "cross_entropy launches at most 65535 rows at once");
     hipLaunchKernelGGL(ce_grad_kernel, dim3(static_cast<unsigned>(ceil_div(vocab, 256)), static_cast<unsigned>(rows)),
