@@ -735,6 +735,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 }
 
 // C[i][j] = partial[0][i][j] + partial[1][i][j] + ... in float, window order (trainer.py:328-332).
+// Contiguous output (ldc == J, 16-byte aligned, I J % 4 == 0): four elements per thread, the windows' loads issued
+// eight at a time ahead of the adds, which stay in window order.
+__global__ __launch_bounds__(256) void window_sum4_kernel(const float4* __restrict__ partial, int64_t n4, int nseg,
+                                                          float4* __restrict__ C) {
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; e < n4;
+         e += static_cast<int64_t>(gridDim.x) * 256) {
+        float4 t = partial[e];
+        for (int s0 = 1; s0 < nseg; s0 += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (s0 + k < nseg) v[k] = partial[static_cast<int64_t>(s0 + k) * n4 + e];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (s0 + k < nseg) {
+                    t.x = t.x + v[k].x;
+                    t.y = t.y + v[k].y;
+                    t.z = t.z + v[k].z;
+                    t.w = t.w + v[k].w;
+                }
+        }
+        C[e] = t;
+    }
+}
+
 __global__ __launch_bounds__(256) void window_sum_kernel(const float* __restrict__ partial, int64_t I, int64_t J,
                                                          int nseg, float* __restrict__ C, int64_t ldc) {
     const int64_t n = I * J;
@@ -950,8 +975,14 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
         if (p.partial) {
             const int64_t n = g.I * g.J;
             const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 256), 8192));
-            hipLaunchKernelGGL(window_sum_kernel, dim3(blocks), dim3(256), 0, stream, p.partial, g.I, g.J, g.nseg,
-                               g.C, g.ldc);
+            if (g.ldc == g.J && (g.I * g.J) % 4 == 0 && reinterpret_cast<uintptr_t>(g.C) % 16 == 0 &&
+                reinterpret_cast<uintptr_t>(p.partial) % 16 == 0)
+                hipLaunchKernelGGL(window_sum4_kernel, dim3(blocks), dim3(256), 0, stream,
+                                   reinterpret_cast<const float4*>(p.partial), g.I * g.J / 4, g.nseg,
+                                   reinterpret_cast<float4*>(g.C));
+            else
+                hipLaunchKernelGGL(window_sum_kernel, dim3(blocks), dim3(256), 0, stream, p.partial, g.I, g.J, g.nseg,
+                                   g.C, g.ldc);
             return check_launch("gemm window sum");
         }
         return kOk;

@@ -115,6 +115,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
         const int64_t base = (r0 + r) * dim;
         if (kBackward) {
             const double coef = row_coef[r];
+#pragma unroll 8
             for (int64_t i = lane; i < dim; i += 64) {
                 const double g = norm_scale_backward(w, i, unit_offset);
                 float v = static_cast<float>(inv * g * static_cast<double>(dy[base + i]) -
@@ -123,6 +124,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
                 out[base + i] = v;
             }
         } else {
+#pragma unroll 8
             for (int64_t i = lane; i < dim; i += 64)
                 out[base + i] = static_cast<float>(static_cast<double>(x[base + i]) * inv * norm_scale(w, i, unit_offset));
         }
