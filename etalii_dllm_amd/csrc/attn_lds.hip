@@ -197,17 +197,30 @@ __device__ __forceinline__ void widen(const RowOperands<CJ>& r, double (&b)[CJ])
     for (int c = 0; c < CJ; ++c) b[c] = r.b[c];
 }
 
+// A full stage (every row takes every step): the wave's 16 A values of a step are read from LDS at one address for
+// all lanes (a broadcast, on the LDS pipe), so the vector ALU issues only the conversions and the multiply-adds.
 template <int CJ>
 __device__ __forceinline__ void stage_all(const Stage<CJ>& st, int wave, int lane, double (&acc)[16][CJ]) {
-    RowOperands<CJ> cur = read_row<CJ>(st, 0, wave, lane);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        RowOperands<CJ> next = cur;
-        if (k + 1 < kChunk) next = read_row<CJ>(st, k + 1, wave, lane);
+        const RowOperands<CJ> r = read_row<CJ>(st, k, wave, lane);
         double b[CJ];
-        widen<CJ>(cur, b);
-        step_rows<CJ, true, 0>(acc, cur.a, b, 0u);
-        cur = next;
+        widen<CJ>(r, b);
+        const double2* ar = reinterpret_cast<const double2*>(&st.a[k][wave * 16]);
+        double aq[16];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const double2 v = ar[q];
+            aq[2 * q] = v.x;
+            aq[2 * q + 1] = v.y;
+        }
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+#pragma unroll
+            for (int c = 0; c < CJ; ++c) {
+                const double prod = aq[q] * b[c];
+                acc[q][c] = acc[q][c] + prod;
+            }
     }
 }
 
@@ -247,7 +260,7 @@ __device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ
 template <int CJ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4 : 2))) void attn_tile_kernel(
     TileParams p) {
-    __shared__ Stage<CJ> st[2];
+    __shared__ __align__(16) Stage<CJ> st[2];
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int lane = static_cast<int>(threadIdx.x) & 63;
     // block -> (rank by work, column tile, set, z): the longest reductions go first
