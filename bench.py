@@ -268,6 +268,90 @@ def traffic_summary(config: str, fetch_csv: str, write_csv: str, copy_fetch_csv:
     return 0
 
 
+def kernel_suite(iters: int = 20) -> int:
+    """The per-kernel entry points beyond the step (quantised inference linears, encoder/T5 kernels), each on
+    device-resident inputs: time per call over `iters` back-to-back calls after 3 warmups, and the rate against the
+    bound that applies. One JSON line per case on stdout."""
+    from etalii_dllm_amd import kernels as K
+
+    lib, rng = K.lib, np.random.default_rng(0)
+
+    def timed(run) -> float:
+        for _ in range(3):
+            run()
+        K.check(lib.dllm_hip_synchronize())
+        t = time.perf_counter()
+        for _ in range(iters):
+            run()
+        K.check(lib.dllm_hip_synchronize())
+        return (time.perf_counter() - t) / iters
+
+    def report(case: str, seconds: float, **rates) -> None:
+        print(json.dumps({"kernel_suite": case, "us_per_call": round(seconds * 1e6, 2), **rates}), flush=True)
+
+    hbm, fp64_lane_ops = 8.0e12, 78.6e12 / 2  # bytes/s; vector FP64 instructions x 64 lanes per second
+    for rows, inf, outf in [(1, 1536, 8960), (1, 8960, 1536), (8, 4096, 4096), (512, 1536, 8960), (4096, 1536, 8960)]:
+        x = K.Device.of(rng.standard_normal((rows, inf)).astype(np.float32))
+        q, sc = K.quantize_q8_0((rng.standard_normal((outf, inf)) * 0.02).astype(np.float32))
+        dq, ds, out = K.Device.of(q), K.Device.of(sc), K.Device(rows * outf * 4)
+        ws = K.Device(lib.dllm_hip_linear_q8_workspace(rows, inf))
+        t = timed(lambda: K.check(lib.dllm_hip_linear_q8(x.ptr, dq.ptr, ds.ptr, None, out.ptr, rows, inf, outf, ws.ptr,
+                                                         ws.nbytes, None)))
+        weight_bytes = q.nbytes + sc.nbytes
+        combine = 4.0 * rows * outf * (inf // 32) / fp64_lane_ops  # scale product, conversion, multiply, add
+        report(f"linear_q8 rows={rows} in={inf} out={outf}", t, weights_GBps=round(weight_bytes / t / 1e9, 1),
+               hbm_frac=round(weight_bytes / t / hbm, 3), int8_equiv_TOPs=round(2 * rows * inf * outf / t / 1e12, 2),
+               combine_bound_frac=round(combine / t, 3))
+    for rows, inf, outf in [(1, 1536, 8960), (1, 8960, 1536)]:
+        x = K.Device.of(rng.standard_normal((rows, inf)).astype(np.float32))
+        pk, sc = K.quantize_q4_0((rng.standard_normal((outf, inf)) * 0.02).astype(np.float32))
+        dq, ds, out = K.Device.of(pk), K.Device.of(sc), K.Device(rows * outf * 4)
+        ws = K.Device(lib.dllm_hip_linear_q4_workspace(rows, inf, outf))
+        t = timed(lambda: K.check(lib.dllm_hip_linear_q4(x.ptr, dq.ptr, ds.ptr, None, out.ptr, rows, inf, outf, ws.ptr,
+                                                         ws.nbytes, None)))
+        weight_bytes = pk.nbytes + sc.nbytes
+        report(f"linear_q4 rows={rows} in={inf} out={outf}", t, weights_GBps=round(weight_bytes / t / 1e9, 1),
+               hbm_frac=round(weight_bytes / t / hbm, 3))
+    n = 1 << 24
+    x = K.Device.of(rng.standard_normal(n).astype(np.float32))
+    o = K.Device(n * 4)
+    t = timed(lambda: K.check(lib.dllm_hip_gelu(x.ptr, o.ptr, n, None)))
+    report(f"gelu n={n}", t, GBps=round(8 * n / t / 1e9, 1), Gelem_per_s=round(n / t / 1e9, 2))
+    t = timed(lambda: K.check(lib.dllm_hip_gelu_backward(x.ptr, x.ptr, o.ptr, n, None)))
+    report(f"gelu_backward n={n}", t, GBps=round(12 * n / t / 1e9, 1), Gelem_per_s=round(n / t / 1e9, 2))
+    for rows, dim in [(4096, 768), (16384, 1024)]:
+        x = K.Device.of(rng.standard_normal((rows, dim)).astype(np.float32))
+        dy = K.Device.of(rng.standard_normal((rows, dim)).astype(np.float32))
+        w = K.Device.of(np.ones(dim, np.float32))
+        out, dx, dw, db = K.Device(rows * dim * 4), K.Device(rows * dim * 4), K.Device(dim * 4), K.Device(dim * 4)
+        ws = K.Device(lib.dllm_hip_layer_norm_backward_workspace(rows))
+        t = timed(lambda: K.check(lib.dllm_hip_layer_norm(x.ptr, w.ptr, w.ptr, out.ptr, rows, dim, 1e-12, None)))
+        report(f"layer_norm {rows}x{dim}", t, GBps=round(8 * rows * dim / t / 1e9, 1),
+               hbm_frac=round(8 * rows * dim / t / hbm, 3))
+        t = timed(lambda: K.check(lib.dllm_hip_layer_norm_backward(x.ptr, w.ptr, dy.ptr, dx.ptr, dw.ptr, db.ptr, rows,
+                                                                   dim, 1e-12, ws.ptr, ws.nbytes, None)))
+        report(f"layer_norm_backward {rows}x{dim}", t, GBps=round(12 * rows * dim / t / 1e9, 1),
+               hbm_frac=round(12 * rows * dim / t / hbm, 3))
+    for T, H, hd in [(512, 12, 64), (1024, 16, 64)]:
+        qkv = K.Device.of(rng.standard_normal((T, H, hd)).astype(np.float32))
+        bias = K.Device.of(rng.standard_normal((H, T, T)).astype(np.float32))
+        out, dq, dk, dv = (K.Device(T * H * hd * 4) for _ in range(4))
+        dbias, wts = K.Device(H * T * T * 4), K.Device(T * H * T * 4)
+        ws = K.Device(lib.dllm_hip_biased_attention_backward_workspace(T, T, H, hd, hd))
+        flop = 4.0 * T * T * H * hd
+        t = timed(lambda: K.check(lib.dllm_hip_biased_attention(qkv.ptr, qkv.ptr, qkv.ptr, bias.ptr, out.ptr, T, T, H,
+                                                                hd, hd, 0.125, ws.ptr, ws.nbytes, None)))
+        report(f"biased_attention T={T} heads={H} head_dim={hd}", t, TFLOPs=round(flop / t / 1e12, 2))
+        t = timed(lambda: K.check(lib.dllm_hip_biased_attention_weights(qkv.ptr, qkv.ptr, bias.ptr, wts.ptr, T, T, H,
+                                                                        hd, 0.125, ws.ptr, ws.nbytes, None)))
+        report(f"biased_attention_weights T={T} heads={H} head_dim={hd}", t, TFLOPs=round(flop / 2 / t / 1e12, 2))
+        t = timed(lambda: K.check(lib.dllm_hip_biased_attention_backward(
+            qkv.ptr, qkv.ptr, qkv.ptr, bias.ptr, qkv.ptr, dq.ptr, dk.ptr, dv.ptr, dbias.ptr, T, T, H, hd, hd, 0.125,
+            ws.ptr, ws.nbytes, None)))
+        report(f"biased_attention_backward T={T} heads={H} head_dim={hd}", t, TFLOPs=round(2 * flop / t / 1e12, 2))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -282,7 +366,12 @@ def main() -> int:
                     help="run only a plain device copy of 1 GiB (the reference kernel for HBM byte counters)")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
                     help="turn rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter files into profiles/gemm_traffic.json")
+    ap.add_argument("--kernels", action="store_true",
+                    help="time the inference linear layers and encoder/T5 kernels instead of the step (one JSON line "
+                         "per case)")
     args = ap.parse_args()
+    if args.kernels:
+        return kernel_suite()
     if args.copy_calibration:
         return copy_calibration()
     if args.traffic_summary:
