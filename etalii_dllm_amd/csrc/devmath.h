@@ -227,10 +227,12 @@ __host__ __device__ inline double derfc(double x) {
 }
 
 // sigmoid (math.hpp:322-328).
+// Both of the reference's branches as one path (a wave whose lanes differ in sign runs one exp and one division,
+// not two of each): x >= 0 gives 1 / (1 + exp(-x)), otherwise exp(x) / (1 + exp(x)); a NaN takes the second form.
 __host__ __device__ inline double dsigmoid(double x) {
-    if (x >= 0) return 1.0 / (1.0 + dexp(-x));
-    const double e = dexp(x);
-    return e / (1.0 + e);
+    const bool nonneg = x >= 0;
+    const double e = dexp(nonneg ? -x : x);
+    return (nonneg ? 1.0 : e) / (1.0 + e);
 }
 
 // silu (nn.hpp:467-470) and its gradient (grad.hpp:177-181), each rounded once to float.

@@ -466,14 +466,23 @@ static_assert(kMTileI == 128, "the transposed-A copy layout assumes 128 rows");
 
 template <int kA>
 struct MStage {
-    float a[kMStage * kMTileI];  // A rows: [l][i]; A transposed: [l / 4][i][l % 4]
-    float b[kMStage * kMTileJ];  // [l][j]
+    float a[kMStage * kMTileI];  // A rows: [l][i ^ 16 (l % 4)]; A transposed: [l / 4][i][l % 4]
+    float b[kMStage * kMTileJ];  // A rows: [l][j ^ 16 (l % 4)]; A transposed: [l][j]
 };
+
+// Row-major stage rows are 128 floats (512 bytes), so the 4 rows a fragment read spans (l = 4s .. 4s + 3, one per
+// 16 lanes) fall on the same LDS banks. With A read as rows (the weight gradients) row l keeps its 16-byte chunks
+// XOR-permuted by 4 (l % 4): element j of row l sits at j ^ (16 (l % 4)), and a fragment read touches 64 consecutive
+// banks. The copies apply the permutation through the source address each lane loads (an LDS copy's destination is
+// fixed by the lane). Measured on MI355X, the permutation speeds up those matmuls by 1% and slows the transposed-A
+// ones (whose A reads are already conflict-free) by 2%, so only the former use it.
+__host__ __device__ __forceinline__ int mswizzle_chunk(int row) { return (row & 3) << 2; }
 
 // The global source of copy `id` of a stage at row l, with every index clamped in bounds (rows past `last` repeat
 // row `last`; their values are masked); the LDS destination of copy id is 16 * id bytes into the operand's array.
+template <int kA>
 __host__ __device__ __forceinline__ const float* msrc_b(const GemmParams& p, int id, int64_t j_blk, int64_t l, int64_t last) {
-    const int r = id / (kMTileJ / 4), cc = id % (kMTileJ / 4);
+    const int r = id / (kMTileJ / 4), cc = (id % (kMTileJ / 4)) ^ (kA == kAFloatRows ? mswizzle_chunk(r) : 0);
     const int64_t lr = l + r <= last ? l + r : last;
     const int64_t j = j_blk + cc * 4 <= p.J - 4 ? j_blk + cc * 4 : p.J - 4;
     return p.B + lr * p.ldb + j;
@@ -482,7 +491,7 @@ __host__ __device__ __forceinline__ const float* msrc_b(const GemmParams& p, int
 template <int kA>
 __host__ __device__ __forceinline__ const float* msrc_a(const GemmParams& p, int id, int64_t i_blk, int64_t l, int64_t last) {
     if constexpr (kA == kAFloatRows) {
-        const int r = id / (kMTileI / 4), cc = id % (kMTileI / 4);
+        const int r = id / (kMTileI / 4), cc = (id % (kMTileI / 4)) ^ mswizzle_chunk(id / (kMTileI / 4));
         const int64_t lr = l + r <= last ? l + r : last;
         const int64_t i = i_blk + cc * 4 <= p.I - 4 ? i_blk + cc * 4 : p.I - 4;
         return p.Af + lr * p.lda + i;
@@ -501,7 +510,7 @@ __device__ __forceinline__ void missue_stage(const GemmParams& p, MStage<kA>& st
     const int wave_base = tid & ~63;
 #pragma unroll
     for (int t = 0; t < kMPiecesB; ++t)
-        copy16_to_lds(msrc_b(p, t * 256 + tid, j_blk, l, last), &st.b[(t * 256 + wave_base) * 4]);
+        copy16_to_lds(msrc_b<kA>(p, t * 256 + tid, j_blk, l, last), &st.b[(t * 256 + wave_base) * 4]);
 #pragma unroll
     for (int t = 0; t < kMPiecesA; ++t)
         copy16_to_lds(msrc_a<kA>(p, t * 256 + tid, i_blk, l, last), &st.a[(t * 256 + wave_base) * 4]);
@@ -520,7 +529,7 @@ __host__ __device__ __forceinline__ MCopyOffsets mcopy_offsets(const GemmParams&
     const int64_t big = int64_t{1} << 40;  // no l clamp
 #pragma unroll
     for (int t = 0; t < kMPiecesB; ++t)
-        o.b[t] = static_cast<uint32_t>(reinterpret_cast<const char*>(msrc_b(p, t * 256 + tid, j_blk, 0, big)) -
+        o.b[t] = static_cast<uint32_t>(reinterpret_cast<const char*>(msrc_b<kA>(p, t * 256 + tid, j_blk, 0, big)) -
                                        reinterpret_cast<const char*>(p.B));
 #pragma unroll
     for (int t = 0; t < kMPiecesA; ++t) {
@@ -554,11 +563,12 @@ __device__ __forceinline__ void mread_frags(const MStage<kA>& st, int s, int wi,
         if constexpr (kA == kAFloatT)
             a[q] = static_cast<double>(st.a[(s * kMTileI + i) * 4 + k]);
         else
-            a[q] = static_cast<double>(st.a[(4 * s + k) * kMTileI + i]);
+            a[q] = static_cast<double>(st.a[(4 * s + k) * kMTileI + (i ^ (k << 4))]);
     }
 #pragma unroll
     for (int q = 0; q < kMBJ; ++q)
-        b[q] = static_cast<double>(st.b[(4 * s + k) * kMTileJ + wj * 16 * kMBJ + 16 * q + c16]);
+        b[q] = static_cast<double>(
+            st.b[(4 * s + k) * kMTileJ + ((wj * 16 * kMBJ + 16 * q + c16) ^ (kA == kAFloatRows ? k << 4 : 0))]);
 }
 
 __device__ __forceinline__ void mfma_step(const double (&a)[kMBI], const double (&b)[kMBJ],

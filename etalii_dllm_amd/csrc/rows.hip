@@ -26,7 +26,7 @@ __device__ __forceinline__ double norm_scale_backward(const float* w, int64_t i,
     return (unit_offset ? 1.0 : 0.0) + static_cast<double>(w[i]);
 }
 
-constexpr int kNormRows = 16;  // rows per 256-thread workgroup of the norm kernels
+constexpr int kNormRows = 4;  // rows per 256-thread workgroup of the norm kernels (one per wave)
 
 // Adds terms[0 .. n) to `chain` in index order, reading them from LDS 16 at a time ahead of the dependent adds.
 __device__ __forceinline__ void chain_add(double& chain, const double* terms, int n) {
@@ -41,9 +41,10 @@ __device__ __forceinline__ void chain_add(double& chain, const double* terms, in
     for (; k < n; ++k) chain += terms[k];
 }
 
-// rms_norm (nn.hpp:391-408) and rms_norm_backward's dx (grad.hpp:83-104), 16 rows per workgroup. Per row the serial
-// chains run one lane per row out of LDS: the four waves stage the terms of 16 rows x 64 columns (x^2, and for the
-// backward (g dy) x) in one of two buffers, then lanes 0-15 of wave 0 add the squares and lanes 16-31 the products
+// rms_norm (nn.hpp:391-408) and rms_norm_backward's dx (grad.hpp:83-104), kNormRows rows per workgroup. Per row the serial
+// chains run one lane per row out of LDS: the four waves stage the terms of kNormRows rows x 64 columns (x^2, and for
+// the backward (g dy) x) in one of two buffers, then lanes 0 .. kNormRows - 1 of wave 0 add the squares and the next
+// kNormRows lanes the products
 // in ascending column order, while the next 64 columns' loads are in flight. Then every thread writes its elements:
 //   forward   out = f32((x inv) scale),              inv = 1 / sqrt(sum x^2 / dim + eps)
 //   backward  dx = f32((inv g) dy - x coef) (+ addend), coef = D inv inv inv / dim, D = sum (g dy) x
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
             if (kBackward) products[c & 1][r][lane] = g * static_cast<double>(dv[k]) * xd;
         }
     };
-    double chain = 0.0;  // wave 0: lanes 0-15 the squares of row lane, lanes 16-31 the products of row lane - 16
+    double chain = 0.0;  // wave 0: lane r < kNormRows the squares of row r, lane kNormRows + r the products of row r
     load(0);
     store(0);
     __syncthreads();

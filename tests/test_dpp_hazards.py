@@ -1,11 +1,11 @@
 """Static checks of the hand-written instructions in the matmul and attention kernels (no GPU needed).
 
-The FMAs and moves with the DPP64 modifier row_newbcast sit in inline assembly, so the compiler's hazard recognizer
+The VALU fallback matmul's FMAs with the DPP64 modifier row_newbcast sit in inline assembly, so the compiler's hazard recognizer
 does not see them. The CDNA rule they must obey: a DPP instruction comes at least two wait states after any vector
 ALU write of a VGPR it reads (the previous instruction and `s_nop n` count 1 and n + 1 states). This test compiles
 the two kernel sources to gfx950 assembly with the library's own flags and walks back from every DPP instruction.
 
-The matrix-core matmul's stage copies are inline-assembly memory loads whose base address is an SGPR pair. A vector
+The matrix-core matmul's and attention kernels' stage copies are inline-assembly memory loads whose base address is an SGPR pair. A vector
 ALU instruction that writes an SGPR (readfirstlane, readlane, a compare into an SGPR pair) must come at least five
 wait states before a memory instruction that reads it; the same walk-back checks that rule for every load that names
 an SGPR base.
@@ -110,11 +110,11 @@ def _device_asm(tmp_path, source):
 @pytest.mark.parametrize("source", SOURCES)
 def test_hand_written_instructions_respect_their_wait_states(tmp_path, source):
     asm = _device_asm(tmp_path, source)
-    checked, bad = dpp_hazards(asm)
-    assert checked > 0
+    dpp_checked, bad = dpp_hazards(asm)
     assert not bad, f"{len(bad)} DPP hazards, e.g. {bad[:3]}"
-    checked, bad = sgpr_base_hazards(asm)
+    sgpr_checked, bad = sgpr_base_hazards(asm)
     assert not bad, f"{len(bad)} SGPR-base hazards, e.g. {bad[:3]}"
+    assert dpp_checked + sgpr_checked > 0  # the walk found the hand-written instructions it is meant to check
 
 
 def test_the_checkers_find_a_hazard():
