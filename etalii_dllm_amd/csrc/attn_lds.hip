@@ -10,10 +10,10 @@
 // The products with a double factor are not exact, so they are a rounded multiply and a rounded add, as the
 // reference computes them (grad.hpp:262-301, nn.hpp:535-569); attn_tile_kernel runs them on the vector ALU.
 //
-// attn_tile_kernel mapping: a wave owns 16 consecutive rows (its A values broadcast to all 64 lanes) by 64 CJ
-// columns (CJ per lane). A stage is 16 consecutive l: the workgroup's A (16 l x 64 rows) and B (16 l x 64 CJ
-// columns) are copied global -> LDS with gfx950's direct-to-LDS loads while the previous stage is computed. The
-// broadcast is the DPP64 row_newbcast modifier on a 64-bit move feeding the multiply.
+// attn_tile_kernel mapping: a wave owns 16 consecutive rows by 64 CJ columns; each lane holds a 4-row x 4 CJ-column
+// register tile, so the LDS bytes read per multiply-add are few (the vector ALU, not the LDS, sets the pace). A stage
+// is 16 consecutive l: the workgroup's A (16 l x 64 rows) and B (16 l x 64 CJ columns) are copied global -> LDS with
+// gfx950's direct-to-LDS loads while the previous stage is computed.
 // Causal rows have ragged spans: stages inside every row's span of the wave run unpredicated; at the ragged ends
 // each (row, l) is taken only when l lies in that row's span (a wave-uniform test), so every row adds exactly its
 // own steps, in order, and nothing else. Tiles are dispatched longest reduction first.
@@ -137,90 +137,57 @@ __device__ __forceinline__ void issue_stage(Stage<CJ>& st, const double* a_base,
     }
 }
 
+// A lane's register tile: 4 consecutive rows (4 rg .. 4 rg + 3 of the wave's 16, rg = lane / 16) by 4 CJ columns
+// (CJ groups of 4: columns 64 c + 4 cg .. 64 c + 4 cg + 3, cg = lane % 16). Per step a lane reads its 4 A values
+// (two 16-byte LDS reads shared by 16 lanes) and its 4 CJ B values (CJ 16-byte reads, each a contiguous 256 bytes
+// over the 16 column groups): 32 + 16 CJ bytes per lane for 16 CJ multiply-adds.
 template <int CJ>
-struct RowOperands {
-    double a;
-    float b[CJ];
-};
-
-template <int CJ>
-__device__ __forceinline__ RowOperands<CJ> read_row(const Stage<CJ>& st, int k, int wave, int lane) {
-    RowOperands<CJ> r;
-    r.a = st.a[k][wave * 16 + (lane & 15)];
-    if constexpr (CJ == 2) {
-        const float2 v = *reinterpret_cast<const float2*>(&st.b[k][lane * 2]);
-        r.b[0] = v.x;
-        r.b[1] = v.y;
-    } else {
-        r.b[0] = st.b[k][lane];
+__device__ __forceinline__ void read_step(const Stage<CJ>& st, int k, int wave, int rg, int cg, double (&a)[4],
+                                          double (&b)[4 * CJ]) {
+    const double2* ar = reinterpret_cast<const double2*>(&st.a[k][wave * 16 + 4 * rg]);
+    const double2 a01 = ar[0], a23 = ar[1];
+    a[0] = a01.x;
+    a[1] = a01.y;
+    a[2] = a23.x;
+    a[3] = a23.y;
+#pragma unroll
+    for (int c = 0; c < CJ; ++c) {
+        const float4 v = *reinterpret_cast<const float4*>(&st.b[k][64 * c + 4 * cg]);
+        b[4 * c] = v.x;
+        b[4 * c + 1] = v.y;
+        b[4 * c + 2] = v.z;
+        b[4 * c + 3] = v.w;
     }
-    return r;
 }
 
-// A[l][rows Q .. Q + 3] in every lane (DPP64 moves); the wait states before the first move as above.
-template <int Q>
-__device__ __forceinline__ void broadcast_rows4(double a, double (&r)[4]) {
-    asm volatile("s_nop 1\n\t"
-                 "v_mov_b64_dpp %0, %4 row_newbcast:%5 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_mov_b64_dpp %1, %4 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_mov_b64_dpp %2, %4 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_mov_b64_dpp %3, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf"
-                 : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-                 : "v"(a), "n"(Q), "n"(Q + 1), "n"(Q + 2), "n"(Q + 3));
-}
-
-// One step for the wave's 16 rows; kAll: every row takes it, otherwise row q only when `take` has bit q. The
-// broadcast moves are DPP instructions: they read their source two wait states after its last vector write (the
-// s_nop 1 in broadcast_rows4; tests/test_dpp_hazards.py checks the built code).
-template <int CJ, bool kAll, int Q>
-__device__ __forceinline__ void step_rows(double (&acc)[16][CJ], double a, const double (&b)[CJ], uint32_t take) {
-    if constexpr (Q < 16) {
-        double aq[4];
-        broadcast_rows4<Q>(a, aq);
+// One step on the lane's tile: each product rounded, then added (the reference's multiply, then add).
+template <int CJ>
+__device__ __forceinline__ void step_tile(double (&acc)[4][4 * CJ], const double (&a)[4], const double (&b)[4 * CJ]) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (kAll || (take >> (Q + k)) & 1u) {
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int c = 0; c < CJ; ++c) {
-                    const double prod = aq[k] * b[c];
-                    acc[Q + k][c] = acc[Q + k][c] + prod;
-                }
-            }
+        for (int c = 0; c < 4 * CJ; ++c) {
+            const double prod = a[i] * b[c];
+            acc[i][c] = acc[i][c] + prod;
         }
-        step_rows<CJ, kAll, Q + 4>(acc, a, b, take);
-    }
 }
 
+// A full stage (every row takes every step), the next step's operands read while the current step computes.
 template <int CJ>
-__device__ __forceinline__ void widen(const RowOperands<CJ>& r, double (&b)[CJ]) {
-#pragma unroll
-    for (int c = 0; c < CJ; ++c) b[c] = r.b[c];
-}
-
-// A full stage (every row takes every step): the wave's 16 A values of a step are read from LDS at one address for
-// all lanes (a broadcast, on the LDS pipe), so the vector ALU issues only the conversions and the multiply-adds.
-template <int CJ>
-__device__ __forceinline__ void stage_all(const Stage<CJ>& st, int wave, int lane, double (&acc)[16][CJ]) {
+__device__ __forceinline__ void stage_all(const Stage<CJ>& st, int wave, int rg, int cg, double (&acc)[4][4 * CJ]) {
+    double a[4], b[4 * CJ];
+    read_step<CJ>(st, 0, wave, rg, cg, a, b);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        const RowOperands<CJ> r = read_row<CJ>(st, k, wave, lane);
-        double b[CJ];
-        widen<CJ>(r, b);
-        const double2* ar = reinterpret_cast<const double2*>(&st.a[k][wave * 16]);
-        double aq[16];
+        double an[4], bn[4 * CJ];
+        if (k + 1 < kChunk) read_step<CJ>(st, k + 1, wave, rg, cg, an, bn);
+        step_tile<CJ>(acc, a, b);
+        if (k + 1 < kChunk) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const double2 v = ar[q];
-            aq[2 * q] = v.x;
-            aq[2 * q + 1] = v.y;
+            for (int i = 0; i < 4; ++i) a[i] = an[i];
+#pragma unroll
+            for (int c = 0; c < 4 * CJ; ++c) b[c] = bn[c];
         }
-#pragma unroll
-        for (int q = 0; q < 16; ++q)
-#pragma unroll
-            for (int c = 0; c < CJ; ++c) {
-                const double prod = aq[q] * b[c];
-                acc[q][c] = acc[q][c] + prod;
-            }
     }
 }
 
@@ -243,17 +210,28 @@ __device__ __forceinline__ uint32_t rows_taking(const TileParams& p, int64_t l, 
     return upto & ~((1u << qa) - 1u);
 }
 
-// Steps l0 .. l0 + n - 1 of a stage, each taken by the rows whose span holds it.
+// Steps l0 .. l0 + n - 1 of a stage, each taken by the rows whose span holds it (the lane's rows: bits 4 rg .. 4 rg + 3
+// of the wave's mask).
 template <int CJ>
-__device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ>& st, int wave, int lane, int64_t l0,
-                                             int n, int64_t tw, int64_t rows_n, int64_t I, double (&acc)[16][CJ]) {
+__device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ>& st, int wave, int rg, int cg,
+                                             int64_t l0, int n, int64_t tw, int64_t rows_n, int64_t I,
+                                             double (&acc)[4][4 * CJ]) {
     for (int k = 0; k < n; ++k) {
         const uint32_t take = __builtin_amdgcn_readfirstlane(rows_taking(p, l0 + k, tw, rows_n, I));
         if (take == 0) continue;
-        const RowOperands<CJ> r = read_row<CJ>(st, k, wave, lane);
-        double b[CJ];
-        widen<CJ>(r, b);
-        step_rows<CJ, false, 0>(acc, r.a, b, take);
+        double a[4], b[4 * CJ];
+        read_step<CJ>(st, k, wave, rg, cg, a, b);
+        const uint32_t mine = take >> (4 * rg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if ((mine >> i) & 1u) {
+#pragma unroll
+                for (int c = 0; c < 4 * CJ; ++c) {
+                    const double prod = a[i] * b[c];
+                    acc[i][c] = acc[i][c] + prod;
+                }
+            }
+        }
     }
 }
 
@@ -296,11 +274,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     const float* B = op_base<float>(o.B, w, seg_w, hz);
     const int64_t chunk = j0 + 4 * (lane % (16 * CJ));
     const int64_t b_col = chunk + 4 <= p.b_row_alloc ? chunk : p.b_row_alloc - 4;
-    double acc[16][CJ];
+    const int rg = lane >> 4, cg = lane & 15;
+    double acc[4][4 * CJ];
 #pragma unroll
-    for (int q = 0; q < 16; ++q)
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int c = 0; c < CJ; ++c) acc[q][c] = 0.0;
+        for (int c = 0; c < 4 * CJ; ++c) acc[q][c] = 0.0;
     const int64_t steps = t_hi - t_lo;
     const int64_t stages = steps > 0 ? (steps + kChunk - 1) / kChunk : 0;
     const int64_t last = t_hi - 1;
@@ -315,9 +294,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
         const int64_t l0 = t_lo + s * kChunk;
         const int n_steps = static_cast<int>(t_hi - l0 < kChunk ? t_hi - l0 : kChunk);
         if (n_steps == kChunk && l0 >= w_lo && l0 + kChunk <= w_hi)
-            stage_all<CJ>(st[s & 1], wave, lane, acc);
+            stage_all<CJ>(st[s & 1], wave, rg, cg, acc);
         else
-            stage_masked<CJ>(p, st[s & 1], wave, lane, l0, n_steps, tw, n, I, acc);
+            stage_masked<CJ>(p, st[s & 1], wave, rg, cg, l0, n_steps, tw, n, I, acc);
         workgroup_barrier();  // every wave is done with this stage before the next issue refills it
     }
     // the output rows' base and stride, opaque so the compiler keeps no per-element addresses across the reduction
@@ -327,14 +306,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     asm volatile("" : "+s"(c_base), "+s"(c_ld));
     const double* rs = p.rowscale ? p.rowscale + z * p.rowscale_zstride + tw : nullptr;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+    for (int i = 0; i < 4; ++i) {
+        const int q = 4 * rg + i;
         if (tw + q >= I) break;
+        const double scale = rs ? rs[q] : 1.0;
 #pragma unroll
-        for (int c = 0; c < CJ; ++c) {
-            const int64_t jl = lane * CJ + c;
+        for (int c = 0; c < 4 * CJ; ++c) {
+            const int64_t jl = 64 * (c >> 2) + 4 * cg + (c & 3);
             if (j0 + jl >= J) continue;
-            double v = acc[q][c];
-            if (rs) v = v * rs[q];
+            double v = acc[i][c];
+            if (rs) v = v * scale;
             c_base[q * c_ld + jl] = static_cast<float>(v);
         }
     }

@@ -623,6 +623,57 @@ struct dllm_hip_trainer {
         return kOk;
     }
 
+    // The q, k and v projections of every layer read the same h1: one grouped launch per layer runs all three (their
+    // tiles together fill the chip; k and v alone are 2 x 64 tiles at the c3 shapes). Each output's bits are those of
+    // its own launch. The tables depend on the row count R and are rebuilt (after the stream drains) when it changes.
+    char* qkv_tables = nullptr;
+    std::vector<GemmGroup> qkv_groups;
+    int64_t qkv_rows = -1;
+    bool qkv_grouped = false;
+
+    int prepare_qkv_groups(int64_t R, hipStream_t s) {
+        if (R == qkv_rows) return kOk;
+        const size_t gb = gemm_group_bytes(3);
+        if (qkv_tables == nullptr) DLLM_TRY(make(&qkv_tables, gb * static_cast<size_t>(c.layers)));
+        std::vector<char> host(gb * static_cast<size_t>(c.layers));
+        qkv_groups.assign(static_cast<size_t>(c.layers), GemmGroup{});
+        // the grouped kernel takes whole 16-byte chunks of the operands; other shapes keep one launch per projection
+        qkv_grouped = R > 0 && H % 4 == 0;
+        for (int64_t l = 0; l < c.layers && qkv_grouped; ++l) {
+            const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+            Saved& sv = saved[static_cast<size_t>(l)];
+            const GemmCall calls[3] = {fwd_call(sv.h1, R, H, L.q, Popt(L.qb), sv.q_raw, nullptr),
+                                       fwd_call(sv.h1, R, H, L.k, Popt(L.kb), sv.k_raw, nullptr),
+                                       fwd_call(sv.h1, R, H, L.v, Popt(L.vb), sv.v, nullptr)};
+            for (const GemmCall& g : calls) qkv_grouped = qkv_grouped && g.J % 4 == 0 && g.ldb % 4 == 0;
+            if (!qkv_grouped) break;
+            DLLM_TRY(gemm_group_prepare(calls, 3, 3, host.data() + gb * static_cast<size_t>(l),
+                                        &qkv_groups[static_cast<size_t>(l)]));
+        }
+        if (qkv_grouped) {
+            DLLM_TRY(check_hip(hipStreamSynchronize(s), "qkv tables"));  // no launch still reads the old tables
+            DLLM_TRY(check_hip(hipMemcpy(qkv_tables, host.data(), host.size(), hipMemcpyHostToDevice), "upload"));
+        }
+        qkv_rows = R;
+        return kOk;
+    }
+
+    int qkv_forward(int64_t l, int64_t R, hipStream_t s) {
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        Saved& sv = saved[static_cast<size_t>(l)];
+        if (qkv_grouped && qkv_rows == R) {
+            const double flops = 2.0 * static_cast<double>(R) * static_cast<double>(H) *
+                                 static_cast<double>(tensors[static_cast<size_t>(L.q)].rows +
+                                                     tensors[static_cast<size_t>(L.k)].rows +
+                                                     tensors[static_cast<size_t>(L.v)].rows);
+            return gemm_group(qkv_groups[static_cast<size_t>(l)], qkv_tables + gemm_group_bytes(3) * static_cast<size_t>(l),
+                              flops, s);
+        }
+        DLLM_TRY(linear_fwd(sv.h1, R, H, L.q, Popt(L.qb), sv.q_raw, nullptr, s));
+        DLLM_TRY(linear_fwd(sv.h1, R, H, L.k, Popt(L.kb), sv.k_raw, nullptr, s));
+        return linear_fwd(sv.h1, R, H, L.v, Popt(L.vb), sv.v, nullptr, s);
+    }
+
     // out[R][N] (+)= x[R][K] @ W^T (+ bias); the matmul reads x itself (A transposed: A[k][r] = x[r][k]).
     int linear_fwd(const float* x, int64_t R, int64_t K, int w_id, const float* bias, float* out, const float* addsrc,
                    hipStream_t s) {
@@ -772,7 +823,9 @@ struct dllm_hip_trainer {
     }
 
     // Columns per lane of the head_dim-wide attention outputs: whole 64-column tiles of head_dim.
-    int value_cols_per_lane() const { return c.head_dim > 64 ? 2 : 1; }
+    // 64-column tiles for every head_dim: their 4 x 4 register tiles leave room for four waves per SIMD (the 4 x 8
+    // tiles of 128 columns hold two), which keeps the vector ALU busier than the halved A reuse costs
+    int value_cols_per_lane() const { return 1; }
 
     // attention_backward (grad.hpp:206-301) of every (window, head): dq_t, dk_t, dv_t from dattended.
     int attention_backward(int64_t l, const Saved& sv, const AttentionBatch& b, hipStream_t s) {
@@ -842,9 +895,7 @@ struct dllm_hip_trainer {
         Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
         DLLM_TRY(launch_rms_norm(sv.x_in, P(L.attn_norm), sv.h1, R, H, eps, 0, nullptr, s));
-        DLLM_TRY(linear_fwd(sv.h1, R, H, L.q, Popt(L.qb), sv.q_raw, nullptr, s));
-        DLLM_TRY(linear_fwd(sv.h1, R, H, L.k, Popt(L.kb), sv.k_raw, nullptr, s));
-        DLLM_TRY(linear_fwd(sv.h1, R, H, L.v, Popt(L.vb), sv.v, nullptr, s));
+        DLLM_TRY(qkv_forward(l, R, s));
         const float* qsrc = sv.q_raw;
         const float* ksrc = sv.k_raw;
         if (c.qk_norm == 2) {
@@ -1170,6 +1221,7 @@ struct dllm_hip_trainer {
             DLLM_TRY(prepare_lora(s));
         else if (!wt_valid)
             DLLM_TRY(refresh_transposes(s));
+        DLLM_TRY(prepare_qkv_groups(R, s));
         const int nseg = static_cast<int>(windows);
         nwin = windows;
         router_scale_cur = router_scale;
