@@ -326,7 +326,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
 //
 // v_mfma_f64_16x16x4_f64 adds its four products to the accumulator as four FMAs in ascending k, each rounded: one
 // instruction per 4 consecutive l is the serial chain over l = 0 .. head_dim - 1 that the vector FMAs computed
-// (head_dim is a multiple of 4, so no step is padded). Same tiles as attn_tile_kernel<4, true, true, *>: 64 rows
+// (head_dim is a multiple of 4, so no step is padded). 64 rows
 // (keys) x 256 columns (queries); the 4 waves sit side by side along the columns, each owning 64 x 64 outputs as
 // 4 x 4 MFMA blocks. A stage is 16 l: A as [l / 4][row][l % 4] (one 16-byte copy per thread) and B as [l][column]
 // (four per thread).

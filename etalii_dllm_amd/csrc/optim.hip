@@ -55,7 +55,22 @@ __global__ void sum_squares_kernel(const float* __restrict__ x, int64_t n, doubl
     *out = chain_squares(x, n);
 }
 
-// adamw_step (grad.hpp:484-494) on chunk c = blockIdx.y-major tiles of the arena.
+// One element of adamw_step (grad.hpp:484-494): g = grad * scale; m, v updated and rounded to float; the parameter
+// from the rounded moments.
+__device__ __forceinline__ void adamw_element(float& param, float grad, float& m, float& v, double gs, double decay,
+                                              const AdamWArgs& a) {
+    const double g = static_cast<double>(grad) * gs;
+    const float m_new = static_cast<float>(a.beta1 * static_cast<double>(m) + (1.0 - a.beta1) * g);
+    const float v_new = static_cast<float>(a.beta2 * static_cast<double>(v) + (1.0 - a.beta2) * g * g);
+    m = m_new;
+    v = v_new;
+    const double m_hat = static_cast<double>(m_new) / a.bc1;
+    const double v_hat = static_cast<double>(v_new) / a.bc2;
+    param = static_cast<float>(static_cast<double>(param) * decay - a.lr * m_hat / (sqrt(v_hat) + a.eps));
+}
+
+// adamw_step on chunk c = one workgroup's range [chunk_start, chunk_end) of the arena: 16-byte vectors of the four
+// arrays where the range starts on one (every arena tensor does), then the range's last elements one by one.
 __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ param, const float* __restrict__ grad,
                                                     float* __restrict__ m, float* __restrict__ v,
                                                     const int64_t* __restrict__ chunk_start,
@@ -66,16 +81,25 @@ __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ param, c
     const int64_t i0 = chunk_start[c], i1 = chunk_end[c];
     const double gs = grad_scale_dev ? grad_scale_dev[0] : a.grad_scale;
     const double decay = 1.0 - a.lr * chunk_decay[c];
-    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
-        const double g = static_cast<double>(grad[i]) * gs;
-        const float m_new = static_cast<float>(a.beta1 * static_cast<double>(m[i]) + (1.0 - a.beta1) * g);
-        const float v_new = static_cast<float>(a.beta2 * static_cast<double>(v[i]) + (1.0 - a.beta2) * g * g);
-        m[i] = m_new;
-        v[i] = v_new;
-        const double m_hat = static_cast<double>(m_new) / a.bc1;
-        const double v_hat = static_cast<double>(v_new) / a.bc2;
-        param[i] = static_cast<float>(static_cast<double>(param[i]) * decay - a.lr * m_hat / (sqrt(v_hat) + a.eps));
+    const bool aligned = ((reinterpret_cast<uintptr_t>(param + i0) | reinterpret_cast<uintptr_t>(grad + i0) |
+                           reinterpret_cast<uintptr_t>(m + i0) | reinterpret_cast<uintptr_t>(v + i0)) & 15) == 0;
+    const int64_t n4 = aligned ? (i1 - i0) >> 2 : 0;
+    float4* p4 = reinterpret_cast<float4*>(param + i0);
+    const float4* g4 = reinterpret_cast<const float4*>(grad + i0);
+    float4* m4 = reinterpret_cast<float4*>(m + i0);
+    float4* v4 = reinterpret_cast<float4*>(v + i0);
+    for (int64_t q = threadIdx.x; q < n4; q += 256) {
+        float4 pp = p4[q], mm = m4[q], vv = v4[q];
+        const float4 gg = g4[q];
+        adamw_element(pp.x, gg.x, mm.x, vv.x, gs, decay, a);
+        adamw_element(pp.y, gg.y, mm.y, vv.y, gs, decay, a);
+        adamw_element(pp.z, gg.z, mm.z, vv.z, gs, decay, a);
+        adamw_element(pp.w, gg.w, mm.w, vv.w, gs, decay, a);
+        m4[q] = mm;
+        v4[q] = vv;
+        p4[q] = pp;
     }
+    for (int64_t i = i0 + 4 * n4 + threadIdx.x; i < i1; i += 256) adamw_element(param[i], grad[i], m[i], v[i], gs, decay, a);
 }
 
 // adamw_step over one tensor of n elements (a single weight decay).

@@ -5,6 +5,8 @@
 // by lane 0 of the row's wave, in index order, after the other lanes are done loading; the per-element work around
 // them is spread over the 64 lanes. Every float32 glue operation is one IEEE float op per element, in the
 // reference's operand order.
+#include <initializer_list>
+
 #include "common.h"
 #include "devmath.h"
 #include "kernels.h"
@@ -346,6 +348,38 @@ __global__ __launch_bounds__(256) void swiglu_forward_kernel(const float* __rest
     }
 }
 
+// The same two kernels on 16-byte vectors (four independent elements per thread in flight), for 16-byte aligned
+// arrays; the launchers run the scalar kernels on the last n % 4 elements.
+__device__ __forceinline__ float4 load4(const float* p, int64_t q) { return reinterpret_cast<const float4*>(p)[q]; }
+__device__ __forceinline__ void store4(float* p, int64_t q, float4 v) { reinterpret_cast<float4*>(p)[q] = v; }
+
+__global__ __launch_bounds__(256) void swiglu_forward4_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                              float* __restrict__ gate_act, float* __restrict__ product,
+                                                              int64_t n4) {
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; q < n4;
+         q += static_cast<int64_t>(gridDim.x) * 256) {
+        const float4 g = load4(gate, q), u = load4(up, q);
+        const float4 a = {dsilu(g.x), dsilu(g.y), dsilu(g.z), dsilu(g.w)};
+        if (gate_act) store4(gate_act, q, a);
+        store4(product, q, float4{a.x * u.x, a.y * u.y, a.z * u.z, a.w * u.w});
+    }
+}
+
+__global__ __launch_bounds__(256) void swiglu_backward4_kernel(const float* __restrict__ gate,
+                                                               const float* __restrict__ up,
+                                                               const float* __restrict__ gate_act,
+                                                               const float* __restrict__ dproduct,
+                                                               float* __restrict__ dgate, float* __restrict__ dup,
+                                                               int64_t n4) {
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; q < n4;
+         q += static_cast<int64_t>(gridDim.x) * 256) {
+        const float4 dp = load4(dproduct, q), u = load4(up, q), g = load4(gate, q), a = load4(gate_act, q);
+        store4(dgate, q, float4{dsilu_backward(g.x, dp.x * u.x), dsilu_backward(g.y, dp.y * u.y),
+                                dsilu_backward(g.z, dp.z * u.z), dsilu_backward(g.w, dp.w * u.w)});
+        store4(dup, q, float4{dp.x * a.x, dp.y * a.y, dp.z * a.z, dp.w * a.w});
+    }
+}
+
 __global__ __launch_bounds__(256) void silu_backward_kernel(const float* __restrict__ x, const float* __restrict__ dy,
                                                             float* __restrict__ out, int64_t n) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
@@ -404,6 +438,13 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restric
     if (r >= rows) return;
     const float* src = table + index[r] * dim;
     for (int64_t i = threadIdx.x; i < dim; i += 256) out[r * dim + i] = src[i];
+}
+
+// Every non-null pointer 16-byte aligned.
+bool aligned16(std::initializer_list<const float*> ptrs) {
+    for (const float* p : ptrs)
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+    return true;
 }
 
 unsigned elementwise_grid(int64_t n) {
@@ -492,8 +533,14 @@ int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream) {
 int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
                           hipStream_t stream) {
     if (n == 0) return kOk;
-    hipLaunchKernelGGL(swiglu_forward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, gate, up, gate_act,
-                       product, n);
+    const int64_t n4 = aligned16({gate, up, gate_act, product}) ? n / 4 : 0;
+    if (n4 > 0)
+        hipLaunchKernelGGL(swiglu_forward4_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, stream, gate, up,
+                           gate_act, product, n4);
+    const int64_t d = 4 * n4;
+    if (n > d)
+        hipLaunchKernelGGL(swiglu_forward_kernel, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
+                           up + d, gate_act ? gate_act + d : nullptr, product + d, n - d);
     return check_launch("swiglu");
 }
 
@@ -518,8 +565,14 @@ int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
                            float* dgate, float* dup, int64_t n, hipStream_t stream) {
     if (n == 0) return kOk;
-    hipLaunchKernelGGL(swiglu_backward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, gate, up, gate_act,
-                       dproduct, dgate, dup, n);
+    const int64_t n4 = aligned16({gate, up, gate_act, dproduct, dgate, dup}) ? n / 4 : 0;
+    if (n4 > 0)
+        hipLaunchKernelGGL(swiglu_backward4_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, stream, gate, up,
+                           gate_act, dproduct, dgate, dup, n4);
+    const int64_t d = 4 * n4;
+    if (n > d)
+        hipLaunchKernelGGL(swiglu_backward_kernel, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
+                           up + d, gate_act + d, dproduct + d, dgate + d, dup + d, n - d);
     return check_launch("swiglu_backward");
 }
 
