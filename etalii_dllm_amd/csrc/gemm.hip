@@ -842,6 +842,29 @@ __global__ __launch_bounds__(256) void transpose_batch_kernel(const TransposeJob
     const int64_t t = id - tile_start[lo];
     const int64_t tiles_c = (jb.cols + 63) / 64;
     const int64_t r0 = t / tiles_c * 64, c0 = t % tiles_c * 64;
+    if (jb.rows % 4 == 0 && jb.cols % 4 == 0 &&
+        ((reinterpret_cast<uintptr_t>(jb.src) | reinterpret_cast<uintptr_t>(jb.dst)) & 15) == 0) {
+        // 16-byte vectors both ways: thread (row k, column group g) reads src[r0 + k][c0 + 4g .. + 3], then writes
+        // dst[c0 + k][r0 + 4g .. + 3]; with both sizes multiples of 4 a vector is wholly inside or outside
+        const int g = threadIdx.x & 15, k0 = threadIdx.x >> 4;
+        for (int k = k0; k < 64; k += 16) {
+            const int64_t r = r0 + k, c = c0 + 4 * g;
+            float4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (r < jb.rows && c < jb.cols) v = *reinterpret_cast<const float4*>(jb.src + r * jb.cols + c);
+            tile[k][4 * g] = v.x;
+            tile[k][4 * g + 1] = v.y;
+            tile[k][4 * g + 2] = v.z;
+            tile[k][4 * g + 3] = v.w;
+        }
+        __syncthreads();
+        for (int k = k0; k < 64; k += 16) {
+            const int64_t c = c0 + k, r = r0 + 4 * g;
+            if (c < jb.cols && r < jb.rows)
+                *reinterpret_cast<float4*>(jb.dst + c * jb.rows + r) =
+                    float4{tile[4 * g][k], tile[4 * g + 1][k], tile[4 * g + 2][k], tile[4 * g + 3][k]};
+        }
+        return;
+    }
     const int tx = threadIdx.x & 63;
     const int ty = threadIdx.x >> 6;
     for (int k = ty; k < 64; k += 4) {
