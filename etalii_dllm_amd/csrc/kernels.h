@@ -191,7 +191,8 @@ int launch_norm_finish(const double* per_tensor, int64_t tensors, double max_gra
                        hipStream_t stream);
 
 // ---- exact parallel sum of squares (sumsq.hip) ----
-// Tensors of one arena split into fixed blocks; the plan arrays live in device memory.
+// Tensors of one arena split into fixed blocks of kSumSquaresBlock values; the plan arrays live in device memory.
+constexpr int64_t kSumSquaresBlock = 8192;
 struct ExactSumPlan {
     int64_t tensors = 0, blocks = 0;
     const int64_t* tfirst = nullptr;   // [tensors] first block of each tensor

@@ -28,7 +28,7 @@ namespace dllm_hip {
 
 namespace {
 
-constexpr int kBlockElems = 8192;  // 256 threads x 32 consecutive elements
+constexpr int kBlockElems = static_cast<int>(kSumSquaresBlock);  // 256 threads x 32 consecutive elements
 constexpr int64_t kTop = (1LL << 53) - 1;
 
 // A parity function: for incoming parity p, add d[p] to M and leave parity par[p].

@@ -125,6 +125,13 @@ size_t dllm_hip_sum_squares_workspace(size_t n);
 int dllm_hip_sum_squares(const float* values, size_t n, double* result, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* sum_squares without a workspace and without any allocation: the same bits as dllm_hip_sum_squares, its scratch
+ * (plan, block sums, block functions, result) in a fixed 4 MiB device array that each GPU holds until the process
+ * ends. n is at most 2^29 (larger is an invalid argument, refused before any launch). Calls that overlap on one GPU
+ * race on that array. No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under graph capture, tight serving loops, harnesses that forbid hipMalloc). Waits for the stream. */
+int dllm_hip_sum_squares_noalloc(const float* values, size_t n, double* result, void* stream);
+
 /* One in-place AdamW step. Replaces kernels.cpp:1045-1057 `adamw_step` (grad.hpp:481-495). */
 int dllm_hip_adamw_step(float* param, const float* grad, float* m, float* v, size_t n, double lr, double beta1,
                         double beta2, double eps, double weight_decay, double bias_correction1,
