@@ -100,12 +100,13 @@ __device__ __forceinline__ double first_max(const double* sc, int64_t count, int
     return __shfl(best, 0, 64);
 }
 
-// Forward (nn.hpp:535-569, 574-615). Dynamic LDS: max_kv doubles per wave.
+// Forward (nn.hpp:535-569, 574-615). The row's scores are staged in dynamic LDS (max_kv doubles per wave) or, for key
+// lengths past kMaxKvLds, in the row's slice of `stage` (max_kv doubles per (query, head) row).
 __global__ __launch_bounds__(64) void attention_forward_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                                const float* __restrict__ v, float* __restrict__ out,
-                                                               AttentionShape sh, AttentionBatch b) {
+                                                               AttentionShape sh, AttentionBatch b, double* stage) {
     extern __shared__ double lds[];
-    double* sc = lds;
+    double* sc = stage ? stage + static_cast<int64_t>(blockIdx.x) * b.max_kv : lds;
     const int lane = threadIdx.x;
     const int64_t packed_q = blockIdx.x / sh.q_heads;
     const int64_t h = blockIdx.x % sh.q_heads;
@@ -142,19 +143,21 @@ __global__ __launch_bounds__(64) void attention_forward_kernel(const float* __re
 }
 
 // Pass A of the backward (grad.hpp:221-292 per row): dq, plus p and ds per visible key into the workspace rows
-// (indexed by sequence-local key), for pass B. Dynamic LDS: 3 * max_kv doubles.
+// (indexed by sequence-local key), for pass B. Staging: 3 * max_kv doubles of dynamic LDS, or (key lengths past
+// kMaxKvLds) the row's 3 * max_kv doubles of `stage`.
 __global__ __launch_bounds__(64) void attention_backward_rows_kernel(const float* __restrict__ q,
                                                                      const float* __restrict__ k,
                                                                      const float* __restrict__ v,
                                                                      const float* __restrict__ dout,
                                                                      float* __restrict__ dq, double* __restrict__ P,
                                                                      double* __restrict__ DS, AttentionShape sh,
-                                                                     AttentionBatch b) {
+                                                                     AttentionBatch b, double* stage) {
     extern __shared__ double lds[];
     const int lane = threadIdx.x;
-    double* pr = lds;                 // scores, then probabilities
-    double* dpr = lds + b.max_kv;     // dp, then ds
-    double* slope = lds + 2 * b.max_kv;
+    double* base = stage ? stage + static_cast<int64_t>(blockIdx.x) * 3 * b.max_kv : lds;
+    double* pr = base;                 // scores, then probabilities
+    double* dpr = base + b.max_kv;     // dp, then ds
+    double* slope = base + 2 * b.max_kv;
     const int64_t packed_q = blockIdx.x / sh.q_heads;
     const int64_t h = blockIdx.x % sh.q_heads;
     const RowRef ref = locate(b, sh.q_heads, packed_q);
@@ -248,19 +251,27 @@ __global__ __launch_bounds__(64) void attention_backward_keys_kernel(const float
     }
 }
 
-constexpr int64_t kMaxKvLds = 2048;  // pass A stages 3 doubles per key in LDS (48 KB)
+constexpr int64_t kMaxKvLds = 2048;  // LDS staging up to here (pass A: 3 doubles per key, 48 KB)
+
+size_t rows_of(const AttentionShape& s) { return static_cast<size_t>(s.q_len) * static_cast<size_t>(s.q_heads); }
 
 }  // namespace
 
+size_t attention_stage_bytes(const AttentionShape& s, const AttentionBatch& b, bool backward) {
+    if (b.max_kv <= kMaxKvLds) return 0;
+    return rows_of(s) * static_cast<size_t>(b.max_kv) * sizeof(double) * (backward ? 3 : 1);
+}
+
 int launch_attention(const float* q, const float* k, const float* v, float* out, const AttentionShape& s,
-                     const AttentionBatch& b, hipStream_t stream) {
+                     const AttentionBatch& b, void* stage, hipStream_t stream) {
     DLLM_REQUIRE(s.kv_heads > 0 && s.q_heads % s.kv_heads == 0, "q_heads must be a multiple of kv_heads");
-    DLLM_REQUIRE(b.max_kv <= kMaxKvLds, "attention supports key lengths up to 2048 per sequence");
+    DLLM_REQUIRE(b.max_kv <= kMaxKvLds || stage != nullptr, "attention past 2048 keys needs its staging workspace");
     const int64_t total_q = s.q_len;  // packed queries of all sequences
     if (total_q == 0 || s.q_heads == 0) return kOk;
-    const size_t lds = static_cast<size_t>(b.max_kv > 0 ? b.max_kv : 1) * sizeof(double);
+    const bool in_lds = b.max_kv <= kMaxKvLds;
+    const size_t lds = in_lds ? static_cast<size_t>(b.max_kv > 0 ? b.max_kv : 1) * sizeof(double) : 0;
     hipLaunchKernelGGL(attention_forward_kernel, dim3(static_cast<unsigned>(total_q * s.q_heads)), dim3(64), lds,
-                       stream, q, k, v, out, s, b);
+                       stream, q, k, v, out, s, b, in_lds ? nullptr : static_cast<double*>(stage));
     return check_launch("attention");
 }
 
@@ -271,15 +282,16 @@ size_t attention_backward_workspace(const AttentionShape& s, const AttentionBatc
 
 int launch_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,
                               float* dv, const AttentionShape& s, const AttentionBatch& b, int64_t total_q,
-                              int64_t total_kv, void* workspace, hipStream_t stream) {
+                              int64_t total_kv, void* workspace, void* stage, hipStream_t stream) {
     DLLM_REQUIRE(s.kv_heads > 0 && s.q_heads % s.kv_heads == 0, "q_heads must be a multiple of kv_heads");
-    DLLM_REQUIRE(b.max_kv <= kMaxKvLds, "attention supports key lengths up to 2048 per sequence");
+    DLLM_REQUIRE(b.max_kv <= kMaxKvLds || stage != nullptr, "attention past 2048 keys needs its staging workspace");
     double* P = static_cast<double*>(workspace);
     double* DS = P + static_cast<size_t>(total_q) * s.q_heads * (b.max_kv > 0 ? b.max_kv : 1);
     if (total_q > 0 && s.q_heads > 0) {
-        const size_t lds = static_cast<size_t>(b.max_kv > 0 ? b.max_kv : 1) * sizeof(double) * 3;
+        const bool in_lds = b.max_kv <= kMaxKvLds;
+        const size_t lds = in_lds ? static_cast<size_t>(b.max_kv > 0 ? b.max_kv : 1) * sizeof(double) * 3 : 0;
         hipLaunchKernelGGL(attention_backward_rows_kernel, dim3(static_cast<unsigned>(total_q * s.q_heads)), dim3(64),
-                           lds, stream, q, k, v, dout, dq, P, DS, s, b);
+                           lds, stream, q, k, v, dout, dq, P, DS, s, b, in_lds ? nullptr : static_cast<double*>(stage));
         DLLM_TRY(check_launch("attention_backward_rows"));
     }
     if (total_kv > 0 && s.kv_heads > 0) {

@@ -121,12 +121,6 @@ int dllm_hip_rope(const float* x, const int64_t* positions, const double* inv_fr
                        static_cast<int64_t>(head_dim), static_cast<int64_t>(rotary_dim), interleaved, inverse, s);
 }
 
-size_t dllm_hip_attention_workspace(void) {
-    Layout l;
-    l.add<AttnBatchStorage>(1);
-    return l.bytes;
-}
-
 static int single_sequence(size_t q_len, size_t kv_len, void* ws, hipStream_t s, AttentionBatch* b) {
     const int64_t host[4] = {0, static_cast<int64_t>(q_len), 0, static_cast<int64_t>(kv_len)};
     int64_t* d = static_cast<int64_t*>(ws);
@@ -156,17 +150,47 @@ static int attention_shape(size_t q_len, size_t kv_len, size_t q_heads, size_t k
     return kOk;
 }
 
+// The row kernels' staging bytes for a call's shape (0 when every row's keys fit in LDS).
+static size_t row_stage_bytes(size_t q_len, size_t kv_len, size_t q_heads, bool backward) {
+    AttentionShape sh{};
+    sh.q_len = static_cast<int64_t>(q_len);
+    sh.q_heads = static_cast<int64_t>(q_heads);
+    AttentionBatch b{};
+    b.max_kv = static_cast<int64_t>(kv_len);
+    return attention_stage_bytes(sh, b, backward);
+}
+
+size_t dllm_hip_attention_workspace(size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads, size_t head_dim,
+                                    size_t value_dim, int causal, int64_t q_offset, size_t window, double softcap) {
+    if (self_attention_fast(q_len, kv_len, q_heads, kv_heads, head_dim, value_dim, causal, q_offset, window, softcap))
+        return self_attention_workspace(q_len, q_heads, kv_heads, head_dim, false);
+    Layout l;
+    l.add<AttnBatchStorage>(1);
+    l.add<char>(row_stage_bytes(q_len, kv_len, q_heads, false));
+    return l.bytes;
+}
+
 int dllm_hip_attention(const float* q, const float* k, const float* v, float* out, size_t q_len, size_t kv_len,
                        size_t q_heads, size_t kv_heads, size_t head_dim, size_t value_dim, double scale, int causal,
                        int64_t q_offset, size_t window, double softcap, void* workspace, size_t workspace_bytes,
                        void* stream) {
-    DLLM_REQUIRE(workspace_bytes >= dllm_hip_attention_workspace(), "workspace too small for attention");
     AttentionShape sh;
     DLLM_TRY(attention_shape(q_len, kv_len, q_heads, kv_heads, head_dim, value_dim, scale, causal, q_offset, window,
                              softcap, &sh));
+    DLLM_REQUIRE(workspace_bytes >= dllm_hip_attention_workspace(q_len, kv_len, q_heads, kv_heads, head_dim, value_dim,
+                                                                 causal, q_offset, window, softcap),
+                 "workspace too small for attention");
+    const hipStream_t s = as_stream(stream);
+    if (self_attention_fast(q_len, kv_len, q_heads, kv_heads, head_dim, value_dim, causal, q_offset, window, softcap))
+        return self_attention_forward(q, k, v, out, q_len, q_heads, kv_heads, head_dim, scale, causal,
+                                      static_cast<int64_t>(window), workspace, s);
+    Carve c(workspace, workspace_bytes);
+    AttnBatchStorage* bs = c.take<AttnBatchStorage>(1);
+    char* stage = c.take<char>(row_stage_bytes(q_len, kv_len, q_heads, false));
+    DLLM_REQUIRE(!c.overflow, "workspace layout overflow");
     AttentionBatch b;
-    DLLM_TRY(single_sequence(q_len, kv_len, workspace, as_stream(stream), &b));
-    return launch_attention(q, k, v, out, sh, b, as_stream(stream));
+    DLLM_TRY(single_sequence(q_len, kv_len, bs, s, &b));
+    return launch_attention(q, k, v, out, sh, b, stage, s);
 }
 
 int dllm_hip_silu(const float* x, float* out, size_t n, void* stream) {
@@ -279,10 +303,15 @@ int dllm_hip_silu_backward(const float* x, const float* dy, float* out, size_t n
     return launch_silu_backward(x, dy, out, static_cast<int64_t>(n), as_stream(stream));
 }
 
-size_t dllm_hip_attention_backward_workspace(size_t q_len, size_t kv_len, size_t q_heads) {
+size_t dllm_hip_attention_backward_workspace(size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads,
+                                             size_t head_dim, size_t value_dim, int causal, int64_t q_offset,
+                                             size_t window, double softcap) {
+    if (self_attention_fast(q_len, kv_len, q_heads, kv_heads, head_dim, value_dim, causal, q_offset, window, softcap))
+        return self_attention_workspace(q_len, q_heads, kv_heads, head_dim, true);
     Layout l;
     l.add<AttnBatchStorage>(1);
     l.add<double>(2 * q_len * q_heads * std::max<size_t>(kv_len, 1));
+    l.add<char>(row_stage_bytes(q_len, kv_len, q_heads, true));
     return l.bytes;
 }
 
@@ -291,20 +320,26 @@ int dllm_hip_attention_backward(const float* q, const float* k, const float* v, 
                                 size_t head_dim, size_t value_dim, double scale, int causal, int64_t q_offset,
                                 size_t window, double softcap, void* workspace, size_t workspace_bytes,
                                 void* stream) {
-    DLLM_REQUIRE(workspace_bytes >= dllm_hip_attention_backward_workspace(q_len, kv_len, q_heads),
-                 "workspace too small for attention_backward");
     AttentionShape sh;
     DLLM_TRY(attention_shape(q_len, kv_len, q_heads, kv_heads, head_dim, value_dim, scale, causal, q_offset, window,
                              softcap, &sh));
+    DLLM_REQUIRE(workspace_bytes >= dllm_hip_attention_backward_workspace(q_len, kv_len, q_heads, kv_heads, head_dim,
+                                                                          value_dim, causal, q_offset, window,
+                                                                          softcap),
+                 "workspace too small for attention_backward");
+    const hipStream_t s = as_stream(stream);
+    if (self_attention_fast(q_len, kv_len, q_heads, kv_heads, head_dim, value_dim, causal, q_offset, window, softcap))
+        return self_attention_backward(q, k, v, dout, dq, dk, dv, q_len, q_heads, kv_heads, head_dim, scale, causal,
+                                       static_cast<int64_t>(window), workspace, s);
     Carve c(workspace, workspace_bytes);
     AttnBatchStorage* bs = c.take<AttnBatchStorage>(1);
     double* pds = c.take<double>(2 * q_len * q_heads * std::max<size_t>(kv_len, 1));
+    char* stage = c.take<char>(row_stage_bytes(q_len, kv_len, q_heads, true));
     DLLM_REQUIRE(!c.overflow, "workspace layout overflow");
     AttentionBatch b;
-    const hipStream_t s = as_stream(stream);
     DLLM_TRY(single_sequence(q_len, kv_len, bs, s, &b));
     return launch_attention_backward(q, k, v, dout, dq, dk, dv, sh, b, static_cast<int64_t>(q_len),
-                                     static_cast<int64_t>(kv_len), pds, s);
+                                     static_cast<int64_t>(kv_len), pds, stage, s);
 }
 
 size_t dllm_hip_cross_entropy_workspace(size_t rows) {

@@ -157,13 +157,29 @@ struct AttentionBatch {
     int64_t max_q, max_kv;    // host bounds of the lengths
 };
 
+// Rows (query, head) whose keys do not fit the kernels' LDS staging (more than 2048) stage them in device memory:
+// `stage` holds attention_stage_bytes (0 when every row fits in LDS).
+size_t attention_stage_bytes(const AttentionShape& s, const AttentionBatch& b, bool backward);
 int launch_attention(const float* q, const float* k, const float* v, float* out, const AttentionShape& s,
-                     const AttentionBatch& b, hipStream_t stream);
-// Workspace bytes of attention_backward: row statistics plus the probabilities and score gradients.
+                     const AttentionBatch& b, void* stage, hipStream_t stream);
+// Workspace bytes of attention_backward: the probabilities and score gradients of every row.
 size_t attention_backward_workspace(const AttentionShape& s, const AttentionBatch& b, int64_t total_q);
 int launch_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,
                               float* dv, const AttentionShape& s, const AttentionBatch& b, int64_t total_q,
-                              int64_t total_kv, void* workspace, hipStream_t stream);
+                              int64_t total_kv, void* workspace, void* stage, hipStream_t stream);
+
+// ---- self-attention on the matrix-core tiles (attn_abi.hip) ----
+// One sequence with q_len == kv_len = n, q_offset 0 (or negative), no soft-cap, head_dim == value_dim (a multiple
+// of 4), causal with an optional sliding window or every key visible: the training step's attention path.
+bool self_attention_fast(size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads, size_t head_dim,
+                         size_t value_dim, int causal, int64_t q_offset, size_t window, double softcap);
+size_t self_attention_workspace(size_t n, size_t q_heads, size_t kv_heads, size_t head_dim, bool backward);
+int self_attention_forward(const float* q, const float* k, const float* v, float* out, size_t n, size_t q_heads,
+                           size_t kv_heads, size_t head_dim, double scale, int causal, int64_t window, void* ws,
+                           hipStream_t s);
+int self_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,
+                            float* dv, size_t n, size_t q_heads, size_t kv_heads, size_t head_dim, double scale,
+                            int causal, int64_t window, void* ws, hipStream_t s);
 
 // ---- loss and embedding (loss.hip) ----
 

@@ -40,7 +40,9 @@ def _load() -> C.CDLL:
     lib.dllm_hip_linear_workspace.argtypes = [_sz, _sz, _sz]
     lib.dllm_hip_linear_backward_workspace.argtypes = [_sz, _sz, _sz]
     lib.dllm_hip_rope_workspace.argtypes = [_sz, _sz]
-    lib.dllm_hip_attention_backward_workspace.argtypes = [_sz, _sz, _sz]
+    lib.dllm_hip_attention_backward_workspace.argtypes = [_sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int64, _sz,
+                                                          C.c_double]
+    lib.dllm_hip_attention_workspace.argtypes = [_sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.c_int64, _sz, C.c_double]
     lib.dllm_hip_cross_entropy_workspace.argtypes = [_sz]
     lib.dllm_hip_embedding_backward_workspace.argtypes = [_sz]
     lib.dllm_hip_rms_norm_backward_workspace.argtypes = [_sz]
@@ -222,7 +224,8 @@ def attention(q, k, v, scale, causal=True, q_offset=-1, window=0, softcap=0.0, r
     q, k, v = _f32(q), _f32(k), _f32(v)
     q_offset = _attention_args(q, k, v, q_offset)
     out_shape = (q.shape[0], q.shape[1], v.shape[2])
-    ws = Device(lib.dllm_hip_attention_workspace())
+    ws = Device(lib.dllm_hip_attention_workspace(q.shape[0], k.shape[0], q.shape[1], k.shape[1], q.shape[2],
+                                                 v.shape[2], int(causal), int(q_offset), int(window), float(softcap)))
     dq, dk, dv, out = Device.of(q), Device.of(k), Device.of(v), Device(int(np.prod(out_shape)) * 4)
     check(lib.dllm_hip_attention(dq.ptr, dk.ptr, dv.ptr, out.ptr, q.shape[0], k.shape[0], q.shape[1], k.shape[1],
                                  q.shape[2], v.shape[2], float(scale), int(causal), int(q_offset), int(window),
@@ -306,7 +309,9 @@ def attention_backward(q, k, v, dout, scale, causal=True, q_offset=-1, window=0,
     q_offset = _attention_args(q, k, v, q_offset)
     if dout.ndim != 3 or dout.shape != (q.shape[0], q.shape[1], v.shape[2]):
         raise ValueError("dout must be [q_len, q_heads, value_dim]")
-    ws = Device(lib.dllm_hip_attention_backward_workspace(q.shape[0], k.shape[0], q.shape[1]))
+    ws = Device(lib.dllm_hip_attention_backward_workspace(q.shape[0], k.shape[0], q.shape[1], k.shape[1], q.shape[2],
+                                                          v.shape[2], int(causal), int(q_offset), int(window),
+                                                          float(softcap)))
     d = [Device.of(a) for a in (q, k, v, dout)]
     gq, gk, gv = Device(q.nbytes), Device(k.nbytes), Device(v.nbytes)
     check(lib.dllm_hip_attention_backward(d[0].ptr, d[1].ptr, d[2].ptr, d[3].ptr, gq.ptr, gk.ptr, gv.ptr, q.shape[0],

@@ -134,7 +134,7 @@ class Trainer:
         self.names = [lib.dllm_hip_trainer_tensor_name(handle, i).decode() for i in range(count.value)]
 
     def close(self) -> None:
-        if self.handle:
+        if getattr(self, "handle", None):
             lib.dllm_hip_trainer_destroy(self.handle)
             self.handle = None
 

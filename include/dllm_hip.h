@@ -60,8 +60,13 @@ int dllm_hip_rope(const float* x, const int64_t* positions, const double* inv_fr
 
 /* Causal / windowed grouped-query attention, q[q_len, q_heads, head_dim], k[kv_len, kv_heads, head_dim],
  * v[kv_len, kv_heads, value_dim] -> out[q_len, q_heads, value_dim]; q_offset < 0 means kv_len - q_len.
- * Replaces kernels.cpp:680-705 `attention` (nn.hpp:761-796). Key lengths up to 2048. */
-size_t dllm_hip_attention_workspace(void);
+ * Replaces kernels.cpp:680-705 `attention` (nn.hpp:761-796). Any key length. Self-attention shapes (q_len == kv_len,
+ * no cached prefix, no soft-cap, head_dim == value_dim a multiple of 4; causal, or non-causal without a window) run on
+ * the training step's matrix-core tiles, with a workspace of about q_heads * q_len^2 doubles (four times that for the
+ * backward); other shapes run one wave per (query, head). Both give the reference's bits. The workspace functions
+ * take the call's shape arguments. */
+size_t dllm_hip_attention_workspace(size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads, size_t head_dim,
+                                    size_t value_dim, int causal, int64_t q_offset, size_t window, double softcap);
 int dllm_hip_attention(const float* q, const float* k, const float* v, float* out, size_t q_len, size_t kv_len,
                        size_t q_heads, size_t kv_heads, size_t head_dim, size_t value_dim, double scale, int causal,
                        int64_t q_offset, size_t window, double softcap, void* workspace, size_t workspace_bytes,
@@ -97,7 +102,9 @@ int dllm_hip_gelu_tanh_backward(const float* x, const float* dy, float* out, siz
 int dllm_hip_softcap_backward(const float* x, const float* dy, float* out, size_t n, double cap, void* stream);
 
 /* (dq, dk, dv) of attention. Replaces kernels.cpp:930-959 `attention_backward` (grad.hpp:206-301). */
-size_t dllm_hip_attention_backward_workspace(size_t q_len, size_t kv_len, size_t q_heads);
+size_t dllm_hip_attention_backward_workspace(size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads,
+                                             size_t head_dim, size_t value_dim, int causal, int64_t q_offset,
+                                             size_t window, double softcap);
 int dllm_hip_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq,
                                 float* dk, float* dv, size_t q_len, size_t kv_len, size_t q_heads, size_t kv_heads,
                                 size_t head_dim, size_t value_dim, double scale, int causal, int64_t q_offset,

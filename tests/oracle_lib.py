@@ -677,10 +677,11 @@ def _power(base: float, exponent: int) -> float:
 
 
 def lora_train_step(kern: Kernels, d: Decoder, base, adapters, m, v, windows, opt: AdamWConfig, step: int,
-                    total_steps: int, lora: Lora, router_aux_loss: float = 0.0):
+                    total_steps: int, lora: Lora, router_aux_loss: float = 0.0, out: dict | None = None):
     """FineTuner.train_step for a LoRA run (trainer.py:290-335, 463-474; optimizer.py:66-109): gradients of the
     merged weights summed over the windows in float32 (the first copied), the adapters' gradients, then AdamW over
-    the adapters in tensor order. Updates adapters, m and v in place; returns (loss, gradient norm)."""
+    the adapters in tensor order. Updates adapters, m and v in place; returns (loss, gradient norm). With `out`, its
+    "weight_grads" and "adapter_grads" receive the summed merged-weight gradients and the adapters' gradients."""
     merged = merged_weights(kern, d, base, adapters, lora)
     targets_total = sum(len(w) - 1 for w in windows)
     scale = 1.0 / targets_total
@@ -702,6 +703,8 @@ def lora_train_step(kern: Kernels, d: Decoder, base, adapters, m, v, windows, op
             a_name = weight + ".lora_a"
             result[a_name], result[name] = adapter_gradients(kern, grads[weight], adapters[a_name], adapters[name],
                                                              lora.scale)
+    if out is not None:
+        out["weight_grads"], out["adapter_grads"] = grads, result
     total = 0.0
     for name in tensor_order(result):
         total += kern.sum_squares(result[name])

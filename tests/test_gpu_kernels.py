@@ -91,22 +91,31 @@ def test_rope(K, ora, rotary, theta, interleaved):
                     f"rope inverse={inverse}")
 
 
-@pytest.mark.parametrize(("q_len", "kv_len", "heads", "kvh", "hd", "window", "softcap", "offset"), [
-    (9, 9, 6, 2, 8, 0, 0.0, 0),
-    (5, 9, 6, 2, 8, 0, 0.0, 4),
-    (9, 9, 6, 3, 8, 3, 0.0, 0),
-    (9, 9, 4, 4, 8, 0, 0.7, 0),
-    (130, 130, 4, 2, 64, 0, 0.0, 0),
-    (70, 70, 2, 1, 128, 17, 0.0, 0),
+@pytest.mark.parametrize(("q_len", "kv_len", "heads", "kvh", "hd", "window", "softcap", "offset", "causal"), [
+    (9, 9, 6, 2, 8, 0, 0.0, 0, True),
+    (5, 9, 6, 2, 8, 0, 0.0, 4, True),
+    (9, 9, 6, 3, 8, 3, 0.0, 0, True),
+    (9, 9, 4, 4, 8, 0, 0.7, 0, True),
+    (130, 130, 4, 2, 64, 0, 0.0, 0, True),
+    (70, 70, 2, 1, 128, 17, 0.0, 0, True),
+    (70, 70, 6, 2, 12, 0, 0.0, 0, False),  # every key visible (matrix-core tiles)
+    (33, 33, 4, 4, 6, 5, 0.0, 0, False),  # non-causal window (row kernels)
+    (65, 65, 3, 1, 5, 0, 0.0, 0, True),  # head_dim not a multiple of 4 (row kernels)
+    (4, 3000, 4, 2, 16, 0, 0.0, 2996, True),  # past 2048 keys: staged in device memory
+    (2100, 2100, 2, 1, 8, 0, 0.5, 0, True),  # soft-capped, past 2048 keys
+    (2300, 2300, 4, 2, 16, 0, 0.0, 0, True),  # past 2048 keys on the tiles
 ])
-def test_attention_forward_and_backward(K, ora, q_len, kv_len, heads, kvh, hd, window, softcap, offset):
+def test_attention_forward_and_backward(K, ora, q_len, kv_len, heads, kvh, hd, window, softcap, offset, causal):
+    """Both paths of the C-ABI attention against the oracle, bit for bit: the training step's matrix-core tiles for
+    self-attention shapes, the row kernels for the rest (cached prefix, soft-cap, odd head_dim, non-causal windows),
+    including key lengths past the row kernels' LDS staging."""
     q, k, v = O.gaussian(12, q_len, heads, hd), O.gaussian(13, kv_len, kvh, hd), O.gaussian(14, kv_len, kvh, hd)
     dout = O.gaussian(15, q_len, heads, hd)
     scale = 1.0 / np.sqrt(hd)
-    assert_same(K.attention(q, k, v, scale, True, offset, window, softcap),
-                ora.attention(q, k, v, scale, True, offset, window, softcap), "attention")
-    got = K.attention_backward(q, k, v, dout, scale, True, offset, window, softcap)
-    want = ora.attention_backward(q, k, v, dout, scale, True, offset, window, softcap)
+    assert_same(K.attention(q, k, v, scale, causal, offset, window, softcap),
+                ora.attention(q, k, v, scale, causal, offset, window, softcap), "attention")
+    got = K.attention_backward(q, k, v, dout, scale, causal, offset, window, softcap)
+    want = ora.attention_backward(q, k, v, dout, scale, causal, offset, window, softcap)
     for g, w, name in zip(got, want, ("dq", "dk", "dv")):
         assert_same(g, w, name)
 

@@ -6,8 +6,9 @@ Row-local outputs (linear, dX, RMSNorm forward and dx, RoPE, SiLU/SwiGLU and the
 must be bit-identical for every M: each M's rows equal the first M rows of the largest run. Reductions over rows (dW,
 db, the norm weight's dw, dk, dv) must equal the CPU oracle at each M: dW and db on a subset of their outputs (each
 output's chain runs over the rows only, so the oracle on the matching columns of x and dy gives those outputs
-exactly), the norm's dw whole, dk and dv where the oracle's attention finishes in seconds (M <= 64; the C-ABI
-attention takes up to 2048 keys). AdamW runs once over the layer's 14.9 M parameters.
+exactly), the norm's dw whole, dk and dv whole where the oracle's attention finishes in seconds (M <= 64) and, at every
+M, on the last keys: only the last queries see them, so the oracle's attention backward of those queries over all M
+keys (a cached-prefix call) gives their dk and dv exactly. AdamW runs once over the layer's 14.9 M parameters.
 """
 
 from __future__ import annotations
@@ -22,7 +23,7 @@ pytestmark = pytest.mark.gpu
 HIDDEN, INTER, HEADS, KV_HEADS, HEAD_DIM, THETA = 896, 4864, 14, 2, 64, 1e6
 SWEEP = (1, 7, 64, 2048, 8192)
 M_MAX = SWEEP[-1]
-ATTN_MAX = 2048
+ATTN_TAIL = 16  # last keys (and queries) checked against the oracle at every M
 COLS_OUT = np.array([0, 1, 63, 64, 127, 300, 895])  # sampled output features (< 896) for dW / db
 COLS_IN = np.array([0, 5, 127, 128, 511, 890, 895])  # sampled input features (< 896)
 
@@ -128,7 +129,7 @@ def test_swiglu_sweep(K, ora, data):
 
 
 def test_causal_gqa_attention_sweep(K, ora, data):
-    n = ATTN_MAX
+    n = M_MAX
     q = data["x"][:n, : HEADS * HEAD_DIM].reshape(n, HEADS, HEAD_DIM)
     k = O.gaussian(131, n, KV_HEADS, HEAD_DIM)
     v = O.gaussian(132, n, KV_HEADS, HEAD_DIM)
@@ -136,12 +137,24 @@ def test_causal_gqa_attention_sweep(K, ora, data):
     scale = 1.0 / np.sqrt(HEAD_DIM)
     full_out = K.attention(q, k, v, scale, True)
     full_dq, _, _ = K.attention_backward(q, k, v, dout, scale, True)
-    for m in [s for s in SWEEP if s <= n]:
+    for m in SWEEP:
         args = (q[:m], k[:m], v[:m])
         out = K.attention(*args, scale, True)
         dq, dk, dv = K.attention_backward(*args, dout[:m], scale, True)
         assert_same(out, full_out[:m], f"attention out M={m}")
         assert_same(dq, full_dq[:m], f"attention dq M={m}")
+        s = min(m, ATTN_TAIL)
+        tail = (q[m - s:m], k[:m], v[:m])
+        want_out = ora.attention(*tail, scale, True, m - s)
+        want = ora.attention_backward(*tail, dout[m - s:m], scale, True, m - s)
+        assert_same(out[m - s:], want_out, f"attention out of the last queries vs oracle M={m}")
+        assert_same(dq[m - s:], want[0], f"attention dq of the last queries vs oracle M={m}")
+        assert_same(dk[m - s:], want[1][m - s:], f"attention dk of the last keys vs oracle M={m}")
+        assert_same(dv[m - s:], want[2][m - s:], f"attention dv of the last keys vs oracle M={m}")
+        # the same tail through the row kernels (a cached-prefix call), past 2048 keys where M is
+        got_tail = K.attention_backward(*tail, dout[m - s:m], scale, True, m - s)
+        for g, w, what in zip(got_tail, want, ("dq", "dk", "dv")):
+            assert_same(g, w, f"cached-prefix attention {what} M={m}")
         if m <= 64:
             assert_same(out, ora.attention(*args, scale, True), f"attention out vs oracle M={m}")
             want = ora.attention_backward(*args, dout[:m], scale, True)
