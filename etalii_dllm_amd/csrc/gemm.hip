@@ -44,6 +44,9 @@ constexpr int kTileJ = 256;    // columns per wave (4 per lane)
 constexpr int kBlockI = kTileI * kWavesI;
 constexpr int64_t kParallelWindowsBelow = 2048;  // tiles
 constexpr int64_t kGroupRows = 8;                // row blocks per L2 group
+// Matrix-core launches of fewer 128 x 128 tiles take smaller ones (measured on the SmolLM2-135M step: 21.8k tokens/s
+// against 12.3k with 128 x 128 tiles only; thresholds 512 and 2048 measure alike, 128 slower).
+constexpr int64_t kSmallTilesBelow = 512;
 
 struct GemmParams {
     const double* A;
@@ -448,55 +451,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // +0.0 and the accumulator is never -0.0 (it starts at +0.0, and a round-to-nearest sum is -0.0 only when both
 // addends are), so acc + 0 == acc bit for bit, infinities and NaNs included.
 //
-// Mapping: a workgroup computes a kMTileI x kMTileJ tile with 4 waves in a 2 x 2 grid; a wave owns 64 i x 16 kMBJ j
-// as 4 x kMBJ MFMA blocks (32 kMBJ accumulator VGPRs). Stages of kMStage l of both operands are copied global -> LDS
-// with direct-to-LDS loads, double-buffered; per 4-l step a wave reads 4 + kMBJ fragment values from LDS, converts
-// them, and issues 4 kMBJ MFMAs. On gfx950 the FP64 matrix core and the vector ALU share issue cycles, so the copies
-// run without vector instructions (SGPR base + fixed lane offset) and each fragment value feeds 4 or kMBJ MFMAs.
+// Mapping: a workgroup computes a (32 kBI) x (32 kBJ) tile with 4 waves in a 2 x 2 grid; a wave owns 16 kBI i x 16 kBJ
+// j as kBI x kBJ MFMA blocks (8 kBI kBJ accumulator VGPRs). Stages of kMStage l of both operands are copied
+// global -> LDS with direct-to-LDS loads, double-buffered; per 4-l step a wave reads kBI + kBJ fragment values from
+// LDS, converts them, and issues kBI kBJ MFMAs. On gfx950 the FP64 matrix core and the vector ALU share issue cycles,
+// so the copies run without vector instructions (SGPR base + fixed lane offset) and each fragment value feeds kBJ or
+// kBI MFMAs: the 4 x 4 waves of the large launches spend about 6% of the matrix core's cycles on them, the 1 x 1 waves
+// of the smallest grids about a quarter.
 typedef double mf_v4d __attribute__((ext_vector_type(4)));
-constexpr int kMBI = 4;                  // MFMA blocks per wave along i
-constexpr int kMBJ = 4;                  // MFMA blocks per wave along j
-constexpr int kMTileI = 2 * 16 * kMBI;   // workgroup tile along i (128)
-constexpr int kMTileJ = 2 * 16 * kMBJ;   // workgroup tile along j (128)
-constexpr int kMStage = 32;              // l per LDS stage
-constexpr int kMPiecesA = kMStage * kMTileI / 4 / 256;  // 16-byte copies per thread per stage
-constexpr int kMPiecesB = kMStage * kMTileJ / 4 / 256;
-static_assert(kMStage * kMTileI % 1024 == 0 && kMStage * kMTileJ % 1024 == 0, "whole copies per thread");
-static_assert(kMTileI == 128, "the transposed-A copy layout assumes 128 rows");
+constexpr int kMStage = 32;  // l per LDS stage
 
-template <int kA>
-struct MStage {
-    float a[kMStage * kMTileI];  // A rows: [l][i ^ 16 (l % 4)]; A transposed: [l / 4][i][l % 4]
-    float b[kMStage * kMTileJ];  // A rows: [l][j ^ 16 (l % 4)]; A transposed: [l][j]
+// A workgroup tile of 2 x 2 waves, each wave kBI x kBJ MFMA blocks of 16 x 16: (32 kBI) x (32 kBJ) outputs. The
+// step's large matmuls take 4 x 4 (128 x 128 tiles); launches whose 128 x 128 grid would leave most CUs idle take
+// 2 x 2 or 1 x 1 (64 x 64, 32 x 32): the same per-output chain, more workgroups.
+template <int kBI, int kBJ>
+struct MTile {
+    static constexpr int I = 32 * kBI;                     // workgroup tile along i
+    static constexpr int J = 32 * kBJ;                     // workgroup tile along j
+    static constexpr int PA = kMStage * I / 4 / 256;       // 16-byte copies per thread per stage
+    static constexpr int PB = kMStage * J / 4 / 256;
+    static constexpr bool swizzle = I >= 64 && J >= 64;  // the l % 4 chunk permutation needs 16 chunks a row
+    static_assert(kMStage * I % 1024 == 0 && kMStage * J % 1024 == 0, "whole copies per thread");
 };
 
-// Row-major stage rows are 128 floats (512 bytes), so the 4 rows a fragment read spans (l = 4s .. 4s + 3, one per
-// 16 lanes) fall on the same LDS banks. With A read as rows (the weight gradients) row l keeps its 16-byte chunks
+template <int kA, int kBI, int kBJ>
+struct MStage {
+    float a[kMStage * MTile<kBI, kBJ>::I];  // A rows: [l][i ^ 16 (l % 4)]; A transposed: [l / 4][i][l % 4]
+    float b[kMStage * MTile<kBI, kBJ>::J];  // A rows: [l][j ^ 16 (l % 4)]; A transposed: [l][j]
+};
+
+// Row-major stage rows of 128 floats (512 bytes) put the 4 rows a fragment read spans (l = 4s .. 4s + 3, one per
+// 16 lanes) on the same LDS banks. With A read as rows (the weight gradients) row l keeps its 16-byte chunks
 // XOR-permuted by 4 (l % 4): element j of row l sits at j ^ (16 (l % 4)), and a fragment read touches 64 consecutive
 // banks. The copies apply the permutation through the source address each lane loads (an LDS copy's destination is
 // fixed by the lane). Measured on MI355X, the permutation speeds up those matmuls by 1% and slows the transposed-A
 // ones (whose A reads are already conflict-free) by 2%, so only the former use it.
-__host__ __device__ __forceinline__ int mswizzle_chunk(int row) { return (row & 3) << 2; }
+template <int kA, int kBI, int kBJ>
+__host__ __device__ __forceinline__ int mswizzle_chunk(int row) {
+    return kA == kAFloatRows && MTile<kBI, kBJ>::swizzle ? (row & 3) << 2 : 0;
+}
 
 // The global source of copy `id` of a stage at row l, with every index clamped in bounds (rows past `last` repeat
 // row `last`; their values are masked); the LDS destination of copy id is 16 * id bytes into the operand's array.
-template <int kA>
-__host__ __device__ __forceinline__ const float* msrc_b(const GemmParams& p, int id, int64_t j_blk, int64_t l, int64_t last) {
-    const int r = id / (kMTileJ / 4), cc = (id % (kMTileJ / 4)) ^ (kA == kAFloatRows ? mswizzle_chunk(r) : 0);
+template <int kA, int kBI, int kBJ>
+__host__ __device__ __forceinline__ const float* msrc_b(const GemmParams& p, int id, int64_t j_blk, int64_t l,
+                                                       int64_t last) {
+    constexpr int TJ = MTile<kBI, kBJ>::J;
+    const int r = id / (TJ / 4), cc = (id % (TJ / 4)) ^ mswizzle_chunk<kA, kBI, kBJ>(r);
     const int64_t lr = l + r <= last ? l + r : last;
     const int64_t j = j_blk + cc * 4 <= p.J - 4 ? j_blk + cc * 4 : p.J - 4;
     return p.B + lr * p.ldb + j;
 }
 
-template <int kA>
-__host__ __device__ __forceinline__ const float* msrc_a(const GemmParams& p, int id, int64_t i_blk, int64_t l, int64_t last) {
+template <int kA, int kBI, int kBJ>
+__host__ __device__ __forceinline__ const float* msrc_a(const GemmParams& p, int id, int64_t i_blk, int64_t l,
+                                                       int64_t last) {
+    constexpr int TI = MTile<kBI, kBJ>::I;
     if constexpr (kA == kAFloatRows) {
-        const int r = id / (kMTileI / 4), cc = (id % (kMTileI / 4)) ^ mswizzle_chunk(id / (kMTileI / 4));
+        const int r = id / (TI / 4), cc = (id % (TI / 4)) ^ mswizzle_chunk<kA, kBI, kBJ>(id / (TI / 4));
         const int64_t lr = l + r <= last ? l + r : last;
         const int64_t i = i_blk + cc * 4 <= p.I - 4 ? i_blk + cc * 4 : p.I - 4;
         return p.Af + lr * p.lda + i;
     } else {
-        const int c = id / kMTileI, ii = id % kMTileI;
+        const int c = id / TI, ii = id % TI;
         const int64_t row = i_blk + ii < p.I ? i_blk + ii : p.I - 1;
         const int64_t lc = l + 4 * c <= p.l1 - 4 ? l + 4 * c : p.l1 - 4;
         return p.Af + row * p.lda + lc;
@@ -504,162 +521,177 @@ __host__ __device__ __forceinline__ const float* msrc_a(const GemmParams& p, int
 }
 
 // A stage with rows past the segment's end (the last one): every address clamped per lane.
-template <int kA>
-__device__ __forceinline__ void missue_stage(const GemmParams& p, MStage<kA>& st, int64_t i_blk, int64_t j_blk,
-                                             int64_t l, int64_t last, int tid) {
+template <int kA, int kBI, int kBJ>
+__device__ __forceinline__ void missue_stage(const GemmParams& p, MStage<kA, kBI, kBJ>& st, int64_t i_blk,
+                                             int64_t j_blk, int64_t l, int64_t last, int tid) {
+    using T = MTile<kBI, kBJ>;
     const int wave_base = tid & ~63;
 #pragma unroll
-    for (int t = 0; t < kMPiecesB; ++t)
-        copy16_to_lds(msrc_b<kA>(p, t * 256 + tid, j_blk, l, last), &st.b[(t * 256 + wave_base) * 4]);
+    for (int t = 0; t < T::PB; ++t)
+        copy16_to_lds(msrc_b<kA, kBI, kBJ>(p, t * 256 + tid, j_blk, l, last), &st.b[(t * 256 + wave_base) * 4]);
 #pragma unroll
-    for (int t = 0; t < kMPiecesA; ++t)
-        copy16_to_lds(msrc_a<kA>(p, t * 256 + tid, i_blk, l, last), &st.a[(t * 256 + wave_base) * 4]);
+    for (int t = 0; t < T::PA; ++t)
+        copy16_to_lds(msrc_a<kA, kBI, kBJ>(p, t * 256 + tid, i_blk, l, last), &st.a[(t * 256 + wave_base) * 4]);
 }
 
 // Steady-state copies: a stage whose rows all lie inside the segment needs no clamping along l, so each copy is a
 // wave-uniform base (SGPRs, advanced per stage by scalar adds) plus this lane's fixed 32-bit byte offset, computed
 // once per workgroup from the stage at l = 0.
+template <int kBI, int kBJ>
 struct MCopyOffsets {
-    uint32_t b[kMPiecesB], a[kMPiecesA];
+    uint32_t b[MTile<kBI, kBJ>::PB], a[MTile<kBI, kBJ>::PA];
 };
 
-template <int kA>
-__host__ __device__ __forceinline__ MCopyOffsets mcopy_offsets(const GemmParams& p, int64_t i_blk, int64_t j_blk, int tid) {
-    MCopyOffsets o;
+template <int kA, int kBI, int kBJ>
+__host__ __device__ __forceinline__ MCopyOffsets<kBI, kBJ> mcopy_offsets(const GemmParams& p, int64_t i_blk,
+                                                                        int64_t j_blk, int tid) {
+    using T = MTile<kBI, kBJ>;
+    MCopyOffsets<kBI, kBJ> o;
     const int64_t big = int64_t{1} << 40;  // no l clamp
 #pragma unroll
-    for (int t = 0; t < kMPiecesB; ++t)
-        o.b[t] = static_cast<uint32_t>(reinterpret_cast<const char*>(msrc_b<kA>(p, t * 256 + tid, j_blk, 0, big)) -
-                                       reinterpret_cast<const char*>(p.B));
+    for (int t = 0; t < T::PB; ++t)
+        o.b[t] = static_cast<uint32_t>(
+            reinterpret_cast<const char*>(msrc_b<kA, kBI, kBJ>(p, t * 256 + tid, j_blk, 0, big)) -
+            reinterpret_cast<const char*>(p.B));
 #pragma unroll
-    for (int t = 0; t < kMPiecesA; ++t) {
+    for (int t = 0; t < T::PA; ++t) {
         GemmParams q = p;
         q.l1 = big;
-        o.a[t] = static_cast<uint32_t>(reinterpret_cast<const char*>(msrc_a<kA>(q, t * 256 + tid, i_blk, 0, big)) -
-                                       reinterpret_cast<const char*>(p.Af));
+        o.a[t] = static_cast<uint32_t>(
+            reinterpret_cast<const char*>(msrc_a<kA, kBI, kBJ>(q, t * 256 + tid, i_blk, 0, big)) -
+            reinterpret_cast<const char*>(p.Af));
     }
     return o;
 }
 
-template <int kA>
-__device__ __forceinline__ void missue_full(const GemmParams& p, MStage<kA>& st, const MCopyOffsets& o, int64_t l,
-                                            int wave) {
+template <int kA, int kBI, int kBJ>
+__device__ __forceinline__ void missue_full(const GemmParams& p, MStage<kA, kBI, kBJ>& st,
+                                            const MCopyOffsets<kBI, kBJ>& o, int64_t l, int wave) {
+    using T = MTile<kBI, kBJ>;
     const float* bb = p.B + l * p.ldb;
     const float* ab = kA == kAFloatT ? p.Af + l : p.Af + l * p.lda;
 #pragma unroll
-    for (int t = 0; t < kMPiecesB; ++t) copy16_to_lds_s(bb, o.b[t], &st.b[(t * 256 + wave * 64) * 4]);
+    for (int t = 0; t < T::PB; ++t) copy16_to_lds_s(bb, o.b[t], &st.b[(t * 256 + wave * 64) * 4]);
 #pragma unroll
-    for (int t = 0; t < kMPiecesA; ++t) copy16_to_lds_s(ab, o.a[t], &st.a[(t * 256 + wave * 64) * 4]);
+    for (int t = 0; t < T::PA; ++t) copy16_to_lds_s(ab, o.a[t], &st.a[(t * 256 + wave * 64) * 4]);
 }
 
 // The fragments of 4-l step s: a[q] = A[l = 4s + L/16][i = wave row base + 16q + L%16], b[q] likewise for j.
-template <int kA>
-__device__ __forceinline__ void mread_frags(const MStage<kA>& st, int s, int wi, int wj, int lane,
-                                            double (&a)[kMBI], double (&b)[kMBJ]) {
+template <int kA, int kBI, int kBJ>
+__device__ __forceinline__ void mread_frags(const MStage<kA, kBI, kBJ>& st, int s, int wi, int wj, int lane,
+                                            double (&a)[kBI], double (&b)[kBJ]) {
+    using T = MTile<kBI, kBJ>;
+    constexpr bool sw = kA == kAFloatRows && T::swizzle;
     const int k = lane >> 4, c16 = lane & 15;
 #pragma unroll
-    for (int q = 0; q < kMBI; ++q) {
-        const int i = wi * 16 * kMBI + 16 * q + c16;
+    for (int q = 0; q < kBI; ++q) {
+        const int i = wi * 16 * kBI + 16 * q + c16;
         if constexpr (kA == kAFloatT)
-            a[q] = static_cast<double>(st.a[(s * kMTileI + i) * 4 + k]);
+            a[q] = static_cast<double>(st.a[(s * T::I + i) * 4 + k]);
         else
-            a[q] = static_cast<double>(st.a[(4 * s + k) * kMTileI + (i ^ (k << 4))]);
+            a[q] = static_cast<double>(st.a[(4 * s + k) * T::I + (sw ? (i ^ (k << 4)) : i)]);
     }
 #pragma unroll
-    for (int q = 0; q < kMBJ; ++q)
-        b[q] = static_cast<double>(
-            st.b[(4 * s + k) * kMTileJ + ((wj * 16 * kMBJ + 16 * q + c16) ^ (kA == kAFloatRows ? k << 4 : 0))]);
+    for (int q = 0; q < kBJ; ++q) {
+        const int j = wj * 16 * kBJ + 16 * q + c16;
+        b[q] = static_cast<double>(st.b[(4 * s + k) * T::J + (sw ? (j ^ (k << 4)) : j)]);
+    }
 }
 
-__device__ __forceinline__ void mfma_step(const double (&a)[kMBI], const double (&b)[kMBJ],
-                                          mf_v4d (&acc)[kMBI][kMBJ]) {
+template <int kBI, int kBJ>
+__device__ __forceinline__ void mfma_step(const double (&a)[kBI], const double (&b)[kBJ], mf_v4d (&acc)[kBI][kBJ]) {
 #pragma unroll
-    for (int bi = 0; bi < kMBI; ++bi)
+    for (int bi = 0; bi < kBI; ++bi)
 #pragma unroll
-        for (int bj = 0; bj < kMBJ; ++bj)
+        for (int bj = 0; bj < kBJ; ++bj)
             acc[bi][bj] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[bi], b[bj], acc[bi][bj], 0, 0, 0);
 }
 
 // A full stage, the fragments of step s + 1 read while the MFMAs of step s run.
-template <int kA>
-__device__ __forceinline__ void mstage_full(const MStage<kA>& st, int wi, int wj, int lane,
-                                            mf_v4d (&acc)[kMBI][kMBJ]) {
-    double a[kMBI], b[kMBJ];
-    mread_frags<kA>(st, 0, wi, wj, lane, a, b);
+template <int kA, int kBI, int kBJ>
+__device__ __forceinline__ void mstage_full(const MStage<kA, kBI, kBJ>& st, int wi, int wj, int lane,
+                                            mf_v4d (&acc)[kBI][kBJ]) {
+    double a[kBI], b[kBJ];
+    mread_frags<kA, kBI, kBJ>(st, 0, wi, wj, lane, a, b);
 #pragma unroll
     for (int s = 0; s < kMStage / 4; ++s) {
-        double an[kMBI], bn[kMBJ];
-        if (s + 1 < kMStage / 4) mread_frags<kA>(st, s + 1, wi, wj, lane, an, bn);
-        mfma_step(a, b, acc);
+        double an[kBI], bn[kBJ];
+        if (s + 1 < kMStage / 4) mread_frags<kA, kBI, kBJ>(st, s + 1, wi, wj, lane, an, bn);
+        mfma_step<kBI, kBJ>(a, b, acc);
         if (s + 1 < kMStage / 4) {
 #pragma unroll
-            for (int q = 0; q < kMBI; ++q) a[q] = an[q];
+            for (int q = 0; q < kBI; ++q) a[q] = an[q];
 #pragma unroll
-            for (int q = 0; q < kMBJ; ++q) b[q] = bn[q];
+            for (int q = 0; q < kBJ; ++q) b[q] = bn[q];
         }
     }
 }
 
 // The last, partial stage: n < kMStage valid rows; lanes whose l is past the end feed +0.0 in both operands.
-template <int kA>
-__device__ __forceinline__ void mstage_tail(const MStage<kA>& st, int n, int wi, int wj, int lane,
-                                            mf_v4d (&acc)[kMBI][kMBJ]) {
+template <int kA, int kBI, int kBJ>
+__device__ __forceinline__ void mstage_tail(const MStage<kA, kBI, kBJ>& st, int n, int wi, int wj, int lane,
+                                            mf_v4d (&acc)[kBI][kBJ]) {
     const int k = lane >> 4;
     for (int s = 0; 4 * s < n; ++s) {
-        double a[kMBI], b[kMBJ];
-        mread_frags<kA>(st, s, wi, wj, lane, a, b);
+        double a[kBI], b[kBJ];
+        mread_frags<kA, kBI, kBJ>(st, s, wi, wj, lane, a, b);
         if (4 * s + k >= n) {
 #pragma unroll
-            for (int q = 0; q < kMBI; ++q) a[q] = 0.0;
+            for (int q = 0; q < kBI; ++q) a[q] = 0.0;
 #pragma unroll
-            for (int q = 0; q < kMBJ; ++q) b[q] = 0.0;
+            for (int q = 0; q < kBJ; ++q) b[q] = 0.0;
         }
-        mfma_step(a, b, acc);
+        mfma_step<kBI, kBJ>(a, b, acc);
     }
 }
 
-// One segment's sums: acc = sum over l in [l0, l1), ascending, through the double-buffered LDS pipeline.
-template <int kA>
-__device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA> (&st)[2], const MCopyOffsets& o,
-                                            int64_t i_blk, int64_t j_blk, int tid, int wi, int wj, int lane,
-                                            int64_t l0, int64_t l1, mf_v4d (&acc)[kMBI][kMBJ]) {
+// One segment's sums: acc = sum over l in [l0, l1), ascending, through the double-buffered LDS pipeline. (Keeping
+// three stages in flight instead of one measured slower for the small tiles too: their stages are bound by the LDS
+// fragment reads, not by the copies.)
+template <int kA, int kBI, int kBJ>
+__device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA, kBI, kBJ> (&st)[2],
+                                            const MCopyOffsets<kBI, kBJ>& o, int64_t i_blk, int64_t j_blk, int tid,
+                                            int wi, int wj, int lane, int64_t l0, int64_t l1,
+                                            mf_v4d (&acc)[kBI][kBJ]) {
+    using T = MTile<kBI, kBJ>;
 #pragma unroll
-    for (int bi = 0; bi < kMBI; ++bi)
+    for (int bi = 0; bi < kBI; ++bi)
 #pragma unroll
-        for (int bj = 0; bj < kMBJ; ++bj) acc[bi][bj] = mf_v4d{0.0, 0.0, 0.0, 0.0};
+        for (int bj = 0; bj < kBJ; ++bj) acc[bi][bj] = mf_v4d{0.0, 0.0, 0.0, 0.0};
     if (l0 >= l1) return;
     const int64_t last = l1 - 1;
     const int64_t full = (l1 - l0) / kMStage;
     const int tail = static_cast<int>((l1 - l0) % kMStage);
     const int64_t chunks = full + (tail ? 1 : 0);
     const int wave = wi * 2 + wj;
-    auto issue = [&](MStage<kA>& buf, int64_t l) {
-        if (l + kMStage - 1 <= last) missue_full<kA>(p, buf, o, l, wave);
-        else missue_stage<kA>(p, buf, i_blk, j_blk, l, last, tid);
+    auto issue = [&](MStage<kA, kBI, kBJ>& buf, int64_t l) {
+        if (l + kMStage - 1 <= last) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave);
+        else missue_stage<kA, kBI, kBJ>(p, buf, i_blk, j_blk, l, last, tid);
     };
     issue(st[0], l0);
     for (int64_t c = 0; c < full; ++c) {
         if (c + 1 < chunks) {
             issue(st[(c + 1) & 1], l0 + (c + 1) * kMStage);
-            wait_stage<kMPiecesA + kMPiecesB>();  // this stage landed; the next one's copies in flight
+            wait_stage<T::PA + T::PB>();  // this stage landed; the next one's copies in flight
         } else {
             wait_stage<0>();
         }
-        mstage_full<kA>(st[c & 1], wi, wj, lane, acc);
+        mstage_full<kA, kBI, kBJ>(st[c & 1], wi, wj, lane, acc);
         workgroup_barrier();  // every wave has read the stage before the next issue overwrites it
     }
     if (tail) {
         wait_stage<0>();
-        mstage_tail<kA>(st[full & 1], tail, wi, wj, lane, acc);
+        mstage_tail<kA, kBI, kBJ>(st[full & 1], tail, wi, wj, lane, acc);
         workgroup_barrier();
     }
 }
 
-template <int kMode, int kA, bool kGrouped = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_mfma_kernel(
-    GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmParams* __restrict__ groups,
-    const int64_t* __restrict__ tile_start, int ngroups) {
-    __shared__ MStage<kA> st[2];
+template <int kMode, int kA, bool kGrouped = false, int kBI = 4, int kBJ = 4>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, kBI * kBJ >= 16 ? 2 : 4))) void
+gemm_mfma_kernel(GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmParams* __restrict__ groups,
+                 const int64_t* __restrict__ tile_start, int ngroups) {
+    using T = MTile<kBI, kBJ>;
+    __shared__ MStage<kA, kBI, kBJ> st[2];
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -675,8 +707,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         p = groups[lo];
         id -= tile_start[lo];
-        gx = (p.J + kMTileJ - 1) / kMTileJ;
-        gy = (p.I + kMTileI - 1) / kMTileI;
+        gx = (p.J + T::J - 1) / T::J;
+        gy = (p.I + T::I - 1) / T::I;
         gz = 1;
     } else {
         id = xcd_contiguous(blockIdx.x, gx * gy * gz);
@@ -687,23 +719,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int64_t rows_in_group = gy - first < kGroupRows ? gy - first : kGroupRows;
     const int64_t by = first + (t % (kGroupRows * gx)) % rows_in_group;
     const int64_t bx = (t % (kGroupRows * gx)) / rows_in_group;
-    const int64_t i_blk = by * kMTileI, j_blk = bx * kMTileJ;
-    const int64_t iw = i_blk + wi * 16 * kMBI;  // this wave's first row
-    const int64_t jw = j_blk + wj * 16 * kMBJ + (lane & 15);
+    const int64_t i_blk = by * T::I, j_blk = bx * T::J;
+    const int64_t iw = i_blk + wi * 16 * kBI;  // this wave's first row
+    const int64_t jw = j_blk + wj * 16 * kBJ + (lane & 15);
     const int ri = lane >> 4;
-    const MCopyOffsets o = mcopy_offsets<kA>(p, i_blk, j_blk, tid);
-    mf_v4d acc[kMBI][kMBJ];
+    const MCopyOffsets<kBI, kBJ> o = mcopy_offsets<kA, kBI, kBJ>(p, i_blk, j_blk, tid);
+    mf_v4d acc[kBI][kBJ];
     if (kMode == kPlain) {
-        maccumulate<kA>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.l0, p.l1, acc);
+        maccumulate<kA, kBI, kBJ>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.l0, p.l1, acc);
         if (iw >= p.I) return;
 #pragma unroll
-        for (int bi = 0; bi < kMBI; ++bi)
+        for (int bi = 0; bi < kBI; ++bi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t i = iw + 16 * bi + ri + 4 * r;
                 if (i >= p.I) continue;
 #pragma unroll
-                for (int bj = 0; bj < kMBJ; ++bj) {
+                for (int bj = 0; bj < kBJ; ++bj) {
                     const int64_t j = jw + 16 * bj;
                     if (j >= p.J) continue;
                     double v = acc[bi][bj][r];
@@ -718,13 +750,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int s_begin = kMode == kWindowsInParallel ? static_cast<int>(bz) : 0;
     const int s_end = kMode == kWindowsInParallel ? s_begin + 1 : p.nseg;
     for (int s = s_begin; s < s_end; ++s) {
-        maccumulate<kA>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.seg[s], p.seg[s + 1], acc);
+        maccumulate<kA, kBI, kBJ>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.seg[s], p.seg[s + 1], acc);
         if (iw >= p.I) continue;
         float* out_base = kMode == kWindowsInParallel ? p.partial + static_cast<int64_t>(s) * p.I * p.J : p.C;
         int64_t ld_out = kMode == kWindowsInParallel ? p.J : p.ldc;
         asm volatile("" : "+s"(out_base), "+s"(ld_out));
 #pragma unroll
-        for (int bi = 0; bi < kMBI; ++bi)
+        for (int bi = 0; bi < kBI; ++bi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t i = iw + 16 * bi + ri + 4 * r;
@@ -732,7 +764,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const int arow = p.seg_addrow ? p.seg_addrow[static_cast<int64_t>(s) * p.I + i] : -1;
                 float* out = out_base + i * ld_out;
 #pragma unroll
-                for (int bj = 0; bj < kMBJ; ++bj) {
+                for (int bj = 0; bj < kBJ; ++bj) {
                     const int64_t j = jw + 16 * bj;
                     if (j >= p.J) continue;
                     float v = static_cast<float>(acc[bi][bj][r]);
@@ -920,7 +952,7 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
         if (g.I == 0 || g.J == 0) continue;
         ps[used] = params_of(g);
         starts[used] = tiles;
-        tiles += static_cast<int64_t>(ceil_div(g.J, kMTileJ) * ceil_div(g.I, kMTileI));
+        tiles += static_cast<int64_t>(ceil_div(g.J, MTile<4, 4>::J) * ceil_div(g.I, MTile<4, 4>::I));
         ++used;
     }
     starts[used] = tiles;
@@ -976,8 +1008,8 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     }
     if (vec && (ak != kADouble || ((g.lda % 2 == 0) && (reinterpret_cast<uintptr_t>(g.A) % 16 == 0)))) {
         const bool mfma = ak != kADouble;
-        const int64_t gx = mfma ? ceil_div(g.J, kMTileJ) : ceil_div(g.J, kTileJ);
-        const int64_t gy = mfma ? ceil_div(g.I, kMTileI) : ceil_div(g.I, kBlockI);
+        int64_t gx = mfma ? ceil_div(g.J, MTile<4, 4>::J) : ceil_div(g.J, kTileJ);
+        int64_t gy = mfma ? ceil_div(g.I, MTile<4, 4>::I) : ceil_div(g.I, kBlockI);
         int64_t gz = 1;
         // windows in parallel when the tile grid alone leaves most of the 256 CUs x 3 workgroups idle
         if (g.seg && g.nseg > 1 && g.seg_partial && gx * gy < kParallelWindowsBelow &&
@@ -985,12 +1017,28 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
             p.partial = g.seg_partial;
             gz = g.nseg;
         }
+        // matrix-core tiles: 128 x 128, or 64 x 64 / 32 x 32 when the larger tiles' grid leaves CUs idle
+        int tile = 4;
+        if (mfma) {
+            while (tile > 1 && gx * gy * gz < kSmallTilesBelow) {
+                tile /= 2;
+                gx = ceil_div(g.J, 32 * tile);
+                gy = ceil_div(g.I, 32 * tile);
+            }
+        }
         DLLM_REQUIRE(gx * gy * gz < (int64_t{1} << 31), "matmul grid too large for one launch");
         const dim3 grid(static_cast<unsigned>(gx * gy * gz));
 #define DLLM_GEMM_LAUNCH(MODE, AK) \
     hipLaunchKernelGGL((gemm_lds_kernel<MODE, AK>), grid, dim3(256), 0, stream, p, gx, gy, gz, nullptr, nullptr, 0)
-#define DLLM_GEMM_MFMA(MODE, AK) \
-    hipLaunchKernelGGL((gemm_mfma_kernel<MODE, AK>), grid, dim3(256), 0, stream, p, gx, gy, gz, nullptr, nullptr, 0)
+#define DLLM_GEMM_MFMA_T(MODE, AK, T)                                                                            \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MODE, AK, false, T, T>), grid, dim3(256), 0, stream, p, gx, gy, gz, nullptr, \
+                       nullptr, 0)
+#define DLLM_GEMM_MFMA(MODE, AK)                        \
+    do {                                                \
+        if (tile == 4) DLLM_GEMM_MFMA_T(MODE, AK, 4);   \
+        else if (tile == 2) DLLM_GEMM_MFMA_T(MODE, AK, 2); \
+        else DLLM_GEMM_MFMA_T(MODE, AK, 1);             \
+    } while (0)
         if (ak == kAFloatT) {
             DLLM_GEMM_MFMA(kPlain, kAFloatT);
         } else if (ak == kAFloatRows) {
@@ -1004,6 +1052,7 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
         }
 #undef DLLM_GEMM_LAUNCH
 #undef DLLM_GEMM_MFMA
+#undef DLLM_GEMM_MFMA_T
         DLLM_TRY(check_launch("gemm"));
         if (p.partial) {
             const int64_t n = g.I * g.J;

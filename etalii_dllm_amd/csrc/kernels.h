@@ -97,6 +97,9 @@ int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream);
 int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
                           hipStream_t stream);
 int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
+// gelu_tanh elementwise (nn.hpp:481-485) and the gated form f32(gelu_tanh(gate)) * up (nn.hpp:488-492).
+int launch_gelu_tanh(const float* x, float* out, int64_t n, hipStream_t stream);
+int launch_geglu_tanh(const float* gate, const float* up, float* out, int64_t n, hipStream_t stream);
 int launch_gelu_tanh_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
 int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t n, double cap, hipStream_t stream);
 // _swiglu_backward's elementwise glue (backprop.py:301-303): dgate = silu_backward(gate, dproduct * up),

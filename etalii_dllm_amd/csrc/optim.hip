@@ -88,16 +88,34 @@ __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ param, c
     const float4* g4 = reinterpret_cast<const float4*>(grad + i0);
     float4* m4 = reinterpret_cast<float4*>(m + i0);
     float4* v4 = reinterpret_cast<float4*>(v + i0);
-    for (int64_t q = threadIdx.x; q < n4; q += 256) {
-        float4 pp = p4[q], mm = m4[q], vv = v4[q];
-        const float4 gg = g4[q];
-        adamw_element(pp.x, gg.x, mm.x, vv.x, gs, decay, a);
-        adamw_element(pp.y, gg.y, mm.y, vv.y, gs, decay, a);
-        adamw_element(pp.z, gg.z, mm.z, vv.z, gs, decay, a);
-        adamw_element(pp.w, gg.w, mm.w, vv.w, gs, decay, a);
-        m4[q] = mm;
-        v4[q] = vv;
-        p4[q] = pp;
+    // software-pipelined: the next vector of each array is loaded before the current one is updated, so the loads'
+    // latency overlaps the update's double arithmetic
+    int64_t q = threadIdx.x;
+    if (q < n4) {
+        float4 pp = p4[q], mm = m4[q], vv = v4[q], gg = g4[q];
+        for (;;) {
+            const int64_t qn = q + 256;
+            float4 pn, mn, vn, gn;
+            if (qn < n4) {
+                pn = p4[qn];
+                mn = m4[qn];
+                vn = v4[qn];
+                gn = g4[qn];
+            }
+            adamw_element(pp.x, gg.x, mm.x, vv.x, gs, decay, a);
+            adamw_element(pp.y, gg.y, mm.y, vv.y, gs, decay, a);
+            adamw_element(pp.z, gg.z, mm.z, vv.z, gs, decay, a);
+            adamw_element(pp.w, gg.w, mm.w, vv.w, gs, decay, a);
+            m4[q] = mm;
+            v4[q] = vv;
+            p4[q] = pp;
+            if (qn >= n4) break;
+            q = qn;
+            pp = pn;
+            mm = mn;
+            vv = vn;
+            gg = gn;
+        }
     }
     for (int64_t i = i0 + 4 * n4 + threadIdx.x; i < i1; i += 256) adamw_element(param[i], grad[i], m[i], v[i], gs, decay, a);
 }

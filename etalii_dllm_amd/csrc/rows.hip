@@ -337,6 +337,29 @@ __global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ x, 
         out[i] = dsilu(x[i]);
 }
 
+// gelu_tanh (nn.hpp:481-485): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), in double, rounded once.
+__device__ __forceinline__ float dgelu_tanh(float x) {
+    const double c = 7.97884560802865355879e-01;  // sqrt(2 / pi)
+    const double d = x;
+    return static_cast<float>(0.5 * d * (1.0 + dtanh(c * (d + 0.044715 * d * d * d))));
+}
+
+__global__ __launch_bounds__(256) void gelu_tanh_kernel(const float* __restrict__ x, float* __restrict__ out,
+                                                        int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        out[i] = dgelu_tanh(x[i]);
+}
+
+// The gated GELU-tanh activation (gated_activation<gelu_tanh>, nn.hpp:488-492): the activation rounded, then a float
+// multiply.
+__global__ __launch_bounds__(256) void geglu_tanh_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                         float* __restrict__ out, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        out[i] = dgelu_tanh(gate[i]) * up[i];
+}
+
 __global__ __launch_bounds__(256) void swiglu_forward_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                              float* __restrict__ gate_act, float* __restrict__ product,
                                                              int64_t n) {
@@ -542,6 +565,18 @@ int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, f
         hipLaunchKernelGGL(swiglu_forward_kernel, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
                            up + d, gate_act ? gate_act + d : nullptr, product + d, n - d);
     return check_launch("swiglu");
+}
+
+int launch_gelu_tanh(const float* x, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(gelu_tanh_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, out, n);
+    return check_launch("gelu_tanh");
+}
+
+int launch_geglu_tanh(const float* gate, const float* up, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(geglu_tanh_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, gate, up, out, n);
+    return check_launch("swiglu gelu_tanh");
 }
 
 int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream) {

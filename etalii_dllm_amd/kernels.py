@@ -57,7 +57,8 @@ def _load() -> C.CDLL:
     lib.dllm_hip_attention.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, C.c_double, C.c_int,
                                        C.c_int64, _sz, C.c_double, _vp, _sz, _vp]
     lib.dllm_hip_silu.argtypes = [_vp, _vp, _sz, _vp]
-    lib.dllm_hip_swiglu.argtypes = [_vp, _vp, _vp, _sz, _vp]
+    lib.dllm_hip_swiglu.argtypes = [_vp, _vp, _vp, _sz, C.c_int, _vp]
+    lib.dllm_hip_gelu_tanh.argtypes = [_vp, _vp, _sz, _vp]
     lib.dllm_hip_linear_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
     lib.dllm_hip_rms_norm_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, C.c_double, C.c_int, _vp, _sz,
                                                _vp]
@@ -240,15 +241,23 @@ def silu(x) -> np.ndarray:
     return out.download(x.shape)
 
 
+def gelu_tanh(x) -> np.ndarray:
+    """kernels.cpp:632: elementwise tanh-approximated GELU."""
+    x = _f32(x)
+    dx, out = Device.of(x), Device(x.nbytes)
+    check(lib.dllm_hip_gelu_tanh(dx.ptr, out.ptr, x.size, None))
+    return out.download(x.shape)
+
+
 def swiglu(gate, up, kind=0) -> np.ndarray:
-    """kernels.cpp:633-649 (kind 0, silu; the tanh-GELU kind is outside this backend's families)."""
+    """kernels.cpp:633-649: f32(act(gate)) * up, act silu (kind 0) or gelu_tanh (kind 2)."""
     gate, up = _f32(gate), _f32(up)
     if gate.size != up.size:
         raise ValueError("gate and up must have the same size")
-    if kind != 0:
-        raise ValueError("kind must be silu (0)")
+    if kind not in (0, 2):
+        raise ValueError("kind must be silu (0) or gelu_tanh (2)")
     dg, du, out = Device.of(gate), Device.of(up), Device(gate.nbytes)
-    check(lib.dllm_hip_swiglu(dg.ptr, du.ptr, out.ptr, gate.size, None))
+    check(lib.dllm_hip_swiglu(dg.ptr, du.ptr, out.ptr, gate.size, int(kind), None))
     return out.download(gate.shape)
 
 

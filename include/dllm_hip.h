@@ -72,10 +72,12 @@ int dllm_hip_attention(const float* q, const float* k, const float* v, float* ou
                        int64_t q_offset, size_t window, double softcap, void* workspace, size_t workspace_bytes,
                        void* stream);
 
-/* silu elementwise (kernels.cpp:628, nn.hpp:467-470) and swiglu = f32(silu(gate)) * up (kernels.cpp:633-649 with
- * kind 0, nn.hpp:489-492). */
+/* silu elementwise (kernels.cpp:628, nn.hpp:467-470), gelu_tanh elementwise (kernels.cpp:632, nn.hpp:481-485) and
+ * swiglu = f32(act(gate)) * up with act silu (kind 0) or gelu_tanh (kind 2); another kind is an invalid argument
+ * (kernels.cpp:633-649, nn.hpp:488-492). */
 int dllm_hip_silu(const float* x, float* out, size_t n, void* stream);
-int dllm_hip_swiglu(const float* gate, const float* up, float* out, size_t n, void* stream);
+int dllm_hip_gelu_tanh(const float* x, float* out, size_t n, void* stream);
+int dllm_hip_swiglu(const float* gate, const float* up, float* out, size_t n, int kind, void* stream);
 
 /* ---- backward kernels ---- */
 

@@ -473,6 +473,13 @@ float orc_silu_backward(float x, float dy) {
     return (float)((double)dy * s * (1.0 + d * (1.0 - s)));
 }
 
+/* gelu_tanh (nn.hpp:481-485): 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in double, rounded once. */
+float orc_gelu_tanh(float x) {
+    const double c = 7.97884560802865355879e-01; /* sqrt(2 / pi) */
+    const double d = x;
+    return (float)(0.5 * d * (1.0 + orc_tanh(c * (d + 0.044715 * d * d * d))));
+}
+
 /* gelu_tanh_backward (grad.hpp:183-191): u = sqrt(2/pi) (x + 0.044715 x^3), t = tanh(u), dy times
  * 0.5 (1 + t) + 0.5 x (1 - t^2) sqrt(2/pi) (1 + 3 0.044715 x^2), in double, rounded once. */
 float orc_gelu_tanh_backward(float x, float dy) {

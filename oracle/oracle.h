@@ -60,6 +60,7 @@ void orc_linear_backward(const float* x, const float* w, const float* dy, float*
 void orc_rms_norm_backward(const float* x, const float* w, const float* dy, float* dx, float* dw, size_t rows,
                            size_t dim, double eps, int unit_offset);     /* grad.hpp:79-111 */
 float orc_silu_backward(float x, float dy);                              /* grad.hpp:177-181 */
+float orc_gelu_tanh(float x);                                            /* nn.hpp:481-485 */
 float orc_gelu_tanh_backward(float x, float dy);                         /* grad.hpp:183-191 */
 float orc_softcap_backward(float x, float dy, double cap);               /* grad.hpp:193-197 */
 void orc_attention_backward(const float* q, const float* k, const float* v, const float* dout, float* dq, float* dk,

@@ -139,6 +139,7 @@ double ref_tanh(double x) { FpEnvGuard g; return dllm::tanh(x); }
 double ref_sigmoid(double x) { FpEnvGuard g; return dllm::sigmoid(x); }
 float ref_silu(float x) { FpEnvGuard g; return dllm::silu(x); }
 float ref_silu_backward(float x, float dy) { FpEnvGuard g; return dllm::silu_backward(x, dy); }
+float ref_gelu_tanh(float x) { FpEnvGuard g; return dllm::gelu_tanh(x); }
 float ref_gelu_tanh_backward(float x, float dy) { FpEnvGuard g; return dllm::gelu_tanh_backward(x, dy); }
 float ref_softcap_backward(float x, float dy, double cap) { FpEnvGuard g; return dllm::softcap_backward(x, dy, cap); }
 

@@ -62,6 +62,8 @@ def oracle() -> C.CDLL:
         lib.orc_silu.argtypes = [C.c_float]
         lib.orc_silu_backward.restype = C.c_float
         lib.orc_silu_backward.argtypes = [C.c_float, C.c_float]
+        lib.orc_gelu_tanh.restype = C.c_float
+        lib.orc_gelu_tanh.argtypes = [C.c_float]
         lib.orc_gelu_tanh_backward.restype = C.c_float
         lib.orc_gelu_tanh_backward.argtypes = [C.c_float, C.c_float]
         lib.orc_softcap_backward.restype = C.c_float
@@ -92,6 +94,8 @@ def ref() -> C.CDLL:
         lib.ref_silu.argtypes = [C.c_float]
         lib.ref_silu_backward.restype = C.c_float
         lib.ref_silu_backward.argtypes = [C.c_float, C.c_float]
+        lib.ref_gelu_tanh.restype = C.c_float
+        lib.ref_gelu_tanh.argtypes = [C.c_float]
         lib.ref_gelu_tanh_backward.restype = C.c_float
         lib.ref_gelu_tanh_backward.argtypes = [C.c_float, C.c_float]
         lib.ref_softcap_backward.restype = C.c_float
@@ -968,6 +972,12 @@ def q8_0_cases() -> dict[str, np.ndarray]:
     special[96:128] = 0.0
     cases["special"] = special
     return cases
+
+
+def gelu_tanh(x) -> np.ndarray:
+    """The oracle's gelu_tanh (nn.hpp:481-485), elementwise."""
+    f = oracle().orc_gelu_tanh
+    return np.array([f(float(a)) for a in np.ravel(x)], np.float32).reshape(np.shape(x))
 
 
 def gelu_tanh_backward(x, dy) -> np.ndarray:

@@ -126,12 +126,19 @@ def test_elementwise(K, ora):
     assert_same(K.silu(g), ora.silu(g), "silu")
     assert_same(K.swiglu(g, up), ora.swiglu(g, up), "swiglu")
     assert_same(K.silu_backward(g, up), ora.silu_backward(g, up), "silu_backward")
+    assert_same(K.gelu_tanh(g), O.gelu_tanh(g), "gelu_tanh")
+    assert_same(K.swiglu(g, up, 2), O.gelu_tanh(g) * up, "swiglu kind 2 (gelu_tanh, rounded, then the multiply)")
+    with pytest.raises(ValueError, match="kind"):
+        K.swiglu(g, up, 1)
 
 
-@pytest.mark.parametrize(("rows", "vocab"), [(6, 301), (3, 5000), (2, 49152)])
+@pytest.mark.parametrize(("rows", "vocab"), [(6, 301), (3, 5000), (2, 49152), (6, 1024), (5, 515), (9, 2049),
+                                             (6, 151936)])
 def test_cross_entropy(K, ora, rows, vocab):
+    """Row counts that do and do not fill the 4-row waves; vocabularies of whole 512-column chunks, a partial last
+    chunk, one that is not a multiple of 4 (the scalar loads) and the full 151936."""
     logits = O.gaussian(16, rows, vocab, scale=4.0)
-    targets = np.array([3, -1, vocab - 1, 0, 17, 17][:rows], np.int64)
+    targets = np.array([3, -1, vocab - 1, 0, 17, 17, 5, -1, 2][:rows], np.int64)
     la, da = K.cross_entropy(logits, targets, 0.25)
     lb, db = ora.cross_entropy(logits, targets, 0.25)
     assert la == lb
@@ -390,3 +397,48 @@ def test_biased_attention_and_backward_match_the_oracle(K, q_len, kv_len, heads,
                                enc.biased_attention_backward(q, k, v, bias, dout, 0.25),
                                ("dq", "dk", "dv", "dbias")):
         assert_same_or_nan(got, want, f"biased_attention_backward {what}")
+
+
+def test_elementwise_scalar_tails_and_misaligned_views(K, ora):
+    """The 16-byte vector kernels (SwiGLU, AdamW) hand n % 4 tail elements and arrays that are not 16-byte aligned to
+    their scalar kernels: n = 5001, and device views starting 4 bytes into an allocation, through the C ABI."""
+    import ctypes as C
+
+    n = 5001
+    g, up = O.gaussian(51, n, scale=6.0), O.gaussian(52, n)
+    assert_same(K.swiglu(g, up), ora.swiglu(g, up), "swiglu n % 4 = 1")
+    assert_same(K.silu_backward(g, up), ora.silu_backward(g, up), "silu_backward n % 4 = 1")
+    lib, Device = K.lib, K.Device
+
+    def shifted(values):  # a device copy that starts 4 bytes into its allocation
+        d = Device(values.nbytes + 16)
+        K.check(lib.dllm_hip_upload(C.c_void_p(d.ptr.value + 4), values.ctypes.data, values.nbytes))
+        return d, C.c_void_p(d.ptr.value + 4)
+
+    def fetch(p, count):
+        out = np.empty(count, np.float32)
+        K.check(lib.dllm_hip_download(out.ctypes.data, p, out.nbytes))
+        return out
+
+    dg, pg = shifted(g)
+    du, pu = shifted(up)
+    do, po = shifted(np.zeros(n, np.float32))
+    K.check(lib.dllm_hip_swiglu(pg, pu, po, n, 0, None))
+    assert_same(fetch(po, n), ora.swiglu(g, up), "swiglu misaligned")
+    p, grad = O.gaussian(53, n, scale=0.02), O.gaussian(54, n, scale=1e-3)
+    m, v = O.gaussian(55, n, scale=1e-4), np.abs(O.gaussian(56, n, scale=1e-6))
+    args = (1e-3, 0.9, 0.999, 1e-8, 0.01, 1 - 0.9 ** 2, 1 - 0.999 ** 2, 0.7)
+    dp, pp = shifted(p)
+    dgr, pgr = shifted(grad)
+    dm, pm = shifted(m)
+    dv, pv = shifted(v)
+    K.check(lib.dllm_hip_adamw_step(pp, pgr, pm, pv, n, *args, None))
+    want_p, want_m, want_v = p.copy(), m.copy(), v.copy()
+    ora.adamw_step(want_p, grad, want_m, want_v, *args)
+    assert_same(fetch(pp, n), want_p, "adamw param misaligned")
+    assert_same(fetch(pm, n), want_m, "adamw m misaligned")
+    assert_same(fetch(pv, n), want_v, "adamw v misaligned")
+    K.adamw_step(p, grad, m, v, *args)  # aligned, n % 4 = 1
+    assert_same(p, want_p, "adamw param n % 4 = 1")
+    assert_same(m, want_m, "adamw m n % 4 = 1")
+    assert_same(v, want_v, "adamw v n % 4 = 1")

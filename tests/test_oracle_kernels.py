@@ -298,9 +298,25 @@ def test_gelu_tanh_and_softcap_backward_match_reference():
     dy = O.gaussian(33, x.size)
     want = np.array([r.ref_gelu_tanh_backward(float(a), float(b)) for a, b in zip(x, dy)], np.float32)
     assert same(O.gelu_tanh_backward(x, dy), want)
+    assert same(O.gelu_tanh(x), np.array([r.ref_gelu_tanh(float(a)) for a in x], np.float32))
     for cap in (30.0, 50.0, 0.5):
         want = np.array([r.ref_softcap_backward(float(a), float(b), cap) for a, b in zip(x, dy)], np.float32)
         assert same(O.softcap_backward(x, dy, cap), want)
+
+
+def test_gelu_tanh_matches_the_closed_form():
+    """nn.hpp:481-485 against numpy's tanh in double, rounded once: within one float ulp for x >= -4 (the portable tanh
+    differs from libm's by a few double ulps, which moves a float rounding at most one step), and within 1e-13
+    absolutely in the negative tail, where 1 + tanh cancels and those double ulps dominate the tiny result."""
+    x = np.concatenate([O.gaussian(35, 2000, scale=3.0), np.array([0.0, -0.0, 30.0, -30.0, 1e-20], np.float32)])
+    c = np.sqrt(2.0 / np.pi)
+    d = x.astype(np.float64)
+    want = (0.5 * d * (1.0 + np.tanh(c * (d + 0.044715 * d * d * d)))).astype(np.float32)
+    got = O.gelu_tanh(x)
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert np.all(ulps[x >= -4] <= 1)
+    assert np.all(np.abs(got.astype(np.float64) - want.astype(np.float64)) <= 1e-13)
+    assert got[-5] == 0.0 and got[-3] == np.float32(30.0) and got[-2] == 0.0
 
 
 def test_gelu_tanh_and_softcap_backward_match_numeric_gradients():
