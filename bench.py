@@ -150,25 +150,21 @@ def matmul_flops_per_step(cfg) -> float:
     return 6.0 * params * cfg["batch"] * cfg["seq"]
 
 
-def cpu_baseline(cfg) -> dict | None:
-    """The reference CPU path (its own kernels from oracle/_ref, or the oracle's C restatement when that library is
-    absent), driven by the oracle's step orchestration, timed on a bounded sample of the step and scaled to it:
-      one window of `seq` tokens through a 1-layer model of this architecture with a 4096-token vocabulary;
-      the head (linear, cross-entropy, linear_backward) at 8192 vocabulary rows over seq rows, scaled to the vocab;
-      adamw_step and sum_squares on 16M elements, scaled to the parameter count.
-    step = batch x (layers x (window - head share) + head x vocab / 8192) + optimizer x params / 16M."""
-    sys.path.insert(0, str(ROOT / "tests"))
-    import oracle_lib as O
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    kind = "reference" if O.reference_available() else "port"
-    cores = 1
-    if kind == "reference":
-        kern = O.ref_kernels()
-        cores = min(16, os.cpu_count() or 1)
-        O.ref().ref_set_threads(C.c_size_t(cores))
-    else:
-        kern = O.oracle_kernels()
-    T, V, H = min(cfg["seq"], 1024), cfg["vocab"], cfg["hidden"]
+
+def _cpu_sample(O, kern, cfg, T: int, head_rows: int, n_opt: int):
+    """Seconds of (one window of T tokens through a 1-layer model of this architecture, vocab 4096), (the head at
+    head_rows vocabulary rows over T rows: linear, cross-entropy, linear_backward) and (sum_squares + adamw_step on
+    n_opt elements)."""
+    H = cfg["hidden"]
     small = O.Decoder("sample", vocab=4096, hidden=H, inter=cfg["intermediate"], layers=1, heads=cfg["heads"],
                       kv_heads=cfg["kv_heads"], head_dim=cfg["head_dim"], eps=cfg["rms_norm_eps"],
                       rope_theta=cfg["rope_theta"], tied=cfg["tie_embeddings"], attn_bias=cfg["attention_bias"],
@@ -183,39 +179,72 @@ def cpu_baseline(cfg) -> dict | None:
                        router_scale=cfg.get("router_aux_loss", 0.0) / cfg["batch"])
     t_window = time.perf_counter() - t0
     hidden = O.gaussian(SEED + 1, T, H)
-    head = O.gaussian(SEED + 2, 8192, H, scale=0.02)
-    targets = np.array([rng.next_u64() % 8192 for _ in range(T)], np.int64)
+    head = O.gaussian(SEED + 2, head_rows, H, scale=0.02)
+    targets = np.array([rng.next_u64() % head_rows for _ in range(T)], np.int64)
     t0 = time.perf_counter()
     logits = kern.linear(hidden, head)
     _, dlogits = kern.cross_entropy(logits, targets, 1.0 / T)
     kern.linear_backward(hidden, head, dlogits)
     t_head = time.perf_counter() - t0
-    n = 16 * 1024 * 1024
-    p, g = O.gaussian(SEED + 3, n, scale=0.02), O.gaussian(SEED + 4, n, scale=1e-3)
-    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    p, g = O.gaussian(SEED + 3, n_opt, scale=0.02), O.gaussian(SEED + 4, n_opt, scale=1e-3)
+    m, v = np.zeros(n_opt, np.float32), np.zeros(n_opt, np.float32)
     t0 = time.perf_counter()
     kern.sum_squares(g)
     kern.adamw_step(p, g, m, v, 1e-4, 0.9, 0.999, 1e-8, 0.01, 0.1, 0.001, 1.0)
     t_opt = time.perf_counter() - t0
+    return t_window, t_head, t_opt
+
+
+def cpu_baseline(cfg) -> dict | None:
+    """The reference CPU path (its own kernels from oracle/_ref, or the oracle's C restatement when that library is
+    absent), driven by the oracle's step orchestration, timed on a bounded sample of the step and scaled to it, with
+    the reference's thread pool at this host's cores (nproc, capped at the 16 cores a one-GPU box grants a job) and
+    again at 1 thread:
+      one window of T tokens through a 1-layer model of this architecture with a 4096-token vocabulary;
+      the head (linear, cross-entropy, linear_backward) at R vocabulary rows over T rows, scaled to the vocab;
+      adamw_step and sum_squares on N elements, scaled to the parameter count.
+    step = batch x (seq / T) x (layers x (window - head share) + head x vocab / R) + optimizer x params / N.
+    The many-thread sample is T = 1024, R = 8192, N = 16M; the 1-thread one T = 256, R = 2048, N = 4M."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O
+
+    kind = "reference" if O.reference_available() else "port"
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = min(16, nproc) if kind == "reference" else 1
+    kern = O.ref_kernels() if kind == "reference" else O.oracle_kernels()
     params = sum(int(np.prod(s)) for s in tensor_shapes(cfg).values())
     if "lora" in cfg:  # AdamW runs over the adapters only
-        q, kv, inter = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"], cfg["intermediate"]
+        H, q, kv, inter = cfg["hidden"], cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"], cfg["intermediate"]
         params = cfg["layers"] * cfg["lora"]["rank"] * (2 * (H + q) + 2 * (H + kv) + 3 * (H + inter))
-    stretch = cfg["seq"] / T  # a window longer than the sample: linear in tokens (understates the attention)
-    layer = t_window - t_head * 4096 / 8192
-    step = cfg["batch"] * stretch * (cfg["layers"] * layer + t_head * V / 8192) + t_opt * params / n
-    tokens_per_step = cfg["batch"] * cfg["seq"]
+    V, tokens_per_step = cfg["vocab"], cfg["batch"] * cfg["seq"]
+
+    def extrapolate(T, R, N, t_window, t_head, t_opt):
+        stretch = cfg["seq"] / T  # a window longer than the sample: linear in tokens (understates the attention)
+        layer = t_window - t_head * 4096 / R
+        return cfg["batch"] * stretch * (cfg["layers"] * layer + t_head * V / R) + t_opt * params / N
+
+    runs = {}
+    for n_threads, (T, R, N) in ((threads, (min(cfg["seq"], 1024), 8192, 16 << 20)), (1, (256, 2048, 4 << 20))):
+        if kind == "reference":
+            O.ref().ref_set_threads(C.c_size_t(n_threads))
+        times = _cpu_sample(O, kern, cfg, T, R, N)
+        runs[n_threads] = (T, R, N, times, extrapolate(T, R, N, *times))
+    T, R, N, (t_window, t_head, t_opt), step = runs[threads]
+    step1 = runs[1][4]
     return {
         "value": tokens_per_step / step,
         "unit": "tokens/s",
-        "cores": cores,
+        "cores": threads,
         "kind": kind,
-        "sample": (f"1-layer {cfg['name']}-shaped model, 1 window x {T} tokens, vocab 4096 ({t_window:.2f} s); "
-                   + (f"scaled linearly to {cfg['seq']}-token windows; " if stretch != 1 else "")
-                   + ("the base's gradients stand for the LoRA step; " if "lora" in cfg else "") +
-                   f"head at 8192 vocab rows ({t_head:.2f} s); optimizer on 16M params ({t_opt:.2f} s); "
-                   f"scaled to {cfg['layers']} layers, vocab {V}, batch {cfg['batch']}, {params} params: "
-                   f"{step:.1f} s per step (extrapolated)"),
+        "value_1_thread": tokens_per_step / step1,
+        "nproc": nproc,
+        "cpu_model": _cpu_model(),
+        "sample": (f"{threads} threads of {nproc} ({_cpu_model()}): 1-layer {cfg['name']}-shaped model, 1 window x {T} "
+                   f"tokens, vocab 4096 ({t_window:.2f} s); head at {R} vocab rows ({t_head:.2f} s); optimizer on "
+                   f"{N} params ({t_opt:.2f} s); scaled to {cfg['layers']} layers, {cfg['seq']}-token windows, vocab "
+                   f"{V}, batch {cfg['batch']}, {params} params: {step:.1f} s per step (extrapolated)"
+                   + ("; the base's gradients stand for the LoRA step" if "lora" in cfg else "")
+                   + f". 1 thread (T {runs[1][0]}, {runs[1][1]} head rows, {runs[1][2]} params): {step1:.1f} s per step"),
     }
 
 
@@ -223,15 +252,15 @@ COPY_BYTES = 1 << 30
 
 
 def copy_calibration() -> int:
-    """A plain copy kernel of known size (1 GiB read, 1 GiB written), three times: under rocprofv3 --pmc its
+    """A plain copy kernel of known size (the library's dllm_hip_copy of 1 GiB), three times: under rocprofv3 --pmc its
     FETCH_SIZE / WRITE_SIZE give the counters' scale against bytes actually moved."""
-    import torch
+    from etalii_dllm_amd import kernels as K
 
-    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
-    dst = torch.empty_like(src)
+    src, dst = K.Device(COPY_BYTES), K.Device(COPY_BYTES)
+    K.check(K.lib.dllm_hip_memset(src.ptr, 1, COPY_BYTES))
     for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+        K.check(K.lib.dllm_hip_copy(dst.ptr, src.ptr, COPY_BYTES, None))
+    K.check(K.lib.dllm_hip_synchronize())
     return 0
 
 
@@ -352,12 +381,131 @@ def kernel_suite(iters: int = 20) -> int:
     return 0
 
 
+C2_SHAPES = dict(hidden=896, heads=14, kv_heads=2, head_dim=64, intermediate=4864, rope_theta=1e6)
+C2_SWEEP = (1, 7, 64, 2048, 8192)
+
+
+def c2_microbench(iters: int = 20) -> int:
+    """the per-op backward kernels at Qwen2.5-0.5B layer shapes through the C ABI on
+    device-resident inputs (weights N(0, 0.02), activations N(0, 1), upstream gradients N(0, 1e-3)), at each row count
+    M of the sweep: the layer's seven linear_backward calls (dX and dW), dX and dW of the gate projection alone,
+    rms_norm_backward, the RoPE backward of q and k, silu_backward over the SwiGLU width, causal GQA
+    attention_backward over one sequence of M tokens, and one adamw_step over the layer's 14.9M parameters. Each op's
+    time per call (mean of `iters` calls after 3 warmups) and its rate against the bound that applies: FP64 78.6
+    TFLOP/s for the matmuls and attention, HBM 8 TB/s for the rest (plus the rate of the library's own device copy on
+    this box, the practical streaming ceiling). One JSON line."""
+    from etalii_dllm_amd import kernels as K
+
+    lib, rng = K.lib, np.random.default_rng(0)
+    H, nh, nkv, hd, inter = (C2_SHAPES[k] for k in ("hidden", "heads", "kv_heads", "head_dim", "intermediate"))
+    hbm = 8.0e12
+
+    def gauss(*shape, scale=1.0):
+        return K.Device.of((rng.standard_normal(shape) * scale).astype(np.float32))
+
+    def timed(run, n=iters) -> float:
+        for _ in range(3):
+            run()
+        K.check(lib.dllm_hip_synchronize())
+        t = time.perf_counter()
+        for _ in range(n):
+            run()
+        K.check(lib.dllm_hip_synchronize())
+        return (time.perf_counter() - t) / n
+
+    ops = []
+
+    def report(op, m, seconds, work, bound):
+        rate = work / seconds
+        if bound == "fp64":
+            entry = {"op": op, "M": m, "us": round(seconds * 1e6, 2), "TFLOPs": round(rate / 1e12, 3),
+                     "frac": round(rate / (FP64_PEAK_TFLOPS * 1e12), 4)}
+        else:
+            entry = {"op": op, "M": m, "us": round(seconds * 1e6, 2), "GBps": round(rate / 1e9, 1),
+                     "frac": round(rate / hbm, 4)}
+        ops.append(entry)
+        log(json.dumps(entry))
+
+    copy_bytes = 1 << 30
+    src, dst = K.Device(copy_bytes), K.Device(copy_bytes)
+    t_copy = timed(lambda: K.check(lib.dllm_hip_copy(dst.ptr, src.ptr, copy_bytes, None)), 10)
+    copy_rate = 2.0 * copy_bytes / t_copy
+    del src, dst
+    mats = {"q": (H, nh * hd), "k": (H, nkv * hd), "v": (H, nkv * hd), "o": (nh * hd, H), "gate": (H, inter),
+            "up": (H, inter), "down": (inter, H)}  # (in, out)
+    weights = {n: gauss(o, i, scale=0.02) for n, (i, o) in mats.items()}
+    mmax = C2_SWEEP[-1]
+    x_in = {i: gauss(mmax, i) for i in {H, nh * hd, inter}}
+    dy_out = {o: gauss(mmax, o, scale=1e-3) for o in {H, nh * hd, nkv * hd, inter}}
+    dx = K.Device(mmax * max(H, inter, nh * hd) * 4)
+    dw = K.Device(max(i * o for i, o in mats.values()) * 4)
+    db = K.Device(max(o for _, o in mats.values()) * 4)
+    norm_w = gauss(H, scale=0.02)
+    qh, kh = gauss(mmax, nh, hd), gauss(mmax, nkv, hd)
+    vh, douth = gauss(mmax, nkv, hd), gauss(mmax, nh, hd, scale=1e-3)
+    gq, gk, gv = K.Device(mmax * nh * hd * 4), K.Device(mmax * nkv * hd * 4), K.Device(mmax * nkv * hd * 4)
+    inv = np.ascontiguousarray(1.0 / (C2_SHAPES["rope_theta"] ** (np.arange(0, hd, 2, dtype=np.float64) / hd)))
+    inv_d = K.Device.of(inv)
+    pos_d = K.Device.of(np.arange(mmax, dtype=np.int64))
+    n_params = sum(i * o for i, o in mats.values()) + 2 * H
+    pp, gg = gauss(n_params, scale=0.02), gauss(n_params, scale=1e-3)
+    mm, vv = gauss(n_params, scale=1e-4), K.Device.of(np.abs(rng.standard_normal(n_params) * 1e-6).astype(np.float32))
+    for m in C2_SWEEP:
+        n_it = iters if m >= 2048 else 5 * iters
+        total, flop = 0.0, 0.0
+        for name, (i, o) in mats.items():
+            ws = K.Device(lib.dllm_hip_linear_backward_workspace(m, i, o))
+            t = timed(lambda: K.check(lib.dllm_hip_linear_backward(x_in[i].ptr, weights[name].ptr, dy_out[o].ptr,
+                                                                   dx.ptr, dw.ptr, None, m, i, o, ws.ptr, ws.nbytes,
+                                                                   None)), n_it)
+            total += t
+            flop += 4.0 * m * i * o
+        report("linear_backward (7 layer matrices, dX + dW)", m, total, flop, "fp64")
+        i, o = mats["gate"]
+        ws = K.Device(lib.dllm_hip_linear_backward_workspace(m, i, o))
+        t = timed(lambda: K.check(lib.dllm_hip_linear_backward(x_in[i].ptr, weights["gate"].ptr, dy_out[o].ptr, dx.ptr,
+                                                               None, None, m, i, o, ws.ptr, ws.nbytes, None)), n_it)
+        report("dX gate (896 -> 4864)", m, t, 2.0 * m * i * o, "fp64")
+        t = timed(lambda: K.check(lib.dllm_hip_linear_backward(x_in[i].ptr, weights["gate"].ptr, dy_out[o].ptr, None,
+                                                               dw.ptr, db.ptr, m, i, o, ws.ptr, ws.nbytes, None)), n_it)
+        report("dW + db gate (896 -> 4864)", m, t, 2.0 * m * i * o, "fp64")
+        ws = K.Device(lib.dllm_hip_rms_norm_backward_workspace(m))
+        t = timed(lambda: K.check(lib.dllm_hip_rms_norm_backward(x_in[H].ptr, norm_w.ptr, dy_out[H].ptr, dx.ptr,
+                                                                 dw.ptr, m, H, 1e-6, 0, ws.ptr, ws.nbytes, None)), n_it)
+        report("rms_norm_backward (dx, dw)", m, t, 12.0 * m * H, "hbm")
+        wsq = K.Device(lib.dllm_hip_rope_workspace(m, hd))
+        t = timed(lambda: (K.check(lib.dllm_hip_rope(qh.ptr, pos_d.ptr, inv_d.ptr, gq.ptr, m, nh, hd, hd, 0, 1,
+                                                     wsq.ptr, wsq.nbytes, None)),
+                           K.check(lib.dllm_hip_rope(kh.ptr, pos_d.ptr, inv_d.ptr, gk.ptr, m, nkv, hd, hd, 0, 1,
+                                                     wsq.ptr, wsq.nbytes, None))), n_it)
+        report("rope backward (q and k)", m, t, 8.0 * m * (nh + nkv) * hd, "hbm")
+        t = timed(lambda: K.check(lib.dllm_hip_silu_backward(x_in[inter].ptr, dy_out[inter].ptr, dx.ptr, m * inter,
+                                                             None)), n_it)
+        report("silu_backward (SwiGLU width)", m, t, 12.0 * m * inter, "hbm")
+        wsa = K.Device(lib.dllm_hip_attention_backward_workspace(m, m, nh, nkv, hd, hd, 1, 0, 0, 0.0))
+        t = timed(lambda: K.check(lib.dllm_hip_attention_backward(
+            qh.ptr, kh.ptr, vh.ptr, douth.ptr, gq.ptr, gk.ptr, gv.ptr, m, m, nh, nkv, hd, hd, 1.0 / np.sqrt(hd), 1, 0,
+            0, 0.0, wsa.ptr, wsa.nbytes, None)), max(3, n_it // 4) if m >= 2048 else n_it)
+        del wsa
+        report("attention_backward (causal GQA 14/2 x 64)", m, t, 10.0 * hd * nh * m * (m + 1) / 2, "fp64")
+    t = timed(lambda: K.check(lib.dllm_hip_adamw_step(pp.ptr, gg.ptr, mm.ptr, vv.ptr, n_params, 1e-4, 0.9, 0.999, 1e-8,
+                                                      0.01, 0.1, 0.001, 1.0, None)))
+    report("adamw_step (layer, 14.9M params)", n_params, t, 28.0 * n_params, "hbm")
+    print(json.dumps({"metric": "C2 per-op backward microbench, Qwen2.5-0.5B layer shapes, bit-exact vs CPU",
+                      "unit": "us per call", "higher_is_better": False, "n_gpus": 1, "dtype": "f64",
+                      "data": "synthetic (Gaussian weights x 0.02, activations x 1, gradients x 1e-3)",
+                      "config": {"workload": "Qwen2.5-0.5B layer backward ops", "M": list(C2_SWEEP), **C2_SHAPES},
+                      "hbm_copy_GBps": round(copy_rate / 1e9, 1), "hbm_copy_frac": round(copy_rate / hbm, 4),
+                      "ops": ops}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c2"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--export-timing", action="store_true",
                     help="after the timed steps, time the model and checkpoint fingerprints streamed from device "
@@ -372,6 +520,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.kernels:
         return kernel_suite()
+    if args.config == "c2":
+        return c2_microbench()
     if args.copy_calibration:
         return copy_calibration()
     if args.traffic_summary:

@@ -52,6 +52,9 @@ int dllm_hip_download(void* dst, const void* src, size_t bytes) {
 }
 int dllm_hip_memset(void* p, int value, size_t bytes) { return check_hip(hipMemset(p, value, bytes), "memset"); }
 int dllm_hip_synchronize(void) { return check_hip(hipDeviceSynchronize(), "synchronize"); }
+int dllm_hip_copy(void* dst, const void* src, size_t bytes, void* stream) {
+    return launch_device_copy(dst, src, bytes, static_cast<hipStream_t>(stream));
+}
 
 namespace {
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }

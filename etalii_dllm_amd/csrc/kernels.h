@@ -97,6 +97,8 @@ int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream);
 int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
                           hipStream_t stream);
 int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
+// A device-to-device copy of `bytes` (16-byte vectors when both pointers allow).
+int launch_device_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);
 // gelu_tanh elementwise (nn.hpp:481-485) and the gated form f32(gelu_tanh(gate)) * up (nn.hpp:488-492).
 int launch_gelu_tanh(const float* x, float* out, int64_t n, hipStream_t stream);
 int launch_geglu_tanh(const float* gate, const float* up, float* out, int64_t n, hipStream_t stream);

@@ -7,6 +7,8 @@
 // reference's operand order.
 #include <initializer_list>
 
+#include <algorithm>
+
 #include "common.h"
 #include "devmath.h"
 #include "kernels.h"
@@ -565,6 +567,36 @@ int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, f
         hipLaunchKernelGGL(swiglu_forward_kernel, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
                            up + d, gate_act ? gate_act + d : nullptr, product + d, n - d);
     return check_launch("swiglu");
+}
+
+// A plain device copy of n4 16-byte vectors, four in flight per thread, then the n % 16 tail bytes one by one.
+__global__ __launch_bounds__(256) void device_copy_kernel(const float4* __restrict__ src, float4* __restrict__ dst,
+                                                          int64_t n4, const unsigned char* __restrict__ src_tail,
+                                                          unsigned char* __restrict__ dst_tail, int64_t tail) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * 4;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * 256 * 4 + threadIdx.x;
+    for (; i + 3 * 256 < n4; i += stride) {
+        float4 t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = src[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dst[i + u * 256] = t[u];
+    }
+    for (; i < n4; i += 256) dst[i] = src[i];
+    if (blockIdx.x == 0 && threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
+}
+
+int launch_device_copy(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return kOk;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) == 0;
+    if (!aligned) return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, stream), "copy");
+    const int64_t n4 = static_cast<int64_t>(bytes / 16), tail = static_cast<int64_t>(bytes % 16);
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n4, 1024), 16384));
+    hipLaunchKernelGGL(device_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       static_cast<const float4*>(src), static_cast<float4*>(dst), n4,
+                       static_cast<const unsigned char*>(src) + 16 * n4, static_cast<unsigned char*>(dst) + 16 * n4,
+                       tail);
+    return check_launch("copy");
 }
 
 int launch_gelu_tanh(const float* x, float* out, int64_t n, hipStream_t stream) {

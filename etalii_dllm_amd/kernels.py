@@ -51,6 +51,7 @@ def _load() -> C.CDLL:
     lib.dllm_hip_upload.argtypes = [_vp, _vp, _sz]
     lib.dllm_hip_download.argtypes = [_vp, _vp, _sz]
     lib.dllm_hip_memset.argtypes = [_vp, C.c_int, _sz]
+    lib.dllm_hip_copy.argtypes = [_vp, _vp, _sz, _vp]
     lib.dllm_hip_linear.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
     lib.dllm_hip_rms_norm.argtypes = [_vp, _vp, _vp, _sz, _sz, C.c_double, C.c_int, _vp]
     lib.dllm_hip_rope.argtypes = [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, C.c_int, C.c_int, _vp, _sz, _vp]

@@ -38,6 +38,8 @@ int dllm_hip_upload(void* device_dst, const void* host_src, size_t bytes);
 int dllm_hip_download(void* host_dst, const void* device_src, size_t bytes);
 int dllm_hip_memset(void* device_ptr, int value, size_t bytes);
 int dllm_hip_synchronize(void);
+/* Device-to-device copy on `stream` (asynchronous): the library's own streaming kernel. */
+int dllm_hip_copy(void* device_dst, const void* device_src, size_t bytes, void* stream);
 
 /* ---- forward kernels ---- */
 

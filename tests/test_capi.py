@@ -66,3 +66,40 @@ def test_natural_tensor_order_and_names_match_the_oracle_layout():
                                      "token_embedding.weight"]
     assert trainer.DecoderConfig  # the structure is defined and matches the header's field count
     assert len(trainer.DecoderConfig._fields_) == 19
+
+
+@needs_library
+def test_library_random_inputs_match_the_oracle_and_the_reference_goldens():
+    """dllm_hip_random_tokens / dllm_hip_fill_gaussian (host functions: no GPU) are Random (random.hpp) and
+    fill_gaussian (kernels.cpp:206-218): the first two draws of Random(42) are the reference's RANDOM_FIRST and
+    RANDOM_SECOND (checked modulo several vocabularies, the form the library returns them in), and the Gaussians equal
+    the oracle's (and the compiled reference's where it is built) bit for bit, scaled by one float multiply."""
+    import json
+
+    import oracle_lib as O
+    from etalii_dllm_amd.kernels import lib
+
+    golden = json.loads((ROOT / "tests" / "golden" / "reference_goldens.json").read_text())
+    first, second = golden["RANDOM_FIRST"], golden["RANDOM_SECOND"]
+    for vocab in (2, 3, 151936, 49152, 50304, (1 << 61) - 1, (1 << 63) - 1):
+        out = np.empty(2, np.int64)
+        assert lib.dllm_hip_random_tokens(ctypes.c_uint64(42), out.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(2),
+                                          ctypes.c_int64(vocab)) == 0
+        assert out.tolist() == [first % vocab, second % vocab], vocab
+    r = O.Random(7)
+    want = np.array([r.next_u64() % 151936 for _ in range(1000)], np.int64)
+    got = np.empty(1000, np.int64)
+    lib.dllm_hip_random_tokens(ctypes.c_uint64(7), got.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(1000),
+                               ctypes.c_int64(151936))
+    assert np.array_equal(got, want)
+    for seed, n in ((0, 1), (11000, 4099), (2**63 + 5, 777)):
+        want = O.fill_gaussian(seed, n)
+        for scale in (1.0, 0.02):
+            got = np.empty(n, np.float32)
+            assert lib.dllm_hip_fill_gaussian(ctypes.c_uint64(seed), got.ctypes.data_as(ctypes.c_void_p),
+                                              ctypes.c_size_t(n), ctypes.c_float(scale)) == 0
+            assert got.tobytes() == (want * np.float32(scale)).tobytes(), (seed, n, scale)
+        if O.reference_available():
+            ref = np.empty(n, np.float32)
+            O.ref().ref_fill_gaussian(ctypes.c_uint64(seed), ref.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(n))
+            assert ref.tobytes() == want.tobytes()

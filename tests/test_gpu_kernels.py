@@ -442,3 +442,18 @@ def test_elementwise_scalar_tails_and_misaligned_views(K, ora):
     assert_same(p, want_p, "adamw param n % 4 = 1")
     assert_same(m, want_m, "adamw m n % 4 = 1")
     assert_same(v, want_v, "adamw v n % 4 = 1")
+
+
+def test_device_copy(K):
+    """dllm_hip_copy: whole 16-byte vectors plus a byte tail, and a misaligned pair (the runtime's copy)."""
+    import ctypes as C
+
+    for nbytes, offset in ((0, 0), (7, 0), (4096 * 16 + 13, 0), ((1 << 22) + 5, 0), (1000, 4)):
+        src = np.frombuffer(np.random.default_rng(nbytes).bytes(nbytes + 16), np.uint8).copy()
+        ds, dd = K.Device.of(src), K.Device(nbytes + 16)
+        K.check(K.lib.dllm_hip_copy(C.c_void_p(dd.ptr.value + offset), C.c_void_p(ds.ptr.value + offset), nbytes,
+                                    None))
+        K.check(K.lib.dllm_hip_synchronize())
+        got = np.empty(nbytes + 16, np.uint8)
+        K.check(K.lib.dllm_hip_download(got.ctypes.data, dd.ptr, got.nbytes))
+        assert got[offset:offset + nbytes].tobytes() == src[offset:offset + nbytes].tobytes(), nbytes
