@@ -3,9 +3,11 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <vector>
 
 #include "common.h"
+#include "devmath.h"
 #include "dllm_hip.h"
 #include "kernels.h"
 #include "workspace.h"
@@ -61,6 +63,62 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 }  // namespace
 
 size_t dllm_hip_linear_workspace(size_t rows, size_t in, size_t out) { return linear_ws(rows, in, out); }
+
+// rope_inv_freq (numerics.py:267-349): the default frequencies exp(-(2i / dim) log theta) with the portable exp and
+// log, then the scaling, every step in the Python code's double operation order (its ints divide as correctly
+// rounded doubles; min, max, floor and ceil as written).
+int dllm_hip_rope_inv_freq(size_t head_dim, double theta, size_t rotary_dim, const dllm_hip_rope_scaling* sc,
+                           double* out) {
+    const size_t dim = rotary_dim == 0 ? head_dim : rotary_dim;
+    DLLM_REQUIRE(dim > 0 && dim % 2 == 0 && dim <= head_dim, "rotary_dim must be even, positive and at most head_dim");
+    DLLM_REQUIRE(out != nullptr, "null output");
+    const int64_t kind = sc ? sc->kind : 0;
+    DLLM_REQUIRE(kind >= 0 && kind <= 4, "unsupported rope scaling kind");
+    DLLM_REQUIRE(kind != 3 || sc->factors != nullptr, "longrope needs its factors");
+    const size_t pairs = dim / 2;
+    const double log_theta = dlog(theta);
+    for (size_t i = 0; i < pairs; ++i)
+        out[i] = dexp(-(static_cast<double>(2 * i) / static_cast<double>(dim)) * log_theta);
+    const double pi = 3.141592653589793;  // math.pi
+    if (kind == 1) {  // linear: positions divided by the factor
+        for (size_t i = 0; i < pairs; ++i) out[i] = out[i] / sc->factor;
+    } else if (kind == 2) {  // llama3
+        const double low = sc->low_freq_factor, high = sc->high_freq_factor;
+        const double original = sc->original_max_position_embeddings;
+        const double low_freq_wavelen = original / low, high_freq_wavelen = original / high;
+        for (size_t i = 0; i < pairs; ++i) {
+            const double f = out[i];
+            const double wavelen = 2 * pi / f;
+            if (wavelen < high_freq_wavelen) continue;
+            if (wavelen > low_freq_wavelen) {
+                out[i] = f / sc->factor;
+            } else {
+                const double smooth = (original / wavelen - low) / (high - low);
+                out[i] = (1 - smooth) * f / sc->factor + smooth * f;
+            }
+        }
+    } else if (kind == 3) {  // longrope: each frequency divided by its factor (the chosen short or long set)
+        for (size_t i = 0; i < pairs; ++i) out[i] = out[i] / sc->factors[i];
+    } else if (kind == 4) {  // yarn (_yarn, numerics.py:325-349)
+        const double d = static_cast<double>(dim), original = sc->original_max_position_embeddings;
+        double low = d * dlog(original / (sc->beta_fast * 2 * pi)) / (2 * log_theta);
+        double high = d * dlog(original / (sc->beta_slow * 2 * pi)) / (2 * log_theta);
+        if (sc->truncate) {
+            low = std::floor(low);
+            high = std::ceil(high);
+        }
+        if (low < 0) low = 0;
+        if (high > d - 1) high = d - 1;
+        if (low == high) high += 0.001;
+        for (size_t i = 0; i < pairs; ++i) {
+            double ramp = (static_cast<double>(i) - low) / (high - low);
+            ramp = std::min(std::max(ramp, 0.0), 1.0);  // 0: extrapolate, 1: interpolate
+            const double f = out[i];
+            out[i] = f / sc->factor * ramp + f * (1 - ramp);
+        }
+    }
+    return kOk;
+}
 
 int dllm_hip_linear(const float* x, const float* w, const float* bias, float* out, size_t rows, size_t in, size_t out_f,
                     void* workspace, size_t workspace_bytes, void* stream) {

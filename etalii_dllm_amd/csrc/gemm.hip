@@ -68,6 +68,7 @@ struct GemmParams {
     float* partial;  // segment-parallel mode: [nseg][I][J] per-window results (null: windows run in sequence)
     const float* Af;  // float A operands: [L][lda] (A rows) or [I][lda] (A transposed: Af[i][l] = A[l][i])
     const float* seg_weight;  // segmented mode: per-window factors on each window's result (null: none)
+    const float* seg_rowscale;  // segmented mode: per-row factors on each window's result, before seg_weight
 };
 
 // The raw B values of row l for this lane's 4 columns. Lanes past J read a clamped in-bounds column instead (their
@@ -762,6 +763,7 @@ gemm_mfma_kernel(GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmPar
                 const int64_t i = iw + 16 * bi + ri + 4 * r;
                 if (i >= p.I) continue;
                 const int arow = p.seg_addrow ? p.seg_addrow[static_cast<int64_t>(s) * p.I + i] : -1;
+                const float rscale = p.seg_rowscale ? p.seg_rowscale[i] : 1.0f;
                 float* out = out_base + i * ld_out;
 #pragma unroll
                 for (int bj = 0; bj < kBJ; ++bj) {
@@ -769,6 +771,7 @@ gemm_mfma_kernel(GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmPar
                     if (j >= p.J) continue;
                     float v = static_cast<float>(acc[bi][bj][r]);
                     if (p.seg_addrow) v = v + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j] : 0.0f);
+                    if (p.seg_rowscale) v = v * rscale;  // the window's gradient unfolded (RoPE attention factor)
                     if (p.seg_weight) v = v * p.seg_weight[s];  // the window's whole gradient times its factor
                     out[j] = (kMode == kWindowsInParallel || s == 0) ? v : out[j] + v;
                 }
@@ -918,7 +921,8 @@ namespace {
 
 GemmParams params_of(const GemmCall& g) {
     return GemmParams{g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.I, g.J, g.l0, g.l1, g.seg, g.nseg, g.bias, g.addsrc,
-                      g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af, g.seg_weight};
+                      g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af, g.seg_weight,
+                      g.seg_rowscale};
 }
 
 }  // namespace
@@ -989,6 +993,8 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     DLLM_REQUIRE(g.I >= 0 && g.J >= 0, "negative matmul size");
     DLLM_REQUIRE(g.seg == nullptr || g.nseg >= 1, "segmented matmul needs at least one segment");
     DLLM_REQUIRE(g.seg != nullptr || g.seg_addrow == nullptr, "per-window addends need segments");
+    DLLM_REQUIRE(g.seg_rowscale == nullptr || (g.seg != nullptr && g.a_kind == kAFloatRows),
+                 "per-row factors are for windowed weight gradients with float A rows");
     DLLM_REQUIRE(g.seg_weight == nullptr || (g.seg != nullptr && g.a_kind == kAFloatRows),
                  "per-window factors are for windowed weight gradients with float A rows");
     const int ak = g.a_kind;

@@ -37,6 +37,9 @@ struct GemmCall {
     int64_t seg_partial_cap = 0;
     // segmented, float A rows: optional per-window float factors (device, nseg): window s adds f32(result * w[s])
     const float* seg_weight = nullptr;
+    // segmented, float A rows: optional per-row float factors (device, I): row i of each window's result times
+    // rowscale[i], before the window factor (the RoPE attention factor's unfold of a window's gradient)
+    const float* seg_rowscale = nullptr;
 };
 
 int launch_gemm(const GemmCall& g, hipStream_t stream);
@@ -82,10 +85,11 @@ int launch_rms_norm_backward_dx(const float* x, const float* w, const float* dy,
 // Column sums over segments of rows with a float sum over segments (rms_norm dw, linear db):
 //   part[s][i] = f32(sum over rows r of segment s, ascending, of term(r, i))   then out[i] = window-ordered sum.
 // kind 0: term = dy[r][i] (bias); kind 1: term = (dy[r][i] x[r][i]) inv_rms[r] (norm weight). weights (device,
-// nseg floats, may be null): each segment's sum is multiplied by its factor before the window-ordered sum.
+// nseg floats, may be null): each segment's sum is multiplied by its factor before the window-ordered sum; colscale
+// (device, dim floats, may be null): each segment's column i is first multiplied by colscale[i].
 int launch_column_sums(int kind, const float* dy, const float* x, const double* inv_rms, int64_t dim,
                        const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream,
-                       const float* weights = nullptr);
+                       const float* weights = nullptr, const float* colscale = nullptr);
 // rope (nn.hpp:501-530) with precomputed cos/sin tables [positions][half] (double, sin already negated for inverse).
 int launch_rope_tables(const int64_t* positions, int64_t n, const double* inv_freq, int64_t half, double* cos_table,
                        double* sin_table, hipStream_t stream);

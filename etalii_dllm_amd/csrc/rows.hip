@@ -279,14 +279,20 @@ __global__ __launch_bounds__(1024) void column_partial_lds_kernel(int kind, cons
 // out = part[0] + part[1] + ... in float, window order, the first copied; with factors, each window's part is first
 // multiplied by its factor (window s adds f32(part[s] * w[s])).
 __global__ __launch_bounds__(256) void segment_float_sum_kernel(const float* __restrict__ part, int64_t dim, int nseg,
-                                                                const float* __restrict__ w, float* __restrict__ out) {
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ colscale,
+                                                                float* __restrict__ out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= dim) return;
-    float t = w ? part[i] * w[0] : part[i];
-    for (int s = 1; s < nseg; ++s) {
-        const float v = part[static_cast<int64_t>(s) * dim + i];
-        t = t + (w ? v * w[s] : v);
-    }
+    // each window's column sum times its column factor (when given), then its window factor, added in window order
+    const auto term = [&](int s) {
+        float v = part[static_cast<int64_t>(s) * dim + i];
+        if (colscale) v = v * colscale[i];
+        if (w) v = v * w[s];
+        return v;
+    };
+    float t = term(0);
+    for (int s = 1; s < nseg; ++s) t = t + term(s);
     out[i] = t;
 }
 
@@ -500,12 +506,12 @@ int launch_rms_norm_backward_dx(const float* x, const float* w, const float* dy,
 
 int launch_column_sums(int kind, const float* dy, const float* x, const double* inv_rms, int64_t dim,
                        const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream,
-                       const float* weights) {
+                       const float* weights, const float* colscale) {
     if (dim == 0) return kOk;
     DLLM_REQUIRE(nseg >= 1, "column sums need a segment");
-    DLLM_REQUIRE((nseg == 1 && !weights) || partial != nullptr,
+    DLLM_REQUIRE((nseg == 1 && !weights && !colscale) || partial != nullptr,
                  "column sums over several segments (or with factors) need a partial buffer");
-    const bool direct = nseg == 1 && !weights;
+    const bool direct = nseg == 1 && !weights && !colscale;
     const unsigned col_blocks = static_cast<unsigned>(ceil_div(dim, 64));
     // the direct-to-LDS kernel: whole 16-byte pieces of rows
     const bool ring = dim % 4 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0 &&
@@ -526,7 +532,7 @@ int launch_column_sums(int kind, const float* dy, const float* x, const double* 
     const unsigned blocks = static_cast<unsigned>(ceil_div(dim, 256));
     if (!direct)
         hipLaunchKernelGGL(segment_float_sum_kernel, dim3(blocks), dim3(256), 0, stream, partial, dim, nseg, weights,
-                           out);
+                           colscale, out);
     return check_launch("column_sums");
 }
 

@@ -111,6 +111,17 @@ struct TensorInfo {
     int64_t wt_offset = -1;  // transposed copy for the forward matmul, if it is a linear weight
 };
 
+// fold_scales' RoPE attention factor (transformer.py:212-245): dst = src with the entries of every row r whose
+// (r % head_dim) < rotary_dim multiplied by the float factor; rows of `cols` elements (1 for vectors).
+__global__ void rope_fold_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n, int64_t cols,
+                                 int64_t head_dim, int64_t rotary_dim, float factor) {
+    for (int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; e < n;
+         e += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t r = e / cols;
+        dst[e] = (r % head_dim) < rotary_dim ? src[e] * factor : src[e];
+    }
+}
+
 // rope_inv_freq (numerics.py:267-297, default scaling): exp(-(2i / dim) log(theta)) with the portable exp and log.
 __global__ void inv_freq_kernel(int64_t rotary_dim, double theta, double* out) {
     const int64_t i = threadIdx.x + static_cast<int64_t>(blockIdx.x) * blockDim.x;
@@ -231,6 +242,14 @@ struct dllm_hip_trainer {
     }
     DevBuf lora_p, lora_g, lora_m, lora_v, merged;
     std::vector<int64_t> merged_offset;  // per tensor id: offset in `merged`, or -1
+    // The LongRoPE / YaRN attention factor (fold_scales, transformer.py:224-245): the step reads the q/k rows feeding
+    // the rotated dimensions (or the QK-norm entries) times the factor, from `folded`; each window's gradients of
+    // those tensors are multiplied by it again (_unfold, backprop.py:380-394) before the window sum.
+    bool fold_on = false;
+    double rope_factor = 1.0;
+    DevBuf folded;
+    std::vector<int64_t> fold_offset;  // per tensor id: offset in `folded`, or -1
+    float* rope_rowscale = nullptr;    // [q heads x head_dim]: the factor on rotated entries, 1 elsewhere
     bool base_ready = true;              // the Q8_0 base has been applied to the current parameters
     void* lora_ws = nullptr;
     size_t lora_ws_bytes = 0;
@@ -528,9 +547,76 @@ struct dllm_hip_trainer {
         return check_hip(hipDeviceSynchronize(), "trainer setup");
     }
 
-    float* P(int id) const {
+    // The weight as the stored model holds it (LoRA targets: merged)
+    float* Psrc(int id) const {
         const int64_t mo = merged_offset.empty() ? -1 : merged_offset[static_cast<size_t>(id)];
         return mo >= 0 ? merged.as<float>() + mo : params.as<float>() + tensors[static_cast<size_t>(id)].offset;
+    }
+    // The weight as the step uses it (fold_scales applied)
+    float* P(int id) const {
+        const int64_t fo = fold_offset.empty() ? -1 : fold_offset[static_cast<size_t>(id)];
+        return fo >= 0 ? folded.as<float>() + fo : Psrc(id);
+    }
+    // The per-row factors of a tensor's window gradients (the attention factor's unfold), or null
+    const float* unfold_scale(int id) const {
+        return id >= 0 && !fold_offset.empty() && fold_offset[static_cast<size_t>(id)] >= 0 ? rope_rowscale : nullptr;
+    }
+
+    // The folded copies of the rope-scaled tensors from their current values.
+    int fold_weights(hipStream_t s) {
+        for (size_t i = 0; i < tensors.size(); ++i) {
+            if (fold_offset[i] < 0) continue;
+            const TensorInfo& t = tensors[i];
+            const int64_t cols = t.cols > 0 ? t.cols : 1;
+            const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(t.numel, 256), 4096));
+            hipLaunchKernelGGL(rope_fold_kernel, dim3(blocks), dim3(256), 0, s, Psrc(static_cast<int>(i)),
+                               folded.as<float>() + fold_offset[i], t.numel, cols, c.head_dim, c.rotary_dim,
+                               static_cast<float>(rope_factor));
+            DLLM_TRY(check_launch("rope fold"));
+        }
+        return kOk;
+    }
+
+    // rope_inv_freq with its scaling, and the attention factor (dllm_hip_trainer_set_rope).
+    int set_rope(const double* host_inv_freq, int64_t pairs, double factor) {
+        DLLM_REQUIRE(pairs == c.rotary_dim / 2, "set_rope needs rotary_dim / 2 inverse frequencies");
+        DLLM_REQUIRE(factor > 0.0 && factor == factor, "the RoPE attention factor must be positive");
+        DLLM_TRY(check_hip(hipDeviceSynchronize(), "set_rope"));
+        DLLM_TRY(check_hip(hipMemcpy(inv_freq, host_inv_freq, static_cast<size_t>(pairs) * sizeof(double),
+                                     hipMemcpyHostToDevice), "upload"));
+        DLLM_TRY(launch_rope_tables(nullptr, T_max, inv_freq, c.rotary_dim / 2, cos_t, sin_t, nullptr));
+        rope_factor = factor;
+        const bool want = factor != 1.0;
+        if (want && !fold_on) {
+            fold_offset.assign(tensors.size(), -1);
+            int64_t off = 0;
+            for (const LayerIds& L : layer_ids) {
+                const int ids[4] = {c.qk_norm ? L.qn : L.q, c.qk_norm ? L.kn : L.k, c.qk_norm ? -1 : L.qb,
+                                    c.qk_norm ? -1 : L.kb};
+                for (int id : ids) {
+                    if (id < 0) continue;
+                    fold_offset[static_cast<size_t>(id)] = off;
+                    off += static_cast<int64_t>(round_up(static_cast<size_t>(tensors[static_cast<size_t>(id)].numel), 64));
+                }
+            }
+            DLLM_TRY(folded.alloc(static_cast<size_t>(off > 0 ? off : 1) * sizeof(float)));
+            DLLM_TRY(make(&rope_rowscale, static_cast<size_t>(QD)));
+        }
+        if (want) {
+            std::vector<float> rs(static_cast<size_t>(QD));
+            for (int64_t i = 0; i < QD; ++i) rs[static_cast<size_t>(i)] = (i % c.head_dim) < c.rotary_dim ? static_cast<float>(factor) : 1.0f;
+            DLLM_TRY(check_hip(hipMemcpy(rope_rowscale, rs.data(), rs.size() * sizeof(float), hipMemcpyHostToDevice),
+                               "upload"));
+        } else if (fold_on) {
+            fold_offset.assign(tensors.size(), -1);
+        }
+        fold_on = want;
+        // the step's weight addresses changed: rebuild the transposes' job table and the qkv groups
+        wt_jobs = nullptr;
+        qkv_rows = -1;
+        wt_valid = false;
+        merged_valid = false;
+        return check_hip(hipDeviceSynchronize(), "set_rope");
     }
     float* G(int id) const { return grads.as<float>() + tensors[static_cast<size_t>(id)].offset; }
     float* WT(int id) const { return wt.as<float>() + tensors[static_cast<size_t>(id)].wt_offset; }
@@ -728,9 +814,12 @@ struct dllm_hip_trainer {
     // grad[w] = window-ordered float sum of per-window dW = sum over window rows of dy[r][n] x[r][k]. The windows are
     // the step's (seg_d), or those of an expert's group (seg, over `rows` grouped rows).
     int linear_dw(const float* dyv, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
-                  const float* addend, hipStream_t s, const int64_t* seg = nullptr, int64_t rows = -1) {
+                  const float* addend, hipStream_t s, const int64_t* seg = nullptr, int64_t rows = -1,
+                  const float* rowscale = nullptr) {
         if (!grad_wanted(out)) return kOk;
-        return gemm(dw_call(dyv, N, x, K, nseg, out, addrow_, addend, seg, rows), s);
+        GemmCall g = dw_call(dyv, N, x, K, nseg, out, addrow_, addend, seg, rows);
+        g.seg_rowscale = rowscale;
+        return gemm(g, s);
     }
 
     GemmCall dw_call(const float* dyv, int64_t N, const float* x, int64_t K, int nseg, float* out, const int* addrow_,
@@ -759,11 +848,11 @@ struct dllm_hip_trainer {
     }
 
     int norm_dw(const float* dyv, const float* x, const double* inv, int64_t dim, int64_t rows_per_token, int nseg,
-                float* out, hipStream_t s) {
+                float* out, hipStream_t s, const float* colscale = nullptr) {
         if (!grad_wanted(out)) return kOk;
         std::vector<int64_t> seg(seg_host.size());
         for (size_t i = 0; i < seg.size(); ++i) seg[i] = seg_host[i] * rows_per_token;
-        return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s, window_weights());
+        return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s, window_weights(), colscale);
     }
 
     // ---- attention (attn_lds.hip, attn_chains.hip) ----
@@ -953,17 +1042,17 @@ struct dllm_hip_trainer {
         if (c.qk_norm == 1) {
             DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R * c.heads, c.head_dim, eps, 0,
                                                  inv_rms, s));
-            DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, c.head_dim, c.heads, nseg, G(L.qn), s));
+            DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, c.head_dim, c.heads, nseg, G(L.qn), s, unfold_scale(L.qn)));
             DLLM_TRY(launch_rms_norm_backward_dx(sv.k_raw, P(L.kn), dk, dk2, nullptr, R * c.kv_heads, c.head_dim, eps,
                                                  0, inv_rms, s));
-            DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, c.head_dim, c.kv_heads, nseg, G(L.kn), s));
+            DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, c.head_dim, c.kv_heads, nseg, G(L.kn), s, unfold_scale(L.kn)));
             dqf = dq2;
             dkf = dk2;
         } else if (c.qk_norm == 2) {
             DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R, QD, eps, 0, inv_rms, s));
-            DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, QD, 1, nseg, G(L.qn), s));
+            DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, QD, 1, nseg, G(L.qn), s, unfold_scale(L.qn)));
             DLLM_TRY(launch_rms_norm_backward_dx(sv.k_raw, P(L.kn), dk, dk2, nullptr, R, KVD, eps, 0, inv_rms, s));
-            DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, KVD, 1, nseg, G(L.kn), s));
+            DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, KVD, 1, nseg, G(L.kn), s, unfold_scale(L.kn)));
             dqf = dq2;
             dkf = dk2;
         }
@@ -974,10 +1063,11 @@ struct dllm_hip_trainer {
         const int64_t ns[3] = {QD, KVD, KVD};
         for (int p = 0; p < 3; ++p) {
             DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
-            DLLM_TRY(linear_dw(ds[p], ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s));
+            DLLM_TRY(linear_dw(ds[p], ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s, nullptr, -1,
+                               unfold_scale(ws_[p])));
             if (bs_[p] >= 0 && grad_wanted(G(bs_[p])))
                 DLLM_TRY(launch_column_sums(0, ds[p], nullptr, nullptr, ns[p], seg_host.data(), nseg, col_part,
-                                            G(bs_[p]), s, window_weights()));
+                                            G(bs_[p]), s, window_weights(), unfold_scale(bs_[p])));
         }
         // attention norm; dx = dx_mid + dh1'
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh, dx, dx_mid, R, H, eps, 0, inv_rms, s));
@@ -1217,10 +1307,12 @@ struct dllm_hip_trainer {
         int64_t R = 0, groups = 0;
         AttentionBatch b{};
         DLLM_TRY(prepare(tokens, offsets, lengths, windows, &R, &b, &groups, s));
-        if (lora_on)
+        if (lora_on) {
             DLLM_TRY(prepare_lora(s));
-        else if (!wt_valid)
+        } else if (!wt_valid) {
+            if (fold_on) DLLM_TRY(fold_weights(s));
             DLLM_TRY(refresh_transposes(s));
+        }
         DLLM_TRY(prepare_qkv_groups(R, s));
         const int nseg = static_cast<int>(windows);
         nwin = windows;
@@ -1552,6 +1644,7 @@ struct dllm_hip_trainer {
                                        t.cols, lc.rank, lora_scale, lora_ws, lora_ws_bytes, s));
         }
         merged_valid = true;
+        if (fold_on) DLLM_TRY(fold_weights(s));
         return refresh_transposes(s);
     }
 
@@ -1709,6 +1802,11 @@ int dllm_hip_trainer_tensor(dllm_hip_trainer* t, const char* name, int which, fl
         if (t->lora_on && t->lc.base_quantize) t->base_ready = false;
     }
     return kOk;
+}
+
+int dllm_hip_trainer_set_rope(dllm_hip_trainer* t, const double* inv_freq, int64_t pairs, double attention_factor) {
+    DLLM_REQUIRE(t && inv_freq, "null argument");
+    return t->set_rope(inv_freq, pairs, attention_factor);
 }
 
 int dllm_hip_trainer_tensor_count(dllm_hip_trainer* t, int64_t* count) {

@@ -725,6 +725,60 @@ def lora_adapter_gradients(gradient, a, b, scale: float) -> tuple[np.ndarray, np
     return ga.download(a.shape), gb.download(b.shape)
 
 
+class RopeScaling(C.Structure):
+    """dllm_hip_rope_scaling."""
+
+    _fields_ = [("kind", C.c_int64)] + [(name, C.c_double) for name in (
+        "factor", "low_freq_factor", "high_freq_factor", "original_max_position_embeddings", "beta_fast",
+        "beta_slow")] + [("truncate", C.c_int64), ("factors", C.c_void_p)]
+
+
+ROPE_KINDS = {"default": 0, "linear": 1, "llama3": 2, "longrope": 3, "yarn": 4}
+lib.dllm_hip_rope_inv_freq.argtypes = [_sz, C.c_double, _sz, C.POINTER(RopeScaling), _f64p]
+
+
+def rope_inv_freq(head_dim: int, theta: float = 10000.0, *, rotary_dim: int | None = None, scaling=None) -> np.ndarray:
+    """numerics.py:267-324: rotary inverse frequencies theta^(-2i / rotary_dim) in double from the portable exp and
+    log, with a Hugging Face rope_scaling dict ("default", "linear", "llama3", "longrope" with its short or long
+    factors, "yarn"); ValueError for an odd or too large rotary_dim, an unknown kind or a wrong number of factors."""
+    dim = head_dim if rotary_dim is None else rotary_dim
+    if dim <= 0 or dim % 2 or dim > head_dim:
+        raise ValueError("rotary_dim must be even, positive and at most head_dim")
+    kind = "default" if not scaling else str(scaling.get("rope_type", scaling.get("type", "default")))
+    if kind not in ROPE_KINDS:
+        raise ValueError(f"unsupported rope scaling {kind!r}")
+    sc = RopeScaling()
+    sc.kind = ROPE_KINDS[kind]
+    factors = None
+    if kind in ("linear", "llama3", "yarn"):
+        sc.factor = float(scaling["factor"])
+    if kind == "llama3":
+        sc.low_freq_factor = float(scaling.get("low_freq_factor", 1.0))
+        sc.high_freq_factor = float(scaling.get("high_freq_factor", 4.0))
+        sc.original_max_position_embeddings = float(scaling.get("original_max_position_embeddings", 8192))
+    elif kind == "longrope":
+        name = "long_factor" if scaling.get("factor_set") == "long" else "short_factor"
+        factors = np.ascontiguousarray([float(f) for f in scaling[name]], dtype=np.float64)
+        if factors.size != dim // 2:
+            raise ValueError(f"longrope {name} needs {dim // 2} values, got {factors.size}")
+        sc.factors = factors.ctypes.data
+    elif kind == "yarn":
+        sc.original_max_position_embeddings = float(scaling["original_max_position_embeddings"])
+        sc.beta_fast = float(scaling.get("beta_fast", 32.0))
+        sc.beta_slow = float(scaling.get("beta_slow", 1.0))
+        sc.truncate = int(bool(scaling.get("truncate", True)))
+    out = np.empty(dim // 2, np.float64)
+    check(lib.dllm_hip_rope_inv_freq(head_dim, float(theta), dim, C.byref(sc), out.ctypes.data_as(_f64p)))
+    return out
+
+
+def rope_attention_factor(scaling) -> float:
+    """architecture.py:331-336: the attention_factor of LongRoPE or YaRN (1 otherwise)."""
+    if not scaling or scaling.get("rope_type", scaling.get("type")) not in ("longrope", "yarn"):
+        return 1.0
+    return float(scaling.get("attention_factor", 1.0))
+
+
 def attention_scale(head_dim: int) -> float:
     """architecture.py:311-312: 1 / sqrt(head_dim)."""
     return 1.0 / math.sqrt(head_dim)

@@ -67,6 +67,7 @@ lib.dllm_hip_trainer_tensor_count.argtypes = [C.c_void_p, C.POINTER(C.c_int64)]
 lib.dllm_hip_trainer_gradients.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_int64, C.c_double, C.c_double,
                                            C.POINTER(C.c_double), C.c_void_p]
 lib.dllm_hip_trainer_router_loss.argtypes = [C.c_void_p, C.POINTER(C.c_double)]
+lib.dllm_hip_trainer_set_rope.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.c_int64, C.c_double]
 lib.dllm_hip_trainer_step.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, C.c_int64, C.POINTER(AdamWArgs),
                                       C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_void_p]
 lib.dllm_hip_trainer_dpo_step.argtypes = [C.c_void_p, _i64p, _i64p, _i64p, _i64p, C.c_int64, C.POINTER(C.c_double),
@@ -97,13 +98,16 @@ class Decoder:
     experts_per_token: int = 0
     normalize_expert_weights: bool = False
     expert_intermediate: int = 0  # 0: the intermediate size
+    rotary_dim: int = 0  # 0: head_dim (partial rotary: only the first rotary_dim dimensions of each head rotate)
+    rope_scaling: dict | None = None  # a Hugging Face rope_scaling (linear, llama3, longrope, yarn), as the config's
 
     def native(self) -> DecoderConfig:
         return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
                              self.head_dim, int(self.attention_bias), self.qk_norm, self.sliding_window,
                              int(self.tie_embeddings), self.experts, self.experts_per_token,
-                             int(self.normalize_expert_weights), self.expert_intermediate, self.head_dim,
-                             self.rms_norm_eps, self.rope_theta, 1.0 / float(np.sqrt(np.float64(self.head_dim))))
+                             int(self.normalize_expert_weights), self.expert_intermediate,
+                             self.rotary_dim or self.head_dim, self.rms_norm_eps, self.rope_theta,
+                             1.0 / float(np.sqrt(np.float64(self.head_dim))))
 
 
 def _windows(windows):
@@ -130,6 +134,13 @@ class Trainer:
                                                max_tokens, max_windows, max_window_tokens, C.byref(handle)))
         self.handle = handle
         count = C.c_int64()
+        if decoder.rope_scaling:
+            from etalii_dllm_amd.kernels import rope_attention_factor, rope_inv_freq
+
+            inv = rope_inv_freq(decoder.head_dim, decoder.rope_theta, rotary_dim=decoder.rotary_dim or None,
+                                scaling=decoder.rope_scaling)
+            check(lib.dllm_hip_trainer_set_rope(handle, inv.ctypes.data_as(C.POINTER(C.c_double)), inv.size,
+                                                rope_attention_factor(decoder.rope_scaling)))
         check(lib.dllm_hip_trainer_tensor_count(handle, C.byref(count)))
         self.names = [lib.dllm_hip_trainer_tensor_name(handle, i).decode() for i in range(count.value)]
 

@@ -60,6 +60,20 @@ int dllm_hip_rope(const float* x, const int64_t* positions, const double* inv_fr
                   size_t heads, size_t head_dim, size_t rotary_dim, int interleaved, int inverse, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* rope_inv_freq (numerics.py:267-349, a host function): rotary_dim / 2 inverse frequencies theta^(-2i / rotary_dim)
+ * from the portable exp and log (rotary_dim 0: head_dim), with a Hugging Face rope_scaling: kind 0 default, 1 linear
+ * (factor), 2 llama3 (factor, low/high_freq_factor, original_max_position_embeddings), 3 longrope (factors: the
+ * chosen short or long set, one per pair), 4 yarn (factor, original_max_position_embeddings, beta_fast, beta_slow,
+ * truncate). Same bits as the reference's Python double arithmetic. */
+typedef struct {
+    int64_t kind;
+    double factor, low_freq_factor, high_freq_factor, original_max_position_embeddings, beta_fast, beta_slow;
+    int64_t truncate;
+    const double* factors;
+} dllm_hip_rope_scaling;
+int dllm_hip_rope_inv_freq(size_t head_dim, double theta, size_t rotary_dim, const dllm_hip_rope_scaling* scaling,
+                           double* out);
+
 /* Causal / windowed grouped-query attention, q[q_len, q_heads, head_dim], k[kv_len, kv_heads, head_dim],
  * v[kv_len, kv_heads, value_dim] -> out[q_len, q_heads, value_dim]; q_offset < 0 means kv_len - q_len.
  * Replaces kernels.cpp:680-705 `attention` (nn.hpp:761-796). Any key length. Self-attention shapes (q_len == kv_len,
@@ -296,6 +310,15 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
  * Parameters written through this pointer take effect at the next step. */
 int dllm_hip_trainer_tensor(dllm_hip_trainer* trainer, const char* name, int which, float** device_ptr,
                             int64_t* numel);
+/* The rotary inverse frequencies (rotary_dim / 2 values, host array: dllm_hip_rope_inv_freq with the model's scaling)
+ * and the LongRoPE / YaRN attention factor (architecture.py:331-336; 1 for none) of the next steps. The factor is
+ * folded into the rows of the q and k projections (and biases) feeding the rotated dimensions, or into the QK-norm
+ * weights' rotated entries when the model has QK-norm (fold_scales, transformer.py:204-245), and each window's
+ * gradients of those tensors are multiplied by it again (_unfold, backprop.py:380-394). Without this call a trainer
+ * uses theta's default frequencies and no factor. No counterpart in the kernel module: DecoderGradients reads both
+ * from the TransformerConfig. */
+int dllm_hip_trainer_set_rope(dllm_hip_trainer* trainer, const double* inv_freq, int64_t pairs,
+                              double attention_factor);
 /* Tensor names in natural order (modelfile.py:40-47); index in [0, count). */
 int dllm_hip_trainer_tensor_count(dllm_hip_trainer* trainer, int64_t* count);
 const char* dllm_hip_trainer_tensor_name(dllm_hip_trainer* trainer, int64_t index);

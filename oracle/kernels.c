@@ -1053,6 +1053,63 @@ void orc_rope_inv_freq(size_t rotary_dim, double theta, double* out) {
     }
 }
 
+/* rope_inv_freq with rope_scaling (numerics.py:267-349 and _yarn 325-349), every step in the Python code's double
+ * operation order: Python ints divide as correctly rounded doubles, min/max/floor/ceil as written. */
+int orc_rope_inv_freq_scaled(size_t rotary_dim, double theta, const orc_rope_scaling* sc, double* out) {
+    const size_t pairs = rotary_dim / 2;
+    const double log_theta = orc_log(theta);
+    for (size_t i = 0; i < pairs; ++i) out[i] = orc_exp(-((double)(2 * (int64_t)i) / (double)rotary_dim) * log_theta);
+    const int64_t kind = sc ? sc->kind : 0;
+    const double pi = 3.141592653589793; /* math.pi */
+    if (kind == 0) return 0;
+    if (kind == 1) {
+        for (size_t i = 0; i < pairs; ++i) out[i] = out[i] / sc->factor;
+        return 0;
+    }
+    if (kind == 2) {
+        const double low = sc->low_freq_factor, high = sc->high_freq_factor, original = sc->original;
+        const double low_freq_wavelen = original / low, high_freq_wavelen = original / high;
+        for (size_t i = 0; i < pairs; ++i) {
+            const double f = out[i];
+            const double wavelen = 2 * pi / f;
+            if (wavelen < high_freq_wavelen) {
+                out[i] = f;
+            } else if (wavelen > low_freq_wavelen) {
+                out[i] = f / sc->factor;
+            } else {
+                const double smooth = (original / wavelen - low) / (high - low);
+                out[i] = (1 - smooth) * f / sc->factor + smooth * f;
+            }
+        }
+        return 0;
+    }
+    if (kind == 3) {
+        for (size_t i = 0; i < pairs; ++i) out[i] = out[i] / sc->factors[i];
+        return 0;
+    }
+    if (kind == 4) {
+        const double dim = (double)rotary_dim, original = sc->original;
+        double low = dim * orc_log(original / (sc->beta_fast * 2 * pi)) / (2 * log_theta);
+        double high = dim * orc_log(original / (sc->beta_slow * 2 * pi)) / (2 * log_theta);
+        if (sc->truncate) {
+            low = floor(low);
+            high = ceil(high);
+        }
+        if (low < 0) low = 0; /* max(low, 0) */
+        if (high > dim - 1) high = dim - 1; /* min(high, dim - 1) */
+        if (low == high) high += 0.001;
+        for (size_t i = 0; i < pairs; ++i) {
+            double ramp = ((double)(int64_t)i - low) / (high - low);
+            if (ramp < 0.0) ramp = 0.0;
+            if (ramp > 1.0) ramp = 1.0;
+            const double f = out[i];
+            out[i] = f / sc->factor * ramp + f * (1 - ramp);
+        }
+        return 0;
+    }
+    return 1;
+}
+
 /* ---- the oracle's kernel table ---- */
 static void silu_n(const float* x, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = orc_silu(x[i]);

@@ -106,6 +106,16 @@ void orc_linear_q4(const float* x, const uint8_t* wq, const float* ws, const flo
 
 /* ---- rotary frequencies: src/etalii_dllm/numerics.py:267-297 (default scaling) ---- */
 void orc_rope_inv_freq(size_t rotary_dim, double theta, double* out);
+/* rope_inv_freq with a Hugging Face rope_scaling (numerics.py:267-349): kind 0 default, 1 linear (factor), 2 llama3
+ * (factor, low_freq_factor, high_freq_factor, original_max_position_embeddings), 3 longrope (factors[i], the chosen
+ * short or long set), 4 yarn (factor, original, beta_fast, beta_slow, truncate). Returns 0, or 1 for an unknown kind. */
+typedef struct {
+    int64_t kind;
+    double factor, low_freq_factor, high_freq_factor, original, beta_fast, beta_slow;
+    int64_t truncate;
+    const double* factors;
+} orc_rope_scaling;
+int orc_rope_inv_freq_scaled(size_t rotary_dim, double theta, const orc_rope_scaling* scaling, double* out);
 
 /* ---- the kernel table a step driver calls (the oracle's own, or the reference's through oracle/_ref) ---- */
 typedef struct {
@@ -146,6 +156,8 @@ typedef struct {
     int64_t experts, topk, normalize, expert_inter; /* mixture of experts; experts == 0 for dense */
     int64_t rotary_dim;
     double eps, rope_theta, attention_scale;
+    const double* inv_freq;        /* rotary_dim / 2 scaled inverse frequencies, or NULL for theta's defaults */
+    double rope_attention_factor;  /* LongRoPE / YaRN attention factor folded into the q/k rows (1 or 0: none) */
 } orc_config;
 
 /*

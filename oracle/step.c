@@ -280,17 +280,84 @@ static void init_state(fwd_state* st, const orc_ops* ops, const orc_config* c, f
     st->positions = (int64_t*)malloc((size_t)n * sizeof(int64_t));
     for (int64_t t = 0; t < n; ++t) st->positions[t] = t;
     st->inv_freq = (double*)malloc((size_t)(c->rotary_dim / 2 + 1) * sizeof(double));
-    orc_rope_inv_freq((size_t)c->rotary_dim, c->rope_theta, st->inv_freq);
+    if (c->inv_freq)
+        memcpy(st->inv_freq, c->inv_freq, (size_t)(c->rotary_dim / 2) * sizeof(double));
+    else
+        orc_rope_inv_freq((size_t)c->rotary_dim, c->rope_theta, st->inv_freq);
     st->layers = (layer_saved*)calloc((size_t)c->layers, sizeof(layer_saved));
 }
 
-int orc_logits(const orc_ops* ops, const orc_config* c, float* const* w, const int64_t* tokens, int64_t n,
+/* rope_scaled_tensors (transformer.py:204-209): the QK-norm weights when the model has QK-norm, else the q and k
+ * projections and their biases. */
+static int rope_scaled_slots(const orc_config* c, int64_t layer, int64_t* out) {
+    int k = 0;
+    if (c->qk_norm) {
+        out[k++] = orc_slot(c, layer, ORC_QNORM);
+        out[k++] = orc_slot(c, layer, ORC_KNORM);
+    } else {
+        out[k++] = orc_slot(c, layer, ORC_Q);
+        out[k++] = orc_slot(c, layer, ORC_K);
+        if (c->attn_bias) {
+            out[k++] = orc_slot(c, layer, ORC_QB);
+            out[k++] = orc_slot(c, layer, ORC_KB);
+        }
+    }
+    return k;
+}
+
+/* _rope_scaled (transformer.py:212-221) and _unfold (backprop.py:388-393): the entries of each head's first
+ * rotary_dim rows times f32(factor), elementwise in float. */
+static void scale_rotary_rows(const orc_config* c, int64_t slot, const float* src, float* dst, float factor) {
+    int64_t d0 = 0, d1 = 0;
+    const int nd = (int)slot_shape(c, slot, &d0, &d1);
+    const int64_t cols = nd == 2 ? d1 : 1;
+    for (int64_t r = 0; r < d0; ++r) {
+        const int rotated = (r % c->head_dim) < c->rotary_dim;
+        for (int64_t j = 0; j < cols; ++j) dst[r * cols + j] = rotated ? src[r * cols + j] * factor : src[r * cols + j];
+    }
+}
+
+/* fold_scales's RoPE attention factor (transformer.py:224-245) over a weight table: a table whose rope-scaled slots
+ * point to folded copies (owned[] holds them, to free), or NULL when the factor is 1 (or unset). */
+static float** fold_weights(const orc_config* c, float* const* w, float*** owned_out) {
+    const double a = c->rope_attention_factor;
+    *owned_out = NULL;
+    if (a == 0.0 || a == 1.0) return NULL;
+    const int64_t slots = orc_slot_count(c);
+    float** folded = (float**)calloc((size_t)slots, sizeof(float*));
+    float** owned = (float**)calloc((size_t)slots, sizeof(float*));
+    for (int64_t s = 0; s < slots; ++s) folded[s] = w[s];
+    for (int64_t l = 0; l < c->layers; ++l) {
+        int64_t list[4];
+        const int k = rope_scaled_slots(c, l, list);
+        for (int i = 0; i < k; ++i) {
+            owned[list[i]] = falloc(orc_tensor_numel(c, list[i]));
+            scale_rotary_rows(c, list[i], w[list[i]], owned[list[i]], (float)a);
+            folded[list[i]] = owned[list[i]];
+        }
+    }
+    *owned_out = owned;
+    return folded;
+}
+
+static void free_folded(const orc_config* c, float** folded, float** owned) {
+    if (!folded) return;
+    for (int64_t s = 0; s < orc_slot_count(c); ++s) free(owned[s]);
+    free(owned);
+    free(folded);
+}
+
+int orc_logits(const orc_ops* ops, const orc_config* c, float* const* w_stored, const int64_t* tokens, int64_t n,
                float* logits) {
+    float** owned;
+    float** folded = fold_weights(c, w_stored, &owned);
+    float* const* w = folded ? folded : w_stored;
     fwd_state st;
     init_state(&st, ops, c, w, n);
     forward(&st, tokens);
     ops->linear(st.hidden, w[c->tied ? ORC_EMBEDDING : ORC_LM_HEAD], NULL, logits, n, c->hidden, c->vocab);
     free_state(&st);
+    free_folded(c, folded, owned);
     return 0;
 }
 
@@ -371,9 +438,9 @@ static void experts_backward(const fwd_state* st, int64_t l, const float* dmlp, 
     free(dweights); free(dprob); free(dlogits); free(dh2_router);
 }
 
-int orc_window_gradients(const orc_ops* ops, const orc_config* c, float* const* w, const int64_t* tokens,
-                         const int64_t* targets, int64_t n, double scale, double router_scale, float* const* g,
-                         double* loss, double* router_loss_out) {
+static int window_gradients(const orc_ops* ops, const orc_config* c, float* const* w, const int64_t* tokens,
+                            const int64_t* targets, int64_t n, double scale, double router_scale, float* const* g,
+                            double* loss, double* router_loss_out) {
     if (n <= 0) return -1;
     for (int64_t t = 0; t < n; ++t)
         if (tokens[t] < 0 || tokens[t] >= c->vocab) return -2;
@@ -484,6 +551,24 @@ int orc_window_gradients(const orc_ops* ops, const orc_config* c, float* const* 
     free(grad_row);
     free_state(&st);
     return 0;
+}
+
+/* DecoderGradients.losses_and_gradients of one window (backprop.py:88-118): with a RoPE attention factor the
+ * weights are folded first (_folded, backprop.py:529-537) and the gradients unfolded after (_unfold). */
+int orc_window_gradients(const orc_ops* ops, const orc_config* c, float* const* w, const int64_t* tokens,
+                         const int64_t* targets, int64_t n, double scale, double router_scale, float* const* g,
+                         double* loss, double* router_loss_out) {
+    float** owned;
+    float** folded = fold_weights(c, w, &owned);
+    const int rc = window_gradients(ops, c, folded ? folded : w, tokens, targets, n, scale, router_scale, g, loss,
+                                    router_loss_out);
+    for (int64_t l = 0; folded && rc == 0 && l < c->layers; ++l) {
+        int64_t list[4];
+        const int k = rope_scaled_slots(c, l, list);
+        for (int i = 0; i < k; ++i) scale_rotary_rows(c, list[i], g[list[i]], g[list[i]], (float)c->rope_attention_factor);
+    }
+    free_folded(c, folded, owned);
+    return rc;
 }
 
 /* _power (optimizer.py:59-63): base^exponent by repeated multiplication. */

@@ -13,7 +13,8 @@ import sys
 from pathlib import Path
 
 KEEP = ("RANDOM_FIRST", "RANDOM_SECOND", "KERNEL_FINGERPRINTS", "GRADIENT_FINGERPRINT", "FINETUNE_FINGERPRINT",
-        "LORA_FINETUNE_FINGERPRINT", "DPO_FINETUNE_FINGERPRINT")
+        "LORA_FINETUNE_FINGERPRINT", "DPO_FINETUNE_FINGERPRINT", "LONG_CONTEXT_FINGERPRINTS",
+        "TINY_LOGITS_FINGERPRINT")
 
 
 def main(reference: Path, out: Path) -> None:

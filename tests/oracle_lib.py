@@ -31,7 +31,17 @@ class OrcConfig(C.Structure):
     _fields_ = [(name, C.c_int64) for name in (
         "vocab", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "attn_bias", "qk_norm", "window",
         "tied", "experts", "topk", "normalize", "expert_inter", "rotary_dim")] + [
-        ("eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double)]
+        ("eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
+        ("inv_freq", C.c_void_p), ("rope_attention_factor", C.c_double)]
+
+
+class OrcRopeScaling(C.Structure):
+    _fields_ = [("kind", C.c_int64)] + [(name, C.c_double) for name in (
+        "factor", "low_freq_factor", "high_freq_factor", "original", "beta_fast", "beta_slow")] + [
+        ("truncate", C.c_int64), ("factors", C.c_void_p)]
+
+
+ROPE_KINDS = {"default": 0, "linear": 1, "llama3": 2, "longrope": 3, "yarn": 4}
 
 
 class OrcAdamW(C.Structure):
@@ -288,6 +298,32 @@ def rope_inv_freq(rotary_dim: int, theta: float) -> np.ndarray:
     return out
 
 
+def rope_inv_freq_scaled(rotary_dim: int, theta: float, scaling: dict | None = None) -> np.ndarray:
+    """The oracle's rope_inv_freq with a Hugging Face rope_scaling dict (numerics.py:267-349)."""
+    sc = OrcRopeScaling()
+    kind = "default" if not scaling else str(scaling.get("rope_type", scaling.get("type", "default")))
+    sc.kind = ROPE_KINDS[kind]
+    keep = None
+    if scaling:
+        sc.factor = float(scaling.get("factor", 1.0))
+        sc.low_freq_factor = float(scaling.get("low_freq_factor", 1.0))
+        sc.high_freq_factor = float(scaling.get("high_freq_factor", 4.0))
+        default_original = 8192 if kind == "llama3" else 0
+        sc.original = float(scaling.get("original_max_position_embeddings", default_original))
+        sc.beta_fast = float(scaling.get("beta_fast", 32.0))
+        sc.beta_slow = float(scaling.get("beta_slow", 1.0))
+        sc.truncate = int(bool(scaling.get("truncate", True)))
+        if kind == "longrope":
+            name = "long_factor" if scaling.get("factor_set") == "long" else "short_factor"
+            keep = np.ascontiguousarray(scaling[name], dtype=np.float64)
+            assert keep.size == rotary_dim // 2
+            sc.factors = keep.ctypes.data
+    out = np.empty(rotary_dim // 2, np.float64)
+    rc = oracle().orc_rope_inv_freq_scaled(C.c_size_t(rotary_dim), C.c_double(theta), C.byref(sc), ptr(out, _f64p))
+    assert rc == 0
+    return out
+
+
 def tensor_fingerprint(values: np.ndarray) -> str:
     """Tensor.fingerprint (src/etalii_dllm/tensor.py:93-98): SHA-256 of the shape as int64 LE, '|', then the bits."""
     digest = hashlib.sha256(np.asarray(values.shape, dtype="<i8").tobytes())
@@ -323,16 +359,25 @@ class Decoder:
     topk: int = 0
     normalize: bool = False
     expert_inter: int = 0
+    rotary_dim: int = 0  # 0: head_dim (partial rotary: the first rotary_dim dimensions of each head rotate)
+    inv_freq: tuple[float, ...] | None = None  # scaled inverse frequencies (rope_scaling), rotary_dim / 2 of them
+    rope_attention_factor: float = 1.0  # LongRoPE / YaRN attention factor folded into the q/k rows
 
     @property
     def attention_scale(self) -> float:
         return 1.0 / math.sqrt(self.head_dim)
 
     def c(self) -> OrcConfig:
-        return OrcConfig(self.vocab, self.hidden, self.inter, self.layers, self.heads, self.kv_heads, self.head_dim,
-                         int(self.attn_bias), self.qk_norm, self.window, int(self.tied), self.experts, self.topk,
-                         int(self.normalize), self.expert_inter or self.inter, self.head_dim, self.eps,
-                         self.rope_theta, self.attention_scale)
+        cfg = OrcConfig(self.vocab, self.hidden, self.inter, self.layers, self.heads, self.kv_heads, self.head_dim,
+                        int(self.attn_bias), self.qk_norm, self.window, int(self.tied), self.experts, self.topk,
+                        int(self.normalize), self.expert_inter or self.inter, self.rotary_dim or self.head_dim,
+                        self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor)
+        if self.inv_freq is not None:
+            table = np.ascontiguousarray(self.inv_freq, dtype=np.float64)
+            assert table.size == (self.rotary_dim or self.head_dim) // 2
+            cfg.inv_freq = table.ctypes.data
+            cfg._keep = table  # the table must outlive the call that reads it
+        return cfg
 
     def tensor_shapes(self) -> dict[str, tuple[int, ...]]:
         """architecture.py:418-468 (pre-norm decoders)."""

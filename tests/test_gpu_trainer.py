@@ -399,3 +399,95 @@ def test_dpo_step_matches_the_oracle_on_ragged_pairs():
             assert t.get(name, shape).tobytes() == params[name].tobytes(), name
             assert t.get(name, shape, t.M).tobytes() == m[name].tobytes(), name
             assert t.get(name, shape, t.V).tobytes() == v[name].tobytes(), name
+
+
+ROPE_CASES = {
+    # Phi-3-style: partial rotary (8 of 16 dimensions) with LongRoPE short factors and its attention factor, q/k biases
+    "longrope-partial": (O.Decoder("qwen2", vocab=300, hidden=64, inter=96, layers=2, heads=4, kv_heads=2,
+                                   head_dim=16, eps=1e-6, rope_theta=1e4, tied=False, attn_bias=True, rotary_dim=8),
+                         {"rope_type": "longrope", "short_factor": [1.0, 1.5, 3.25, 7.0],
+                          "long_factor": [2.0, 3.0, 4.0, 5.0], "attention_factor": 1.1902380714238083}, None),
+    # Qwen3 with YaRN: the factor folds into the per-head QK-norm weights
+    "yarn-qk-norm": (O.Decoder("qwen3", vocab=256, hidden=64, inter=128, layers=2, heads=4, kv_heads=2, head_dim=16,
+                               eps=1e-6, rope_theta=1e6, tied=True, qk_norm=1),
+                     {"rope_type": "yarn", "factor": 4.0, "original_max_position_embeddings": 64, "beta_fast": 32.0,
+                      "beta_slow": 1.0, "truncate": True, "attention_factor": 1.1386294361119891}, None),
+    # llama3 frequencies (no attention factor) with partial rotary, whole-projection QK-norm and routed experts
+    "llama3-olmoe": (O.Decoder("olmoe", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=4, head_dim=16,
+                               eps=1e-5, rope_theta=5e5, tied=False, qk_norm=2, experts=8, topk=2, normalize=False,
+                               expert_inter=32, rotary_dim=12),
+                     {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                      "original_max_position_embeddings": 64}, None),
+    # LoRA on q and k of a YaRN model: the factor folds into the merged weights
+    "yarn-lora": (O.Decoder("llama", vocab=300, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16,
+                            eps=1e-5, rope_theta=1e5, tied=True),
+                  {"rope_type": "yarn", "factor": 2.0, "original_max_position_embeddings": 32, "beta_fast": 32.0,
+                   "beta_slow": 1.0, "truncate": True, "attention_factor": 1.0693147180559945},
+                  O.Lora(rank=4, alpha=8.0, targets=("q", "k", "o"))),
+}
+
+
+@pytest.mark.parametrize("case", sorted(ROPE_CASES))
+def test_step_with_rope_scaling_matches_the_oracle(case):
+    """RoPE scaling in the trainer (numerics.py:267-349): the scaled inverse frequencies (LongRoPE short factors,
+    YaRN, llama3), partial rotary, and the LongRoPE / YaRN attention factor folded into the q/k rows or the QK-norm
+    weights (transformer.py:204-245) with the per-window gradient unfold (backprop.py:380-394); two steps over ragged
+    windows against the oracle, every gradient, parameter and moment (adapters and their moments for LoRA)."""
+    from dataclasses import replace
+
+    from etalii_dllm_amd import kernels as K
+    from etalii_dllm_amd.trainer import Decoder, Trainer, lora_config
+
+    d, scaling, lora = ROPE_CASES[case]
+    inv = K.rope_inv_freq(d.head_dim, d.rope_theta, rotary_dim=d.rotary_dim or None, scaling=scaling)
+    assert inv.tobytes() == O.rope_inv_freq_scaled(d.rotary_dim or d.head_dim, d.rope_theta, scaling).tobytes()
+    od = replace(d, inv_freq=tuple(inv), rope_attention_factor=K.rope_attention_factor(scaling))
+    weights = O.synthetic_weights(d, seed=31, scale=0.05)
+    rng = O.Random(33)
+    windows = [[rng.next_u64() % d.vocab for _ in range(n)] for n in (33, 2, 70, 17)]
+    gd = Decoder(d.vocab, d.hidden, d.inter, d.layers, d.heads, d.kv_heads, d.head_dim, d.eps, d.rope_theta, d.tied,
+                 d.attn_bias, d.qk_norm, d.window, d.experts, d.topk, d.normalize, d.expert_inter,
+                 rotary_dim=d.rotary_dim, rope_scaling=scaling)
+    opt = O.AdamWConfig(learning_rate=1e-3, schedule="constant")
+    if lora is None:
+        t = Trainer(gd, 256, 4, 128)
+        t.load(weights)
+        params = {n: a.copy() for n, a in weights.items()}
+        m = {n: np.zeros_like(a) for n, a in params.items()}
+        v = {n: np.zeros_like(a) for n, a in params.items()}
+        for step in (1, 2):
+            loss_gpu, norm_gpu = t.step(windows, 1e-3, step, router_aux_loss=0.02 if d.experts else 0.0)
+            loss_cpu, _, norm_cpu, grads = O.train_step(O.oracle_kernels(), od, params, m, v, windows, opt, step, 2,
+                                                        router_aux_loss=0.02 if d.experts else 0.0)
+            assert loss_gpu == loss_cpu and norm_gpu == norm_cpu, (step, loss_gpu, loss_cpu)
+            for name in t.names:
+                shape = d.tensor_shapes()[name]
+                assert t.get(name, shape, t.GRAD).tobytes() == grads[name].tobytes(), (step, name)
+                assert t.get(name, shape).tobytes() == params[name].tobytes(), (step, name)
+                assert t.get(name, shape, t.M).tobytes() == m[name].tobytes(), (step, name)
+                assert t.get(name, shape, t.V).tobytes() == v[name].tobytes(), (step, name)
+    else:
+        adapters = O.init_adapters(d, lora, 5)
+        for name in adapters:
+            if name.endswith(".lora_b"):
+                adapters[name] = O.gaussian(len(name) + 7, *adapters[name].shape, scale=0.02)
+        t = Trainer(gd, 256, 4, 128, lora=lora_config(lora.rank, lora.alpha, lora.targets, lora.rslora))
+        t.load(weights)
+        t.load(adapters)
+        params = {n: a.copy() for n, a in adapters.items()}
+        m = {n: np.zeros_like(a) for n, a in params.items()}
+        v = {n: np.zeros_like(a) for n, a in params.items()}
+        for step in (1, 2):
+            loss_gpu, norm_gpu = t.step(windows, 1e-3, step)
+            out: dict = {}
+            loss_cpu, norm_cpu = O.lora_train_step(O.oracle_kernels(), od, weights, params, m, v, windows, opt, step,
+                                                   2, lora, out=out)
+            assert loss_gpu == loss_cpu and norm_gpu == norm_cpu, (step, loss_gpu, loss_cpu)
+            for name, a in params.items():
+                assert t.get(name, a.shape).tobytes() == a.tobytes(), (step, name)
+                assert t.get(name, a.shape, t.M).tobytes() == m[name].tobytes(), (step, name)
+                assert t.get(name, a.shape, t.V).tobytes() == v[name].tobytes(), (step, name)
+            for name in O.lora_target_weights(d, lora):
+                shape = d.tensor_shapes()[name]
+                assert t.get(name, shape, t.GRAD).tobytes() == out["weight_grads"][name].tobytes(), (step, name)
+    t.close()

@@ -175,3 +175,125 @@ def test_oracle_reproduces_the_dpo_finetune_fingerprint(family):
         losses.append(loss)
     assert losses[0] == O.oracle().orc_log(2.0)  # the model is its own reference at step 1 (z = 0)
     assert O.data_fingerprint(params) == GOLDEN["DPO_FINETUNE_FINGERPRINT"][family]
+
+
+# ---- RoPE scaling (numerics.py:267-349) and the LongRoPE / YaRN attention factor (transformer.py:204-245) ----
+
+PROMPT = [1, 17, 42, 5, 63, 0, 9, 9, 30]  # reference tests/test_transformer.py:17
+
+
+def yarn_scaling(factor: float, original: int) -> dict:
+    """importer.yarn_scaling (importing/importer.py:180-201) with its defaults: beta_fast 32, beta_slow 1, truncated,
+    attention factor 0.1 ln(factor) + 1 in the portable log (_yarn_mscale, :176-177)."""
+    return {"rope_type": "yarn", "factor": factor, "original_max_position_embeddings": original, "beta_fast": 32.0,
+            "beta_slow": 1.0, "truncate": True,
+            "attention_factor": 0.1 * 1.0 * O.oracle().orc_log(factor) + 1.0 if factor > 1.0 else 1.0}
+
+
+@pytest.mark.parametrize("family", ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe"])
+def test_forward_logits_match_tiny_logits_fingerprint(family):
+    """The next-token logits of PROMPT on the tiny imported models (golden_values.py TINY_LOGITS_FINGERPRINT)."""
+    d = O.FIXTURES[family]
+    logits = O.logits(O.oracle_kernels(), d, O.fixture_weights(d), PROMPT)
+    assert O.fingerprint(logits[-1]) == GOLDEN["TINY_LOGITS_FINGERPRINT"][family]
+
+
+@pytest.mark.parametrize(("name", "family", "factor", "original"), [
+    ("llama-yarn", "llama", 4.0, 2048),  # dllm import --context-length 8192 of the tiny Llama (2048 positions)
+    ("qwen3-yarn", "qwen3", 4.0, 4),  # Qwen3 with a YaRN rope_scaling: the factor folds into its QK-norm weights
+])
+def test_yarn_models_match_long_context_fingerprints(name, family, factor, original):
+    """reference tests/test_long_context.py:168-189 (LONG_MODELS): the YaRN frequencies and the attention factor
+    folded into the q/k rows (or the QK-norm weights), through the whole forward pass, against the reference's
+    LONG_CONTEXT_FINGERPRINTS."""
+    from dataclasses import replace
+
+    d = O.FIXTURES[family]
+    scaling = yarn_scaling(factor, original)
+    scaled = replace(d, inv_freq=tuple(O.rope_inv_freq_scaled(d.head_dim, d.rope_theta, scaling)),
+                     rope_attention_factor=scaling["attention_factor"])
+    logits = O.logits(O.oracle_kernels(), scaled, O.fixture_weights(d), PROMPT)
+    assert O.fingerprint(logits[-1]) == GOLDEN["LONG_CONTEXT_FINGERPRINTS"][name]
+
+
+def test_rope_scaling_closed_forms():
+    """reference tests/test_kernels.py:190-209 and test_long_context.py:29-50: linear and LongRoPE divide each default
+    frequency by their factor (one correctly rounded division); llama3 keeps the short wavelengths, divides the long
+    ones by the factor and interpolates strictly between in the band; YaRN follows transformers' float64 formula to
+    1e-13, its fastest pair extrapolates and its slowest interpolates exactly; the default is theta^(-2i/d)."""
+    plain = O.rope_inv_freq_scaled(64, 500000.0)
+    np.testing.assert_allclose(plain, [500000.0 ** (-2 * i / 64) for i in range(32)], rtol=1e-14)
+    assert plain.tobytes() == O.rope_inv_freq(64, 500000.0).tobytes()
+    linear = O.rope_inv_freq_scaled(64, 500000.0, {"type": "linear", "factor": 4.0})
+    assert linear.tobytes() == (plain / 4).tobytes()
+    factors = [1.0 + 0.37 * i for i in range(16)]
+    longrope = O.rope_inv_freq_scaled(32, 10000.0, {"rope_type": "longrope", "short_factor": factors,
+                                                    "long_factor": [2.0] * 16})
+    assert longrope.tobytes() == (O.rope_inv_freq_scaled(32, 10000.0) / np.array(factors)).tobytes()
+    long = O.rope_inv_freq_scaled(32, 10000.0, {"rope_type": "longrope", "short_factor": factors,
+                                                "long_factor": [2.0] * 16, "factor_set": "long"})
+    assert long.tobytes() == (O.rope_inv_freq_scaled(32, 10000.0) / 2.0).tobytes()
+    llama3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+              "original_max_position_embeddings": 8192}
+    plain = O.rope_inv_freq_scaled(128, 500000.0)
+    scaled = O.rope_inv_freq_scaled(128, 500000.0, llama3)
+    assert scaled[0] == plain[0] and scaled[-1] == plain[-1] / 8
+    band = [i for i, f in enumerate(plain) if 2048 < 2 * np.pi / f < 8192]
+    assert band and all(plain[i] / 8 < scaled[i] < plain[i] for i in band)
+    for scaling in ({"factor": 4.0, "original_max_position_embeddings": 32768},
+                    {"factor": 2.5, "original_max_position_embeddings": 4096, "beta_fast": 16.0, "beta_slow": 2.0},
+                    {"factor": 8.0, "original_max_position_embeddings": 2048, "truncate": False},
+                    {"factor": 4.0, "original_max_position_embeddings": 64}):
+        scaling = {"rope_type": "yarn", **scaling}
+        ours = O.rope_inv_freq_scaled(128, 1_000_000.0, scaling)
+        base = 1_000_000.0 ** (-np.arange(0, 128, 2, dtype=np.float64) / 128)
+
+        def correction(rotations):
+            return 128 * np.log(scaling["original_max_position_embeddings"] / (rotations * 2 * np.pi)) / (
+                2 * np.log(1_000_000.0))
+
+        low, high = correction(scaling.get("beta_fast", 32)), correction(scaling.get("beta_slow", 1))
+        if scaling.get("truncate", True):
+            low, high = np.floor(low), np.ceil(high)
+        low, high = max(low, 0), min(high, 127)
+        high = high + 0.001 if low == high else high
+        extrapolation = 1 - np.clip((np.arange(64) - low) / (high - low), 0, 1)
+        want = base / scaling["factor"] * (1 - extrapolation) + base * extrapolation
+        np.testing.assert_allclose(ours, want, rtol=1e-13, atol=0)
+        default = O.rope_inv_freq_scaled(128, 1_000_000.0)
+        assert ours[0] == default[0] and ours[-1] == default[-1] / scaling["factor"]
+    tiny = O.rope_inv_freq_scaled(8, 10000.0, {"rope_type": "yarn", "factor": 2.0,
+                                               "original_max_position_embeddings": 1, "truncate": True})
+    assert np.all(np.isfinite(tiny))
+
+
+def test_attention_factor_fold_is_a_weight_scale():
+    """The attention factor is fold_scales (transformer.py:224-245): the model with factor a equals the unscaled model
+    on weights whose rotated q/k rows are multiplied by f32(a), and the gradients of the stored weights are those
+    of the folded ones with the same rows times f32(a) (_unfold, backprop.py:380-394). Partial rotary: rows past
+    rotary_dim in each head keep their values."""
+    from dataclasses import replace
+
+    d = replace(O.FIXTURES["qwen2"], rotary_dim=2)  # head_dim 4 (attention biases: the bias rows fold too)
+    w = O.fixture_weights(d)
+    a = 1.25
+    folded = dict(w)
+    hd, rd = d.head_dim, d.rotary_dim
+    for name in w:
+        if name.endswith(("attention.q.weight", "attention.q.bias", "attention.k.weight", "attention.k.bias")):
+            rows = w[name].reshape(-1, hd, *w[name].shape[1:]).copy()
+            rows[:, :rd] *= np.float32(a)
+            folded[name] = rows.reshape(w[name].shape)
+    scaled = replace(d, rope_attention_factor=a)
+    kern = O.oracle_kernels()
+    assert O.logits(kern, scaled, w, PROMPT).tobytes() == O.logits(kern, d, folded, PROMPT).tobytes()
+    loss_a, _, g_a = O.window_gradients(kern, scaled, w, PROMPT[:-1], PROMPT[1:])
+    loss_f, _, g_f = O.window_gradients(kern, d, folded, PROMPT[:-1], PROMPT[1:])
+    assert loss_a == loss_f
+    for name in w:
+        want = g_f[name]
+        if name in folded and folded[name] is not w[name]:
+            rows = want.reshape(-1, hd, *want.shape[1:]).copy()
+            rows[:, :rd] *= np.float32(a)
+            want = rows.reshape(want.shape)
+        assert g_a[name].tobytes() == want.tobytes(), name
