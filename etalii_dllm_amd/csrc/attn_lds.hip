@@ -12,8 +12,9 @@
 //
 // attn_tile_kernel mapping: a wave owns 16 consecutive rows by 64 CJ columns; each lane holds a 4-row x 4 CJ-column
 // register tile, so the LDS bytes read per multiply-add are few (the vector ALU, not the LDS, sets the pace). A stage
-// is 16 consecutive l: the workgroup's A (16 l x 64 rows) and B (16 l x 64 CJ columns) are copied global -> LDS with
-// gfx950's direct-to-LDS loads while the previous stage is computed.
+// is 16 consecutive l: the workgroup's A (16 l x 64 rows) is copied global -> LDS with gfx950's direct-to-LDS loads
+// and B (16 l x 64 CJ columns) loaded into registers while the previous stage is computed, then widened to double
+// as it is written to LDS.
 // Causal rows have ragged spans: stages inside every row's span of the wave run unpredicated; at the ragged ends
 // each (row, l) is taken only when l lies in that row's span (a wave-uniform test), so every row adds exactly its
 // own steps, in order, and nothing else. Tiles are dispatched longest reduction first.
@@ -86,10 +87,12 @@ __device__ __forceinline__ void row_span(const TileParams& p, int64_t r, int64_t
     }
 }
 
+// B arrives as floats and is widened to double once, when its stage is written to LDS: each of the 4 lanes of a wave
+// (and the 4 waves) that read a B value takes it ready, and the inner loop has no conversions.
 template <int CJ>
 struct Stage {
     double a[kChunk][kTileRows];
-    float b[kChunk][64 * CJ];
+    double b[kChunk][64 * CJ];
 };
 
 template <int CJ>
@@ -97,22 +100,25 @@ constexpr int stage_copies() {
     return 2 + CJ;
 }
 
+// Waits until at most `pending` of this wave's vector-memory operations are outstanding and its LDS writes have
+// landed, then joins the workgroup.
 template <int kPending>
 __device__ __forceinline__ void wait_stage() {
     if (kPending == 0)
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     else
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPending) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kPending) : "memory");
 }
 
 __device__ __forceinline__ void workgroup_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// Copies of the stage holding steps l .. l + 15 (steps past `last` repeat step `last`; they are never used). Wave w
-// copies A rows (steps) 4w .. 4w + 3 (doubles: two per instruction) and B rows 4w .. 4w + 3.
+// The stage holding steps l .. l + 15 (steps past `last` repeat step `last`; they are never used). Wave w copies A
+// rows (steps) 4w .. 4w + 3 straight to LDS (doubles: two per instruction) and loads B rows 4w .. 4w + 3 into
+// registers (16 bytes per lane), which store_stage_b widens and writes once the current stage has been computed.
 template <int CJ>
 __device__ __forceinline__ void issue_stage(Stage<CJ>& st, const double* a_base, const Op& ao, int64_t i0,
                                             const float* b_base, const Op& bo, int64_t b_col, int64_t l, int64_t last,
-                                            int wave, int lane) {
+                                            int wave, int lane, float4 (&breg)[CJ]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int r = 4 * wave + 2 * t;
@@ -133,7 +139,20 @@ __device__ __forceinline__ void issue_stage(Stage<CJ>& st, const double* a_base,
             const uint32_t g = static_cast<uint32_t>(bo.group), u = static_cast<uint32_t>(lr), qt = u / g;
             row = static_cast<int64_t>(qt) * bo.ld + static_cast<int64_t>(u - qt * g) * bo.ld_inner;
         }
-        copy16_to_lds(b_base + row + b_col, &st.b[4 * wave + t * kRowsPerCopy][0]);
+        breg[t] = *reinterpret_cast<const float4*>(b_base + row + b_col);
+    }
+}
+
+template <int CJ>
+__device__ __forceinline__ void store_stage_b(Stage<CJ>& st, int wave, int lane, const float4 (&breg)[CJ]) {
+    constexpr int kLanesPerRow = 16 * CJ;
+    constexpr int kRowsPerCopy = 64 / kLanesPerRow;
+    const int sub = lane / kLanesPerRow, col = 4 * (lane % kLanesPerRow);
+#pragma unroll
+    for (int t = 0; t < CJ; ++t) {
+        double2* dst = reinterpret_cast<double2*>(&st.b[4 * wave + t * kRowsPerCopy + sub][col]);
+        dst[0] = double2{breg[t].x, breg[t].y};
+        dst[1] = double2{breg[t].z, breg[t].w};
     }
 }
 
@@ -152,11 +171,12 @@ __device__ __forceinline__ void read_step(const Stage<CJ>& st, int k, int wave, 
     a[3] = a23.y;
 #pragma unroll
     for (int c = 0; c < CJ; ++c) {
-        const float4 v = *reinterpret_cast<const float4*>(&st.b[k][64 * c + 4 * cg]);
-        b[4 * c] = v.x;
-        b[4 * c + 1] = v.y;
-        b[4 * c + 2] = v.z;
-        b[4 * c + 3] = v.w;
+        const double2* br = reinterpret_cast<const double2*>(&st.b[k][64 * c + 4 * cg]);
+        const double2 b01 = br[0], b23 = br[1];
+        b[4 * c] = b01.x;
+        b[4 * c + 1] = b01.y;
+        b[4 * c + 2] = b23.x;
+        b[4 * c + 3] = b23.y;
     }
 }
 
@@ -283,10 +303,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     const int64_t steps = t_hi - t_lo;
     const int64_t stages = steps > 0 ? (steps + kChunk - 1) / kChunk : 0;
     const int64_t last = t_hi - 1;
-    if (stages > 0) issue_stage<CJ>(st[0], A, o.A, i0, B, o.B, b_col, t_lo, last, wave, lane);
+    float4 breg[CJ];
+    if (stages > 0) {
+        issue_stage<CJ>(st[0], A, o.A, i0, B, o.B, b_col, t_lo, last, wave, lane, breg);
+        store_stage_b<CJ>(st[0], wave, lane, breg);
+    }
     for (int64_t s = 0; s < stages; ++s) {
         if (s + 1 < stages) {
-            issue_stage<CJ>(st[(s + 1) & 1], A, o.A, i0, B, o.B, b_col, t_lo + (s + 1) * kChunk, last, wave, lane);
+            issue_stage<CJ>(st[(s + 1) & 1], A, o.A, i0, B, o.B, b_col, t_lo + (s + 1) * kChunk, last, wave, lane,
+                            breg);
             wait_stage<stage_copies<CJ>()>();
         } else {
             wait_stage<0>();
@@ -297,6 +322,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
             stage_all<CJ>(st[s & 1], wave, rg, cg, acc);
         else
             stage_masked<CJ>(p, st[s & 1], wave, rg, cg, l0, n_steps, tw, n, I, acc);
+        // the next stage's B, widened, into the other buffer (last read two stages ago, before the last barrier)
+        if (s + 1 < stages) store_stage_b<CJ>(st[(s + 1) & 1], wave, lane, breg);
         workgroup_barrier();  // every wave is done with this stage before the next issue refills it
     }
     // the output rows' base and stride, opaque so the compiler keeps no per-element addresses across the reduction
