@@ -41,6 +41,14 @@ __device__ __forceinline__ const T* op_base(const Op& o, int64_t w, int64_t seg_
     return static_cast<const T*>(o.ptr) + w * o.w_stride + seg_w * o.seg_stride + (hz / o.head_div) * o.head_stride;
 }
 
+// A wave-uniform 64-bit value the compiler cannot prove uniform (loaded through a pointer), kept in scalar registers.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint64_t u = static_cast<uint64_t>(v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u & 0xffffffffu)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32)));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 struct OperandSet {
     Op A, B, C;
 };
@@ -97,7 +105,7 @@ struct Stage {
 
 template <int CJ>
 constexpr int stage_copies() {
-    return 2 + CJ;
+    return 2 + 2 * CJ;
 }
 
 // Waits until at most `pending` of this wave's vector-memory operations are outstanding and its LDS writes have
@@ -112,54 +120,111 @@ __device__ __forceinline__ void wait_stage() {
 
 __device__ __forceinline__ void workgroup_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// The stage holding steps l .. l + 15 (steps past `last` repeat step `last`; they are never used). Wave w copies A
+// Where the next stage's copies start, as wave-uniform values (scalar registers): step l, A's row of step l (from
+// column i0), and B's row of query l / group (head 0 of the group; B rows are (query, head of the group) pairs) with
+// rs = l % group. Each lane adds its own byte offsets.
+struct StageCursor {
+    int64_t l;
+    const double* a;
+    const float* b;
+    int64_t rs;
+};
+
+// One stage's advance of the cursor, computed once per tile: A moves kChunk rows; B moves kChunk (query, head)
+// pairs: kChunk / G queries, and one more when the head (rs + kChunk % G) wraps.
+struct StageStep {
+    int64_t a, b, b_carry, rs, group;
+};
+
+__device__ __forceinline__ StageStep stage_step(const Op& ao, const Op& bo) {
+    StageStep t;
+    t.group = bo.group;
+    t.a = kChunk * ao.ld;
+    t.b = (kChunk / bo.group) * bo.ld;
+    t.b_carry = bo.ld;
+    t.rs = kChunk % bo.group;
+    return t;
+}
+
+// Advances the cursor by one stage with scalar arithmetic only.
+__device__ __forceinline__ void advance(StageCursor& c, const StageStep& t) {
+    c.l += kChunk;
+    c.a += t.a;
+    c.b += t.b;
+    c.rs += t.rs;
+    if (c.rs >= t.group) {
+        c.rs -= t.group;
+        c.b += t.b_carry;
+    }
+}
+
+// The per-lane constants of the copies: A's byte column and its row stride; B's byte columns (two float2 chunks
+// per 64-column block: 2cg, 2cg + 1 and 32 + 2cg, 33 + 2cg, cg = the lane's position among the block's 16 lanes,
+// so that the doubles 16 lanes write, and later read, are 256 contiguous bytes: no LDS bank conflicts), its row
+// strides and the divisor of grouped rows.
+struct LaneCopy {
+    uint32_t a_col, a_ld8;
+    uint32_t b_col[2], b_ld4, b_in4;
+    uint32_t group, magic;  // x / group == (x * magic) >> 16 for the x < 32 used here
+};
+
+// The stage of steps c.l .. c.l + 15 (steps past `last` repeat step `last`; they are never used). Wave w copies A
 // rows (steps) 4w .. 4w + 3 straight to LDS (doubles: two per instruction) and loads B rows 4w .. 4w + 3 into
-// registers (16 bytes per lane), which store_stage_b widens and writes once the current stage has been computed.
+// registers, which store_stage_b widens and writes once the current stage has been computed.
 template <int CJ>
-__device__ __forceinline__ void issue_stage(Stage<CJ>& st, const double* a_base, const Op& ao, int64_t i0,
-                                            const float* b_base, const Op& bo, int64_t b_col, int64_t l, int64_t last,
-                                            int wave, int lane, float4 (&breg)[CJ]) {
+__device__ __forceinline__ void issue_stage(Stage<CJ>& st, const StageCursor& c, const LaneCopy& lc, int64_t last,
+                                            int wave, int lane, float2 (&breg)[2 * CJ]) {
+    const int64_t left = last - c.l;  // the stage's steps past this one repeat it
+    const uint32_t d = static_cast<uint32_t>(left < kChunk ? left : kChunk);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        const int r = 4 * wave + 2 * t;
-        const int64_t lr = l + r + (lane >> 5) <= last ? l + r + (lane >> 5) : last;
-        copy16_to_lds(a_base + lr * ao.ld + i0 + (lane & 31) * 2, &st.a[r][0]);
+        const uint32_t r = static_cast<uint32_t>(4 * wave + 2 * t + (lane >> 5));
+        const uint32_t off = (r < d ? r : d) * lc.a_ld8 + lc.a_col;
+        copy16_to_lds_s(c.a, off, &st.a[4 * wave + 2 * t][0]);
     }
     constexpr int kLanesPerRow = 16 * CJ;
     constexpr int kRowsPerCopy = 64 / kLanesPerRow;
     const int sub = lane / kLanesPerRow;
+    const char* b = reinterpret_cast<const char*>(c.b);
 #pragma unroll
     for (int t = 0; t < CJ; ++t) {
-        const int r = 4 * wave + t * kRowsPerCopy + sub;
-        const int64_t lr = l + r <= last ? l + r : last;
-        int64_t row;
-        if (bo.group == 1) {
-            row = lr * bo.ld;
-        } else {  // (query, head of the group) rows; l < 2^32
-            const uint32_t g = static_cast<uint32_t>(bo.group), u = static_cast<uint32_t>(lr), qt = u / g;
-            row = static_cast<int64_t>(qt) * bo.ld + static_cast<int64_t>(u - qt * g) * bo.ld_inner;
+        const uint32_t r = static_cast<uint32_t>(4 * wave + t * kRowsPerCopy + sub);
+        const uint32_t rr = r < d ? r : d;
+        uint32_t off;
+        if (lc.group == 1) {
+            off = rr * lc.b_ld4;
+        } else {
+            const uint32_t x = rr + static_cast<uint32_t>(c.rs), q = (x * lc.magic) >> 16;
+            off = q * lc.b_ld4 + (x - q * lc.group) * lc.b_in4;
         }
-        breg[t] = *reinterpret_cast<const float4*>(b_base + row + b_col);
+        breg[2 * t] = *reinterpret_cast<const float2*>(b + static_cast<uint64_t>(off + lc.b_col[0]));
+        breg[2 * t + 1] = *reinterpret_cast<const float2*>(b + static_cast<uint64_t>(off + lc.b_col[1]));
     }
 }
 
 template <int CJ>
-__device__ __forceinline__ void store_stage_b(Stage<CJ>& st, int wave, int lane, const float4 (&breg)[CJ]) {
+__device__ __forceinline__ void store_stage_b(Stage<CJ>& st, int wave, int lane, const float2 (&breg)[2 * CJ]) {
     constexpr int kLanesPerRow = 16 * CJ;
     constexpr int kRowsPerCopy = 64 / kLanesPerRow;
-    const int sub = lane / kLanesPerRow, col = 4 * (lane % kLanesPerRow);
+    const int sub = lane / kLanesPerRow, q = lane % kLanesPerRow;
+    const int col = 64 * (q >> 4) + 2 * (q & 15);
 #pragma unroll
     for (int t = 0; t < CJ; ++t) {
-        double2* dst = reinterpret_cast<double2*>(&st.b[4 * wave + t * kRowsPerCopy + sub][col]);
-        dst[0] = double2{breg[t].x, breg[t].y};
-        dst[1] = double2{breg[t].z, breg[t].w};
+        double* row = &st.b[4 * wave + t * kRowsPerCopy + sub][0];
+        *reinterpret_cast<double2*>(row + col) = double2{breg[2 * t].x, breg[2 * t].y};
+        *reinterpret_cast<double2*>(row + col + 32) = double2{breg[2 * t + 1].x, breg[2 * t + 1].y};
     }
 }
 
 // A lane's register tile: 4 consecutive rows (4 rg .. 4 rg + 3 of the wave's 16, rg = lane / 16) by 4 CJ columns
-// (CJ groups of 4: columns 64 c + 4 cg .. 64 c + 4 cg + 3, cg = lane % 16). Per step a lane reads its 4 A values
-// (two 16-byte LDS reads shared by 16 lanes) and its 4 CJ B values (CJ 16-byte reads, each a contiguous 256 bytes
-// over the 16 column groups): 32 + 16 CJ bytes per lane for 16 CJ multiply-adds.
+// (per 64-column block c: 64 c + 2 cg, + 1, 64 c + 32 + 2 cg, + 1; cg = lane % 16). Per step a lane reads its 4 A
+// values (two 16-byte LDS reads shared by 16 lanes) and its 4 CJ B values (2 CJ 16-byte reads, 16 lanes reading 256
+// contiguous bytes): 32 + 16 CJ bytes per lane for 16 CJ multiply-adds.
+template <int CJ>
+__device__ __forceinline__ int64_t tile_column(int c, int cg) {
+    return 64 * (c >> 2) + ((c & 2) ? 32 : 0) + 2 * cg + (c & 1);
+}
+
 template <int CJ>
 __device__ __forceinline__ void read_step(const Stage<CJ>& st, int k, int wave, int rg, int cg, double (&a)[4],
                                           double (&b)[4 * CJ]) {
@@ -171,8 +236,8 @@ __device__ __forceinline__ void read_step(const Stage<CJ>& st, int k, int wave, 
     a[3] = a23.y;
 #pragma unroll
     for (int c = 0; c < CJ; ++c) {
-        const double2* br = reinterpret_cast<const double2*>(&st.b[k][64 * c + 4 * cg]);
-        const double2 b01 = br[0], b23 = br[1];
+        const double2 b01 = *reinterpret_cast<const double2*>(&st.b[k][64 * c + 2 * cg]);
+        const double2 b23 = *reinterpret_cast<const double2*>(&st.b[k][64 * c + 32 + 2 * cg]);
         b[4 * c] = b01.x;
         b[4 * c + 1] = b01.y;
         b[4 * c + 2] = b23.x;
@@ -273,7 +338,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     const int64_t z = zz % p.Z;
     const OperandSet& o = p.set[set];
     const int64_t w = z / p.heads, hz = z % p.heads;
-    const int64_t seg_w = p.seg[w], n = p.seg[w + 1] - seg_w;
+    const int64_t seg_w = uniform64(p.seg[w]), n = uniform64(p.seg[w + 1]) - seg_w;
     const int64_t I = p.rows_kind == 0 ? n : p.head_dim;
     const int64_t J = p.cols_kind == 0 ? n : p.head_dim;
     const int64_t i0 = ti * kTileRows, j0 = tj * 64 * CJ;
@@ -290,10 +355,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     } else {
         w_lo = w_hi = 0;
     }
-    const double* A = op_base<double>(o.A, w, seg_w, hz);
-    const float* B = op_base<float>(o.B, w, seg_w, hz);
-    const int64_t chunk = j0 + 4 * (lane % (16 * CJ));
-    const int64_t b_col = chunk + 4 <= p.b_row_alloc ? chunk : p.b_row_alloc - 4;
+    LaneCopy lc;
+    lc.a_col = static_cast<uint32_t>((lane & 31) * 16);
+    lc.a_ld8 = static_cast<uint32_t>(o.A.ld * 8);
+    {
+        const int q = lane % (16 * CJ);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t col = j0 + 64 * (q >> 4) + 32 * h + 2 * (q & 15);
+            lc.b_col[h] = static_cast<uint32_t>((col + 2 <= p.b_row_alloc ? col : p.b_row_alloc - 2) * 4);
+        }
+    }
+    lc.b_ld4 = static_cast<uint32_t>(o.B.ld * 4);
+    lc.b_in4 = static_cast<uint32_t>(o.B.ld_inner * 4);
+    lc.group = static_cast<uint32_t>(o.B.group);
+    lc.magic = (65536u + lc.group - 1) / lc.group;
+    StageCursor cur;
+    cur.l = t_lo;
+    cur.a = op_base<double>(o.A, w, seg_w, hz) + t_lo * o.A.ld + i0;
+    cur.rs = t_lo % o.B.group;
+    cur.b = op_base<float>(o.B, w, seg_w, hz) + (t_lo / o.B.group) * o.B.ld;
     const int rg = lane >> 4, cg = lane & 15;
     double acc[4][4 * CJ];
 #pragma unroll
@@ -303,15 +384,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     const int64_t steps = t_hi - t_lo;
     const int64_t stages = steps > 0 ? (steps + kChunk - 1) / kChunk : 0;
     const int64_t last = t_hi - 1;
-    float4 breg[CJ];
+    float2 breg[2 * CJ];
     if (stages > 0) {
-        issue_stage<CJ>(st[0], A, o.A, i0, B, o.B, b_col, t_lo, last, wave, lane, breg);
+        issue_stage<CJ>(st[0], cur, lc, last, wave, lane, breg);
         store_stage_b<CJ>(st[0], wave, lane, breg);
     }
+    const StageStep step = stage_step(o.A, o.B);
     for (int64_t s = 0; s < stages; ++s) {
         if (s + 1 < stages) {
-            issue_stage<CJ>(st[(s + 1) & 1], A, o.A, i0, B, o.B, b_col, t_lo + (s + 1) * kChunk, last, wave, lane,
-                            breg);
+            advance(cur, step);
+            issue_stage<CJ>(st[(s + 1) & 1], cur, lc, last, wave, lane, breg);
             wait_stage<stage_copies<CJ>()>();
         } else {
             wait_stage<0>();
@@ -331,6 +413,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
                     (hz / o.C.head_div) * o.C.head_stride + tw * o.C.ld + j0;
     int64_t c_ld = o.C.ld;
     asm volatile("" : "+s"(c_base), "+s"(c_ld));
+    const auto c_out = global_ptr(c_base);
     const double* rs = p.rowscale ? p.rowscale + z * p.rowscale_zstride + tw : nullptr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -339,11 +422,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
         const double scale = rs ? rs[q] : 1.0;
 #pragma unroll
         for (int c = 0; c < 4 * CJ; ++c) {
-            const int64_t jl = 64 * (c >> 2) + 4 * cg + (c & 3);
+            const int64_t jl = tile_column<CJ>(c, cg);
             if (j0 + jl >= J) continue;
             double v = acc[i][c];
             if (rs) v = v * scale;
-            c_base[q * c_ld + jl] = static_cast<float>(v);
+            c_out[q * c_ld + jl] = static_cast<float>(v);
         }
     }
 }
@@ -360,9 +443,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
 typedef double ma_v4d __attribute__((ext_vector_type(4)));
 constexpr int kMfmaChunk = 16;
 
+// B rows are padded by 16 floats so the four l rows a wave reads at once (lanes 16k .. 16k + 15 read row k) start
+// in different banks.
+constexpr int kMfmaBRow = 256 + 16;
+
 struct MfmaStage {
     float a[kMfmaChunk * kTileRows];  // [l / 4][row][l % 4]
-    float b[kMfmaChunk * 256];        // [l][column]
+    float b[kMfmaChunk * kMfmaBRow];  // [l][column]
 };
 
 // The copies: a wave-uniform base (SGPRs) plus this lane's byte offset, computed once per tile, so a stage's copies
@@ -406,7 +493,7 @@ __device__ __forceinline__ void mfma_issue(MfmaStage& st, const float* A, int64_
             const int64_t over = l + ((t * 256 + tid) >> 6) - (L - 1);
             if (over > 0) vb -= static_cast<uint32_t>(over * b_ld * 4);
         }
-        copy16_to_lds_s(B + l * b_ld, vb, &st.b[(t * 256 + wave * 64) * 4]);
+        copy16_to_lds_s(B + l * b_ld, vb, &st.b[(4 * t + wave) * kMfmaBRow]);  // row 4t + wave
     }
 }
 
@@ -416,7 +503,7 @@ __device__ __forceinline__ void mfma_frags(const MfmaStage& st, int s, int wave,
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         a[q] = static_cast<double>(st.a[(s * kTileRows + 16 * q + c16) * 4 + k]);
-        b[q] = static_cast<double>(st.b[(4 * s + k) * 256 + wave * 64 + 16 * q + c16]);
+        b[q] = static_cast<double>(st.b[(4 * s + k) * kMfmaBRow + wave * 64 + 16 * q + c16]);
     }
 }
 
@@ -493,6 +580,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                    (w * o.C.w_stride + seg_w * o.C.seg_stride + (hz / o.C.head_div) * o.C.head_stride) * elem;
     int64_t c_ld = o.C.ld * elem;
     asm volatile("" : "+s"(c_base), "+s"(c_ld));  // no output addresses kept live across the reduction
+    const auto c_out = global_ptr(c_base);
     const double* rs = p.rowscale ? p.rowscale + zz * p.rowscale_zstride : nullptr;
     const int64_t jw = j0 + wave * 64 + (lane & 15);
 #pragma unroll
@@ -501,17 +589,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int r = 0; r < 4; ++r) {
             const int64_t i = i0 + 16 * bi + (lane >> 4) + 4 * r;
             if (i >= I) continue;
-            char* row = c_base + i * c_ld;
+            const auto row = c_out + i * c_ld;
 #pragma unroll
             for (int bj = 0; bj < 4; ++bj) {
                 const int64_t j = jw + 16 * bj;
                 if (j >= J) continue;
                 if constexpr (kOutDouble) {
-                    reinterpret_cast<double*>(row)[j] = acc[bi][bj][r] * p.out_scale;
+                    reinterpret_cast<global_pointer<double>>(row)[j] = acc[bi][bj][r] * p.out_scale;
                 } else {
                     double v = acc[bi][bj][r];
                     if (rs) v = v * rs[i];
-                    reinterpret_cast<float*>(row)[j] = static_cast<float>(v);
+                    reinterpret_cast<global_pointer<float>>(row)[j] = static_cast<float>(v);
                 }
             }
         }

@@ -9,6 +9,17 @@
 
 namespace dllm_hip {
 
+// A pointer restated as addressing global memory. A copy the compiler cannot follow (e.g. one passed through inline
+// assembly to keep it in scalar registers) loses that, and its loads and stores become flat ones, which wait on both
+// the vector-memory and the LDS counters.
+template <typename T>
+using global_pointer = __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ global_pointer<T> global_ptr(T* p) {
+    return (global_pointer<T>)p;
+}
+
 enum Status : int {
     kOk = 0,
     kInvalidArgument = 1,  // the reference raises ValueError for these (cpp/kernels.cpp:97-101)

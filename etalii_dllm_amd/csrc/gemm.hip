@@ -28,7 +28,9 @@
 // When the tile grid is too small to fill the GPU and a scratch buffer is given, the windows run as separate
 // workgroups into per-window float partials, and a second pass adds them in window order: the same roundings in
 // the same order.
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "common.h"
 #include "lds_copy.h"
@@ -44,6 +46,7 @@ constexpr int kTileJ = 256;    // columns per wave (4 per lane)
 constexpr int kBlockI = kTileI * kWavesI;
 constexpr int64_t kParallelWindowsBelow = 2048;  // tiles
 constexpr int64_t kGroupRows = 8;                // row blocks per L2 group
+constexpr int kXcdRanges = 8;                    // XCDs (workgroups are dealt round-robin over them)
 // Matrix-core launches of fewer 128 x 128 tiles take smaller ones (measured on the SmolLM2-135M step: 21.8k tokens/s
 // against 12.3k with 128 x 128 tiles only; thresholds 512 and 2048 measure alike, 128 slower).
 constexpr int64_t kSmallTilesBelow = 512;
@@ -426,7 +429,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             const int64_t i = i0 + q;
             if (i >= p.I) break;
             const int arow = p.seg_addrow ? p.seg_addrow[static_cast<int64_t>(s) * p.I + i] : -1;
-            float* out = out_base + i * ld_out + j0;
+            const auto out = global_ptr(out_base) + i * ld_out + j0;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 if (j0 + c >= p.J) continue;
@@ -653,7 +656,8 @@ template <int kA, int kBI, int kBJ>
 __device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA, kBI, kBJ> (&st)[2],
                                             const MCopyOffsets<kBI, kBJ>& o, int64_t i_blk, int64_t j_blk, int tid,
                                             int wi, int wj, int lane, int64_t l0, int64_t l1,
-                                            mf_v4d (&acc)[kBI][kBJ]) {
+                                            mf_v4d (&acc)[kBI][kBJ], bool primed = false, int64_t next_l0 = 0,
+                                            int64_t next_l1 = 0) {
     using T = MTile<kBI, kBJ>;
 #pragma unroll
     for (int bi = 0; bi < kBI; ++bi)
@@ -665,14 +669,14 @@ __device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA, kBI,
     const int tail = static_cast<int>((l1 - l0) % kMStage);
     const int64_t chunks = full + (tail ? 1 : 0);
     const int wave = wi * 2 + wj;
-    auto issue = [&](MStage<kA, kBI, kBJ>& buf, int64_t l) {
-        if (l + kMStage - 1 <= last) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave);
-        else missue_stage<kA, kBI, kBJ>(p, buf, i_blk, j_blk, l, last, tid);
+    auto issue = [&](MStage<kA, kBI, kBJ>& buf, int64_t l, int64_t end) {
+        if (l + kMStage <= end) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave);
+        else missue_stage<kA, kBI, kBJ>(p, buf, i_blk, j_blk, l, end - 1, tid);
     };
-    issue(st[0], l0);
+    if (!primed) issue(st[0], l0, l1);
     for (int64_t c = 0; c < full; ++c) {
         if (c + 1 < chunks) {
-            issue(st[(c + 1) & 1], l0 + (c + 1) * kMStage);
+            issue(st[(c + 1) & 1], l0 + (c + 1) * kMStage, l1);
             wait_stage<T::PA + T::PB>();  // this stage landed; the next one's copies in flight
         } else {
             wait_stage<0>();
@@ -685,6 +689,9 @@ __device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA, kBI,
         mstage_tail<kA, kBI, kBJ>(st[full & 1], tail, wi, wj, lane, acc);
         workgroup_barrier();
     }
+    // the next window's first stage (both buffers are free after the last barrier): its copies fly during this
+    // window's epilogue
+    if (next_l0 < next_l1) issue(st[0], next_l0, next_l1);
 }
 
 template <int kMode, int kA, bool kGrouped = false, int kBI = 4, int kBJ = 4>
@@ -699,7 +706,12 @@ gemm_mfma_kernel(GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmPar
     const int wi = wave >> 1, wj = wave & 1;
     int64_t id;
     if constexpr (kGrouped) {
-        id = xcd_contiguous(blockIdx.x, gx);
+        // the XCD ranges follow the tile starts of the table (gy: its capacity); workgroups past their XCD's range
+        // have no tile
+        const int64_t* xcd_first = tile_start + gy + 1;
+        const int64_t x = blockIdx.x % kXcdRanges;
+        id = xcd_first[x] + blockIdx.x / kXcdRanges;
+        if (id >= xcd_first[x + 1]) return;
         int lo = 0, hi = ngroups - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
@@ -729,8 +741,30 @@ gemm_mfma_kernel(GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmPar
     if (kMode == kPlain) {
         maccumulate<kA, kBI, kBJ>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.l0, p.l1, acc);
         if (iw >= p.I) return;
+        // Per row block bi, the loads (bias, addend) are issued before the block's stores: interleaved, each store
+        // could alias the next load and serialise the memory round trips. The addend is either the output itself
+        // (same rows) or disjoint from it, so reading it first gives the same values.
+        const auto C = global_ptr(p.C);
+        const auto bias = global_ptr(p.bias);
+        const auto addsrc = global_ptr(p.addsrc);
 #pragma unroll
-        for (int bi = 0; bi < kBI; ++bi)
+        for (int bi = 0; bi < kBI; ++bi) {
+            float val[4][kBJ];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t i = iw + 16 * bi + ri + 4 * r;
+                const int64_t ic = i < p.I ? i : p.I - 1;
+#pragma unroll
+                for (int bj = 0; bj < kBJ; ++bj) {
+                    const int64_t j = jw + 16 * bj;
+                    const int64_t jc = j < p.J ? j : p.J - 1;
+                    double v = acc[bi][bj][r];
+                    if (p.bias) v += static_cast<double>(bias[jc]);
+                    float out = static_cast<float>(v);
+                    if (p.addsrc) out = addsrc[ic * p.ld_add + jc] + out;
+                    val[r][bj] = out;
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t i = iw + 16 * bi + ri + 4 * r;
@@ -738,44 +772,94 @@ gemm_mfma_kernel(GemmParams p, int64_t gx, int64_t gy, int64_t gz, const GemmPar
 #pragma unroll
                 for (int bj = 0; bj < kBJ; ++bj) {
                     const int64_t j = jw + 16 * bj;
-                    if (j >= p.J) continue;
-                    double v = acc[bi][bj][r];
-                    if (p.bias) v += static_cast<double>(p.bias[j]);
-                    float out = static_cast<float>(v);
-                    if (p.addsrc) out = p.addsrc[i * p.ld_add + j] + out;
-                    p.C[i * p.ldc + j] = out;
+                    if (j < p.J) C[i * p.ldc + j] = val[r][bj];
                 }
             }
+        }
         return;
     }
     const int s_begin = kMode == kWindowsInParallel ? static_cast<int>(bz) : 0;
     const int s_end = kMode == kWindowsInParallel ? s_begin + 1 : p.nseg;
+    const auto seg = global_ptr(p.seg);
+    // windows in sequence: each window's reduction issues the next one's first stage before this epilogue
+    bool primed = false;
     for (int s = s_begin; s < s_end; ++s) {
-        maccumulate<kA, kBI, kBJ>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, p.seg[s], p.seg[s + 1], acc);
+        const int64_t l0 = seg[s], l1 = seg[s + 1];
+        const int64_t n0 = s + 1 < s_end && l0 < l1 ? seg[s + 1] : 0, n1 = s + 1 < s_end && l0 < l1 ? seg[s + 2] : 0;
+        maccumulate<kA, kBI, kBJ>(p, st, o, i_blk, j_blk, tid, wi, wj, lane, l0, l1, acc, primed, n0, n1);
+        primed = n0 < n1;
         if (iw >= p.I) continue;
         float* out_base = kMode == kWindowsInParallel ? p.partial + static_cast<int64_t>(s) * p.I * p.J : p.C;
         int64_t ld_out = kMode == kWindowsInParallel ? p.J : p.ldc;
         asm volatile("" : "+s"(out_base), "+s"(ld_out));
+        const auto out_g = global_ptr(out_base);
+        // Per row block bi, every load of the epilogue (the running sum of the earlier windows, the addend rows, the
+        // row factors) is issued before the block's first store, each kind unconditionally or under one uniform
+        // branch: a load under a per-element branch, or next to a store that could alias it, costs a whole memory
+        // round trip per element.
+        const bool add_to_out = kMode == kWindowsInSequence && s > 0;
+        const float wscale = p.seg_weight ? global_ptr(p.seg_weight)[s] : 1.0f;
+        const auto seg_addrow = global_ptr(p.seg_addrow);
+        const auto seg_addend = global_ptr(p.seg_addend);
+        const auto seg_rowscale = global_ptr(p.seg_rowscale);
+        // the row and column of this lane, opaque per window: their many derived addresses are recomputed here
+        // rather than kept (or spilled) across the reduction
+        int64_t iw_e = iw, jw_e = jw;
+        asm volatile("" : "+s"(iw_e), "+v"(jw_e));
 #pragma unroll
-        for (int bi = 0; bi < kBI; ++bi)
+        for (int bi = 0; bi < kBI; ++bi) {
+            int64_t ic[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t i = iw + 16 * bi + ri + 4 * r;
+                const int64_t i = iw_e + 16 * bi + ri + 4 * r;
+                ic[r] = i < p.I ? i : p.I - 1;
+            }
+            int64_t jc[kBJ];
+#pragma unroll
+            for (int bj = 0; bj < kBJ; ++bj) {
+                const int64_t j = jw_e + 16 * bj;
+                jc[bj] = j < p.J ? j : p.J - 1;
+            }
+            float run[4][kBJ];  // read even for the first window (unused there): no branch around the loads
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int bj = 0; bj < kBJ; ++bj) run[r][bj] = out_g[ic[r] * ld_out + jc[bj]];
+            float addend[4][kBJ];
+            if (p.seg_addrow) {
+                int arow[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) arow[r] = seg_addrow[static_cast<int64_t>(s) * p.I + ic[r]];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int bj = 0; bj < kBJ; ++bj) {  // row 0 stands in for "no addend" (loaded, then dropped)
+                        const float a = seg_addend[(arow[r] >= 0 ? arow[r] : 0) * p.ld_seg_add + jc[bj]];
+                        addend[r][bj] = arow[r] >= 0 ? a : 0.0f;
+                    }
+            }
+            float rscale[4];
+            if (p.seg_rowscale) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) rscale[r] = seg_rowscale[ic[r]];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t i = iw_e + 16 * bi + ri + 4 * r;
                 if (i >= p.I) continue;
-                const int arow = p.seg_addrow ? p.seg_addrow[static_cast<int64_t>(s) * p.I + i] : -1;
-                const float rscale = p.seg_rowscale ? p.seg_rowscale[i] : 1.0f;
-                float* out = out_base + i * ld_out;
+                const auto out = out_g + i * ld_out;
 #pragma unroll
                 for (int bj = 0; bj < kBJ; ++bj) {
-                    const int64_t j = jw + 16 * bj;
+                    const int64_t j = jw_e + 16 * bj;
                     if (j >= p.J) continue;
                     float v = static_cast<float>(acc[bi][bj][r]);
-                    if (p.seg_addrow) v = v + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j] : 0.0f);
-                    if (p.seg_rowscale) v = v * rscale;  // the window's gradient unfolded (RoPE attention factor)
-                    if (p.seg_weight) v = v * p.seg_weight[s];  // the window's whole gradient times its factor
-                    out[j] = (kMode == kWindowsInParallel || s == 0) ? v : out[j] + v;
+                    if (p.seg_addrow) v = v + addend[r][bj];
+                    if (p.seg_rowscale) v = v * rscale[r];  // the window's gradient unfolded (RoPE attention factor)
+                    if (p.seg_weight) v = v * wscale;       // the window's whole gradient times its factor
+                    out[j] = add_to_out ? run[r][bj] + v : v;
                 }
             }
+        }
     }
 }
 
@@ -927,8 +1011,10 @@ GemmParams params_of(const GemmCall& g) {
 
 }  // namespace
 
+// The table: GemmParams[capacity], then the tile starts (capacity + 1), then the first tile of each XCD's range (9).
 size_t gemm_group_bytes(int n) {
-    return round_up(sizeof(GemmParams) * static_cast<size_t>(n), 8) + sizeof(int64_t) * (static_cast<size_t>(n) + 1);
+    return round_up(sizeof(GemmParams) * static_cast<size_t>(n), 8) +
+           sizeof(int64_t) * (static_cast<size_t>(n) + 1 + kXcdRanges + 1);
 }
 
 int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_table, GemmGroup* group) {
@@ -961,6 +1047,39 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
     }
     starts[used] = tiles;
     DLLM_REQUIRE(tiles < (int64_t{1} << 31), "matmul group too large for one launch");
+    // Each XCD takes a contiguous range of tiles (its L2 serves the A and B blocks they share) holding an equal share
+    // of the work. A tile's work is its reduction length plus a fixed cost; the tiles of the experts' weight
+    // gradients all have the size of the output, so equal tile counts would load an XCD by the rows of its experts.
+    int64_t* xcd_first = starts + capacity + 1;
+    {
+        std::vector<double> work(static_cast<size_t>(used));
+        double total = 0.0;
+        for (int k = 0; k < used; ++k) {
+            const GemmParams& q = ps[k];
+            work[static_cast<size_t>(k)] = static_cast<double>(q.l1 - q.l0) + 64.0;
+            total += work[static_cast<size_t>(k)] * static_cast<double>(starts[k + 1] - starts[k]);
+        }
+        int64_t longest = 0;
+        int k = 0;
+        double before = 0.0;  // work of the tiles ahead of group k
+        xcd_first[0] = 0;
+        for (int x = 1; x <= kXcdRanges; ++x) {
+            if (x == kXcdRanges) {
+                xcd_first[x] = tiles;
+            } else {
+                const double target = total * x / kXcdRanges;
+                while (k < used && before + work[static_cast<size_t>(k)] * (starts[k + 1] - starts[k]) <= target) {
+                    before += work[static_cast<size_t>(k)] * static_cast<double>(starts[k + 1] - starts[k]);
+                    ++k;
+                }
+                int64_t t = k < used ? starts[k] + static_cast<int64_t>((target - before) / work[static_cast<size_t>(k)])
+                                     : tiles;
+                xcd_first[x] = std::min(std::max(t, xcd_first[x - 1]), tiles);
+            }
+            longest = std::max(longest, xcd_first[x] - xcd_first[x - 1]);
+        }
+        group->grid = longest * kXcdRanges;
+    }
     group->count = used;
     group->tiles = tiles;
     group->a_kind = ak;
@@ -976,16 +1095,17 @@ int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStrea
     const int64_t* starts = reinterpret_cast<const int64_t*>(
         static_cast<const char*>(device_table) + round_up(sizeof(GemmParams) * static_cast<size_t>(group.capacity), 8));
     const GemmParams none{};
-    const dim3 grid(static_cast<unsigned>(group.tiles));
+    const dim3 grid(static_cast<unsigned>(group.grid));
+    DLLM_REQUIRE(group.grid < (int64_t{1} << 31), "matmul group too large for one launch");
     if (group.a_kind == kAFloatT)
         hipLaunchKernelGGL((gemm_mfma_kernel<kPlain, kAFloatT, true>), grid, dim3(256), 0, stream, none, group.tiles,
-                           int64_t{0}, int64_t{1}, ps, starts, group.count);
+                           int64_t{group.capacity}, int64_t{1}, ps, starts, group.count);
     else if (group.segmented)
         hipLaunchKernelGGL((gemm_mfma_kernel<kWindowsInSequence, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
-                           group.tiles, int64_t{0}, int64_t{1}, ps, starts, group.count);
+                           group.tiles, int64_t{group.capacity}, int64_t{1}, ps, starts, group.count);
     else
         hipLaunchKernelGGL((gemm_mfma_kernel<kPlain, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
-                           group.tiles, int64_t{0}, int64_t{1}, ps, starts, group.count);
+                           group.tiles, int64_t{group.capacity}, int64_t{1}, ps, starts, group.count);
     return check_launch("gemm group");
 }
 
