@@ -170,28 +170,81 @@ __global__ __launch_bounds__(256) void moe_dweights_kernel(const float* __restri
 }
 
 // One workgroup per window w: rows = (seg[w + 1] - seg[w]) * layers; probs of layer l at probs + l * layer_stride.
+// Each expert's mean is one serial chain over (layer, row) ascending; the rows reach the chains through LDS in
+// chunks of kStatRows (x E floats) that the whole workgroup loads ahead, so the chains wait on LDS, not on HBM.
+constexpr int kStatFloats = 8192;  // floats per LDS chunk
+
 __global__ __launch_bounds__(256) void router_stats_kernel(const float* __restrict__ probs, int64_t layer_stride,
                                                            int64_t layers, const int64_t* __restrict__ seg,
                                                            const int64_t* __restrict__ counts, int64_t E,
                                                            double router_scale, double* __restrict__ loss,
                                                            float* __restrict__ grad_row) {
-    extern __shared__ float frac_mean[];  // [E] fractions, [E] means
+    __shared__ float chunk[2][kStatFloats];
+    __shared__ float frac_mean[2 * 8192];  // [E] fractions, [E] means
     const int64_t w = blockIdx.x;
     const int64_t r0 = seg[w], n = seg[w + 1] - r0;
     const int64_t rows = n * layers;
     const int64_t* cnt = counts + w * E;
-    for (int64_t e = threadIdx.x; e < E; e += 256) {
-        double total = 0.0;
-        for (int64_t l = 0; l < layers; ++l)
-            for (int64_t r = r0; r < r0 + n; ++r) total += static_cast<double>(probs[l * layer_stride + r * E + e]);
-        frac_mean[E + e] = rows > 0 ? static_cast<float>(total / static_cast<double>(rows)) : 0.0f;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int64_t per = E <= kStatFloats ? kStatFloats / E : 1;  // rows per chunk
+    // an expert's chain lives in thread e % 256 (experts e, e + 256, ...); 32 chains per thread at most
+    double total[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) total[k] = 0.0;
+    const int64_t chunks = (rows + per - 1) / per;
+    // element f of chunk c: row q = c per + f / E (layer q / n, row q % n of the window), expert f % E
+    const uint32_t E32 = static_cast<uint32_t>(E), n32 = static_cast<uint32_t>(n > 0 ? n : 1);
+    auto load = [&](int64_t c, float (&reg)[kStatFloats / 256]) {
+#pragma unroll
+        for (int k = 0; k < kStatFloats / 256; ++k) {
+            const uint32_t f = static_cast<uint32_t>(k * 256 + tid);
+            const uint32_t fr = f / E32;
+            const int64_t q = c * per + fr;
+            const uint32_t l = static_cast<uint32_t>(q) / n32;
+            reg[k] = (fr < per && q < rows)
+                         ? probs[l * layer_stride + (r0 + (static_cast<uint32_t>(q) - l * n32)) * E + (f - fr * E32)]
+                         : 0.0f;
+        }
+    };
+    float reg[kStatFloats / 256];
+    if (chunks > 0) {
+        load(0, reg);
+#pragma unroll
+        for (int k = 0; k < kStatFloats / 256; ++k) chunk[0][k * 256 + tid] = reg[k];
+    }
+    __syncthreads();
+    for (int64_t c = 0; c < chunks; ++c) {
+        if (c + 1 < chunks) load(c + 1, reg);  // in flight while the chains run
+        const float* cur = chunk[c & 1];
+        const int64_t in_chunk = rows - c * per < per ? rows - c * per : per;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const int64_t e = tid + 256 * k;
+            if (e >= E) break;
+            double t = total[k];
+            for (int64_t q = 0; q < in_chunk; ++q) t += static_cast<double>(cur[q * E + e]);
+            total[k] = t;
+        }
+        if (c + 1 < chunks) {
+#pragma unroll
+            for (int k = 0; k < kStatFloats / 256; ++k) chunk[(c + 1) & 1][k * 256 + tid] = reg[k];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const int64_t e = tid + 256 * k;
+        if (e >= E) break;
+        frac_mean[E + e] = rows > 0 ? static_cast<float>(total[k] / static_cast<double>(rows)) : 0.0f;
+    }
+    for (int64_t e = tid; e < E; e += 256) {
         frac_mean[e] = static_cast<float>(static_cast<double>(cnt[e]) / static_cast<double>(rows));
         if (grad_row)
             grad_row[w * E + e] = static_cast<float>(router_scale * static_cast<double>(E) *
                                                      static_cast<double>(cnt[e]) / static_cast<double>(rows * rows));
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         double acc = 0.0;
         for (int64_t e = 0; e < E; ++e)
             acc += static_cast<double>(frac_mean[e]) * static_cast<double>(frac_mean[E + e]);
@@ -281,9 +334,8 @@ int launch_router_stats(const float* probs, int64_t layer_stride, int64_t layers
                         hipStream_t stream) {
     DLLM_REQUIRE(experts <= 8192, "too many experts for the router statistics");
     if (nseg == 0) return kOk;
-    hipLaunchKernelGGL(router_stats_kernel, dim3(static_cast<unsigned>(nseg)), dim3(256),
-                       2 * experts * sizeof(float), stream, probs, layer_stride, layers, seg, counts, experts,
-                       router_scale, loss, grad_row);
+    hipLaunchKernelGGL(router_stats_kernel, dim3(static_cast<unsigned>(nseg)), dim3(256), 0, stream, probs,
+                       layer_stride, layers, seg, counts, experts, router_scale, loss, grad_row);
     return check_launch("router_stats");
 }
 

@@ -92,16 +92,91 @@ __device__ __forceinline__ Fn shfl_down_fn(const Fn& f, int off) {
               __shfl_down(f.p1, off, 64)};
 }
 
+__device__ __forceinline__ long long readlane64(long long v, int k) {
+    const int lo = __builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffLL), k);
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), k);
+    return (static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo);
+}
+
 __device__ __forceinline__ double sq(float x) { return static_cast<double>(x) * static_cast<double>(x); }
 
 __device__ __forceinline__ double infinity() { return __longlong_as_double(0x7ff0000000000000LL); }
 
+// The function of elements x[i0, i0 + n) (n <= 32) in order at ulp 1 / inv_u; false if one of them is outside the
+// integer form.
+__device__ __forceinline__ bool run_fn(const float* __restrict__ x, int64_t i0, int n, double inv_u, Fn* f) {
+    Fn r = identity_fn();
+    bool ok = true;
+    if (n == 32 && reinterpret_cast<uintptr_t>(x + i0) % 16 == 0) {
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 q4 = reinterpret_cast<const float4*>(x + i0)[k];
+            v[4 * k] = q4.x;
+            v[4 * k + 1] = q4.y;
+            v[4 * k + 2] = q4.z;
+            v[4 * k + 3] = q4.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            Fn g;
+            long long q;
+            ok = ok && element_fn(sq(v[k]), inv_u, &g, &q);
+            r = compose(r, g);
+        }
+    } else {
+        for (int k = 0; k < n; ++k) {
+            Fn g;
+            long long q;
+            ok = ok && element_fn(sq(x[i0 + k]), inv_u, &g, &q);
+            r = compose(r, g);
+        }
+    }
+    *f = r;
+    return ok;
+}
+
 // The exact serial chain over x[begin, end) from state s, with the 64 lanes of one wave (all lanes call it with the
 // same arguments; all return the same s).
+//
+// Coarse steps first: 2048 elements at once, 32 consecutive per lane composed in order, then scanned in lane order.
+// The state only grows, so a lane's run is covered when the state after it is at most 2^53 - 1 (each M_j + Q_j is
+// at most the next M). The lanes before the first uncovered run are applied at once; that run goes to the fine steps
+// below (64 elements at a time, up to the element that needs a real add), then the coarse steps resume.
 __device__ double walk(const float* __restrict__ x, int64_t begin, int64_t end, double s) {
     const int lane = static_cast<int>(threadIdx.x) & 63;
     int64_t i = begin;
+    int64_t fine_until = begin;  // the fine steps take [i, fine_until): a coarse run failed there
     while (i < end) {
+        if (i >= fine_until && end - i >= 2048 && s == s && s > 0.0 && s < infinity()) {
+            const int e = binade(s);
+            const double inv_u = pow2(52 - e);
+            const long long M = static_cast<long long>(s * inv_u);
+            const int p = static_cast<int>(M & 1);
+            Fn f;
+            const bool ok = run_fn(x, i + 32 * lane, 32, inv_u, &f);
+            // inclusive scan in lane order: lane k's state after its run
+            Fn inc = f;
+            for (int off = 1; off < 64; off <<= 1) {
+                const Fn g = shfl_up_fn(inc, off);
+                if (lane >= off) inc = compose(g, inc);
+            }
+            const long long after = M + (p ? inc.d1 : inc.d0);
+            // the first lane whose run is not covered (a value outside the integer form, or the state past the
+            // binade); the lanes before it are applied at once
+            const unsigned long long bad = __ballot(!ok || after > kTop);
+            if (bad == 0) {
+                s = static_cast<double>(readlane64(after, 63)) * pow2(e - 52);
+                i += 2048;
+                continue;
+            }
+            const int k = __ffsll(static_cast<long long>(bad)) - 1;
+            if (k > 0) {
+                s = static_cast<double>(readlane64(after, k - 1)) * pow2(e - 52);
+                i += 32 * k;
+            }
+            fine_until = i + 32;  // the fine steps take the run that is not covered
+        }
         const int64_t idx = i + lane;
         const double a = idx < end ? sq(x[idx]) : 0.0;
         if (s != s) return s;  // NaN absorbs everything
@@ -113,7 +188,17 @@ __device__ double walk(const float* __restrict__ x, int64_t begin, int64_t end, 
             continue;
         }
         if (s == 0.0) {
-            // leading zeros keep s = +0; the first non-zero element becomes s exactly
+            // leading zeros keep s = +0; the first non-zero element becomes s exactly. Runs of 2048 zeros at a time
+            // first (a square is zero only for +-0: the smallest float squared is a normal double)
+            if (end - i >= 2048 + 64) {
+                bool zero = true;
+                const float* r = x + i + 64 + 32 * lane;
+                for (int k = 0; k < 32; ++k) zero = zero && r[k] == 0.0f;
+                if (__ballot(!zero) == 0 && __ballot(a != 0.0) == 0) {
+                    i += 2048 + 64;
+                    continue;
+                }
+            }
             const unsigned long long nz = __ballot(a != 0.0);
             if (nz == 0) {
                 i += 64;
@@ -154,6 +239,7 @@ __device__ double walk(const float* __restrict__ x, int64_t begin, int64_t end, 
         s = static_cast<double>(M + (p ? before.d1 : before.d0)) * u;
         s = s + __shfl(a, k, 64);  // the reference's own add for the element the integer form does not cover
         i += k + 1;
+        fine_until = i;  // past the element that needed a real add: coarse steps again
     }
     return s;
 }
@@ -282,11 +368,6 @@ __global__ __launch_bounds__(256) void block_fn_kernel(const float* __restrict__
 // takes block k's fields from lane k. While consecutive regular blocks share a binade e the state stays the integer
 // M (s = M 2^(e-52), M in [2^52, 2^53)): after an application M + tot <= 2^53 - 1 and tot >= 0, so s stays in
 // binade e and the next block's M = s 2^(52-e) is that same integer. s is formed only when the walk leaves that path.
-__device__ __forceinline__ long long readlane64(long long v, int k) {
-    const int lo = __builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffLL), k);
-    const int hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), k);
-    return (static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo);
-}
 
 __global__ __launch_bounds__(64) void tensor_walk_kernel(const float* __restrict__ arena,
                                                          const int64_t* __restrict__ tfirst,
@@ -294,6 +375,7 @@ __global__ __launch_bounds__(64) void tensor_walk_kernel(const float* __restrict
                                                          const int64_t* __restrict__ bstart,
                                                          const int64_t* __restrict__ bcount,
                                                          const BlockRec* __restrict__ rec,
+                                                         const double* __restrict__ bsum,
                                                          double* __restrict__ per_tensor) {
     const int64_t t = blockIdx.x;
     const int lane = static_cast<int>(threadIdx.x);
@@ -345,6 +427,7 @@ __global__ __launch_bounds__(64) void tensor_walk_kernel(const float* __restrict
                 }
             }
             const int64_t b = bc + k;
+            if (s == 0.0 && bsum[b] == 0.0) continue;  // a block of zeros keeps s = +0 (its squares are exact)
             s = walk(arena, bstart[b], bstart[b] + bcount[b], s);
         }
     }
@@ -396,7 +479,7 @@ int launch_exact_sum_squares(const float* arena, const ExactSumPlan& plan, void*
                        rec);
     DLLM_TRY(check_launch("sum_squares pass B"));
     hipLaunchKernelGGL(tensor_walk_kernel, dim3(nt), dim3(64), 0, stream, arena, plan.tfirst, plan.tblocks,
-                       plan.bstart, plan.bcount, rec, per_tensor);
+                       plan.bstart, plan.bcount, rec, bsum, per_tensor);
     return check_launch("sum_squares pass C");
 }
 

@@ -199,6 +199,20 @@ def sum_squares_cases():
     nan_case[17000] = np.nan
     cases["nan"] = nan_case
     cases["one"] = np.array([3.0], np.float32)
+    # sizes where most blocks are regular and the irregular ones take the 2048-element runs of the walk
+    cases["gaussian_2M"] = O.gaussian(42, 2_000_003)
+    rows = np.zeros((3000, 1024), np.float32)
+    picked = np.unique((O.gaussian(43, 400) * 700 + 1500).astype(np.int64) % 3000)
+    rows[picked] = O.gaussian(44, picked.size, 1024)
+    cases["sparse_rows"] = rows.ravel()
+    long_ties = np.tile(odd, 40)
+    long_ties[0] = np.float32(1.5)
+    cases["ties_long"] = long_ties
+    late = np.zeros(1_500_000 + 40_000, np.float32)
+    late[1_500_003:] = O.gaussian(45, 40_000 - 3)
+    late[1_500_001] = np.float32(-0.0)
+    cases["zeros_then_gaussian"] = late
+    cases["all_zero_big"] = np.zeros(300_001, np.float32)
     return cases
 
 
