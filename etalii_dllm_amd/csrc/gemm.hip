@@ -1143,7 +1143,8 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
             p.partial = g.seg_partial;
             gz = g.nseg;
         }
-        // matrix-core tiles: 128 x 128, or 64 x 64 / 32 x 32 when the larger tiles' grid leaves CUs idle
+        // matrix-core tiles: 128 x 128, or 64 x 64 / 32 x 32 when the larger tiles' grid leaves CUs idle (128 x 192
+        // tiles, which fit a [rows x 1536] output in one round of the 512 workgroup slots, measured slower)
         int tile = 4;
         if (mfma) {
             while (tile > 1 && gx * gy * gz < kSmallTilesBelow) {

@@ -40,7 +40,9 @@ def assert_same(a, b, what=""):
         raise AssertionError(f"{what}: {len(diff)} of {a.size} elements differ, first at {diff[:5]}")
 
 
-@pytest.mark.parametrize(("rows", "inf", "outf"), [(1, 37, 19), (7, 64, 259), (64, 128, 256), (130, 96, 64)])
+# (8192, 64, 1536): a forward of 768 tiles of 128 x 128 (more than one round of the 512 workgroup slots)
+@pytest.mark.parametrize(("rows", "inf", "outf"),
+                         [(1, 37, 19), (7, 64, 259), (64, 128, 256), (130, 96, 64), (8192, 64, 1536)])
 @pytest.mark.parametrize("kind", ["gaussian", "adversarial"])
 def test_linear_forward_and_backward(K, ora, rows, inf, outf, kind):
     make = adversarial if kind == "adversarial" else O.gaussian
