@@ -25,7 +25,7 @@ __global__ void self_seg_kernel(int64_t* seg, int64_t n) {
 
 struct SelfLayout {
     int64_t n = 0, Tp = 0, nh = 0, nkv = 0, hd = 0, G = 1;
-    size_t seg = 0, qt = 0, et = 0, inv = 0, forward = 0;
+    size_t seg = 0, qt = 0, et = 0, inv = 0, tmax = 0, forward = 0;
     size_t dot = 0, dpt = 0, dvec = 0, pg = 0, dsg = 0, backward = 0;
 };
 
@@ -48,6 +48,7 @@ SelfLayout self_layout(size_t n, size_t nh, size_t nkv, size_t hd) {
     L.qt = take(nh * hd * Tp * sizeof(float));
     L.et = take(sq);
     L.inv = take(nh * Tp * sizeof(double));
+    L.tmax = take(nh * (Tp / 64) * Tp * sizeof(double));
     L.forward = off;
     L.dot = take(nh * hd * Tp * sizeof(float));
     L.dpt = take(sq);
@@ -103,9 +104,12 @@ int self_probabilities(const float* q, const float* k, const SelfLayout& L, doub
     g.exact_products = true;
     g.out_double = true;
     g.out_scale = scale;
+    g.tile_max = at<double>(ws, L.tmax);
+    g.tile_max_zstride = (L.Tp / 64) * L.Tp;
+    g.tile_max_ld = L.Tp;
     DLLM_TRY(launch_attn_tiles(g, s));
     return launch_softmax_rows(et, L.Tp, L.Tp * L.Tp, seg, 1, L.nh, L.n, chain_window(causal, window),
-                               at<double>(ws, L.inv), L.Tp, s);
+                               at<double>(ws, L.inv), L.Tp, s, g.tile_max, g.tile_max_zstride, g.tile_max_ld);
 }
 
 // C[t] = sum over the keys t sees of A[j][t] B[j] (multiply, then add), into [n][heads][hd] rows.

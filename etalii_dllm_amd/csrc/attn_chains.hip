@@ -4,10 +4,13 @@
 // Layout: scores are kept transposed, S^T[j][t] (key j, query t) per (window, head), so the columns a query owns are
 // contiguous across queries: the chains run one lane per query over keys ascending, with coalesced loads.
 //
-//   forward   E^T = exp(S^T - max_t), total_t serial, inv_t = 1 / total_t       (one kernel)
+//   forward   E^T = exp(S^T - max_t), total_t serial, inv_t = 1 / total_t       (one kernel; max_t from the score
+//             tiles' maxima when the scores kernel provides them, else a first walk)
 //   backward  D_t = sum over keys ascending of (e inv_t) dp (serial); p = e inv_t, dS = p (dp - D_t) scale
 //             elementwise, dS written over dP^T and p, dS in the key-row layout dk / dv read (two kernels: a fused
-//             one, a wave per 64 queries, measured slower, its LDS tiles limiting it to one wave per SIMD)
+//             one, a wave per 64 queries, measured slower, its LDS tiles limiting it to one wave per SIMD; so was
+//             writing p and dS in place only, with dk / dv gathering key rows from the query-major storage: its
+//             tiles took 182 against 156 ms per step at T = 2048 for 16 ms less here)
 // Each chain visits exactly the keys the reference visits, in its order.
 #include "attn_step.h"
 #include "common.h"
@@ -67,6 +70,54 @@ __global__ __launch_bounds__(64) void softmax_fused_kernel(double* __restrict__ 
     }
     double total = 0.0;
     j = lo;
+    for (; j + kChainUnroll <= hi; j += kChainUnroll) {
+        double v[kChainUnroll];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) v[k] = s[(j + k) * ld];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) {
+            const double e = dexp(v[k] - mx);
+            s[(j + k) * ld] = e;
+            total += e;
+        }
+    }
+    for (; j < hi; ++j) {
+        const double e = dexp(s[j * ld] - mx);
+        s[j * ld] = e;
+        total += e;
+    }
+    inv[z * inv_zstride + t] = 1.0 / total;
+}
+
+// The forward softmax with the maximum from the score tiles' maxima (attn_mfma_kernel): the value of the reference's
+// first maximum is the first score when that is NaN, else the largest non-NaN score (a strictly greater one replaces
+// it), which the tile maxima give in any order; e = exp(s - mx) is the same for mx = +0 and -0. Then one walk: e over
+// S^T and total_t = the serial sum of the e in key order; inv_t = 1 / total_t.
+__global__ __launch_bounds__(64) void softmax_tiles_kernel(double* __restrict__ st, int64_t ld, int64_t zstride,
+                                                           const int64_t* __restrict__ seg, int64_t heads,
+                                                           int64_t window, double* __restrict__ inv,
+                                                           int64_t inv_zstride, const double* __restrict__ tile_max,
+                                                           int64_t tm_zstride, int64_t tm_ld) {
+    const int64_t z = blockIdx.y;
+    const int64_t w = z / heads;
+    const int64_t n = seg[w + 1] - seg[w];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (t >= n) return;
+    double* s = st + z * zstride + t;
+    int64_t lo, hi;
+    query_span(t, n, window, &lo, &hi);
+    const double first = s[lo * ld];
+    double mx = first;
+    if (first == first) {
+        const double* tm = tile_max + z * tm_zstride + t;
+        mx = -__builtin_huge_val();
+        for (int64_t k = lo / 64; k <= (hi - 1) / 64; ++k) {
+            const double m = tm[k * tm_ld];
+            if (m > mx) mx = m;
+        }
+    }
+    double total = 0.0;
+    int64_t j = lo;
     for (; j + kChainUnroll <= hi; j += kChainUnroll) {
         double v[kChainUnroll];
 #pragma unroll
@@ -214,11 +265,16 @@ __global__ __launch_bounds__(256) void heads_transpose_kernel(const float* __res
 }  // namespace
 
 int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
-                        int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream) {
+                        int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream,
+                        const double* tile_max, int64_t tile_max_zstride, int64_t tile_max_ld) {
     if (max_len == 0 || windows * heads == 0) return kOk;
     const dim3 lanes(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(windows * heads));
-    hipLaunchKernelGGL(softmax_fused_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
-                       inv_zstride);
+    if (tile_max)
+        hipLaunchKernelGGL(softmax_tiles_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
+                           inv_zstride, tile_max, tile_max_zstride, tile_max_ld);
+    else
+        hipLaunchKernelGGL(softmax_fused_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
+                           inv_zstride);
     return check_launch("attention softmax");
 }
 

@@ -59,6 +59,8 @@ struct TileParams {
     const double* rowscale;    // float outputs: value * rowscale[z][i] before rounding; may be null
     int64_t rowscale_zstride;
     double out_scale;          // double outputs: value * out_scale
+    double* tile_max;          // scores: per 64-key tile and query, the largest visible score (may be null)
+    int64_t tile_max_zstride, tile_max_ld;
     const int64_t* seg;
     int64_t heads, Z;          // z = w * heads + hz in [0, Z)
     int rows_kind, cols_kind;  // 0: window positions, 1: head_dim
@@ -583,6 +585,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const auto c_out = global_ptr(c_base);
     const double* rs = p.rowscale ? p.rowscale + zz * p.rowscale_zstride : nullptr;
     const int64_t jw = j0 + wave * 64 + (lane & 15);
+    if constexpr (kOutDouble) {
+        // the largest score of this 64-key tile each query sees (visible keys only; NaN scores skipped, -inf when
+        // none): the softmax takes its maximum from these instead of a walk over the scores
+        if (p.tile_max) {
+            const auto tm = global_ptr(p.tile_max + zz * p.tile_max_zstride + (i0 / 64) * p.tile_max_ld);
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) {
+                const int64_t t = jw + 16 * bj;
+                double m = -__builtin_huge_val();
+#pragma unroll
+                for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t i = i0 + 16 * bi + (lane >> 4) + 4 * r;
+                        const bool seen = i < I && t < J &&
+                                          (p.mask != kMaskTileCausal || (i <= t && (p.window == 0 || t - i < p.window)));
+                        const double v = acc[bi][bj][r] * p.out_scale;
+                        if (seen && v > m) m = v;
+                    }
+                const double m16 = __shfl_xor(m, 16, 64);
+                m = m16 > m ? m16 : m;
+                const double m32 = __shfl_xor(m, 32, 64);
+                m = m32 > m ? m32 : m;
+                if ((lane >> 4) == 0 && t < J) tm[t] = m;
+            }
+        }
+    }
 #pragma unroll
     for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
@@ -620,6 +649,13 @@ int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream) {
     p.rowscale = c.rowscale;
     p.rowscale_zstride = c.rowscale_zstride;
     p.out_scale = c.out_scale;
+    p.tile_max = c.tile_max;
+    p.tile_max_zstride = c.tile_max_zstride;
+    p.tile_max_ld = c.tile_max_ld;
+    if (c.tile_max)
+        DLLM_REQUIRE(c.a_float && c.out_double && (c.mask == kMaskTileCausal || c.mask == kMaskNone) &&
+                         c.rows_kind == 0 && c.cols_kind == 0,
+                     "tile maxima are for the scores (keys x queries)");
     p.seg = c.seg;
     p.heads = c.heads;
     p.Z = c.windows * c.heads;

@@ -47,11 +47,18 @@ struct AttnTileCall {
     bool exact_products = true;  // float x float products: fused multiply-add is exact
     bool out_double = false;
     double out_scale = 1.0;
+    // scores only: tile_max[z * tile_max_zstride + (key / 64) * tile_max_ld + query] = the largest score of that
+    // 64-key tile the query sees (visible keys; NaN skipped; -inf when none)
+    double* tile_max = nullptr;
+    int64_t tile_max_zstride = 0, tile_max_ld = 0;
 };
 
 int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream);
+// The forward softmax chains over S^T in place (E^T and inv). With tile maxima (the scores' tile_max, same z and ld
+// layout as there) the maximum comes from them and the scores are walked once; without, twice.
 int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
-                        int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream);
+                        int64_t max_len, int64_t window, double* inv, int64_t inv_zstride, hipStream_t stream,
+                        const double* tile_max = nullptr, int64_t tile_max_zstride = 0, int64_t tile_max_ld = 0);
 // The softmax backward (grad.hpp:262-278): D per query (dvec: windows * heads * inv_zstride doubles of workspace),
 // then ds written over dpt and p, ds in the key-row layout of dk / dv:
 // pg / dsg[w][g][(t * group + hh)][j] (dst_ld per row, dst_zstride per (window, kv head)).

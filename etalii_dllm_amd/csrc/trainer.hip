@@ -260,6 +260,7 @@ struct dllm_hip_trainer {
     int64_t Tp = 0;
     double* attn_dvec = nullptr;  // the softmax backward's per-query D
     double *attn_et = nullptr, *attn_inv = nullptr, *attn_dpt = nullptr, *attn_pg = nullptr, *attn_dsg = nullptr;
+    double* attn_tmax = nullptr;  // the scores' per-64-key-tile maxima of each query [z][Tp / 64][Tp]
     float *attn_qt = nullptr, *attn_dot = nullptr;
 
     template <typename T>
@@ -530,6 +531,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&attn_pg, W_max * kvh * Tp * G * Tp));
         DLLM_TRY(make(&attn_dsg, W_max * kvh * Tp * G * Tp));
         DLLM_TRY(make(&attn_dvec, W_max * heads * Tp));
+        DLLM_TRY(make(&attn_tmax, W_max * heads * (Tp / 64) * Tp));
         DLLM_TRY(make(&tok_in, R));
         DLLM_TRY(make(&tok_tgt, R));
         DLLM_TRY(make(&pos_index, R));
@@ -890,10 +892,15 @@ struct dllm_hip_trainer {
         g.exact_products = true;
         g.out_double = true;
         g.out_scale = c.attention_scale;
+        g.tile_max = attn_tmax;
+        g.tile_max_zstride = (Tp / 64) * Tp;
+        g.tile_max_ld = Tp;
         DLLM_TRY(launch_attn_tiles(g, s));
-        DLLM_TRY(launch_softmax_rows(et, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp, s));
+        DLLM_TRY(launch_softmax_rows(et, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp, s,
+                                     attn_tmax, (Tp / 64) * Tp, Tp));
         // out[t] = f32((sum_j e_j v_j) inv_t)
         AttnTileCall o = g;
+        o.tile_max = nullptr;
         o.A = AttnOperand{et, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
         o.a_float = false;
         o.B = AttnOperand{sv.v, 0, KVD, hd, G, KVD, 0, 1};
