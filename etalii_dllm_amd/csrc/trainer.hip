@@ -1726,7 +1726,6 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     DLLM_REQUIRE(c.vocab % 4 == 0 && c.hidden % 4 == 0 && c.intermediate % 4 == 0,
                  "vocabulary, hidden and intermediate sizes must be multiples of 4 (16-byte matmul operand chunks)");
     DLLM_REQUIRE(max_tokens > 0 && max_windows > 0 && max_window_tokens > 0, "capacities must be positive");
-    DLLM_REQUIRE(max_window_tokens <= 2048, "windows longer than 2048 tokens are not supported");
     DLLM_REQUIRE(max_tokens <= 65535, "at most 65535 tokens per step");
     std::unique_ptr<dllm_hip_trainer> t(new dllm_hip_trainer());
     t->c = c;

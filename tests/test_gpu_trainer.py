@@ -345,6 +345,31 @@ def test_attention_at_head_dim_128_matches_the_oracle(window):
         assert t.get(name, d.tensor_shapes()[name], t.GRAD).tobytes() == want[name].tobytes(), name
 
 
+@pytest.mark.parametrize("window", [0, 1000])
+def test_windows_past_2048_tokens_match_the_oracle(window):
+    """Windows of 2600 and 300 tokens (the step has no window-length cap; the reference has none): scores, softmax
+    chains and the multiply-add tiles past 2048 keys per query, causal and with a sliding window, every gradient of
+    one gradients() call against the oracle."""
+    d = O.Decoder("mistral", vocab=128, hidden=64, inter=64, layers=1, heads=2, kv_heads=1, head_dim=32, eps=1e-5,
+                  rope_theta=1e4, tied=False, window=window)
+    weights = O.synthetic_weights(d, seed=41, scale=0.05)
+    rng = O.Random(43)
+    windows = [[rng.next_u64() % d.vocab for _ in range(n)] for n in (2601, 301)]
+    t = make_trainer(d, weights, max_tokens=2900, max_windows=2, max_window=2600)
+    scale = 1.0 / sum(len(w) - 1 for w in windows)
+    loss = t.gradients(windows, scale=scale)
+    kern = O.oracle_kernels()
+    want_loss, want = 0.0, {}
+    for w in windows:
+        l, _, g = O.window_gradients(kern, d, weights, w[:-1], w[1:], scale=scale)
+        want_loss += l
+        for name, value in g.items():
+            want[name] = want[name] + value if name in want else value.copy()
+    assert loss == want_loss
+    for name in t.names:
+        assert t.get(name, d.tensor_shapes()[name], t.GRAD).tobytes() == want[name].tobytes(), name
+
+
 DPO_RECORDS = [("the quick brown", " fox", " cat"), ("pack my box", " with jugs", " of"),
                ("two plus two is", " four", " five and a lot more words"), ("hello", " there", " go away"),
                ("the lazy", " dog", " frog")]
