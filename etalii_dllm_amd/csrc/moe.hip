@@ -75,6 +75,131 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
             weights[r * K + j] = static_cast<float>(static_cast<double>(weights[r * K + j]) / total);
 }
 
+// Rows of at most 256 experts run one wave per row (expert e = lane + 64 m on lane `lane`), the row's probabilities
+// in registers. moe_route_wave_kernel: rank j takes the first untaken expert when its p is NaN (nothing is greater
+// than NaN), else the largest untaken non-NaN p, the lower expert on ties: the reference's scan in which only a
+// strictly greater p replaces the best.
+constexpr int kRouteLanesPer = 4;
+
+__device__ __forceinline__ double readlane_f64(double v, int k) {
+    const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), k));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), k));
+    return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// The row's probabilities in a wave, pv[m] for expert lane + 64 m (row_softmax and row_prob restated: the maximum's
+// value is the first logit when that is NaN, else the largest non-NaN one; the total is the serial sum over e
+// ascending, read lane by lane).
+__device__ __forceinline__ void wave_row_probs(const float* __restrict__ l, int64_t E, int lane,
+                                               float (&pv)[kRouteLanesPer]) {
+    float lv[kRouteLanesPer];
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m) {
+        const int64_t e = lane + 64 * m;
+        lv[m] = e < E ? l[e] : 0.0f;
+    }
+    const float first = __shfl(lv[0], 0, 64);
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m)
+        if (lane + 64 * m < E && lv[m] > mx) mx = lv[m];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float o = __shfl_xor(mx, off, 64);
+        mx = o > mx ? o : mx;
+    }
+    if (first != first) mx = first;
+    const double dmax = static_cast<double>(mx);
+    double ev[kRouteLanesPer];
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m)
+        ev[m] = lane + 64 * m < E ? dexp(static_cast<double>(lv[m]) - dmax) : 0.0;
+    double total = 0.0;
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m) {
+        if (64 * m >= E) break;
+        const int n = E - 64 * m < 64 ? static_cast<int>(E - 64 * m) : 64;
+        for (int k = 0; k < n; ++k) total += readlane_f64(ev[m], k);
+    }
+    const double inv = 1.0 / total;
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m) pv[m] = static_cast<float>(ev[m] * inv);
+}
+
+// the probability of expert e (uniform across the wave)
+__device__ __forceinline__ float wave_prob(const float (&pv)[kRouteLanesPer], int64_t e) {
+    const int l = static_cast<int>(e & 63), mm = static_cast<int>(e >> 6);
+    float p = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m)
+        if (m == mm) p = __shfl(pv[m], l, 64);
+    return p;
+}
+
+__global__ __launch_bounds__(256) void moe_route_wave_kernel(const float* __restrict__ logits, int64_t rows,
+                                                             int64_t E, int64_t K, int normalize,
+                                                             int64_t* __restrict__ indices,
+                                                             float* __restrict__ weights, float* __restrict__ probs) {
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    float pv[kRouteLanesPer];
+    wave_row_probs(logits + r * E, E, lane, pv);
+    if (probs)
+#pragma unroll
+        for (int m = 0; m < kRouteLanesPer; ++m)
+            if (lane + 64 * m < E) probs[r * E + lane + 64 * m] = pv[m];
+    uint32_t taken = 0;  // bit m: expert lane + 64 m chosen
+    double wtotal = 0.0;
+    for (int64_t j = 0; j < K; ++j) {
+        // the first untaken expert
+        int64_t e0 = E;
+#pragma unroll
+        for (int m = kRouteLanesPer - 1; m >= 0; --m) {
+            const bool open = lane + 64 * m < E && !((taken >> m) & 1u);
+            const unsigned long long b = __ballot(open);
+            if (b) e0 = 64 * m + (__ffsll(static_cast<long long>(b)) - 1);
+        }
+        const float p0 = wave_prob(pv, e0);
+        int64_t best;
+        if (p0 != p0) {
+            best = e0;
+        } else {
+            float bv = -1.0f;  // below every probability (p >= +0)
+            int64_t bi = E;
+#pragma unroll
+            for (int m = 0; m < kRouteLanesPer; ++m) {
+                const int64_t e = lane + 64 * m;
+                if (e < E && !((taken >> m) & 1u) && pv[m] > bv) {
+                    bv = pv[m];
+                    bi = e;
+                }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int64_t oi = __shfl_xor(bi, off, 64);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            best = bi;
+        }
+        const float pb = wave_prob(pv, best);
+        if (lane == static_cast<int>(best & 63)) taken |= 1u << (best >> 6);
+        if (lane == 0) {
+            indices[r * K + j] = best;
+            weights[r * K + j] = pb;
+        }
+        wtotal += static_cast<double>(pb);
+    }
+    if (normalize && lane == 0)
+        for (int64_t j = 0; j < K; ++j)
+            weights[r * K + j] = static_cast<float>(static_cast<double>(weights[r * K + j]) / wtotal);
+}
+
 __global__ __launch_bounds__(256) void moe_route_backward_kernel(const float* __restrict__ logits,
                                                                  const int64_t* __restrict__ indices,
                                                                  const float* __restrict__ dweights,
@@ -109,6 +234,57 @@ __global__ __launch_bounds__(256) void moe_route_backward_kernel(const float* __
         dlogits[r * E + e] = static_cast<float>(static_cast<double>(row_prob(l, s, e)) * (dp_of(e) - dot));
 }
 
+// moe_route_backward with one wave per row (E <= 256), the probabilities from wave_row_probs; the rank sums and
+// the dot over e run serially in the reference's order, the per-expert terms one lane each.
+__global__ __launch_bounds__(256) void moe_route_backward_wave_kernel(const float* __restrict__ logits,
+                                                                      const int64_t* __restrict__ indices,
+                                                                      const float* __restrict__ dweights,
+                                                                      const float* __restrict__ dprob, int64_t rows,
+                                                                      int64_t E, int64_t K, int normalize,
+                                                                      float* __restrict__ dlogits) {
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    float pv[kRouteLanesPer];
+    wave_row_probs(logits + r * E, E, lane, pv);
+    const int64_t* idx = indices + r * K;
+    const float* dw = dweights + r * K;
+    double total = 0.0, weighted = 0.0;
+    for (int64_t j = 0; j < K; ++j) {
+        const double p = static_cast<double>(wave_prob(pv, idx[j]));
+        total += p;
+        weighted += static_cast<double>(dw[j]) * p;
+    }
+    double dp[kRouteLanesPer], term[kRouteLanesPer];
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m) {
+        const int64_t e = lane + 64 * m;
+        dp[m] = dprob && e < E ? static_cast<double>(dprob[r * E + e]) : 0.0;
+    }
+    for (int64_t j = 0; j < K; ++j) {
+        const int64_t e = idx[j];
+        const double d = static_cast<double>(dw[j]);
+        const double add = normalize ? d / total - weighted / (total * total) : d;
+#pragma unroll
+        for (int m = 0; m < kRouteLanesPer; ++m)
+            if (lane + 64 * m == e) dp[m] += add;
+    }
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m) term[m] = static_cast<double>(pv[m]) * dp[m];
+    double dot = 0.0;
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m) {
+        if (64 * m >= E) break;
+        const int n = E - 64 * m < 64 ? static_cast<int>(E - 64 * m) : 64;
+        for (int k = 0; k < n; ++k) dot += readlane_f64(term[m], k);
+    }
+#pragma unroll
+    for (int m = 0; m < kRouteLanesPer; ++m) {
+        const int64_t e = lane + 64 * m;
+        if (e < E) dlogits[r * E + e] = static_cast<float>(static_cast<double>(pv[m]) * (dp[m] - dot));
+    }
+}
+
 // out[r][d] = (0 + sum over the row's choices in expert order of term) + addend[r][d]; term = y[p][d] * w (weights
 // given) or y[p][d]. order[r * K + i] is the grouped position p of the row's i-th choice by expert, slot[p] its
 // index into the routing weights.
@@ -131,40 +307,98 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     }
 }
 
+// The same sums, one workgroup per row and 4 columns per thread (H % 4 == 0, 16-byte aligned rows): the row's
+// choices are wave-uniform scalar loads, and the expert rows are read as 16-byte vectors.
+__global__ __launch_bounds__(256) void moe_combine4_kernel(const float4* __restrict__ y,
+                                                           const int64_t* __restrict__ order,
+                                                           const int64_t* __restrict__ slot,
+                                                           const float* __restrict__ weights,
+                                                           const float4* __restrict__ addend, float4* __restrict__ out,
+                                                           int64_t K, int64_t H4) {
+    const int64_t r = blockIdx.x;
+    for (int64_t d = threadIdx.x; d < H4; d += 256) {
+        float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int64_t k = 0; k < K; ++k) {
+            const int64_t p = order[r * K + k];
+            const float4 v = y[p * H4 + d];
+            if (weights) {
+                const float wk = weights[slot[p]];
+                acc.x = acc.x + v.x * wk;
+                acc.y = acc.y + v.y * wk;
+                acc.z = acc.z + v.z * wk;
+                acc.w = acc.w + v.w * wk;
+            } else {
+                acc.x = acc.x + v.x;
+                acc.y = acc.y + v.y;
+                acc.z = acc.z + v.z;
+                acc.w = acc.w + v.w;
+            }
+        }
+        const float4 a = addend[r * H4 + d];
+        out[r * H4 + d] = float4{acc.x + a.x, acc.y + a.y, acc.z + a.z, acc.w + a.w};
+    }
+}
+
 // Per grouped position p (row r = row_of[p], routing slot q = slot[p]):
 //   dweights[q] = f32(sum over d ascending of dout[r][d] y[p][d])   (dllm::dot, one lane per position)
 //   dy[p][d]    = dout[r][d] * weights[q]
 // A workgroup takes 64 positions; its four waves stage 64-column tiles of the products in LDS (writing dy on the
-// way), then wave 0 runs the 64 chains.
+// way), then wave 0 runs the 64 chains. The tiles are double-buffered and the next tile's loads are in flight while
+// wave 0 walks the current one: one barrier per tile.
 __global__ __launch_bounds__(256) void moe_dweights_kernel(const float* __restrict__ dout, const float* __restrict__ y,
                                                            const int64_t* __restrict__ row_of,
                                                            const int64_t* __restrict__ slot,
                                                            const float* __restrict__ weights, int64_t positions,
                                                            int64_t H, float* __restrict__ dweights,
                                                            float* __restrict__ dy) {
-    __shared__ double prod[64][65];
+    constexpr int kPer = 16;  // positions per wave
+    __shared__ double prod[2][64][65];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = static_cast<int>(threadIdx.x) >> 6;
     const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 64;
     const int64_t np = positions - p0 < 64 ? positions - p0 : 64;
+    // this wave's positions: rows of dout, their routing weights (positions past the end repeat the last one)
+    const float* grow[kPer];
+    const float* yrow[kPer];
+    float* dyrow[kPer];
+    float wq[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int q = wave * kPer + k;
+        const int64_t p = p0 + (q < np ? q : np - 1);
+        grow[k] = dout + row_of[p] * H;
+        yrow[k] = y + p * H;
+        dyrow[k] = dy + p * H;
+        wq[k] = weights[slot[p]];
+    }
+    float g[kPer], yv[kPer];
+    auto load = [&](int64_t c0) {
+        const int64_t c = c0 + lane < H ? c0 + lane : H - 1;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            g[k] = grow[k][c];
+            yv[k] = yrow[k][c];
+        }
+    };
+    load(0);
     double chain = 0.0;
-    for (int64_t c0 = 0; c0 < H; c0 += 64) {
+    int buf = 0;
+    for (int64_t c0 = 0; c0 < H; c0 += 64, buf ^= 1) {
         const int n = static_cast<int>(H - c0 < 64 ? H - c0 : 64);
         if (lane < n) {
-            for (int k = 0; k < 16; ++k) {
-                const int q = wave * 16 + k;
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int q = wave * kPer + k;
                 if (q < np) {
-                    const int64_t p = p0 + q;
-                    const float g = dout[row_of[p] * H + c0 + lane];
-                    prod[q][lane] = static_cast<double>(g) * static_cast<double>(y[p * H + c0 + lane]);
-                    dy[p * H + c0 + lane] = g * weights[slot[p]];
+                    prod[buf][q][lane] = static_cast<double>(g[k]) * static_cast<double>(yv[k]);
+                    dyrow[k][c0 + lane] = g[k] * wq[k];
                 }
             }
         }
         __syncthreads();
+        if (c0 + 64 < H) load(c0 + 64);
         if (wave == 0 && lane < np)
-            for (int c = 0; c < n; ++c) chain += prod[lane][c];
-        __syncthreads();
+            for (int c = 0; c < n; ++c) chain += prod[buf][lane][c];
     }
     if (wave == 0 && lane < np) dweights[slot[p0 + lane]] = static_cast<float>(chain);
 }
@@ -295,8 +529,12 @@ int launch_moe_route(const float* logits, int64_t rows, int64_t experts, int64_t
                      float* weights, float* probs, hipStream_t stream) {
     DLLM_REQUIRE(k >= 1 && k <= experts, "experts per token must be between 1 and the number of experts");
     if (rows == 0) return kOk;
-    hipLaunchKernelGGL(moe_route_kernel, dim3(row_grid(rows)), dim3(256), 0, stream, logits, rows, experts, k,
-                       normalize, indices, weights, probs);
+    if (experts <= 64 * kRouteLanesPer)
+        hipLaunchKernelGGL(moe_route_wave_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, stream,
+                           logits, rows, experts, k, normalize, indices, weights, probs);
+    else
+        hipLaunchKernelGGL(moe_route_kernel, dim3(row_grid(rows)), dim3(256), 0, stream, logits, rows, experts, k,
+                           normalize, indices, weights, probs);
     return check_launch("moe_route");
 }
 
@@ -305,8 +543,12 @@ int launch_moe_route_backward(const float* logits, const int64_t* indices, const
                               hipStream_t stream) {
     DLLM_REQUIRE(k >= 1 && k <= experts, "indices must be [rows, k] with k between 1 and the number of experts");
     if (rows == 0) return kOk;
-    hipLaunchKernelGGL(moe_route_backward_kernel, dim3(row_grid(rows)), dim3(256), 0, stream, logits, indices,
-                       dweights, dprob, rows, experts, k, normalize, dlogits);
+    if (experts <= 64 * kRouteLanesPer)
+        hipLaunchKernelGGL(moe_route_backward_wave_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
+                           0, stream, logits, indices, dweights, dprob, rows, experts, k, normalize, dlogits);
+    else
+        hipLaunchKernelGGL(moe_route_backward_kernel, dim3(row_grid(rows)), dim3(256), 0, stream, logits, indices,
+                           dweights, dprob, rows, experts, k, normalize, dlogits);
     return check_launch("moe_route_backward");
 }
 
@@ -314,6 +556,14 @@ int launch_moe_combine(const float* y, const int64_t* order, const int64_t* slot
                        const float* addend, float* out, int64_t rows, int64_t k, int64_t dim, hipStream_t stream) {
     const int64_t n = rows * dim;
     if (n == 0) return kOk;
+    const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(addend) |
+                                      reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    if (vec && rows < (int64_t{1} << 31)) {
+        hipLaunchKernelGGL(moe_combine4_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream,
+                           reinterpret_cast<const float4*>(y), order, slot, weights,
+                           reinterpret_cast<const float4*>(addend), reinterpret_cast<float4*>(out), k, dim / 4);
+        return check_launch("moe_combine");
+    }
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 256), 16384));
     hipLaunchKernelGGL(moe_combine_kernel, dim3(blocks), dim3(256), 0, stream, y, order, slot, weights, addend, out,
                        rows, k, dim);

@@ -245,7 +245,7 @@ def test_lora_merge_and_adapter_gradients(K, ora, out_f, in_f, rank):
         assert_same(got, want, name)
 
 
-@pytest.mark.parametrize("rows,experts,k", [(1, 4, 1), (37, 8, 2), (300, 64, 8), (5, 128, 4)])
+@pytest.mark.parametrize("rows,experts,k", [(1, 4, 1), (37, 8, 2), (300, 64, 8), (5, 128, 4), (9, 200, 6), (6, 300, 3)])
 @pytest.mark.parametrize("normalize", [False, True])
 def test_moe_route_and_backward(K, ora, rows, experts, k, normalize):
     """nn.hpp:864-896 and grad.hpp:507-541: Gaussian logits plus rows of exact ties (the lower expert wins) and a row
@@ -255,16 +255,20 @@ def test_moe_route_and_backward(K, ora, rows, experts, k, normalize):
         logits[1] = 0.5  # every probability equal
         logits[2, ::2] = logits[2, 1::2]  # pairs of equal probabilities
     logits[0, experts // 2] = 40.0
+    if rows > 5:
+        logits[3, 0] = np.nan  # NaN first logit: a NaN maximum, every probability NaN (the first experts win)
+        logits[4, experts - 1] = np.nan  # NaN last logit: a NaN total, every probability NaN
+        logits[5, : experts // 2] = -np.inf
     ia, wa = K.moe_route(logits, k, normalize)
     ib, wb = ora.moe_route(logits, k, normalize)
     assert ia.tobytes() == ib.tobytes()
-    assert_same(wa, wb, "weights")
+    assert_same_or_nan(wa, wb, "weights")
     dw = O.gaussian(rows + 3, rows, k)
     dp = O.gaussian(rows + 4, rows, experts, scale=1e-2)
-    assert_same(K.moe_route_backward(logits, ia, dw, dp, normalize),
-                ora.moe_route_backward(logits, ib, dw, dp, normalize), "dlogits")
-    assert_same(K.moe_route_backward(logits, ia, dw, None, normalize),
-                ora.moe_route_backward(logits, ib, dw, None, normalize), "dlogits without dprobabilities")
+    assert_same_or_nan(K.moe_route_backward(logits, ia, dw, dp, normalize),
+                       ora.moe_route_backward(logits, ib, dw, dp, normalize), "dlogits")
+    assert_same_or_nan(K.moe_route_backward(logits, ia, dw, None, normalize),
+                       ora.moe_route_backward(logits, ib, dw, None, normalize), "dlogits without dprobabilities")
 
 
 def test_moe_route_rejects_bad_k(K):
