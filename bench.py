@@ -4,8 +4,10 @@ state; random-init seeded Gaussians), one full step = forward + backward over ba
 next-token cross-entropy, global-norm clipping and AdamW, bit-identical to the reference CPU kernels.
 
 Prints one JSON line (the driver's contract): tokens/s of whole steps with inputs already resident in HBM, the
-roofline of the dominant kernel (the FP64-FMA matmul, timed live with HIP events on its stream during the timed
-steps) and the reference CPU path timed on this host's cores for a bounded sample of the same step.
+roofline of the dominant kernel (the FP64-FMA matmul, timed live with a pair of HIP events on its stream around
+every launch, over as many steps again run right after the timed ones: the events cost the small configs several
+percent of their step, so the throughput steps run without them) and the reference CPU path timed on this host's
+cores for a bounded sample of the same step.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c1] [--no-cpu-baseline]
 """
@@ -507,6 +509,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c2"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--roofline-steps", type=int, default=None,
+                    help="steps of the matmul-timing pass after the timed steps (default: --steps; 0 skips it)")
     ap.add_argument("--export-timing", action="store_true",
                     help="after the timed steps, time the model and checkpoint fingerprints streamed from device "
                          "memory (stderr only)")
@@ -556,20 +560,30 @@ def main() -> int:
     if lora is not None:
         init_adapters(trainer, lib, cfg)
     log(f"weights ready in {time.perf_counter() - t0:.1f} s")
-    windows = [make_windows(lib, cfg, s) for s in range(args.warmup + args.steps)]
+    roofline_steps = args.steps if args.roofline_steps is None else args.roofline_steps
+    total = args.warmup + args.steps + roofline_steps
+    windows = [make_windows(lib, cfg, s) for s in range(total)]
     for s in range(args.warmup):
         t1 = time.perf_counter()
         loss, norm = trainer.step(windows[s], LEARNING_RATE, s + 1, router_aux_loss=router_aux)
         log(f"warmup step {s + 1}: loss {loss:.6f} norm {norm:.6f} ({time.perf_counter() - t1:.2f} s)")
+    # the timed steps: the step alone, nothing recorded around its launches
     check(lib.dllm_hip_synchronize())
-    check(lib.dllm_hip_trainer_profile(trainer.handle, 1))
     t0 = time.perf_counter()
-    for s in range(args.steps):
-        loss, norm = trainer.step(windows[args.warmup + s], LEARNING_RATE, args.warmup + s + 1,
-                                  router_aux_loss=router_aux)
-        log(f"step {args.warmup + s + 1}: loss {loss:.6f} norm {norm:.6f}")
+    for s in range(args.warmup, args.warmup + args.steps):
+        loss, norm = trainer.step(windows[s], LEARNING_RATE, s + 1, router_aux_loss=router_aux)
+        log(f"step {s + 1}: loss {loss:.6f} norm {norm:.6f}")
     check(lib.dllm_hip_synchronize())
     elapsed = time.perf_counter() - t0
+    # the matmul-timing steps: the same step with a pair of HIP events around every matmul launch on its stream
+    # (the events add host and queue overhead to the step, so these steps are not the throughput figure)
+    check(lib.dllm_hip_trainer_profile(trainer.handle, 1))
+    t_roof = time.perf_counter()
+    for s in range(args.warmup + args.steps, total):
+        loss, norm = trainer.step(windows[s], LEARNING_RATE, s + 1, router_aux_loss=router_aux)
+        log(f"matmul-timing step {s + 1}: loss {loss:.6f} norm {norm:.6f}")
+    check(lib.dllm_hip_synchronize())
+    roof_elapsed = time.perf_counter() - t_roof
     launches, ms, flops = C.c_int64(), C.c_double(), C.c_double()
     check(lib.dllm_hip_trainer_profile_read(trainer.handle, C.byref(launches), C.byref(ms), C.byref(flops)))
     check(lib.dllm_hip_trainer_profile(trainer.handle, 0))
@@ -581,9 +595,11 @@ def main() -> int:
             log(f"{what} fingerprint {digest[:16]}...: {seconds:.2f} s")
     trainer.close()
     ms_per_step = elapsed * 1000.0 / args.steps
-    achieved = flops.value / (ms.value * 1e9) if ms.value > 0 else 0.0  # TFLOP/s
-    log(f"matmuls: {launches.value} launches, {ms.value:.1f} ms, {flops.value:.3e} flop "
-        f"({100.0 * ms.value / (elapsed * 1000.0):.1f}% of step time)")
+    achieved = flops.value / (ms.value * 1e9) if ms.value > 0 else None  # TFLOP/s
+    if roofline_steps:
+        log(f"matmuls: {launches.value} launches over {roofline_steps} steps, {ms.value:.1f} ms, {flops.value:.3e} "
+            f"flop ({100.0 * ms.value / (roof_elapsed * 1000.0):.1f}% of those steps' time, "
+            f"{roof_elapsed * 1000.0 / roofline_steps:.1f} ms per step with the events)")
     traffic = None
     traffic_file = ROOT / "profiles" / "gemm_traffic.json"
     if traffic_file.exists():
@@ -612,8 +628,9 @@ def main() -> int:
                    "global_batch": cfg["batch"], "seq_len": cfg["seq"], "parallelism": "single GPU",
                    "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"]},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic,
-                     "kernel": "gemm_mfma_kernel (FP64 MFMA matmul, all launches of the timed steps)",
+                     "frac": achieved / FP64_PEAK_TFLOPS if achieved else None, "traffic": traffic,
+                     "kernel": "gemm_mfma_kernel (FP64 MFMA matmul, every launch of the matmul-timing steps)",
+                     "timing_steps": roofline_steps,
                      "step_fraction_of_peak": matmul_flops_per_step(cfg) / (ms_per_step * 1e9) / FP64_PEAK_TFLOPS},
         "cpu_baseline": baseline,
     }

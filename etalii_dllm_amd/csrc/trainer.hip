@@ -190,7 +190,8 @@ struct dllm_hip_trainer {
     float *x_final = nullptr, *hidden = nullptr, *logits = nullptr, *dlogits = nullptr;
     float *dx = nullptr, *dh = nullptr, *dx_mid = nullptr, *dattended = nullptr, *dq_t = nullptr, *dk_t = nullptr,
           *dv_t = nullptr, *dq = nullptr, *dk = nullptr, *dq2 = nullptr, *dk2 = nullptr, *dproduct = nullptr,
-          *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *emb_rows = nullptr, *gemm_part = nullptr;
+          *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *col_part_side = nullptr, *emb_rows = nullptr,
+          *gemm_part = nullptr;
     int64_t gemm_part_cap = 0;  // floats: per-window partials of the layer weight gradients
     // routed experts: E experts, K per token, EI expert intermediate size; shared buffers of the grouped rows
     int64_t E = 0, K = 0, EI = 0, RK = 0;
@@ -507,6 +508,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&dgate, dmlp));
         DLLM_TRY(make(&dup, dmlp));
         DLLM_TRY(make(&col_part, W_max * std::max<int64_t>({H, QD, KVD, I})));
+        DLLM_TRY(make(&col_part_side, W_max * std::max<int64_t>({QD, KVD})));
         if (W_max > 1) {
             gemm_part_cap = W_max * H * std::max<int64_t>({QD, KVD, I, EI, E});
             DLLM_TRY(make(&gemm_part, gemm_part_cap));
@@ -623,6 +625,65 @@ struct dllm_hip_trainer {
     float* G(int id) const { return grads.as<float>() + tensors[static_cast<size_t>(id)].offset; }
     float* WT(int id) const { return wt.as<float>() + tensors[static_cast<size_t>(id)].wt_offset; }
     const float* Popt(int id) const { return id >= 0 ? P(id) : nullptr; }
+
+    // ---- weight gradients on a second stream ----
+    // The backward's dense weight-gradient matmuls (and the bias column sums) read only buffers the input-gradient
+    // chain has finished writing, plus the saved activations, and write only their own gradient tensors; each result
+    // is the same launch on the same inputs whichever stream runs it. So they run on a second stream, overlapped with
+    // the chain (whose small launches leave most CUs idle): a batch of them waits for the chain up to the point where
+    // it is issued (the fork event), and the chain waits for a batch's completion event before it next overwrites a
+    // buffer the batch reads. The stream is joined before the embedding gradients and the optimizer, which read every
+    // gradient, and before the next step's forward rewrites the saved activations. While the matmuls are being timed
+    // everything stays on the caller's stream, so each launch is timed alone.
+    enum SideEvent { kSideDown, kSideMlp, kSideO, kSideQkv, kSideJoin, kSideEvents };
+    hipStream_t side = nullptr;
+    hipEvent_t side_fork = nullptr;
+    hipEvent_t side_done[kSideEvents] = {};
+    bool side_pending[kSideEvents] = {};
+    bool side_on = false;  // this step's backward uses the second stream
+
+    int side_setup() {
+        if (side) return kOk;
+        DLLM_TRY(check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "stream"));
+        DLLM_TRY(check_hip(hipEventCreateWithFlags(&side_fork, hipEventDisableTiming), "event"));
+        for (hipEvent_t& e : side_done) DLLM_TRY(check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event"));
+        return kOk;
+    }
+
+    // The stream the next weight-gradient batch runs on, after it has been ordered behind the chain's work so far.
+    int side_fork_from(hipStream_t s, hipStream_t* out) {
+        if (!side_on) {
+            *out = s;
+            return kOk;
+        }
+        DLLM_TRY(check_hip(hipEventRecord(side_fork, s), "event"));
+        DLLM_TRY(check_hip(hipStreamWaitEvent(side, side_fork, 0), "event"));
+        *out = side;
+        return kOk;
+    }
+
+    int side_mark(SideEvent e) {
+        if (!side_on) return kOk;
+        DLLM_TRY(check_hip(hipEventRecord(side_done[e], side), "event"));
+        side_pending[e] = true;
+        return kOk;
+    }
+
+    // The chain waits for the last batch marked `e` before overwriting what that batch reads.
+    int side_wait(SideEvent e, hipStream_t s) {
+        if (!side_on || !side_pending[e]) return kOk;
+        side_pending[e] = false;
+        return check_hip(hipStreamWaitEvent(s, side_done[e], 0), "event");
+    }
+
+    int side_join(hipStream_t s) {
+        if (!side_on) return kOk;
+        DLLM_TRY(check_hip(hipEventRecord(side_done[kSideJoin], side), "event"));
+        DLLM_TRY(check_hip(hipStreamWaitEvent(s, side_done[kSideJoin], 0), "event"));
+        for (bool& b : side_pending) b = false;
+        side_on = false;
+        return kOk;
+    }
 
     // ---- matmul timing (dllm_hip_trainer_profile) ----
     bool profiling = false;
@@ -1023,24 +1084,35 @@ struct dllm_hip_trainer {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
         const Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
+        hipStream_t ws = s;  // the stream of the weight-gradient batches
         if (E > 0) {
+            DLLM_TRY(side_wait(kSideMlp, s));  // the previous layer's router dW reads dlogits_r
             DLLM_TRY(moe_backward(l, R, nseg, s));
         } else {
             // SwiGLU (backprop.py:289-306)
             DLLM_TRY(linear_dx(dx, R, L.down, dproduct, nullptr, s));
-            DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, s));
+            DLLM_TRY(side_fork_from(s, &ws));
+            DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, ws));
+            DLLM_TRY(side_mark(kSideDown));
+            DLLM_TRY(side_wait(kSideMlp, s));  // the previous layer's gate and up dW read dgate, dup
             DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s));
+            DLLM_TRY(side_fork_from(s, &ws));
+            DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, ws));
+            DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, ws));
+            DLLM_TRY(side_mark(kSideMlp));
             DLLM_TRY(linear_dx(dgate, R, L.gate, dh, nullptr, s));
-            DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, s));
             DLLM_TRY(linear_dx(dup, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
-            DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, s));
         }
         // mlp norm; dx_mid = dx + dh2'
+        DLLM_TRY(side_wait(kSideO, s));  // the previous layer's o dW reads dx_mid
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_rms, s));
         DLLM_TRY(norm_dw(dh, sv.x_mid, inv_rms, H, 1, nseg, G(L.mlp_norm), s));
         // attention output projection
         DLLM_TRY(linear_dx(dx_mid, R, L.o, dattended, nullptr, s));
-        DLLM_TRY(linear_dw(dx_mid, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, s));
+        DLLM_TRY(side_fork_from(s, &ws));
+        DLLM_TRY(linear_dw(dx_mid, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, ws));
+        DLLM_TRY(side_mark(kSideO));
+        DLLM_TRY(side_wait(kSideQkv, s));  // the previous layer's q/k/v dW read dq, dk (dq2, dk2) and dv_t
         DLLM_TRY(attention_backward(l, sv, b, s));
         DLLM_TRY(launch_rope(dq_t, pos_index, cos_t, sin_t, dq, R, c.heads, c.head_dim, c.rotary_dim, 0, 1, s));
         DLLM_TRY(launch_rope(dk_t, pos_index, cos_t, sin_t, dk, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 1, s));
@@ -1068,15 +1140,19 @@ struct dllm_hip_trainer {
         const int ws_[3] = {L.q, L.k, L.v};
         const int bs_[3] = {L.qb, L.kb, L.vb};
         const int64_t ns[3] = {QD, KVD, KVD};
+        DLLM_TRY(side_fork_from(s, &ws));
         for (int p = 0; p < 3; ++p) {
-            DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
-            DLLM_TRY(linear_dw(ds[p], ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, s, nullptr, -1,
+            DLLM_TRY(linear_dw(ds[p], ns[p], sv.h1, H, nseg, G(ws_[p]), nullptr, nullptr, ws, nullptr, -1,
                                unfold_scale(ws_[p])));
             if (bs_[p] >= 0 && grad_wanted(G(bs_[p])))
-                DLLM_TRY(launch_column_sums(0, ds[p], nullptr, nullptr, ns[p], seg_host.data(), nseg, col_part,
-                                            G(bs_[p]), s, window_weights(), unfold_scale(bs_[p])));
+                DLLM_TRY(launch_column_sums(0, ds[p], nullptr, nullptr, ns[p], seg_host.data(), nseg,
+                                            ws == s ? col_part : col_part_side, G(bs_[p]), ws, window_weights(),
+                                            unfold_scale(bs_[p])));
         }
+        DLLM_TRY(side_mark(kSideQkv));
+        for (int p = 0; p < 3; ++p) DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
         // attention norm; dx = dx_mid + dh1'
+        DLLM_TRY(side_wait(kSideDown, s));  // this layer's down dW reads dx
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh, dx, dx_mid, R, H, eps, 0, inv_rms, s));
         return norm_dw(dh, sv.x_in, inv_rms, H, 1, nseg, G(L.attn_norm), s);
     }
@@ -1235,8 +1311,11 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_moe_route_backward(sv.router_logits, sv.chosen, dweights,
                                            router_scale_cur != 0.0 ? dprob : nullptr, R, E, K,
                                            c.normalize_expert_weights ? 1 : 0, dlogits_r, s));
+        hipStream_t ws = s;  // dlogits_r is rewritten only after the next layer's wait on this mark
+        DLLM_TRY(side_fork_from(s, &ws));
+        DLLM_TRY(linear_dw(dlogits_r, E, sv.h2, H, nseg, G(L.router), nullptr, nullptr, ws));
+        DLLM_TRY(side_mark(kSideMlp));
         DLLM_TRY(linear_dx(dlogits_r, R, L.router, dh2r, nullptr, s));
-        DLLM_TRY(linear_dw(dlogits_r, E, sv.h2, H, nseg, G(L.router), nullptr, nullptr, s));
         // dh2 = (0 + the experts' dx in expert order) + dh2_router
         return launch_moe_combine(dxg, sv.order, sv.slot, nullptr, dh2r, dh, R, K, H, s);
     }
@@ -1350,7 +1429,14 @@ struct dllm_hip_trainer {
         DLLM_TRY(linear_dx(dlogits, R, head, dhidden, nullptr, s));
         DLLM_TRY(launch_rms_norm_backward_dx(x_final, P(final_norm), dhidden, dx, nullptr, R, H, eps, 0, inv_rms, s));
         DLLM_TRY(norm_dw(dhidden, x_final, inv_rms, H, 1, nseg, G(final_norm), s));
+        for (bool& pending : side_pending) pending = false;
+        side_on = false;
+        if (!profiling) {
+            DLLM_TRY(side_setup());
+            side_on = true;
+        }
         for (int64_t l = c.layers - 1; l >= 0; --l) DLLM_TRY(backward_layer(l, R, nseg, b, s));
+        DLLM_TRY(side_join(s));
         // embedding (backprop.py:112-117): per-window token rows, then the head's dW with them as the tied addend
         if (lora_on) return finish_gradients(windows, loss, router_loss, s);  // neither is adapted
         DLLM_TRY(launch_embedding_groups(dx, H, grp_order, grp_start, grp_out, groups, emb_rows, H, s));
@@ -1757,6 +1843,11 @@ int dllm_hip_trainer_destroy(dllm_hip_trainer* t) {
     if (t) {
         (void)hipDeviceSynchronize();
         for (hipEvent_t e : t->events) (void)hipEventDestroy(e);
+        if (t->side) {
+            (void)hipEventDestroy(t->side_fork);
+            for (hipEvent_t e : t->side_done) (void)hipEventDestroy(e);
+            (void)hipStreamDestroy(t->side);
+        }
     }
     delete t;
     return kOk;
