@@ -10,7 +10,8 @@
 // The products with a double factor are not exact, so they are a rounded multiply and a rounded add, as the
 // reference computes them (grad.hpp:262-301, nn.hpp:535-569); attn_tile_kernel runs them on the vector ALU.
 //
-// (Measured alternative: waves owning 8 rows by every column, the rows' A values scalar-loaded into SGPRs as
+// (Measured alternatives: a ring of three LDS stages, two in flight, for the small grids of T = 256: 14% slower.
+// Waves owning 8 rows by every column, the rows' A values scalar-loaded into SGPRs as
 // multiply operands and B loaded per lane, no LDS: 106 against 63 ms per step at T = 1024, the scalar loads' latency
 // exposed every few steps with only 64 SGPRs of them in flight.)
 // attn_tile_kernel mapping: a wave owns 16 consecutive rows by 64 CJ columns; each lane holds a 4-row x 4 CJ-column
@@ -282,14 +283,14 @@ __device__ __forceinline__ void stage_all(const Stage<CJ>& st, int wave, int rg,
 }
 
 // The wave's rows (tw + q, q < 16) that take step l, as a bit mask: the spans are intervals whose ends grow with the
-// row, so the rows taking l are one run of q, from the span formulas of row_span.
-__device__ __forceinline__ uint32_t rows_taking(const TileParams& p, int64_t l, int64_t tw, int64_t n, int64_t I) {
+// row, so the rows taking l are one run of q, from the span formulas of row_span. `t` is l / group (key rows: the
+// query of step l), kept by the caller.
+__device__ __forceinline__ uint32_t rows_taking(const TileParams& p, int64_t l, int64_t t, int64_t tw, int64_t I) {
     int64_t qa = 0, qb = (I - tw < 16 ? I - tw : 16) - 1;  // rows q in [qa, qb]
     if (p.mask == kMaskQueryRows) {  // l < t + 1, and l >= t + 1 - window
         qa = l - tw > qa ? l - tw : qa;
         if (p.window != 0) qb = l - tw + p.window - 1 < qb ? l - tw + p.window - 1 : qb;
     } else if (p.mask == kMaskKeyRows) {  // l >= j G, and (windowed) l / G < j + window
-        const int64_t t = l / p.group;
         qb = t - tw < qb ? t - tw : qb;
         if (p.window != 0) qa = t - tw - p.window + 1 > qa ? t - tw - p.window + 1 : qa;
     } else if (l >= p.L) {
@@ -301,16 +302,20 @@ __device__ __forceinline__ uint32_t rows_taking(const TileParams& p, int64_t l, 
 }
 
 // Steps l0 .. l0 + n - 1 of a stage, each taken by the rows whose span holds it (the lane's rows: bits 4 rg .. 4 rg + 3
-// of the wave's mask).
+// of the wave's mask). The query of a step (key rows) advances with it, one division per stage; the next step's
+// operands are read while the current one computes.
 template <int CJ>
 __device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ>& st, int wave, int rg, int cg,
-                                             int64_t l0, int n, int64_t tw, int64_t rows_n, int64_t I,
-                                             double (&acc)[4][4 * CJ]) {
+                                             int64_t l0, int n, int64_t tw, int64_t I, double (&acc)[4][4 * CJ]) {
+    const uint32_t G = p.mask == kMaskKeyRows ? static_cast<uint32_t>(p.group) : 1u;
+    uint32_t t = static_cast<uint32_t>(l0) / G;  // steps of one (window, head) stay below 2^31
+    uint32_t r = static_cast<uint32_t>(l0) - t * G;
+    double a[4], b[4 * CJ];
+    read_step<CJ>(st, 0, wave, rg, cg, a, b);
     for (int k = 0; k < n; ++k) {
-        const uint32_t take = __builtin_amdgcn_readfirstlane(rows_taking(p, l0 + k, tw, rows_n, I));
-        if (take == 0) continue;
-        double a[4], b[4 * CJ];
-        read_step<CJ>(st, k, wave, rg, cg, a, b);
+        double an[4], bn[4 * CJ];
+        read_step<CJ>(st, k + 1 < n ? k + 1 : k, wave, rg, cg, an, bn);
+        const uint32_t take = __builtin_amdgcn_readfirstlane(rows_taking(p, l0 + k, t, tw, I));
         const uint32_t mine = take >> (4 * rg);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -321,6 +326,14 @@ __device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ
                     acc[i][c] = acc[i][c] + prod;
                 }
             }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = an[i];
+#pragma unroll
+        for (int c = 0; c < 4 * CJ; ++c) b[c] = bn[c];
+        if (++r == G) {
+            r = 0;
+            ++t;
         }
     }
 }
@@ -408,7 +421,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
         if (n_steps == kChunk && l0 >= w_lo && l0 + kChunk <= w_hi)
             stage_all<CJ>(st[s & 1], wave, rg, cg, acc);
         else
-            stage_masked<CJ>(p, st[s & 1], wave, rg, cg, l0, n_steps, tw, n, I, acc);
+            stage_masked<CJ>(p, st[s & 1], wave, rg, cg, l0, n_steps, tw, I, acc);
         // the next stage's B, widened, into the other buffer (last read two stages ago, before the last barrier)
         if (s + 1 < stages) store_stage_b<CJ>(st[(s + 1) & 1], wave, lane, breg);
         workgroup_barrier();  // every wave is done with this stage before the next issue refills it

@@ -637,6 +637,9 @@ struct dllm_hip_trainer {
     // everything stays on the caller's stream, so each launch is timed alone.
     enum SideEvent { kSideDown, kSideMlp, kSideO, kSideQkv, kSideJoin, kSideEvents };
     hipStream_t side = nullptr;
+    // a third stream for the attention backward's dq, which runs beside dk and dv (independent inputs and outputs)
+    hipStream_t aux = nullptr;
+    hipEvent_t aux_fork = nullptr, aux_done = nullptr;
     hipEvent_t side_fork = nullptr;
     hipEvent_t side_done[kSideEvents] = {};
     bool side_pending[kSideEvents] = {};
@@ -645,6 +648,9 @@ struct dllm_hip_trainer {
     int side_setup() {
         if (side) return kOk;
         DLLM_TRY(check_hip(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "stream"));
+        DLLM_TRY(check_hip(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking), "stream"));
+        DLLM_TRY(check_hip(hipEventCreateWithFlags(&aux_fork, hipEventDisableTiming), "event"));
+        DLLM_TRY(check_hip(hipEventCreateWithFlags(&aux_done, hipEventDisableTiming), "event"));
         DLLM_TRY(check_hip(hipEventCreateWithFlags(&side_fork, hipEventDisableTiming), "event"));
         for (hipEvent_t& e : side_done) DLLM_TRY(check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "event"));
         return kOk;
@@ -1031,7 +1037,13 @@ struct dllm_hip_trainer {
         q.b_row_alloc = 0;
         q.exact_products = false;
         q.out_double = false;
-        DLLM_TRY(launch_attn_tiles(q, s));
+        hipStream_t qs = s;  // dq beside dk and dv: it reads the dS rows and k, they read p, ds, q and dout
+        if (side_on) {
+            DLLM_TRY(check_hip(hipEventRecord(aux_fork, s), "event"));
+            DLLM_TRY(check_hip(hipStreamWaitEvent(aux, aux_fork, 0), "event"));
+            qs = aux;
+        }
+        DLLM_TRY(launch_attn_tiles(q, qs));
         // dk[j] = sum over (t, hh) of ds q and dv[j] = sum of p dout, in one launch
         AttnTileCall k = q;
         k.heads = nkv;
@@ -1043,7 +1055,12 @@ struct dllm_hip_trainer {
         k.B2 = AttnOperand{dattended, 0, QD, G * hd, 1, QD, hd, G};
         k.C2 = AttnOperand{dv_t, 0, KVD, hd, 1, KVD, 0, 1};
         k.mask = kMaskKeyRows;
-        return launch_attn_tiles(k, s);
+        DLLM_TRY(launch_attn_tiles(k, s));
+        if (qs != s) {  // everything after reads dq_t, and the next layer rewrites the dS rows
+            DLLM_TRY(check_hip(hipEventRecord(aux_done, qs), "event"));
+            DLLM_TRY(check_hip(hipStreamWaitEvent(s, aux_done, 0), "event"));
+        }
+        return kOk;
     }
 
     // One layer's forward (backprop.py:423-487).
@@ -1847,6 +1864,9 @@ int dllm_hip_trainer_destroy(dllm_hip_trainer* t) {
             (void)hipEventDestroy(t->side_fork);
             for (hipEvent_t e : t->side_done) (void)hipEventDestroy(e);
             (void)hipStreamDestroy(t->side);
+            (void)hipEventDestroy(t->aux_fork);
+            (void)hipEventDestroy(t->aux_done);
+            (void)hipStreamDestroy(t->aux);
         }
     }
     delete t;
