@@ -1025,6 +1025,17 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
     GemmParams* ps = static_cast<GemmParams*>(host_table);
     int64_t* starts = reinterpret_cast<int64_t*>(static_cast<char*>(host_table) +
                                                  round_up(sizeof(GemmParams) * static_cast<size_t>(capacity), 8));
+    // plain groups whose 128 x 128 tiles would leave most CUs idle take 64 x 64 or 32 x 32 ones (as launch_gemm)
+    int tile = 4;
+    if (!seg) {
+        while (tile > 1) {
+            int64_t count = 0;
+            for (int k = 0; k < n; ++k)
+                count += ceil_div(calls[k].J, 32 * tile) * ceil_div(calls[k].I, 32 * tile);
+            if (count >= kSmallTilesBelow) break;
+            tile /= 2;
+        }
+    }
     int64_t tiles = 0;
     int used = 0;
     for (int k = 0; k < n; ++k) {
@@ -1042,7 +1053,7 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
         if (g.I == 0 || g.J == 0) continue;
         ps[used] = params_of(g);
         starts[used] = tiles;
-        tiles += static_cast<int64_t>(ceil_div(g.J, MTile<4, 4>::J) * ceil_div(g.I, MTile<4, 4>::I));
+        tiles += static_cast<int64_t>(ceil_div(g.J, 32 * tile) * ceil_div(g.I, 32 * tile));
         ++used;
     }
     starts[used] = tiles;
@@ -1081,6 +1092,7 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
         group->grid = longest * kXcdRanges;
     }
     group->count = used;
+    group->tile = tile;
     group->tiles = tiles;
     group->a_kind = ak;
     group->segmented = seg ? 1 : 0;
@@ -1097,15 +1109,23 @@ int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStrea
     const GemmParams none{};
     const dim3 grid(static_cast<unsigned>(group.grid));
     DLLM_REQUIRE(group.grid < (int64_t{1} << 31), "matmul group too large for one launch");
-    if (group.a_kind == kAFloatT)
-        hipLaunchKernelGGL((gemm_mfma_kernel<kPlain, kAFloatT, true>), grid, dim3(256), 0, stream, none, group.tiles,
-                           int64_t{group.capacity}, int64_t{1}, ps, starts, group.count);
-    else if (group.segmented)
-        hipLaunchKernelGGL((gemm_mfma_kernel<kWindowsInSequence, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
-                           group.tiles, int64_t{group.capacity}, int64_t{1}, ps, starts, group.count);
-    else
-        hipLaunchKernelGGL((gemm_mfma_kernel<kPlain, kAFloatRows, true>), grid, dim3(256), 0, stream, none,
-                           group.tiles, int64_t{group.capacity}, int64_t{1}, ps, starts, group.count);
+    DLLM_REQUIRE(group.tile == 4 || (!group.segmented && (group.tile == 2 || group.tile == 1)),
+                 "grouped matmul tiles are 128, or for plain groups 64 or 32, square");
+#define DLLM_GROUP_LAUNCH(MODE, AK, T)                                                                            \
+    hipLaunchKernelGGL((gemm_mfma_kernel<MODE, AK, true, T, T>), grid, dim3(256), 0, stream, none, group.tiles, \
+                       int64_t{group.capacity}, int64_t{1}, ps, starts, group.count)
+    if (group.segmented) {
+        DLLM_GROUP_LAUNCH(kWindowsInSequence, kAFloatRows, 4);
+    } else if (group.a_kind == kAFloatT) {
+        if (group.tile == 4) DLLM_GROUP_LAUNCH(kPlain, kAFloatT, 4);
+        else if (group.tile == 2) DLLM_GROUP_LAUNCH(kPlain, kAFloatT, 2);
+        else DLLM_GROUP_LAUNCH(kPlain, kAFloatT, 1);
+    } else {
+        if (group.tile == 4) DLLM_GROUP_LAUNCH(kPlain, kAFloatRows, 4);
+        else if (group.tile == 2) DLLM_GROUP_LAUNCH(kPlain, kAFloatRows, 2);
+        else DLLM_GROUP_LAUNCH(kPlain, kAFloatRows, 1);
+    }
+#undef DLLM_GROUP_LAUNCH
     return check_launch("gemm group");
 }
 

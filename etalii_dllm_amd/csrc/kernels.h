@@ -51,6 +51,7 @@ int launch_gemm(const GemmCall& g, hipStream_t stream);
 // call.
 struct GemmGroup {
     int count = 0, capacity = 0, a_kind = 0, segmented = 0;
+    int tile = 4;                 // workgroup tiles of 32 tile x 32 tile outputs
     int64_t tiles = 0, grid = 0;  // grid: workgroups of the launch (8 XCD ranges of equal work, padded)
 };
 size_t gemm_group_bytes(int n);
