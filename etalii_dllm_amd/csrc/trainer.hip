@@ -256,6 +256,7 @@ struct dllm_hip_trainer {
     size_t lora_ws_bytes = 0;
     int8_t* q8_values = nullptr;
     float* q8_scales = nullptr;
+    uint8_t* q4_packed = nullptr;  // a Q4_0 base: the packed values before unpacking
     // attention as batched matmuls (attn_lds.hip, attn_chains.hip): per (window, head) transposed operands and score
     // matrices
     int64_t Tp = 0;
@@ -1713,6 +1714,7 @@ struct dllm_hip_trainer {
         if (l.base_quantize) {
             DLLM_TRY(make(&q8_values, static_cast<size_t>(std::max<int64_t>(largest, 32))));
             DLLM_TRY(make(&q8_scales, static_cast<size_t>(std::max<int64_t>(largest / 32, 1))));
+            if (l.base_quantize == 2) DLLM_TRY(make(&q4_packed, static_cast<size_t>(std::max<int64_t>(largest / 2, 16))));
             base_ready = false;
         }
         return build_optimizer(adapters, lora_p.as<float>(), lora_g.as<float>(), lora_m.as<float>(),
@@ -1731,14 +1733,20 @@ struct dllm_hip_trainer {
         return false;
     }
 
-    // Before a step: the Q8_0 base once per parameter write (QuantizedBase: reading a quantised matrix gives its
-    // dequantised values), then W' = merge(W, A, B) for every target (lora.py:271-287) and their W'^T.
+    // Before a step: the quantised base once per parameter write (QuantizedBase: reading a quantised matrix gives its
+    // dequantised values, int8 value times block scale in float32 for Q8_0 and for unpacked Q4_0 alike,
+    // numerics.py:131-139), then W' = merge(W, A, B) for every target (lora.py:271-287) and their W'^T.
     int prepare_lora(hipStream_t s) {
         if (!base_ready) {
             for (const TensorInfo& t : tensors) {
                 if (!quantizable(t)) continue;
                 float* w = params.as<float>() + t.offset;
-                DLLM_TRY(launch_quantize_q8_0(w, q8_values, q8_scales, t.numel, s));
+                if (lc.base_quantize == 2) {
+                    DLLM_TRY(dllm_hip_quantize_q4_0(w, q4_packed, q8_scales, static_cast<size_t>(t.numel), s));
+                    DLLM_TRY(dllm_hip_unpack_q4_0(q4_packed, q8_values, static_cast<size_t>(t.numel), s));
+                } else {
+                    DLLM_TRY(launch_quantize_q8_0(w, q8_values, q8_scales, t.numel, s));
+                }
                 DLLM_TRY(launch_dequantize_q8_0(q8_values, q8_scales, w, t.numel, s));
             }
             base_ready = true;
@@ -1812,7 +1820,8 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     if (lora) {
         DLLM_REQUIRE(lora->rank >= 1, "the LoRA rank must be positive");
         DLLM_REQUIRE(lora->targets > 0 && lora->targets < 128, "LoRA targets must be a non-empty subset of q k v o gate up down");
-        DLLM_REQUIRE(lora->base_quantize == 0 || lora->base_quantize == 1, "base_quantize must be 0 (float) or 1 (q8_0)");
+        DLLM_REQUIRE(lora->base_quantize >= 0 && lora->base_quantize <= 2,
+                     "base_quantize must be 0 (float), 1 (q8_0) or 2 (q4_0)");
     }
     const dllm_hip_decoder_config& c = *config;
     const int64_t ei = c.experts > 0 ? (c.expert_intermediate > 0 ? c.expert_intermediate : c.intermediate) : 0;

@@ -51,12 +51,13 @@ LORA_TARGET_BITS = {"q": 1, "k": 2, "v": 4, "o": 8, "gate": 16, "up": 32, "down"
 
 def lora_config(rank: int, alpha: float, targets=tuple(LORA_TARGET_BITS), rslora: bool = False,
                 base_quantize: str | None = None) -> LoraConfig:
-    if base_quantize not in (None, "q8_0"):
-        raise ValueError(f"unsupported base quantisation {base_quantize!r}; supported: q8_0")
+    kinds = {None: 0, "q8_0": 1, "q4_0": 2}
+    if base_quantize not in kinds:
+        raise ValueError(f"unknown base quantisation {base_quantize!r}; supported: q8_0, q4_0")
     mask = 0
     for t in targets:
         mask |= LORA_TARGET_BITS[t]
-    return LoraConfig(rank, alpha, mask, int(rslora), 1 if base_quantize == "q8_0" else 0)
+    return LoraConfig(rank, alpha, mask, int(rslora), kinds[base_quantize])
 
 
 lib.dllm_hip_trainer_create_lora.argtypes = [C.POINTER(DecoderConfig), C.POINTER(LoraConfig), C.c_int64, C.c_int64,

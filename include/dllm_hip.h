@@ -283,8 +283,9 @@ typedef struct dllm_hip_trainer dllm_hip_trainer;
  * windows, each at most max_window_tokens long. Weights start at zero; moments at zero. */
 /* LoRA runs (src/etalii_dllm/lora.py, training/trainer.py:463-474): AdamW updates the adapters only. Targets are a
  * mask of q (1) k (2) v (4) o (8) gate (16) up (32) down (64); scale = alpha / rank (alpha / sqrt(rank) with
- * rslora). base_quantize 1 holds the quantisable matrices (lora.py:300-302) as their Q8_0-dequantised values, applied
- * at the step after the parameters are written (QuantizedBase: a quantised run is LoRA on the dequantised base). */
+ * rslora). base_quantize 1 (q8_0) or 2 (q4_0) holds the quantisable matrices (lora.py:319-324) as their dequantised
+ * values, applied at the step after the parameters are written (QuantizedBase: a quantised run is LoRA on the
+ * dequantised base, lora.py:327-375). */
 typedef struct {
     int64_t rank;
     double alpha;

@@ -14,7 +14,7 @@ from pathlib import Path
 
 KEEP = ("RANDOM_FIRST", "RANDOM_SECOND", "KERNEL_FINGERPRINTS", "GRADIENT_FINGERPRINT", "FINETUNE_FINGERPRINT",
         "LORA_FINETUNE_FINGERPRINT", "DPO_FINETUNE_FINGERPRINT", "LONG_CONTEXT_FINGERPRINTS",
-        "TINY_LOGITS_FINGERPRINT")
+        "TINY_LOGITS_FINGERPRINT", "QLORA_FINETUNE_FINGERPRINT")
 
 
 def main(reference: Path, out: Path) -> None:

@@ -460,6 +460,13 @@ FIXTURES = {
 }
 
 
+# tests/test_quantized_finetuning.py:34-37: the tiny configs with hidden size 32 and a 264-token vocabulary
+QLORA_FIXTURES = {
+    "llama": Decoder("llama", tied=True, **{**TINY, "hidden": 32, "vocab": 264, "head_dim": 8}),
+    "qwen3": Decoder("qwen3", tied=True, qk_norm=1, **{**TINY, "hidden": 32, "vocab": 264, "head_dim": 8}),
+}
+
+
 def bf16_round(values: np.ndarray) -> np.ndarray:
     """model_fixtures.py:196-204: round to bfloat16 (nearest even) and back to float32."""
     bits = np.ascontiguousarray(values, dtype="<f4").view("<u4").astype(np.uint64)
@@ -997,6 +1004,14 @@ def oracle_encoder() -> Encoder:
 
 def ref_encoder() -> Encoder:
     return Encoder(ref(), "ref")
+
+
+QUANTIZED_MATRICES = tuple(f".{m}.weight" for m in ("q", "k", "v", "o", "gate", "up", "down"))
+
+
+def quantizable(name: str, shape) -> bool:
+    """lora.py:319-324: the matrices a quantised base holds quantised (rows of whole 32-value blocks)."""
+    return name.endswith(QUANTIZED_MATRICES) and len(shape) == 2 and shape[1] % 32 == 0
 
 
 def dequantize_q8_0(q: np.ndarray, scales: np.ndarray) -> np.ndarray:

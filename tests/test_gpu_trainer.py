@@ -179,6 +179,22 @@ def test_lora_finetune_fingerprint_on_gpu(family):
     assert t.fingerprint() == GOLDEN["LORA_FINETUNE_FINGERPRINT"][family]  # merged on and hashed from the device
 
 
+@pytest.mark.parametrize("family", sorted(O.QLORA_FIXTURES))
+def test_qlora_finetune_fingerprint_on_gpu(family):
+    """LoRA on a Q4_0 base (tests/test_quantized_finetuning.py:27-29,96-112): 4 steps, batch 2, seed 3, lr 3e-2,
+    rank 2 alpha 4 on every target of the hidden-32 models; the GPU quantises and dequantises the base itself, and
+    the merged export is the reference's QLORA_FINETUNE_FINGERPRINT."""
+    d = O.QLORA_FIXTURES[family]
+    lora = O.Lora(rank=2, alpha=4.0)
+    t = make_lora_trainer(d, O.fixture_weights(d), lora, O.init_adapters(d, lora, 3), "q4_0")
+    windows = ascii_windows()
+    opt = O.AdamWConfig(learning_rate=3e-2)
+    for step in range(4):
+        batch = [windows[i] for i in O.batch_indices(len(windows), step, 2, 3)]
+        t.step(batch, opt.learning_rate_at(step + 1, 4), step + 1)
+    assert t.fingerprint() == GOLDEN["QLORA_FINETUNE_FINGERPRINT"][family]
+
+
 def test_lora_checkpoint_holds_the_adapters_and_restores_the_run(tmp_path):
     """A LoRA checkpoint holds the adapters and their moments only (trainer.py:519-522, 616-622); restored into a
     trainer on the same base, the export is the reference's LORA_FINETUNE_FINGERPRINT."""

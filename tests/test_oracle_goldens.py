@@ -297,3 +297,46 @@ def test_attention_factor_fold_is_a_weight_scale():
             rows[:, :rd] *= np.float32(a)
             want = rows.reshape(want.shape)
         assert g_a[name].tobytes() == want.tobytes(), name
+
+
+# -- LoRA on a Q4_0 base (reference tests/test_quantized_finetuning.py:27-29,34-37,96-112): the tiny models with
+#    hidden size 32 and vocabulary 264, every quantisable matrix replaced by its dequantised Q4_0 blocks.
+
+QLORA_FIXTURES = O.QLORA_FIXTURES
+
+
+def q4_0_base(d, weights):
+    """lora.py:322-375 (dequantized_weights): q/k/v/o/gate/up/down matrices whose rows hold whole 32-value blocks
+    become int8(unpacked Q4_0) * their block scale, elementwise in float32 (numerics.py:135-137)."""
+    base = dict(weights)
+    for name, shape in d.tensor_shapes().items():
+        if O.quantizable(name, shape):
+            packed, scales = O.quantize_q4_0(O.oracle().orc_quantize_q4_0, weights[name])
+            values = O.unpack_q4_0(O.oracle().orc_unpack_q4_0, packed)
+            base[name] = O.dequantize_q8_0(values, scales).reshape(shape)
+    return base
+
+
+def qlora_run(family, kern, on_step=None):
+    """RUN = 4 steps, batch 2, sequence 8, seed 3, lr 3e-2 cosine, LoRA rank 2 alpha 4 on every target."""
+    d = QLORA_FIXTURES[family]
+    lora = O.Lora(rank=2, alpha=4.0)
+    base = q4_0_base(d, O.fixture_weights(d))
+    adapters = O.init_adapters(d, lora, 3)
+    m = {n: np.zeros_like(a) for n, a in adapters.items()}
+    v = {n: np.zeros_like(a) for n, a in adapters.items()}
+    windows = ascii_windows()
+    opt = O.AdamWConfig(learning_rate=3e-2)
+    for step in range(4):
+        batch = [windows[i] for i in O.batch_indices(len(windows), step, 2, 3)]
+        O.lora_train_step(kern, d, base, adapters, m, v, batch, opt, step + 1, 4, lora)
+    return d, lora, base, adapters
+
+
+@pytest.mark.parametrize("family", sorted(QLORA_FIXTURES))
+def test_qlora_finetune_fingerprint(family):
+    """The merged export of the Q4_0-base run equals the reference's QLORA_FINETUNE_FINGERPRINT."""
+    kern = O.oracle_kernels()
+    d, lora, base, adapters = qlora_run(family, kern)
+    merged = O.merged_weights(kern, d, base, adapters, lora)
+    assert O.data_fingerprint(merged) == GOLDEN["QLORA_FINETUNE_FINGERPRINT"][family]
