@@ -496,6 +496,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&dlogits, R * V));
         DLLM_TRY(make(&dx, R * H));
         DLLM_TRY(make(&dh, R * H));
+        DLLM_TRY(make(&dh_b, R * H));
+        DLLM_TRY(make(&dh_c, R * H));
         DLLM_TRY(make(&dx_mid, R * H));
         DLLM_TRY(make(&dattended, R * QD));
         DLLM_TRY(make(&dq_t, R * QD));
@@ -618,7 +620,7 @@ struct dllm_hip_trainer {
         fold_on = want;
         // the step's weight addresses changed: rebuild the transposes' job table and the qkv groups
         wt_jobs = nullptr;
-        qkv_rows = -1;
+        grp_rows = -1;
         wt_valid = false;
         merged_valid = false;
         return check_hip(hipDeviceSynchronize(), "set_rope");
@@ -782,49 +784,85 @@ struct dllm_hip_trainer {
     // The q, k and v projections of every layer read the same h1: one grouped launch per layer runs all three (their
     // tiles together fill the chip; k and v alone are 2 x 64 tiles at the c3 shapes). Each output's bits are those of
     // its own launch. The tables depend on the row count R and are rebuilt (after the stream drains) when it changes.
-    char* qkv_tables = nullptr;
-    std::vector<GemmGroup> qkv_groups;
-    int64_t qkv_rows = -1;
-    bool qkv_grouped = false;
+    // One grouped matmul launch per layer and kind (a table each, prepared per row count): the q/k/v forward and
+    // the gate/up forward (independent outputs), and, when the row count is small enough that each of these
+    // matmuls alone leaves CUs idle, the input gradients of gate/up and of q/k/v, each into its own buffer (dh,
+    // dh_b, dh_c) and then added in the reference's order: dh2 = dx_gate + dx_up, dh1 = (dh_q + dh_k) + dh_v.
+    enum LayerGroup { kGrpQkvFwd, kGrpMlpFwd, kGrpMlpDx, kGrpQkvDx, kLayerGroups };
+    static constexpr int kGroupCap = 3;  // matmuls per group table
+    char* grp_tables = nullptr;          // [layer][kind]
+    std::vector<GemmGroup> grp;          // [layer * kLayerGroups + kind]
+    bool grp_on[kLayerGroups] = {};
+    std::vector<double> grp_flops;       // algorithmic flop of each group (matmul timing)
+    int64_t grp_rows = -1;               // the row count the tables were prepared for
+    float *dh_b = nullptr, *dh_c = nullptr;
 
-    int prepare_qkv_groups(int64_t R, hipStream_t s) {
-        if (R == qkv_rows) return kOk;
-        const size_t gb = gemm_group_bytes(3);
-        if (qkv_tables == nullptr) DLLM_TRY(make(&qkv_tables, gb * static_cast<size_t>(c.layers)));
-        std::vector<char> host(gb * static_cast<size_t>(c.layers));
-        qkv_groups.assign(static_cast<size_t>(c.layers), GemmGroup{});
-        // the grouped kernel takes whole 16-byte chunks of the operands; other shapes keep one launch per projection
-        qkv_grouped = R > 0 && H % 4 == 0;
-        for (int64_t l = 0; l < c.layers && qkv_grouped; ++l) {
+    const GemmGroup& group_of(int64_t l, int kind) const { return grp[static_cast<size_t>(l * kLayerGroups + kind)]; }
+    const char* table_of(int64_t l, int kind) const {
+        return grp_tables + gemm_group_bytes(kGroupCap) * static_cast<size_t>(l * kLayerGroups + kind);
+    }
+
+    int prepare_groups(int64_t R, hipStream_t s) {
+        if (R == grp_rows) return kOk;
+        const size_t gb = gemm_group_bytes(kGroupCap);
+        const size_t n = static_cast<size_t>(c.layers) * kLayerGroups;
+        if (grp_tables == nullptr) DLLM_TRY(make(&grp_tables, gb * n));
+        std::vector<char> host(gb * n, 0);
+        grp.assign(n, GemmGroup{});
+        grp_flops.assign(n, 0.0);
+        // the grouped kernel takes whole 16-byte chunks of the operands; other shapes keep one launch per matmul
+        const bool rows_ok = R > 0 && H % 4 == 0;
+        for (int k = 0; k < kLayerGroups; ++k) grp_on[k] = rows_ok && (E == 0 || k == kGrpQkvFwd || k == kGrpQkvDx);
+        const float* dqf = c.qk_norm ? dq2 : dq;
+        const float* dkf = c.qk_norm ? dk2 : dk;
+        for (int64_t l = 0; l < c.layers; ++l) {
             const LayerIds& L = layer_ids[static_cast<size_t>(l)];
             Saved& sv = saved[static_cast<size_t>(l)];
-            const GemmCall calls[3] = {fwd_call(sv.h1, R, H, L.q, Popt(L.qb), sv.q_raw, nullptr),
-                                       fwd_call(sv.h1, R, H, L.k, Popt(L.kb), sv.k_raw, nullptr),
-                                       fwd_call(sv.h1, R, H, L.v, Popt(L.vb), sv.v, nullptr)};
-            for (const GemmCall& g : calls) qkv_grouped = qkv_grouped && g.J % 4 == 0 && g.ldb % 4 == 0;
-            if (!qkv_grouped) break;
-            DLLM_TRY(gemm_group_prepare(calls, 3, 3, host.data() + gb * static_cast<size_t>(l),
-                                        &qkv_groups[static_cast<size_t>(l)]));
+            for (int k = 0; k < kLayerGroups; ++k) {
+                if (!grp_on[k]) continue;
+                GemmCall calls[kGroupCap];
+                int nc = 0;
+                if (k == kGrpQkvFwd) {
+                    calls[nc++] = fwd_call(sv.h1, R, H, L.q, Popt(L.qb), sv.q_raw, nullptr);
+                    calls[nc++] = fwd_call(sv.h1, R, H, L.k, Popt(L.kb), sv.k_raw, nullptr);
+                    calls[nc++] = fwd_call(sv.h1, R, H, L.v, Popt(L.vb), sv.v, nullptr);
+                } else if (k == kGrpMlpFwd) {
+                    calls[nc++] = fwd_call(sv.h2, R, H, L.gate, nullptr, sv.gate, nullptr);
+                    calls[nc++] = fwd_call(sv.h2, R, H, L.up, nullptr, sv.up, nullptr);
+                } else if (k == kGrpMlpDx) {
+                    calls[nc++] = dx_call(dgate, R, L.gate, dh, nullptr);
+                    calls[nc++] = dx_call(dup, R, L.up, dh_b, nullptr);
+                } else {
+                    calls[nc++] = dx_call(dqf, R, L.q, dh, nullptr);
+                    calls[nc++] = dx_call(dkf, R, L.k, dh_b, nullptr);
+                    calls[nc++] = dx_call(dv_t, R, L.v, dh_c, nullptr);
+                }
+                bool ok = true;
+                for (int i = 0; i < nc; ++i) ok = ok && calls[i].J % 4 == 0 && calls[i].ldb % 4 == 0;
+                GemmGroup& g = grp[static_cast<size_t>(l * kLayerGroups + k)];
+                const size_t gi = static_cast<size_t>(l * kLayerGroups + k);
+                if (ok) DLLM_TRY(gemm_group_prepare(calls, nc, kGroupCap, host.data() + gb * gi, &g));
+                for (int i = 0; i < nc; ++i) grp_flops[gi] += flops_of(calls[i]);
+                // the input-gradient groups only where the separate launches would take small tiles
+                const bool dx_kind = k == kGrpMlpDx || k == kGrpQkvDx;
+                if (!ok || (dx_kind && g.tile == 4)) grp_on[k] = false;
+            }
         }
-        if (qkv_grouped) {
-            DLLM_TRY(check_hip(hipStreamSynchronize(s), "qkv tables"));  // no launch still reads the old tables
-            DLLM_TRY(check_hip(hipMemcpy(qkv_tables, host.data(), host.size(), hipMemcpyHostToDevice), "upload"));
-        }
-        qkv_rows = R;
+        DLLM_TRY(check_hip(hipStreamSynchronize(s), "group tables"));  // no launch still reads the old tables
+        DLLM_TRY(check_hip(hipMemcpy(grp_tables, host.data(), host.size(), hipMemcpyHostToDevice), "upload"));
+        grp_rows = R;
         return kOk;
+    }
+
+    int group_launch(int64_t l, int kind, hipStream_t s) {
+        const size_t i = static_cast<size_t>(l * kLayerGroups + kind);
+        return gemm_group(grp[i], table_of(l, kind), grp_flops[i], s);
     }
 
     int qkv_forward(int64_t l, int64_t R, hipStream_t s) {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
         Saved& sv = saved[static_cast<size_t>(l)];
-        if (qkv_grouped && qkv_rows == R) {
-            const double flops = 2.0 * static_cast<double>(R) * static_cast<double>(H) *
-                                 static_cast<double>(tensors[static_cast<size_t>(L.q)].rows +
-                                                     tensors[static_cast<size_t>(L.k)].rows +
-                                                     tensors[static_cast<size_t>(L.v)].rows);
-            return gemm_group(qkv_groups[static_cast<size_t>(l)], qkv_tables + gemm_group_bytes(3) * static_cast<size_t>(l),
-                              flops, s);
-        }
+        if (grp_on[kGrpQkvFwd] && grp_rows == R) return group_launch(l, kGrpQkvFwd, s);
         DLLM_TRY(linear_fwd(sv.h1, R, H, L.q, Popt(L.qb), sv.q_raw, nullptr, s));
         DLLM_TRY(linear_fwd(sv.h1, R, H, L.k, Popt(L.kb), sv.k_raw, nullptr, s));
         return linear_fwd(sv.h1, R, H, L.v, Popt(L.vb), sv.v, nullptr, s);
@@ -1090,8 +1128,12 @@ struct dllm_hip_trainer {
         DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
         DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
         if (E > 0) return moe_forward(l, R, x_out, s);
-        DLLM_TRY(linear_fwd(sv.h2, R, H, L.gate, nullptr, sv.gate, nullptr, s));
-        DLLM_TRY(linear_fwd(sv.h2, R, H, L.up, nullptr, sv.up, nullptr, s));
+        if (grp_on[kGrpMlpFwd] && grp_rows == R) {
+            DLLM_TRY(group_launch(l, kGrpMlpFwd, s));
+        } else {
+            DLLM_TRY(linear_fwd(sv.h2, R, H, L.gate, nullptr, sv.gate, nullptr, s));
+            DLLM_TRY(linear_fwd(sv.h2, R, H, L.up, nullptr, sv.up, nullptr, s));
+        }
         DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * I, s));
         return linear_fwd(sv.product, R, I, L.down, nullptr, x_out, sv.x_mid, s);  // x_out = x_mid + mlp
     }
@@ -1118,8 +1160,13 @@ struct dllm_hip_trainer {
             DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, ws));
             DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, ws));
             DLLM_TRY(side_mark(kSideMlp));
-            DLLM_TRY(linear_dx(dgate, R, L.gate, dh, nullptr, s));
-            DLLM_TRY(linear_dx(dup, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
+            if (grp_on[kGrpMlpDx] && grp_rows == R) {
+                DLLM_TRY(group_launch(l, kGrpMlpDx, s));
+                DLLM_TRY(launch_add(dh, dh_b, dh, R * H, s));  // dh2 = dx_gate + dx_up
+            } else {
+                DLLM_TRY(linear_dx(dgate, R, L.gate, dh, nullptr, s));
+                DLLM_TRY(linear_dx(dup, R, L.up, dh, dh, s));  // dh2 = dx_gate + dx_up
+            }
         }
         // mlp norm; dx_mid = dx + dh2'
         DLLM_TRY(side_wait(kSideO, s));  // the previous layer's o dW reads dx_mid
@@ -1168,7 +1215,13 @@ struct dllm_hip_trainer {
                                             unfold_scale(bs_[p])));
         }
         DLLM_TRY(side_mark(kSideQkv));
-        for (int p = 0; p < 3; ++p) DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
+        if (grp_on[kGrpQkvDx] && grp_rows == R) {
+            DLLM_TRY(group_launch(l, kGrpQkvDx, s));
+            DLLM_TRY(launch_add(dh, dh_b, dh, R * H, s));  // (dh_q + dh_k) + dh_v
+            DLLM_TRY(launch_add(dh, dh_c, dh, R * H, s));
+        } else {
+            for (int p = 0; p < 3; ++p) DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
+        }
         // attention norm; dx = dx_mid + dh1'
         DLLM_TRY(side_wait(kSideDown, s));  // this layer's down dW reads dx
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh, dx, dx_mid, R, H, eps, 0, inv_rms, s));
@@ -1417,7 +1470,7 @@ struct dllm_hip_trainer {
             if (fold_on) DLLM_TRY(fold_weights(s));
             DLLM_TRY(refresh_transposes(s));
         }
-        DLLM_TRY(prepare_qkv_groups(R, s));
+        DLLM_TRY(prepare_groups(R, s));
         const int nseg = static_cast<int>(windows);
         nwin = windows;
         router_scale_cur = router_scale;
