@@ -94,6 +94,10 @@ int launch_column_sums(int kind, const float* dy, const float* x, const double* 
 // rope (nn.hpp:501-530) with precomputed cos/sin tables [positions][half] (double, sin already negated for inverse).
 int launch_rope_tables(const int64_t* positions, int64_t n, const double* inv_freq, int64_t half, double* cos_table,
                        double* sin_table, hipStream_t stream);
+// rope (non-interleaved) of two tensors of the same tokens in one launch.
+int launch_rope_pair(const float* x1, float* out1, int64_t heads1, const float* x2, float* out2, int64_t heads2,
+                     const int64_t* pos_index, const double* cos_table, const double* sin_table, int64_t tokens,
+                     int64_t head_dim, int64_t rotary_dim, int inverse, hipStream_t stream);
 int launch_rope(const float* x, const int64_t* pos_index, const double* cos_table, const double* sin_table,
                 float* out, int64_t tokens, int64_t heads, int64_t head_dim, int64_t rotary_dim, int interleaved,
                 int inverse, hipStream_t stream);
@@ -114,6 +118,7 @@ int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
                            float* dgate, float* dup, int64_t n, hipStream_t stream);
 int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream);
+int launch_add3(const float* a, const float* b, const float* c, float* out, int64_t n, hipStream_t stream);
 int launch_gather_rows(const float* table, const int64_t* index, float* out, int64_t rows, int64_t dim,
                        hipStream_t stream);
 

@@ -310,14 +310,13 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const int64_t* __restri
 }
 
 // rope (nn.hpp:515-527); inverse negates the sine exactly.
-__global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, const int64_t* __restrict__ pos_index,
-                                                   const double* __restrict__ ct, const double* __restrict__ st,
-                                                   float* __restrict__ out, int64_t tokens, int64_t heads,
-                                                   int64_t head_dim, int64_t rotary_dim, int interleaved, int inverse) {
+// Element idx of one tensor's rotation (pair k of head h of token t, or a pass-through value past rotary_dim).
+__device__ __forceinline__ void rope_element(int64_t idx, const float* __restrict__ x,
+                                             const int64_t* __restrict__ pos_index, const double* __restrict__ ct,
+                                             const double* __restrict__ st, float* __restrict__ out, int64_t heads,
+                                             int64_t head_dim, int64_t rotary_dim, int interleaved, int inverse) {
     const int64_t half = rotary_dim / 2;
     const int64_t per_head = half + (head_dim - rotary_dim);
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= tokens * heads * per_head) return;
     const int64_t t = idx / (heads * per_head);
     const int64_t rem = idx % (heads * per_head);
     const int64_t h = rem / per_head, k = rem % per_head;
@@ -337,6 +336,32 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, 
     const double b = xh[i1];
     oh[i0] = static_cast<float>(a * c - b * s);
     oh[i1] = static_cast<float>(a * s + b * c);
+}
+
+__global__ __launch_bounds__(256) void rope_kernel(const float* __restrict__ x, const int64_t* __restrict__ pos_index,
+                                                   const double* __restrict__ ct, const double* __restrict__ st,
+                                                   float* __restrict__ out, int64_t tokens, int64_t heads,
+                                                   int64_t head_dim, int64_t rotary_dim, int interleaved, int inverse) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= tokens * heads * (rotary_dim / 2 + head_dim - rotary_dim)) return;
+    rope_element(idx, x, pos_index, ct, st, out, heads, head_dim, rotary_dim, interleaved, inverse);
+}
+
+// Two tensors of the same tokens (the queries and the keys) in one launch: the first n1 elements are the first's.
+__global__ __launch_bounds__(256) void rope_pair_kernel(const float* __restrict__ x1, float* __restrict__ out1,
+                                                        int64_t heads1, const float* __restrict__ x2,
+                                                        float* __restrict__ out2, int64_t heads2,
+                                                        const int64_t* __restrict__ pos_index,
+                                                        const double* __restrict__ ct, const double* __restrict__ st,
+                                                        int64_t tokens, int64_t head_dim, int64_t rotary_dim,
+                                                        int inverse) {
+    const int64_t per_head = rotary_dim / 2 + head_dim - rotary_dim;
+    const int64_t n1 = tokens * heads1 * per_head;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx < n1)
+        rope_element(idx, x1, pos_index, ct, st, out1, heads1, head_dim, rotary_dim, 0, inverse);
+    else if (idx - n1 < tokens * heads2 * per_head)
+        rope_element(idx - n1, x2, pos_index, ct, st, out2, heads2, head_dim, rotary_dim, 0, inverse);
 }
 
 __global__ __launch_bounds__(256) void silu_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t n) {
@@ -544,6 +569,18 @@ int launch_rope_tables(const int64_t* positions, int64_t n, const double* inv_fr
     return check_launch("rope_tables");
 }
 
+int launch_rope_pair(const float* x1, float* out1, int64_t heads1, const float* x2, float* out2, int64_t heads2,
+                     const int64_t* pos_index, const double* cos_table, const double* sin_table, int64_t tokens,
+                     int64_t head_dim, int64_t rotary_dim, int inverse, hipStream_t stream) {
+    DLLM_REQUIRE(rotary_dim % 2 == 0 && rotary_dim <= head_dim, "rotary_dim must be even and at most head_dim");
+    const int64_t n = tokens * (heads1 + heads2) * (rotary_dim / 2 + head_dim - rotary_dim);
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(rope_pair_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream, x1, out1,
+                       heads1, x2, out2, heads2, pos_index, cos_table, sin_table, tokens, head_dim, rotary_dim,
+                       inverse);
+    return check_launch("rope");
+}
+
 int launch_rope(const float* x, const int64_t* pos_index, const double* cos_table, const double* sin_table,
                 float* out, int64_t tokens, int64_t heads, int64_t head_dim, int64_t rotary_dim, int interleaved,
                 int inverse, hipStream_t stream) {
@@ -647,6 +684,22 @@ int launch_swiglu_backward(const float* gate, const float* up, const float* gate
         hipLaunchKernelGGL(swiglu_backward_kernel, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
                            up + d, gate_act + d, dproduct + d, dgate + d, dup + d, n - d);
     return check_launch("swiglu_backward");
+}
+
+// out = (a + b) + c, elementwise in float (c may be null: a + b).
+__global__ __launch_bounds__(256) void add3_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                   const float* __restrict__ c, float* __restrict__ out, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const float ab = a[i] + b[i];
+        out[i] = c ? ab + c[i] : ab;
+    }
+}
+
+int launch_add3(const float* a, const float* b, const float* c, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(add3_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, a, b, c, out, n);
+    return check_launch("add3");
 }
 
 int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream) {

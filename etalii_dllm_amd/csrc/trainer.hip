@@ -257,6 +257,8 @@ struct dllm_hip_trainer {
     int8_t* q8_values = nullptr;
     float* q8_scales = nullptr;
     uint8_t* q4_packed = nullptr;  // a Q4_0 base: the packed values before unpacking
+    char* staging = nullptr;       // pinned host memory: a step's inputs on their way to the device
+    size_t staging_bytes = 0;
     // attention as batched matmuls (attn_lds.hip, attn_chains.hip): per (window, head) transposed operands and score
     // matrices
     int64_t Tp = 0;
@@ -547,6 +549,9 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&grp_out, R));
         DLLM_TRY(make(&addrow, W_max * V));
         DLLM_TRY(make(&err_flag, 1));
+        staging_bytes = static_cast<size_t>(8 * (7 * R_max + 5 * W_max + 8) + 4 * W_max * V) + 9 * 256;
+        DLLM_TRY(check_hip(hipHostMalloc(reinterpret_cast<void**>(&staging), staging_bytes, hipHostMallocDefault),
+                           "pinned staging"));
         // RoPE tables for positions 0 .. T_max - 1 (every window starts at position 0)
         hipLaunchKernelGGL(inv_freq_kernel, dim3(1), dim3(1024), 0, nullptr, c.rotary_dim, c.rope_theta, inv_freq);
         DLLM_TRY(check_launch("inv_freq"));
@@ -1122,8 +1127,8 @@ struct dllm_hip_trainer {
             qsrc = sv.qn;
             ksrc = sv.kn;
         }
-        DLLM_TRY(launch_rope(qsrc, pos_index, cos_t, sin_t, sv.q, R, c.heads, c.head_dim, c.rotary_dim, 0, 0, s));
-        DLLM_TRY(launch_rope(ksrc, pos_index, cos_t, sin_t, sv.k, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 0, s));
+        DLLM_TRY(launch_rope_pair(qsrc, sv.q, c.heads, ksrc, sv.k, c.kv_heads, pos_index, cos_t, sin_t, R, c.head_dim,
+                                  c.rotary_dim, 0, s));
         DLLM_TRY(attention_forward(l, sv, b, s));
         DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
         DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
@@ -1179,8 +1184,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(side_mark(kSideO));
         DLLM_TRY(side_wait(kSideQkv, s));  // the previous layer's q/k/v dW read dq, dk (dq2, dk2) and dv_t
         DLLM_TRY(attention_backward(l, sv, b, s));
-        DLLM_TRY(launch_rope(dq_t, pos_index, cos_t, sin_t, dq, R, c.heads, c.head_dim, c.rotary_dim, 0, 1, s));
-        DLLM_TRY(launch_rope(dk_t, pos_index, cos_t, sin_t, dk, R, c.kv_heads, c.head_dim, c.rotary_dim, 0, 1, s));
+        DLLM_TRY(launch_rope_pair(dq_t, dq, c.heads, dk_t, dk, c.kv_heads, pos_index, cos_t, sin_t, R, c.head_dim,
+                                  c.rotary_dim, 1, s));
         const float* dqf = dq;
         const float* dkf = dk;
         if (c.qk_norm == 1) {
@@ -1217,8 +1222,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(side_mark(kSideQkv));
         if (grp_on[kGrpQkvDx] && grp_rows == R) {
             DLLM_TRY(group_launch(l, kGrpQkvDx, s));
-            DLLM_TRY(launch_add(dh, dh_b, dh, R * H, s));  // (dh_q + dh_k) + dh_v
-            DLLM_TRY(launch_add(dh, dh_c, dh, R * H, s));
+            DLLM_TRY(launch_add3(dh, dh_b, dh_c, dh, R * H, s));  // (dh_q + dh_k) + dh_v
         } else {
             for (int p = 0; p < 3; ++p) DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
         }
@@ -1437,15 +1441,25 @@ struct dllm_hip_trainer {
         batch.insert(batch.end(), ql.begin(), ql.end());
         batch.insert(batch.end(), qs.begin(), qs.end());
         batch.insert(batch.end(), ql.begin(), ql.end());
-        DLLM_TRY(check_hip(hipMemcpy(tok_in, in.data(), R * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(tok_tgt, tgt.data(), R * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(pos_index, pos.data(), R * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(seg_d, seg.data(), seg.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(batch_d, batch.data(), batch.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(grp_order, order.data(), order.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(grp_start, starts.data(), starts.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(grp_out, outs.data(), outs.size() * 8, hipMemcpyHostToDevice), "upload"));
-        DLLM_TRY(check_hip(hipMemcpy(addrow, amap.data(), amap.size() * sizeof(int), hipMemcpyHostToDevice), "upload"));
+        // the step's inputs through the pinned staging buffer, copied on the stream (the previous step, which read
+        // the device copies and the staging buffer, has been waited for)
+        size_t staged = 0;
+        auto upload = [&](void* dst, const void* src, size_t bytes) -> int {
+            DLLM_REQUIRE(staged + bytes <= staging_bytes, "step inputs exceed the staging buffer");
+            memcpy(staging + staged, src, bytes);
+            const int rc = check_hip(hipMemcpyAsync(dst, staging + staged, bytes, hipMemcpyHostToDevice, s), "upload");
+            staged += (bytes + 255) & ~size_t{255};
+            return rc;
+        };
+        DLLM_TRY(upload(tok_in, in.data(), R * 8));
+        DLLM_TRY(upload(tok_tgt, tgt.data(), R * 8));
+        DLLM_TRY(upload(pos_index, pos.data(), R * 8));
+        DLLM_TRY(upload(seg_d, seg.data(), seg.size() * 8));
+        DLLM_TRY(upload(batch_d, batch.data(), batch.size() * 8));
+        DLLM_TRY(upload(grp_order, order.data(), order.size() * 8));
+        DLLM_TRY(upload(grp_start, starts.data(), starts.size() * 8));
+        DLLM_TRY(upload(grp_out, outs.data(), outs.size() * 8));
+        DLLM_TRY(upload(addrow, amap.data(), amap.size() * sizeof(int)));
         b->q_start = batch_d;
         b->q_len = batch_d + windows;
         b->kv_start = batch_d + 2 * windows;
@@ -1922,6 +1936,7 @@ int dllm_hip_trainer_destroy(dllm_hip_trainer* t) {
     if (t) {
         (void)hipDeviceSynchronize();
         for (hipEvent_t e : t->events) (void)hipEventDestroy(e);
+        if (t->staging) (void)hipHostFree(t->staging);
         if (t->side) {
             (void)hipEventDestroy(t->side_fork);
             for (hipEvent_t e : t->side_done) (void)hipEventDestroy(e);
