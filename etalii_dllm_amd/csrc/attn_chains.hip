@@ -5,7 +5,8 @@
 // contiguous across queries: the chains run one lane per query over keys ascending, with coalesced loads.
 //
 //   forward   E^T = exp(S^T - max_t), total_t serial, inv_t = 1 / total_t       (one kernel; max_t from the score
-//             tiles' maxima when the scores kernel provides them, else a first walk)
+//             tiles' maxima when the scores kernel provides them, else a first walk; small launches split it into
+//             maximum, exps and totals)
 //   backward  D_t = sum over keys ascending of (e inv_t) dp (serial); p = e inv_t, dS = p (dp - D_t) scale
 //             elementwise, dS written over dP^T and p, dS in the key-row layout dk / dv read (two kernels: a fused
 //             one, a wave per 64 queries, measured slower, its LDS tiles limiting it to one wave per SIMD; so was
@@ -236,6 +237,83 @@ __global__ __launch_bounds__(256) void dsoftmax_apply_regroup_kernel(
     }
 }
 
+// Small launches (few windows x heads x 64-query blocks leave most of the GPU idle with one lane per query): the
+// forward softmax splits so that its exps spread over the GPU. The maximum first (one lane per query, into the inv
+// slot), then e = exp(s - mx) over S^T by one thread per key run, then one lane per query adds the e in key order and
+// writes inv = 1 / total over the maximum. The same values and the same serial sums. (Split the same way, the
+// backward's D chain measured no faster at T = 256: its terms are one multiply each.)
+constexpr int64_t kSplitChainsBelow = 512;  // windows x heads x 64-query blocks
+constexpr int kTermKeys = 32;                // keys per workgroup of the exp kernel (8 per wave)
+
+__global__ __launch_bounds__(64) void softmax_max_kernel(const double* __restrict__ st, int64_t ld, int64_t zstride,
+                                                         const int64_t* __restrict__ seg, int64_t heads,
+                                                         int64_t window, double* __restrict__ mx_out,
+                                                         int64_t inv_zstride, const double* __restrict__ tile_max,
+                                                         int64_t tm_zstride, int64_t tm_ld) {
+    const int64_t z = blockIdx.y;
+    const int64_t n = seg[z / heads + 1] - seg[z / heads];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (t >= n) return;
+    int64_t lo, hi;
+    query_span(t, n, window, &lo, &hi);
+    const double first = st[z * zstride + lo * ld + t];
+    double mx = first;
+    if (first == first) {
+        const double* tm = tile_max + z * tm_zstride + t;
+        mx = -__builtin_huge_val();
+        for (int64_t k = lo / 64; k <= (hi - 1) / 64; ++k) {
+            const double m = tm[k * tm_ld];
+            if (m > mx) mx = m;
+        }
+    }
+    mx_out[z * inv_zstride + t] = mx;
+}
+
+__global__ __launch_bounds__(256) void softmax_exp_kernel(double* __restrict__ st, int64_t ld, int64_t zstride,
+                                                          const int64_t* __restrict__ seg, int64_t heads,
+                                                          int64_t window, const double* __restrict__ mx_in,
+                                                          int64_t inv_zstride) {
+    const int64_t z = blockIdx.z;
+    const int64_t n = seg[z / heads + 1] - seg[z / heads];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + (threadIdx.x & 63);
+    const int64_t j0 = static_cast<int64_t>(blockIdx.y) * kTermKeys + (threadIdx.x >> 6) * (kTermKeys / 4);
+    if (t >= n) return;
+    int64_t lo, hi;
+    query_span(t, n, window, &lo, &hi);
+    if (j0 >= hi || j0 + kTermKeys / 4 <= lo) return;
+    const double mx = mx_in[z * inv_zstride + t];
+    double* s = st + z * zstride + t;
+#pragma unroll
+    for (int k = 0; k < kTermKeys / 4; ++k) {
+        const int64_t j = j0 + k;
+        if (j >= lo && j < hi) s[j * ld] = dexp(s[j * ld] - mx);
+    }
+}
+
+__global__ __launch_bounds__(64) void softmax_total_kernel(const double* __restrict__ et, int64_t ld, int64_t zstride,
+                                                           const int64_t* __restrict__ seg, int64_t heads,
+                                                           int64_t window, double* __restrict__ inv,
+                                                           int64_t inv_zstride) {
+    const int64_t z = blockIdx.y;
+    const int64_t n = seg[z / heads + 1] - seg[z / heads];
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    if (t >= n) return;
+    int64_t lo, hi;
+    query_span(t, n, window, &lo, &hi);
+    const double* e = et + z * zstride + t;
+    double total = 0.0;
+    int64_t j = lo;
+    for (; j + kChainUnroll <= hi; j += kChainUnroll) {
+        double v[kChainUnroll];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) v[k] = e[(j + k) * ld];
+#pragma unroll
+        for (int k = 0; k < kChainUnroll; ++k) total += v[k];
+    }
+    for (; j < hi; ++j) total += e[j * ld];
+    inv[z * inv_zstride + t] = 1.0 / total;
+}
+
 // Per (window, head): dst[i][t] = src[(seg[w] + t) * row_stride + head * head_dim + i], as double or float.
 template <typename T>
 __global__ __launch_bounds__(256) void heads_transpose_kernel(const float* __restrict__ src, int64_t row_stride,
@@ -269,7 +347,16 @@ int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* 
                         const double* tile_max, int64_t tile_max_zstride, int64_t tile_max_ld) {
     if (max_len == 0 || windows * heads == 0) return kOk;
     const dim3 lanes(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(windows * heads));
-    if (tile_max)
+    if (tile_max && windows * heads * ceil_div(max_len, 64) < kSplitChainsBelow) {
+        const dim3 terms(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(ceil_div(max_len, kTermKeys)),
+                         static_cast<unsigned>(windows * heads));
+        hipLaunchKernelGGL(softmax_max_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
+                           inv_zstride, tile_max, tile_max_zstride, tile_max_ld);
+        hipLaunchKernelGGL(softmax_exp_kernel, terms, dim3(256), 0, stream, st, ld, zstride, seg, heads, window, inv,
+                           inv_zstride);
+        hipLaunchKernelGGL(softmax_total_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
+                           inv_zstride);
+    } else if (tile_max)
         hipLaunchKernelGGL(softmax_tiles_kernel, lanes, dim3(64), 0, stream, st, ld, zstride, seg, heads, window, inv,
                            inv_zstride, tile_max, tile_max_zstride, tile_max_ld);
     else
