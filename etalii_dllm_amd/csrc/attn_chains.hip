@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void dsoftmax_apply_regroup_kernel(
 // slot), then e = exp(s - mx) over S^T by one thread per key run, then one lane per query adds the e in key order and
 // writes inv = 1 / total over the maximum. The same values and the same serial sums. (Split the same way, the
 // backward's D chain measured no faster at T = 256: its terms are one multiply each.)
-constexpr int64_t kSplitChainsBelow = 512;  // windows x heads x 64-query blocks
+constexpr int64_t kSplitChainsBelow = 512;  // windows x heads x 64-query blocks (more: one walk, measured faster)
 constexpr int kTermKeys = 32;                // keys per workgroup of the exp kernel (8 per wave)
 
 __global__ __launch_bounds__(64) void softmax_max_kernel(const double* __restrict__ st, int64_t ld, int64_t zstride,
