@@ -202,6 +202,7 @@ struct dllm_hip_trainer {
     int64_t* counts_d = nullptr;
     std::vector<int64_t> counts_host;  // [windows][E] choices per window over all layers
     double router_scale_cur = 0.0, last_router_loss = 0.0;
+    double *inv_mlp = nullptr, *inv_attn = nullptr;  // the layer norms' inverse rms, read by their weights' gradients
     double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
            *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
     void* attn_ws = nullptr;
@@ -513,13 +514,16 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&dgate, dmlp));
         DLLM_TRY(make(&dup, dmlp));
         DLLM_TRY(make(&col_part, W_max * std::max<int64_t>({H, QD, KVD, I})));
-        DLLM_TRY(make(&col_part_side, W_max * std::max<int64_t>({QD, KVD})));
+        DLLM_TRY(make(&col_part_side, W_max * std::max<int64_t>({H, QD, KVD})));
         if (W_max > 1) {
             gemm_part_cap = W_max * H * std::max<int64_t>({QD, KVD, I, EI, E});
             DLLM_TRY(make(&gemm_part, gemm_part_cap));
         }
         DLLM_TRY(make(&emb_rows, R * H));
         DLLM_TRY(make(&inv_rms, R * std::max<int64_t>(heads, 1)));
+        DLLM_TRY(make(&inv_mlp, R));
+        DLLM_TRY(make(&inv_attn, R));
+        DLLM_TRY(make(&dh1, R * H));
         DLLM_TRY(make(&row_max, R));
         DLLM_TRY(make(&row_total, R));
         DLLM_TRY(make(&row_loss, R));
@@ -643,7 +647,7 @@ struct dllm_hip_trainer {
     // buffer the batch reads. The stream is joined before the embedding gradients and the optimizer, which read every
     // gradient, and before the next step's forward rewrites the saved activations. While the matmuls are being timed
     // everything stays on the caller's stream, so each launch is timed alone.
-    enum SideEvent { kSideDown, kSideMlp, kSideO, kSideQkv, kSideJoin, kSideEvents };
+    enum SideEvent { kSideDown, kSideMlp, kSideO, kSideQkv, kSideNormMlp, kSideNormAttn, kSideJoin, kSideEvents };
     hipStream_t side = nullptr;
     // a third stream for the attention backward's dq, which runs beside dk and dv (independent inputs and outputs)
     hipStream_t aux = nullptr;
@@ -801,6 +805,7 @@ struct dllm_hip_trainer {
     std::vector<double> grp_flops;       // algorithmic flop of each group (matmul timing)
     int64_t grp_rows = -1;               // the row count the tables were prepared for
     float *dh_b = nullptr, *dh_c = nullptr;
+    float* dh1 = nullptr;  // the attention block's input gradient (dh holds the MLP block's)
 
     const GemmGroup& group_of(int64_t l, int kind) const { return grp[static_cast<size_t>(l * kLayerGroups + kind)]; }
     const char* table_of(int64_t l, int kind) const {
@@ -838,7 +843,7 @@ struct dllm_hip_trainer {
                     calls[nc++] = dx_call(dgate, R, L.gate, dh, nullptr);
                     calls[nc++] = dx_call(dup, R, L.up, dh_b, nullptr);
                 } else {
-                    calls[nc++] = dx_call(dqf, R, L.q, dh, nullptr);
+                    calls[nc++] = dx_call(dqf, R, L.q, dh1, nullptr);
                     calls[nc++] = dx_call(dkf, R, L.k, dh_b, nullptr);
                     calls[nc++] = dx_call(dv_t, R, L.v, dh_c, nullptr);
                 }
@@ -965,7 +970,8 @@ struct dllm_hip_trainer {
         if (!grad_wanted(out)) return kOk;
         std::vector<int64_t> seg(seg_host.size());
         for (size_t i = 0; i < seg.size(); ++i) seg[i] = seg_host[i] * rows_per_token;
-        return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, col_part, out, s, window_weights(), colscale);
+        return launch_column_sums(1, dyv, x, inv, dim, seg.data(), nseg, s == side && side_on ? col_part_side : col_part,
+                                  out, s, window_weights(), colscale);
     }
 
     // ---- attention (attn_lds.hip, attn_chains.hip) ----
@@ -1151,7 +1157,8 @@ struct dllm_hip_trainer {
         const double eps = c.rms_norm_eps;
         hipStream_t ws = s;  // the stream of the weight-gradient batches
         if (E > 0) {
-            DLLM_TRY(side_wait(kSideMlp, s));  // the previous layer's router dW reads dlogits_r
+            DLLM_TRY(side_wait(kSideMlp, s));      // the previous layer's router dW reads dlogits_r
+            DLLM_TRY(side_wait(kSideNormMlp, s));  // its mlp norm's dW reads dh
             DLLM_TRY(moe_backward(l, R, nseg, s));
         } else {
             // SwiGLU (backprop.py:289-306)
@@ -1165,6 +1172,7 @@ struct dllm_hip_trainer {
             DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, ws));
             DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, ws));
             DLLM_TRY(side_mark(kSideMlp));
+            DLLM_TRY(side_wait(kSideNormMlp, s));  // the previous layer's mlp norm dW reads dh
             if (grp_on[kGrpMlpDx] && grp_rows == R) {
                 DLLM_TRY(group_launch(l, kGrpMlpDx, s));
                 DLLM_TRY(launch_add(dh, dh_b, dh, R * H, s));  // dh2 = dx_gate + dx_up
@@ -1175,8 +1183,10 @@ struct dllm_hip_trainer {
         }
         // mlp norm; dx_mid = dx + dh2'
         DLLM_TRY(side_wait(kSideO, s));  // the previous layer's o dW reads dx_mid
-        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_rms, s));
-        DLLM_TRY(norm_dw(dh, sv.x_mid, inv_rms, H, 1, nseg, G(L.mlp_norm), s));
+        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_mlp, s));
+        DLLM_TRY(side_fork_from(s, &ws));
+        DLLM_TRY(norm_dw(dh, sv.x_mid, inv_mlp, H, 1, nseg, G(L.mlp_norm), ws));
+        DLLM_TRY(side_mark(kSideNormMlp));
         // attention output projection
         DLLM_TRY(linear_dx(dx_mid, R, L.o, dattended, nullptr, s));
         DLLM_TRY(side_fork_from(s, &ws));
@@ -1220,16 +1230,19 @@ struct dllm_hip_trainer {
                                             unfold_scale(bs_[p])));
         }
         DLLM_TRY(side_mark(kSideQkv));
+        DLLM_TRY(side_wait(kSideNormAttn, s));  // the previous layer's attention norm dW reads dh1
         if (grp_on[kGrpQkvDx] && grp_rows == R) {
             DLLM_TRY(group_launch(l, kGrpQkvDx, s));
-            DLLM_TRY(launch_add3(dh, dh_b, dh_c, dh, R * H, s));  // (dh_q + dh_k) + dh_v
+            DLLM_TRY(launch_add3(dh1, dh_b, dh_c, dh1, R * H, s));  // (dh_q + dh_k) + dh_v
         } else {
-            for (int p = 0; p < 3; ++p) DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh, p == 0 ? nullptr : dh, s));
+            for (int p = 0; p < 3; ++p) DLLM_TRY(linear_dx(ds[p], R, ws_[p], dh1, p == 0 ? nullptr : dh1, s));
         }
         // attention norm; dx = dx_mid + dh1'
         DLLM_TRY(side_wait(kSideDown, s));  // this layer's down dW reads dx
-        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh, dx, dx_mid, R, H, eps, 0, inv_rms, s));
-        return norm_dw(dh, sv.x_in, inv_rms, H, 1, nseg, G(L.attn_norm), s);
+        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh1, dx, dx_mid, R, H, eps, 0, inv_attn, s));
+        DLLM_TRY(side_fork_from(s, &ws));
+        DLLM_TRY(norm_dw(dh1, sv.x_in, inv_attn, H, 1, nseg, G(L.attn_norm), ws));
+        return side_mark(kSideNormAttn);
     }
 
     // ---- routed experts (backprop.py:308-377, 501-527) ----
