@@ -848,7 +848,8 @@ struct dllm_hip_trainer {
                     calls[nc++] = dx_call(dv_t, R, L.v, dh_c, nullptr);
                 }
                 bool ok = true;
-                for (int i = 0; i < nc; ++i) ok = ok && calls[i].J % 4 == 0 && calls[i].ldb % 4 == 0;
+                for (int i = 0; i < nc; ++i)
+                    ok = ok && calls[i].J % 4 == 0 && calls[i].ldb % 4 == 0 && calls[i].a_kind == calls[0].a_kind;
                 GemmGroup& g = grp[static_cast<size_t>(l * kLayerGroups + k)];
                 const size_t gi = static_cast<size_t>(l * kLayerGroups + k);
                 if (ok) DLLM_TRY(gemm_group_prepare(calls, nc, kGroupCap, host.data() + gb * gi, &g));
@@ -1609,10 +1610,12 @@ struct dllm_hip_trainer {
         DLLM_TRY(scale_decay(o, a->weight_decay));
         DLLM_TRY(launch_adamw(o.p, o.g, o.m, o.v, o.chunk_start, o.chunk_end, o.chunk_decay_scaled, o.chunks, args,
                               stats + 2, s));
-        if (lora_on)
+        if (lora_on) {
             merged_valid = false;  // the next step merges the updated adapters
-        else
+        } else {
+            if (fold_on) DLLM_TRY(fold_weights(s));  // the folded copies of the updated q/k rows (or QK-norm weights)
             DLLM_TRY(refresh_transposes(s));
+        }
         double st[3];
         DLLM_TRY(check_hip(hipMemcpyAsync(st, stats, sizeof st, hipMemcpyDeviceToHost, s), "download"));
         DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));

@@ -496,17 +496,20 @@ def test_step_with_rope_scaling_matches_the_oracle(case):
         params = {n: a.copy() for n, a in weights.items()}
         m = {n: np.zeros_like(a) for n, a in params.items()}
         v = {n: np.zeros_like(a) for n, a in params.items()}
-        for step in (1, 2):
+        # the parameters are read back only after the last step (reading them marks them as written, which would
+        # rebuild the folded copies before the next step whatever the step itself keeps up to date)
+        for step in (1, 2, 3):
             loss_gpu, norm_gpu = t.step(windows, 1e-3, step, router_aux_loss=0.02 if d.experts else 0.0)
-            loss_cpu, _, norm_cpu, grads = O.train_step(O.oracle_kernels(), od, params, m, v, windows, opt, step, 2,
+            loss_cpu, _, norm_cpu, grads = O.train_step(O.oracle_kernels(), od, params, m, v, windows, opt, step, 3,
                                                         router_aux_loss=0.02 if d.experts else 0.0)
             assert loss_gpu == loss_cpu and norm_gpu == norm_cpu, (step, loss_gpu, loss_cpu)
             for name in t.names:
                 shape = d.tensor_shapes()[name]
                 assert t.get(name, shape, t.GRAD).tobytes() == grads[name].tobytes(), (step, name)
-                assert t.get(name, shape).tobytes() == params[name].tobytes(), (step, name)
                 assert t.get(name, shape, t.M).tobytes() == m[name].tobytes(), (step, name)
                 assert t.get(name, shape, t.V).tobytes() == v[name].tobytes(), (step, name)
+        for name in t.names:
+            assert t.get(name, d.tensor_shapes()[name]).tobytes() == params[name].tobytes(), name
     else:
         adapters = O.init_adapters(d, lora, 5)
         for name in adapters:
