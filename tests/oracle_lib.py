@@ -362,6 +362,14 @@ class Decoder:
     rotary_dim: int = 0  # 0: head_dim (partial rotary: the first rotary_dim dimensions of each head rotate)
     inv_freq: tuple[float, ...] | None = None  # scaled inverse frequencies (rope_scaling), rotary_dim / 2 of them
     rope_attention_factor: float = 1.0  # LongRoPE / YaRN attention factor folded into the q/k rows
+    # a Hugging Face rope_scaling dict as (key, value) pairs (lists as tuples); without inv_freq, the frequencies are
+    # computed from it when the configuration is handed to the oracle
+    rope_scaling: tuple | None = None
+
+    def scaling(self) -> dict | None:
+        if not self.rope_scaling:
+            return None
+        return {k: list(v) if isinstance(v, tuple) else v for k, v in self.rope_scaling}
 
     @property
     def attention_scale(self) -> float:
@@ -372,8 +380,11 @@ class Decoder:
                         int(self.attn_bias), self.qk_norm, self.window, int(self.tied), self.experts, self.topk,
                         int(self.normalize), self.expert_inter or self.inter, self.rotary_dim or self.head_dim,
                         self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor)
-        if self.inv_freq is not None:
-            table = np.ascontiguousarray(self.inv_freq, dtype=np.float64)
+        inv_freq = self.inv_freq
+        if inv_freq is None and self.rope_scaling:
+            inv_freq = rope_inv_freq_scaled(self.rotary_dim or self.head_dim, self.rope_theta, self.scaling())
+        if inv_freq is not None:
+            table = np.ascontiguousarray(inv_freq, dtype=np.float64)
             assert table.size == (self.rotary_dim or self.head_dim) // 2
             cfg.inv_freq = table.ctypes.data
             cfg._keep = table  # the table must outlive the call that reads it
@@ -448,6 +459,16 @@ def tensor_order(names) -> list[str]:
 
 TINY = dict(vocab=64, hidden=16, inter=32, layers=2, heads=4, kv_heads=2, head_dim=4, eps=1e-5, rope_theta=1e5)
 
+def frozen_scaling(scaling: dict) -> tuple:
+    return tuple((k, tuple(v) if isinstance(v, list) else v) for k, v in scaling.items())
+
+
+# Phi-3's tiny config (tests/model_fixtures.py tiny_config): LongRoPE as the importer reads it (_longrope_from_hf:
+# the short factors unless the model file asks for the long ones, the given attention factor), half of each head
+# rotated, a 3-token window, hidden 32 (so head_dim 8), untied
+PHI3_SCALING = {"rope_type": "longrope", "short_factor": [4.0, 1.0], "long_factor": [2.0, 4.0],
+                "original_max_position_embeddings": 64, "attention_factor": 4.0}
+
 # tests/model_fixtures.py:38-171 and the importer's reading of them (importing/importer.py:291-343)
 FIXTURES = {
     "llama": Decoder("llama", tied=True, **TINY),
@@ -457,6 +478,8 @@ FIXTURES = {
     "mixtral": Decoder("mixtral", tied=False, experts=4, topk=2, normalize=True, **TINY),
     "olmoe": Decoder("olmoe", tied=False, qk_norm=2, experts=4, topk=2, normalize=False,
                      **{**TINY, "inter": 8}),
+    "phi3": Decoder("phi3", tied=False, window=3, rotary_dim=4, rope_attention_factor=4.0,
+                    rope_scaling=frozen_scaling(PHI3_SCALING), **{**TINY, "hidden": 32, "head_dim": 8}),
 }
 
 

@@ -190,7 +190,7 @@ def yarn_scaling(factor: float, original: int) -> dict:
             "attention_factor": 0.1 * 1.0 * O.oracle().orc_log(factor) + 1.0 if factor > 1.0 else 1.0}
 
 
-@pytest.mark.parametrize("family", ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe"])
+@pytest.mark.parametrize("family", sorted(O.FIXTURES))
 def test_forward_logits_match_tiny_logits_fingerprint(family):
     """The next-token logits of PROMPT on the tiny imported models (golden_values.py TINY_LOGITS_FINGERPRINT)."""
     d = O.FIXTURES[family]
@@ -214,6 +214,18 @@ def test_yarn_models_match_long_context_fingerprints(name, family, factor, origi
                      rope_attention_factor=scaling["attention_factor"])
     logits = O.logits(O.oracle_kernels(), scaled, O.fixture_weights(d), PROMPT)
     assert O.fingerprint(logits[-1]) == GOLDEN["LONG_CONTEXT_FINGERPRINTS"][name]
+
+
+def test_phi3_long_factors_match_the_long_context_fingerprint():
+    """reference tests/test_long_context.py:113-118,160 ("phi3-long"): Phi-3 imported with a 1024-token context takes
+    the LongRoPE long factors (factor_set "long"), the attention factor unchanged; its logits of PROMPT."""
+    from dataclasses import replace
+
+    d = O.FIXTURES["phi3"]
+    long = replace(d, rope_scaling=O.frozen_scaling({**O.PHI3_SCALING, "factor_set": "long"}))
+    assert long.c().rope_attention_factor == d.c().rope_attention_factor
+    logits = O.logits(O.oracle_kernels(), long, O.fixture_weights(d), PROMPT)
+    assert O.fingerprint(logits[-1]) == GOLDEN["LONG_CONTEXT_FINGERPRINTS"]["phi3-long"]
 
 
 def test_rope_scaling_closed_forms():
