@@ -118,6 +118,8 @@ int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
                            float* dgate, float* dup, int64_t n, hipStream_t stream);
 int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream);
+// x = f32(x * f), or f32(x / f) with divide, in place
+int launch_scale(float* x, int64_t n, float f, bool divide, hipStream_t stream);
 int launch_add3(const float* a, const float* b, const float* c, float* out, int64_t n, hipStream_t stream);
 int launch_gather_rows(const float* table, const int64_t* index, float* out, int64_t rows, int64_t dim,
                        hipStream_t stream);

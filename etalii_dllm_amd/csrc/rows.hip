@@ -702,6 +702,23 @@ int launch_add3(const float* a, const float* b, const float* c, float* out, int6
     return check_launch("add3");
 }
 
+// x = f32(x * f) or f32(x / f) in place (numpy's float32 array times or over np.float32): the product or quotient
+// formed in double and rounded once, which is the correctly rounded float result (a float product is exact in double;
+// a double quotient of floats rounds to the float quotient, 53 >= 2 * 24 + 2 bits).
+__global__ __launch_bounds__(256) void scale_kernel(float* __restrict__ x, int64_t n, float f, int divide) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const double v = static_cast<double>(x[i]);
+        x[i] = static_cast<float>(divide ? v / static_cast<double>(f) : v * static_cast<double>(f));
+    }
+}
+
+int launch_scale(float* x, int64_t n, float f, bool divide, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(scale_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, n, f, divide ? 1 : 0);
+    return check_launch("scale");
+}
+
 int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream) {
     if (n == 0) return kOk;
     hipLaunchKernelGGL(add_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, a, b, out, n);

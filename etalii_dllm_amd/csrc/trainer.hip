@@ -22,6 +22,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <map>
 #include <memory>
@@ -111,15 +112,15 @@ struct TensorInfo {
     int64_t wt_offset = -1;  // transposed copy for the forward matmul, if it is a linear weight
 };
 
-// fold_scales' RoPE attention factor (transformer.py:212-245): dst = src with the entries of every row r whose
-// (r % head_dim) < rotary_dim multiplied by the float factor; rows of `cols` elements (1 for vectors).
-__global__ void rope_fold_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n, int64_t cols,
-                                 int64_t head_dim, int64_t rotary_dim, float factor) {
+// fold_scales (transformer.py:212-245): dst = src with every entry of row r times the float rowscale[r]; rows of
+// `cols` elements (1 for vectors). The RoPE attention factor's table holds the factor on the rows feeding rotated
+// dimensions ((r % head_dim) < rotary_dim) and 1 elsewhere (x * 1 is x); the residual multiplier's holds it on every
+// row.
+__global__ void fold_rows_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n, int64_t cols,
+                                 const float* __restrict__ rowscale) {
     for (int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; e < n;
-         e += static_cast<int64_t>(gridDim.x) * 256) {
-        const int64_t r = e / cols;
-        dst[e] = (r % head_dim) < rotary_dim ? src[e] * factor : src[e];
-    }
+         e += static_cast<int64_t>(gridDim.x) * 256)
+        dst[e] = src[e] * rowscale[e / cols];
 }
 
 // rope_inv_freq (numerics.py:267-297, default scaling): exp(-(2i / dim) log(theta)) with the portable exp and log.
@@ -244,14 +245,17 @@ struct dllm_hip_trainer {
     }
     DevBuf lora_p, lora_g, lora_m, lora_v, merged;
     std::vector<int64_t> merged_offset;  // per tensor id: offset in `merged`, or -1
-    // The LongRoPE / YaRN attention factor (fold_scales, transformer.py:224-245): the step reads the q/k rows feeding
-    // the rotated dimensions (or the QK-norm entries) times the factor, from `folded`; each window's gradients of
-    // those tensors are multiplied by it again (_unfold, backprop.py:380-394) before the window sum.
+    // fold_scales (transformer.py:224-245): the step reads the q/k rows feeding the rotated dimensions (or the QK-norm
+    // entries) times the LongRoPE / YaRN attention factor, and the output and down projections times Granite's
+    // residual multiplier, from `folded`; each window's gradients of those tensors are multiplied by the same factors
+    // (_unfold, backprop.py:380-394) before the window sum.
     bool fold_on = false;
     double rope_factor = 1.0;
     DevBuf folded;
-    std::vector<int64_t> fold_offset;  // per tensor id: offset in `folded`, or -1
-    float* rope_rowscale = nullptr;    // [q heads x head_dim]: the factor on rotated entries, 1 elsewhere
+    std::vector<int64_t> fold_offset;      // per tensor id: offset in `folded`, or -1
+    std::vector<const float*> fold_table;  // per tensor id: its per-row factors, or null
+    float* rope_rowscale = nullptr;        // [q heads x head_dim]: the factor on rotated entries, 1 elsewhere
+    float* resid_rowscale = nullptr;       // [hidden]: the residual multiplier
     bool base_ready = true;              // the Q8_0 base has been applied to the current parameters
     void* lora_ws = nullptr;
     size_t lora_ws_bytes = 0;
@@ -573,23 +577,66 @@ struct dllm_hip_trainer {
         const int64_t fo = fold_offset.empty() ? -1 : fold_offset[static_cast<size_t>(id)];
         return fo >= 0 ? folded.as<float>() + fo : Psrc(id);
     }
-    // The per-row factors of a tensor's window gradients (the attention factor's unfold), or null
+    // The per-row factors of a tensor's window gradients (the unfold), or null
     const float* unfold_scale(int id) const {
-        return id >= 0 && !fold_offset.empty() && fold_offset[static_cast<size_t>(id)] >= 0 ? rope_rowscale : nullptr;
+        return id >= 0 && !fold_table.empty() ? fold_table[static_cast<size_t>(id)] : nullptr;
     }
 
-    // The folded copies of the rope-scaled tensors from their current values.
+    // The folded copies of the scaled tensors from their current values.
     int fold_weights(hipStream_t s) {
         for (size_t i = 0; i < tensors.size(); ++i) {
             if (fold_offset[i] < 0) continue;
             const TensorInfo& t = tensors[i];
             const int64_t cols = t.cols > 0 ? t.cols : 1;
             const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(t.numel, 256), 4096));
-            hipLaunchKernelGGL(rope_fold_kernel, dim3(blocks), dim3(256), 0, s, Psrc(static_cast<int>(i)),
-                               folded.as<float>() + fold_offset[i], t.numel, cols, c.head_dim, c.rotary_dim,
-                               static_cast<float>(rope_factor));
-            DLLM_TRY(check_launch("rope fold"));
+            hipLaunchKernelGGL(fold_rows_kernel, dim3(blocks), dim3(256), 0, s, Psrc(static_cast<int>(i)),
+                               folded.as<float>() + fold_offset[i], t.numel, cols, fold_table[i]);
+            DLLM_TRY(check_launch("fold"));
         }
+        return kOk;
+    }
+
+    bool residual_on() const { return c.residual_multiplier != 1.0; }
+
+    // Which tensors are folded and by which row factors: the rope-scaled ones (rope_scaled_tensors,
+    // transformer.py:204-209: the QK-norm weights, else the q/k projections and biases) when the attention factor is
+    // not 1, the "attention.o.weight" and "down.weight" tensors (every expert's) when the residual multiplier is not
+    // 1. The sets are disjoint.
+    int setup_fold() {
+        const bool rope = rope_factor != 1.0, resid = residual_on();
+        fold_offset.assign(tensors.size(), -1);
+        fold_table.assign(tensors.size(), nullptr);
+        int64_t off = 0;
+        auto add = [&](int id, const float* table) {
+            if (id < 0) return;
+            fold_offset[static_cast<size_t>(id)] = off;
+            fold_table[static_cast<size_t>(id)] = table;
+            off += static_cast<int64_t>(round_up(static_cast<size_t>(tensors[static_cast<size_t>(id)].numel), 64));
+        };
+        for (const LayerIds& L : layer_ids) {
+            if (rope) {
+                const int ids[4] = {c.qk_norm ? L.qn : L.q, c.qk_norm ? L.kn : L.k, c.qk_norm ? -1 : L.qb,
+                                    c.qk_norm ? -1 : L.kb};
+                for (int id : ids) add(id, rope_rowscale);
+            }
+            if (resid) {
+                add(L.o, resid_rowscale);
+                add(L.down, resid_rowscale);
+                for (int id : L.edown) add(id, resid_rowscale);
+            }
+        }
+        const size_t bytes = static_cast<size_t>(off > 0 ? off : 1) * sizeof(float);
+        if (off > 0 && folded.bytes < bytes) {
+            if (folded.p) DLLM_TRY(check_hip(hipFree(folded.p), "hipFree"));
+            folded.p = nullptr;
+            DLLM_TRY(folded.alloc(bytes));
+        }
+        fold_on = off > 0;
+        // the step's weight addresses changed: rebuild the transposes' job table and the qkv groups
+        wt_jobs = nullptr;
+        grp_rows = -1;
+        wt_valid = false;
+        merged_valid = false;
         return kOk;
     }
 
@@ -602,36 +649,14 @@ struct dllm_hip_trainer {
                                      hipMemcpyHostToDevice), "upload"));
         DLLM_TRY(launch_rope_tables(nullptr, T_max, inv_freq, c.rotary_dim / 2, cos_t, sin_t, nullptr));
         rope_factor = factor;
-        const bool want = factor != 1.0;
-        if (want && !fold_on) {
-            fold_offset.assign(tensors.size(), -1);
-            int64_t off = 0;
-            for (const LayerIds& L : layer_ids) {
-                const int ids[4] = {c.qk_norm ? L.qn : L.q, c.qk_norm ? L.kn : L.k, c.qk_norm ? -1 : L.qb,
-                                    c.qk_norm ? -1 : L.kb};
-                for (int id : ids) {
-                    if (id < 0) continue;
-                    fold_offset[static_cast<size_t>(id)] = off;
-                    off += static_cast<int64_t>(round_up(static_cast<size_t>(tensors[static_cast<size_t>(id)].numel), 64));
-                }
-            }
-            DLLM_TRY(folded.alloc(static_cast<size_t>(off > 0 ? off : 1) * sizeof(float)));
-            DLLM_TRY(make(&rope_rowscale, static_cast<size_t>(QD)));
-        }
-        if (want) {
+        if (factor != 1.0) {
+            if (!rope_rowscale) DLLM_TRY(make(&rope_rowscale, static_cast<size_t>(QD)));
             std::vector<float> rs(static_cast<size_t>(QD));
             for (int64_t i = 0; i < QD; ++i) rs[static_cast<size_t>(i)] = (i % c.head_dim) < c.rotary_dim ? static_cast<float>(factor) : 1.0f;
             DLLM_TRY(check_hip(hipMemcpy(rope_rowscale, rs.data(), rs.size() * sizeof(float), hipMemcpyHostToDevice),
                                "upload"));
-        } else if (fold_on) {
-            fold_offset.assign(tensors.size(), -1);
         }
-        fold_on = want;
-        // the step's weight addresses changed: rebuild the transposes' job table and the qkv groups
-        wt_jobs = nullptr;
-        grp_rows = -1;
-        wt_valid = false;
-        merged_valid = false;
+        DLLM_TRY(setup_fold());
         return check_hip(hipDeviceSynchronize(), "set_rope");
     }
     float* G(int id) const { return grads.as<float>() + tensors[static_cast<size_t>(id)].offset; }
@@ -1165,7 +1190,8 @@ struct dllm_hip_trainer {
             // SwiGLU (backprop.py:289-306)
             DLLM_TRY(linear_dx(dx, R, L.down, dproduct, nullptr, s));
             DLLM_TRY(side_fork_from(s, &ws));
-            DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, ws));
+            DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, ws, nullptr, -1,
+                               unfold_scale(L.down)));
             DLLM_TRY(side_mark(kSideDown));
             DLLM_TRY(side_wait(kSideMlp, s));  // the previous layer's gate and up dW read dgate, dup
             DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s));
@@ -1191,7 +1217,8 @@ struct dllm_hip_trainer {
         // attention output projection
         DLLM_TRY(linear_dx(dx_mid, R, L.o, dattended, nullptr, s));
         DLLM_TRY(side_fork_from(s, &ws));
-        DLLM_TRY(linear_dw(dx_mid, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, ws));
+        DLLM_TRY(linear_dw(dx_mid, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, ws, nullptr, -1,
+                           unfold_scale(L.o)));
         DLLM_TRY(side_mark(kSideO));
         DLLM_TRY(side_wait(kSideQkv, s));  // the previous layer's q/k/v dW read dq, dk (dq2, dk2) and dv_t
         DLLM_TRY(attention_backward(l, sv, b, s));
@@ -1329,6 +1356,7 @@ struct dllm_hip_trainer {
                         if (!grad_wanted(G(L.edown[e]))) continue;
                         g = dw_call(dyg + st * H, H, sv.product + st * EI, EI, static_cast<int>(nwin), G(L.edown[e]),
                                     nullptr, nullptr, es, n);
+                        g.seg_rowscale = unfold_scale(L.edown[e]);
                         break;
                     case kDxGate: g = dx_call(dgate + st * EI, n, L.egate[e], dxg + st * H, nullptr); break;
                     case kDwGate:
@@ -1506,6 +1534,8 @@ struct dllm_hip_trainer {
         const double eps = c.rms_norm_eps;
         // forward (backprop.py:411-490)
         DLLM_TRY(launch_gather_rows(P(emb), tok_in, saved[0].x_in, R, H, s));
+        if (c.embedding_multiplier != 1.0)
+            DLLM_TRY(launch_scale(saved[0].x_in, R * H, static_cast<float>(c.embedding_multiplier), false, s));
         for (int64_t l = 0; l < c.layers; ++l) {
             float* x_out = l + 1 < c.layers ? saved[static_cast<size_t>(l + 1)].x_in : x_final;
             DLLM_TRY(forward_layer(l, R, b, x_out, s));
@@ -1519,10 +1549,13 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_rms_norm(x_final, P(final_norm), hidden, R, H, eps, 0, nullptr, s));
         const int head = c.tie_embeddings ? emb : lm_head;
         DLLM_TRY(linear_fwd(hidden, R, H, head, nullptr, logits, nullptr, s));
-        // loss and the head (backprop.py:183-206)
+        // loss and the head (backprop.py:174-206): Granite's logits scaling divides the logits and their gradient
+        const bool logit_div = c.logits_scaling != 1.0;
+        if (logit_div) DLLM_TRY(launch_scale(logits, R * V, static_cast<float>(c.logits_scaling), true, s));
         DLLM_TRY(check_hip(hipMemsetAsync(err_flag, 0, sizeof(int), s), "memset"));
         DLLM_TRY(launch_cross_entropy(logits, tok_tgt, dlogits, R, V, scale, seg_d, nseg, row_max, row_total, row_loss,
                                       loss_w, err_flag, s));
+        if (logit_div) DLLM_TRY(launch_scale(dlogits, R * V, static_cast<float>(c.logits_scaling), true, s));
         if (dpo.on) DLLM_TRY(dpo_weights(windows, s));
         float* dhidden = dh;
         DLLM_TRY(linear_dx(dlogits, R, head, dhidden, nullptr, s));
@@ -1538,6 +1571,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(side_join(s));
         // embedding (backprop.py:112-117): per-window token rows, then the head's dW with them as the tied addend
         if (lora_on) return finish_gradients(windows, loss, router_loss, s);  // neither is adapted
+        if (c.embedding_multiplier != 1.0)  // backprop.py:110-111
+            DLLM_TRY(launch_scale(dx, R * H, static_cast<float>(c.embedding_multiplier), false, s));
         DLLM_TRY(launch_embedding_groups(dx, H, grp_order, grp_start, grp_out, groups, emb_rows, H, s));
         if (c.tie_embeddings) {
             DLLM_TRY(linear_dw(dlogits, V, hidden, H, nseg, G(emb), addrow, emb_rows, s));
@@ -1922,8 +1957,13 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
                  "vocabulary, hidden and intermediate sizes must be multiples of 4 (16-byte matmul operand chunks)");
     DLLM_REQUIRE(max_tokens > 0 && max_windows > 0 && max_window_tokens > 0, "capacities must be positive");
     DLLM_REQUIRE(max_tokens <= 65535, "at most 65535 tokens per step");
+    for (double m : {c.embedding_multiplier, c.residual_multiplier, c.logits_scaling})
+        DLLM_REQUIRE(m >= 0.0 && std::isfinite(m), "multipliers must be finite and non-negative (0: none)");
+    DLLM_REQUIRE(c.attention_scale > 0.0 && std::isfinite(c.attention_scale), "attention_scale must be positive");
     std::unique_ptr<dllm_hip_trainer> t(new dllm_hip_trainer());
     t->c = c;
+    for (double* m : {&t->c.embedding_multiplier, &t->c.residual_multiplier, &t->c.logits_scaling})
+        if (*m == 0.0) *m = 1.0;  // unset
     t->R_max = max_tokens;
     t->W_max = max_windows;
     t->T_max = max_window_tokens;
@@ -1939,6 +1979,13 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     DLLM_TRY(t->build_tensors());
     if (lora) DLLM_TRY(t->build_lora(*lora));
     DLLM_TRY(t->build_activations());
+    if (t->residual_on()) {
+        DLLM_TRY(t->make(&t->resid_rowscale, static_cast<size_t>(t->H)));
+        const std::vector<float> rs(static_cast<size_t>(t->H), static_cast<float>(t->c.residual_multiplier));
+        DLLM_TRY(check_hip(hipMemcpy(t->resid_rowscale, rs.data(), rs.size() * sizeof(float), hipMemcpyHostToDevice),
+                           "upload"));
+        DLLM_TRY(t->setup_fold());
+    }
     *out = t.release();
     return kOk;
 }

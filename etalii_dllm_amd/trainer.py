@@ -25,7 +25,8 @@ class DecoderConfig(C.Structure):
         "vocab", "hidden", "intermediate", "layers", "heads", "kv_heads", "head_dim", "attention_bias", "qk_norm",
         "sliding_window", "tie_embeddings", "experts", "experts_per_token", "normalize_expert_weights",
         "expert_intermediate", "rotary_dim")] + [
-        ("rms_norm_eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double)]
+        ("rms_norm_eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
+        ("embedding_multiplier", C.c_double), ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double)]
 
 
 class AdamWArgs(C.Structure):
@@ -100,7 +101,13 @@ class Decoder:
     normalize_expert_weights: bool = False
     expert_intermediate: int = 0  # 0: the intermediate size
     rotary_dim: int = 0  # 0: head_dim (partial rotary: only the first rotary_dim dimensions of each head rotate)
-    rope_scaling: dict | None = None  # a Hugging Face rope_scaling (linear, llama3, longrope, yarn), as the config's
+    rope_scaling: dict | None = None  # a Hugging Face rope_scaling dict (linear, llama3, longrope or yarn)
+    # Granite's multipliers (architecture.py's TransformerConfig, importer.py:427-434): attention_multiplier replaces
+    # the attention scale 1/sqrt(head_dim)
+    embedding_multiplier: float = 1.0
+    attention_multiplier: float | None = None
+    residual_multiplier: float = 1.0
+    logits_scaling: float = 1.0
 
     def native(self) -> DecoderConfig:
         return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
@@ -108,7 +115,9 @@ class Decoder:
                              int(self.tie_embeddings), self.experts, self.experts_per_token,
                              int(self.normalize_expert_weights), self.expert_intermediate,
                              self.rotary_dim or self.head_dim, self.rms_norm_eps, self.rope_theta,
-                             1.0 / float(np.sqrt(np.float64(self.head_dim))))
+                             1.0 / float(np.sqrt(np.float64(self.head_dim))) if self.attention_multiplier is None
+                             else self.attention_multiplier, self.embedding_multiplier, self.residual_multiplier,
+                             self.logits_scaling)
 
 
 def _windows(windows):

@@ -275,6 +275,11 @@ typedef struct {
     int64_t experts, experts_per_token, normalize_expert_weights, expert_intermediate; /* 0 experts: dense */
     int64_t rotary_dim;
     double rms_norm_eps, rope_theta, attention_scale;
+    /* Granite's multipliers (architecture.py TransformerConfig; 0 or 1: none): the embedding rows times
+     * embedding_multiplier (backprop.py:418-419), the attention and MLP outputs times residual_multiplier (folded into
+     * the output and down projections, transformer.py:231-239), the logits divided by logits_scaling
+     * (backprop.py:174-181). Granite's attention_multiplier is attention_scale. */
+    double embedding_multiplier, residual_multiplier, logits_scaling;
 } dllm_hip_decoder_config;
 
 typedef struct dllm_hip_trainer dllm_hip_trainer;

@@ -158,6 +158,9 @@ typedef struct {
     double eps, rope_theta, attention_scale;
     const double* inv_freq;        /* rotary_dim / 2 scaled inverse frequencies, or NULL for theta's defaults */
     double rope_attention_factor;  /* LongRoPE / YaRN attention factor folded into the q/k rows (1 or 0: none) */
+    /* Granite's multipliers (architecture.py; 1 or 0: none): the embedding rows times embedding_multiplier, the
+     * attention and MLP output projections times residual_multiplier (folded), the logits divided by logits_scaling */
+    double embedding_multiplier, residual_multiplier, logits_scaling;
 } orc_config;
 
 /*

@@ -142,6 +142,19 @@ typedef struct {
     float* hidden;
 } fwd_state;
 
+/* A multiplier of the config that is present (neither 1 nor unset). */
+static int has_multiplier(double m) { return m != 0.0 && m != 1.0; }
+
+/* x = x * f, elementwise in float (numpy's array times np.float32). */
+static void vscale(float* x, float f, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = x[i] * f;
+}
+
+/* x = x / f, elementwise in float (_finish, backprop.py:174-181, and the head gradient, :197-200). */
+static void vdivide(float* x, float f, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = x[i] / f;
+}
+
 /* _forward (backprop.py:399-490) and _experts (backprop.py:501-527). */
 static void forward(fwd_state* st, const int64_t* tokens) {
     const orc_ops* ops = st->ops;
@@ -151,6 +164,7 @@ static void forward(fwd_state* st, const int64_t* tokens) {
     const int64_t qd = c->heads * hd, kvd = c->kv_heads * hd;
     float* x = falloc(n * H);
     for (int64_t t = 0; t < n; ++t) memcpy(x + t * H, w[ORC_EMBEDDING] + tokens[t] * H, (size_t)H * sizeof(float));
+    if (has_multiplier(c->embedding_multiplier)) vscale(x, (float)c->embedding_multiplier, n * H);
     for (int64_t l = 0; l < c->layers; ++l) {
         layer_saved* s = &st->layers[l];
         memset(s, 0, sizeof *s);
@@ -317,25 +331,54 @@ static void scale_rotary_rows(const orc_config* c, int64_t slot, const float* sr
     }
 }
 
-/* fold_scales's RoPE attention factor (transformer.py:224-245) over a weight table: a table whose rope-scaled slots
- * point to folded copies (owned[] holds them, to free), or NULL when the factor is 1 (or unset). */
+/* The tensors the residual multiplier folds into (fold_scales, transformer.py:231-239): every name ending in
+ * "attention.o.weight" or "down.weight", so each layer's output projection and its MLP's (or every expert's) down
+ * projection. */
+static int residual_scaled_slots(const orc_config* c, int64_t layer, int64_t* out) {
+    int k = 0;
+    out[k++] = orc_slot(c, layer, ORC_O);
+    if (c->experts == 0) {
+        out[k++] = orc_slot(c, layer, ORC_DOWN);
+    } else {
+        for (int64_t e = 0; e < c->experts; ++e) out[k++] = orc_expert_slot(c, layer, e, 2);
+    }
+    return k;
+}
+
+/* fold_scales (transformer.py:224-245) over a weight table: a table whose residual-scaled and rope-scaled slots point
+ * to folded copies (owned[] holds them, to free), or NULL when neither the residual multiplier nor the RoPE attention
+ * factor is present. The two sets of tensors are disjoint. */
 static float** fold_weights(const orc_config* c, float* const* w, float*** owned_out) {
     const double a = c->rope_attention_factor;
+    const int rope = has_multiplier(a), residual = has_multiplier(c->residual_multiplier);
     *owned_out = NULL;
-    if (a == 0.0 || a == 1.0) return NULL;
+    if (!rope && !residual) return NULL;
     const int64_t slots = orc_slot_count(c);
     float** folded = (float**)calloc((size_t)slots, sizeof(float*));
     float** owned = (float**)calloc((size_t)slots, sizeof(float*));
     for (int64_t s = 0; s < slots; ++s) folded[s] = w[s];
+    int64_t* list = (int64_t*)malloc((size_t)(c->experts + 4) * sizeof(int64_t));
     for (int64_t l = 0; l < c->layers; ++l) {
-        int64_t list[4];
-        const int k = rope_scaled_slots(c, l, list);
-        for (int i = 0; i < k; ++i) {
-            owned[list[i]] = falloc(orc_tensor_numel(c, list[i]));
-            scale_rotary_rows(c, list[i], w[list[i]], owned[list[i]], (float)a);
-            folded[list[i]] = owned[list[i]];
+        if (residual) {
+            const int k = residual_scaled_slots(c, l, list);
+            for (int i = 0; i < k; ++i) {
+                const int64_t numel = orc_tensor_numel(c, list[i]);
+                owned[list[i]] = falloc(numel);
+                memcpy(owned[list[i]], w[list[i]], (size_t)numel * sizeof(float));
+                vscale(owned[list[i]], (float)c->residual_multiplier, numel);
+                folded[list[i]] = owned[list[i]];
+            }
+        }
+        if (rope) {
+            const int k = rope_scaled_slots(c, l, list);
+            for (int i = 0; i < k; ++i) {
+                owned[list[i]] = falloc(orc_tensor_numel(c, list[i]));
+                scale_rotary_rows(c, list[i], w[list[i]], owned[list[i]], (float)a);
+                folded[list[i]] = owned[list[i]];
+            }
         }
     }
+    free(list);
     *owned_out = owned;
     return folded;
 }
@@ -356,6 +399,7 @@ int orc_logits(const orc_ops* ops, const orc_config* c, float* const* w_stored, 
     init_state(&st, ops, c, w, n);
     forward(&st, tokens);
     ops->linear(st.hidden, w[c->tied ? ORC_EMBEDDING : ORC_LM_HEAD], NULL, logits, n, c->hidden, c->vocab);
+    if (has_multiplier(c->logits_scaling)) vdivide(logits, (float)c->logits_scaling, n * c->vocab);
     free_state(&st);
     free_folded(c, folded, owned);
     return 0;
@@ -463,8 +507,10 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     float* logits = falloc(n * V);
     float* dlogits = falloc(n * V);
     ops->linear(st.hidden, head, NULL, logits, n, H, V);
+    if (has_multiplier(c->logits_scaling)) vdivide(logits, (float)c->logits_scaling, n * V);
     *loss = ops->cross_entropy(logits, targets, dlogits, n, V, scale);
     free(logits);
+    if (has_multiplier(c->logits_scaling)) vdivide(dlogits, (float)c->logits_scaling, n * V);
     float* dhidden = falloc(n * H);
     float* dhead = falloc(V * H);
     ops->linear_backward(st.hidden, head, dlogits, dhidden, dhead, NULL, n, H, V);
@@ -536,7 +582,8 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     free(dh2); free(dtmp); free(dx_mid); free(dattended); free(dq_t); free(dk_t); free(dv_t); free(dq); free(dk);
     free(dq2); free(dk2); free(dh1); free(dh);
 
-    /* embedding_backward, tied head (backprop.py:112-117) */
+    /* embedding_backward, tied head (backprop.py:110-117), after the embedding multiplier's gradient */
+    if (has_multiplier(c->embedding_multiplier)) vscale(dx, (float)c->embedding_multiplier, n * H);
     float* demb = falloc(V * H);
     ops->embedding_backward(dx, tokens, demb, n, H, V);
     if (c->tied) {
@@ -553,8 +600,8 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     return 0;
 }
 
-/* DecoderGradients.losses_and_gradients of one window (backprop.py:88-118): with a RoPE attention factor the
- * weights are folded first (_folded, backprop.py:529-537) and the gradients unfolded after (_unfold). */
+/* DecoderGradients.losses_and_gradients of one window (backprop.py:88-118): with a residual multiplier or a RoPE
+ * attention factor the weights are folded first (_folded, backprop.py:529-537) and the gradients unfolded after (_unfold). */
 int orc_window_gradients(const orc_ops* ops, const orc_config* c, float* const* w, const int64_t* tokens,
                          const int64_t* targets, int64_t n, double scale, double router_scale, float* const* g,
                          double* loss, double* router_loss_out) {
@@ -562,11 +609,20 @@ int orc_window_gradients(const orc_ops* ops, const orc_config* c, float* const* 
     float** folded = fold_weights(c, w, &owned);
     const int rc = window_gradients(ops, c, folded ? folded : w, tokens, targets, n, scale, router_scale, g, loss,
                                     router_loss_out);
+    int64_t* list = (int64_t*)malloc((size_t)(c->experts + 4) * sizeof(int64_t));
     for (int64_t l = 0; folded && rc == 0 && l < c->layers; ++l) {
-        int64_t list[4];
-        const int k = rope_scaled_slots(c, l, list);
-        for (int i = 0; i < k; ++i) scale_rotary_rows(c, list[i], g[list[i]], g[list[i]], (float)c->rope_attention_factor);
+        if (has_multiplier(c->residual_multiplier)) {
+            const int k = residual_scaled_slots(c, l, list);
+            for (int i = 0; i < k; ++i)
+                vscale(g[list[i]], (float)c->residual_multiplier, orc_tensor_numel(c, list[i]));
+        }
+        if (has_multiplier(c->rope_attention_factor)) {
+            const int k = rope_scaled_slots(c, l, list);
+            for (int i = 0; i < k; ++i)
+                scale_rotary_rows(c, list[i], g[list[i]], g[list[i]], (float)c->rope_attention_factor);
+        }
     }
+    free(list);
     free_folded(c, folded, owned);
     return rc;
 }

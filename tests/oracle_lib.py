@@ -32,7 +32,8 @@ class OrcConfig(C.Structure):
         "vocab", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "attn_bias", "qk_norm", "window",
         "tied", "experts", "topk", "normalize", "expert_inter", "rotary_dim")] + [
         ("eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
-        ("inv_freq", C.c_void_p), ("rope_attention_factor", C.c_double)]
+        ("inv_freq", C.c_void_p), ("rope_attention_factor", C.c_double), ("embedding_multiplier", C.c_double),
+        ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double)]
 
 
 class OrcRopeScaling(C.Structure):
@@ -365,6 +366,12 @@ class Decoder:
     # a Hugging Face rope_scaling dict as (key, value) pairs (lists as tuples); without inv_freq, the frequencies are
     # computed from it when the configuration is handed to the oracle
     rope_scaling: tuple | None = None
+    # Granite's multipliers (architecture.py:95-100, importer.py:427-434); attention_multiplier replaces the
+    # attention scale 1/sqrt(head_dim) (architecture.py:311-312)
+    embedding_multiplier: float = 1.0
+    attention_multiplier: float | None = None
+    residual_multiplier: float = 1.0
+    logits_scaling: float = 1.0
 
     def scaling(self) -> dict | None:
         if not self.rope_scaling:
@@ -373,13 +380,14 @@ class Decoder:
 
     @property
     def attention_scale(self) -> float:
-        return 1.0 / math.sqrt(self.head_dim)
+        return 1.0 / math.sqrt(self.head_dim) if self.attention_multiplier is None else self.attention_multiplier
 
     def c(self) -> OrcConfig:
         cfg = OrcConfig(self.vocab, self.hidden, self.inter, self.layers, self.heads, self.kv_heads, self.head_dim,
                         int(self.attn_bias), self.qk_norm, self.window, int(self.tied), self.experts, self.topk,
                         int(self.normalize), self.expert_inter or self.inter, self.rotary_dim or self.head_dim,
-                        self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor)
+                        self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor,
+                        self.embedding_multiplier, self.residual_multiplier, self.logits_scaling)
         inv_freq = self.inv_freq
         if inv_freq is None and self.rope_scaling:
             inv_freq = rope_inv_freq_scaled(self.rotary_dim or self.head_dim, self.rope_theta, self.scaling())
@@ -478,6 +486,11 @@ FIXTURES = {
     "mixtral": Decoder("mixtral", tied=False, experts=4, topk=2, normalize=True, **TINY),
     "olmoe": Decoder("olmoe", tied=False, qk_norm=2, experts=4, topk=2, normalize=False,
                      **{**TINY, "inter": 8}),
+    "granite": Decoder("granite", tied=True, embedding_multiplier=12.0, attention_multiplier=0.125,
+                       residual_multiplier=0.22, logits_scaling=8.0, **TINY),
+    "granitemoe": Decoder("granitemoe", tied=True, experts=4, topk=2, normalize=True, embedding_multiplier=12.0,
+                          attention_multiplier=0.125, residual_multiplier=0.22, logits_scaling=8.0,
+                          **{**TINY, "inter": 8}),
     "phi3": Decoder("phi3", tied=False, window=3, rotary_dim=4, rope_attention_factor=4.0,
                     rope_scaling=frozen_scaling(PHI3_SCALING), **{**TINY, "hidden": 32, "head_dim": 8}),
 }
@@ -487,6 +500,7 @@ FIXTURES = {
 QLORA_FIXTURES = {
     "llama": Decoder("llama", tied=True, **{**TINY, "hidden": 32, "vocab": 264, "head_dim": 8}),
     "qwen3": Decoder("qwen3", tied=True, qk_norm=1, **{**TINY, "hidden": 32, "vocab": 264, "head_dim": 8}),
+    "granite": replace(FIXTURES["granite"], hidden=32, vocab=264, head_dim=8),
 }
 
 

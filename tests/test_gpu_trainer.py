@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_goldens.json").read_text())
 TOKENS = [1, 17, 42, 5, 63, 0, 9, 9, 30]
-FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3"]
+FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe"]
 
 
 def gpu_decoder(d: O.Decoder):
@@ -24,7 +24,9 @@ def gpu_decoder(d: O.Decoder):
 
     return Decoder(d.vocab, d.hidden, d.inter, d.layers, d.heads, d.kv_heads, d.head_dim, d.eps, d.rope_theta,
                    d.tied, d.attn_bias, d.qk_norm, d.window, d.experts, d.topk, d.normalize, d.expert_inter,
-                   rotary_dim=d.rotary_dim, rope_scaling=d.scaling())
+                   rotary_dim=d.rotary_dim, rope_scaling=d.scaling(), embedding_multiplier=d.embedding_multiplier,
+                   attention_multiplier=d.attention_multiplier, residual_multiplier=d.residual_multiplier,
+                   logits_scaling=d.logits_scaling)
 
 
 def make_trainer(d: O.Decoder, weights, max_tokens=64, max_windows=8, max_window=32):
