@@ -292,6 +292,15 @@ struct dllm_hip_trainer {
         return kOk;
     }
 
+    // Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346): every
+    // layer of a model with experts except those in dense_layers.
+    bool sparse(int64_t l) const { return E > 0 && !(l < 64 && ((c.dense_layers >> l) & 1)); }
+    int64_t sparse_layers() const {
+        int64_t n = 0;
+        for (int64_t l = 0; l < c.layers; ++l) n += sparse(l) ? 1 : 0;
+        return n;
+    }
+
     int build_tensors() {
         const auto& k = c;
         add_tensor("token_embedding.weight", V, H, k.tie_embeddings != 0);
@@ -312,7 +321,7 @@ struct dllm_hip_trainer {
             }
             add_tensor(p + "attention.o.weight", H, QD, true);
             add_tensor(p + "mlp_norm.weight", H, 0, false);
-            if (E > 0) {  // architecture.py: a routed layer has the router and E experts instead of the dense MLP
+            if (sparse(l)) {  // architecture.py: a routed layer has the router and E experts instead of the dense MLP
                 add_tensor(p + "mlp.router.weight", E, H, true);
                 for (int64_t e = 0; e < E; ++e) {
                     const std::string x = p + "mlp.experts." + std::to_string(e) + ".";
@@ -445,11 +454,12 @@ struct dllm_hip_trainer {
     int build_activations() {
         const int64_t R = R_max, heads = c.heads, kvh = c.kv_heads;
         saved.resize(static_cast<size_t>(c.layers));
-        if (E > 0) DLLM_TRY(make(&probs_all, c.layers * R * E));  // [layer][row][expert], the router statistics' input
+        // [sparse layer][row][expert], the router statistics' input
+        if (E > 0) DLLM_TRY(make(&probs_all, std::max<int64_t>(sparse_layers(), 1) * R * E));
         // x_in of layer l + 1 is x_out of layer l: one chain of L + 1 residual buffers.
         std::vector<float*> xs(static_cast<size_t>(c.layers) + 1);
         for (auto& p : xs) DLLM_TRY(make(&p, R * H));
-        for (int64_t l = 0; l < c.layers; ++l) {
+        for (int64_t l = 0, routed = 0; l < c.layers; ++l) {
             Saved& s = saved[static_cast<size_t>(l)];
             s.x_in = xs[static_cast<size_t>(l)];
             DLLM_TRY(make(&s.h1, R * H));
@@ -466,14 +476,14 @@ struct dllm_hip_trainer {
             DLLM_TRY(make(&s.attended, R * QD));
             DLLM_TRY(make(&s.x_mid, R * H));
             DLLM_TRY(make(&s.h2, R * H));
-            const int64_t mlp_rows = E > 0 ? RK : R, mlp_inter = E > 0 ? EI : I;
+            const int64_t mlp_rows = sparse(l) ? RK : R, mlp_inter = sparse(l) ? EI : I;
             DLLM_TRY(make(&s.gate, mlp_rows * mlp_inter));
             DLLM_TRY(make(&s.up, mlp_rows * mlp_inter));
             DLLM_TRY(make(&s.gate_act, mlp_rows * mlp_inter));
             DLLM_TRY(make(&s.product, mlp_rows * mlp_inter));
-            if (E > 0) {
+            if (sparse(l)) {
                 DLLM_TRY(make(&s.router_logits, R * E));
-                s.probs = probs_all + l * R * E;
+                s.probs = probs_all + (routed++) * R * E;
                 DLLM_TRY(make(&s.routing, RK));
                 DLLM_TRY(make(&s.y, RK * H));
                 DLLM_TRY(make(&s.chosen, RK));
@@ -1164,7 +1174,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(attention_forward(l, sv, b, s));
         DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
         DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
-        if (E > 0) return moe_forward(l, R, x_out, s);
+        if (sparse(l)) return moe_forward(l, R, x_out, s);
         if (grp_on[kGrpMlpFwd] && grp_rows == R) {
             DLLM_TRY(group_launch(l, kGrpMlpFwd, s));
         } else {
@@ -1182,7 +1192,7 @@ struct dllm_hip_trainer {
         const Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
         hipStream_t ws = s;  // the stream of the weight-gradient batches
-        if (E > 0) {
+        if (sparse(l)) {
             DLLM_TRY(side_wait(kSideMlp, s));      // the previous layer's router dW reads dlogits_r
             DLLM_TRY(side_wait(kSideNormMlp, s));  // its mlp norm's dW reads dh
             DLLM_TRY(moe_backward(l, R, nseg, s));
@@ -1540,10 +1550,10 @@ struct dllm_hip_trainer {
             float* x_out = l + 1 < c.layers ? saved[static_cast<size_t>(l + 1)].x_in : x_final;
             DLLM_TRY(forward_layer(l, R, b, x_out, s));
         }
-        if (E > 0) {  // _router_loss (backprop.py:359-377): per window, over every layer's rows
+        if (E > 0) {  // _router_loss (backprop.py:359-377): per window, over every sparse layer's rows
             DLLM_TRY(check_hip(hipMemcpyAsync(counts_d, counts_host.data(), counts_host.size() * 8,
                                               hipMemcpyHostToDevice, s), "upload"));
-            DLLM_TRY(launch_router_stats(probs_all, R_max * E, c.layers, seg_d, nseg, counts_d, E, router_scale,
+            DLLM_TRY(launch_router_stats(probs_all, R_max * E, sparse_layers(), seg_d, nseg, counts_d, E, router_scale,
                                          router_loss_w, router_scale != 0.0 ? grad_row : nullptr, s));
         }
         DLLM_TRY(launch_rms_norm(x_final, P(final_norm), hidden, R, H, eps, 0, nullptr, s));
@@ -1773,7 +1783,7 @@ struct dllm_hip_trainer {
             for (int t = 0; t < 7; ++t) {
                 if (!(l.targets & (int64_t{1} << t))) continue;
                 const LayerIds& L = layer_ids[static_cast<size_t>(layer)];
-                if (t >= 4 && E > 0) {  // gate, up, down of a routed layer: every expert's (the router never)
+                if (t >= 4 && sparse(layer)) {  // gate, up, down of a routed layer: every expert's (the router never)
                     const std::vector<int>& ids = t == 4 ? L.egate : (t == 5 ? L.eup : L.edown);
                     weights.insert(weights.end(), ids.begin(), ids.end());
                 } else {
@@ -1960,6 +1970,13 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     for (double m : {c.embedding_multiplier, c.residual_multiplier, c.logits_scaling})
         DLLM_REQUIRE(m >= 0.0 && std::isfinite(m), "multipliers must be finite and non-negative (0: none)");
     DLLM_REQUIRE(c.attention_scale > 0.0 && std::isfinite(c.attention_scale), "attention_scale must be positive");
+    if (c.experts > 0) {
+        bool any_sparse = false;
+        for (int64_t l = 0; l < c.layers; ++l) any_sparse = any_sparse || l >= 64 || !((c.dense_layers >> l) & 1);
+        DLLM_REQUIRE(any_sparse, "a model with experts needs at least one sparse layer");
+    } else {
+        DLLM_REQUIRE(c.dense_layers == 0, "dense_layers needs experts");
+    }
     std::unique_ptr<dllm_hip_trainer> t(new dllm_hip_trainer());
     t->c = c;
     for (double* m : {&t->c.embedding_multiplier, &t->c.residual_multiplier, &t->c.logits_scaling})

@@ -280,6 +280,9 @@ typedef struct {
      * the output and down projections, transformer.py:231-239), the logits divided by logits_scaling
      * (backprop.py:174-181). Granite's attention_multiplier is attention_scale. */
     double embedding_multiplier, residual_multiplier, logits_scaling;
+    /* dense_layers (architecture.py:128, 344-346; Qwen3-MoE's mlp_only_layers): bit l set = layer l keeps a dense
+     * MLP of `intermediate` in a model with experts; layers from 64 on are routed */
+    int64_t dense_layers;
 } dllm_hip_decoder_config;
 
 typedef struct dllm_hip_trainer dllm_hip_trainer;

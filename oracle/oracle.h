@@ -161,7 +161,13 @@ typedef struct {
     /* Granite's multipliers (architecture.py; 1 or 0: none): the embedding rows times embedding_multiplier, the
      * attention and MLP output projections times residual_multiplier (folded), the logits divided by logits_scaling */
     double embedding_multiplier, residual_multiplier, logits_scaling;
+    /* dense_layers (architecture.py:128, 344-346): bit l set = layer l keeps a dense MLP in a model with experts
+     * (Qwen3-MoE's mlp_only_layers); layers from 64 on are sparse */
+    int64_t dense_layers;
 } orc_config;
+
+/* Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346). */
+int orc_is_sparse(const orc_config* c, int64_t layer);
 
 /*
  * Tensor slots. Every tensor of the decoder has a fixed slot: the globals, then per layer a block of

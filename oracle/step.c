@@ -21,6 +21,10 @@ int64_t orc_expert_slot(const orc_config* c, int64_t layer, int64_t expert, int6
     return orc_slot(c, layer, ORC_LAYER_FIXED + 3 * expert + which);
 }
 
+int orc_is_sparse(const orc_config* c, int64_t layer) {
+    return c->experts > 0 && !(layer < 64 && ((c->dense_layers >> layer) & 1));
+}
+
 /* Shapes of architecture.py:418-468 for the decoder families a step here covers. */
 static int64_t slot_shape(const orc_config* c, int64_t slot, int64_t* d0, int64_t* d1) {
     const int64_t H = c->hidden, q = c->heads * c->head_dim, kv = c->kv_heads * c->head_dim;
@@ -29,7 +33,7 @@ static int64_t slot_shape(const orc_config* c, int64_t slot, int64_t* d0, int64_
     if (slot == ORC_FINAL_NORM) { *d0 = H; return 1; }
     if (slot == ORC_LM_HEAD) { if (c->tied) return 0; *d0 = c->vocab; *d1 = H; return 2; }
     const int64_t kind = (slot - ORC_GLOBALS) % orc_layer_slots(c);
-    const int sparse = c->experts > 0;
+    const int sparse = orc_is_sparse(c, (slot - ORC_GLOBALS) / orc_layer_slots(c));
     switch (kind) {
         case ORC_ATTN_NORM: *d0 = H; return 1;
         case ORC_Q: *d0 = q; *d1 = H; return 2;
@@ -44,6 +48,7 @@ static int64_t slot_shape(const orc_config* c, int64_t slot, int64_t* d0, int64_
         case ORC_DOWN: if (sparse) return 0; *d0 = H; *d1 = c->inter; return 2;
         case ORC_ROUTER: if (!sparse) return 0; *d0 = c->experts; *d1 = H; return 2;
         default: {
+            if (!sparse) return 0;
             const int64_t which = (kind - ORC_LAYER_FIXED) % 3;
             if (which == 2) { *d0 = H; *d1 = c->expert_inter; } else { *d0 = c->expert_inter; *d1 = H; }
             return 2;
@@ -209,7 +214,7 @@ static void forward(fwd_state* st, const int64_t* tokens) {
         vadd(x, s->out, s->x_mid, n * H);
         s->h2 = falloc(n * H);
         ops->rms_norm(s->x_mid, w[orc_slot(c, l, ORC_MLP_NORM)], s->h2, n, H, c->eps, 0);
-        if (c->experts == 0) {
+        if (!orc_is_sparse(c, l)) {
             s->dense.rows = n;
             s->dense.x = s->h2;
             swiglu_forward(ops, w, orc_slot(c, l, ORC_GATE), orc_slot(c, l, ORC_UP), orc_slot(c, l, ORC_DOWN), c->inter,
@@ -266,7 +271,7 @@ static void free_state(fwd_state* st) {
         layer_saved* s = &st->layers[l];
         free(s->x_in); free(s->h1); free(s->q_raw); free(s->k_raw); free(s->q); free(s->k); free(s->v);
         free(s->attended); free(s->out); free(s->x_mid); free(s->h2);
-        if (c->experts == 0) {
+        if (!orc_is_sparse(c, l)) {
             swiglu_free(&s->dense);
         } else {
             free(s->mlp); free(s->router_logits); free(s->chosen); free(s->routing);
@@ -337,7 +342,7 @@ static void scale_rotary_rows(const orc_config* c, int64_t slot, const float* sr
 static int residual_scaled_slots(const orc_config* c, int64_t layer, int64_t* out) {
     int k = 0;
     out[k++] = orc_slot(c, layer, ORC_O);
-    if (c->experts == 0) {
+    if (!orc_is_sparse(c, layer)) {
         out[k++] = orc_slot(c, layer, ORC_DOWN);
     } else {
         for (int64_t e = 0; e < c->experts; ++e) out[k++] = orc_expert_slot(c, layer, e, 2);
@@ -410,13 +415,17 @@ static double router_loss(const fwd_state* st, double router_scale, float* grad_
     const orc_ops* ops = st->ops;
     const orc_config* c = st->c;
     const int64_t n = st->n, E = c->experts, K = c->topk, L = c->layers;
-    const int64_t rows = n * L;
+    int64_t sparse_layers = 0;
+    for (int64_t l = 0; l < L; ++l) sparse_layers += orc_is_sparse(c, l);
+    const int64_t rows = n * sparse_layers;
     float* probs = falloc(rows * E);
     int64_t* counts = (int64_t*)calloc((size_t)E, sizeof(int64_t));
-    for (int64_t l = 0; l < L; ++l) {
+    for (int64_t l = 0, b = 0; l < L; ++l) {
+        if (!orc_is_sparse(c, l)) continue;
         const layer_saved* s = &st->layers[l];
-        for (int64_t r = 0; r < n; ++r) ops->softmax(s->router_logits + r * E, probs + (l * n + r) * E, E);
+        for (int64_t r = 0; r < n; ++r) ops->softmax(s->router_logits + r * E, probs + (b * n + r) * E, E);
         for (int64_t i = 0; i < n * K; ++i) counts[s->chosen[i]] += 1;
+        ++b;
     }
     float* fractions = falloc(E);
     float* means = falloc(E);
@@ -535,7 +544,7 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     float* dh = falloc(n * H);
     for (int64_t l = c->layers - 1; l >= 0; --l) {
         const layer_saved* s = &st.layers[l];
-        if (c->experts == 0) {
+        if (!orc_is_sparse(c, l)) {
             swiglu_backward(ops, w, g, orc_slot(c, l, ORC_GATE), orc_slot(c, l, ORC_UP), orc_slot(c, l, ORC_DOWN),
                             c->inter, H, &s->dense, dx, dh2);
         } else {

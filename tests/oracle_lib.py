@@ -33,7 +33,7 @@ class OrcConfig(C.Structure):
         "tied", "experts", "topk", "normalize", "expert_inter", "rotary_dim")] + [
         ("eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
         ("inv_freq", C.c_void_p), ("rope_attention_factor", C.c_double), ("embedding_multiplier", C.c_double),
-        ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double)]
+        ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double), ("dense_layers", C.c_int64)]
 
 
 class OrcRopeScaling(C.Structure):
@@ -372,6 +372,11 @@ class Decoder:
     attention_multiplier: float | None = None
     residual_multiplier: float = 1.0
     logits_scaling: float = 1.0
+    dense_layers: tuple[int, ...] = ()  # layers keeping a dense MLP in a model with experts (architecture.py:128)
+
+    def is_sparse(self, layer: int) -> bool:
+        """architecture.py:344-346."""
+        return self.experts > 0 and layer not in self.dense_layers
 
     def scaling(self) -> dict | None:
         if not self.rope_scaling:
@@ -387,7 +392,8 @@ class Decoder:
                         int(self.attn_bias), self.qk_norm, self.window, int(self.tied), self.experts, self.topk,
                         int(self.normalize), self.expert_inter or self.inter, self.rotary_dim or self.head_dim,
                         self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor,
-                        self.embedding_multiplier, self.residual_multiplier, self.logits_scaling)
+                        self.embedding_multiplier, self.residual_multiplier, self.logits_scaling,
+                        sum(1 << layer for layer in self.dense_layers))
         inv_freq = self.inv_freq
         if inv_freq is None and self.rope_scaling:
             inv_freq = rope_inv_freq_scaled(self.rotary_dim or self.head_dim, self.rope_theta, self.scaling())
@@ -417,7 +423,7 @@ class Decoder:
                 shapes[p + "attention.k_norm.weight"] = (kv if self.qk_norm == 2 else self.head_dim,)
             shapes[p + "attention.o.weight"] = (H, q)
             shapes[p + "mlp_norm.weight"] = (H,)
-            if self.experts:
+            if self.is_sparse(i):
                 e_inter = self.expert_inter or self.inter
                 shapes[p + "mlp.router.weight"] = (self.experts, H)
                 for e in range(self.experts):
@@ -491,6 +497,8 @@ FIXTURES = {
     "granitemoe": Decoder("granitemoe", tied=True, experts=4, topk=2, normalize=True, embedding_multiplier=12.0,
                           attention_multiplier=0.125, residual_multiplier=0.22, logits_scaling=8.0,
                           **{**TINY, "inter": 8}),
+    "qwen3_moe": Decoder("qwen3_moe", tied=True, qk_norm=1, experts=4, topk=2, normalize=True, expert_inter=8,
+                         dense_layers=(0,), **{**TINY, "head_dim": 8}),
     "phi3": Decoder("phi3", tied=False, window=3, rotary_dim=4, rope_attention_factor=4.0,
                     rope_scaling=frozen_scaling(PHI3_SCALING), **{**TINY, "hidden": 32, "head_dim": 8}),
 }
@@ -501,6 +509,7 @@ QLORA_FIXTURES = {
     "llama": Decoder("llama", tied=True, **{**TINY, "hidden": 32, "vocab": 264, "head_dim": 8}),
     "qwen3": Decoder("qwen3", tied=True, qk_norm=1, **{**TINY, "hidden": 32, "vocab": 264, "head_dim": 8}),
     "granite": replace(FIXTURES["granite"], hidden=32, vocab=264, head_dim=8),
+    "qwen3_moe": replace(FIXTURES["qwen3_moe"], hidden=32, vocab=264),
 }
 
 
@@ -708,7 +717,7 @@ def lora_target_weights(d: Decoder, lora: Lora) -> list[str]:
     names = []
     for layer in range(d.layers):
         for target in lora.targets:
-            if target in ("gate", "up", "down") and d.experts:
+            if target in ("gate", "up", "down") and d.is_sparse(layer):
                 names.extend(f"layers.{layer}.mlp.experts.{e}.{target}.weight" for e in range(d.experts))
             else:
                 names.append(f"layers.{layer}.{LORA_WEIGHT_NAMES[target]}")

@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_goldens.json").read_text())
 TOKENS = [1, 17, 42, 5, 63, 0, 9, 9, 30]
-FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe"]
+FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe", "qwen3_moe"]
 
 
 def gpu_decoder(d: O.Decoder):
@@ -26,7 +26,7 @@ def gpu_decoder(d: O.Decoder):
                    d.tied, d.attn_bias, d.qk_norm, d.window, d.experts, d.topk, d.normalize, d.expert_inter,
                    rotary_dim=d.rotary_dim, rope_scaling=d.scaling(), embedding_multiplier=d.embedding_multiplier,
                    attention_multiplier=d.attention_multiplier, residual_multiplier=d.residual_multiplier,
-                   logits_scaling=d.logits_scaling)
+                   logits_scaling=d.logits_scaling, dense_layers=d.dense_layers)
 
 
 def make_trainer(d: O.Decoder, weights, max_tokens=64, max_windows=8, max_window=32):
@@ -271,6 +271,15 @@ MOE = {
     "olmoe": O.Decoder("olmoe", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=4, head_dim=16,
                        eps=1e-5, rope_theta=1e4, tied=False, qk_norm=2, experts=16, topk=4, normalize=False,
                        expert_inter=32),
+    # a dense first layer among routed ones (mlp_only_layers), per-head QK-norm
+    "qwen3_moe": O.Decoder("qwen3_moe", vocab=256, hidden=64, inter=96, layers=3, heads=4, kv_heads=2, head_dim=16,
+                           eps=1e-6, rope_theta=1e6, tied=True, qk_norm=1, experts=8, topk=2, normalize=True,
+                           expert_inter=32, dense_layers=(0,)),
+    # Granite's multipliers with routed experts: every expert's down projection folds the residual multiplier
+    "granitemoe": O.Decoder("granitemoe", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16,
+                            eps=1e-6, rope_theta=1e4, tied=True, experts=8, topk=2, normalize=True, expert_inter=32,
+                            embedding_multiplier=12.0, attention_multiplier=0.0625, residual_multiplier=0.22,
+                            logits_scaling=6.0),
 }
 
 
@@ -310,7 +319,7 @@ def test_moe_step_matches_the_oracle_on_ragged_windows(family):
         got = t.get(name, d.tensor_shapes()[name], t.GRAD)
         assert got.tobytes() == want[name].tobytes(), name
         unreached += ".experts." in name and not np.any(got)
-    assert unreached >= 3 * (d.experts - d.topk) * d.layers
+    assert unreached >= 3 * (d.experts - d.topk) * sum(d.is_sparse(layer) for layer in range(d.layers))
 
 
 def test_moe_lora_step_matches_the_oracle():
