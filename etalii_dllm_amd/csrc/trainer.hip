@@ -165,6 +165,7 @@ struct dllm_hip_trainer {
     struct LayerIds {
         int attn_norm, q, k, v, qb = -1, kb = -1, vb = -1, qn = -1, kn = -1, o, mlp_norm, gate, up, down;
         int router = -1;
+        int attn_post = -1, mlp_post = -1;   // post norms (OLMo 2; sandwich with the pre norms)
         std::vector<int> egate, eup, edown;  // routed experts
     };
     std::vector<LayerIds> layer_ids;
@@ -172,6 +173,7 @@ struct dllm_hip_trainer {
 
     struct Saved {
         float *x_in, *h1, *q_raw, *k_raw, *qn, *kn, *q, *k, *v, *attended, *x_mid, *h2, *gate, *up, *gate_act, *product;
+        float *out = nullptr, *mlp = nullptr;  // post norms: the attention and MLP outputs before their norms
         // routed experts: router logits and probabilities [R][E], the choices [R][K] (rank order), the expert
         // outputs y [R K][H] in grouped order (gate, up, gate_act, product are grouped [R K][EI] then)
         float *router_logits = nullptr, *probs = nullptr, *routing = nullptr, *y = nullptr;
@@ -203,7 +205,8 @@ struct dllm_hip_trainer {
     int64_t* counts_d = nullptr;
     std::vector<int64_t> counts_host;  // [windows][E] choices per window over all layers
     double router_scale_cur = 0.0, last_router_loss = 0.0;
-    double *inv_mlp = nullptr, *inv_attn = nullptr;  // the layer norms' inverse rms, read by their weights' gradients
+    double *inv_mlp = nullptr, *inv_attn = nullptr, *inv_post = nullptr;
+    float *post_tmp = nullptr, *dpost = nullptr;  // post norms: a normalised block output; a norm's input gradient  // the layer norms' inverse rms, read by their weights' gradients
     double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
            *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
     void* attn_ws = nullptr;
@@ -295,6 +298,9 @@ struct dllm_hip_trainer {
     // Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346): every
     // layer of a model with experts except those in dense_layers.
     bool sparse(int64_t l) const { return E > 0 && !(l < 64 && ((c.dense_layers >> l) & 1)); }
+    // Norm placement (architecture.py:315-320): pre (each block's input), post (its output; OLMo 2) or both.
+    bool pre_norms() const { return c.norm_placement != 1; }
+    bool post_norms() const { return c.norm_placement != 0; }
     int64_t sparse_layers() const {
         int64_t n = 0;
         for (int64_t l = 0; l < c.layers; ++l) n += sparse(l) ? 1 : 0;
@@ -306,7 +312,7 @@ struct dllm_hip_trainer {
         add_tensor("token_embedding.weight", V, H, k.tie_embeddings != 0);
         for (int64_t l = 0; l < k.layers; ++l) {
             const std::string p = "layers." + std::to_string(l) + ".";
-            add_tensor(p + "attention_norm.weight", H, 0, false);
+            if (pre_norms()) add_tensor(p + "attention_norm.weight", H, 0, false);
             add_tensor(p + "attention.q.weight", QD, H, true);
             add_tensor(p + "attention.k.weight", KVD, H, true);
             add_tensor(p + "attention.v.weight", KVD, H, true);
@@ -320,7 +326,11 @@ struct dllm_hip_trainer {
                 add_tensor(p + "attention.k_norm.weight", k.qk_norm == 2 ? KVD : k.head_dim, 0, false);
             }
             add_tensor(p + "attention.o.weight", H, QD, true);
-            add_tensor(p + "mlp_norm.weight", H, 0, false);
+            if (post_norms()) {
+                add_tensor(p + "attention_post_norm.weight", H, 0, false);
+                add_tensor(p + "mlp_post_norm.weight", H, 0, false);
+            }
+            if (pre_norms()) add_tensor(p + "mlp_norm.weight", H, 0, false);
             if (sparse(l)) {  // architecture.py: a routed layer has the router and E experts instead of the dense MLP
                 add_tensor(p + "mlp.router.weight", E, H, true);
                 for (int64_t e = 0; e < E; ++e) {
@@ -380,6 +390,8 @@ struct dllm_hip_trainer {
             L.kn = id(p + "attention.k_norm.weight");
             L.o = id(p + "attention.o.weight");
             L.mlp_norm = id(p + "mlp_norm.weight");
+            L.attn_post = id(p + "attention_post_norm.weight");
+            L.mlp_post = id(p + "mlp_post_norm.weight");
             L.gate = id(p + "mlp.gate.weight");
             L.up = id(p + "mlp.up.weight");
             L.down = id(p + "mlp.down.weight");
@@ -462,7 +474,8 @@ struct dllm_hip_trainer {
         for (int64_t l = 0, routed = 0; l < c.layers; ++l) {
             Saved& s = saved[static_cast<size_t>(l)];
             s.x_in = xs[static_cast<size_t>(l)];
-            DLLM_TRY(make(&s.h1, R * H));
+            if (pre_norms()) DLLM_TRY(make(&s.h1, R * H));
+            else s.h1 = s.x_in;  // without pre norms the blocks read the residual stream itself
             DLLM_TRY(make(&s.q_raw, R * QD));
             DLLM_TRY(make(&s.k_raw, R * KVD));
             s.qn = s.kn = nullptr;
@@ -475,7 +488,12 @@ struct dllm_hip_trainer {
             DLLM_TRY(make(&s.v, R * KVD));
             DLLM_TRY(make(&s.attended, R * QD));
             DLLM_TRY(make(&s.x_mid, R * H));
-            DLLM_TRY(make(&s.h2, R * H));
+            if (pre_norms()) DLLM_TRY(make(&s.h2, R * H));
+            else s.h2 = s.x_mid;
+            if (post_norms()) {
+                DLLM_TRY(make(&s.out, R * H));
+                DLLM_TRY(make(&s.mlp, R * H));
+            }
             const int64_t mlp_rows = sparse(l) ? RK : R, mlp_inter = sparse(l) ? EI : I;
             DLLM_TRY(make(&s.gate, mlp_rows * mlp_inter));
             DLLM_TRY(make(&s.up, mlp_rows * mlp_inter));
@@ -537,6 +555,11 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&inv_rms, R * std::max<int64_t>(heads, 1)));
         DLLM_TRY(make(&inv_mlp, R));
         DLLM_TRY(make(&inv_attn, R));
+        if (post_norms()) {
+            DLLM_TRY(make(&inv_post, R));
+            DLLM_TRY(make(&post_tmp, R * H));
+            DLLM_TRY(make(&dpost, R * H));
+        }
         DLLM_TRY(make(&dh1, R * H));
         DLLM_TRY(make(&row_max, R));
         DLLM_TRY(make(&row_total, R));
@@ -1154,7 +1177,7 @@ struct dllm_hip_trainer {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
         Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
-        DLLM_TRY(launch_rms_norm(sv.x_in, P(L.attn_norm), sv.h1, R, H, eps, 0, nullptr, s));
+        if (pre_norms()) DLLM_TRY(launch_rms_norm(sv.x_in, P(L.attn_norm), sv.h1, R, H, eps, 0, nullptr, s));
         DLLM_TRY(qkv_forward(l, R, s));
         const float* qsrc = sv.q_raw;
         const float* ksrc = sv.k_raw;
@@ -1172,8 +1195,14 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_rope_pair(qsrc, sv.q, c.heads, ksrc, sv.k, c.kv_heads, pos_index, cos_t, sin_t, R, c.head_dim,
                                   c.rotary_dim, 0, s));
         DLLM_TRY(attention_forward(l, sv, b, s));
-        DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
-        DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
+        if (post_norms()) {  // x_mid = x + post_norm(out)
+            DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.out, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.out, P(L.attn_post), post_tmp, R, H, eps, 0, nullptr, s));
+            DLLM_TRY(launch_add(sv.x_in, post_tmp, sv.x_mid, R * H, s));
+        } else {
+            DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
+        }
+        if (pre_norms()) DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
         if (sparse(l)) return moe_forward(l, R, x_out, s);
         if (grp_on[kGrpMlpFwd] && grp_rows == R) {
             DLLM_TRY(group_launch(l, kGrpMlpFwd, s));
@@ -1182,6 +1211,11 @@ struct dllm_hip_trainer {
             DLLM_TRY(linear_fwd(sv.h2, R, H, L.up, nullptr, sv.up, nullptr, s));
         }
         DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * I, s));
+        if (post_norms()) {  // x_out = x_mid + post_norm(mlp)
+            DLLM_TRY(linear_fwd(sv.product, R, I, L.down, nullptr, sv.mlp, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.mlp, P(L.mlp_post), post_tmp, R, H, eps, 0, nullptr, s));
+            return launch_add(sv.x_mid, post_tmp, x_out, R * H, s);
+        }
         return linear_fwd(sv.product, R, I, L.down, nullptr, x_out, sv.x_mid, s);  // x_out = x_mid + mlp
     }
 
@@ -1192,15 +1226,22 @@ struct dllm_hip_trainer {
         const Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
         hipStream_t ws = s;  // the stream of the weight-gradient batches
+        // post norms (backprop.py:224-229): the MLP's output gradient through its norm (one stream: side is off)
+        const float* dmlp = dx;
+        if (post_norms()) {
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.mlp, P(L.mlp_post), dx, dpost, nullptr, R, H, eps, 0, inv_post, s));
+            DLLM_TRY(norm_dw(dx, sv.mlp, inv_post, H, 1, nseg, G(L.mlp_post), s));
+            dmlp = dpost;
+        }
         if (sparse(l)) {
             DLLM_TRY(side_wait(kSideMlp, s));      // the previous layer's router dW reads dlogits_r
             DLLM_TRY(side_wait(kSideNormMlp, s));  // its mlp norm's dW reads dh
             DLLM_TRY(moe_backward(l, R, nseg, s));
         } else {
             // SwiGLU (backprop.py:289-306)
-            DLLM_TRY(linear_dx(dx, R, L.down, dproduct, nullptr, s));
+            DLLM_TRY(linear_dx(dmlp, R, L.down, dproduct, nullptr, s));
             DLLM_TRY(side_fork_from(s, &ws));
-            DLLM_TRY(linear_dw(dx, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, ws, nullptr, -1,
+            DLLM_TRY(linear_dw(dmlp, H, sv.product, I, nseg, G(L.down), nullptr, nullptr, ws, nullptr, -1,
                                unfold_scale(L.down)));
             DLLM_TRY(side_mark(kSideDown));
             DLLM_TRY(side_wait(kSideMlp, s));  // the previous layer's gate and up dW read dgate, dup
@@ -1220,14 +1261,25 @@ struct dllm_hip_trainer {
         }
         // mlp norm; dx_mid = dx + dh2'
         DLLM_TRY(side_wait(kSideO, s));  // the previous layer's o dW reads dx_mid
-        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_mlp, s));
+        if (pre_norms()) {
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_mlp, s));
+            DLLM_TRY(side_fork_from(s, &ws));
+            DLLM_TRY(norm_dw(dh, sv.x_mid, inv_mlp, H, 1, nseg, G(L.mlp_norm), ws));
+            DLLM_TRY(side_mark(kSideNormMlp));
+        } else {
+            DLLM_TRY(launch_add(dx, dh, dx_mid, R * H, s));  // dx_mid = dx + dh2
+        }
+        // attention output projection (through its post norm, backprop.py:237-242)
+        const float* dout = dx_mid;
+        if (post_norms()) {
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.out, P(L.attn_post), dx_mid, dpost, nullptr, R, H, eps, 0, inv_post,
+                                                 s));
+            DLLM_TRY(norm_dw(dx_mid, sv.out, inv_post, H, 1, nseg, G(L.attn_post), s));
+            dout = dpost;
+        }
+        DLLM_TRY(linear_dx(dout, R, L.o, dattended, nullptr, s));
         DLLM_TRY(side_fork_from(s, &ws));
-        DLLM_TRY(norm_dw(dh, sv.x_mid, inv_mlp, H, 1, nseg, G(L.mlp_norm), ws));
-        DLLM_TRY(side_mark(kSideNormMlp));
-        // attention output projection
-        DLLM_TRY(linear_dx(dx_mid, R, L.o, dattended, nullptr, s));
-        DLLM_TRY(side_fork_from(s, &ws));
-        DLLM_TRY(linear_dw(dx_mid, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, ws, nullptr, -1,
+        DLLM_TRY(linear_dw(dout, H, sv.attended, QD, nseg, G(L.o), nullptr, nullptr, ws, nullptr, -1,
                            unfold_scale(L.o)));
         DLLM_TRY(side_mark(kSideO));
         DLLM_TRY(side_wait(kSideQkv, s));  // the previous layer's q/k/v dW read dq, dk (dq2, dk2) and dv_t
@@ -1277,6 +1329,7 @@ struct dllm_hip_trainer {
         }
         // attention norm; dx = dx_mid + dh1'
         DLLM_TRY(side_wait(kSideDown, s));  // this layer's down dW reads dx
+        if (!pre_norms()) return launch_add(dx_mid, dh1, dx, R * H, s);
         DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh1, dx, dx_mid, R, H, eps, 0, inv_attn, s));
         DLLM_TRY(side_fork_from(s, &ws));
         DLLM_TRY(norm_dw(dh1, sv.x_in, inv_attn, H, 1, nseg, G(L.attn_norm), ws));
@@ -1573,7 +1626,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(norm_dw(dhidden, x_final, inv_rms, H, 1, nseg, G(final_norm), s));
         for (bool& pending : side_pending) pending = false;
         side_on = false;
-        if (!profiling) {
+        if (!profiling && !post_norms()) {  // the post norms' buffers are ordered by the one stream
             DLLM_TRY(side_setup());
             side_on = true;
         }
@@ -1970,6 +2023,8 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     for (double m : {c.embedding_multiplier, c.residual_multiplier, c.logits_scaling})
         DLLM_REQUIRE(m >= 0.0 && std::isfinite(m), "multipliers must be finite and non-negative (0: none)");
     DLLM_REQUIRE(c.attention_scale > 0.0 && std::isfinite(c.attention_scale), "attention_scale must be positive");
+    DLLM_REQUIRE(c.norm_placement >= 0 && c.norm_placement <= 2, "norm_placement must be 0 (pre), 1 (post) or 2 (both)");
+    DLLM_REQUIRE(c.norm_placement == 0 || c.experts == 0, "post norms are built for dense MLPs only");
     if (c.experts > 0) {
         bool any_sparse = false;
         for (int64_t l = 0; l < c.layers; ++l) any_sparse = any_sparse || l >= 64 || !((c.dense_layers >> l) & 1);

@@ -27,7 +27,7 @@ class DecoderConfig(C.Structure):
         "expert_intermediate", "rotary_dim")] + [
         ("rms_norm_eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
         ("embedding_multiplier", C.c_double), ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double),
-        ("dense_layers", C.c_int64)]
+        ("dense_layers", C.c_int64), ("norm_placement", C.c_int64)]
 
 
 class AdamWArgs(C.Structure):
@@ -110,6 +110,7 @@ class Decoder:
     residual_multiplier: float = 1.0
     logits_scaling: float = 1.0
     dense_layers: tuple[int, ...] = ()  # layers keeping a dense MLP in a model with experts (Qwen3-MoE)
+    norm_placement: int = 0  # 0 pre, 1 post (OLMo 2), 2 both (architecture.py:315-320)
 
     def native(self) -> DecoderConfig:
         return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
@@ -119,7 +120,8 @@ class Decoder:
                              self.rotary_dim or self.head_dim, self.rms_norm_eps, self.rope_theta,
                              1.0 / float(np.sqrt(np.float64(self.head_dim))) if self.attention_multiplier is None
                              else self.attention_multiplier, self.embedding_multiplier, self.residual_multiplier,
-                             self.logits_scaling, sum(1 << layer for layer in self.dense_layers if layer < 64))
+                             self.logits_scaling, sum(1 << layer for layer in self.dense_layers if layer < 64),
+                             self.norm_placement)
 
 
 def _windows(windows):

@@ -283,6 +283,9 @@ typedef struct {
     /* dense_layers (architecture.py:128, 344-346; Qwen3-MoE's mlp_only_layers): bit l set = layer l keeps a dense
      * MLP of `intermediate` in a model with experts; layers from 64 on are routed */
     int64_t dense_layers;
+    /* norm_placement (architecture.py:315-320): 0 pre (RMSNorm on each block's input), 1 post (on each block's
+     * output before the residual add, OLMo 2), 2 both; post norms with routed experts are not built */
+    int64_t norm_placement;
 } dllm_hip_decoder_config;
 
 typedef struct dllm_hip_trainer dllm_hip_trainer;

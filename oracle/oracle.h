@@ -164,6 +164,9 @@ typedef struct {
     /* dense_layers (architecture.py:128, 344-346): bit l set = layer l keeps a dense MLP in a model with experts
      * (Qwen3-MoE's mlp_only_layers); layers from 64 on are sparse */
     int64_t dense_layers;
+    /* norm_placement (architecture.py:315-320): 0 pre (norms on each block's input), 1 post (on each block's output,
+     * OLMo 2), 2 sandwich (both) */
+    int64_t norm_placement;
 } orc_config;
 
 /* Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346). */
@@ -178,7 +181,7 @@ enum {
     ORC_EMBEDDING = 0, ORC_FINAL_NORM = 1, ORC_LM_HEAD = 2, ORC_GLOBALS = 3,
     ORC_ATTN_NORM = 0, ORC_Q = 1, ORC_K = 2, ORC_V = 3, ORC_QB = 4, ORC_KB = 5, ORC_VB = 6, ORC_QNORM = 7,
     ORC_KNORM = 8, ORC_O = 9, ORC_MLP_NORM = 10, ORC_GATE = 11, ORC_UP = 12, ORC_DOWN = 13, ORC_ROUTER = 14,
-    ORC_LAYER_FIXED = 15
+    ORC_ATTN_POST_NORM = 15, ORC_MLP_POST_NORM = 16, ORC_LAYER_FIXED = 17
 };
 int64_t orc_layer_slots(const orc_config* c);
 int64_t orc_slot_count(const orc_config* c);

@@ -21,6 +21,9 @@ int64_t orc_expert_slot(const orc_config* c, int64_t layer, int64_t expert, int6
     return orc_slot(c, layer, ORC_LAYER_FIXED + 3 * expert + which);
 }
 
+static int has_pre_norms(const orc_config* c) { return c->norm_placement != 1; }
+static int has_post_norms(const orc_config* c) { return c->norm_placement != 0; }
+
 int orc_is_sparse(const orc_config* c, int64_t layer) {
     return c->experts > 0 && !(layer < 64 && ((c->dense_layers >> layer) & 1));
 }
@@ -35,7 +38,8 @@ static int64_t slot_shape(const orc_config* c, int64_t slot, int64_t* d0, int64_
     const int64_t kind = (slot - ORC_GLOBALS) % orc_layer_slots(c);
     const int sparse = orc_is_sparse(c, (slot - ORC_GLOBALS) / orc_layer_slots(c));
     switch (kind) {
-        case ORC_ATTN_NORM: *d0 = H; return 1;
+        case ORC_ATTN_NORM: case ORC_MLP_NORM: if (!has_pre_norms(c)) return 0; *d0 = H; return 1;
+        case ORC_ATTN_POST_NORM: case ORC_MLP_POST_NORM: if (!has_post_norms(c)) return 0; *d0 = H; return 1;
         case ORC_Q: *d0 = q; *d1 = H; return 2;
         case ORC_K: case ORC_V: *d0 = kv; *d1 = H; return 2;
         case ORC_QB: if (!c->attn_bias) return 0; *d0 = q; return 1;
@@ -43,7 +47,6 @@ static int64_t slot_shape(const orc_config* c, int64_t slot, int64_t* d0, int64_
         case ORC_QNORM: if (!c->qk_norm) return 0; *d0 = c->qk_norm == 2 ? q : c->head_dim; return 1;
         case ORC_KNORM: if (!c->qk_norm) return 0; *d0 = c->qk_norm == 2 ? kv : c->head_dim; return 1;
         case ORC_O: *d0 = H; *d1 = q; return 2;
-        case ORC_MLP_NORM: *d0 = H; return 1;
         case ORC_GATE: case ORC_UP: if (sparse) return 0; *d0 = c->inter; *d1 = H; return 2;
         case ORC_DOWN: if (sparse) return 0; *d0 = H; *d1 = c->inter; return 2;
         case ORC_ROUTER: if (!sparse) return 0; *d0 = c->experts; *d1 = H; return 2;
@@ -88,6 +91,7 @@ typedef struct {
 
 typedef struct {
     float *x_in, *h1, *q_raw, *k_raw, *q, *k, *v, *attended, *out, *x_mid, *h2, *mlp;
+    float *out_normed, *mlp_normed; /* post norms: the normalised block outputs (NULL without) */
     swiglu_saved dense;
     float* router_logits; /* [n, experts] */
     int64_t* chosen;      /* [n, topk] */
@@ -175,7 +179,10 @@ static void forward(fwd_state* st, const int64_t* tokens) {
         memset(s, 0, sizeof *s);
         s->x_in = x;
         s->h1 = falloc(n * H);
-        ops->rms_norm(x, w[orc_slot(c, l, ORC_ATTN_NORM)], s->h1, n, H, c->eps, 0);
+        if (has_pre_norms(c))
+            ops->rms_norm(x, w[orc_slot(c, l, ORC_ATTN_NORM)], s->h1, n, H, c->eps, 0);
+        else
+            memcpy(s->h1, x, (size_t)(n * H) * sizeof(float));
         s->q_raw = falloc(n * qd);
         s->k_raw = falloc(n * kvd);
         s->v = falloc(n * kvd);
@@ -211,9 +218,16 @@ static void forward(fwd_state* st, const int64_t* tokens) {
         s->out = falloc(n * H);
         ops->linear(s->attended, w[orc_slot(c, l, ORC_O)], NULL, s->out, n, qd, H);
         s->x_mid = falloc(n * H);
-        vadd(x, s->out, s->x_mid, n * H);
+        if (has_post_norms(c)) {
+            s->out_normed = falloc(n * H);
+            ops->rms_norm(s->out, w[orc_slot(c, l, ORC_ATTN_POST_NORM)], s->out_normed, n, H, c->eps, 0);
+        }
+        vadd(x, has_post_norms(c) ? s->out_normed : s->out, s->x_mid, n * H);
         s->h2 = falloc(n * H);
-        ops->rms_norm(s->x_mid, w[orc_slot(c, l, ORC_MLP_NORM)], s->h2, n, H, c->eps, 0);
+        if (has_pre_norms(c))
+            ops->rms_norm(s->x_mid, w[orc_slot(c, l, ORC_MLP_NORM)], s->h2, n, H, c->eps, 0);
+        else
+            memcpy(s->h2, s->x_mid, (size_t)(n * H) * sizeof(float));
         if (!orc_is_sparse(c, l)) {
             s->dense.rows = n;
             s->dense.x = s->h2;
@@ -257,7 +271,11 @@ static void forward(fwd_state* st, const int64_t* tokens) {
             }
         }
         float* x_out = falloc(n * H);
-        vadd(s->x_mid, s->mlp, x_out, n * H);
+        if (has_post_norms(c)) {
+            s->mlp_normed = falloc(n * H);
+            ops->rms_norm(s->mlp, w[orc_slot(c, l, ORC_MLP_POST_NORM)], s->mlp_normed, n, H, c->eps, 0);
+        }
+        vadd(s->x_mid, has_post_norms(c) ? s->mlp_normed : s->mlp, x_out, n * H);
         x = x_out;
     }
     st->final_input = x;
@@ -270,7 +288,7 @@ static void free_state(fwd_state* st) {
     for (int64_t l = 0; l < c->layers; ++l) {
         layer_saved* s = &st->layers[l];
         free(s->x_in); free(s->h1); free(s->q_raw); free(s->k_raw); free(s->q); free(s->k); free(s->v);
-        free(s->attended); free(s->out); free(s->x_mid); free(s->h2);
+        free(s->attended); free(s->out); free(s->x_mid); free(s->h2); free(s->out_normed); free(s->mlp_normed);
         if (!orc_is_sparse(c, l)) {
             swiglu_free(&s->dense);
         } else {
@@ -531,6 +549,7 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     /* _backward_layer (backprop.py:208-287), layers in reverse */
     float* dh2 = falloc(n * H);
     float* dtmp = falloc(n * H);
+    float* dpost = falloc(n * H);
     float* dx_mid = falloc(n * H);
     float* dattended = falloc(n * qd);
     float* dq_t = falloc(n * qd);
@@ -544,17 +563,33 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     float* dh = falloc(n * H);
     for (int64_t l = c->layers - 1; l >= 0; --l) {
         const layer_saved* s = &st.layers[l];
+        const float* dmlp = dx;
+        if (has_post_norms(c)) {
+            const int64_t pn = orc_slot(c, l, ORC_MLP_POST_NORM);
+            ops->rms_norm_backward(s->mlp, w[pn], dx, dpost, g[pn], n, H, c->eps, 0);
+            dmlp = dpost;
+        }
         if (!orc_is_sparse(c, l)) {
             swiglu_backward(ops, w, g, orc_slot(c, l, ORC_GATE), orc_slot(c, l, ORC_UP), orc_slot(c, l, ORC_DOWN),
-                            c->inter, H, &s->dense, dx, dh2);
+                            c->inter, H, &s->dense, dmlp, dh2);
         } else {
-            experts_backward(&st, l, dx, g, router_scale != 0.0 ? grad_row : NULL, dh2);
+            experts_backward(&st, l, dmlp, g, router_scale != 0.0 ? grad_row : NULL, dh2);
         }
-        const int64_t mn = orc_slot(c, l, ORC_MLP_NORM);
-        ops->rms_norm_backward(s->x_mid, w[mn], dh2, dtmp, g[mn], n, H, c->eps, 0);
-        vadd(dx, dtmp, dx_mid, n * H);
+        if (has_pre_norms(c)) {
+            const int64_t mn = orc_slot(c, l, ORC_MLP_NORM);
+            ops->rms_norm_backward(s->x_mid, w[mn], dh2, dtmp, g[mn], n, H, c->eps, 0);
+            vadd(dx, dtmp, dx_mid, n * H);
+        } else {
+            vadd(dx, dh2, dx_mid, n * H);
+        }
+        const float* dout = dx_mid;
+        if (has_post_norms(c)) {
+            const int64_t pn = orc_slot(c, l, ORC_ATTN_POST_NORM);
+            ops->rms_norm_backward(s->out, w[pn], dx_mid, dpost, g[pn], n, H, c->eps, 0);
+            dout = dpost;
+        }
         const int64_t os = orc_slot(c, l, ORC_O);
-        ops->linear_backward(s->attended, w[os], dx_mid, dattended, g[os], NULL, n, qd, H);
+        ops->linear_backward(s->attended, w[os], dout, dattended, g[os], NULL, n, qd, H);
         ops->attention_backward(s->q, s->k, s->v, dattended, dq_t, dk_t, dv_t, n, n, c->heads, c->kv_heads, hd, hd,
                                 c->attention_scale, 1, 0, c->window, 0.0);
         ops->rope(dq_t, st.positions, st.inv_freq, dq, n, c->heads, hd, c->rotary_dim, 0, 1);
@@ -584,11 +619,15 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
                                  outs[p]);
             if (p > 0) vadd(dh1, dh, dh1, n * H);
         }
-        const int64_t an = orc_slot(c, l, ORC_ATTN_NORM);
-        ops->rms_norm_backward(s->x_in, w[an], dh1, dtmp, g[an], n, H, c->eps, 0);
-        vadd(dx_mid, dtmp, dx, n * H);
+        if (has_pre_norms(c)) {
+            const int64_t an = orc_slot(c, l, ORC_ATTN_NORM);
+            ops->rms_norm_backward(s->x_in, w[an], dh1, dtmp, g[an], n, H, c->eps, 0);
+            vadd(dx_mid, dtmp, dx, n * H);
+        } else {
+            vadd(dx_mid, dh1, dx, n * H);
+        }
     }
-    free(dh2); free(dtmp); free(dx_mid); free(dattended); free(dq_t); free(dk_t); free(dv_t); free(dq); free(dk);
+    free(dh2); free(dtmp); free(dpost); free(dx_mid); free(dattended); free(dq_t); free(dk_t); free(dv_t); free(dq); free(dk);
     free(dq2); free(dk2); free(dh1); free(dh);
 
     /* embedding_backward, tied head (backprop.py:110-117), after the embedding multiplier's gradient */

@@ -33,7 +33,8 @@ class OrcConfig(C.Structure):
         "tied", "experts", "topk", "normalize", "expert_inter", "rotary_dim")] + [
         ("eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
         ("inv_freq", C.c_void_p), ("rope_attention_factor", C.c_double), ("embedding_multiplier", C.c_double),
-        ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double), ("dense_layers", C.c_int64)]
+        ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double), ("dense_layers", C.c_int64),
+        ("norm_placement", C.c_int64)]
 
 
 class OrcRopeScaling(C.Structure):
@@ -373,6 +374,7 @@ class Decoder:
     residual_multiplier: float = 1.0
     logits_scaling: float = 1.0
     dense_layers: tuple[int, ...] = ()  # layers keeping a dense MLP in a model with experts (architecture.py:128)
+    norm_placement: int = 0  # architecture.py:315-320: 0 pre, 1 post (OLMo 2), 2 sandwich (Gemma 2 and 3)
 
     def is_sparse(self, layer: int) -> bool:
         """architecture.py:344-346."""
@@ -393,7 +395,7 @@ class Decoder:
                         int(self.normalize), self.expert_inter or self.inter, self.rotary_dim or self.head_dim,
                         self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor,
                         self.embedding_multiplier, self.residual_multiplier, self.logits_scaling,
-                        sum(1 << layer for layer in self.dense_layers))
+                        sum(1 << layer for layer in self.dense_layers), self.norm_placement)
         inv_freq = self.inv_freq
         if inv_freq is None and self.rope_scaling:
             inv_freq = rope_inv_freq_scaled(self.rotary_dim or self.head_dim, self.rope_theta, self.scaling())
@@ -410,7 +412,8 @@ class Decoder:
         shapes = {"token_embedding.weight": (self.vocab, H)}
         for i in range(self.layers):
             p = f"layers.{i}."
-            shapes[p + "attention_norm.weight"] = (H,)
+            if self.norm_placement != 1:
+                shapes[p + "attention_norm.weight"] = (H,)
             shapes[p + "attention.q.weight"] = (q, H)
             shapes[p + "attention.k.weight"] = (kv, H)
             shapes[p + "attention.v.weight"] = (kv, H)
@@ -422,7 +425,11 @@ class Decoder:
                 shapes[p + "attention.q_norm.weight"] = (q if self.qk_norm == 2 else self.head_dim,)
                 shapes[p + "attention.k_norm.weight"] = (kv if self.qk_norm == 2 else self.head_dim,)
             shapes[p + "attention.o.weight"] = (H, q)
-            shapes[p + "mlp_norm.weight"] = (H,)
+            if self.norm_placement != 0:
+                shapes[p + "attention_post_norm.weight"] = (H,)
+                shapes[p + "mlp_post_norm.weight"] = (H,)
+            if self.norm_placement != 1:
+                shapes[p + "mlp_norm.weight"] = (H,)
             if self.is_sparse(i):
                 e_inter = self.expert_inter or self.inter
                 shapes[p + "mlp.router.weight"] = (self.experts, H)
@@ -448,17 +455,17 @@ class Decoder:
                  "attention.v.weight": 3, "attention.q.bias": 4, "attention.k.bias": 5, "attention.v.bias": 6,
                  "attention.q_norm.weight": 7, "attention.k_norm.weight": 8, "attention.o.weight": 9,
                  "mlp_norm.weight": 10, "mlp.gate.weight": 11, "mlp.up.weight": 12, "mlp.down.weight": 13,
-                 "mlp.router.weight": 14}
+                 "mlp.router.weight": 14, "attention_post_norm.weight": 15, "mlp_post_norm.weight": 16}
         _, layer, rest = name.split(".", 2)
-        per_layer = 15 + 3 * self.experts
+        per_layer = 17 + 3 * self.experts
         base = 3 + int(layer) * per_layer
         if rest in kinds:
             return base + kinds[rest]
         _, _, expert, which, _ = rest.split(".")
-        return base + 15 + 3 * int(expert) + {"gate": 0, "up": 1, "down": 2}[which]
+        return base + 17 + 3 * int(expert) + {"gate": 0, "up": 1, "down": 2}[which]
 
     def slot_count(self) -> int:
-        return 3 + self.layers * (15 + 3 * self.experts)
+        return 3 + self.layers * (17 + 3 * self.experts)
 
 
 def natural_key(name: str):
@@ -499,6 +506,7 @@ FIXTURES = {
                           **{**TINY, "inter": 8}),
     "qwen3_moe": Decoder("qwen3_moe", tied=True, qk_norm=1, experts=4, topk=2, normalize=True, expert_inter=8,
                          dense_layers=(0,), **{**TINY, "head_dim": 8}),
+    "olmo2": Decoder("olmo2", tied=False, qk_norm=2, norm_placement=1, **TINY),
     "phi3": Decoder("phi3", tied=False, window=3, rotary_dim=4, rope_attention_factor=4.0,
                     rope_scaling=frozen_scaling(PHI3_SCALING), **{**TINY, "hidden": 32, "head_dim": 8}),
 }

@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_goldens.json").read_text())
 TOKENS = [1, 17, 42, 5, 63, 0, 9, 9, 30]
-FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe", "qwen3_moe"]
+FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe", "qwen3_moe", "olmo2"]
 
 
 def gpu_decoder(d: O.Decoder):
@@ -26,7 +26,7 @@ def gpu_decoder(d: O.Decoder):
                    d.tied, d.attn_bias, d.qk_norm, d.window, d.experts, d.topk, d.normalize, d.expert_inter,
                    rotary_dim=d.rotary_dim, rope_scaling=d.scaling(), embedding_multiplier=d.embedding_multiplier,
                    attention_multiplier=d.attention_multiplier, residual_multiplier=d.residual_multiplier,
-                   logits_scaling=d.logits_scaling, dense_layers=d.dense_layers)
+                   logits_scaling=d.logits_scaling, dense_layers=d.dense_layers, norm_placement=d.norm_placement)
 
 
 def make_trainer(d: O.Decoder, weights, max_tokens=64, max_windows=8, max_window=32):
@@ -547,3 +547,38 @@ def test_step_with_rope_scaling_matches_the_oracle(case):
                 shape = d.tensor_shapes()[name]
                 assert t.get(name, shape, t.GRAD).tobytes() == out["weight_grads"][name].tobytes(), (step, name)
     t.close()
+
+
+NORM_CASES = {
+    # OLMo 2: RMSNorm on each block's output before the residual add, whole-projection QK-norm, untied head
+    "post": O.Decoder("olmo2", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16, eps=1e-6,
+                      rope_theta=5e5, tied=False, qk_norm=2, norm_placement=1),
+    # both placements (the Gemma layout's norms) with a residual multiplier folded into the output projections
+    "sandwich": O.Decoder("llama", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16,
+                          eps=1e-5, rope_theta=1e4, tied=True, norm_placement=2, residual_multiplier=0.5),
+}
+
+
+@pytest.mark.parametrize("case", sorted(NORM_CASES))
+def test_norm_placement_step_matches_the_oracle(case):
+    """Post and sandwich norm placement (backprop.py:222-287, 452-463): two steps over ragged windows, every gradient,
+    parameter and moment against the oracle."""
+    d = NORM_CASES[case]
+    weights = O.synthetic_weights(d, seed=41, scale=0.05)
+    rng = O.Random(43)
+    windows = [[rng.next_u64() % d.vocab for _ in range(n)] for n in (33, 2, 70, 17)]
+    t = make_trainer(d, weights, max_tokens=256, max_windows=4, max_window=128)
+    params = {n: a.copy() for n, a in weights.items()}
+    m = {n: np.zeros_like(a) for n, a in params.items()}
+    v = {n: np.zeros_like(a) for n, a in params.items()}
+    opt = O.AdamWConfig(learning_rate=1e-3, schedule="constant")
+    for step in (1, 2):
+        loss_gpu, norm_gpu = t.step(windows, 1e-3, step)
+        loss_cpu, _, norm_cpu, grads = O.train_step(O.oracle_kernels(), d, params, m, v, windows, opt, step, 2)
+        assert loss_gpu == loss_cpu and norm_gpu == norm_cpu
+    for name in t.names:
+        shape = d.tensor_shapes()[name]
+        assert t.get(name, shape, t.GRAD).tobytes() == grads[name].tobytes(), name
+        assert t.get(name, shape).tobytes() == params[name].tobytes(), name
+        assert t.get(name, shape, t.M).tobytes() == m[name].tobytes(), name
+        assert t.get(name, shape, t.V).tobytes() == v[name].tobytes(), name

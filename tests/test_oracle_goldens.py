@@ -201,6 +201,7 @@ def test_forward_logits_match_tiny_logits_fingerprint(family):
 @pytest.mark.parametrize(("name", "family", "factor", "original"), [
     ("llama-yarn", "llama", 4.0, 2048),  # dllm import --context-length 8192 of the tiny Llama (2048 positions)
     ("qwen3-yarn", "qwen3", 4.0, 4),  # Qwen3 with a YaRN rope_scaling: the factor folds into its QK-norm weights
+    ("olmo2-yarn", "olmo2", 2.0, 2048),  # --context-length 4096 of OLMo 2: folds into its whole-projection QK-norm
 ])
 def test_yarn_models_match_long_context_fingerprints(name, family, factor, original):
     """reference tests/test_long_context.py:168-189 (LONG_MODELS): the YaRN frequencies and the attention factor
