@@ -1118,10 +1118,25 @@ static void silu_backward_n(const float* x, const float* dy, float* out, size_t 
     for (size_t i = 0; i < n; ++i) out[i] = orc_silu_backward(x[i], dy[i]);
 }
 
+static void gelu_tanh_n(const float* x, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_gelu_tanh(x[i]);
+}
+static void gelu_tanh_backward_n(const float* x, const float* dy, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_gelu_tanh_backward(x[i], dy[i]);
+}
+/* softcap (nn.hpp:457-461): cap tanh(x / cap) in double, rounded once. */
+static void softcap_n(const float* x, float* out, size_t n, double cap) {
+    for (size_t i = 0; i < n; ++i) out[i] = (float)(cap * orc_tanh((double)x[i] / cap));
+}
+static void softcap_backward_n(const float* x, const float* dy, float* out, size_t n, double cap) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_softcap_backward(x[i], dy[i], cap);
+}
+
 static const orc_ops default_ops = {
     orc_linear, orc_linear_backward, orc_rms_norm, orc_rms_norm_backward, orc_rope, orc_attention,
     orc_attention_backward, silu_n, orc_swiglu, silu_backward_n, orc_cross_entropy, orc_embedding_backward,
     orc_sum_squares, orc_adamw_step, orc_softmax, orc_moe_route, orc_moe_route_backward, orc_column_mean, orc_dot,
+    gelu_tanh_n, gelu_tanh_backward_n, softcap_n, softcap_backward_n,
 };
 
 const orc_ops* orc_default_ops(void) { return &default_ops; }

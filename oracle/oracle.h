@@ -142,6 +142,10 @@ typedef struct {
                                size_t, int);
     void (*column_mean)(const float*, float*, size_t, size_t);
     float (*dot)(const float*, const float*, size_t);
+    void (*gelu_tanh)(const float*, float*, size_t);
+    void (*gelu_tanh_backward)(const float*, const float*, float*, size_t);
+    void (*softcap)(const float*, float*, size_t, double);
+    void (*softcap_backward)(const float*, const float*, float*, size_t, double);
 } orc_ops;
 
 const orc_ops* orc_default_ops(void);
@@ -167,6 +171,13 @@ typedef struct {
     /* norm_placement (architecture.py:315-320): 0 pre (norms on each block's input), 1 post (on each block's output,
      * OLMo 2), 2 sandwich (both) */
     int64_t norm_placement;
+    /* Gemma 2 and 3 (architecture.py): RMSNorm weights used as 1 + w (norm_unit_offset); activation 0 SiLU, 1 GELU with
+     * the tanh approximation; full_attention_layers: bit l set = layer l ignores the sliding window (the layers not in
+     * sliding_window_layers, architecture.py:353-359); local_rope_theta (0: none) rotates the windowed layers with that
+     * base and no scaling (architecture.py:322-324, backprop.py:63-67); attention_softcap and logits_softcap (0: none)
+     * map scores and logits s to cap tanh(s / cap) */
+    int64_t norm_unit_offset, activation, full_attention_layers;
+    double local_rope_theta, attention_softcap, logits_softcap;
 } orc_config;
 
 /* Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346). */

@@ -116,10 +116,27 @@ float dot(const float* a, const float* b, size_t n) {
     return dllm::dot(a, b, n);
 }
 
+void gelu_tanh(const float* x, float* out, size_t n) {
+    FpEnvGuard guard;
+    for (size_t i = 0; i < n; ++i) out[i] = dllm::gelu_tanh(x[i]);
+}
+void gelu_tanh_backward(const float* x, const float* dy, float* out, size_t n) {
+    FpEnvGuard guard;
+    for (size_t i = 0; i < n; ++i) out[i] = dllm::gelu_tanh_backward(x[i], dy[i]);
+}
+void softcap(const float* x, float* out, size_t n, double cap) {
+    FpEnvGuard guard;
+    dllm::softcap(x, out, n, cap);
+}
+void softcap_backward(const float* x, const float* dy, float* out, size_t n, double cap) {
+    FpEnvGuard guard;
+    for (size_t i = 0; i < n; ++i) out[i] = dllm::softcap_backward(x[i], dy[i], cap);
+}
+
 const orc_ops kRefOps = {
     linear, linear_backward, rms_norm, rms_norm_backward, rope, attention, attention_backward, silu, swiglu,
     silu_backward, cross_entropy, embedding_backward, sum_squares, adamw_step, softmax, moe_route,
-    moe_route_backward, column_mean, dot,
+    moe_route_backward, column_mean, dot, gelu_tanh, gelu_tanh_backward, softcap, softcap_backward,
 };
 
 }  // namespace

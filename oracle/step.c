@@ -100,7 +100,7 @@ typedef struct {
 } layer_saved;
 
 static void swiglu_forward(const orc_ops* ops, float* const* w, int64_t gate_slot, int64_t up_slot, int64_t down_slot,
-                           int64_t inter, int64_t H, swiglu_saved* s) {
+                           int64_t inter, int64_t H, swiglu_saved* s, int act) {
     const int64_t n = s->rows;
     s->gate = falloc(n * inter);
     s->up = falloc(n * inter);
@@ -109,7 +109,10 @@ static void swiglu_forward(const orc_ops* ops, float* const* w, int64_t gate_slo
     s->y = falloc(n * H);
     ops->linear(s->x, w[gate_slot], NULL, s->gate, n, H, inter);
     ops->linear(s->x, w[up_slot], NULL, s->up, n, H, inter);
-    ops->silu(s->gate, s->gate_act, n * inter);
+    if (act == 1)
+        ops->gelu_tanh(s->gate, s->gate_act, n * inter);
+    else
+        ops->silu(s->gate, s->gate_act, n * inter);
     vmul(s->gate_act, s->up, s->product, n * inter);
     ops->linear(s->product, w[down_slot], NULL, s->y, n, inter, H);
 }
@@ -121,7 +124,7 @@ static void swiglu_free(swiglu_saved* s) {
 /* _swiglu_backward (backprop.py:289-306): returns dx = dx_gate + dx_up in `dx`. */
 static void swiglu_backward(const orc_ops* ops, float* const* w, float* const* g, int64_t gate_slot, int64_t up_slot,
                             int64_t down_slot, int64_t inter, int64_t H, const swiglu_saved* s, const float* dy,
-                            float* dx) {
+                            float* dx, int act) {
     const int64_t n = s->rows;
     float* dproduct = falloc(n * inter);
     float* t = falloc(n * inter);
@@ -131,7 +134,10 @@ static void swiglu_backward(const orc_ops* ops, float* const* w, float* const* g
     float* dx_up = falloc(n * H);
     ops->linear_backward(s->product, w[down_slot], dy, dproduct, g[down_slot], NULL, n, inter, H);
     vmul(dproduct, s->up, t, n * inter);
-    ops->silu_backward(s->gate, t, dgate, n * inter);
+    if (act == 1)
+        ops->gelu_tanh_backward(s->gate, t, dgate, n * inter);
+    else
+        ops->silu_backward(s->gate, t, dgate, n * inter);
     vmul(dproduct, s->gate_act, dup, n * inter);
     ops->linear_backward(s->x, w[gate_slot], dgate, dx_gate, g[gate_slot], NULL, n, H, inter);
     ops->linear_backward(s->x, w[up_slot], dup, dx_up, g[up_slot], NULL, n, H, inter);
@@ -146,10 +152,22 @@ typedef struct {
     int64_t n;
     int64_t* positions;
     double* inv_freq;
+    double* local_inv_freq; /* the windowed layers' (Gemma 3), or inv_freq itself */
     layer_saved* layers;
     float* final_input;
     float* hidden;
 } fwd_state;
+
+/* TransformerConfig.window (architecture.py:353-359): the layer's window, 0 for full causal attention. */
+static int64_t layer_window(const orc_config* c, int64_t layer) {
+    if (c->window == 0) return 0;
+    return layer < 64 && ((c->full_attention_layers >> layer) & 1) ? 0 : c->window;
+}
+
+/* The inverse frequencies layer l rotates with (uses_local_rope, architecture.py:322-324). */
+static const double* layer_inv_freq(const fwd_state* st, int64_t layer) {
+    return st->c->local_rope_theta != 0.0 && layer_window(st->c, layer) != 0 ? st->local_inv_freq : st->inv_freq;
+}
 
 /* A multiplier of the config that is present (neither 1 nor unset). */
 static int has_multiplier(double m) { return m != 0.0 && m != 1.0; }
@@ -180,7 +198,7 @@ static void forward(fwd_state* st, const int64_t* tokens) {
         s->x_in = x;
         s->h1 = falloc(n * H);
         if (has_pre_norms(c))
-            ops->rms_norm(x, w[orc_slot(c, l, ORC_ATTN_NORM)], s->h1, n, H, c->eps, 0);
+            ops->rms_norm(x, w[orc_slot(c, l, ORC_ATTN_NORM)], s->h1, n, H, c->eps, (int)c->norm_unit_offset);
         else
             memcpy(s->h1, x, (size_t)(n * H) * sizeof(float));
         s->q_raw = falloc(n * qd);
@@ -197,42 +215,42 @@ static void forward(fwd_state* st, const int64_t* tokens) {
             qtmp = falloc(n * qd);
             ktmp = falloc(n * kvd);
             if (c->qk_norm == 2) {
-                ops->rms_norm(s->q_raw, w[orc_slot(c, l, ORC_QNORM)], qtmp, n, qd, c->eps, 0);
-                ops->rms_norm(s->k_raw, w[orc_slot(c, l, ORC_KNORM)], ktmp, n, kvd, c->eps, 0);
+                ops->rms_norm(s->q_raw, w[orc_slot(c, l, ORC_QNORM)], qtmp, n, qd, c->eps, (int)c->norm_unit_offset);
+                ops->rms_norm(s->k_raw, w[orc_slot(c, l, ORC_KNORM)], ktmp, n, kvd, c->eps, (int)c->norm_unit_offset);
             } else {
-                ops->rms_norm(s->q_raw, w[orc_slot(c, l, ORC_QNORM)], qtmp, n * c->heads, hd, c->eps, 0);
-                ops->rms_norm(s->k_raw, w[orc_slot(c, l, ORC_KNORM)], ktmp, n * c->kv_heads, hd, c->eps, 0);
+                ops->rms_norm(s->q_raw, w[orc_slot(c, l, ORC_QNORM)], qtmp, n * c->heads, hd, c->eps, (int)c->norm_unit_offset);
+                ops->rms_norm(s->k_raw, w[orc_slot(c, l, ORC_KNORM)], ktmp, n * c->kv_heads, hd, c->eps, (int)c->norm_unit_offset);
             }
             qn = qtmp;
             kn = ktmp;
         }
         s->q = falloc(n * qd);
         s->k = falloc(n * kvd);
-        ops->rope(qn, st->positions, st->inv_freq, s->q, n, c->heads, hd, c->rotary_dim, 0, 0);
-        ops->rope(kn, st->positions, st->inv_freq, s->k, n, c->kv_heads, hd, c->rotary_dim, 0, 0);
+        ops->rope(qn, st->positions, layer_inv_freq(st, l), s->q, n, c->heads, hd, c->rotary_dim, 0, 0);
+        ops->rope(kn, st->positions, layer_inv_freq(st, l), s->k, n, c->kv_heads, hd, c->rotary_dim, 0, 0);
         free(qtmp);
         free(ktmp);
         s->attended = falloc(n * qd);
         ops->attention(s->q, s->k, s->v, s->attended, n, n, c->heads, c->kv_heads, hd, hd, c->attention_scale, 1, 0,
-                       c->window, 0.0);
+                       layer_window(c, l), c->attention_softcap);
         s->out = falloc(n * H);
         ops->linear(s->attended, w[orc_slot(c, l, ORC_O)], NULL, s->out, n, qd, H);
         s->x_mid = falloc(n * H);
         if (has_post_norms(c)) {
             s->out_normed = falloc(n * H);
-            ops->rms_norm(s->out, w[orc_slot(c, l, ORC_ATTN_POST_NORM)], s->out_normed, n, H, c->eps, 0);
+            ops->rms_norm(s->out, w[orc_slot(c, l, ORC_ATTN_POST_NORM)], s->out_normed, n, H, c->eps, (int)c->norm_unit_offset);
         }
         vadd(x, has_post_norms(c) ? s->out_normed : s->out, s->x_mid, n * H);
         s->h2 = falloc(n * H);
         if (has_pre_norms(c))
-            ops->rms_norm(s->x_mid, w[orc_slot(c, l, ORC_MLP_NORM)], s->h2, n, H, c->eps, 0);
+            ops->rms_norm(s->x_mid, w[orc_slot(c, l, ORC_MLP_NORM)], s->h2, n, H, c->eps, (int)c->norm_unit_offset);
         else
             memcpy(s->h2, s->x_mid, (size_t)(n * H) * sizeof(float));
         if (!orc_is_sparse(c, l)) {
             s->dense.rows = n;
             s->dense.x = s->h2;
             swiglu_forward(ops, w, orc_slot(c, l, ORC_GATE), orc_slot(c, l, ORC_UP), orc_slot(c, l, ORC_DOWN), c->inter,
-                           H, &s->dense);
+                           H, &s->dense, (int)c->activation);
             s->mlp = s->dense.y;
         } else {
             const int64_t E = c->experts, K = c->topk;
@@ -262,7 +280,7 @@ static void forward(fwd_state* st, const int64_t* tokens) {
                             ++m;
                         }
                 swiglu_forward(ops, w, orc_expert_slot(c, l, e, 0), orc_expert_slot(c, l, e, 1),
-                               orc_expert_slot(c, l, e, 2), c->expert_inter, H, gsv);
+                               orc_expert_slot(c, l, e, 2), c->expert_inter, H, gsv, (int)c->activation);
                 for (int64_t i = 0; i < count; ++i) {
                     const float weight = s->routing[gsv->row_index[i] * K + gsv->rank[i]];
                     float* o = s->mlp + gsv->row_index[i] * H;
@@ -273,14 +291,14 @@ static void forward(fwd_state* st, const int64_t* tokens) {
         float* x_out = falloc(n * H);
         if (has_post_norms(c)) {
             s->mlp_normed = falloc(n * H);
-            ops->rms_norm(s->mlp, w[orc_slot(c, l, ORC_MLP_POST_NORM)], s->mlp_normed, n, H, c->eps, 0);
+            ops->rms_norm(s->mlp, w[orc_slot(c, l, ORC_MLP_POST_NORM)], s->mlp_normed, n, H, c->eps, (int)c->norm_unit_offset);
         }
         vadd(s->x_mid, has_post_norms(c) ? s->mlp_normed : s->mlp, x_out, n * H);
         x = x_out;
     }
     st->final_input = x;
     st->hidden = falloc(n * H);
-    ops->rms_norm(x, w[ORC_FINAL_NORM], st->hidden, n, H, c->eps, 0);
+    ops->rms_norm(x, w[ORC_FINAL_NORM], st->hidden, n, H, c->eps, (int)c->norm_unit_offset);
 }
 
 static void free_state(fwd_state* st) {
@@ -306,6 +324,7 @@ static void free_state(fwd_state* st) {
     free(st->hidden);
     free(st->layers);
     free(st->positions);
+    if (st->local_inv_freq != st->inv_freq) free(st->local_inv_freq);
     free(st->inv_freq);
 }
 
@@ -321,6 +340,11 @@ static void init_state(fwd_state* st, const orc_ops* ops, const orc_config* c, f
         memcpy(st->inv_freq, c->inv_freq, (size_t)(c->rotary_dim / 2) * sizeof(double));
     else
         orc_rope_inv_freq((size_t)c->rotary_dim, c->rope_theta, st->inv_freq);
+    st->local_inv_freq = st->inv_freq;
+    if (c->local_rope_theta != 0.0) {
+        st->local_inv_freq = (double*)malloc((size_t)(c->rotary_dim / 2 + 1) * sizeof(double));
+        orc_rope_inv_freq((size_t)c->rotary_dim, c->local_rope_theta, st->local_inv_freq);
+    }
     st->layers = (layer_saved*)calloc((size_t)c->layers, sizeof(layer_saved));
 }
 
@@ -423,6 +447,7 @@ int orc_logits(const orc_ops* ops, const orc_config* c, float* const* w_stored, 
     forward(&st, tokens);
     ops->linear(st.hidden, w[c->tied ? ORC_EMBEDDING : ORC_LM_HEAD], NULL, logits, n, c->hidden, c->vocab);
     if (has_multiplier(c->logits_scaling)) vdivide(logits, (float)c->logits_scaling, n * c->vocab);
+    if (c->logits_softcap != 0.0) ops->softcap(logits, logits, (size_t)(n * c->vocab), c->logits_softcap);
     free_state(&st);
     free_folded(c, folded, owned);
     return 0;
@@ -488,7 +513,7 @@ static void experts_backward(const fwd_state* st, int64_t l, const float* dmlp, 
             for (int64_t d = 0; d < H; ++d) dy[i * H + d] = dout[i * H + d] * weight;
         }
         swiglu_backward(ops, w, g, orc_expert_slot(c, l, e, 0), orc_expert_slot(c, l, e, 1),
-                        orc_expert_slot(c, l, e, 2), c->expert_inter, H, gsv, dy, dx);
+                        orc_expert_slot(c, l, e, 2), c->expert_inter, H, gsv, dy, dx, (int)c->activation);
         for (int64_t i = 0; i < m; ++i) {
             float* o = dh2 + gsv->row_index[i] * H;
             for (int64_t d = 0; d < H; ++d) o[d] = o[d] + dx[i * H + d];
@@ -535,7 +560,14 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     float* dlogits = falloc(n * V);
     ops->linear(st.hidden, head, NULL, logits, n, H, V);
     if (has_multiplier(c->logits_scaling)) vdivide(logits, (float)c->logits_scaling, n * V);
-    *loss = ops->cross_entropy(logits, targets, dlogits, n, V, scale);
+    float* capped = NULL; /* _finish (backprop.py:174-181): the capped logits; `logits` keeps the uncapped ones */
+    if (c->logits_softcap != 0.0) {
+        capped = falloc(n * V);
+        ops->softcap(logits, capped, (size_t)(n * V), c->logits_softcap);
+    }
+    *loss = ops->cross_entropy(capped ? capped : logits, targets, dlogits, n, V, scale);
+    if (capped) ops->softcap_backward(logits, dlogits, dlogits, (size_t)(n * V), c->logits_softcap);
+    free(capped);
     free(logits);
     if (has_multiplier(c->logits_scaling)) vdivide(dlogits, (float)c->logits_scaling, n * V);
     float* dhidden = falloc(n * H);
@@ -543,7 +575,7 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
     ops->linear_backward(st.hidden, head, dlogits, dhidden, dhead, NULL, n, H, V);
     free(dlogits);
     float* dx = falloc(n * H);
-    ops->rms_norm_backward(st.final_input, w[ORC_FINAL_NORM], dhidden, dx, g[ORC_FINAL_NORM], n, H, c->eps, 0);
+    ops->rms_norm_backward(st.final_input, w[ORC_FINAL_NORM], dhidden, dx, g[ORC_FINAL_NORM], n, H, c->eps, (int)c->norm_unit_offset);
     free(dhidden);
 
     /* _backward_layer (backprop.py:208-287), layers in reverse */
@@ -566,18 +598,18 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
         const float* dmlp = dx;
         if (has_post_norms(c)) {
             const int64_t pn = orc_slot(c, l, ORC_MLP_POST_NORM);
-            ops->rms_norm_backward(s->mlp, w[pn], dx, dpost, g[pn], n, H, c->eps, 0);
+            ops->rms_norm_backward(s->mlp, w[pn], dx, dpost, g[pn], n, H, c->eps, (int)c->norm_unit_offset);
             dmlp = dpost;
         }
         if (!orc_is_sparse(c, l)) {
             swiglu_backward(ops, w, g, orc_slot(c, l, ORC_GATE), orc_slot(c, l, ORC_UP), orc_slot(c, l, ORC_DOWN),
-                            c->inter, H, &s->dense, dmlp, dh2);
+                            c->inter, H, &s->dense, dmlp, dh2, (int)c->activation);
         } else {
             experts_backward(&st, l, dmlp, g, router_scale != 0.0 ? grad_row : NULL, dh2);
         }
         if (has_pre_norms(c)) {
             const int64_t mn = orc_slot(c, l, ORC_MLP_NORM);
-            ops->rms_norm_backward(s->x_mid, w[mn], dh2, dtmp, g[mn], n, H, c->eps, 0);
+            ops->rms_norm_backward(s->x_mid, w[mn], dh2, dtmp, g[mn], n, H, c->eps, (int)c->norm_unit_offset);
             vadd(dx, dtmp, dx_mid, n * H);
         } else {
             vadd(dx, dh2, dx_mid, n * H);
@@ -585,25 +617,25 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
         const float* dout = dx_mid;
         if (has_post_norms(c)) {
             const int64_t pn = orc_slot(c, l, ORC_ATTN_POST_NORM);
-            ops->rms_norm_backward(s->out, w[pn], dx_mid, dpost, g[pn], n, H, c->eps, 0);
+            ops->rms_norm_backward(s->out, w[pn], dx_mid, dpost, g[pn], n, H, c->eps, (int)c->norm_unit_offset);
             dout = dpost;
         }
         const int64_t os = orc_slot(c, l, ORC_O);
         ops->linear_backward(s->attended, w[os], dout, dattended, g[os], NULL, n, qd, H);
         ops->attention_backward(s->q, s->k, s->v, dattended, dq_t, dk_t, dv_t, n, n, c->heads, c->kv_heads, hd, hd,
-                                c->attention_scale, 1, 0, c->window, 0.0);
-        ops->rope(dq_t, st.positions, st.inv_freq, dq, n, c->heads, hd, c->rotary_dim, 0, 1);
-        ops->rope(dk_t, st.positions, st.inv_freq, dk, n, c->kv_heads, hd, c->rotary_dim, 0, 1);
+                                c->attention_scale, 1, 0, layer_window(c, l), c->attention_softcap);
+        ops->rope(dq_t, st.positions, layer_inv_freq(&st, l), dq, n, c->heads, hd, c->rotary_dim, 0, 1);
+        ops->rope(dk_t, st.positions, layer_inv_freq(&st, l), dk, n, c->kv_heads, hd, c->rotary_dim, 0, 1);
         const float* dqf = dq;
         const float* dkf = dk;
         if (c->qk_norm) {
             const int64_t qs = orc_slot(c, l, ORC_QNORM), ks = orc_slot(c, l, ORC_KNORM);
             if (c->qk_norm == 1) {
-                ops->rms_norm_backward(s->q_raw, w[qs], dq, dq2, g[qs], n * c->heads, hd, c->eps, 0);
-                ops->rms_norm_backward(s->k_raw, w[ks], dk, dk2, g[ks], n * c->kv_heads, hd, c->eps, 0);
+                ops->rms_norm_backward(s->q_raw, w[qs], dq, dq2, g[qs], n * c->heads, hd, c->eps, (int)c->norm_unit_offset);
+                ops->rms_norm_backward(s->k_raw, w[ks], dk, dk2, g[ks], n * c->kv_heads, hd, c->eps, (int)c->norm_unit_offset);
             } else {
-                ops->rms_norm_backward(s->q_raw, w[qs], dq, dq2, g[qs], n, qd, c->eps, 0);
-                ops->rms_norm_backward(s->k_raw, w[ks], dk, dk2, g[ks], n, kvd, c->eps, 0);
+                ops->rms_norm_backward(s->q_raw, w[qs], dq, dq2, g[qs], n, qd, c->eps, (int)c->norm_unit_offset);
+                ops->rms_norm_backward(s->k_raw, w[ks], dk, dk2, g[ks], n, kvd, c->eps, (int)c->norm_unit_offset);
             }
             dqf = dq2;
             dkf = dk2;
@@ -621,7 +653,7 @@ static int window_gradients(const orc_ops* ops, const orc_config* c, float* cons
         }
         if (has_pre_norms(c)) {
             const int64_t an = orc_slot(c, l, ORC_ATTN_NORM);
-            ops->rms_norm_backward(s->x_in, w[an], dh1, dtmp, g[an], n, H, c->eps, 0);
+            ops->rms_norm_backward(s->x_in, w[an], dh1, dtmp, g[an], n, H, c->eps, (int)c->norm_unit_offset);
             vadd(dx_mid, dtmp, dx, n * H);
         } else {
             vadd(dx_mid, dh1, dx, n * H);

@@ -34,7 +34,9 @@ class OrcConfig(C.Structure):
         ("eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
         ("inv_freq", C.c_void_p), ("rope_attention_factor", C.c_double), ("embedding_multiplier", C.c_double),
         ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double), ("dense_layers", C.c_int64),
-        ("norm_placement", C.c_int64)]
+        ("norm_placement", C.c_int64), ("norm_unit_offset", C.c_int64), ("activation", C.c_int64),
+        ("full_attention_layers", C.c_int64), ("local_rope_theta", C.c_double), ("attention_softcap", C.c_double),
+        ("logits_softcap", C.c_double)]
 
 
 class OrcRopeScaling(C.Structure):
@@ -375,6 +377,21 @@ class Decoder:
     logits_scaling: float = 1.0
     dense_layers: tuple[int, ...] = ()  # layers keeping a dense MLP in a model with experts (architecture.py:128)
     norm_placement: int = 0  # architecture.py:315-320: 0 pre, 1 post (OLMo 2), 2 sandwich (Gemma 2 and 3)
+    # Gemma (architecture.py, importer.py:283-345, 416-424, 438-461): norms as 1 + w, GELU-tanh MLPs, the window on
+    # the layers in window_layers only (None: every layer), a RoPE base of their own for those, soft-capped scores and
+    # logits
+    unit_offset: bool = False
+    activation: int = 0  # 0 SiLU, 1 GELU (tanh approximation)
+    window_layers: tuple[int, ...] | None = None
+    local_rope_theta: float | None = None
+    attention_softcap: float | None = None
+    logits_softcap: float | None = None
+
+    def full_attention_mask(self) -> int:
+        """Bit l set: layer l ignores the sliding window (not in window_layers)."""
+        if self.window_layers is None:
+            return 0
+        return sum(1 << layer for layer in range(self.layers) if layer not in self.window_layers)
 
     def is_sparse(self, layer: int) -> bool:
         """architecture.py:344-346."""
@@ -395,7 +412,9 @@ class Decoder:
                         int(self.normalize), self.expert_inter or self.inter, self.rotary_dim or self.head_dim,
                         self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor,
                         self.embedding_multiplier, self.residual_multiplier, self.logits_scaling,
-                        sum(1 << layer for layer in self.dense_layers), self.norm_placement)
+                        sum(1 << layer for layer in self.dense_layers), self.norm_placement, int(self.unit_offset),
+                        self.activation, self.full_attention_mask(), self.local_rope_theta or 0.0,
+                        self.attention_softcap or 0.0, self.logits_softcap or 0.0)
         inv_freq = self.inv_freq
         if inv_freq is None and self.rope_scaling:
             inv_freq = rope_inv_freq_scaled(self.rotary_dim or self.head_dim, self.rope_theta, self.scaling())
@@ -507,6 +526,13 @@ FIXTURES = {
     "qwen3_moe": Decoder("qwen3_moe", tied=True, qk_norm=1, experts=4, topk=2, normalize=True, expert_inter=8,
                          dense_layers=(0,), **{**TINY, "head_dim": 8}),
     "olmo2": Decoder("olmo2", tied=False, qk_norm=2, norm_placement=1, **TINY),
+    "gemma2": Decoder("gemma2", tied=True, norm_placement=2, unit_offset=True, activation=1, window=3,
+                      window_layers=(0,), embedding_multiplier=math.sqrt(16), attention_multiplier=12.0 ** -0.5,
+                      attention_softcap=0.02, logits_softcap=0.05, **{**TINY, "head_dim": 8}),
+    "gemma3": Decoder("gemma3", tied=True, qk_norm=1, norm_placement=2, unit_offset=True, activation=1, window=3,
+                      window_layers=(0,), local_rope_theta=100.0, embedding_multiplier=math.sqrt(16),
+                      attention_multiplier=12.0 ** -0.5, rope_scaling=(("rope_type", "linear"), ("factor", 2.0)),
+                      **{**TINY, "head_dim": 8}),
     "phi3": Decoder("phi3", tied=False, window=3, rotary_dim=4, rope_attention_factor=4.0,
                     rope_scaling=frozen_scaling(PHI3_SCALING), **{**TINY, "hidden": 32, "head_dim": 8}),
 }
@@ -518,6 +544,7 @@ QLORA_FIXTURES = {
     "qwen3": Decoder("qwen3", tied=True, qk_norm=1, **{**TINY, "hidden": 32, "vocab": 264, "head_dim": 8}),
     "granite": replace(FIXTURES["granite"], hidden=32, vocab=264, head_dim=8),
     "qwen3_moe": replace(FIXTURES["qwen3_moe"], hidden=32, vocab=264),
+    "gemma2": replace(FIXTURES["gemma2"], hidden=32, vocab=264, embedding_multiplier=math.sqrt(32)),
 }
 
 
