@@ -102,9 +102,10 @@ int launch_rope(const float* x, const int64_t* pos_index, const double* cos_tabl
                 float* out, int64_t tokens, int64_t heads, int64_t head_dim, int64_t rotary_dim, int interleaved,
                 int inverse, hipStream_t stream);
 int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream);
-// gate_act = silu(gate) (saved), product = gate_act * up (nn.hpp:489-492 and backprop.py:492-499).
+// gate_act = silu(gate) (saved), product = gate_act * up (nn.hpp:489-492 and backprop.py:492-499); activation 1
+// takes gelu_tanh instead of silu.
 int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
-                          hipStream_t stream);
+                          hipStream_t stream, int activation = 0);
 int launch_silu_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
 // A device-to-device copy of `bytes` (16-byte vectors when both pointers allow).
 int launch_device_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);
@@ -113,10 +114,12 @@ int launch_gelu_tanh(const float* x, float* out, int64_t n, hipStream_t stream);
 int launch_geglu_tanh(const float* gate, const float* up, float* out, int64_t n, hipStream_t stream);
 int launch_gelu_tanh_backward(const float* x, const float* dy, float* out, int64_t n, hipStream_t stream);
 int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t n, double cap, hipStream_t stream);
+// softcap (nn.hpp:457-461): out = f32(cap tanh(x / cap)), in double
+int launch_softcap(const float* x, float* out, int64_t n, double cap, hipStream_t stream);
 // _swiglu_backward's elementwise glue (backprop.py:301-303): dgate = silu_backward(gate, dproduct * up),
 // dup = dproduct * gate_act.
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
-                           float* dgate, float* dup, int64_t n, hipStream_t stream);
+                           float* dgate, float* dup, int64_t n, hipStream_t stream, int activation = 0);
 int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream);
 // x = f32(x * f), or f32(x / f) with divide, in place
 int launch_scale(float* x, int64_t n, float f, bool divide, hipStream_t stream);

@@ -393,12 +393,33 @@ __global__ __launch_bounds__(256) void geglu_tanh_kernel(const float* __restrict
         out[i] = dgelu_tanh(gate[i]) * up[i];
 }
 
+// gelu_tanh_backward (grad.hpp:183-191): dy times 0.5 (1 + t) + 0.5 x (1 - t^2) sqrt(2/pi) (1 + 3 0.044715 x^2),
+// t = tanh(sqrt(2/pi) (x + 0.044715 x^3)), in double, rounded once.
+__device__ __forceinline__ float dgelu_tanh_backward(float x, float dy) {
+    const double c = 7.97884560802865355879e-01;  // sqrt(2 / pi)
+    const double d = x;
+    const double t = dtanh(c * (d + 0.044715 * d * d * d));
+    const double slope = 0.5 * (1.0 + t) + 0.5 * d * (1.0 - t * t) * c * (1.0 + 3.0 * 0.044715 * d * d);
+    return static_cast<float>(static_cast<double>(dy) * slope);
+}
+
+// The gated MLP's activation: kAct 0 SiLU, 1 GELU with the tanh approximation (backprop.py:163-171).
+template <int kAct>
+__device__ __forceinline__ float gate_activation(float x) {
+    return kAct == 1 ? dgelu_tanh(x) : dsilu(x);
+}
+template <int kAct>
+__device__ __forceinline__ float gate_activation_backward(float x, float dy) {
+    return kAct == 1 ? dgelu_tanh_backward(x, dy) : dsilu_backward(x, dy);
+}
+
+template <int kAct>
 __global__ __launch_bounds__(256) void swiglu_forward_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                              float* __restrict__ gate_act, float* __restrict__ product,
                                                              int64_t n) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * 256) {
-        const float a = dsilu(gate[i]);
+        const float a = gate_activation<kAct>(gate[i]);
         if (gate_act) gate_act[i] = a;
         product[i] = a * up[i];
     }
@@ -450,10 +471,8 @@ __global__ __launch_bounds__(256) void gelu_tanh_backward_kernel(const float* __
     const double c = 7.97884560802865355879e-01;  // sqrt(2 / pi)
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * 256) {
-        const double d = x[i];
-        const double t = dtanh(c * (d + 0.044715 * d * d * d));
-        const double slope = 0.5 * (1.0 + t) + 0.5 * d * (1.0 - t * t) * c * (1.0 + 3.0 * 0.044715 * d * d);
-        out[i] = static_cast<float>(static_cast<double>(dy[i]) * slope);
+        (void)c;
+        out[i] = dgelu_tanh_backward(x[i], dy[i]);
     }
 }
 
@@ -466,6 +485,7 @@ __global__ __launch_bounds__(256) void softcap_backward_kernel(const float* __re
     }
 }
 
+template <int kAct>
 __global__ __launch_bounds__(256) void swiglu_backward_kernel(const float* __restrict__ gate,
                                                               const float* __restrict__ up,
                                                               const float* __restrict__ gate_act,
@@ -475,7 +495,7 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const float* __res
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * 256) {
         const float dp = dproduct[i];
-        dgate[i] = dsilu_backward(gate[i], dp * up[i]);
+        dgate[i] = gate_activation_backward<kAct>(gate[i], dp * up[i]);
         dup[i] = dp * gate_act[i];
     }
 }
@@ -599,15 +619,20 @@ int launch_silu(const float* x, float* out, int64_t n, hipStream_t stream) {
 }
 
 int launch_swiglu_forward(const float* gate, const float* up, float* gate_act, float* product, int64_t n,
-                          hipStream_t stream) {
+                          hipStream_t stream, int activation) {
     if (n == 0) return kOk;
+    if (activation == 1) {
+        hipLaunchKernelGGL(swiglu_forward_kernel<1>, dim3(elementwise_grid(n)), dim3(256), 0, stream, gate, up,
+                           gate_act, product, n);
+        return check_launch("geglu");
+    }
     const int64_t n4 = aligned16({gate, up, gate_act, product}) ? n / 4 : 0;
     if (n4 > 0)
         hipLaunchKernelGGL(swiglu_forward4_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, stream, gate, up,
                            gate_act, product, n4);
     const int64_t d = 4 * n4;
     if (n > d)
-        hipLaunchKernelGGL(swiglu_forward_kernel, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
+        hipLaunchKernelGGL(swiglu_forward_kernel<0>, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
                            up + d, gate_act ? gate_act + d : nullptr, product + d, n - d);
     return check_launch("swiglu");
 }
@@ -666,6 +691,19 @@ int launch_gelu_tanh_backward(const float* x, const float* dy, float* out, int64
     return check_launch("gelu_tanh_backward");
 }
 
+__global__ __launch_bounds__(256) void softcap_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t n,
+                                                      double cap) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        out[i] = static_cast<float>(cap * dtanh(static_cast<double>(x[i]) / cap));
+}
+
+int launch_softcap(const float* x, float* out, int64_t n, double cap, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(softcap_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, out, n, cap);
+    return check_launch("softcap");
+}
+
 int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t n, double cap, hipStream_t stream) {
     if (n == 0) return kOk;
     hipLaunchKernelGGL(softcap_backward_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, dy, out, n, cap);
@@ -673,15 +711,20 @@ int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t
 }
 
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
-                           float* dgate, float* dup, int64_t n, hipStream_t stream) {
+                           float* dgate, float* dup, int64_t n, hipStream_t stream, int activation) {
     if (n == 0) return kOk;
+    if (activation == 1) {
+        hipLaunchKernelGGL(swiglu_backward_kernel<1>, dim3(elementwise_grid(n)), dim3(256), 0, stream, gate, up,
+                           gate_act, dproduct, dgate, dup, n);
+        return check_launch("geglu_backward");
+    }
     const int64_t n4 = aligned16({gate, up, gate_act, dproduct, dgate, dup}) ? n / 4 : 0;
     if (n4 > 0)
         hipLaunchKernelGGL(swiglu_backward4_kernel, dim3(elementwise_grid(n4)), dim3(256), 0, stream, gate, up,
                            gate_act, dproduct, dgate, dup, n4);
     const int64_t d = 4 * n4;
     if (n > d)
-        hipLaunchKernelGGL(swiglu_backward_kernel, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
+        hipLaunchKernelGGL(swiglu_backward_kernel<0>, dim3(elementwise_grid(n - d)), dim3(256), 0, stream, gate + d,
                            up + d, gate_act + d, dproduct + d, dgate + d, dup + d, n - d);
     return check_launch("swiglu_backward");
 }

@@ -191,6 +191,7 @@ struct dllm_hip_trainer {
     std::vector<Saved> saved;
     std::vector<std::unique_ptr<DevBuf>> owned;
     float *x_final = nullptr, *hidden = nullptr, *logits = nullptr, *dlogits = nullptr;
+    float* logits_capped = nullptr;  // Gemma 2's soft-capped logits (the uncapped ones stay in `logits`)
     float *dx = nullptr, *dh = nullptr, *dx_mid = nullptr, *dattended = nullptr, *dq_t = nullptr, *dk_t = nullptr,
           *dv_t = nullptr, *dq = nullptr, *dk = nullptr, *dq2 = nullptr, *dk2 = nullptr, *dproduct = nullptr,
           *dgate = nullptr, *dup = nullptr, *col_part = nullptr, *col_part_side = nullptr, *emb_rows = nullptr,
@@ -209,6 +210,8 @@ struct dllm_hip_trainer {
     float *post_tmp = nullptr, *dpost = nullptr;  // post norms: a normalised block output; a norm's input gradient  // the layer norms' inverse rms, read by their weights' gradients
     double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
            *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+    // Gemma 3's windowed layers rotate with a base of their own and no scaling (backprop.py:63-67)
+    double *inv_local = nullptr, *cos_local = nullptr, *sin_local = nullptr;
     void* attn_ws = nullptr;
     int64_t *tok_in = nullptr, *tok_tgt = nullptr, *pos_index = nullptr, *seg_d = nullptr, *batch_d = nullptr,
             *grp_order = nullptr, *grp_start = nullptr, *grp_out = nullptr;
@@ -300,6 +303,17 @@ struct dllm_hip_trainer {
     bool sparse(int64_t l) const { return E > 0 && !(l < 64 && ((c.dense_layers >> l) & 1)); }
     // Norm placement (architecture.py:315-320): pre (each block's input), post (its output; OLMo 2) or both.
     bool pre_norms() const { return c.norm_placement != 1; }
+    int uo() const { return c.norm_unit_offset ? 1 : 0; }  // norms with 1 + w (Gemma)
+    int act() const { return static_cast<int>(c.activation); }
+    // TransformerConfig.window (architecture.py:353-359): the sliding window of layer l, 0 for full attention
+    int64_t layer_window(int64_t l) const {
+        if (c.sliding_window == 0) return 0;
+        return l < 64 && ((c.full_attention_layers >> l) & 1) ? 0 : c.sliding_window;
+    }
+    // The RoPE tables of layer l (uses_local_rope, architecture.py:322-324)
+    bool local_rope(int64_t l) const { return c.local_rope_theta != 0.0 && layer_window(l) != 0; }
+    const double* cos_of(int64_t l) const { return local_rope(l) ? cos_local : cos_t; }
+    const double* sin_of(int64_t l) const { return local_rope(l) ? sin_local : sin_t; }
     bool post_norms() const { return c.norm_placement != 0; }
     int64_t sparse_layers() const {
         int64_t n = 0;
@@ -597,6 +611,16 @@ struct dllm_hip_trainer {
         hipLaunchKernelGGL(inv_freq_kernel, dim3(1), dim3(1024), 0, nullptr, c.rotary_dim, c.rope_theta, inv_freq);
         DLLM_TRY(check_launch("inv_freq"));
         DLLM_TRY(launch_rope_tables(nullptr, T_max, inv_freq, c.rotary_dim / 2, cos_t, sin_t, nullptr));
+        if (c.local_rope_theta != 0.0) {
+            DLLM_TRY(make(&inv_local, std::max<int64_t>(c.rotary_dim / 2, 1)));
+            DLLM_TRY(make(&cos_local, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
+            DLLM_TRY(make(&sin_local, T_max * std::max<int64_t>(c.rotary_dim / 2, 1)));
+            hipLaunchKernelGGL(inv_freq_kernel, dim3(1), dim3(1024), 0, nullptr, c.rotary_dim, c.local_rope_theta,
+                               inv_local);
+            DLLM_TRY(check_launch("inv_freq"));
+            DLLM_TRY(launch_rope_tables(nullptr, T_max, inv_local, c.rotary_dim / 2, cos_local, sin_local, nullptr));
+        }
+        if (c.logits_softcap != 0.0) DLLM_TRY(make(&logits_capped, R * V));
         return check_hip(hipDeviceSynchronize(), "trainer setup");
     }
 
@@ -1052,7 +1076,7 @@ struct dllm_hip_trainer {
         g.max_len = n;
         g.head_dim = hd;
         g.group = G;
-        g.window = c.sliding_window;
+        g.window = layer_window(l);
         // S^T[j][t] = sum_i k[j][i] q[t][i], times scale: A = the key rows themselves, read transposed
         g.A = AttnOperand{sv.k, 0, KVD, hd, G, KVD, 0, 1};
         g.a_float = true;
@@ -1072,7 +1096,7 @@ struct dllm_hip_trainer {
         g.tile_max_zstride = (Tp / 64) * Tp;
         g.tile_max_ld = Tp;
         DLLM_TRY(launch_attn_tiles(g, s));
-        DLLM_TRY(launch_softmax_rows(et, Tp, Tp * Tp, seg_d, nwin, nh, n, c.sliding_window, inv_of(l), Tp, s,
+        DLLM_TRY(launch_softmax_rows(et, Tp, Tp * Tp, seg_d, nwin, nh, n, layer_window(l), inv_of(l), Tp, s,
                                      attn_tmax, (Tp / 64) * Tp, Tp));
         // out[t] = f32((sum_j e_j v_j) inv_t)
         AttnTileCall o = g;
@@ -1111,7 +1135,7 @@ struct dllm_hip_trainer {
         g.max_len = n;
         g.head_dim = hd;
         g.group = G;
-        g.window = c.sliding_window;
+        g.window = layer_window(l);
         // dP^T[j][t] = sum_i v[j][i] dout[t][i]
         g.A = AttnOperand{sv.v, 0, KVD, hd, G, KVD, 0, 1};
         g.a_float = true;
@@ -1131,7 +1155,7 @@ struct dllm_hip_trainer {
         // D, p = e inv and ds = p (dp - D) scale: ds over dP^T (dq's operand), p and ds in the key-row layout
         // [w][g][(t, hh)][j] of dk and dv
         const int64_t gz = Tp * G * Tp;
-        DLLM_TRY(launch_dsoftmax_regroup(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, G, n, c.sliding_window, inv_of(l),
+        DLLM_TRY(launch_dsoftmax_regroup(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, G, n, layer_window(l), inv_of(l),
                                          Tp, c.attention_scale, attn_dvec, attn_pg, attn_dsg, Tp, gz, s));
         // dq[t] = sum_j ds[t][j] k[j]
         AttnTileCall q = g;
@@ -1177,32 +1201,32 @@ struct dllm_hip_trainer {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
         Saved& sv = saved[static_cast<size_t>(l)];
         const double eps = c.rms_norm_eps;
-        if (pre_norms()) DLLM_TRY(launch_rms_norm(sv.x_in, P(L.attn_norm), sv.h1, R, H, eps, 0, nullptr, s));
+        if (pre_norms()) DLLM_TRY(launch_rms_norm(sv.x_in, P(L.attn_norm), sv.h1, R, H, eps, uo(), nullptr, s));
         DLLM_TRY(qkv_forward(l, R, s));
         const float* qsrc = sv.q_raw;
         const float* ksrc = sv.k_raw;
         if (c.qk_norm == 2) {
-            DLLM_TRY(launch_rms_norm(sv.q_raw, P(L.qn), sv.qn, R, QD, eps, 0, nullptr, s));
-            DLLM_TRY(launch_rms_norm(sv.k_raw, P(L.kn), sv.kn, R, KVD, eps, 0, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.q_raw, P(L.qn), sv.qn, R, QD, eps, uo(), nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.k_raw, P(L.kn), sv.kn, R, KVD, eps, uo(), nullptr, s));
             qsrc = sv.qn;
             ksrc = sv.kn;
         } else if (c.qk_norm == 1) {
-            DLLM_TRY(launch_rms_norm(sv.q_raw, P(L.qn), sv.qn, R * c.heads, c.head_dim, eps, 0, nullptr, s));
-            DLLM_TRY(launch_rms_norm(sv.k_raw, P(L.kn), sv.kn, R * c.kv_heads, c.head_dim, eps, 0, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.q_raw, P(L.qn), sv.qn, R * c.heads, c.head_dim, eps, uo(), nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.k_raw, P(L.kn), sv.kn, R * c.kv_heads, c.head_dim, eps, uo(), nullptr, s));
             qsrc = sv.qn;
             ksrc = sv.kn;
         }
-        DLLM_TRY(launch_rope_pair(qsrc, sv.q, c.heads, ksrc, sv.k, c.kv_heads, pos_index, cos_t, sin_t, R, c.head_dim,
+        DLLM_TRY(launch_rope_pair(qsrc, sv.q, c.heads, ksrc, sv.k, c.kv_heads, pos_index, cos_of(l), sin_of(l), R, c.head_dim,
                                   c.rotary_dim, 0, s));
         DLLM_TRY(attention_forward(l, sv, b, s));
         if (post_norms()) {  // x_mid = x + post_norm(out)
             DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.out, nullptr, s));
-            DLLM_TRY(launch_rms_norm(sv.out, P(L.attn_post), post_tmp, R, H, eps, 0, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.out, P(L.attn_post), post_tmp, R, H, eps, uo(), nullptr, s));
             DLLM_TRY(launch_add(sv.x_in, post_tmp, sv.x_mid, R * H, s));
         } else {
             DLLM_TRY(linear_fwd(sv.attended, R, QD, L.o, nullptr, sv.x_mid, sv.x_in, s));  // x_mid = x + out
         }
-        if (pre_norms()) DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, 0, nullptr, s));
+        if (pre_norms()) DLLM_TRY(launch_rms_norm(sv.x_mid, P(L.mlp_norm), sv.h2, R, H, eps, uo(), nullptr, s));
         if (sparse(l)) return moe_forward(l, R, x_out, s);
         if (grp_on[kGrpMlpFwd] && grp_rows == R) {
             DLLM_TRY(group_launch(l, kGrpMlpFwd, s));
@@ -1210,10 +1234,10 @@ struct dllm_hip_trainer {
             DLLM_TRY(linear_fwd(sv.h2, R, H, L.gate, nullptr, sv.gate, nullptr, s));
             DLLM_TRY(linear_fwd(sv.h2, R, H, L.up, nullptr, sv.up, nullptr, s));
         }
-        DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * I, s));
+        DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * I, s, act()));
         if (post_norms()) {  // x_out = x_mid + post_norm(mlp)
             DLLM_TRY(linear_fwd(sv.product, R, I, L.down, nullptr, sv.mlp, nullptr, s));
-            DLLM_TRY(launch_rms_norm(sv.mlp, P(L.mlp_post), post_tmp, R, H, eps, 0, nullptr, s));
+            DLLM_TRY(launch_rms_norm(sv.mlp, P(L.mlp_post), post_tmp, R, H, eps, uo(), nullptr, s));
             return launch_add(sv.x_mid, post_tmp, x_out, R * H, s);
         }
         return linear_fwd(sv.product, R, I, L.down, nullptr, x_out, sv.x_mid, s);  // x_out = x_mid + mlp
@@ -1229,7 +1253,7 @@ struct dllm_hip_trainer {
         // post norms (backprop.py:224-229): the MLP's output gradient through its norm (one stream: side is off)
         const float* dmlp = dx;
         if (post_norms()) {
-            DLLM_TRY(launch_rms_norm_backward_dx(sv.mlp, P(L.mlp_post), dx, dpost, nullptr, R, H, eps, 0, inv_post, s));
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.mlp, P(L.mlp_post), dx, dpost, nullptr, R, H, eps, uo(), inv_post, s));
             DLLM_TRY(norm_dw(dx, sv.mlp, inv_post, H, 1, nseg, G(L.mlp_post), s));
             dmlp = dpost;
         }
@@ -1245,7 +1269,7 @@ struct dllm_hip_trainer {
                                unfold_scale(L.down)));
             DLLM_TRY(side_mark(kSideDown));
             DLLM_TRY(side_wait(kSideMlp, s));  // the previous layer's gate and up dW read dgate, dup
-            DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s));
+            DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, R * I, s, act()));
             DLLM_TRY(side_fork_from(s, &ws));
             DLLM_TRY(linear_dw(dgate, I, sv.h2, H, nseg, G(L.gate), nullptr, nullptr, ws));
             DLLM_TRY(linear_dw(dup, I, sv.h2, H, nseg, G(L.up), nullptr, nullptr, ws));
@@ -1262,7 +1286,7 @@ struct dllm_hip_trainer {
         // mlp norm; dx_mid = dx + dh2'
         DLLM_TRY(side_wait(kSideO, s));  // the previous layer's o dW reads dx_mid
         if (pre_norms()) {
-            DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, 0, inv_mlp, s));
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.x_mid, P(L.mlp_norm), dh, dx_mid, dx, R, H, eps, uo(), inv_mlp, s));
             DLLM_TRY(side_fork_from(s, &ws));
             DLLM_TRY(norm_dw(dh, sv.x_mid, inv_mlp, H, 1, nseg, G(L.mlp_norm), ws));
             DLLM_TRY(side_mark(kSideNormMlp));
@@ -1272,7 +1296,7 @@ struct dllm_hip_trainer {
         // attention output projection (through its post norm, backprop.py:237-242)
         const float* dout = dx_mid;
         if (post_norms()) {
-            DLLM_TRY(launch_rms_norm_backward_dx(sv.out, P(L.attn_post), dx_mid, dpost, nullptr, R, H, eps, 0, inv_post,
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.out, P(L.attn_post), dx_mid, dpost, nullptr, R, H, eps, uo(), inv_post,
                                                  s));
             DLLM_TRY(norm_dw(dx_mid, sv.out, inv_post, H, 1, nseg, G(L.attn_post), s));
             dout = dpost;
@@ -1284,23 +1308,23 @@ struct dllm_hip_trainer {
         DLLM_TRY(side_mark(kSideO));
         DLLM_TRY(side_wait(kSideQkv, s));  // the previous layer's q/k/v dW read dq, dk (dq2, dk2) and dv_t
         DLLM_TRY(attention_backward(l, sv, b, s));
-        DLLM_TRY(launch_rope_pair(dq_t, dq, c.heads, dk_t, dk, c.kv_heads, pos_index, cos_t, sin_t, R, c.head_dim,
+        DLLM_TRY(launch_rope_pair(dq_t, dq, c.heads, dk_t, dk, c.kv_heads, pos_index, cos_of(l), sin_of(l), R, c.head_dim,
                                   c.rotary_dim, 1, s));
         const float* dqf = dq;
         const float* dkf = dk;
         if (c.qk_norm == 1) {
-            DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R * c.heads, c.head_dim, eps, 0,
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R * c.heads, c.head_dim, eps, uo(),
                                                  inv_rms, s));
             DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, c.head_dim, c.heads, nseg, G(L.qn), s, unfold_scale(L.qn)));
             DLLM_TRY(launch_rms_norm_backward_dx(sv.k_raw, P(L.kn), dk, dk2, nullptr, R * c.kv_heads, c.head_dim, eps,
-                                                 0, inv_rms, s));
+                                                 uo(), inv_rms, s));
             DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, c.head_dim, c.kv_heads, nseg, G(L.kn), s, unfold_scale(L.kn)));
             dqf = dq2;
             dkf = dk2;
         } else if (c.qk_norm == 2) {
-            DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R, QD, eps, 0, inv_rms, s));
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.q_raw, P(L.qn), dq, dq2, nullptr, R, QD, eps, uo(), inv_rms, s));
             DLLM_TRY(norm_dw(dq, sv.q_raw, inv_rms, QD, 1, nseg, G(L.qn), s, unfold_scale(L.qn)));
-            DLLM_TRY(launch_rms_norm_backward_dx(sv.k_raw, P(L.kn), dk, dk2, nullptr, R, KVD, eps, 0, inv_rms, s));
+            DLLM_TRY(launch_rms_norm_backward_dx(sv.k_raw, P(L.kn), dk, dk2, nullptr, R, KVD, eps, uo(), inv_rms, s));
             DLLM_TRY(norm_dw(dk, sv.k_raw, inv_rms, KVD, 1, nseg, G(L.kn), s, unfold_scale(L.kn)));
             dqf = dq2;
             dkf = dk2;
@@ -1330,7 +1354,7 @@ struct dllm_hip_trainer {
         // attention norm; dx = dx_mid + dh1'
         DLLM_TRY(side_wait(kSideDown, s));  // this layer's down dW reads dx
         if (!pre_norms()) return launch_add(dx_mid, dh1, dx, R * H, s);
-        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh1, dx, dx_mid, R, H, eps, 0, inv_attn, s));
+        DLLM_TRY(launch_rms_norm_backward_dx(sv.x_in, P(L.attn_norm), dh1, dx, dx_mid, R, H, eps, uo(), inv_attn, s));
         DLLM_TRY(side_fork_from(s, &ws));
         DLLM_TRY(norm_dw(dh1, sv.x_in, inv_attn, H, 1, nseg, G(L.attn_norm), ws));
         return side_mark(kSideNormAttn);
@@ -1466,7 +1490,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_gather_rows(sv.h2, sv.row_of, xg, R * K, H, s));
         DLLM_TRY(expert_matmul(sv, kFwdGate, s));
         DLLM_TRY(expert_matmul(sv, kFwdUp, s));
-        DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * K * EI, s));
+        DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * K * EI, s, act()));
         DLLM_TRY(expert_matmul(sv, kFwdDown, s));
         return launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sv.x_mid, x_out, R, K, H, s);
     }
@@ -1480,7 +1504,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_gather_rows(sv.h2, sv.row_of, xg, P, H, s));
         DLLM_TRY(expert_matmul(sv, kDxDown, s));
         DLLM_TRY(expert_matmul(sv, kDwDown, s));
-        DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, P * EI, s));
+        DLLM_TRY(launch_swiglu_backward(sv.gate, sv.up, sv.gate_act, dproduct, dgate, dup, P * EI, s, act()));
         DLLM_TRY(expert_matmul(sv, kDxGate, s));
         DLLM_TRY(expert_matmul(sv, kDwGate, s));
         DLLM_TRY(expert_matmul(sv, kDxUp, s));  // dx_gate + dx_up
@@ -1609,20 +1633,23 @@ struct dllm_hip_trainer {
             DLLM_TRY(launch_router_stats(probs_all, R_max * E, sparse_layers(), seg_d, nseg, counts_d, E, router_scale,
                                          router_loss_w, router_scale != 0.0 ? grad_row : nullptr, s));
         }
-        DLLM_TRY(launch_rms_norm(x_final, P(final_norm), hidden, R, H, eps, 0, nullptr, s));
+        DLLM_TRY(launch_rms_norm(x_final, P(final_norm), hidden, R, H, eps, uo(), nullptr, s));
         const int head = c.tie_embeddings ? emb : lm_head;
         DLLM_TRY(linear_fwd(hidden, R, H, head, nullptr, logits, nullptr, s));
         // loss and the head (backprop.py:174-206): Granite's logits scaling divides the logits and their gradient
         const bool logit_div = c.logits_scaling != 1.0;
         if (logit_div) DLLM_TRY(launch_scale(logits, R * V, static_cast<float>(c.logits_scaling), true, s));
         DLLM_TRY(check_hip(hipMemsetAsync(err_flag, 0, sizeof(int), s), "memset"));
-        DLLM_TRY(launch_cross_entropy(logits, tok_tgt, dlogits, R, V, scale, seg_d, nseg, row_max, row_total, row_loss,
-                                      loss_w, err_flag, s));
+        if (c.logits_softcap != 0.0) DLLM_TRY(launch_softcap(logits, logits_capped, R * V, c.logits_softcap, s));
+        DLLM_TRY(launch_cross_entropy(c.logits_softcap != 0.0 ? logits_capped : logits, tok_tgt, dlogits, R, V, scale,
+                                      seg_d, nseg, row_max, row_total, row_loss, loss_w, err_flag, s));
+        if (c.logits_softcap != 0.0)
+            DLLM_TRY(launch_softcap_backward(logits, dlogits, dlogits, R * V, c.logits_softcap, s));
         if (logit_div) DLLM_TRY(launch_scale(dlogits, R * V, static_cast<float>(c.logits_scaling), true, s));
         if (dpo.on) DLLM_TRY(dpo_weights(windows, s));
         float* dhidden = dh;
         DLLM_TRY(linear_dx(dlogits, R, head, dhidden, nullptr, s));
-        DLLM_TRY(launch_rms_norm_backward_dx(x_final, P(final_norm), dhidden, dx, nullptr, R, H, eps, 0, inv_rms, s));
+        DLLM_TRY(launch_rms_norm_backward_dx(x_final, P(final_norm), dhidden, dx, nullptr, R, H, eps, uo(), inv_rms, s));
         DLLM_TRY(norm_dw(dhidden, x_final, inv_rms, H, 1, nseg, G(final_norm), s));
         for (bool& pending : side_pending) pending = false;
         side_on = false;
@@ -2025,6 +2052,10 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     DLLM_REQUIRE(c.attention_scale > 0.0 && std::isfinite(c.attention_scale), "attention_scale must be positive");
     DLLM_REQUIRE(c.norm_placement >= 0 && c.norm_placement <= 2, "norm_placement must be 0 (pre), 1 (post) or 2 (both)");
     DLLM_REQUIRE(c.norm_placement == 0 || c.experts == 0, "post norms are built for dense MLPs only");
+    DLLM_REQUIRE(c.activation == 0 || c.activation == 1, "activation must be 0 (silu) or 1 (gelu_tanh)");
+    DLLM_REQUIRE(c.local_rope_theta >= 0.0 && c.attention_softcap >= 0.0 && c.logits_softcap >= 0.0,
+                 "local_rope_theta and the soft-caps must be non-negative (0: none)");
+    DLLM_REQUIRE(c.attention_softcap == 0.0, "soft-capped attention scores are not built in the trainer");
     if (c.experts > 0) {
         bool any_sparse = false;
         for (int64_t l = 0; l < c.layers; ++l) any_sparse = any_sparse || l >= 64 || !((c.dense_layers >> l) & 1);

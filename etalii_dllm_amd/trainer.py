@@ -27,7 +27,9 @@ class DecoderConfig(C.Structure):
         "expert_intermediate", "rotary_dim")] + [
         ("rms_norm_eps", C.c_double), ("rope_theta", C.c_double), ("attention_scale", C.c_double),
         ("embedding_multiplier", C.c_double), ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double),
-        ("dense_layers", C.c_int64), ("norm_placement", C.c_int64)]
+        ("dense_layers", C.c_int64), ("norm_placement", C.c_int64), ("norm_unit_offset", C.c_int64),
+        ("activation", C.c_int64), ("full_attention_layers", C.c_int64), ("local_rope_theta", C.c_double),
+        ("attention_softcap", C.c_double), ("logits_softcap", C.c_double)]
 
 
 class AdamWArgs(C.Structure):
@@ -111,6 +113,14 @@ class Decoder:
     logits_scaling: float = 1.0
     dense_layers: tuple[int, ...] = ()  # layers keeping a dense MLP in a model with experts (Qwen3-MoE)
     norm_placement: int = 0  # 0 pre, 1 post (OLMo 2), 2 both (architecture.py:315-320)
+    # Gemma: norms as 1 + w, GELU-tanh MLPs, the window on the layers in window_layers only (None: every layer), a RoPE
+    # base of their own for those, soft-capped logits (soft-capped attention scores are not built)
+    norm_unit_offset: bool = False
+    activation: int = 0  # 0 SiLU, 1 GELU (tanh approximation)
+    window_layers: tuple[int, ...] | None = None
+    local_rope_theta: float | None = None
+    attention_softcap: float | None = None
+    logits_softcap: float | None = None
 
     def native(self) -> DecoderConfig:
         return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
@@ -121,7 +131,10 @@ class Decoder:
                              1.0 / float(np.sqrt(np.float64(self.head_dim))) if self.attention_multiplier is None
                              else self.attention_multiplier, self.embedding_multiplier, self.residual_multiplier,
                              self.logits_scaling, sum(1 << layer for layer in self.dense_layers if layer < 64),
-                             self.norm_placement)
+                             self.norm_placement, int(self.norm_unit_offset), self.activation,
+                             0 if self.window_layers is None else
+                             sum(1 << i for i in range(min(self.layers, 64)) if i not in self.window_layers),
+                             self.local_rope_theta or 0.0, self.attention_softcap or 0.0, self.logits_softcap or 0.0)
 
 
 def _windows(windows):
