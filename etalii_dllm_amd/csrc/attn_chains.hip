@@ -173,11 +173,12 @@ __global__ __launch_bounds__(64) void dsoftmax_dot_kernel(const double* __restri
 // (key j, query t) of head h = g G + hh, p = e inv_t and ds = (p (dp - D_t)) scale; ds is written over dP^T[j][t]
 // (dq's operand) and p, ds to pg / dsg[w][g][(t G + hh)][j]. A 64 x 64 tile goes through LDS so both the reads
 // (along t) and the regrouped writes (along j) are coalesced.
+template <bool kSlope>
 __global__ __launch_bounds__(256) void dsoftmax_apply_regroup_kernel(
     const double* __restrict__ et, double* __restrict__ dpt, int64_t ld, int64_t zstride,
     const int64_t* __restrict__ seg, int64_t heads, int64_t group, int64_t window, const double* __restrict__ inv,
     int64_t inv_zstride, const double* __restrict__ dvec, double scale, double* __restrict__ pg,
-    double* __restrict__ dsg, int64_t dst_ld, int64_t dst_zstride) {
+    double* __restrict__ dsg, int64_t dst_ld, int64_t dst_zstride, const double* __restrict__ slope) {
     constexpr int kJ = 32;  // keys per tile (64 queries)
     __shared__ double tp[kJ][65];
     __shared__ double td[kJ][65];
@@ -199,20 +200,23 @@ __global__ __launch_bounds__(256) void dsoftmax_apply_regroup_kernel(
         const double D = t < n ? dvec[z * inv_zstride + t] : 0.0;
         const double* e = et + z * zstride + t;
         double* d = dpt + z * zstride + t;
-        double ev[kJ / 4], dv[kJ / 4];
+        const double* sl = kSlope ? slope + z * zstride + t : nullptr;
+        double ev[kJ / 4], dv[kJ / 4], sv[kJ / 4];
 #pragma unroll
         for (int k = 0; k < kJ / 4; ++k) {  // every load issued before the first use
             const int64_t j = j0 + ty + 4 * k;
             const bool vis = j >= lo && j < hi;
             ev[k] = vis ? e[j * ld] : 0.0;
             dv[k] = vis ? d[j * ld] : 0.0;
+            if (kSlope) sv[k] = vis ? sl[j * ld] : 1.0;
         }
 #pragma unroll
         for (int k = 0; k < kJ / 4; ++k) {
             const int64_t j = j0 + ty + 4 * k;
             if (j >= lo && j < hi) {
                 const double p = ev[k] * iv;
-                const double ds = p * (dv[k] - D) * scale;
+                // ((p (dp - D)) slope) scale, the slope of a soft-capped score (1 without a cap: the product is exact)
+                const double ds = kSlope ? p * (dv[k] - D) * sv[k] * scale : p * (dv[k] - D) * scale;
                 d[j * ld] = ds;
                 tp[ty + 4 * k][tx] = p;
                 td[ty + 4 * k][tx] = ds;
@@ -365,18 +369,41 @@ int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* 
     return check_launch("attention softmax");
 }
 
+__global__ __launch_bounds__(256) void softcap_scores_kernel(double* __restrict__ st, double* __restrict__ slope,
+                                                             int64_t count, double cap) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < count;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const double t = dtanh(st[i] / cap);
+        st[i] = cap * t;
+        slope[i] = 1.0 - t * t;
+    }
+}
+
+int launch_softcap_scores(double* st, double* slope, int64_t count, double cap, hipStream_t stream) {
+    if (count == 0) return kOk;
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(count, 256), 16384));
+    hipLaunchKernelGGL(softcap_scores_kernel, dim3(blocks), dim3(256), 0, stream, st, slope, count, cap);
+    return check_launch("softcap scores");
+}
+
 int launch_dsoftmax_regroup(const double* et, double* dpt, int64_t ld, int64_t zstride, const int64_t* seg,
                             int64_t windows, int64_t heads, int64_t group, int64_t max_len, int64_t window,
                             const double* inv, int64_t inv_zstride, double scale, double* dvec, double* pg,
-                            double* dsg, int64_t dst_ld, int64_t dst_zstride, hipStream_t stream) {
+                            double* dsg, int64_t dst_ld, int64_t dst_zstride, hipStream_t stream,
+                            const double* slope) {
     if (max_len == 0 || windows * heads == 0) return kOk;
     const dim3 lanes(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(windows * heads));
     hipLaunchKernelGGL(dsoftmax_dot_kernel, lanes, dim3(64), 0, stream, et, dpt, ld, zstride, seg, heads, window, inv,
                        inv_zstride, dvec);
     const dim3 tiles(static_cast<unsigned>(ceil_div(max_len, 64)), static_cast<unsigned>(ceil_div(max_len, 32)),
                      static_cast<unsigned>(windows * heads));
-    hipLaunchKernelGGL(dsoftmax_apply_regroup_kernel, tiles, dim3(256), 0, stream, et, dpt, ld, zstride, seg, heads,
-                       group, window, inv, inv_zstride, dvec, scale, pg, dsg, dst_ld, dst_zstride);
+    if (slope)
+        hipLaunchKernelGGL(dsoftmax_apply_regroup_kernel<true>, tiles, dim3(256), 0, stream, et, dpt, ld, zstride, seg,
+                           heads, group, window, inv, inv_zstride, dvec, scale, pg, dsg, dst_ld, dst_zstride, slope);
+    else
+        hipLaunchKernelGGL(dsoftmax_apply_regroup_kernel<false>, tiles, dim3(256), 0, stream, et, dpt, ld, zstride,
+                           seg, heads, group, window, inv, inv_zstride, dvec, scale, pg, dsg, dst_ld, dst_zstride,
+                           nullptr);
     return check_launch("attention softmax backward");
 }
 

@@ -65,7 +65,11 @@ int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* 
 int launch_dsoftmax_regroup(const double* et, double* dpt, int64_t ld, int64_t zstride, const int64_t* seg,
                             int64_t windows, int64_t heads, int64_t group, int64_t max_len, int64_t window,
                             const double* inv, int64_t inv_zstride, double scale, double* dvec, double* pg,
-                            double* dsg, int64_t dst_ld, int64_t dst_zstride, hipStream_t stream);
+                            double* dsg, int64_t dst_ld, int64_t dst_zstride, hipStream_t stream,
+                            const double* slope = nullptr);
+// Soft-capped scores (Gemma 2; grad.hpp:247-251 and nn.hpp:539-541): every one of `count` scaled scores s becomes
+// cap t with t = tanh(s / cap), and slope gets 1 - t t (the backward's factor), in double.
+int launch_softcap_scores(double* st, double* slope, int64_t count, double cap, hipStream_t stream);
 int launch_heads_transpose(const float* src, int64_t row_stride, int64_t head_dim, void* dst, bool to_double,
                            int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,
                            int64_t max_len, hipStream_t stream);

@@ -274,6 +274,7 @@ struct dllm_hip_trainer {
     // matrices
     int64_t Tp = 0;
     double* attn_dvec = nullptr;  // the softmax backward's per-query D
+    double* attn_slope = nullptr;
     double *attn_et = nullptr, *attn_inv = nullptr, *attn_dpt = nullptr, *attn_pg = nullptr, *attn_dsg = nullptr;
     double* attn_tmax = nullptr;  // the scores' per-64-key-tile maxima of each query [z][Tp / 64][Tp]
     float *attn_qt = nullptr, *attn_dot = nullptr;
@@ -588,6 +589,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(make(&attn_qt, W_max * heads * hd * Tp));
         DLLM_TRY(make(&attn_dot, W_max * heads * hd * Tp));
         DLLM_TRY(make(&attn_et, c.layers * W_max * heads * Tp * Tp));  // E^T saved per layer for the backward
+        // soft-capped scores: the backward's factor 1 - tanh^2 of every score, saved per layer
+        if (c.attention_softcap != 0.0) DLLM_TRY(make(&attn_slope, c.layers * W_max * heads * Tp * Tp));
         DLLM_TRY(make(&attn_inv, c.layers * W_max * heads * Tp));
         DLLM_TRY(make(&attn_dpt, W_max * heads * Tp * Tp));
         DLLM_TRY(make(&attn_pg, W_max * kvh * Tp * G * Tp));
@@ -1062,6 +1065,7 @@ struct dllm_hip_trainer {
 
     double* et_of(int64_t l) const { return attn_et + l * W_max * c.heads * Tp * Tp; }
     double* inv_of(int64_t l) const { return attn_inv + l * W_max * c.heads * Tp; }
+    double* slope_of(int64_t l) const { return attn_slope + l * W_max * c.heads * Tp * Tp; }
 
     // attention() of every (window, head) of the step (nn.hpp:761-796): S^T = K Q^T scale, the softmax chains per
     // query, out = (E V) inv.
@@ -1092,12 +1096,14 @@ struct dllm_hip_trainer {
         g.exact_products = true;
         g.out_double = true;
         g.out_scale = c.attention_scale;
-        g.tile_max = attn_tmax;
+        const bool capped = c.attention_softcap != 0.0;  // the tiles' maxima are of the uncapped scores
+        g.tile_max = capped ? nullptr : attn_tmax;
         g.tile_max_zstride = (Tp / 64) * Tp;
         g.tile_max_ld = Tp;
         DLLM_TRY(launch_attn_tiles(g, s));
+        if (capped) DLLM_TRY(launch_softcap_scores(et, slope_of(l), nwin * nh * Tp * Tp, c.attention_softcap, s));
         DLLM_TRY(launch_softmax_rows(et, Tp, Tp * Tp, seg_d, nwin, nh, n, layer_window(l), inv_of(l), Tp, s,
-                                     attn_tmax, (Tp / 64) * Tp, Tp));
+                                     g.tile_max, (Tp / 64) * Tp, Tp));
         // out[t] = f32((sum_j e_j v_j) inv_t)
         AttnTileCall o = g;
         o.tile_max = nullptr;
@@ -1156,7 +1162,8 @@ struct dllm_hip_trainer {
         // [w][g][(t, hh)][j] of dk and dv
         const int64_t gz = Tp * G * Tp;
         DLLM_TRY(launch_dsoftmax_regroup(et, attn_dpt, Tp, Tp * Tp, seg_d, nwin, nh, G, n, layer_window(l), inv_of(l),
-                                         Tp, c.attention_scale, attn_dvec, attn_pg, attn_dsg, Tp, gz, s));
+                                         Tp, c.attention_scale, attn_dvec, attn_pg, attn_dsg, Tp, gz, s,
+                                         c.attention_softcap != 0.0 ? slope_of(l) : nullptr));
         // dq[t] = sum_j ds[t][j] k[j]
         AttnTileCall q = g;
         q.A = AttnOperand{attn_dpt, nh * Tp * Tp, 0, Tp * Tp, 1, Tp, 0, 1};
@@ -2055,7 +2062,6 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     DLLM_REQUIRE(c.activation == 0 || c.activation == 1, "activation must be 0 (silu) or 1 (gelu_tanh)");
     DLLM_REQUIRE(c.local_rope_theta >= 0.0 && c.attention_softcap >= 0.0 && c.logits_softcap >= 0.0,
                  "local_rope_theta and the soft-caps must be non-negative (0: none)");
-    DLLM_REQUIRE(c.attention_softcap == 0.0, "soft-capped attention scores are not built in the trainer");
     if (c.experts > 0) {
         bool any_sparse = false;
         for (int64_t l = 0; l < c.layers; ++l) any_sparse = any_sparse || l >= 64 || !((c.dense_layers >> l) & 1);

@@ -114,7 +114,7 @@ class Decoder:
     dense_layers: tuple[int, ...] = ()  # layers keeping a dense MLP in a model with experts (Qwen3-MoE)
     norm_placement: int = 0  # 0 pre, 1 post (OLMo 2), 2 both (architecture.py:315-320)
     # Gemma: norms as 1 + w, GELU-tanh MLPs, the window on the layers in window_layers only (None: every layer), a RoPE
-    # base of their own for those, soft-capped logits (soft-capped attention scores are not built)
+    # base of their own for those, soft-capped attention scores and logits
     norm_unit_offset: bool = False
     activation: int = 0  # 0 SiLU, 1 GELU (tanh approximation)
     window_layers: tuple[int, ...] | None = None

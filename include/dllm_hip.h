@@ -289,8 +289,7 @@ typedef struct {
     /* Gemma 2 and 3 (architecture.py, importer.py:283-345): norms with 1 + w (norm_unit_offset); the MLP's activation
      * 0 SiLU, 1 GELU-tanh; full_attention_layers: bit l set = layer l ignores sliding_window (the layers outside
      * sliding_window_layers); local_rope_theta (0: none) rotates the windowed layers with that base and no scaling;
-     * logits_softcap (0: none) maps the logits to cap tanh(logit / cap). attention_softcap must be 0: soft-capped
-     * attention scores are not built in the trainer. */
+     * attention_softcap and logits_softcap (0: none) map each scaled score and each logit x to cap tanh(x / cap). */
     int64_t norm_unit_offset, activation, full_attention_layers;
     double local_rope_theta, attention_softcap, logits_softcap;
 } dllm_hip_decoder_config;

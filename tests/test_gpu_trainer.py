@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_goldens.json").read_text())
 TOKENS = [1, 17, 42, 5, 63, 0, 9, 9, 30]
-FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe", "qwen3_moe", "olmo2", "gemma3"]
+FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe", "qwen3_moe", "olmo2", "gemma3", "gemma2"]
 
 
 def gpu_decoder(d: O.Decoder):
@@ -185,8 +185,7 @@ def test_lora_finetune_fingerprint_on_gpu(family):
     assert t.fingerprint() == GOLDEN["LORA_FINETUNE_FINGERPRINT"][family]  # merged on and hashed from the device
 
 
-# soft-capped attention scores (Gemma 2) are not built in the trainer; the oracle covers gemma2's run
-@pytest.mark.parametrize("family", [f for f in sorted(O.QLORA_FIXTURES) if O.QLORA_FIXTURES[f].attention_softcap is None])
+@pytest.mark.parametrize("family", sorted(O.QLORA_FIXTURES))
 def test_qlora_finetune_fingerprint_on_gpu(family):
     """LoRA on a Q4_0 base (tests/test_quantized_finetuning.py:27-29,96-112): 4 steps, batch 2, seed 3, lr 3e-2,
     rank 2 alpha 4 on every target of the hidden-32 models; the GPU quantises and dequantises the base itself, and
@@ -560,12 +559,12 @@ NORM_CASES = {
     # both placements (the Gemma layout's norms) with a residual multiplier folded into the output projections
     "sandwich": O.Decoder("llama", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16,
                           eps=1e-5, rope_theta=1e4, tied=True, norm_placement=2, residual_multiplier=0.5),
-    # Gemma 3's layout at a larger shape, with Gemma 2's logit soft-cap: unit-offset norms, GELU-tanh, the window on
-    # layer 0 only (rotating with its own base), per-head QK-norm
+    # Gemma 3's layout at a larger shape, with Gemma 2's soft-capped scores and logits: unit-offset norms, GELU-tanh,
+    # the window on layer 0 only (rotating with its own base), per-head QK-norm
     "gemma": O.Decoder("gemma3", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16, eps=1e-6,
                        rope_theta=1e6, tied=True, qk_norm=1, norm_placement=2, unit_offset=True, activation=1,
                        window=9, window_layers=(0,), local_rope_theta=1e4, embedding_multiplier=8.0,
-                       attention_multiplier=0.25, logits_softcap=2.0),
+                       attention_multiplier=0.25, attention_softcap=0.8, logits_softcap=2.0),
 }
 
 
