@@ -178,6 +178,10 @@ typedef struct {
      * map scores and logits s to cap tanh(s / cap) */
     int64_t norm_unit_offset, activation, full_attention_layers;
     double local_rope_theta, attention_softcap, logits_softcap;
+    /* shared_expert_intermediate_size (0: none) and shared_expert_gate (architecture.py; backprop.py:308-357,
+     * 501-527): a SwiGLU expert every row of a sparse layer goes through, its output times the sigmoid of a [1, hidden]
+     * gate's score when gated (Qwen2-MoE), added after the routed experts */
+    int64_t shared_inter, shared_gate;
 } orc_config;
 
 /* Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346). */
@@ -192,7 +196,8 @@ enum {
     ORC_EMBEDDING = 0, ORC_FINAL_NORM = 1, ORC_LM_HEAD = 2, ORC_GLOBALS = 3,
     ORC_ATTN_NORM = 0, ORC_Q = 1, ORC_K = 2, ORC_V = 3, ORC_QB = 4, ORC_KB = 5, ORC_VB = 6, ORC_QNORM = 7,
     ORC_KNORM = 8, ORC_O = 9, ORC_MLP_NORM = 10, ORC_GATE = 11, ORC_UP = 12, ORC_DOWN = 13, ORC_ROUTER = 14,
-    ORC_ATTN_POST_NORM = 15, ORC_MLP_POST_NORM = 16, ORC_LAYER_FIXED = 17
+    ORC_ATTN_POST_NORM = 15, ORC_MLP_POST_NORM = 16, ORC_SHARED_GATE = 17, ORC_SHARED_UP = 18, ORC_SHARED_DOWN = 19,
+    ORC_SHARED_GATE_W = 20, ORC_LAYER_FIXED = 21
 };
 int64_t orc_layer_slots(const orc_config* c);
 int64_t orc_slot_count(const orc_config* c);

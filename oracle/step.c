@@ -50,6 +50,11 @@ static int64_t slot_shape(const orc_config* c, int64_t slot, int64_t* d0, int64_
         case ORC_GATE: case ORC_UP: if (sparse) return 0; *d0 = c->inter; *d1 = H; return 2;
         case ORC_DOWN: if (sparse) return 0; *d0 = H; *d1 = c->inter; return 2;
         case ORC_ROUTER: if (!sparse) return 0; *d0 = c->experts; *d1 = H; return 2;
+        case ORC_SHARED_GATE: case ORC_SHARED_UP:
+            if (!sparse || c->shared_inter == 0) return 0;
+            *d0 = c->shared_inter; *d1 = H; return 2;
+        case ORC_SHARED_DOWN: if (!sparse || c->shared_inter == 0) return 0; *d0 = H; *d1 = c->shared_inter; return 2;
+        case ORC_SHARED_GATE_W: if (!sparse || c->shared_inter == 0 || !c->shared_gate) return 0; *d0 = 1; *d1 = H; return 2;
         default: {
             if (!sparse) return 0;
             const int64_t which = (kind - ORC_LAYER_FIXED) % 3;
@@ -93,6 +98,8 @@ typedef struct {
     float *x_in, *h1, *q_raw, *k_raw, *q, *k, *v, *attended, *out, *x_mid, *h2, *mlp;
     float *out_normed, *mlp_normed; /* post norms: the normalised block outputs (NULL without) */
     swiglu_saved dense;
+    swiglu_saved shared; /* the shared expert over every row (rows == 0 without one) */
+    float* shared_s;     /* [n]: its gate's sigmoid */
     float* router_logits; /* [n, experts] */
     int64_t* chosen;      /* [n, topk] */
     float* routing;       /* [n, topk] */
@@ -287,6 +294,22 @@ static void forward(fwd_state* st, const int64_t* tokens) {
                     for (int64_t d = 0; d < H; ++d) o[d] = o[d] + gsv->y[i * H + d] * weight;
                 }
             }
+            if (c->shared_inter > 0) { /* out = out + y (times the gate's sigmoid) */
+                s->shared.rows = n;
+                s->shared.x = s->h2;
+                swiglu_forward(ops, w, orc_slot(c, l, ORC_SHARED_GATE), orc_slot(c, l, ORC_SHARED_UP),
+                               orc_slot(c, l, ORC_SHARED_DOWN), c->shared_inter, H, &s->shared, (int)c->activation);
+                if (c->shared_gate) {
+                    s->shared_s = falloc(n);
+                    ops->linear(s->h2, w[orc_slot(c, l, ORC_SHARED_GATE_W)], NULL, s->shared_s, n, H, 1);
+                    for (int64_t r = 0; r < n; ++r) s->shared_s[r] = (float)orc_sigmoid((double)s->shared_s[r]);
+                }
+                for (int64_t r = 0; r < n; ++r)
+                    for (int64_t d = 0; d < H; ++d) {
+                        const float y = s->shared.y[r * H + d];
+                        s->mlp[r * H + d] = s->mlp[r * H + d] + (c->shared_gate ? y * s->shared_s[r] : y);
+                    }
+            }
         }
         float* x_out = falloc(n * H);
         if (has_post_norms(c)) {
@@ -318,6 +341,8 @@ static void free_state(fwd_state* st) {
                 swiglu_free(g);
             }
             free(s->groups);
+            if (s->shared.rows) swiglu_free(&s->shared);
+            free(s->shared_s);
         }
     }
     free(st->final_input);
@@ -388,6 +413,7 @@ static int residual_scaled_slots(const orc_config* c, int64_t layer, int64_t* ou
         out[k++] = orc_slot(c, layer, ORC_DOWN);
     } else {
         for (int64_t e = 0; e < c->experts; ++e) out[k++] = orc_expert_slot(c, layer, e, 2);
+        if (c->shared_inter > 0) out[k++] = orc_slot(c, layer, ORC_SHARED_DOWN);
     }
     return k;
 }
@@ -404,7 +430,7 @@ static float** fold_weights(const orc_config* c, float* const* w, float*** owned
     float** folded = (float**)calloc((size_t)slots, sizeof(float*));
     float** owned = (float**)calloc((size_t)slots, sizeof(float*));
     for (int64_t s = 0; s < slots; ++s) folded[s] = w[s];
-    int64_t* list = (int64_t*)malloc((size_t)(c->experts + 4) * sizeof(int64_t));
+    int64_t* list = (int64_t*)malloc((size_t)(c->experts + 5) * sizeof(int64_t));
     for (int64_t l = 0; l < c->layers; ++l) {
         if (residual) {
             const int k = residual_scaled_slots(c, l, list);
@@ -524,6 +550,30 @@ static void experts_backward(const fwd_state* st, int64_t l, const float* dmlp, 
     if (dprob_row) {
         dprob = falloc(n * E);
         for (int64_t r = 0; r < n; ++r) memcpy(dprob + r * E, dprob_row, (size_t)E * sizeof(float));
+    }
+    if (c->shared_inter > 0) { /* the shared expert and its gate (backprop.py:339-351) */
+        float* dy = falloc(n * H);
+        float* dscore = falloc(n);
+        float* dxs = falloc(n * H);
+        for (int64_t r = 0; r < n; ++r) {
+            if (c->shared_gate) {
+                const float sg = s->shared_s[r];
+                for (int64_t d = 0; d < H; ++d) dy[r * H + d] = dmlp[r * H + d] * sg;
+                const float ds = ops->dot(dmlp + r * H, s->shared.y + r * H, H);
+                dscore[r] = (ds * sg) * (1.0f - sg);
+            } else {
+                memcpy(dy + r * H, dmlp + r * H, (size_t)H * sizeof(float));
+            }
+        }
+        swiglu_backward(ops, w, g, orc_slot(c, l, ORC_SHARED_GATE), orc_slot(c, l, ORC_SHARED_UP),
+                        orc_slot(c, l, ORC_SHARED_DOWN), c->shared_inter, H, &s->shared, dy, dxs, (int)c->activation);
+        vadd(dh2, dxs, dh2, n * H);
+        if (c->shared_gate) {
+            const int64_t gs = orc_slot(c, l, ORC_SHARED_GATE_W);
+            ops->linear_backward(s->h2, w[gs], dscore, dxs, g[gs], NULL, n, H, 1);
+            vadd(dh2, dxs, dh2, n * H);
+        }
+        free(dy); free(dscore); free(dxs);
     }
     float* dlogits = falloc(n * E);
     ops->moe_route_backward(s->router_logits, s->chosen, dweights, dprob, dlogits, n, E, K, (int)c->normalize);
@@ -689,7 +739,7 @@ int orc_window_gradients(const orc_ops* ops, const orc_config* c, float* const* 
     float** folded = fold_weights(c, w, &owned);
     const int rc = window_gradients(ops, c, folded ? folded : w, tokens, targets, n, scale, router_scale, g, loss,
                                     router_loss_out);
-    int64_t* list = (int64_t*)malloc((size_t)(c->experts + 4) * sizeof(int64_t));
+    int64_t* list = (int64_t*)malloc((size_t)(c->experts + 5) * sizeof(int64_t));
     for (int64_t l = 0; folded && rc == 0 && l < c->layers; ++l) {
         if (has_multiplier(c->residual_multiplier)) {
             const int k = residual_scaled_slots(c, l, list);

@@ -36,7 +36,7 @@ class OrcConfig(C.Structure):
         ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double), ("dense_layers", C.c_int64),
         ("norm_placement", C.c_int64), ("norm_unit_offset", C.c_int64), ("activation", C.c_int64),
         ("full_attention_layers", C.c_int64), ("local_rope_theta", C.c_double), ("attention_softcap", C.c_double),
-        ("logits_softcap", C.c_double)]
+        ("logits_softcap", C.c_double), ("shared_inter", C.c_int64), ("shared_gate", C.c_int64)]
 
 
 class OrcRopeScaling(C.Structure):
@@ -386,6 +386,8 @@ class Decoder:
     local_rope_theta: float | None = None
     attention_softcap: float | None = None
     logits_softcap: float | None = None
+    shared_inter: int = 0  # a shared expert's intermediate size in the sparse layers (Qwen2-MoE, Granite MoE shared)
+    shared_gate: bool = False  # the shared expert's output times the sigmoid of a [1, hidden] gate (Qwen2-MoE)
 
     def full_attention_mask(self) -> int:
         """Bit l set: layer l ignores the sliding window (not in window_layers)."""
@@ -414,7 +416,8 @@ class Decoder:
                         self.embedding_multiplier, self.residual_multiplier, self.logits_scaling,
                         sum(1 << layer for layer in self.dense_layers), self.norm_placement, int(self.unit_offset),
                         self.activation, self.full_attention_mask(), self.local_rope_theta or 0.0,
-                        self.attention_softcap or 0.0, self.logits_softcap or 0.0)
+                        self.attention_softcap or 0.0, self.logits_softcap or 0.0, self.shared_inter,
+                        int(self.shared_gate))
         inv_freq = self.inv_freq
         if inv_freq is None and self.rope_scaling:
             inv_freq = rope_inv_freq_scaled(self.rotary_dim or self.head_dim, self.rope_theta, self.scaling())
@@ -456,6 +459,12 @@ class Decoder:
                     shapes[p + f"mlp.experts.{e}.gate.weight"] = (e_inter, H)
                     shapes[p + f"mlp.experts.{e}.up.weight"] = (e_inter, H)
                     shapes[p + f"mlp.experts.{e}.down.weight"] = (H, e_inter)
+                if self.shared_inter:
+                    shapes[p + "mlp.shared.gate.weight"] = (self.shared_inter, H)
+                    shapes[p + "mlp.shared.up.weight"] = (self.shared_inter, H)
+                    shapes[p + "mlp.shared.down.weight"] = (H, self.shared_inter)
+                    if self.shared_gate:
+                        shapes[p + "mlp.shared_gate.weight"] = (1, H)
             else:
                 shapes[p + "mlp.gate.weight"] = (self.inter, H)
                 shapes[p + "mlp.up.weight"] = (self.inter, H)
@@ -474,17 +483,19 @@ class Decoder:
                  "attention.v.weight": 3, "attention.q.bias": 4, "attention.k.bias": 5, "attention.v.bias": 6,
                  "attention.q_norm.weight": 7, "attention.k_norm.weight": 8, "attention.o.weight": 9,
                  "mlp_norm.weight": 10, "mlp.gate.weight": 11, "mlp.up.weight": 12, "mlp.down.weight": 13,
-                 "mlp.router.weight": 14, "attention_post_norm.weight": 15, "mlp_post_norm.weight": 16}
+                 "mlp.router.weight": 14, "attention_post_norm.weight": 15, "mlp_post_norm.weight": 16,
+                 "mlp.shared.gate.weight": 17, "mlp.shared.up.weight": 18, "mlp.shared.down.weight": 19,
+                 "mlp.shared_gate.weight": 20}
         _, layer, rest = name.split(".", 2)
-        per_layer = 17 + 3 * self.experts
+        per_layer = 21 + 3 * self.experts
         base = 3 + int(layer) * per_layer
         if rest in kinds:
             return base + kinds[rest]
         _, _, expert, which, _ = rest.split(".")
-        return base + 17 + 3 * int(expert) + {"gate": 0, "up": 1, "down": 2}[which]
+        return base + 21 + 3 * int(expert) + {"gate": 0, "up": 1, "down": 2}[which]
 
     def slot_count(self) -> int:
-        return 3 + self.layers * (17 + 3 * self.experts)
+        return 3 + self.layers * (21 + 3 * self.experts)
 
 
 def natural_key(name: str):
@@ -533,6 +544,11 @@ FIXTURES = {
                       window_layers=(0,), local_rope_theta=100.0, embedding_multiplier=math.sqrt(16),
                       attention_multiplier=12.0 ** -0.5, rope_scaling=(("rope_type", "linear"), ("factor", 2.0)),
                       **{**TINY, "head_dim": 8}),
+    "qwen2_moe": Decoder("qwen2_moe", tied=False, attn_bias=True, experts=4, topk=2, normalize=False, expert_inter=8,
+                         shared_inter=12, shared_gate=True, **TINY),
+    "granitemoeshared": Decoder("granitemoeshared", tied=True, experts=4, topk=2, normalize=True,
+                                embedding_multiplier=12.0, attention_multiplier=0.125, residual_multiplier=0.22,
+                                logits_scaling=8.0, shared_inter=12, **{**TINY, "inter": 8}),
     "phi3": Decoder("phi3", tied=False, window=3, rotary_dim=4, rope_attention_factor=4.0,
                     rope_scaling=frozen_scaling(PHI3_SCALING), **{**TINY, "hidden": 32, "head_dim": 8}),
 }
@@ -545,6 +561,7 @@ QLORA_FIXTURES = {
     "granite": replace(FIXTURES["granite"], hidden=32, vocab=264, head_dim=8),
     "qwen3_moe": replace(FIXTURES["qwen3_moe"], hidden=32, vocab=264),
     "gemma2": replace(FIXTURES["gemma2"], hidden=32, vocab=264, embedding_multiplier=math.sqrt(32)),
+    "qwen2_moe": replace(FIXTURES["qwen2_moe"], hidden=32, vocab=264, head_dim=8),
 }
 
 
@@ -754,6 +771,8 @@ def lora_target_weights(d: Decoder, lora: Lora) -> list[str]:
         for target in lora.targets:
             if target in ("gate", "up", "down") and d.is_sparse(layer):
                 names.extend(f"layers.{layer}.mlp.experts.{e}.{target}.weight" for e in range(d.experts))
+                if d.shared_inter:
+                    names.append(f"layers.{layer}.mlp.shared.{target}.weight")
             else:
                 names.append(f"layers.{layer}.{LORA_WEIGHT_NAMES[target]}")
     return tensor_order(names)
