@@ -121,6 +121,17 @@ int launch_softcap(const float* x, float* out, int64_t n, double cap, hipStream_
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,
                            float* dgate, float* dup, int64_t n, hipStream_t stream, int activation = 0);
 int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t stream);
+// out[i] = window-ordered float sum over s of f32(partial[s][i] weights[s]) (weights null: 1)
+int launch_segment_sums(const float* partial, int64_t dim, int nseg, const float* weights, float* out,
+                        hipStream_t stream);
+// The shared expert's gate (backprop.py:339-351, 519-524): forward s = f32(sigmoid(h2 w)), term = f32(y s) (w null:
+// term = y); backward dy = f32(dmlp s), dscore = f32(f32(dot(dmlp, y) s) (1 - s)), then dh += f32(dscore w) (dh
+// non-null) and part[window][k] = the window's f32(sum dscore h2[.][k]) (part non-null).
+int launch_shared_gate_forward(const float* h2, const float* w, const float* y, float* s, float* term, int64_t rows,
+                               int64_t H, hipStream_t stream);
+int launch_shared_gate_backward(const float* dmlp, const float* y, const float* s, const float* w, const float* h2,
+                                float* dy, float* dscore, float* dh, const int64_t* seg, int nseg, float* part,
+                                int64_t rows, int64_t H, hipStream_t stream);
 // x = f32(x * f), or f32(x / f) with divide, in place
 int launch_scale(float* x, int64_t n, float f, bool divide, hipStream_t stream);
 int launch_add3(const float* a, const float* b, const float* c, float* out, int64_t n, hipStream_t stream);

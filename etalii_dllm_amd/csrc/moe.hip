@@ -552,6 +552,103 @@ int launch_moe_route_backward(const float* logits, const int64_t* indices, const
     return check_launch("moe_route_backward");
 }
 
+// The shared expert's gate (backprop.py:519-524), one 64-lane workgroup per row r: lane 0 forms the score
+// f32(sum over k ascending of h2[r][k] w[k]) in double (linear with one output) and s[r] = f32(sigmoid(score));
+// then term[r][d] = f32(y[r][d] s[r]). Without a gate (w null) term = y.
+__global__ __launch_bounds__(64) void shared_gate_forward_kernel(const float* __restrict__ h2,
+                                                                 const float* __restrict__ w,
+                                                                 const float* __restrict__ y, float* __restrict__ s_out,
+                                                                 float* __restrict__ term, int64_t H) {
+    const int64_t r = blockIdx.x;
+    __shared__ float sg;
+    if (w == nullptr) {
+        for (int64_t d = threadIdx.x; d < H; d += 64) term[r * H + d] = y[r * H + d];
+        return;
+    }
+    if (threadIdx.x == 0) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < H; ++k) acc += static_cast<double>(h2[r * H + k]) * static_cast<double>(w[k]);
+        sg = static_cast<float>(dsigmoid(static_cast<double>(static_cast<float>(acc))));
+        s_out[r] = sg;
+    }
+    __syncthreads();
+    for (int64_t d = threadIdx.x; d < H; d += 64) term[r * H + d] = y[r * H + d] * sg;
+}
+
+// Its backward (backprop.py:339-351), one 64-lane workgroup per row: dy[r][d] = f32(dmlp[r][d] s[r]) and
+// dscore[r] = f32(f32(ds s) (1 - s)) with ds = dot(dmlp[r], y[r]) (dllm::dot: ascending, in double, rounded once).
+__global__ __launch_bounds__(64) void shared_gate_backward_kernel(const float* __restrict__ dmlp,
+                                                                  const float* __restrict__ y,
+                                                                  const float* __restrict__ s,
+                                                                  float* __restrict__ dy, float* __restrict__ dscore,
+                                                                  int64_t H) {
+    const int64_t r = blockIdx.x;
+    const float sg = s[r];
+    for (int64_t d = threadIdx.x; d < H; d += 64) dy[r * H + d] = dmlp[r * H + d] * sg;
+    if (threadIdx.x == 0) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < H; ++k) acc += static_cast<double>(dmlp[r * H + k]) * static_cast<double>(y[r * H + k]);
+        const float ds = static_cast<float>(acc);
+        dscore[r] = (ds * sg) * (1.0f - sg);
+    }
+}
+
+// The gate's input gradient added to dh (linear_backward with one output, then dh2 + dh2_gate):
+// dh[r][k] = dh[r][k] + f32(dscore[r] w[k]) (the product of two floats is exact in double).
+__global__ __launch_bounds__(256) void shared_gate_dx_kernel(const float* __restrict__ dscore,
+                                                             const float* __restrict__ w, float* __restrict__ dh,
+                                                             int64_t rows, int64_t H) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < rows * H;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        dh[i] = dh[i] + static_cast<float>(static_cast<double>(dscore[i / H]) * static_cast<double>(w[i % H]));
+}
+
+// The gate's weight gradient per window s: part[s][k] = f32(sum over the window's rows r ascending of
+// dscore[r] h2[r][k]) in double (linear_backward's dw with one output).
+__global__ __launch_bounds__(256) void shared_gate_dw_kernel(const float* __restrict__ dscore,
+                                                             const float* __restrict__ h2,
+                                                             const int64_t* __restrict__ seg, float* __restrict__ part,
+                                                             int64_t H) {
+    const int64_t k = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int w = blockIdx.y;
+    if (k >= H) return;
+    double acc = 0.0;
+    for (int64_t r = seg[w]; r < seg[w + 1]; ++r)
+        acc += static_cast<double>(dscore[r]) * static_cast<double>(h2[r * H + k]);
+    part[static_cast<int64_t>(w) * H + k] = static_cast<float>(acc);
+}
+
+int launch_shared_gate_forward(const float* h2, const float* w, const float* y, float* s, float* term, int64_t rows,
+                               int64_t H, hipStream_t stream) {
+    if (rows == 0) return kOk;
+    DLLM_REQUIRE(rows < (int64_t{1} << 31), "too many rows for the shared expert's gate");
+    hipLaunchKernelGGL(shared_gate_forward_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, stream, h2, w, y,
+                       s, term, H);
+    return check_launch("shared gate");
+}
+
+int launch_shared_gate_backward(const float* dmlp, const float* y, const float* s, const float* w, const float* h2,
+                                float* dy, float* dscore, float* dh, const int64_t* seg, int nseg, float* part,
+                                int64_t rows, int64_t H, hipStream_t stream) {
+    if (rows == 0) return kOk;
+    DLLM_REQUIRE(rows < (int64_t{1} << 31), "too many rows for the shared expert's gate");
+    hipLaunchKernelGGL(shared_gate_backward_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, stream, dmlp, y, s,
+                       dy, dscore, H);
+    DLLM_TRY(check_launch("shared gate backward"));
+    if (dh) {
+        const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(rows * H, 256), 16384));
+        hipLaunchKernelGGL(shared_gate_dx_kernel, dim3(blocks), dim3(256), 0, stream, dscore, w, dh, rows, H);
+        DLLM_TRY(check_launch("shared gate dx"));
+    }
+    if (part) {
+        hipLaunchKernelGGL(shared_gate_dw_kernel, dim3(static_cast<unsigned>(ceil_div(H, 256)),
+                                                       static_cast<unsigned>(nseg)),
+                           dim3(256), 0, stream, dscore, h2, seg, part, H);
+        DLLM_TRY(check_launch("shared gate dw"));
+    }
+    return kOk;
+}
+
 int launch_moe_combine(const float* y, const int64_t* order, const int64_t* slot, const float* weights,
                        const float* addend, float* out, int64_t rows, int64_t k, int64_t dim, hipStream_t stream) {
     const int64_t n = rows * dim;

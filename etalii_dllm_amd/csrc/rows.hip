@@ -549,6 +549,14 @@ int launch_rms_norm_backward_dx(const float* x, const float* w, const float* dy,
     return check_launch("rms_norm_backward");
 }
 
+int launch_segment_sums(const float* partial, int64_t dim, int nseg, const float* weights, float* out,
+                        hipStream_t stream) {
+    if (dim == 0) return kOk;
+    hipLaunchKernelGGL(segment_float_sum_kernel, dim3(static_cast<unsigned>(ceil_div(dim, 256))), dim3(256), 0, stream,
+                       partial, dim, nseg, weights, nullptr, out);
+    return check_launch("segment sums");
+}
+
 int launch_column_sums(int kind, const float* dy, const float* x, const double* inv_rms, int64_t dim,
                        const int64_t* seg_host, int nseg, float* partial, float* out, hipStream_t stream,
                        const float* weights, const float* colscale) {

@@ -166,6 +166,7 @@ struct dllm_hip_trainer {
         int attn_norm, q, k, v, qb = -1, kb = -1, vb = -1, qn = -1, kn = -1, o, mlp_norm, gate, up, down;
         int router = -1;
         int attn_post = -1, mlp_post = -1;   // post norms (OLMo 2; sandwich with the pre norms)
+        int sgate = -1, sup = -1, sdown = -1, sgw = -1;  // the shared expert and its gate (Qwen2-MoE)
         std::vector<int> egate, eup, edown;  // routed experts
     };
     std::vector<LayerIds> layer_ids;
@@ -174,6 +175,9 @@ struct dllm_hip_trainer {
     struct Saved {
         float *x_in, *h1, *q_raw, *k_raw, *qn, *kn, *q, *k, *v, *attended, *x_mid, *h2, *gate, *up, *gate_act, *product;
         float *out = nullptr, *mlp = nullptr;  // post norms: the attention and MLP outputs before their norms
+        // the shared expert over every row: gate/up/activation/product [R][SI], y [R][H], the gate's sigmoid [R]
+        float *sh_gate = nullptr, *sh_up = nullptr, *sh_act = nullptr, *sh_product = nullptr, *sh_y = nullptr,
+              *sh_s = nullptr;
         // routed experts: router logits and probabilities [R][E], the choices [R][K] (rank order), the expert
         // outputs y [R K][H] in grouped order (gate, up, gate_act, product are grouped [R K][EI] then)
         float *router_logits = nullptr, *probs = nullptr, *routing = nullptr, *y = nullptr;
@@ -207,7 +211,11 @@ struct dllm_hip_trainer {
     std::vector<int64_t> counts_host;  // [windows][E] choices per window over all layers
     double router_scale_cur = 0.0, last_router_loss = 0.0;
     double *inv_mlp = nullptr, *inv_attn = nullptr, *inv_post = nullptr;
-    float *post_tmp = nullptr, *dpost = nullptr;  // post norms: a normalised block output; a norm's input gradient  // the layer norms' inverse rms, read by their weights' gradients
+    float *post_tmp = nullptr, *dpost = nullptr;
+    // shared experts: the gated output term and the MLP output [R][H]; the backward's dy, dx [R][H], its dproduct,
+    // dgate, dup [R][SI], the gate score's gradient [R] and the gate dW's per-window partial sums [W][H]
+    float *sh_term = nullptr, *sh_out = nullptr, *dsh_dy = nullptr, *dsh_x = nullptr, *dsh_product = nullptr,
+          *dsh_gate = nullptr, *dsh_up = nullptr, *dsh_score = nullptr, *sh_part = nullptr;  // post norms: a normalised block output; a norm's input gradient  // the layer norms' inverse rms, read by their weights' gradients
     double *inv_rms = nullptr, *row_max = nullptr, *row_total = nullptr, *row_loss = nullptr, *loss_w = nullptr,
            *stats = nullptr, *inv_freq = nullptr, *cos_t = nullptr, *sin_t = nullptr;
     // Gemma 3's windowed layers rotate with a base of their own and no scaling (backprop.py:63-67)
@@ -354,6 +362,12 @@ struct dllm_hip_trainer {
                     add_tensor(x + "up.weight", EI, H, true);
                     add_tensor(x + "down.weight", H, EI, true);
                 }
+                if (k.shared_inter > 0) {
+                    add_tensor(p + "mlp.shared.gate.weight", k.shared_inter, H, true);
+                    add_tensor(p + "mlp.shared.up.weight", k.shared_inter, H, true);
+                    add_tensor(p + "mlp.shared.down.weight", H, k.shared_inter, true);
+                    if (k.shared_gate) add_tensor(p + "mlp.shared_gate.weight", 1, H, false);
+                }
             } else {
                 add_tensor(p + "mlp.gate.weight", I, H, true);
                 add_tensor(p + "mlp.up.weight", I, H, true);
@@ -406,6 +420,10 @@ struct dllm_hip_trainer {
             L.o = id(p + "attention.o.weight");
             L.mlp_norm = id(p + "mlp_norm.weight");
             L.attn_post = id(p + "attention_post_norm.weight");
+            L.sgate = id(p + "mlp.shared.gate.weight");
+            L.sup = id(p + "mlp.shared.up.weight");
+            L.sdown = id(p + "mlp.shared.down.weight");
+            L.sgw = id(p + "mlp.shared_gate.weight");
             L.mlp_post = id(p + "mlp_post_norm.weight");
             L.gate = id(p + "mlp.gate.weight");
             L.up = id(p + "mlp.up.weight");
@@ -525,7 +543,23 @@ struct dllm_hip_trainer {
                 DLLM_TRY(make(&s.order, RK));
                 DLLM_TRY(make(&s.eseg, E * (W_max + 1)));
                 DLLM_TRY(make(&s.tables, kExpertMatmuls * gemm_group_bytes(static_cast<int>(E))));
+                if (c.shared_inter > 0) {
+                    const int64_t SI = c.shared_inter;
+                    DLLM_TRY(make(&s.sh_gate, R * SI));
+                    DLLM_TRY(make(&s.sh_up, R * SI));
+                    DLLM_TRY(make(&s.sh_act, R * SI));
+                    DLLM_TRY(make(&s.sh_product, R * SI));
+                    DLLM_TRY(make(&s.sh_y, R * H));
+                    DLLM_TRY(make(&s.sh_s, R));
+                }
             }
+        }
+        if (E > 0 && c.shared_inter > 0) {
+            const int64_t SI = c.shared_inter;
+            for (float** b : {&sh_term, &sh_out, &dsh_dy, &dsh_x}) DLLM_TRY(make(b, R * H));
+            for (float** b : {&dsh_product, &dsh_gate, &dsh_up}) DLLM_TRY(make(b, R * SI));
+            DLLM_TRY(make(&dsh_score, R));
+            DLLM_TRY(make(&sh_part, W_max * H));
         }
         if (E > 0) {
             DLLM_TRY(make(&xg, RK * H));
@@ -683,6 +717,7 @@ struct dllm_hip_trainer {
                 add(L.o, resid_rowscale);
                 add(L.down, resid_rowscale);
                 for (int id : L.edown) add(id, resid_rowscale);
+                add(L.sdown, resid_rowscale);
             }
         }
         const size_t bytes = static_cast<size_t>(off > 0 ? off : 1) * sizeof(float);
@@ -1499,7 +1534,17 @@ struct dllm_hip_trainer {
         DLLM_TRY(expert_matmul(sv, kFwdUp, s));
         DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * K * EI, s, act()));
         DLLM_TRY(expert_matmul(sv, kFwdDown, s));
-        return launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sv.x_mid, x_out, R, K, H, s);
+        if (c.shared_inter == 0) return launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sv.x_mid, x_out, R, K, H, s);
+        // the shared expert over every row; out = (0 + the row's experts' f32(y w), ascending) + its (gated) output,
+        // then x_out = x_mid + out (backprop.py:519-525)
+        const int64_t SI = c.shared_inter;
+        DLLM_TRY(linear_fwd(sv.h2, R, H, L.sgate, nullptr, sv.sh_gate, nullptr, s));
+        DLLM_TRY(linear_fwd(sv.h2, R, H, L.sup, nullptr, sv.sh_up, nullptr, s));
+        DLLM_TRY(launch_swiglu_forward(sv.sh_gate, sv.sh_up, sv.sh_act, sv.sh_product, R * SI, s, act()));
+        DLLM_TRY(linear_fwd(sv.sh_product, R, SI, L.sdown, nullptr, sv.sh_y, nullptr, s));
+        DLLM_TRY(launch_shared_gate_forward(sv.h2, L.sgw >= 0 ? P(L.sgw) : nullptr, sv.sh_y, sv.sh_s, sh_term, R, H, s));
+        DLLM_TRY(launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sh_term, sh_out, R, K, H, s));
+        return launch_add(sv.x_mid, sh_out, x_out, R * H, s);
     }
 
     // _experts_backward (backprop.py:308-357): dh (dh2) from dx (the gradient of the layer's MLP output).
@@ -1528,7 +1573,38 @@ struct dllm_hip_trainer {
         DLLM_TRY(side_mark(kSideMlp));
         DLLM_TRY(linear_dx(dlogits_r, R, L.router, dh2r, nullptr, s));
         // dh2 = (0 + the experts' dx in expert order) + dh2_router
-        return launch_moe_combine(dxg, sv.order, sv.slot, nullptr, dh2r, dh, R, K, H, s);
+        if (c.shared_inter == 0) return launch_moe_combine(dxg, sv.order, sv.slot, nullptr, dh2r, dh, R, K, H, s);
+        // with a shared expert (backprop.py:339-352): dh2 = (((0 + experts' dx) + shared dx) + gate dx) + router dx
+        const int64_t SI = c.shared_inter;
+        const bool gated = L.sgw >= 0;
+        const float* dys = dx;
+        if (gated) {
+            const bool gate_dw = grad_wanted(G(L.sgw));
+            DLLM_TRY(launch_shared_gate_backward(dx, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, dsh_dy, dsh_score, nullptr,
+                                                 seg_d, nseg, gate_dw ? sh_part : nullptr, R, H, s));
+            if (gate_dw) DLLM_TRY(launch_segment_sums(sh_part, H, nseg, window_weights(), G(L.sgw), s));
+            dys = dsh_dy;
+        }
+        DLLM_TRY(linear_dx(dys, R, L.sdown, dsh_product, nullptr, s));
+        DLLM_TRY(launch_swiglu_backward(sv.sh_gate, sv.sh_up, sv.sh_act, dsh_product, dsh_gate, dsh_up, R * SI, s, act()));
+        // the shared expert's dW with the other weight gradients (their window partial sums share one buffer): the
+        // next routed layer waits for kSideMlp before rewriting dsh_dy, dsh_gate, dsh_up, and dx is kept until
+        // kSideDown when the down dW reads it
+        hipStream_t sws = s;
+        DLLM_TRY(side_fork_from(s, &sws));
+        DLLM_TRY(linear_dw(dys, H, sv.sh_product, SI, nseg, G(L.sdown), nullptr, nullptr, sws, nullptr, -1,
+                           unfold_scale(L.sdown)));
+        if (dys == dx) DLLM_TRY(side_mark(kSideDown));
+        DLLM_TRY(linear_dw(dsh_gate, SI, sv.h2, H, nseg, G(L.sgate), nullptr, nullptr, sws));
+        DLLM_TRY(linear_dw(dsh_up, SI, sv.h2, H, nseg, G(L.sup), nullptr, nullptr, sws));
+        DLLM_TRY(side_mark(kSideMlp));
+        DLLM_TRY(linear_dx(dsh_gate, R, L.sgate, dsh_x, nullptr, s));
+        DLLM_TRY(linear_dx(dsh_up, R, L.sup, dsh_x, dsh_x, s));  // dx_gate + dx_up
+        DLLM_TRY(launch_moe_combine(dxg, sv.order, sv.slot, nullptr, dsh_x, dh, R, K, H, s));
+        if (gated)  // + f32(dscore w), the gate's input gradient
+            DLLM_TRY(launch_shared_gate_backward(dx, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, dsh_dy, dsh_score, dh, seg_d,
+                                                 nseg, nullptr, R, H, s));
+        return launch_add(dh, dh2r, dh, R * H, s);
     }
 
     // Host preparation of a batch of windows; returns the packed row count.
@@ -1873,6 +1949,8 @@ struct dllm_hip_trainer {
                 if (t >= 4 && sparse(layer)) {  // gate, up, down of a routed layer: every expert's (the router never)
                     const std::vector<int>& ids = t == 4 ? L.egate : (t == 5 ? L.eup : L.edown);
                     weights.insert(weights.end(), ids.begin(), ids.end());
+                    const int shared = t == 4 ? L.sgate : (t == 5 ? L.sup : L.sdown);  // and the shared expert's
+                    if (shared >= 0) weights.push_back(shared);
                 } else {
                     weights.push_back(index["layers." + std::to_string(layer) + "." + kTargets[t]]);
                 }
@@ -2059,6 +2137,9 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     DLLM_REQUIRE(c.attention_scale > 0.0 && std::isfinite(c.attention_scale), "attention_scale must be positive");
     DLLM_REQUIRE(c.norm_placement >= 0 && c.norm_placement <= 2, "norm_placement must be 0 (pre), 1 (post) or 2 (both)");
     DLLM_REQUIRE(c.norm_placement == 0 || c.experts == 0, "post norms are built for dense MLPs only");
+    DLLM_REQUIRE(c.shared_inter >= 0 && c.shared_inter % 4 == 0, "the shared expert's size must be a multiple of 4");
+    DLLM_REQUIRE(c.shared_inter == 0 || c.experts > 0, "a shared expert needs routed experts");
+    DLLM_REQUIRE(c.shared_gate == 0 || c.shared_inter > 0, "a shared expert gate needs a shared expert");
     DLLM_REQUIRE(c.activation == 0 || c.activation == 1, "activation must be 0 (silu) or 1 (gelu_tanh)");
     DLLM_REQUIRE(c.local_rope_theta >= 0.0 && c.attention_softcap >= 0.0 && c.logits_softcap >= 0.0,
                  "local_rope_theta and the soft-caps must be non-negative (0: none)");

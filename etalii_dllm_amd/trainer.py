@@ -29,7 +29,8 @@ class DecoderConfig(C.Structure):
         ("embedding_multiplier", C.c_double), ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double),
         ("dense_layers", C.c_int64), ("norm_placement", C.c_int64), ("norm_unit_offset", C.c_int64),
         ("activation", C.c_int64), ("full_attention_layers", C.c_int64), ("local_rope_theta", C.c_double),
-        ("attention_softcap", C.c_double), ("logits_softcap", C.c_double)]
+        ("attention_softcap", C.c_double), ("logits_softcap", C.c_double), ("shared_inter", C.c_int64),
+        ("shared_gate", C.c_int64)]
 
 
 class AdamWArgs(C.Structure):
@@ -121,6 +122,8 @@ class Decoder:
     local_rope_theta: float | None = None
     attention_softcap: float | None = None
     logits_softcap: float | None = None
+    shared_inter: int = 0  # a shared expert's SwiGLU size in every routed layer (Qwen2-MoE, Granite MoE shared)
+    shared_gate: bool = False  # its output times the sigmoid of a [1, hidden] gate (Qwen2-MoE)
 
     def native(self) -> DecoderConfig:
         return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
@@ -134,7 +137,8 @@ class Decoder:
                              self.norm_placement, int(self.norm_unit_offset), self.activation,
                              0 if self.window_layers is None else
                              sum(1 << i for i in range(min(self.layers, 64)) if i not in self.window_layers),
-                             self.local_rope_theta or 0.0, self.attention_softcap or 0.0, self.logits_softcap or 0.0)
+                             self.local_rope_theta or 0.0, self.attention_softcap or 0.0, self.logits_softcap or 0.0,
+                             self.shared_inter, int(self.shared_gate))
 
 
 def _windows(windows):

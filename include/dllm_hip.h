@@ -292,6 +292,11 @@ typedef struct {
      * attention_softcap and logits_softcap (0: none) map each scaled score and each logit x to cap tanh(x / cap). */
     int64_t norm_unit_offset, activation, full_attention_layers;
     double local_rope_theta, attention_softcap, logits_softcap;
+    /* A shared expert in every routed layer (architecture.py shared_expert_intermediate_size, shared_expert_gate;
+     * backprop.py:308-357, 501-527): shared_inter (0: none, else a multiple of 4) is its SwiGLU size; every row goes
+     * through it, and with shared_gate its output is multiplied by the sigmoid of a [1, hidden] gate's score (Qwen2-MoE);
+     * its output is added after the routed experts'. */
+    int64_t shared_inter, shared_gate;
 } dllm_hip_decoder_config;
 
 typedef struct dllm_hip_trainer dllm_hip_trainer;

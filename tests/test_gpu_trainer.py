@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_goldens.json").read_text())
 TOKENS = [1, 17, 42, 5, 63, 0, 9, 9, 30]
-FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe", "qwen3_moe", "olmo2", "gemma3", "gemma2"]
+FAMILIES = ["llama", "mistral", "qwen2", "qwen3", "mixtral", "olmoe", "phi3", "granite", "granitemoe", "qwen3_moe", "olmo2", "gemma3", "gemma2", "qwen2_moe", "granitemoeshared"]
 
 
 def gpu_decoder(d: O.Decoder):
@@ -29,7 +29,7 @@ def gpu_decoder(d: O.Decoder):
                    logits_scaling=d.logits_scaling, dense_layers=d.dense_layers, norm_placement=d.norm_placement,
                    norm_unit_offset=d.unit_offset, activation=d.activation, window_layers=d.window_layers,
                    local_rope_theta=d.local_rope_theta, attention_softcap=d.attention_softcap,
-                   logits_softcap=d.logits_softcap)
+                   logits_softcap=d.logits_softcap, shared_inter=d.shared_inter, shared_gate=d.shared_gate)
 
 
 def make_trainer(d: O.Decoder, weights, max_tokens=64, max_windows=8, max_window=32):
@@ -283,6 +283,10 @@ MOE = {
                             eps=1e-6, rope_theta=1e4, tied=True, experts=8, topk=2, normalize=True, expert_inter=32,
                             embedding_multiplier=12.0, attention_multiplier=0.0625, residual_multiplier=0.22,
                             logits_scaling=6.0),
+    # a gated shared expert beside the routed ones, q/k/v biases
+    "qwen2_moe": O.Decoder("qwen2_moe", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2, head_dim=16,
+                           eps=1e-6, rope_theta=1e6, tied=False, attn_bias=True, experts=8, topk=2, normalize=False,
+                           expert_inter=32, shared_inter=48, shared_gate=True),
 }
 
 
