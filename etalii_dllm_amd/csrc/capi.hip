@@ -262,6 +262,15 @@ int dllm_hip_gelu_tanh(const float* x, float* out, size_t n, void* stream) {
     return launch_gelu_tanh(x, out, static_cast<int64_t>(n), as_stream(stream));
 }
 
+int dllm_hip_softcap(const float* x, float* out, size_t n, double cap, void* stream) {
+    DLLM_REQUIRE(cap > 0.0, "cap must be positive");
+    return launch_softcap(x, out, static_cast<int64_t>(n), cap, as_stream(stream));
+}
+
+int dllm_hip_sigmoid_elementwise(const float* x, float* out, size_t n, void* stream) {
+    return launch_sigmoid(x, out, static_cast<int64_t>(n), as_stream(stream));
+}
+
 int dllm_hip_swiglu(const float* gate, const float* up, float* out, size_t n, int kind, void* stream) {
     DLLM_REQUIRE(kind == 0 || kind == 2, "kind must be silu (0) or gelu_tanh (2)");
     if (kind == 2) return launch_geglu_tanh(gate, up, out, static_cast<int64_t>(n), as_stream(stream));

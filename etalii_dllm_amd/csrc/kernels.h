@@ -116,6 +116,8 @@ int launch_gelu_tanh_backward(const float* x, const float* dy, float* out, int64
 int launch_softcap_backward(const float* x, const float* dy, float* out, int64_t n, double cap, hipStream_t stream);
 // softcap (nn.hpp:457-461): out = f32(cap tanh(x / cap)), in double
 int launch_softcap(const float* x, float* out, int64_t n, double cap, hipStream_t stream);
+// out = f32(sigmoid(x)) elementwise (nn.hpp:464)
+int launch_sigmoid(const float* x, float* out, int64_t n, hipStream_t stream);
 // _swiglu_backward's elementwise glue (backprop.py:301-303): dgate = silu_backward(gate, dproduct * up),
 // dup = dproduct * gate_act.
 int launch_swiglu_backward(const float* gate, const float* up, const float* gate_act, const float* dproduct,

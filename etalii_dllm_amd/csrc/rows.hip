@@ -706,6 +706,19 @@ __global__ __launch_bounds__(256) void softcap_kernel(const float* __restrict__ 
         out[i] = static_cast<float>(cap * dtanh(static_cast<double>(x[i]) / cap));
 }
 
+__global__ __launch_bounds__(256) void sigmoid_kernel(const float* __restrict__ x, float* __restrict__ out,
+                                                      int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        out[i] = static_cast<float>(dsigmoid(static_cast<double>(x[i])));
+}
+
+int launch_sigmoid(const float* x, float* out, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(sigmoid_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, out, n);
+    return check_launch("sigmoid");
+}
+
 int launch_softcap(const float* x, float* out, int64_t n, double cap, hipStream_t stream) {
     if (n == 0) return kOk;
     hipLaunchKernelGGL(softcap_kernel, dim3(elementwise_grid(n)), dim3(256), 0, stream, x, out, n, cap);

@@ -60,6 +60,8 @@ def _load() -> C.CDLL:
     lib.dllm_hip_silu.argtypes = [_vp, _vp, _sz, _vp]
     lib.dllm_hip_swiglu.argtypes = [_vp, _vp, _vp, _sz, C.c_int, _vp]
     lib.dllm_hip_gelu_tanh.argtypes = [_vp, _vp, _sz, _vp]
+    lib.dllm_hip_softcap.argtypes = [_vp, _vp, _sz, C.c_double, _vp]
+    lib.dllm_hip_sigmoid_elementwise.argtypes = [_vp, _vp, _sz, _vp]
     lib.dllm_hip_linear_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp]
     lib.dllm_hip_rms_norm_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _sz, _sz, C.c_double, C.c_int, _vp, _sz,
                                                _vp]
@@ -247,6 +249,24 @@ def gelu_tanh(x) -> np.ndarray:
     x = _f32(x)
     dx, out = Device.of(x), Device(x.nbytes)
     check(lib.dllm_hip_gelu_tanh(dx.ptr, out.ptr, x.size, None))
+    return out.download(x.shape)
+
+
+def softcap(x, cap: float) -> np.ndarray:
+    """kernels.cpp:650-660: elementwise cap * tanh(x / cap), in double; cap must be positive."""
+    x = _f32(x)
+    if not cap > 0.0:
+        raise ValueError("cap must be positive")
+    dx, out = Device.of(x), Device(x.nbytes)
+    check(lib.dllm_hip_softcap(dx.ptr, out.ptr, x.size, float(cap), None))
+    return out.download(x.shape)
+
+
+def sigmoid_elementwise(x) -> np.ndarray:
+    """kernels.cpp:629-630: elementwise logistic sigmoid, in double, rounded once."""
+    x = _f32(x)
+    dx, out = Device.of(x), Device(x.nbytes)
+    check(lib.dllm_hip_sigmoid_elementwise(dx.ptr, out.ptr, x.size, None))
     return out.download(x.shape)
 
 

@@ -94,6 +94,11 @@ int dllm_hip_attention(const float* q, const float* k, const float* v, float* ou
 int dllm_hip_silu(const float* x, float* out, size_t n, void* stream);
 int dllm_hip_gelu_tanh(const float* x, float* out, size_t n, void* stream);
 int dllm_hip_swiglu(const float* gate, const float* up, float* out, size_t n, int kind, void* stream);
+/* f32(cap tanh(x / cap)) elementwise in double; cap > 0. Replaces kernels.cpp:650-660 `softcap` (nn.hpp:457-461). */
+int dllm_hip_softcap(const float* x, float* out, size_t n, double cap, void* stream);
+/* f32(sigmoid(x)) elementwise with the portable sigmoid. Replaces kernels.cpp:629-630 `sigmoid_elementwise`
+ * (nn.hpp:464, math.hpp:322-328). */
+int dllm_hip_sigmoid_elementwise(const float* x, float* out, size_t n, void* stream);
 
 /* ---- backward kernels ---- */
 

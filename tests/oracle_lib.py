@@ -1146,6 +1146,18 @@ def gelu_tanh_backward(x, dy) -> np.ndarray:
     return np.array([f(float(a), float(b)) for a, b in zip(np.ravel(x), np.ravel(dy))], np.float32).reshape(np.shape(x))
 
 
+def softcap(x, cap: float) -> np.ndarray:
+    """softcap (nn.hpp:457-461): f32(cap tanh(x / cap)) in double with the oracle's tanh, elementwise."""
+    t = oracle().orc_tanh
+    return np.array([np.float32(cap * t(float(a) / cap)) for a in np.ravel(x)], np.float32).reshape(np.shape(x))
+
+
+def sigmoid_elementwise(x) -> np.ndarray:
+    """sigmoid_float (nn.hpp:464): f32(sigmoid(x)) with the oracle's sigmoid, elementwise."""
+    f = oracle().orc_sigmoid
+    return np.array([np.float32(f(float(a))) for a in np.ravel(x)], np.float32).reshape(np.shape(x))
+
+
 def softcap_backward(x, dy, cap: float) -> np.ndarray:
     """The oracle's softcap_backward (grad.hpp:193-197), elementwise."""
     f = oracle().orc_softcap_backward

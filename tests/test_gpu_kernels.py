@@ -294,6 +294,12 @@ def test_gelu_tanh_and_softcap_backward(K):
         same_up_to_nan_bits(K.softcap_backward(x, dy, cap), O.softcap_backward(x, dy, cap), f"softcap {cap}")
     with pytest.raises(ValueError):
         K.softcap_backward(x, dy, 0.0)
+    # the forward soft-cap and the elementwise sigmoid (kernels.cpp:629-630, 650-660)
+    for cap in (30.0, 0.05):
+        same_up_to_nan_bits(K.softcap(x, cap), O.softcap(x, cap), f"softcap forward {cap}")
+    same_up_to_nan_bits(K.sigmoid_elementwise(x), O.sigmoid_elementwise(x), "sigmoid_elementwise")
+    with pytest.raises(ValueError):
+        K.softcap(x, -1.0)
 
 
 def test_softmax_column_mean_and_dot(K, ora):
