@@ -569,6 +569,13 @@ NORM_CASES = {
                        rope_theta=1e6, tied=True, qk_norm=1, norm_placement=2, unit_offset=True, activation=1,
                        window=9, window_layers=(0,), local_rope_theta=1e4, embedding_multiplier=8.0,
                        attention_multiplier=0.25, attention_softcap=0.8, logits_softcap=2.0),
+    # Gemma's real head size (256) with one kv head, and Phi-3-mini's (96)
+    "head256": O.Decoder("gemma2", vocab=256, hidden=64, inter=96, layers=2, heads=2, kv_heads=1, head_dim=256,
+                         eps=1e-6, rope_theta=1e4, tied=True, norm_placement=2, unit_offset=True, activation=1,
+                         window=20, window_layers=(0,), embedding_multiplier=8.0, attention_multiplier=0.0625,
+                         attention_softcap=50.0, logits_softcap=30.0),
+    "head96": O.Decoder("phi3", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=4, head_dim=96,
+                        eps=1e-5, rope_theta=1e4, tied=False, window=40),
 }
 
 
