@@ -126,6 +126,9 @@ class Decoder:
     shared_gate: bool = False  # its output times the sigmoid of a [1, hidden] gate (Qwen2-MoE)
 
     def native(self) -> DecoderConfig:
+        # per-layer choices travel as 64-bit masks (layers from 64 on are routed and windowed)
+        if self.layers > 64 and (self.dense_layers or self.window_layers is not None):
+            raise ValueError("dense_layers and window_layers are supported for models of at most 64 layers")
         return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
                              self.head_dim, int(self.attention_bias), self.qk_norm, self.sliding_window,
                              int(self.tie_embeddings), self.experts, self.experts_per_token,
