@@ -128,7 +128,8 @@ int launch_segment_sums(const float* partial, int64_t dim, int nseg, const float
                         hipStream_t stream);
 // The shared expert's gate (backprop.py:339-351, 519-524): forward s = f32(sigmoid(h2 w)), term = f32(y s) (w null:
 // term = y); backward dy = f32(dmlp s), dscore = f32(f32(dot(dmlp, y) s) (1 - s)), then dh += f32(dscore w) (dh
-// non-null) and part[window][k] = the window's f32(sum dscore h2[.][k]) (part non-null).
+// non-null) and part[window][k] = the window's f32(sum dscore h2[.][k]) (part non-null); with dy null, dscore is
+// taken as already formed.
 int launch_shared_gate_forward(const float* h2, const float* w, const float* y, float* s, float* term, int64_t rows,
                                int64_t H, hipStream_t stream);
 int launch_shared_gate_backward(const float* dmlp, const float* y, const float* s, const float* w, const float* h2,

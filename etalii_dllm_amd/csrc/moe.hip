@@ -632,9 +632,11 @@ int launch_shared_gate_backward(const float* dmlp, const float* y, const float* 
                                 int64_t rows, int64_t H, hipStream_t stream) {
     if (rows == 0) return kOk;
     DLLM_REQUIRE(rows < (int64_t{1} << 31), "too many rows for the shared expert's gate");
-    hipLaunchKernelGGL(shared_gate_backward_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, stream, dmlp, y, s,
-                       dy, dscore, H);
-    DLLM_TRY(check_launch("shared gate backward"));
+    if (dy) {  // null: dscore is already formed
+        hipLaunchKernelGGL(shared_gate_backward_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, stream, dmlp,
+                           y, s, dy, dscore, H);
+        DLLM_TRY(check_launch("shared gate backward"));
+    }
     if (dh) {
         const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(rows * H, 256), 16384));
         hipLaunchKernelGGL(shared_gate_dx_kernel, dim3(blocks), dim3(256), 0, stream, dscore, w, dh, rows, H);

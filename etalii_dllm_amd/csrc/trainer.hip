@@ -1602,8 +1602,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(linear_dx(dsh_up, R, L.sup, dsh_x, dsh_x, s));  // dx_gate + dx_up
         DLLM_TRY(launch_moe_combine(dxg, sv.order, sv.slot, nullptr, dsh_x, dh, R, K, H, s));
         if (gated)  // + f32(dscore w), the gate's input gradient
-            DLLM_TRY(launch_shared_gate_backward(dx, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, dsh_dy, dsh_score, dh, seg_d,
-                                                 nseg, nullptr, R, H, s));
+            DLLM_TRY(launch_shared_gate_backward(dx, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, nullptr, dsh_score, dh,
+                                                 seg_d, nseg, nullptr, R, H, s));
         return launch_add(dh, dh2r, dh, R * H, s);
     }
 
