@@ -8,8 +8,8 @@ digests of every gradient, parameter and AdamW moment after each step (tests/gol
 test regenerates the same inputs, runs the same steps on the GPU and compares digests. Equal SHA-256 digests are equal
 bits.
 
-Shapes follow BASELINE's configurations (SmolLM2-135M, Qwen2.5-1.5B, Qwen3-0.6B with LoRA on a Q8_0 base, OLMoE-1B-7B)
-with fewer layers where the full depth only repeats the same launches; the vocabulary, hidden size, heads,
+Shapes follow BASELINE's configurations (SmolLM2-135M, Qwen2.5-1.5B, Qwen3-0.6B with LoRA on a Q8_0 base, OLMoE-1B-7B),
+plus Gemma-2-2B's layer (256-wide heads, soft-caps, sandwich norms, vocabulary 256000), with fewer layers where the full depth only repeats the same launches; the vocabulary, hidden size, heads,
 intermediate sizes, window lengths and expert counts are the real ones, so every size-selected code path of the step
 (matmul grid layouts, the windows-in-sequence tied-embedding dW, the transposes, the window sums, the attention tiles
 at T = 2048, the cross-entropy at vocab 151936, the grouped expert matmuls) runs at the shape it runs at in the bench.
@@ -49,7 +49,14 @@ def _configs() -> dict[str, RealShape]:
     olmoe = O.Decoder("olmoe", vocab=50304, hidden=2048, inter=1024, layers=1, heads=16, kv_heads=16, head_dim=128,
                       eps=1e-5, rope_theta=1e4, tied=False, qk_norm=2, experts=64, topk=8, normalize=False,
                       expert_inter=1024)
+    gemma2 = O.Decoder("gemma2", vocab=256000, hidden=2304, inter=9216, layers=2, heads=8, kv_heads=4, head_dim=256,
+                       eps=1e-6, rope_theta=1e4, tied=True, norm_placement=2, unit_offset=True, activation=1,
+                       window=300, window_layers=(0,), embedding_multiplier=float(np.sqrt(2304.0)),
+                       attention_multiplier=256.0 ** -0.5, attention_softcap=50.0, logits_softcap=30.0)
     return {
+        "gemma2": RealShape("gemma2", gemma2, (513, 257), seed=6,
+                            notes="Gemma-2-2B layer shapes, 2 of 26 layers (one windowed, one global), vocabulary "
+                                  "256000, 256-wide heads, soft-capped scores and logits, windows of 512 and 256"),
         "c1": RealShape("c1", smollm, (257, 257, 257, 257), steps=2, seed=1,
                         notes="SmolLM2-135M, full depth, 4 x 256 tokens, two steps"),
         "c3": RealShape("c3", qwen25, (1025, 1025), seed=3,

@@ -35,7 +35,13 @@ def make_trainer(cfg: R.RealShape):
 
     d = cfg.decoder
     decoder = Decoder(d.vocab, d.hidden, d.inter, d.layers, d.heads, d.kv_heads, d.head_dim, d.eps, d.rope_theta,
-                      d.tied, d.attn_bias, d.qk_norm, d.window, d.experts, d.topk, d.normalize, d.expert_inter)
+                      d.tied, d.attn_bias, d.qk_norm, d.window, d.experts, d.topk, d.normalize, d.expert_inter,
+                      rotary_dim=d.rotary_dim, rope_scaling=d.scaling(), embedding_multiplier=d.embedding_multiplier,
+                      attention_multiplier=d.attention_multiplier, residual_multiplier=d.residual_multiplier,
+                      logits_scaling=d.logits_scaling, dense_layers=d.dense_layers, norm_placement=d.norm_placement,
+                      norm_unit_offset=d.unit_offset, activation=d.activation, window_layers=d.window_layers,
+                      local_rope_theta=d.local_rope_theta, attention_softcap=d.attention_softcap,
+                      logits_softcap=d.logits_softcap, shared_inter=d.shared_inter, shared_gate=d.shared_gate)
     lora = None
     if cfg.lora is not None:
         lora = lora_config(cfg.lora.rank, cfg.lora.alpha, cfg.lora.targets, cfg.lora.rslora, cfg.base_quantize)
