@@ -9,8 +9,8 @@ test regenerates the same inputs, runs the same steps on the GPU and compares di
 bits.
 
 Shapes follow BASELINE's configurations (SmolLM2-135M, Qwen2.5-1.5B, Qwen3-0.6B with LoRA on a Q8_0 base, OLMoE-1B-7B),
-plus Gemma-2-2B's layer (256-wide heads, soft-caps, sandwich norms, vocabulary 256000) and Qwen1.5-MoE-A2.7B's (60
-experts and a gated shared expert), with fewer layers where the full depth only repeats the same launches; the vocabulary, hidden size, heads,
+plus Gemma-2-2B's layer (256-wide heads, soft-caps, sandwich norms, vocabulary 256000) Qwen1.5-MoE-A2.7B's (60
+experts and a gated shared expert) and OLMo-2-1B's (post norms), with fewer layers where the full depth only repeats the same launches; the vocabulary, hidden size, heads,
 intermediate sizes, window lengths and expert counts are the real ones, so every size-selected code path of the step
 (matmul grid layouts, the windows-in-sequence tied-embedding dW, the transposes, the window sums, the attention tiles
 at T = 2048, the cross-entropy at vocab 151936, the grouped expert matmuls) runs at the shape it runs at in the bench.
@@ -57,7 +57,12 @@ def _configs() -> dict[str, RealShape]:
     qwen2_moe = O.Decoder("qwen2_moe", vocab=151936, hidden=2048, inter=5632, layers=1, heads=16, kv_heads=16,
                           head_dim=128, eps=1e-6, rope_theta=1e6, tied=False, attn_bias=True, experts=60, topk=4,
                           normalize=False, expert_inter=1408, shared_inter=5632, shared_gate=True)
+    olmo2 = O.Decoder("olmo2", vocab=100352, hidden=2048, inter=8192, layers=2, heads=16, kv_heads=16, head_dim=128,
+                      eps=1e-6, rope_theta=5e5, tied=False, qk_norm=2, norm_placement=1)
     return {
+        "olmo2": RealShape("olmo2", olmo2, (1025, 257), seed=8,
+                           notes="OLMo-2-1B layer shapes, 2 of 16 layers, post norms and whole-projection QK-norm, "
+                                 "windows of 1024 and 256"),
         "qwen2_moe": RealShape("qwen2_moe", qwen2_moe, (513, 257), router_aux_loss=0.001, seed=7,
                                notes="Qwen1.5-MoE-A2.7B layer shapes, 1 of 24 layers, 60 experts top 4 with the gated "
                                      "shared expert of 5632, windows of 512 and 256, router_aux_loss 0.001"),
