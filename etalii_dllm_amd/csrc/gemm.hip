@@ -170,6 +170,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                 if (j >= p.J) continue;
                 float r = static_cast<float>(acc[q][c]);
                 if (p.seg_addrow) r = r + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j] : 0.0f);
+                if (p.seg_rowscale) r = r * p.seg_rowscale[i];  // the window's gradient unfolded
+                if (p.seg_weight) r = r * p.seg_weight[s];      // the window's whole gradient times its factor
                 float* out = p.C + i * p.ldc + j;
                 *out = s == 0 ? r : *out + r;
             }
@@ -435,6 +437,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                 if (j0 + c >= p.J) continue;
                 float r = static_cast<float>(acc[q][c]);
                 if (p.seg_addrow) r = r + (arow >= 0 ? p.seg_addend[arow * p.ld_seg_add + j0 + c] : 0.0f);
+                if (p.seg_rowscale) r = r * p.seg_rowscale[i];
+                if (p.seg_weight) r = r * p.seg_weight[s];
                 out[c] = (kMode == kWindowsInParallel || s == 0) ? r : out[c] + r;
             }
         }
@@ -1003,6 +1007,14 @@ int64_t padded_rows(int64_t n) { return static_cast<int64_t>(round_up(static_cas
 
 namespace {
 
+// Whether a float-A call fits the matrix-core kernel's 16-byte staging (the conditions launch_gemm requires).
+bool mfma_shape(const GemmCall& g) {
+    const bool vec = g.J % 4 == 0 && g.ldb % 4 == 0 && reinterpret_cast<uintptr_t>(g.B) % 16 == 0;
+    if (!vec || g.lda % 4 != 0 || reinterpret_cast<uintptr_t>(g.Af) % 16 != 0) return false;
+    if (g.a_kind == kAFloatRows) return g.I % 4 == 0 && g.lda >= g.I;
+    return g.seg == nullptr && g.l0 == 0 && g.l1 % 4 == 0 && g.l1 >= 4 && g.lda >= g.l1;
+}
+
 GemmParams params_of(const GemmCall& g) {
     return GemmParams{g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.I, g.J, g.l0, g.l1, g.seg, g.nseg, g.bias, g.addsrc,
                       g.ld_add, g.seg_addend, g.seg_addrow, g.ld_seg_add, nullptr, g.Af, g.seg_weight,
@@ -1010,6 +1022,8 @@ GemmParams params_of(const GemmCall& g) {
 }
 
 }  // namespace
+
+bool gemm_mfma_shape(const GemmCall& g) { return g.a_kind != kADouble && mfma_shape(g); }
 
 // The table: GemmParams[capacity], then the tile starts (capacity + 1), then the first tile of each XCD's range (9).
 size_t gemm_group_bytes(int n) {
@@ -1133,10 +1147,27 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     DLLM_REQUIRE(g.I >= 0 && g.J >= 0, "negative matmul size");
     DLLM_REQUIRE(g.seg == nullptr || g.nseg >= 1, "segmented matmul needs at least one segment");
     DLLM_REQUIRE(g.seg != nullptr || g.seg_addrow == nullptr, "per-window addends need segments");
-    DLLM_REQUIRE(g.seg_rowscale == nullptr || (g.seg != nullptr && g.a_kind == kAFloatRows),
-                 "per-row factors are for windowed weight gradients with float A rows");
-    DLLM_REQUIRE(g.seg_weight == nullptr || (g.seg != nullptr && g.a_kind == kAFloatRows),
-                 "per-window factors are for windowed weight gradients with float A rows");
+    DLLM_REQUIRE(g.seg_rowscale == nullptr || g.seg != nullptr, "per-row factors are for windowed weight gradients");
+    DLLM_REQUIRE(g.seg_weight == nullptr || g.seg != nullptr, "per-window factors are for windowed weight gradients");
+    if (g.a_kind != kADouble && g.a_scratch != nullptr && !mfma_shape(g)) {
+        // Float A in a shape the matrix-core kernel cannot stage (a size or a row stride that is not a whole number
+        // of 16-byte chunks): A is widened into the caller's double scratch ([l][i], rows padded to whole tiles) and
+        // the VALU kernels run the same per-output chain over l ascending, so the bits are those of any other path.
+        if (g.I == 0 || g.J == 0) return kOk;
+        const int64_t ld = padded_rows(g.I), L = g.l1;
+        DLLM_REQUIRE(L >= 0 && L * ld <= g.a_scratch_cap, "matmul scratch too small for the widened operand");
+        GemmCall d = g;
+        if (g.a_kind == kAFloatRows)
+            DLLM_TRY(launch_to_double(g.Af, L, g.I, g.lda, g.a_scratch, ld, nullptr, 0, stream));
+        else
+            DLLM_TRY(launch_to_double(g.Af, g.I, L, g.lda, nullptr, 0, g.a_scratch, ld, stream));
+        d.a_kind = kADouble;
+        d.A = g.a_scratch;
+        d.lda = ld;
+        d.Af = nullptr;
+        d.a_scratch = nullptr;
+        return launch_gemm(d, stream);
+    }
     const int ak = g.a_kind;
     DLLM_REQUIRE(ak == kADouble || ak == kAFloatRows || ak == kAFloatT, "unknown A operand kind");
     if (ak == kADouble) DLLM_REQUIRE(g.lda >= padded_rows(g.I), "the double operand must be padded to whole row tiles");

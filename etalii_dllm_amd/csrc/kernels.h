@@ -40,7 +40,13 @@ struct GemmCall {
     // segmented, float A rows: optional per-row float factors (device, I): row i of each window's result times
     // rowscale[i], before the window factor (the RoPE attention factor's unfold of a window's gradient)
     const float* seg_rowscale = nullptr;
+    // float A in a shape the matrix-core kernel cannot stage: when given, A is widened into this double scratch
+    // (a_scratch_cap doubles, at least l1 x padded_rows(I)) and the call runs on the VALU kernels with the same bits
+    double* a_scratch = nullptr;
+    int64_t a_scratch_cap = 0;
 };
+// Whether a float-A call runs on the matrix-core kernel (every operand row a whole number of 16-byte chunks).
+bool gemm_mfma_shape(const GemmCall& g);
 
 int launch_gemm(const GemmCall& g, hipStream_t stream);
 

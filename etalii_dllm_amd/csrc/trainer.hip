@@ -189,6 +189,8 @@ struct dllm_hip_trainer {
         // the layer's expert matmuls, one grouped launch per kind (tables in device memory, made by group_rows)
         GemmGroup groups[9];
         double group_flops[9] = {};
+        // a kind whose matmuls the grouped kernel cannot stage (sizes not whole 16-byte chunks): one launch each
+        std::vector<GemmCall> loose[9];
         char* tables = nullptr;
     };
     enum ExpertMatmul { kFwdGate, kFwdUp, kFwdDown, kDxDown, kDwDown, kDxGate, kDwGate, kDxUp, kDwUp, kExpertMatmuls };
@@ -227,6 +229,14 @@ struct dllm_hip_trainer {
     int* err_flag = nullptr;
     std::vector<int64_t> seg_host;
     bool wt_valid = false;
+    // per-layer choices (dense_layers, full_attention_layers): from the config's flag arrays, or its 64-bit masks
+    std::vector<char> dense_flag, full_flag;
+    // Model sizes that are not whole 16-byte chunks (a vocabulary of 50257, an intermediate size of 30): the matmuls
+    // whose operands cannot be staged by the matrix-core kernel widen their A operand into this double scratch and
+    // run on the VALU kernels (same per-output chains, same bits). One scratch, so such steps keep to one stream.
+    bool odd_shapes = false;
+    double* mm_scratch = nullptr;
+    int64_t mm_scratch_cap = 0;
 
     // What AdamW updates: parameters, gradients and moments of one set of tensors in one arena each, the chunk table
     // of the fused update and the plan of the exact global norm (optimizer.py:66-109).
@@ -309,7 +319,7 @@ struct dllm_hip_trainer {
 
     // Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346): every
     // layer of a model with experts except those in dense_layers.
-    bool sparse(int64_t l) const { return E > 0 && !(l < 64 && ((c.dense_layers >> l) & 1)); }
+    bool sparse(int64_t l) const { return E > 0 && !dense_flag[static_cast<size_t>(l)]; }
     // Norm placement (architecture.py:315-320): pre (each block's input), post (its output; OLMo 2) or both.
     bool pre_norms() const { return c.norm_placement != 1; }
     int uo() const { return c.norm_unit_offset ? 1 : 0; }  // norms with 1 + w (Gemma)
@@ -317,7 +327,7 @@ struct dllm_hip_trainer {
     // TransformerConfig.window (architecture.py:353-359): the sliding window of layer l, 0 for full attention
     int64_t layer_window(int64_t l) const {
         if (c.sliding_window == 0) return 0;
-        return l < 64 && ((c.full_attention_layers >> l) & 1) ? 0 : c.sliding_window;
+        return full_flag[static_cast<size_t>(l)] ? 0 : c.sliding_window;
     }
     // The RoPE tables of layer l (uses_local_rope, architecture.py:322-324)
     bool local_rope(int64_t l) const { return c.local_rope_theta != 0.0 && layer_window(l) != 0; }
@@ -622,6 +632,21 @@ struct dllm_hip_trainer {
         const int64_t hd = c.head_dim, G = heads / kvh;
         DLLM_TRY(make(&attn_qt, W_max * heads * hd * Tp));
         DLLM_TRY(make(&attn_dot, W_max * heads * hd * Tp));
+        {
+            // the saved attention numerators, and with soft-capped scores their 1 - tanh^2 factors: layers x windows x
+            // heads x Tp^2 doubles each (quadratic in the window length), refused up front with the formula rather
+            // than failing in the allocator
+            const double saved_bytes = static_cast<double>(c.layers) * W_max * heads * Tp * Tp * 8.0 *
+                                       (c.attention_softcap != 0.0 ? 2.0 : 1.0);
+            size_t free_bytes = 0, total_bytes = 0;
+            DLLM_TRY(check_hip(hipMemGetInfo(&free_bytes, &total_bytes), "hipMemGetInfo"));
+            if (saved_bytes > static_cast<double>(free_bytes))
+                return fail(kOutOfMemory,
+                            "the saved attention scores need layers x max_windows x heads x Tp^2 x 8 bytes (Tp = "
+                            "max_window_tokens rounded up to 64; twice that with attention_softcap): " +
+                                std::to_string(saved_bytes / 1e9) + " GB, more than the " +
+                                std::to_string(static_cast<double>(free_bytes) / 1e9) + " GB free");
+        }
         DLLM_TRY(make(&attn_et, c.layers * W_max * heads * Tp * Tp));  // E^T saved per layer for the backward
         // soft-capped scores: the backward's factor 1 - tanh^2 of every score, saved per layer
         if (c.attention_softcap != 0.0) DLLM_TRY(make(&attn_slope, c.layers * W_max * heads * Tp * Tp));
@@ -658,6 +683,15 @@ struct dllm_hip_trainer {
             DLLM_TRY(launch_rope_tables(nullptr, T_max, inv_local, c.rotary_dim / 2, cos_local, sin_local, nullptr));
         }
         if (c.logits_softcap != 0.0) DLLM_TRY(make(&logits_capped, R * V));
+        // the matmul scratch of sizes that are not whole 16-byte chunks: the widest A operand is [l][i] with
+        // l x i = (a model size) x (the rows) either way round, i padded to whole row tiles
+        const int64_t SI = c.shared_inter;
+        for (int64_t d : {V, H, I, EI, E, SI}) odd_shapes = odd_shapes || d % 4 != 0;
+        if (odd_shapes) {
+            const int64_t widest = std::max<int64_t>({V, H, QD, KVD, I, EI, E, SI});
+            mm_scratch_cap = std::max(widest * padded_rows(R), R * padded_rows(widest));
+            DLLM_TRY(make(&mm_scratch, static_cast<size_t>(mm_scratch_cap)));
+        }
         return check_hip(hipDeviceSynchronize(), "trainer setup");
     }
 
@@ -969,7 +1003,7 @@ struct dllm_hip_trainer {
                 }
                 bool ok = true;
                 for (int i = 0; i < nc; ++i)
-                    ok = ok && calls[i].J % 4 == 0 && calls[i].ldb % 4 == 0 && calls[i].a_kind == calls[0].a_kind;
+                    ok = ok && gemm_mfma_shape(calls[i]) && calls[i].a_kind == calls[0].a_kind;
                 GemmGroup& g = grp[static_cast<size_t>(l * kLayerGroups + k)];
                 const size_t gi = static_cast<size_t>(l * kLayerGroups + k);
                 if (ok) DLLM_TRY(gemm_group_prepare(calls, nc, kGroupCap, host.data() + gb * gi, &g));
@@ -1023,6 +1057,8 @@ struct dllm_hip_trainer {
         g.bias = bias;
         g.addsrc = addsrc;
         g.ld_add = N;
+        g.a_scratch = mm_scratch;
+        g.a_scratch_cap = mm_scratch_cap;
         return g;
     }
 
@@ -1047,6 +1083,8 @@ struct dllm_hip_trainer {
         g.l1 = t.rows;
         g.addsrc = addsrc;
         g.ld_add = t.cols;
+        g.a_scratch = mm_scratch;
+        g.a_scratch_cap = mm_scratch_cap;
         return g;
     }
 
@@ -1083,6 +1121,8 @@ struct dllm_hip_trainer {
         g.seg_partial = gemm_part;
         g.seg_partial_cap = gemm_part_cap;
         g.seg_weight = window_weights();
+        g.a_scratch = mm_scratch;
+        g.a_scratch_cap = mm_scratch_cap;
         return g;
     }
 
@@ -1507,7 +1547,14 @@ struct dllm_hip_trainer {
             GemmGroup& grp = sv.groups[kind];
             grp = GemmGroup{};
             sv.group_flops[kind] = 0.0;
+            sv.loose[kind].clear();
             if (calls.empty()) continue;
+            bool grouped = true;
+            for (const GemmCall& g : calls) grouped = grouped && gemm_mfma_shape(g);
+            if (!grouped) {
+                sv.loose[kind] = calls;
+                continue;
+            }
             DLLM_TRY(gemm_group_prepare(calls.data(), static_cast<int>(calls.size()), static_cast<int>(E),
                                         out->data() + kind * gb, &grp));
             for (const GemmCall& g : calls) sv.group_flops[kind] += flops_of(g);
@@ -1516,6 +1563,10 @@ struct dllm_hip_trainer {
     }
 
     int expert_matmul(const Saved& sv, int kind, hipStream_t s) {
+        if (!sv.loose[kind].empty()) {
+            for (const GemmCall& g : sv.loose[kind]) DLLM_TRY(gemm(g, s));
+            return kOk;
+        }
         const size_t gb = gemm_group_bytes(static_cast<int>(E));
         return gemm_group(sv.groups[kind], sv.tables + kind * gb, sv.group_flops[kind], s);
     }
@@ -1736,7 +1787,8 @@ struct dllm_hip_trainer {
         DLLM_TRY(norm_dw(dhidden, x_final, inv_rms, H, 1, nseg, G(final_norm), s));
         for (bool& pending : side_pending) pending = false;
         side_on = false;
-        if (!profiling && !post_norms()) {  // the post norms' buffers are ordered by the one stream
+        if (!profiling && !post_norms() && !odd_shapes) {  // the post norms' buffers (and the matmul scratch) are
+                                                              // ordered by the one stream
             DLLM_TRY(side_setup());
             side_on = true;
         }
@@ -2122,36 +2174,45 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
     if (c.experts > 0) {
         DLLM_REQUIRE(c.experts_per_token >= 1 && c.experts_per_token <= c.experts,
                      "experts per token must be between 1 and the number of experts");
-        DLLM_REQUIRE(c.experts % 4 == 0 && ei % 4 == 0,
-                     "the number of experts and the expert intermediate size must be multiples of 4");
+        DLLM_REQUIRE(ei > 0, "the expert intermediate size must be positive");
     }
     DLLM_REQUIRE(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, "heads must be a multiple of kv_heads");
     DLLM_REQUIRE(c.rotary_dim > 0 && c.rotary_dim % 2 == 0 && c.rotary_dim <= c.head_dim, "invalid rotary_dim");
-    DLLM_REQUIRE(c.head_dim % 4 == 0, "head_dim must be a multiple of 4");
-    DLLM_REQUIRE(c.vocab % 4 == 0 && c.hidden % 4 == 0 && c.intermediate % 4 == 0,
-                 "vocabulary, hidden and intermediate sizes must be multiples of 4 (16-byte matmul operand chunks)");
+    DLLM_REQUIRE(c.head_dim % 4 == 0, "head_dim must be a multiple of 4 (the attention tiles' 16-byte operand rows)");
+    DLLM_REQUIRE(c.vocab > 0 && c.hidden > 0 && c.intermediate > 0 && c.layers > 0, "sizes must be positive");
     DLLM_REQUIRE(max_tokens > 0 && max_windows > 0 && max_window_tokens > 0, "capacities must be positive");
-    DLLM_REQUIRE(max_tokens <= 65535, "at most 65535 tokens per step");
+    // the attention chains run one workgroup row per (window, head) in the grid's second dimension
+    DLLM_REQUIRE(max_windows * c.heads <= 65535, "at most 65535 (window, head) pairs per step");
     for (double m : {c.embedding_multiplier, c.residual_multiplier, c.logits_scaling})
         DLLM_REQUIRE(m >= 0.0 && std::isfinite(m), "multipliers must be finite and non-negative (0: none)");
     DLLM_REQUIRE(c.attention_scale > 0.0 && std::isfinite(c.attention_scale), "attention_scale must be positive");
     DLLM_REQUIRE(c.norm_placement >= 0 && c.norm_placement <= 2, "norm_placement must be 0 (pre), 1 (post) or 2 (both)");
     DLLM_REQUIRE(c.norm_placement == 0 || c.experts == 0, "post norms are built for dense MLPs only");
-    DLLM_REQUIRE(c.shared_inter >= 0 && c.shared_inter % 4 == 0, "the shared expert's size must be a multiple of 4");
+    DLLM_REQUIRE(c.shared_inter >= 0, "the shared expert's size must not be negative");
     DLLM_REQUIRE(c.shared_inter == 0 || c.experts > 0, "a shared expert needs routed experts");
     DLLM_REQUIRE(c.shared_gate == 0 || c.shared_inter > 0, "a shared expert gate needs a shared expert");
     DLLM_REQUIRE(c.activation == 0 || c.activation == 1, "activation must be 0 (silu) or 1 (gelu_tanh)");
     DLLM_REQUIRE(c.local_rope_theta >= 0.0 && c.attention_softcap >= 0.0 && c.logits_softcap >= 0.0,
                  "local_rope_theta and the soft-caps must be non-negative (0: none)");
+    std::vector<char> dense(static_cast<size_t>(c.layers)), full(static_cast<size_t>(c.layers));
+    for (int64_t l = 0; l < c.layers; ++l) {
+        dense[static_cast<size_t>(l)] = c.dense_layer_flags ? c.dense_layer_flags[l] != 0
+                                                            : l < 64 && ((c.dense_layers >> l) & 1);
+        full[static_cast<size_t>(l)] = c.full_attention_layer_flags ? c.full_attention_layer_flags[l] != 0
+                                                                    : l < 64 && ((c.full_attention_layers >> l) & 1);
+    }
     if (c.experts > 0) {
         bool any_sparse = false;
-        for (int64_t l = 0; l < c.layers; ++l) any_sparse = any_sparse || l >= 64 || !((c.dense_layers >> l) & 1);
+        for (char d : dense) any_sparse = any_sparse || !d;
         DLLM_REQUIRE(any_sparse, "a model with experts needs at least one sparse layer");
     } else {
-        DLLM_REQUIRE(c.dense_layers == 0, "dense_layers needs experts");
+        for (char d : dense) DLLM_REQUIRE(!d, "dense_layers needs experts");
     }
     std::unique_ptr<dllm_hip_trainer> t(new dllm_hip_trainer());
     t->c = c;
+    t->c.dense_layer_flags = t->c.full_attention_layer_flags = nullptr;  // the caller's arrays are not kept
+    t->dense_flag = dense;
+    t->full_flag = full;
     for (double* m : {&t->c.embedding_multiplier, &t->c.residual_multiplier, &t->c.logits_scaling})
         if (*m == 0.0) *m = 1.0;  // unset
     t->R_max = max_tokens;

@@ -30,7 +30,8 @@ class DecoderConfig(C.Structure):
         ("dense_layers", C.c_int64), ("norm_placement", C.c_int64), ("norm_unit_offset", C.c_int64),
         ("activation", C.c_int64), ("full_attention_layers", C.c_int64), ("local_rope_theta", C.c_double),
         ("attention_softcap", C.c_double), ("logits_softcap", C.c_double), ("shared_inter", C.c_int64),
-        ("shared_gate", C.c_int64)]
+        ("shared_gate", C.c_int64), ("dense_layer_flags", C.POINTER(C.c_uint8)),
+        ("full_attention_layer_flags", C.POINTER(C.c_uint8))]
 
 
 class AdamWArgs(C.Structure):
@@ -126,22 +127,28 @@ class Decoder:
     shared_gate: bool = False  # its output times the sigmoid of a [1, hidden] gate (Qwen2-MoE)
 
     def native(self) -> DecoderConfig:
-        # per-layer choices travel as 64-bit masks (layers from 64 on are routed and windowed)
-        if self.layers > 64 and (self.dense_layers or self.window_layers is not None):
-            raise ValueError("dense_layers and window_layers are supported for models of at most 64 layers")
-        return DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
+        # architecture.py:237-254 rejects layer indices outside the model
+        if any(not 0 <= layer < self.layers for layer in self.dense_layers):
+            raise ValueError("dense_layers must be layer indices")
+        if self.window_layers is not None and any(not 0 <= layer < self.layers for layer in self.window_layers):
+            raise ValueError("sliding_window_layers must be layer indices")
+        # per-layer choices travel as one byte per layer (any depth); the 64-bit masks stay zero
+        dense = (C.c_uint8 * self.layers)(*[int(layer in self.dense_layers) for layer in range(self.layers)])
+        full = (C.c_uint8 * self.layers)(*[int(self.window_layers is not None and layer not in self.window_layers)
+                                           for layer in range(self.layers)])
+        cfg = DecoderConfig(self.vocab, self.hidden, self.intermediate, self.layers, self.heads, self.kv_heads,
                              self.head_dim, int(self.attention_bias), self.qk_norm, self.sliding_window,
                              int(self.tie_embeddings), self.experts, self.experts_per_token,
                              int(self.normalize_expert_weights), self.expert_intermediate,
                              self.rotary_dim or self.head_dim, self.rms_norm_eps, self.rope_theta,
                              1.0 / float(np.sqrt(np.float64(self.head_dim))) if self.attention_multiplier is None
                              else self.attention_multiplier, self.embedding_multiplier, self.residual_multiplier,
-                             self.logits_scaling, sum(1 << layer for layer in self.dense_layers if layer < 64),
-                             self.norm_placement, int(self.norm_unit_offset), self.activation,
-                             0 if self.window_layers is None else
-                             sum(1 << i for i in range(min(self.layers, 64)) if i not in self.window_layers),
-                             self.local_rope_theta or 0.0, self.attention_softcap or 0.0, self.logits_softcap or 0.0,
-                             self.shared_inter, int(self.shared_gate))
+                             self.logits_scaling, 0, self.norm_placement, int(self.norm_unit_offset),
+                             self.activation, 0, self.local_rope_theta or 0.0, self.attention_softcap or 0.0,
+                             self.logits_softcap or 0.0, self.shared_inter, int(self.shared_gate),
+                             C.cast(dense, C.POINTER(C.c_uint8)), C.cast(full, C.POINTER(C.c_uint8)))
+        cfg._flags = (dense, full)  # kept alive with the structure until the trainer has read them
+        return cfg
 
 
 def _windows(windows):

@@ -157,8 +157,8 @@ int dllm_hip_sum_squares(const float* values, size_t n, double* result, void* wo
 
 /* sum_squares without a workspace and without any allocation: the same bits as dllm_hip_sum_squares, its scratch
  * (plan, block sums, block functions, result) in a fixed 4 MiB device array that each GPU holds until the process
- * ends. n is at most 2^29 (larger is an invalid argument, refused before any launch). Calls that overlap on one GPU
- * race on that array. No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * ends. n is at most 2^29 (larger is an invalid argument, refused before any launch). Calls on one GPU are
+ * serialised on that array (a per-GPU lock held until the call's stream has finished). No counterpart in the reference: it is for callers that cannot allocate device memory (code
  * under graph capture, tight serving loops, harnesses that forbid hipMalloc). Waits for the stream. */
 int dllm_hip_sum_squares_noalloc(const float* values, size_t n, double* result, void* stream);
 
@@ -286,7 +286,8 @@ typedef struct {
      * (backprop.py:174-181). Granite's attention_multiplier is attention_scale. */
     double embedding_multiplier, residual_multiplier, logits_scaling;
     /* dense_layers (architecture.py:128, 344-346; Qwen3-MoE's mlp_only_layers): bit l set = layer l keeps a dense
-     * MLP of `intermediate` in a model with experts; layers from 64 on are routed */
+     * MLP of `intermediate` in a model with experts; layers from 64 on are routed (dense_layer_flags below reaches
+     * any depth) */
     int64_t dense_layers;
     /* norm_placement (architecture.py:315-320): 0 pre (RMSNorm on each block's input), 1 post (on each block's
      * output before the residual add, OLMo 2), 2 both; post norms with routed experts are not built */
@@ -298,10 +299,15 @@ typedef struct {
     int64_t norm_unit_offset, activation, full_attention_layers;
     double local_rope_theta, attention_softcap, logits_softcap;
     /* A shared expert in every routed layer (architecture.py shared_expert_intermediate_size, shared_expert_gate;
-     * backprop.py:308-357, 501-527): shared_inter (0: none, else a multiple of 4) is its SwiGLU size; every row goes
+     * backprop.py:308-357, 501-527): shared_inter (0: none) is its SwiGLU size; every row goes
      * through it, and with shared_gate its output is multiplied by the sigmoid of a [1, hidden] gate's score (Qwen2-MoE);
      * its output is added after the routed experts'. */
     int64_t shared_inter, shared_gate;
+    /* Per-layer choices for models of any depth (NULL: the masks above, which reach layers 0-63 only): `layers`
+     * bytes each, nonzero = layer l keeps a dense MLP (dense_layers) / ignores sliding_window (full attention).
+     * Read at creation only. */
+    const uint8_t* dense_layer_flags;
+    const uint8_t* full_attention_layer_flags;
 } dllm_hip_decoder_config;
 
 typedef struct dllm_hip_trainer dllm_hip_trainer;

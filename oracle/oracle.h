@@ -182,6 +182,9 @@ typedef struct {
      * 501-527): a SwiGLU expert every row of a sparse layer goes through, its output times the sigmoid of a [1, hidden]
      * gate's score when gated (Qwen2-MoE), added after the routed experts */
     int64_t shared_inter, shared_gate;
+    /* per-layer choices for any depth (NULL: the masks above): `layers` bytes, nonzero = dense MLP / full attention */
+    const uint8_t* dense_layer_flags;
+    const uint8_t* full_attention_layer_flags;
 } orc_config;
 
 /* Whether layer l's MLP is a mixture of experts (TransformerConfig.is_sparse, architecture.py:344-346). */

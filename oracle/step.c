@@ -25,7 +25,9 @@ static int has_pre_norms(const orc_config* c) { return c->norm_placement != 1; }
 static int has_post_norms(const orc_config* c) { return c->norm_placement != 0; }
 
 int orc_is_sparse(const orc_config* c, int64_t layer) {
-    return c->experts > 0 && !(layer < 64 && ((c->dense_layers >> layer) & 1));
+    if (c->experts <= 0) return 0;
+    if (c->dense_layer_flags) return !c->dense_layer_flags[layer];
+    return !(layer < 64 && ((c->dense_layers >> layer) & 1));
 }
 
 /* Shapes of architecture.py:418-468 for the decoder families a step here covers. */
@@ -168,6 +170,7 @@ typedef struct {
 /* TransformerConfig.window (architecture.py:353-359): the layer's window, 0 for full causal attention. */
 static int64_t layer_window(const orc_config* c, int64_t layer) {
     if (c->window == 0) return 0;
+    if (c->full_attention_layer_flags) return c->full_attention_layer_flags[layer] ? 0 : c->window;
     return layer < 64 && ((c->full_attention_layers >> layer) & 1) ? 0 : c->window;
 }
 

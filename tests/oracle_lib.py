@@ -36,7 +36,8 @@ class OrcConfig(C.Structure):
         ("residual_multiplier", C.c_double), ("logits_scaling", C.c_double), ("dense_layers", C.c_int64),
         ("norm_placement", C.c_int64), ("norm_unit_offset", C.c_int64), ("activation", C.c_int64),
         ("full_attention_layers", C.c_int64), ("local_rope_theta", C.c_double), ("attention_softcap", C.c_double),
-        ("logits_softcap", C.c_double), ("shared_inter", C.c_int64), ("shared_gate", C.c_int64)]
+        ("logits_softcap", C.c_double), ("shared_inter", C.c_int64), ("shared_gate", C.c_int64),
+        ("dense_layer_flags", C.c_void_p), ("full_attention_layer_flags", C.c_void_p)]
 
 
 class OrcRopeScaling(C.Structure):
@@ -414,10 +415,17 @@ class Decoder:
                         int(self.normalize), self.expert_inter or self.inter, self.rotary_dim or self.head_dim,
                         self.eps, self.rope_theta, self.attention_scale, None, self.rope_attention_factor,
                         self.embedding_multiplier, self.residual_multiplier, self.logits_scaling,
-                        sum(1 << layer for layer in self.dense_layers), self.norm_placement, int(self.unit_offset),
-                        self.activation, self.full_attention_mask(), self.local_rope_theta or 0.0,
-                        self.attention_softcap or 0.0, self.logits_softcap or 0.0, self.shared_inter,
-                        int(self.shared_gate))
+                        0, self.norm_placement, int(self.unit_offset), self.activation, 0,
+                        self.local_rope_theta or 0.0, self.attention_softcap or 0.0, self.logits_softcap or 0.0,
+                        self.shared_inter, int(self.shared_gate))
+        # per-layer flags (any depth) instead of the 64-bit masks
+        flags = np.zeros((2, max(self.layers, 1)), dtype=np.uint8)
+        for layer in range(self.layers):
+            flags[0, layer] = layer in self.dense_layers
+            flags[1, layer] = self.window_layers is not None and layer not in self.window_layers
+        cfg.dense_layer_flags = flags[0].ctypes.data
+        cfg.full_attention_layer_flags = flags[1].ctypes.data
+        cfg._flags = flags
         inv_freq = self.inv_freq
         if inv_freq is None and self.rope_scaling:
             inv_freq = rope_inv_freq_scaled(self.rotary_dim or self.head_dim, self.rope_theta, self.scaling())

@@ -65,7 +65,7 @@ def test_natural_tensor_order_and_names_match_the_oracle_layout():
                                      "layers.2.attention.q.weight", "layers.10.mlp.up.weight",
                                      "token_embedding.weight"]
     assert trainer.DecoderConfig  # the structure is defined and matches the header's field count
-    assert len(trainer.DecoderConfig._fields_) == 32
+    assert len(trainer.DecoderConfig._fields_) == 34
 
 
 @needs_library
@@ -103,3 +103,23 @@ def test_library_random_inputs_match_the_oracle_and_the_reference_goldens():
             ref = np.empty(n, np.float32)
             O.ref().ref_fill_gaussian(ctypes.c_uint64(seed), ref.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(n))
             assert ref.tobytes() == want.tobytes()
+
+
+@needs_library
+def test_layer_indices_outside_the_model_are_refused():
+    """architecture.py:237-254 raises ValueError for dense_layers / sliding_window_layers outside the model; so does
+    the trainer's configuration, and indices past 63 travel as per-layer flags."""
+    from etalii_dllm_amd.trainer import Decoder
+
+    base = dict(vocab=64, hidden=16, intermediate=24, layers=66, heads=2, kv_heads=1, head_dim=8, rms_norm_eps=1e-6,
+                rope_theta=1e6, tie_embeddings=True, sliding_window=4, experts=4, experts_per_token=2)
+    with pytest.raises(ValueError, match="dense_layers must be layer indices"):
+        Decoder(**base, dense_layers=(66,)).native()
+    with pytest.raises(ValueError, match="dense_layers must be layer indices"):
+        Decoder(**base, dense_layers=(-1,)).native()
+    with pytest.raises(ValueError, match="sliding_window_layers must be layer indices"):
+        Decoder(**base, window_layers=(0, 70)).native()
+    cfg = Decoder(**base, dense_layers=(1, 65), window_layers=(0, 64)).native()
+    assert [cfg.dense_layer_flags[i] for i in range(66)] == [int(i in (1, 65)) for i in range(66)]
+    assert [cfg.full_attention_layer_flags[i] for i in range(66)] == [int(i not in (0, 64)) for i in range(66)]
+    assert cfg.dense_layers == 0 and cfg.full_attention_layers == 0
