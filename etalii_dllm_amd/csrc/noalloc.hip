@@ -4,8 +4,10 @@
 //
 // Each GPU holds its own copy of `scratch` at its own address, found once per device with hipGetSymbolAddress and
 // kept in g_scratch[device]; host code only ever passes that address, never the array's name (on the host the name
-// is a stand-in, not a device address). Every call on one GPU shares that GPU's array: calls that overlap on one GPU
-// (two host threads, or two streams) race.
+// is a stand-in, not a device address). Every call on one GPU shares that GPU's array, so the calls on one GPU are
+// serialised: each holds that GPU's call lock from its first launch until its stream has finished the result (the
+// call waits for its stream before returning anyway), and calls from two host threads or on two streams never
+// overlap on the array.
 #include <mutex>
 
 #include "common.h"
@@ -43,9 +45,10 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_lock;
 char* g_scratch[kMaxDevices] = {};
+std::mutex g_call[kMaxDevices];  // one call at a time per GPU on its scratch array
 
 // The device address of this GPU's scratch array (looked up on the first call with the device current).
-int device_scratch(char** out) {
+int device_scratch(char** out, int* device_out) {
     int device = 0;
     DLLM_TRY(check_hip(hipGetDevice(&device), "hipGetDevice"));
     DLLM_REQUIRE(device >= 0 && device < kMaxDevices, "sum_squares_noalloc supports devices 0..63");
@@ -56,6 +59,7 @@ int device_scratch(char** out) {
         g_scratch[device] = static_cast<char*>(p);
     }
     *out = g_scratch[device];
+    *device_out = device;
     return kOk;
 }
 
@@ -85,7 +89,9 @@ extern "C" int dllm_hip_sum_squares_noalloc(const float* values, size_t n, doubl
     const size_t blocks = n > 0 ? ceil_div(n, kBlockElems) : 1;
     DLLM_REQUIRE(scratch_layout(blocks) <= kScratchBytes, "sum_squares_noalloc scratch layout overflow");
     char* base = nullptr;
-    DLLM_TRY(device_scratch(&base));
+    int device = 0;
+    DLLM_TRY(device_scratch(&base, &device));
+    std::lock_guard<std::mutex> call(g_call[device]);  // until this call's stream has finished with the array
     Carve c(base, kScratchBytes);
     int64_t* d_head = c.take<int64_t>(2);
     int64_t* d_table = c.take<int64_t>(2 * blocks);
