@@ -544,11 +544,21 @@ __device__ __forceinline__ void missue_stage(const GemmParams& p, MStage<kA, kBI
 
 // Steady-state copies: a stage whose rows all lie inside the segment needs no clamping along l, so each copy is a
 // wave-uniform base (SGPRs, advanced per stage by scalar adds) plus this lane's fixed 32-bit byte offset, computed
-// once per workgroup from the stage at l = 0.
+// once per workgroup from the stage at l = 0. The offsets are taken from the workgroup's own block of the operands
+// (B's stage rows; A's stage rows, or with A transposed the tile's first row), never from an operand's start: the
+// logits' gradient that the head's dX reads transposed is 8184 x 151936 floats (4.97 GB) at the c3 bench shape,
+// and offsets from its start past 2^32 bytes wrapped around.
 template <int kBI, int kBJ>
 struct MCopyOffsets {
     uint32_t b[MTile<kBI, kBJ>::PB], a[MTile<kBI, kBJ>::PA];
 };
+
+// Where the workgroup's A copies are measured from: the operand's start for A rows (the stage rows move the base),
+// the tile's first row for A transposed (rows of the whole reduction; the base moves along l).
+template <int kA>
+__host__ __device__ __forceinline__ const float* a_block(const GemmParams& p, int64_t i_blk) {
+    return kA == kAFloatT ? p.Af + i_blk * p.lda : p.Af;
+}
 
 template <int kA, int kBI, int kBJ>
 __host__ __device__ __forceinline__ MCopyOffsets<kBI, kBJ> mcopy_offsets(const GemmParams& p, int64_t i_blk,
@@ -567,17 +577,17 @@ __host__ __device__ __forceinline__ MCopyOffsets<kBI, kBJ> mcopy_offsets(const G
         q.l1 = big;
         o.a[t] = static_cast<uint32_t>(
             reinterpret_cast<const char*>(msrc_a<kA, kBI, kBJ>(q, t * 256 + tid, i_blk, 0, big)) -
-            reinterpret_cast<const char*>(p.Af));
+            reinterpret_cast<const char*>(a_block<kA>(p, i_blk)));
     }
     return o;
 }
 
 template <int kA, int kBI, int kBJ>
 __device__ __forceinline__ void missue_full(const GemmParams& p, MStage<kA, kBI, kBJ>& st,
-                                            const MCopyOffsets<kBI, kBJ>& o, int64_t l, int wave) {
+                                            const MCopyOffsets<kBI, kBJ>& o, int64_t l, int wave, int64_t i_blk) {
     using T = MTile<kBI, kBJ>;
     const float* bb = p.B + l * p.ldb;
-    const float* ab = kA == kAFloatT ? p.Af + l : p.Af + l * p.lda;
+    const float* ab = kA == kAFloatT ? a_block<kA>(p, i_blk) + l : p.Af + l * p.lda;
 #pragma unroll
     for (int t = 0; t < T::PB; ++t) copy16_to_lds_s(bb, o.b[t], &st.b[(t * 256 + wave * 64) * 4]);
 #pragma unroll
@@ -674,7 +684,7 @@ __device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA, kBI,
     const int64_t chunks = full + (tail ? 1 : 0);
     const int wave = wi * 2 + wj;
     auto issue = [&](MStage<kA, kBI, kBJ>& buf, int64_t l, int64_t end) {
-        if (l + kMStage <= end) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave);
+        if (l + kMStage <= end) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave, i_blk);
         else missue_stage<kA, kBI, kBJ>(p, buf, i_blk, j_blk, l, end - 1, tid);
     };
     if (!primed) issue(st[0], l0, l1);
@@ -1007,10 +1017,19 @@ int64_t padded_rows(int64_t n) { return static_cast<int64_t>(round_up(static_cas
 
 namespace {
 
+// Whether the matrix-core kernel's 32-bit per-lane copy offsets reach every element of a workgroup's block: 128 A
+// rows (transposed) or 32 stage rows of A and B, from the block's base.
+bool mfma_offsets_fit(const GemmCall& g) {
+    constexpr int64_t kLimit = int64_t{1} << 32;
+    const int64_t a = g.a_kind == kAFloatT ? 128 * g.lda : 32 * g.lda + g.I;
+    return 4 * a < kLimit && 4 * (32 * g.ldb + g.J) < kLimit;
+}
+
 // Whether a float-A call fits the matrix-core kernel's 16-byte staging (the conditions launch_gemm requires).
 bool mfma_shape(const GemmCall& g) {
     const bool vec = g.J % 4 == 0 && g.ldb % 4 == 0 && reinterpret_cast<uintptr_t>(g.B) % 16 == 0;
     if (!vec || g.lda % 4 != 0 || reinterpret_cast<uintptr_t>(g.Af) % 16 != 0) return false;
+    if (!mfma_offsets_fit(g)) return false;
     if (g.a_kind == kAFloatRows) return g.I % 4 == 0 && g.lda >= g.I;
     return g.seg == nullptr && g.l0 == 0 && g.l1 % 4 == 0 && g.l1 >= 4 && g.lda >= g.l1;
 }
@@ -1056,6 +1075,7 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
         const GemmCall& g = calls[k];
         DLLM_REQUIRE(g.a_kind == ak && (g.seg != nullptr) == seg, "the matmuls of a group share their mode");
         DLLM_REQUIRE(g.seg_addrow == nullptr && g.seg_partial == nullptr, "grouped matmuls take no window addends");
+        DLLM_REQUIRE(mfma_offsets_fit(g), "matmul operand rows too long for the matrix-core kernel's copy offsets");
         DLLM_REQUIRE(g.J % 4 == 0 && g.ldb % 4 == 0 && reinterpret_cast<uintptr_t>(g.B) % 16 == 0,
                      "float A operands need B rows of whole 16-byte chunks");
         DLLM_REQUIRE(g.lda % 4 == 0 && reinterpret_cast<uintptr_t>(g.Af) % 16 == 0,
@@ -1112,6 +1132,117 @@ int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_ta
     group->segmented = seg ? 1 : 0;
     group->capacity = capacity;
     return kOk;
+}
+
+// ---- row groups: the matmuls of a group take consecutive row ranges of shared operands, known on the device ----
+//
+// The routed experts' matmuls: matmul k reads and writes rows [start[k], start[k + 1]) of the grouped operands
+// (start in device memory, from the grouping kernels), so its row count and operand addresses are only known on the
+// device. The host lays out a template table once (every matmul at row 0 with no rows); before each launch a
+// one-workgroup kernel writes the live table from it: operand addresses advanced by the start times each operand's
+// row stride, the row count as I (plain) or as the reduction length (segmented), the tile starts and the XCD ranges
+// of equal work, each at most `cap` tiles so that the host's grid (8 cap workgroups) covers every tile.
+
+namespace {
+
+__global__ __launch_bounds__(256) void gemm_row_group_fill_kernel(const GemmParams* __restrict__ templ,
+                                                                  GemmParams* __restrict__ table, int n,
+                                                                  int capacity, const int64_t* __restrict__ start,
+                                                                  GemmRowShift shift, int tile, int64_t cap) {
+    constexpr int kMaxGroup = 1024;
+    __shared__ int64_t ntiles[kMaxGroup];
+    __shared__ double nwork[kMaxGroup];
+    int64_t* starts = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(table) +
+                                                 ((sizeof(GemmParams) * static_cast<size_t>(capacity) + 7) & ~size_t{7}));
+    int64_t* xcd_first = starts + capacity + 1;
+    for (int k = threadIdx.x; k < n; k += 256) {
+        GemmParams q = templ[k];
+        const int64_t st = start[k], rows = start[k + 1] - st;
+        q.Af += st * shift.a;
+        q.B += st * shift.b;
+        q.C += st * shift.c;
+        if (q.addsrc) q.addsrc += st * shift.add;
+        if (shift.rows_in_reduction) q.l1 = rows;
+        else q.I = rows;
+        table[k] = q;
+        ntiles[k] = q.I > 0 && q.J > 0 ? ((q.J + 32 * tile - 1) / (32 * tile)) * ((q.I + 32 * tile - 1) / (32 * tile)) : 0;
+        nwork[k] = static_cast<double>(q.l1 - q.l0) + 64.0;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    int64_t tiles = 0;
+    double total = 0.0;
+    for (int k = 0; k < n; ++k) {
+        starts[k] = tiles;
+        tiles += ntiles[k];
+        total += nwork[k] * static_cast<double>(ntiles[k]);
+    }
+    starts[n] = tiles;
+    // XCD x takes tiles [xcd_first[x], xcd_first[x + 1]): cut at equal shares of the work, each range at most cap
+    // tiles and the ranges left able to hold the tiles left
+    xcd_first[0] = 0;
+    int k = 0;
+    double before = 0.0;
+    for (int x = 1; x <= kXcdRanges; ++x) {
+        int64_t t = tiles;
+        if (x < kXcdRanges) {
+            const double target = total * x / kXcdRanges;
+            while (k < n && before + nwork[k] * static_cast<double>(ntiles[k]) <= target) {
+                before += nwork[k] * static_cast<double>(ntiles[k]);
+                ++k;
+            }
+            t = k < n ? starts[k] + static_cast<int64_t>((target - before) / nwork[k]) : tiles;
+        }
+        const int64_t lo = xcd_first[x - 1];
+        t = t < lo ? lo : t;
+        t = t > lo + cap ? lo + cap : t;                             // this range at most cap tiles
+        const int64_t need = tiles - cap * (kXcdRanges - x);         // the later ranges hold the rest
+        t = t < need ? need : t;
+        xcd_first[x] = t > tiles ? tiles : t;
+    }
+}
+
+}  // namespace
+
+int gemm_row_group_prepare(const GemmCall* calls, int n, int capacity, int tile, int64_t max_tiles, void* host_table,
+                           GemmGroup* group) {
+    DLLM_REQUIRE(n >= 1 && n <= capacity && capacity <= 1024, "a row group holds 1 to 1024 matmuls");
+    const int ak = calls[0].a_kind;
+    const bool seg = calls[0].seg != nullptr;
+    DLLM_REQUIRE(ak == kAFloatRows || ak == kAFloatT, "grouped matmuls read float A operands");
+    DLLM_REQUIRE(tile == 4 || (!seg && (tile == 2 || tile == 1)), "row groups take 128 tiles, or plain 64 or 32");
+    GemmParams* ps = static_cast<GemmParams*>(host_table);
+    for (int k = 0; k < n; ++k) {
+        const GemmCall& g = calls[k];
+        DLLM_REQUIRE(g.a_kind == ak && (g.seg != nullptr) == seg, "the matmuls of a group share their mode");
+        DLLM_REQUIRE(g.seg_addrow == nullptr && g.seg_partial == nullptr, "grouped matmuls take no window addends");
+        DLLM_REQUIRE(mfma_offsets_fit(g), "matmul operand rows too long for the matrix-core kernel's copy offsets");
+        DLLM_REQUIRE(g.J % 4 == 0 && g.ldb % 4 == 0 && g.lda % 4 == 0 && reinterpret_cast<uintptr_t>(g.B) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(g.Af) % 16 == 0,
+                     "row groups need operand rows of whole 16-byte chunks");
+        if (ak == kAFloatRows) DLLM_REQUIRE(g.I % 4 == 0 && g.lda >= g.I, "float A rows must hold whole chunks of I");
+        if (ak == kAFloatT) DLLM_REQUIRE(!seg && g.l0 == 0 && g.l1 % 4 == 0 && g.l1 >= 4 && g.lda >= g.l1,
+                                         "transposed float A needs a plain reduction over whole 16-byte chunks");
+        ps[k] = params_of(g);
+    }
+    DLLM_REQUIRE(max_tiles >= 1 && max_tiles < (int64_t{1} << 28), "row group too large for one launch");
+    group->count = n;
+    group->capacity = capacity;
+    group->tile = tile;
+    group->tiles = max_tiles;  // an upper bound: the kernel finds each workgroup's tile in the live table
+    group->a_kind = ak;
+    group->segmented = seg ? 1 : 0;
+    // the fill keeps every XCD range within cap tiles: twice an even share leaves room for the equal-work cuts
+    group->grid = 2 * static_cast<int64_t>(ceil_div(static_cast<size_t>(max_tiles), kXcdRanges)) * kXcdRanges;
+    return kOk;
+}
+
+int launch_gemm_row_group_fill(const void* device_templ, void* device_table, const GemmGroup& group,
+                               const int64_t* device_start, const GemmRowShift& shift, hipStream_t stream) {
+    hipLaunchKernelGGL(gemm_row_group_fill_kernel, dim3(1), dim3(256), 0, stream,
+                       static_cast<const GemmParams*>(device_templ), static_cast<GemmParams*>(device_table),
+                       group.count, group.capacity, device_start, shift, group.tile, group.grid / kXcdRanges);
+    return check_launch("gemm row group fill");
 }
 
 int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStream_t stream) {
@@ -1177,6 +1308,7 @@ int launch_gemm(const GemmCall& g, hipStream_t stream) {
     if (ak != kADouble) {
         // float A: 16-byte chunks of whole rows (and, transposed, a plain reduction over l in [0, l1))
         DLLM_REQUIRE(vec, "float A operands need B rows of whole 16-byte chunks");
+        DLLM_REQUIRE(mfma_offsets_fit(g), "matmul operand rows too long for the matrix-core kernel's copy offsets");
         DLLM_REQUIRE(g.lda % 4 == 0 && reinterpret_cast<uintptr_t>(g.Af) % 16 == 0, "float A rows must be 16-byte aligned");
         if (ak == kAFloatRows) DLLM_REQUIRE(g.I % 4 == 0 && g.lda >= g.I, "float A rows must hold whole chunks of I");
         if (ak == kAFloatT)

@@ -19,7 +19,9 @@ at T = 2048, the cross-entropy at vocab 151936, the grouped expert matmuls) runs
 from __future__ import annotations
 
 import hashlib
-from dataclasses import dataclass
+import os
+from concurrent.futures import ThreadPoolExecutor
+from dataclasses import dataclass, replace
 
 import numpy as np
 
@@ -71,19 +73,25 @@ def _configs() -> dict[str, RealShape]:
                                   "256000, 256-wide heads, soft-capped scores and logits, windows of 512 and 256"),
         "c1": RealShape("c1", smollm, (257, 257, 257, 257), steps=2, seed=1,
                         notes="SmolLM2-135M, full depth, 4 x 256 tokens, two steps"),
-        "c3": RealShape("c3", qwen25, (1025, 1025), seed=3,
-                        notes="Qwen2.5-1.5B layer shapes, 2 of 28 layers, full vocabulary, 2 x 1024 tokens"),
-        "c4": RealShape("c4", qwen3, (2049, 701), steps=2, lora=O.Lora(rank=16, alpha=32.0), base_quantize="q8_0",
-                        seed=4, learning_rate=1e-3,
+        "c3": RealShape("c3", qwen25, (1025,) * 8, seed=3,
+                        notes="Qwen2.5-1.5B layer shapes, 2 of 28 layers, full vocabulary, the bench's 8 x 1024 "
+                              "tokens"),
+        "c4": RealShape("c4", qwen3, (2049, 2049, 2049, 701), steps=2, lora=O.Lora(rank=16, alpha=32.0),
+                        base_quantize="q8_0", seed=4, learning_rate=1e-3,
                         notes="Qwen3-0.6B layer shapes, 2 of 28 layers, LoRA r16 on all 7 targets over a Q8_0 base, "
-                              "windows of 2048 and 700 tokens, two steps (B non-zero)"),
+                              "windows of 2048, 2048, 2048 and 700 tokens, two steps (B non-zero)"),
         "c5": RealShape("c5", olmoe, (2049, 501), router_aux_loss=0.01, seed=5,
                         notes="OLMoE-1B-7B layer shapes, 1 of 16 layers, 64 experts top 8, windows of 2048 and 500 "
                               "tokens, router_aux_loss 0.01"),
+        "c5_depth": RealShape("c5_depth", replace(olmoe, layers=16), (129, 65), router_aux_loss=0.01, seed=9,
+                              notes="OLMoE-1B-7B at full depth: all 16 layers, the whole 6.92 B-parameter arena "
+                                    "(more than 2^32 values per arena, 3219 tensors in the AdamW chunk table and "
+                                    "the exact-norm plan), windows of 128 and 64 tokens, router_aux_loss 0.01"),
     }
 
 
 CONFIGS = _configs()
+WORKERS = min(16, os.cpu_count() or 1)
 
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
 _M2 = np.uint64(0x94D049BB133111EB)
@@ -112,15 +120,20 @@ def weights(cfg: RealShape) -> dict[str, np.ndarray]:
     """Parameters in natural order: norms 1.0, everything else uniform with std 0.02 (routers 0.1, so the top-k
     choices spread), seeded per tensor."""
     shapes = cfg.decoder.tensor_shapes()
-    out = {}
-    for index, name in enumerate(O.tensor_order(shapes)):
+    names = O.tensor_order(shapes)
+
+    def make(index: int) -> np.ndarray:
+        name = names[index]
         shape = shapes[name]
         if name.endswith("norm.weight"):
-            out[name] = np.ones(shape, np.float32)
-        else:
-            std = 0.1 if name.endswith("router.weight") else 0.02
-            out[name] = uniform(cfg.seed * 100003 + index, int(np.prod(shape)), std).reshape(shape)
-    return out
+            return np.ones(shape, np.float32)
+        std = 0.1 if name.endswith("router.weight") else 0.02
+        return uniform(cfg.seed * 100003 + index, int(np.prod(shape)), std).reshape(shape)
+
+    # tensors are independent (each seeded by its index): generated on a thread pool (numpy releases the GIL)
+    with ThreadPoolExecutor(max_workers=WORKERS) as pool:
+        values = list(pool.map(make, range(len(names))))
+    return dict(zip(names, values))
 
 
 def adapters(cfg: RealShape) -> dict[str, np.ndarray]:
@@ -150,7 +163,15 @@ def quantized_base(cfg: RealShape, base: dict[str, np.ndarray], quantize) -> dic
 
 
 def digest(values: np.ndarray) -> str:
-    return hashlib.sha256(np.ascontiguousarray(values, dtype=np.float32).tobytes()).hexdigest()
+    return hashlib.sha256(memoryview(np.ascontiguousarray(values, dtype=np.float32)).cast("B")).hexdigest()
+
+
+def digest_of_concatenation(arrays) -> str:
+    """digest(np.concatenate of the arrays' flattened values), without forming the concatenation."""
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(memoryview(np.ascontiguousarray(a, dtype=np.float32)).cast("B"))
+    return h.hexdigest()
 
 
 def double_hex(x: float) -> str:

@@ -67,6 +67,24 @@ def test_linear_rows_are_batch_invariant(K):
         assert_same(K.linear_backward(x_all[:m], dyw, dy_all[:m])[0], dfull[:m], f"dx M={m}")
 
 
+def test_linear_dx_of_an_operand_past_4_gib(K, ora):
+    """dX of the head at c3's batch: dy [8192, 151936] is 4.98 GB, read transposed by the matrix-core kernel, whose
+    32-bit per-lane copy offsets are taken from each workgroup's own rows (taken from the operand's start they wrapped
+    past 2^32 bytes, from row 7065 on). Rows on both sides of that boundary and the last rows against the oracle, and
+    the first rows against a 64-row call (batch invariance)."""
+    rows, inf, outf = 8192, 1536, 151936
+    rng = np.random.default_rng(71)  # 1.2 G values: numpy's generator rather than the reference's serial one
+    x = rng.standard_normal((rows, inf), dtype=np.float32)
+    w = rng.standard_normal((outf, inf), dtype=np.float32) * np.float32(0.02)
+    dy = rng.standard_normal((rows, outf), dtype=np.float32) * np.float32(1e-4)
+    dx, _, _ = K.linear_backward(x, w, dy)
+    small, _, _ = K.linear_backward(x[:64], w, dy[:64])
+    assert_same(dx[:64], small, "rows 0-63 against a 64-row call")
+    for sel in ([7063, 7064, 7065, 7066], [8190, 8191]):
+        want, _, _ = ora.linear_backward(np.ascontiguousarray(x[sel]), w, np.ascontiguousarray(dy[sel]))
+        assert_same(dx[sel], want, f"rows {sel}")
+
+
 @pytest.mark.parametrize(("rows", "dim"), [(1, 8), (9, 48), (33, 576), (5, 1536)])
 def test_rms_norm_forward_and_backward(K, ora, rows, dim):
     x, w, dy = O.gaussian(5, rows, dim, scale=3.0), O.gaussian(6, dim), O.gaussian(7, rows, dim)

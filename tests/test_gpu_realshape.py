@@ -11,6 +11,7 @@ sums, cross-entropy at vocab 151936, the attention tiles at T = 2048, LoRA over 
 from __future__ import annotations
 
 import json
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 import pytest
@@ -56,10 +57,15 @@ def compare(t, shapes: dict, step_record: dict, loss: float, norm: float) -> lis
     if R.double_hex(norm) != step_record["norm"]:
         bad.append(f"norm {norm!r} != {float.fromhex(step_record['norm'])!r}")
     which = {"param": t.PARAM, "grad": t.GRAD, "m": t.M, "v": t.V}
-    for name, digests in step_record["tensors"].items():
-        for kind, want in digests.items():
-            if R.digest(t.get(name, shapes[name], which[kind])) != want:
-                bad.append(f"{name} {kind}")
+    jobs = [(name, kind, want) for name, digests in step_record["tensors"].items() for kind, want in digests.items()]
+
+    def check(job):
+        name, kind, want = job
+        return None if R.digest(t.get(name, shapes[name], which[kind])) == want else f"{name} {kind}"
+
+    # the copies and the hashing of many tensors (the 6.92 B-parameter arena at full depth) on a thread pool
+    with ThreadPoolExecutor(max_workers=R.WORKERS) as pool:
+        bad += [b for b in pool.map(check, jobs) if b is not None]
     return bad
 
 
@@ -70,7 +76,7 @@ def test_step_at_real_shape_matches_the_oracle(name):
     cfg = R.CONFIGS[name]
     d = cfg.decoder
     base = R.weights(cfg)
-    assert R.digest(O.concatenated(base)) == record["inputs"], "the input generator differs from the recording's"
+    assert R.digest_of_concatenation(base.values()) == record["inputs"], "the input generator differs from the recording's"
     t = make_trainer(cfg)
     try:
         t.load(base)
@@ -86,6 +92,8 @@ def test_step_at_real_shape_matches_the_oracle(name):
             loss, norm = t.step(windows, cfg.learning_rate, step, router_aux_loss=cfg.router_aux_loss)
             bad = compare(t, shapes, step_record, loss, norm)
             print(f"{name} step {step}: loss {loss!r} norm {norm!r}, {len(bad)} mismatches", flush=True)
+            if bad:
+                print("mismatches:", " | ".join(bad), flush=True)
             assert not bad, f"{name} step {step}: {len(bad)} mismatches, first {bad[:12]}"
     finally:
         t.close()
