@@ -63,6 +63,19 @@ struct GemmGroup {
 size_t gemm_group_bytes(int n);
 int gemm_group_prepare(const GemmCall* calls, int n, int capacity, void* host_table, GemmGroup* group);
 int launch_gemm_group(const GemmGroup& group, const void* device_table, hipStream_t stream);
+// Row groups: matmul k of the group reads and writes rows [start[k], start[k + 1]) of shared grouped operands, the
+// starts in device memory (the routed experts, grouped on the device). gemm_row_group_prepare lays out the template
+// table (each call as at row 0) in host_table (gemm_group_bytes(capacity) bytes, copied to device memory by the
+// caller) and the launch shape for at most max_tiles tiles; launch_gemm_row_group_fill writes the live table from the
+// template and the starts before each launch_gemm_group. Each output is bit-identical to launch_gemm of its call.
+struct GemmRowShift {
+    int64_t a = 0, b = 0, c = 0, add = 0;  // elements each operand advances per grouped row
+    int rows_in_reduction = 0;            // the row count is the reduction length (weight gradients), else I
+};
+int gemm_row_group_prepare(const GemmCall* calls, int n, int capacity, int tile, int64_t max_tiles, void* host_table,
+                           GemmGroup* group);
+int launch_gemm_row_group_fill(const void* device_templ, void* device_table, const GemmGroup& group,
+                               const int64_t* device_start, const GemmRowShift& shift, hipStream_t stream);
 
 // dst[r][c] = src[r][c] and dstT[c][r] = src[r][c] as doubles (either may be null).
 int launch_to_double(const float* src, int64_t rows, int64_t cols, int64_t lds, double* dst, int64_t ldd,
@@ -163,6 +176,16 @@ int launch_moe_combine(const float* y, const int64_t* order, const int64_t* slot
 int launch_moe_dweights(const float* dout, const float* y, const int64_t* row_of, const int64_t* slot,
                         const float* weights, int64_t positions, int64_t dim, float* dweights, float* dy,
                         hipStream_t stream);
+// Groups the rows of one routed layer by expert on the device (experts ascending, rows ascending in each expert:
+// np.nonzero's order): estart [E + 1] the group starts, eseg [E][eseg_ld] each group's window boundaries (nseg + 1
+// used), row_of / slot [rows K] the row and choice of each grouped position, order [rows K] each row's positions by
+// ascending expert, pos_of [rows K] scratch, counts [nseg][E] += the layer's choices per window (router
+// statistics), err set to 1 for an expert out of range; cnt_scratch holds nseg E 8-byte counters.
+int launch_moe_group_rows(const int64_t* chosen, int64_t rows, int64_t K, int64_t E, const int64_t* seg, int nseg,
+                          void* cnt_scratch, int64_t* estart, int64_t* eseg, int64_t eseg_ld, int64_t* row_of,
+                          int64_t* slot, int64_t* order, int64_t* pos_of, int64_t* counts, int* err,
+                          hipStream_t stream);
+int launch_zero_i64(int64_t* x, int64_t n, hipStream_t stream);
 // The router load-balancing loss per window (backprop.py:359-377); grad_row [nseg][experts] may be null.
 int launch_router_stats(const float* probs, int64_t layer_stride, int64_t layers, const int64_t* seg, int nseg,
                         const int64_t* counts, int64_t experts, double router_scale, double* loss, float* grad_row,

@@ -14,6 +14,8 @@
 //
 // The per-row chains are serial, as in the reference, one lane per row. Each probability is recomputed where it is
 // needed from the row's max and total (exp is deterministic), so no per-row scratch is kept.
+#include <algorithm>
+
 #include "common.h"
 #include "devmath.h"
 #include "kernels.h"
@@ -521,6 +523,113 @@ __global__ void dot_kernel(const float* __restrict__ a, const float* __restrict_
     *result = static_cast<float>(acc);
 }
 
+// ---- grouping the routed rows by expert on the device (backprop.py:308-357) ----
+// The reference runs each expert over np.nonzero(indices == e): its rows ascending. Here the step's rows are grouped
+// by expert (experts ascending, rows ascending inside an expert), which puts each window's rows of an expert in one
+// contiguous run, and every quantity is an integer count or position, so the grouping is the same whatever order the
+// threads run in:
+//   moe_count_kernel   cnt[w][e]: rows of window w choosing expert e (integer atomics: order-free)
+//   moe_starts_kernel  estart[e] (group starts), eseg[e][w] (window boundaries inside e's group), the router
+//                      statistics' per-window counts += cnt
+//   moe_place_kernel   one workgroup per expert walks the rows ascending; a row choosing e gets the next position
+//                      (a block-wide prefix of the choosing rows): row_of[p], slot[p], pos_of[r K + j] = p
+//   moe_order_kernel   order[r K + i] = the position of row r's i-th choice by ascending expert
+__global__ __launch_bounds__(256) void moe_count_kernel(const int64_t* __restrict__ chosen, int64_t rows, int64_t K,
+                                                        int64_t E, const int64_t* __restrict__ seg, int nseg,
+                                                        unsigned long long* __restrict__ cnt, int* __restrict__ err) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < rows * K;
+         i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int64_t e = chosen[i], r = i / K;
+        if (e < 0 || e >= E) {
+            *err = 1;
+            continue;
+        }
+        int lo = 0, hi = nseg - 1;  // the window of row r: the last w with seg[w] <= r
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (seg[mid] <= r) lo = mid;
+            else hi = mid - 1;
+        }
+        atomicAdd(&cnt[static_cast<int64_t>(lo) * E + e], 1ull);
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_starts_kernel(const unsigned long long* __restrict__ cnt, int64_t E, int nseg,
+                                                         int64_t eseg_ld, int64_t* __restrict__ estart,
+                                                         int64_t* __restrict__ eseg, int64_t* __restrict__ counts) {
+    __shared__ int64_t total[1024];
+    for (int64_t e = threadIdx.x; e < E; e += 256) {
+        int64_t run = 0;
+        eseg[e * eseg_ld] = 0;
+        for (int w = 0; w < nseg; ++w) {
+            const int64_t c = static_cast<int64_t>(cnt[static_cast<int64_t>(w) * E + e]);
+            run += c;
+            eseg[e * eseg_ld + w + 1] = run;
+            counts[static_cast<int64_t>(w) * E + e] += c;
+        }
+        total[e] = run;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int64_t at = 0;
+        for (int64_t e = 0; e < E; ++e) {
+            estart[e] = at;
+            at += total[e];
+        }
+        estart[E] = at;
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restrict__ chosen, int64_t rows, int64_t K,
+                                                        const int64_t* __restrict__ estart,
+                                                        int64_t* __restrict__ row_of, int64_t* __restrict__ slot,
+                                                        int64_t* __restrict__ pos_of) {
+    __shared__ int64_t wave_count[4];
+    const int64_t e = blockIdx.x;
+    const int lane = static_cast<int>(threadIdx.x) & 63, wave = static_cast<int>(threadIdx.x) >> 6;
+    int64_t next = estart[e];  // the position the next choosing row takes
+    for (int64_t r0 = 0; r0 < rows; r0 += 256) {
+        const int64_t r = r0 + threadIdx.x;
+        int64_t j = -1;
+        if (r < rows)
+            for (int64_t k = 0; k < K; ++k)
+                if (chosen[r * K + k] == e) j = k;  // a row chooses an expert at most once
+        const uint64_t mask = __ballot(j >= 0);
+        const int64_t below = __popcll(mask & ((uint64_t{1} << lane) - 1));
+        if (lane == 0) wave_count[wave] = __popcll(mask);
+        __syncthreads();
+        int64_t before = 0;
+        for (int w = 0; w < wave; ++w) before += wave_count[w];
+        if (j >= 0) {
+            const int64_t p = next + before + below;
+            row_of[p] = r;
+            slot[p] = r * K + j;
+            pos_of[r * K + j] = p;
+        }
+        next += wave_count[0] + wave_count[1] + wave_count[2] + wave_count[3];
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_order_kernel(const int64_t* __restrict__ chosen,
+                                                        const int64_t* __restrict__ pos_of, int64_t rows, int64_t K,
+                                                        int64_t* __restrict__ order) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (r >= rows) return;
+    // the row's choices by ascending expert: each output slot i takes the choice with exactly i smaller experts
+    for (int64_t j = 0; j < K; ++j) {
+        const int64_t e = chosen[r * K + j];
+        int64_t rank = 0;
+        for (int64_t k = 0; k < K; ++k) rank += chosen[r * K + k] < e ? 1 : 0;
+        order[r * K + rank] = pos_of[r * K + j];
+    }
+}
+
+__global__ __launch_bounds__(256) void zero_u64_kernel(unsigned long long* __restrict__ x, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+        x[i] = 0ull;
+}
+
 unsigned row_grid(int64_t rows) { return static_cast<unsigned>(ceil_div(static_cast<size_t>(rows), 256)); }
 
 }  // namespace
@@ -713,6 +822,32 @@ int launch_broadcast_window_rows(const float* grad_row, const int64_t* seg, int 
     hipLaunchKernelGGL(broadcast_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, grad_row, seg,
                        nseg, experts, out);
     return check_launch("broadcast_window_rows");
+}
+
+int launch_moe_group_rows(const int64_t* chosen, int64_t rows, int64_t K, int64_t E, const int64_t* seg, int nseg,
+                          void* cnt_scratch, int64_t* estart, int64_t* eseg, int64_t eseg_ld, int64_t* row_of,
+                          int64_t* slot, int64_t* order, int64_t* pos_of, int64_t* counts, int* err,
+                          hipStream_t stream) {
+    DLLM_REQUIRE(E >= 1 && E <= 1024 && K >= 1 && K <= E && nseg >= 1, "grouping needs 1..1024 experts");
+    if (rows == 0) return kOk;
+    auto* cnt = static_cast<unsigned long long*>(cnt_scratch);
+    const int64_t ncnt = static_cast<int64_t>(nseg) * E;
+    hipLaunchKernelGGL(zero_u64_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(ncnt, 256), 1024))),
+                       dim3(256), 0, stream, cnt, ncnt);
+    hipLaunchKernelGGL(moe_count_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(rows * K, 256), 4096))),
+                       dim3(256), 0, stream, chosen, rows, K, E, seg, nseg, cnt, err);
+    hipLaunchKernelGGL(moe_starts_kernel, dim3(1), dim3(256), 0, stream, cnt, E, nseg, eseg_ld, estart, eseg, counts);
+    hipLaunchKernelGGL(moe_place_kernel, dim3(static_cast<unsigned>(E)), dim3(256), 0, stream, chosen, rows, K, estart,
+                       row_of, slot, pos_of);
+    hipLaunchKernelGGL(moe_order_kernel, dim3(row_grid(rows)), dim3(256), 0, stream, chosen, pos_of, rows, K, order);
+    return check_launch("moe grouping");
+}
+
+int launch_zero_i64(int64_t* x, int64_t n, hipStream_t stream) {
+    if (n == 0) return kOk;
+    hipLaunchKernelGGL(zero_u64_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 256), 1024))),
+                       dim3(256), 0, stream, reinterpret_cast<unsigned long long*>(x), n);
+    return check_launch("zero");
 }
 
 }  // namespace dllm_hip

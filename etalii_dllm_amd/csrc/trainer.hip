@@ -191,6 +191,11 @@ struct dllm_hip_trainer {
         double group_flops[9] = {};
         // a kind whose matmuls the grouped kernel cannot stage (sizes not whole 16-byte chunks): one launch each
         std::vector<GemmCall> loose[9];
+        // grouping on the device: the group starts [E + 1] and each kind's template table (gemm_row_group_prepare),
+        // valid for the step shape in tmpl_key
+        int64_t* estart_d = nullptr;
+        char* tmpl = nullptr;
+        std::vector<int64_t> tmpl_key;
         char* tables = nullptr;
     };
     enum ExpertMatmul { kFwdGate, kFwdUp, kFwdDown, kDxDown, kDwDown, kDxGate, kDwGate, kDxUp, kDwUp, kExpertMatmuls };
@@ -210,6 +215,10 @@ struct dllm_hip_trainer {
     double* router_loss_w = nullptr;
     float* probs_all = nullptr;
     int64_t* counts_d = nullptr;
+    int64_t* pos_of = nullptr;     // grouping scratch [R K]: each choice's grouped position
+    void* group_cnt = nullptr;     // grouping scratch [W][E] 8-byte counters
+    int* route_err = nullptr;      // set by the grouping for an expert out of range
+    int64_t tmpl_version = 0;      // bumped when the step's weight addresses change (fold, merge)
     std::vector<int64_t> counts_host;  // [windows][E] choices per window over all layers
     double router_scale_cur = 0.0, last_router_loss = 0.0;
     double *inv_mlp = nullptr, *inv_attn = nullptr, *inv_post = nullptr;
@@ -553,6 +562,8 @@ struct dllm_hip_trainer {
                 DLLM_TRY(make(&s.order, RK));
                 DLLM_TRY(make(&s.eseg, E * (W_max + 1)));
                 DLLM_TRY(make(&s.tables, kExpertMatmuls * gemm_group_bytes(static_cast<int>(E))));
+                DLLM_TRY(make(&s.tmpl, kExpertMatmuls * gemm_group_bytes(static_cast<int>(E))));
+                DLLM_TRY(make(&s.estart_d, E + 1));
                 if (c.shared_inter > 0) {
                     const int64_t SI = c.shared_inter;
                     DLLM_TRY(make(&s.sh_gate, R * SI));
@@ -582,6 +593,11 @@ struct dllm_hip_trainer {
             DLLM_TRY(make(&grad_row, W_max * E));
             DLLM_TRY(make(&router_loss_w, W_max));
             DLLM_TRY(make(&counts_d, W_max * E));
+            DLLM_TRY(make(&pos_of, RK));
+            char* gc = nullptr;
+            DLLM_TRY(make(&gc, static_cast<size_t>(W_max * E) * 8));
+            group_cnt = gc;
+            DLLM_TRY(make(&route_err, 1));
         }
         const int64_t dmlp = std::max(R * I, RK * EI);
         x_final = xs.back();
@@ -764,6 +780,7 @@ struct dllm_hip_trainer {
         // the step's weight addresses changed: rebuild the transposes' job table and the qkv groups
         wt_jobs = nullptr;
         grp_rows = -1;
+        ++tmpl_version;
         wt_valid = false;
         merged_valid = false;
         return kOk;
@@ -1446,7 +1463,7 @@ struct dllm_hip_trainer {
 
     // Groups the step's rows by expert from the layer's choices (host; the choices come back first): experts
     // ascending, within an expert rows ascending (np.nonzero), and the per-window split of each group.
-    int group_rows(int64_t l, Saved& sv, int64_t R, hipStream_t s) {
+    int group_rows_host(int64_t l, Saved& sv, int64_t R, hipStream_t s) {
         std::vector<int64_t> chosen(static_cast<size_t>(R * K));
         DLLM_TRY(check_hip(hipMemcpyAsync(chosen.data(), sv.chosen, chosen.size() * 8, hipMemcpyDeviceToHost, s),
                            "download"));
@@ -1503,6 +1520,60 @@ struct dllm_hip_trainer {
     // The layer's nine kinds of expert matmuls over the grouped rows (expert e's rows are st .. st + n - 1):
     //   forward  gate/up = xg W^T, y = product Wd^T;  backward  dproduct = dy Wd, dxg = dgate Wg (+ dup Wu),
     //   and each weight's dW over the expert's rows split at the window boundaries.
+    // Expert e's matmul of one kind over its grouped rows st .. st + n - 1; false when the gradient it forms reaches
+    // no optimizer (LoRA runs without that target).
+    bool expert_call(const LayerIds& L, const Saved& sv, int kind, int64_t e, int64_t st, int64_t n, GemmCall* out) const {
+        const int64_t* es = sv.eseg + e * (W_max + 1);
+        GemmCall g;
+        switch (kind) {
+            case kFwdGate: g = fwd_call(xg + st * H, n, H, L.egate[e], nullptr, sv.gate + st * EI, nullptr); break;
+            case kFwdUp: g = fwd_call(xg + st * H, n, H, L.eup[e], nullptr, sv.up + st * EI, nullptr); break;
+            case kFwdDown: g = fwd_call(sv.product + st * EI, n, EI, L.edown[e], nullptr, sv.y + st * H, nullptr); break;
+            case kDxDown: g = dx_call(dyg + st * H, n, L.edown[e], dproduct + st * EI, nullptr); break;
+            case kDwDown:
+                if (!grad_wanted(G(L.edown[e]))) return false;
+                g = dw_call(dyg + st * H, H, sv.product + st * EI, EI, static_cast<int>(nwin), G(L.edown[e]), nullptr,
+                            nullptr, es, n);
+                g.seg_rowscale = unfold_scale(L.edown[e]);
+                break;
+            case kDxGate: g = dx_call(dgate + st * EI, n, L.egate[e], dxg + st * H, nullptr); break;
+            case kDwGate:
+                if (!grad_wanted(G(L.egate[e]))) return false;
+                g = dw_call(dgate + st * EI, EI, xg + st * H, H, static_cast<int>(nwin), G(L.egate[e]), nullptr,
+                            nullptr, es, n);
+                break;
+            case kDxUp: g = dx_call(dup + st * EI, n, L.eup[e], dxg + st * H, dxg + st * H); break;
+            default:
+                if (!grad_wanted(G(L.eup[e]))) return false;
+                g = dw_call(dup + st * EI, EI, xg + st * H, H, static_cast<int>(nwin), G(L.eup[e]), nullptr, nullptr, es,
+                            n);
+                break;
+        }
+        g.seg_partial = nullptr;
+        g.seg_partial_cap = 0;
+        *out = g;
+        return true;
+    }
+
+    // How each kind's operands advance per grouped row (the fill kernel's shifts of the template table).
+    GemmRowShift expert_shift(int kind) const {
+        GemmRowShift sh;
+        switch (kind) {
+            case kFwdGate: case kFwdUp: sh.a = H; sh.c = EI; break;
+            case kFwdDown: sh.a = EI; sh.c = H; break;
+            case kDxDown: sh.a = H; sh.c = EI; break;
+            case kDxGate: sh.a = EI; sh.c = H; break;
+            case kDxUp: sh.a = EI; sh.c = H; sh.add = H; break;
+            case kDwDown: sh.a = H; sh.b = EI; sh.rows_in_reduction = 1; break;
+            default: sh.a = EI; sh.b = H; sh.rows_in_reduction = 1; break;  // kDwGate, kDwUp
+        }
+        return sh;
+    }
+
+    // The layer's nine kinds of expert matmuls over the grouped rows (expert e's rows are st .. st + n - 1):
+    //   forward  gate/up = xg W^T, y = product Wd^T;  backward  dproduct = dy Wd, dxg = dgate Wg (+ dup Wu),
+    //   and each weight's dW over the expert's rows split at the window boundaries. Host grouping (model sizes the
+    //   grouped kernel cannot stage): the tables from the host's group starts.
     int expert_tables(int64_t l, Saved& sv, std::vector<char>* out) {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
         const size_t gb = gemm_group_bytes(static_cast<int>(E));
@@ -1511,38 +1582,8 @@ struct dllm_hip_trainer {
         for (int kind = 0; kind < kExpertMatmuls; ++kind) {
             calls.clear();
             for (int64_t e = 0; e < E; ++e) {
-                const int64_t st = sv.estart[e], n = sv.estart[e + 1] - st;
-                const int64_t* es = sv.eseg + e * (W_max + 1);
                 GemmCall g;
-                switch (kind) {
-                    case kFwdGate: g = fwd_call(xg + st * H, n, H, L.egate[e], nullptr, sv.gate + st * EI, nullptr); break;
-                    case kFwdUp: g = fwd_call(xg + st * H, n, H, L.eup[e], nullptr, sv.up + st * EI, nullptr); break;
-                    case kFwdDown:
-                        g = fwd_call(sv.product + st * EI, n, EI, L.edown[e], nullptr, sv.y + st * H, nullptr);
-                        break;
-                    case kDxDown: g = dx_call(dyg + st * H, n, L.edown[e], dproduct + st * EI, nullptr); break;
-                    case kDwDown:
-                        if (!grad_wanted(G(L.edown[e]))) continue;
-                        g = dw_call(dyg + st * H, H, sv.product + st * EI, EI, static_cast<int>(nwin), G(L.edown[e]),
-                                    nullptr, nullptr, es, n);
-                        g.seg_rowscale = unfold_scale(L.edown[e]);
-                        break;
-                    case kDxGate: g = dx_call(dgate + st * EI, n, L.egate[e], dxg + st * H, nullptr); break;
-                    case kDwGate:
-                        if (!grad_wanted(G(L.egate[e]))) continue;
-                        g = dw_call(dgate + st * EI, EI, xg + st * H, H, static_cast<int>(nwin), G(L.egate[e]),
-                                    nullptr, nullptr, es, n);
-                        break;
-                    case kDxUp: g = dx_call(dup + st * EI, n, L.eup[e], dxg + st * H, dxg + st * H); break;
-                    default:
-                        if (!grad_wanted(G(L.eup[e]))) continue;
-                        g = dw_call(dup + st * EI, EI, xg + st * H, H, static_cast<int>(nwin), G(L.eup[e]), nullptr,
-                                    nullptr, es, n);
-                        break;
-                }
-                g.seg_partial = nullptr;
-                g.seg_partial_cap = 0;
-                calls.push_back(g);
+                if (expert_call(L, sv, kind, e, sv.estart[e], sv.estart[e + 1] - sv.estart[e], &g)) calls.push_back(g);
             }
             GemmGroup& grp = sv.groups[kind];
             grp = GemmGroup{};
@@ -1560,6 +1601,75 @@ struct dllm_hip_trainer {
             for (const GemmCall& g : calls) sv.group_flops[kind] += flops_of(g);
         }
         return kOk;
+    }
+
+    // Device grouping: each kind's template table (every expert at grouped row 0 with no rows), rebuilt only when the
+    // step's shape (rows, windows, DPO factors) or the weights' addresses change. The plain kinds take the tile size
+    // an even spread of the rows over the experts would take (as gemm_group_prepare); the bits do not depend on it.
+    int expert_templates(int64_t l, Saved& sv, int64_t R, hipStream_t s) {
+        const std::vector<int64_t> key = {R, nwin, dpo.on ? 1 : 0, tmpl_version};
+        if (sv.tmpl_key == key) return kOk;
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        const size_t gb = gemm_group_bytes(static_cast<int>(E));
+        std::vector<char> host(kExpertMatmuls * gb, 0);
+        std::vector<GemmCall> calls(static_cast<size_t>(E));
+        const int64_t even = ceil_div(R * K, E);  // rows per expert if the choices spread evenly
+        for (int kind = 0; kind < kExpertMatmuls; ++kind) {
+            GemmGroup& grp = sv.groups[kind];
+            grp = GemmGroup{};
+            sv.loose[kind].clear();
+            bool wanted = true;
+            for (int64_t e = 0; e < E; ++e) wanted = expert_call(L, sv, kind, e, 0, 0, &calls[static_cast<size_t>(e)]);
+            if (!wanted) continue;  // no expert's gradient of this kind is trained
+            const GemmCall& g0 = calls[0];
+            const bool seg = g0.seg != nullptr;
+            int tile = 4;
+            while (!seg && tile > 1 && E * ceil_div(g0.J, 32 * tile) * ceil_div(even, 32 * tile) < 512) tile /= 2;
+            const int64_t T = 32 * tile;
+            const int64_t max_tiles = seg ? E * ceil_div(g0.I, T) * ceil_div(g0.J, T)
+                                          : ceil_div(g0.J, T) * (ceil_div(R * K, T) + E);
+            DLLM_TRY(gemm_row_group_prepare(calls.data(), static_cast<int>(E), static_cast<int>(E), tile, max_tiles,
+                                            host.data() + kind * gb, &grp));
+        }
+        DLLM_TRY(check_hip(hipStreamSynchronize(s), "expert templates"));  // no fill still reads the old template
+        DLLM_TRY(check_hip(hipMemcpy(sv.tmpl, host.data(), host.size(), hipMemcpyHostToDevice), "upload"));
+        sv.tmpl_key = key;
+        return kOk;
+    }
+
+    // Groups the layer's rows by expert on the device and writes the live tables of its expert matmuls: no host
+    // round trip, so the stream keeps running through routed layers.
+    int group_rows_device(int64_t l, Saved& sv, int64_t R, hipStream_t s) {
+        DLLM_TRY(expert_templates(l, sv, R, s));
+        DLLM_TRY(launch_moe_group_rows(sv.chosen, R, K, E, seg_d, static_cast<int>(nwin), group_cnt, sv.estart_d,
+                                       sv.eseg, W_max + 1, sv.row_of, sv.slot, sv.order, pos_of, counts_d,
+                                       route_err, s));
+        const size_t gb = gemm_group_bytes(static_cast<int>(E));
+        for (int kind = 0; kind < kExpertMatmuls; ++kind) {
+            if (sv.groups[kind].count == 0) continue;
+            DLLM_TRY(launch_gemm_row_group_fill(sv.tmpl + kind * gb, sv.tables + kind * gb, sv.groups[kind],
+                                                sv.estart_d, expert_shift(kind), s));
+        }
+        if (profiling) {  // the matmul timing's algorithmic flop needs the group sizes (not a timed step)
+            sv.estart.assign(static_cast<size_t>(E + 1), 0);
+            DLLM_TRY(check_hip(hipMemcpyAsync(sv.estart.data(), sv.estart_d, sv.estart.size() * 8,
+                                              hipMemcpyDeviceToHost, s), "download"));
+            DLLM_TRY(check_hip(hipStreamSynchronize(s), "group sizes"));
+            const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+            for (int kind = 0; kind < kExpertMatmuls; ++kind) {
+                sv.group_flops[kind] = 0.0;
+                for (int64_t e = 0; e < E && sv.groups[kind].count > 0; ++e) {
+                    GemmCall g;
+                    if (expert_call(L, sv, kind, e, sv.estart[e], sv.estart[e + 1] - sv.estart[e], &g))
+                        sv.group_flops[kind] += flops_of(g);
+                }
+            }
+        }
+        return kOk;
+    }
+
+    int group_rows(int64_t l, Saved& sv, int64_t R, hipStream_t s) {
+        return odd_shapes ? group_rows_host(l, sv, R, s) : group_rows_device(l, sv, R, s);
     }
 
     int expert_matmul(const Saved& sv, int kind, hipStream_t s) {
@@ -1751,7 +1861,11 @@ struct dllm_hip_trainer {
         const int nseg = static_cast<int>(windows);
         nwin = windows;
         router_scale_cur = router_scale;
-        if (E > 0) counts_host.assign(static_cast<size_t>(windows * E), 0);
+        if (E > 0) {  // the router statistics' per-window choice counts, summed over the sparse layers
+            counts_host.assign(static_cast<size_t>(windows * E), 0);
+            if (!odd_shapes) DLLM_TRY(launch_zero_i64(counts_d, windows * E, s));
+            DLLM_TRY(check_hip(hipMemsetAsync(route_err, 0, sizeof(int), s), "memset"));
+        }
         const double eps = c.rms_norm_eps;
         // forward (backprop.py:411-490)
         DLLM_TRY(launch_gather_rows(P(emb), tok_in, saved[0].x_in, R, H, s));
@@ -1762,8 +1876,9 @@ struct dllm_hip_trainer {
             DLLM_TRY(forward_layer(l, R, b, x_out, s));
         }
         if (E > 0) {  // _router_loss (backprop.py:359-377): per window, over every sparse layer's rows
-            DLLM_TRY(check_hip(hipMemcpyAsync(counts_d, counts_host.data(), counts_host.size() * 8,
-                                              hipMemcpyHostToDevice, s), "upload"));
+            if (odd_shapes)  // host grouping counted them on the host
+                DLLM_TRY(check_hip(hipMemcpyAsync(counts_d, counts_host.data(), counts_host.size() * 8,
+                                                  hipMemcpyHostToDevice, s), "upload"));
             DLLM_TRY(launch_router_stats(probs_all, R_max * E, sparse_layers(), seg_d, nseg, counts_d, E, router_scale,
                                          router_loss_w, router_scale != 0.0 ? grad_row : nullptr, s));
         }
@@ -1819,8 +1934,13 @@ struct dllm_hip_trainer {
             DLLM_TRY(check_hip(hipMemcpyAsync(rw.data(), router_loss_w, rw.size() * 8, hipMemcpyDeviceToHost, s),
                                "download"));
         DLLM_TRY(check_hip(hipMemcpyAsync(&flag, err_flag, sizeof flag, hipMemcpyDeviceToHost, s), "download"));
+        int route_flag = 0;
+        if (E > 0)
+            DLLM_TRY(check_hip(hipMemcpyAsync(&route_flag, route_err, sizeof route_flag, hipMemcpyDeviceToHost, s),
+                               "download"));
         DLLM_TRY(check_hip(hipStreamSynchronize(s), "step"));
         DLLM_REQUIRE(flag == 0, "target out of range");
+        DLLM_REQUIRE(route_flag == 0, "routing produced an expert out of range");
         window_losses = lw;
         double total = 0.0;
         for (double x : lw) total += x;  // trainer.py:326 (loss_total += loss, batch order)
