@@ -584,10 +584,11 @@ __host__ __device__ __forceinline__ MCopyOffsets<kBI, kBJ> mcopy_offsets(const G
 
 template <int kA, int kBI, int kBJ>
 __device__ __forceinline__ void missue_full(const GemmParams& p, MStage<kA, kBI, kBJ>& st,
-                                            const MCopyOffsets<kBI, kBJ>& o, int64_t l, int wave, int64_t i_blk) {
+                                            const MCopyOffsets<kBI, kBJ>& o, int64_t l, int wave,
+                                            const float* a_base) {
     using T = MTile<kBI, kBJ>;
     const float* bb = p.B + l * p.ldb;
-    const float* ab = kA == kAFloatT ? a_block<kA>(p, i_blk) + l : p.Af + l * p.lda;
+    const float* ab = kA == kAFloatT ? a_base + l : a_base + l * p.lda;
 #pragma unroll
     for (int t = 0; t < T::PB; ++t) copy16_to_lds_s(bb, o.b[t], &st.b[(t * 256 + wave * 64) * 4]);
 #pragma unroll
@@ -683,8 +684,9 @@ __device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA, kBI,
     const int tail = static_cast<int>((l1 - l0) % kMStage);
     const int64_t chunks = full + (tail ? 1 : 0);
     const int wave = wi * 2 + wj;
+    const float* a_base = a_block<kA>(p, i_blk);  // the copies' A base, once per tile
     auto issue = [&](MStage<kA, kBI, kBJ>& buf, int64_t l, int64_t end) {
-        if (l + kMStage <= end) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave, i_blk);
+        if (l + kMStage <= end) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave, a_base);
         else missue_stage<kA, kBI, kBJ>(p, buf, i_blk, j_blk, l, end - 1, tid);
     };
     if (!primed) issue(st[0], l0, l1);
