@@ -467,7 +467,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 // kBI MFMAs: the 4 x 4 waves of the large launches spend about 6% of the matrix core's cycles on them, the 1 x 1 waves
 // of the smallest grids about a quarter.
 typedef double mf_v4d __attribute__((ext_vector_type(4)));
-constexpr int kMStage = 32;  // l per LDS stage
+constexpr int kMStage = 32;  // l per LDS stage (the 32 x 32 tiles take twice as many: MTile::S)
 
 // A workgroup tile of 2 x 2 waves, each wave kBI x kBJ MFMA blocks of 16 x 16: (32 kBI) x (32 kBJ) outputs. The
 // step's large matmuls take 4 x 4 (128 x 128 tiles); launches whose 128 x 128 grid would leave most CUs idle take
@@ -476,16 +476,19 @@ template <int kBI, int kBJ>
 struct MTile {
     static constexpr int I = 32 * kBI;                     // workgroup tile along i
     static constexpr int J = 32 * kBJ;                     // workgroup tile along j
-    static constexpr int PA = kMStage * I / 4 / 256;       // 16-byte copies per thread per stage
-    static constexpr int PB = kMStage * J / 4 / 256;
+    // l per stage: the smallest tiles' stages are short on compute next to a copy's round trip, so they take 64
+    // (c1 34.2-34.4 -> 34.0 ms per step; 128 for them, or 64 for the 64 x 64 tiles too, measured 34.8-35.0)
+    static constexpr int S = kBI == 1 && kBJ == 1 ? 2 * kMStage : kMStage;
+    static constexpr int PA = S * I / 4 / 256;             // 16-byte copies per thread per stage
+    static constexpr int PB = S * J / 4 / 256;
     static constexpr bool swizzle = I >= 64 && J >= 64;  // the l % 4 chunk permutation needs 16 chunks a row
-    static_assert(kMStage * I % 1024 == 0 && kMStage * J % 1024 == 0, "whole copies per thread");
+    static_assert(S * I % 1024 == 0 && S * J % 1024 == 0, "whole copies per thread");
 };
 
 template <int kA, int kBI, int kBJ>
 struct MStage {
-    float a[kMStage * MTile<kBI, kBJ>::I];  // A rows: [l][i ^ 16 (l % 4)]; A transposed: [l / 4][i][l % 4]
-    float b[kMStage * MTile<kBI, kBJ>::J];  // A rows: [l][j ^ 16 (l % 4)]; A transposed: [l][j]
+    float a[MTile<kBI, kBJ>::S * MTile<kBI, kBJ>::I];  // A rows: [l][i ^ 16 (l % 4)]; A transposed: [l / 4][i][l % 4]
+    float b[MTile<kBI, kBJ>::S * MTile<kBI, kBJ>::J];  // A rows: [l][j ^ 16 (l % 4)]; A transposed: [l][j]
 };
 
 // Row-major stage rows of 128 floats (512 bytes) put the 4 rows a fragment read spans (l = 4s .. 4s + 3, one per
@@ -630,14 +633,15 @@ __device__ __forceinline__ void mfma_step(const double (&a)[kBI], const double (
 template <int kA, int kBI, int kBJ>
 __device__ __forceinline__ void mstage_full(const MStage<kA, kBI, kBJ>& st, int wi, int wj, int lane,
                                             mf_v4d (&acc)[kBI][kBJ]) {
+    using T = MTile<kBI, kBJ>;
     double a[kBI], b[kBJ];
     mread_frags<kA, kBI, kBJ>(st, 0, wi, wj, lane, a, b);
 #pragma unroll
-    for (int s = 0; s < kMStage / 4; ++s) {
+    for (int s = 0; s < T::S / 4; ++s) {
         double an[kBI], bn[kBJ];
-        if (s + 1 < kMStage / 4) mread_frags<kA, kBI, kBJ>(st, s + 1, wi, wj, lane, an, bn);
+        if (s + 1 < T::S / 4) mread_frags<kA, kBI, kBJ>(st, s + 1, wi, wj, lane, an, bn);
         mfma_step<kBI, kBJ>(a, b, acc);
-        if (s + 1 < kMStage / 4) {
+        if (s + 1 < T::S / 4) {
 #pragma unroll
             for (int q = 0; q < kBI; ++q) a[q] = an[q];
 #pragma unroll
@@ -680,19 +684,19 @@ __device__ __forceinline__ void maccumulate(const GemmParams& p, MStage<kA, kBI,
         for (int bj = 0; bj < kBJ; ++bj) acc[bi][bj] = mf_v4d{0.0, 0.0, 0.0, 0.0};
     if (l0 >= l1) return;
     const int64_t last = l1 - 1;
-    const int64_t full = (l1 - l0) / kMStage;
-    const int tail = static_cast<int>((l1 - l0) % kMStage);
+    const int64_t full = (l1 - l0) / T::S;
+    const int tail = static_cast<int>((l1 - l0) % T::S);
     const int64_t chunks = full + (tail ? 1 : 0);
     const int wave = wi * 2 + wj;
     const float* a_base = a_block<kA>(p, i_blk);  // the copies' A base, once per tile
     auto issue = [&](MStage<kA, kBI, kBJ>& buf, int64_t l, int64_t end) {
-        if (l + kMStage <= end) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave, a_base);
+        if (l + T::S <= end) missue_full<kA, kBI, kBJ>(p, buf, o, l, wave, a_base);
         else missue_stage<kA, kBI, kBJ>(p, buf, i_blk, j_blk, l, end - 1, tid);
     };
     if (!primed) issue(st[0], l0, l1);
     for (int64_t c = 0; c < full; ++c) {
         if (c + 1 < chunks) {
-            issue(st[(c + 1) & 1], l0 + (c + 1) * kMStage, l1);
+            issue(st[(c + 1) & 1], l0 + (c + 1) * T::S, l1);
             wait_stage<T::PA + T::PB>();  // this stage landed; the next one's copies in flight
         } else {
             wait_stage<0>();
@@ -1020,11 +1024,11 @@ int64_t padded_rows(int64_t n) { return static_cast<int64_t>(round_up(static_cas
 namespace {
 
 // Whether the matrix-core kernel's 32-bit per-lane copy offsets reach every element of a workgroup's block: 128 A
-// rows (transposed) or 32 stage rows of A and B, from the block's base.
+// rows (transposed) or a stage's rows of A and B (at most 64), from the block's base.
 bool mfma_offsets_fit(const GemmCall& g) {
     constexpr int64_t kLimit = int64_t{1} << 32;
-    const int64_t a = g.a_kind == kAFloatT ? 128 * g.lda : 32 * g.lda + g.I;
-    return 4 * a < kLimit && 4 * (32 * g.ldb + g.J) < kLimit;
+    const int64_t a = g.a_kind == kAFloatT ? 128 * g.lda : 2 * kMStage * g.lda + g.I;
+    return 4 * a < kLimit && 4 * (2 * kMStage * g.ldb + g.J) < kLimit;
 }
 
 // Whether a float-A call fits the matrix-core kernel's 16-byte staging (the conditions launch_gemm requires).
