@@ -177,6 +177,10 @@ int dllm_hip_rope(const float* x, const int64_t* positions, const double* inv_fr
     double* st = c.take<double>(tokens * half);
     DLLM_REQUIRE(!c.overflow, "workspace layout overflow");
     const hipStream_t s = as_stream(stream);
+    if (half + static_cast<int64_t>(head_dim - rotary_dim) <= 64)
+        return launch_rope_direct(x, positions, inv_freq, out, static_cast<int64_t>(tokens), static_cast<int64_t>(heads),
+                                  static_cast<int64_t>(head_dim), static_cast<int64_t>(rotary_dim), interleaved,
+                                  inverse, s);
     DLLM_TRY(launch_rope_tables(positions, static_cast<int64_t>(tokens), inv_freq, half, ct, st, s));
     return launch_rope(x, nullptr, ct, st, out, static_cast<int64_t>(tokens), static_cast<int64_t>(heads),
                        static_cast<int64_t>(head_dim), static_cast<int64_t>(rotary_dim), interleaved, inverse, s);

@@ -164,6 +164,22 @@ __device__ inline double dcos(double x) {
     }
 }
 
+// The sine and cosine of pos x freq, the same values as dsin and dcos of that product: one reduction, both
+// polynomials, and the quadrant picks which one (and its sign) each result takes, with no divergent branch.
+__device__ inline void dsincos(double pos, double freq, double* sin_out, double* cos_out) {
+    const double x = pos * freq;
+    if (dnonfinite(x)) {
+        *sin_out = *cos_out = __longlong_as_double(0x7ff8000000000000LL);
+        return;
+    }
+    int q;
+    const double r = dreduce_half_pi(x, &q);
+    const double ps = dsin_kernel(r), pc = dcos_kernel(r);
+    const double s = (q & 1) ? pc : ps, c = (q & 1) ? ps : pc;
+    *sin_out = (q & 2) ? -s : s;
+    *cos_out = ((q + 1) & 2) ? -c : c;
+}
+
 // tanh (math.hpp:296-319).
 __device__ inline double dtanh(double x) {
     if (x != x) return x;

@@ -117,6 +117,10 @@ int launch_rope_tables(const int64_t* positions, int64_t n, const double* inv_fr
 int launch_rope_pair(const float* x1, float* out1, int64_t heads1, const float* x2, float* out2, int64_t heads2,
                      const int64_t* pos_index, const double* cos_table, const double* sin_table, int64_t tokens,
                      int64_t head_dim, int64_t rotary_dim, int inverse, hipStream_t stream);
+// rope without tables (cos and sin computed per token in the kernel); rows of at most 64 elements
+int launch_rope_direct(const float* x, const int64_t* positions, const double* inv_freq, float* out, int64_t tokens,
+                       int64_t heads, int64_t head_dim, int64_t rotary_dim, int interleaved, int inverse,
+                       hipStream_t stream);
 int launch_rope(const float* x, const int64_t* pos_index, const double* cos_table, const double* sin_table,
                 float* out, int64_t tokens, int64_t heads, int64_t head_dim, int64_t rotary_dim, int interleaved,
                 int inverse, hipStream_t stream);

@@ -111,6 +111,20 @@ def test_rope(K, ora, rotary, theta, interleaved):
                     f"rope inverse={inverse}")
 
 
+# Head counts past four rows per wave (the in-kernel cos/sin path batches four heads' loads), partial rotary, and a
+# 256-wide head (rows of 128 elements: the table path).
+@pytest.mark.parametrize(("heads", "hd", "rotary"), [(14, 64, 64), (2, 64, 64), (7, 128, 128), (9, 96, 32),
+                                                     (4, 256, 256), (17, 16, 16)])
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope_many_heads(K, ora, heads, hd, rotary, interleaved):
+    x = O.gaussian(10, 37, heads, hd)
+    pos = (np.arange(37, dtype=np.int64) * 977) % 5003
+    inv = O.rope_inv_freq(rotary, 1e6)
+    for inverse in (False, True):
+        assert_same(K.rope(x, pos, inv, interleaved, inverse), ora.rope(x, pos, inv, interleaved, inverse),
+                    f"rope heads={heads} hd={hd} rotary={rotary} inverse={inverse}")
+
+
 @pytest.mark.parametrize(("q_len", "kv_len", "heads", "kvh", "hd", "window", "softcap", "offset", "causal"), [
     (9, 9, 6, 2, 8, 0, 0.0, 0, True),
     (5, 9, 6, 2, 8, 0, 0.0, 4, True),
