@@ -173,7 +173,8 @@ int launch_moe_route(const float* logits, int64_t rows, int64_t experts, int64_t
 int launch_moe_route_backward(const float* logits, const int64_t* indices, const float* dweights, const float* dprob,
                               int64_t rows, int64_t experts, int64_t k, int normalize, float* dlogits,
                               hipStream_t stream);
-// out[r] = (0 + the row's k terms in expert order) + addend[r]; term = y[order] * weights[slot] or y[order].
+// out[r] = (0 + the row's k terms in expert order) + addend[r] (addend may be null: no addition); term =
+// y[order] * weights[slot] or y[order].
 int launch_moe_combine(const float* y, const int64_t* order, const int64_t* slot, const float* weights,
                        const float* addend, float* out, int64_t rows, int64_t k, int64_t dim, hipStream_t stream);
 // dweights[slot[p]] = dot(dout[row_of[p]], y[p]) and dy[p] = dout[row_of[p]] * weights[slot[p]] per position p.

@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
             const float v = y[p * H + d];
             acc = acc + (weights ? v * weights[slot[p]] : v);
         }
-        out[i] = acc + addend[i];
+        out[i] = addend ? acc + addend[i] : acc;
     }
 }
 
@@ -336,8 +336,11 @@ __global__ __launch_bounds__(256) void moe_combine4_kernel(const float4* __restr
                 acc.w = acc.w + v.w;
             }
         }
-        const float4 a = addend[r * H4 + d];
-        out[r * H4 + d] = float4{acc.x + a.x, acc.y + a.y, acc.z + a.z, acc.w + a.w};
+        if (addend) {
+            const float4 a = addend[r * H4 + d];
+            acc = float4{acc.x + a.x, acc.y + a.y, acc.z + a.z, acc.w + a.w};
+        }
+        out[r * H4 + d] = acc;
     }
 }
 

@@ -1336,8 +1336,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * I, s, act()));
         if (post_norms()) {  // x_out = x_mid + post_norm(mlp)
             DLLM_TRY(linear_fwd(sv.product, R, I, L.down, nullptr, sv.mlp, nullptr, s));
-            DLLM_TRY(launch_rms_norm(sv.mlp, P(L.mlp_post), post_tmp, R, H, eps, uo(), nullptr, s));
-            return launch_add(sv.x_mid, post_tmp, x_out, R * H, s);
+            return mlp_post_norm(l, R, x_out, s);
         }
         return linear_fwd(sv.product, R, I, L.down, nullptr, x_out, sv.x_mid, s);  // x_out = x_mid + mlp
     }
@@ -1359,7 +1358,7 @@ struct dllm_hip_trainer {
         if (sparse(l)) {
             DLLM_TRY(side_wait(kSideMlp, s));      // the previous layer's router dW reads dlogits_r
             DLLM_TRY(side_wait(kSideNormMlp, s));  // its mlp norm's dW reads dh
-            DLLM_TRY(moe_backward(l, R, nseg, s));
+            DLLM_TRY(moe_backward(l, R, nseg, dmlp, s));
         } else {
             // SwiGLU (backprop.py:289-306)
             DLLM_TRY(linear_dx(dmlp, R, L.down, dproduct, nullptr, s));
@@ -1695,7 +1694,12 @@ struct dllm_hip_trainer {
         DLLM_TRY(expert_matmul(sv, kFwdUp, s));
         DLLM_TRY(launch_swiglu_forward(sv.gate, sv.up, sv.gate_act, sv.product, R * K * EI, s, act()));
         DLLM_TRY(expert_matmul(sv, kFwdDown, s));
-        if (c.shared_inter == 0) return launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sv.x_mid, x_out, R, K, H, s);
+        // with post norms (backprop.py:462-463) the experts' sum is the MLP output sv.mlp, normalised, then added
+        if (c.shared_inter == 0) {
+            if (!post_norms()) return launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sv.x_mid, x_out, R, K, H, s);
+            DLLM_TRY(launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, nullptr, sv.mlp, R, K, H, s));
+            return mlp_post_norm(l, R, x_out, s);
+        }
         // the shared expert over every row; out = (0 + the row's experts' f32(y w), ascending) + its (gated) output,
         // then x_out = x_mid + out (backprop.py:519-525)
         const int64_t SI = c.shared_inter;
@@ -1704,16 +1708,29 @@ struct dllm_hip_trainer {
         DLLM_TRY(launch_swiglu_forward(sv.sh_gate, sv.sh_up, sv.sh_act, sv.sh_product, R * SI, s, act()));
         DLLM_TRY(linear_fwd(sv.sh_product, R, SI, L.sdown, nullptr, sv.sh_y, nullptr, s));
         DLLM_TRY(launch_shared_gate_forward(sv.h2, L.sgw >= 0 ? P(L.sgw) : nullptr, sv.sh_y, sv.sh_s, sh_term, R, H, s));
+        if (post_norms()) {
+            DLLM_TRY(launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sh_term, sv.mlp, R, K, H, s));
+            return mlp_post_norm(l, R, x_out, s);
+        }
         DLLM_TRY(launch_moe_combine(sv.y, sv.order, sv.slot, sv.routing, sh_term, sh_out, R, K, H, s));
         return launch_add(sv.x_mid, sh_out, x_out, R * H, s);
     }
 
-    // _experts_backward (backprop.py:308-357): dh (dh2) from dx (the gradient of the layer's MLP output).
-    int moe_backward(int64_t l, int64_t R, int nseg, hipStream_t s) {
+    // x_out = x_mid + post_norm(mlp) (backprop.py:462-463)
+    int mlp_post_norm(int64_t l, int64_t R, float* x_out, hipStream_t s) {
+        const LayerIds& L = layer_ids[static_cast<size_t>(l)];
+        const Saved& sv = saved[static_cast<size_t>(l)];
+        DLLM_TRY(launch_rms_norm(sv.mlp, P(L.mlp_post), post_tmp, R, H, c.rms_norm_eps, uo(), nullptr, s));
+        return launch_add(sv.x_mid, post_tmp, x_out, R * H, s);
+    }
+
+    // _experts_backward (backprop.py:308-357): dh (dh2) from dmlp, the gradient of the layer's MLP output (dx, or
+    // with post norms the gradient through the MLP's post norm).
+    int moe_backward(int64_t l, int64_t R, int nseg, const float* dmlp, hipStream_t s) {
         const LayerIds& L = layer_ids[static_cast<size_t>(l)];
         const Saved& sv = saved[static_cast<size_t>(l)];
         const int64_t P = R * K;
-        DLLM_TRY(launch_moe_dweights(dx, sv.y, sv.row_of, sv.slot, sv.routing, P, H, dweights, dyg, s));
+        DLLM_TRY(launch_moe_dweights(dmlp, sv.y, sv.row_of, sv.slot, sv.routing, P, H, dweights, dyg, s));
         DLLM_TRY(launch_gather_rows(sv.h2, sv.row_of, xg, P, H, s));
         DLLM_TRY(expert_matmul(sv, kDxDown, s));
         DLLM_TRY(expert_matmul(sv, kDwDown, s));
@@ -1738,10 +1755,10 @@ struct dllm_hip_trainer {
         // with a shared expert (backprop.py:339-352): dh2 = (((0 + experts' dx) + shared dx) + gate dx) + router dx
         const int64_t SI = c.shared_inter;
         const bool gated = L.sgw >= 0;
-        const float* dys = dx;
+        const float* dys = dmlp;
         if (gated) {
             const bool gate_dw = grad_wanted(G(L.sgw));
-            DLLM_TRY(launch_shared_gate_backward(dx, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, dsh_dy, dsh_score, nullptr,
+            DLLM_TRY(launch_shared_gate_backward(dmlp, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, dsh_dy, dsh_score, nullptr,
                                                  seg_d, nseg, gate_dw ? sh_part : nullptr, R, H, s));
             if (gate_dw) DLLM_TRY(launch_segment_sums(sh_part, H, nseg, window_weights(), G(L.sgw), s));
             dys = dsh_dy;
@@ -1755,7 +1772,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(side_fork_from(s, &sws));
         DLLM_TRY(linear_dw(dys, H, sv.sh_product, SI, nseg, G(L.sdown), nullptr, nullptr, sws, nullptr, -1,
                            unfold_scale(L.sdown)));
-        if (dys == dx) DLLM_TRY(side_mark(kSideDown));
+        if (dys == dx) DLLM_TRY(side_mark(kSideDown));  // (with post norms the step runs on one stream)
         DLLM_TRY(linear_dw(dsh_gate, SI, sv.h2, H, nseg, G(L.sgate), nullptr, nullptr, sws));
         DLLM_TRY(linear_dw(dsh_up, SI, sv.h2, H, nseg, G(L.sup), nullptr, nullptr, sws));
         DLLM_TRY(side_mark(kSideMlp));
@@ -1763,7 +1780,7 @@ struct dllm_hip_trainer {
         DLLM_TRY(linear_dx(dsh_up, R, L.sup, dsh_x, dsh_x, s));  // dx_gate + dx_up
         DLLM_TRY(launch_moe_combine(dxg, sv.order, sv.slot, nullptr, dsh_x, dh, R, K, H, s));
         if (gated)  // + f32(dscore w), the gate's input gradient
-            DLLM_TRY(launch_shared_gate_backward(dx, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, nullptr, dsh_score, dh,
+            DLLM_TRY(launch_shared_gate_backward(dmlp, sv.sh_y, sv.sh_s, this->P(L.sgw), sv.h2, nullptr, dsh_score, dh,
                                                  seg_d, nseg, nullptr, R, H, s));
         return launch_add(dh, dh2r, dh, R * H, s);
     }
@@ -2307,7 +2324,6 @@ int dllm_hip_trainer_create_lora(const dllm_hip_decoder_config* config, const dl
         DLLM_REQUIRE(m >= 0.0 && std::isfinite(m), "multipliers must be finite and non-negative (0: none)");
     DLLM_REQUIRE(c.attention_scale > 0.0 && std::isfinite(c.attention_scale), "attention_scale must be positive");
     DLLM_REQUIRE(c.norm_placement >= 0 && c.norm_placement <= 2, "norm_placement must be 0 (pre), 1 (post) or 2 (both)");
-    DLLM_REQUIRE(c.norm_placement == 0 || c.experts == 0, "post norms are built for dense MLPs only");
     DLLM_REQUIRE(c.shared_inter >= 0, "the shared expert's size must not be negative");
     DLLM_REQUIRE(c.shared_inter == 0 || c.experts > 0, "a shared expert needs routed experts");
     DLLM_REQUIRE(c.shared_gate == 0 || c.shared_inter > 0, "a shared expert gate needs a shared expert");

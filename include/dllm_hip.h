@@ -290,7 +290,7 @@ typedef struct {
      * any depth) */
     int64_t dense_layers;
     /* norm_placement (architecture.py:315-320): 0 pre (RMSNorm on each block's input), 1 post (on each block's
-     * output before the residual add, OLMo 2), 2 both; post norms with routed experts are not built */
+     * output before the residual add, OLMo 2), 2 both; with routed experts too */
     int64_t norm_placement;
     /* Gemma 2 and 3 (architecture.py, importer.py:283-345): norms with 1 + w (norm_unit_offset); the MLP's activation
      * 0 SiLU, 1 GELU-tanh; full_attention_layers: bit l set = layer l ignores sliding_window (the layers outside

@@ -576,6 +576,15 @@ NORM_CASES = {
                          attention_softcap=50.0, logits_softcap=30.0),
     "head96": O.Decoder("phi3", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=4, head_dim=96,
                         eps=1e-5, rope_theta=1e4, tied=False, window=40),
+    # post norms around routed experts (backprop.py:224-229, 462-463: the experts' sum is the normalised MLP output)
+    "post_moe": O.Decoder("olmoe", vocab=256, hidden=64, inter=48, layers=2, heads=4, kv_heads=2, head_dim=16,
+                          eps=1e-6, rope_theta=5e5, tied=False, qk_norm=2, norm_placement=1, experts=4, topk=2,
+                          normalize=False),
+    # sandwich norms with unit offsets around routed experts and a gated shared expert, layer 0 dense
+    "sandwich_moe": O.Decoder("qwen2_moe", vocab=256, hidden=64, inter=96, layers=2, heads=4, kv_heads=2,
+                              head_dim=16, eps=1e-5, rope_theta=1e4, tied=True, norm_placement=2, unit_offset=True,
+                              experts=4, topk=2, normalize=True, expert_inter=24, shared_inter=40, shared_gate=True,
+                              dense_layers=(0,)),
 }
 
 
