@@ -103,15 +103,27 @@ __device__ __forceinline__ void row_span(const TileParams& p, int64_t r, int64_t
 
 // B arrives as floats and is widened to double once, when its stage is written to LDS: each of the 4 lanes of a wave
 // (and the 4 waves) that read a B value takes it ready, and the inner loop has no conversions.
+// CJ = 1, 2, 4: a workgroup covers 64 CJ columns, a lane 4 CJ of them; CJ = 0: 32 columns, a lane 2 of them (small
+// grids: half the multiply-adds per step and twice the workgroups).
+template <int CJ>
+constexpr int tile_cols() {
+    return CJ == 0 ? 32 : 64 * CJ;
+}
+
+template <int CJ>
+constexpr int lane_cols() {
+    return CJ == 0 ? 2 : 4 * CJ;
+}
+
 template <int CJ>
 struct Stage {
     double a[kChunk][kTileRows];
-    double b[kChunk][64 * CJ];
+    double b[kChunk][tile_cols<CJ>()];
 };
 
 template <int CJ>
 constexpr int stage_copies() {
-    return 2 + 2 * CJ;
+    return CJ == 0 ? 3 : 2 + 2 * CJ;
 }
 
 // Waits until at most `pending` of this wave's vector-memory operations are outstanding and its LDS writes have
@@ -179,7 +191,7 @@ struct LaneCopy {
 // registers, which store_stage_b widens and writes once the current stage has been computed.
 template <int CJ>
 __device__ __forceinline__ void issue_stage(Stage<CJ>& st, const StageCursor& c, const LaneCopy& lc, int64_t last,
-                                            int wave, int lane, float2 (&breg)[2 * CJ]) {
+                                            int wave, int lane, float2 (&breg)[CJ == 0 ? 2 : 2 * CJ]) {
     const int64_t left = last - c.l;  // the stage's steps past this one repeat it
     const uint32_t d = static_cast<uint32_t>(left < kChunk ? left : kChunk);
 #pragma unroll
@@ -188,12 +200,12 @@ __device__ __forceinline__ void issue_stage(Stage<CJ>& st, const StageCursor& c,
         const uint32_t off = (r < d ? r : d) * lc.a_ld8 + lc.a_col;
         copy16_to_lds_s(c.a, off, &st.a[4 * wave + 2 * t][0]);
     }
-    constexpr int kLanesPerRow = 16 * CJ;
+    constexpr int kLanesPerRow = CJ == 0 ? 16 : 16 * CJ;
     constexpr int kRowsPerCopy = 64 / kLanesPerRow;
     const int sub = lane / kLanesPerRow;
     const char* b = reinterpret_cast<const char*>(c.b);
 #pragma unroll
-    for (int t = 0; t < CJ; ++t) {
+    for (int t = 0; t < (CJ == 0 ? 1 : CJ); ++t) {
         const uint32_t r = static_cast<uint32_t>(4 * wave + t * kRowsPerCopy + sub);
         const uint32_t rr = r < d ? r : d;
         uint32_t off;
@@ -204,21 +216,22 @@ __device__ __forceinline__ void issue_stage(Stage<CJ>& st, const StageCursor& c,
             off = q * lc.b_ld4 + (x - q * lc.group) * lc.b_in4;
         }
         breg[2 * t] = *reinterpret_cast<const float2*>(b + static_cast<uint64_t>(off + lc.b_col[0]));
-        breg[2 * t + 1] = *reinterpret_cast<const float2*>(b + static_cast<uint64_t>(off + lc.b_col[1]));
+        if (CJ != 0) breg[2 * t + 1] = *reinterpret_cast<const float2*>(b + static_cast<uint64_t>(off + lc.b_col[1]));
     }
 }
 
 template <int CJ>
-__device__ __forceinline__ void store_stage_b(Stage<CJ>& st, int wave, int lane, const float2 (&breg)[2 * CJ]) {
-    constexpr int kLanesPerRow = 16 * CJ;
+__device__ __forceinline__ void store_stage_b(Stage<CJ>& st, int wave, int lane,
+                                              const float2 (&breg)[CJ == 0 ? 2 : 2 * CJ]) {
+    constexpr int kLanesPerRow = CJ == 0 ? 16 : 16 * CJ;
     constexpr int kRowsPerCopy = 64 / kLanesPerRow;
     const int sub = lane / kLanesPerRow, q = lane % kLanesPerRow;
     const int col = 64 * (q >> 4) + 2 * (q & 15);
 #pragma unroll
-    for (int t = 0; t < CJ; ++t) {
+    for (int t = 0; t < (CJ == 0 ? 1 : CJ); ++t) {
         double* row = &st.b[4 * wave + t * kRowsPerCopy + sub][0];
         *reinterpret_cast<double2*>(row + col) = double2{breg[2 * t].x, breg[2 * t].y};
-        *reinterpret_cast<double2*>(row + col + 32) = double2{breg[2 * t + 1].x, breg[2 * t + 1].y};
+        if (CJ != 0) *reinterpret_cast<double2*>(row + col + 32) = double2{breg[2 * t + 1].x, breg[2 * t + 1].y};
     }
 }
 
@@ -228,18 +241,25 @@ __device__ __forceinline__ void store_stage_b(Stage<CJ>& st, int wave, int lane,
 // contiguous bytes): 32 + 16 CJ bytes per lane for 16 CJ multiply-adds.
 template <int CJ>
 __device__ __forceinline__ int64_t tile_column(int c, int cg) {
+    if (CJ == 0) return 2 * cg + c;
     return 64 * (c >> 2) + ((c & 2) ? 32 : 0) + 2 * cg + (c & 1);
 }
 
 template <int CJ>
 __device__ __forceinline__ void read_step(const Stage<CJ>& st, int k, int wave, int rg, int cg, double (&a)[4],
-                                          double (&b)[4 * CJ]) {
+                                          double (&b)[lane_cols<CJ>()]) {
     const double2* ar = reinterpret_cast<const double2*>(&st.a[k][wave * 16 + 4 * rg]);
     const double2 a01 = ar[0], a23 = ar[1];
     a[0] = a01.x;
     a[1] = a01.y;
     a[2] = a23.x;
     a[3] = a23.y;
+    if (CJ == 0) {
+        const double2 b01 = *reinterpret_cast<const double2*>(&st.b[k][2 * cg]);
+        b[0] = b01.x;
+        b[1] = b01.y;
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < CJ; ++c) {
         const double2 b01 = *reinterpret_cast<const double2*>(&st.b[k][64 * c + 2 * cg]);
@@ -253,11 +273,11 @@ __device__ __forceinline__ void read_step(const Stage<CJ>& st, int k, int wave, 
 
 // One step on the lane's tile: each product rounded, then added (the reference's multiply, then add).
 template <int CJ>
-__device__ __forceinline__ void step_tile(double (&acc)[4][4 * CJ], const double (&a)[4], const double (&b)[4 * CJ]) {
+__device__ __forceinline__ void step_tile(double (&acc)[4][lane_cols<CJ>()], const double (&a)[4], const double (&b)[lane_cols<CJ>()]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int c = 0; c < 4 * CJ; ++c) {
+        for (int c = 0; c < lane_cols<CJ>(); ++c) {
             const double prod = a[i] * b[c];
             acc[i][c] = acc[i][c] + prod;
         }
@@ -265,19 +285,19 @@ __device__ __forceinline__ void step_tile(double (&acc)[4][4 * CJ], const double
 
 // A full stage (every row takes every step), the next step's operands read while the current step computes.
 template <int CJ>
-__device__ __forceinline__ void stage_all(const Stage<CJ>& st, int wave, int rg, int cg, double (&acc)[4][4 * CJ]) {
-    double a[4], b[4 * CJ];
+__device__ __forceinline__ void stage_all(const Stage<CJ>& st, int wave, int rg, int cg, double (&acc)[4][lane_cols<CJ>()]) {
+    double a[4], b[lane_cols<CJ>()];
     read_step<CJ>(st, 0, wave, rg, cg, a, b);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        double an[4], bn[4 * CJ];
+        double an[4], bn[lane_cols<CJ>()];
         if (k + 1 < kChunk) read_step<CJ>(st, k + 1, wave, rg, cg, an, bn);
         step_tile<CJ>(acc, a, b);
         if (k + 1 < kChunk) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) a[i] = an[i];
 #pragma unroll
-            for (int c = 0; c < 4 * CJ; ++c) b[c] = bn[c];
+            for (int c = 0; c < lane_cols<CJ>(); ++c) b[c] = bn[c];
         }
     }
 }
@@ -306,14 +326,14 @@ __device__ __forceinline__ uint32_t rows_taking(const TileParams& p, int64_t l, 
 // operands are read while the current one computes.
 template <int CJ>
 __device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ>& st, int wave, int rg, int cg,
-                                             int64_t l0, int n, int64_t tw, int64_t I, double (&acc)[4][4 * CJ]) {
+                                             int64_t l0, int n, int64_t tw, int64_t I, double (&acc)[4][lane_cols<CJ>()]) {
     const uint32_t G = p.mask == kMaskKeyRows ? static_cast<uint32_t>(p.group) : 1u;
     uint32_t t = static_cast<uint32_t>(l0) / G;  // steps of one (window, head) stay below 2^31
     uint32_t r = static_cast<uint32_t>(l0) - t * G;
-    double a[4], b[4 * CJ];
+    double a[4], b[lane_cols<CJ>()];
     read_step<CJ>(st, 0, wave, rg, cg, a, b);
     for (int k = 0; k < n; ++k) {
-        double an[4], bn[4 * CJ];
+        double an[4], bn[lane_cols<CJ>()];
         read_step<CJ>(st, k + 1 < n ? k + 1 : k, wave, rg, cg, an, bn);
         const uint32_t take = __builtin_amdgcn_readfirstlane(rows_taking(p, l0 + k, t, tw, I));
         const uint32_t mine = take >> (4 * rg);
@@ -321,7 +341,7 @@ __device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ
         for (int i = 0; i < 4; ++i) {
             if ((mine >> i) & 1u) {
 #pragma unroll
-                for (int c = 0; c < 4 * CJ; ++c) {
+                for (int c = 0; c < lane_cols<CJ>(); ++c) {
                     const double prod = a[i] * b[c];
                     acc[i][c] = acc[i][c] + prod;
                 }
@@ -330,7 +350,7 @@ __device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ
 #pragma unroll
         for (int i = 0; i < 4; ++i) a[i] = an[i];
 #pragma unroll
-        for (int c = 0; c < 4 * CJ; ++c) b[c] = bn[c];
+        for (int c = 0; c < lane_cols<CJ>(); ++c) b[c] = bn[c];
         if (++r == G) {
             r = 0;
             ++t;
@@ -339,7 +359,7 @@ __device__ __forceinline__ void stage_masked(const TileParams& p, const Stage<CJ
 }
 
 template <int CJ>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4 : 2))) void attn_tile_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ <= 1 ? 4 : 2))) void attn_tile_kernel(
     TileParams p) {
     __shared__ __align__(16) Stage<CJ> st[2];
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
@@ -359,7 +379,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     const int64_t seg_w = uniform64(p.seg[w]), n = uniform64(p.seg[w + 1]) - seg_w;
     const int64_t I = p.rows_kind == 0 ? n : p.head_dim;
     const int64_t J = p.cols_kind == 0 ? n : p.head_dim;
-    const int64_t i0 = ti * kTileRows, j0 = tj * 64 * CJ;
+    const int64_t i0 = ti * kTileRows, j0 = tj * tile_cols<CJ>();
     if (i0 >= I || j0 >= J) return;
     // spans are intervals whose ends grow with the row: the tile's steps are [lo(first row), hi(last row)), and the
     // steps every row of this wave takes are [lo(its last row), hi(its first row))
@@ -377,7 +397,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     lc.a_col = static_cast<uint32_t>((lane & 31) * 16);
     lc.a_ld8 = static_cast<uint32_t>(o.A.ld * 8);
     {
-        const int q = lane % (16 * CJ);
+        const int q = lane % (CJ == 0 ? 16 : 16 * CJ);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int64_t col = j0 + 64 * (q >> 4) + 32 * h + 2 * (q & 15);
@@ -394,15 +414,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
     cur.rs = t_lo % o.B.group;
     cur.b = op_base<float>(o.B, w, seg_w, hz) + (t_lo / o.B.group) * o.B.ld;
     const int rg = lane >> 4, cg = lane & 15;
-    double acc[4][4 * CJ];
+    double acc[4][lane_cols<CJ>()];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int c = 0; c < 4 * CJ; ++c) acc[q][c] = 0.0;
+        for (int c = 0; c < lane_cols<CJ>(); ++c) acc[q][c] = 0.0;
     const int64_t steps = t_hi - t_lo;
     const int64_t stages = steps > 0 ? (steps + kChunk - 1) / kChunk : 0;
     const int64_t last = t_hi - 1;
-    float2 breg[2 * CJ];
+    float2 breg[CJ == 0 ? 2 : 2 * CJ];
     if (stages > 0) {
         issue_stage<CJ>(st[0], cur, lc, last, wave, lane, breg);
         store_stage_b<CJ>(st[0], wave, lane, breg);
@@ -439,7 +459,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CJ == 1 ? 4
         if (tw + q >= I) break;
         const double scale = rs ? rs[q] : 1.0;
 #pragma unroll
-        for (int c = 0; c < 4 * CJ; ++c) {
+        for (int c = 0; c < lane_cols<CJ>(); ++c) {
             const int64_t jl = tile_column<CJ>(c, cg);
             if (j0 + jl >= J) continue;
             double v = acc[i][c];
@@ -688,8 +708,8 @@ int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream) {
     p.b_row_alloc = c.b_row_alloc > 0 ? c.b_row_alloc : J;
     p.a_row_alloc = c.a_row_alloc;
     p.tiles_i = static_cast<int64_t>(ceil_div(I, kTileRows));
-    p.tiles_j = static_cast<int64_t>(ceil_div(J, 64 * cj));
-    DLLM_REQUIRE(cj == 1 || cj == 2 || cj == 4, "attention tiles are 64 rows x 64, 128 or 256 columns");
+    p.tiles_j = static_cast<int64_t>(ceil_div(J, cj == 0 ? 32 : 64 * cj));
+    DLLM_REQUIRE(cj == 0 || cj == 1 || cj == 2 || cj == 4, "attention tiles are 64 rows x 32, 64, 128 or 256 columns");
     DLLM_REQUIRE(p.b_row_alloc % 4 == 0 && p.b_row_alloc >= J, "attention operand rows must hold whole 16-byte chunks");
     if (c.a_float)
         DLLM_REQUIRE(c.exact_products && cj == 4 && c.mask != kMaskQueryRows && c.mask != kMaskKeyRows &&
@@ -716,7 +736,8 @@ int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream) {
                      "double A operands are the probability and dS rows (multiply, then add; float outputs)");
         if (cj == 2) hipLaunchKernelGGL(attn_tile_kernel<2>, grid, dim3(256), 0, stream, p);
         else if (cj == 1) hipLaunchKernelGGL(attn_tile_kernel<1>, grid, dim3(256), 0, stream, p);
-        else return fail(kInvalidArgument, "double A operands take 64 or 128 columns per tile");
+        else if (cj == 0) hipLaunchKernelGGL(attn_tile_kernel<0>, grid, dim3(256), 0, stream, p);
+        else return fail(kInvalidArgument, "double A operands take 32, 64 or 128 columns per tile");
     }
     return check_launch("attention tiles");
 }

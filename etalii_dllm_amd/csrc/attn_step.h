@@ -40,7 +40,7 @@ struct AttnTileCall {
     int64_t windows = 0, heads = 0, max_len = 0, head_dim = 0, group = 1, window = 0, L = 0;
     int rows_kind = 0, cols_kind = 0;  // 0: window positions, 1: head_dim
     int mask = kMaskNone;
-    int cols_per_lane = 4;    // 1, 2 or 4: a workgroup covers 64 x cols_per_lane columns
+    int cols_per_lane = 4;    // 1, 2 or 4: a workgroup covers 64 x cols_per_lane columns; 0: 32 columns
     int64_t b_row_alloc = 0;  // floats readable per B row from column 0 (multiple of 4, >= J); 0: J
     bool a_float = false;
     int64_t a_row_alloc = 0;  // a_float: floats readable in each A row (multiple of 4, >= L)
