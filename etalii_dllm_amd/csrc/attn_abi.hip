@@ -124,7 +124,7 @@ AttnTileCall query_sum(const SelfLayout& L, const int64_t* seg, int causal, int6
     c.cols_kind = 1;
     c.L = causal ? 0 : L.n;
     c.mask = causal ? kMaskQueryRows : kMaskNone;
-    c.cols_per_lane = 1;
+    c.cols_per_lane = attn_value_cols(L.n, L.hd, L.nh, 1, 1);
     c.exact_products = false;
     c.out_double = false;
     return c;
@@ -207,7 +207,7 @@ int self_attention_backward(const float* q, const float* k, const float* v, cons
     kc.cols_kind = 1;
     kc.L = causal ? 0 : L.n * G;
     kc.mask = causal ? kMaskKeyRows : kMaskNone;
-    kc.cols_per_lane = 1;
+    kc.cols_per_lane = attn_value_cols(L.n, L.hd, L.nkv, 1, 2);
     kc.exact_products = false;
     kc.out_double = false;
     return launch_attn_tiles(kc, s);

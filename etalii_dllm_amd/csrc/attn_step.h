@@ -54,6 +54,18 @@ struct AttnTileCall {
 };
 
 int launch_attn_tiles(const AttnTileCall& c, hipStream_t stream);
+
+#ifndef DLLM_ATTN_NARROW_BELOW
+#define DLLM_ATTN_NARROW_BELOW 1024
+#endif
+// cols_per_lane of a head_dim-wide multiply-add output (out, dq, dk/dv) over `rows` rows of `heads` heads in
+// `windows` windows, `sets` matmuls per launch: 64-column tiles (their 4 x 4 register tiles leave room for four waves
+// per SIMD, which keeps the vector ALU busier than wider tiles' A reuse), or 32-column tiles (0) when the 64-column
+// grid would leave the chip short of workgroups: twice the workgroups, each step half the work.
+inline int attn_value_cols(int64_t rows, int64_t head_dim, int64_t heads, int64_t windows, int64_t sets) {
+    const int64_t workgroups = (rows + 63) / 64 * ((head_dim + 63) / 64) * heads * windows * sets;
+    return workgroups < DLLM_ATTN_NARROW_BELOW ? 0 : 1;
+}
 // The forward softmax chains over S^T in place (E^T and inv). With tile maxima (the scores' tile_max, same z and ld
 // layout as there) the maximum comes from them and the scores are walked once; without, twice.
 int launch_softmax_rows(double* st, int64_t ld, int64_t zstride, const int64_t* seg, int64_t windows, int64_t heads,

@@ -1207,7 +1207,7 @@ struct dllm_hip_trainer {
         o.cols_kind = 1;
         o.L = 0;
         o.mask = kMaskQueryRows;
-        o.cols_per_lane = value_cols_per_lane(value_workgroups(n, nh, 1));
+        o.cols_per_lane = value_cols(n, nh, 1);
         o.b_row_alloc = 0;
         o.exact_products = false;
         o.out_double = false;
@@ -1216,15 +1216,9 @@ struct dllm_hip_trainer {
         return launch_attn_tiles(o, s);
     }
 
-    // Columns per lane of the head_dim-wide attention outputs, given the launch's workgroups with 64-column tiles:
-    // 64-column tiles for every head_dim (their 4 x 4 register tiles leave room for four waves per SIMD, the 4 x 8
-    // tiles of 128 columns hold two, which keeps the vector ALU busier than the halved A reuse costs), and 32-column
-    // tiles (cols_per_lane 0) when that grid would leave CUs idle: twice the workgroups, each step half the work.
-    static int value_cols_per_lane(int64_t workgroups64) { return workgroups64 < 512 ? 0 : 1; }
-
-    // Workgroups of a head_dim-wide attention output launch with 64-column tiles.
-    int64_t value_workgroups(int64_t rows, int64_t heads, int64_t sets) const {
-        return ceil_div(rows, 64) * ceil_div(c.head_dim, 64) * nwin * heads * sets;
+    // Columns per lane of a head_dim-wide attention output launch (attn_value_cols).
+    int value_cols(int64_t rows, int64_t heads, int64_t sets) const {
+        return attn_value_cols(rows, c.head_dim, heads, nwin, sets);
     }
 
     // attention_backward (grad.hpp:206-301) of every (window, head): dq_t, dk_t, dv_t from dattended.
@@ -1271,7 +1265,7 @@ struct dllm_hip_trainer {
         q.cols_kind = 1;
         q.L = 0;
         q.mask = kMaskQueryRows;
-        q.cols_per_lane = value_cols_per_lane(value_workgroups(n, nh, 1));
+        q.cols_per_lane = value_cols(n, nh, 1);
         q.b_row_alloc = 0;
         q.exact_products = false;
         q.out_double = false;
@@ -1293,7 +1287,7 @@ struct dllm_hip_trainer {
         k.B2 = AttnOperand{dattended, 0, QD, G * hd, 1, QD, hd, G};
         k.C2 = AttnOperand{dv_t, 0, KVD, hd, 1, KVD, 0, 1};
         k.mask = kMaskKeyRows;
-        k.cols_per_lane = value_cols_per_lane(value_workgroups(n, nkv, 2));
+        k.cols_per_lane = value_cols(n, nkv, 2);
         DLLM_TRY(launch_attn_tiles(k, s));
         if (qs != s) {  // everything after reads dq_t, and the next layer rewrites the dS rows
             DLLM_TRY(check_hip(hipEventRecord(aux_done, qs), "event"));
