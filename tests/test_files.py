@@ -106,3 +106,32 @@ def test_header_sections_follow_write_model_file(F):
 def test_writer_rejects_a_header_without_placeholder(F, tmp_path):
     with pytest.raises(ValueError, match="placeholder"):
         F.write_tensor_file(tmp_path / "x.dllm", 0, b'{"fingerprint":"abc"}', [np.ones(2, np.float32)])
+
+
+# Files written by the reference's own write_model_file (tests/golden/make_model_file_goldens.py): the header bytes,
+# fingerprint and whole-file hash for two architectures, with non-ASCII text, a float that needs 17 digits and the
+# optional sections in the metadata.
+MODEL_FILES = json.loads((Path(__file__).parent / "golden" / "model_file_header.json").read_text(encoding="utf-8"))
+
+
+def golden_tensor_values(name: str, shape) -> np.ndarray:
+    """The tensor values of those files: ((7 i + len(name)) mod 13 - 6) / 8 over the flat index i."""
+    n = int(np.prod(shape)) if len(shape) else 1
+    i = np.arange(n, dtype=np.int64)
+    return (((7 * i + len(name)) % 13 - 6).astype(np.float32) / np.float32(8)).reshape(shape)
+
+
+@pytest.mark.parametrize("case", sorted(MODEL_FILES))
+def test_writer_matches_files_the_reference_wrote(F, tmp_path, case):
+    import oracle_lib as O
+
+    g = MODEL_FILES[case]
+    order = O.tensor_order(g["shapes"])
+    header = F.model_header(g["architecture"], g["shapes"], g["metadata"], order)
+    path = tmp_path / "model.dllm"
+    fingerprint = F.write_tensor_file(path, 0, header, [golden_tensor_values(n, g["shapes"][n]) for n in order])
+    raw = path.read_bytes()
+    length = struct.unpack_from("<Q", raw, 8)[0]
+    assert raw[16:16 + length].decode("utf-8") == g["header"]
+    assert fingerprint == g["fingerprint"] and F.file_fingerprint(path, F.MODEL) == g["fingerprint"]
+    assert len(raw) == g["file_bytes"] and hashlib.sha256(raw).hexdigest() == g["file_sha256"]

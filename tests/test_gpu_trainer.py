@@ -125,6 +125,35 @@ def test_export_and_checkpoint_resume_on_gpu(family, tmp_path):
     assert second.fingerprint(files.CHECKPOINT) == final  # a rejected file leaves the state alone
 
 
+MODEL_FILES = json.loads((Path(__file__).parent / "golden" / "model_file_header.json").read_text(encoding="utf-8"))
+EXPORT_DECODERS = {
+    "llama_tied": O.Decoder("llama", vocab=64, hidden=16, inter=32, layers=2, heads=4, kv_heads=2, head_dim=4,
+                            eps=1e-5, rope_theta=1e5, tied=True),
+    "moe_post_norms": O.Decoder("olmoe", vocab=48, hidden=8, inter=12, layers=2, heads=2, kv_heads=1, head_dim=4,
+                                eps=1e-6, rope_theta=1e4, tied=False, qk_norm=2, norm_placement=1, experts=4, topk=2,
+                                normalize=False, expert_inter=6),
+}
+
+
+@pytest.mark.parametrize("case", sorted(EXPORT_DECODERS))
+def test_export_matches_files_the_reference_wrote(case, tmp_path):
+    """The trainer's export from device memory against model files the reference's own write_model_file wrote
+    (tests/golden/make_model_file_goldens.py): the same bytes, header included."""
+    import hashlib
+
+    from test_files import golden_tensor_values
+
+    d, g = EXPORT_DECODERS[case], MODEL_FILES[case]
+    shapes = d.tensor_shapes()
+    assert {n: list(s) for n, s in shapes.items()} == g["shapes"]
+    t = make_trainer(d, {n: golden_tensor_values(n, s) for n, s in shapes.items()})
+    fingerprint = t.export(tmp_path / "model.dllm", g["architecture"], g["metadata"], shapes)
+    raw = (tmp_path / "model.dllm").read_bytes()
+    assert fingerprint == g["fingerprint"]
+    assert len(raw) == g["file_bytes"] and hashlib.sha256(raw).hexdigest() == g["file_sha256"]
+    t.close()
+
+
 def test_step_matches_the_oracle_on_ragged_windows():
     d = O.Decoder("qwen2", vocab=300, hidden=64, inter=160, layers=2, heads=4, kv_heads=2, head_dim=16, eps=1e-6,
                   rope_theta=1e6, tied=True, attn_bias=True)
