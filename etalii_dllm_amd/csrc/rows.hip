@@ -210,39 +210,45 @@ __global__ __launch_bounds__(256) void column_partial_kernel(int kind, const flo
 // formed; a wave that only runs the chains (two chunks behind, three term buffers) measured no faster.
 constexpr int kCsRing = 8;
 
+template <int kC>
 struct CsSlot {
-    float dy[64][16];
-    float x[64][16];
+    float dy[64][kC];
+    float x[64][kC];
     double inv[64];
 };
 
-__global__ __launch_bounds__(1024) void column_partial_lds_kernel(int kind, const float* __restrict__ dy,
-                                                                  const float* __restrict__ x,
-                                                                  const double* __restrict__ inv, int64_t dim,
-                                                                  ColSegments seg, float* __restrict__ part) {
-    __shared__ __align__(16) CsSlot ring[kCsRing];
-    __shared__ double terms[2][64][16];
+template <int kC>
+__global__ __launch_bounds__(64 * kC) void column_partial_lds_kernel(int kind, const float* __restrict__ dy,
+                                                                     const float* __restrict__ x,
+                                                                     const double* __restrict__ inv, int64_t dim,
+                                                                     ColSegments seg, float* __restrict__ part) {
+    constexpr int kLanesPerRow = kC / 4;            // 16-byte pieces of a row's kC columns
+    constexpr int kRowsPerCopy = 64 / kLanesPerRow;  // rows one wave's copy covers
+    constexpr int kWaves = 64 / kRowsPerCopy;         // waves copying dy (and as many x)
+    __shared__ __align__(16) CsSlot<kC> ring[kCsRing];
+    __shared__ double terms[2][64][kC];
     const int tid = static_cast<int>(threadIdx.x);
     const int wave = tid >> 6, lane = tid & 63;
-    const int c16 = tid & 15, slot = tid >> 4;
-    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int c16 = tid % kC, slot = tid / kC;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kC;
     const int64_t r0 = seg.off[blockIdx.y], r1 = seg.off[blockIdx.y + 1];
     const int64_t chunks = (r1 - r0 + 63) / 64;
     double acc = 0.0;
     if (chunks > 0) {
         const auto issue = [&](int64_t c) {
             const int64_t cc = c < chunks ? c : chunks - 1;
-            CsSlot& dst = ring[cc % kCsRing];
+            CsSlot<kC>& dst = ring[cc % kCsRing];
             const int64_t base = r0 + cc * 64;
-            if (wave < 8) {
-                if (wave >= 4 && kind == 0) return;
-                const int rr = 16 * (wave & 3) + lane / 4;
+            if (wave < 2 * kWaves) {
+                if (wave >= kWaves && kind == 0) return;
+                const int w = wave % kWaves;
+                const int rr = kRowsPerCopy * w + lane / kLanesPerRow;
                 const int64_t r = base + rr < r1 ? base + rr : r1 - 1;
-                const int64_t g = col0 + 4 * (lane & 3) < dim ? col0 + 4 * (lane & 3) : dim - 4;
-                copy16_to_lds((wave < 4 ? dy : x) + r * dim + g,
-                              wave < 4 ? &dst.dy[16 * (wave & 3)][0] : &dst.x[16 * (wave & 3)][0]);
-            } else if (wave < 10 && kind != 0) {
-                const int half = wave - 8;  // rows 32 half .. 32 half + 31, two 4-byte lanes each
+                const int64_t g = col0 + 4 * (lane % kLanesPerRow) < dim ? col0 + 4 * (lane % kLanesPerRow) : dim - 4;
+                copy16_to_lds((wave < kWaves ? dy : x) + r * dim + g,
+                              wave < kWaves ? &dst.dy[kRowsPerCopy * w][0] : &dst.x[kRowsPerCopy * w][0]);
+            } else if (wave < 2 * kWaves + 2 && kind != 0) {
+                const int half = wave - 2 * kWaves;  // rows 32 half .. 32 half + 31, two 4-byte lanes each
                 const int64_t rr = 32 * half + lane / 2;
                 const int64_t r = base + rr < r1 ? base + rr : r1 - 1;
                 copy4_to_lds(reinterpret_cast<const char*>(inv + r) + 4 * (lane & 1), &dst.inv[32 * half]);
@@ -254,13 +260,13 @@ __global__ __launch_bounds__(1024) void column_partial_lds_kernel(int kind, cons
             // every wave is done reading the ring slot the next copy refills
             asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kCsRing - 2) : "memory");
             issue(c + kCsRing - 1);
-            const CsSlot& src = ring[(c < chunks ? c : chunks - 1) % kCsRing];
+            const CsSlot<kC>& src = ring[(c < chunks ? c : chunks - 1) % kCsRing];
             const int buf = static_cast<int>(c & 1);
             double t = static_cast<double>(src.dy[slot][c16]);
             if (kind != 0) t = t * static_cast<double>(src.x[slot][c16]) * src.inv[slot];
             terms[buf][slot][c16] = t;
-            if (c > 0 && tid < 16) {
-                const double(&tp)[64][16] = terms[buf ^ 1];
+            if (c > 0 && tid < kC) {
+                const double(&tp)[64][kC] = terms[buf ^ 1];
                 const int64_t rs = (c - 1) * 64;
                 const int n = r1 - r0 - rs < 64 ? static_cast<int>(r1 - r0 - rs) : 64;
                 if (n == 64) {
@@ -290,7 +296,7 @@ __global__ __launch_bounds__(1024) void column_partial_lds_kernel(int kind, cons
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies past the end drain before exit
     }
-    if (tid < 16 && col0 + tid < dim)
+    if (tid < kC && col0 + tid < dim)
         part[static_cast<int64_t>(blockIdx.y) * dim + col0 + tid] = static_cast<float>(acc);
 }
 
@@ -680,9 +686,34 @@ int launch_column_sums(int kind, const float* dy, const float* x, const double* 
         for (int s = 0; s <= count; ++s) seg.off[s] = seg_host[s0 + s];
         float* part = direct ? out : partial + static_cast<int64_t>(s0) * dim;
         if (ring)
-            hipLaunchKernelGGL(column_partial_lds_kernel, dim3(static_cast<unsigned>(ceil_div(dim, 16)),
-                                                               static_cast<unsigned>(count)),
-                               dim3(1024), 0, stream, kind, dy, x, inv_rms, dim, seg, part);
+        {
+            // 16, 8 or 4 columns per workgroup: the fewest rounds of workgroups over the CUs (their LDS rings hold
+            // 1, 3 or 6 workgroups per CU). Every column's chain takes the same time, so a launch lasts about its
+            // rounds x one workgroup's time. On a tie the wider, unless a segment is long (4096 rows or more: there a
+            // narrower workgroup's smaller copies per chunk shorten its time; one window of 8192 x 896 took 84 us
+            // with 16 columns, 78 with 4; short windows measured slower with the narrower ones).
+            const auto rounds = [&](int c, int per_cu) {
+                return ceil_div(ceil_div(dim, c) * count, static_cast<int64_t>(per_cu) * 256);
+            };
+            int64_t longest = 0;
+            for (int s = 0; s < count; ++s) longest = std::max<int64_t>(longest, seg.off[s + 1] - seg.off[s]);
+            const int64_t r16 = rounds(16, 1), r8 = rounds(8, 3), r4 = rounds(4, 6);
+            int kc;
+            if (longest >= 4096) kc = r4 <= r8 && r4 <= r16 ? 4 : r8 <= r16 ? 8 : 16;
+            else kc = r16 <= r8 && r16 <= r4 ? 16 : r8 <= r4 ? 8 : 4;
+            if (kc == 16)
+                hipLaunchKernelGGL(column_partial_lds_kernel<16>, dim3(static_cast<unsigned>(ceil_div(dim, 16)),
+                                                                       static_cast<unsigned>(count)),
+                                   dim3(1024), 0, stream, kind, dy, x, inv_rms, dim, seg, part);
+            else if (kc == 8)
+                hipLaunchKernelGGL(column_partial_lds_kernel<8>, dim3(static_cast<unsigned>(ceil_div(dim, 8)),
+                                                                      static_cast<unsigned>(count)),
+                                   dim3(512), 0, stream, kind, dy, x, inv_rms, dim, seg, part);
+            else
+                hipLaunchKernelGGL(column_partial_lds_kernel<4>, dim3(static_cast<unsigned>(ceil_div(dim, 4)),
+                                                                      static_cast<unsigned>(count)),
+                                   dim3(256), 0, stream, kind, dy, x, inv_rms, dim, seg, part);
+        }
         else
             hipLaunchKernelGGL(column_partial_kernel, dim3(col_blocks, static_cast<unsigned>(count)), dim3(256), 0,
                                stream, kind, dy, x, inv_rms, dim, seg, part);
