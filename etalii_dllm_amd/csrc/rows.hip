@@ -687,20 +687,20 @@ int launch_column_sums(int kind, const float* dy, const float* x, const double* 
         float* part = direct ? out : partial + static_cast<int64_t>(s0) * dim;
         if (ring)
         {
-            // 16, 8 or 4 columns per workgroup: the fewest rounds of workgroups over the CUs (their LDS rings hold
-            // 1, 3 or 6 workgroups per CU). Every column's chain takes the same time, so a launch lasts about its
-            // rounds x one workgroup's time. On a tie the wider, unless a segment is long (4096 rows or more: there a
-            // narrower workgroup's smaller copies per chunk shorten its time; one window of 8192 x 896 took 84 us
-            // with 16 columns, 78 with 4; short windows measured slower with the narrower ones).
+            // 16, 8 or 4 columns per workgroup. For segments of 4096 rows or more, the narrowest that still puts
+            // at most one workgroup on each CU: a narrower workgroup's smaller copies per chunk shorten its time
+            // (one window of 8192 x 896: 84 us with 16 columns, 78 with 4), but workgroups sharing a CU slow each
+            // other (8192 x 4864 with 4 columns, 1216 workgroups: 233 us against 155 with 16). Otherwise the fewest
+            // rounds of workgroups over the CUs (their LDS rings hold 1, 3 or 6 per CU), the wider on a tie.
+            const auto groups = [&](int c) { return ceil_div(dim, c) * count; };
             const auto rounds = [&](int c, int per_cu) {
-                return ceil_div(ceil_div(dim, c) * count, static_cast<int64_t>(per_cu) * 256);
+                return ceil_div(groups(c), static_cast<int64_t>(per_cu) * 256);
             };
             int64_t longest = 0;
             for (int s = 0; s < count; ++s) longest = std::max<int64_t>(longest, seg.off[s + 1] - seg.off[s]);
             const int64_t r16 = rounds(16, 1), r8 = rounds(8, 3), r4 = rounds(4, 6);
-            int kc;
-            if (longest >= 4096) kc = r4 <= r8 && r4 <= r16 ? 4 : r8 <= r16 ? 8 : 16;
-            else kc = r16 <= r8 && r16 <= r4 ? 16 : r8 <= r4 ? 8 : 4;
+            int kc = r16 <= r8 && r16 <= r4 ? 16 : r8 <= r4 ? 8 : 4;
+            if (longest >= 4096 && groups(16) <= 256) kc = groups(4) <= 256 ? 4 : groups(8) <= 256 ? 8 : 16;
             if (kc == 16)
                 hipLaunchKernelGGL(column_partial_lds_kernel<16>, dim3(static_cast<unsigned>(ceil_div(dim, 16)),
                                                                        static_cast<unsigned>(count)),
