@@ -532,7 +532,7 @@ def main() -> int:
         return traffic_summary(args.config, *args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this backend runs the step on a single MI355X (got --gpus {args.gpus}); "
-              "the multi-GPU design is described in DESIGN.md", file=sys.stderr)
+              "on more GPUs each would take whole windows, their gradients summed in window order", file=sys.stderr)
         return 2
     cfg = CONFIGS[args.config]
     from etalii_dllm_amd.kernels import check, lib
