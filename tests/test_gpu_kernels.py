@@ -99,6 +99,22 @@ def test_rms_norm_forward_and_backward(K, ora, rows, dim):
         assert_same(got, want, name)
 
 
+# The column sums' workgroup widths (16, 8 or 4 columns by the rows and columns of the launch): long windows with
+# widths whose last workgroup is partial (dims multiples of 4, not of 8 or 16), so the copies clamp, against the
+# oracle: the norm weight's dw and a bias gradient (db).
+@pytest.mark.parametrize(("rows", "dim"), [(4100, 36), (4099, 100), (2048, 1540), (5000, 4)])
+def test_column_sums_at_every_workgroup_width(K, ora, rows, dim):
+    x, w, dy = O.gaussian(11, rows, dim, scale=2.0), O.gaussian(12, dim), O.gaussian(13, rows, dim)
+    for got, want, name in zip(K.rms_norm_backward(x, w, dy, 1e-6), ora.rms_norm_backward(x, w, dy, 1e-6),
+                               ("dx", "dw")):
+        assert_same(got, want, f"rms_norm_backward {name}")
+    x8, wl = O.gaussian(14, rows, 8), O.gaussian(15, dim, 8, scale=0.1)  # db sums dy's dim columns
+    got = K.linear_backward(x8, wl, dy, with_bias=True)
+    want = ora.linear_backward(x8, wl, dy, with_bias=True)
+    for g, e, name in zip(got, want, ("dx", "dw", "db")):
+        assert_same(g, e, f"linear_backward {name}")
+
+
 @pytest.mark.parametrize(("rotary", "theta"), [(16, 1e6), (8, 1e4), (128, 1e6)])
 @pytest.mark.parametrize("interleaved", [False, True])
 def test_rope(K, ora, rotary, theta, interleaved):
