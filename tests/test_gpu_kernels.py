@@ -129,7 +129,7 @@ def test_rope(K, ora, rotary, theta, interleaved):
 
 # Head counts past four rows per wave (the in-kernel cos/sin path batches four heads' loads), partial rotary, and a
 # 256-wide head (rows of 128 elements: the table path).
-@pytest.mark.parametrize(("heads", "hd", "rotary"), [(14, 64, 64), (2, 64, 64), (7, 128, 128), (9, 96, 32),
+@pytest.mark.parametrize(("heads", "hd", "rotary"), [(14, 64, 64), (2, 64, 64), (7, 128, 128), (9, 96, 32), (5, 80, 64),
                                                      (4, 256, 256), (17, 16, 16)])
 @pytest.mark.parametrize("interleaved", [False, True])
 def test_rope_many_heads(K, ora, heads, hd, rotary, interleaved):
