@@ -447,10 +447,11 @@ __global__ __launch_bounds__(256) void rope_direct_kernel(const float* __restric
     }
 }
 
-// Two tensors of the same tokens (the queries and the keys) in one launch, one wave per (token, head) row at a time:
-// the row's token is one wave-uniform division per row, and lane k takes pairs k, k + 64, ... of the row (coalesced
-// loads and stores). Rows [0, tokens heads1) are the first tensor's, the next tokens heads2 the second's. (One thread
-// per pair with 64-bit index divisions made the kernel compute-bound: 3.3 TB/s at c3's 8192 x 1792 values.)
+// Two tensors of the same tokens (the queries and the keys) in one launch, one wave per (token, head) row at a time,
+// or 64 / per_head rows at once for rows of at most 32 elements (rope_lanes): lane k takes pairs k, k + 64, ... of its
+// row (coalesced loads and stores), its token a 32-bit division (row_token). Rows [0, tokens heads1) are the first
+// tensor's, the next tokens heads2 the second's. (One thread per pair with 64-bit index divisions made the kernel
+// compute-bound: 3.3 TB/s at c3's 8192 x 1792 values.)
 __global__ __launch_bounds__(256) void rope_pair_kernel(const float* __restrict__ x1, float* __restrict__ out1,
                                                         int64_t heads1, const float* __restrict__ x2,
                                                         float* __restrict__ out2, int64_t heads2,
